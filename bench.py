@@ -1,0 +1,267 @@
+"""Benchmark: achieved HBM GB/s of the unpopped-hip reduce / scan / gather / dequant kernels on
+one MI355X, against the 8 TB/s peak.
+
+One step is one pass of the suite over the seeded synthetic inputs, each kernel launched once:
+  cfg2   row Sum + Max of an f32 8192 x 4096 matrix, read once (normal(0,1), seed 1)
+  cfg3a  inclusive i32 Sum scan of 2^28 elements in [0, 16) (seed 2)
+  cfg3b  inclusive f32 Sum scan of 2^26 dyadic uniforms in [0, 1) (seed 2)
+  cfg4u  bf16 262144 x 4096 row gather of 65536 uniform ids (seed 3)
+  cfg4z  the same gather with Zipf(1.1) ids (seed 3)
+  cfg5   U4 8192 x 28672 dequant, f16 scales and U4 zeros per 128 columns, bf16 out (seed 4)
+Inputs are resident in HBM before the timed region.  Each kernel's time is the average over the
+timed steps of the HIP-event interval around its launch on the launch stream; `value` is the
+suite's algorithmic bytes over the suite's kernel time.  The CPU baseline is the oracle (the
+C restatement of the reference's serial algorithms, one thread) on a bounded sample of each
+configuration.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_GBPS = 8000.0
+METRIC = "achieved HBM GB/s (% of ~8 TB/s peak) for reduce/scan/gather/dequant, 1 MI355X"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Case:
+    def __init__(self, name, what, nbytes, elements, setup):
+        self.name, self.what, self.nbytes, self.elements, self.setup = name, what, nbytes, elements, setup
+        self.launch = None
+
+
+def build_cases(u, synth):
+    from unpopped_amd import forms as H
+
+    cases = []
+
+    def cfg2():
+        R, Cc = 8192, 4096
+        x = synth.normal_f32(1, R * Cc)
+        ex = H.executor(kind="row_reduce2", dtype="F32", rank=2, op="Sum", op1="Max", reduced_from=1)
+        din = u.DeviceBuffer.from_array(x)
+        o0, o1 = u.DeviceBuffer(R * 4), u.DeviceBuffer(R * 4)
+        return lambda: ex.launch(din, o0, o1, R, Cc), ex
+    cases.append(Case("cfg2", "f32 8192x4096 row sum+max (fused, read once)", 8192 * 4096 * 4 + 2 * 8192 * 4,
+                      8192 * 4096, cfg2))
+
+    def cfg3a():
+        n = 1 << 28
+        x = synth.int16_i32(2, n)
+        ex = H.executor(kind="scan", dtype="I32", rank=1, op="Sum")
+        din = u.DeviceBuffer.from_array(x)
+        dout = u.DeviceBuffer(n * 4)
+        return lambda: ex.launch(din, dout, n), ex
+    cases.append(Case("cfg3a", "i32 inclusive sum scan 2^28", 2 * (1 << 28) * 4, 1 << 28, cfg3a))
+
+    def cfg3b():
+        n = 1 << 26
+        x = synth.uniform_01_f32(2, n)
+        ex = H.executor(kind="scan", dtype="F32", rank=1, op="Sum")
+        din = u.DeviceBuffer.from_array(x)
+        dout = u.DeviceBuffer(n * 4)
+        return lambda: ex.launch(din, dout, n), ex
+    cases.append(Case("cfg3b", "f32 inclusive sum scan 2^26 (f64 carry)", 2 * (1 << 26) * 4, 1 << 26, cfg3b))
+
+    table_holder = {}
+
+    def gather(dist):
+        def setup():
+            V, D, N = 262144, 4096, 65536
+            if "table" not in table_holder:
+                log("[bench] generating the 2 GiB bf16 table")
+                t = synth.normal_bf16_bits(3, V * D, 0.02)
+                table_holder["table"] = u.DeviceBuffer.from_array(t)
+                del t
+            ids = synth.uniform_ids_i32(3, N, V) if dist == "uniform" else synth.zipf_ids_i32(3, N, V, 1.1)
+            ex = H.executor(kind="gather", dtype="Bf16", rank=2, index_dtype="I32", oob="ZeroFill")
+            dids = u.DeviceBuffer.from_array(ids)
+            dout = u.DeviceBuffer(N * D * 2)
+            dt = table_holder["table"]
+            return lambda: ex.launch(dt, dids, dout, N, D, V), ex
+        return setup
+    gbytes = 65536 * 4096 * 2 * 2 + 65536 * 4
+    cases.append(Case("cfg4u", "bf16 262144x4096 gather, 65536 uniform ids", gbytes, 65536 * 4096, gather("uniform")))
+    cases.append(Case("cfg4z", "bf16 262144x4096 gather, 65536 Zipf(1.1) ids", gbytes, 65536 * 4096, gather("zipf")))
+
+    def cfg5():
+        R, Cc, G = 8192, 28672, 128
+        q = synth.nibbles(4, R * Cc)
+        z = synth.nibbles(41, R * (Cc // G))
+        s = synth.uniform_f16_bits(42, R * (Cc // G), 0.001, 0.02)
+        ex = H.executor(kind="dequant4", q_kind="U4", z_kind="U4", group=G, out_kind="Bf16")
+        dq, ds, dz = u.DeviceBuffer.from_array(q), u.DeviceBuffer.from_array(s), u.DeviceBuffer.from_array(z)
+        do = u.DeviceBuffer(R * Cc * 2)
+        return lambda: ex.launch(dq, ds, dz, do, R, Cc), ex
+    dq_bytes = 8192 * 28672 // 2 + 8192 * 224 * 2 + 8192 * 224 // 2 + 8192 * 28672 * 2
+    cases.append(Case("cfg5", "U4 8192x28672 -> bf16 dequant, g128", dq_bytes, 8192 * 28672, cfg5))
+    return cases
+
+
+def cpu_baseline(synth, budget_s: float = 20.0) -> dict:
+    """The oracle (single-threaded C) on a bounded sample of each configuration."""
+    import oracle
+
+    legs = []
+
+    def timed(fn, nbytes, what):
+        fn()  # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            dt = time.perf_counter() - t0
+            if dt > budget_s / 6 or reps >= 5:
+                break
+        legs.append({"sample": what, "bytes": nbytes, "s": dt / reps})
+
+    x2 = synth.normal_f32(1, 1024 * 4096).reshape(1024, 4096)
+    timed(lambda: (oracle.reduce_rows(x2, "Sum"), oracle.reduce_rows(x2, "Max")), x2.nbytes + 2 * 1024 * 4,
+          "cfg2 1024 of 8192 rows")
+    x3 = synth.int16_i32(2, 1 << 24).reshape(1, -1)
+    timed(lambda: oracle.scan_rows(x3, "Sum"), 2 * x3.nbytes, "cfg3a 2^24 of 2^28")
+    x3b = synth.uniform_01_f32(2, 1 << 24).reshape(1, -1)
+    timed(lambda: oracle.scan_rows(x3b, "Sum"), 2 * x3b.nbytes, "cfg3b 2^24 of 2^26")
+    V, D, N = 16384, 4096, 4096
+    t = synth.normal_bf16_bits(3, V * D, 0.02).reshape(V, D)
+    ids = synth.uniform_ids_i32(3, N, V)
+    timed(lambda: oracle.gather_rows(t, ids, "ZeroFill"), 2 * N * D * 2 + N * 4, "cfg4 4096 rows from a 16384-row table")
+    R, Cc, G = 256, 28672, 128
+    q, z = synth.nibbles(4, R * Cc), synth.nibbles(41, R * (Cc // G))
+    s = synth.uniform_f16_bits(42, R * (Cc // G), 0.001, 0.02)
+    timed(lambda: oracle.dequant4_bf16(q, s, z, R, Cc, G), R * Cc // 2 + R * 224 * 3 + R * Cc * 2,
+          "cfg5 256 of 8192 rows")
+    total_b = sum(l["bytes"] for l in legs)
+    total_s = sum(l["s"] for l in legs)
+    return {
+        "value": round(total_b / total_s / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": "; ".join(f"{l['sample']}: {l['bytes'] / l['s'] / 1e9:.3f} GB/s" for l in legs),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", default="", help="comma-separated case names (default: the whole suite)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    import unpopped_amd as u
+    from unpopped_amd import synth
+
+    if u.device_count() < 1:
+        print("no HIP device", file=sys.stderr)
+        return 1
+    arch, cus = u.device_info()
+    log(f"[bench] device {arch}, {cus} CUs")
+    cases = build_cases(u, synth)
+    if args.only:
+        keep = set(args.only.split(","))
+        cases = [c for c in cases if c.name in keep]
+    for c in cases:
+        log(f"[bench] setup {c.name}: {c.what}")
+        c.launch, c.exec = c.setup()
+    for c in cases:
+        log(f"[bench] warmup {c.name}")
+        for _ in range(args.warmup):
+            c.launch()
+    u.synchronize()
+
+    events = [[u.Event() for _ in range(len(cases) + 1)] for _ in range(args.steps)]
+    log(f"[bench] timing {args.steps} steps")
+    u.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        ev = events[s]
+        ev[0].record()
+        for i, c in enumerate(cases):
+            c.launch()
+            ev[i + 1].record()
+    u.synchronize()
+    wall = time.perf_counter() - t0
+
+    per = []
+    for i, c in enumerate(cases):
+        ms = sum(events[s][i].elapsed_ms(events[s][i + 1]) for s in range(args.steps)) / args.steps
+        gbps = c.nbytes / (ms * 1e-3) / 1e9
+        per.append({
+            "name": c.name, "what": c.what, "entry": c.exec.last_launch()["entry"],
+            "grid": c.exec.last_launch()["grid"][0], "bytes": c.nbytes, "us": round(ms * 1e3, 2),
+            "GBps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_GBPS, 4),
+            "elements_per_s": round(c.elements / (ms * 1e-3), 1),
+        })
+        log(f"[bench] {c.name}: {ms * 1e3:.1f} us, {gbps:.0f} GB/s ({100 * gbps / PEAK_GBPS:.1f}% of peak)")
+    total_bytes = sum(c.nbytes for c in cases)
+    ms_step = sum(p["us"] for p in per) / 1e3
+    value = total_bytes / (ms_step * 1e-3) / 1e9
+    dom = max(per, key=lambda p: p["us"])
+
+    traffic = None
+    tf = ROOT / "profiles" / "traffic.json"
+    if tf.exists():
+        t = json.loads(tf.read_text()).get(dom["name"])
+        if t:
+            traffic = t.get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] CPU baseline (oracle, 1 thread)")
+        cpu = cpu_baseline(synth)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (f64 accumulate), i32, bf16 (raw move), u4 -> bf16",
+        "data": "synthetic: seeded LCG streams (dyadic uniforms, Box-Muller normals, Zipf ids)",
+        "config": {
+            "workload": "suite: " + ", ".join(c.name for c in cases),
+            "device": arch,
+            "cu_count": cus,
+            "wall_s_timed_region": round(wall, 4),
+            "kernels": per,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom["name"],
+            "achieved": dom["GBps"],
+            "peak": PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(dom["GBps"] / PEAK_GBPS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,208 @@
+/*
+ * unpopped-hip: an MI355X (gfx950) backend for the Unpopped kernel generator, as a C ABI.
+ *
+ * The reference (EvansLaboratories/Unpopped 0.56.5) defines two seams a device backend
+ * implements, both Rust traits:
+ *
+ *   trait Backend   crates/unpopped/src/backend.rs:668-807   (name, provider, lower,
+ *                   lower_kernel, supports_dtype, total_integer_ops, effective_count_width,
+ *                   lower_variants)
+ *   trait Compiler  crates/unpopped/src/jit.rs:271-285       (compile, artifact_kind)
+ *
+ * and stops before the launch (no reference source writes a launch: docs/PATENT-SWEEP.md
+ * :265-272).  This library is the HIP side of both seams plus the launch layer a consumer
+ * needs: a thin FFI over the HIP runtime (hipModuleLoadData, hipModuleLaunchKernel,
+ * hipMalloc, hipEvent*) and a prepared-kernel executor that owns the look-back / partial
+ * workspaces and picks the launch geometry from the device.
+ *
+ * Conventions (backend.rs:703-707, jit.rs:397-401): every entry point returns a status
+ * code and never aborts; a refusal is a typed code plus a diagnostic string that is for
+ * people, not for matching.  Everything the library allocates is released by the
+ * matching unp_*_free / _destroy call.  Handles are not thread-safe; one caller at a time.
+ */
+#ifndef UNPOPPED_HIP_H
+#define UNPOPPED_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------------------------
+ * Status codes.  1..6 mirror LowerError (crates/unpopped/src/backend.rs:386-440) in
+ * declaration order; the rest are this library's own.
+ * ------------------------------------------------------------------------------------- */
+enum unp_status {
+  UNP_OK = 0,
+  UNP_UNSUPPORTED_DTYPE = 1,      /* LowerError::UnsupportedDtype      backend.rs:388 */
+  UNP_UNSUPPORTED_SCHEDULE = 2,   /* LowerError::UnsupportedSchedule   backend.rs:396 */
+  UNP_UNSUPPORTED_OP = 3,         /* LowerError::UnsupportedOp         backend.rs:402 */
+  UNP_UNSUPPORTED_PLAN_SHAPE = 4, /* LowerError::UnsupportedPlanShape  backend.rs:408 */
+  UNP_INADMISSIBLE_PLAN = 5,      /* LowerError::InadmissiblePlan      backend.rs:424 */
+  UNP_UNSUPPORTED_KERNEL = 6,     /* LowerError::UnsupportedKernel     backend.rs:436 */
+  UNP_LIFT_DECLINE = 10,          /* LiftDecline (kernel_lift.rs:48-85); detail names it */
+  UNP_COMPILE_ERROR = 20,         /* Compiler::compile Err(String)     jit.rs:278 */
+  UNP_HIP_ERROR = 30,             /* a HIP runtime call failed; detail has hipGetErrorString */
+  UNP_INVALID_ARGUMENT = 40,      /* a launch argument does not fit the kernel's interface */
+  UNP_PARSE_ERROR = 50            /* kernel JSON text that is not a KernelFn */
+};
+
+typedef struct unp_error {
+  int32_t code;
+  char detail[512];
+} unp_error;
+
+/* ---------------------------------------------------------------------------------------
+ * Element kinds: the reference's ElementKind (crates/unpopped-vocab/src/element.rs:1052)
+ * in declaration order; the JSON form uses the variant names (crates/unpopped/src/text.rs:56).
+ * ------------------------------------------------------------------------------------- */
+enum unp_element_kind {
+  UNP_F16 = 0, UNP_BF16 = 1, UNP_F32 = 2, UNP_F32_STRICT = 3, UNP_F64 = 4,
+  UNP_I8 = 5, UNP_I16 = 6, UNP_U8 = 7, UNP_U16 = 8, UNP_I32 = 9, UNP_I64 = 10, UNP_BOOL = 11,
+  UNP_FP8_E4M3FN = 12, UNP_FP8_E4M3FNUZ = 13, UNP_FP8_E5M2 = 14, UNP_F8_E8M0 = 15,
+  UNP_F8_E6M2 = 16, UNP_FP8_E5M2FNUZ = 17, UNP_I4 = 18, UNP_U4 = 19, UNP_B1 = 20,
+  UNP_COMPLEX64 = 21, UNP_COMPLEX128 = 22, UNP_U32 = 23, UNP_U64 = 24,
+  UNP_F4_E2M1 = 25, UNP_F6_E2M3 = 26, UNP_F6_E3M2 = 27
+};
+
+/* DtypeSupport (backend.rs:645-655). */
+enum unp_dtype_support { UNP_SUPPORTED = 0, UNP_UNSUPPORTED = 1, UNP_NOT_EXPRESSIBLE = 2 };
+
+/* ArtifactKind (crates/unpopped/src/jit.rs:139-152); this compiler answers HipCodeObject. */
+enum unp_artifact_kind {
+  UNP_ARTIFACT_PTX = 0, UNP_ARTIFACT_CUBIN = 1, UNP_ARTIFACT_HIP_CODE_OBJECT = 2,
+  UNP_ARTIFACT_SPIRV = 3, UNP_ARTIFACT_STUB = 4
+};
+
+/* ---------------------------------------------------------------------------------------
+ * Backend seam (trait Backend, backend.rs:668-807).
+ * ------------------------------------------------------------------------------------- */
+
+/* Backend::name (backend.rs:671): "hip". */
+const char* unp_hip_name(void);
+/* Backend::provider (backend.rs:681): "unpopped-hip". */
+const char* unp_hip_provider(void);
+/* Backend::total_integer_ops (backend.rs:692): 0, the default. */
+int32_t unp_hip_total_integer_ops(void);
+/* Backend::supports_dtype (backend.rs:779): one of unp_dtype_support for an element kind on
+ * a target id such as "rocm:gfx950" (crates/unpopped-vocab/src/target.rs:188). */
+int32_t unp_hip_supports_dtype(int32_t kind, const char* target);
+
+/* GeneratedKernel (backend.rs:105-193): name, source and the launch interface as JSON. */
+typedef struct unp_generated unp_generated;
+const char* unp_generated_name(const unp_generated* g);
+const char* unp_generated_source(const unp_generated* g);
+const char* unp_generated_interface_json(const unp_generated* g);
+/* FNV-1a 64 over the source text (crates/unpopped/src/revision.rs). */
+uint64_t unp_generated_revision_hash(const unp_generated* g);
+void unp_generated_free(unp_generated* g);
+
+/* A lowering request in the backend's own terms: the launched reduction, scan, gather,
+ * sub-byte dequant and fused row-reduce forms that lower_kernel recognises in a KernelFn.
+ * Fields not used by a form are ignored. */
+enum unp_form_kind {
+  UNP_FORM_REDUCTION = 0, /* Access::Reduction, launched (kernel_lift/block_reduce.rs:50) */
+  UNP_FORM_SCAN = 1,      /* Access::Scan, launched (kernel_lift/scan_launched.rs:54) */
+  UNP_FORM_GATHER = 2,    /* ReadIndex::Indexed gather (kernel_lift/gather.rs:35) */
+  UNP_FORM_DEQUANT4 = 3,  /* U4/I4 x f16 scale x 4-bit zero -> bf16 (tests/support/dequant.rs) */
+  UNP_FORM_ROW_REDUCE2 = 4 /* two folds of each row read once (Sum and Max: softmax prologue) */
+};
+/* ReduceOp subset (crates/unpopped/src/ir.rs:1700). */
+enum unp_reduce_op { UNP_OP_SUM = 0, UNP_OP_PROD = 1, UNP_OP_MAX = 2, UNP_OP_MIN = 3, UNP_OP_MEAN = 4 };
+/* OobPolicy (ir.rs:2582). */
+enum unp_oob_policy { UNP_OOB_SKIP = 0, UNP_OOB_ZEROFILL = 1, UNP_OOB_CLAMP = 2 };
+
+typedef struct unp_form {
+  int32_t kind;        /* unp_form_kind */
+  int32_t dtype;       /* element kind of the data (gather: of the table) */
+  int32_t rank;        /* input rank (reduction/scan), output rank (gather); 2 for dequant */
+  int32_t op0, op1;    /* unp_reduce_op; op1 only for UNP_FORM_ROW_REDUCE2 */
+  int32_t reduced_from;/* reduction: first reduced axis; axes reduced_from..rank-1 fold */
+  int32_t exclusive;   /* scan */
+  int32_t reverse;     /* scan */
+  int32_t index_dtype; /* gather: I32, I64 or U32 */
+  int32_t oob;         /* gather: unp_oob_policy */
+  int32_t data_slot;   /* gather: which input (0 or 1) is the table; the other is the index */
+  int32_t q_kind;      /* dequant: U4 or I4 weights */
+  int32_t z_kind;      /* dequant: U4 or I4 zero points */
+  int32_t group;       /* dequant: columns per scale/zero group */
+  int32_t out_kind;    /* dequant: Bf16 */
+} unp_form;
+
+/* Lower one form to HIP source (the work Backend::lower_kernel does once it has recognised
+ * the lifted kernel).  *out is owned by the caller (unp_generated_free). */
+int32_t unp_hip_lower_form(const unp_form* form, unp_generated** out, unp_error* err);
+
+/* ---------------------------------------------------------------------------------------
+ * Compiler seam (trait Compiler, jit.rs:271-285), through hipRTC for gfx950.
+ * ------------------------------------------------------------------------------------- */
+
+/* Compiler::compile (jit.rs:278): source -> code-object bytes.  max_compile_ms = 0 means no
+ * budget; a compile that overruns a nonzero budget is an error.  *bytes is freed with
+ * unp_free_bytes, *diag (the compiler log, may be NULL) with unp_free_str. */
+int32_t unp_hip_compile(const char* source, const char* entry, uint32_t max_compile_ms,
+                        uint8_t** bytes, size_t* len, char** diag);
+/* Compiler::artifact_kind (jit.rs:282): UNP_ARTIFACT_HIP_CODE_OBJECT. */
+int32_t unp_hip_artifact_kind(void);
+void unp_free_bytes(uint8_t* p);
+void unp_free_str(char* s);
+
+/* ---------------------------------------------------------------------------------------
+ * HIP runtime FFI (the consumer's launch layer; no reference counterpart by design).
+ * ------------------------------------------------------------------------------------- */
+typedef struct unp_module unp_module;
+typedef struct unp_function unp_function;
+typedef struct unp_event unp_event;
+
+int32_t unp_hip_device_count(int32_t* count);
+int32_t unp_hip_set_device(int32_t device);
+/* gcnArchName (e.g. "gfx950:sramecc+:xnack-") and compute-unit count of the current device. */
+int32_t unp_hip_device_info(char* arch, size_t arch_len, int32_t* cu_count);
+int32_t unp_hip_module_load(const uint8_t* image, size_t len, unp_module** out, unp_error* err);
+int32_t unp_hip_module_unload(unp_module* m);
+int32_t unp_hip_get_function(unp_module* m, const char* name, unp_function** out, unp_error* err);
+/* Launch with a packed kernel-argument block (the layout the interface JSON states). */
+int32_t unp_hip_launch(unp_function* f, const uint32_t grid[3], const uint32_t block[3],
+                       uint32_t shared_bytes, void* stream, const void* kernarg, size_t kernarg_size,
+                       unp_error* err);
+int32_t unp_hip_malloc(void** p, size_t bytes);
+int32_t unp_hip_free(void* p);
+int32_t unp_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int32_t unp_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int32_t unp_hip_memset(void* p, int32_t value, size_t bytes);
+int32_t unp_hip_synchronize(void);
+int32_t unp_hip_event_create(unp_event** e);
+int32_t unp_hip_event_destroy(unp_event* e);
+int32_t unp_hip_event_record(unp_event* e, void* stream);
+int32_t unp_hip_event_synchronize(unp_event* e);
+int32_t unp_hip_event_elapsed_ms(unp_event* start, unp_event* stop, float* ms);
+
+/* ---------------------------------------------------------------------------------------
+ * Prepared kernels: a lowered kernel compiled (in-process, compile-once per source) and
+ * loaded on the current device, with the workspace its schedule needs.
+ * ------------------------------------------------------------------------------------- */
+typedef struct unp_exec unp_exec;
+
+/* One launch argument, in the lowered KernelFn's parameter order: a buffer is a device
+ * pointer, a scalar is an integer (the reference's extents are I32 scalars). */
+typedef struct unp_arg {
+  int32_t is_buffer;
+  int32_t pad;
+  uint64_t value; /* device address or scalar value */
+} unp_arg;
+
+int32_t unp_hip_exec_create(const unp_generated* g, unp_exec** out, unp_error* err);
+int32_t unp_hip_exec_launch(unp_exec* e, const unp_arg* args, size_t nargs, void* stream,
+                            unp_error* err);
+/* The last launch's geometry and chosen entry point (for reports). */
+int32_t unp_hip_exec_last_launch(const unp_exec* e, uint32_t grid[3], uint32_t block[3],
+                                 char* entry, size_t entry_len);
+void unp_hip_exec_destroy(unp_exec* e);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UNPOPPED_HIP_H */

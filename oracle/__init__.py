@@ -1,0 +1,177 @@
+"""CPU oracle for the unpopped-hip hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg may import
+this package, and only as the checker (or the timed CPU baseline); the product path never
+calls it.  The C restatement is ``oracle.c`` (each function cites the reference file:line it
+follows); this module binds it with ctypes and numpy.
+
+Parity pinning: every function here is checked in ``tests/test_oracle.py`` against the
+reference's own golden vectors where its tests hold them, and against closed forms, independent
+library routines (numpy float16, torch bfloat16) or brute force otherwise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+
+SUM, PROD, MAX, MIN, MEAN = 0, 1, 2, 3, 4
+OPS = {"Sum": SUM, "Prod": PROD, "Max": MAX, "Min": MIN, "Mean": MEAN}
+SKIP, ZEROFILL, CLAMP = 0, 1, 2
+POLICIES = {"Skip": SKIP, "ZeroFill": ZEROFILL, "Clamp": CLAMP}
+IDX_KINDS = {"I32": 9, "I64": 10, "U32": 23}
+
+_L = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+def lib() -> C.CDLL:
+    global _L
+    if _L is None:
+        if not LIB.exists():
+            build()
+        L = C.CDLL(str(LIB))
+        P, i64, i32, d, f = C.c_void_p, C.c_int64, C.c_int, C.c_double, C.c_float
+        sig = {
+            "orc_f32_to_bf16_bits": (C.c_uint16, [f]),
+            "orc_bf16_to_f64": (d, [C.c_uint16]),
+            "orc_f16_to_f64": (d, [C.c_uint16]),
+            "orc_f32_to_f16_bits": (C.c_uint16, [f]),
+            "orc_f64_to_f32_odd": (f, [d]),
+            "orc_store_bf16": (C.c_uint16, [d]),
+            "orc_f32_to_bf16_array": (None, [P, i64, P]),
+            "orc_f16_to_f64_array": (None, [P, i64, P]),
+            "orc_u4_load": (C.c_int32, [P, i64]),
+            "orc_i4_load": (C.c_int32, [P, i64]),
+            "orc_sub4_store": (None, [P, i64, C.c_int32]),
+            "orc_reduce_rows_f32": (None, [P, i64, i64, i32, P]),
+            "orc_reduce_rows_f64": (None, [P, i64, i64, i32, P]),
+            "orc_reduce_rows_i32": (None, [P, i64, i64, i32, P]),
+            "orc_reduce_rows_i64": (None, [P, i64, i64, i32, P]),
+            "orc_sum_launched_order": (d, [P, i64, i64, i32]),
+            "orc_sum_bound": (d, [P, i64, i32, i32, d]),
+            "orc_neumaier": (d, [P, i64]),
+            "orc_scan_rows_f32": (None, [P, i64, i64, i32, i32, i32, P]),
+            "orc_scan_rows_f64": (None, [P, i64, i64, i32, i32, i32, P]),
+            "orc_scan_rows_i32": (None, [P, i64, i64, i32, i32, i32, P]),
+            "orc_scan_rows_i64": (None, [P, i64, i64, i32, i32, i32, P]),
+            "orc_scan_launched_order_f32": (None, [P, i64, i64, i32, i32, P]),
+            "orc_gather_rows": (None, [P, i64, i64, P, i32, i64, i32, P]),
+            "orc_dequant4_bf16": (None, [P, i32, P, P, i32, i64, i64, i64, P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _L = L
+    return _L
+
+
+def _p(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# ---- codecs ---------------------------------------------------------------------------
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty(x.size, np.uint16)
+    lib().orc_f32_to_bf16_array(_p(x), x.size, _p(out))
+    return out
+
+
+def f16_to_f64(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16).ravel()
+    out = np.empty(h.size, np.float64)
+    lib().orc_f16_to_f64_array(_p(h), h.size, _p(out))
+    return out
+
+
+# ---- reductions -----------------------------------------------------------------------
+
+_RED = {np.float32: "orc_reduce_rows_f32", np.float64: "orc_reduce_rows_f64",
+        np.int32: "orc_reduce_rows_i32", np.int64: "orc_reduce_rows_i64"}
+
+
+def reduce_rows(x: np.ndarray, op: str) -> np.ndarray:
+    """Fold each row of a 2-D array (the serial reduction lift's order and rounding)."""
+    x = np.ascontiguousarray(x)
+    rows, cols = x.shape
+    out = np.empty(rows, x.dtype)
+    getattr(lib(), _RED[x.dtype.type])(_p(x), rows, cols, OPS[op], _p(out))
+    return out
+
+
+def sum_launched_order(xs: np.ndarray, block: int, mean: bool = False) -> float:
+    xs = np.ascontiguousarray(xs, dtype=np.float64)
+    return lib().orc_sum_launched_order(_p(xs), xs.size, block, int(mean))
+
+
+def sum_bound(xs: np.ndarray, got: float, mean: bool = False, f32: bool = True) -> float:
+    xs = np.ascontiguousarray(xs, dtype=np.float64)
+    return lib().orc_sum_bound(_p(xs), xs.size, int(mean), int(f32), float(got))
+
+
+def neumaier(xs: np.ndarray) -> float:
+    xs = np.ascontiguousarray(xs, dtype=np.float64)
+    return lib().orc_neumaier(_p(xs), xs.size)
+
+
+# ---- scans ----------------------------------------------------------------------------
+
+_SCAN = {np.float32: "orc_scan_rows_f32", np.float64: "orc_scan_rows_f64",
+         np.int32: "orc_scan_rows_i32", np.int64: "orc_scan_rows_i64"}
+
+
+def scan_rows(x: np.ndarray, op: str, exclusive: bool = False, reverse: bool = False) -> np.ndarray:
+    """Scan each row of a 2-D array along its last axis (the serial scan lift)."""
+    x = np.ascontiguousarray(x)
+    rows, cols = x.shape
+    out = np.empty_like(x)
+    getattr(lib(), _SCAN[x.dtype.type])(_p(x), rows, cols, OPS[op], int(exclusive), int(reverse), _p(out))
+    return out
+
+
+def scan_launched_order_f32(x: np.ndarray, block: int, exclusive=False, reverse=False) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().orc_scan_launched_order_f32(_p(x), x.size, block, int(exclusive), int(reverse), _p(out))
+    return out
+
+
+# ---- gather ---------------------------------------------------------------------------
+
+def gather_rows(table: np.ndarray, ids: np.ndarray, policy: str, out_init: np.ndarray | None = None,
+                src_extent: int | None = None) -> np.ndarray:
+    """``out[r] = table[clamp(ids[r])]`` under the policy; rows are raw bytes."""
+    table = np.ascontiguousarray(table)
+    ids = np.ascontiguousarray(ids)
+    ext = table.shape[0] if src_extent is None else src_extent
+    row_bytes = table[0].nbytes if table.shape[0] else int(np.prod(table.shape[1:])) * table.itemsize
+    n = ids.shape[0]
+    out = (np.zeros((n,) + table.shape[1:], table.dtype) if out_init is None
+           else np.ascontiguousarray(out_init).copy())
+    kind = {np.int32: 9, np.int64: 10, np.uint32: 23}[ids.dtype.type]
+    lib().orc_gather_rows(_p(table), ext, row_bytes, _p(ids), kind, n, POLICIES[policy], _p(out))
+    return out
+
+
+# ---- dequant --------------------------------------------------------------------------
+
+def dequant4_bf16(q_packed: np.ndarray, scales_f16_bits: np.ndarray, zeros_packed: np.ndarray, rows: int,
+                  cols: int, group: int, q_signed: bool = False, z_signed: bool = False) -> np.ndarray:
+    q = np.ascontiguousarray(q_packed, dtype=np.uint8)
+    s = np.ascontiguousarray(scales_f16_bits, dtype=np.uint16)
+    z = np.ascontiguousarray(zeros_packed, dtype=np.uint8)
+    out = np.empty(rows * cols, np.uint16)
+    lib().orc_dequant4_bf16(_p(q), int(q_signed), _p(s), _p(z), int(z_signed), rows, cols, group, _p(out))
+    return out.reshape(rows, cols)

@@ -1,0 +1,386 @@
+/*
+ * CPU oracle for the unpopped-hip hot path.  TEST INFRASTRUCTURE ONLY (see oracle.h): the
+ * parity tests, the smoke check and the benchmark's CPU-baseline leg call it as the checker.
+ *
+ * Single-threaded plain C, compiled with -O2 -ffp-contract=off like the reference's C leg
+ * (crates/unpopped-cpu-c/tests/support/cc.rs:163-176), so every float operation rounds as
+ * written.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+static uint32_t bits32(float f) {
+  uint32_t b;
+  memcpy(&b, &f, 4);
+  return b;
+}
+static float from32(uint32_t b) {
+  float f;
+  memcpy(&f, &b, 4);
+  return f;
+}
+
+/* ======================================================================================
+ * Codecs
+ * ==================================================================================== */
+
+/* f32 -> bf16, nearest even; a NaN keeps its top half and is quieted.
+ * crates/unpopped/src/oracle/float_codec.rs:259-266 */
+uint16_t orc_f32_to_bf16_bits(float x) {
+  const uint32_t b = bits32(x);
+  if (x != x) return (uint16_t)((b >> 16) | 0x40u);
+  return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+/* bf16 is the top half of an f32.  float_codec.rs:201-204 */
+double orc_bf16_to_f64(uint16_t b) { return (double)from32((uint32_t)b << 16); }
+
+/* binary16 decode, subnormals as mant * 2^-24, a NaN keeps its sign.  float_codec.rs:11-28 */
+double orc_f16_to_f64(uint16_t h) {
+  const double sign = (h & 0x8000u) ? -1.0 : 1.0;
+  const int e = (h >> 10) & 0x1f;
+  const int m = h & 0x3ff;
+  if (e == 0) return sign * ldexp((double)m, -24);
+  if (e == 0x1f) return m ? copysign(NAN, sign) : sign * INFINITY;
+  return sign * ldexp(1.0 + (double)m / 1024.0, e - 15);
+}
+
+/* f32 -> binary16, nearest even, overflow to infinity.  float_codec.rs:206-257 */
+uint16_t orc_f32_to_f16_bits(float x) {
+  const uint32_t b = bits32(x);
+  const uint16_t sign = (uint16_t)((b >> 16) & 0x8000u);
+  const int exp = (int)((b >> 23) & 0xff);
+  const uint32_t mant = b & 0x7fffffu;
+  if (exp == 0xff) return (uint16_t)(sign | (mant ? 0x7e00u : 0x7c00u));
+  const int e = exp - 127 + 15;
+  if (e >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return sign;
+    const uint32_t m = mant | 0x800000u;
+    const uint32_t shift = (uint32_t)(14 - e);
+    const uint32_t half = 1u << (shift - 1), rem = m & ((1u << shift) - 1);
+    uint32_t r = m >> shift;
+    if (rem > half || (rem == half && (r & 1u))) r += 1;
+    return (uint16_t)(sign | r);
+  }
+  const uint32_t rem = mant & 0x1fffu;
+  uint32_t m10 = mant >> 13;
+  int ee = e;
+  if (rem > 0x1000u || (rem == 0x1000u && (m10 & 1u))) {
+    if (++m10 == 0x400u) {
+      m10 = 0;
+      if (++ee >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+    }
+  }
+  return (uint16_t)(sign | ((uint32_t)ee << 10) | m10);
+}
+
+/* f64 -> f32 rounded to odd, so a second rounding to a 16-bit float is correct.
+ * crates/unpopped/src/oracle/expr_eval.rs:503-518 */
+float orc_f64_to_f32_odd(double f) {
+  const float r = (float)f;
+  if (!isfinite(f) || f == 0.0 || (double)r == f) return r;
+  uint32_t b = bits32(r);
+  if (fabs((double)r) > fabs(f)) b -= 1; /* step back toward zero */
+  return from32(b | 1u);
+}
+
+/* Storing an f64 compute value into a Bf16 buffer.  expr_eval.rs:520-527 (encode_float) */
+uint16_t orc_store_bf16(double v) { return orc_f32_to_bf16_bits(orc_f64_to_f32_odd(v)); }
+
+void orc_f32_to_bf16_array(const float* x, int64_t n, uint16_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_f32_to_bf16_bits(x[i]);
+}
+void orc_f16_to_f64_array(const uint16_t* h, int64_t n, double* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_f16_to_f64(h[i]);
+}
+
+/* ======================================================================================
+ * Sub-byte elements: two per byte, element i in byte i/2, low nibble = even index; U4
+ * zero-extends, I4 sign-extends.  crates/unpopped/src/cfamily.rs:446-475,
+ * crates/unpopped-cpu-c/src/kernel.rs:515-536
+ * ==================================================================================== */
+int32_t orc_u4_load(const uint8_t* p, int64_t i) { return (int32_t)((p[i >> 1] >> ((i & 1) * 4)) & 15u); }
+int32_t orc_i4_load(const uint8_t* p, int64_t i) {
+  const int32_t n = orc_u4_load(p, i);
+  return n >= 8 ? n - 16 : n;
+}
+void orc_sub4_store(uint8_t* p, int64_t i, int32_t v) {
+  const uint8_t nib = (uint8_t)(v & 15);
+  uint8_t* b = &p[i >> 1];
+  *b = (i & 1) ? (uint8_t)((*b & 0x0f) | (nib << 4)) : (uint8_t)((*b & 0xf0) | nib);
+}
+
+/* ======================================================================================
+ * Reductions: lift_reduction_opdef's order (crates/unpopped/src/kernel_lift.rs:447-484,
+ * ReductionShape :838-1025): per kept row, the reduced elements ascending into an
+ * accumulator (f64 for a float, the dtype itself for an integer), Max/Min with a `have` flag
+ * that keeps a NaN once seen (extremum_step :1097-1160), Mean divides by the reduced extent,
+ * and one cast down at the store (:965-983).  An empty fold stores the starting value.
+ * ==================================================================================== */
+
+static double fold_f64(int op, double acc, double v, int* have) {
+  switch (op) {
+    case ORC_SUM:
+    case ORC_MEAN:
+      return acc + v;
+    case ORC_PROD:
+      return acc * v;
+    case ORC_MAX:
+    case ORC_MIN: {
+      double r = acc;
+      if (!*have) r = v;
+      else if (v != v) r = v;
+      else if (op == ORC_MAX ? v > acc : v < acc) r = v;
+      *have = 1;
+      return r;
+    }
+  }
+  return acc;
+}
+
+static double row_fold_f64(const double* xs, int64_t n, int op) {
+  double acc = (op == ORC_PROD) ? 1.0 : 0.0;
+  int have = 0;
+  for (int64_t i = 0; i < n; ++i) acc = fold_f64(op, acc, xs[i], &have);
+  if (op == ORC_MEAN) acc = acc / (double)n;
+  return acc;
+}
+
+void orc_reduce_rows_f32(const float* in, int64_t rows, int64_t cols, int op, float* out) {
+  double* tmp = (double*)malloc((size_t)(cols > 0 ? cols : 1) * sizeof(double));
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t c = 0; c < cols; ++c) tmp[c] = (double)in[r * cols + c];
+    out[r] = (float)row_fold_f64(tmp, cols, op);
+  }
+  free(tmp);
+}
+
+void orc_reduce_rows_f64(const double* in, int64_t rows, int64_t cols, int op, double* out) {
+  for (int64_t r = 0; r < rows; ++r) out[r] = row_fold_f64(in + r * cols, cols, op);
+}
+
+/* Integers fold exactly at their own width, wrapping (kernel_lift.rs:883-889). */
+#define INT_REDUCE(NAME, T, U)                                                       \
+  void NAME(const T* in, int64_t rows, int64_t cols, int op, T* out) {             \
+    for (int64_t r = 0; r < rows; ++r) {                                           \
+      U acc = (op == ORC_PROD) ? 1u : 0u;                                          \
+      int have = 0;                                                                \
+      for (int64_t c = 0; c < cols; ++c) {                                         \
+        const T v = in[r * cols + c];                                              \
+        if (op == ORC_SUM) acc = acc + (U)v;                                       \
+        else if (op == ORC_PROD) acc = acc * (U)v;                                 \
+        else if (!have || (op == ORC_MAX ? v > (T)acc : v < (T)acc)) acc = (U)v;   \
+        have = 1;                                                                  \
+      }                                                                            \
+      out[r] = (T)acc;                                                             \
+    }                                                                              \
+  }
+INT_REDUCE(orc_reduce_rows_i32, int32_t, uint32_t)
+INT_REDUCE(orc_reduce_rows_i64, int64_t, uint64_t)
+
+/* The launched lift's float Sum order (kernel_lift/block_reduce.rs:14-24, Fold::rounds
+ * :207-220): thread t folds xs[t], xs[t+B], ... from 0 in f64; then acc[t] += acc[t+s] for
+ * s = B/2 .. 1; thread 0's total (divided by n for Mean).  Unrounded. */
+double orc_sum_launched_order(const double* xs, int64_t n, int64_t block, int mean) {
+  double* acc = (double*)calloc((size_t)block, sizeof(double));
+  for (int64_t t = 0; t < block; ++t)
+    for (int64_t i = t; i < n; i += block) acc[t] = acc[t] + xs[i];
+  for (int64_t s = block / 2; s > 0; s /= 2)
+    for (int64_t t = 0; t < s; ++t) acc[t] = acc[t] + acc[t + s];
+  const double total = mean ? acc[0] / (double)n : acc[0];
+  free(acc);
+  return total;
+}
+
+/* Neumaier's compensated sum, the near-exact reference of the bound test
+ * (crates/unpopped/tests/kernel_parallel_reduction_float_sum_bound.rs:171-186). */
+double orc_neumaier(const double* xs, int64_t n) {
+  double s = 0.0, c = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    const double x = xs[i];
+    const double t = s + x;
+    c += (fabs(s) >= fabs(x)) ? (s - t) + x : (x - t) + s;
+    s = t;
+  }
+  return s + c;
+}
+
+/* The declared bound on a Sum/Mean result `got`: gamma_(n-1) * sum|x| (scaled for Mean),
+ * half an ulp of the f32 rounding, and 4u |exact| for the reference sum's own error
+ * (kernel_parallel_reduction_float_sum_bound.rs:188-214; the statement of the bound is
+ * kernel_lift/block_reduce.rs:14-24). */
+double orc_sum_bound(const double* xs, int64_t n, int mean, int f32, double got) {
+  const double u = ldexp(1.0, -53);
+  const double k = n > 1 ? (double)(n - 1) : 0.0;
+  const double gamma = k * u / (1.0 - k * u);
+  double sum_abs = 0.0;
+  for (int64_t i = 0; i < n; ++i) sum_abs += fabs(xs[i]);
+  const double scale = mean ? 1.0 / (double)n : 1.0;
+  double rounding = 0.0;
+  if (f32) {
+    const uint32_t b = bits32(fabsf((float)got));
+    rounding = 0.5 * ((double)from32(b + 1) - (double)from32(b));
+  }
+  return gamma * sum_abs * scale + rounding + 4.0 * u * fabs(orc_neumaier(xs, n)) * scale;
+}
+
+/* ======================================================================================
+ * Scans: lift_scan_opdef's order (kernel_lift.rs:504-753): per row the prefix starts at the
+ * monoid identity (0, 1, -inf/+inf, or the integer extremes: scan_identity :712-753), each
+ * element is folded in (f64 for a float, wrapping for an integer), and the prefix is written
+ * after the fold (inclusive) or before it (exclusive), walking the row descending for a
+ * reverse scan; one cast down per written element.  A Mean scan writes acc / count.
+ * ==================================================================================== */
+
+static double scan_identity_f64(int op) {
+  switch (op) {
+    case ORC_PROD: return 1.0;
+    case ORC_MAX: return -INFINITY;
+    case ORC_MIN: return INFINITY;
+    default: return 0.0;
+  }
+}
+
+static void scan_row_f64(const double* x, int64_t n, int op, int excl, int rev, double* prefix_out) {
+  double acc = scan_identity_f64(op);
+  int have = 0;
+  int64_t count = 0; /* a running Mean divides by the elements folded so far (0/0 first) */
+  for (int64_t s = 0; s < n; ++s) {
+    const int64_t i = rev ? n - 1 - s : s;
+    if (excl) prefix_out[i] = (op == ORC_MEAN) ? acc / (double)count : acc;
+    acc = fold_f64(op, acc, x[i], &have);
+    ++count;
+    if (!excl) prefix_out[i] = (op == ORC_MEAN) ? acc / (double)count : acc;
+  }
+}
+
+void orc_scan_rows_f64(const double* in, int64_t rows, int64_t cols, int op, int exclusive, int reverse, double* out) {
+  for (int64_t r = 0; r < rows; ++r) scan_row_f64(in + r * cols, cols, op, exclusive, reverse, out + r * cols);
+}
+
+void orc_scan_rows_f32(const float* in, int64_t rows, int64_t cols, int op, int exclusive, int reverse, float* out) {
+  const size_t n = (size_t)(cols > 0 ? cols : 1);
+  double* x = (double*)malloc(n * sizeof(double));
+  double* p = (double*)malloc(n * sizeof(double));
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t c = 0; c < cols; ++c) x[c] = (double)in[r * cols + c];
+    scan_row_f64(x, cols, op, exclusive, reverse, p);
+    for (int64_t c = 0; c < cols; ++c) out[r * cols + c] = (float)p[c];
+  }
+  free(x);
+  free(p);
+}
+
+#define INT_SCAN(NAME, T, U, LO, HI)                                                  \
+  void NAME(const T* in, int64_t rows, int64_t cols, int op, int excl, int rev, T* out) { \
+    for (int64_t r = 0; r < rows; ++r) {                                              \
+      U acc = (op == ORC_PROD) ? 1u : (op == ORC_MAX ? (U)(LO) : (op == ORC_MIN ? (U)(HI) : 0u)); \
+      int have = 0;                                                                   \
+      for (int64_t s = 0; s < cols; ++s) {                                            \
+        const int64_t i = rev ? cols - 1 - s : s;                                     \
+        const T v = in[r * cols + i];                                                 \
+        if (excl) out[r * cols + i] = (T)acc;                                         \
+        if (op == ORC_SUM) acc = acc + (U)v;                                          \
+        else if (op == ORC_PROD) acc = acc * (U)v;                                    \
+        else if (!have || (op == ORC_MAX ? v > (T)acc : v < (T)acc)) acc = (U)v;      \
+        have = 1;                                                                     \
+        if (!excl) out[r * cols + i] = (T)acc;                                        \
+      }                                                                               \
+    }                                                                                 \
+  }
+INT_SCAN(orc_scan_rows_i32, int32_t, uint32_t, INT32_MIN, INT32_MAX)
+INT_SCAN(orc_scan_rows_i64, int64_t, uint64_t, INT64_MIN, INT64_MAX)
+
+/* The launched scan's order for an f32 Sum row (kernel_lift/scan_launched.rs:1-26):
+ * c = ceil(n / B); thread t folds scan positions [t*c, min(t*c + c, n)); a Kogge-Stone scan
+ * over the B totals (total[t] = total[t] + total[t - d], own value on the left, old values);
+ * thread t re-walks its chunk from total[t - 1] (the identity for t = 0). */
+void orc_scan_launched_order_f32(const float* in, int64_t n, int64_t block, int exclusive, int reverse, float* out) {
+  int64_t c = 0;
+  while (c * block < n) ++c;
+  double* tot = (double*)calloc((size_t)block, sizeof(double));
+  double* old = (double*)calloc((size_t)block, sizeof(double));
+  for (int64_t t = 0; t < block; ++t) {
+    const int64_t lo = t * c, hi = lo + c < n ? lo + c : n;
+    for (int64_t p = lo; p < hi; ++p) tot[t] = tot[t] + (double)in[reverse ? n - 1 - p : p];
+  }
+  for (int64_t d = 1; d < block; d *= 2) {
+    memcpy(old, tot, (size_t)block * sizeof(double));
+    for (int64_t t = d; t < block; ++t) tot[t] = old[t] + old[t - d];
+  }
+  for (int64_t t = 0; t < block; ++t) {
+    double acc = t == 0 ? 0.0 : tot[t - 1];
+    const int64_t lo = t * c, hi = lo + c < n ? lo + c : n;
+    for (int64_t p = lo; p < hi; ++p) {
+      const int64_t i = reverse ? n - 1 - p : p;
+      if (exclusive) out[i] = (float)acc;
+      acc = acc + (double)in[i];
+      if (!exclusive) out[i] = (float)acc;
+    }
+  }
+  free(tot);
+  free(old);
+}
+
+/* ======================================================================================
+ * Gather (crates/unpopped/src/kernel_lift/gather.rs:184-232): load the index once, clamp the
+ * load address into [0, extent - 1] at the index dtype, then apply the policy to the store:
+ * Skip leaves the row, ZeroFill writes zero, Clamp stores the clamped row.  The move is a raw
+ * bit copy (oracle/expr_eval.rs:480-485: a Raw value of the output's dtype moves verbatim).
+ * ==================================================================================== */
+void orc_gather_rows(const uint8_t* table, int64_t src_extent, int64_t row_bytes, const void* ids, int idx_kind,
+                     int64_t n_rows, int policy, uint8_t* out) {
+  for (int64_t r = 0; r < n_rows; ++r) {
+    int below = 0, above = 0;
+    int64_t clamped = 0;
+    if (idx_kind == ORC_IDX_U32) {
+      const uint32_t raw = ((const uint32_t*)ids)[r];
+      const uint32_t last = (uint32_t)src_extent - 1u;
+      above = !(raw < (uint32_t)src_extent);
+      clamped = (int64_t)(raw < last ? raw : last);
+    } else {
+      const int64_t raw = idx_kind == ORC_IDX_I32 ? (int64_t)((const int32_t*)ids)[r] : ((const int64_t*)ids)[r];
+      below = raw < 0;
+      above = raw >= src_extent;
+      const int64_t lo = raw > 0 ? raw : 0;
+      clamped = lo < src_extent - 1 ? lo : src_extent - 1;
+    }
+    uint8_t* dst = out + r * row_bytes;
+    if (below || above) {
+      if (policy == ORC_SKIP) continue;
+      if (policy == ORC_ZEROFILL) {
+        memset(dst, 0, (size_t)row_bytes);
+        continue;
+      }
+    }
+    if (clamped < 0 || clamped >= src_extent) continue; /* an empty source: nothing to read */
+    memcpy(dst, table + clamped * row_bytes, (size_t)row_bytes);
+  }
+}
+
+/* ======================================================================================
+ * Sub-byte dequant: the KernelFn chain Load U4/I4 -> Cast I32 (zero/sign extend, widen to an
+ * integer first: crates/unpopped/tests/kernel_subbyte_load.rs:206-212) -> Sub zero (exact) ->
+ * Cast F32 -> Mul scale (F16 decoded exactly) -> store Bf16 (f32_to_bf16_bits after the
+ * round-to-odd narrowing, expr_eval.rs:520-527).  Group g = column / group; the scale and the
+ * zero point of (row, g) are element row * ceil(cols / group) + g of their buffers.
+ * ==================================================================================== */
+void orc_dequant4_bf16(const uint8_t* q, int q_signed, const uint16_t* scale, const uint8_t* zero, int z_signed,
+                       int64_t rows, int64_t cols, int64_t group, uint16_t* out) {
+  const int64_t ng = (cols + group - 1) / group;
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t c = 0; c < cols; ++c) {
+      const int64_t e = r * cols + c;
+      const int64_t zi = r * ng + c / group;
+      const int32_t qv = q_signed ? orc_i4_load(q, e) : orc_u4_load(q, e);
+      const int32_t zv = z_signed ? orc_i4_load(zero, zi) : orc_u4_load(zero, zi);
+      const float d = (float)(qv - zv);
+      const double v = (double)d * orc_f16_to_f64(scale[zi]);
+      out[e] = orc_store_bf16(v);
+    }
+  }
+}

@@ -1,0 +1,66 @@
+/*
+ * CPU oracle for the unpopped-hip hot path.  TEST INFRASTRUCTURE ONLY: the parity tests, the
+ * smoke check and the benchmark's CPU-baseline leg call it as the checker.  No product code
+ * links or calls it.
+ *
+ * A plain-C restatement of the reference's semantics for the forms the HIP backend lowers
+ * (EvansLaboratories/Unpopped 0.56.5, Rust, which has no toolchain here and cannot be
+ * built or imported).  Each function cites the reference file:line it follows; the pinning
+ * of each one (golden vectors, closed forms, library routines, brute force) lives in
+ * tests/test_oracle.py.
+ */
+#ifndef UNPOPPED_ORACLE_H
+#define UNPOPPED_ORACLE_H
+
+#include <stdint.h>
+
+/* ReduceOp subset and OobPolicy codes (as include/unpopped_hip.h). */
+enum { ORC_SUM = 0, ORC_PROD = 1, ORC_MAX = 2, ORC_MIN = 3, ORC_MEAN = 4 };
+enum { ORC_SKIP = 0, ORC_ZEROFILL = 1, ORC_CLAMP = 2 };
+enum { ORC_IDX_I32 = 9, ORC_IDX_I64 = 10, ORC_IDX_U32 = 23 };
+
+/* ---- codecs ------------------------------------------------------------------------- */
+uint16_t orc_f32_to_bf16_bits(float x);
+double orc_bf16_to_f64(uint16_t b);
+double orc_f16_to_f64(uint16_t h);
+uint16_t orc_f32_to_f16_bits(float x);
+float orc_f64_to_f32_odd(double f);
+uint16_t orc_store_bf16(double v);
+void orc_f32_to_bf16_array(const float* x, int64_t n, uint16_t* out);
+void orc_f16_to_f64_array(const uint16_t* h, int64_t n, double* out);
+
+/* ---- sub-byte ------------------------------------------------------------------------ */
+int32_t orc_u4_load(const uint8_t* p, int64_t i);
+int32_t orc_i4_load(const uint8_t* p, int64_t i);
+void orc_sub4_store(uint8_t* p, int64_t i, int32_t v);
+
+/* ---- reductions (serial lift order) --------------------------------------------------- */
+void orc_reduce_rows_f32(const float* in, int64_t rows, int64_t cols, int op, float* out);
+void orc_reduce_rows_f64(const double* in, int64_t rows, int64_t cols, int op, double* out);
+void orc_reduce_rows_i32(const int32_t* in, int64_t rows, int64_t cols, int op, int32_t* out);
+void orc_reduce_rows_i64(const int64_t* in, int64_t rows, int64_t cols, int op, int64_t* out);
+/* The launched lift's documented order for one row of floats (Sum/Mean): thread t of `block`
+ * folds elements t, t+block, ... in f64, then the tree; one rounding at the end. */
+double orc_sum_launched_order(const double* xs, int64_t n, int64_t block, int mean);
+/* The declared bound on a float Sum/Mean row result `got` (stored at f32 when f32 != 0). */
+double orc_sum_bound(const double* xs, int64_t n, int mean, int f32, double got);
+double orc_neumaier(const double* xs, int64_t n);
+
+/* ---- scans (serial lift order) -------------------------------------------------------- */
+void orc_scan_rows_f32(const float* in, int64_t rows, int64_t cols, int op, int exclusive, int reverse, float* out);
+void orc_scan_rows_f64(const double* in, int64_t rows, int64_t cols, int op, int exclusive, int reverse, double* out);
+void orc_scan_rows_i32(const int32_t* in, int64_t rows, int64_t cols, int op, int exclusive, int reverse, int32_t* out);
+void orc_scan_rows_i64(const int64_t* in, int64_t rows, int64_t cols, int op, int exclusive, int reverse, int64_t* out);
+/* The launched scan's three-phase order for one row of f32 Sum (chunk c = ceil(n/block)). */
+void orc_scan_launched_order_f32(const float* in, int64_t n, int64_t block, int exclusive, int reverse, float* out);
+
+/* ---- gather ------------------------------------------------------------------------- */
+/* out[r, :] = table[clamp(ids[r]), :] (rows of row_bytes raw bytes) under the policy. */
+void orc_gather_rows(const uint8_t* table, int64_t src_extent, int64_t row_bytes, const void* ids, int idx_kind,
+                     int64_t n_rows, int policy, uint8_t* out);
+
+/* ---- sub-byte dequant ----------------------------------------------------------------- */
+void orc_dequant4_bf16(const uint8_t* q, int q_signed, const uint16_t* scale, const uint8_t* zero, int z_signed,
+                       int64_t rows, int64_t cols, int64_t group, uint16_t* out);
+
+#endif

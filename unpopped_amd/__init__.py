@@ -1,0 +1,251 @@
+"""unpopped-hip: the MI355X (gfx950) backend for the Unpopped kernel generator.
+
+The host side mirrors the reference's two seams over the C ABI (``include/unpopped_hip.h``):
+
+* :class:`HipBackend` is ``trait Backend`` (crates/unpopped/src/backend.rs:668-807);
+* :class:`HipCompiler` is ``trait Compiler`` (crates/unpopped/src/jit.rs:271-285);
+* :class:`Executor` and :class:`DeviceBuffer` are the consumer's launch layer, which the
+  reference leaves out by rule and this backend provides as a thin FFI over the HIP runtime.
+
+Nothing here computes on the CPU: every result comes from a HIP kernel, and a missing
+library raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import json
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import UnpError, check
+
+ELEMENT_KINDS = {
+    "F16": 0, "Bf16": 1, "F32": 2, "F32Strict": 3, "F64": 4, "I8": 5, "I16": 6, "U8": 7,
+    "U16": 8, "I32": 9, "I64": 10, "Bool": 11, "Fp8E4M3FN": 12, "Fp8E4M3FNUZ": 13,
+    "Fp8E5M2": 14, "F8E8M0": 15, "F8E6M2": 16, "Fp8E5M2FNUZ": 17, "I4": 18, "U4": 19, "B1": 20,
+    "Complex64": 21, "Complex128": 22, "U32": 23, "U64": 24, "F4E2M1": 25, "F6E2M3": 26,
+    "F6E3M2": 27,
+}
+REDUCE_OPS = {"Sum": 0, "Prod": 1, "Max": 2, "Min": 3, "Mean": 4}
+OOB_POLICIES = {"Skip": 0, "ZeroFill": 1, "Clamp": 2}
+FORMS = {"reduction": 0, "scan": 1, "gather": 2, "dequant4": 3, "row_reduce2": 4}
+DTYPE_SUPPORT = {0: "Supported", 1: "Unsupported", 2: "NotExpressible"}
+ARTIFACT_KINDS = {0: "Ptx", 1: "Cubin", 2: "HipCodeObject", 3: "SpirV", 4: "Stub"}
+
+
+@dataclass
+class GeneratedKernel:
+    """``GeneratedKernel`` (backend.rs:105-193): name, source text and launch interface."""
+
+    name: str
+    source: str
+    interface: dict
+    _handle: C.c_void_p
+
+    def revision_hash(self) -> int:
+        """FNV-1a 64 over the source (crates/unpopped/src/revision.rs)."""
+        return int(_lib.lib().unp_generated_revision_hash(self._handle))
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h:
+            _lib.lib().unp_generated_free(h)
+            self._handle = None
+
+
+class HipBackend:
+    """The ``Backend`` seam for ``rocm:gfx950``."""
+
+    def name(self) -> str:
+        return _lib.lib().unp_hip_name().decode()
+
+    def provider(self) -> str:
+        return _lib.lib().unp_hip_provider().decode()
+
+    def total_integer_ops(self) -> bool:
+        return bool(_lib.lib().unp_hip_total_integer_ops())
+
+    def supports_dtype(self, dtype: str, target: str) -> str:
+        return DTYPE_SUPPORT[_lib.lib().unp_hip_supports_dtype(ELEMENT_KINDS[dtype], target.encode())]
+
+    def lower_form(self, kind: str, dtype: str = "F32", rank: int = 1, op: str = "Sum",
+                   op1: str = "Max", reduced_from: int | None = None, exclusive: bool = False,
+                   reverse: bool = False, index_dtype: str = "I32", oob: str = "ZeroFill",
+                   data_slot: int = 0, q_kind: str = "U4", z_kind: str = "U4", group: int = 128,
+                   out_kind: str = "Bf16") -> GeneratedKernel:
+        f = _lib.Form()
+        f.kind = FORMS[kind]
+        f.dtype = ELEMENT_KINDS[dtype]
+        f.rank = rank
+        f.op0 = REDUCE_OPS[op]
+        f.op1 = REDUCE_OPS[op1]
+        f.reduced_from = (rank - 1) if reduced_from is None else reduced_from
+        f.exclusive = int(exclusive)
+        f.reverse = int(reverse)
+        f.index_dtype = ELEMENT_KINDS[index_dtype]
+        f.oob = OOB_POLICIES[oob]
+        f.data_slot = data_slot
+        f.q_kind = ELEMENT_KINDS[q_kind]
+        f.z_kind = ELEMENT_KINDS[z_kind]
+        f.group = group
+        f.out_kind = ELEMENT_KINDS[out_kind]
+        return self._wrap(lambda out, err: _lib.lib().unp_hip_lower_form(C.byref(f), out, err))
+
+    @staticmethod
+    def _wrap(call) -> GeneratedKernel:
+        L = _lib.lib()
+        out = C.c_void_p()
+        err = _lib.Error()
+        check(call(C.byref(out), C.byref(err)), err)
+        return GeneratedKernel(
+            name=L.unp_generated_name(out).decode(),
+            source=L.unp_generated_source(out).decode(),
+            interface=json.loads(L.unp_generated_interface_json(out).decode()),
+            _handle=out,
+        )
+
+
+class HipCompiler:
+    """The ``Compiler`` seam: hipRTC for gfx950, artifacts are HIP code objects."""
+
+    def compile(self, source: str, entry: str, max_compile_ms: int = 0) -> bytes:
+        L = _lib.lib()
+        data = C.POINTER(C.c_uint8)()
+        n = C.c_size_t()
+        diag = C.c_void_p()
+        rc = L.unp_hip_compile(source.encode(), entry.encode(), max_compile_ms, C.byref(data),
+                               C.byref(n), C.byref(diag))
+        log = C.string_at(diag).decode(errors="replace") if diag.value else ""
+        if diag.value:
+            L.unp_free_str(diag)
+        if rc != _lib.OK:
+            raise UnpError(rc, log)
+        try:
+            return C.string_at(data, n.value)
+        finally:
+            L.unp_free_bytes(data)
+
+    def artifact_kind(self) -> str:
+        return ARTIFACT_KINDS[_lib.lib().unp_hip_artifact_kind()]
+
+
+def device_count() -> int:
+    n = C.c_int32()
+    _lib.lib().unp_hip_device_count(C.byref(n))
+    return int(n.value)
+
+
+def device_info() -> tuple[str, int]:
+    arch = C.create_string_buffer(128)
+    cus = C.c_int32()
+    check(_lib.lib().unp_hip_device_info(arch, 128, C.byref(cus)), what="unp_hip_device_info")
+    return arch.value.decode(), int(cus.value)
+
+
+def synchronize() -> None:
+    check(_lib.lib().unp_hip_synchronize(), what="hipDeviceSynchronize")
+
+
+class DeviceBuffer:
+    """Device memory from ``hipMalloc``, with host copies through numpy arrays."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        check(_lib.lib().unp_hip_malloc(C.byref(p), self.nbytes), what=f"hipMalloc({nbytes})")
+        self.ptr = int(p.value)
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(max(a.nbytes, 1))
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        if a.nbytes:
+            check(_lib.lib().unp_hip_memcpy_h2d(self.ptr, a.ctypes.data, a.nbytes), what="hipMemcpy H2D")
+
+    def download(self, dtype, count: int) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        if out.nbytes:
+            check(_lib.lib().unp_hip_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes), what="hipMemcpy D2H")
+        return out
+
+    def fill(self, byte: int) -> None:
+        check(_lib.lib().unp_hip_memset(self.ptr, byte, self.nbytes), what="hipMemset")
+
+    def free(self) -> None:
+        if self.ptr:
+            _lib.lib().unp_hip_free(self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Executor:
+    """A lowered kernel compiled, loaded and ready to launch on the current device."""
+
+    def __init__(self, kernel: GeneratedKernel):
+        self.kernel = kernel
+        h = C.c_void_p()
+        err = _lib.Error()
+        check(_lib.lib().unp_hip_exec_create(kernel._handle, C.byref(h), C.byref(err)), err)
+        self._h = h
+
+    def launch(self, *args, stream: int = 0) -> None:
+        """Arguments in the KernelFn's parameter order: buffers, then integer scalars."""
+        arr = (_lib.Arg * len(args))()
+        for i, a in enumerate(args):
+            if isinstance(a, DeviceBuffer):
+                arr[i].is_buffer, arr[i].value = 1, a.ptr
+            else:
+                arr[i].is_buffer, arr[i].value = 0, int(a) & 0xFFFFFFFFFFFFFFFF
+        err = _lib.Error()
+        check(_lib.lib().unp_hip_exec_launch(self._h, arr, len(args), stream, C.byref(err)), err)
+
+    def last_launch(self) -> dict:
+        g = (C.c_uint32 * 3)()
+        b = (C.c_uint32 * 3)()
+        name = C.create_string_buffer(256)
+        _lib.lib().unp_hip_exec_last_launch(self._h, g, b, name, 256)
+        return {"grid": list(g), "block": list(b), "entry": name.value.decode()}
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.lib().unp_hip_exec_destroy(h)
+            self._h = None
+
+
+class Event:
+    def __init__(self):
+        h = C.c_void_p()
+        check(_lib.lib().unp_hip_event_create(C.byref(h)), what="hipEventCreate")
+        self._h = h
+
+    def record(self, stream: int = 0) -> None:
+        check(_lib.lib().unp_hip_event_record(self._h, stream), what="hipEventRecord")
+
+    def synchronize(self) -> None:
+        check(_lib.lib().unp_hip_event_synchronize(self._h), what="hipEventSynchronize")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        check(_lib.lib().unp_hip_event_elapsed_ms(self._h, end._h, C.byref(ms)), what="hipEventElapsedTime")
+        return float(ms.value)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.lib().unp_hip_event_destroy(h)
+            self._h = None

@@ -1,0 +1,480 @@
+// The HIP emitter: one lowered form -> kernel source (the device template library plus the
+// `extern "C"` entry points that instantiate it) and the launch interface as JSON.
+//
+// The emitted text is what GeneratedKernel::source carries (crates/unpopped/src/backend.rs
+// :105-125); the interface JSON carries the KernelInterface fields the launch needs
+// (crates/unpopped/src/kernel_interface.rs:200-237): launch geometry, parameters, entry
+// symbols, launch bounds, compiler arguments and fidelity notes.
+#include <sstream>
+
+#include "unp_internal.hpp"
+
+namespace unp {
+
+extern const char* const kDeviceLibrary;  // unp_device.hip, embedded at build time
+
+namespace {
+
+struct KindInfo {
+  int32_t kind;
+  const char* name;
+  size_t bytes;
+};
+
+const KindInfo kKinds[] = {
+    {UNP_F16, "F16", 2},       {UNP_BF16, "Bf16", 2},
+    {UNP_F32, "F32", 4},       {UNP_F32_STRICT, "F32Strict", 4},
+    {UNP_F64, "F64", 8},       {UNP_I8, "I8", 1},
+    {UNP_I16, "I16", 2},       {UNP_U8, "U8", 1},
+    {UNP_U16, "U16", 2},       {UNP_I32, "I32", 4},
+    {UNP_I64, "I64", 8},       {UNP_BOOL, "Bool", 1},
+    {UNP_FP8_E4M3FN, "Fp8E4M3FN", 1},   {UNP_FP8_E4M3FNUZ, "Fp8E4M3FNUZ", 1},
+    {UNP_FP8_E5M2, "Fp8E5M2", 1},       {UNP_F8_E8M0, "F8E8M0", 1},
+    {UNP_F8_E6M2, "F8E6M2", 1},         {UNP_FP8_E5M2FNUZ, "Fp8E5M2FNUZ", 1},
+    {UNP_I4, "I4", 0},         {UNP_U4, "U4", 0},
+    {UNP_B1, "B1", 0},         {UNP_COMPLEX64, "Complex64", 8},
+    {UNP_COMPLEX128, "Complex128", 16}, {UNP_U32, "U32", 4},
+    {UNP_U64, "U64", 8},       {UNP_F4_E2M1, "F4E2M1", 0},
+    {UNP_F6_E2M3, "F6E2M3", 0}, {UNP_F6_E3M2, "F6E3M2", 0},
+};
+
+const char* op_name(int32_t op) {
+  switch (op) {
+    case UNP_OP_SUM: return "sum";
+    case UNP_OP_PROD: return "prod";
+    case UNP_OP_MAX: return "max";
+    case UNP_OP_MIN: return "min";
+    case UNP_OP_MEAN: return "mean";
+    default: return nullptr;
+  }
+}
+
+const char* oob_name(int32_t p) {
+  switch (p) {
+    case UNP_OOB_SKIP: return "Skip";
+    case UNP_OOB_ZEROFILL: return "ZeroFill";
+    case UNP_OOB_CLAMP: return "Clamp";
+    default: return nullptr;
+  }
+}
+
+// The C++ element type the device library instantiates for a compute kind.
+const char* ctype(int32_t kind) {
+  switch (kind) {
+    case UNP_F32: return "float";
+    case UNP_F64: return "double";
+    case UNP_I32: return "int";
+    case UNP_I64: return "long long";
+    case UNP_U32: return "unsigned int";
+    default: return nullptr;
+  }
+}
+
+const char* lower_name(int32_t kind) {
+  switch (kind) {
+    case UNP_F32: return "f32";
+    case UNP_F64: return "f64";
+    case UNP_I32: return "i32";
+    case UNP_I64: return "i64";
+    case UNP_U32: return "u32";
+    case UNP_BF16: return "bf16";
+    case UNP_F16: return "f16";
+    case UNP_U4: return "u4";
+    case UNP_I4: return "i4";
+    default: return "x";
+  }
+}
+
+std::string json_str(const std::string& s) {
+  std::string o = "\"";
+  for (char c : s) {
+    if (c == '"' || c == '\\') {
+      o += '\\';
+      o += c;
+    } else if (c == '\n') {
+      o += "\\n";
+    } else {
+      o += c;
+    }
+  }
+  return o + "\"";
+}
+
+// The folds the reduction forms accept: those of lift_reduction_opdef_launched
+// (crates/unpopped/src/kernel_lift/block_reduce.rs:97-133) at F32/F64/I32/I64
+// (kernel_lift.rs:763-803): float Sum/Mean/Max/Min, integer Sum/Prod/Max/Min.
+bool reduction_ok(int32_t dtype, int32_t op, std::string& why) {
+  if (!ctype(dtype) || dtype == UNP_U32) {
+    why = "a reduction outside F32, F64, I32 and I64";
+    return false;
+  }
+  if (!op_name(op)) {
+    why = "a reduce op this backend has no fold for";
+    return false;
+  }
+  const bool is_int = kind_is_int(dtype);
+  if (is_int && op == UNP_OP_MEAN) {
+    why = "an integer Mean";
+    return false;
+  }
+  if (!is_int && op == UNP_OP_PROD) {
+    why = "a float Prod in a launched reduction (not order-independent, and no declared bound)";
+    return false;
+  }
+  return true;
+}
+
+int vec_of(int32_t dtype) { return 16 / (int)kind_bytes(dtype); }
+
+std::string header(const std::string& name, const unp_form& f) {
+  std::ostringstream s;
+  s << "// unpopped-hip kernel `" << name << "` for rocm:gfx950 (form " << f.kind << ").\n";
+  s << kDeviceLibrary << "\n";
+  return s.str();
+}
+
+const char* kLaunchBounds = "__launch_bounds__(256)";
+
+}  // namespace
+
+const char* kind_name(int32_t kind) {
+  for (const auto& k : kKinds)
+    if (k.kind == kind) return k.name;
+  return nullptr;
+}
+
+int32_t kind_from_name(const std::string& s) {
+  for (const auto& k : kKinds)
+    if (s == k.name) return k.kind;
+  return -1;
+}
+
+size_t kind_bytes(int32_t kind) {
+  for (const auto& k : kKinds)
+    if (k.kind == kind) return k.bytes;
+  return 0;
+}
+
+bool kind_is_float(int32_t kind) {
+  return kind == UNP_F32 || kind == UNP_F64 || kind == UNP_F16 || kind == UNP_BF16 ||
+         kind == UNP_F32_STRICT;
+}
+bool kind_is_int(int32_t kind) {
+  return kind == UNP_I32 || kind == UNP_I64 || kind == UNP_U32 || kind == UNP_I8 ||
+         kind == UNP_I16 || kind == UNP_U8 || kind == UNP_U16 || kind == UNP_U64;
+}
+
+uint64_t fnv1a64(const std::string& s) {
+  uint64_t h = 0xcbf29ce484222325ull;
+  for (unsigned char c : s) {
+    h ^= c;
+    h *= 0x00000100000001b3ull;
+  }
+  return h;
+}
+
+void set_error(unp_error* err, int32_t code, const std::string& detail) {
+  if (!err) return;
+  err->code = code;
+  std::snprintf(err->detail, sizeof(err->detail), "%s", detail.c_str());
+}
+
+static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) {
+  const bool two = f.kind == UNP_FORM_ROW_REDUCE2;
+  if (f.rank < 1 || f.rank > 8) {
+    why = "rank is zero or more than 8";
+    return UNP_LIFT_DECLINE;
+  }
+  if (f.reduced_from < 0 || f.reduced_from >= f.rank) {
+    why = "the reduced axes must be a trailing run of axes (the last axis at least)";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (!reduction_ok(f.dtype, f.op0, why) || (two && !reduction_ok(f.dtype, f.op1, why)))
+    return UNP_UNSUPPORTED_KERNEL;
+  const char* T = ctype(f.dtype);
+  const int V = vec_of(f.dtype);
+  L.reduce_all = (f.reduced_from == 0) && !two;
+  std::ostringstream name;
+  name << (L.reduce_all ? "unp_reduce_all_" : "unp_rowreduce_") << op_name(f.op0);
+  if (two) name << "_" << op_name(f.op1);
+  name << "_" << lower_name(f.dtype);
+  L.name = name.str();
+  std::ostringstream src;
+  src << header(L.name, f);
+  for (int fast = 1; fast >= 0; --fast) {
+    Entry e;
+    e.fast = fast;
+    e.vec = fast ? V : 1;
+    e.symbol = L.name + (fast ? "_v" : "_s");
+    const int unroll = fast ? 4 : 8;
+    if (L.reduce_all) {
+      L.blocks_per_cu = 4;
+      src << "extern \"C\" __global__ void " << kLaunchBounds << " " << e.symbol << "(const " << T
+          << "* in, " << T << "* out, long long n, typename unp::acc<" << T << ", " << f.op0
+          << ">::type* partials, unsigned* counter) {\n  unp::reduce_all<" << T << ", " << f.op0
+          << ", " << e.vec << ", 256, " << unroll << ">(in, out, n, partials, counter);\n}\n";
+    } else {
+      L.blocks_per_cu = 8;
+      src << "extern \"C\" __global__ void " << kLaunchBounds << " " << e.symbol << "(const " << T
+          << "* in, " << T << "* out0, " << T << "* out1, long long rows, long long cols) {\n"
+          << "  unp::rowreduce<" << T << ", " << f.op0 << ", " << (two ? f.op1 : f.op0) << ", "
+          << (two ? 2 : 1) << ", " << e.vec << ", 256, " << unroll
+          << ">(in, out0, out1, rows, cols);\n}\n";
+    }
+    L.entries.push_back(e);
+  }
+  L.source = src.str();
+  std::ostringstream j;
+  j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":"
+    << (two ? "\"row_reduce2\"" : "\"reduction\"") << ",\"dtype\":\"" << kind_name(f.dtype)
+    << "\",\"ops\":[\"" << op_name(f.op0) << "\"" << (two ? std::string(",\"") + op_name(f.op1) + "\"" : "")
+    << "],\"rank\":" << f.rank << ",\"reduced_axes_from\":" << f.reduced_from
+    << ",\"params\":[{\"name\":\"in0\",\"kind\":\"buffer\",\"role\":\"Read\"},"
+    << (two ? "{\"name\":\"out0\",\"kind\":\"buffer\",\"role\":\"Write\"},{\"name\":\"out1\",\"kind\":\"buffer\",\"role\":\"Write\"}"
+            : "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}");
+  for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
+  j << "],\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
+    << "\",\"grid_policy\":\"device-class constant; "
+    << (L.reduce_all ? "blocks stride over 16-byte vectors, last-ticket block folds the partials"
+                     : "blocks stride over rows")
+    << "\"},\"entries\":[";
+  for (size_t i = 0; i < L.entries.size(); ++i)
+    j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
+      << ",\"when\":\"" << (L.entries[i].fast ? "reduced extent % vec == 0 and in0 16-byte aligned" : "otherwise")
+      << "\"}";
+  j << "],\"workspace\":"
+    << (L.reduce_all ? "{\"partials\":\"grid * accumulator bytes\",\"counter\":4}" : "null")
+    << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
+    << ",\"fidelity_notes\":["
+    << json_str(kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN || (two && (f.op1 == UNP_OP_SUM || f.op1 == UNP_OP_MEAN)))
+                    ? "float Sum/Mean: f64 accumulation in an order fixed by (grid, block=256, vector width); "
+                      "within the declared bound gamma_(n-1)*sum|x| + 1/2 ulp, not the KernelFn's (block, grid) order"
+                    : "order-independent fold: bit-exact against the serial kernel except NaN payload and the sign of a zero in Max/Min")
+    << "," << json_str("the launch geometry is the device's (cu_count x blocks), not the KernelFn's LaunchShape")
+    << "]}";
+  L.interface_json = j.str();
+  return UNP_OK;
+}
+
+static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
+  if (f.rank < 1 || f.rank > 8) {
+    why = "rank is zero or more than 8";
+    return UNP_LIFT_DECLINE;
+  }
+  if (!ctype(f.dtype) || f.dtype == UNP_U32) {
+    why = "a scan outside F32, F64, I32 and I64";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (f.op0 != UNP_OP_SUM && f.op0 != UNP_OP_MAX && f.op0 != UNP_OP_MIN && f.op0 != UNP_OP_PROD) {
+    why = "a Mean scan in a launched scan (a running mean has no declared bound)";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (f.op0 == UNP_OP_PROD && kind_is_float(f.dtype)) {
+    why = "a float Prod scan in a launched scan (not order-independent, and no declared bound)";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  const char* T = ctype(f.dtype);
+  std::ostringstream name;
+  name << "unp_scan_" << (f.exclusive ? "excl_" : "incl_") << (f.reverse ? "rev_" : "") << op_name(f.op0)
+       << "_" << lower_name(f.dtype);
+  L.name = name.str();
+  L.blocks_per_cu = 4;
+  // Tile = 64 lanes x VEC x K.  An 8-byte carry (f32 Sum in f64, F64, I64) halves K to keep
+  // the per-lane registers (K vectors in flight plus K carries) within occupancy.
+  const bool wide_carry = (f.dtype == UNP_F32 && f.op0 == UNP_OP_SUM) || kind_bytes(f.dtype) == 8;
+  std::ostringstream src;
+  src << header(L.name, f);
+  for (int fast = 1; fast >= 0; --fast) {
+    Entry e;
+    e.fast = fast;
+    e.vec = fast ? vec_of(f.dtype) : 1;
+    e.k = fast ? (wide_carry ? 8 : 16) : (wide_carry ? 16 : 32);
+    e.symbol = L.name + (fast ? "_v" : "_s");
+    src << "extern \"C\" __global__ void " << kLaunchBounds << " " << e.symbol << "(const " << T
+        << "* in, " << T << "* out, long long rows, long long cols, unsigned long long* status, "
+        << "unsigned* counter, unsigned ticket_base, unsigned epoch) {\n  unp::scan_lookback<" << T << ", "
+        << f.op0 << ", " << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false")
+        << ", " << e.vec << ", " << e.k << ">(in, out, rows, cols, status, counter, ticket_base, epoch);\n}\n";
+    L.entries.push_back(e);
+  }
+  L.source = src.str();
+  std::ostringstream j;
+  j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"scan\",\"dtype\":\"" << kind_name(f.dtype)
+    << "\",\"op\":\"" << op_name(f.op0) << "\",\"exclusive\":" << (f.exclusive ? "true" : "false")
+    << ",\"reverse\":" << (f.reverse ? "true" : "false") << ",\"rank\":" << f.rank
+    << ",\"params\":[{\"name\":\"in0\",\"kind\":\"buffer\",\"role\":\"Read\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
+  for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
+  j << "],\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
+    << "\",\"grid_policy\":\"persistent waves draw tile tickets; one wave per tile\"},\"entries\":[";
+  for (size_t i = 0; i < L.entries.size(); ++i)
+    j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
+      << ",\"k\":" << L.entries[i].k << ",\"tile\":" << 64 * L.entries[i].vec * L.entries[i].k << ",\"when\":\""
+      << (L.entries[i].fast ? "scanned extent % vec == 0 and in0/out 16-byte aligned" : "otherwise") << "\"}";
+  j << "],\"workspace\":{\"status\":\"tiles * " << (wide_carry ? 32 : 16)
+    << " bytes, zeroed once\",\"counter\":4,\"host_state\":[\"epoch\",\"ticket_base\"]}"
+    << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
+    << ",\"fidelity_notes\":["
+    << json_str(kind_is_float(f.dtype) && f.op0 == UNP_OP_SUM
+                    ? "float Sum: every prefix is an f64 fold of the same elements in a different order (tile-local "
+                      "striped scan plus decoupled look-back); within the declared per-prefix bound "
+                      "gamma_(n-1)*sum|x| + 1/2 ulp; bit-equal whenever the f64 partial sums are exact"
+                    : "order-independent fold: bit-exact against the serial scan except NaN payload and the sign of a zero in Max/Min")
+    << "," << json_str("one single-pass decoupled look-back launch replaces the KernelFn's block-per-row three-phase schedule")
+    << "]}";
+  L.interface_json = j.str();
+  return UNP_OK;
+}
+
+static int32_t lower_gather(const unp_form& f, Lowered& L, std::string& why) {
+  if (f.rank < 1 || f.rank > 8) {
+    why = "a rank-0 gather has no loop";
+    return UNP_LIFT_DECLINE;
+  }
+  const size_t eb = kind_bytes(f.dtype);
+  if (eb == 0) {
+    why = "a gather of a sub-byte or unknown element kind";
+    return UNP_UNSUPPORTED_DTYPE;
+  }
+  if (f.index_dtype != UNP_I32 && f.index_dtype != UNP_I64 && f.index_dtype != UNP_U32) {
+    why = "a non-integer gather index";
+    return UNP_LIFT_DECLINE;
+  }
+  if (!oob_name(f.oob)) {
+    why = "an unknown out-of-range policy";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (f.data_slot != 0 && f.data_slot != 1) {
+    why = "an ill-formed gather";
+    return UNP_LIFT_DECLINE;
+  }
+  const char* I = ctype(f.index_dtype);
+  std::ostringstream name;
+  name << "unp_gather_rows_" << lower_name(f.dtype) << "_by_" << lower_name(f.index_dtype) << "_"
+       << oob_name(f.oob);
+  L.name = name.str();
+  L.blocks_per_cu = 8;
+  std::ostringstream src;
+  src << header(L.name, f);
+  const int units[2] = {16, (int)eb};
+  for (int i = 0; i < 2; ++i) {
+    if (i == 1 && units[1] == 16) break;
+    Entry e;
+    e.fast = (i == 0);
+    e.vec = units[i];
+    e.symbol = L.name + (i == 0 ? "_u16" : "_u" + std::to_string(units[i]));
+    const int U = units[i] == 16 ? 8 : 16;
+    src << "extern \"C\" __global__ void " << kLaunchBounds << " " << e.symbol
+        << "(const unsigned char* table, const " << I << "* ids, unsigned char* out, long long n_rows, "
+        << "long long row_bytes, " << I << " src_extent) {\n  unp::gather_rows<" << I << ", " << f.oob << ", "
+        << units[i] << ", 256, " << U << ">(table, ids, out, n_rows, row_bytes, src_extent);\n}\n";
+    L.entries.push_back(e);
+  }
+  L.source = src.str();
+  std::ostringstream j;
+  j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"gather\",\"dtype\":\"" << kind_name(f.dtype)
+    << "\",\"index_dtype\":\"" << kind_name(f.index_dtype) << "\",\"oob\":\"" << oob_name(f.oob)
+    << "\",\"axis\":0,\"rank\":" << f.rank << ",\"params\":[{\"name\":\"in0\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\""
+    << kind_name(f.data_slot == 0 ? f.dtype : f.index_dtype) << "\"},{\"name\":\"in1\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\""
+    << kind_name(f.data_slot == 1 ? f.dtype : f.index_dtype)
+    << "\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
+  for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
+  j << ",{\"name\":\"src_extent\",\"kind\":\"scalar\",\"dtype\":\"" << kind_name(f.index_dtype)
+    << "\"}],\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
+    << "\",\"grid_policy\":\"one wave per output row, waves stride over rows\"},\"entries\":[";
+  for (size_t i = 0; i < L.entries.size(); ++i)
+    j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"unit_bytes\":" << L.entries[i].vec
+      << ",\"when\":\"" << (L.entries[i].fast ? "row bytes % 16 == 0 and table/out 16-byte aligned" : "otherwise")
+      << "\"}";
+  j << "],\"workspace\":null,\"fidelity_notes\":[" << json_str("a raw bit move: bit-exact for every grid and block")
+    << "]}";
+  L.interface_json = j.str();
+  return UNP_OK;
+}
+
+static int32_t lower_dequant(const unp_form& f, Lowered& L, std::string& why) {
+  if (f.q_kind != UNP_U4 && f.q_kind != UNP_I4) {
+    why = "dequant weights must be U4 or I4";
+    return UNP_UNSUPPORTED_DTYPE;
+  }
+  if (f.z_kind != UNP_U4 && f.z_kind != UNP_I4) {
+    why = "dequant zero points must be U4 or I4";
+    return UNP_UNSUPPORTED_DTYPE;
+  }
+  if (f.out_kind != UNP_BF16) {
+    why = "dequant output other than Bf16";
+    return UNP_UNSUPPORTED_DTYPE;
+  }
+  if (f.group < 1) {
+    why = "a dequant group of zero columns";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  const bool qs = f.q_kind == UNP_I4, zs = f.z_kind == UNP_I4;
+  std::ostringstream name;
+  name << "unp_dequant_" << lower_name(f.q_kind) << "_z" << lower_name(f.z_kind) << "_g" << f.group << "_bf16";
+  L.name = name.str();
+  L.blocks_per_cu = 8;
+  std::ostringstream src;
+  src << header(L.name, f);
+  const char* sig =
+      "(const unsigned char* q, const unsigned short* scale, const unsigned char* zero, unsigned short* out, "
+      "long long rows, long long cols)";
+  if (f.group % 32 == 0) {
+    Entry e;
+    e.fast = true;
+    e.vec = 32;
+    e.symbol = L.name + "_v";
+    src << "extern \"C\" __global__ void " << kLaunchBounds << " " << e.symbol << sig << " {\n  unp::dequant4_bf16<"
+        << (qs ? "true" : "false") << ", " << (zs ? "true" : "false") << ", " << f.group
+        << ", 256>(q, scale, zero, out, rows, cols);\n}\n";
+    L.entries.push_back(e);
+  }
+  {
+    Entry e;
+    e.fast = false;
+    e.vec = 1;
+    e.symbol = L.name + "_s";
+    src << "extern \"C\" __global__ void " << kLaunchBounds << " " << e.symbol << sig << " {\n  unp::dequant4_bf16_any<"
+        << (qs ? "true" : "false") << ", " << (zs ? "true" : "false") << ", " << f.group
+        << ", 256>(q, scale, zero, out, rows, cols);\n}\n";
+    L.entries.push_back(e);
+  }
+  L.source = src.str();
+  std::ostringstream j;
+  j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"dequant4\",\"q\":\"" << kind_name(f.q_kind)
+    << "\",\"zero\":\"" << kind_name(f.z_kind) << "\",\"scale\":\"F16\",\"out\":\"Bf16\",\"group\":" << f.group
+    << ",\"params\":[{\"name\":\"w\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\"" << kind_name(f.q_kind)
+    << "\"},{\"name\":\"scale\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\"F16\"},{\"name\":\"zero\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\""
+    << kind_name(f.z_kind)
+    << "\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\",\"dtype\":\"Bf16\"},{\"name\":\"n0\",\"kind\":\"scalar\",\"dtype\":\"I32\"},{\"name\":\"n1\",\"kind\":\"scalar\",\"dtype\":\"I32\"}]"
+    << ",\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
+    << "\",\"grid_policy\":\"32-column chunks stride over the grid\"},\"entries\":[";
+  for (size_t i = 0; i < L.entries.size(); ++i)
+    j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"when\":\""
+      << (L.entries[i].fast ? "cols % 32 == 0 and w/out 16-byte aligned" : "otherwise") << "\"}";
+  j << "],\"workspace\":null,\"fidelity_notes\":["
+    << json_str("exact integer difference and exact f32 product; one round-to-nearest-even to bf16: bit-exact")
+    << "]}";
+  L.interface_json = j.str();
+  return UNP_OK;
+}
+
+int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail) {
+  out = Lowered{};
+  out.form = f;
+  switch (f.kind) {
+    case UNP_FORM_REDUCTION:
+    case UNP_FORM_ROW_REDUCE2:
+      return lower_reduction(f, out, detail);
+    case UNP_FORM_SCAN:
+      return lower_scan(f, out, detail);
+    case UNP_FORM_GATHER:
+      return lower_gather(f, out, detail);
+    case UNP_FORM_DEQUANT4:
+      return lower_dequant(f, out, detail);
+    default:
+      detail = "an unknown form";
+      return UNP_UNSUPPORTED_KERNEL;
+  }
+}
+
+}  // namespace unp

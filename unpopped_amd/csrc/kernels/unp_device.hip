@@ -1,0 +1,748 @@
+// unpopped-hip device template library (gfx950, wave64).
+//
+// The HIP emitter writes a kernel source as: this library + one `extern "C" __global__`
+// entry that instantiates one template below with the form's element type, fold, launch
+// geometry and policy.  The Compiler turns that text into a code object (hipRTC); the
+// runtime loads it with hipModuleLoadData and launches it with hipModuleLaunchKernel.
+//
+// Numerics follow the reference's lifts:
+//   * float Sum / Mean fold in f64 and round once to the element type at the store
+//     (crates/unpopped/src/kernel_lift.rs:883-896, :965-983);
+//   * Max / Min keep a NaN once seen: `!have || v != v || better(v, acc)`
+//     (kernel_lift.rs:1097-1160); the `have` flag is replaced by the monoid identity
+//     (-inf / +inf / INT_MIN / INT_MAX), which the NaN-keeping step leaves unchanged;
+//   * integer folds wrap at the element width (kernel_lift.rs:883-889);
+//   * an empty fold stores the fold's starting value: 0 for Sum/Max/Min, 1 for Prod,
+//     0/0 for Mean (kernel_lift.rs:915-924, :941-963);
+//   * bf16 stores round to nearest even, a NaN keeps its top bits and is quieted
+//     (crates/unpopped/src/oracle/float_codec.rs:259-266).
+// The reduction order inside a kernel is fixed by the launch geometry, as the launched
+// lifts fix theirs by (grid, block) (kernel_lift/block_reduce.rs:14-24); a float Sum is held
+// to the declared bound gamma_(n-1) * sum|x| + half an ulp of the final rounding.
+//
+// Cross-lane work uses DPP (row_shr, wave_shr) and v_readlane; cross-wave work goes
+// through LDS.  Global loads and stores are 128-bit where the host has checked the
+// alignment (the `VEC` / `UNIT` template arguments).
+
+#if !defined(__HIPCC_RTC__)
+#include <hip/hip_runtime.h>
+#endif
+
+namespace unp {
+
+typedef unsigned char u8;
+typedef unsigned short u16;
+typedef unsigned int u32;
+typedef unsigned long long u64;
+typedef int i32;
+typedef long long i64;
+
+#define UNP_DEV __device__ __forceinline__
+
+enum : int { OP_SUM = 0, OP_PROD = 1, OP_MAX = 2, OP_MIN = 3, OP_MEAN = 4 };
+enum : int { OOB_SKIP = 0, OOB_ZEROFILL = 1, OOB_CLAMP = 2 };
+
+template <class T> struct traits;
+template <> struct traits<float> {
+  static constexpr bool is_float = true;
+  typedef u32 uns;
+};
+template <> struct traits<double> {
+  static constexpr bool is_float = true;
+  typedef u64 uns;
+};
+template <> struct traits<i32> {
+  static constexpr bool is_float = false;
+  typedef u32 uns;
+  static constexpr i32 lo = -2147483647 - 1;
+  static constexpr i32 hi = 2147483647;
+};
+template <> struct traits<i64> {
+  static constexpr bool is_float = false;
+  typedef u64 uns;
+  static constexpr i64 lo = -9223372036854775807LL - 1;
+  static constexpr i64 hi = 9223372036854775807LL;
+};
+
+// The accumulator: a float Sum or Mean folds in f64, every other fold at the element type
+// (exact for Max/Min; wrapping for the integers).
+template <class T, int OP> struct acc { typedef T type; };
+template <> struct acc<float, OP_SUM> { typedef double type; };
+template <> struct acc<float, OP_MEAN> { typedef double type; };
+
+template <class A, int OP> struct fold;
+
+template <class A> struct fold_sum {
+  static UNP_DEV A identity() { return A(0); }
+  static UNP_DEV A apply(A a, A b) {
+    if constexpr (traits<A>::is_float) {
+      return a + b;
+    } else {
+      typedef typename traits<A>::uns U;
+      return (A)((U)a + (U)b);
+    }
+  }
+};
+template <class A> struct fold<A, OP_SUM> : fold_sum<A> {};
+template <class A> struct fold<A, OP_MEAN> : fold_sum<A> {};
+
+template <class A> struct fold<A, OP_PROD> {
+  static UNP_DEV A identity() { return A(1); }
+  static UNP_DEV A apply(A a, A b) {
+    if constexpr (traits<A>::is_float) {
+      return a * b;
+    } else {
+      typedef typename traits<A>::uns U;
+      return (A)((U)a * (U)b);
+    }
+  }
+};
+
+template <class A> struct fold<A, OP_MAX> {
+  static UNP_DEV A identity() {
+    if constexpr (traits<A>::is_float) return A(-__builtin_inf());
+    else return traits<A>::lo;
+  }
+  // `a` is the earlier partial; a NaN on either side is kept once seen.
+  static UNP_DEV A apply(A a, A b) {
+    if constexpr (traits<A>::is_float) return (b > a || b != b) ? b : a;
+    else return b > a ? b : a;
+  }
+};
+
+template <class A> struct fold<A, OP_MIN> {
+  static UNP_DEV A identity() {
+    if constexpr (traits<A>::is_float) return A(__builtin_inf());
+    else return traits<A>::hi;
+  }
+  static UNP_DEV A apply(A a, A b) {
+    if constexpr (traits<A>::is_float) return (b < a || b != b) ? b : a;
+    else return b < a ? b : a;
+  }
+};
+
+// The value stored for a finished fold over `n` elements.
+template <class T, int OP, class A> UNP_DEV T finish(A a, i64 n) {
+  if constexpr (OP == OP_MEAN) {
+    return (T)(a / (double)n);
+  } else if constexpr (OP == OP_MAX || OP == OP_MIN) {
+    return n == 0 ? T(0) : (T)a;
+  } else {
+    return (T)a;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Vectors and lane primitives
+// ---------------------------------------------------------------------------------------
+
+template <class T, int N> struct alignas(sizeof(T) * N) vec {
+  T e[N];
+};
+
+template <class T, int N> UNP_DEV vec<T, N> ld(const T* p) {
+  return *reinterpret_cast<const vec<T, N>*>(p);
+}
+template <class T, int N> UNP_DEV void stv(T* p, const vec<T, N>& v) {
+  *reinterpret_cast<vec<T, N>*>(p) = v;
+}
+
+template <class X> UNP_DEV u64 to_bits64(X v) {
+  if constexpr (sizeof(X) == 4) return (u64)__builtin_bit_cast(u32, v);
+  else return __builtin_bit_cast(u64, v);
+}
+template <class X> UNP_DEV X from_bits64(u64 b) {
+  if constexpr (sizeof(X) == 4) return __builtin_bit_cast(X, (u32)b);
+  else return __builtin_bit_cast(X, b);
+}
+
+// v_mov_b32_dpp: lanes whose source is outside the row (or the wave) keep `old`.
+template <int CTRL, int ROW_MASK> UNP_DEV u32 dpp32(u32 old, u32 src) {
+  return (u32)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, ROW_MASK, 0xF, false);
+}
+
+template <int CTRL, int ROW_MASK, class X> UNP_DEV X dpp(X old, X src) {
+  if constexpr (sizeof(X) == 4) {
+    return __builtin_bit_cast(
+        X, dpp32<CTRL, ROW_MASK>(__builtin_bit_cast(u32, old), __builtin_bit_cast(u32, src)));
+  } else {
+    static_assert(sizeof(X) == 8, "4- or 8-byte lanes");
+    const u64 o = __builtin_bit_cast(u64, old), s = __builtin_bit_cast(u64, src);
+    const u32 lo = dpp32<CTRL, ROW_MASK>((u32)o, (u32)s);
+    const u32 hi = dpp32<CTRL, ROW_MASK>((u32)(o >> 32), (u32)(s >> 32));
+    return __builtin_bit_cast(X, ((u64)hi << 32) | (u64)lo);
+  }
+}
+
+template <class X> UNP_DEV X readlane(X v, int lane) {
+  if constexpr (sizeof(X) == 4) {
+    return __builtin_bit_cast(X, (u32)__builtin_amdgcn_readlane((int)__builtin_bit_cast(u32, v), lane));
+  } else {
+    const u64 b = __builtin_bit_cast(u64, v);
+    const u32 lo = (u32)__builtin_amdgcn_readlane((int)(u32)b, lane);
+    const u32 hi = (u32)__builtin_amdgcn_readlane((int)(u32)(b >> 32), lane);
+    return __builtin_bit_cast(X, ((u64)hi << 32) | (u64)lo);
+  }
+}
+
+// DPP control words (GFX9 encoding).
+enum : int {
+  DPP_ROW_SHR1 = 0x111,
+  DPP_ROW_SHR2 = 0x112,
+  DPP_ROW_SHR4 = 0x114,
+  DPP_ROW_SHR8 = 0x118,
+  DPP_WAVE_SHR1 = 0x138,
+};
+
+// Inclusive scan inside each 16-lane row (Hillis-Steele over row_shr 1, 2, 4, 8; the
+// earlier lane is the left operand).  Must be called with all 64 lanes active.
+template <class A, int OP> UNP_DEV A row_inclusive_scan(A x) {
+  typedef fold<A, OP> F;
+  const A I = F::identity();
+  x = F::apply(dpp<DPP_ROW_SHR1, 0xF>(I, x), x);
+  x = F::apply(dpp<DPP_ROW_SHR2, 0xF>(I, x), x);
+  x = F::apply(dpp<DPP_ROW_SHR4, 0xF>(I, x), x);
+  x = F::apply(dpp<DPP_ROW_SHR8, 0xF>(I, x), x);
+  return x;
+}
+
+// The fold of all 64 lanes, the same value in every lane.
+template <class A, int OP> UNP_DEV A wave_reduce(A x) {
+  typedef fold<A, OP> F;
+  x = row_inclusive_scan<A, OP>(x);
+  return F::apply(F::apply(F::apply(readlane(x, 15), readlane(x, 31)), readlane(x, 47)),
+                  readlane(x, 63));
+}
+
+// Inclusive scan over the 64 lanes (lane order = fold order).
+template <class A, int OP> UNP_DEV A wave_inclusive_scan(A x, int lane) {
+  typedef fold<A, OP> F;
+  x = row_inclusive_scan<A, OP>(x);
+  const A r0 = readlane(x, 15);
+  const A r01 = F::apply(r0, readlane(x, 31));
+  const A r012 = F::apply(r01, readlane(x, 47));
+  const int row = lane >> 4;
+  const A pre = row == 1 ? r0 : (row == 2 ? r01 : r012);
+  return row == 0 ? x : F::apply(pre, x);
+}
+
+// Lane l receives lane l-1's value; lane 0 receives `fill`.
+template <class A> UNP_DEV A wave_shr1(A x, A fill) { return dpp<DPP_WAVE_SHR1, 0xF>(fill, x); }
+
+// Fold of a value held by every thread of a block, in wave order; the same result in every
+// thread.  `s` has one slot per wave.
+template <class A, int OP, int THREADS> UNP_DEV A block_reduce(A x, A* s) {
+  typedef fold<A, OP> F;
+  constexpr int WAVES = THREADS / 64;
+  x = wave_reduce<A, OP>(x);
+  if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = x;
+  __syncthreads();
+  A r = s[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) r = F::apply(r, s[w]);
+  __syncthreads();
+  return r;
+}
+
+// Device-scope (all XCDs) coherent scalar accesses: relaxed agent-scope atomics bypass the
+// non-coherent part of the cache hierarchy on gfx950.
+template <class X> UNP_DEV void store_agent(X* p, X v) {
+  if constexpr (sizeof(X) == 4) {
+    __hip_atomic_store(reinterpret_cast<u32*>(p), __builtin_bit_cast(u32, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    __hip_atomic_store(reinterpret_cast<u64*>(p), __builtin_bit_cast(u64, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+template <class X> UNP_DEV X load_agent(const X* p) {
+  if constexpr (sizeof(X) == 4) {
+    return __builtin_bit_cast(X, __hip_atomic_load(reinterpret_cast<const u32*>(p), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT));
+  } else {
+    return __builtin_bit_cast(X, __hip_atomic_load(reinterpret_cast<const u64*>(p), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT));
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Row reduction: rows x cols row-major, one or two folds of each row read once.
+// Blocks stride over rows (row = blockIdx.x; += gridDim.x), as the launched reduction
+// lift strides over its outermost kept axis (kernel_lift/block_reduce.rs:313-338).
+// Inside a row, thread t folds the vectors t, t + THREADS, ... (VEC elements each) in
+// ascending order; waves combine by DPP, blocks by LDS in wave order.
+// ---------------------------------------------------------------------------------------
+template <class T, int OP0, int OP1, int NOUT, int VEC, int THREADS, int UNROLL>
+UNP_DEV void rowreduce(const T* __restrict__ in, T* __restrict__ out0, T* __restrict__ out1, i64 rows,
+                       i64 cols) {
+  typedef typename acc<T, OP0>::type A0;
+  typedef typename acc<T, OP1>::type A1;
+  typedef fold<A0, OP0> F0;
+  typedef fold<A1, OP1> F1;
+  constexpr int WAVES = THREADS / 64;
+  constexpr i64 STEP = (i64)THREADS * VEC;
+  __shared__ A0 s0[2][WAVES];
+  __shared__ A1 s1[2][WAVES];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int par = 0;
+  for (i64 row = blockIdx.x; row < rows; row += gridDim.x) {
+    const T* __restrict__ p = in + row * cols;
+    A0 a0 = F0::identity();
+    A1 a1 = F1::identity();
+    i64 c = (i64)tid * VEC;
+    for (; c + (UNROLL - 1) * STEP < cols; c += UNROLL * STEP) {
+      vec<T, VEC> v[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) v[u] = ld<T, VEC>(p + c + u * STEP);
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          a0 = F0::apply(a0, (A0)v[u].e[e]);
+          if constexpr (NOUT > 1) a1 = F1::apply(a1, (A1)v[u].e[e]);
+        }
+      }
+    }
+    for (; c < cols; c += STEP) {
+      const vec<T, VEC> v = ld<T, VEC>(p + c);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        a0 = F0::apply(a0, (A0)v.e[e]);
+        if constexpr (NOUT > 1) a1 = F1::apply(a1, (A1)v.e[e]);
+      }
+    }
+    a0 = wave_reduce<A0, OP0>(a0);
+    if constexpr (NOUT > 1) a1 = wave_reduce<A1, OP1>(a1);
+    if (lane == 0) {
+      s0[par][wave] = a0;
+      if constexpr (NOUT > 1) s1[par][wave] = a1;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      A0 r0 = s0[par][0];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) r0 = F0::apply(r0, s0[par][w]);
+      out0[row] = finish<T, OP0>(r0, cols);
+      if constexpr (NOUT > 1) {
+        A1 r1 = s1[par][0];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) r1 = F1::apply(r1, s1[par][w]);
+        out1[row] = finish<T, OP1>(r1, cols);
+      }
+    }
+    // The next row writes the other half of the LDS slots; the row after that reuses these
+    // only after every thread has passed the next row's barrier.
+    par ^= 1;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Full reduction of n elements to one value (no kept axis), in one launch: every block
+// folds a grid-strided slice, publishes its partial, and the block that draws the last
+// ticket folds the partials in block order and stores.  The order depends on
+// (gridDim.x, THREADS, VEC, UNROLL) only, so the result is reproducible run to run.
+// `counter` is zero on entry and is left zero.
+// ---------------------------------------------------------------------------------------
+template <class T, int OP, int VEC, int THREADS, int UNROLL>
+UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
+                        typename acc<T, OP>::type* __restrict__ partials, u32* __restrict__ counter) {
+  typedef typename acc<T, OP>::type A;
+  typedef fold<A, OP> F;
+  constexpr int WAVES = THREADS / 64;
+  __shared__ A s[WAVES];
+  __shared__ u32 last;
+  const int tid = threadIdx.x;
+  const i64 STEP = (i64)gridDim.x * THREADS * VEC;
+  A a = F::identity();
+  i64 c = ((i64)blockIdx.x * THREADS + tid) * VEC;
+  for (; c + (UNROLL - 1) * STEP < n; c += UNROLL * STEP) {
+    vec<T, VEC> v[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) v[u] = ld<T, VEC>(in + c + u * STEP);
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) a = F::apply(a, (A)v[u].e[e]);
+    }
+  }
+  for (; c < n; c += STEP) {
+    const vec<T, VEC> v = ld<T, VEC>(in + c);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) a = F::apply(a, (A)v.e[e]);
+  }
+  a = block_reduce<A, OP, THREADS>(a, s);
+  if (tid == 0) {
+    store_agent(&partials[blockIdx.x], a);
+    const u32 ticket =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    last = (ticket == gridDim.x - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (last == 0u) return;
+  A b = F::identity();
+  for (u32 i = tid; i < gridDim.x; i += THREADS) b = F::apply(b, load_agent(&partials[i]));
+  b = block_reduce<A, OP, THREADS>(b, s);
+  if (tid == 0) {
+    out[0] = finish<T, OP>(b, n);
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Single-pass scan with decoupled look-back, along the innermost axis of rows x cols.
+//
+// A tile is TILE = 64 * VEC * K consecutive scan positions of one row, owned by one wave.
+// Waves are persistent: each draws tile tickets from `counter` until the tickets run out,
+// so a wave only ever waits on tiles whose tickets were drawn earlier (forward progress).
+// Loads are striped: load k of lane l covers positions (k * 64 + l) * VEC .. + VEC, so every
+// load instruction of a wave reads 64 * VEC contiguous elements.
+//
+// Tile status: per tile an aggregate slot and an inclusive slot of W 64-bit words
+// (W = 1 for a 4-byte carry, 2 for an 8-byte one).  Each word carries the launch's epoch in
+// its high half and 32 bits of the value in its low half, so a reader accepts a slot only
+// when every word of it carries this launch's epoch: no fence and no reset between launches.
+// The host advances `epoch` (never 0) and `ticket_base` (by tiles + waves) per launch.
+// ---------------------------------------------------------------------------------------
+template <class A> struct tile_status {
+  static constexpr int W = sizeof(A) == 4 ? 1 : 2;
+  static constexpr int STRIDE = 2 * W;
+
+  static UNP_DEV void publish(u64* st, u64 tile, int slot, A v, u32 epoch) {
+    u64* p = st + tile * STRIDE + slot * W;
+    const u64 b = to_bits64(v);
+    const u64 tag = (u64)epoch << 32;
+    __hip_atomic_store(p, tag | (b & 0xffffffffull), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (W == 2) {
+      __hip_atomic_store(p + 1, tag | (b >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+
+  // 2: inclusive prefix in `v`; 1: aggregate in `v`; 0: nothing yet.
+  static UNP_DEV int probe(const u64* st, u64 tile, u32 epoch, A& v) {
+    const u64* p = st + tile * STRIDE;
+    const u64 i0 = __hip_atomic_load(p + W, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (W == 1) {
+      if ((u32)(i0 >> 32) == epoch) {
+        v = from_bits64<A>(i0 & 0xffffffffull);
+        return 2;
+      }
+      const u64 a0 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((u32)(a0 >> 32) == epoch) {
+        v = from_bits64<A>(a0 & 0xffffffffull);
+        return 1;
+      }
+      return 0;
+    } else {
+      const u64 i1 = __hip_atomic_load(p + W + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((u32)(i0 >> 32) == epoch && (u32)(i1 >> 32) == epoch) {
+        v = from_bits64<A>((i0 & 0xffffffffull) | (i1 << 32));
+        return 2;
+      }
+      const u64 a0 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const u64 a1 = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((u32)(a0 >> 32) == epoch && (u32)(a1 >> 32) == epoch) {
+        v = from_bits64<A>((a0 & 0xffffffffull) | (a1 << 32));
+        return 1;
+      }
+      return 0;
+    }
+  }
+};
+
+// The fold of every earlier tile of this row (j = tile's index in its row, j >= 1).
+// Lane l inspects the tile l + 1 back; the walk stops at the first inclusive prefix.
+template <class A, int OP>
+UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch) {
+  typedef fold<A, OP> F;
+  typedef tile_status<A> S;
+  const A I = F::identity();
+  A excl = I;
+  i64 pj = j - 1 - lane;
+  for (;;) {
+    A v = I;
+    int state = 2;  // before the row's first tile: the identity, final
+    if (pj >= 0) {
+      const u64 pt = tile - (u64)(j - pj);
+      state = S::probe(st, pt, epoch, v);
+      while (state == 0) {
+        __builtin_amdgcn_s_sleep(1);
+        state = S::probe(st, pt, epoch, v);
+      }
+    }
+    const u64 incl = __ballot(state == 2);
+    const int f = incl ? __builtin_ctzll(incl) : 63;
+    const A c = lane <= f ? v : I;
+    excl = F::apply(wave_reduce<A, OP>(c), excl);
+    if (incl) return excl;
+    pj -= 64;
+  }
+}
+
+template <class T, int OP, bool EXCL, bool REV, int VEC, int K>
+UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
+                           u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base,
+                           u32 epoch) {
+  typedef typename acc<T, OP>::type A;
+  typedef fold<A, OP> F;
+  typedef tile_status<A> S;
+  constexpr i64 TILE = (i64)64 * VEC * K;
+  const int lane = threadIdx.x & 63;
+  const A I = F::identity();
+  const T pad = (T)I;  // the identity, exactly representable at the element type
+  const i64 tpr = (cols + TILE - 1) / TILE;
+  const u64 total = (u64)rows * (u64)tpr;
+  for (;;) {
+    u32 ticket = 0;
+    if (lane == 0) ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ticket = (u32)__builtin_amdgcn_readfirstlane((int)ticket);
+    const u64 tile = (u64)(u32)(ticket - ticket_base);
+    if (tile >= total) break;
+    const i64 row = (i64)(tile / (u64)tpr);
+    const i64 j = (i64)tile - row * tpr;
+    const i64 p0 = j * TILE;
+    const bool full = p0 + TILE <= cols;
+    const T* __restrict__ rin = in + row * cols;
+    T* __restrict__ rout = out + row * cols;
+
+    // Load the tile, elements in scan order.
+    vec<T, VEC> x[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
+      if (full || pos + VEC <= cols) {
+        if constexpr (REV) {
+          const vec<T, VEC> r = ld<T, VEC>(rin + (cols - VEC - pos));
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) x[k].e[e] = r.e[VEC - 1 - e];
+        } else {
+          x[k] = ld<T, VEC>(rin + pos);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const i64 q = pos + e;
+          x[k].e[e] = q < cols ? rin[REV ? cols - 1 - q : q] : pad;
+        }
+      }
+    }
+
+    // Tile-local prefixes: pre[k] is the fold of every element before lane's vector k.
+    A pre[K];
+    A carry = I;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      A s = (A)x[k].e[0];
+#pragma unroll
+      for (int e = 1; e < VEC; ++e) s = F::apply(s, (A)x[k].e[e]);
+      const A inc = wave_inclusive_scan<A, OP>(s, lane);
+      pre[k] = F::apply(carry, wave_shr1(inc, I));
+      carry = F::apply(carry, readlane(inc, 63));
+    }
+
+    A base = I;
+    if (j == 0) {
+      if (lane == 0) S::publish(st, tile, 1, carry, epoch);
+    } else {
+      if (lane == 0) S::publish(st, tile, 0, carry, epoch);
+      base = lookback<A, OP>(st, tile, j, lane, epoch);
+      if (lane == 0) S::publish(st, tile, 1, F::apply(base, carry), epoch);
+    }
+
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      A v = F::apply(base, pre[k]);
+      vec<T, VEC> o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        if constexpr (EXCL) {
+          o.e[e] = (T)v;
+          v = F::apply(v, (A)x[k].e[e]);
+        } else {
+          v = F::apply(v, (A)x[k].e[e]);
+          o.e[e] = (T)v;
+        }
+      }
+      const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
+      if (full || pos + VEC <= cols) {
+        if constexpr (REV) {
+          vec<T, VEC> r;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) r.e[e] = o.e[VEC - 1 - e];
+          stv<T, VEC>(rout + (cols - VEC - pos), r);
+        } else {
+          stv<T, VEC>(rout + pos, o);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const i64 q = pos + e;
+          if (q < cols) rout[REV ? cols - 1 - q : q] = o.e[e];
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Row gather: out[r, :] = table[clamp(ids[r]), :] with the out-of-range policy applied to
+// the store (crates/unpopped/src/kernel_lift/gather.rs:184-232): Skip leaves the row,
+// ZeroFill writes zero bytes, Clamp stores the clamped row.  Rows are moved as raw bytes
+// in UNIT-byte pieces; one wave per output row, waves stride over rows.
+// ---------------------------------------------------------------------------------------
+template <int UNIT> struct unit_type;
+template <> struct unit_type<16> { typedef vec<u32, 4> type; };
+template <> struct unit_type<8> { typedef vec<u32, 2> type; };
+template <> struct unit_type<4> { typedef u32 type; };
+template <> struct unit_type<2> { typedef u16 type; };
+template <> struct unit_type<1> { typedef u8 type; };
+
+template <class IDX> UNP_DEV bool below_zero(IDX v) {
+  if constexpr ((IDX)(-1) < (IDX)0) return v < (IDX)0;
+  else return false;
+}
+
+template <class IDX, int POLICY, int UNIT, int THREADS, int U>
+UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ ids, u8* __restrict__ out,
+                         i64 n_rows, i64 row_bytes, IDX src_extent) {
+  typedef typename unit_type<UNIT>::type V;
+  constexpr int WAVES = THREADS / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const i64 units = row_bytes / UNIT;
+  for (i64 r = (i64)blockIdx.x * WAVES + wave; r < n_rows; r += (i64)gridDim.x * WAVES) {
+    const IDX raw = ids[r];
+    const bool below = below_zero(raw);
+    const bool oob = below || !(raw < src_extent);
+    V* __restrict__ dst = reinterpret_cast<V*>(out + r * row_bytes);
+    if (oob && POLICY != OOB_CLAMP) {
+      if constexpr (POLICY == OOB_ZEROFILL) {
+        V z;
+        __builtin_memset(&z, 0, sizeof(V));
+        for (i64 u = lane; u < units; u += 64) dst[u] = z;
+      }
+      continue;
+    }
+    const IDX cl = below ? (IDX)0 : (oob ? (IDX)(src_extent - (IDX)1) : raw);
+    const V* __restrict__ src = reinterpret_cast<const V*>(table + (i64)cl * row_bytes);
+    for (i64 u = lane; u < units; u += 64 * U) {
+      V v[U];
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const i64 uu = u + 64 * k;
+        if (uu < units) v[k] = src[uu];
+      }
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const i64 uu = u + 64 * k;
+        if (uu < units) dst[uu] = v[k];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Sub-byte dequant: out[r, c] = bf16_rne((q[r, c] - z[r, c / G]) * s[r, c / G]).
+// q and z are packed two 4-bit elements per byte, low nibble first (element k lives in
+// byte k / 2, bits 4 * (k & 1)), flat row-major; s is f16.  The integer difference is
+// exact, converting it to f32 is exact, and the product (at most 5 x 11 significant bits)
+// is exact in f32, so the one rounding is the bf16 store.
+// ---------------------------------------------------------------------------------------
+UNP_DEV u32 bf16_rne_bits(float f) {
+  const u32 b = __builtin_bit_cast(u32, f);
+  if (f != f) return (b >> 16) | 0x40u;
+  return (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+}
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two finite f32 values to two bf16 (round to nearest even), low element first.
+UNP_DEV u32 bf16x2_rne_finite(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(u32, __builtin_convertvector(v, bf16x2_t));
+}
+
+template <bool SIGNED> UNP_DEV i32 nibble_value(u32 n) {
+  if constexpr (SIGNED) return (i32)(n ^ 8u) - 8;
+  else return (i32)n;
+}
+
+UNP_DEV float f16_to_f32(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// Fast path: cols % 32 == 0 and G % 32 == 0, so a 32-column chunk lies in one group and
+// its 16 bytes of q are 16-byte aligned.  Work item = one chunk; items stride over the grid.
+template <bool QS, bool ZS, int G, int THREADS>
+UNP_DEV void dequant4_bf16(const u8* __restrict__ q, const u16* __restrict__ sc, const u8* __restrict__ zp,
+                           u16* __restrict__ out, i64 rows, i64 cols) {
+  const i64 cpr = cols >> 5;  // chunks per row
+  const i64 ng = (cols + G - 1) / G;
+  const i64 items = rows * cpr;
+  const i64 step = (i64)gridDim.x * THREADS;
+  i64 it = (i64)blockIdx.x * THREADS + threadIdx.x;
+  if (it >= items) return;
+  // (r, cc) of the current item, advanced without a division per item.
+  i64 r = it / cpr, cc = it - r * cpr;
+  const i64 dr = step / cpr, dc = step - dr * cpr;
+  for (; it < items; it += step) {
+    const i64 e0 = r * cols + (cc << 5);
+    const vec<u32, 4> w = ld<u32, 4>(reinterpret_cast<const u32*>(q + (e0 >> 1)));
+    const i64 zi = r * ng + ((cc << 5) / G);
+    const float s = f16_to_f32(sc[zi]);
+    const u32 zb = zp[zi >> 1];
+    const i32 z = nibble_value<ZS>((zi & 1) ? (zb >> 4) : (zb & 15u));
+    const float fz = (float)z;
+    vec<u32, 4> o[4];
+    if (__builtin_isfinite(s)) {
+#pragma unroll
+      for (int wi = 0; wi < 4; ++wi) {
+        const u32 wv = w.e[wi];
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {
+          const float a = ((float)nibble_value<QS>((wv >> (8 * pr)) & 15u) - fz) * s;
+          const float b = ((float)nibble_value<QS>((wv >> (8 * pr + 4)) & 15u) - fz) * s;
+          o[wi].e[pr] = bf16x2_rne_finite(a, b);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int wi = 0; wi < 4; ++wi) {
+        const u32 wv = w.e[wi];
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {
+          const float a = (float)(nibble_value<QS>((wv >> (8 * pr)) & 15u) - z) * s;
+          const float b = (float)(nibble_value<QS>((wv >> (8 * pr + 4)) & 15u) - z) * s;
+          o[wi].e[pr] = bf16_rne_bits(a) | (bf16_rne_bits(b) << 16);
+        }
+      }
+    }
+    u16* dst = out + e0;
+#pragma unroll
+    for (int wi = 0; wi < 4; ++wi) stv<u32, 4>(reinterpret_cast<u32*>(dst) + 4 * wi, o[wi]);
+    r += dr;
+    cc += dc;
+    if (cc >= cpr) {
+      cc -= cpr;
+      ++r;
+    }
+  }
+}
+
+// General path: any cols and G; one element per thread step, rows block-strided.
+template <bool QS, bool ZS, int G, int THREADS>
+UNP_DEV void dequant4_bf16_any(const u8* __restrict__ q, const u16* __restrict__ sc, const u8* __restrict__ zp,
+                               u16* __restrict__ out, i64 rows, i64 cols) {
+  const i64 ng = (cols + G - 1) / G;
+  for (i64 r = blockIdx.x; r < rows; r += gridDim.x) {
+    for (i64 c = threadIdx.x; c < cols; c += THREADS) {
+      const i64 e = r * cols + c;
+      const u32 qb = q[e >> 1];
+      const i32 qv = nibble_value<QS>((e & 1) ? (qb >> 4) : (qb & 15u));
+      const i64 zi = r * ng + c / G;
+      const u32 zb = zp[zi >> 1];
+      const i32 z = nibble_value<ZS>((zi & 1) ? (zb >> 4) : (zb & 15u));
+      const float s = f16_to_f32(sc[zi]);
+      out[e] = (u16)bf16_rne_bits((float)(qv - z) * s);
+    }
+  }
+}
+
+}  // namespace unp

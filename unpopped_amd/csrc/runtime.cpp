@@ -1,0 +1,562 @@
+// The backend's C entry points, the HIP runtime FFI and the prepared-kernel executor.
+//
+// The executor is the consumer-side launch layer the reference leaves out by rule
+// (docs/PATENT-SWEEP.md:265-272): it compiles a lowered kernel's source once, loads it with
+// hipModuleLoadData, picks the entry point whose alignment preconditions the arguments meet,
+// sizes the grid from the device (a device-class constant, never from an extent), owns the
+// scan's tile-status and the full reduction's partials workspaces, and launches with
+// hipModuleLaunchKernel.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
+
+#include "unp_internal.hpp"
+
+using unp::set_error;
+
+namespace {
+
+int32_t hip_fail(unp_error* err, const char* what, hipError_t e) {
+  set_error(err, UNP_HIP_ERROR, std::string(what) + ": " + hipGetErrorString(e));
+  return UNP_HIP_ERROR;
+}
+
+bool valid_target(const char* t) {
+  if (!t) return false;
+  int colons = 0;
+  size_t n = std::strlen(t), at = 0;
+  for (size_t i = 0; i < n; ++i) {
+    const unsigned char c = (unsigned char)t[i];
+    if (c == ':') {
+      ++colons;
+      at = i;
+    }
+    if (c <= 0x20 || c >= 0x7f || c == '|' || c == ';' || c == '/') return false;
+  }
+  return colons == 1 && at > 0 && at + 1 < n;
+}
+
+}  // namespace
+
+struct unp_module {
+  hipModule_t m = nullptr;
+};
+struct unp_function {
+  hipFunction_t f = nullptr;
+};
+struct unp_event {
+  hipEvent_t e = nullptr;
+};
+
+struct unp_exec {
+  unp::Lowered l;
+  hipModule_t mod = nullptr;
+  std::vector<hipFunction_t> fns;
+  int device = 0;
+  int cu_count = 0;
+  void* ws = nullptr;  // scan: tile status words; full reduction: block partials
+  size_t ws_bytes = 0;
+  uint32_t* counter = nullptr;
+  uint32_t epoch = 0;
+  uint32_t ticket_base = 0;
+  uint32_t grid[3] = {0, 0, 0};
+  uint32_t block[3] = {0, 0, 0};
+  std::string last_entry;
+};
+
+extern "C" {
+
+// ---------------------------------------------------------------------------------------
+// Backend seam
+// ---------------------------------------------------------------------------------------
+
+const char* unp_hip_name(void) { return "hip"; }
+const char* unp_hip_provider(void) { return "unpopped-hip"; }
+int32_t unp_hip_total_integer_ops(void) { return 0; }
+
+int32_t unp_hip_supports_dtype(int32_t kind, const char* target) {
+  if (!valid_target(target)) return UNP_UNSUPPORTED;
+  const std::string t(target);
+  if (t.rfind("rocm:gfx950", 0) != 0) return UNP_UNSUPPORTED;
+  switch (kind) {
+    case UNP_F16: case UNP_BF16: case UNP_F32: case UNP_F32_STRICT: case UNP_F64:
+    case UNP_I8: case UNP_I16: case UNP_U8: case UNP_U16: case UNP_I32: case UNP_I64:
+    case UNP_BOOL: case UNP_U32: case UNP_U64: case UNP_I4: case UNP_U4:
+      return UNP_SUPPORTED;
+    default:
+      return UNP_UNSUPPORTED;
+  }
+}
+
+int32_t unp_hip_lower_form(const unp_form* form, unp_generated** out, unp_error* err) {
+  if (out) *out = nullptr;
+  if (!form || !out) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null form or output");
+    return UNP_INVALID_ARGUMENT;
+  }
+  auto* g = new unp_generated();
+  std::string why;
+  const int32_t rc = unp::lower_form(*form, g->l, why);
+  if (rc != UNP_OK) {
+    delete g;
+    set_error(err, rc, why);
+    return rc;
+  }
+  set_error(err, UNP_OK, "");
+  *out = g;
+  return UNP_OK;
+}
+
+const char* unp_generated_name(const unp_generated* g) { return g ? g->l.name.c_str() : nullptr; }
+const char* unp_generated_source(const unp_generated* g) { return g ? g->l.source.c_str() : nullptr; }
+const char* unp_generated_interface_json(const unp_generated* g) {
+  return g ? g->l.interface_json.c_str() : nullptr;
+}
+uint64_t unp_generated_revision_hash(const unp_generated* g) { return g ? unp::fnv1a64(g->l.source) : 0; }
+void unp_generated_free(unp_generated* g) { delete g; }
+
+// ---------------------------------------------------------------------------------------
+// HIP runtime FFI
+// ---------------------------------------------------------------------------------------
+
+int32_t unp_hip_device_count(int32_t* count) {
+  int n = 0;
+  const hipError_t e = hipGetDeviceCount(&n);
+  if (count) *count = (e == hipSuccess) ? n : 0;
+  return e == hipSuccess ? UNP_OK : UNP_HIP_ERROR;
+}
+
+int32_t unp_hip_set_device(int32_t device) { return hipSetDevice(device) == hipSuccess ? UNP_OK : UNP_HIP_ERROR; }
+
+int32_t unp_hip_device_info(char* arch, size_t arch_len, int32_t* cu_count) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return UNP_HIP_ERROR;
+  hipDeviceProp_t p;
+  if (hipGetDeviceProperties(&p, dev) != hipSuccess) return UNP_HIP_ERROR;
+  if (arch && arch_len) std::snprintf(arch, arch_len, "%s", p.gcnArchName);
+  if (cu_count) *cu_count = p.multiProcessorCount;
+  return UNP_OK;
+}
+
+int32_t unp_hip_module_load(const uint8_t* image, size_t len, unp_module** out, unp_error* err) {
+  if (out) *out = nullptr;
+  if (!image || !len || !out) {
+    set_error(err, UNP_INVALID_ARGUMENT, "empty code object");
+    return UNP_INVALID_ARGUMENT;
+  }
+  hipModule_t m = nullptr;
+  const hipError_t e = hipModuleLoadData(&m, image);
+  if (e != hipSuccess) return hip_fail(err, "hipModuleLoadData", e);
+  *out = new unp_module{m};
+  return UNP_OK;
+}
+
+int32_t unp_hip_module_unload(unp_module* m) {
+  if (!m) return UNP_OK;
+  const hipError_t e = hipModuleUnload(m->m);
+  delete m;
+  return e == hipSuccess ? UNP_OK : UNP_HIP_ERROR;
+}
+
+int32_t unp_hip_get_function(unp_module* m, const char* name, unp_function** out, unp_error* err) {
+  if (out) *out = nullptr;
+  if (!m || !name || !out) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null module, name or output");
+    return UNP_INVALID_ARGUMENT;
+  }
+  hipFunction_t f = nullptr;
+  const hipError_t e = hipModuleGetFunction(&f, m->m, name);
+  if (e != hipSuccess) return hip_fail(err, "hipModuleGetFunction", e);
+  *out = new unp_function{f};
+  return UNP_OK;
+}
+
+int32_t unp_hip_launch(unp_function* f, const uint32_t grid[3], const uint32_t block[3], uint32_t shared_bytes,
+                       void* stream, const void* kernarg, size_t kernarg_size, unp_error* err) {
+  if (!f || !grid || !block || (kernarg_size && !kernarg)) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null function, geometry or argument block");
+    return UNP_INVALID_ARGUMENT;
+  }
+  size_t size = kernarg_size;
+  void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(kernarg), HIP_LAUNCH_PARAM_BUFFER_SIZE,
+                    &size, HIP_LAUNCH_PARAM_END};
+  const hipError_t e = hipModuleLaunchKernel(f->f, grid[0], grid[1], grid[2], block[0], block[1], block[2],
+                                             shared_bytes, (hipStream_t)stream, nullptr, config);
+  if (e != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel", e);
+  return UNP_OK;
+}
+
+int32_t unp_hip_malloc(void** p, size_t bytes) {
+  if (!p) return UNP_INVALID_ARGUMENT;
+  *p = nullptr;
+  return hipMalloc(p, bytes ? bytes : 1) == hipSuccess ? UNP_OK : UNP_HIP_ERROR;
+}
+int32_t unp_hip_free(void* p) { return hipFree(p) == hipSuccess ? UNP_OK : UNP_HIP_ERROR; }
+int32_t unp_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) == hipSuccess ? UNP_OK : UNP_HIP_ERROR;
+}
+int32_t unp_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) == hipSuccess ? UNP_OK : UNP_HIP_ERROR;
+}
+int32_t unp_hip_memset(void* p, int32_t value, size_t bytes) {
+  return hipMemset(p, value, bytes) == hipSuccess ? UNP_OK : UNP_HIP_ERROR;
+}
+int32_t unp_hip_synchronize(void) { return hipDeviceSynchronize() == hipSuccess ? UNP_OK : UNP_HIP_ERROR; }
+
+int32_t unp_hip_event_create(unp_event** e) {
+  if (!e) return UNP_INVALID_ARGUMENT;
+  hipEvent_t h = nullptr;
+  if (hipEventCreate(&h) != hipSuccess) return UNP_HIP_ERROR;
+  *e = new unp_event{h};
+  return UNP_OK;
+}
+int32_t unp_hip_event_destroy(unp_event* e) {
+  if (!e) return UNP_OK;
+  const hipError_t r = hipEventDestroy(e->e);
+  delete e;
+  return r == hipSuccess ? UNP_OK : UNP_HIP_ERROR;
+}
+int32_t unp_hip_event_record(unp_event* e, void* stream) {
+  if (!e) return UNP_INVALID_ARGUMENT;
+  return hipEventRecord(e->e, (hipStream_t)stream) == hipSuccess ? UNP_OK : UNP_HIP_ERROR;
+}
+int32_t unp_hip_event_synchronize(unp_event* e) {
+  if (!e) return UNP_INVALID_ARGUMENT;
+  return hipEventSynchronize(e->e) == hipSuccess ? UNP_OK : UNP_HIP_ERROR;
+}
+int32_t unp_hip_event_elapsed_ms(unp_event* start, unp_event* stop, float* ms) {
+  if (!start || !stop || !ms) return UNP_INVALID_ARGUMENT;
+  return hipEventElapsedTime(ms, start->e, stop->e) == hipSuccess ? UNP_OK : UNP_HIP_ERROR;
+}
+
+// ---------------------------------------------------------------------------------------
+// Prepared kernels
+// ---------------------------------------------------------------------------------------
+
+int32_t unp_hip_exec_create(const unp_generated* g, unp_exec** out, unp_error* err) {
+  if (out) *out = nullptr;
+  if (!g || !out) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null kernel or output");
+    return UNP_INVALID_ARGUMENT;
+  }
+  auto* x = new unp_exec();
+  x->l = g->l;
+  if (hipGetDevice(&x->device) != hipSuccess) {
+    delete x;
+    set_error(err, UNP_HIP_ERROR, "hipGetDevice failed (no HIP device)");
+    return UNP_HIP_ERROR;
+  }
+  hipDeviceProp_t p;
+  hipError_t e = hipGetDeviceProperties(&p, x->device);
+  if (e != hipSuccess) {
+    delete x;
+    return hip_fail(err, "hipGetDeviceProperties", e);
+  }
+  x->cu_count = p.multiProcessorCount;
+  std::vector<uint8_t> code;
+  std::string log;
+  const int32_t rc = unp::compile_source(x->l.source, x->l.name, 0, code, log);
+  if (rc != UNP_OK) {
+    delete x;
+    set_error(err, rc, log);
+    return rc;
+  }
+  e = hipModuleLoadData(&x->mod, code.data());
+  if (e != hipSuccess) {
+    delete x;
+    return hip_fail(err, "hipModuleLoadData", e);
+  }
+  for (const auto& en : x->l.entries) {
+    hipFunction_t f = nullptr;
+    e = hipModuleGetFunction(&f, x->mod, en.symbol.c_str());
+    if (e != hipSuccess) {
+      hipModuleUnload(x->mod);
+      delete x;
+      return hip_fail(err, ("hipModuleGetFunction " + en.symbol).c_str(), e);
+    }
+    x->fns.push_back(f);
+  }
+  set_error(err, UNP_OK, "");
+  *out = x;
+  return UNP_OK;
+}
+
+void unp_hip_exec_destroy(unp_exec* x) {
+  if (!x) return;
+  if (x->ws) hipFree(x->ws);
+  if (x->counter) hipFree(x->counter);
+  if (x->mod) hipModuleUnload(x->mod);
+  delete x;
+}
+
+int32_t unp_hip_exec_last_launch(const unp_exec* x, uint32_t grid[3], uint32_t block[3], char* entry,
+                                 size_t entry_len) {
+  if (!x) return UNP_INVALID_ARGUMENT;
+  for (int i = 0; i < 3; ++i) {
+    if (grid) grid[i] = x->grid[i];
+    if (block) block[i] = x->block[i];
+  }
+  if (entry && entry_len) std::snprintf(entry, entry_len, "%s", x->last_entry.c_str());
+  return UNP_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+bool aligned16(uint64_t p) { return (p & 15u) == 0; }
+
+// Reads the KernelFn-ordered arguments: `nbuf` buffers then `nscal` scalars.
+struct Args {
+  std::vector<uint64_t> buf;
+  std::vector<int64_t> ext;
+};
+
+int32_t take_args(const unp_arg* a, size_t n, size_t nbuf, size_t nscal, Args& out, unp_error* err) {
+  if (n != nbuf + nscal || (n && !a)) {
+    set_error(err, UNP_INVALID_ARGUMENT,
+              "expected " + std::to_string(nbuf) + " buffers and " + std::to_string(nscal) + " scalars, got " +
+                  std::to_string(n) + " arguments");
+    return UNP_INVALID_ARGUMENT;
+  }
+  for (size_t i = 0; i < n; ++i) {
+    const bool want_buf = i < nbuf;
+    if ((a[i].is_buffer != 0) != want_buf) {
+      set_error(err, UNP_INVALID_ARGUMENT, "argument " + std::to_string(i) + (want_buf ? " must be a buffer" : " must be a scalar"));
+      return UNP_INVALID_ARGUMENT;
+    }
+    if (want_buf) out.buf.push_back(a[i].value);
+    else out.ext.push_back((int64_t)a[i].value);
+  }
+  return UNP_OK;
+}
+
+// The reference's extents are I32 scalars: read the low 32 bits as signed.
+int32_t extents_i32(Args& A, size_t count, unp_error* err) {
+  for (size_t i = 0; i < count; ++i) {
+    const int64_t v = (int64_t)(int32_t)(uint32_t)(uint64_t)A.ext[i];
+    if (v < 0) {
+      set_error(err, UNP_INVALID_ARGUMENT, "extent n" + std::to_string(i) + " is negative");
+      return UNP_INVALID_ARGUMENT;
+    }
+    A.ext[i] = v;
+  }
+  return UNP_OK;
+}
+
+int32_t need_buffers(const Args& A, bool any_elements, unp_error* err) {
+  if (!any_elements) return UNP_OK;
+  for (size_t i = 0; i < A.buf.size(); ++i)
+    if (A.buf[i] == 0) {
+      set_error(err, UNP_INVALID_ARGUMENT, "buffer argument " + std::to_string(i) + " is null");
+      return UNP_INVALID_ARGUMENT;
+    }
+  return UNP_OK;
+}
+
+int32_t ensure_ws(unp_exec* x, size_t bytes, bool need_counter, unp_error* err) {
+  if (need_counter && !x->counter) {
+    hipError_t e = hipMalloc((void**)&x->counter, sizeof(uint32_t));
+    if (e != hipSuccess) return hip_fail(err, "hipMalloc(counter)", e);
+    e = hipMemset(x->counter, 0, sizeof(uint32_t));
+    if (e != hipSuccess) return hip_fail(err, "hipMemset(counter)", e);
+  }
+  if (bytes > x->ws_bytes) {
+    if (x->ws) {
+      hipFree(x->ws);
+      x->ws = nullptr;
+      x->ws_bytes = 0;
+    }
+    hipError_t e = hipMalloc(&x->ws, bytes);
+    if (e != hipSuccess) return hip_fail(err, "hipMalloc(workspace)", e);
+    e = hipMemset(x->ws, 0, bytes);
+    if (e != hipSuccess) return hip_fail(err, "hipMemset(workspace)", e);
+    x->ws_bytes = bytes;
+  }
+  return UNP_OK;
+}
+
+int32_t launch(unp_exec* x, size_t entry, uint32_t grid, void** params, hipStream_t s, unp_error* err) {
+  x->grid[0] = grid;
+  x->grid[1] = x->grid[2] = 1;
+  x->block[0] = (uint32_t)x->l.threads;
+  x->block[1] = x->block[2] = 1;
+  x->last_entry = x->l.entries[entry].symbol;
+  const hipError_t e = hipModuleLaunchKernel(x->fns[entry], grid, 1, 1, (uint32_t)x->l.threads, 1, 1, 0, s, params,
+                                             nullptr);
+  if (e != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel", e);
+  return UNP_OK;
+}
+
+size_t pick(const unp_exec* x, bool fast_ok) {
+  for (size_t i = 0; i < x->l.entries.size(); ++i)
+    if (x->l.entries[i].fast == fast_ok) return i;
+  return x->l.entries.size() - 1;
+}
+
+int64_t product(const std::vector<int64_t>& v, size_t from, size_t to) {
+  int64_t p = 1;
+  for (size_t i = from; i < to; ++i) p *= v[i];
+  return p;
+}
+
+int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  const unp_form& f = x->l.form;
+  const bool two = f.kind == UNP_FORM_ROW_REDUCE2;
+  Args A;
+  int32_t rc = take_args(a, n, two ? 3 : 2, (size_t)f.rank, A, err);
+  if (rc == UNP_OK) rc = extents_i32(A, (size_t)f.rank, err);
+  if (rc != UNP_OK) return rc;
+  const long long rows = product(A.ext, 0, (size_t)f.reduced_from);
+  const long long cols = product(A.ext, (size_t)f.reduced_from, (size_t)f.rank);
+  if ((rc = need_buffers(A, rows > 0, err)) != UNP_OK) return rc;
+  if (rows == 0) return UNP_OK;
+  const int vec = 16 / (int)unp::kind_bytes(f.dtype);
+  uint64_t in = A.buf[0], o0 = A.buf[1], o1 = two ? A.buf[2] : A.buf[1];
+  const size_t entry = pick(x, cols % vec == 0 && aligned16(in));
+  const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+  if (x->l.reduce_all) {
+    const size_t acc_bytes = 8;
+    if ((rc = ensure_ws(x, grid * acc_bytes, true, err)) != UNP_OK) return rc;
+    long long nn = cols;
+    void* ws = x->ws;
+    void* cnt = x->counter;
+    void* params[] = {&in, &o0, &nn, &ws, &cnt};
+    return launch(x, entry, grid, params, s, err);
+  }
+  long long r = rows, c = cols;
+  void* params[] = {&in, &o0, &o1, &r, &c};
+  return launch(x, entry, grid, params, s, err);
+}
+
+int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  const unp_form& f = x->l.form;
+  Args A;
+  int32_t rc = take_args(a, n, 2, (size_t)f.rank, A, err);
+  if (rc == UNP_OK) rc = extents_i32(A, (size_t)f.rank, err);
+  if (rc != UNP_OK) return rc;
+  long long rows = product(A.ext, 0, (size_t)f.rank - 1);
+  long long cols = A.ext[(size_t)f.rank - 1];
+  if ((rc = need_buffers(A, rows > 0 && cols > 0, err)) != UNP_OK) return rc;
+  if (rows == 0 || cols == 0) return UNP_OK;
+  const int vec = 16 / (int)unp::kind_bytes(f.dtype);
+  uint64_t in = A.buf[0], out = A.buf[1];
+  const size_t entry = pick(x, cols % vec == 0 && aligned16(in) && aligned16(out));
+  const unp::Entry& en = x->l.entries[entry];
+  const long long tile = 64LL * en.vec * en.k;
+  const unsigned long long tiles = (unsigned long long)rows * (unsigned long long)((cols + tile - 1) / tile);
+  const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+  const unsigned long long waves = (unsigned long long)grid * (x->l.threads / 64);
+  if (tiles + waves >= (1ull << 31)) {
+    set_error(err, UNP_INVALID_ARGUMENT, "too many scan tiles for one launch");
+    return UNP_INVALID_ARGUMENT;
+  }
+  const bool wide = (f.dtype == UNP_F32 && f.op0 == UNP_OP_SUM) || unp::kind_bytes(f.dtype) == 8;
+  const size_t words = wide ? 4 : 2;
+  if ((rc = ensure_ws(x, (size_t)tiles * words * 8, true, err)) != UNP_OK) return rc;
+  if (x->epoch == 0xffffffffu) {
+    // After 2^32 - 1 launches the tags would repeat: clear the words and restart at epoch 1.
+    const hipError_t e = hipMemsetAsync(x->ws, 0, x->ws_bytes, s);
+    if (e != hipSuccess) return hip_fail(err, "hipMemsetAsync(status)", e);
+    x->epoch = 0;
+  }
+  x->epoch += 1;  // the words start zeroed, so epoch 1 is never seen before the first launch
+  uint32_t tb = x->ticket_base, ep = x->epoch;
+  void* st = x->ws;
+  void* cnt = x->counter;
+  void* params[] = {&in, &out, &rows, &cols, &st, &cnt, &tb, &ep};
+  rc = launch(x, entry, grid, params, s, err);
+  if (rc == UNP_OK) x->ticket_base = (uint32_t)(x->ticket_base + (uint32_t)(tiles + waves));
+  return rc;
+}
+
+int32_t run_gather(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  const unp_form& f = x->l.form;
+  Args A;
+  int32_t rc = take_args(a, n, 3, (size_t)f.rank + 1, A, err);
+  if (rc == UNP_OK) rc = extents_i32(A, (size_t)f.rank, err);
+  if (rc != UNP_OK) return rc;
+  const long long n_rows = A.ext[0];
+  const long long row_elems = product(A.ext, 1, (size_t)f.rank);
+  const long long row_bytes = row_elems * (long long)unp::kind_bytes(f.dtype);
+  if ((rc = need_buffers(A, n_rows > 0 && row_bytes > 0, err)) != UNP_OK) return rc;
+  if (n_rows == 0 || row_bytes == 0) return UNP_OK;
+  uint64_t table = A.buf[f.data_slot == 0 ? 0 : 1];
+  uint64_t ids = A.buf[f.data_slot == 0 ? 1 : 0];
+  uint64_t out = A.buf[2];
+  const uint64_t raw_ext = (uint64_t)A.ext[(size_t)f.rank];
+  int32_t ext32 = 0;
+  uint32_t extu32 = 0;
+  long long ext64 = 0;
+  bool empty_source = false;
+  if (f.index_dtype == UNP_I32) {
+    ext32 = (int32_t)(uint32_t)raw_ext;
+    empty_source = ext32 <= 0;
+  } else if (f.index_dtype == UNP_U32) {
+    extu32 = (uint32_t)raw_ext;
+    empty_source = extu32 == 0;
+  } else {
+    ext64 = (long long)raw_ext;
+    empty_source = ext64 <= 0;
+  }
+  if (empty_source && f.oob == UNP_OOB_CLAMP) {
+    // Clamping into an empty source has no row to read.
+    set_error(err, UNP_INVALID_ARGUMENT, "a Clamp gather needs a source extent of at least 1");
+    return UNP_INVALID_ARGUMENT;
+  }
+  const size_t entry = pick(x, row_bytes % 16 == 0 && aligned16(table) && aligned16(out));
+  const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+  long long nr = n_rows, rb = row_bytes;
+  void* ext_arg = f.index_dtype == UNP_I32 ? (void*)&ext32 : (f.index_dtype == UNP_U32 ? (void*)&extu32 : (void*)&ext64);
+  void* params[] = {&table, &ids, &out, &nr, &rb, ext_arg};
+  return launch(x, entry, grid, params, s, err);
+}
+
+int32_t run_dequant(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  Args A;
+  int32_t rc = take_args(a, n, 4, 2, A, err);
+  if (rc == UNP_OK) rc = extents_i32(A, 2, err);
+  if (rc != UNP_OK) return rc;
+  long long rows = A.ext[0], cols = A.ext[1];
+  if ((rc = need_buffers(A, rows > 0 && cols > 0, err)) != UNP_OK) return rc;
+  if (rows == 0 || cols == 0) return UNP_OK;
+  uint64_t q = A.buf[0], sc = A.buf[1], zp = A.buf[2], out = A.buf[3];
+  const bool fast_ok = cols % 32 == 0 && aligned16(q) && aligned16(out) && (sc & 1) == 0;
+  size_t entry = pick(x, fast_ok);
+  if (x->l.entries[entry].fast && !fast_ok) entry = x->l.entries.size() - 1;
+  const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+  void* params[] = {&q, &sc, &zp, &out, &rows, &cols};
+  return launch(x, entry, grid, params, s, err);
+}
+
+}  // namespace
+
+extern "C" int32_t unp_hip_exec_launch(unp_exec* x, const unp_arg* args, size_t nargs, void* stream,
+                                       unp_error* err) {
+  if (!x) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null executor");
+    return UNP_INVALID_ARGUMENT;
+  }
+  set_error(err, UNP_OK, "");
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur != x->device) {
+    set_error(err, UNP_INVALID_ARGUMENT, "the executor was created on another device");
+    return UNP_INVALID_ARGUMENT;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  switch (x->l.form.kind) {
+    case UNP_FORM_REDUCTION:
+    case UNP_FORM_ROW_REDUCE2:
+      return run_reduction(x, args, nargs, s, err);
+    case UNP_FORM_SCAN:
+      return run_scan(x, args, nargs, s, err);
+    case UNP_FORM_GATHER:
+      return run_gather(x, args, nargs, s, err);
+    case UNP_FORM_DEQUANT4:
+      return run_dequant(x, args, nargs, s, err);
+    default:
+      set_error(err, UNP_UNSUPPORTED_KERNEL, "unknown form");
+      return UNP_UNSUPPORTED_KERNEL;
+  }
+}

@@ -1,0 +1,59 @@
+// Internal declarations shared by the unpopped-hip host library's translation units.
+#pragma once
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/unpopped_hip.h"
+
+namespace unp {
+
+// Element kinds the HIP forms move or compute (names as the reference's JSON spells them,
+// crates/unpopped/src/text.rs:56-91).
+const char* kind_name(int32_t kind);
+int32_t kind_from_name(const std::string& s);  // -1 when unknown
+size_t kind_bytes(int32_t kind);                // 0 for sub-byte and unknown kinds
+bool kind_is_float(int32_t kind);
+bool kind_is_int(int32_t kind);
+
+// One entry point of a lowered kernel and when the executor picks it.
+struct Entry {
+  std::string symbol;
+  int vec = 1;        // elements per lane-vector (reduce/scan), bytes per unit (gather)
+  int k = 1;          // vectors per lane per tile (scan)
+  bool fast = false;  // the 16-byte-aligned path
+};
+
+// A lowered form: what the executor needs to launch it.
+struct Lowered {
+  unp_form form{};
+  std::string name;
+  std::string source;
+  std::string interface_json;
+  std::vector<Entry> entries;
+  bool reduce_all = false;  // a reduction with no kept axis
+  int threads = 256;
+  int blocks_per_cu = 8;
+};
+
+// Emit the HIP source and interface for `f`; on refusal returns a nonzero unp_status and
+// fills `detail`.
+int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail);
+
+// hipRTC for gfx950, with an in-process compile-once cache keyed by source text.
+int32_t compile_source(const std::string& source, const std::string& entry, uint32_t max_ms,
+                       std::vector<uint8_t>& code, std::string& log);
+
+// FNV-1a 64 (crates/unpopped/src/revision.rs).
+uint64_t fnv1a64(const std::string& s);
+
+void set_error(unp_error* err, int32_t code, const std::string& detail);
+
+}  // namespace unp
+
+struct unp_generated {
+  unp::Lowered l;
+};

@@ -1,0 +1,98 @@
+"""Run one lowered form on the GPU through the C ABI: numpy in, numpy out.
+
+Used by the GPU parity tests, the smoke check and the benchmark; every result comes
+from a HIP kernel launched by ``unp_hip_exec_launch``.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import unpopped_amd as u
+
+_backend = u.HipBackend()
+_execs: dict = {}
+
+NP_KIND = {np.float32: "F32", np.float64: "F64", np.int32: "I32", np.int64: "I64", np.uint32: "U32",
+           np.uint16: "Bf16", np.uint8: "U8"}
+
+
+def executor(**form) -> u.Executor:
+    key = tuple(sorted(form.items()))
+    if key not in _execs:
+        _execs[key] = u.Executor(_backend.lower_form(**form))
+    return _execs[key]
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+
+
+def reduce_rows(x: np.ndarray, op: str, op1: str | None = None):
+    """Fold each row of a 2-D array (op1: a second fold of the same read, ROW_REDUCE2)."""
+    rows, cols = x.shape
+    kind = NP_KIND[x.dtype.type]
+    two = op1 is not None
+    ex = executor(kind="row_reduce2" if two else "reduction", dtype=kind, rank=2, op=op,
+                  op1=op1 or "Max", reduced_from=1)
+    din = u.DeviceBuffer.from_array(x)
+    o0 = u.DeviceBuffer(max(rows, 1) * x.itemsize)
+    if two:
+        o1 = u.DeviceBuffer(max(rows, 1) * x.itemsize)
+        ex.launch(din, o0, o1, rows, cols)
+    else:
+        ex.launch(din, o0, rows, cols)
+    u.synchronize()
+    r0 = o0.download(x.dtype, rows)
+    return (r0, o1.download(x.dtype, rows)) if two else r0
+
+
+def reduce_all(x: np.ndarray, op: str):
+    kind = NP_KIND[x.dtype.type]
+    ex = executor(kind="reduction", dtype=kind, rank=1, op=op, reduced_from=0)
+    din = u.DeviceBuffer.from_array(x)
+    out = u.DeviceBuffer(16)
+    ex.launch(din, out, x.size)
+    u.synchronize()
+    return out.download(x.dtype, 1)[0]
+
+
+def scan_rows(x: np.ndarray, op: str, exclusive=False, reverse=False) -> np.ndarray:
+    x2 = x.reshape(1, -1) if x.ndim == 1 else x
+    rows, cols = x2.shape
+    kind = NP_KIND[x.dtype.type]
+    ex = executor(kind="scan", dtype=kind, rank=2, op=op, exclusive=exclusive, reverse=reverse)
+    din = u.DeviceBuffer.from_array(x2)
+    dout = u.DeviceBuffer(max(x2.nbytes, 1))
+    ex.launch(din, dout, rows, cols)
+    u.synchronize()
+    return dout.download(x.dtype, rows * cols).reshape(x.shape)
+
+
+def gather_rows(table: np.ndarray, ids: np.ndarray, oob: str, out_init: np.ndarray | None = None,
+                src_extent: int | None = None, elem_kind: str | None = None) -> np.ndarray:
+    """out[r] = table[clamp(ids[r])] under the policy; ``table`` is (V, ...) of any dtype."""
+    n = ids.shape[0]
+    inner = table.shape[1:]
+    kind = elem_kind or NP_KIND[table.dtype.type]
+    rank = 1 + len(inner)
+    ex = executor(kind="gather", dtype=kind, rank=rank, index_dtype=NP_KIND[ids.dtype.type], oob=oob)
+    dt = u.DeviceBuffer.from_array(table)
+    di = u.DeviceBuffer.from_array(ids)
+    out_shape = (n,) + inner
+    out0 = np.zeros(out_shape, table.dtype) if out_init is None else out_init
+    do = u.DeviceBuffer.from_array(out0)
+    ext = table.shape[0] if src_extent is None else src_extent
+    ex.launch(dt, di, do, n, *inner, ext)
+    u.synchronize()
+    return do.download(table.dtype, int(np.prod(out_shape))).reshape(out_shape)
+
+
+def dequant4(q_packed, scales, zeros_packed, rows, cols, group, q_kind="U4", z_kind="U4") -> np.ndarray:
+    ex = executor(kind="dequant4", q_kind=q_kind, z_kind=z_kind, group=group, out_kind="Bf16")
+    dq = u.DeviceBuffer.from_array(q_packed)
+    ds = u.DeviceBuffer.from_array(scales)
+    dz = u.DeviceBuffer.from_array(zeros_packed)
+    do = u.DeviceBuffer(max(rows * cols * 2, 1))
+    ex.launch(dq, ds, dz, do, rows, cols)
+    u.synchronize()
+    return do.download(np.uint16, rows * cols).reshape(rows, cols)
