@@ -201,27 +201,41 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
   L.name = name.str();
   std::ostringstream src;
   src << header(L.name, f);
-  for (int fast = 1; fast >= 0; --fast) {
-    Entry e;
-    e.fast = fast;
-    e.vec = fast ? V : 1;
-    e.symbol = L.name + (fast ? "_v" : "_s");
-    const int unroll = fast ? 4 : 8;
-    if (L.reduce_all) {
-      L.blocks_per_cu = 4;
-      src << "extern \"C\" __global__ void " << kLaunchBounds << " " << e.symbol << "(const " << T
-          << "* in, " << T << "* out, long long n, typename unp::acc<" << T << ", " << f.op0
-          << ">::type* partials, unsigned* counter) {\n  unp::reduce_all<" << T << ", " << f.op0
-          << ", " << e.vec << ", 256, " << unroll << ">(in, out, n, partials, counter);\n}\n";
-    } else {
-      L.blocks_per_cu = 8;
-      src << "extern \"C\" __global__ void " << kLaunchBounds << " " << e.symbol << "(const " << T
-          << "* in, " << T << "* out0, " << T << "* out1, long long rows, long long cols) {\n"
-          << "  unp::rowreduce<" << T << ", " << f.op0 << ", " << (two ? f.op1 : f.op0) << ", "
-          << (two ? 2 : 1) << ", " << e.vec << ", 256, " << unroll
-          << ">(in, out0, out1, rows, cols);\n}\n";
+  if (L.reduce_all) {
+    // One block per CU (8 waves): the read rate peaks with few streams per CU.
+    L.threads = 512;
+    L.blocks_per_cu = 1;
+    for (int fast = 1; fast >= 0; --fast) {
+      Entry e;
+      e.fast = fast;
+      e.vec = fast ? V : 1;
+      e.symbol = L.name + (fast ? "_v" : "_s");
+      src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol << "(const " << T << "* in, " << T
+          << "* out, long long n, typename unp::acc<" << T << ", " << f.op0
+          << ">::type* partials, unsigned* counter) {\n  unp::reduce_all<" << T << ", " << f.op0 << ", " << e.vec
+          << ", 512, " << (fast ? 4 : 8) << ">(in, out, n, partials, counter);\n}\n";
+      L.entries.push_back(e);
     }
-    L.entries.push_back(e);
+  } else {
+    // Rows up to kWideRow (32768) elements: one wave per row (no barrier); longer rows: one
+    // block per row with the LDS combine.  Both read the row once and stream it past the caches.
+    L.threads = 512;
+    L.blocks_per_cu = 1;
+    for (int wide = 0; wide <= 1; ++wide) {
+      for (int fast = 1; fast >= 0; --fast) {
+        Entry e;
+        e.fast = fast;
+        e.wide = wide;
+        e.vec = fast ? V : 1;
+        e.symbol = L.name + (wide ? "_b" : "_w") + (fast ? "v" : "s");
+        const int unroll = wide ? (fast ? 4 : 8) : (fast ? 8 : 16);
+        src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol << "(const " << T << "* in, " << T
+            << "* out0, " << T << "* out1, long long rows, long long cols) {\n  unp::"
+            << (wide ? "rowreduce<" : "rowreduce_wave<") << T << ", " << f.op0 << ", " << (two ? f.op1 : f.op0) << ", "
+            << (two ? 2 : 1) << ", " << e.vec << ", 512, " << unroll << ">(in, out0, out1, rows, cols);\n}\n";
+        L.entries.push_back(e);
+      }
+    }
   }
   L.source = src.str();
   std::ostringstream j;
@@ -233,15 +247,15 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
     << (two ? "{\"name\":\"out0\",\"kind\":\"buffer\",\"role\":\"Write\"},{\"name\":\"out1\",\"kind\":\"buffer\",\"role\":\"Write\"}"
             : "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}");
   for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
-  j << "],\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
+  j << "],\"launch\":{\"block\":[" << L.threads << ",1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
     << "\",\"grid_policy\":\"device-class constant; "
     << (L.reduce_all ? "blocks stride over 16-byte vectors, last-ticket block folds the partials"
-                     : "blocks stride over rows")
+                     : "waves stride over rows (one wave per row); rows longer than 32768 elements: one block per row")
     << "\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
-      << ",\"when\":\"" << (L.entries[i].fast ? "reduced extent % vec == 0 and in0 16-byte aligned" : "otherwise")
-      << "\"}";
+      << ",\"when\":\"" << (L.entries[i].wide ? "reduced extent > 32768; " : "")
+      << (L.entries[i].fast ? "reduced extent % vec == 0 and in0 16-byte aligned" : "otherwise") << "\"}";
   j << "],\"workspace\":"
     << (L.reduce_all ? "{\"partials\":\"grid * accumulator bytes\",\"counter\":4}" : "null")
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
@@ -278,7 +292,10 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
   name << "unp_scan_" << (f.exclusive ? "excl_" : "incl_") << (f.reverse ? "rev_" : "") << op_name(f.op0)
        << "_" << lower_name(f.dtype);
   L.name = name.str();
-  L.blocks_per_cu = 4;
+  // One block of kScanWaves waves per CU; one ticket per block per round.
+  constexpr int kScanWaves = 8;
+  L.threads = 64 * kScanWaves;
+  L.blocks_per_cu = 1;
   // Tile = 64 lanes x VEC x K.  An 8-byte carry (f32 Sum in f64, F64, I64) halves K to keep
   // the per-lane registers (K vectors in flight plus K carries) within occupancy.
   const bool wide_carry = (f.dtype == UNP_F32 && f.op0 == UNP_OP_SUM) || kind_bytes(f.dtype) == 8;
@@ -289,12 +306,14 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     e.fast = fast;
     e.vec = fast ? vec_of(f.dtype) : 1;
     e.k = fast ? (wide_carry ? 8 : 16) : (wide_carry ? 16 : 32);
+    e.wpb = kScanWaves;
     e.symbol = L.name + (fast ? "_v" : "_s");
-    src << "extern \"C\" __global__ void " << kLaunchBounds << " " << e.symbol << "(const " << T
+    src << "extern \"C\" __global__ void __launch_bounds__(" << L.threads << ") " << e.symbol << "(const " << T
         << "* in, " << T << "* out, long long rows, long long cols, unsigned long long* status, "
         << "unsigned* counter, unsigned ticket_base, unsigned epoch) {\n  unp::scan_lookback<" << T << ", "
         << f.op0 << ", " << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false")
-        << ", " << e.vec << ", " << e.k << ">(in, out, rows, cols, status, counter, ticket_base, epoch);\n}\n";
+        << ", " << e.vec << ", " << e.k << ", " << e.wpb
+        << ">(in, out, rows, cols, status, counter, ticket_base, epoch);\n}\n";
     L.entries.push_back(e);
   }
   L.source = src.str();
@@ -304,8 +323,9 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     << ",\"reverse\":" << (f.reverse ? "true" : "false") << ",\"rank\":" << f.rank
     << ",\"params\":[{\"name\":\"in0\",\"kind\":\"buffer\",\"role\":\"Read\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
   for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
-  j << "],\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
-    << "\",\"grid_policy\":\"persistent waves draw tile tickets; one wave per tile\"},\"entries\":[";
+  j << "],\"launch\":{\"block\":[" << L.threads << ",1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
+    << "\",\"grid_policy\":\"persistent blocks draw one group ticket per round; wave w takes tile ticket*"
+    << kScanWaves << "+w\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
       << ",\"k\":" << L.entries[i].k << ",\"tile\":" << 64 * L.entries[i].vec * L.entries[i].k << ",\"when\":\""
@@ -352,7 +372,8 @@ static int32_t lower_gather(const unp_form& f, Lowered& L, std::string& why) {
   name << "unp_gather_rows_" << lower_name(f.dtype) << "_by_" << lower_name(f.index_dtype) << "_"
        << oob_name(f.oob);
   L.name = name.str();
-  L.blocks_per_cu = 8;
+  L.threads = 256;
+  L.blocks_per_cu = 1;
   std::ostringstream src;
   src << header(L.name, f);
   const int units[2] = {16, (int)eb};
@@ -412,7 +433,8 @@ static int32_t lower_dequant(const unp_form& f, Lowered& L, std::string& why) {
   std::ostringstream name;
   name << "unp_dequant_" << lower_name(f.q_kind) << "_z" << lower_name(f.z_kind) << "_g" << f.group << "_bf16";
   L.name = name.str();
-  L.blocks_per_cu = 8;
+  L.threads = 256;
+  L.blocks_per_cu = 1;
   std::ostringstream src;
   src << header(L.name, f);
   const char* sig =

@@ -147,6 +147,34 @@ template <class T, int N> UNP_DEV void stv(T* p, const vec<T, N>& v) {
   *reinterpret_cast<vec<T, N>*>(p) = v;
 }
 
+// Streaming (nontemporal) 16/8/4-byte vector accesses: data read or written once are not
+// kept in the caches.  Other widths fall back to plain accesses.
+typedef u32 u32x4_t __attribute__((ext_vector_type(4)));
+typedef u32 u32x2_t __attribute__((ext_vector_type(2)));
+
+template <class T, int N> UNP_DEV vec<T, N> ld_nt(const T* p) {
+  if constexpr (sizeof(T) * N == 16) {
+    return __builtin_bit_cast(vec<T, N>, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
+  } else if constexpr (sizeof(T) * N == 8) {
+    return __builtin_bit_cast(vec<T, N>, __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p)));
+  } else if constexpr (sizeof(T) * N == 4) {
+    return __builtin_bit_cast(vec<T, N>, __builtin_nontemporal_load(reinterpret_cast<const u32*>(p)));
+  } else {
+    return ld<T, N>(p);
+  }
+}
+template <class T, int N> UNP_DEV void st_nt(T* p, const vec<T, N>& v) {
+  if constexpr (sizeof(T) * N == 16) {
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), reinterpret_cast<u32x4_t*>(p));
+  } else if constexpr (sizeof(T) * N == 8) {
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x2_t, v), reinterpret_cast<u32x2_t*>(p));
+  } else if constexpr (sizeof(T) * N == 4) {
+    __builtin_nontemporal_store(__builtin_bit_cast(u32, v), reinterpret_cast<u32*>(p));
+  } else {
+    stv<T, N>(p, v);
+  }
+}
+
 template <class X> UNP_DEV u64 to_bits64(X v) {
   if constexpr (sizeof(X) == 4) return (u64)__builtin_bit_cast(u32, v);
   else return __builtin_bit_cast(u64, v);
@@ -266,8 +294,59 @@ template <class X> UNP_DEV X load_agent(const X* p) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Row reduction: rows x cols row-major, one or two folds of each row read once.
-// Blocks stride over rows (row = blockIdx.x; += gridDim.x), as the launched reduction
+// Row reduction, one wave per row: waves stride over rows (the outermost kept axis, as
+// kernel_lift/block_reduce.rs:313-338 strides blocks over it); lane l folds the vectors
+// l, l + 64, ... of its row (U of them in flight), then the wave combines by DPP and lane 0
+// stores.  No LDS and no barrier: the schedule for rows up to a few thousand vectors.
+// ---------------------------------------------------------------------------------------
+template <class T, int OP0, int OP1, int NOUT, int VEC, int THREADS, int U>
+UNP_DEV void rowreduce_wave(const T* __restrict__ in, T* __restrict__ out0, T* __restrict__ out1, i64 rows,
+                            i64 cols) {
+  typedef typename acc<T, OP0>::type A0;
+  typedef typename acc<T, OP1>::type A1;
+  typedef fold<A0, OP0> F0;
+  typedef fold<A1, OP1> F1;
+  constexpr i64 STEP = (i64)64 * VEC;
+  const int lane = threadIdx.x & 63;
+  const i64 nwaves = (i64)gridDim.x * (THREADS / 64);
+  for (i64 row = (i64)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6); row < rows; row += nwaves) {
+    const T* __restrict__ p = in + row * cols;
+    A0 a0 = F0::identity();
+    A1 a1 = F1::identity();
+    i64 c = (i64)lane * VEC;
+    for (; c + (U - 1) * STEP < cols; c += U * STEP) {
+      vec<T, VEC> v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = ld_nt<T, VEC>(p + c + u * STEP);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          a0 = F0::apply(a0, (A0)v[u].e[e]);
+          if constexpr (NOUT > 1) a1 = F1::apply(a1, (A1)v[u].e[e]);
+        }
+      }
+    }
+    for (; c < cols; c += STEP) {
+      const vec<T, VEC> v = ld_nt<T, VEC>(p + c);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        a0 = F0::apply(a0, (A0)v.e[e]);
+        if constexpr (NOUT > 1) a1 = F1::apply(a1, (A1)v.e[e]);
+      }
+    }
+    a0 = wave_reduce<A0, OP0>(a0);
+    if constexpr (NOUT > 1) a1 = wave_reduce<A1, OP1>(a1);
+    if (lane == 0) {
+      out0[row] = finish<T, OP0>(a0, cols);
+      if constexpr (NOUT > 1) out1[row] = finish<T, OP1>(a1, cols);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Row reduction, one block per row: rows x cols row-major, one or two folds of each row read
+// once.  Blocks stride over rows (row = blockIdx.x; += gridDim.x), as the launched reduction
 // lift strides over its outermost kept axis (kernel_lift/block_reduce.rs:313-338).
 // Inside a row, thread t folds the vectors t, t + THREADS, ... (VEC elements each) in
 // ascending order; waves combine by DPP, blocks by LDS in wave order.
@@ -293,7 +372,7 @@ UNP_DEV void rowreduce(const T* __restrict__ in, T* __restrict__ out0, T* __rest
     for (; c + (UNROLL - 1) * STEP < cols; c += UNROLL * STEP) {
       vec<T, VEC> v[UNROLL];
 #pragma unroll
-      for (int u = 0; u < UNROLL; ++u) v[u] = ld<T, VEC>(p + c + u * STEP);
+      for (int u = 0; u < UNROLL; ++u) v[u] = ld_nt<T, VEC>(p + c + u * STEP);
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) {
 #pragma unroll
@@ -304,7 +383,7 @@ UNP_DEV void rowreduce(const T* __restrict__ in, T* __restrict__ out0, T* __rest
       }
     }
     for (; c < cols; c += STEP) {
-      const vec<T, VEC> v = ld<T, VEC>(p + c);
+      const vec<T, VEC> v = ld_nt<T, VEC>(p + c);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         a0 = F0::apply(a0, (A0)v.e[e]);
@@ -358,7 +437,7 @@ UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
   for (; c + (UNROLL - 1) * STEP < n; c += UNROLL * STEP) {
     vec<T, VEC> v[UNROLL];
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) v[u] = ld<T, VEC>(in + c + u * STEP);
+    for (int u = 0; u < UNROLL; ++u) v[u] = ld_nt<T, VEC>(in + c + u * STEP);
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
 #pragma unroll
@@ -366,7 +445,7 @@ UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
     }
   }
   for (; c < n; c += STEP) {
-    const vec<T, VEC> v = ld<T, VEC>(in + c);
+    const vec<T, VEC> v = ld_nt<T, VEC>(in + c);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) a = F::apply(a, (A)v.e[e]);
   }
@@ -392,16 +471,20 @@ UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
 // Single-pass scan with decoupled look-back, along the innermost axis of rows x cols.
 //
 // A tile is TILE = 64 * VEC * K consecutive scan positions of one row, owned by one wave.
-// Waves are persistent: each draws tile tickets from `counter` until the tickets run out,
-// so a wave only ever waits on tiles whose tickets were drawn earlier (forward progress).
-// Loads are striped: load k of lane l covers positions (k * 64 + l) * VEC .. + VEC, so every
-// load instruction of a wave reads 64 * VEC contiguous elements.
+// Blocks of WPB waves are persistent: each round, one thread draws a group ticket from
+// `counter` and wave w of the block takes tile ticket * WPB + w.  A wave only ever waits on
+// tiles of lower index, which belong to lower waves of its own block (resident with it) or
+// to groups whose tickets were drawn earlier (by running blocks), so every wait ends.  The
+// next round's ticket is drawn at the start of the current round, so its latency overlaps
+// the tile's work.  Loads are striped: load k of lane l covers positions
+// (k * 64 + l) * VEC .. + VEC, so every load instruction of a wave reads 64 * VEC contiguous
+// elements, streamed past the caches; the scan across a stripe is DPP (no LDS staging).
 //
 // Tile status: per tile an aggregate slot and an inclusive slot of W 64-bit words
 // (W = 1 for a 4-byte carry, 2 for an 8-byte one).  Each word carries the launch's epoch in
 // its high half and 32 bits of the value in its low half, so a reader accepts a slot only
 // when every word of it carries this launch's epoch: no fence and no reset between launches.
-// The host advances `epoch` (never 0) and `ticket_base` (by tiles + waves) per launch.
+// The host advances `epoch` (never 0) and `ticket_base` (by groups + blocks) per launch.
 // ---------------------------------------------------------------------------------------
 template <class A> struct tile_status {
   static constexpr int W = sizeof(A) == 4 ? 1 : 2;
@@ -478,108 +561,123 @@ UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch) {
   }
 }
 
+// One wave's tile: load, tile-local scan, publish, look back, store.
 template <class T, int OP, bool EXCL, bool REV, int VEC, int K>
-UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
-                           u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base,
-                           u32 epoch) {
+UNP_DEV void scan_tile(const T* __restrict__ in, T* __restrict__ out, i64 cols, i64 tpr, u64 tile,
+                       u64* __restrict__ st, u32 epoch, int lane) {
   typedef typename acc<T, OP>::type A;
   typedef fold<A, OP> F;
   typedef tile_status<A> S;
   constexpr i64 TILE = (i64)64 * VEC * K;
-  const int lane = threadIdx.x & 63;
   const A I = F::identity();
   const T pad = (T)I;  // the identity, exactly representable at the element type
-  const i64 tpr = (cols + TILE - 1) / TILE;
-  const u64 total = (u64)rows * (u64)tpr;
-  for (;;) {
-    u32 ticket = 0;
-    if (lane == 0) ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ticket = (u32)__builtin_amdgcn_readfirstlane((int)ticket);
-    const u64 tile = (u64)(u32)(ticket - ticket_base);
-    if (tile >= total) break;
-    const i64 row = (i64)(tile / (u64)tpr);
-    const i64 j = (i64)tile - row * tpr;
-    const i64 p0 = j * TILE;
-    const bool full = p0 + TILE <= cols;
-    const T* __restrict__ rin = in + row * cols;
-    T* __restrict__ rout = out + row * cols;
+  const i64 row = (i64)(tile / (u64)tpr);
+  const i64 j = (i64)tile - row * tpr;
+  const i64 p0 = j * TILE;
+  const bool full = p0 + TILE <= cols;
+  const T* __restrict__ rin = in + row * cols;
+  T* __restrict__ rout = out + row * cols;
 
-    // Load the tile, elements in scan order.
-    vec<T, VEC> x[K];
+  // Load the tile, elements in scan order.
+  vec<T, VEC> x[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
-      if (full || pos + VEC <= cols) {
-        if constexpr (REV) {
-          const vec<T, VEC> r = ld<T, VEC>(rin + (cols - VEC - pos));
+  for (int k = 0; k < K; ++k) {
+    const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
+    if (full || pos + VEC <= cols) {
+      if constexpr (REV) {
+        const vec<T, VEC> r = ld_nt<T, VEC>(rin + (cols - VEC - pos));
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) x[k].e[e] = r.e[VEC - 1 - e];
-        } else {
-          x[k] = ld<T, VEC>(rin + pos);
-        }
+        for (int e = 0; e < VEC; ++e) x[k].e[e] = r.e[VEC - 1 - e];
       } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const i64 q = pos + e;
-          x[k].e[e] = q < cols ? rin[REV ? cols - 1 - q : q] : pad;
-        }
+        x[k] = ld_nt<T, VEC>(rin + pos);
       }
-    }
-
-    // Tile-local prefixes: pre[k] is the fold of every element before lane's vector k.
-    A pre[K];
-    A carry = I;
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      A s = (A)x[k].e[0];
-#pragma unroll
-      for (int e = 1; e < VEC; ++e) s = F::apply(s, (A)x[k].e[e]);
-      const A inc = wave_inclusive_scan<A, OP>(s, lane);
-      pre[k] = F::apply(carry, wave_shr1(inc, I));
-      carry = F::apply(carry, readlane(inc, 63));
-    }
-
-    A base = I;
-    if (j == 0) {
-      if (lane == 0) S::publish(st, tile, 1, carry, epoch);
     } else {
-      if (lane == 0) S::publish(st, tile, 0, carry, epoch);
-      base = lookback<A, OP>(st, tile, j, lane, epoch);
-      if (lane == 0) S::publish(st, tile, 1, F::apply(base, carry), epoch);
-    }
-
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      A v = F::apply(base, pre[k]);
-      vec<T, VEC> o;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        if constexpr (EXCL) {
-          o.e[e] = (T)v;
-          v = F::apply(v, (A)x[k].e[e]);
-        } else {
-          v = F::apply(v, (A)x[k].e[e]);
-          o.e[e] = (T)v;
-        }
-      }
-      const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
-      if (full || pos + VEC <= cols) {
-        if constexpr (REV) {
-          vec<T, VEC> r;
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) r.e[e] = o.e[VEC - 1 - e];
-          stv<T, VEC>(rout + (cols - VEC - pos), r);
-        } else {
-          stv<T, VEC>(rout + pos, o);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const i64 q = pos + e;
-          if (q < cols) rout[REV ? cols - 1 - q : q] = o.e[e];
-        }
+        const i64 q = pos + e;
+        x[k].e[e] = q < cols ? rin[REV ? cols - 1 - q : q] : pad;
       }
     }
+  }
+
+  // Tile-local prefixes: pre[k] is the fold of every element before lane's vector k.
+  A pre[K];
+  A carry = I;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    A s = (A)x[k].e[0];
+#pragma unroll
+    for (int e = 1; e < VEC; ++e) s = F::apply(s, (A)x[k].e[e]);
+    const A inc = wave_inclusive_scan<A, OP>(s, lane);
+    pre[k] = F::apply(carry, wave_shr1(inc, I));
+    carry = F::apply(carry, readlane(inc, 63));
+  }
+
+  A base = I;
+  if (j == 0) {
+    if (lane == 0) S::publish(st, tile, 1, carry, epoch);
+  } else {
+    if (lane == 0) S::publish(st, tile, 0, carry, epoch);
+    base = lookback<A, OP>(st, tile, j, lane, epoch);
+    if (lane == 0) S::publish(st, tile, 1, F::apply(base, carry), epoch);
+  }
+
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    A v = F::apply(base, pre[k]);
+    vec<T, VEC> o;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      if constexpr (EXCL) {
+        o.e[e] = (T)v;
+        v = F::apply(v, (A)x[k].e[e]);
+      } else {
+        v = F::apply(v, (A)x[k].e[e]);
+        o.e[e] = (T)v;
+      }
+    }
+    const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
+    if (full || pos + VEC <= cols) {
+      if constexpr (REV) {
+        vec<T, VEC> r;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) r.e[e] = o.e[VEC - 1 - e];
+        st_nt<T, VEC>(rout + (cols - VEC - pos), r);
+      } else {
+        st_nt<T, VEC>(rout + pos, o);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const i64 q = pos + e;
+        if (q < cols) rout[REV ? cols - 1 - q : q] = o.e[e];
+      }
+    }
+  }
+}
+
+template <class T, int OP, bool EXCL, bool REV, int VEC, int K, int WPB>
+UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
+                           u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base,
+                           u32 epoch) {
+  constexpr i64 TILE = (i64)64 * VEC * K;
+  __shared__ u32 slot[2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const i64 tpr = (cols + TILE - 1) / TILE;
+  const u64 total = (u64)rows * (u64)tpr;
+  const u64 groups = (total + WPB - 1) / WPB;
+  if (threadIdx.x == 0)
+    slot[0] = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - ticket_base;
+  __syncthreads();
+  for (int r = 0;; ++r) {
+    const u64 g = slot[r & 1];
+    if (g >= groups) break;  // uniform across the block
+    u32 next = 0;
+    if (threadIdx.x == 0) next = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const u64 tile = g * WPB + (u64)wave;
+    if (tile < total) scan_tile<T, OP, EXCL, REV, VEC, K>(in, out, cols, tpr, tile, st, epoch, lane);
+    if (threadIdx.x == 0) slot[(r + 1) & 1] = next - ticket_base;
+    __syncthreads();
   }
 }
 
@@ -590,11 +688,11 @@ UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 ro
 // in UNIT-byte pieces; one wave per output row, waves stride over rows.
 // ---------------------------------------------------------------------------------------
 template <int UNIT> struct unit_type;
-template <> struct unit_type<16> { typedef vec<u32, 4> type; };
-template <> struct unit_type<8> { typedef vec<u32, 2> type; };
-template <> struct unit_type<4> { typedef u32 type; };
-template <> struct unit_type<2> { typedef u16 type; };
-template <> struct unit_type<1> { typedef u8 type; };
+template <> struct unit_type<16> { typedef u32 elem; static constexpr int n = 4; };
+template <> struct unit_type<8> { typedef u32 elem; static constexpr int n = 2; };
+template <> struct unit_type<4> { typedef u32 elem; static constexpr int n = 1; };
+template <> struct unit_type<2> { typedef u16 elem; static constexpr int n = 1; };
+template <> struct unit_type<1> { typedef u8 elem; static constexpr int n = 1; };
 
 template <class IDX> UNP_DEV bool below_zero(IDX v) {
   if constexpr ((IDX)(-1) < (IDX)0) return v < (IDX)0;
@@ -604,7 +702,9 @@ template <class IDX> UNP_DEV bool below_zero(IDX v) {
 template <class IDX, int POLICY, int UNIT, int THREADS, int U>
 UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ ids, u8* __restrict__ out,
                          i64 n_rows, i64 row_bytes, IDX src_extent) {
-  typedef typename unit_type<UNIT>::type V;
+  typedef typename unit_type<UNIT>::elem E;
+  constexpr int N = unit_type<UNIT>::n;
+  typedef vec<E, N> V;
   constexpr int WAVES = THREADS / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const i64 units = row_bytes / UNIT;
@@ -612,28 +712,28 @@ UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ i
     const IDX raw = ids[r];
     const bool below = below_zero(raw);
     const bool oob = below || !(raw < src_extent);
-    V* __restrict__ dst = reinterpret_cast<V*>(out + r * row_bytes);
+    E* __restrict__ dst = reinterpret_cast<E*>(out + r * row_bytes);
     if (oob && POLICY != OOB_CLAMP) {
       if constexpr (POLICY == OOB_ZEROFILL) {
         V z;
         __builtin_memset(&z, 0, sizeof(V));
-        for (i64 u = lane; u < units; u += 64) dst[u] = z;
+        for (i64 u = lane; u < units; u += 64) st_nt<E, N>(dst + u * N, z);
       }
       continue;
     }
     const IDX cl = below ? (IDX)0 : (oob ? (IDX)(src_extent - (IDX)1) : raw);
-    const V* __restrict__ src = reinterpret_cast<const V*>(table + (i64)cl * row_bytes);
+    const E* __restrict__ src = reinterpret_cast<const E*>(table + (i64)cl * row_bytes);
     for (i64 u = lane; u < units; u += 64 * U) {
       V v[U];
 #pragma unroll
       for (int k = 0; k < U; ++k) {
         const i64 uu = u + 64 * k;
-        if (uu < units) v[k] = src[uu];
+        if (uu < units) v[k] = ld_nt<E, N>(src + uu * N);
       }
 #pragma unroll
       for (int k = 0; k < U; ++k) {
         const i64 uu = u + 64 * k;
-        if (uu < units) dst[uu] = v[k];
+        if (uu < units) st_nt<E, N>(dst + uu * N, v[k]);
       }
     }
   }
@@ -669,7 +769,9 @@ template <bool SIGNED> UNP_DEV i32 nibble_value(u32 n) {
 UNP_DEV float f16_to_f32(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
 
 // Fast path: cols % 32 == 0 and G % 32 == 0, so a 32-column chunk lies in one group and
-// its 16 bytes of q are 16-byte aligned.  Work item = one chunk; items stride over the grid.
+// its 16 bytes of q are 16-byte aligned.  Work item = one chunk; items stride over the grid,
+// the next item's q is loaded before the current one is converted, and the 64 output bytes
+// of a chunk are streamed past the caches.
 template <bool QS, bool ZS, int G, int THREADS>
 UNP_DEV void dequant4_bf16(const u8* __restrict__ q, const u16* __restrict__ sc, const u8* __restrict__ zp,
                            u16* __restrict__ out, i64 rows, i64 cols) {
@@ -682,9 +784,18 @@ UNP_DEV void dequant4_bf16(const u8* __restrict__ q, const u16* __restrict__ sc,
   // (r, cc) of the current item, advanced without a division per item.
   i64 r = it / cpr, cc = it - r * cpr;
   const i64 dr = step / cpr, dc = step - dr * cpr;
+  vec<u32, 4> wn = ld_nt<u32, 4>(reinterpret_cast<const u32*>(q + ((r * cols + (cc << 5)) >> 1)));
   for (; it < items; it += step) {
     const i64 e0 = r * cols + (cc << 5);
-    const vec<u32, 4> w = ld<u32, 4>(reinterpret_cast<const u32*>(q + (e0 >> 1)));
+    const vec<u32, 4> w = wn;
+    if (it + step < items) {
+      i64 r2 = r + dr, c2 = cc + dc;
+      if (c2 >= cpr) {
+        c2 -= cpr;
+        ++r2;
+      }
+      wn = ld_nt<u32, 4>(reinterpret_cast<const u32*>(q + ((r2 * cols + (c2 << 5)) >> 1)));
+    }
     const i64 zi = r * ng + ((cc << 5) / G);
     const float s = f16_to_f32(sc[zi]);
     const u32 zb = zp[zi >> 1];
@@ -716,7 +827,7 @@ UNP_DEV void dequant4_bf16(const u8* __restrict__ q, const u16* __restrict__ sc,
     }
     u16* dst = out + e0;
 #pragma unroll
-    for (int wi = 0; wi < 4; ++wi) stv<u32, 4>(reinterpret_cast<u32*>(dst) + 4 * wi, o[wi]);
+    for (int wi = 0; wi < 4; ++wi) st_nt<u32, 4>(reinterpret_cast<u32*>(dst) + 4 * wi, o[wi]);
     r += dr;
     cc += dc;
     if (cc >= cpr) {

@@ -389,9 +389,11 @@ int32_t launch(unp_exec* x, size_t entry, uint32_t grid, void** params, hipStrea
   return UNP_OK;
 }
 
-size_t pick(const unp_exec* x, bool fast_ok) {
+size_t pick(const unp_exec* x, bool fast_ok, bool wide = false) {
   for (size_t i = 0; i < x->l.entries.size(); ++i)
-    if (x->l.entries[i].fast == fast_ok) return i;
+    if (x->l.entries[i].fast == fast_ok && x->l.entries[i].wide == wide) return i;
+  for (size_t i = 0; i < x->l.entries.size(); ++i)
+    if (!x->l.entries[i].fast && x->l.entries[i].wide == wide) return i;
   return x->l.entries.size() - 1;
 }
 
@@ -414,7 +416,7 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
   if (rows == 0) return UNP_OK;
   const int vec = 16 / (int)unp::kind_bytes(f.dtype);
   uint64_t in = A.buf[0], o0 = A.buf[1], o1 = two ? A.buf[2] : A.buf[1];
-  const size_t entry = pick(x, cols % vec == 0 && aligned16(in));
+  const size_t entry = pick(x, cols % vec == 0 && aligned16(in), !x->l.reduce_all && cols > unp::kWideRow);
   const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
   if (x->l.reduce_all) {
     const size_t acc_bytes = 8;
@@ -447,8 +449,9 @@ int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_err
   const long long tile = 64LL * en.vec * en.k;
   const unsigned long long tiles = (unsigned long long)rows * (unsigned long long)((cols + tile - 1) / tile);
   const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
-  const unsigned long long waves = (unsigned long long)grid * (x->l.threads / 64);
-  if (tiles + waves >= (1ull << 31)) {
+  // One ticket per group of wpb tiles, plus the one failing draw that ends each block.
+  const unsigned long long groups = (tiles + en.wpb - 1) / en.wpb;
+  if (tiles + grid >= (1ull << 31)) {
     set_error(err, UNP_INVALID_ARGUMENT, "too many scan tiles for one launch");
     return UNP_INVALID_ARGUMENT;
   }
@@ -467,7 +470,7 @@ int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_err
   void* cnt = x->counter;
   void* params[] = {&in, &out, &rows, &cols, &st, &cnt, &tb, &ep};
   rc = launch(x, entry, grid, params, s, err);
-  if (rc == UNP_OK) x->ticket_base = (uint32_t)(x->ticket_base + (uint32_t)(tiles + waves));
+  if (rc == UNP_OK) x->ticket_base = (uint32_t)(x->ticket_base + (uint32_t)(groups + grid));
   return rc;
 }
 

@@ -24,8 +24,13 @@ struct Entry {
   std::string symbol;
   int vec = 1;        // elements per lane-vector (reduce/scan), bytes per unit (gather)
   int k = 1;          // vectors per lane per tile (scan)
+  int wpb = 1;        // waves per ticket group (scan)
   bool fast = false;  // the 16-byte-aligned path
+  bool wide = false;  // reduction: the block-per-row schedule (long rows)
 };
+
+// Reductions over more than kWideRow elements per row use the block-per-row schedule.
+constexpr long long kWideRow = 32768;
 
 // A lowered form: what the executor needs to launch it.
 struct Lowered {
