@@ -300,7 +300,7 @@ def test_gather_empty_source_zero_fills(hip_device):
 # Dequant
 # ---------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("rows,cols,group", [(8, 256, 128), (3, 96, 32), (5, 100, 10), (2, 30, 7), (7, 4096, 128),
+@pytest.mark.parametrize("rows,cols,group", [(8, 256, 128), (3, 96, 32), (5, 100, 10), (2, 30, 7), (7, 4096, 128), (6, 240, 24), (3, 1000, 8),
                                              (4, 320, 96), (1, 32, 32)])
 @pytest.mark.parametrize("q_kind,z_kind", [("U4", "U4"), ("I4", "U4"), ("U4", "I4"), ("I4", "I4")])
 def test_dequant_bit_exact(hip_device, rows, cols, group, q_kind, z_kind):

@@ -219,8 +219,9 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
   } else {
     // Rows up to kWideRow (32768) elements: one wave per row (no barrier); longer rows: one
     // block per row with the LDS combine.  Both read the row once and stream it past the caches.
-    L.threads = 512;
-    L.blocks_per_cu = 1;
+    // Two blocks of four waves per CU (measured best for an 8192 x 4096 f32 row read).
+    L.threads = 256;
+    L.blocks_per_cu = 2;
     for (int wide = 0; wide <= 1; ++wide) {
       for (int fast = 1; fast >= 0; --fast) {
         Entry e;
@@ -228,11 +229,11 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
         e.wide = wide;
         e.vec = fast ? V : 1;
         e.symbol = L.name + (wide ? "_b" : "_w") + (fast ? "v" : "s");
-        const int unroll = wide ? (fast ? 4 : 8) : (fast ? 8 : 16);
-        src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol << "(const " << T << "* in, " << T
+        const int unroll = wide ? (fast ? 4 : 8) : 16;
+        src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(const " << T << "* in, " << T
             << "* out0, " << T << "* out1, long long rows, long long cols) {\n  unp::"
             << (wide ? "rowreduce<" : "rowreduce_wave<") << T << ", " << f.op0 << ", " << (two ? f.op1 : f.op0) << ", "
-            << (two ? 2 : 1) << ", " << e.vec << ", 512, " << unroll << ">(in, out0, out1, rows, cols);\n}\n";
+            << (two ? 2 : 1) << ", " << e.vec << ", 256, " << unroll << ">(in, out0, out1, rows, cols);\n}\n";
         L.entries.push_back(e);
       }
     }
@@ -292,20 +293,21 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
   name << "unp_scan_" << (f.exclusive ? "excl_" : "incl_") << (f.reverse ? "rev_" : "") << op_name(f.op0)
        << "_" << lower_name(f.dtype);
   L.name = name.str();
-  // One block of kScanWaves waves per CU; one ticket per block per round.
-  constexpr int kScanWaves = 8;
-  L.threads = 64 * kScanWaves;
-  L.blocks_per_cu = 1;
-  // Tile = 64 lanes x VEC x K.  An 8-byte carry (f32 Sum in f64, F64, I64) halves K to keep
-  // the per-lane registers (K vectors in flight plus K carries) within occupancy.
+  // Block tile = waves x 64 lanes x VEC x K positions; one ticket per block per round.
+  // Measured on MI355X at 2^28 i32 / 2^26 f32: a 4-byte carry runs best with 8 waves,
+  // K = 32 and 3 blocks per CU; an 8-byte carry (f32 Sum in f64, F64, I64; twice the
+  // registers per carry) with 16 waves, K = 8 and 1 block per CU.
   const bool wide_carry = (f.dtype == UNP_F32 && f.op0 == UNP_OP_SUM) || kind_bytes(f.dtype) == 8;
+  const int kScanWaves = wide_carry ? 16 : 8;
+  L.threads = 64 * kScanWaves;
+  L.blocks_per_cu = wide_carry ? 1 : 3;
   std::ostringstream src;
   src << header(L.name, f);
   for (int fast = 1; fast >= 0; --fast) {
     Entry e;
     e.fast = fast;
     e.vec = fast ? vec_of(f.dtype) : 1;
-    e.k = fast ? (wide_carry ? 8 : 16) : (wide_carry ? 16 : 32);
+    e.k = fast ? (wide_carry ? 8 : 32) : (wide_carry ? 16 : 32);
     e.wpb = kScanWaves;
     e.symbol = L.name + (fast ? "_v" : "_s");
     src << "extern \"C\" __global__ void __launch_bounds__(" << L.threads << ") " << e.symbol << "(const " << T
@@ -324,11 +326,11 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     << ",\"params\":[{\"name\":\"in0\",\"kind\":\"buffer\",\"role\":\"Read\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
   for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
   j << "],\"launch\":{\"block\":[" << L.threads << ",1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
-    << "\",\"grid_policy\":\"persistent blocks draw one group ticket per round; wave w takes tile ticket*"
-    << kScanWaves << "+w\"},\"entries\":[";
+    << "\",\"grid_policy\":\"persistent blocks draw one block-tile ticket per round\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
-      << ",\"k\":" << L.entries[i].k << ",\"tile\":" << 64 * L.entries[i].vec * L.entries[i].k << ",\"when\":\""
+      << ",\"k\":" << L.entries[i].k << ",\"waves\":" << L.entries[i].wpb
+      << ",\"block_tile\":" << 64 * L.entries[i].vec * L.entries[i].k * L.entries[i].wpb << ",\"when\":\""
       << (L.entries[i].fast ? "scanned extent % vec == 0 and in0/out 16-byte aligned" : "otherwise") << "\"}";
   j << "],\"workspace\":{\"status\":\"tiles * " << (wide_carry ? 32 : 16)
     << " bytes, zeroed once\",\"counter\":4,\"host_state\":[\"epoch\",\"ticket_base\"]}"
@@ -433,21 +435,23 @@ static int32_t lower_dequant(const unp_form& f, Lowered& L, std::string& why) {
   std::ostringstream name;
   name << "unp_dequant_" << lower_name(f.q_kind) << "_z" << lower_name(f.z_kind) << "_g" << f.group << "_bf16";
   L.name = name.str();
+  // Eight blocks of four waves per CU: the scale/zero loads of a step wait on each other,
+  // so more waves than a plain copy needs hide that latency (measured best at 8192 x 28672).
   L.threads = 256;
-  L.blocks_per_cu = 1;
+  L.blocks_per_cu = 8;
   std::ostringstream src;
   src << header(L.name, f);
   const char* sig =
       "(const unsigned char* q, const unsigned short* scale, const unsigned char* zero, unsigned short* out, "
       "long long rows, long long cols)";
-  if (f.group % 32 == 0) {
+  if (f.group % 8 == 0) {
     Entry e;
     e.fast = true;
-    e.vec = 32;
+    e.vec = 8;
     e.symbol = L.name + "_v";
     src << "extern \"C\" __global__ void " << kLaunchBounds << " " << e.symbol << sig << " {\n  unp::dequant4_bf16<"
         << (qs ? "true" : "false") << ", " << (zs ? "true" : "false") << ", " << f.group
-        << ", 256>(q, scale, zero, out, rows, cols);\n}\n";
+        << ", 256, 8>(q, scale, zero, out, rows, cols);\n}\n";
     L.entries.push_back(e);
   }
   {
@@ -469,10 +473,10 @@ static int32_t lower_dequant(const unp_form& f, Lowered& L, std::string& why) {
     << kind_name(f.z_kind)
     << "\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\",\"dtype\":\"Bf16\"},{\"name\":\"n0\",\"kind\":\"scalar\",\"dtype\":\"I32\"},{\"name\":\"n1\",\"kind\":\"scalar\",\"dtype\":\"I32\"}]"
     << ",\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
-    << "\",\"grid_policy\":\"32-column chunks stride over the grid\"},\"entries\":[";
+    << "\",\"grid_policy\":\"waves take 512 consecutive 8-element items per step and stride over the grid\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"when\":\""
-      << (L.entries[i].fast ? "cols % 32 == 0 and w/out 16-byte aligned" : "otherwise") << "\"}";
+      << (L.entries[i].fast ? "cols % group == 0, w 4-byte and out 16-byte aligned" : "otherwise") << "\"}";
   j << "],\"workspace\":null,\"fidelity_notes\":["
     << json_str("exact integer difference and exact f32 product; one round-to-nearest-even to bf16: bit-exact")
     << "]}";

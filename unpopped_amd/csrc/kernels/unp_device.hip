@@ -470,21 +470,20 @@ UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
 // ---------------------------------------------------------------------------------------
 // Single-pass scan with decoupled look-back, along the innermost axis of rows x cols.
 //
-// A tile is TILE = 64 * VEC * K consecutive scan positions of one row, owned by one wave.
-// Blocks of WPB waves are persistent: each round, one thread draws a group ticket from
-// `counter` and wave w of the block takes tile ticket * WPB + w.  A wave only ever waits on
-// tiles of lower index, which belong to lower waves of its own block (resident with it) or
-// to groups whose tickets were drawn earlier (by running blocks), so every wait ends.  The
-// next round's ticket is drawn at the start of the current round, so its latency overlaps
-// the tile's work.  Loads are striped: load k of lane l covers positions
-// (k * 64 + l) * VEC .. + VEC, so every load instruction of a wave reads 64 * VEC contiguous
-// elements, streamed past the caches; the scan across a stripe is DPP (no LDS staging).
+// A block tile is BT = WPB * 64 * VEC * K consecutive scan positions of one row.  Blocks are
+// persistent: each round, one thread draws a tile ticket from `counter` (the next round's
+// ticket is drawn at the start of the current round, so its latency overlaps the work).  A
+// block only ever waits on tiles of lower index, whose tickets were drawn earlier by running
+// blocks, so every wait ends.  Inside the tile wave w owns positions w * 64 * VEC * K ..:
+// load k of lane l covers (k * 64 + l) * VEC .. + VEC of them, so every load instruction
+// reads 64 * VEC contiguous elements, streamed past the caches.  The scan across a stripe is
+// DPP; the waves' aggregates meet in LDS; one look-back per block tile (64 tiles per probe).
 //
 // Tile status: per tile an aggregate slot and an inclusive slot of W 64-bit words
 // (W = 1 for a 4-byte carry, 2 for an 8-byte one).  Each word carries the launch's epoch in
 // its high half and 32 bits of the value in its low half, so a reader accepts a slot only
 // when every word of it carries this launch's epoch: no fence and no reset between launches.
-// The host advances `epoch` (never 0) and `ticket_base` (by groups + blocks) per launch.
+// The host advances `epoch` (never 0) and `ticket_base` (by tiles + blocks) per launch.
 // ---------------------------------------------------------------------------------------
 template <class A> struct tile_status {
   static constexpr int W = sizeof(A) == 4 ? 1 : 2;
@@ -562,122 +561,133 @@ UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch) {
 }
 
 // One wave's tile: load, tile-local scan, publish, look back, store.
-template <class T, int OP, bool EXCL, bool REV, int VEC, int K>
-UNP_DEV void scan_tile(const T* __restrict__ in, T* __restrict__ out, i64 cols, i64 tpr, u64 tile,
-                       u64* __restrict__ st, u32 epoch, int lane) {
-  typedef typename acc<T, OP>::type A;
-  typedef fold<A, OP> F;
-  typedef tile_status<A> S;
-  constexpr i64 TILE = (i64)64 * VEC * K;
-  const A I = F::identity();
-  const T pad = (T)I;  // the identity, exactly representable at the element type
-  const i64 row = (i64)(tile / (u64)tpr);
-  const i64 j = (i64)tile - row * tpr;
-  const i64 p0 = j * TILE;
-  const bool full = p0 + TILE <= cols;
-  const T* __restrict__ rin = in + row * cols;
-  T* __restrict__ rout = out + row * cols;
-
-  // Load the tile, elements in scan order.
-  vec<T, VEC> x[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
-    if (full || pos + VEC <= cols) {
-      if constexpr (REV) {
-        const vec<T, VEC> r = ld_nt<T, VEC>(rin + (cols - VEC - pos));
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) x[k].e[e] = r.e[VEC - 1 - e];
-      } else {
-        x[k] = ld_nt<T, VEC>(rin + pos);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const i64 q = pos + e;
-        x[k].e[e] = q < cols ? rin[REV ? cols - 1 - q : q] : pad;
-      }
-    }
-  }
-
-  // Tile-local prefixes: pre[k] is the fold of every element before lane's vector k.
-  A pre[K];
-  A carry = I;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    A s = (A)x[k].e[0];
-#pragma unroll
-    for (int e = 1; e < VEC; ++e) s = F::apply(s, (A)x[k].e[e]);
-    const A inc = wave_inclusive_scan<A, OP>(s, lane);
-    pre[k] = F::apply(carry, wave_shr1(inc, I));
-    carry = F::apply(carry, readlane(inc, 63));
-  }
-
-  A base = I;
-  if (j == 0) {
-    if (lane == 0) S::publish(st, tile, 1, carry, epoch);
-  } else {
-    if (lane == 0) S::publish(st, tile, 0, carry, epoch);
-    base = lookback<A, OP>(st, tile, j, lane, epoch);
-    if (lane == 0) S::publish(st, tile, 1, F::apply(base, carry), epoch);
-  }
-
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    A v = F::apply(base, pre[k]);
-    vec<T, VEC> o;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      if constexpr (EXCL) {
-        o.e[e] = (T)v;
-        v = F::apply(v, (A)x[k].e[e]);
-      } else {
-        v = F::apply(v, (A)x[k].e[e]);
-        o.e[e] = (T)v;
-      }
-    }
-    const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
-    if (full || pos + VEC <= cols) {
-      if constexpr (REV) {
-        vec<T, VEC> r;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) r.e[e] = o.e[VEC - 1 - e];
-        st_nt<T, VEC>(rout + (cols - VEC - pos), r);
-      } else {
-        st_nt<T, VEC>(rout + pos, o);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const i64 q = pos + e;
-        if (q < cols) rout[REV ? cols - 1 - q : q] = o.e[e];
-      }
-    }
-  }
-}
-
+// One block tile: every wave loads and scans its stripe set (WT = 64 * VEC * K positions),
+// the waves' aggregates are combined in LDS, wave 0 publishes the block tile's aggregate,
+// looks back and publishes its inclusive prefix, and every wave stores its prefixes.
 template <class T, int OP, bool EXCL, bool REV, int VEC, int K, int WPB>
 UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
                            u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base,
                            u32 epoch) {
-  constexpr i64 TILE = (i64)64 * VEC * K;
+  typedef typename acc<T, OP>::type A;
+  typedef fold<A, OP> F;
+  typedef tile_status<A> S;
+  constexpr i64 WT = (i64)64 * VEC * K;
+  constexpr i64 BT = WT * WPB;
   __shared__ u32 slot[2];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const i64 tpr = (cols + TILE - 1) / TILE;
+  __shared__ A wagg[WPB];
+  __shared__ A gbase;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const A I = F::identity();
+  const T pad = (T)I;  // the identity, exactly representable at the element type
+  const i64 tpr = (cols + BT - 1) / BT;
   const u64 total = (u64)rows * (u64)tpr;
-  const u64 groups = (total + WPB - 1) / WPB;
-  if (threadIdx.x == 0)
+  if (tid == 0)
     slot[0] = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - ticket_base;
   __syncthreads();
   for (int r = 0;; ++r) {
     const u64 g = slot[r & 1];
-    if (g >= groups) break;  // uniform across the block
+    if (g >= total) break;  // uniform across the block
     u32 next = 0;
-    if (threadIdx.x == 0) next = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const u64 tile = g * WPB + (u64)wave;
-    if (tile < total) scan_tile<T, OP, EXCL, REV, VEC, K>(in, out, cols, tpr, tile, st, epoch, lane);
-    if (threadIdx.x == 0) slot[(r + 1) & 1] = next - ticket_base;
+    if (tid == 0) next = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const i64 row = (i64)(g / (u64)tpr);
+    const i64 j = (i64)g - row * tpr;
+    const i64 p0 = j * BT + (i64)wave * WT;
+    const bool full = p0 + WT <= cols;
+    const T* __restrict__ rin = in + row * cols;
+    T* __restrict__ rout = out + row * cols;
+
+    // Load this wave's positions, elements in scan order.
+    vec<T, VEC> x[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
+      if (full || pos + VEC <= cols) {
+        if constexpr (REV) {
+          const vec<T, VEC> v = ld_nt<T, VEC>(rin + (cols - VEC - pos));
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) x[k].e[e] = v.e[VEC - 1 - e];
+        } else {
+          x[k] = ld_nt<T, VEC>(rin + pos);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const i64 q = pos + e;
+          x[k].e[e] = q < cols ? rin[REV ? cols - 1 - q : q] : pad;
+        }
+      }
+    }
+
+    // Wave-local prefixes: pre[k] is the fold of this wave's elements before lane's vector k.
+    A pre[K];
+    A carry = I;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      A s = (A)x[k].e[0];
+#pragma unroll
+      for (int e = 1; e < VEC; ++e) s = F::apply(s, (A)x[k].e[e]);
+      const A inc = wave_inclusive_scan<A, OP>(s, lane);
+      pre[k] = F::apply(carry, wave_shr1(inc, I));
+      carry = F::apply(carry, readlane(inc, 63));
+    }
+    if (lane == 0) wagg[wave] = carry;
     __syncthreads();
+
+    // The fold of the earlier waves of this block tile.
+    A wex = I;
+    for (int w = 0; w < wave; ++w) wex = F::apply(wex, wagg[w]);
+    if (wave == 0) {
+      A agg = wagg[0];
+#pragma unroll
+      for (int w = 1; w < WPB; ++w) agg = F::apply(agg, wagg[w]);
+      A gex = I;
+      if (j == 0) {
+        if (lane == 0) S::publish(st, g, 1, agg, epoch);
+      } else {
+        if (lane == 0) S::publish(st, g, 0, agg, epoch);
+        gex = lookback<A, OP>(st, g, j, lane, epoch);
+        if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
+      }
+      if (lane == 0) {
+        gbase = gex;
+        slot[(r + 1) & 1] = next - ticket_base;
+      }
+    }
+    __syncthreads();
+    const A base = F::apply(gbase, wex);
+
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      A v = F::apply(base, pre[k]);
+      vec<T, VEC> o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        if constexpr (EXCL) {
+          o.e[e] = (T)v;
+          v = F::apply(v, (A)x[k].e[e]);
+        } else {
+          v = F::apply(v, (A)x[k].e[e]);
+          o.e[e] = (T)v;
+        }
+      }
+      const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
+      if (full || pos + VEC <= cols) {
+        if constexpr (REV) {
+          vec<T, VEC> v2;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) v2.e[e] = o.e[VEC - 1 - e];
+          st_nt<T, VEC>(rout + (cols - VEC - pos), v2);
+        } else {
+          st_nt<T, VEC>(rout + pos, o);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const i64 q = pos + e;
+          if (q < cols) rout[REV ? cols - 1 - q : q] = o.e[e];
+        }
+      }
+    }
   }
 }
 
@@ -768,71 +778,80 @@ template <bool SIGNED> UNP_DEV i32 nibble_value(u32 n) {
 
 UNP_DEV float f16_to_f32(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
 
-// Fast path: cols % 32 == 0 and G % 32 == 0, so a 32-column chunk lies in one group and
-// its 16 bytes of q are 16-byte aligned.  Work item = one chunk; items stride over the grid,
-// the next item's q is loaded before the current one is converted, and the 64 output bytes
-// of a chunk are streamed past the caches.
-template <bool QS, bool ZS, int G, int THREADS>
+// Eight consecutive elements (one dword of packed q, nibble i = element i) under one scale s
+// and one zero point z, to eight bf16 (four dwords, low element first).
+//   s > 0 and finite: the nibbles n are widened with v_cvt_f32_ubyte* on the bytes of
+//   (q & 0x0F0F0F0F) and (q >> 4 & 0x0F0F0F0F) (an I4 nibble goes through n ^ 8, then - 8),
+//   and (n - z) * s is computed as fma(n', s, -(z - off) * s): both products are exact (at most
+//   5 x 11 significant bits), so the sum is the exact (n - z) * s, and it is +0 exactly when
+//   the reference's (n - z) * s is (+0 times a positive s).  v_cvt_pk_bf16_f32 rounds to
+//   nearest even, which is the reference's codec on finite values.
+//   Otherwise (a zero, negative, infinite or NaN scale): the reference's chain literally,
+//   (float)(n - z) * s, and the software codec with its NaN rule.
+template <bool QS> UNP_DEV vec<u32, 4> dequant8(u32 w, float s, i32 z) {
+  vec<u32, 4> o;
+  if (s > 0.0f && s < __builtin_inff()) {
+    const u32 flip = QS ? 0x08080808u : 0u;
+    const u32 lo = (w & 0x0F0F0F0Fu) ^ flip;
+    const u32 hi = ((w >> 4) & 0x0F0F0F0Fu) ^ flip;
+    const float nzs = -(float)(z + (QS ? 8 : 0)) * s;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = __builtin_fmaf((float)((lo >> (8 * i)) & 0xFFu), s, nzs);
+      const float b = __builtin_fmaf((float)((hi >> (8 * i)) & 0xFFu), s, nzs);
+      o.e[i] = bf16x2_rne_finite(a, b);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = (float)(nibble_value<QS>((w >> (8 * i)) & 15u) - z) * s;
+      const float b = (float)(nibble_value<QS>((w >> (8 * i + 4)) & 15u) - z) * s;
+      o.e[i] = bf16_rne_bits(a) | (bf16_rne_bits(b) << 16);
+    }
+  }
+  return o;
+}
+
+// Fast path: cols % G == 0 and G % 8 == 0, so element e's scale and zero point are element
+// e / G of their buffers (row * cols / G + col / G) and an 8-element item never straddles a
+// row or a group.  A wave takes IPL x 64 consecutive items per step: each of its q loads
+// reads 256 contiguous bytes and each of its stores writes 1 KiB contiguous, both streamed
+// past the caches; the next step's q is loaded before the current step is converted.
+template <bool QS, bool ZS, int G, int THREADS, int IPL>
 UNP_DEV void dequant4_bf16(const u8* __restrict__ q, const u16* __restrict__ sc, const u8* __restrict__ zp,
                            u16* __restrict__ out, i64 rows, i64 cols) {
-  const i64 cpr = cols >> 5;  // chunks per row
-  const i64 ng = (cols + G - 1) / G;
-  const i64 items = rows * cpr;
-  const i64 step = (i64)gridDim.x * THREADS;
-  i64 it = (i64)blockIdx.x * THREADS + threadIdx.x;
-  if (it >= items) return;
-  // (r, cc) of the current item, advanced without a division per item.
-  i64 r = it / cpr, cc = it - r * cpr;
-  const i64 dr = step / cpr, dc = step - dr * cpr;
-  vec<u32, 4> wn = ld_nt<u32, 4>(reinterpret_cast<const u32*>(q + ((r * cols + (cc << 5)) >> 1)));
-  for (; it < items; it += step) {
-    const i64 e0 = r * cols + (cc << 5);
-    const vec<u32, 4> w = wn;
-    if (it + step < items) {
-      i64 r2 = r + dr, c2 = cc + dc;
-      if (c2 >= cpr) {
-        c2 -= cpr;
-        ++r2;
-      }
-      wn = ld_nt<u32, 4>(reinterpret_cast<const u32*>(q + ((r2 * cols + (c2 << 5)) >> 1)));
+  const i64 items = rows * cols / 8;
+  const int lane = threadIdx.x & 63;
+  const i64 nwaves = (i64)gridDim.x * (THREADS / 64);
+  const u32* __restrict__ q32 = reinterpret_cast<const u32*>(q);
+  constexpr i64 PER = (i64)64 * IPL;
+  i64 base = ((i64)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6)) * PER;
+  u32 wn[IPL];
+#pragma unroll
+  for (int k = 0; k < IPL; ++k) {
+    const i64 it = base + 64 * k + lane;
+    wn[k] = it < items ? __builtin_nontemporal_load(q32 + it) : 0u;
+  }
+  for (; base < items; base += nwaves * PER) {
+    u32 w[IPL];
+#pragma unroll
+    for (int k = 0; k < IPL; ++k) w[k] = wn[k];
+    const i64 nb = base + nwaves * PER;
+#pragma unroll
+    for (int k = 0; k < IPL; ++k) {
+      const i64 it = nb + 64 * k + lane;
+      if (it < items) wn[k] = __builtin_nontemporal_load(q32 + it);
     }
-    const i64 zi = r * ng + ((cc << 5) / G);
-    const float s = f16_to_f32(sc[zi]);
-    const u32 zb = zp[zi >> 1];
-    const i32 z = nibble_value<ZS>((zi & 1) ? (zb >> 4) : (zb & 15u));
-    const float fz = (float)z;
-    vec<u32, 4> o[4];
-    if (__builtin_isfinite(s)) {
 #pragma unroll
-      for (int wi = 0; wi < 4; ++wi) {
-        const u32 wv = w.e[wi];
-#pragma unroll
-        for (int pr = 0; pr < 4; ++pr) {
-          const float a = ((float)nibble_value<QS>((wv >> (8 * pr)) & 15u) - fz) * s;
-          const float b = ((float)nibble_value<QS>((wv >> (8 * pr + 4)) & 15u) - fz) * s;
-          o[wi].e[pr] = bf16x2_rne_finite(a, b);
-        }
+    for (int k = 0; k < IPL; ++k) {
+      const i64 it = base + 64 * k + lane;
+      if (it < items) {
+        const i64 zi = (it * 8) / G;
+        const float s = f16_to_f32(sc[zi]);
+        const u32 zb = zp[zi >> 1];
+        const i32 z = nibble_value<ZS>((zi & 1) ? (zb >> 4) : (zb & 15u));
+        st_nt<u32, 4>(reinterpret_cast<u32*>(out + it * 8), dequant8<QS>(w[k], s, z));
       }
-    } else {
-#pragma unroll
-      for (int wi = 0; wi < 4; ++wi) {
-        const u32 wv = w.e[wi];
-#pragma unroll
-        for (int pr = 0; pr < 4; ++pr) {
-          const float a = (float)(nibble_value<QS>((wv >> (8 * pr)) & 15u) - z) * s;
-          const float b = (float)(nibble_value<QS>((wv >> (8 * pr + 4)) & 15u) - z) * s;
-          o[wi].e[pr] = bf16_rne_bits(a) | (bf16_rne_bits(b) << 16);
-        }
-      }
-    }
-    u16* dst = out + e0;
-#pragma unroll
-    for (int wi = 0; wi < 4; ++wi) st_nt<u32, 4>(reinterpret_cast<u32*>(dst) + 4 * wi, o[wi]);
-    r += dr;
-    cc += dc;
-    if (cc >= cpr) {
-      cc -= cpr;
-      ++r;
     }
   }
 }

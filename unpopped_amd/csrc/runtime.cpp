@@ -446,11 +446,10 @@ int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_err
   uint64_t in = A.buf[0], out = A.buf[1];
   const size_t entry = pick(x, cols % vec == 0 && aligned16(in) && aligned16(out));
   const unp::Entry& en = x->l.entries[entry];
-  const long long tile = 64LL * en.vec * en.k;
+  // A block tile: wpb waves x 64 lanes x vec x k positions of one row.
+  const long long tile = 64LL * en.vec * en.k * en.wpb;
   const unsigned long long tiles = (unsigned long long)rows * (unsigned long long)((cols + tile - 1) / tile);
   const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
-  // One ticket per group of wpb tiles, plus the one failing draw that ends each block.
-  const unsigned long long groups = (tiles + en.wpb - 1) / en.wpb;
   if (tiles + grid >= (1ull << 31)) {
     set_error(err, UNP_INVALID_ARGUMENT, "too many scan tiles for one launch");
     return UNP_INVALID_ARGUMENT;
@@ -470,7 +469,8 @@ int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_err
   void* cnt = x->counter;
   void* params[] = {&in, &out, &rows, &cols, &st, &cnt, &tb, &ep};
   rc = launch(x, entry, grid, params, s, err);
-  if (rc == UNP_OK) x->ticket_base = (uint32_t)(x->ticket_base + (uint32_t)(groups + grid));
+  // One ticket per tile, plus the one failing draw that ends each block.
+  if (rc == UNP_OK) x->ticket_base = (uint32_t)(x->ticket_base + (uint32_t)(tiles + grid));
   return rc;
 }
 
@@ -525,7 +525,8 @@ int32_t run_dequant(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_
   if ((rc = need_buffers(A, rows > 0 && cols > 0, err)) != UNP_OK) return rc;
   if (rows == 0 || cols == 0) return UNP_OK;
   uint64_t q = A.buf[0], sc = A.buf[1], zp = A.buf[2], out = A.buf[3];
-  const bool fast_ok = cols % 32 == 0 && aligned16(q) && aligned16(out) && (sc & 1) == 0;
+  const long long group = x->l.form.group;
+  const bool fast_ok = cols % group == 0 && (q & 3) == 0 && aligned16(out) && (sc & 1) == 0;
   size_t entry = pick(x, fast_ok);
   if (x->l.entries[entry].fast && !fast_ok) entry = x->l.entries.size() - 1;
   const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
