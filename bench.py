@@ -154,6 +154,38 @@ def cpu_baseline(synth, budget_s: float = 20.0) -> dict:
     }
 
 
+COPY_PROBE_SRC = r"""
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+extern "C" __global__ void __launch_bounds__(256) unp_copy_probe(const u32x4* __restrict__ s, u32x4* __restrict__ d,
+                                                                  long long n) {
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) d[i] = s[i];
+}
+"""
+
+
+def copy_probe(u, nbytes: int = 256 << 20) -> None:
+    """A plain copy of `nbytes` (read nbytes, write nbytes): the reference point that converts
+    the FETCH_SIZE / WRITE_SIZE counters of a profiled run into bytes."""
+    import ctypes as C
+
+    from unpopped_amd import _lib
+
+    L = _lib.lib()
+    co = u.HipCompiler().compile(COPY_PROBE_SRC, "unp_copy_probe")
+    img = C.create_string_buffer(co, len(co))
+    m, f, err = C.c_void_p(), C.c_void_p(), _lib.Error()
+    _lib.check(L.unp_hip_module_load(img, len(co), C.byref(m), C.byref(err)), err)
+    _lib.check(L.unp_hip_get_function(m, b"unp_copy_probe", C.byref(f), C.byref(err)), err)
+    a, b = u.DeviceBuffer(nbytes), u.DeviceBuffer(nbytes)
+    a.fill(1)
+    args = (C.c_uint64 * 3)(a.ptr, b.ptr, nbytes // 16)
+    g, blk = (C.c_uint32 * 3)(1024, 1, 1), (C.c_uint32 * 3)(256, 1, 1)
+    for _ in range(3):
+        _lib.check(L.unp_hip_launch(f, g, blk, 0, None, args, C.sizeof(args), C.byref(err)), err)
+    u.synchronize()
+    log(f"[bench] copy probe: 3 launches of a {nbytes} B copy")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -161,6 +193,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", default="", help="comma-separated case names (default: the whole suite)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only launch a plain 256 MiB copy (calibrates the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -174,6 +208,9 @@ def main() -> int:
         return 1
     arch, cus = u.device_info()
     log(f"[bench] device {arch}, {cus} CUs")
+    if args.copy_probe:
+        copy_probe(u)
+        return 0
     cases = build_cases(u, synth)
     if args.only:
         keep = set(args.only.split(","))

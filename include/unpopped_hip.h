@@ -135,6 +135,45 @@ typedef struct unp_form {
  * the lifted kernel).  *out is owned by the caller (unp_generated_free). */
 int32_t unp_hip_lower_form(const unp_form* form, unp_generated** out, unp_error* err);
 
+/* Backend::lower_kernel (backend.rs:726-737): lower a kernel-layer KernelFn, given as the JSON
+ * serde writes for the reference's `KernelFn` (crates/unpopped/src/kernel.rs:1223-1250; element
+ * kinds by variant name, crates/unpopped/src/text.rs:56-91).  The kernel is recognised as one of
+ * the lifts below (or the two kernels this backend authors) by lifting each candidate form its
+ * signature admits and comparing the trees; anything else is UNP_UNSUPPORTED_KERNEL, and text that
+ * is not a KernelFn is UNP_PARSE_ERROR.  The interface JSON carries the kernel's declared launch
+ * and parameters (KernelInterface::of, kernel_interface.rs:237-262) beside the HIP launch. */
+int32_t unp_hip_lower_kernel(const char* kernel_json, unp_generated** out, unp_error* err);
+
+/* ---------------------------------------------------------------------------------------
+ * The lifts, restated (each returns the KernelFn as JSON in *json, freed with unp_free_str;
+ * a refusal is UNP_LIFT_DECLINE with the LiftDecline variant in err->detail).  block = grid = 0
+ * asks for the serial lift; otherwise the launched lift on grid blocks of block threads.
+ * ------------------------------------------------------------------------------------- */
+
+/* lift_reduction_opdef (kernel_lift.rs:447-484) / lift_reduction_opdef_launched
+ * (kernel_lift/block_reduce.rs:50-93) of OpDef::reduction_axes(name, 1, [dtype], Input(0), op,
+ * axes, keepdim) (ir.rs:3186-3214): axes_mask bit d reduces axis d, 0 is the last axis. */
+int32_t unp_lift_reduction(const char* name, int32_t dtype, int32_t rank, int32_t op, uint32_t axes_mask,
+                           int32_t keepdim, uint32_t block, uint32_t grid, char** json, unp_error* err);
+/* lift_scan_opdef (kernel_lift.rs:504-519) / lift_scan_opdef_launched (kernel_lift/scan_launched.rs
+ * :54-102) of OpDef::scan_simple (ir.rs:3422-3441): identity pre-map, no post. */
+int32_t unp_lift_scan(const char* name, int32_t dtype, int32_t rank, int32_t op, int32_t axis, int32_t exclusive,
+                      int32_t reverse, uint32_t block, uint32_t grid, char** json, unp_error* err);
+/* lift_gather_opdef (kernel_lift/gather.rs:35-55) / lift_gather_opdef_launched (kernel_lift.rs
+ * :183-191) of OpDef::gather(name, [dtype, index_dtype], axis, oob, index_dtype) (ir.rs:3838-3855);
+ * OpDef::embedding is axis 0 with ZeroFill (ir.rs:3884-3886). */
+int32_t unp_lift_gather(const char* name, int32_t dtype, int32_t rank, int32_t index_dtype, int32_t axis,
+                        int32_t oob, uint32_t block, uint32_t grid, char** json, unp_error* err);
+/* No reference lift: the fused two-fold row reduction (softmax prologue) this backend authors,
+ * each fold exactly a serial lifted reduction's; launched, rows grid-strided. */
+int32_t unp_kernel_row_reduce2(const char* name, int32_t dtype, int32_t op0, int32_t op1, uint32_t block,
+                               uint32_t grid, char** json, unp_error* err);
+/* No reference lift: the int4 dequant this backend authors after the dequant-GEMM fixture
+ * (crates/unpopped/tests/support/dequant.rs:58-143): out[r, c] = Bf16_rne((q - z) * s) with a U4/I4
+ * weight, a U4/I4 zero point and an F16 scale per `group` columns. */
+int32_t unp_kernel_dequant4(const char* name, int32_t q_kind, int32_t z_kind, int32_t group, uint32_t block,
+                            uint32_t grid, char** json, unp_error* err);
+
 /* ---------------------------------------------------------------------------------------
  * Compiler seam (trait Compiler, jit.rs:271-285), through hipRTC for gfx950.
  * ------------------------------------------------------------------------------------- */

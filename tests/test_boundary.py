@@ -1,0 +1,271 @@
+"""The drop-in boundary on the CPU: the C-ABI library loads and exports every declared symbol, the
+Backend and Compiler seams answer as the reference's traits do, the lifts build the reference's
+kernels (and decline where it declines), and lower_kernel recognises exactly those kernels."""
+from __future__ import annotations
+
+import copy
+import ctypes as C
+import json
+import re
+from pathlib import Path
+
+import pytest
+
+import unpopped_amd as u
+from unpopped_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols() -> list[str]:
+    text = (ROOT / "include" / "unpopped_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(unp_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = C.CDLL(str(_lib.LIB_PATH))
+    names = declared_symbols()
+    assert len(names) >= 40
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_backend_identity():
+    b = u.HipBackend()
+    assert b.name() == "hip"
+    assert b.provider() == "unpopped-hip"
+    assert b.total_integer_ops() is False
+
+
+def test_supports_dtype_is_target_conditional():
+    b = u.HipBackend()
+    for dt in ("F32", "F64", "I32", "I64", "Bf16", "F16", "U4", "I4", "U32"):
+        assert b.supports_dtype(dt, "rocm:gfx950") == "Supported", dt
+    assert b.supports_dtype("F32", "cuda:sm89") == "Unsupported"
+    assert b.supports_dtype("F32", "rocm:gfx942") == "Unsupported"
+    assert b.supports_dtype("Fp8E4M3FN", "rocm:gfx950") == "Unsupported"
+    for bad in ("rocm", "rocm:", ":gfx950", "rocm:gfx|950", "rocm:gfx 950", "a:b:c"):
+        assert b.supports_dtype("F32", bad) == "Unsupported", bad
+
+
+def test_compiler_produces_a_gfx950_code_object():
+    cc = u.HipCompiler()
+    assert cc.artifact_kind() == "HipCodeObject"
+    src = 'extern "C" __global__ void k(float* x) { x[threadIdx.x] *= 2.0f; }'
+    co = cc.compile(src, "k")
+    assert co[:4] == b"\x7fELF"
+    assert b"gfx950" in co
+    with pytest.raises(_lib.UnpError) as e:
+        cc.compile("this is not HIP", "k")
+    assert e.value.kind == "CompileError" and "error" in e.value.detail
+
+
+def test_revision_hash_is_fnv1a_over_the_source():
+    g = u.HipBackend().lower_kernel(u.lift_scan("s", "I32", 1, "Sum", launch=(64, 1)))
+    h = 0xCBF29CE484222325
+    for byte in g.source.encode():
+        h = ((h ^ byte) * 0x100000001B3) & ((1 << 64) - 1)
+    assert g.revision_hash() == h
+
+
+# ---------------------------------------------------------------------------------------
+# The lifts
+# ---------------------------------------------------------------------------------------
+
+def stmts(kernel):
+    """Every statement of a kernel body, depth first."""
+    out = []
+
+    def walk(block):
+        for s in block:
+            out.append(s)
+            (name, body), = s.items() if isinstance(s, dict) else (("", None),)
+            if isinstance(body, dict):
+                for key in ("then", "els", "body"):
+                    if key in body:
+                        walk(body[key])
+
+    walk(kernel["body"])
+    return out
+
+
+def test_launched_reduction_has_the_reference_shape():
+    """kernel_lift/block_reduce.rs: Shared `partial` (f64 for a float) and `partial_have` for
+    Max/Min, log2(block) tree rounds each followed by a barrier, launch [block,1,1] x [grid,1,1]."""
+    k = u.lift_reduction("r", "F32", 2, "Max", launch=(128, 7))
+    assert [a["name"] for a in k["allocs"]] == ["partial", "partial_have"]
+    assert k["allocs"][0]["elem"] == "F64" and k["allocs"][0]["extent"] == {"Static": 128}
+    assert k["launch"]["block"] == [128, 1, 1] and k["launch"]["grid"] == [7, 1, 1]
+    barriers = [s for s in stmts(k) if "Barrier" in s]
+    assert len(barriers) == 1 + 7  # after the publish, then one per tree round (128 = 2^7)
+    assert [p["name"] for p in k["params"]] == ["in0", "out", "n0", "n1"]
+    s = u.lift_reduction("r", "I64", 2, "Sum", launch=(64, 1))
+    assert [a["name"] for a in s["allocs"]] == ["partial"] and s["allocs"][0]["elem"] == "I64"
+    serial = u.lift_reduction("r", "F32", 2, "Sum")
+    assert serial["launch"] is None and serial["allocs"] == []
+
+
+def test_launched_scan_has_the_reference_shape():
+    k = u.lift_scan("s", "F32", 1, "Sum", launch=(16, 1))
+    first = k["body"][0]
+    assert first == {"Let": {"local": 7, "init": {"ConstInt": [0, "I32"]}}}  # chunk = 0 (scan_launched.rs:190)
+    assert "While" in k["body"][1]
+    barriers = [s for s in stmts(k) if "Barrier" in s]
+    assert len(barriers) == 1 + 2 * 4 + 1  # publish, 2 per Kogge-Stone round (16 = 2^4), end of row
+
+
+def test_lift_declines_match_the_reference():
+    def decline(fn, *a, **kw):
+        with pytest.raises(_lib.UnpError) as e:
+            fn(*a, **kw)
+        assert e.value.kind == "LiftDecline"
+        return e.value.detail
+
+    assert decline(u.lift_reduction, "r", "F32", 1, "Sum", launch=(96, 1)) == "BadLaunch"  # not a power of two
+    assert decline(u.lift_reduction, "r", "F32", 1, "Sum", launch=(64, 0)) == "BadLaunch"
+    assert "float Prod" in decline(u.lift_reduction, "r", "F32", 1, "Prod", launch=(64, 1))
+    assert "integer Mean" in decline(u.lift_reduction, "r", "I32", 1, "Mean")
+    assert decline(u.lift_reduction, "r", "F32", 9, "Sum") == "BadRank"
+    assert "outside F32" in decline(u.lift_reduction, "r", "Bf16", 1, "Sum")
+    assert "non-innermost" in decline(u.lift_scan, "s", "F32", 2, "Sum", axis=0, launch=(64, 1))
+    assert "Mean scan" in decline(u.lift_scan, "s", "F32", 1, "Mean", launch=(64, 1))
+    assert "non-integer" in decline(u.lift_gather, "g", "F32", 2, "F32")
+    assert decline(u.lift_gather, "g", "F32", 2, launch=(64, 0)) == "BadLaunch"
+    # the serial lifts accept what the launched ones decline
+    u.lift_reduction("r", "F32", 1, "Prod")
+    u.lift_scan("s", "F32", 2, "Sum", axis=0)
+    u.lift_scan("s", "F64", 1, "Mean")
+
+
+# ---------------------------------------------------------------------------------------
+# lower_kernel
+# ---------------------------------------------------------------------------------------
+
+CASES = [
+    (lambda: u.lift_reduction("r", "F32", 2, "Sum", launch=(256, 64)), "lift_reduction_opdef_launched", "unp_rowreduce_sum_f32"),
+    (lambda: u.lift_reduction("r", "F32", 1, "Sum", launch=(256, 1)), "lift_reduction_opdef_launched", "unp_reduce_all_sum_f32"),
+    (lambda: u.lift_reduction("r", "F64", 3, "Mean", axes=(1, 2), keepdim=True), "lift_reduction_opdef", "unp_rowreduce_mean_f64"),
+    (lambda: u.lift_reduction("r", "I64", 2, "Prod", launch=(32, 3)), "lift_reduction_opdef_launched", "unp_rowreduce_prod_i64"),
+    (lambda: u.lift_reduction("r", "I32", 2, "Min", axes=(0, 1)), "lift_reduction_opdef", "unp_reduce_all_min_i32"),
+    (lambda: u.lift_scan("s", "I32", 1, "Sum", launch=(256, 1)), "lift_scan_opdef_launched", "unp_scan_incl_sum_i32"),
+    (lambda: u.lift_scan("s", "F32", 3, "Max", exclusive=True, reverse=True), "lift_scan_opdef", "unp_scan_excl_rev_max_f32"),
+    (lambda: u.lift_scan("s", "I64", 2, "Prod", exclusive=True, launch=(64, 8)), "lift_scan_opdef_launched", "unp_scan_excl_prod_i64"),
+    (lambda: u.lift_gather("e", "Bf16", 2, "I32", launch=(256, 4096)), "lift_gather_opdef_launched", "unp_gather_rows_bf16_by_i32_ZeroFill"),
+    (lambda: u.lift_gather("g", "U8", 3, "I64", oob="Skip"), "lift_gather_opdef", "unp_gather_rows_x_by_i64_Skip"),
+    (lambda: u.lift_gather("g", "F64", 2, "U32", oob="Clamp", launch=(64, 2)), "lift_gather_opdef_launched", "unp_gather_rows_f64_by_u32_Clamp"),
+    (lambda: u.kernel_row_reduce2("p", "F32", "Sum", "Max"), "row_reduce2", "unp_rowreduce_sum_max_f32"),
+    (lambda: u.kernel_dequant4("d", "I4", "U4", 128, launch=(64, 64)), "dequant4", "unp_dequant_i4_zu4_g128_bf16"),
+]
+
+
+@pytest.mark.parametrize("make,lift,name", CASES)
+def test_lower_kernel_recognises_the_lifts(make, lift, name):
+    k = make()
+    g = u.HipBackend().lower_kernel(k)
+    assert g.interface["lift"] == lift
+    assert g.name == name
+    assert g.interface["kernel"] == k["name"]
+    assert g.interface["declared_launch"] == k["launch"]
+    assert g.interface["kernel_params"] == k["params"]
+    assert 'extern "C" __global__' in g.source and "rocm:gfx950" in g.source
+    assert g.interface["fidelity_notes"]
+
+
+def test_lower_kernel_accepts_serde_defaults_left_out():
+    k = u.lift_reduction("r", "F32", 2, "Sum", launch=(256, 64))
+    slim = copy.deepcopy(k)
+    for key in ("allocs", "result", "results"):
+        slim.pop(key)
+    slim["allocs"] = k["allocs"]  # a launched reduction needs its allocations
+    for key in ("cluster", "devices", "grid_dims"):
+        slim["launch"].pop(key)
+
+    def drop_unroll(x):
+        if isinstance(x, dict):
+            if "For" in x and isinstance(x["For"], dict):
+                x["For"].pop("unroll", None)
+            for v in x.values():
+                drop_unroll(v)
+        elif isinstance(x, list):
+            for v in x:
+                drop_unroll(v)
+
+    drop_unroll(slim)
+    assert u.HipBackend().lower_kernel(json.dumps(slim)).interface["lift"] == "lift_reduction_opdef_launched"
+
+
+def mutated(k, path, value):
+    k = copy.deepcopy(k)
+    node = k
+    for p in path[:-1]:
+        node = node[p]
+    node[path[-1]] = value
+    return k
+
+
+def test_lower_kernel_refuses_anything_else():
+    b = u.HipBackend()
+
+    def refused(k, kind="UnsupportedKernel"):
+        with pytest.raises(_lib.UnpError) as e:
+            b.lower_kernel(k)
+        assert e.value.kind == kind, e.value.detail
+        return e.value.detail
+
+    k = u.lift_reduction("r", "F32", 2, "Sum", launch=(256, 64))
+    # a different fold (Sub instead of Add in the accumulate) is not a lift's kernel
+    text = json.dumps(k).replace('{"Assign": {"local": 5, "value": {"Add":', '{"Assign": {"local": 5, "value": {"Sub":', 1)
+    assert text != json.dumps(k)
+    refused(text)
+    # an extra statement
+    extra = copy.deepcopy(k)
+    extra["body"].append({"Barrier": {"scope": "Block", "kind": "Full"}})
+    refused(extra)
+    # a different launch geometry inside the tree than declared
+    refused(mutated(k, ["launch", "block"], [128, 1, 1]))
+    # not JSON, not a KernelFn
+    refused("{not json", "ParseError")
+    refused(json.dumps([1, 2, 3]), "ParseError")
+    # a gather along axis 1 is recognised and refused by name
+    assert "axis 1" in refused(u.lift_gather("g", "F32", 2, axis=1))
+    # a float Prod (serial lift exists; this backend has no kernel for it)
+    refused(u.lift_reduction("r", "F32", 2, "Prod"))
+    # a scan along a non-innermost axis
+    refused(u.lift_scan("s", "F32", 2, "Sum", axis=0))
+    # an elementwise body different from the identity load (x * x) is refused
+    sq = json.dumps(u.lift_reduction("r", "F64", 1, "Sum")).replace(
+        '{"Let": {"local": 5, "init": {"Local": 2}}}',
+        '{"Let": {"local": 5, "init": {"Mul": [{"Local": 2}, {"Local": 2}]}}}')
+    assert '"Mul"' in sq
+    refused(sq)
+
+
+def test_lower_form_declines_unsupported_forms():
+    b = u.HipBackend()
+    for form, kind in [
+        (dict(kind="reduction", dtype="F32", op="Prod", rank=1, reduced_from=0), "UnsupportedKernel"),
+        (dict(kind="reduction", dtype="I32", op="Mean", rank=1, reduced_from=0), "UnsupportedKernel"),
+        (dict(kind="scan", dtype="F32", op="Mean"), "UnsupportedKernel"),
+        (dict(kind="gather", dtype="U4", rank=2), "UnsupportedDtype"),
+        (dict(kind="dequant4", out_kind="F32"), "UnsupportedDtype"),
+        (dict(kind="dequant4", group=0), "UnsupportedKernel"),
+        (dict(kind="reduction", dtype="F32", rank=9), "LiftDecline"),
+    ]:
+        with pytest.raises(_lib.UnpError) as e:
+            b.lower_form(**form)
+        assert e.value.kind == kind, (form, e.value.kind, e.value.detail)
+
+
+def test_every_lowered_source_compiles_for_gfx950():
+    """The Compiler seam on each form's emitted source (hipRTC needs no GPU)."""
+    b, cc = u.HipBackend(), u.HipCompiler()
+    seen = set()
+    for make, _, _ in CASES:
+        g = b.lower_kernel(make())
+        if g.name in seen:
+            continue
+        seen.add(g.name)
+        co = cc.compile(g.source, g.name)
+        for e in g.interface["entries"]:
+            assert e["symbol"].encode() in co

@@ -1,0 +1,386 @@
+"""Pins for the CPU oracle (oracle/oracle.c).  CPU only.
+
+Every oracle function is checked here against something that is not itself:
+  * golden vectors the reference's own tests hold (sub-byte packing, bf16 bit patterns, the
+    dequant-GEMM known answer);
+  * independent library routines (numpy float16 conversions, torch bfloat16 rounding, numpy's
+    int32 wrapping sums, Python's exact rationals);
+  * closed forms (dyadic sums are exact in f64, so every order rounds to RN32(exact)) and brute
+    force on tiny inputs;
+and planted mistakes (an f32 accumulator, a dropped element, a swapped nibble order) are shown
+to fail the same checks.
+"""
+from __future__ import annotations
+
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.golden import corpora
+from unpopped_amd import synth
+
+rng = np.random.default_rng
+
+
+def bits32(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+
+
+def torch_bf16_bits(x: np.ndarray) -> np.ndarray:
+    t = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+# ---------------------------------------------------------------------------------------
+# bf16 / f16 codecs (crates/unpopped/src/oracle/float_codec.rs)
+# ---------------------------------------------------------------------------------------
+
+def test_bf16_codec_matches_torch_round_to_nearest_even():
+    r = rng(0)
+    x = np.concatenate([
+        r.normal(size=200000).astype(np.float32),
+        (r.normal(size=50000) * 1e30).astype(np.float32),
+        (r.normal(size=50000) * 1e-38).astype(np.float32),  # f32 subnormals
+        np.array([0.0, -0.0, np.inf, -np.inf, 3.3895314e38, -3.3895314e38, 1.0, 257.0, 6.0], np.float32),
+    ])
+    # every tie: the low 16 bits exactly 0x8000, both parities of the kept half
+    ties = (r.integers(0, 1 << 15, size=20000, dtype=np.uint32) << 16 | 0x8000).astype(np.uint32).view(np.float32)
+    x = np.concatenate([x, ties[np.isfinite(ties)]])
+    assert np.array_equal(oracle.f32_to_bf16_bits(x), torch_bf16_bits(x))
+
+
+def test_bf16_codec_reference_vectors():
+    # crates/unpopped/tests/kernel_atomic_half.rs:76-94: 1.0 = 0x3F80, 256 = 0x4380,
+    # 256 + 1 rounds (tie, even) to 0x4380, 12 * 0.5 = 6.0 = 0x40C0
+    got = oracle.f32_to_bf16_bits(np.array([1.0, 256.0, 257.0, 6.0], np.float32))
+    assert list(got) == [0x3F80, 0x4380, 0x4380, 0x40C0]
+    # a NaN keeps its top half and is quieted (float_codec.rs:259-266)
+    nans = np.array([0x7FC50000, 0x7F800001, 0xFFA00000, 0x7FFFFFFF], np.uint32).view(np.float32)
+    assert list(oracle.f32_to_bf16_bits(nans)) == [0x7FC5, 0x7FC0, 0xFFE0, 0x7FFF]
+
+
+def test_f16_decode_all_patterns_match_numpy():
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    got = oracle.f16_to_f64(h)
+    want = h.view(np.float16).astype(np.float64)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.array_equal(np.signbit(got), np.signbit(want))  # a NaN keeps its sign too
+
+
+def test_f16_encode_matches_numpy():
+    L = oracle.lib()
+    r = rng(1)
+    x = np.concatenate([r.normal(size=20000) * 1e3, r.normal(size=5000) * 1e-5, r.normal(size=1000) * 7e4,
+                        np.array([0.0, -0.0, 65504.0, 65520.0, 65519.99, 6e-8, 2.98e-8, np.inf, -np.inf])]).astype(np.float32)
+    got = np.array([L.orc_f32_to_f16_bits(float(v)) for v in x], np.uint16)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    assert L.orc_f32_to_f16_bits(float("nan")) == 0x7E00
+
+
+def test_round_to_odd_then_bf16_is_correctly_rounded():
+    """expr_eval.rs:503-527: bf16(odd(v)) must equal the correctly rounded bf16 of the f64 value
+    (checked with exact rationals), where a plain f64 -> f32 -> bf16 double-rounds."""
+    L = oracle.lib()
+    r = rng(2)
+    # values just off a bf16 tie, where double rounding bites
+    base = r.integers(0x3F800000, 0x4F000000, size=3000, dtype=np.uint64).astype(np.uint32)
+    base = (base & 0xFFFF0000) | 0x8000
+    vals = base.view(np.float32).astype(np.float64) * (1 + r.choice([-1, 1], size=base.size) * 2.0 ** -40)
+    double_rounding_seen = 0
+    for v in vals:
+        got = L.orc_store_bf16(float(v))
+        # exact: the two neighbouring bf16 values of v, pick nearest, ties to even
+        f = Fraction(float(v))
+        lo_bits = int(np.float32(v).view(np.uint32)) >> 16
+        cands = [lo_bits - 1, lo_bits, lo_bits + 1]
+        vals_c = [Fraction(float(np.uint32(c << 16).view(np.float32))) for c in cands]
+        best = min(range(3), key=lambda i: (abs(vals_c[i] - f), cands[i] & 1))
+        assert got == cands[best], (v, hex(got), hex(cands[best]))
+        if oracle.f32_to_bf16_bits(np.float32(v))[0] != got:
+            double_rounding_seen += 1
+    assert double_rounding_seen > 0  # the naive path really is wrong on these inputs
+
+
+# ---------------------------------------------------------------------------------------
+# Sub-byte elements (crates/unpopped/tests/kernel_subbyte_load.rs, sub_byte_packing.rs)
+# ---------------------------------------------------------------------------------------
+
+def test_nibble_golden_vectors():
+    L = oracle.lib()
+    nib = np.array([0x8, 0xF, 0x0, 0x1, 0x7, 0x3, 0xC, 0x5], np.int32)
+    packed = np.zeros(4, np.uint8)
+    for i, v in enumerate(nib):
+        L.orc_sub4_store(packed.ctypes.data, i, int(v))
+    assert list(packed) == [0xF8, 0x10, 0x37, 0x5C]  # low nibble first (kernel_subbyte_load.rs:129)
+    assert [L.orc_u4_load(packed.ctypes.data, i) for i in range(8)] == [8, 15, 0, 1, 7, 3, 12, 5]
+    assert [L.orc_i4_load(packed.ctypes.data, i) for i in range(8)] == [-8, -1, 0, 1, 7, 3, -4, 5]
+    two = np.zeros(2, np.uint8)
+    for i, v in enumerate([1, 2, 3, 4]):
+        L.orc_sub4_store(two.ctypes.data, i, v)
+    assert list(two) == [0x21, 0x43]  # sub_byte_packing.rs:31-38, :128
+    L.orc_sub4_store(two.ctypes.data, 1, 9)  # a store keeps its byte neighbour
+    assert list(two) == [0x91, 0x43]
+
+
+def test_synth_nibbles_are_low_nibble_first():
+    s = synth.nibbles(4, 1001)
+    vals = np.array([oracle.lib().orc_u4_load(s.ctypes.data, i) for i in range(1001)])
+    # the same stream, drawn by the LCG directly
+    st, want = 4, []
+    for _ in range(1001):
+        st = (st * 6364136223846793005 + 1442695040888963407) & ((1 << 64) - 1)
+        want.append(st >> 60)
+    assert np.array_equal(vals, want)
+
+
+# ---------------------------------------------------------------------------------------
+# Dequant
+# ---------------------------------------------------------------------------------------
+
+def _dequant_numpy(q, s, z, rows, cols, group, q_signed, z_signed):
+    qv = np.stack([q & 15, q >> 4], axis=1).ravel()[: rows * cols].astype(np.int64)
+    ng = -(-cols // group)
+    zv = np.stack([z & 15, z >> 4], axis=1).ravel()[: rows * ng].astype(np.int64)
+    if q_signed:
+        qv = np.where(qv >= 8, qv - 16, qv)
+    if z_signed:
+        zv = np.where(zv >= 8, zv - 16, zv)
+    sv = s.view(np.float16).astype(np.float64)
+    g = (np.arange(rows)[:, None] * ng + np.arange(cols)[None, :] // group).ravel()
+    v = (qv - zv[g]).astype(np.float64) * sv[g]
+    return torch_bf16_bits(v.astype(np.float32)).reshape(rows, cols)  # exact products: one rounding
+
+
+@pytest.mark.parametrize("qs,zs", [(False, False), (True, False), (False, True), (True, True)])
+def test_dequant_matches_numpy_and_torch_rounding(qs, zs):
+    rows, cols, group = 9, 200, 24
+    ng = -(-cols // group)
+    q, z = synth.nibbles(4, rows * cols), synth.nibbles(5, rows * ng)
+    s = synth.uniform_f16_bits(6, rows * ng, 0.001, 0.02)
+    got = oracle.dequant4_bf16(q, s, z, rows, cols, group, qs, zs)
+    assert np.array_equal(got, _dequant_numpy(q, s, z, rows, cols, group, qs, zs))
+    # a swapped nibble order is caught
+    swapped = ((q >> 4) | (q << 4)).astype(np.uint8)
+    assert not np.array_equal(oracle.dequant4_bf16(swapped, s, z, rows, cols, group, qs, zs), got)
+
+
+def test_dequant_gemm_known_answer():
+    """crates/unpopped/tests/support/dequant.rs:145-181 (R=4, K=8, C=4, GROUP=4): the int4 GEMM's
+    host answer, reproduced from the oracle's dequantized weights (exact in bf16) times x."""
+    R, K, C, GROUP = 4, 8, 4, 4
+    G = K // GROUP
+    nib = [(r * 5 + k * 3 + 1) % 16 for r in range(R) for k in range(K)]
+    packed = np.array([nib[i] | nib[i + 1] << 4 for i in range(0, len(nib), 2)], np.uint8)
+    zero = [(i % 3) - 1 for i in range(R * G)]
+    scale = [1 + (i * 2 % 3) for i in range(R * G)]
+    x = np.array([(i * 7 % 9) - 4 for i in range(K * C)], np.int64).reshape(K, C)
+    zp = np.array([(zero[i] & 15) | ((zero[i + 1] & 15) << 4) for i in range(0, R * G, 2)], np.uint8)
+    sc = np.array(scale, np.float16).view(np.uint16)
+    for signed in (False, True):
+        w = oracle.dequant4_bf16(packed, sc, zp, R, K, GROUP, q_signed=signed, z_signed=True)
+        wv = (w.astype(np.uint32) << 16).view(np.float32).astype(np.int64)
+        got = wv @ x
+        want = np.zeros((R, C), np.int64)  # the fixture's own host formula
+        for r in range(R):
+            for c in range(C):
+                for k in range(K):
+                    n = nib[r * K + k]
+                    n = n - 16 if signed and n >= 8 else n
+                    g = r * G + k // GROUP
+                    want[r, c] += (n - zero[g]) * scale[g] * x[k, c]
+        assert np.array_equal(got, want)
+
+
+def test_dequant_special_scales_follow_the_codec():
+    rows, cols, group = 2, 64, 8
+    ng = cols // group
+    s = np.array([0xBC00, 0x0001, 0x0000, 0x8000, 0x7C00, 0xFC00, 0x7E00, 0x7BFF] * 2, np.uint16)
+    q, z = synth.nibbles(7, rows * cols), synth.nibbles(8, rows * ng)
+    got = oracle.dequant4_bf16(q, s, z, rows, cols, group)
+    qv = np.stack([q & 15, q >> 4], 1).ravel().astype(np.int64)
+    zv = np.stack([z & 15, z >> 4], 1).ravel().astype(np.int64)
+    g = np.arange(rows * cols) // group
+    with np.errstate(invalid="ignore"):
+        v = ((qv - zv[g]).astype(np.float32) * s.view(np.float16).astype(np.float32)[g]).ravel()
+    nan = np.isnan(v)
+    assert np.array_equal((got.ravel() & 0x7FFF) > 0x7F80, nan)
+    assert np.array_equal(got.ravel()[~nan], torch_bf16_bits(v[~nan]))
+    assert np.array_equal(got.ravel()[~nan] >> 15, np.signbit(v[~nan]).astype(np.uint16))  # signed zeros
+
+
+# ---------------------------------------------------------------------------------------
+# Reductions
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+def test_int_reductions_wrap_and_match_numpy(dtype):
+    info = np.iinfo(dtype)
+    x = rng(3).integers(info.min, info.max, size=(7, 1001), dtype=dtype, endpoint=True)
+    assert np.array_equal(oracle.reduce_rows(x, "Sum"), np.sum(x, axis=1, dtype=dtype))
+    assert np.array_equal(oracle.reduce_rows(x, "Prod"), np.prod(x, axis=1, dtype=dtype))
+    assert np.array_equal(oracle.reduce_rows(x, "Max"), x.max(axis=1))
+    assert np.array_equal(oracle.reduce_rows(x, "Min"), x.min(axis=1))
+
+
+def test_float_extrema_keep_nan_and_empty_rows_store_zero():
+    x = rng(4).normal(size=(5, 300)).astype(np.float32)
+    x[1, 7] = np.nan
+    x[2, :] = -np.inf
+    assert np.array_equal(oracle.reduce_rows(x, "Max"), x.max(axis=1), equal_nan=True)
+    assert np.array_equal(oracle.reduce_rows(x, "Min"), x.min(axis=1), equal_nan=True)
+    empty = np.zeros((3, 0), np.float32)
+    assert list(oracle.reduce_rows(empty, "Max")) == [0.0] * 3  # the fold's starting value
+    assert np.isnan(oracle.reduce_rows(empty, "Mean")).all()  # 0 / 0
+
+
+def test_dyadic_sums_round_the_exact_sum_and_an_f32_accumulator_fails():
+    x = synth.uniform_pm1_f32(0, 1 << 20).reshape(4, -1)
+    exact = [sum(Fraction(float(v)) for v in row[:4096]) for row in x[:, :4096]]
+    got = oracle.reduce_rows(np.ascontiguousarray(x[:, :4096]), "Sum")
+    assert all(float(np.float32(float(e))) == g for e, g in zip(exact, got))
+    full = oracle.reduce_rows(x, "Sum")
+    assert np.array_equal(full, x.astype(np.float64).sum(axis=1).astype(np.float32))
+    f32_acc = np.array([np.add.reduce(r, dtype=np.float32) for r in x])  # a planted mistake
+    assert not np.array_equal(f32_acc, full)
+
+
+def test_neumaier_is_near_exact():
+    r = rng(5)
+    for _ in range(20):
+        xs = r.normal(size=500) * 10.0 ** r.integers(-8, 8, size=500)
+        exact = float(sum(Fraction(v) for v in xs))
+        assert abs(oracle.neumaier(xs) - exact) <= 4 * 2.0 ** -53 * abs(exact) + 1e-300
+
+
+def test_launched_order_and_bound_on_the_reference_corpus():
+    """tests/kernel_parallel_reduction_float_sum_bound.rs: the declared bound holds for the
+    launched order at every geometry, block 1 is the serial order, and the corpus makes the
+    bound bite (a visible difference between orders)."""
+    corpus = corpora.float_sum_bound_corpus()
+    orders_differ = False
+    for row in corpus:
+        serial = oracle.reduce_rows(row.reshape(1, -1), "Sum")[0]
+        for block in (1, 2, 8, 32, 128):
+            for mean in (False, True):
+                tot = oracle.sum_launched_order(row, block, mean)
+                exact = float(sum(Fraction(float(v)) for v in row)) / (row.size if mean else 1)
+                b = oracle.sum_bound(row, tot, mean=mean, f32=False)
+                assert abs(tot - exact) <= b
+            orders_differ |= oracle.sum_launched_order(row, block) != serial
+        # block 1 folds in the serial order
+        assert oracle.sum_launched_order(row, 1) == serial
+    assert orders_differ
+    # the corpus rows generated from the reference's LCG (values drawn, not retyped)
+    assert corpus[1, 1] == -1.0e8 and corpus[3, 5] == 0.1
+
+
+def test_sum_bound_rejects_a_dropped_element():
+    x = rng(6).normal(size=(1, 4000)).astype(np.float64)
+    got = oracle.reduce_rows(x, "Sum")[0]
+    assert abs(got - oracle.neumaier(x[0])) <= oracle.sum_bound(x[0], got, f32=False)
+    wrong = got - x[0, 17]  # a dropped term
+    assert abs(wrong - oracle.neumaier(x[0])) > oracle.sum_bound(x[0], wrong, f32=False)
+
+
+# ---------------------------------------------------------------------------------------
+# Scans
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+def test_int_scans_match_numpy(dtype):
+    info = np.iinfo(dtype)
+    x = rng(7).integers(info.min, info.max, size=(3, 777), dtype=dtype, endpoint=True)
+    inc = np.cumsum(x, axis=1, dtype=dtype)
+    assert np.array_equal(oracle.scan_rows(x, "Sum"), inc)
+    exc = np.concatenate([np.zeros((3, 1), dtype), inc[:, :-1]], axis=1)
+    assert np.array_equal(oracle.scan_rows(x, "Sum", exclusive=True), exc)
+    rev = np.flip(np.cumsum(np.flip(x, 1), axis=1, dtype=dtype), 1)
+    assert np.array_equal(oracle.scan_rows(x, "Sum", reverse=True), rev)
+    assert np.array_equal(oracle.scan_rows(x, "Max"), np.maximum.accumulate(x, axis=1))
+    ex_max = oracle.scan_rows(x, "Max", exclusive=True)
+    assert (ex_max[:, 0] == info.min).all()  # the integer Max identity (scan_identity)
+    assert np.array_equal(oracle.scan_rows(x, "Min"), np.minimum.accumulate(x, axis=1))
+    assert np.array_equal(oracle.scan_rows(x, "Prod"), np.cumprod(x, axis=1, dtype=dtype))
+
+
+def test_float_scans():
+    x = synth.uniform_01_f32(2, 3 * 5000).reshape(3, 5000)
+    assert np.array_equal(oracle.scan_rows(x, "Sum"), np.cumsum(x.astype(np.float64), axis=1).astype(np.float32))
+    y = rng(8).normal(size=(2, 3000)).astype(np.float32)
+    y[0, 1500] = np.nan
+    assert np.array_equal(oracle.scan_rows(y, "Max"), np.maximum.accumulate(y, axis=1), equal_nan=True)
+    ex = oracle.scan_rows(y, "Max", exclusive=True)
+    assert ex[0, 0] == -np.inf and np.isnan(ex[0, 1501]) and not np.isnan(ex[0, 1500])
+    m = oracle.scan_rows(y[1:].astype(np.float64), "Mean")
+    assert np.allclose(m[0], np.cumsum(y[1].astype(np.float64)) / np.arange(1, 3001), rtol=1e-12)
+    assert np.isnan(oracle.scan_rows(y[1:].astype(np.float64), "Mean", exclusive=True)[0, 0])  # 0 / 0
+
+
+def test_launched_scan_order():
+    x = synth.uniform_01_f32(2, 10007)
+    serial = oracle.scan_rows(x.reshape(1, -1), "Sum").ravel()
+    for block in (1, 4, 64, 256):
+        for ex in (False, True):
+            for rev in (False, True):
+                got = oracle.scan_launched_order_f32(x, block, ex, rev)
+                assert np.array_equal(got, oracle.scan_rows(x.reshape(1, -1), "Sum", ex, rev).ravel())
+    y = rng(9).normal(size=5000).astype(np.float32)
+    assert np.array_equal(oracle.scan_launched_order_f32(y, 1), oracle.scan_rows(y.reshape(1, -1), "Sum").ravel())
+    assert not np.array_equal(serial[1:], serial[:-1])
+
+
+# ---------------------------------------------------------------------------------------
+# Gather
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("idx", [np.int32, np.int64, np.uint32])
+@pytest.mark.parametrize("policy", ["Skip", "ZeroFill", "Clamp"])
+def test_gather_policies_match_numpy(idx, policy):
+    V, D, N = 50, 7, 300
+    table = rng(10).normal(size=(V, D)).astype(np.float32)
+    ids = rng(11).integers(-20 if idx != np.uint32 else 0, V + 20, size=N).astype(idx)
+    init = np.full((N, D), 123.0, np.float32)
+    got = oracle.gather_rows(table, ids, policy, out_init=init)
+    raw = ids.astype(np.int64)
+    oob = (raw < 0) | (raw >= V)
+    want = table[np.clip(raw, 0, V - 1)].copy()
+    if policy == "Skip":
+        want[oob] = 123.0
+    elif policy == "ZeroFill":
+        want[oob] = 0.0
+    assert np.array_equal(got, want)
+
+
+def test_gather_empty_source():
+    ids = np.array([0, -1, 3], np.int32)
+    got = oracle.gather_rows(np.zeros((1, 4), np.uint16), ids, "ZeroFill", out_init=np.full((3, 4), 9, np.uint16),
+                             src_extent=0)
+    assert not got.any()
+
+
+# ---------------------------------------------------------------------------------------
+# The synthetic generator (inputs of the parity tests and the benchmark)
+# ---------------------------------------------------------------------------------------
+
+def test_synth_parallel_chunks_equal_the_sequential_stream():
+    n = (1 << 20) + 5  # crosses the generator's chunk boundary
+    got = synth.uniform_pm1_f32(0, n)
+    s, M = 0, (1 << 64) - 1
+    idx = [0, 1, 2, (1 << 20) - 1, 1 << 20, (1 << 20) + 4]
+    want = {}
+    for i in range(n):
+        s = (s * 6364136223846793005 + 1442695040888963407) & M
+        if i in idx:
+            want[i] = ((s >> 39) - (1 << 24)) / float(1 << 24)
+    assert all(got[i] == want[i] for i in idx)
+    assert got.min() >= -1.0 and got.max() < 1.0
+    z = synth.zipf_ids_i32(3, 65536, 262144, 1.1)
+    assert z.min() >= 0 and z.max() < 262144
+    assert np.bincount(z).max() > 1000  # heavy-tailed: the top row repeats

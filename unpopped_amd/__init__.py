@@ -93,6 +93,12 @@ class HipBackend:
         f.out_kind = ELEMENT_KINDS[out_kind]
         return self._wrap(lambda out, err: _lib.lib().unp_hip_lower_form(C.byref(f), out, err))
 
+    def lower_kernel(self, kernel) -> GeneratedKernel:
+        """``Backend::lower_kernel`` (backend.rs:726-737): ``kernel`` is a KernelFn as its serde
+        JSON (a ``str``) or as the parsed ``dict``."""
+        text = kernel if isinstance(kernel, str) else json.dumps(kernel)
+        return self._wrap(lambda out, err: _lib.lib().unp_hip_lower_kernel(text.encode(), out, err))
+
     @staticmethod
     def _wrap(call) -> GeneratedKernel:
         L = _lib.lib()
@@ -105,6 +111,60 @@ class HipBackend:
             interface=json.loads(L.unp_generated_interface_json(out).decode()),
             _handle=out,
         )
+
+
+def _lifted(call) -> dict:
+    out = C.c_void_p()
+    err = _lib.Error()
+    check(call(C.byref(out), C.byref(err)), err)
+    try:
+        return json.loads(C.string_at(out).decode())
+    finally:
+        _lib.lib().unp_free_str(out)
+
+
+def _geom(launch) -> tuple[int, int]:
+    return (0, 0) if launch is None else (int(launch[0]), int(launch[1]))
+
+
+def lift_reduction(name: str, dtype: str, rank: int, op: str, axes: tuple = (), keepdim: bool = False,
+                   launch: tuple | None = None) -> dict:
+    """The reduction lift (serial, or launched on ``launch = (block, grid)``) as a KernelFn dict."""
+    mask = 0
+    for d in axes:
+        mask |= 1 << d
+    b, g = _geom(launch)
+    return _lifted(lambda o, e: _lib.lib().unp_lift_reduction(name.encode(), ELEMENT_KINDS[dtype], rank,
+                                                             REDUCE_OPS[op], mask, int(keepdim), b, g, o, e))
+
+
+def lift_scan(name: str, dtype: str, rank: int, op: str, axis: int | None = None, exclusive: bool = False,
+              reverse: bool = False, launch: tuple | None = None) -> dict:
+    b, g = _geom(launch)
+    ax = rank - 1 if axis is None else axis
+    return _lifted(lambda o, e: _lib.lib().unp_lift_scan(name.encode(), ELEMENT_KINDS[dtype], rank, REDUCE_OPS[op],
+                                                        ax, int(exclusive), int(reverse), b, g, o, e))
+
+
+def lift_gather(name: str, dtype: str, rank: int, index_dtype: str = "I32", axis: int = 0, oob: str = "ZeroFill",
+                launch: tuple | None = None) -> dict:
+    b, g = _geom(launch)
+    return _lifted(lambda o, e: _lib.lib().unp_lift_gather(name.encode(), ELEMENT_KINDS[dtype], rank,
+                                                          ELEMENT_KINDS[index_dtype], axis, OOB_POLICIES[oob],
+                                                          b, g, o, e))
+
+
+def kernel_row_reduce2(name: str, dtype: str, op0: str = "Sum", op1: str = "Max", launch: tuple | None = None) -> dict:
+    b, g = _geom(launch)
+    return _lifted(lambda o, e: _lib.lib().unp_kernel_row_reduce2(name.encode(), ELEMENT_KINDS[dtype],
+                                                                 REDUCE_OPS[op0], REDUCE_OPS[op1], b, g, o, e))
+
+
+def kernel_dequant4(name: str, q_kind: str = "U4", z_kind: str = "U4", group: int = 128,
+                    launch: tuple | None = None) -> dict:
+    b, g = _geom(launch)
+    return _lifted(lambda o, e: _lib.lib().unp_kernel_dequant4(name.encode(), ELEMENT_KINDS[q_kind],
+                                                              ELEMENT_KINDS[z_kind], group, b, g, o, e))
 
 
 class HipCompiler:

@@ -1,0 +1,838 @@
+// The lifts the HIP backend lowers, restated in C++ over the serde JSON form of a KernelFn, and
+// the recognizer behind Backend::lower_kernel.
+//
+// Each lift builds exactly the KernelFn the reference's lift builds (same statements, locals,
+// parameters, launch shape and shared allocations), for the op forms this backend lowers: a
+// reduction or scan of one input with the identity body and no fused post, and a gather whose
+// body is the identity copy of the data input.  lower_kernel recognises a kernel by lifting
+// every candidate form its signature admits and comparing the trees: a kernel equal to a lift's
+// output is that form; anything else is refused with UnsupportedKernel (refuse rather than
+// approximate, crates/unpopped/src/backend.rs:703-707).
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <sstream>
+
+#include "kernel_ir.hpp"
+#include "unp_internal.hpp"
+
+namespace unp {
+namespace {
+
+using kir::J;
+using namespace kir;
+
+// A LiftDecline (crates/unpopped/src/kernel_lift.rs:48-85): the variant and its reason.
+struct Decline {
+  std::string what;
+};
+
+const char* EK(int32_t kind) { return kind_name(kind); }
+bool is_int_kernel_dtype(int32_t k) { return k == UNP_I32 || k == UNP_I64; }
+bool pow2(uint32_t v) { return v != 0 && (v & (v - 1)) == 0; }
+
+J thread() { return e_exec("ThreadIdx", 0); }
+J as_i32(J e) { return e_cast(std::move(e), "I32"); }
+J uconst(uint32_t v) { return e_int(v, "U32"); }
+J int_(int64_t v) { return e_int(v, "I32"); }
+J loc(uint32_t l) { return e_local(l); }
+
+const char* reduce_op_name(int32_t op) {
+  switch (op) {
+    case UNP_OP_SUM: return "Sum";
+    case UNP_OP_PROD: return "Prod";
+    case UNP_OP_MAX: return "Max";
+    case UNP_OP_MIN: return "Min";
+    case UNP_OP_MEAN: return "Mean";
+    default: return nullptr;
+  }
+}
+
+// `for counter(d) in 0..extent(d) { inner }` (kernel_lift.rs:1037-1047).
+std::vector<J> for_axis(uint32_t d, uint32_t r, std::vector<J> inner) {
+  return {s_for(r + d, int_(0), loc(d), int_(1), std::move(inner))};
+}
+
+// The Max/Min step with the NaN rule (kernel_lift.rs:1097-1160).
+std::vector<J> extremum_step(int32_t rop, uint32_t acc, uint32_t have, uint32_t val, bool is_int) {
+  const char* better = rop == UNP_OP_MAX ? "CmpGt" : "CmpLt";
+  J keep_going = s_if(e_bin(better, loc(val), loc(acc)), {s_assign(acc, loc(val))}, {});
+  J nan_check = is_int ? keep_going
+                       : s_if(e_bin("CmpNe", loc(val), loc(val)), {s_assign(acc, loc(val))}, {keep_going});
+  return {s_if(loc(have), {nan_check}, {s_assign(acc, loc(val))}), s_assign(have, int_(1))};
+}
+
+// The fold step (kernel_lift.rs:1049-1069) for the ops lowered here.
+std::vector<J> fold_step(int32_t rop, uint32_t acc, uint32_t have, uint32_t val, bool is_int) {
+  switch (rop) {
+    case UNP_OP_SUM:
+    case UNP_OP_MEAN:
+      return {s_assign(acc, e_add(loc(acc), loc(val)))};
+    case UNP_OP_PROD:
+      return {s_assign(acc, e_mul(loc(acc), loc(val)))};
+    default:
+      return extremum_step(rop, acc, have, val, is_int);
+  }
+}
+
+// A float-to-float (or int-to-float) cast that rounds to nearest even (kernel_lift.rs:1027-1034).
+J widen(J e, const char* to) { return e_cast(std::move(e), to); }
+
+// ReductionShape (kernel_lift.rs:838-1025) for one input.
+struct Shape {
+  int32_t dtype;
+  uint32_t r;
+  uint32_t n = 1;
+  std::vector<uint32_t> reduced, kept;
+  uint32_t acc, have, val, red;
+
+  Shape(int32_t dt, uint32_t rank, uint32_t axes_mask) : dtype(dt), r(rank) {
+    if (axes_mask == 0) reduced.push_back(r - 1);
+    else
+      for (uint32_t d = 0; d < r; ++d)
+        if (axes_mask & (1u << d)) reduced.push_back(d);
+    for (uint32_t d = 0; d < r; ++d)
+      if (std::find(reduced.begin(), reduced.end(), d) == reduced.end()) kept.push_back(d);
+    acc = 2 * r + n;
+    have = acc + 1;
+    val = acc + 2;
+    red = acc + 3;
+  }
+  uint32_t counter(uint32_t d) const { return r + d; }
+  uint32_t loaded(uint32_t k) const { return 2 * r + k; }
+  bool is_int() const { return is_int_kernel_dtype(dtype); }
+  const char* acc_ty() const { return is_int() ? EK(dtype) : "F64"; }
+  J up(J e) const { return (dtype == UNP_F64 || is_int()) ? e : widen(std::move(e), "F64"); }
+  J fold_identity(int32_t rop) const {
+    const bool one = rop == UNP_OP_PROD;
+    return is_int() ? e_int(one ? 1 : 0, EK(dtype)) : up(e_const(one ? 1.0 : 0.0));
+  }
+  std::vector<J> counters() const {
+    std::vector<J> c;
+    for (uint32_t d = 0; d < r; ++d) c.push_back(loc(counter(d)));
+    return c;
+  }
+  std::vector<J> reduce_loop(int32_t rop) const {
+    std::vector<J> inner = {s_load(loaded(0), p_logical(0, counters())), s_let(val, up(loc(loaded(0))))};
+    for (auto& s : fold_step(rop, acc, have, val, is_int())) inner.push_back(s);
+    for (auto it = reduced.rbegin(); it != reduced.rend(); ++it) inner = for_axis(*it, r, inner);
+    return inner;
+  }
+  std::vector<J> out_coords(bool keepdim) const {
+    std::vector<J> c;
+    for (uint32_t d = 0; d < r; ++d) {
+      const bool k = std::find(kept.begin(), kept.end(), d) != kept.end();
+      if (k) c.push_back(loc(counter(d)));
+      else if (keepdim) c.push_back(int_(0));
+    }
+    return c;
+  }
+  J stored(int32_t rop) const {
+    J v = loc(acc);
+    if (rop == UNP_OP_MEAN) {
+      J div;
+      bool first = true;
+      for (uint32_t d : reduced) {
+        J f = widen(loc(d), "F64");
+        div = first ? f : e_mul(div, f);
+        first = false;
+      }
+      v = e_div(v, div);
+    }
+    return (dtype == UNP_F64 || is_int()) ? v : widen(v, EK(dtype));
+  }
+  void signature(uint32_t out_rank, std::vector<J>& params, std::vector<J>& locals) const {
+    params = {param_buffer("in0", EK(dtype), "Read", (int)r), param_buffer("out", EK(dtype), "Write", (int)out_rank)};
+    for (uint32_t d = 0; d < r; ++d) params.push_back(param_scalar("n" + std::to_string(d), "I32", d));
+    locals.clear();
+    for (uint32_t i = 0; i < 2 * r; ++i) locals.push_back(local_decl("I32"));
+    locals.push_back(local_decl(EK(dtype)));
+    locals.push_back(local_decl(acc_ty()));
+    locals.push_back(local_decl("I32"));
+    locals.push_back(local_decl(acc_ty()));
+  }
+};
+
+// check_accumulated_dtype (kernel_lift.rs:763-803) for the ops lifted here.
+void check_accumulated(int32_t dtype, int32_t rop, const char* what) {
+  if (!reduce_op_name(rop)) throw Decline{"UnsupportedForm: a reduce op outside Sum, Prod, Max, Min and Mean"};
+  if (dtype == UNP_F32 || dtype == UNP_F64) return;
+  if (!is_int_kernel_dtype(dtype))
+    throw Decline{std::string("UnsupportedForm: ") + what + " outside F32, F64, I32 and I64"};
+  if (rop == UNP_OP_MEAN) throw Decline{"UnsupportedForm: an integer Mean"};
+}
+
+void check_rank(int32_t rank) {
+  if (rank < 1 || rank > 8) throw Decline{"BadRank"};
+}
+
+J launch_or_null(uint32_t block, uint32_t grid) { return (block || grid) ? launch_shape(block, grid) : J::null(); }
+
+// lift_reduction_opdef (kernel_lift.rs:447-484) and lift_reduction_opdef_launched
+// (kernel_lift/block_reduce.rs:50-93).
+J lift_reduction(const std::string& name, int32_t dtype, int32_t rank, int32_t rop, uint32_t axes, bool keepdim,
+                 uint32_t block, uint32_t grid) {
+  check_accumulated(dtype, rop, "a reduction");
+  check_rank(rank);
+  if (axes >> rank) throw Decline{"UnsupportedForm: a reduced axis outside the rank"};
+  const Shape sh(dtype, (uint32_t)rank, axes);
+  std::vector<J> params, locals;
+  const uint32_t out_rank = keepdim ? sh.r : (uint32_t)sh.kept.size();
+  sh.signature(out_rank, params, locals);
+  if (!block && !grid) {
+    std::vector<J> body = {s_let(sh.acc, sh.fold_identity(rop)), s_let(sh.have, int_(0))};
+    for (auto& s : sh.reduce_loop(rop)) body.push_back(s);
+    body.push_back(s_store(p_logical(sh.n, sh.out_coords(keepdim)), sh.stored(rop)));
+    for (auto it = sh.kept.rbegin(); it != sh.kept.rend(); ++it) body = for_axis(*it, sh.r, body);
+    return kernel_fn(name, EK(dtype), params, locals, body, J::null(), {});
+  }
+  if (grid == 0 || !pow2(block)) throw Decline{"BadLaunch"};
+  // check_order_independent (block_reduce.rs:97-133)
+  if ((rop == UNP_OP_PROD && !sh.is_int()) || (rop == UNP_OP_MEAN && sh.is_int()))
+    throw Decline{"UnsupportedForm: an integer Mean or a float Prod in a launched reduction"};
+  const bool flag = rop == UNP_OP_MAX || rop == UNP_OP_MIN;
+  const uint32_t partner_have = sh.red + 1;
+  auto publish = [&]() {
+    std::vector<J> v = {s_store(p_alloc(0, as_i32(thread())), loc(sh.acc))};
+    if (flag) v.push_back(s_store(p_alloc(1, as_i32(thread())), loc(sh.have)));
+    return v;
+  };
+  std::vector<J> row = {s_let(sh.acc, sh.fold_identity(rop)), s_let(sh.have, int_(0))};
+  std::vector<J> slice = sh.reduce_loop(rop);
+  // Tree::slice (block_reduce.rs:278-288): the outermost reduced loop starts at the thread
+  // and steps by the block.
+  J& f = slice[0].o[0].second;
+  for (auto& kv : f.o) {
+    if (kv.first == "start") kv.second = as_i32(thread());
+    if (kv.first == "step") kv.second = as_i32(e_exec("BlockDim", 0));
+  }
+  for (auto& s : slice) row.push_back(s);
+  for (auto& s : publish()) row.push_back(s);
+  row.push_back(s_barrier());
+  for (uint32_t s = block / 2; s > 0; s /= 2) {
+    const J partner = as_i32(e_add(thread(), uconst(s)));
+    std::vector<J> rb = {s_load(sh.val, p_alloc(0, partner))};
+    const std::vector<J> combine = fold_step(rop, sh.acc, sh.have, sh.val, sh.is_int());
+    if (flag) {
+      rb.push_back(s_load(partner_have, p_alloc(1, partner)));
+      rb.push_back(s_if(loc(partner_have), combine, {}));
+    } else {
+      for (auto& c : combine) rb.push_back(c);
+    }
+    for (auto& p : publish()) rb.push_back(p);
+    row.push_back(s_if(e_bin("CmpLt", thread(), uconst(s)), rb, {}));
+    row.push_back(s_barrier());
+  }
+  row.push_back(s_if(e_bin("CmpEq", thread(), uconst(0)), {s_store(p_logical(sh.n, sh.out_coords(keepdim)), sh.stored(rop))}, {}));
+  std::vector<J> body;
+  if (sh.kept.empty()) {
+    body = {s_if(e_bin("CmpEq", e_exec("BlockIdx", 0), uconst(0)), row, {})};
+  } else {
+    body = row;
+    for (auto it = sh.kept.rbegin(); it != sh.kept.rend(); ++it) body = for_axis(*it, sh.r, body);
+    J& outer = body[0].o[0].second;
+    for (auto& kv : outer.o) {
+      if (kv.first == "start") kv.second = as_i32(e_exec("BlockIdx", 0));
+      if (kv.first == "step") kv.second = as_i32(e_exec("GridDim", 0));
+    }
+  }
+  locals.push_back(local_decl(EK(dtype)));
+  locals.push_back(local_decl("I32"));
+  std::vector<J> allocs = {alloc_shared("partial", sh.acc_ty(), block)};
+  if (flag) allocs.push_back(alloc_shared("partial_have", "I32", block));
+  return kernel_fn(name, EK(dtype), params, locals, body, launch_shape(block, grid), allocs);
+}
+
+// scan_identity (kernel_lift.rs:712-753): the integer extremes, or the float identities with
+// the infinities built by Bitcast of their bit patterns.
+J scan_identity(int32_t rop, int32_t dtype) {
+  if (is_int_kernel_dtype(dtype)) {
+    const bool w = dtype == UNP_I64;
+    const int64_t lo = w ? INT64_MIN : INT32_MIN, hi = w ? INT64_MAX : INT32_MAX;
+    const int64_t v = rop == UNP_OP_PROD ? 1 : rop == UNP_OP_MAX ? lo : rop == UNP_OP_MIN ? hi : 0;
+    return e_int(v, EK(dtype));
+  }
+  auto inf = [&](bool neg) {
+    if (dtype == UNP_F64) {
+      const uint64_t b = neg ? 0xFFF0000000000000ull : 0x7FF0000000000000ull;
+      return e_bitcast(e_int((int64_t)b, "I64"), "F64");
+    }
+    const uint32_t b = neg ? 0xFF800000u : 0x7F800000u;
+    return e_bitcast(e_int((int64_t)(int32_t)b, "I32"), EK(dtype));
+  };
+  switch (rop) {
+    case UNP_OP_PROD: return e_const(1.0);
+    case UNP_OP_MAX: return inf(true);
+    case UNP_OP_MIN: return inf(false);
+    default: return e_const(0.0);
+  }
+}
+
+bool dtype_is_f64(const Shape& sh) { return sh.dtype == UNP_F64; }
+
+// scan_pass (kernel_lift.rs:548-576) with the identity pre-map and no post.
+std::vector<J> scan_pass(const Shape& sh, int32_t rop, bool exclusive) {
+  std::vector<J> pass = {s_load(sh.loaded(0), p_logical(0, sh.counters())), s_let(sh.val, sh.up(loc(sh.loaded(0))))};
+  // scan_stored (kernel_lift.rs:604-619): a running Mean divides by the count folded so far.
+  J stored = sh.stored(rop);
+  if (rop == UNP_OP_MEAN) {
+    J mean = e_div(loc(sh.acc), widen(loc(sh.have), "F64"));
+    stored = dtype_is_f64(sh) ? mean : widen(mean, EK(sh.dtype));
+  }
+  J write = s_store(p_logical(sh.n, sh.counters()), stored);
+  std::vector<J> fold = fold_step(rop, sh.acc, sh.have, sh.val, sh.is_int());
+  if (rop == UNP_OP_MEAN) fold.push_back(s_assign(sh.have, e_add(loc(sh.have), int_(1))));
+  if (exclusive) {
+    pass.push_back(write);
+    for (auto& s : fold) pass.push_back(s);
+  } else {
+    for (auto& s : fold) pass.push_back(s);
+    pass.push_back(write);
+  }
+  return pass;
+}
+
+// lift_scan_opdef (kernel_lift.rs:504-519) and lift_scan_opdef_launched
+// (kernel_lift/scan_launched.rs:54-102), identity pre-map, no post.
+J lift_scan(const std::string& name, int32_t dtype, int32_t rank, int32_t rop, int32_t axis, bool exclusive,
+            bool reverse, uint32_t block, uint32_t grid) {
+  check_accumulated(dtype, rop, "a scan");
+  check_rank(rank);
+  const bool launched = block || grid;
+  if (axis < 0 || axis >= rank) throw Decline{"UnsupportedForm: a scan axis outside the rank"};
+  if (launched && axis != rank - 1) throw Decline{"UnsupportedForm: a scan over a non-innermost axis in a launched scan"};
+  if (rop == UNP_OP_MEAN && dtype != UNP_F32 && dtype != UNP_F64) throw Decline{"UnsupportedForm: an integer Mean"};
+  if (!launched) {
+    const Shape sh(dtype, (uint32_t)rank, 1u << axis);
+    const uint32_t scanned = sh.reduced[0];
+    std::vector<J> pass = scan_pass(sh, rop, exclusive);
+    J start = reverse ? e_sub(loc(scanned), int_(1)) : int_(0);
+    J end = reverse ? int_(-1) : loc(scanned);
+    J step = reverse ? int_(-1) : int_(1);
+    std::vector<J> row = {s_let(sh.acc, sh.up(scan_identity(rop, dtype))), s_let(sh.have, int_(0)),
+                          s_for(sh.counter(scanned), start, end, step, pass)};
+    for (auto it = sh.kept.rbegin(); it != sh.kept.rend(); ++it) row = for_axis(*it, sh.r, row);
+    std::vector<J> params, locals;
+    sh.signature(sh.r, params, locals);
+    return kernel_fn(name, EK(dtype), params, locals, row, J::null(), {});
+  }
+  if (grid == 0 || !pow2(block)) throw Decline{"BadLaunch"};
+  const Shape sh(dtype, (uint32_t)rank, 0);
+  if (rop == UNP_OP_MEAN) throw Decline{"UnsupportedForm: a Mean scan in a launched scan"};
+  if (rop == UNP_OP_PROD && !sh.is_int()) throw Decline{"UnsupportedForm: a float Prod scan in a launched scan"};
+  const bool flag = rop == UNP_OP_MAX || rop == UNP_OP_MIN;
+  const uint32_t base = sh.red + 1;
+  const uint32_t chunk = base, lo = base + 1, hi = base + 2, partner = base + 3, flag_tmp = base + 4;
+  const uint32_t scanned = sh.reduced[0];
+  auto identity = [&]() { return sh.up(scan_identity(rop, dtype)); };
+  auto tid = [&]() { return as_i32(thread()); };
+  auto publish = [&]() {
+    std::vector<J> v = {s_store(p_alloc(0, as_i32(thread())), loc(sh.acc))};
+    if (flag) v.push_back(s_store(p_alloc(1, as_i32(thread())), loc(sh.have)));
+    return v;
+  };
+  auto walk = [&](std::vector<J> body) {
+    J n = loc(scanned);
+    if (reverse)
+      return s_for(sh.counter(scanned), e_sub(e_sub(n, int_(1)), loc(lo)), e_sub(e_sub(n, int_(1)), loc(hi)), int_(-1), body);
+    return s_for(sh.counter(scanned), loc(lo), loc(hi), int_(1), body);
+  };
+  std::vector<J> fold_only = {s_load(sh.loaded(0), p_logical(0, sh.counters())), s_let(sh.val, sh.up(loc(sh.loaded(0))))};
+  for (auto& s : fold_step(rop, sh.acc, sh.have, sh.val, sh.is_int())) fold_only.push_back(s);
+  std::vector<J> row = {s_let(sh.acc, identity()), s_let(sh.have, int_(0)), s_let(partner, identity()), walk(fold_only)};
+  for (auto& s : publish()) row.push_back(s);
+  row.push_back(s_barrier());
+  for (uint32_t d = 1; d < block; d *= 2) {
+    J active = e_bin("CmpGe", thread(), uconst(d));
+    std::vector<J> read = {s_load(sh.val, p_alloc(0, as_i32(e_sub(thread(), uconst(d))))), s_assign(partner, loc(sh.val))};
+    std::vector<J> comb = fold_step(rop, sh.acc, sh.have, partner, sh.is_int());
+    for (auto& s : publish()) comb.push_back(s);
+    row.push_back(s_if(active, read, {}));
+    row.push_back(s_barrier());
+    row.push_back(s_if(active, comb, {}));
+    row.push_back(s_barrier());
+  }
+  {
+    const J prev = as_i32(e_sub(thread(), uconst(1)));
+    std::vector<J> load = {s_load(sh.val, p_alloc(0, prev)), s_assign(sh.acc, loc(sh.val))};
+    if (flag) {
+      load.push_back(s_load(flag_tmp, p_alloc(1, prev)));
+      load.push_back(s_assign(sh.have, loc(flag_tmp)));
+    }
+    row.push_back(s_if(e_bin("CmpEq", thread(), uconst(0)), {s_assign(sh.acc, identity()), s_assign(sh.have, int_(0))}, load));
+  }
+  row.push_back(walk(scan_pass(sh, rop, exclusive)));
+  row.push_back(s_barrier());
+  std::vector<J> body;
+  if (sh.kept.empty()) {
+    body = {s_if(e_bin("CmpEq", e_exec("BlockIdx", 0), uconst(0)), row, {})};
+  } else {
+    body = row;
+    for (auto it = sh.kept.rbegin(); it != sh.kept.rend(); ++it) body = for_axis(*it, sh.r, body);
+    J& outer = body[0].o[0].second;
+    for (auto& kv : outer.o) {
+      if (kv.first == "start") kv.second = as_i32(e_exec("BlockIdx", 0));
+      if (kv.first == "step") kv.second = as_i32(e_exec("GridDim", 0));
+    }
+  }
+  // Scan::bounds (scan_launched.rs:173-207), spliced in front of the body.
+  J n = loc(scanned);
+  std::vector<J> bounds = {
+      s_let(chunk, int_(0)),
+      s_while(e_bin("CmpLt", e_mul(loc(chunk), int_(block)), n), {s_assign(chunk, e_add(loc(chunk), int_(1)))}),
+      s_let(lo, e_mul(tid(), loc(chunk))),
+      s_let(hi, e_bin("Min", e_add(loc(lo), loc(chunk)), n)),
+  };
+  body.insert(body.begin(), bounds.begin(), bounds.end());
+  std::vector<J> params, locals;
+  sh.signature(sh.r, params, locals);
+  locals.push_back(local_decl(EK(dtype)));
+  for (int i = 0; i < 3; ++i) locals.push_back(local_decl("I32"));
+  locals.push_back(local_decl(sh.acc_ty()));
+  locals.push_back(local_decl("I32"));
+  std::vector<J> allocs = {alloc_shared("partial", sh.acc_ty(), block)};
+  if (flag) allocs.push_back(alloc_shared("partial_have", "I32", block));
+  return kernel_fn(name, EK(dtype), params, locals, body, launch_shape(block, grid), allocs);
+}
+
+// grid_stride_outermost (kernel_lift.rs:288-312): the outermost loop becomes a grid-stride loop.
+void grid_stride(J& k, uint32_t block, uint32_t grid) {
+  if (block == 0 || grid == 0) throw Decline{"BadLaunch"};
+  J* body = nullptr;
+  for (auto& kv : k.o)
+    if (kv.first == "body") body = &kv.second;
+  J& outer = body->a[0].o[0].second;
+  for (auto& kv : outer.o) {
+    if (kv.first == "start")
+      kv.second = as_i32(e_add(e_mul(e_exec("BlockIdx", 0), e_exec("BlockDim", 0)), e_exec("ThreadIdx", 0)));
+    if (kv.first == "step") kv.second = as_i32(e_mul(e_exec("GridDim", 0), e_exec("BlockDim", 0)));
+  }
+  for (auto& kv : k.o)
+    if (kv.first == "launch") kv.second = launch_shape(block, grid);
+}
+
+// lift_gather_opdef (kernel_lift/gather.rs:35-55, cell :184-232) for OpDef::gather's inputs:
+// Input(0) the data, Input(1) the index, the identity copy body; launched by grid_stride.
+J lift_gather(const std::string& name, int32_t dtype, int32_t rank, int32_t idx, int32_t axis, int32_t oob,
+              uint32_t block, uint32_t grid) {
+  check_rank(rank);
+  if (idx != UNP_I32 && idx != UNP_I64 && idx != UNP_U32) throw Decline{"UnsupportedForm: a non-integer gather index"};
+  if (axis < 0 || axis >= rank) throw Decline{"UnsupportedForm: an ill-formed gather"};
+  if (!kind_name(dtype) || kind_bytes(dtype) == 0) throw Decline{"UnsupportedForm: a gather of a sub-byte dtype"};
+  const uint32_t r = (uint32_t)rank, n = 2, data = 0, index = 1;
+  const uint32_t loaded0 = 2 * r, loaded1 = 2 * r + 1, extent = 2 * r + n, clamped = extent + 1;
+  auto at = [&](uint32_t buffer, int via_axis, uint32_t via) {
+    std::vector<J> c;
+    for (uint32_t d = 0; d < r; ++d) c.push_back(((int)d == via_axis) ? loc(via) : loc(r + d));
+    return p_logical(buffer, c);
+  };
+  auto ic = [&](int64_t v) { return e_int(v, EK(idx)); };
+  J raw = loc(loaded1);
+  J clamp = e_bin("Min", e_bin("Max", raw, ic(0)), e_sub(loc(extent), ic(1)));
+  J zero = (dtype == UNP_I32 || dtype == UNP_I64 || dtype == UNP_U32 || dtype == UNP_I8 || dtype == UNP_I16 ||
+            dtype == UNP_U8 || dtype == UNP_U16 || dtype == UNP_U64)
+               ? e_int(0, EK(dtype))
+               : e_const(0.0);
+  std::vector<J> compute = {s_load(loaded0, at(data, axis, clamped)), s_store(at(n, -1, 0), loc(loaded0))};
+  auto guarded = [&](std::vector<J> oobb) {
+    J upper = s_if(e_bin("CmpGe", raw, loc(extent)), oobb, compute);
+    return s_if(e_bin("CmpLt", raw, ic(0)), oobb, {upper});
+  };
+  std::vector<J> cell = {s_load(loaded1, at(index, -1, 0)), s_let(clamped, clamp)};
+  if (oob == UNP_OOB_SKIP) cell.push_back(guarded({}));
+  else if (oob == UNP_OOB_ZEROFILL) cell.push_back(guarded({s_store(at(n, -1, 0), zero)}));
+  else if (oob == UNP_OOB_CLAMP)
+    for (auto& s : compute) cell.push_back(s);
+  else throw Decline{"UnsupportedForm: an unknown out-of-range policy"};
+  std::vector<J> body = cell;
+  for (int d = (int)r - 1; d >= 0; --d) body = {s_for(r + d, int_(0), loc((uint32_t)d), int_(1), body)};
+  std::vector<J> params = {param_buffer("in0", EK(dtype), "Read", rank), param_buffer("in1", EK(idx), "Read", rank),
+                           param_buffer("out", EK(dtype), "Write", rank)};
+  for (uint32_t d = 0; d < r; ++d) params.push_back(param_scalar("n" + std::to_string(d), "I32", d));
+  params.push_back(param_scalar("src_extent", EK(idx), extent));
+  std::vector<J> locals;
+  for (uint32_t i = 0; i < 2 * r; ++i) locals.push_back(local_decl("I32"));
+  locals.push_back(local_decl(EK(dtype)));
+  locals.push_back(local_decl(EK(idx)));
+  locals.push_back(local_decl(EK(idx)));
+  locals.push_back(local_decl(EK(idx)));
+  J k = kernel_fn(name, EK(dtype), params, locals, body, J::null(), {});
+  if (block || grid) grid_stride(k, block, grid);
+  return k;
+}
+
+// The fused row fold this backend authors for the softmax prologue: out0[r] and out1[r] fold
+// row r of a rank-2 input once, each exactly as a serial lifted reduction folds it (kept axis
+// outer, reduced axis ascending, f64 accumulator for a float, Max/Min with the NaN rule, one
+// cast down at each store).  Launched: rows grid-strided, one thread per row.
+J row_reduce2(const std::string& name, int32_t dtype, int32_t op0, int32_t op1, uint32_t block, uint32_t grid) {
+  check_accumulated(dtype, op0, "a reduction");
+  check_accumulated(dtype, op1, "a reduction");
+  const Shape sh(dtype, 2, 0);
+  const uint32_t x = 4, a0 = 5, h0 = 6, a1 = 7, h1 = 8, v = 9;
+  auto stored = [&](int32_t op, uint32_t acc) {
+    J e = loc(acc);
+    if (op == UNP_OP_MEAN) e = e_div(e, widen(loc(1), "F64"));
+    return (dtype == UNP_F64 || sh.is_int()) ? e : widen(e, EK(dtype));
+  };
+  std::vector<J> inner = {s_load(x, p_logical(0, {loc(2), loc(3)})), s_let(v, sh.up(loc(x)))};
+  for (auto& s : fold_step(op0, a0, h0, v, sh.is_int())) inner.push_back(s);
+  for (auto& s : fold_step(op1, a1, h1, v, sh.is_int())) inner.push_back(s);
+  std::vector<J> row = {s_let(a0, sh.fold_identity(op0)), s_let(h0, int_(0)), s_let(a1, sh.fold_identity(op1)),
+                        s_let(h1, int_(0)), s_for(3, int_(0), loc(1), int_(1), inner),
+                        s_store(p_logical(1, {loc(2)}), stored(op0, a0)), s_store(p_logical(2, {loc(2)}), stored(op1, a1))};
+  std::vector<J> body = {s_for(2, int_(0), loc(0), int_(1), row)};
+  std::vector<J> params = {param_buffer("in0", EK(dtype), "Read", 2), param_buffer("out0", EK(dtype), "Write", 1),
+                           param_buffer("out1", EK(dtype), "Write", 1), param_scalar("n0", "I32", 0),
+                           param_scalar("n1", "I32", 1)};
+  std::vector<J> locals = {local_decl("I32"), local_decl("I32"), local_decl("I32"), local_decl("I32"),
+                           local_decl(EK(dtype)), local_decl(sh.acc_ty()), local_decl("I32"), local_decl(sh.acc_ty()),
+                           local_decl("I32"), local_decl(sh.acc_ty())};
+  J k = kernel_fn(name, EK(dtype), params, locals, body, J::null(), {});
+  if (block || grid) grid_stride(k, block, grid);
+  return k;
+}
+
+// The sub-byte dequant this backend authors (the reference has no dequant lift; this follows
+// the dequant-GEMM fixture, crates/unpopped/tests/support/dequant.rs:58-143): for row r and
+// column c of a rows x cols matrix, load the 4-bit weight (element r * cols + c of a flat
+// U4/I4 buffer), the zero point and the f16 scale of group g (element r * ng + g, ng = ceil(cols
+// / G), found by counting since the kernel integer subset has no division), widen the sub-byte
+// values to I32 first (kernel_subbyte_load.rs:206-212), subtract, cast to F32, multiply by the
+// scale cast to F32, and store the product cast to Bf16 with round-to-nearest-even.  The group
+// index advances with an in-group counter.  Launched: rows grid-strided, one thread per row.
+J dequant4(const std::string& name, int32_t qk, int32_t zk, int32_t group, uint32_t block, uint32_t grid) {
+  if ((qk != UNP_U4 && qk != UNP_I4) || (zk != UNP_U4 && zk != UNP_I4))
+    throw Decline{"UnsupportedForm: dequant weights and zero points are U4 or I4"};
+  if (group < 1) throw Decline{"UnsupportedForm: a dequant group of zero columns"};
+  const uint32_t R = 2, Cc = 3, NG = 4, G = 5, J_ = 6, Q = 7, Z = 8, S = 9, D = 10, F = 11;
+  J e = e_add(e_mul(loc(R), loc(1)), loc(Cc));
+  J zi = e_add(e_mul(loc(R), loc(NG)), loc(G));
+  std::vector<J> inner = {
+      s_load(Q, p_logical(0, {e})),
+      s_load(Z, p_logical(2, {zi})),
+      s_load(S, p_logical(1, {zi})),
+      s_let(D, e_sub(e_cast(loc(Q), "I32"), e_cast(loc(Z), "I32"))),
+      s_let(F, e_mul(e_cast(loc(D), "F32"), e_cast(loc(S), "F32"))),
+      s_store(p_logical(3, {e}), e_cast(loc(F), "Bf16")),
+      s_assign(J_, e_add(loc(J_), int_(1))),
+      s_if(e_bin("CmpEq", loc(J_), int_(group)), {s_assign(J_, int_(0)), s_assign(G, e_add(loc(G), int_(1)))}, {}),
+  };
+  std::vector<J> row = {
+      s_let(NG, int_(0)),
+      s_while(e_bin("CmpLt", e_mul(loc(NG), int_(group)), loc(1)), {s_assign(NG, e_add(loc(NG), int_(1)))}),
+      s_let(G, int_(0)),
+      s_let(J_, int_(0)),
+      s_for(Cc, int_(0), loc(1), int_(1), inner),
+  };
+  std::vector<J> body = {s_for(R, int_(0), loc(0), int_(1), row)};
+  std::vector<J> params = {param_buffer("w", EK(qk), "Read", 1), param_buffer("scale", "F16", "Read", 1),
+                           param_buffer("zero", EK(zk), "Read", 1), param_buffer("out", "Bf16", "Write", 1),
+                           param_scalar("n0", "I32", 0), param_scalar("n1", "I32", 1)};
+  std::vector<J> locals = {local_decl("I32"), local_decl("I32"), local_decl("I32"), local_decl("I32"),
+                           local_decl("I32"), local_decl("I32"), local_decl("I32"), local_decl(EK(qk)),
+                           local_decl(EK(zk)), local_decl("F16"), local_decl("I32"), local_decl("F32")};
+  J k = kernel_fn(name, "F32", params, locals, body, J::null(), {});
+  if (block || grid) grid_stride(k, block, grid);
+  return k;
+}
+
+// ---- recognition -------------------------------------------------------------------------
+
+// Fill the serde defaults a writer may omit (KernelFn: launch, allocs, result, results;
+// LaunchShape: cluster, devices, grid_dims; For: unroll), recursively.
+void normalize(J& j, bool top) {
+  if (j.t == J::Arr) {
+    for (auto& x : j.a) normalize(x, false);
+    return;
+  }
+  if (j.t != J::Obj) return;
+  auto ensure = [&](const char* key, J v) {
+    if (!j.get(key)) j.o.emplace_back(key, std::move(v));
+  };
+  if (top) {
+    ensure("launch", J::null());
+    ensure("allocs", J::arr());
+    ensure("result", J::null());
+    ensure("results", J::arr());
+    for (auto& kv : j.o)
+      if (kv.first == "launch" && kv.second.t == J::Obj) {
+        J& l = kv.second;
+        if (!l.get("subgroup")) l.o.emplace_back("subgroup", J::null());
+        if (!l.get("cluster")) l.o.emplace_back("cluster", J::null());
+        if (!l.get("devices")) l.o.emplace_back("devices", J::integer(1));
+        if (!l.get("grid_dims")) l.o.emplace_back("grid_dims", J::null());
+      }
+  }
+  if (j.o.size() == 1 && j.o[0].first == "For" && j.o[0].second.t == J::Obj) {
+    J& f = j.o[0].second;
+    if (!f.get("unroll")) f.o.emplace_back("unroll", unit("None"));
+  }
+  for (auto& kv : j.o)
+    if (!(top && kv.first == "launch")) normalize(kv.second, false);
+}
+
+struct ParamInfo {
+  bool buffer = false;
+  int32_t elem = -1;
+  std::string role;
+  int rank = -1;
+};
+
+bool read_params(const J& k, std::vector<ParamInfo>& out) {
+  const J* ps = k.get("params");
+  if (!ps || ps->t != J::Arr) return false;
+  for (const J& p : ps->a) {
+    const J* kind = p.get("kind");
+    if (!kind || kind->t != J::Obj || kind->o.size() != 1) return false;
+    ParamInfo pi;
+    const J& body = kind->o[0].second;
+    if (kind->o[0].first == "Buffer") {
+      pi.buffer = true;
+      const J* e = body.get("elem");
+      const J* role = body.get("role");
+      const J* rank = body.get("rank");
+      if (!e || e->t != J::Str || !role || role->t != J::Str) return false;
+      pi.elem = kind_from_name(e->s);
+      pi.role = role->s;
+      pi.rank = (rank && rank->t == J::Num) ? (int)rank->i : -1;
+    } else if (kind->o[0].first == "Scalar") {
+      const J* t = body.get("ty");
+      if (!t || t->t != J::Str) return false;
+      pi.elem = kind_from_name(t->s);
+    } else {
+      return false;
+    }
+    out.push_back(pi);
+  }
+  return true;
+}
+
+}  // namespace
+
+int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& why) {
+  J k;
+  if (!kir::parse(text, k, why)) {
+    why = "kernel JSON: " + why;
+    return UNP_PARSE_ERROR;
+  }
+  if (k.t != J::Obj || !k.get("name") || k.get("name")->t != J::Str || !k.get("compute") || !k.get("body")) {
+    why = "not a KernelFn: expected an object with name, compute, params, locals and body";
+    return UNP_PARSE_ERROR;
+  }
+  normalize(k, true);
+  const std::string name = k.get("name")->s;
+  std::vector<ParamInfo> ps;
+  if (!read_params(k, ps)) {
+    why = "not a KernelFn: malformed params";
+    return UNP_PARSE_ERROR;
+  }
+  uint32_t block = 0, grid = 0;
+  const J* launch = k.get("launch");
+  if (launch->t == J::Obj) {
+    const J* b = launch->get("block");
+    const J* g = launch->get("grid");
+    if (b && b->t == J::Arr && !b->a.empty() && b->a[0].is_int) block = (uint32_t)b->a[0].i;
+    if (g && g->t == J::Arr && !g->a.empty() && g->a[0].is_int) grid = (uint32_t)g->a[0].i;
+    if (!block || !grid) {
+      why = "a launch shape with a zero block or grid";
+      return UNP_UNSUPPORTED_KERNEL;
+    }
+  }
+  out.name = name;
+  out.launch = *launch;
+  out.params = *k.get("params");
+  auto matches = [&](const J& cand) {
+    J c = cand;
+    for (auto& kv : c.o)
+      if (kv.first == "name") kv.second = J::str(name);
+    return c == k;
+  };
+  auto attempt = [&](auto&& make) {
+    try {
+      return matches(make());
+    } catch (const Decline&) {
+      return false;
+    }
+  };
+  const size_t np = ps.size();
+  // Reduction or scan: in0 Read (rank r), out Write, then r I32 extents.
+  if (np >= 3 && ps[0].buffer && ps[0].role == "Read" && ps[1].buffer && ps[1].role == "Write" &&
+      ps[0].rank >= 1 && (size_t)ps[0].rank + 2 == np) {
+    const int32_t dt = ps[0].elem, r = ps[0].rank, orank = ps[1].rank;
+    static const int32_t ops[] = {UNP_OP_SUM, UNP_OP_PROD, UNP_OP_MAX, UNP_OP_MIN, UNP_OP_MEAN};
+    for (int32_t op : ops) {
+      for (int32_t from = r - 1; from >= 0; --from) {
+        uint32_t mask = 0;
+        for (int32_t d = from; d < r; ++d) mask |= 1u << d;
+        for (int keep = 0; keep <= 1; ++keep) {
+          const int32_t want = keep ? r : from;
+          if (orank != want) continue;
+          if (attempt([&] { return lift_reduction(name, dt, r, op, mask, keep, block, grid); })) {
+            out.form.kind = UNP_FORM_REDUCTION;
+            out.form.dtype = dt;
+            out.form.rank = r;
+            out.form.op0 = op;
+            out.form.reduced_from = from;
+            out.lift = block ? "lift_reduction_opdef_launched" : "lift_reduction_opdef";
+            return UNP_OK;
+          }
+        }
+      }
+      if (orank == r) {
+        for (int ex = 0; ex <= 1; ++ex)
+          for (int rev = 0; rev <= 1; ++rev)
+            if (attempt([&] { return lift_scan(name, dt, r, op, r - 1, ex, rev, block, grid); })) {
+              out.form.kind = UNP_FORM_SCAN;
+              out.form.dtype = dt;
+              out.form.rank = r;
+              out.form.op0 = op;
+              out.form.exclusive = ex;
+              out.form.reverse = rev;
+              out.lift = block ? "lift_scan_opdef_launched" : "lift_scan_opdef";
+              return UNP_OK;
+            }
+      }
+    }
+  }
+  // Fused row fold: in0 Read rank 2, out0 / out1 Write rank 1, two I32 extents.
+  if (np == 5 && ps[0].buffer && ps[0].rank == 2 && ps[1].buffer && ps[2].buffer && !ps[3].buffer && !ps[4].buffer) {
+    static const int32_t ops[] = {UNP_OP_SUM, UNP_OP_PROD, UNP_OP_MAX, UNP_OP_MIN, UNP_OP_MEAN};
+    for (int32_t a : ops)
+      for (int32_t b : ops)
+        if (attempt([&] { return row_reduce2(name, ps[0].elem, a, b, block, grid); })) {
+          out.form.kind = UNP_FORM_ROW_REDUCE2;
+          out.form.dtype = ps[0].elem;
+          out.form.rank = 2;
+          out.form.op0 = a;
+          out.form.op1 = b;
+          out.form.reduced_from = 1;
+          out.lift = "row_reduce2";
+          return UNP_OK;
+        }
+  }
+  // Gather: in0 data, in1 index, out, r I32 extents, src_extent.
+  if (np >= 5 && ps[0].buffer && ps[1].buffer && ps[2].buffer && ps[2].role == "Write" && ps[0].rank >= 1 &&
+      (size_t)ps[0].rank + 4 == np) {
+    const int32_t r = ps[0].rank;
+    static const int32_t pols[] = {UNP_OOB_SKIP, UNP_OOB_ZEROFILL, UNP_OOB_CLAMP};
+    for (int32_t axis = 0; axis < r; ++axis)
+      for (int32_t pol : pols)
+        if (attempt([&] { return lift_gather(name, ps[0].elem, r, ps[1].elem, axis, pol, block, grid); })) {
+          if (axis != 0) {
+            why = "a gather along axis " + std::to_string(axis) + " (this backend lowers row gathers, axis 0)";
+            return UNP_UNSUPPORTED_KERNEL;
+          }
+          out.form.kind = UNP_FORM_GATHER;
+          out.form.dtype = ps[0].elem;
+          out.form.rank = r;
+          out.form.index_dtype = ps[1].elem;
+          out.form.oob = pol;
+          out.form.data_slot = 0;
+          out.lift = block ? "lift_gather_opdef_launched" : "lift_gather_opdef";
+          return UNP_OK;
+        }
+  }
+  // Dequant: w (U4/I4), scale (F16), zero (U4/I4), out (Bf16), two I32 extents; the group is
+  // the constant of the column-group counting loop.
+  if (np == 6 && ps[0].buffer && ps[1].buffer && ps[2].buffer && ps[3].buffer && ps[1].elem == UNP_F16 &&
+      ps[3].elem == UNP_BF16) {
+    int64_t group = -1;
+    const J* body = k.get("body");
+    // body[0] = For rows { .., While(CmpLt(Mul(ng, G), n1)) .. }
+    if (body && body->t == J::Arr && !body->a.empty() && body->a[0].get("For")) {
+      const J* rowb = body->a[0].get("For")->get("body");
+      if (rowb && rowb->t == J::Arr && rowb->a.size() > 1 && rowb->a[1].get("While")) {
+        const J* cond = rowb->a[1].get("While")->get("cond");
+        const J* bin = cond ? cond->get("Binary") : nullptr;
+        if (bin && bin->t == J::Arr && bin->a.size() == 3) {
+          const J* mul = bin->a[1].get("Mul");
+          if (mul && mul->t == J::Arr && mul->a.size() == 2) {
+            const J* ci = mul->a[1].get("ConstInt");
+            if (ci && ci->t == J::Arr && !ci->a.empty() && ci->a[0].is_int) group = ci->a[0].i;
+          }
+        }
+      }
+    }
+    if (group >= 1 && group <= (1 << 30) &&
+        attempt([&] { return dequant4(name, ps[0].elem, ps[2].elem, (int32_t)group, block, grid); })) {
+      out.form.kind = UNP_FORM_DEQUANT4;
+      out.form.q_kind = ps[0].elem;
+      out.form.z_kind = ps[2].elem;
+      out.form.group = (int32_t)group;
+      out.form.out_kind = UNP_BF16;
+      out.lift = "dequant4";
+      return UNP_OK;
+    }
+  }
+  why = "kernel `" + name +
+        "` is not one of the forms this backend lowers (a lifted reduction, scan or row gather of one input "
+        "with the identity body, the fused row fold, or the int4 dequant)";
+  return UNP_UNSUPPORTED_KERNEL;
+}
+
+namespace {
+
+int32_t emit(J k, char** json, unp_error* err) {
+  const std::string s = kir::write(k);
+  *json = static_cast<char*>(std::malloc(s.size() + 1));
+  if (!*json) {
+    set_error(err, UNP_INVALID_ARGUMENT, "out of memory");
+    return UNP_INVALID_ARGUMENT;
+  }
+  std::memcpy(*json, s.c_str(), s.size() + 1);
+  set_error(err, UNP_OK, "");
+  return UNP_OK;
+}
+
+template <class F> int32_t lift_call(char** json, unp_error* err, F&& f) {
+  if (!json) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null output");
+    return UNP_INVALID_ARGUMENT;
+  }
+  *json = nullptr;
+  try {
+    return emit(f(), json, err);
+  } catch (const Decline& d) {
+    set_error(err, UNP_LIFT_DECLINE, d.what);
+    return UNP_LIFT_DECLINE;
+  }
+}
+
+}  // namespace
+}  // namespace unp
+
+extern "C" {
+
+int32_t unp_lift_reduction(const char* name, int32_t dtype, int32_t rank, int32_t op, uint32_t axes_mask,
+                           int32_t keepdim, uint32_t block, uint32_t grid, char** json, unp_error* err) {
+  return unp::lift_call(json, err, [&] {
+    return unp::lift_reduction(name ? name : "reduce", dtype, rank, op, axes_mask, keepdim != 0, block, grid);
+  });
+}
+
+int32_t unp_lift_scan(const char* name, int32_t dtype, int32_t rank, int32_t op, int32_t axis, int32_t exclusive,
+                      int32_t reverse, uint32_t block, uint32_t grid, char** json, unp_error* err) {
+  return unp::lift_call(json, err, [&] {
+    return unp::lift_scan(name ? name : "scan", dtype, rank, op, axis, exclusive != 0, reverse != 0, block, grid);
+  });
+}
+
+int32_t unp_lift_gather(const char* name, int32_t dtype, int32_t rank, int32_t index_dtype, int32_t axis,
+                        int32_t oob, uint32_t block, uint32_t grid, char** json, unp_error* err) {
+  return unp::lift_call(json, err, [&] {
+    return unp::lift_gather(name ? name : "gather", dtype, rank, index_dtype, axis, oob, block, grid);
+  });
+}
+
+int32_t unp_kernel_row_reduce2(const char* name, int32_t dtype, int32_t op0, int32_t op1, uint32_t block,
+                               uint32_t grid, char** json, unp_error* err) {
+  return unp::lift_call(json, err, [&] { return unp::row_reduce2(name ? name : "row_reduce2", dtype, op0, op1, block, grid); });
+}
+
+int32_t unp_kernel_dequant4(const char* name, int32_t q_kind, int32_t z_kind, int32_t group, uint32_t block,
+                            uint32_t grid, char** json, unp_error* err) {
+  return unp::lift_call(json, err, [&] { return unp::dequant4(name ? name : "dequant4", q_kind, z_kind, group, block, grid); });
+}
+
+}  // extern "C"

@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cstdlib>
 
+#include "kernel_ir.hpp"
 #include "unp_internal.hpp"
 
 using unp::set_error;
@@ -103,6 +104,39 @@ int32_t unp_hip_lower_form(const unp_form* form, unp_generated** out, unp_error*
     set_error(err, rc, why);
     return rc;
   }
+  set_error(err, UNP_OK, "");
+  *out = g;
+  return UNP_OK;
+}
+
+int32_t unp_hip_lower_kernel(const char* kernel_json, unp_generated** out, unp_error* err) {
+  if (out) *out = nullptr;
+  if (!kernel_json || !out) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null kernel or output");
+    return UNP_INVALID_ARGUMENT;
+  }
+  unp::Recognized rec;
+  std::string why;
+  int32_t rc = unp::recognize_kernel(kernel_json, rec, why);
+  if (rc != UNP_OK) {
+    set_error(err, rc, why);
+    return rc;
+  }
+  auto* g = new unp_generated();
+  rc = unp::lower_form(rec.form, g->l, why);
+  if (rc != UNP_OK) {
+    delete g;
+    // A recognised lift whose form this backend has no kernel for is a refusal of the kernel.
+    set_error(err, UNP_UNSUPPORTED_KERNEL, why);
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  // The interface's core half (KernelInterface::of, kernel_interface.rs:237-262): the kernel's
+  // declared launch and parameters, beside the emitter half the form wrote.
+  std::string& j = g->l.interface_json;
+  j.pop_back();
+  j += ",\"kernel\":" + unp::kir::write(unp::kir::J::str(rec.name)) + ",\"lift\":\"" + rec.lift +
+       "\",\"declared_launch\":" + unp::kir::write(rec.launch) + ",\"kernel_params\":" + unp::kir::write(rec.params) +
+       "}";
   set_error(err, UNP_OK, "");
   *out = g;
   return UNP_OK;

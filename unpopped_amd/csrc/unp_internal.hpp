@@ -8,6 +8,7 @@
 #include <vector>
 
 #include "../../include/unpopped_hip.h"
+#include "kernel_ir.hpp"
 
 namespace unp {
 
@@ -47,6 +48,18 @@ struct Lowered {
 // Emit the HIP source and interface for `f`; on refusal returns a nonzero unp_status and
 // fills `detail`.
 int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail);
+
+// Backend::lower_kernel's recognizer (lifts.cpp): the form a KernelFn's JSON is, or a refusal.
+// A recognised kernel: the form to lower, the lift it matched, and the kernel's name, declared
+// launch and parameters (the core half of its interface).
+struct Recognized {
+  unp_form form{};
+  std::string lift;
+  kir::J launch;
+  kir::J params;
+  std::string name;
+};
+int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& why);
 
 // hipRTC for gfx950, with an in-process compile-once cache keyed by source text.
 int32_t compile_source(const std::string& source, const std::string& entry, uint32_t max_ms,

@@ -12,14 +12,38 @@ import unpopped_amd as u
 _backend = u.HipBackend()
 _execs: dict = {}
 
+# The KernelFn a caller hands the backend: the reference's launched lift at a caller-chosen
+# geometry (the backend substitutes its own device-class launch and says so in the interface).
+CALLER_LAUNCH = (256, 64)
+
+
+def kernel_for(kind: str, dtype: str = "F32", rank: int = 1, op: str = "Sum", op1: str = "Max",
+               reduced_from: int | None = None, exclusive: bool = False, reverse: bool = False,
+               index_dtype: str = "I32", oob: str = "ZeroFill", q_kind: str = "U4", z_kind: str = "U4",
+               group: int = 128, **_ignored) -> dict:
+    """The KernelFn (as its serde JSON dict) of the lift or authored kernel for a form."""
+    if kind == "reduction":
+        k = rank - 1 if reduced_from is None else reduced_from
+        return u.lift_reduction("reduce", dtype, rank, op, axes=tuple(range(k, rank)), launch=CALLER_LAUNCH)
+    if kind == "row_reduce2":
+        return u.kernel_row_reduce2("row_fold", dtype, op, op1, launch=CALLER_LAUNCH)
+    if kind == "scan":
+        return u.lift_scan("scan", dtype, rank, op, exclusive=exclusive, reverse=reverse, launch=CALLER_LAUNCH)
+    if kind == "gather":
+        return u.lift_gather("gather", dtype, rank, index_dtype, 0, oob, launch=CALLER_LAUNCH)
+    if kind == "dequant4":
+        return u.kernel_dequant4("dequant", q_kind, z_kind, group, launch=CALLER_LAUNCH)
+    raise ValueError(kind)
+
 NP_KIND = {np.float32: "F32", np.float64: "F64", np.int32: "I32", np.int64: "I64", np.uint32: "U32",
            np.uint16: "Bf16", np.uint8: "U8"}
 
 
 def executor(**form) -> u.Executor:
+    """Lift the form's KernelFn, lower it with Backend::lower_kernel, compile and load it."""
     key = tuple(sorted(form.items()))
     if key not in _execs:
-        _execs[key] = u.Executor(_backend.lower_form(**form))
+        _execs[key] = u.Executor(_backend.lower_kernel(kernel_for(**form)))
     return _execs[key]
 
 
