@@ -110,39 +110,54 @@ def build_cases(u, synth):
     return cases
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
 def cpu_baseline(synth, budget_s: float = 20.0) -> dict:
-    """The oracle (single-threaded C) on a bounded sample of each configuration."""
+    """The oracle (single-threaded C, -O2 -ffp-contract=off) on a bounded sample of each
+    configuration, pinned to one host core: the median of up to 5 runs after a warm-up."""
     import oracle
 
     legs = []
 
     def timed(fn, nbytes, what):
         fn()  # warm-up
-        reps, t0 = 0, time.perf_counter()
-        while True:
+        runs, t0 = [], time.perf_counter()
+        while len(runs) < 5 and time.perf_counter() - t0 < budget_s / 5:
+            t1 = time.perf_counter()
             fn()
-            reps += 1
-            dt = time.perf_counter() - t0
-            if dt > budget_s / 6 or reps >= 5:
-                break
-        legs.append({"sample": what, "bytes": nbytes, "s": dt / reps})
+            runs.append(time.perf_counter() - t1)
+        legs.append({"sample": what, "bytes": nbytes, "s": float(np.median(runs))})
 
-    x2 = synth.normal_f32(1, 1024 * 4096).reshape(1024, 4096)
-    timed(lambda: (oracle.reduce_rows(x2, "Sum"), oracle.reduce_rows(x2, "Max")), x2.nbytes + 2 * 1024 * 4,
-          "cfg2 1024 of 8192 rows")
-    x3 = synth.int16_i32(2, 1 << 24).reshape(1, -1)
-    timed(lambda: oracle.scan_rows(x3, "Sum"), 2 * x3.nbytes, "cfg3a 2^24 of 2^28")
-    x3b = synth.uniform_01_f32(2, 1 << 24).reshape(1, -1)
-    timed(lambda: oracle.scan_rows(x3b, "Sum"), 2 * x3b.nbytes, "cfg3b 2^24 of 2^26")
-    V, D, N = 16384, 4096, 4096
-    t = synth.normal_bf16_bits(3, V * D, 0.02).reshape(V, D)
-    ids = synth.uniform_ids_i32(3, N, V)
-    timed(lambda: oracle.gather_rows(t, ids, "ZeroFill"), 2 * N * D * 2 + N * 4, "cfg4 4096 rows from a 16384-row table")
-    R, Cc, G = 256, 28672, 128
-    q, z = synth.nibbles(4, R * Cc), synth.nibbles(41, R * (Cc // G))
-    s = synth.uniform_f16_bits(42, R * (Cc // G), 0.001, 0.02)
-    timed(lambda: oracle.dequant4_bf16(q, s, z, R, Cc, G), R * Cc // 2 + R * 224 * 3 + R * Cc * 2,
-          "cfg5 256 of 8192 rows")
+    saved = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, {min(saved)})
+    try:
+        x2 = synth.normal_f32(1, 1024 * 4096).reshape(1024, 4096)
+        timed(lambda: (oracle.reduce_rows(x2, "Sum"), oracle.reduce_rows(x2, "Max")), x2.nbytes + 2 * 1024 * 4,
+              "cfg2 1024 of 8192 rows")
+        x3 = synth.int16_i32(2, 1 << 24).reshape(1, -1)
+        timed(lambda: oracle.scan_rows(x3, "Sum"), 2 * x3.nbytes, "cfg3a 2^24 of 2^28")
+        x3b = synth.uniform_01_f32(2, 1 << 24).reshape(1, -1)
+        timed(lambda: oracle.scan_rows(x3b, "Sum"), 2 * x3b.nbytes, "cfg3b 2^24 of 2^26")
+        V, D, N = 16384, 4096, 4096
+        t = synth.normal_bf16_bits(3, V * D, 0.02).reshape(V, D)
+        ids = synth.uniform_ids_i32(3, N, V)
+        timed(lambda: oracle.gather_rows(t, ids, "ZeroFill"), 2 * N * D * 2 + N * 4,
+              "cfg4 4096 rows from a 16384-row table")
+        R, Cc, G = 256, 28672, 128
+        q, z = synth.nibbles(4, R * Cc), synth.nibbles(41, R * (Cc // G))
+        s = synth.uniform_f16_bits(42, R * (Cc // G), 0.001, 0.02)
+        timed(lambda: oracle.dequant4_bf16(q, s, z, R, Cc, G), R * Cc // 2 + R * 224 * 3 + R * Cc * 2,
+              "cfg5 256 of 8192 rows")
+    finally:
+        os.sched_setaffinity(0, saved)
     total_b = sum(l["bytes"] for l in legs)
     total_s = sum(l["s"] for l in legs)
     return {
@@ -150,7 +165,8 @@ def cpu_baseline(synth, budget_s: float = 20.0) -> dict:
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": "; ".join(f"{l['sample']}: {l['bytes'] / l['s'] / 1e9:.3f} GB/s" for l in legs),
+        "sample": f"one core of {os.cpu_count()} ({cpu_model()}), median of up to 5 runs; "
+                  + "; ".join(f"{l['sample']}: {l['bytes'] / l['s'] / 1e9:.3f} GB/s" for l in legs),
     }
 
 
@@ -253,12 +269,17 @@ def main() -> int:
     value = total_bytes / (ms_step * 1e-3) / 1e9
     dom = max(per, key=lambda p: p["us"])
 
+    # HBM bytes per launch from the committed FETCH_SIZE/WRITE_SIZE passes (each scaled by what
+    # the counter reads for a plain copy of known size); null when no profile covers the kernel.
     traffic = None
     tf = ROOT / "profiles" / "traffic.json"
     if tf.exists():
-        t = json.loads(tf.read_text()).get(dom["name"])
-        if t:
-            traffic = t.get("hbm_bytes_per_launch")
+        known = json.loads(tf.read_text()).get("cases", {})
+        for p in per:
+            t = known.get(p["name"])
+            if t and t.get("kernel") == p["entry"]:
+                p["traffic"] = t["traffic_bytes"]
+        traffic = dom.get("traffic")
 
     cpu = None
     if not args.no_cpu:
