@@ -293,31 +293,53 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
   name << "unp_scan_" << (f.exclusive ? "excl_" : "incl_") << (f.reverse ? "rev_" : "") << op_name(f.op0)
        << "_" << lower_name(f.dtype);
   L.name = name.str();
-  // Block tile = waves x 64 lanes x VEC x K positions; one ticket per block per round.
-  // Measured on MI355X at 2^28 i32 / 2^26 f32: a 4-byte carry runs best with 8 waves,
-  // K = 32 and 3 blocks per CU; an 8-byte carry (f32 Sum in f64, F64, I64; twice the
-  // registers per carry) with 16 waves, K = 8 and 1 block per CU.
+  // Two schedules, one ticket per block tile per round:
+  //  _v  rows of a multiple of 16 bytes, 16-byte aligned: the LDS-staged scan, one producer
+  //      wave streaming the next tile into LDS by DMA plus NC consumer waves, one block per
+  //      CU (two LDS buffers of one 72 KiB tile each);
+  //  _s  anything else: the register scan, one element per lane-vector.
+  // Measured on MI355X at 2^28 i32 / 2^26 f32: a 4-byte carry runs best with 6 consumer waves
+  // of K = 12 vectors, an 8-byte carry (f32 Sum in f64, F64, I64) with 4 waves of K = 18.
   const bool wide_carry = (f.dtype == UNP_F32 && f.op0 == UNP_OP_SUM) || kind_bytes(f.dtype) == 8;
-  const int kScanWaves = wide_carry ? 16 : 8;
-  L.threads = 64 * kScanWaves;
-  L.blocks_per_cu = wide_carry ? 1 : 3;
+  const int vec16 = vec_of(f.dtype);
   std::ostringstream src;
   src << header(L.name, f);
-  for (int fast = 1; fast >= 0; --fast) {
+  {
     Entry e;
-    e.fast = fast;
-    e.vec = fast ? vec_of(f.dtype) : 1;
-    e.k = fast ? (wide_carry ? 8 : 32) : (wide_carry ? 16 : 32);
-    e.wpb = kScanWaves;
-    e.symbol = L.name + (fast ? "_v" : "_s");
-    src << "extern \"C\" __global__ void __launch_bounds__(" << L.threads << ") " << e.symbol << "(const " << T
+    e.fast = true;
+    e.vec = vec16;
+    e.k = wide_carry ? 18 : 12;
+    e.wpb = wide_carry ? 4 : 6;  // consumer waves
+    e.threads = 64 * (e.wpb + 1);
+    e.blocks_per_cu = 1;
+    e.symbol = L.name + "_v";
+    src << "extern \"C\" __global__ void __launch_bounds__(" << e.threads << ") " << e.symbol << "(const " << T
         << "* in, " << T << "* out, long long rows, long long cols, unsigned long long* status, "
-        << "unsigned* counter, unsigned ticket_base, unsigned epoch) {\n  unp::scan_lookback<" << T << ", "
-        << f.op0 << ", " << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false")
-        << ", " << e.vec << ", " << e.k << ", " << e.wpb
+        << "unsigned* counter, unsigned ticket_base, unsigned epoch) {\n  unp::scan_staged<" << T << ", " << f.op0
+        << ", " << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false") << ", " << e.vec << ", "
+        << e.k << ", " << e.wpb << ", " << kScanStatusWords
         << ">(in, out, rows, cols, status, counter, ticket_base, epoch);\n}\n";
     L.entries.push_back(e);
   }
+  {
+    Entry e;
+    e.fast = false;
+    e.vec = 1;
+    e.k = wide_carry ? 16 : 32;
+    e.wpb = wide_carry ? 16 : 8;
+    e.threads = 64 * e.wpb;
+    e.blocks_per_cu = wide_carry ? 1 : 3;
+    e.symbol = L.name + "_s";
+    src << "extern \"C\" __global__ void __launch_bounds__(" << e.threads << ") " << e.symbol << "(const " << T
+        << "* in, " << T << "* out, long long rows, long long cols, unsigned long long* status, "
+        << "unsigned* counter, unsigned ticket_base, unsigned epoch) {\n  unp::scan_lookback<" << T << ", " << f.op0
+        << ", " << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false") << ", 1, " << e.k
+        << ", " << e.wpb << ", " << kScanStatusWords
+        << ">(in, out, rows, cols, status, counter, ticket_base, epoch);\n}\n";
+    L.entries.push_back(e);
+  }
+  L.threads = L.entries[0].threads;
+  L.blocks_per_cu = 1;
   L.source = src.str();
   std::ostringstream j;
   j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"scan\",\"dtype\":\"" << kind_name(f.dtype)
@@ -330,9 +352,10 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
       << ",\"k\":" << L.entries[i].k << ",\"waves\":" << L.entries[i].wpb
+      << ",\"block\":" << L.entries[i].threads << ",\"blocks_per_cu\":" << L.entries[i].blocks_per_cu
       << ",\"block_tile\":" << 64 * L.entries[i].vec * L.entries[i].k * L.entries[i].wpb << ",\"when\":\""
       << (L.entries[i].fast ? "scanned extent % vec == 0 and in0/out 16-byte aligned" : "otherwise") << "\"}";
-  j << "],\"workspace\":{\"status\":\"tiles * " << (wide_carry ? 32 : 16)
+  j << "],\"workspace\":{\"status\":\"tiles * " << kScanStatusWords * 8
     << " bytes, zeroed once\",\"counter\":4,\"host_state\":[\"epoch\",\"ticket_base\"]}"
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["

@@ -293,6 +293,14 @@ template <class X> UNP_DEV X load_agent(const X* p) {
   }
 }
 
+// Draw the next ticket of a device-scope counter (one lane).  An atomic increment, not an
+// add: the compiler's atomic optimizer rewrites a one-lane add into a wave-aggregated form
+// that waits for the returned value at once, where an increment's value is waited for only
+// where it is used, so the draw's latency overlaps the loads issued after it.
+UNP_DEV u32 draw_ticket(u32* counter) {
+  return __builtin_amdgcn_atomic_inc32(counter, 0xffffffffu, __ATOMIC_RELAXED, "agent");
+}
+
 // ---------------------------------------------------------------------------------------
 // Row reduction, one wave per row: waves stride over rows (the outermost kept axis, as
 // kernel_lift/block_reduce.rs:313-338 strides blocks over it); lane l folds the vectors
@@ -479,84 +487,99 @@ UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
 // reads 64 * VEC contiguous elements, streamed past the caches.  The scan across a stripe is
 // DPP; the waves' aggregates meet in LDS; one look-back per block tile (64 tiles per probe).
 //
-// Tile status: per tile an aggregate slot and an inclusive slot of W 64-bit words
-// (W = 1 for a 4-byte carry, 2 for an 8-byte one).  Each word carries the launch's epoch in
-// its high half and 32 bits of the value in its low half, so a reader accepts a slot only
-// when every word of it carries this launch's epoch: no fence and no reset between launches.
-// The host advances `epoch` (never 0) and `ticket_base` (by tiles + blocks) per launch.
+// Tile status: per tile W 64-bit words (W = 1 for a 4-byte carry, 2 for an 8-byte one), each
+// [launch epoch: 31 bits | inclusive flag: 1 bit | 32 bits of the value].  A tile publishes
+// its aggregate (flag 0) and later overwrites it with its inclusive prefix (flag 1).  A reader
+// takes the words only when every one carries this launch's epoch and the same flag (a W = 2
+// reader that catches the overwrite half done sees mixed flags and reads again), so one load
+// per word answers a probe, and no fence and no reset is needed between launches.  The host
+// advances `epoch` (1 .. 2^31 - 1) and `ticket_base` per launch.
 // ---------------------------------------------------------------------------------------
-template <class A> struct tile_status {
+template <class A, int SP = 0> struct tile_status {
   static constexpr int W = sizeof(A) == 4 ? 1 : 2;
-  static constexpr int STRIDE = 2 * W;
+  // Words from one tile's status to the next: W packs them densely; a wider stride spreads
+  // the status of consecutive tiles, which every block probes at once, over cache lines and
+  // memory channels.
+  static constexpr int STRIDE = SP > W ? SP : W;
 
+  // slot 0: the aggregate, slot 1: the inclusive prefix.
   static UNP_DEV void publish(u64* st, u64 tile, int slot, A v, u32 epoch) {
-    u64* p = st + tile * STRIDE + slot * W;
+    u64* p = st + tile * STRIDE;
     const u64 b = to_bits64(v);
-    const u64 tag = (u64)epoch << 32;
+    const u64 tag = ((u64)epoch << 33) | ((u64)(slot == 1) << 32);
     __hip_atomic_store(p, tag | (b & 0xffffffffull), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if constexpr (W == 2) {
       __hip_atomic_store(p + 1, tag | (b >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 
-  // 2: inclusive prefix in `v`; 1: aggregate in `v`; 0: nothing yet.
-  static UNP_DEV int probe(const u64* st, u64 tile, u32 epoch, A& v) {
+  // Load a tile's words (all in flight together: one round trip).
+  static UNP_DEV void fetch(const u64* st, u64 tile, u64 (&w)[W]) {
     const u64* p = st + tile * STRIDE;
-    const u64 i0 = __hip_atomic_load(p + W, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if constexpr (W == 1) {
-      if ((u32)(i0 >> 32) == epoch) {
-        v = from_bits64<A>(i0 & 0xffffffffull);
-        return 2;
-      }
-      const u64 a0 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((u32)(a0 >> 32) == epoch) {
-        v = from_bits64<A>(a0 & 0xffffffffull);
-        return 1;
-      }
-      return 0;
-    } else {
-      const u64 i1 = __hip_atomic_load(p + W + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((u32)(i0 >> 32) == epoch && (u32)(i1 >> 32) == epoch) {
-        v = from_bits64<A>((i0 & 0xffffffffull) | (i1 << 32));
-        return 2;
-      }
-      const u64 a0 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const u64 a1 = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((u32)(a0 >> 32) == epoch && (u32)(a1 >> 32) == epoch) {
-        v = from_bits64<A>((a0 & 0xffffffffull) | (a1 << 32));
-        return 1;
-      }
-      return 0;
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[i] = __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // 2: inclusive prefix in `v`; 1: aggregate in `v`; 0: nothing usable yet.
+  static UNP_DEV int decode(const u64 (&w)[W], u32 epoch, A& v) {
+    const u64 inc = (w[0] >> 32) & 1;
+    bool ok = (w[0] >> 33) == (u64)epoch;
+    u64 b = w[0] & 0xffffffffull;
+    if constexpr (W == 2) {
+      ok = ok && (w[1] >> 33) == (u64)epoch && ((w[1] >> 32) & 1) == inc;
+      b |= w[1] << 32;
     }
+    v = from_bits64<A>(b);
+    return ok ? (inc ? 2 : 1) : 0;
+  }
+  static UNP_DEV int probe(const u64* st, u64 tile, u32 epoch, A& v) {
+    u64 w[W];
+    fetch(st, tile, w);
+    return decode(w, epoch, v);
   }
 };
 
 // The fold of every earlier tile of this row (j = tile's index in its row, j >= 1).
-// Lane l inspects the tile l + 1 back; the walk stops at the first inclusive prefix.
-template <class A, int OP>
+// Lane l inspects the tiles l + 1, l + 65, ... back, P windows of 64 per round trip (the
+// probes of all P are in flight together); the walk stops at the first inclusive prefix.
+template <class A, int OP, int P = 1, int SP = 0>
 UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch) {
   typedef fold<A, OP> F;
-  typedef tile_status<A> S;
+  typedef tile_status<A, SP> S;
   const A I = F::identity();
   A excl = I;
-  i64 pj = j - 1 - lane;
+  i64 near = j - 1 - lane;
   for (;;) {
-    A v = I;
-    int state = 2;  // before the row's first tile: the identity, final
-    if (pj >= 0) {
-      const u64 pt = tile - (u64)(j - pj);
-      state = S::probe(st, pt, epoch, v);
-      while (state == 0) {
-        __builtin_amdgcn_s_sleep(1);
-        state = S::probe(st, pt, epoch, v);
-      }
+    A v[P];
+    int state[P];
+    u64 w[P][S::W];
+    // Issue every probe of the P windows before decoding any: lanes before the row's first
+    // tile read the current tile's own words (a valid address) and take the identity.
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const i64 pj = near - 64 * p;
+      S::fetch(st, pj >= 0 ? tile - (u64)(j - pj) : tile, w[p]);
     }
-    const u64 incl = __ballot(state == 2);
-    const int f = incl ? __builtin_ctzll(incl) : 63;
-    const A c = lane <= f ? v : I;
-    excl = F::apply(wave_reduce<A, OP>(c), excl);
-    if (incl) return excl;
-    pj -= 64;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const i64 pj = near - 64 * p;
+      v[p] = I;
+      state[p] = pj >= 0 ? S::decode(w[p], epoch, v[p]) : 2;
+      if (pj < 0) v[p] = I;
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const i64 pj = near - 64 * p;
+      while (state[p] == 0) {
+        __builtin_amdgcn_s_sleep(1);
+        state[p] = S::probe(st, tile - (u64)(j - pj), epoch, v[p]);
+      }
+      const u64 incl = __ballot(state[p] == 2);
+      const int f = incl ? __builtin_ctzll(incl) : 63;
+      const A c = lane <= f ? v[p] : I;
+      excl = F::apply(wave_reduce<A, OP>(c), excl);
+      if (incl) return excl;
+    }
+    near -= 64 * P;
   }
 }
 
@@ -564,13 +587,13 @@ UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch) {
 // One block tile: every wave loads and scans its stripe set (WT = 64 * VEC * K positions),
 // the waves' aggregates are combined in LDS, wave 0 publishes the block tile's aggregate,
 // looks back and publishes its inclusive prefix, and every wave stores its prefixes.
-template <class T, int OP, bool EXCL, bool REV, int VEC, int K, int WPB>
+template <class T, int OP, bool EXCL, bool REV, int VEC, int K, int WPB, int SP>
 UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
                            u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base,
                            u32 epoch) {
   typedef typename acc<T, OP>::type A;
   typedef fold<A, OP> F;
-  typedef tile_status<A> S;
+  typedef tile_status<A, SP> S;
   constexpr i64 WT = (i64)64 * VEC * K;
   constexpr i64 BT = WT * WPB;
   __shared__ u32 slot[2];
@@ -582,13 +605,13 @@ UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 ro
   const i64 tpr = (cols + BT - 1) / BT;
   const u64 total = (u64)rows * (u64)tpr;
   if (tid == 0)
-    slot[0] = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - ticket_base;
+    slot[0] = draw_ticket(counter) - ticket_base;
   __syncthreads();
   for (int r = 0;; ++r) {
     const u64 g = slot[r & 1];
     if (g >= total) break;  // uniform across the block
     u32 next = 0;
-    if (tid == 0) next = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) next = draw_ticket(counter);
     const i64 row = (i64)(g / (u64)tpr);
     const i64 j = (i64)g - row * tpr;
     const i64 p0 = j * BT + (i64)wave * WT;
@@ -645,7 +668,7 @@ UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 ro
         if (lane == 0) S::publish(st, g, 1, agg, epoch);
       } else {
         if (lane == 0) S::publish(st, g, 0, agg, epoch);
-        gex = lookback<A, OP>(st, g, j, lane, epoch);
+        gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch);
         if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
       }
       if (lane == 0) {
@@ -688,6 +711,234 @@ UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 ro
         }
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// LDS-staged single-pass scan with decoupled look-back, for rows whose scanned extent is a
+// multiple of VEC (in / out 16-byte aligned).
+//
+// A block has NC consumer waves and one producer wave.  The block tile (BT = NC * 64 * VEC * K
+// consecutive positions of one row) is staged in one of two LDS buffers.  Consumer wave c owns
+// positions c * WT .. (WT = 64 * VEC * K); its load k of lane l is positions
+// (k * 64 + l) * VEC .. + VEC, the layout one 16-byte global->LDS DMA load writes.
+//
+// Round r:
+//   producer   draws the ticket of round r + 1, streams that tile from HBM into the other
+//              buffer (DMA loads: no VGPRs hold data in flight), waits for it, folds each
+//              consumer wave's share into wagg[(r + 1) & 1][c] and publishes the tile's
+//              aggregate (its inclusive prefix for a row's first tile) at once;
+//   consumers  scan the tile of round r out of LDS with the aggregates the producer left,
+//              wave 0 looks back and publishes the inclusive prefix and hands the exclusive
+//              prefix to the other waves through an LDS flag, every wave stores;
+//   barrier    the only block-wide barrier: the next tile is in LDS, this one is done with.
+// A tile's aggregate is out about one DMA latency after its ticket is drawn, whatever the
+// consumers are doing, so a look-back seldom waits on a predecessor.  A block holds at most
+// two tickets, processed in increasing order, and a tile waits only on tiles of lower ticket,
+// all held by running blocks, so every wait ends.  Each block draws exactly one ticket past
+// the last tile: the host advances `ticket_base` by tiles + blocks per launch.
+//
+// Float Sum: the producer folds a wave's share lane by lane then across the wave, the
+// consumers scan it in stripe order, so the f64 carry across waves and tiles is associated
+// differently from the within-stripe prefixes; every output is still one f64 fold of exactly
+// its prefix, held to the declared bound.
+// ---------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Wait until at most N vector memory operations of this wave are outstanding (gfx9
+// s_waitcnt encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt left at their maximum).
+template <int N> UNP_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
+}
+UNP_DEV void wait_vm_all() { wait_vm<0>(); }
+
+// A block barrier that orders LDS only: no wait on outstanding global stores.  A wave with
+// global->LDS DMA in flight must wait for it first (the DMA counts as LDS writes).
+UNP_DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <class T, int OP, bool EXCL, bool REV, int VEC, int K, int NC, int SP>
+UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
+                         u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base,
+                         u32 epoch) {
+  typedef typename acc<T, OP>::type A;
+  typedef fold<A, OP> F;
+  typedef tile_status<A, SP> S;
+  static_assert(sizeof(T) * VEC == 16, "one 16-byte DMA load per lane");
+  constexpr i64 WT = (i64)64 * VEC * K;
+  constexpr i64 BT = WT * NC;
+  __shared__ __attribute__((aligned(16))) T buf[2][BT];
+  __shared__ A wagg[2][NC];
+  __shared__ u32 tk[2];
+  __shared__ A gbase;
+  __shared__ u32 ready;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const i64 tpr = (cols + BT - 1) / BT;
+  const u64 total = (u64)rows * (u64)tpr;
+  const A I = F::identity();
+  const T pad = (T)I;  // the identity, exactly representable at the element type
+
+  if (wave == NC) {
+    // ---- producer ----
+    // Stage tile g into buffer b, fold each consumer wave's share and publish the aggregate.
+    // A full tile (every position inside the row, uniform) takes no per-lane predicate, so
+    // its DMA and LDS reads issue back to back.
+    auto load = [&](const T* __restrict__ rin, i64 t0, int b, bool full) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const i64 pos = t0 + (i64)c * WT + ((i64)k * 64 + lane) * VEC;
+          if (full || pos + VEC <= cols)
+            __builtin_amdgcn_global_load_lds(rin + (REV ? cols - VEC - pos : pos),
+                                             (lds_void*)&buf[b][c * WT + k * 64 * VEC], 16, 0, 2 /* nt */);
+        }
+      }
+    };
+    auto share = [&](i64 t0, int b, int c, bool full) {
+      A s = I;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const i64 pos = t0 + (i64)c * WT + ((i64)k * 64 + lane) * VEC;
+        vec<T, VEC> v = *reinterpret_cast<const vec<T, VEC>*>(&buf[b][c * WT + (k * 64 + lane) * VEC]);
+        if (!full && pos + VEC > cols) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) v.e[e] = pad;
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s = F::apply(s, (A)v.e[e]);
+      }
+      return s;
+    };
+    auto stage = [&](u64 g, int b) {
+      const i64 row = (i64)(g / (u64)tpr);
+      const i64 j = (i64)g - row * tpr;
+      const T* __restrict__ rin = in + row * cols;
+      const i64 t0 = j * BT;
+      const bool full = t0 + BT <= cols;
+      if (full) load(rin, t0, b, true);
+      else load(rin, t0, b, false);
+      wait_vm_all();
+      A agg = I;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const A w = wave_reduce<A, OP>(full ? share(t0, b, c, true) : share(t0, b, c, false));
+        if (lane == 0) wagg[b][c] = w;
+        agg = F::apply(agg, w);
+      }
+      if (lane == 0) S::publish(st, g, j == 0 ? 1 : 0, agg, epoch);
+    };
+    u32 t0 = 0;
+    if (lane == 0) {
+      t0 = draw_ticket(counter) - ticket_base;
+      tk[0] = t0;
+      ready = 0;
+    }
+    const u64 g0 = (u32)__builtin_amdgcn_readfirstlane((int)t0);
+    if (g0 < total) stage(g0, 0);
+    lds_barrier();  // B0
+    for (int r = 0;; ++r) {
+      if ((u64)tk[r & 1] >= total) break;
+      u32 t = 0;
+      if (lane == 0) {
+        t = draw_ticket(counter) - ticket_base;
+        tk[(r + 1) & 1] = t;
+      }
+      const u64 gn = (u32)__builtin_amdgcn_readfirstlane((int)t);
+      if (gn < total) stage(gn, (r + 1) & 1);
+      lds_barrier();  // B
+    }
+    return;
+  }
+
+  // ---- consumers ----
+  lds_barrier();  // B0
+  for (int r = 0;; ++r) {
+    const u64 g = tk[r & 1];
+    if (g >= total) break;
+    const i64 row = (i64)(g / (u64)tpr);
+    const i64 j = (i64)g - row * tpr;
+    const i64 p0 = j * BT + (i64)wave * WT;
+    const T* __restrict__ tile = &buf[r & 1][wave * WT];
+    T* __restrict__ rout = out + row * cols;
+
+    const bool full = p0 + WT <= cols;  // uniform per wave
+    vec<T, VEC> x[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const vec<T, VEC> v = *reinterpret_cast<const vec<T, VEC>*>(tile + (k * 64 + lane) * VEC);
+      const bool in_row = full || p0 + ((i64)k * 64 + lane) * VEC + VEC <= cols;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[k].e[e] = in_row ? v.e[REV ? VEC - 1 - e : e] : pad;
+    }
+    A wex = I;
+    for (int w = 0; w < wave; ++w) wex = F::apply(wex, wagg[r & 1][w]);
+
+    A pre[K];
+    A carry = I;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      A s = (A)x[k].e[0];
+#pragma unroll
+      for (int e = 1; e < VEC; ++e) s = F::apply(s, (A)x[k].e[e]);
+      const A inc = wave_inclusive_scan<A, OP>(s, lane);
+      pre[k] = F::apply(carry, wave_shr1(inc, I));
+      carry = F::apply(carry, readlane(inc, 63));
+    }
+
+    A gex = I;
+    if (wave == 0) {
+      if (j > 0) {
+        A agg = wagg[r & 1][0];
+#pragma unroll
+        for (int w = 1; w < NC; ++w) agg = F::apply(agg, wagg[r & 1][w]);
+        gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch);
+        if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
+      }
+      if (lane == 0) {
+        gbase = gex;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __hip_atomic_store(&ready, (u32)r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    } else {
+      while (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (u32)r + 1)
+        __builtin_amdgcn_s_sleep(1);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+      gex = gbase;
+    }
+    const A base = F::apply(gex, wex);
+
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      A v = F::apply(base, pre[k]);
+      vec<T, VEC> o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        if constexpr (EXCL) {
+          o.e[e] = (T)v;
+          v = F::apply(v, (A)x[k].e[e]);
+        } else {
+          v = F::apply(v, (A)x[k].e[e]);
+          o.e[e] = (T)v;
+        }
+      }
+      const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
+      if (full || pos + VEC <= cols) {
+        if constexpr (REV) {
+          vec<T, VEC> v2;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) v2.e[e] = o.e[VEC - 1 - e];
+          st_nt<T, VEC>(rout + (cols - VEC - pos), v2);
+        } else {
+          st_nt<T, VEC>(rout + pos, o);
+        }
+      }
+    }
+    lds_barrier();  // B
   }
 }
 

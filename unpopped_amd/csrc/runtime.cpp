@@ -412,13 +412,13 @@ int32_t ensure_ws(unp_exec* x, size_t bytes, bool need_counter, unp_error* err) 
 }
 
 int32_t launch(unp_exec* x, size_t entry, uint32_t grid, void** params, hipStream_t s, unp_error* err) {
+  const uint32_t threads = (uint32_t)(x->l.entries[entry].threads ? x->l.entries[entry].threads : x->l.threads);
   x->grid[0] = grid;
   x->grid[1] = x->grid[2] = 1;
-  x->block[0] = (uint32_t)x->l.threads;
+  x->block[0] = threads;
   x->block[1] = x->block[2] = 1;
   x->last_entry = x->l.entries[entry].symbol;
-  const hipError_t e = hipModuleLaunchKernel(x->fns[entry], grid, 1, 1, (uint32_t)x->l.threads, 1, 1, 0, s, params,
-                                             nullptr);
+  const hipError_t e = hipModuleLaunchKernel(x->fns[entry], grid, 1, 1, threads, 1, 1, 0, s, params, nullptr);
   if (e != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel", e);
   return UNP_OK;
 }
@@ -480,19 +480,18 @@ int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_err
   uint64_t in = A.buf[0], out = A.buf[1];
   const size_t entry = pick(x, cols % vec == 0 && aligned16(in) && aligned16(out));
   const unp::Entry& en = x->l.entries[entry];
-  // A block tile: wpb waves x 64 lanes x vec x k positions of one row.
+  // A block tile: wpb (consumer) waves x 64 lanes x vec x k positions of one row.
   const long long tile = 64LL * en.vec * en.k * en.wpb;
   const unsigned long long tiles = (unsigned long long)rows * (unsigned long long)((cols + tile - 1) / tile);
-  const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+  const uint32_t grid = (uint32_t)(x->cu_count * (en.blocks_per_cu ? en.blocks_per_cu : x->l.blocks_per_cu));
   if (tiles + grid >= (1ull << 31)) {
     set_error(err, UNP_INVALID_ARGUMENT, "too many scan tiles for one launch");
     return UNP_INVALID_ARGUMENT;
   }
-  const bool wide = (f.dtype == UNP_F32 && f.op0 == UNP_OP_SUM) || unp::kind_bytes(f.dtype) == 8;
-  const size_t words = wide ? 4 : 2;
-  if ((rc = ensure_ws(x, (size_t)tiles * words * 8, true, err)) != UNP_OK) return rc;
-  if (x->epoch == 0xffffffffu) {
-    // After 2^32 - 1 launches the tags would repeat: clear the words and restart at epoch 1.
+  if ((rc = ensure_ws(x, (size_t)tiles * unp::kScanStatusWords * 8, true, err)) != UNP_OK) return rc;
+  if (x->epoch == 0x7fffffffu) {
+    // The status words hold a 31-bit epoch: after 2^31 - 1 launches the tags would repeat, so
+    // clear the words and restart at epoch 1.
     const hipError_t e = hipMemsetAsync(x->ws, 0, x->ws_bytes, s);
     if (e != hipSuccess) return hip_fail(err, "hipMemsetAsync(status)", e);
     x->epoch = 0;

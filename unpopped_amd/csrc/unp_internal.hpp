@@ -28,7 +28,13 @@ struct Entry {
   int wpb = 1;        // waves per ticket group (scan)
   bool fast = false;  // the 16-byte-aligned path
   bool wide = false;  // reduction: the block-per-row schedule (long rows)
+  int threads = 0;    // block size of this entry (0: the form's)
+  int blocks_per_cu = 0;  // persistent blocks per CU of this entry (0: the form's)
 };
+
+// Scan tile status: words per tile (a 256-byte stride: the status of consecutive tiles, which
+// every block probes at once, spreads over cache lines and memory channels).
+constexpr int kScanStatusWords = 32;
 
 // Reductions over more than kWideRow elements per row use the block-per-row schedule.
 constexpr long long kWideRow = 32768;
