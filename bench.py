@@ -202,6 +202,95 @@ def copy_probe(u, nbytes: int = 256 << 20) -> None:
     log(f"[bench] copy probe: 3 launches of a {nbytes} B copy")
 
 
+CEILING_SRC = r"""
+typedef unsigned int u32;
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+// Plain streaming kernels, 16 bytes per lane, 4 in flight, nontemporal: what this device moves
+// for a pure read, a pure write and a 1:1 copy, with no algorithm in the way.
+extern "C" __global__ void __launch_bounds__(256) unp_ceiling_read(const u32x4* __restrict__ s, u32* __restrict__ sink,
+                                                                    long long n) {
+  const long long st = (long long)gridDim.x * 256;
+  long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  u32 acc = 0;
+  for (; i + 3 * st < n; i += 4 * st) {
+    const u32x4 a = __builtin_nontemporal_load(s + i), b = __builtin_nontemporal_load(s + i + st);
+    const u32x4 c = __builtin_nontemporal_load(s + i + 2 * st), d = __builtin_nontemporal_load(s + i + 3 * st);
+    acc ^= a.x ^ b.y ^ c.z ^ d.w;
+  }
+  for (; i < n; i += st) acc ^= s[i].x;
+  if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+extern "C" __global__ void __launch_bounds__(256) unp_ceiling_write(u32x4* __restrict__ d, long long n) {
+  const long long st = (long long)gridDim.x * 256;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += st) {
+    const u32x4 v = {(u32)i, 1u, 2u, 3u};
+    __builtin_nontemporal_store(v, d + i);
+  }
+}
+extern "C" __global__ void __launch_bounds__(256) unp_ceiling_copy(const u32x4* __restrict__ s, u32x4* __restrict__ d,
+                                                                    long long n) {
+  const long long st = (long long)gridDim.x * 256;
+  long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  for (; i + 3 * st < n; i += 4 * st) {
+    const u32x4 a = __builtin_nontemporal_load(s + i), b = __builtin_nontemporal_load(s + i + st);
+    const u32x4 c = __builtin_nontemporal_load(s + i + 2 * st), e = __builtin_nontemporal_load(s + i + 3 * st);
+    __builtin_nontemporal_store(a, d + i);
+    __builtin_nontemporal_store(b, d + i + st);
+    __builtin_nontemporal_store(c, d + i + 2 * st);
+    __builtin_nontemporal_store(e, d + i + 3 * st);
+  }
+  for (; i < n; i += st) __builtin_nontemporal_store(__builtin_nontemporal_load(s + i), d + i);
+}
+"""
+
+
+def ceilings(u, cus: int, nbytes: int = 1 << 30, reps: int = 10) -> None:
+    """Streaming read / write / copy rates of this device on 1 GiB buffers (median of `reps`
+    launches, one block of 256 threads per CU per grid step): the practical ceilings that the
+    suite's kernels are read against, beside the 8 TB/s peak."""
+    import ctypes as C
+
+    from unpopped_amd import _lib
+
+    L = _lib.lib()
+    co = u.HipCompiler().compile(CEILING_SRC, "unp_ceiling_copy")
+    img = C.create_string_buffer(co, len(co))
+    m, err = C.c_void_p(), _lib.Error()
+    _lib.check(L.unp_hip_module_load(img, len(co), C.byref(m), C.byref(err)), err)
+    fns = {}
+    for name in ("unp_ceiling_read", "unp_ceiling_write", "unp_ceiling_copy"):
+        f = C.c_void_p()
+        _lib.check(L.unp_hip_get_function(m, name.encode(), C.byref(f), C.byref(err)), err)
+        fns[name] = f
+    a, b, sink = u.DeviceBuffer(nbytes), u.DeviceBuffer(nbytes), u.DeviceBuffer(64)
+    a.fill(1)
+    n = nbytes // 16
+    cases = [("read", "unp_ceiling_read", (a.ptr, sink.ptr, n), nbytes),
+             ("write", "unp_ceiling_write", (b.ptr, n), nbytes),
+             ("copy", "unp_ceiling_copy", (a.ptr, b.ptr, n), 2 * nbytes)]
+    for label, name, vals, moved in cases:
+        args = (C.c_uint64 * len(vals))(*vals)
+        best = None
+        for bpc in (1, 2, 4):
+            g, blk = (C.c_uint32 * 3)(cus * bpc, 1, 1), (C.c_uint32 * 3)(256, 1, 1)
+            ts = []
+            for i in range(reps + 2):
+                e0, e1 = u.Event(), u.Event()
+                e0.record()
+                _lib.check(L.unp_hip_launch(fns[name], g, blk, 0, None, args, C.sizeof(args), C.byref(err)), err)
+                e1.record()
+                e1.synchronize()
+                if i >= 2:
+                    ts.append(e0.elapsed_ms(e1))
+            ms = float(np.median(ts))
+            gbps = moved / (ms * 1e-3) / 1e9
+            log(f"[bench] ceiling {label}: {cus * bpc} blocks, {ms * 1e3:.1f} us, {gbps:.0f} GB/s")
+            if best is None or gbps > best[0]:
+                best = (gbps, cus * bpc, ms)
+        print(json.dumps({"ceiling": label, "bytes": moved, "blocks": best[1], "us": round(best[2] * 1e3, 1),
+                          "GBps": round(best[0], 1), "frac_of_peak": round(best[0] / PEAK_GBPS, 4)}), flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -211,6 +300,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only launch a plain 256 MiB copy (calibrates the HBM byte counters)")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="only measure this device's streaming read / write / copy rates on 1 GiB")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -226,6 +317,9 @@ def main() -> int:
     log(f"[bench] device {arch}, {cus} CUs")
     if args.copy_probe:
         copy_probe(u)
+        return 0
+    if args.ceilings:
+        ceilings(u, cus)
         return 0
     cases = build_cases(u, synth)
     if args.only:
