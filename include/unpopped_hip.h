@@ -107,7 +107,10 @@ enum unp_form_kind {
   UNP_FORM_SCAN = 1,      /* Access::Scan, launched (kernel_lift/scan_launched.rs:54) */
   UNP_FORM_GATHER = 2,    /* ReadIndex::Indexed gather (kernel_lift/gather.rs:35) */
   UNP_FORM_DEQUANT4 = 3,  /* U4/I4 x f16 scale x 4-bit zero -> bf16 (tests/support/dequant.rs) */
-  UNP_FORM_ROW_REDUCE2 = 4 /* two folds of each row read once (Sum and Max: softmax prologue) */
+  UNP_FORM_ROW_REDUCE2 = 4, /* two folds of each row read once (Sum and Max: softmax prologue) */
+  UNP_FORM_ROW_REDUCE = 5   /* Access::RowReduce: staged row folds, then a full-width epilogue
+                               (kernel_lift/row_reduce.rs:31, row_reduce_launched.rs:47); its
+                               expressions come only through unp_hip_lower_kernel */
 };
 /* ReduceOp subset (crates/unpopped/src/ir.rs:1700). */
 enum unp_reduce_op { UNP_OP_SUM = 0, UNP_OP_PROD = 1, UNP_OP_MAX = 2, UNP_OP_MIN = 3, UNP_OP_MEAN = 4 };
@@ -172,6 +175,16 @@ int32_t unp_kernel_row_reduce2(const char* name, int32_t dtype, int32_t op0, int
  * (crates/unpopped/tests/support/dequant.rs:58-143): out[r, c] = Bf16_rne((q - z) * s) with a U4/I4
  * weight, a U4/I4 zero point and an F16 scale per `group` columns. */
 int32_t unp_kernel_dequant4(const char* name, int32_t q_kind, int32_t z_kind, int32_t group, uint32_t block,
+                            uint32_t grid, char** json, unp_error* err);
+
+/* lift_row_reduce_opdef (crates/unpopped/src/kernel_lift/row_reduce.rs:31-49) and, with a
+ * launch, lift_row_reduce_opdef_launched (kernel_lift/row_reduce_launched.rs:47-86) of the
+ * Access::RowReduce op (crates/unpopped/src/ir.rs:2114-2125, OpDef::row_reduce ir.rs:3268):
+ * `stages_json` is the JSON array of its ReduceStage {pre, op} (ir.rs:2049), `epilogue_json` the
+ * epilogue ScalarExpr, both over Input(k) and Reduced(t) leaves; `n_inputs` inputs of `dtype`
+ * (F32 or F64) and rank `rank`.  block = grid = 0 lifts the serial kernel. */
+int32_t unp_lift_row_reduce(const char* name, int32_t dtype, int32_t rank, int32_t n_inputs,
+                            const char* stages_json, const char* epilogue_json, uint32_t block,
                             uint32_t grid, char** json, unp_error* err);
 
 /* ---------------------------------------------------------------------------------------

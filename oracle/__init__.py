@@ -58,6 +58,8 @@ def lib() -> C.CDLL:
             "orc_reduce_rows_i32": (None, [P, i64, i64, i32, P]),
             "orc_reduce_rows_i64": (None, [P, i64, i64, i32, P]),
             "orc_sum_launched_order": (d, [P, i64, i64, i32]),
+            "orc_rx_eval": (d, [P, C.c_int32, P, P, i32]),
+            "orc_row_reduce": (None, [P, C.c_int32, i64, i64, i32, C.c_int32, P, P, P, P, C.c_int32, P]),
             "orc_sum_bound": (d, [P, i64, i32, i32, d]),
             "orc_neumaier": (d, [P, i64]),
             "orc_scan_rows_f32": (None, [P, i64, i64, i32, i32, i32, P]),
@@ -175,3 +177,82 @@ def dequant4_bf16(q_packed: np.ndarray, scales_f16_bits: np.ndarray, zeros_packe
     out = np.empty(rows * cols, np.uint16)
     lib().orc_dequant4_bf16(_p(q), int(q_signed), _p(s), _p(z), int(z_signed), rows, cols, group, _p(out))
     return out.reshape(rows, cols)
+
+
+# ---- row reduction -----------------------------------------------------------------------
+
+ORC_UNARY_NAMES = ["Neg", "Abs", "Sqr", "Sqrt", "Rsqrt", "Recip", "Exp", "Log", "Tanh", "Sigmoid", "Relu", "Erf",
+                   "Gelu", "Silu", "Sin", "Cos", "Floor", "Ceil", "Round", "Sign", "Step", "Erfc", "Trunc", "Exp2",
+                   "Expm1", "Log2", "Log10", "Log1p", "Sinh", "Cosh", "Tan", "Asin", "Acos", "Atan", "Asinh", "Acosh",
+                   "Atanh", "Cbrt"]
+ORC_BINARY_NAMES = ["Max", "Min", "Pow", "Rem", "RemTrunc", "Atan2", "Copysign", "FmaxIeee", "FminIeee", "CmpEq",
+                    "CmpNe", "CmpLt", "CmpLe", "CmpGt", "CmpGe"]
+
+
+class RX(C.Structure):
+    _fields_ = [("op", C.c_int32), ("arg", C.c_int32), ("c", C.c_double)]
+
+
+def program(e) -> list[tuple[int, int, float]]:
+    """A ScalarExpr (serde dict, or an ``unpopped_amd.expr.Expr``) as the C oracle's postfix
+    program of (op, arg, const)."""
+    if hasattr(e, "j"):
+        e = e.j
+    (tag, p), = e.items()
+    if tag == "Input":
+        return [(1, int(p), 0.0)]
+    if tag == "Reduced":
+        return [(2, int(p), 0.0)]
+    if tag == "Const":
+        v = {"NaN": float("nan"), "inf": float("inf"), "-inf": float("-inf")}.get(p, p) if isinstance(p, str) else p
+        return [(3, 0, float(v))]
+    arith = {"Add": 4, "Sub": 5, "Mul": 6, "Div": 7}
+    if tag in arith:
+        return program(p[0]) + program(p[1]) + [(arith[tag], 0, 0.0)]
+    if tag in ("Fma", "Select"):
+        return program(p[0]) + program(p[1]) + program(p[2]) + [(8 if tag == "Fma" else 9, 0, 0.0)]
+    if tag == "Unary":
+        return program(p[1]) + [(10, ORC_UNARY_NAMES.index(p[0]), 0.0)]
+    if tag == "Binary":
+        return program(p[1]) + program(p[2]) + [(11, ORC_BINARY_NAMES.index(p[0]), 0.0)]
+    raise ValueError(f"the oracle has no {tag}")
+
+
+def _rx_array(e):
+    prog = program(e)
+    depth = peak = 0
+    for op, _, _ in prog:
+        depth += 1 if op <= 3 else (0 if op == 10 else (-2 if op in (8, 9) else -1))
+        peak = max(peak, depth)
+    if peak > 64:
+        raise ValueError("expression deeper than the oracle's stack")
+    arr = (RX * len(prog))(*[RX(op, arg, c) for op, arg, c in prog])
+    return arr, len(prog)
+
+
+def rx_eval(e, x, red=(), f32: bool = True) -> float:
+    arr, n = _rx_array(e)
+    xs = np.ascontiguousarray(np.asarray(x, np.float64).reshape(-1))
+    rs = np.ascontiguousarray(np.asarray(list(red) + [0.0], np.float64))
+    return lib().orc_rx_eval(arr, n, _p(xs), _p(rs), int(f32))
+
+
+def row_reduce(inputs, stages, epilogue) -> np.ndarray:
+    """The serial lifted row reduction over the innermost axis of the inputs (all the same shape
+    and dtype, float32 or float64); ``stages`` is [(pre, op)], ``epilogue`` the output expression."""
+    xs = [np.ascontiguousarray(a) for a in inputs]
+    dt = xs[0].dtype
+    assert dt in (np.float32, np.float64) and all(a.dtype == dt and a.shape == xs[0].shape for a in xs)
+    assert 1 <= len(xs) <= 16 and 1 <= len(stages) <= 16
+    cols = xs[0].shape[-1] if xs[0].ndim else 1
+    rows = xs[0].size // cols if cols else 0
+    out = np.empty(xs[0].shape, dt)
+    progs = [_rx_array(pre) for pre, _ in stages]
+    ops = (C.c_int32 * len(stages))(*[OPS[op] for _, op in stages])
+    pre_ptrs = (C.c_void_p * len(stages))(*[C.cast(a, C.c_void_p) for a, _ in progs])
+    pre_lens = (C.c_int32 * len(stages))(*[n for _, n in progs])
+    epi, epi_n = _rx_array(epilogue)
+    ins = (C.c_void_p * len(xs))(*[_p(a) for a in xs])
+    lib().orc_row_reduce(ins, len(xs), rows, cols, int(dt == np.float64), len(stages), ops, pre_ptrs, pre_lens, epi,
+                         epi_n, _p(out))
+    return out

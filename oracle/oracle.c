@@ -384,3 +384,133 @@ void orc_dequant4_bf16(const uint8_t* q, int q_signed, const uint16_t* scale, co
     }
   }
 }
+
+/* ---- row reduction --------------------------------------------------------------------- */
+/* UnaryOp codes: the order of ORC_UNARY_NAMES in oracle/__init__.py. */
+static double rx_unary(int32_t code, double x, int f32) {
+  switch (code) {
+    case 0: return -x;                                  /* Neg */
+    case 1: return fabs(x);                             /* Abs */
+    case 2: return x * x;                               /* Sqr */
+    case 3: return sqrt(x);                             /* Sqrt */
+    case 4: return 1.0 / sqrt(x);                       /* Rsqrt */
+    case 5: return 1.0 / x;                             /* Recip */
+    case 6: return exp(x);                              /* Exp */
+    case 7: return log(x);                              /* Log */
+    case 8: return tanh(x);                             /* Tanh */
+    case 9: return 1.0 / (1.0 + exp(-x));               /* Sigmoid */
+    case 10: return x < 0.0 ? 0.0 : x;                  /* Relu: NaN and -0 pass */
+    case 11: return erf(x);                             /* Erf */
+    case 12: return 0.5 * x * (1.0 + erf(x * 0.70710678118654752440)); /* Gelu */
+    case 13: return x * (1.0 / (1.0 + exp(-x)));        /* Silu */
+    case 14: return sin(x);
+    case 15: return cos(x);
+    case 16: return floor(x);
+    case 17: return ceil(x);
+    case 18: return nearbyint(x);                       /* Round: ties to even */
+    case 19: { const double c = f32 ? (double)(float)x : x; return c > 0.0 ? 1.0 : (c < 0.0 ? -1.0 : 0.0); } /* Sign */
+    case 20: { const double c = f32 ? (double)(float)x : x; return c > 0.0 ? 1.0 : 0.0; }                   /* Step */
+    case 21: return erfc(x);
+    case 22: return trunc(x);
+    case 23: return exp2(x);
+    case 24: return expm1(x);
+    case 25: return log2(x);
+    case 26: return log10(x);
+    case 27: return log1p(x);
+    case 28: return sinh(x);
+    case 29: return cosh(x);
+    case 30: return tan(x);
+    case 31: return asin(x);
+    case 32: return acos(x);
+    case 33: return atan(x);
+    case 34: return asinh(x);
+    case 35: return acosh(x);
+    case 36: return copysign(atanh(fabs(x)), x);        /* Atanh, on |x| (scalar_ops.rs) */
+    case 37: return cbrt(x);
+    default: return NAN;
+  }
+}
+
+/* BinaryOp codes: the order of ORC_BINARY_NAMES in oracle/__init__.py. */
+static double rx_binary(int32_t code, double a, double b) {
+  switch (code) {
+    case 0: return a != a ? a : (b != b ? b : (a >= b ? a : b)); /* Max: NaN-propagating, a on ties */
+    case 1: return a != a ? a : (b != b ? b : (a <= b ? a : b)); /* Min */
+    case 2: return pow(a, b);
+    case 3: return a - floor(a / b) * b;                         /* Rem: floored */
+    case 4: return fmod(a, b);                                   /* RemTrunc */
+    case 5: return atan2(a, b);
+    case 6: return copysign(a, b);
+    case 7: return fmax(a, b);                                   /* FmaxIeee */
+    case 8: return fmin(a, b);                                   /* FminIeee */
+    case 9: return a == b ? 1.0 : 0.0;
+    case 10: return a != b ? 1.0 : 0.0;
+    case 11: return a < b ? 1.0 : 0.0;
+    case 12: return a <= b ? 1.0 : 0.0;
+    case 13: return a > b ? 1.0 : 0.0;
+    case 14: return a >= b ? 1.0 : 0.0;
+    default: return NAN;
+  }
+}
+
+double orc_rx_eval(const orc_rx* prog, int32_t len, const double* x, const double* red, int f32) {
+  double st[64];
+  int sp = 0;
+  for (int32_t i = 0; i < len; ++i) {
+    const orc_rx* p = &prog[i];
+    switch (p->op) {
+      case ORC_RX_INPUT: st[sp++] = x[p->arg]; break;
+      case ORC_RX_REDUCED: st[sp++] = red[p->arg]; break;
+      case ORC_RX_CONST: st[sp++] = p->c; break;
+      case ORC_RX_ADD: sp--; st[sp - 1] = st[sp - 1] + st[sp]; break;
+      case ORC_RX_SUB: sp--; st[sp - 1] = st[sp - 1] - st[sp]; break;
+      case ORC_RX_MUL: sp--; st[sp - 1] = st[sp - 1] * st[sp]; break;
+      case ORC_RX_DIV: sp--; st[sp - 1] = st[sp - 1] / st[sp]; break;
+      case ORC_RX_FMA: sp -= 2; st[sp - 1] = fma(st[sp - 1], st[sp], st[sp + 1]); break;
+      case ORC_RX_SELECT: sp -= 2; st[sp - 1] = st[sp - 1] != 0.0 ? st[sp] : st[sp + 1]; break;
+      case ORC_RX_UNARY: st[sp - 1] = rx_unary(p->arg, st[sp - 1], f32); break;
+      case ORC_RX_BINARY: sp--; st[sp - 1] = rx_binary(p->arg, st[sp - 1], st[sp]); break;
+      default: return NAN;
+    }
+  }
+  return sp == 1 ? st[0] : NAN;
+}
+
+void orc_row_reduce(const void* const* ins, int32_t n_inputs, int64_t rows, int64_t cols, int f64, int32_t n_stages,
+                    const int32_t* ops, const orc_rx* const* pres, const int32_t* pre_lens, const orc_rx* epi,
+                    int32_t epi_len, void* out) {
+  double x[16], red[16];
+  const int f32 = !f64;
+#define ORC_LOAD(k, i) (f64 ? ((const double*)ins[k])[i] : (double)((const float*)ins[k])[i])
+#define ORC_ROUND(v) (f64 ? (v) : (double)(float)(v))
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int32_t s = 0; s < n_stages; ++s) {
+      double acc = ops[s] == ORC_PROD ? 1.0 : 0.0;
+      int have = 0;
+      for (int64_t c = 0; c < cols; ++c) {
+        for (int32_t k = 0; k < n_inputs; ++k) x[k] = ORC_LOAD(k, r * cols + c);
+        const double v = ORC_ROUND(orc_rx_eval(pres[s], pre_lens[s], x, red, f32));
+        switch (ops[s]) {
+          case ORC_SUM:
+          case ORC_MEAN: acc = acc + v; break;
+          case ORC_PROD: acc = acc * v; break;
+          default:
+            if (!have) acc = v;
+            else if (v != v) acc = v;
+            else if (ops[s] == ORC_MAX ? v > acc : v < acc) acc = v;
+            have = 1;
+        }
+      }
+      const double fin = ops[s] == ORC_MEAN ? acc / (double)cols : acc;
+      red[s] = ORC_ROUND(fin);
+    }
+    for (int64_t c = 0; c < cols; ++c) {
+      for (int32_t k = 0; k < n_inputs; ++k) x[k] = ORC_LOAD(k, r * cols + c);
+      const double v = orc_rx_eval(epi, epi_len, x, red, f32);
+      if (f64) ((double*)out)[r * cols + c] = v;
+      else ((float*)out)[r * cols + c] = (float)v;
+    }
+  }
+#undef ORC_LOAD
+#undef ORC_ROUND
+}

@@ -63,4 +63,28 @@ void orc_gather_rows(const uint8_t* table, int64_t src_extent, int64_t row_bytes
 void orc_dequant4_bf16(const uint8_t* q, int q_signed, const uint16_t* scale, const uint8_t* zero, int z_signed,
                        int64_t rows, int64_t cols, int64_t group, uint16_t* out);
 
+/* ---- row reduction (Access::RowReduce) ------------------------------------------------- */
+/* An expression as a postfix program over a stack of doubles: leaves push, operators pop their
+ * operands and push the result.  `arg` is the leaf's index or the operator's code. */
+enum {
+  ORC_RX_INPUT = 1, ORC_RX_REDUCED, ORC_RX_CONST, ORC_RX_ADD, ORC_RX_SUB, ORC_RX_MUL, ORC_RX_DIV,
+  ORC_RX_FMA, ORC_RX_SELECT, ORC_RX_UNARY, ORC_RX_BINARY
+};
+typedef struct orc_rx {
+  int32_t op;
+  int32_t arg;
+  double c;
+} orc_rx;
+/* Evaluate a program in f64 (crates/unpopped/src/oracle/expr_eval.rs over scalar_ops.rs);
+ * `f32` is the compute dtype's width for Sign and Step. */
+double orc_rx_eval(const orc_rx* prog, int32_t len, const double* x, const double* red, int f32);
+/* The lifted serial row reduction (kernel_lift/row_reduce.rs:31-231 as the kernel evaluator
+ * runs it): per row, each stage folds round_T(pre) in f64 in ascending column order (Max/Min
+ * with the NaN rule), finalises and rounds once to T; the epilogue is evaluated in f64 and
+ * rounded once at the store.  `f64` picks T (F64, else F32); `ins` are n_inputs row-major
+ * rows x cols arrays of T. */
+void orc_row_reduce(const void* const* ins, int32_t n_inputs, int64_t rows, int64_t cols, int f64, int32_t n_stages,
+                    const int32_t* ops, const orc_rx* const* pres, const int32_t* pre_lens, const orc_rx* epi,
+                    int32_t epi_len, void* out);
+
 #endif

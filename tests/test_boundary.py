@@ -269,3 +269,91 @@ def test_every_lowered_source_compiles_for_gfx950():
         co = cc.compile(g.source, g.name)
         for e in g.interface["entries"]:
             assert e["symbol"].encode() in co
+
+
+# ---------------------------------------------------------------------------------------
+# Access::RowReduce (kernel_lift/row_reduce.rs, row_reduce_launched.rs)
+# ---------------------------------------------------------------------------------------
+
+from unpopped_amd import expr as X  # noqa: E402
+
+ROW_REDUCTIONS = {"softmax": X.softmax(), "centred_quotient": X.centred_quotient(), "rms_norm": X.rms_norm(),
+                  "identity_sum": ([(X.input(0), "Sum")], X.reduced(0))}
+
+
+@pytest.mark.parametrize("which", sorted(ROW_REDUCTIONS))
+@pytest.mark.parametrize("dtype", ["F32", "F64"])
+@pytest.mark.parametrize("launch", [None, (256, 64), (1, 3)])
+def test_row_reduce_lifts_round_trip(which, dtype, launch):
+    stages, epi = ROW_REDUCTIONS[which]
+    k = u.lift_row_reduce(which, dtype, 2, stages, epi, launch=launch)
+    g = u.HipBackend().lower_kernel(k)
+    assert g.interface["lift"] == ("lift_row_reduce_opdef_launched" if launch else "lift_row_reduce_opdef")
+    assert [s["op"] for s in g.interface["stages"]] == [op for _, op in stages]
+    assert g.name.startswith(f"unp_row_reduce_{dtype.lower()}_s{len(stages)}_")
+    assert [e["symbol"][-2:] for e in g.interface["entries"]] == ["_c", "_v", "_s"]
+
+
+def test_row_reduce_launched_shape():
+    """row_reduce_launched.rs: per stage a strided fold, the block tree, thread 0's rounding into
+    Shared slot s and a broadcast load; allocations partial (F64), partial_have, stage_result."""
+    stages, epi = X.softmax()
+    k = u.lift_row_reduce("sm", "F32", 2, stages, epi, launch=(16, 2))
+    assert [a["name"] for a in k["allocs"]] == ["partial", "partial_have", "stage_result"]
+    assert [a["elem"] for a in k["allocs"]] == ["F64", "I32", "F32"]
+    assert k["allocs"][2]["extent"] == {"Static": 2}
+    barriers = [s for s in stmts(k) if "Barrier" in s]
+    assert len(barriers) == 2 * (1 + 4 + 1)  # per stage: publish, log2(16) rounds, the broadcast
+    # serial: locals 2r + (S+1)n + 4S; launched: one more (the partner's have)
+    ks = u.lift_row_reduce("sm", "F32", 2, stages, epi)
+    assert len(ks["locals"]) == 4 + 3 + 8 and len(k["locals"]) == 4 + 3 + 8 + 1
+
+
+def test_row_reduce_declines():
+    def decline(*a, **kw):
+        with pytest.raises(_lib.UnpError) as e:
+            u.lift_row_reduce(*a, **kw)
+        assert e.value.kind == "LiftDecline"
+        return e.value.detail
+
+    sm = X.softmax()
+    assert "Prod stage" in decline("p", "F32", 2, [(X.input(0), "Prod")], X.reduced(0), launch=(64, 1))
+    assert "leading axis" in decline("p", "F32", 1, *sm, launch=(64, 1))
+    assert decline("p", "F32", 2, *sm, launch=(96, 1)) == "BadLaunch"
+    assert "non-float" in decline("p", "F16", 2, *sm)
+    assert "empty stage" in decline("p", "F32", 2, [], X.input(0))
+    assert "later stage" in decline("p", "F32", 2, [(X.reduced(0), "Sum")], X.input(0))
+    assert "Param" in decline("p", "F32", 2, [({"Param": 0}, "Sum")], X.reduced(0))
+    assert decline("p", "F32", 9, *sm) == "BadRank"
+    # the serial lift takes a Prod stage
+    u.lift_row_reduce("p", "F32", 2, [(X.input(0), "Prod")], X.reduced(0))
+
+
+def test_row_reduce_refusals_are_typed():
+    b = u.HipBackend()
+    # a Prod stage lifts (serially) but this backend declares no order-independent kernel for it
+    k = u.lift_row_reduce("p", "F32", 2, [(X.input(0), "Prod")], X.reduced(0))
+    with pytest.raises(_lib.UnpError) as e:
+        b.lower_kernel(k)
+    assert e.value.kind == "UnsupportedKernel" and "Prod" in e.value.detail
+    # an op this backend has no spelling for is an UnsupportedOp
+    k = u.lift_row_reduce("g", "F32", 2, [(X.input(0).unary("Lgamma"), "Sum")], X.reduced(0))
+    with pytest.raises(_lib.UnpError) as e:
+        b.lower_kernel(k)
+    assert e.value.kind == "UnsupportedOp" and "Lgamma" in e.value.detail
+    # a perturbed kernel is not a row reduction: the epilogue stored into the wrong buffer
+    k = u.lift_row_reduce("sm", "F32", 2, *X.softmax(), launch=(64, 4))
+    text = json.dumps(k).replace('{"Barrier": {"scope": "Block", "kind": "Full"}}', '{"Barrier": {"scope": "Block", "kind": "Full"}}, {"Barrier": {"scope": "Block", "kind": "Full"}}', 1)
+    with pytest.raises(_lib.UnpError) as e:
+        b.lower_kernel(text)
+    assert e.value.kind == "UnsupportedKernel"
+
+
+def test_row_reduce_two_inputs_and_rank_three():
+    b = u.HipBackend()
+    k = u.lift_row_reduce("two", "F64", 3, [(X.input(0) * X.input(1), "Sum")],
+                          X.input(0) * X.reduced(0) + X.input(1), n_inputs=2, launch=(128, 8))
+    g = b.lower_kernel(k)
+    assert g.interface["inputs"] == 2 and g.interface["rank"] == 3
+    assert g.interface["epilogue"] == "((x[0] * r[0]) + x[1])"
+    u.HipCompiler().compile(g.source, g.name)

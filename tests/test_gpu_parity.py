@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import oracle
+import unpopped_amd as u
 from unpopped_amd import forms as H
 from unpopped_amd import synth
 
@@ -244,6 +245,43 @@ def test_scan_multi_row(hip_device, shape):
     assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("exclusive", [False, True])
+@pytest.mark.parametrize("reverse", [False, True])
+def test_scan_many_tiles_several_rows(hip_device, exclusive, reverse):
+    """Rows of many block tiles each: tickets run across row boundaries, look-backs stop at a
+    row's first tile."""
+    H.say(f"[case] scan i32 (4, 400000) excl={exclusive} rev={reverse}")
+    x = rng(15).integers(-2**31, 2**31 - 1, size=(4, 400000), dtype=np.int32)
+    assert np.array_equal(H.scan_rows(x, "Sum", exclusive, reverse), oracle.scan_rows(x, "Sum", exclusive, reverse))
+
+
+@pytest.mark.parametrize("op", ["Sum", "Max", "Prod"])
+def test_scan_eight_byte_staged(hip_device, op):
+    """8-byte elements on the staged path (two status words per tile) over many tiles."""
+    H.say(f"[case] scan i64/f64 {op} (2, 300000)")
+    xi = rng(16).integers(-2**62, 2**62, size=(2, 300000), dtype=np.int64)
+    for excl, rev in ((False, False), (True, True)):
+        assert np.array_equal(H.scan_rows(xi, op, excl, rev), oracle.scan_rows(xi, op, excl, rev)), (excl, rev)
+    if op == "Prod":
+        return
+    xf = synth.uniform_01_f32(5, 600000).astype(np.float64).reshape(2, 300000)  # dyadic: exact in f64
+    for excl, rev in ((False, False), (True, True)):
+        assert np.array_equal(H.scan_rows(xf, op, excl, rev), oracle.scan_rows(xf, op, excl, rev)), (excl, rev)
+
+
+def test_scan_unaligned_takes_the_register_path(hip_device):
+    """A row whose extent is not a multiple of 16 bytes runs the register entry at size."""
+    H.say("[case] scan i32 unaligned (1, 1000003)")
+    x = rng(17).integers(-1000, 1000, size=(1, 1000003), dtype=np.int32)
+    ex = H.executor(kind="scan", dtype="I32", rank=2, op="Sum")
+    din = u.DeviceBuffer.from_array(x)
+    dout = u.DeviceBuffer(x.nbytes)
+    ex.launch(din, dout, 1, x.shape[1])
+    u.synchronize()
+    assert ex.last_launch()["entry"].endswith("_s")
+    assert np.array_equal(dout.download(np.int32, x.size).reshape(x.shape), oracle.scan_rows(x, "Sum"))
+
+
 def test_scan_repeated_launches_reuse_state(hip_device):
     """The look-back state is reused across launches (epoch tags): results stay exact."""
     H.say("[case] scan repeated launches")
@@ -329,6 +367,164 @@ def test_dequant_special_scales(hip_device):
     nan_g, nan_w = (got & 0x7FFF) > 0x7F80, (want & 0x7FFF) > 0x7F80
     assert np.array_equal(nan_g, nan_w)
     assert np.array_equal(got[~nan_g], want[~nan_w])
+
+
+# ---------------------------------------------------------------------------------------
+# Fused row reductions: the launched Access::RowReduce lift (softmax, RMS norm, ...)
+#
+# Bars: Max/Min stages bit-exact (kernel_parallel_row_reduce_agrees.rs:255-268); identity Sum/Mean
+# epilogues within the declared bound (:270-303); F32 epilogues within 2 ulps of the serial lift
+# (kernel_row_reduce_agrees.rs:25, :180-194); transcendental F64 epilogues within 4 ulps
+# (kernel_parallel_row_reduce_agrees.rs:368-388) plus the Sum stage's own order term; same NaN cells.
+# ---------------------------------------------------------------------------------------
+
+from unpopped_amd import expr as X  # noqa: E402
+
+
+def ulps(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Distance in representable values (+0 and -0 are one value); NaN against NaN is 0, NaN
+    against a number is infinite."""
+    it = np.int32 if a.dtype == np.float32 else np.int64
+    lo = np.int64(np.iinfo(it).min)
+
+    def key(x):
+        k = x.view(it).astype(np.int64)
+        with np.errstate(over="ignore"):
+            return np.where(k < 0, lo - k, k)  # monotone in the value
+
+    ka, kb = key(a), key(b)
+    same = (ka >= 0) == (kb >= 0)
+    with np.errstate(over="ignore"):
+        d = np.where(same, np.abs(ka - kb).astype(np.float64), np.abs(ka.astype(np.float64) - kb.astype(np.float64)))
+    an, bn = np.isnan(a), np.isnan(b)
+    return np.where(an | bn, np.where(an == bn, 0.0, np.inf), d)
+
+
+def gentle(rows, cols, dtype):
+    """Values in [-2, 4] (kernel_parallel_row_reduce_agrees.rs:58-63)."""
+    i = np.arange(rows * cols)
+    return (((i * 7 + 3) % 19) * 0.37 - 2.0).astype(dtype).reshape(rows, cols)
+
+
+def dyadic(seed, shape, dtype):
+    """Every partial sum exact in f64 (and the mean a single rounding), so any order agrees."""
+    return (rng(seed).integers(-64, 65, size=shape) / 8.0).astype(dtype)
+
+
+RR_SHAPES = [(1, 1), (3, 13), (5, 96), (4, 256), (7, 1000), (3, 4096), (2, 8192), (2, 8200), (3, 20000),
+             (2, 100003), (300, 20), (0, 7), (4, 0)]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape", RR_SHAPES)
+def test_row_reduce_identity_epilogues(hip_device, dtype, shape):
+    H.say(f"[case] row_reduce identity {np.dtype(dtype).name} {shape}")
+    x = rng(31).normal(size=shape).astype(dtype) * 100
+    for op in ("Sum", "Mean", "Max", "Min"):
+        got = H.row_reduce([x], [(X.input(0), op)], X.reduced(0))
+        want = oracle.row_reduce([x], [(X.input(0), op)], X.reduced(0))
+        if x.size == 0:
+            assert got.shape == want.shape
+        elif op in ("Max", "Min"):
+            assert equal_extremum(got, want), op
+        else:
+            assert (got == got[:, :1]).all()  # the stage result broadcast along the row
+            assert_sum_within_bound(x, got[:, 0], mean=(op == "Mean"))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("which", ["rms_norm", "centred_quotient"])
+@pytest.mark.parametrize("shape", [(3, 13), (5, 96), (9, 1000), (4, 8192), (2, 30000)])
+def test_row_reduce_dyadic_rows_are_bit_exact(hip_device, dtype, which, shape):
+    """With every partial sum exact the order cannot matter.  Centred quotient is then exact
+    arithmetic and equals the oracle bit for bit; rms norm also takes a square root in f64,
+    within 1 ulp at F32 and the 4 ulps of the transcendental bar at F64."""
+    H.say(f"[case] row_reduce dyadic {which} {np.dtype(dtype).name} {shape}")
+    x = dyadic(32, shape, dtype)
+    stages, epi = getattr(X, which)()
+    got = H.row_reduce([x], stages, epi)
+    want = oracle.row_reduce([x], stages, epi)
+    if which == "centred_quotient":
+        assert np.array_equal(got, want, equal_nan=True)
+    else:
+        assert ulps(got, want).max() <= (1 if dtype == np.float32 else 4)
+
+
+def f64_order_tolerance(x, want, which):
+    """The Sum stage of softmax and the Mean of rms norm fold only nonnegative terms, so each
+    order lies within gamma_(n-1) relative of the exact value; two orders differ by twice that."""
+    n = x.shape[1]
+    u = 2.0 ** -53
+    g = (n - 1) * u / (1 - (n - 1) * u)
+    rel = 2 * g if which == "softmax" else g  # x / sqrt(m): half the relative error of m
+    return np.abs(want) * 2 * rel + 4 * np.spacing(np.abs(want))
+
+
+@pytest.mark.parametrize("which", ["softmax", "rms_norm"])
+@pytest.mark.parametrize("shape", [(5, 96), (3, 13), (64, 4096), (4, 20000), (2, 100003)])
+def test_row_reduce_transcendental_epilogues(hip_device, which, shape):
+    H.say(f"[case] row_reduce {which} {shape}")
+    stages, epi = getattr(X, which)()
+    for dtype in (np.float32, np.float64):
+        x = gentle(*shape, dtype) if shape == (5, 96) else rng(33).normal(size=shape).astype(dtype) * 3
+        got = H.row_reduce([x], stages, epi)
+        want = oracle.row_reduce([x], stages, epi)
+        if dtype == np.float32:
+            assert ulps(got, want).max() <= 2, which
+        else:
+            far = ulps(got, want) > 4
+            assert (np.abs(got - want)[far] <= f64_order_tolerance(x, want, which)[far]).all(), which
+
+
+def test_row_reduce_centred_quotient_f32(hip_device):
+    """The two-stage form on the reference's gentle rows and on wide rows."""
+    stages, epi = X.centred_quotient()
+    for x in (gentle(5, 96, np.float32), rng(34).normal(size=(16, 5000)).astype(np.float32)):
+        H.say(f"[case] row_reduce centred quotient f32 {x.shape}")
+        got = H.row_reduce([x], stages, epi)
+        want = oracle.row_reduce([x], stages, epi)
+        assert ulps(got, want).max() <= 2
+
+
+def test_row_reduce_nan_and_infinity_rows(hip_device):
+    """kernel_row_reduce_agrees.rs:232-264: the same cells are NaN, the rest within 2 ulps."""
+    H.say("[case] row_reduce nan/inf rows")
+    x = np.array([[1.0, np.nan, 2.0, 3.0], [np.inf, 1.0, 2.0, -np.inf], [0.0, -0.0, 1.0, 2.0]], np.float32)
+    for stages, epi in (X.softmax(), X.centred_quotient()):
+        for arr in (x, np.repeat(x, 64, axis=1)):  # the second takes the vector entry
+            got = H.row_reduce([arr], stages, epi)
+            want = oracle.row_reduce([arr], stages, epi)
+            assert np.array_equal(np.isnan(got), np.isnan(want))
+            assert ulps(got, want).max() <= 2
+
+
+def test_row_reduce_two_inputs_rank_three(hip_device):
+    """Two inputs, rank 3 (rows are the product of the leading extents)."""
+    H.say("[case] row_reduce two inputs rank 3")
+    a, b = dyadic(35, (2, 3, 700), np.float32), dyadic(36, (2, 3, 700), np.float32)
+    stages = [(X.input(0) * X.input(1), "Sum"), (X.input(0) - X.reduced(0), "Max")]
+    epi = X.fma(X.input(0), X.reduced(1), X.input(1) - X.reduced(0))
+    got = H.row_reduce([a, b], stages, epi)
+    want = oracle.row_reduce([a, b], stages, epi)
+    assert np.array_equal(got, want)
+
+
+def test_row_reduce_entries_and_reproducibility(hip_device):
+    """Each entry runs where it should, and a launch repeats bit for bit."""
+    stages, epi = X.softmax()
+    for shape, suffix in (((8, 4096), "_c"), ((8, 8196), "_v"), ((8, 4099), "_s")):
+        H.say(f"[case] row_reduce entry {suffix} {shape}")
+        x = rng(37).normal(size=shape).astype(np.float32)
+        ex = H.row_reduce_executor("F32", 2, stages, epi)
+        din, dout = u.DeviceBuffer.from_array(x), u.DeviceBuffer(x.nbytes)
+        outs = []
+        for _ in range(2):
+            ex.launch(din, dout, *shape)
+            u.synchronize()
+            outs.append(dout.download(np.float32, x.size).reshape(shape))
+        assert ex.last_launch()["entry"].endswith(suffix)
+        assert np.array_equal(outs[0], outs[1])
+        assert ulps(outs[0], oracle.row_reduce([x], stages, epi)).max() <= 2
 
 
 # ---------------------------------------------------------------------------------------

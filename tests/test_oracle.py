@@ -384,3 +384,115 @@ def test_synth_parallel_chunks_equal_the_sequential_stream():
     z = synth.zipf_ids_i32(3, 65536, 262144, 1.1)
     assert z.min() >= 0 and z.max() < 262144
     assert np.bincount(z).max() > 1000  # heavy-tailed: the top row repeats
+
+
+# ---------------------------------------------------------------------------------------
+# Row reductions (crates/unpopped/src/kernel_lift/row_reduce.rs; tests/kernel_row_reduce_agrees.rs)
+# ---------------------------------------------------------------------------------------
+
+import math  # noqa: E402
+from functools import reduce as _fold  # noqa: E402
+
+from unpopped_amd import expr as X  # noqa: E402
+
+# the corpus of kernel_row_reduce_agrees.rs:33-35 and :141-145
+RR_VALUES = [1.0e8, 1.0, -1.0e8, 0.5, 3.25, -2.0, 7.0, 0.1, -0.75, 12.0, -5.5, 0.3, 2.0]
+
+
+def rr_data(rows, k, dtype):
+    return np.array([RR_VALUES[i % 13] * (1.0 + (i // 13) * 0.37) for i in range(rows * k)]).astype(dtype).reshape(rows, k)
+
+
+def rnd(v, dtype):
+    return float(np.asarray(v, dtype=dtype)) if dtype == np.float32 else v
+
+
+def test_row_reduce_identity_epilogues_equal_the_reduction_oracle():
+    """kernel_row_reduce_agrees.rs:148-160: an identity epilogue is the lifted reduction."""
+    x = rr_data(3, 13, np.float32)
+    for op in ("Sum", "Mean", "Max", "Min"):
+        got = oracle.row_reduce([x], [(X.input(0), op)], X.reduced(0))
+        want = oracle.reduce_rows(x, op)
+        assert np.array_equal(got, np.repeat(want[:, None], 13, axis=1)), op
+
+
+def test_row_reduce_wide_accumulator_known_answer():
+    """kernel_row_reduce_agrees.rs:213-229: 1e8 + 1 - 1e8 in a row needs an f64 accumulator."""
+    x = np.array([[1.0e8, 1.0, -1.0e8, 0.5, 2.0]], np.float32)
+    got = oracle.row_reduce([x], [(X.input(0), "Sum")], X.reduced(0))
+    assert got[0, 0] == 3.5
+
+
+def closed_form(x, dtype, which):
+    """The serial lifted kernel restated with Python floats (f64) and math (the host libm, as
+    Rust's f64 methods call it): ascending folds, one rounding per statement."""
+    out = np.empty_like(x)
+    for r, row in enumerate(x.astype(np.float64)):
+        if which == "softmax":
+            m = rnd(_fold(lambda a, v: v if (v != v or v > a) else a, row), dtype)
+            s = rnd(_fold(lambda a, v: a + rnd(math.exp(v - m), dtype), row, 0.0), dtype)
+            out[r] = [math.exp(v - m) / s for v in row]
+        elif which == "rms_norm":
+            mean = rnd(_fold(lambda a, v: a + rnd(v * v, dtype), row, 0.0) / len(row), dtype)
+            out[r] = [v / math.sqrt(mean + 1.0e-3) for v in row]
+        else:  # centred quotient
+            mean = rnd(_fold(lambda a, v: a + v, row, 0.0) / len(row), dtype)
+            mx = rnd(_fold(lambda a, v: v if (v != v or v > a) else a, [rnd(v - mean, dtype) for v in row]), dtype)
+            out[r] = [(v - mean) / mx for v in row]
+    return out
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("which", ["softmax", "rms_norm", "centred_quotient"])
+def test_row_reduce_matches_the_closed_form(dtype, which):
+    x = rr_data(5, 13, dtype)
+    stages, epi = getattr(X, which)()
+    got = oracle.row_reduce([x], stages, epi)
+    assert np.array_equal(got, closed_form(x, dtype, which))
+    # a planted mistake: the stage value left unrounded at f32 moves some softmax output
+    if dtype == np.float32 and which == "softmax":
+        moved = False
+        for rows in range(1, 40):
+            src = np.array([((i * 7 + 3) % 19) * 0.37 - 2.0 for i in range(rows * 11)], np.float32).reshape(rows, 11)
+            exact = closed_form(src.astype(np.float64), np.float64, "softmax").astype(np.float32)
+            moved |= not np.array_equal(oracle.row_reduce([src], stages, epi), exact)
+        assert moved  # kernel_row_reduce_agrees.rs:186-204: the rounding is not vacuous
+
+
+def test_row_reduce_nan_and_infinity_rows():
+    """kernel_row_reduce_agrees.rs:232-260: NaN and infinite rows."""
+    x = np.array([[1.0, np.nan, 2.0, 3.0], [np.inf, 1.0, 2.0, -np.inf], [0.0, -0.0, 1.0, 2.0]], np.float32)
+    sm = oracle.row_reduce([x], *X.softmax())
+    assert np.isnan(sm[0]).all()            # a NaN max poisons its row
+    assert np.isnan(sm[1]).all()            # max is inf, exp(inf - inf) is NaN, so the sum is NaN
+    assert np.allclose(sm[2].sum(), 1.0, rtol=1e-6)
+    cq = oracle.row_reduce([x], *X.centred_quotient())
+    assert np.isnan(cq[0]).all()
+
+
+def test_rx_program_ops_follow_the_host_libm():
+    """Every op the programs carry, against Python's math (the same libm)."""
+    for v in (-2.5, -0.3, 0.0, 0.7, 1.9):
+        for name, f in [("Neg", lambda a: -a), ("Abs", abs), ("Sqr", lambda a: a * a), ("Exp", math.exp),
+                        ("Tanh", math.tanh), ("Sigmoid", lambda a: 1.0 / (1.0 + math.exp(-a))),
+                        ("Relu", lambda a: 0.0 if a < 0.0 else a), ("Erf", math.erf), ("Sin", math.sin),
+                        ("Cos", math.cos), ("Floor", math.floor), ("Ceil", math.ceil), ("Trunc", math.trunc),
+                        ("Expm1", math.expm1), ("Atan", math.atan), ("Asinh", math.asinh), ("Sinh", math.sinh),
+                        ("Silu", lambda a: a * (1.0 / (1.0 + math.exp(-a)))),
+                        ("Gelu", lambda a: 0.5 * a * (1.0 + math.erf(a * 0.70710678118654752440)))]:
+            assert oracle.rx_eval(X.input(0).unary(name), [v]) == float(f(v)), (name, v)
+        if v > 0:
+            for name, f in [("Sqrt", math.sqrt), ("Log", math.log), ("Log2", math.log2), ("Log10", math.log10),
+                            ("Rsqrt", lambda a: 1.0 / math.sqrt(a)), ("Recip", lambda a: 1.0 / a)]:
+                assert oracle.rx_eval(X.input(0).unary(name), [v]) == f(v), (name, v)
+    # Max/Min: NaN-propagating, the left operand on ties (scalar_ops.rs:90-112)
+    mx = X.input(0).maximum(X.input(1))
+    assert oracle.rx_eval(mx, [-0.0, 0.0]) == 0.0 and math.copysign(1, oracle.rx_eval(mx, [-0.0, 0.0])) < 0
+    assert math.isnan(oracle.rx_eval(mx, [1.0, float("nan")]))
+    # Sign decides on the argument rounded to the compute dtype first (expr_eval.rs:130-137)
+    tiny = 1e-50
+    assert oracle.rx_eval(X.input(0).unary("Sign"), [tiny], f32=True) == 0.0
+    assert oracle.rx_eval(X.input(0).unary("Sign"), [tiny], f32=False) == 1.0
+    # Fma rounds once: 0.1 * 10 - 1 is exactly 2^-54 (0.1 is 0x1.999999999999ap-4), the two-step form gives 0
+    assert oracle.rx_eval(X.fma(X.input(0), X.input(1), X.input(2)), [0.1, 10.0, -1.0]) == 2.0 ** -54
+    assert oracle.rx_eval(X.input(0) * X.input(1) + X.input(2), [0.1, 10.0, -1.0]) == 0.0

@@ -167,6 +167,20 @@ def kernel_dequant4(name: str, q_kind: str = "U4", z_kind: str = "U4", group: in
                                                               ELEMENT_KINDS[z_kind], group, b, g, o, e))
 
 
+def lift_row_reduce(name: str, dtype: str, rank: int, stages, epilogue, n_inputs: int = 1,
+                    launch: tuple | None = None) -> dict:
+    """The Access::RowReduce lift (serial, or launched on ``launch = (block, grid)``) as a KernelFn
+    dict.  ``stages`` is a list of ``(pre, op)`` with ``pre`` a ScalarExpr (an ``expr.Expr`` or its
+    serde dict) over ``Input(k)`` and earlier ``Reduced(t)``; ``epilogue`` the full-width output."""
+    from . import expr as X
+
+    b, g = _geom(launch)
+    st = json.dumps([{"pre": X.as_json(pre), "op": op} for pre, op in stages])
+    ep = json.dumps(X.as_json(epilogue))
+    return _lifted(lambda o, e: _lib.lib().unp_lift_row_reduce(name.encode(), ELEMENT_KINDS[dtype], rank, n_inputs,
+                                                              st.encode(), ep.encode(), b, g, o, e))
+
+
 class HipCompiler:
     """The ``Compiler`` seam: hipRTC for gfx950, artifacts are HIP code objects."""
 

@@ -507,6 +507,241 @@ static int32_t lower_dequant(const unp_form& f, Lowered& L, std::string& why) {
   return UNP_OK;
 }
 
+// ---- Access::RowReduce ---------------------------------------------------------------------
+
+namespace {
+
+// A ScalarExpr over Input(k) / Reduced(t) leaves as a C++ double expression (f64 evaluation,
+// the caller rounds once).  False, with the node named in `why`, outside the vocabulary this
+// backend spells.
+bool expr_cpp(const kir::J& e, const char* T, std::string& out, std::string& why) {
+  using kir::J;
+  if (e.t != J::Obj || e.o.size() != 1) {
+    why = "a malformed ScalarExpr";
+    return false;
+  }
+  const std::string& tag = e.o[0].first;
+  const J& p = e.o[0].second;
+  auto sub = [&](size_t i, std::string& o) { return p.t == J::Arr && i < p.a.size() && expr_cpp(p.a[i], T, o, why); };
+  if (tag == "Input" || tag == "Reduced") {
+    if (!p.is_int || p.i < 0) {
+      why = "a malformed leaf";
+      return false;
+    }
+    out = std::string(tag == "Input" ? "x[" : "r[") + std::to_string(p.i) + "]";
+    return true;
+  }
+  if (tag == "Const") {
+    if (p.t == J::Str) {
+      if (p.s == "NaN") out = "__builtin_nan(\"\")";
+      else if (p.s == "inf") out = "__builtin_inf()";
+      else if (p.s == "-inf") out = "(-__builtin_inf())";
+      else {
+        why = "a Const tag `" + p.s + "`";
+        return false;
+      }
+      return true;
+    }
+    if (p.t != J::Num) {
+      why = "a malformed Const";
+      return false;
+    }
+    char buf[64];
+    std::snprintf(buf, sizeof buf, "%a", p.d);  // exact: a hexadecimal floating literal
+    out = std::string("(") + buf + ")";
+    return true;
+  }
+  std::string a, b, c;
+  if (tag == "Add" || tag == "Sub" || tag == "Mul" || tag == "Div") {
+    if (!sub(0, a) || !sub(1, b)) return false;
+    const char* o = tag == "Add" ? " + " : tag == "Sub" ? " - " : tag == "Mul" ? " * " : " / ";
+    out = "(" + a + o + b + ")";
+    return true;
+  }
+  if (tag == "Fma" || tag == "Select") {
+    if (!sub(0, a) || !sub(1, b) || !sub(2, c)) return false;
+    out = (tag == "Fma" ? "fma(" : "unp::xf::select(") + a + ", " + b + ", " + c + ")";
+    return true;
+  }
+  if (tag == "Unary") {
+    if (p.t != J::Arr || p.a.size() != 2 || p.a[0].t != J::Str || !sub(1, a)) {
+      if (why.empty()) why = "a malformed Unary";
+      return false;
+    }
+    static const struct {
+      const char* op;
+      const char* fn;
+    } un[] = {{"Abs", "fabs"},         {"Sqr", "unp::xf::sqr"},   {"Sqrt", "sqrt"},
+              {"Rsqrt", "unp::xf::rsqrt"}, {"Recip", "unp::xf::recip"}, {"Exp", "exp"},
+              {"Log", "log"},          {"Tanh", "tanh"},          {"Sigmoid", "unp::xf::sigmoid"},
+              {"Relu", "unp::xf::relu"}, {"Erf", "erf"},           {"Gelu", "unp::xf::gelu"},
+              {"Silu", "unp::xf::silu"}, {"Sin", "sin"},           {"Cos", "cos"},
+              {"Floor", "floor"},      {"Ceil", "ceil"},          {"Round", "rint"},
+              {"Erfc", "erfc"},        {"Trunc", "trunc"},        {"Exp2", "exp2"},
+              {"Expm1", "expm1"},      {"Log2", "log2"},          {"Log10", "log10"},
+              {"Log1p", "log1p"},      {"Sinh", "sinh"},          {"Cosh", "cosh"},
+              {"Tan", "tan"},          {"Asin", "asin"},          {"Acos", "acos"},
+              {"Atan", "atan"},        {"Asinh", "asinh"},        {"Acosh", "acosh"},
+              {"Atanh", "unp::xf::atanh_odd"}, {"Cbrt", "cbrt"}};
+    const std::string& op = p.a[0].s;
+    if (op == "Neg") {
+      out = "(-" + a + ")";
+      return true;
+    }
+    if (op == "Sign" || op == "Step") {
+      out = std::string("unp::xf::") + (op == "Sign" ? "sign<" : "step<") + T + ">(" + a + ")";
+      return true;
+    }
+    for (const auto& u : un)
+      if (op == u.op) {
+        out = std::string(u.fn) + "(" + a + ")";
+        return true;
+      }
+    why = "the unary op " + op;
+    return false;
+  }
+  if (tag == "Binary") {
+    if (p.t != J::Arr || p.a.size() != 3 || p.a[0].t != J::Str || !sub(1, a) || !sub(2, b)) {
+      if (why.empty()) why = "a malformed Binary";
+      return false;
+    }
+    const std::string& op = p.a[0].s;
+    static const struct {
+      const char* op;
+      const char* fn;
+    } bn[] = {{"Max", "unp::xf::max_prop"}, {"Min", "unp::xf::min_prop"}, {"Pow", "pow"},
+              {"Rem", "unp::xf::rem_floor"}, {"RemTrunc", "fmod"},         {"Atan2", "atan2"},
+              {"Copysign", "copysign"},     {"FmaxIeee", "fmax"},         {"FminIeee", "fmin"}};
+    for (const auto& u : bn)
+      if (op == u.op) {
+        out = std::string(u.fn) + "(" + a + ", " + b + ")";
+        return true;
+      }
+    static const struct {
+      const char* op;
+      const char* c;
+    } cmp[] = {{"CmpEq", "=="}, {"CmpNe", "!="}, {"CmpLt", "<"}, {"CmpLe", "<="}, {"CmpGt", ">"}, {"CmpGe", ">="}};
+    for (const auto& u : cmp)
+      if (op == u.op) {
+        out = "((" + a + " " + u.c + " " + b + ") ? 1.0 : 0.0)";
+        return true;
+      }
+    why = "the binary op " + op;
+    return false;
+  }
+  why = "the expression node " + tag;
+  return false;
+}
+
+}  // namespace
+
+int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) {
+  L = Lowered{};
+  L.form.kind = UNP_FORM_ROW_REDUCE;
+  L.form.dtype = sp.dtype;
+  L.form.rank = sp.rank;
+  L.rr = sp;
+  if (sp.dtype != UNP_F32 && sp.dtype != UNP_F64) {
+    why = "a row reduction outside F32 and F64";
+    return UNP_UNSUPPORTED_DTYPE;
+  }
+  const size_t NS = sp.ops.size();
+  if (NS == 0 || NS != sp.pres.size() || sp.n_inputs < 1 || sp.n_inputs > 8) {
+    why = "a row reduction needs 1 to 8 inputs and at least one stage";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  for (int32_t op : sp.ops)
+    if (op == UNP_OP_PROD) {
+      why = "a Prod stage (a float product is not order-independent and declares no bound)";
+      return UNP_UNSUPPORTED_KERNEL;
+    }
+  const char* T = ctype(sp.dtype);
+  std::vector<std::string> pre(NS);
+  std::string epi;
+  for (size_t st = 0; st < NS; ++st)
+    if (!expr_cpp(sp.pres[st], T, pre[st], why)) {
+      why = "stage " + std::to_string(st) + ": " + why + " has no spelling here";
+      return UNP_UNSUPPORTED_OP;
+    }
+  if (!expr_cpp(sp.epilogue, T, epi, why)) {
+    why = "epilogue: " + why + " has no spelling here";
+    return UNP_UNSUPPORTED_OP;
+  }
+  // The name carries a hash of the expressions: different row reductions never share a symbol.
+  std::string key = std::string(T) + "|" + std::to_string(sp.n_inputs);
+  for (size_t st = 0; st < NS; ++st) key += "|" + std::to_string(sp.ops[st]) + ":" + pre[st];
+  key += "|" + epi;
+  char hx[17];
+  std::snprintf(hx, sizeof hx, "%016llx", (unsigned long long)fnv1a64(key));
+  L.name = std::string("unp_row_reduce_") + lower_name(sp.dtype) + "_s" + std::to_string(NS) + "_" + std::string(hx, 8);
+  const std::string ops = L.name + "_ops";
+  std::ostringstream src;
+  unp_form f{};
+  f.kind = UNP_FORM_ROW_REDUCE;
+  src << header(L.name, f);
+  src << "struct " << ops << " {\n  static constexpr int op[" << NS << "] = {";
+  for (size_t st = 0; st < NS; ++st) src << (st ? ", " : "") << sp.ops[st];
+  src << "};\n  template <int S> static __device__ __forceinline__ double pre(const double* x, const double* r);\n"
+      << "  static __device__ __forceinline__ double epi(const double* x, const double* r) { (void)x; (void)r; return "
+      << epi << "; }\n};\n";
+  for (size_t st = 0; st < NS; ++st)
+    src << "template <> __device__ __forceinline__ double " << ops << "::pre<" << st
+        << ">(const double* x, const double* r) { (void)x; (void)r; return " << pre[st] << "; }\n";
+  const int vec = vec_of(sp.dtype);
+  struct E {
+    const char* suffix;
+    int vec, r;
+    bool fast;
+  } es[] = {{"_c", vec, 8, true}, {"_v", vec, 0, true}, {"_s", 1, 0, false}};
+  for (const E& e : es) {
+    Entry en;
+    en.symbol = L.name + e.suffix;
+    en.vec = e.vec;
+    en.k = e.r;  // vectors per thread held in registers (0: re-read)
+    en.fast = e.fast;
+    src << "extern \"C\" __global__ void " << kLaunchBounds << " " << en.symbol << "(";
+    for (int k = 0; k < sp.n_inputs; ++k) src << "const " << T << "* in" << k << ", ";
+    src << T << "* out, long long rows, long long cols) {\n  const " << T << "* in[" << sp.n_inputs << "] = {";
+    for (int k = 0; k < sp.n_inputs; ++k) src << (k ? ", " : "") << "in" << k;
+    src << "};\n  unp::row_reduce_staged<" << T << ", " << sp.n_inputs << ", " << NS << ", " << ops << ", 256, " << e.vec
+        << ", " << e.r << ">(in, out, rows, cols);\n}\n";
+    L.entries.push_back(en);
+  }
+  L.source = src.str();
+  L.threads = 256;
+  L.blocks_per_cu = 8;
+  std::ostringstream j;
+  j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"row_reduce\",\"dtype\":\"" << kind_name(sp.dtype)
+    << "\",\"rank\":" << sp.rank << ",\"inputs\":" << sp.n_inputs << ",\"stages\":[";
+  static const char* const opn[] = {"Sum", "Prod", "Max", "Min", "Mean"};
+  for (size_t st = 0; st < NS; ++st)
+    j << (st ? "," : "") << "{\"op\":\"" << opn[sp.ops[st]] << "\",\"pre\":" << json_str(pre[st]) << "}";
+  j << "],\"epilogue\":" << json_str(epi) << ",\"params\":[";
+  for (int k = 0; k < sp.n_inputs; ++k) j << "{\"name\":\"in" << k << "\",\"kind\":\"buffer\",\"role\":\"Read\"},";
+  j << "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
+  for (int d = 0; d < sp.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
+  j << "],\"launch\":{\"block\":[256,1,1],\"grid\":\"min(rows, cu_count*8)\",\"grid_policy\":\"one block per row, rows "
+       "block-strided\"},\"entries\":[";
+  for (size_t i = 0; i < L.entries.size(); ++i)
+    j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
+      << ",\"row_in_registers\":" << (L.entries[i].k ? "true" : "false") << ",\"when\":\""
+      << (L.entries[i].k ? "cols % vec == 0, every buffer 16-byte aligned and cols <= 256 * vec * 8"
+                         : (L.entries[i].fast ? "cols % vec == 0 and every buffer 16-byte aligned" : "otherwise"))
+      << "\"}";
+  j << "],\"workspace\":null"
+    << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
+    << ",\"fidelity_notes\":["
+    << json_str("expressions evaluate in f64 and round once per statement, as the kernel evaluator runs the lifted "
+                "kernel; +, -, *, /, fma, sqrt and the comparisons are exact, the device's f64 transcendentals are "
+                "within an ulp of the host libm's")
+    << "," << json_str("Sum/Mean stages fold in f64 in a geometry-fixed order: within the declared bound "
+                       "gamma_(n-1)*sum|x| of the serial fold, then one rounding; Max/Min stages are exact except NaN "
+                       "payload and the sign of a zero")
+    << "]}";
+  L.interface_json = j.str();
+  return UNP_OK;
+}
+
 int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail) {
   out = Lowered{};
   out.form = f;
@@ -520,6 +755,9 @@ int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail) {
       return lower_gather(f, out, detail);
     case UNP_FORM_DEQUANT4:
       return lower_dequant(f, out, detail);
+    case UNP_FORM_ROW_REDUCE:
+      detail = "a row reduction's expressions come only with its KernelFn (Backend::lower_kernel)";
+      return UNP_UNSUPPORTED_KERNEL;
     default:
       detail = "an unknown form";
       return UNP_UNSUPPORTED_KERNEL;

@@ -1126,4 +1126,159 @@ UNP_DEV void dequant4_bf16_any(const u8* __restrict__ q, const u16* __restrict__
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Access::RowReduce (crates/unpopped/src/ir.rs:2114-2125): per row, NS staged folds, each over
+// a pre expression that may read the inputs and the earlier stages, then a full-width epilogue
+// (softmax, RMSNorm, a centred quotient ...).
+//
+// Numerics follow the lifted kernel as the reference's kernel evaluator runs it
+// (crates/unpopped/src/oracle/kernel_eval.rs:765-770, 924-955): a float expression is evaluated
+// in f64 from its operands and rounded once per statement.  So a stage folds
+// (f64)(T)pre(x, red) into an f64 accumulator (Max/Min with the NaN rule), finalises (Mean
+// divides by the row length; an empty row leaves the accumulator's starting 0), and rounds
+// once to T; the epilogue is evaluated in f64 over the inputs and the rounded stage values and
+// rounded once at the store.  The emitted source supplies OPS: `op[S]`, `pre<S>(x, r)` and
+// `epi(x, r)` over doubles, with the scalar functions below.
+//
+// One block per row (rows block-strided).  R > 0: the row is read once into registers
+// (R vectors of VEC per thread and input, cols <= THREADS * VEC * R); R == 0: each pass reads
+// the row again (the later passes hit in L2).  Inside a pass thread t folds its positions in
+// ascending order; waves combine by DPP, then in wave order, so the order is fixed by the
+// geometry.
+// ---------------------------------------------------------------------------------------
+namespace xf {
+// UnaryOp / BinaryOp in f64, as crates/unpopped/src/oracle/scalar_ops.rs:14-80, 90-150 define
+// them.  Sign and Step decide on the argument rounded to the compute dtype T first
+// (expr_eval.rs:130-137).
+UNP_DEV double sqr(double x) { return x * x; }
+UNP_DEV double rsqrt(double x) { return 1.0 / sqrt(x); }
+UNP_DEV double recip(double x) { return 1.0 / x; }
+UNP_DEV double sigmoid(double x) { return 1.0 / (1.0 + exp(-x)); }
+UNP_DEV double relu(double x) { return x < 0.0 ? 0.0 : x; }
+UNP_DEV double silu(double x) { return x * (1.0 / (1.0 + exp(-x))); }
+UNP_DEV double gelu(double x) { return 0.5 * x * (1.0 + erf(x * 0.70710678118654752440)); }
+UNP_DEV double atanh_odd(double x) { return copysign(atanh(fabs(x)), x); }
+template <class T> UNP_DEV double sign(double x) {
+  const double c = (double)(T)x;
+  return c > 0.0 ? 1.0 : (c < 0.0 ? -1.0 : 0.0);
+}
+template <class T> UNP_DEV double step(double x) { return (double)(T)x > 0.0 ? 1.0 : 0.0; }
+// NaN-propagating, and `a` on ties.
+UNP_DEV double max_prop(double a, double b) { return a != a ? a : (b != b ? b : (a >= b ? a : b)); }
+UNP_DEV double min_prop(double a, double b) { return a != a ? a : (b != b ? b : (a <= b ? a : b)); }
+// Floored remainder (sign of the divisor).
+UNP_DEV double rem_floor(double a, double b) { return a - floor(a / b) * b; }
+UNP_DEV double select(double c, double a, double b) { return c != 0.0 ? a : b; }
+}  // namespace xf
+
+template <class T, int NI, int NS, class OPS, int THREADS, int VEC, int R, int S>
+UNP_DEV void rr_stage(const T* const* rin, const vec<T, VEC> (&xr)[NI][R > 0 ? R : 1], i64 cols, double (&red)[NS],
+                      double* part, double* redsh) {
+  if constexpr (S < NS) {
+    constexpr int OP = OPS::op[S];
+    typedef fold<double, OP> F;
+    constexpr int WAVES = THREADS / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const i64 nvec = cols / VEC;
+    double acc = F::identity();
+    auto fold_vec = [&](const vec<T, VEC> (&v)[NI]) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        double x[NI];
+#pragma unroll
+        for (int k = 0; k < NI; ++k) x[k] = (double)v[k].e[e];
+        acc = F::apply(acc, (double)(T)OPS::template pre<S>(x, red));
+      }
+    };
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int q = 0; q < R; ++q)
+        if ((i64)q * THREADS + tid < nvec) {
+          vec<T, VEC> xv[NI];
+#pragma unroll
+          for (int k = 0; k < NI; ++k) xv[k] = xr[k][q];
+          fold_vec(xv);
+        }
+    } else {
+      for (i64 v = tid; v < nvec; v += THREADS) {
+        vec<T, VEC> xv[NI];
+#pragma unroll
+        for (int k = 0; k < NI; ++k) xv[k] = ld<T, VEC>(rin[k] + v * VEC);
+        fold_vec(xv);
+      }
+    }
+    acc = wave_reduce<double, OP>(acc);
+    if (lane == 0) part[wave] = acc;
+    __syncthreads();
+    if (tid == 0) {
+      double a = part[0];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) a = F::apply(a, part[w]);
+      double fin = a;
+      if constexpr (OP == OP_MEAN) fin = a / (double)cols;
+      if constexpr (OP == OP_MAX || OP == OP_MIN) fin = cols == 0 ? 0.0 : a;
+      redsh[S] = (double)(T)fin;
+    }
+    __syncthreads();
+    red[S] = redsh[S];
+    rr_stage<T, NI, NS, OPS, THREADS, VEC, R, S + 1>(rin, xr, cols, red, part, redsh);
+  }
+}
+
+template <class T, int NI, int NS, class OPS, int THREADS, int VEC, int R>
+UNP_DEV void row_reduce_staged(const T* const* in, T* __restrict__ out, i64 rows, i64 cols) {
+  __shared__ double part[THREADS / 64];
+  __shared__ double redsh[NS];
+  const int tid = threadIdx.x;
+  const i64 nvec = cols / VEC;
+  for (i64 row = blockIdx.x; row < rows; row += gridDim.x) {
+    const T* rin[NI];
+#pragma unroll
+    for (int k = 0; k < NI; ++k) rin[k] = in[k] + row * cols;
+    T* __restrict__ rout = out + row * cols;
+    vec<T, VEC> xr[NI][R > 0 ? R : 1];
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int q = 0; q < R; ++q) {
+        const i64 v = (i64)q * THREADS + tid;
+        if (v < nvec)
+#pragma unroll
+          for (int k = 0; k < NI; ++k) xr[k][q] = ld_nt<T, VEC>(rin[k] + v * VEC);
+      }
+    }
+    double red[NS];
+    rr_stage<T, NI, NS, OPS, THREADS, VEC, R, 0>(rin, xr, cols, red, part, redsh);
+    auto emit = [&](const vec<T, VEC> (&v)[NI], i64 at) {
+      vec<T, VEC> o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        double x[NI];
+#pragma unroll
+        for (int k = 0; k < NI; ++k) x[k] = (double)v[k].e[e];
+        o.e[e] = (T)OPS::epi(x, red);
+      }
+      st_nt<T, VEC>(rout + at * VEC, o);
+    };
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int q = 0; q < R; ++q) {
+        const i64 v = (i64)q * THREADS + tid;
+        if (v < nvec) {
+          vec<T, VEC> xv[NI];
+#pragma unroll
+          for (int k = 0; k < NI; ++k) xv[k] = xr[k][q];
+          emit(xv, v);
+        }
+      }
+    } else {
+      for (i64 v = tid; v < nvec; v += THREADS) {
+        vec<T, VEC> xv[NI];
+#pragma unroll
+        for (int k = 0; k < NI; ++k) xv[k] = ld<T, VEC>(rin[k] + v * VEC);
+        emit(xv, v);
+      }
+    }
+  }
+}
+
 }  // namespace unp

@@ -537,6 +537,316 @@ J dequant4(const std::string& name, int32_t qk, int32_t zk, int32_t group, uint3
   return k;
 }
 
+// ---- Access::RowReduce (kernel_lift/row_reduce.rs, kernel_lift/row_reduce_launched.rs) ------
+
+// The payload items of a ScalarExpr node (crates/unpopped/src/ir.rs:235-420) that are
+// expressions.  False for a node kind this restatement does not carry.
+bool expr_slots(const J& e, std::string& tag, std::vector<size_t>& slots, bool& leaf) {
+  leaf = false;
+  slots.clear();
+  if (e.t != J::Obj || e.o.size() != 1) return false;
+  tag = e.o[0].first;
+  const J& p = e.o[0].second;
+  static const char* const leaves[] = {"Input", "Const", "Param", "Reduced", "Coord", "CoordInt", "ConstInt", "Local",
+                                       "Exec"};
+  for (const char* l : leaves)
+    if (tag == l) {
+      leaf = true;
+      return true;
+    }
+  if (p.t != J::Arr) return false;
+  const size_t n = p.a.size();
+  if (tag == "Add" || tag == "Sub" || tag == "Mul" || tag == "Div") {
+    slots = {0, 1};
+    return n == 2;
+  }
+  if (tag == "Unary") {
+    slots = {1};
+    return n == 2;
+  }
+  if (tag == "Binary") {
+    slots = {1, 2};
+    return n == 3;
+  }
+  if (tag == "Select" || tag == "Fma") {
+    slots = {0, 1, 2};
+    return n == 3;
+  }
+  if (tag == "Cast" || tag == "Bitcast" || tag == "Qualified" || tag == "Extract") {
+    slots = {0};
+    return n == 2;
+  }
+  if (tag == "Pack") {
+    for (size_t i = 0; i < n; ++i) slots.push_back(i);
+    return true;
+  }
+  return false;
+}
+
+int64_t leaf_index(const J& e) {
+  const J& p = e.o[0].second;
+  return p.is_int ? p.i : -1;
+}
+
+// bind (kernel_lift/post.rs): `e` rebuilt with `leaf` tried first at every node.
+template <class F> J map_leaves(const J& e, const F& leaf) {
+  J out;
+  if (leaf(e, out)) return out;
+  std::string tag;
+  std::vector<size_t> slots;
+  bool is_leaf;
+  if (!expr_slots(e, tag, slots, is_leaf))
+    throw Decline{"UnsupportedForm: an expression node outside this backend's vocabulary"};
+  if (is_leaf) return e;
+  J c = e;
+  for (size_t i : slots) c.o[0].second.a[i] = map_leaves(e.o[0].second.a[i], leaf);
+  return c;
+}
+
+// check_post (kernel_lift/post.rs) and leaves_ok (kernel_lift.rs:397-409): a stage's pre may read
+// the stages before it, the epilogue every stage; no Coord, Param, Local or Exec leaf.  An Input
+// must name one of the op's inputs.
+void check_post(const J& e, int64_t available, int64_t n_inputs) {
+  std::string tag;
+  std::vector<size_t> slots;
+  bool leaf;
+  if (!expr_slots(e, tag, slots, leaf))
+    throw Decline{"UnsupportedForm: an expression node outside this backend's vocabulary"};
+  if (leaf) {
+    if (tag == "Reduced" && !(leaf_index(e) >= 0 && leaf_index(e) < available))
+      throw Decline{"UnsupportedLeaf: a Reduced of a later stage"};
+    if (tag == "Coord" || tag == "CoordInt") throw Decline{"UnsupportedLeaf: Coord"};
+    if (tag == "Param") throw Decline{"UnsupportedLeaf: Param"};
+    if (tag == "Local") throw Decline{"UnsupportedLeaf: Local"};
+    if (tag == "Exec") throw Decline{"UnsupportedLeaf: Exec"};
+    if (tag == "Input" && !(leaf_index(e) >= 0 && leaf_index(e) < n_inputs))
+      throw Decline{"UnsupportedForm: an Input beyond the op's inputs"};
+    return;
+  }
+  for (size_t i : slots) check_post(e.o[0].second.a[i], available, n_inputs);
+}
+
+// The local ids of row_reduce.rs's `Row`: extents 0..r, counters r..2r, then per phase (each
+// stage, then the epilogue) one loaded local per input, then per stage the F64 accumulator, the
+// have flag, the current F64 value and the rounded stage result.
+struct Row {
+  int32_t dtype;
+  uint32_t r, n, stages;
+  uint32_t counter(uint32_t d) const { return r + d; }
+  uint32_t loaded(uint32_t phase, uint32_t k) const { return 2 * r + phase * n + k; }
+  uint32_t stage_base(uint32_t s) const { return 2 * r + (stages + 1) * n + 4 * s; }
+  J up(J e) const { return dtype == UNP_F64 ? e : widen(std::move(e), "F64"); }
+  J down(J e) const { return dtype == UNP_F64 ? e : widen(std::move(e), EK(dtype)); }
+  std::vector<J> counters() const {
+    std::vector<J> c;
+    for (uint32_t d = 0; d < r; ++d) c.push_back(loc(counter(d)));
+    return c;
+  }
+  J for_lead(uint32_t d, std::vector<J> inner) const { return s_for(counter(d), int_(0), loc(d), int_(1), std::move(inner)); }
+  J bind(const J& e, uint32_t phase) const {
+    return map_leaves(e, [&](const J& x, J& out) {
+      if (x.t != J::Obj || x.o.size() != 1) return false;
+      if (x.o[0].first == "Input") {
+        out = loc(loaded(phase, (uint32_t)leaf_index(x)));
+        return true;
+      }
+      if (x.o[0].first == "Reduced") {
+        out = loc(stage_base((uint32_t)leaf_index(x)) + 3);
+        return true;
+      }
+      return false;
+    });
+  }
+  std::vector<J> loads(uint32_t phase) const {
+    std::vector<J> v;
+    for (uint32_t k = 0; k < n; ++k) v.push_back(s_load(loaded(phase, k), p_logical(k, counters())));
+    return v;
+  }
+  // One stage: fold the row into an F64 accumulator, then round the finalised value once.
+  std::vector<J> stage(uint32_t s, const J& pre, int32_t op) const {
+    const uint32_t base = stage_base(s), acc = base, have = base + 1, val = base + 2, red = base + 3;
+    std::vector<J> inner = loads(s);
+    inner.push_back(s_let(val, up(bind(pre, s))));
+    for (auto& st : fold_step(op, acc, have, val, false)) inner.push_back(st);
+    J fin = op == UNP_OP_MEAN ? e_div(loc(acc), widen(loc(r - 1), "F64")) : loc(acc);
+    return {s_let(acc, up(e_const(op == UNP_OP_PROD ? 1.0 : 0.0))), s_let(have, int_(0)), for_lead(r - 1, inner),
+            s_let(red, down(fin))};
+  }
+  J epilogue(const J& epi) const {
+    std::vector<J> inner = loads(stages);
+    inner.push_back(s_store(p_logical(n, counters()), bind(epi, stages)));
+    return for_lead(r - 1, inner);
+  }
+  void signature(std::vector<J>& params, std::vector<J>& locals) const {
+    params.clear();
+    for (uint32_t k = 0; k < n; ++k) params.push_back(param_buffer("in" + std::to_string(k), EK(dtype), "Read", (int)r));
+    params.push_back(param_buffer("out", EK(dtype), "Write", (int)r));
+    for (uint32_t d = 0; d < r; ++d) params.push_back(param_scalar("n" + std::to_string(d), "I32", d));
+    locals.clear();
+    for (uint32_t i = 0; i < 2 * r; ++i) locals.push_back(local_decl("I32"));
+    for (uint32_t i = 0; i < (stages + 1) * n; ++i) locals.push_back(local_decl(EK(dtype)));
+    for (uint32_t s = 0; s < stages; ++s) {
+      locals.push_back(local_decl("F64"));
+      locals.push_back(local_decl("I32"));
+      locals.push_back(local_decl("F64"));
+      locals.push_back(local_decl(EK(dtype)));
+    }
+  }
+};
+
+// check_row_reduce (row_reduce.rs:51-70).
+void check_row_reduce(const RowReduceSpec& sp) {
+  if (sp.dtype != UNP_F32 && sp.dtype != UNP_F64) throw Decline{"UnsupportedForm: a non-float row reduction"};
+  if (sp.ops.empty()) throw Decline{"UnsupportedForm: an empty stage list"};
+  if (sp.ops.size() != sp.pres.size()) throw Decline{"UnsupportedForm: a stage without its pre expression"};
+  check_rank(sp.rank);
+  if (sp.n_inputs < 1) throw Decline{"UnsupportedForm: a row reduction with no input"};
+  for (size_t s = 0; s < sp.ops.size(); ++s) {
+    if (!reduce_op_name(sp.ops[s])) throw Decline{"UnsupportedForm: a reduce op outside Sum, Prod, Max, Min and Mean"};
+    check_post(sp.pres[s], (int64_t)s, sp.n_inputs);
+  }
+  check_post(sp.epilogue, (int64_t)sp.ops.size(), sp.n_inputs);
+}
+
+// The block tree of block_reduce.rs's `Fold` (publish, rounds) over the accumulator `acc`,
+// the have flag `have`, the partner value `val` and the partner's flag `partner_have`.
+std::vector<J> fold_publish(int32_t rop, uint32_t acc, uint32_t have) {
+  std::vector<J> v = {s_store(p_alloc(0, as_i32(thread())), loc(acc))};
+  if (rop == UNP_OP_MAX || rop == UNP_OP_MIN) v.push_back(s_store(p_alloc(1, as_i32(thread())), loc(have)));
+  return v;
+}
+std::vector<J> fold_rounds(int32_t rop, uint32_t block, uint32_t acc, uint32_t have, uint32_t val,
+                           uint32_t partner_have, bool is_int) {
+  const bool flag = rop == UNP_OP_MAX || rop == UNP_OP_MIN;
+  std::vector<J> out;
+  for (uint32_t s = block / 2; s > 0; s /= 2) {
+    const J partner = as_i32(e_add(thread(), uconst(s)));
+    std::vector<J> rb = {s_load(val, p_alloc(0, partner))};
+    const std::vector<J> combine = fold_step(rop, acc, have, val, is_int);
+    if (flag) {
+      rb.push_back(s_load(partner_have, p_alloc(1, partner)));
+      rb.push_back(s_if(loc(partner_have), combine, {}));
+    } else {
+      for (auto& c : combine) rb.push_back(c);
+    }
+    for (auto& p : fold_publish(rop, acc, have)) rb.push_back(p);
+    out.push_back(s_if(e_bin("CmpLt", thread(), uconst(s)), rb, {}));
+    out.push_back(s_barrier());
+  }
+  return out;
+}
+
+// A loop statement with its start and step replaced (row_reduce_launched.rs `strided`,
+// `block_stride_outermost`).
+void restride(J& for_stmt, J start, J step) {
+  J& f = for_stmt.o[0].second;
+  for (auto& kv : f.o) {
+    if (kv.first == "start") kv.second = start;
+    if (kv.first == "step") kv.second = step;
+  }
+}
+
+// lift_row_reduce_opdef (row_reduce.rs:31-49) and lift_row_reduce_opdef_launched
+// (row_reduce_launched.rs:47-86).
+J lift_row_reduce(const std::string& name, const RowReduceSpec& sp, uint32_t block, uint32_t grid) {
+  const bool launched = block || grid;
+  if (launched && (grid == 0 || !pow2(block))) throw Decline{"BadLaunch"};
+  check_row_reduce(sp);
+  const Row w{sp.dtype, (uint32_t)sp.rank, (uint32_t)sp.n_inputs, (uint32_t)sp.ops.size()};
+  std::vector<J> params, locals;
+  w.signature(params, locals);
+  std::vector<J> row;
+  if (!launched) {
+    for (uint32_t s = 0; s < w.stages; ++s)
+      for (auto& st : w.stage(s, sp.pres[s], sp.ops[s])) row.push_back(st);
+    row.push_back(w.epilogue(sp.epilogue));
+    std::vector<J> body = row;
+    for (int d = (int)w.r - 2; d >= 0; --d) body = {w.for_lead((uint32_t)d, body)};
+    return kernel_fn(name, EK(sp.dtype), params, locals, body, J::null(), {});
+  }
+  for (int32_t op : sp.ops)
+    if (op == UNP_OP_PROD)
+      throw Decline{"UnsupportedForm: a Prod stage in a launched row reduction (a float product is not "
+                    "order-independent, and no bound is declared)"};
+  if (w.r < 2) throw Decline{"UnsupportedForm: a launched row reduction needs a leading axis to stride blocks over"};
+  const J tid = as_i32(thread());
+  const J bdim = as_i32(e_exec("BlockDim", 0));
+  const uint32_t partner_have = w.stage_base(w.stages);
+  for (uint32_t s = 0; s < w.stages; ++s) {
+    const uint32_t base = w.stage_base(s);
+    std::vector<J> v = w.stage(s, sp.pres[s], sp.ops[s]);
+    const J rounded = v.back().o[0].second.get("init") ? *v.back().o[0].second.get("init") : J::null();
+    v.pop_back();
+    J fold_loop = v.back();
+    v.pop_back();
+    restride(fold_loop, tid, bdim);
+    v.push_back(fold_loop);
+    for (auto& st : fold_publish(sp.ops[s], base, base + 1)) v.push_back(st);
+    v.push_back(s_barrier());
+    for (auto& st : fold_rounds(sp.ops[s], block, base, base + 1, base + 2, partner_have, false)) v.push_back(st);
+    v.push_back(s_if(e_bin("CmpEq", thread(), uconst(0)), {s_store(p_alloc(2, int_(s)), rounded)}, {}));
+    v.push_back(s_barrier());
+    v.push_back(s_load(base + 3, p_alloc(2, int_(s))));
+    for (auto& st : v) row.push_back(st);
+  }
+  J epi = w.epilogue(sp.epilogue);
+  restride(epi, tid, bdim);
+  row.push_back(epi);
+  std::vector<J> body = row;
+  for (int d = (int)w.r - 2; d >= 0; --d) body = {w.for_lead((uint32_t)d, body)};
+  restride(body[0], as_i32(e_exec("BlockIdx", 0)), as_i32(e_exec("GridDim", 0)));
+  locals.push_back(local_decl("I32"));  // the partner's have flag
+  std::vector<J> allocs = {alloc_shared("partial", "F64", block), alloc_shared("partial_have", "I32", block),
+                           alloc_shared("stage_result", EK(sp.dtype), w.stages)};
+  return kernel_fn(name, EK(sp.dtype), params, locals, body, launch_shape(block, grid), allocs);
+}
+
+// Undo Row::bind: the locals of phase `phase`'s loads back to Input(k), stage results back to
+// Reduced(t).  False when the expression reads any other local.
+bool unbind(const Row& w, const J& e, uint32_t phase, J& out) {
+  bool ok = true;
+  try {
+    out = map_leaves(e, [&](const J& x, J& o) {
+      if (x.t != J::Obj || x.o.size() != 1 || x.o[0].first != "Local") return false;
+      const int64_t l = leaf_index(x);
+      for (uint32_t k = 0; k < w.n; ++k)
+        if (l == (int64_t)w.loaded(phase, k)) {
+          o = var("Input", J::integer(k));
+          return true;
+        }
+      for (uint32_t t = 0; t < w.stages; ++t)
+        if (l == (int64_t)w.stage_base(t) + 3) {
+          o = var("Reduced", J::integer(t));
+          return true;
+        }
+      ok = false;
+      o = x;
+      return true;
+    });
+  } catch (const Decline&) {
+    return false;
+  }
+  return ok;
+}
+
+// Depth-first search of a statement list for the first statement `pick` accepts.
+template <class F> const J* find_stmt(const J& block, const F& pick) {
+  if (block.t != J::Arr) return nullptr;
+  for (const J& st : block.a) {
+    if (pick(st)) return &st;
+    if (st.t != J::Obj || st.o.size() != 1) continue;
+    const J& b = st.o[0].second;
+    for (const char* key : {"then", "els", "body"}) {
+      const J* inner = b.get(key);
+      if (inner) {
+        const J* f = find_stmt(*inner, pick);
+        if (f) return f;
+      }
+    }
+  }
+  return nullptr;
+}
+
 // ---- recognition -------------------------------------------------------------------------
 
 // Fill the serde defaults a writer may omit (KernelFn: launch, allocs, result, results;
@@ -765,9 +1075,96 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
       return UNP_OK;
     }
   }
+  // Access::RowReduce: n inputs (Read, rank r), out (Write, rank r), r I32 extents.  The stage
+  // count follows from the locals; each stage's pre and the epilogue are read back from the
+  // tree (un-binding the loaded and stage-result locals), each stage's fold from its accumulate
+  // step, and the candidate is re-lifted and compared as a whole.
+  for (size_t n = 1; n + 2 <= np; ++n) {
+    const size_t r = np - 1 - n;
+    bool shape = ps[n].buffer && ps[n].role == "Write" && (size_t)ps[n].rank == r &&
+                 (ps[0].elem == UNP_F32 || ps[0].elem == UNP_F64);
+    for (size_t i = 0; shape && i < n; ++i)
+      shape = ps[i].buffer && ps[i].role == "Read" && (size_t)ps[i].rank == r && ps[i].elem == ps[0].elem;
+    for (size_t i = n + 1; shape && i < np; ++i) shape = !ps[i].buffer && ps[i].elem == UNP_I32;
+    if (!shape || r < 1 || r > 8) continue;
+    const J* locs = k.get("locals");
+    if (!locs || locs->t != J::Arr) continue;
+    const int64_t L = (int64_t)locs->a.size() - (block ? 1 : 0) - 2 * (int64_t)r - (int64_t)n;
+    if (L <= 0 || L % (int64_t)(n + 4) != 0) continue;
+    const uint32_t S = (uint32_t)(L / (int64_t)(n + 4));
+    if (S > 8) continue;
+    const Row w{ps[0].elem, (uint32_t)r, (uint32_t)n, S};
+    const J& body = *k.get("body");
+    RowReduceSpec sp;
+    sp.dtype = ps[0].elem;
+    sp.rank = (int32_t)r;
+    sp.n_inputs = (int32_t)n;
+    bool ok = true;
+    std::vector<std::vector<int32_t>> cand;
+    for (uint32_t st = 0; ok && st < S; ++st) {
+      const uint32_t val = w.stage_base(st) + 2, acc = w.stage_base(st);
+      const J* let = find_stmt(body, [&](const J& x) {
+        const J* l = x.get("Let");
+        return l && l->get("local") && l->get("local")->is_int && l->get("local")->i == (int64_t)val;
+      });
+      if (!let) {
+        ok = false;
+        break;
+      }
+      J init = *let->get("Let")->get("init");
+      if (w.dtype != UNP_F64) {
+        const J* c = init.get("Cast");
+        if (!c || c->t != J::Arr || c->a.size() != 2) {
+          ok = false;
+          break;
+        }
+        J operand = c->a[0];  // copied out before `init` (which owns it) is replaced
+        init = std::move(operand);
+      }
+      J pre;
+      if (!unbind(w, init, st, pre)) {
+        ok = false;
+        break;
+      }
+      sp.pres.push_back(pre);
+      const J* asg = find_stmt(body, [&](const J& x) {
+        const J* a = x.get("Assign");
+        return a && a->get("local") && a->get("local")->is_int && a->get("local")->i == (int64_t)acc;
+      });
+      const J* value = asg ? asg->get("Assign")->get("value") : nullptr;
+      if (value && value->get("Add")) cand.push_back({UNP_OP_SUM, UNP_OP_MEAN});
+      else if (value && value->get("Mul")) cand.push_back({UNP_OP_PROD});
+      else cand.push_back({UNP_OP_MAX, UNP_OP_MIN});
+    }
+    const J* store = ok ? find_stmt(body, [&](const J& x) {
+      const J* st = x.get("Store");
+      const J* pl = st ? st->get("place") : nullptr;
+      const J* lg = pl ? pl->get("Logical") : nullptr;
+      return lg && lg->get("buffer") && lg->get("buffer")->is_int && lg->get("buffer")->i == (int64_t)n;
+    })
+                        : nullptr;
+    if (!store || !unbind(w, *store->get("Store")->get("value"), S, sp.epilogue)) continue;
+    // every combination of the candidate folds
+    std::vector<size_t> pick(S, 0);
+    for (;;) {
+      sp.ops.clear();
+      for (uint32_t st = 0; st < S; ++st) sp.ops.push_back(cand[st][pick[st]]);
+      if (attempt([&] { return lift_row_reduce(name, sp, block, grid); })) {
+        out.form.kind = UNP_FORM_ROW_REDUCE;
+        out.form.dtype = sp.dtype;
+        out.form.rank = sp.rank;
+        out.rr = sp;
+        out.lift = block ? "lift_row_reduce_opdef_launched" : "lift_row_reduce_opdef";
+        return UNP_OK;
+      }
+      uint32_t st = 0;
+      while (st < S && ++pick[st] == cand[st].size()) pick[st++] = 0;
+      if (st == S) break;
+    }
+  }
   why = "kernel `" + name +
-        "` is not one of the forms this backend lowers (a lifted reduction, scan or row gather of one input "
-        "with the identity body, the fused row fold, or the int4 dequant)";
+        "` is not one of the forms this backend lowers (a lifted reduction, scan, row reduction or row gather, "
+        "the fused row fold, or the int4 dequant)";
   return UNP_UNSUPPORTED_KERNEL;
 }
 
@@ -833,6 +1230,41 @@ int32_t unp_kernel_row_reduce2(const char* name, int32_t dtype, int32_t op0, int
 int32_t unp_kernel_dequant4(const char* name, int32_t q_kind, int32_t z_kind, int32_t group, uint32_t block,
                             uint32_t grid, char** json, unp_error* err) {
   return unp::lift_call(json, err, [&] { return unp::dequant4(name ? name : "dequant4", q_kind, z_kind, group, block, grid); });
+}
+
+int32_t unp_lift_row_reduce(const char* name, int32_t dtype, int32_t rank, int32_t n_inputs, const char* stages_json,
+                            const char* epilogue_json, uint32_t block, uint32_t grid, char** json, unp_error* err) {
+  using unp::kir::J;
+  unp::RowReduceSpec sp;
+  sp.dtype = dtype;
+  sp.rank = rank;
+  sp.n_inputs = n_inputs;
+  J stages, epi;
+  std::string why;
+  if (!stages_json || !unp::kir::parse(stages_json, stages, why) || stages.t != J::Arr) {
+    unp::set_error(err, UNP_PARSE_ERROR, "stages: a JSON array of ReduceStage {pre, op} expected " + why);
+    return UNP_PARSE_ERROR;
+  }
+  if (!epilogue_json || !unp::kir::parse(epilogue_json, epi, why)) {
+    unp::set_error(err, UNP_PARSE_ERROR, "epilogue: a ScalarExpr expected " + why);
+    return UNP_PARSE_ERROR;
+  }
+  for (const J& st : stages.a) {
+    const J* pre = st.get("pre");
+    const J* op = st.get("op");
+    if (!pre || !op || op->t != J::Str) {
+      unp::set_error(err, UNP_PARSE_ERROR, "a ReduceStage is {\"pre\": ScalarExpr, \"op\": ReduceOp}");
+      return UNP_PARSE_ERROR;
+    }
+    int32_t code = -1;
+    static const char* const names[] = {"Sum", "Prod", "Max", "Min", "Mean"};
+    for (int32_t i = 0; i < 5; ++i)
+      if (op->s == names[i]) code = i;
+    sp.ops.push_back(code);
+    sp.pres.push_back(*pre);
+  }
+  sp.epilogue = epi;
+  return unp::lift_call(json, err, [&] { return unp::lift_row_reduce(name ? name : "row_reduce", sp, block, grid); });
 }
 
 }  // extern "C"

@@ -123,12 +123,24 @@ int32_t unp_hip_lower_kernel(const char* kernel_json, unp_generated** out, unp_e
     return rc;
   }
   auto* g = new unp_generated();
-  rc = unp::lower_form(rec.form, g->l, why);
-  if (rc != UNP_OK) {
-    delete g;
-    // A recognised lift whose form this backend has no kernel for is a refusal of the kernel.
-    set_error(err, UNP_UNSUPPORTED_KERNEL, why);
-    return UNP_UNSUPPORTED_KERNEL;
+  if (rec.form.kind == UNP_FORM_ROW_REDUCE) {
+    // A row reduction whose expressions hold a node this backend cannot spell is an
+    // UnsupportedOp (backend.rs:398-403), its other refusals an UnsupportedKernel.
+    rc = unp::lower_row_reduce(rec.rr, g->l, why);
+    if (rc != UNP_OK) {
+      delete g;
+      if (rc != UNP_UNSUPPORTED_OP && rc != UNP_UNSUPPORTED_DTYPE) rc = UNP_UNSUPPORTED_KERNEL;
+      set_error(err, rc, why);
+      return rc;
+    }
+  } else {
+    rc = unp::lower_form(rec.form, g->l, why);
+    if (rc != UNP_OK) {
+      delete g;
+      // A recognised lift whose form this backend has no kernel for is a refusal of the kernel.
+      set_error(err, UNP_UNSUPPORTED_KERNEL, why);
+      return UNP_UNSUPPORTED_KERNEL;
+    }
   }
   // The interface's core half (KernelInterface::of, kernel_interface.rs:237-262): the kernel's
   // declared launch and parameters, beside the emitter half the form wrote.
@@ -507,6 +519,32 @@ int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_err
   return rc;
 }
 
+int32_t run_row_reduce(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  const unp::RowReduceSpec& sp = x->l.rr;
+  const size_t ni = (size_t)sp.n_inputs, r = (size_t)sp.rank;
+  Args A;
+  int32_t rc = take_args(a, n, ni + 1, r, A, err);
+  if (rc == UNP_OK) rc = extents_i32(A, r, err);
+  if (rc != UNP_OK) return rc;
+  long long rows = product(A.ext, 0, r - 1);
+  long long cols = A.ext[r - 1];
+  if ((rc = need_buffers(A, rows > 0 && cols > 0, err)) != UNP_OK) return rc;
+  if (rows == 0 || cols == 0) return UNP_OK;
+  const int vec = 16 / (int)unp::kind_bytes(sp.dtype);
+  bool aligned = cols % vec == 0;
+  for (uint64_t p : A.buf) aligned = aligned && aligned16(p);
+  // entries: 0 the row in registers, 1 vector passes, 2 scalar passes
+  const size_t entry = !aligned ? 2 : (cols <= 256LL * vec * 8 ? 0 : 1);
+  const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
+  const uint32_t grid = (uint32_t)(rows < cap ? rows : cap);
+  std::vector<void*> params;
+  std::vector<uint64_t> ptrs(A.buf.begin(), A.buf.end());
+  for (size_t i = 0; i < ptrs.size(); ++i) params.push_back(&ptrs[i]);
+  params.push_back(&rows);
+  params.push_back(&cols);
+  return launch(x, entry, grid, params.data(), s, err);
+}
+
 int32_t run_gather(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
   const unp_form& f = x->l.form;
   Args A;
@@ -590,6 +628,8 @@ extern "C" int32_t unp_hip_exec_launch(unp_exec* x, const unp_arg* args, size_t 
       return run_scan(x, args, nargs, s, err);
     case UNP_FORM_GATHER:
       return run_gather(x, args, nargs, s, err);
+    case UNP_FORM_ROW_REDUCE:
+      return run_row_reduce(x, args, nargs, s, err);
     case UNP_FORM_DEQUANT4:
       return run_dequant(x, args, nargs, s, err);
     default:

@@ -39,6 +39,17 @@ constexpr int kScanStatusWords = 32;
 // Reductions over more than kWideRow elements per row use the block-per-row schedule.
 constexpr long long kWideRow = 32768;
 
+// An Access::RowReduce (crates/unpopped/src/ir.rs:2114-2125): the stages' pre expressions and
+// folds, then the full-width epilogue, as ScalarExpr JSON over Input(k) and Reduced(t) leaves.
+struct RowReduceSpec {
+  int32_t dtype = 0;     // F32 or F64: the compute dtype of inputs, stages and output
+  int32_t rank = 0;      // the reduced axis is the innermost; the output has the input's shape
+  int32_t n_inputs = 0;
+  std::vector<int32_t> ops;  // ReduceOp per stage
+  std::vector<kir::J> pres;  // pre expression per stage
+  kir::J epilogue;
+};
+
 // A lowered form: what the executor needs to launch it.
 struct Lowered {
   unp_form form{};
@@ -49,17 +60,21 @@ struct Lowered {
   bool reduce_all = false;  // a reduction with no kept axis
   int threads = 256;
   int blocks_per_cu = 8;
+  RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only
 };
 
 // Emit the HIP source and interface for `f`; on refusal returns a nonzero unp_status and
 // fills `detail`.
 int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail);
+// The same for a recognised Access::RowReduce.
+int32_t lower_row_reduce(const RowReduceSpec& spec, Lowered& out, std::string& detail);
 
 // Backend::lower_kernel's recognizer (lifts.cpp): the form a KernelFn's JSON is, or a refusal.
 // A recognised kernel: the form to lower, the lift it matched, and the kernel's name, declared
 // launch and parameters (the core half of its interface).
 struct Recognized {
   unp_form form{};
+  RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only
   std::string lift;
   kir::J launch;
   kir::J params;

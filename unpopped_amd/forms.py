@@ -120,3 +120,30 @@ def dequant4(q_packed, scales, zeros_packed, rows, cols, group, q_kind="U4", z_k
     ex.launch(dq, ds, dz, do, rows, cols)
     u.synchronize()
     return do.download(np.uint16, rows * cols).reshape(rows, cols)
+
+
+def row_reduce_executor(dtype: str, rank: int, stages, epilogue, n_inputs: int = 1) -> u.Executor:
+    """The launched Access::RowReduce lift of these expressions, lowered, compiled and loaded."""
+    import json
+
+    from . import expr as X
+
+    key = ("row_reduce", dtype, rank, n_inputs, json.dumps([(X.as_json(p), op) for p, op in stages]),
+           json.dumps(X.as_json(epilogue)))
+    if key not in _execs:
+        k = u.lift_row_reduce("row_reduce", dtype, rank, stages, epilogue, n_inputs=n_inputs, launch=CALLER_LAUNCH)
+        _execs[key] = u.Executor(_backend.lower_kernel(k))
+    return _execs[key]
+
+
+def row_reduce(inputs, stages, epilogue) -> np.ndarray:
+    """Run a row reduction over the innermost axis of the inputs (same shape, float32/float64)."""
+    xs = [np.ascontiguousarray(a) for a in inputs]
+    x0 = xs[0]
+    rank = max(x0.ndim, 1)
+    ex = row_reduce_executor(NP_KIND[x0.dtype.type], rank, stages, epilogue, n_inputs=len(xs))
+    dins = [u.DeviceBuffer.from_array(a) for a in xs]
+    dout = u.DeviceBuffer(max(x0.nbytes, 1))
+    ex.launch(*dins, dout, *(x0.shape if x0.ndim else (1,)))
+    u.synchronize()
+    return dout.download(x0.dtype, x0.size).reshape(x0.shape)
