@@ -325,6 +325,19 @@ def test_gather_row_widths(hip_device, D):
     assert np.array_equal(H.gather_rows(t32, ids, "Clamp"), oracle.gather_rows(t32, ids, "Clamp"))
 
 
+@pytest.mark.parametrize("oob", ["Skip", "ZeroFill", "Clamp"])
+def test_gather_many_rows_whole_row_path(hip_device, oob):
+    """More output rows than waves, 8 KiB rows (the predicate-free whole-row path): each wave
+    loads its next row's id ahead, across in-range and out-of-range ids."""
+    H.say(f"[case] gather many rows {oob}")
+    V, D, N = 300, 4096, 5000
+    table = synth.normal_bf16_bits(9, V * D, 0.02).reshape(V, D)
+    ids = rng(18).integers(-40, V + 40, size=N).astype(np.int32)
+    init = np.full((N, D), 0x1234, np.uint16)
+    got = H.gather_rows(table, ids, oob, out_init=init, elem_kind="Bf16")
+    assert np.array_equal(got, oracle.gather_rows(table, ids, oob, out_init=init))
+
+
 def test_gather_empty_source_zero_fills(hip_device):
     H.say("[case] gather empty source")
     table = np.zeros((1, 8), np.uint16)
@@ -339,7 +352,7 @@ def test_gather_empty_source_zero_fills(hip_device):
 # ---------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("rows,cols,group", [(8, 256, 128), (3, 96, 32), (5, 100, 10), (2, 30, 7), (7, 4096, 128), (6, 240, 24), (3, 1000, 8),
-                                             (4, 320, 96), (1, 32, 32)])
+                                             (4, 320, 96), (1, 32, 32), (37, 1152, 64), (1101, 4224, 128)])
 @pytest.mark.parametrize("q_kind,z_kind", [("U4", "U4"), ("I4", "U4"), ("U4", "I4"), ("I4", "I4")])
 def test_dequant_bit_exact(hip_device, rows, cols, group, q_kind, z_kind):
     H.say(f"[case] dequant {q_kind}/{z_kind} {rows}x{cols} g{group}")

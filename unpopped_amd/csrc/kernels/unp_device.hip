@@ -947,6 +947,12 @@ UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows
 // the store (crates/unpopped/src/kernel_lift/gather.rs:184-232): Skip leaves the row,
 // ZeroFill writes zero bytes, Clamp stores the clamped row.  Rows are moved as raw bytes
 // in UNIT-byte pieces; one wave per output row, waves stride over rows.
+//
+// gfx9 counts loads and stores on one in-order counter (vmcnt), so a wait for a load also
+// waits for every store issued before it.  The id of a wave's next row is therefore loaded
+// right after this row's data loads and before its stores: the one wait per row (for the
+// data) covers it, and the next row starts without a dependent round trip.  A row of
+// exactly 64 * U units moves with no per-lane predicate.
 // ---------------------------------------------------------------------------------------
 template <int UNIT> struct unit_type;
 template <> struct unit_type<16> { typedef u32 elem; static constexpr int n = 4; };
@@ -969,12 +975,18 @@ UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ i
   constexpr int WAVES = THREADS / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const i64 units = row_bytes / UNIT;
-  for (i64 r = (i64)blockIdx.x * WAVES + wave; r < n_rows; r += (i64)gridDim.x * WAVES) {
-    const IDX raw = ids[r];
+  const bool whole = units == 64 * U;
+  const i64 rstride = (i64)gridDim.x * WAVES;
+  i64 r = (i64)blockIdx.x * WAVES + wave;
+  IDX next = r < n_rows ? ids[r] : (IDX)0;
+  for (; r < n_rows; r += rstride) {
+    const IDX raw = next;
+    const i64 rn = r + rstride;
     const bool below = below_zero(raw);
     const bool oob = below || !(raw < src_extent);
     E* __restrict__ dst = reinterpret_cast<E*>(out + r * row_bytes);
     if (oob && POLICY != OOB_CLAMP) {
+      if (rn < n_rows) next = ids[rn];
       if constexpr (POLICY == OOB_ZEROFILL) {
         V z;
         __builtin_memset(&z, 0, sizeof(V));
@@ -984,6 +996,16 @@ UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ i
     }
     const IDX cl = below ? (IDX)0 : (oob ? (IDX)(src_extent - (IDX)1) : raw);
     const E* __restrict__ src = reinterpret_cast<const E*>(table + (i64)cl * row_bytes);
+    if (whole) {
+      V v[U];
+#pragma unroll
+      for (int k = 0; k < U; ++k) v[k] = ld_nt<E, N>(src + ((i64)lane + 64 * k) * N);
+      if (rn < n_rows) next = ids[rn];
+#pragma unroll
+      for (int k = 0; k < U; ++k) st_nt<E, N>(dst + ((i64)lane + 64 * k) * N, v[k]);
+      continue;
+    }
+    if (rn < n_rows) next = ids[rn];
     for (i64 u = lane; u < units; u += 64 * U) {
       V v[U];
 #pragma unroll
@@ -1065,45 +1087,64 @@ template <bool QS> UNP_DEV vec<u32, 4> dequant8(u32 w, float s, i32 z) {
 
 // Fast path: cols % G == 0 and G % 8 == 0, so element e's scale and zero point are element
 // e / G of their buffers (row * cols / G + col / G) and an 8-element item never straddles a
-// row or a group.  A wave takes IPL x 64 consecutive items per step: each of its q loads
-// reads 256 contiguous bytes and each of its stores writes 1 KiB contiguous, both streamed
-// past the caches; the next step's q is loaded before the current step is converted.
+// row or a group.  A wave tile is IPL x 64 consecutive items: each q load reads 256
+// contiguous bytes, each store writes 1 KiB contiguous, both streamed past the caches.
+// Every load of the next tile (q, scale, zero point) is issued before this tile's stores,
+// with no per-lane predicate, so the one wait per tile (the counter is in order: loads
+// issued before a store do not wait for it) finds the data there.  The tail (fewer than
+// IPL x 64 items) is one item per thread.
 template <bool QS, bool ZS, int G, int THREADS, int IPL>
 UNP_DEV void dequant4_bf16(const u8* __restrict__ q, const u16* __restrict__ sc, const u8* __restrict__ zp,
                            u16* __restrict__ out, i64 rows, i64 cols) {
   const i64 items = rows * cols / 8;
   const int lane = threadIdx.x & 63;
-  const i64 nwaves = (i64)gridDim.x * (THREADS / 64);
+  constexpr int WAVES = THREADS / 64;
+  const i64 nwaves = (i64)gridDim.x * WAVES;
   const u32* __restrict__ q32 = reinterpret_cast<const u32*>(q);
   constexpr i64 PER = (i64)64 * IPL;
-  i64 base = ((i64)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6)) * PER;
-  u32 wn[IPL];
+  const i64 full = items / PER;
+  u32 w[IPL];
+  u16 s16[IPL];
+  u8 zb[IPL];
+  auto fetch = [&](i64 tile) {
+    const i64 b = tile * PER + lane;
 #pragma unroll
-  for (int k = 0; k < IPL; ++k) {
-    const i64 it = base + 64 * k + lane;
-    wn[k] = it < items ? __builtin_nontemporal_load(q32 + it) : 0u;
+    for (int k = 0; k < IPL; ++k) w[k] = __builtin_nontemporal_load(q32 + b + 64 * k);
+#pragma unroll
+    for (int k = 0; k < IPL; ++k) {
+      const i64 zi = ((b + 64 * k) * 8) / G;
+      s16[k] = sc[zi];
+      zb[k] = zp[zi >> 1];
+    }
+  };
+  i64 t = (i64)blockIdx.x * WAVES + (threadIdx.x >> 6);
+  if (t < full) fetch(t);
+  for (; t < full; t += nwaves) {
+    u32 cw[IPL];
+    u16 cs[IPL];
+    u8 cz[IPL];
+#pragma unroll
+    for (int k = 0; k < IPL; ++k) {
+      cw[k] = w[k];
+      cs[k] = s16[k];
+      cz[k] = zb[k];
+    }
+    if (t + nwaves < full) fetch(t + nwaves);
+    const i64 b = t * PER + lane;
+#pragma unroll
+    for (int k = 0; k < IPL; ++k) {
+      const i64 it = b + 64 * k;
+      const i64 zi = (it * 8) / G;
+      const u32 zz = cz[k];
+      const i32 z = nibble_value<ZS>((zi & 1) ? (zz >> 4) : (zz & 15u));
+      st_nt<u32, 4>(reinterpret_cast<u32*>(out + it * 8), dequant8<QS>(cw[k], f16_to_f32(cs[k]), z));
+    }
   }
-  for (; base < items; base += nwaves * PER) {
-    u32 w[IPL];
-#pragma unroll
-    for (int k = 0; k < IPL; ++k) w[k] = wn[k];
-    const i64 nb = base + nwaves * PER;
-#pragma unroll
-    for (int k = 0; k < IPL; ++k) {
-      const i64 it = nb + 64 * k + lane;
-      if (it < items) wn[k] = __builtin_nontemporal_load(q32 + it);
-    }
-#pragma unroll
-    for (int k = 0; k < IPL; ++k) {
-      const i64 it = base + 64 * k + lane;
-      if (it < items) {
-        const i64 zi = (it * 8) / G;
-        const float s = f16_to_f32(sc[zi]);
-        const u32 zb = zp[zi >> 1];
-        const i32 z = nibble_value<ZS>((zi & 1) ? (zb >> 4) : (zb & 15u));
-        st_nt<u32, 4>(reinterpret_cast<u32*>(out + it * 8), dequant8<QS>(w[k], s, z));
-      }
-    }
+  for (i64 it = full * PER + (i64)blockIdx.x * THREADS + threadIdx.x; it < items; it += (i64)gridDim.x * THREADS) {
+    const i64 zi = (it * 8) / G;
+    const u32 zz = zp[zi >> 1];
+    const i32 z = nibble_value<ZS>((zi & 1) ? (zz >> 4) : (zz & 15u));
+    st_nt<u32, 4>(reinterpret_cast<u32*>(out + it * 8), dequant8<QS>(q32[it], f16_to_f32(sc[zi]), z));
   }
 }
 
