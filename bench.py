@@ -110,6 +110,58 @@ def build_cases(u, synth):
     return cases
 
 
+def build_extras(u, synth):
+    """The next row of the hot path, Access::RowReduce (kernel_lift/row_reduce_launched.rs:47-86),
+    on the cfg2 input: softmax and RMS norm of an f32 8192 x 4096 matrix, the row read once and
+    the full-width epilogue written once.  Timed apart from the suite: not part of `value`."""
+    from unpopped_amd import expr as X
+    from unpopped_amd import forms as H
+
+    extras = []
+
+    def row_reduce(which):
+        def setup():
+            R, Cc = 8192, 4096
+            x = synth.normal_f32(1, R * Cc)
+            stages, epi = getattr(X, which)()
+            ex = H.row_reduce_executor("F32", 2, stages, epi)
+            din, dout = u.DeviceBuffer.from_array(x), u.DeviceBuffer(R * Cc * 4)
+            return lambda: ex.launch(din, dout, R, Cc), ex
+        return setup
+    rr_bytes = 2 * 8192 * 4096 * 4
+    extras.append(Case("rr_softmax", "f32 8192x4096 RowReduce softmax (Max, Sum of exp, divide)", rr_bytes,
+                       8192 * 4096, row_reduce("softmax")))
+    extras.append(Case("rr_rmsnorm", "f32 8192x4096 RowReduce RMS norm (Mean of squares, scale)", rr_bytes,
+                       8192 * 4096, row_reduce("rms_norm")))
+    return extras
+
+
+def time_cases(u, cases, steps):
+    """Average HIP-event time of each case's launch over `steps` rounds (one launch per case per
+    round, on the launch stream)."""
+    events = [[u.Event() for _ in range(len(cases) + 1)] for _ in range(steps)]
+    u.synchronize()
+    for s in range(steps):
+        ev = events[s]
+        ev[0].record()
+        for i, c in enumerate(cases):
+            c.launch()
+            ev[i + 1].record()
+    u.synchronize()
+    per = []
+    for i, c in enumerate(cases):
+        ms = sum(events[s][i].elapsed_ms(events[s][i + 1]) for s in range(steps)) / steps
+        gbps = c.nbytes / (ms * 1e-3) / 1e9
+        per.append({
+            "name": c.name, "what": c.what, "entry": c.exec.last_launch()["entry"],
+            "grid": c.exec.last_launch()["grid"][0], "bytes": c.nbytes, "us": round(ms * 1e3, 2),
+            "GBps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_GBPS, 4),
+            "elements_per_s": round(c.elements / (ms * 1e-3), 1),
+        })
+        log(f"[bench] {c.name}: {ms * 1e3:.1f} us, {gbps:.0f} GB/s ({100 * gbps / PEAK_GBPS:.1f}% of peak)")
+    return per
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -291,6 +343,19 @@ def ceilings(u, cus: int, nbytes: int = 1 << 30, reps: int = 10) -> None:
                           "GBps": round(best[0], 1), "frac_of_peak": round(best[0] / PEAK_GBPS, 4)}), flush=True)
 
 
+def attach_traffic(per) -> None:
+    """HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE passes (each counter scaled
+    by what it reads for a plain copy of known size), where a profile covers the kernel."""
+    tf = ROOT / "profiles" / "traffic.json"
+    if not tf.exists():
+        return
+    known = json.loads(tf.read_text()).get("cases", {})
+    for p in per:
+        t = known.get(p["name"])
+        if t and t.get("kernel") == p["entry"]:
+            p["traffic"] = t["traffic_bytes"]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -298,6 +363,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", default="", help="comma-separated case names (default: the whole suite)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the RowReduce lines timed after the suite (not part of `value`)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only launch a plain 256 MiB copy (calibrates the HBM byte counters)")
     ap.add_argument("--ceilings", action="store_true",
@@ -334,30 +401,11 @@ def main() -> int:
             c.launch()
     u.synchronize()
 
-    events = [[u.Event() for _ in range(len(cases) + 1)] for _ in range(args.steps)]
     log(f"[bench] timing {args.steps} steps")
     u.synchronize()
     t0 = time.perf_counter()
-    for s in range(args.steps):
-        ev = events[s]
-        ev[0].record()
-        for i, c in enumerate(cases):
-            c.launch()
-            ev[i + 1].record()
-    u.synchronize()
+    per = time_cases(u, cases, args.steps)
     wall = time.perf_counter() - t0
-
-    per = []
-    for i, c in enumerate(cases):
-        ms = sum(events[s][i].elapsed_ms(events[s][i + 1]) for s in range(args.steps)) / args.steps
-        gbps = c.nbytes / (ms * 1e-3) / 1e9
-        per.append({
-            "name": c.name, "what": c.what, "entry": c.exec.last_launch()["entry"],
-            "grid": c.exec.last_launch()["grid"][0], "bytes": c.nbytes, "us": round(ms * 1e3, 2),
-            "GBps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_GBPS, 4),
-            "elements_per_s": round(c.elements / (ms * 1e-3), 1),
-        })
-        log(f"[bench] {c.name}: {ms * 1e3:.1f} us, {gbps:.0f} GB/s ({100 * gbps / PEAK_GBPS:.1f}% of peak)")
     total_bytes = sum(c.nbytes for c in cases)
     ms_step = sum(p["us"] for p in per) / 1e3
     value = total_bytes / (ms_step * 1e-3) / 1e9
@@ -365,15 +413,20 @@ def main() -> int:
 
     # HBM bytes per launch from the committed FETCH_SIZE/WRITE_SIZE passes (each scaled by what
     # the counter reads for a plain copy of known size); null when no profile covers the kernel.
-    traffic = None
-    tf = ROOT / "profiles" / "traffic.json"
-    if tf.exists():
-        known = json.loads(tf.read_text()).get("cases", {})
-        for p in per:
-            t = known.get(p["name"])
-            if t and t.get("kernel") == p["entry"]:
-                p["traffic"] = t["traffic_bytes"]
-        traffic = dom.get("traffic")
+    attach_traffic(per)
+    traffic = dom.get("traffic")
+
+    extra = None
+    if not args.no_extras and not args.only:
+        xs = build_extras(u, synth)
+        for c in xs:
+            log(f"[bench] setup {c.name}: {c.what}")
+            c.launch, c.exec = c.setup()
+            for _ in range(args.warmup):
+                c.launch()
+        log(f"[bench] timing {args.steps} steps of the RowReduce lines")
+        extra = time_cases(u, xs, args.steps)
+        attach_traffic(extra)
 
     cpu = None
     if not args.no_cpu:
@@ -410,6 +463,7 @@ def main() -> int:
             "traffic": traffic,
         },
         "cpu_baseline": cpu,
+        "extra_kernels": extra,
     }
     print(json.dumps(line), flush=True)
     return 0

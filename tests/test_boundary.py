@@ -291,7 +291,13 @@ def test_row_reduce_lifts_round_trip(which, dtype, launch):
     assert g.interface["lift"] == ("lift_row_reduce_opdef_launched" if launch else "lift_row_reduce_opdef")
     assert [s["op"] for s in g.interface["stages"]] == [op for _, op in stages]
     assert g.name.startswith(f"unp_row_reduce_{dtype.lower()}_s{len(stages)}_")
-    assert [e["symbol"][-2:] for e in g.interface["entries"]] == ["_c", "_v", "_s"]
+    assert [e["symbol"].rsplit("_", 1)[1] for e in g.interface["entries"]] == ["c4", "c", "v", "s"]
+    # softmax's exp(x - max) is the Sum stage's pre value and recurs in the epilogue: the
+    # register-resident entries keep it instead of evaluating exp twice.  Cheap or absent
+    # subexpressions are not held.
+    assert g.interface["epilogue_reuses_stage"] == (1 if which == "softmax" else -1)
+    if which == "softmax":
+        assert "epi_c" in g.source and "c / r[1]" in g.source.replace("(", "").replace(")", "")
 
 
 def test_row_reduce_launched_shape():

@@ -514,15 +514,23 @@ namespace {
 // A ScalarExpr over Input(k) / Reduced(t) leaves as a C++ double expression (f64 evaluation,
 // the caller rounds once).  False, with the node named in `why`, outside the vocabulary this
 // backend spells.
-bool expr_cpp(const kir::J& e, const char* T, std::string& out, std::string& why) {
+// `reuse`, when set, is a subtree whose value the caller already holds: every node equal to it
+// is spelled `c` instead.
+bool expr_cpp(const kir::J& e, const char* T, std::string& out, std::string& why, const kir::J* reuse = nullptr) {
   using kir::J;
+  if (reuse && e == *reuse) {
+    out = "c";
+    return true;
+  }
   if (e.t != J::Obj || e.o.size() != 1) {
     why = "a malformed ScalarExpr";
     return false;
   }
   const std::string& tag = e.o[0].first;
   const J& p = e.o[0].second;
-  auto sub = [&](size_t i, std::string& o) { return p.t == J::Arr && i < p.a.size() && expr_cpp(p.a[i], T, o, why); };
+  auto sub = [&](size_t i, std::string& o) {
+    return p.t == J::Arr && i < p.a.size() && expr_cpp(p.a[i], T, o, why, reuse);
+  };
   if (tag == "Input" || tag == "Reduced") {
     if (!p.is_int || p.i < 0) {
       why = "a malformed leaf";
@@ -633,6 +641,44 @@ bool expr_cpp(const kir::J& e, const char* T, std::string& out, std::string& why
   return false;
 }
 
+// True when evaluating `e` costs a library call or a division in f64: the per-element value
+// is then worth holding in registers between a stage and the epilogue.
+bool costly(const kir::J& e) {
+  using kir::J;
+  if (e.t != J::Obj || e.o.size() != 1) return false;
+  const std::string& tag = e.o[0].first;
+  const J& p = e.o[0].second;
+  if (tag == "Unary" && p.t == J::Arr && !p.a.empty() && p.a[0].t == J::Str) {
+    static const char* const cheap[] = {"Neg", "Abs", "Sqr", "Relu", "Floor", "Ceil", "Round", "Trunc", "Sign", "Step"};
+    bool is_cheap = false;
+    for (const char* c : cheap) is_cheap = is_cheap || p.a[0].s == c;
+    if (!is_cheap) return true;
+  }
+  if (tag == "Binary" && p.t == J::Arr && !p.a.empty() && p.a[0].t == J::Str) {
+    static const char* const dear[] = {"Pow", "Atan2", "Rem", "RemTrunc"};
+    for (const char* c : dear)
+      if (p.a[0].s == c) return true;
+  }
+  if (tag == "Div") return true;
+  if (p.t == J::Arr)
+    for (const J& x : p.a)
+      if (costly(x)) return true;
+  return false;
+}
+
+// True when `sub` occurs in `e` as a subtree.
+bool contains(const kir::J& e, const kir::J& sub) {
+  using kir::J;
+  if (e == sub) return true;
+  if (e.t == J::Obj)
+    for (const auto& kv : e.o)
+      if (contains(kv.second, sub)) return true;
+  if (e.t == J::Arr)
+    for (const J& x : e.a)
+      if (contains(x, sub)) return true;
+  return false;
+}
+
 }  // namespace
 
 int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) {
@@ -667,6 +713,21 @@ int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) 
     why = "epilogue: " + why + " has no spelling here";
     return UNP_UNSUPPORTED_OP;
   }
+  // A stage whose pre expression is costly and recurs in the epilogue (softmax's exp(x - max)):
+  // the register-resident entries keep its per-element f64 value from the stage and the
+  // epilogue reads it back.  It is the same f64 expression of the same operands, so the result
+  // is unchanged; only the second evaluation is saved.
+  int cached = -1;
+  std::string epi_c = epi;
+  for (size_t st = 0; st < NS && cached < 0; ++st)
+    if (costly(sp.pres[st]) && contains(sp.epilogue, sp.pres[st])) {
+      std::string w2;
+      if (!expr_cpp(sp.epilogue, T, epi_c, w2, &sp.pres[st])) {
+        why = "epilogue: " + w2 + " has no spelling here";
+        return UNP_UNSUPPORTED_OP;
+      }
+      cached = (int)st;
+    }
   // The name carries a hash of the expressions: different row reductions never share a symbol.
   std::string key = std::string(T) + "|" + std::to_string(sp.n_inputs);
   for (size_t st = 0; st < NS; ++st) key += "|" + std::to_string(sp.ops[st]) + ":" + pre[st];
@@ -681,9 +742,12 @@ int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) 
   src << header(L.name, f);
   src << "struct " << ops << " {\n  static constexpr int op[" << NS << "] = {";
   for (size_t st = 0; st < NS; ++st) src << (st ? ", " : "") << sp.ops[st];
-  src << "};\n  template <int S> static __device__ __forceinline__ double pre(const double* x, const double* r);\n"
+  src << "};\n  static constexpr int cached = " << cached << ";\n"
+      << "  template <int S> static __device__ __forceinline__ double pre(const double* x, const double* r);\n"
       << "  static __device__ __forceinline__ double epi(const double* x, const double* r) { (void)x; (void)r; return "
-      << epi << "; }\n};\n";
+      << epi << "; }\n"
+      << "  static __device__ __forceinline__ double epi_c(const double* x, const double* r, double c) { (void)x; (void)r; "
+      << "(void)c; return " << epi_c << "; }\n};\n";
   for (size_t st = 0; st < NS; ++st)
     src << "template <> __device__ __forceinline__ double " << ops << "::pre<" << st
         << ">(const double* x, const double* r) { (void)x; (void)r; return " << pre[st] << "; }\n";
@@ -692,7 +756,7 @@ int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) 
     const char* suffix;
     int vec, r;
     bool fast;
-  } es[] = {{"_c", vec, 8, true}, {"_v", vec, 0, true}, {"_s", 1, 0, false}};
+  } es[] = {{"_c4", vec, 4, true}, {"_c", vec, 8, true}, {"_v", vec, 0, true}, {"_s", 1, 0, false}};
   for (const E& e : es) {
     Entry en;
     en.symbol = L.name + e.suffix;
@@ -716,7 +780,7 @@ int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) 
   static const char* const opn[] = {"Sum", "Prod", "Max", "Min", "Mean"};
   for (size_t st = 0; st < NS; ++st)
     j << (st ? "," : "") << "{\"op\":\"" << opn[sp.ops[st]] << "\",\"pre\":" << json_str(pre[st]) << "}";
-  j << "],\"epilogue\":" << json_str(epi) << ",\"params\":[";
+  j << "],\"epilogue\":" << json_str(epi) << ",\"epilogue_reuses_stage\":" << cached << ",\"params\":[";
   for (int k = 0; k < sp.n_inputs; ++k) j << "{\"name\":\"in" << k << "\",\"kind\":\"buffer\",\"role\":\"Read\"},";
   j << "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
   for (int d = 0; d < sp.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
@@ -725,8 +789,9 @@ int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) 
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
       << ",\"row_in_registers\":" << (L.entries[i].k ? "true" : "false") << ",\"when\":\""
-      << (L.entries[i].k ? "cols % vec == 0, every buffer 16-byte aligned and cols <= 256 * vec * 8"
-                         : (L.entries[i].fast ? "cols % vec == 0 and every buffer 16-byte aligned" : "otherwise"))
+      << (L.entries[i].k == 4 ? "cols % vec == 0, every buffer 16-byte aligned and cols <= 256 * vec * 4"
+          : L.entries[i].k     ? "cols % vec == 0, every buffer 16-byte aligned and 256 * vec * 4 < cols <= 256 * vec * 8"
+                               : (L.entries[i].fast ? "cols % vec == 0 and every buffer 16-byte aligned" : "otherwise"))
       << "\"}";
   j << "],\"workspace\":null"
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"

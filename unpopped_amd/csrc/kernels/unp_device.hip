@@ -1183,7 +1183,10 @@ UNP_DEV void dequant4_bf16_any(const u8* __restrict__ q, const u16* __restrict__
 //
 // One block per row (rows block-strided).  R > 0: the row is read once into registers
 // (R vectors of VEC per thread and input, cols <= THREADS * VEC * R); R == 0: each pass reads
-// the row again (the later passes hit in L2).  Inside a pass thread t folds its positions in
+// the row again (the later passes hit in L2).  OPS::cached names a stage whose pre value
+// recurs in the epilogue (softmax's exp(x - max)): with the row in registers its f64 value per
+// element is kept from the stage and OPS::epi_c reads it back in place of a second
+// evaluation, which is the same f64 expression of the same operands.  Inside a pass thread t folds its positions in
 // ascending order; waves combine by DPP, then in wave order, so the order is fixed by the
 // geometry.
 // ---------------------------------------------------------------------------------------
@@ -1214,7 +1217,7 @@ UNP_DEV double select(double c, double a, double b) { return c != 0.0 ? a : b; }
 
 template <class T, int NI, int NS, class OPS, int THREADS, int VEC, int R, int S>
 UNP_DEV void rr_stage(const T* const* rin, const vec<T, VEC> (&xr)[NI][R > 0 ? R : 1], i64 cols, double (&red)[NS],
-                      double* part, double* redsh) {
+                      double* part, double* redsh, double (&cv)[R > 0 ? R : 1][VEC]) {
   if constexpr (S < NS) {
     constexpr int OP = OPS::op[S];
     typedef fold<double, OP> F;
@@ -1231,7 +1234,23 @@ UNP_DEV void rr_stage(const T* const* rin, const vec<T, VEC> (&xr)[NI][R > 0 ? R
         acc = F::apply(acc, (double)(T)OPS::template pre<S>(x, red));
       }
     };
-    if constexpr (R > 0) {
+    if constexpr (R > 0 && S == OPS::cached) {
+      // This stage's per-element value recurs in the epilogue: keep it (in f64, before the
+      // stage's rounding to T) for the epilogue to read back.
+#pragma unroll
+      for (int q = 0; q < R; ++q)
+        if ((i64)q * THREADS + tid < nvec) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            double x[NI];
+#pragma unroll
+            for (int k = 0; k < NI; ++k) x[k] = (double)xr[k][q].e[e];
+            const double p = OPS::template pre<S>(x, red);
+            cv[q][e] = p;
+            acc = F::apply(acc, (double)(T)p);
+          }
+        }
+    } else if constexpr (R > 0) {
 #pragma unroll
       for (int q = 0; q < R; ++q)
         if ((i64)q * THREADS + tid < nvec) {
@@ -1262,7 +1281,7 @@ UNP_DEV void rr_stage(const T* const* rin, const vec<T, VEC> (&xr)[NI][R > 0 ? R
     }
     __syncthreads();
     red[S] = redsh[S];
-    rr_stage<T, NI, NS, OPS, THREADS, VEC, R, S + 1>(rin, xr, cols, red, part, redsh);
+    rr_stage<T, NI, NS, OPS, THREADS, VEC, R, S + 1>(rin, xr, cols, red, part, redsh, cv);
   }
 }
 
@@ -1288,7 +1307,8 @@ UNP_DEV void row_reduce_staged(const T* const* in, T* __restrict__ out, i64 rows
       }
     }
     double red[NS];
-    rr_stage<T, NI, NS, OPS, THREADS, VEC, R, 0>(rin, xr, cols, red, part, redsh);
+    double cv[R > 0 ? R : 1][VEC];
+    rr_stage<T, NI, NS, OPS, THREADS, VEC, R, 0>(rin, xr, cols, red, part, redsh, cv);
     auto emit = [&](const vec<T, VEC> (&v)[NI], i64 at) {
       vec<T, VEC> o;
 #pragma unroll
@@ -1300,7 +1320,23 @@ UNP_DEV void row_reduce_staged(const T* const* in, T* __restrict__ out, i64 rows
       }
       st_nt<T, VEC>(rout + at * VEC, o);
     };
-    if constexpr (R > 0) {
+    if constexpr (R > 0 && OPS::cached >= 0) {
+#pragma unroll
+      for (int q = 0; q < R; ++q) {
+        const i64 v = (i64)q * THREADS + tid;
+        if (v < nvec) {
+          vec<T, VEC> o;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            double x[NI];
+#pragma unroll
+            for (int k = 0; k < NI; ++k) x[k] = (double)xr[k][q].e[e];
+            o.e[e] = (T)OPS::epi_c(x, red, cv[q][e]);
+          }
+          st_nt<T, VEC>(rout + v * VEC, o);
+        }
+      }
+    } else if constexpr (R > 0) {
 #pragma unroll
       for (int q = 0; q < R; ++q) {
         const i64 v = (i64)q * THREADS + tid;

@@ -533,8 +533,9 @@ int32_t run_row_reduce(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, u
   const int vec = 16 / (int)unp::kind_bytes(sp.dtype);
   bool aligned = cols % vec == 0;
   for (uint64_t p : A.buf) aligned = aligned && aligned16(p);
-  // entries: 0 the row in registers, 1 vector passes, 2 scalar passes
-  const size_t entry = !aligned ? 2 : (cols <= 256LL * vec * 8 ? 0 : 1);
+  // entries: 0 the row in registers (4 vectors per thread), 1 in registers (8 vectors per
+  // thread), 2 vector passes, 3 scalar passes
+  const size_t entry = !aligned ? 3 : (cols <= 256LL * vec * 4 ? 0 : (cols <= 256LL * vec * 8 ? 1 : 2));
   const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
   const uint32_t grid = (uint32_t)(rows < cap ? rows : cap);
   std::vector<void*> params;
