@@ -111,9 +111,11 @@ def build_cases(u, synth):
 
 
 def build_extras(u, synth):
-    """The next row of the hot path, Access::RowReduce (kernel_lift/row_reduce_launched.rs:47-86),
-    on the cfg2 input: softmax and RMS norm of an f32 8192 x 4096 matrix, the row read once and
-    the full-width epilogue written once.  Timed apart from the suite: not part of `value`."""
+    """The next rows of the hot path on the cfg2 input (an f32 8192 x 4096 matrix): the reduction
+    over an outer axis (column sums; ReductionShape::new, kernel_lift.rs:854-870), and
+    Access::RowReduce (kernel_lift/row_reduce_launched.rs:47-86) softmax and RMS norm, the row
+    read once and the full-width epilogue written once.  Timed apart from the suite: not part of
+    `value`."""
     from unpopped_amd import expr as X
     from unpopped_amd import forms as H
 
@@ -128,6 +130,23 @@ def build_extras(u, synth):
             din, dout = u.DeviceBuffer.from_array(x), u.DeviceBuffer(R * Cc * 4)
             return lambda: ex.launch(din, dout, R, Cc), ex
         return setup
+    def colsum():
+        R, Cc = 8192, 4096
+        x = synth.normal_f32(1, R * Cc)
+        ex = H.executor(kind="reduction", dtype="F32", rank=2, op="Sum", axes=(0,))
+        din, dout = u.DeviceBuffer.from_array(x), u.DeviceBuffer(Cc * 4)
+        return lambda: ex.launch(din, dout, R, Cc), ex
+    extras.append(Case("rd_colsum", "f32 8192x4096 Sum over axis 0 (column sums, the outer-axis reduction)",
+                       8192 * 4096 * 4 + 4096 * 4, 8192 * 4096, colsum))
+
+    def full_sum():
+        n = 1 << 24
+        x = synth.uniform_pm1_f32(0, n)
+        ex = H.executor(kind="reduction", dtype="F32", rank=1, op="Sum", reduced_from=0)
+        din, dout = u.DeviceBuffer.from_array(x), u.DeviceBuffer(4)
+        return lambda: ex.launch(din, dout, n), ex
+    extras.append(Case("rd_all", "f32 2^24 full Sum (cfg1's data on the GPU; cfg1 itself is the CPU case)",
+                       (1 << 24) * 4 + 4, 1 << 24, full_sum))
     rr_bytes = 2 * 8192 * 4096 * 4
     extras.append(Case("rr_softmax", "f32 8192x4096 RowReduce softmax (Max, Sum of exp, divide)", rr_bytes,
                        8192 * 4096, row_reduce("softmax")))
@@ -364,7 +383,7 @@ def main() -> int:
     ap.add_argument("--only", default="", help="comma-separated case names (default: the whole suite)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument("--no-extras", action="store_true",
-                    help="skip the RowReduce lines timed after the suite (not part of `value`)")
+                    help="skip the column-sum and RowReduce lines timed after the suite (not part of `value`)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only launch a plain 256 MiB copy (calibrates the HBM byte counters)")
     ap.add_argument("--ceilings", action="store_true",
@@ -424,7 +443,7 @@ def main() -> int:
             c.launch, c.exec = c.setup()
             for _ in range(args.warmup):
                 c.launch()
-        log(f"[bench] timing {args.steps} steps of the RowReduce lines")
+        log(f"[bench] timing {args.steps} steps of the extra lines")
         extra = time_cases(u, xs, args.steps)
         attach_traffic(extra)
 

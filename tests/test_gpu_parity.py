@@ -383,6 +383,76 @@ def test_dequant_special_scales(hip_device):
 
 
 # ---------------------------------------------------------------------------------------
+# Reductions over any axis set (ReductionShape::new, kernel_lift.rs:854-870): an outer axis
+# (column sums), a middle run, several runs.  The oracle folds rows of the input with the
+# reduced axes moved last, which keeps the serial lift's row-major order over the reduced
+# coordinates.
+# ---------------------------------------------------------------------------------------
+
+def oracle_axes(x: np.ndarray, axes: tuple, op: str):
+    kept = [d for d in range(x.ndim) if d not in axes]
+    xt = np.ascontiguousarray(np.transpose(x, kept + list(axes)))
+    rows = int(np.prod([x.shape[d] for d in kept], dtype=np.int64))
+    cols = int(np.prod([x.shape[d] for d in axes], dtype=np.int64))
+    x2d = xt.reshape(rows, cols)
+    return x2d, oracle.reduce_rows(x2d, op)
+
+
+AXES_CASES = [((64, 300), (0,)), ((4096, 1024), (0,)), ((1000, 37), (0,)), ((3, 257, 129), (1,)),
+              ((8, 2048, 512), (1,)), ((5, 37, 64), (0, 1)), ((4, 33, 7), (0, 2)), ((2, 3, 4, 5), (1, 2)),
+              ((3, 4, 5, 6), (0, 3)), ((2, 3, 4, 5, 6), (0, 2, 4)), ((7, 1, 9), (1,)), ((0, 5), (0,)), ((5, 0, 3), (1,))]
+
+
+@pytest.mark.parametrize("shape,axes", AXES_CASES)
+@pytest.mark.parametrize("dtype", [np.float32, np.float64, np.int32, np.int64])
+@pytest.mark.parametrize("op", ["Sum", "Max", "Min", "Mean", "Prod"])
+def test_reduce_any_axes(hip_device, shape, axes, dtype, op):
+    if op == "Mean" and dtype in (np.int32, np.int64):
+        pytest.skip("an integer Mean has no lift (check_accumulated_dtype, kernel_lift.rs:763)")
+    if op == "Prod" and dtype in (np.float32, np.float64):
+        pytest.skip("a float Prod is refused (not order-independent, no declared bound)")
+    H.say(f"[case] reduce axes {axes} of {shape} {np.dtype(dtype).name} {op}")
+    r = rng(40)
+    if dtype in (np.int32, np.int64):
+        info = np.iinfo(dtype)
+        x = r.integers(info.min, info.max, size=shape, dtype=dtype, endpoint=True)
+    else:
+        x = r.normal(size=shape).astype(dtype)
+    got = H.reduce_axes(x, axes, op)
+    x2d, want = oracle_axes(x, axes, op)
+    want = want.reshape(got.shape)
+    if op in ("Sum", "Mean") and dtype in (np.float32, np.float64) and x2d.shape[1] > 0:
+        assert_sum_within_bound(x2d, got.ravel(), mean=(op == "Mean"))
+    else:
+        assert np.array_equal(got, want, equal_nan=True)
+
+
+@pytest.mark.parametrize("shape,axes", [((4096, 1024), (0,)), ((8, 2048, 512), (1,)), ((4, 33, 7), (0, 2))])
+def test_reduce_any_axes_dyadic_sum_is_bit_exact_and_repeats(hip_device, shape, axes):
+    """Dyadic data: every f64 partial is exact, so any order gives RN32(exact sum); two
+    launches in a row (the split schedule's ticket counters are left at zero) agree bit for bit."""
+    H.say(f"[case] reduce axes dyadic {axes} of {shape}")
+    x = dyadic(41, shape, np.float32)
+    a = H.reduce_axes(x, axes, "Sum")
+    b = H.reduce_axes(x, axes, "Sum")
+    _, want = oracle_axes(x, axes, "Sum")
+    assert np.array_equal(a.ravel(), want.ravel())
+    assert np.array_equal(a, b)
+
+
+def test_reduce_any_axes_keepdim_and_nan(hip_device):
+    H.say("[case] reduce axes keepdim, NaN column")
+    x = rng(42).normal(size=(300, 3, 70)).astype(np.float32)
+    x[17, 1, 5] = np.nan
+    x[4, 2, 9] = np.inf
+    got = H.reduce_axes(x, (0,), "Max", keepdim=True)
+    assert got.shape == (1, 3, 70)
+    _, want = oracle_axes(x, (0,), "Max")
+    assert np.array_equal(got.ravel(), want.ravel(), equal_nan=True)
+    assert np.isnan(got[0, 1, 5]) and got[0, 2, 9] == np.inf
+
+
+# ---------------------------------------------------------------------------------------
 # Fused row reductions: the launched Access::RowReduce lift (softmax, RMS norm, ...)
 #
 # Bars: Max/Min stages bit-exact (kernel_parallel_row_reduce_agrees.rs:255-268); identity Sum/Mean

@@ -74,7 +74,7 @@ class HipBackend:
                    op1: str = "Max", reduced_from: int | None = None, exclusive: bool = False,
                    reverse: bool = False, index_dtype: str = "I32", oob: str = "ZeroFill",
                    data_slot: int = 0, q_kind: str = "U4", z_kind: str = "U4", group: int = 128,
-                   out_kind: str = "Bf16") -> GeneratedKernel:
+                   out_kind: str = "Bf16", axes: tuple | None = None) -> GeneratedKernel:
         f = _lib.Form()
         f.kind = FORMS[kind]
         f.dtype = ELEMENT_KINDS[dtype]
@@ -91,6 +91,7 @@ class HipBackend:
         f.z_kind = ELEMENT_KINDS[z_kind]
         f.group = group
         f.out_kind = ELEMENT_KINDS[out_kind]
+        f.axes_mask = sum(1 << d for d in axes) if axes else 0
         return self._wrap(lambda out, err: _lib.lib().unp_hip_lower_form(C.byref(f), out, err))
 
     def lower_kernel(self, kernel) -> GeneratedKernel:

@@ -40,7 +40,7 @@ class Error(C.Structure):
 class Form(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "kind", "dtype", "rank", "op0", "op1", "reduced_from", "exclusive", "reverse",
-        "index_dtype", "oob", "data_slot", "q_kind", "z_kind", "group", "out_kind")]
+        "index_dtype", "oob", "data_slot", "q_kind", "z_kind", "group", "out_kind")] + [("axes_mask", C.c_uint32)]
 
 
 class Arg(C.Structure):

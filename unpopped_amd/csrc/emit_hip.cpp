@@ -179,29 +179,88 @@ void set_error(unp_error* err, int32_t code, const std::string& detail) {
   std::snprintf(err->detail, sizeof(err->detail), "%s", detail.c_str());
 }
 
+uint32_t reduction_mask(const unp_form& f) {
+  if (f.axes_mask) return f.axes_mask;
+  uint32_t m = 0;
+  for (int32_t d = f.reduced_from; d < f.rank; ++d) m |= 1u << d;
+  return m;
+}
+
+char reduction_schedule(uint32_t mask, int32_t rank) {
+  std::string runs;  // one letter per run of adjacent axes of a kind
+  for (int32_t d = 0; d < rank; ++d) {
+    const char c = (mask >> d) & 1u ? 'R' : 'K';
+    if (runs.empty() || runs.back() != c) runs.push_back(c);
+  }
+  if (runs == "R") return 'a';
+  if (runs == "KR") return 'r';
+  if (runs == "RK" || runs == "KRK") return 'm';
+  return 'g';
+}
+
 static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) {
   const bool two = f.kind == UNP_FORM_ROW_REDUCE2;
   if (f.rank < 1 || f.rank > 8) {
     why = "rank is zero or more than 8";
     return UNP_LIFT_DECLINE;
   }
-  if (f.reduced_from < 0 || f.reduced_from >= f.rank) {
-    why = "the reduced axes must be a trailing run of axes (the last axis at least)";
+  const uint32_t mask = reduction_mask(f);
+  if (mask == 0 || (mask >> f.rank) != 0) {
+    why = "a reduced axis outside the rank";
+    return UNP_LIFT_DECLINE;
+  }
+  const char sched = reduction_schedule(mask, f.rank);
+  if (two && sched != 'r') {
+    why = "the fused row fold reduces the trailing axis";
     return UNP_UNSUPPORTED_KERNEL;
   }
   if (!reduction_ok(f.dtype, f.op0, why) || (two && !reduction_ok(f.dtype, f.op1, why)))
     return UNP_UNSUPPORTED_KERNEL;
   const char* T = ctype(f.dtype);
   const int V = vec_of(f.dtype);
-  L.reduce_all = (f.reduced_from == 0) && !two;
+  L.axes_mask = mask;
+  L.red_schedule = sched;
+  L.reduce_all = sched == 'a';
+  L.form.reduced_from = f.rank;
+  for (int32_t d = f.rank - 1; d >= 0 && ((mask >> d) & 1u); --d) L.form.reduced_from = d;
   std::ostringstream name;
-  name << (L.reduce_all ? "unp_reduce_all_" : "unp_rowreduce_") << op_name(f.op0);
+  name << (sched == 'a' ? "unp_reduce_all_" : sched == 'm' ? "unp_reduce_mid_" : sched == 'g' ? "unp_reduce_axes_"
+                                                                                            : "unp_rowreduce_")
+       << op_name(f.op0);
   if (two) name << "_" << op_name(f.op1);
   name << "_" << lower_name(f.dtype);
   L.name = name.str();
   std::ostringstream src;
   src << header(L.name, f);
-  if (L.reduce_all) {
+  if (sched == 'm') {
+    // Eight waves per block, one block per CU, 8 rows in flight per lane; blocks split the
+    // reduced extent so that a launch has about cu_count blocks (measured best for an
+    // 8192 x 4096 f32 column sum: more chunks cost more in the partials' final fold than they
+    // add in parallelism).
+    L.threads = 512;
+    L.blocks_per_cu = 1;
+    for (int fast = 1; fast >= 0; --fast) {
+      Entry e;
+      e.fast = fast;
+      e.vec = fast ? V : 1;
+      e.symbol = L.name + (fast ? "_mv" : "_ms");
+      src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol << "(const " << T << "* in, " << T
+          << "* out, long long A, long long R, long long B, long long S, typename unp::acc<" << T << ", " << f.op0
+          << ">::type* partials, unsigned* counters) {\n  unp::reduce_mid<" << T << ", " << f.op0 << ", " << e.vec
+          << ", 512, 8>(in, out, A, R, B, S, partials, counters);\n}\n";
+      L.entries.push_back(e);
+    }
+  } else if (sched == 'g') {
+    L.threads = 256;
+    L.blocks_per_cu = 8;
+    Entry e;
+    e.fast = false;
+    e.vec = 1;
+    e.symbol = L.name + "_g";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(const " << T << "* in, " << T
+        << "* out, unp::axes_desc d) {\n  unp::reduce_generic<" << T << ", " << f.op0 << ", 256>(in, out, d);\n}\n";
+    L.entries.push_back(e);
+  } else if (L.reduce_all) {
     // One block per CU (8 waves): the read rate peaks with few streams per CU.
     L.threads = 512;
     L.blocks_per_cu = 1;
@@ -213,7 +272,7 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
       src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol << "(const " << T << "* in, " << T
           << "* out, long long n, typename unp::acc<" << T << ", " << f.op0
           << ">::type* partials, unsigned* counter) {\n  unp::reduce_all<" << T << ", " << f.op0 << ", " << e.vec
-          << ", 512, " << (fast ? 4 : 8) << ">(in, out, n, partials, counter);\n}\n";
+          << ", 512, " << (fast ? 16 : 8) << ">(in, out, n, partials, counter);\n}\n";
       L.entries.push_back(e);
     }
   } else {
@@ -243,22 +302,34 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
   j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":"
     << (two ? "\"row_reduce2\"" : "\"reduction\"") << ",\"dtype\":\"" << kind_name(f.dtype)
     << "\",\"ops\":[\"" << op_name(f.op0) << "\"" << (two ? std::string(",\"") + op_name(f.op1) + "\"" : "")
-    << "],\"rank\":" << f.rank << ",\"reduced_axes_from\":" << f.reduced_from
+    << "],\"rank\":" << f.rank << ",\"reduced_axes\":[";
+  for (int32_t d = 0, n = 0; d < f.rank; ++d)
+    if ((mask >> d) & 1u) j << (n++ ? "," : "") << d;
+  j << "],\"schedule\":\""
+    << (sched == 'a' ? "all" : sched == 'r' ? "rows" : sched == 'm' ? "mid" : "generic") << "\""
     << ",\"params\":[{\"name\":\"in0\",\"kind\":\"buffer\",\"role\":\"Read\"},"
     << (two ? "{\"name\":\"out0\",\"kind\":\"buffer\",\"role\":\"Write\"},{\"name\":\"out1\",\"kind\":\"buffer\",\"role\":\"Write\"}"
             : "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}");
   for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
   j << "],\"launch\":{\"block\":[" << L.threads << ",1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
     << "\",\"grid_policy\":\"device-class constant; "
-    << (L.reduce_all ? "blocks stride over 16-byte vectors, last-ticket block folds the partials"
-                     : "waves stride over rows (one wave per row); rows longer than 32768 elements: one block per row")
+    << (sched == 'a'   ? "blocks stride over 16-byte vectors, last-ticket block folds the partials"
+        : sched == 'm' ? "the input as A x R x B: a wave per 64 x vec columns, blocks split R into chunks, the "
+                         "last-ticket block of a column strip folds the chunk partials in chunk order"
+        : sched == 'g' ? "one wave per output element, lanes stride over the reduced positions"
+                       : "waves stride over rows (one wave per row); rows longer than 32768 elements: one block per row")
     << "\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
       << ",\"when\":\"" << (L.entries[i].wide ? "reduced extent > 32768; " : "")
-      << (L.entries[i].fast ? "reduced extent % vec == 0 and in0 16-byte aligned" : "otherwise") << "\"}";
+      << (sched == 'g'   ? "always"
+          : sched == 'm' ? (L.entries[i].fast ? "B % vec == 0 and in0 16-byte aligned" : "otherwise")
+                         : (L.entries[i].fast ? "reduced extent % vec == 0 and in0 16-byte aligned" : "otherwise"))
+      << "\"}";
   j << "],\"workspace\":"
-    << (L.reduce_all ? "{\"partials\":\"grid * accumulator bytes\",\"counter\":4}" : "null")
+    << (L.reduce_all   ? "{\"partials\":\"grid * accumulator bytes\",\"counter\":4}"
+        : sched == 'm' ? "{\"partials\":\"strips * chunks * 64 * vec * accumulator bytes\",\"counters\":\"strips * 4\"}"
+                       : "null")
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["
     << json_str(kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN || (two && (f.op1 == UNP_OP_SUM || f.op1 == UNP_OP_MEAN)))

@@ -293,6 +293,19 @@ template <class X> UNP_DEV X load_agent(const X* p) {
   }
 }
 
+// Arrive at a device-scope counter after this wave's agent-scope stores (store_agent) are
+// complete: the stores are written through to the device-coherent level, so waiting for
+// them (vmcnt) is all the ordering a reader that loads with load_agent needs.  An acq_rel
+// atomic would also write back and invalidate this XCD's whole L2 (buffer_wbl2 / buffer_inv),
+// which costs more than the reduction when every block of a launch does it.  Returns the
+// counter's previous value.
+UNP_DEV u32 arrive_after_stores(u32* counter) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): expcnt and lgkmcnt left at their maximum
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Draw the next ticket of a device-scope counter (one lane).  An atomic increment, not an
 // add: the compiler's atomic optimizer rewrites a one-lane add into a wave-aggregated form
 // that waits for the returned value at once, where an increment's value is waited for only
@@ -460,9 +473,7 @@ UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
   a = block_reduce<A, OP, THREADS>(a, s);
   if (tid == 0) {
     store_agent(&partials[blockIdx.x], a);
-    const u32 ticket =
-        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    last = (ticket == gridDim.x - 1) ? 1u : 0u;
+    last = (arrive_after_stores(counter) == gridDim.x - 1) ? 1u : 0u;
   }
   __syncthreads();
   if (last == 0u) return;
@@ -472,6 +483,159 @@ UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
   if (tid == 0) {
     out[0] = finish<T, OP>(b, n);
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Reduction of the middle axis of A x R x B (row-major): out[a, b] = fold_i in[a, i, b].  The
+// shape every reduced-axis set with one contiguous run of reduced axes and kept axes after it
+// takes once adjacent axes of a kind are merged (A = 1: the outer axis, as column sums).
+//
+// A wave covers 64 * VEC consecutive columns b of one a; the block's WAVES waves split the
+// block's run of rows into WAVES consecutive pieces; the blocks of one column strip split R
+// into S consecutive chunks.  Consecutive blocks take consecutive strips of one chunk, so the
+// blocks in flight together read whole rows.  Lane l folds its VEC columns down its rows in ascending order
+// (16-byte loads, every load of a wave instruction contiguous, U rows in flight); the waves
+// meet in LDS in wave order; with S > 1 each block publishes its partials and the block that
+// draws the strip's last ticket folds the S partials in chunk order and stores.  The order is
+// fixed by (S, WAVES, U), so the result is reproducible.  counters[strip] is zero on entry and
+// left zero.
+// ---------------------------------------------------------------------------------------
+template <class T, int OP, int VEC, int THREADS, int U>
+UNP_DEV void reduce_mid(const T* __restrict__ in, T* __restrict__ out, i64 A, i64 R, i64 B, i64 S,
+                        typename acc<T, OP>::type* __restrict__ partials, u32* __restrict__ counters) {
+  typedef typename acc<T, OP>::type Ac;
+  typedef fold<Ac, OP> F;
+  constexpr int WAVES = THREADS / 64;
+  constexpr i64 CW = (i64)64 * VEC;  // columns per strip
+  __shared__ Ac sh[WAVES][64 * VEC];
+  __shared__ u32 last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const i64 ncb = (B + CW - 1) / CW;
+  const i64 nstrips = A * ncb;
+  const i64 strip = (i64)blockIdx.x % nstrips;  // a * ncb + cb
+  const i64 s = (i64)blockIdx.x / nstrips;
+  const i64 a = strip / ncb, cb = strip - a * ncb;
+  const i64 b0 = cb * CW + (i64)lane * VEC;
+  const bool live = b0 < B;  // VEC divides B (the host picks VEC = 1 otherwise)
+  // This block's rows [i0, i1), then this wave's piece of them.
+  const i64 i0 = (R * s) / S, i1 = (R * (s + 1)) / S;
+  const i64 w0 = i0 + ((i1 - i0) * wave) / WAVES, w1 = i0 + ((i1 - i0) * (wave + 1)) / WAVES;
+  Ac acc_[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc_[e] = F::identity();
+  if (live) {
+    const T* __restrict__ p = in + (a * R) * B + b0;
+    i64 i = w0;
+    for (; i + U <= w1; i += U) {
+      vec<T, VEC> v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = ld_nt<T, VEC>(p + (i + u) * B);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc_[e] = F::apply(acc_[e], (Ac)v[u].e[e]);
+    }
+    for (; i < w1; ++i) {
+      const vec<T, VEC> v = ld_nt<T, VEC>(p + i * B);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc_[e] = F::apply(acc_[e], (Ac)v.e[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) sh[wave][lane * VEC + e] = acc_[e];
+  __syncthreads();
+  // Wave 0 folds the waves' partials in wave order.
+  if (wave == 0) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      Ac r = sh[0][lane * VEC + e];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) r = F::apply(r, sh[w][lane * VEC + e]);
+      acc_[e] = r;
+    }
+    if (S == 1) {
+      if (live) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) out[a * B + b0 + e] = finish<T, OP>(acc_[e], R);
+      }
+      return;
+    }
+    Ac* __restrict__ mine = partials + (strip * S + s) * CW + (i64)lane * VEC;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) store_agent(&mine[e], acc_[e]);
+    if (lane == 0) last = (arrive_after_stores(&counters[strip]) == (u32)(S - 1)) ? 1u : 0u;
+  }
+  if (S == 1) return;
+  __syncthreads();
+  if (last == 0u || wave != 0) return;
+  // Every other block's partials were complete before its arrival; the device-coherent loads
+  // see them, 8 chunks in flight at a time.
+  Ac r[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) r[e] = F::identity();
+  const Ac* __restrict__ col = partials + strip * S * CW + (i64)lane * VEC;
+  i64 k = 0;
+  for (; k + 8 <= S; k += 8) {
+    Ac v[8][VEC];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[t][e] = load_agent(&col[(k + t) * CW + e]);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) r[e] = F::apply(r[e], v[t][e]);
+  }
+  for (; k < S; ++k)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) r[e] = F::apply(r[e], load_agent(&col[k * CW + e]));
+  if (live) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) out[a * B + b0 + e] = finish<T, OP>(r[e], R);
+  }
+  if (lane == 0) __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------------------
+// Any reduced-axis set: one wave per output element.  The host passes the kept and the
+// reduced axes (extents and element strides, outermost first, adjacent axes of a kind
+// merged); output o unravels over the kept axes to its base offset, and lane l folds the
+// reduced positions l, l + 64, ... (row-major over the reduced axes) before the wave's DPP
+// combine.  Correct for every mask; the fast shapes above take the common ones.
+// ---------------------------------------------------------------------------------------
+struct axes_desc {
+  i64 nk, nr;           // kept / reduced axis counts (after merging)
+  i64 kext[8], kstr[8];
+  i64 rext[8], rstr[8];
+  i64 outs, count;      // output elements, reduced positions per output
+};
+
+template <class T, int OP, int THREADS>
+UNP_DEV void reduce_generic(const T* __restrict__ in, T* __restrict__ out, const axes_desc& d) {
+  typedef typename acc<T, OP>::type Ac;
+  typedef fold<Ac, OP> F;
+  const int lane = threadIdx.x & 63;
+  const i64 nw = (i64)gridDim.x * (THREADS / 64);
+  for (i64 o = (i64)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6); o < d.outs; o += nw) {
+    i64 base = 0, q = o;
+    for (i64 k = d.nk - 1; k >= 0; --k) {
+      const i64 c = q % d.kext[k];
+      q /= d.kext[k];
+      base += c * d.kstr[k];
+    }
+    Ac a = F::identity();
+    for (i64 t = lane; t < d.count; t += 64) {
+      i64 off = base, u = t;
+      for (i64 k = d.nr - 1; k >= 0; --k) {
+        const i64 c = u % d.rext[k];
+        u /= d.rext[k];
+        off += c * d.rstr[k];
+      }
+      a = F::apply(a, (Ac)in[off]);
+    }
+    a = wave_reduce<Ac, OP>(a);
+    if (lane == 0) out[o] = finish<T, OP>(a, d.count);
   }
 }
 

@@ -971,19 +971,26 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
       ps[0].rank >= 1 && (size_t)ps[0].rank + 2 == np) {
     const int32_t dt = ps[0].elem, r = ps[0].rank, orank = ps[1].rank;
     static const int32_t ops[] = {UNP_OP_SUM, UNP_OP_PROD, UNP_OP_MAX, UNP_OP_MIN, UNP_OP_MEAN};
+    // Every reduced-axis set whose output rank matches (ReductionShape::new,
+    // kernel_lift.rs:854-870), trailing runs first: the reduction most often asked for.
+    std::vector<uint32_t> masks;
+    for (int32_t from = r - 1; from >= 0; --from) masks.push_back(((1u << r) - 1) & ~((1u << from) - 1));
+    for (uint32_t m = 1; m < (1u << r); ++m)
+      if (std::find(masks.begin(), masks.end(), m) == masks.end()) masks.push_back(m);
     for (int32_t op : ops) {
-      for (int32_t from = r - 1; from >= 0; --from) {
-        uint32_t mask = 0;
-        for (int32_t d = from; d < r; ++d) mask |= 1u << d;
+      for (uint32_t mask : masks) {
+        const int32_t kept = r - __builtin_popcount(mask);
         for (int keep = 0; keep <= 1; ++keep) {
-          const int32_t want = keep ? r : from;
+          const int32_t want = keep ? r : kept;
           if (orank != want) continue;
           if (attempt([&] { return lift_reduction(name, dt, r, op, mask, keep, block, grid); })) {
             out.form.kind = UNP_FORM_REDUCTION;
             out.form.dtype = dt;
             out.form.rank = r;
             out.form.op0 = op;
-            out.form.reduced_from = from;
+            out.form.axes_mask = mask;
+            out.form.reduced_from = r;
+            for (int32_t d = r - 1; d >= 0 && ((mask >> d) & 1u); --d) out.form.reduced_from = d;
             out.lift = block ? "lift_reduction_opdef_launched" : "lift_reduction_opdef";
             return UNP_OK;
           }

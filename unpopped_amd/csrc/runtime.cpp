@@ -59,6 +59,8 @@ struct unp_exec {
   void* ws = nullptr;  // scan: tile status words; full reduction: block partials
   size_t ws_bytes = 0;
   uint32_t* counter = nullptr;
+  uint32_t* counters = nullptr;  // reduce_mid: one ticket counter per column strip, left zero
+  size_t n_counters = 0;
   uint32_t epoch = 0;
   uint32_t ticket_base = 0;
   uint32_t grid[3] = {0, 0, 0};
@@ -332,6 +334,7 @@ void unp_hip_exec_destroy(unp_exec* x) {
   if (!x) return;
   if (x->ws) hipFree(x->ws);
   if (x->counter) hipFree(x->counter);
+  if (x->counters) hipFree(x->counters);
   if (x->mod) hipModuleUnload(x->mod);
   delete x;
 }
@@ -423,6 +426,23 @@ int32_t ensure_ws(unp_exec* x, size_t bytes, bool need_counter, unp_error* err) 
   return UNP_OK;
 }
 
+// At least n zeroed ticket counters.  Kernels leave every counter they use at zero, so a
+// larger array is allocated afresh (and zeroed) only when a launch needs more strips.
+int32_t ensure_counters(unp_exec* x, size_t n, unp_error* err) {
+  if (n <= x->n_counters) return UNP_OK;
+  if (x->counters) {
+    hipFree(x->counters);
+    x->counters = nullptr;
+    x->n_counters = 0;
+  }
+  hipError_t e = hipMalloc((void**)&x->counters, n * sizeof(uint32_t));
+  if (e != hipSuccess) return hip_fail(err, "hipMalloc(counters)", e);
+  e = hipMemset(x->counters, 0, n * sizeof(uint32_t));
+  if (e != hipSuccess) return hip_fail(err, "hipMemset(counters)", e);
+  x->n_counters = n;
+  return UNP_OK;
+}
+
 int32_t launch(unp_exec* x, size_t entry, uint32_t grid, void** params, hipStream_t s, unp_error* err) {
   const uint32_t threads = (uint32_t)(x->l.entries[entry].threads ? x->l.entries[entry].threads : x->l.threads);
   x->grid[0] = grid;
@@ -456,11 +476,87 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
   int32_t rc = take_args(a, n, two ? 3 : 2, (size_t)f.rank, A, err);
   if (rc == UNP_OK) rc = extents_i32(A, (size_t)f.rank, err);
   if (rc != UNP_OK) return rc;
+  const int vec = 16 / (int)unp::kind_bytes(f.dtype);
+  const char sched = x->l.red_schedule;
+  const uint32_t mask = x->l.axes_mask;
+  if (sched == 'm' || sched == 'g') {
+    // Output elements and reduced positions per output.
+    long long outs = 1, count = 1;
+    for (int32_t d = 0; d < f.rank; ++d) ((mask >> d) & 1u ? count : outs) *= A.ext[(size_t)d];
+    if ((rc = need_buffers(A, outs > 0, err)) != UNP_OK) return rc;
+    if (outs == 0) return UNP_OK;
+    uint64_t in = A.buf[0], out = A.buf[1];
+    if (sched == 'm') {
+      // A x R x B: the kept axes before the reduced run, the run, the kept axes after it.
+      int32_t fr = 0, lr = f.rank - 1;
+      while (!((mask >> fr) & 1u)) ++fr;
+      while (!((mask >> lr) & 1u)) --lr;
+      long long a = product(A.ext, 0, (size_t)fr), r = product(A.ext, (size_t)fr, (size_t)lr + 1),
+                b = product(A.ext, (size_t)lr + 1, (size_t)f.rank);
+      const size_t entry = (b % vec == 0 && aligned16(in)) ? 0 : 1;
+      const long long cw = 64LL * x->l.entries[entry].vec;
+      const long long strips = a * ((b + cw - 1) / cw);
+      // Chunks of R: about cu_count * blocks_per_cu blocks in all, at least 16 rows per chunk,
+      // at most 1024 chunks.
+      const long long target = (long long)x->cu_count * x->l.blocks_per_cu;
+      long long S = (target + strips - 1) / strips;
+      S = std::min(S, std::max(1LL, r / 16));
+      S = std::max(1LL, std::min(S, 1024LL));
+      const long long grid = strips * S;
+      if (grid > 0x7fffffffLL) {
+        set_error(err, UNP_INVALID_ARGUMENT, "too many column strips for one launch");
+        return UNP_INVALID_ARGUMENT;
+      }
+      const size_t acc_bytes = (unp::kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN))
+                                   ? 8
+                                   : unp::kind_bytes(f.dtype);
+      void* ws = nullptr;
+      void* cnt = nullptr;
+      if (S > 1) {
+        if ((rc = ensure_ws(x, (size_t)(strips * S * cw) * acc_bytes, false, err)) != UNP_OK) return rc;
+        if ((rc = ensure_counters(x, (size_t)strips, err)) != UNP_OK) return rc;
+        ws = x->ws;
+        cnt = x->counters;
+      }
+      void* params[] = {&in, &out, &a, &r, &b, &S, &ws, &cnt};
+      return launch(x, entry, (uint32_t)grid, params, s, err);
+    }
+    // Any other mask: kept and reduced axes with their element strides, adjacent axes of a
+    // kind merged (a merged run's stride is its innermost axis's).
+    unp::axes_desc_host d{};
+    long long stride = 1;
+    std::vector<long long> str((size_t)f.rank);
+    for (int32_t k = f.rank - 1; k >= 0; --k) {
+      str[(size_t)k] = stride;
+      stride *= A.ext[(size_t)k];
+    }
+    for (int32_t k = 0; k < f.rank;) {
+      const bool red = (mask >> k) & 1u;
+      long long ext = 1;
+      int32_t e = k;
+      while (e < f.rank && (((mask >> e) & 1u) != 0) == red) ext *= A.ext[(size_t)e++];
+      const long long st = str[(size_t)(e - 1)];
+      if (red) {
+        d.rext[d.nr] = ext;
+        d.rstr[d.nr++] = st;
+      } else {
+        d.kext[d.nk] = ext;
+        d.kstr[d.nk++] = st;
+      }
+      k = e;
+    }
+    d.outs = outs;
+    d.count = count;
+    const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
+    const long long want = (outs + 3) / 4;
+    const uint32_t grid = (uint32_t)(want < cap ? want : cap);
+    void* params[] = {&in, &out, &d};
+    return launch(x, 0, grid, params, s, err);
+  }
   const long long rows = product(A.ext, 0, (size_t)f.reduced_from);
   const long long cols = product(A.ext, (size_t)f.reduced_from, (size_t)f.rank);
   if ((rc = need_buffers(A, rows > 0, err)) != UNP_OK) return rc;
   if (rows == 0) return UNP_OK;
-  const int vec = 16 / (int)unp::kind_bytes(f.dtype);
   uint64_t in = A.buf[0], o0 = A.buf[1], o1 = two ? A.buf[2] : A.buf[1];
   const size_t entry = pick(x, cols % vec == 0 && aligned16(in), !x->l.reduce_all && cols > unp::kWideRow);
   const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);

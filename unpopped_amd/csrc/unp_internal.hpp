@@ -39,6 +39,19 @@ constexpr int kScanStatusWords = 32;
 // Reductions over more than kWideRow elements per row use the block-per-row schedule.
 constexpr long long kWideRow = 32768;
 
+// The reduced-axis mask of a reduction form (axes_mask, or reduced_from..rank-1 when it is 0)
+// and its schedule class ('r', 'a', 'm' or 'g', as Lowered::red_schedule).
+uint32_t reduction_mask(const unp_form& f);
+char reduction_schedule(uint32_t mask, int32_t rank);
+
+// The host image of the device's axes_desc (reduce_generic's argument, passed by value).
+struct axes_desc_host {
+  long long nk, nr;
+  long long kext[8], kstr[8];
+  long long rext[8], rstr[8];
+  long long outs, count;
+};
+
 // An Access::RowReduce (crates/unpopped/src/ir.rs:2114-2125): the stages' pre expressions and
 // folds, then the full-width epilogue, as ScalarExpr JSON over Input(k) and Reduced(t) leaves.
 struct RowReduceSpec {
@@ -58,6 +71,11 @@ struct Lowered {
   std::string interface_json;
   std::vector<Entry> entries;
   bool reduce_all = false;  // a reduction with no kept axis
+  // A reduction's schedule, from the shape of its reduced-axis set once adjacent axes of a
+  // kind are merged: 'r' kept then reduced (rows), 'a' all reduced, 'm' one reduced run with
+  // kept axes after it (A x R x B), 'g' anything else.
+  char red_schedule = 'r';
+  uint32_t axes_mask = 0;  // the reduced axes, bit d = axis d
   int threads = 256;
   int blocks_per_cu = 8;
   RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only

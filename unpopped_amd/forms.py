@@ -20,11 +20,12 @@ CALLER_LAUNCH = (256, 64)
 def kernel_for(kind: str, dtype: str = "F32", rank: int = 1, op: str = "Sum", op1: str = "Max",
                reduced_from: int | None = None, exclusive: bool = False, reverse: bool = False,
                index_dtype: str = "I32", oob: str = "ZeroFill", q_kind: str = "U4", z_kind: str = "U4",
-               group: int = 128, **_ignored) -> dict:
+               group: int = 128, axes: tuple | None = None, keepdim: bool = False, **_ignored) -> dict:
     """The KernelFn (as its serde JSON dict) of the lift or authored kernel for a form."""
     if kind == "reduction":
         k = rank - 1 if reduced_from is None else reduced_from
-        return u.lift_reduction("reduce", dtype, rank, op, axes=tuple(range(k, rank)), launch=CALLER_LAUNCH)
+        ax = tuple(range(k, rank)) if axes is None else tuple(axes)
+        return u.lift_reduction("reduce", dtype, rank, op, axes=ax, keepdim=keepdim, launch=CALLER_LAUNCH)
     if kind == "row_reduce2":
         return u.kernel_row_reduce2("row_fold", dtype, op, op1, launch=CALLER_LAUNCH)
     if kind == "scan":
@@ -68,6 +69,22 @@ def reduce_rows(x: np.ndarray, op: str, op1: str | None = None):
     u.synchronize()
     r0 = o0.download(x.dtype, rows)
     return (r0, o1.download(x.dtype, rows)) if two else r0
+
+
+def reduce_axes(x: np.ndarray, axes: tuple, op: str, keepdim: bool = False) -> np.ndarray:
+    """Fold `x` over the axes in `axes` (any set) with the reduction lift of that axis set."""
+    kind = NP_KIND[x.dtype.type]
+    axes = tuple(sorted(axes))
+    ex = executor(kind="reduction", dtype=kind, rank=x.ndim, op=op, axes=axes, keepdim=keepdim)
+    kept = tuple(n for d, n in enumerate(x.shape) if d not in axes)
+    outs = int(np.prod(kept, dtype=np.int64))
+    din = u.DeviceBuffer.from_array(x)
+    dout = u.DeviceBuffer(max(outs * x.itemsize, 1))
+    ex.launch(din, dout, *x.shape)
+    u.synchronize()
+    got = dout.download(x.dtype, outs)
+    shape = tuple(1 if d in axes else n for d, n in enumerate(x.shape)) if keepdim else kept
+    return got.reshape(shape)
 
 
 def reduce_all(x: np.ndarray, op: str):
