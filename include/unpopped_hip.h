@@ -160,6 +160,12 @@ int32_t unp_hip_lower_kernel(const char* kernel_json, unp_generated** out, unp_e
  * axes, keepdim) (ir.rs:3186-3214): axes_mask bit d reduces axis d, 0 is the last axis. */
 int32_t unp_lift_reduction(const char* name, int32_t dtype, int32_t rank, int32_t op, uint32_t axes_mask,
                            int32_t keepdim, uint32_t block, uint32_t grid, char** json, unp_error* err);
+/* The same lifts of an OpDef::reduction with n_inputs inputs, a pre-map body over Input(0..n) and
+ * a fused post over Reduced(0) (kernel_lift.rs:807-831, :910-1003; block_reduce.rs:292-307), both
+ * as ScalarExpr JSON; post_json NULL (or `{"Reduced":0}`) is the identity post. */
+int32_t unp_lift_reduction_x(const char* name, int32_t dtype, int32_t rank, int32_t op, uint32_t axes_mask,
+                             int32_t keepdim, int32_t n_inputs, const char* body_json, const char* post_json,
+                             uint32_t block, uint32_t grid, char** json, unp_error* err);
 /* lift_scan_opdef (kernel_lift.rs:504-519) / lift_scan_opdef_launched (kernel_lift/scan_launched.rs
  * :54-102) of OpDef::scan_simple (ir.rs:3422-3441): identity pre-map, no post. */
 int32_t unp_lift_scan(const char* name, int32_t dtype, int32_t rank, int32_t op, int32_t axis, int32_t exclusive,

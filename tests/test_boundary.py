@@ -233,12 +233,18 @@ def test_lower_kernel_refuses_anything_else():
     refused(u.lift_reduction("r", "F32", 2, "Prod"))
     # a scan along a non-innermost axis
     refused(u.lift_scan("s", "F32", 2, "Sum", axis=0))
-    # an elementwise body different from the identity load (x * x) is refused
+    # a pre-map body (x * x) is the lift of OpDef::reduction with that body: recognised, and
+    # spelled into the kernel (kernel_lift.rs:919-941)
     sq = json.dumps(u.lift_reduction("r", "F64", 1, "Sum")).replace(
         '{"Let": {"local": 5, "init": {"Local": 2}}}',
         '{"Let": {"local": 5, "init": {"Mul": [{"Local": 2}, {"Local": 2}]}}}')
     assert '"Mul"' in sq
-    refused(sq)
+    g = b.lower_kernel(sq)
+    assert g.interface["body"] == "(x[0] * x[0])" and g.interface["post"] is None
+    # a body that reads a local other than a loaded input (here an extent) is no lift's kernel
+    ext = json.dumps(u.lift_reduction("r", "F64", 1, "Sum")).replace(
+        '{"Let": {"local": 5, "init": {"Local": 2}}}', '{"Let": {"local": 5, "init": {"Local": 0}}}')
+    refused(ext)
 
 
 def test_lower_form_declines_unsupported_forms():

@@ -453,6 +453,77 @@ def test_reduce_any_axes_keepdim_and_nan(hip_device):
 
 
 # ---------------------------------------------------------------------------------------
+# Reductions with a pre-map body over several inputs and a fused post (the reduction lift's
+# body and post: kernel_lift.rs:807-831, 919-941, 987-1003; block_reduce.rs:292-307).  The
+# oracle is the serial lifted row reduction with that one stage and the post as its epilogue,
+# over the inputs with the reduced axes moved last.
+# ---------------------------------------------------------------------------------------
+
+def oracle_expr(inputs, axes, op, body, post):
+    x0 = inputs[0]
+    kept = [d for d in range(x0.ndim) if d not in axes]
+    rows = int(np.prod([x0.shape[d] for d in kept], dtype=np.int64))
+    cols = int(np.prod([x0.shape[d] for d in axes], dtype=np.int64))
+    xs = [np.ascontiguousarray(np.transpose(a, kept + list(axes))).reshape(rows, cols) for a in inputs]
+    full = oracle.row_reduce(xs, [(body, op)], X.reduced(0) if post is None else post)
+    return xs, full[:, 0]
+
+
+def xr_cases():
+    x0, x1, r0 = X.input(0), X.input(1), X.reduced(0)
+    return [
+        ("sumsq_rows", [(37, 1000)], (1,), "Sum", x0 * x0, None),
+        ("l2norm_rows", [(64, 4096)], (1,), "Sum", x0 * x0, r0.sqrt()),
+        ("rms_rows", [(5, 777)], (1,), "Mean", x0 * x0, (r0 + X.konst(0.5)).sqrt()),
+        ("dot_rows_unaligned", [(9, 1001)] * 2, (1,), "Sum", x0 * x1, None),
+        ("dot_all", [(100003,)] * 2, (0,), "Sum", x0 * x1, None),
+        ("dot_all_rank2", [(64, 4096)] * 2, (0, 1), "Sum", x0 * x1, r0 / X.konst(4.0)),
+        ("weighted_cols", [(300, 70)] * 2, (0,), "Sum", x0 * x1 + x0, None),
+        ("absmean_mid", [(6, 50, 9)], (1,), "Mean", x0.abs(), None),
+        ("max_scaled_generic", [(4, 33, 7)], (0, 2), "Max", x0 - X.konst(1.0), r0 * X.konst(2.0)),
+        ("min_three_inputs", [(11, 513)] * 3, (1,), "Min", x0 * x1 - x0, -r0),
+    ]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("case", range(10))
+def test_reduce_body_and_post_dyadic_bit_exact(hip_device, dtype, case):
+    """Dyadic inputs: every body value and partial sum is exact in f64, so the device's fold
+    order cannot move a bit, and the post (+, -, *, /, sqrt: correctly rounded) matches too."""
+    name, shapes, axes, op, body, post = xr_cases()[case]
+    H.say(f"[case] reduce body/post {name} {np.dtype(dtype).name}")
+    ins = [dyadic(50 + k, sh, dtype) for k, sh in enumerate(shapes)]
+    got = H.reduce_expr(ins, axes, op, body, post)
+    _, want = oracle_expr(ins, axes, op, body, post)
+    assert np.array_equal(got.ravel(), want, equal_nan=True)
+
+
+@pytest.mark.parametrize("case", [0, 3, 4, 6])
+def test_reduce_body_normal_data_within_bound(hip_device, case):
+    """Normal data, no post: every output within the declared bound of the body values' sum."""
+    name, shapes, axes, op, body, post = xr_cases()[case]
+    H.say(f"[case] reduce body normal {name}")
+    ins = [rng(60 + k).normal(size=sh).astype(np.float32) for k, sh in enumerate(shapes)]
+    got = H.reduce_expr(ins, axes, op, body, post)
+    xs, _ = oracle_expr(ins, axes, op, body, post)
+    # The body's value at each position, evaluated in f64 and rounded once: the oracle's row
+    # reduction with the body as its full-width epilogue.
+    vals = oracle.row_reduce(xs, [(X.input(0), "Max")], body)
+    assert_sum_within_bound(vals, got.ravel())
+
+
+def test_reduce_body_and_post_launched_kernel_and_keepdim(hip_device):
+    """The launched lift lowers to the same kernel; keepdim keeps size-1 axes."""
+    H.say("[case] reduce body/post keepdim")
+    x0, r0 = X.input(0), X.reduced(0)
+    x = dyadic(70, (3, 40, 5), np.float32)
+    got = H.reduce_expr([x], (1,), "Sum", x0 * x0, r0.sqrt(), keepdim=True)
+    assert got.shape == (3, 1, 5)
+    _, want = oracle_expr([x], (1,), "Sum", x0 * x0, r0.sqrt())
+    assert np.array_equal(got.ravel(), want)
+
+
+# ---------------------------------------------------------------------------------------
 # Fused row reductions: the launched Access::RowReduce lift (softmax, RMS norm, ...)
 #
 # Bars: Max/Min stages bit-exact (kernel_parallel_row_reduce_agrees.rs:255-268); identity Sum/Mean

@@ -129,14 +129,24 @@ def _geom(launch) -> tuple[int, int]:
 
 
 def lift_reduction(name: str, dtype: str, rank: int, op: str, axes: tuple = (), keepdim: bool = False,
-                   launch: tuple | None = None) -> dict:
-    """The reduction lift (serial, or launched on ``launch = (block, grid)``) as a KernelFn dict."""
+                   launch: tuple | None = None, n_inputs: int = 1, body=None, post=None) -> dict:
+    """The reduction lift (serial, or launched on ``launch = (block, grid)``) as a KernelFn dict.
+    ``body`` is the pre-map over ``Input(0..n_inputs)`` (default ``Input(0)``) and ``post`` a fused
+    post over ``Reduced(0)`` (default the identity), each an ``expr.Expr`` or its serde dict."""
     mask = 0
     for d in axes:
         mask |= 1 << d
     b, g = _geom(launch)
-    return _lifted(lambda o, e: _lib.lib().unp_lift_reduction(name.encode(), ELEMENT_KINDS[dtype], rank,
-                                                             REDUCE_OPS[op], mask, int(keepdim), b, g, o, e))
+    if body is None and post is None and n_inputs == 1:
+        return _lifted(lambda o, e: _lib.lib().unp_lift_reduction(name.encode(), ELEMENT_KINDS[dtype], rank,
+                                                                 REDUCE_OPS[op], mask, int(keepdim), b, g, o, e))
+    from . import expr as X
+
+    bj = json.dumps(X.as_json(X.input(0) if body is None else body)).encode()
+    pj = None if post is None else json.dumps(X.as_json(post)).encode()
+    return _lifted(lambda o, e: _lib.lib().unp_lift_reduction_x(name.encode(), ELEMENT_KINDS[dtype], rank,
+                                                               REDUCE_OPS[op], mask, int(keepdim), n_inputs, bj, pj,
+                                                               b, g, o, e))
 
 
 def lift_scan(name: str, dtype: str, rank: int, op: str, axis: int | None = None, exclusive: bool = False,

@@ -75,6 +75,8 @@ def lib() -> C.CDLL:
         "unp_hip_lower_form": (i32, [C.POINTER(Form), C.POINTER(P), E]),
         "unp_hip_lower_kernel": (i32, [C.c_char_p, C.POINTER(P), E]),
         "unp_lift_reduction": (i32, [C.c_char_p, i32, i32, i32, u32, i32, u32, u32, C.POINTER(C.c_void_p), E]),
+        "unp_lift_reduction_x": (i32, [C.c_char_p, i32, i32, i32, u32, i32, i32, C.c_char_p, C.c_char_p, u32, u32,
+                                       C.POINTER(C.c_void_p), E]),
         "unp_lift_scan": (i32, [C.c_char_p, i32, i32, i32, i32, i32, i32, u32, u32, C.POINTER(C.c_void_p), E]),
         "unp_lift_gather": (i32, [C.c_char_p, i32, i32, i32, i32, i32, u32, u32, C.POINTER(C.c_void_p), E]),
         "unp_kernel_row_reduce2": (i32, [C.c_char_p, i32, i32, i32, u32, u32, C.POINTER(C.c_void_p), E]),

@@ -878,6 +878,147 @@ int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) 
   return UNP_OK;
 }
 
+int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std::string& why) {
+  if (rx.plain) return lower_form(f, L, why);
+  L = Lowered{};
+  L.form = f;
+  L.rx = rx;
+  if (f.rank < 1 || f.rank > 8) {
+    why = "rank is zero or more than 8";
+    return UNP_LIFT_DECLINE;
+  }
+  if (f.dtype != UNP_F32 && f.dtype != UNP_F64) {
+    why = "a reduction with a pre-map body or a fused post at an integer dtype (its integer expressions have no "
+          "spelling here)";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (rx.n_inputs < 1 || rx.n_inputs > 8) {
+    why = "a reduction reads 1 to 8 inputs";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (!reduction_ok(f.dtype, f.op0, why)) return UNP_UNSUPPORTED_KERNEL;
+  const uint32_t mask = reduction_mask(f);
+  if (mask == 0 || (mask >> f.rank) != 0) {
+    why = "a reduced axis outside the rank";
+    return UNP_LIFT_DECLINE;
+  }
+  const char sched = reduction_schedule(mask, f.rank);
+  L.axes_mask = mask;
+  L.red_schedule = sched;
+  L.reduce_all = sched == 'a';
+  L.form.reduced_from = f.rank;
+  for (int32_t d = f.rank - 1; d >= 0 && ((mask >> d) & 1u); --d) L.form.reduced_from = d;
+  const char* T = ctype(f.dtype);
+  std::string pre, post = "r[0]";
+  if (!expr_cpp(rx.body, T, pre, why)) {
+    why = "body: " + why + " has no spelling here";
+    return UNP_UNSUPPORTED_OP;
+  }
+  if (rx.has_post && !expr_cpp(rx.post, T, post, why)) {
+    why = "post: " + why + " has no spelling here";
+    return UNP_UNSUPPORTED_OP;
+  }
+  const int NI = rx.n_inputs;
+  const std::string key = std::string(T) + "|" + std::to_string(NI) + "|" + std::to_string(f.op0) + "|" + sched +
+                          "|" + pre + "|" + (rx.has_post ? post : std::string("-"));
+  char hx[17];
+  std::snprintf(hx, sizeof hx, "%016llx", (unsigned long long)fnv1a64(key));
+  L.name = std::string("unp_xreduce_") + op_name(f.op0) + "_" + lower_name(f.dtype) + "_" + std::string(hx, 8);
+  const std::string ops = L.name + "_ops";
+  std::ostringstream src;
+  src << header(L.name, f);
+  src << "struct " << ops << " {\n  static constexpr bool has_post = " << (rx.has_post ? "true" : "false") << ";\n"
+      << "  static __device__ __forceinline__ double pre(const double* x) { (void)x; return " << pre << "; }\n"
+      << "  static __device__ __forceinline__ double post(const double* r) { (void)r; return " << post << "; }\n};\n";
+  auto sig = [&](std::ostringstream& o) {
+    for (int k = 0; k < NI; ++k) o << "const " << T << "* in" << k << ", ";
+    o << T << "* out";
+  };
+  auto ins = [&](std::ostringstream& o) {
+    o << "  const " << T << "* in[" << NI << "] = {";
+    for (int k = 0; k < NI; ++k) o << (k ? ", " : "") << "in" << k;
+    o << "};\n";
+  };
+  const int V = vec_of(f.dtype);
+  L.threads = 256;
+  if (sched == 'r') {
+    L.blocks_per_cu = 8;
+    for (int fast = 1; fast >= 0; --fast) {
+      Entry e;
+      e.fast = fast;
+      e.vec = fast ? V : 1;
+      e.symbol = L.name + (fast ? "_xwv" : "_xws");
+      src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(";
+      sig(src);
+      src << ", long long rows, long long cols) {\n";
+      ins(src);
+      src << "  unp::xreduce_rows<" << T << ", " << NI << ", " << f.op0 << ", " << ops << ", " << e.vec << ", 256, "
+          << (fast ? 4 : 8) << ">(in, out, rows, cols);\n}\n";
+      L.entries.push_back(e);
+    }
+  } else if (sched == 'a') {
+    L.threads = 512;
+    L.blocks_per_cu = 1;
+    for (int fast = 1; fast >= 0; --fast) {
+      Entry e;
+      e.fast = fast;
+      e.vec = fast ? V : 1;
+      e.symbol = L.name + (fast ? "_xav" : "_xas");
+      src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol << "(";
+      sig(src);
+      src << ", long long n, double* partials, unsigned* counter) {\n";
+      ins(src);
+      src << "  unp::xreduce_all<" << T << ", " << NI << ", " << f.op0 << ", " << ops << ", " << e.vec << ", 512, "
+          << (fast ? 8 : 8) << ">(in, out, n, partials, counter);\n}\n";
+      L.entries.push_back(e);
+    }
+  } else {
+    L.blocks_per_cu = 8;
+    Entry e;
+    e.fast = false;
+    e.vec = 1;
+    e.symbol = L.name + "_xg";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(";
+    sig(src);
+    src << ", unp::axes_desc d) {\n";
+    ins(src);
+    src << "  unp::xreduce_generic<" << T << ", " << NI << ", " << f.op0 << ", " << ops << ", 256>(in, out, d);\n}\n";
+    L.entries.push_back(e);
+  }
+  L.source = src.str();
+  std::ostringstream j;
+  j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"reduction\",\"dtype\":\"" << kind_name(f.dtype)
+    << "\",\"ops\":[\"" << op_name(f.op0) << "\"],\"rank\":" << f.rank << ",\"inputs\":" << NI << ",\"reduced_axes\":[";
+  for (int32_t d = 0, n = 0; d < f.rank; ++d)
+    if ((mask >> d) & 1u) j << (n++ ? "," : "") << d;
+  j << "],\"schedule\":\"" << (sched == 'a' ? "all" : sched == 'r' ? "rows" : "generic") << "\",\"body\":" << json_str(pre)
+    << ",\"post\":" << (rx.has_post ? json_str(post) : std::string("null")) << ",\"params\":[";
+  for (int k = 0; k < NI; ++k) j << "{\"name\":\"in" << k << "\",\"kind\":\"buffer\",\"role\":\"Read\"},";
+  j << "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
+  for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
+  j << "],\"launch\":{\"block\":[" << L.threads << ",1,1],\"grid_policy\":\""
+    << (sched == 'r'   ? "one wave per row, waves stride over rows"
+        : sched == 'a' ? "blocks stride over 16-byte vectors of every input, last-ticket block folds the partials"
+                       : "one wave per output element, lanes stride over the reduced positions")
+    << "\"},\"entries\":[";
+  for (size_t i = 0; i < L.entries.size(); ++i)
+    j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
+      << ",\"when\":\""
+      << (sched == 'm' || sched == 'g' ? "always"
+          : L.entries[i].fast         ? "reduced extent % vec == 0 and every input 16-byte aligned"
+                                      : "otherwise")
+      << "\"}";
+  j << "],\"workspace\":" << (sched == 'a' ? "{\"partials\":\"grid * 8\",\"counter\":4}" : "null")
+    << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
+    << ",\"fidelity_notes\":["
+    << json_str("the body and the post evaluate in f64 and round once per statement, as the kernel evaluator runs the "
+                "lifted kernel; the fold is in f64 in a geometry-fixed order: a Sum/Mean within the declared bound "
+                "gamma_(n-1)*sum|x| of the serial fold, a Max/Min exact except NaN payload and the sign of a zero")
+    << "]}";
+  L.interface_json = j.str();
+  return UNP_OK;
+}
+
 int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail) {
   out = Lowered{};
   out.form = f;

@@ -640,6 +640,148 @@ UNP_DEV void reduce_generic(const T* __restrict__ in, T* __restrict__ out, const
 }
 
 // ---------------------------------------------------------------------------------------
+// Reductions with a pre-map body over NI inputs and a fused post (the reduction lift with a
+// non-plain body or post: kernel_lift.rs:919-941, 987-1003).  Float compute dtypes: at each
+// position the body is evaluated in f64 over the inputs and rounded once to T, the fold runs in
+// f64, the finished fold (Mean divided) is rounded once to T, and the post is evaluated in f64
+// over that value and rounded once at the store.  The emitted source supplies OPS: `pre(x)`
+// over the NI input values and `post(r)` over r[0], both in doubles, and `has_post`.
+// ---------------------------------------------------------------------------------------
+template <class T, int OP, class OPS> UNP_DEV T xfinish(double a, i64 n) {
+  const T red = finish<T, OP>(a, n);
+  if constexpr (OPS::has_post) {
+    const double r[1] = {(double)red};
+    return (T)OPS::post(r);
+  } else {
+    return red;
+  }
+}
+
+// The trailing run: rows x cols, one wave per row (U vectors of each input in flight per lane).
+template <class T, int NI, int OP, class OPS, int VEC, int THREADS, int U>
+UNP_DEV void xreduce_rows(const T* const* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols) {
+  typedef fold<double, OP> F;
+  constexpr i64 STEP = (i64)64 * VEC;
+  const int lane = threadIdx.x & 63;
+  const i64 nwaves = (i64)gridDim.x * (THREADS / 64);
+  for (i64 row = (i64)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6); row < rows; row += nwaves) {
+    double a = F::identity();
+    auto take = [&](const vec<T, VEC> (&v)[NI]) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        double x[NI];
+#pragma unroll
+        for (int k = 0; k < NI; ++k) x[k] = (double)v[k].e[e];
+        a = F::apply(a, (double)(T)OPS::pre(x));
+      }
+    };
+    i64 c = (i64)lane * VEC;
+    for (; c + (U - 1) * STEP < cols; c += U * STEP) {
+      vec<T, VEC> v[U][NI];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int k = 0; k < NI; ++k) v[u][k] = ld_nt<T, VEC>(in[k] + row * cols + c + u * STEP);
+#pragma unroll
+      for (int u = 0; u < U; ++u) take(v[u]);
+    }
+    for (; c < cols; c += STEP) {
+      vec<T, VEC> v[NI];
+#pragma unroll
+      for (int k = 0; k < NI; ++k) v[k] = ld_nt<T, VEC>(in[k] + row * cols + c);
+      take(v);
+    }
+    a = wave_reduce<double, OP>(a);
+    if (lane == 0) out[row] = xfinish<T, OP, OPS>(a, cols);
+  }
+}
+
+// No kept axis: blocks fold grid-strided slices, the last block to arrive folds the partials
+// in block order (the full reduction's protocol; `counter` zero on entry, left zero).
+template <class T, int NI, int OP, class OPS, int VEC, int THREADS, int UNROLL>
+UNP_DEV void xreduce_all(const T* const* __restrict__ in, T* __restrict__ out, i64 n, double* __restrict__ partials,
+                         u32* __restrict__ counter) {
+  typedef fold<double, OP> F;
+  constexpr int WAVES = THREADS / 64;
+  __shared__ double sh[WAVES];
+  __shared__ u32 last;
+  const int tid = threadIdx.x;
+  const i64 STEP = (i64)gridDim.x * THREADS * VEC;
+  double a = F::identity();
+  auto take = [&](const vec<T, VEC> (&v)[NI]) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      double x[NI];
+#pragma unroll
+      for (int k = 0; k < NI; ++k) x[k] = (double)v[k].e[e];
+      a = F::apply(a, (double)(T)OPS::pre(x));
+    }
+  };
+  i64 c = ((i64)blockIdx.x * THREADS + tid) * VEC;
+  for (; c + (UNROLL - 1) * STEP < n; c += UNROLL * STEP) {
+    vec<T, VEC> v[UNROLL][NI];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+      for (int k = 0; k < NI; ++k) v[u][k] = ld_nt<T, VEC>(in[k] + c + u * STEP);
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) take(v[u]);
+  }
+  for (; c < n; c += STEP) {
+    vec<T, VEC> v[NI];
+#pragma unroll
+    for (int k = 0; k < NI; ++k) v[k] = ld_nt<T, VEC>(in[k] + c);
+    take(v);
+  }
+  a = block_reduce<double, OP, THREADS>(a, sh);
+  if (tid == 0) {
+    store_agent(&partials[blockIdx.x], a);
+    last = (arrive_after_stores(counter) == gridDim.x - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (last == 0u) return;
+  double b = F::identity();
+  for (u32 i = tid; i < gridDim.x; i += THREADS) b = F::apply(b, load_agent(&partials[i]));
+  b = block_reduce<double, OP, THREADS>(b, sh);
+  if (tid == 0) {
+    out[0] = xfinish<T, OP, OPS>(b, n);
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Any other reduced-axis set: one wave per output element (as reduce_generic), NI inputs of one
+// shape read at the same offsets.
+template <class T, int NI, int OP, class OPS, int THREADS>
+UNP_DEV void xreduce_generic(const T* const* __restrict__ in, T* __restrict__ out, const axes_desc& d) {
+  typedef fold<double, OP> F;
+  const int lane = threadIdx.x & 63;
+  const i64 nw = (i64)gridDim.x * (THREADS / 64);
+  for (i64 o = (i64)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6); o < d.outs; o += nw) {
+    i64 base = 0, q = o;
+    for (i64 k = d.nk - 1; k >= 0; --k) {
+      const i64 c = q % d.kext[k];
+      q /= d.kext[k];
+      base += c * d.kstr[k];
+    }
+    double a = F::identity();
+    for (i64 t = lane; t < d.count; t += 64) {
+      i64 off = base, u = t;
+      for (i64 k = d.nr - 1; k >= 0; --k) {
+        const i64 c = u % d.rext[k];
+        u /= d.rext[k];
+        off += c * d.rstr[k];
+      }
+      double x[NI];
+#pragma unroll
+      for (int k = 0; k < NI; ++k) x[k] = (double)in[k][off];
+      a = F::apply(a, (double)(T)OPS::pre(x));
+    }
+    a = wave_reduce<double, OP>(a);
+    if (lane == 0) out[o] = xfinish<T, OP, OPS>(a, d.count);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Single-pass scan with decoupled look-back, along the innermost axis of rows x cols.
 //
 // A block tile is BT = WPB * 64 * VEC * K consecutive scan positions of one row.  Blocks are

@@ -78,7 +78,7 @@ std::vector<J> fold_step(int32_t rop, uint32_t acc, uint32_t have, uint32_t val,
 // A float-to-float (or int-to-float) cast that rounds to nearest even (kernel_lift.rs:1027-1034).
 J widen(J e, const char* to) { return e_cast(std::move(e), to); }
 
-// ReductionShape (kernel_lift.rs:838-1025) for one input.
+// ReductionShape (kernel_lift.rs:838-1025).
 struct Shape {
   int32_t dtype;
   uint32_t r;
@@ -86,7 +86,7 @@ struct Shape {
   std::vector<uint32_t> reduced, kept;
   uint32_t acc, have, val, red;
 
-  Shape(int32_t dt, uint32_t rank, uint32_t axes_mask) : dtype(dt), r(rank) {
+  Shape(int32_t dt, uint32_t rank, uint32_t axes_mask, uint32_t n_inputs = 1) : dtype(dt), r(rank), n(n_inputs) {
     if (axes_mask == 0) reduced.push_back(r - 1);
     else
       for (uint32_t d = 0; d < r; ++d)
@@ -112,12 +112,20 @@ struct Shape {
     for (uint32_t d = 0; d < r; ++d) c.push_back(loc(counter(d)));
     return c;
   }
-  std::vector<J> reduce_loop(int32_t rop) const {
-    std::vector<J> inner = {s_load(loaded(0), p_logical(0, counters())), s_let(val, up(loc(loaded(0))))};
+  // reduce_loop (kernel_lift.rs:919-941): one load per input, `val = up(body)` with each
+  // Input(k) bound to the k-th loaded local, the fold step, inside the reduced axes' loops.
+  std::vector<J> reduce_loop(int32_t rop, const J& body) const {
+    std::vector<J> inner;
+    for (uint32_t k = 0; k < n; ++k) inner.push_back(s_load(loaded(k), p_logical(k, counters())));
+    inner.push_back(s_let(val, up(subst_inputs(body))));
     for (auto& s : fold_step(rop, acc, have, val, is_int())) inner.push_back(s);
     for (auto it = reduced.rbegin(); it != reduced.rend(); ++it) inner = for_axis(*it, r, inner);
     return inner;
   }
+  J subst_inputs(const J& body) const;
+  // stored_value (kernel_lift.rs:987-1003): with a fused post, the fold rounded once into `red`
+  // and the post over it.
+  J stored_value(int32_t rop, const J* post, std::vector<J>& body) const;
   std::vector<J> out_coords(bool keepdim) const {
     std::vector<J> c;
     for (uint32_t d = 0; d < r; ++d) {
@@ -141,12 +149,15 @@ struct Shape {
     }
     return (dtype == UNP_F64 || is_int()) ? v : widen(v, EK(dtype));
   }
+  // signature (kernel_lift.rs:1006-1024).
   void signature(uint32_t out_rank, std::vector<J>& params, std::vector<J>& locals) const {
-    params = {param_buffer("in0", EK(dtype), "Read", (int)r), param_buffer("out", EK(dtype), "Write", (int)out_rank)};
+    params.clear();
+    for (uint32_t k = 0; k < n; ++k) params.push_back(param_buffer("in" + std::to_string(k), EK(dtype), "Read", (int)r));
+    params.push_back(param_buffer("out", EK(dtype), "Write", (int)out_rank));
     for (uint32_t d = 0; d < r; ++d) params.push_back(param_scalar("n" + std::to_string(d), "I32", d));
     locals.clear();
     for (uint32_t i = 0; i < 2 * r; ++i) locals.push_back(local_decl("I32"));
-    locals.push_back(local_decl(EK(dtype)));
+    for (uint32_t k = 0; k < n; ++k) locals.push_back(local_decl(EK(dtype)));
     locals.push_back(local_decl(acc_ty()));
     locals.push_back(local_decl("I32"));
     locals.push_back(local_decl(acc_ty()));
@@ -168,22 +179,34 @@ void check_rank(int32_t rank) {
 
 J launch_or_null(uint32_t block, uint32_t grid) { return (block || grid) ? launch_shape(block, grid) : J::null(); }
 
+J input_leaf(uint32_t k);
+J reduced_leaf(uint32_t t);
+void check_reduction_exprs(const J& body, const J* post, uint32_t n_inputs);
+
 // lift_reduction_opdef (kernel_lift.rs:447-484) and lift_reduction_opdef_launched
-// (kernel_lift/block_reduce.rs:50-93).
+// (kernel_lift/block_reduce.rs:50-93): n inputs, a pre-map `body` over them (Input(0) for the
+// plain fold) and an optional fused `post` over Reduced(0) (nullptr for the identity post).
 J lift_reduction(const std::string& name, int32_t dtype, int32_t rank, int32_t rop, uint32_t axes, bool keepdim,
-                 uint32_t block, uint32_t grid) {
+                 uint32_t block, uint32_t grid, uint32_t n_inputs = 1, const J* body_expr = nullptr,
+                 const J* post = nullptr) {
   check_accumulated(dtype, rop, "a reduction");
+  const J plain = input_leaf(0);
+  const J& bexpr = body_expr ? *body_expr : plain;
+  if (post && *post == reduced_leaf(0)) post = nullptr;  // the identity post
+  check_reduction_exprs(bexpr, post, n_inputs);
   check_rank(rank);
   if (axes >> rank) throw Decline{"UnsupportedForm: a reduced axis outside the rank"};
-  const Shape sh(dtype, (uint32_t)rank, axes);
+  const Shape sh(dtype, (uint32_t)rank, axes, n_inputs);
   std::vector<J> params, locals;
   const uint32_t out_rank = keepdim ? sh.r : (uint32_t)sh.kept.size();
   sh.signature(out_rank, params, locals);
   if (!block && !grid) {
     std::vector<J> body = {s_let(sh.acc, sh.fold_identity(rop)), s_let(sh.have, int_(0))};
-    for (auto& s : sh.reduce_loop(rop)) body.push_back(s);
-    body.push_back(s_store(p_logical(sh.n, sh.out_coords(keepdim)), sh.stored(rop)));
+    for (auto& s : sh.reduce_loop(rop, bexpr)) body.push_back(s);
+    const J value = sh.stored_value(rop, post, body);
+    body.push_back(s_store(p_logical(sh.n, sh.out_coords(keepdim)), value));
     for (auto it = sh.kept.rbegin(); it != sh.kept.rend(); ++it) body = for_axis(*it, sh.r, body);
+    if (post) locals.push_back(local_decl(EK(dtype)));  // red: the stage value rounded to the compute dtype
     return kernel_fn(name, EK(dtype), params, locals, body, J::null(), {});
   }
   if (grid == 0 || !pow2(block)) throw Decline{"BadLaunch"};
@@ -198,7 +221,7 @@ J lift_reduction(const std::string& name, int32_t dtype, int32_t rank, int32_t r
     return v;
   };
   std::vector<J> row = {s_let(sh.acc, sh.fold_identity(rop)), s_let(sh.have, int_(0))};
-  std::vector<J> slice = sh.reduce_loop(rop);
+  std::vector<J> slice = sh.reduce_loop(rop, bexpr);
   // Tree::slice (block_reduce.rs:278-288): the outermost reduced loop starts at the thread
   // and steps by the block.
   J& f = slice[0].o[0].second;
@@ -223,7 +246,13 @@ J lift_reduction(const std::string& name, int32_t dtype, int32_t rank, int32_t r
     row.push_back(s_if(e_bin("CmpLt", thread(), uconst(s)), rb, {}));
     row.push_back(s_barrier());
   }
-  row.push_back(s_if(e_bin("CmpEq", thread(), uconst(0)), {s_store(p_logical(sh.n, sh.out_coords(keepdim)), sh.stored(rop))}, {}));
+  {
+    // thread0_stores (block_reduce.rs:292-307)
+    std::vector<J> then;
+    const J value = sh.stored_value(rop, post, then);
+    then.push_back(s_store(p_logical(sh.n, sh.out_coords(keepdim)), value));
+    row.push_back(s_if(e_bin("CmpEq", thread(), uconst(0)), then, {}));
+  }
   std::vector<J> body;
   if (sh.kept.empty()) {
     body = {s_if(e_bin("CmpEq", e_exec("BlockIdx", 0), uconst(0)), row, {})};
@@ -626,6 +655,46 @@ void check_post(const J& e, int64_t available, int64_t n_inputs) {
   for (size_t i : slots) check_post(e.o[0].second.a[i], available, n_inputs);
 }
 
+J input_leaf(uint32_t k) { return var("Input", J::integer(k)); }
+J reduced_leaf(uint32_t t) { return var("Reduced", J::integer(t)); }
+
+// check_reduction (kernel_lift.rs:807-831) and check_common: the body reads only the op's inputs
+// and no Coord, Param, Local, Exec or Reduced leaf; a fused post reads Reduced(0) and no Input.
+void check_reduction_exprs(const J& body, const J* post, uint32_t n_inputs) {
+  check_post(body, 0, (int64_t)n_inputs);
+  if (post) {
+    bool reads_input = false;
+    map_leaves(*post, [&](const J& x, J&) {
+      if (x.t == J::Obj && x.o.size() == 1 && x.o[0].first == "Input") reads_input = true;
+      return false;
+    });
+    if (reads_input) throw Decline{"UnsupportedLeaf: an Input in a reduction post"};
+    check_post(*post, 1, 0);
+  }
+}
+
+J Shape::subst_inputs(const J& body) const {
+  return map_leaves(body, [&](const J& x, J& out) {
+    if (x.t == J::Obj && x.o.size() == 1 && x.o[0].first == "Input") {
+      out = loc(loaded((uint32_t)leaf_index(x)));
+      return true;
+    }
+    return false;
+  });
+}
+
+J Shape::stored_value(int32_t rop, const J* post, std::vector<J>& body) const {
+  if (!post) return stored(rop);
+  body.push_back(s_let(red, stored(rop)));
+  return map_leaves(*post, [&](const J& x, J& out) {
+    if (x.t == J::Obj && x.o.size() == 1 && x.o[0].first == "Reduced") {
+      out = loc(red);
+      return true;
+    }
+    return false;
+  });
+}
+
 // The local ids of row_reduce.rs's `Row`: extents 0..r, counters r..2r, then per phase (each
 // stage, then the epilogue) one loaded local per input, then per stage the F64 accumulator, the
 // have flag, the current F64 value and the rounded stage result.
@@ -966,10 +1035,83 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
     }
   };
   const size_t np = ps.size();
-  // Reduction or scan: in0 Read (rank r), out Write, then r I32 extents.
-  if (np >= 3 && ps[0].buffer && ps[0].role == "Read" && ps[1].buffer && ps[1].role == "Write" &&
-      ps[0].rank >= 1 && (size_t)ps[0].rank + 2 == np) {
-    const int32_t dt = ps[0].elem, r = ps[0].rank, orank = ps[1].rank;
+  // Reduction or scan: in0..in(n-1) Read (rank r, one dtype), out Write, then r I32 extents.
+  // A reduction's body is read back from its `val` Let (the up-cast stripped, the loaded locals
+  // unbound to Input(k)) and a fused post from the output store (Local(red) unbound to
+  // Reduced(0)); each candidate is re-lifted with them and compared as a whole.
+  size_t nin = 0;
+  if (np >= 3 && ps[0].buffer && ps[0].role == "Read" && ps[0].rank >= 1 && (size_t)ps[0].rank + 2 <= np) {
+    nin = np - 1 - (size_t)ps[0].rank;
+    for (size_t i = 0; i < nin && nin; ++i)
+      if (!ps[i].buffer || ps[i].role != "Read" || ps[i].rank != ps[0].rank || ps[i].elem != ps[0].elem) nin = 0;
+    if (nin && !(ps[nin].buffer && ps[nin].role == "Write")) nin = 0;
+    for (size_t i = nin + 1; nin && i < np; ++i)
+      if (ps[i].buffer) nin = 0;
+  }
+  if (nin >= 1 && nin <= 8) {
+    const int32_t dt = ps[0].elem, r = ps[0].rank, orank = ps[nin].rank;
+    const uint32_t n = (uint32_t)nin;
+    J xbody = input_leaf(0), xpost;
+    bool has_post = false, exprs_ok = true;
+    {
+      const uint32_t val = 2 * (uint32_t)r + n + 2, red = val + 1;
+      auto unbind_locals = [&](const J& e, J& o) {
+        bool ok = true;
+        try {
+          o = map_leaves(e, [&](const J& x, J& out2) {
+            if (x.t != J::Obj || x.o.size() != 1 || x.o[0].first != "Local") return false;
+            const int64_t l = leaf_index(x);
+            if (l >= 2 * (int64_t)r && l < 2 * (int64_t)r + (int64_t)n) out2 = input_leaf((uint32_t)(l - 2 * r));
+            else if (l == (int64_t)red) out2 = reduced_leaf(0);
+            else {
+              ok = false;
+              out2 = x;
+            }
+            return true;
+          });
+        } catch (const Decline&) {
+          return false;
+        }
+        return ok;
+      };
+      const J& kb = *k.get("body");
+      const J* let = find_stmt(kb, [&](const J& x) {
+        const J* l = x.get("Let");
+        return l && l->get("local") && l->get("local")->is_int && l->get("local")->i == (int64_t)val;
+      });
+      if (let) {
+        J init = *let->get("Let")->get("init");
+        if (dt == UNP_F32) {
+          const J* c = init.get("Cast");
+          if (c && c->t == J::Arr && c->a.size() == 2) {
+            J operand = c->a[0];
+            init = std::move(operand);
+          } else {
+            exprs_ok = false;
+          }
+        }
+        if (exprs_ok && !unbind_locals(init, xbody)) exprs_ok = false;
+      }
+      const J* store = find_stmt(kb, [&](const J& x) {
+        const J* st = x.get("Store");
+        const J* pl = st ? st->get("place") : nullptr;
+        const J* lg = pl ? pl->get("Logical") : nullptr;
+        return lg && lg->get("buffer") && lg->get("buffer")->is_int && lg->get("buffer")->i == (int64_t)n;
+      });
+      if (exprs_ok && store) {
+        const J& v = *store->get("Store")->get("value");
+        bool reads_red = false;
+        map_leaves(v, [&](const J& x, J&) {
+          if (x.t == J::Obj && x.o.size() == 1 && x.o[0].first == "Local" && leaf_index(x) == (int64_t)red)
+            reads_red = true;
+          return false;
+        });
+        if (reads_red) {
+          has_post = unbind_locals(v, xpost);
+          if (!has_post) exprs_ok = false;
+        }
+      }
+    }
     static const int32_t ops[] = {UNP_OP_SUM, UNP_OP_PROD, UNP_OP_MAX, UNP_OP_MIN, UNP_OP_MEAN};
     // Every reduced-axis set whose output rank matches (ReductionShape::new,
     // kernel_lift.rs:854-870), trailing runs first: the reduction most often asked for.
@@ -983,12 +1125,19 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
         for (int keep = 0; keep <= 1; ++keep) {
           const int32_t want = keep ? r : kept;
           if (orank != want) continue;
-          if (attempt([&] { return lift_reduction(name, dt, r, op, mask, keep, block, grid); })) {
+          if (exprs_ok && attempt([&] {
+                return lift_reduction(name, dt, r, op, mask, keep, block, grid, n, &xbody, has_post ? &xpost : nullptr);
+              })) {
             out.form.kind = UNP_FORM_REDUCTION;
             out.form.dtype = dt;
             out.form.rank = r;
             out.form.op0 = op;
             out.form.axes_mask = mask;
+            out.rx.n_inputs = (int32_t)n;
+            out.rx.body = xbody;
+            out.rx.has_post = has_post;
+            out.rx.post = xpost;
+            out.rx.plain = n == 1 && xbody == input_leaf(0) && !has_post;
             out.form.reduced_from = r;
             for (int32_t d = r - 1; d >= 0 && ((mask >> d) & 1u); --d) out.form.reduced_from = d;
             out.lift = block ? "lift_reduction_opdef_launched" : "lift_reduction_opdef";
@@ -996,7 +1145,7 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
           }
         }
       }
-      if (orank == r) {
+      if (orank == r && n == 1) {
         for (int ex = 0; ex <= 1; ++ex)
           for (int rev = 0; rev <= 1; ++rev)
             if (attempt([&] { return lift_scan(name, dt, r, op, r - 1, ex, rev, block, grid); })) {
@@ -1212,6 +1361,30 @@ int32_t unp_lift_reduction(const char* name, int32_t dtype, int32_t rank, int32_
                            int32_t keepdim, uint32_t block, uint32_t grid, char** json, unp_error* err) {
   return unp::lift_call(json, err, [&] {
     return unp::lift_reduction(name ? name : "reduce", dtype, rank, op, axes_mask, keepdim != 0, block, grid);
+  });
+}
+
+int32_t unp_lift_reduction_x(const char* name, int32_t dtype, int32_t rank, int32_t op, uint32_t axes_mask,
+                             int32_t keepdim, int32_t n_inputs, const char* body_json, const char* post_json,
+                             uint32_t block, uint32_t grid, char** json, unp_error* err) {
+  using unp::kir::J;
+  J body, post;
+  std::string why;
+  if (n_inputs < 1 || n_inputs > 8) {
+    unp::set_error(err, UNP_INVALID_ARGUMENT, "a reduction reads 1 to 8 inputs");
+    return UNP_INVALID_ARGUMENT;
+  }
+  if (!body_json || !unp::kir::parse(body_json, body, why)) {
+    unp::set_error(err, UNP_PARSE_ERROR, "body: a ScalarExpr expected " + why);
+    return UNP_PARSE_ERROR;
+  }
+  if (post_json && !unp::kir::parse(post_json, post, why)) {
+    unp::set_error(err, UNP_PARSE_ERROR, "post: a ScalarExpr expected " + why);
+    return UNP_PARSE_ERROR;
+  }
+  return unp::lift_call(json, err, [&] {
+    return unp::lift_reduction(name ? name : "reduce", dtype, rank, op, axes_mask, keepdim != 0, block, grid,
+                               (uint32_t)n_inputs, &body, post_json ? &post : nullptr);
   });
 }
 

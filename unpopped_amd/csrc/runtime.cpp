@@ -136,7 +136,8 @@ int32_t unp_hip_lower_kernel(const char* kernel_json, unp_generated** out, unp_e
       return rc;
     }
   } else {
-    rc = unp::lower_form(rec.form, g->l, why);
+    rc = rec.form.kind == UNP_FORM_REDUCTION ? unp::lower_reduction_x(rec.form, rec.rx, g->l, why)
+                                            : unp::lower_form(rec.form, g->l, why);
     if (rc != UNP_OK) {
       delete g;
       // A recognised lift whose form this backend has no kernel for is a refusal of the kernel.
@@ -426,6 +427,32 @@ int32_t ensure_ws(unp_exec* x, size_t bytes, bool need_counter, unp_error* err) 
   return UNP_OK;
 }
 
+// The kept and the reduced axes of a row-major input with their element strides, outermost
+// first, adjacent axes of a kind merged (a merged run's stride is its innermost axis's).
+void fill_axes_desc(const std::vector<int64_t>& ext, int32_t rank, uint32_t mask, unp::axes_desc_host& d) {
+  long long stride = 1;
+  std::vector<long long> str((size_t)rank);
+  for (int32_t k = rank - 1; k >= 0; --k) {
+    str[(size_t)k] = stride;
+    stride *= ext[(size_t)k];
+  }
+  for (int32_t k = 0; k < rank;) {
+    const bool red = (mask >> k) & 1u;
+    long long e_ = 1;
+    int32_t e = k;
+    while (e < rank && (((mask >> e) & 1u) != 0) == red) e_ *= ext[(size_t)e++];
+    const long long st = str[(size_t)(e - 1)];
+    if (red) {
+      d.rext[d.nr] = e_;
+      d.rstr[d.nr++] = st;
+    } else {
+      d.kext[d.nk] = e_;
+      d.kstr[d.nk++] = st;
+    }
+    k = e;
+  }
+}
+
 // At least n zeroed ticket counters.  Kernels leave every counter they use at zero, so a
 // larger array is allocated afresh (and zeroed) only when a launch needs more strips.
 int32_t ensure_counters(unp_exec* x, size_t n, unp_error* err) {
@@ -469,7 +496,58 @@ int64_t product(const std::vector<int64_t>& v, size_t from, size_t to) {
   return p;
 }
 
+// A reduction with a pre-map body over NI inputs or a fused post: NI input buffers of the same
+// shape, the output, then the extents.
+int32_t run_xreduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  const unp_form& f = x->l.form;
+  const size_t NI = (size_t)x->l.rx.n_inputs;
+  Args A;
+  int32_t rc = take_args(a, n, NI + 1, (size_t)f.rank, A, err);
+  if (rc == UNP_OK) rc = extents_i32(A, (size_t)f.rank, err);
+  if (rc != UNP_OK) return rc;
+  const uint32_t mask = x->l.axes_mask;
+  long long outs = 1, count = 1;
+  for (int32_t d = 0; d < f.rank; ++d) ((mask >> d) & 1u ? count : outs) *= A.ext[(size_t)d];
+  if ((rc = need_buffers(A, outs > 0, err)) != UNP_OK) return rc;
+  if (outs == 0) return UNP_OK;
+  const int vec = 16 / (int)unp::kind_bytes(f.dtype);
+  std::vector<uint64_t> ptrs(A.buf.begin(), A.buf.end());
+  bool aligned = count % vec == 0;
+  for (size_t k = 0; k < NI; ++k) aligned = aligned && aligned16(ptrs[k]);
+  std::vector<void*> params;
+  for (size_t k = 0; k <= NI; ++k) params.push_back(&ptrs[k]);
+  const char sched = x->l.red_schedule;
+  if (sched == 'r') {
+    long long rows = outs, cols = count;
+    params.push_back(&rows);
+    params.push_back(&cols);
+    const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
+    const long long want = (rows + 3) / 4;
+    return launch(x, aligned ? 0 : 1, (uint32_t)(want < cap ? want : cap), params.data(), s, err);
+  }
+  if (sched == 'a') {
+    const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+    if ((rc = ensure_ws(x, (size_t)grid * 8, true, err)) != UNP_OK) return rc;
+    long long nn = count;
+    void* ws = x->ws;
+    void* cnt = x->counter;
+    params.push_back(&nn);
+    params.push_back(&ws);
+    params.push_back(&cnt);
+    return launch(x, aligned ? 0 : 1, grid, params.data(), s, err);
+  }
+  unp::axes_desc_host d{};
+  fill_axes_desc(A.ext, f.rank, mask, d);
+  d.outs = outs;
+  d.count = count;
+  params.push_back(&d);
+  const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
+  const long long want = (outs + 3) / 4;
+  return launch(x, 0, (uint32_t)(want < cap ? want : cap), params.data(), s, err);
+}
+
 int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  if (!x->l.rx.plain) return run_xreduction(x, a, n, s, err);
   const unp_form& f = x->l.form;
   const bool two = f.kind == UNP_FORM_ROW_REDUCE2;
   Args A;
@@ -521,30 +599,9 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
       void* params[] = {&in, &out, &a, &r, &b, &S, &ws, &cnt};
       return launch(x, entry, (uint32_t)grid, params, s, err);
     }
-    // Any other mask: kept and reduced axes with their element strides, adjacent axes of a
-    // kind merged (a merged run's stride is its innermost axis's).
+    // Any other mask.
     unp::axes_desc_host d{};
-    long long stride = 1;
-    std::vector<long long> str((size_t)f.rank);
-    for (int32_t k = f.rank - 1; k >= 0; --k) {
-      str[(size_t)k] = stride;
-      stride *= A.ext[(size_t)k];
-    }
-    for (int32_t k = 0; k < f.rank;) {
-      const bool red = (mask >> k) & 1u;
-      long long ext = 1;
-      int32_t e = k;
-      while (e < f.rank && (((mask >> e) & 1u) != 0) == red) ext *= A.ext[(size_t)e++];
-      const long long st = str[(size_t)(e - 1)];
-      if (red) {
-        d.rext[d.nr] = ext;
-        d.rstr[d.nr++] = st;
-      } else {
-        d.kext[d.nk] = ext;
-        d.kstr[d.nk++] = st;
-      }
-      k = e;
-    }
+    fill_axes_desc(A.ext, f.rank, mask, d);
     d.outs = outs;
     d.count = count;
     const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;

@@ -63,6 +63,17 @@ struct RowReduceSpec {
   kir::J epilogue;
 };
 
+// A reduction's pre-map body and fused post (the reduction lift's OpDef body and
+// Access::Reduction post, kernel_lift.rs:807-831): `plain` when the body is Input(0) over one
+// input and the post is the identity, which the plain reduction kernels lower.
+struct ReductionExpr {
+  bool plain = true;
+  int32_t n_inputs = 1;
+  kir::J body;  // ScalarExpr over Input(0..n_inputs)
+  bool has_post = false;
+  kir::J post;  // ScalarExpr over Reduced(0)
+};
+
 // A lowered form: what the executor needs to launch it.
 struct Lowered {
   unp_form form{};
@@ -79,11 +90,14 @@ struct Lowered {
   int threads = 256;
   int blocks_per_cu = 8;
   RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only
+  ReductionExpr rx;  // UNP_FORM_REDUCTION: the body and post
 };
 
 // Emit the HIP source and interface for `f`; on refusal returns a nonzero unp_status and
 // fills `detail`.
 int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail);
+// A recognised reduction with its body and post (the plain ones go to lower_form).
+int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& out, std::string& detail);
 // The same for a recognised Access::RowReduce.
 int32_t lower_row_reduce(const RowReduceSpec& spec, Lowered& out, std::string& detail);
 
@@ -93,6 +107,7 @@ int32_t lower_row_reduce(const RowReduceSpec& spec, Lowered& out, std::string& d
 struct Recognized {
   unp_form form{};
   RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only
+  ReductionExpr rx;  // UNP_FORM_REDUCTION only
   std::string lift;
   kir::J launch;
   kir::J params;

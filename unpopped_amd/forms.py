@@ -87,6 +87,38 @@ def reduce_axes(x: np.ndarray, axes: tuple, op: str, keepdim: bool = False) -> n
     return got.reshape(shape)
 
 
+def reduce_expr_executor(dtype: str, rank: int, op: str, axes: tuple, body, post=None, n_inputs: int = 1,
+                         keepdim: bool = False) -> u.Executor:
+    """The reduction lift with a pre-map body and a fused post, lowered, compiled and loaded."""
+    import json
+
+    from . import expr as X
+
+    key = ("reduce_expr", dtype, rank, op, tuple(axes), keepdim, n_inputs, json.dumps(X.as_json(body)),
+           json.dumps(X.as_json(post)) if post is not None else None)
+    if key not in _execs:
+        k = u.lift_reduction("reduce", dtype, rank, op, axes=tuple(axes), keepdim=keepdim, launch=CALLER_LAUNCH,
+                             n_inputs=n_inputs, body=body, post=post)
+        _execs[key] = u.Executor(_backend.lower_kernel(k))
+    return _execs[key]
+
+
+def reduce_expr(inputs, axes: tuple, op: str, body, post=None, keepdim: bool = False) -> np.ndarray:
+    """Fold `body` over the inputs (one shape, float32/float64) along `axes`, then `post`."""
+    xs = [np.ascontiguousarray(a) for a in inputs]
+    x0 = xs[0]
+    axes = tuple(sorted(axes))
+    ex = reduce_expr_executor(NP_KIND[x0.dtype.type], x0.ndim, op, axes, body, post, len(xs), keepdim)
+    kept = tuple(n for d, n in enumerate(x0.shape) if d not in axes)
+    outs = int(np.prod(kept, dtype=np.int64))
+    dins = [u.DeviceBuffer.from_array(a) for a in xs]
+    dout = u.DeviceBuffer(max(outs * x0.itemsize, 1))
+    ex.launch(*dins, dout, *x0.shape)
+    u.synchronize()
+    got = dout.download(x0.dtype, outs)
+    return got.reshape(tuple(1 if d in axes else n for d, n in enumerate(x0.shape)) if keepdim else kept)
+
+
 def reduce_all(x: np.ndarray, op: str):
     kind = NP_KIND[x.dtype.type]
     ex = executor(kind="reduction", dtype=kind, rank=1, op=op, reduced_from=0)
