@@ -479,11 +479,15 @@ static int32_t lower_gather(const unp_form& f, Lowered& L, std::string& why) {
     e.fast = (i == 0);
     e.vec = units[i];
     e.symbol = L.name + (i == 0 ? "_u16" : "_u" + std::to_string(units[i]));
+    // 16-byte units: one wave per block and two blocks per CU, two 8 KiB rows of a wave in
+    // flight (measured best at cfg4's 65536 x 8 KiB); narrower units: four waves per block.
     const int U = units[i] == 16 ? 8 : 16;
-    src << "extern \"C\" __global__ void " << kLaunchBounds << " " << e.symbol
+    e.threads = units[i] == 16 ? 64 : 256;
+    e.blocks_per_cu = units[i] == 16 ? 2 : 1;
+    src << "extern \"C\" __global__ void __launch_bounds__(" << e.threads << ") " << e.symbol
         << "(const unsigned char* table, const " << I << "* ids, unsigned char* out, long long n_rows, "
         << "long long row_bytes, " << I << " src_extent) {\n  unp::gather_rows<" << I << ", " << f.oob << ", "
-        << units[i] << ", 256, " << U << ">(table, ids, out, n_rows, row_bytes, src_extent);\n}\n";
+        << units[i] << ", " << e.threads << ", " << U << ", 2>(table, ids, out, n_rows, row_bytes, src_extent);\n}\n";
     L.entries.push_back(e);
   }
   L.source = src.str();
@@ -496,8 +500,9 @@ static int32_t lower_gather(const unp_form& f, Lowered& L, std::string& why) {
     << "\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
   for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
   j << ",{\"name\":\"src_extent\",\"kind\":\"scalar\",\"dtype\":\"" << kind_name(f.index_dtype)
-    << "\"}],\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
-    << "\",\"grid_policy\":\"one wave per output row, waves stride over rows\"},\"entries\":[";
+    << "\"}],\"launch\":{\"block\":[" << L.entries[0].threads << ",1,1],\"grid\":\"cu_count*"
+    << L.entries[0].blocks_per_cu
+    << "\",\"grid_policy\":\"waves stride over output rows; whole rows of 64 x 8 units two at a time per wave\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"unit_bytes\":" << L.entries[i].vec
       << ",\"when\":\"" << (L.entries[i].fast ? "row bytes % 16 == 0 and table/out 16-byte aligned" : "otherwise")

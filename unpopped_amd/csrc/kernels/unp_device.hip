@@ -1255,10 +1255,10 @@ UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows
 // in UNIT-byte pieces; one wave per output row, waves stride over rows.
 //
 // gfx9 counts loads and stores on one in-order counter (vmcnt), so a wait for a load also
-// waits for every store issued before it.  The id of a wave's next row is therefore loaded
-// right after this row's data loads and before its stores: the one wait per row (for the
-// data) covers it, and the next row starts without a dependent round trip.  A row of
-// exactly 64 * U units moves with no per-lane predicate.
+// waits for every store issued before it.  The ids of a wave's next rows are therefore loaded
+// right after this step's data loads and before its stores: the one wait per step (for the
+// data) covers them, and the next step starts without a dependent round trip.  Rows of
+// exactly 64 * U units move RPW at a time per wave, with no per-lane predicate.
 // ---------------------------------------------------------------------------------------
 template <int UNIT> struct unit_type;
 template <> struct unit_type<16> { typedef u32 elem; static constexpr int n = 4; };
@@ -1272,7 +1272,7 @@ template <class IDX> UNP_DEV bool below_zero(IDX v) {
   else return false;
 }
 
-template <class IDX, int POLICY, int UNIT, int THREADS, int U>
+template <class IDX, int POLICY, int UNIT, int THREADS, int U, int RPW>
 UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ ids, u8* __restrict__ out,
                          i64 n_rows, i64 row_bytes, IDX src_extent) {
   typedef typename unit_type<UNIT>::elem E;
@@ -1281,7 +1281,52 @@ UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ i
   constexpr int WAVES = THREADS / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const i64 units = row_bytes / UNIT;
-  const bool whole = units == 64 * U;
+  if (units == 64 * U) {
+    // Whole rows of 64 * U units: RPW rows of a wave in flight at once (every load of the
+    // RPW rows, then the next ids, then every store).  Table rows are read through the
+    // caches: an id that repeats within a launch is served from L2 or the MALL.
+    const i64 rstride = (i64)gridDim.x * WAVES * RPW;
+    i64 r0 = ((i64)blockIdx.x * WAVES + wave) * RPW;
+    IDX nxt[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) nxt[j] = r0 + j < n_rows ? ids[r0 + j] : (IDX)0;
+    for (; r0 < n_rows; r0 += rstride) {
+      V v[RPW][U];
+      bool take[RPW], zero[RPW];
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) {
+        const IDX raw = nxt[j];
+        const bool live = r0 + j < n_rows;
+        const bool below = below_zero(raw);
+        const bool oob = below || !(raw < src_extent);
+        take[j] = live && !(oob && POLICY != OOB_CLAMP);
+        zero[j] = live && oob && POLICY == OOB_ZEROFILL;
+        if (take[j]) {
+          const IDX cl = below ? (IDX)0 : (oob ? (IDX)(src_extent - (IDX)1) : raw);
+          const E* __restrict__ src = reinterpret_cast<const E*>(table + (i64)cl * row_bytes);
+#pragma unroll
+          for (int k = 0; k < U; ++k) v[j][k] = ld<E, N>(src + ((i64)lane + 64 * k) * N);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) nxt[j] = r0 + rstride + j < n_rows ? ids[r0 + rstride + j] : (IDX)0;
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) {
+        E* __restrict__ dst = reinterpret_cast<E*>(out + (r0 + j) * row_bytes);
+        if (take[j]) {
+#pragma unroll
+          for (int k = 0; k < U; ++k) st_nt<E, N>(dst + ((i64)lane + 64 * k) * N, v[j][k]);
+        } else if (zero[j]) {
+          V z;
+          __builtin_memset(&z, 0, sizeof(V));
+#pragma unroll
+          for (int k = 0; k < U; ++k) st_nt<E, N>(dst + ((i64)lane + 64 * k) * N, z);
+        }
+      }
+    }
+    return;
+  }
+  // Any other row width: a row per wave step, U units of each lane in flight.
   const i64 rstride = (i64)gridDim.x * WAVES;
   i64 r = (i64)blockIdx.x * WAVES + wave;
   IDX next = r < n_rows ? ids[r] : (IDX)0;
@@ -1302,22 +1347,13 @@ UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ i
     }
     const IDX cl = below ? (IDX)0 : (oob ? (IDX)(src_extent - (IDX)1) : raw);
     const E* __restrict__ src = reinterpret_cast<const E*>(table + (i64)cl * row_bytes);
-    if (whole) {
-      V v[U];
-#pragma unroll
-      for (int k = 0; k < U; ++k) v[k] = ld_nt<E, N>(src + ((i64)lane + 64 * k) * N);
-      if (rn < n_rows) next = ids[rn];
-#pragma unroll
-      for (int k = 0; k < U; ++k) st_nt<E, N>(dst + ((i64)lane + 64 * k) * N, v[k]);
-      continue;
-    }
     if (rn < n_rows) next = ids[rn];
     for (i64 u = lane; u < units; u += 64 * U) {
       V v[U];
 #pragma unroll
       for (int k = 0; k < U; ++k) {
         const i64 uu = u + 64 * k;
-        if (uu < units) v[k] = ld_nt<E, N>(src + uu * N);
+        if (uu < units) v[k] = ld<E, N>(src + uu * N);
       }
 #pragma unroll
       for (int k = 0; k < U; ++k) {

@@ -734,7 +734,8 @@ int32_t run_gather(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_e
     return UNP_INVALID_ARGUMENT;
   }
   const size_t entry = pick(x, row_bytes % 16 == 0 && aligned16(table) && aligned16(out));
-  const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+  const int bpc = x->l.entries[entry].blocks_per_cu ? x->l.entries[entry].blocks_per_cu : x->l.blocks_per_cu;
+  const uint32_t grid = (uint32_t)(x->cu_count * bpc);
   long long nr = n_rows, rb = row_bytes;
   void* ext_arg = f.index_dtype == UNP_I32 ? (void*)&ext32 : (f.index_dtype == UNP_U32 ? (void*)&extu32 : (void*)&ext64);
   void* params[] = {&table, &ids, &out, &nr, &rb, ext_arg};
