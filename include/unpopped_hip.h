@@ -108,9 +108,12 @@ enum unp_form_kind {
   UNP_FORM_GATHER = 2,    /* ReadIndex::Indexed gather (kernel_lift/gather.rs:35) */
   UNP_FORM_DEQUANT4 = 3,  /* U4/I4 x f16 scale x 4-bit zero -> bf16 (tests/support/dequant.rs) */
   UNP_FORM_ROW_REDUCE2 = 4, /* two folds of each row read once (Sum and Max: softmax prologue) */
-  UNP_FORM_ROW_REDUCE = 5   /* Access::RowReduce: staged row folds, then a full-width epilogue
+  UNP_FORM_ROW_REDUCE = 5,  /* Access::RowReduce: staged row folds, then a full-width epilogue
                                (kernel_lift/row_reduce.rs:31, row_reduce_launched.rs:47); its
                                expressions come only through unp_hip_lower_kernel */
+  UNP_FORM_DEQUANT_GEMM = 6 /* the dequantizing GEMM (tests/support/dequant.rs:104-181): U4/I4
+                               weights, I32 zero and scale per group, I32 or I8 activations,
+                               I32 out, all wrapping */
 };
 /* ReduceOp subset (crates/unpopped/src/ir.rs:1700). */
 enum unp_reduce_op { UNP_OP_SUM = 0, UNP_OP_PROD = 1, UNP_OP_MAX = 2, UNP_OP_MIN = 3, UNP_OP_MEAN = 4 };
@@ -184,6 +187,17 @@ int32_t unp_kernel_row_reduce2(const char* name, int32_t dtype, int32_t op0, int
  * weight, a U4/I4 zero point and an F16 scale per `group` columns. */
 int32_t unp_kernel_dequant4(const char* name, int32_t q_kind, int32_t z_kind, int32_t group, uint32_t block,
                             uint32_t grid, char** json, unp_error* err);
+/* No reference lift: the dequantizing GEMM of the reference's fixture
+ * (crates/unpopped/tests/support/dequant.rs:104-181; docs/options-u9b-subbyte-dequant.md:28-30)
+ * with the extents as scalars:
+ * out[r][c] = sum over k of (w[r][k] - zero[r][k / group]) * scale[r][k / group] * x[k][c], every
+ * operation an I32 that wraps.  Buffers w (w_kind U4 or I4, R x K, two to a byte, low nibble
+ * first), zero and scale (I32, R x ceil(K / group)), x (x_kind I32 as in the reference, or I8;
+ * K x C), out (I32, R x C); scalars n0 = R, n1 = K, n2 = C.  block = grid = 0: the serial
+ * kernel; otherwise rows grid-strided.  The recognised form carries w_kind in q_kind, x_kind in
+ * dtype and the group in group. */
+int32_t unp_kernel_dequant_gemm(const char* name, int32_t w_kind, int32_t x_kind, int32_t group, uint32_t block,
+                                uint32_t grid, char** json, unp_error* err);
 
 /* lift_row_reduce_opdef (crates/unpopped/src/kernel_lift/row_reduce.rs:31-49) and, with a
  * launch, lift_row_reduce_opdef_launched (kernel_lift/row_reduce_launched.rs:47-86) of the

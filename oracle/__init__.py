@@ -69,6 +69,7 @@ def lib() -> C.CDLL:
             "orc_scan_launched_order_f32": (None, [P, i64, i64, i32, i32, P]),
             "orc_gather_rows": (None, [P, i64, i64, P, i32, i64, i32, P]),
             "orc_dequant4_bf16": (None, [P, i32, P, P, i32, i64, i64, i64, P]),
+            "orc_dequant_gemm_i32": (None, [P, i32, P, P, P, i32, i64, i64, i64, i64, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -176,6 +177,20 @@ def dequant4_bf16(q_packed: np.ndarray, scales_f16_bits: np.ndarray, zeros_packe
     z = np.ascontiguousarray(zeros_packed, dtype=np.uint8)
     out = np.empty(rows * cols, np.uint16)
     lib().orc_dequant4_bf16(_p(q), int(q_signed), _p(s), _p(z), int(z_signed), rows, cols, group, _p(out))
+    return out.reshape(rows, cols)
+
+
+def dequant_gemm_i32(w_packed: np.ndarray, zero: np.ndarray, scale: np.ndarray, x: np.ndarray, rows: int, k: int,
+                     cols: int, group: int, w_signed: bool = False) -> np.ndarray:
+    """The dequantizing GEMM (crates/unpopped/tests/support/dequant.rs:104-181), I32 arithmetic that
+    wraps.  ``x`` is I32 (the reference's activations) or I8, by its numpy dtype."""
+    w = np.ascontiguousarray(w_packed, dtype=np.uint8)
+    z = np.ascontiguousarray(zero, dtype=np.int32)
+    s = np.ascontiguousarray(scale, dtype=np.int32)
+    x_i32 = np.asarray(x).dtype != np.int8
+    xx = np.ascontiguousarray(x, dtype=np.int32 if x_i32 else np.int8)
+    out = np.empty(rows * cols, np.int32)
+    lib().orc_dequant_gemm_i32(_p(w), int(w_signed), _p(z), _p(s), _p(xx), int(x_i32), rows, k, cols, group, _p(out))
     return out.reshape(rows, cols)
 
 

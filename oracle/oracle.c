@@ -387,6 +387,31 @@ void orc_dequant4_bf16(const uint8_t* q, int q_signed, const uint16_t* scale, co
 
 /* ---- row reduction --------------------------------------------------------------------- */
 /* UnaryOp codes: the order of ORC_UNARY_NAMES in oracle/__init__.py. */
+/* The dequantizing GEMM of crates/unpopped/tests/support/dequant.rs:107-181 (ROADMAP U9b S3,
+ * docs/options-u9b-subbyte-dequant.md:28-30): out[r][c] = sum over k of
+ * (w[r][k] - zero[r][k / group]) * scale[r][k / group] * x[k][c], w packed two 4-bit elements to
+ * a byte (U4, or I4 sign-extended), zero and scale I32 per (row, group), the activations int8
+ * widened to I32.  Every operation wraps at 32 bits, as the kernel's I32 arithmetic does; the
+ * groups of a row are ceil(k / group), the last one ragged when group does not divide k. */
+void orc_dequant_gemm_i32(const uint8_t* w, int w_signed, const int32_t* zero, const int32_t* scale, const void* x,
+                          int x_i32, int64_t rows, int64_t k, int64_t cols, int64_t group, int32_t* out) {
+  const int8_t* x8 = (const int8_t*)x;
+  const int32_t* x32 = (const int32_t*)x;
+  const int64_t ng = (k + group - 1) / group;
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < cols; ++c) {
+      uint32_t acc = 0;
+      for (int64_t kk = 0; kk < k; ++kk) {
+        const int64_t gi = r * ng + kk / group;
+        const int32_t wv = w_signed ? orc_i4_load(w, r * k + kk) : orc_u4_load(w, r * k + kk);
+        const uint32_t d = (uint32_t)wv - (uint32_t)zero[gi];
+        const int32_t xv = x_i32 ? x32[kk * cols + c] : (int32_t)x8[kk * cols + c];
+        acc += d * (uint32_t)scale[gi] * (uint32_t)xv;
+      }
+      out[r * cols + c] = (int32_t)acc;
+    }
+}
+
 static double rx_unary(int32_t code, double x, int f32) {
   switch (code) {
     case 0: return -x;                                  /* Neg */

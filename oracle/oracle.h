@@ -60,6 +60,11 @@ void orc_gather_rows(const uint8_t* table, int64_t src_extent, int64_t row_bytes
                      int64_t n_rows, int policy, uint8_t* out);
 
 /* ---- sub-byte dequant ----------------------------------------------------------------- */
+/* The dequantizing GEMM of crates/unpopped/tests/support/dequant.rs:104-181:
+   out[r][c] = sum_k (w[r][k] - zero[r][k/group]) * scale[r][k/group] * x[k][c], every operation an
+   I32 that wraps; w packed 4-bit (I4 sign-extends, U4 zero-extends), x I32 (x_i32) or I8. */
+void orc_dequant_gemm_i32(const uint8_t* w, int w_signed, const int32_t* zero, const int32_t* scale, const void* x,
+                          int x_i32, int64_t rows, int64_t k, int64_t cols, int64_t group, int32_t* out);
 void orc_dequant4_bf16(const uint8_t* q, int q_signed, const uint16_t* scale, const uint8_t* zero, int z_signed,
                        int64_t rows, int64_t cols, int64_t group, uint16_t* out);
 

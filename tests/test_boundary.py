@@ -152,10 +152,12 @@ CASES = [
     (lambda: u.lift_scan("s", "F32", 3, "Max", exclusive=True, reverse=True), "lift_scan_opdef", "unp_scan_excl_rev_max_f32"),
     (lambda: u.lift_scan("s", "I64", 2, "Prod", exclusive=True, launch=(64, 8)), "lift_scan_opdef_launched", "unp_scan_excl_prod_i64"),
     (lambda: u.lift_gather("e", "Bf16", 2, "I32", launch=(256, 4096)), "lift_gather_opdef_launched", "unp_gather_rows_bf16_by_i32_ZeroFill"),
-    (lambda: u.lift_gather("g", "U8", 3, "I64", oob="Skip"), "lift_gather_opdef", "unp_gather_rows_x_by_i64_Skip"),
+    (lambda: u.lift_gather("g", "U8", 3, "I64", oob="Skip"), "lift_gather_opdef", "unp_gather_rows_u8_by_i64_Skip"),
     (lambda: u.lift_gather("g", "F64", 2, "U32", oob="Clamp", launch=(64, 2)), "lift_gather_opdef_launched", "unp_gather_rows_f64_by_u32_Clamp"),
     (lambda: u.kernel_row_reduce2("p", "F32", "Sum", "Max"), "row_reduce2", "unp_rowreduce_sum_max_f32"),
     (lambda: u.kernel_dequant4("d", "I4", "U4", 128, launch=(64, 64)), "dequant4", "unp_dequant_i4_zu4_g128_bf16"),
+    (lambda: u.kernel_dequant_gemm("m", "I4", "I32", 128), "dequant_gemm", "unp_dequant_gemm_i4_g128_i32_i32"),
+    (lambda: u.kernel_dequant_gemm("m", "U4", "I8", 64, launch=(256, 8)), "dequant_gemm", "unp_dequant_gemm_u4_g64_i8_i32"),
 ]
 
 
@@ -256,6 +258,8 @@ def test_lower_form_declines_unsupported_forms():
         (dict(kind="gather", dtype="U4", rank=2), "UnsupportedDtype"),
         (dict(kind="dequant4", out_kind="F32"), "UnsupportedDtype"),
         (dict(kind="dequant4", group=0), "UnsupportedKernel"),
+        (dict(kind="dequant_gemm", q_kind="I8", dtype="I32"), "UnsupportedDtype"),
+        (dict(kind="dequant_gemm", q_kind="U4", dtype="F32"), "UnsupportedDtype"),
         (dict(kind="reduction", dtype="F32", rank=9), "LiftDecline"),
     ]:
         with pytest.raises(_lib.UnpError) as e:
@@ -369,3 +373,25 @@ def test_row_reduce_two_inputs_and_rank_three():
     assert g.interface["inputs"] == 2 and g.interface["rank"] == 3
     assert g.interface["epilogue"] == "((x[0] * r[0]) + x[1])"
     u.HipCompiler().compile(g.source, g.name)
+
+
+def test_dequant_gemm_entries_follow_the_group():
+    """The MFMA entry exists when the group holds whole 32-deep steps; the serial entry always.
+    The chunk staged per LDS pass divides the group."""
+    b = u.HipBackend()
+    for w_kind, x_kind, group, chunk in (("I4", "I32", 128, 128), ("U4", "I32", 512, 128), ("U4", "I8", 1024, 512),
+                                         ("U4", "I8", 96, 96), ("I4", "I32", 7, 0), ("U4", "I8", 48, 0)):
+        g = b.lower_kernel(u.kernel_dequant_gemm("m", w_kind, x_kind, group))
+        assert g.interface["form"] == "dequant_gemm" and g.interface["group"] == group
+        assert g.interface["chunk"] == chunk and (chunk == 0 or group % chunk == 0)
+        syms = [e["symbol"] for e in g.interface["entries"]]
+        assert syms[-1].endswith("_any") and (syms[0].endswith("_mfma") == (chunk > 0))
+
+
+def test_dequant_gemm_refuses_other_element_types():
+    with pytest.raises(_lib.UnpError):
+        u.kernel_dequant_gemm("m", "U4", "F32", 128)
+    k = u.kernel_dequant_gemm("m", "U4", "I32", 128)
+    k["params"][3]["kind"]["Buffer"]["elem"] = "I16"
+    with pytest.raises(_lib.UnpError):
+        u.HipBackend().lower_kernel(k)

@@ -383,6 +383,117 @@ def test_dequant_special_scales(hip_device):
 
 
 # ---------------------------------------------------------------------------------------
+# The dequantizing GEMM (crates/unpopped/tests/support/dequant.rs:104-181;
+# tests/kernel_dequant_gemm.rs): I32 arithmetic that wraps, so every case is bit-exact.
+# ---------------------------------------------------------------------------------------
+
+def _gemm_data(seed, R, K, C, G, x_dtype, full_range=True):
+    r = np.random.default_rng(seed)
+    ng = -(-K // G)
+    w = synth.nibbles(seed, R * K)
+    lo, hi = (-2 ** 31, 2 ** 31) if full_range else (-3, 4)
+    zero = r.integers(lo, hi, size=R * ng, dtype=np.int64).astype(np.int32)
+    scale = r.integers(lo, hi, size=R * ng, dtype=np.int64).astype(np.int32)
+    info = np.iinfo(x_dtype)
+    x = r.integers(int(info.min), int(info.max) + 1, size=K * C, dtype=np.int64).astype(x_dtype)
+    return w, zero, scale, x
+
+
+def _gemm_entry(w_kind, x_dtype, group):
+    kind = "I32" if x_dtype == np.int32 else "I8"
+    return H.executor(kind="dequant_gemm", q_kind=w_kind, dtype=kind, group=group).last_launch()["entry"]
+
+
+def test_dequant_gemm_reference_fixture(hip_device):
+    """kernel_dequant_gemm.rs:26-49 on the fixture of support/dequant.rs:145-181 (R=4, K=8, C=4,
+    GROUP=4): the host loop's answer for I4 and U4 weights, and the two differ."""
+    H.say("[case] dequant GEMM reference fixture")
+    R, K, C, GROUP = 4, 8, 4, 4
+    G = K // GROUP
+    nib = [(r * 5 + k * 3 + 1) % 16 for r in range(R) for k in range(K)]
+    packed = np.array([nib[i] | nib[i + 1] << 4 for i in range(0, len(nib), 2)], np.uint8)
+    zero = np.array([(i % 3) - 1 for i in range(R * G)], np.int32)
+    scale = np.array([1 + (i * 2 % 3) for i in range(R * G)], np.int32)
+    x = np.array([(i * 7 % 9) - 4 for i in range(K * C)], np.int32)
+    answers = []
+    for w_kind, signed in (("I4", True), ("U4", False)):
+        want = np.zeros((R, C), np.int64)
+        for r in range(R):
+            for c in range(C):
+                for k in range(K):
+                    n = nib[r * K + k]
+                    n = n - 16 if signed and n >= 8 else n
+                    g = r * G + k // GROUP
+                    want[r, c] += (n - int(zero[g])) * int(scale[g]) * int(x[k * C + c])
+        got = H.dequant_gemm(packed, zero, scale, x, R, K, C, GROUP, w_kind=w_kind)
+        assert np.array_equal(got, want), w_kind
+        answers.append(got)
+    assert not np.array_equal(answers[0], answers[1])
+
+
+GEMM_MFMA_CASES = [
+    # (R, K, C, group, x dtype): whole groups, C % 4 == 0 -> the MFMA entry
+    (64, 128, 64, 128, np.int32),
+    (130, 384, 132, 128, np.int32),   # ragged row and column tiles
+    (70, 96, 68, 32, np.int32),       # one 32-deep step per group
+    (65, 512, 36, 256, np.int32),     # two chunks per group
+    (1, 256, 4, 64, np.int32),
+    (130, 384, 132, 128, np.int8),
+    (33, 2048, 12, 1024, np.int8),    # two 512-deep chunks per group
+    (200, 1152, 260, 96, np.int8),    # a 96-deep group: three steps
+    (300, 4096, 64, 128, np.int32),
+]
+
+
+@pytest.mark.parametrize("R,K,C,group,xdt", GEMM_MFMA_CASES)
+@pytest.mark.parametrize("w_kind", ["U4", "I4"])
+def test_dequant_gemm_mfma_bit_exact(hip_device, R, K, C, group, xdt, w_kind):
+    H.say(f"[case] dequant GEMM mfma {w_kind} x {np.dtype(xdt).name} {R}x{K}x{C} g{group}")
+    w, zero, scale, x = _gemm_data(R * 7 + K + C, R, K, C, group, xdt)
+    got = H.dequant_gemm(w, zero, scale, x, R, K, C, group, w_kind=w_kind)
+    assert _gemm_entry(w_kind, xdt, group).endswith("_mfma")
+    want = oracle.dequant_gemm_i32(w, zero, scale, x, R, K, C, group, w_signed=w_kind == "I4")
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("R,K,C,group,xdt", [
+    (9, 100, 8, 32, np.int32),   # a ragged last group
+    (17, 128, 5, 64, np.int32),  # C % 4 != 0
+    (6, 70, 3, 7, np.int8),      # a group of 7: no MFMA entry
+    (3, 0, 8, 64, np.int32),     # K = 0: all zeros
+])
+def test_dequant_gemm_serial_entry_bit_exact(hip_device, R, K, C, group, xdt):
+    H.say(f"[case] dequant GEMM serial {np.dtype(xdt).name} {R}x{K}x{C} g{group}")
+    w, zero, scale, x = _gemm_data(R + K * 3 + C, R, max(K, 1), C, group, xdt)
+    w, x = w[: (R * K + 1) // 2] if K else w, x[: K * C] if K else np.zeros(max(C, 1), xdt)
+    if K == 0:
+        zero, scale = np.zeros(1, np.int32), np.zeros(1, np.int32)
+    got = H.dequant_gemm(w, zero, scale, x, R, K, C, group, w_kind="I4")
+    if K:
+        assert _gemm_entry("I4", xdt, group).endswith("_any")
+    want = oracle.dequant_gemm_i32(w, zero, scale, x, R, K, C, group, w_signed=True) if K else np.zeros((R, C), np.int32)
+    assert np.array_equal(got, want)
+
+
+def test_dequant_gemm_mfma_matches_serial_entry_on_unaligned_x(hip_device):
+    """x one element off its alignment forces the serial entry on a shape the MFMA takes; both agree."""
+    H.say("[case] dequant GEMM unaligned x")
+    R, K, C, G = 64, 256, 64, 64
+    w, zero, scale, x = _gemm_data(11, R, K, C, G, np.int32)
+    ex = H.executor(kind="dequant_gemm", q_kind="U4", dtype="I32", group=G)
+    dw, dz, ds = (u.DeviceBuffer.from_array(a) for a in (w, zero, scale))
+    dx = u.DeviceBuffer.from_array(np.concatenate([np.zeros(1, np.int32), x]))
+    do = u.DeviceBuffer(R * C * 4)
+    ex.launch(dw, dz, ds, dx.at(4), do, R, K, C)
+    u.synchronize()
+    assert ex.last_launch()["entry"].endswith("_any")
+    got = do.download(np.int32, R * C).reshape(R, C)
+    want = oracle.dequant_gemm_i32(w, zero, scale, x, R, K, C, G)
+    assert np.array_equal(got, want)
+    assert np.array_equal(H.dequant_gemm(w, zero, scale, x, R, K, C, G), want)
+
+
+# ---------------------------------------------------------------------------------------
 # Reductions over any axis set (ReductionShape::new, kernel_lift.rs:854-870): an outer axis
 # (column sums), a middle run, several runs.  The oracle folds rows of the input with the
 # reduced axes moved last, which keeps the serial lift's row-major order over the reduced

@@ -198,6 +198,90 @@ def test_dequant_gemm_known_answer():
         assert np.array_equal(got, want)
 
 
+def _gemm_fixture():
+    """crates/unpopped/tests/support/dequant.rs:145-163 (R=4, K=8, C=4, GROUP=4)."""
+    R, K, C, GROUP = 4, 8, 4, 4
+    G = K // GROUP
+    nib = [(r * 5 + k * 3 + 1) % 16 for r in range(R) for k in range(K)]
+    packed = np.array([nib[i] | nib[i + 1] << 4 for i in range(0, len(nib), 2)], np.uint8)
+    zero = np.array([(i % 3) - 1 for i in range(R * G)], np.int32)
+    scale = np.array([1 + (i * 2 % 3) for i in range(R * G)], np.int32)
+    x = np.array([(i * 7 % 9) - 4 for i in range(K * C)], np.int32)
+    return R, K, C, GROUP, nib, packed, zero, scale, x
+
+
+def test_dequant_gemm_i32_fixture_known_answer():
+    """The oracle's integer dequant GEMM on the reference's fixture equals the fixture's host
+    answer (support/dequant.rs:166-181), computed here from the nibble formula, for I4 and U4."""
+    R, K, C, GROUP, nib, packed, zero, scale, x = _gemm_fixture()
+    G = K // GROUP
+    xs = x.astype(np.int64).reshape(K, C)
+    answers = []
+    for signed in (False, True):
+        want = np.zeros((R, C), np.int64)
+        for r in range(R):
+            for c in range(C):
+                for k in range(K):
+                    n = nib[r * K + k]
+                    n = n - 16 if signed and n >= 8 else n
+                    g = r * G + k // GROUP
+                    want[r, c] += (n - int(zero[g])) * int(scale[g]) * int(xs[k, c])
+        got = oracle.dequant_gemm_i32(packed, zero, scale, x, R, K, C, GROUP, w_signed=signed)
+        assert np.array_equal(got, want)
+        # the fixture's activations fit I8: the int8-activation form gives the same answer
+        assert np.array_equal(oracle.dequant_gemm_i32(packed, zero, scale, x.astype(np.int8), R, K, C, GROUP,
+                                                      w_signed=signed), want)
+        answers.append(got)
+    # the two weight types give different results, so the check can tell them apart
+    # (kernel_dequant_gemm.rs:52-54)
+    assert not np.array_equal(answers[0], answers[1])
+
+
+def test_dequant_gemm_i32_seeded_mutations_change_the_answer():
+    """docs/options-u9b-subbyte-dequant.md:28-30: nibble order swapped, sign extension dropped,
+    scale group off by one and zero point ignored each move the fixture's answer."""
+    R, K, C, GROUP, nib, packed, zero, scale, x = _gemm_fixture()
+    base = oracle.dequant_gemm_i32(packed, zero, scale, x, R, K, C, GROUP, w_signed=True)
+    swapped = ((packed >> 4) | (packed << 4)).astype(np.uint8)
+    assert not np.array_equal(oracle.dequant_gemm_i32(swapped, zero, scale, x, R, K, C, GROUP, w_signed=True), base)
+    assert not np.array_equal(oracle.dequant_gemm_i32(packed, zero, scale, x, R, K, C, GROUP, w_signed=False), base)
+    shifted = np.roll(scale, 1)
+    assert not np.array_equal(oracle.dequant_gemm_i32(packed, zero, shifted, x, R, K, C, GROUP, w_signed=True), base)
+    assert not np.array_equal(
+        oracle.dequant_gemm_i32(packed, np.zeros_like(zero), scale, x, R, K, C, GROUP, w_signed=True), base)
+
+
+@pytest.mark.parametrize("xdt", [np.int8, np.int32])
+@pytest.mark.parametrize("R,K,C,GROUP", [(7, 96, 5, 32), (3, 100, 9, 7), (16, 256, 33, 128)])
+def test_dequant_gemm_i32_matches_wrapping_int64_einsum(R, K, C, GROUP, xdt):
+    """Random data with full-range I32 scales and zero points: int64 einsum reduced mod 2^32
+    (the ring the kernel's wrapping I32 arithmetic lives in), ragged last group included."""
+    r = np.random.default_rng(R * 1000 + K)
+    G = -(-K // GROUP)
+    nib = r.integers(0, 16, size=R * K)
+    packed = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8) if K % 2 == 0 or R % 2 == 0 else None
+    if packed is None:
+        nib = np.concatenate([nib, [0]])
+        packed = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
+        nib = nib[:-1]
+    zero = r.integers(-2 ** 31, 2 ** 31, size=R * G, dtype=np.int64).astype(np.int32)
+    scale = r.integers(-2 ** 31, 2 ** 31, size=R * G, dtype=np.int64).astype(np.int32)
+    info = np.iinfo(xdt)
+    x = r.integers(int(info.min), int(info.max) + 1, size=K * C, dtype=np.int64).astype(xdt)
+    for signed in (False, True):
+        w = nib.reshape(R, K).astype(np.int64)
+        if signed:
+            w = np.where(w >= 8, w - 16, w)
+        gi = np.arange(K) // GROUP
+        zz = zero.reshape(R, G).astype(np.int64)[:, gi]
+        ss = scale.reshape(R, G).astype(np.int64)[:, gi]
+        d = (((w - zz) % 2 ** 32) * (ss % 2 ** 32)) % 2 ** 32  # (w - z) * s in the ring
+        want = (d @ (x.reshape(K, C).astype(np.int64) % 2 ** 32)) % 2 ** 32
+        want = want.astype(np.uint32).view(np.int32)
+        got = oracle.dequant_gemm_i32(packed, zero, scale, x, R, K, C, GROUP, w_signed=signed)
+        assert np.array_equal(got, want)
+
+
 def test_dequant_special_scales_follow_the_codec():
     rows, cols, group = 2, 64, 8
     ng = cols // group

@@ -30,7 +30,7 @@ ELEMENT_KINDS = {
 }
 REDUCE_OPS = {"Sum": 0, "Prod": 1, "Max": 2, "Min": 3, "Mean": 4}
 OOB_POLICIES = {"Skip": 0, "ZeroFill": 1, "Clamp": 2}
-FORMS = {"reduction": 0, "scan": 1, "gather": 2, "dequant4": 3, "row_reduce2": 4}
+FORMS = {"reduction": 0, "scan": 1, "gather": 2, "dequant4": 3, "row_reduce2": 4, "row_reduce": 5, "dequant_gemm": 6}
 DTYPE_SUPPORT = {0: "Supported", 1: "Unsupported", 2: "NotExpressible"}
 ARTIFACT_KINDS = {0: "Ptx", 1: "Cubin", 2: "HipCodeObject", 3: "SpirV", 4: "Stub"}
 
@@ -178,6 +178,15 @@ def kernel_dequant4(name: str, q_kind: str = "U4", z_kind: str = "U4", group: in
                                                               ELEMENT_KINDS[z_kind], group, b, g, o, e))
 
 
+def kernel_dequant_gemm(name: str, w_kind: str = "U4", x_kind: str = "I32", group: int = 128,
+                        launch: tuple | None = None) -> dict:
+    """The dequantizing GEMM (crates/unpopped/tests/support/dequant.rs:104-181) as a KernelFn dict:
+    buffers w (``w_kind``), zero, scale (I32), x (``x_kind``: I32 or I8), out (I32), scalars R, K, C."""
+    b, g = _geom(launch)
+    return _lifted(lambda o, e: _lib.lib().unp_kernel_dequant_gemm(name.encode(), ELEMENT_KINDS[w_kind],
+                                                                  ELEMENT_KINDS[x_kind], group, b, g, o, e))
+
+
 def lift_row_reduce(name: str, dtype: str, rank: int, stages, epilogue, n_inputs: int = 1,
                     launch: tuple | None = None) -> dict:
     """The Access::RowReduce lift (serial, or launched on ``launch = (block, grid)``) as a KernelFn
@@ -265,7 +274,18 @@ class DeviceBuffer:
     def fill(self, byte: int) -> None:
         check(_lib.lib().unp_hip_memset(self.ptr, byte, self.nbytes), what="hipMemset")
 
+    def at(self, offset: int) -> "DeviceBuffer":
+        """A view ``offset`` bytes into this buffer; it does not own the memory and keeps this
+        buffer alive."""
+        assert 0 <= offset <= self.nbytes
+        v = DeviceBuffer.__new__(DeviceBuffer)
+        v.nbytes, v.ptr, v._owner = self.nbytes - offset, self.ptr + offset, self
+        return v
+
     def free(self) -> None:
+        if getattr(self, "_owner", None) is not None:
+            self.ptr, self._owner = 0, None
+            return
         if self.ptr:
             _lib.lib().unp_hip_free(self.ptr)
             self.ptr = 0

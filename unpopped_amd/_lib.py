@@ -81,6 +81,7 @@ def lib() -> C.CDLL:
         "unp_lift_gather": (i32, [C.c_char_p, i32, i32, i32, i32, i32, u32, u32, C.POINTER(C.c_void_p), E]),
         "unp_kernel_row_reduce2": (i32, [C.c_char_p, i32, i32, i32, u32, u32, C.POINTER(C.c_void_p), E]),
         "unp_kernel_dequant4": (i32, [C.c_char_p, i32, i32, i32, u32, u32, C.POINTER(C.c_void_p), E]),
+        "unp_kernel_dequant_gemm": (i32, [C.c_char_p, i32, i32, i32, u32, u32, C.POINTER(C.c_void_p), E]),
         "unp_lift_row_reduce": (i32, [C.c_char_p, i32, i32, i32, C.c_char_p, C.c_char_p, u32, u32,
                                       C.POINTER(C.c_void_p), E]),
         "unp_hip_compile": (i32, [C.c_char_p, C.c_char_p, u32, C.POINTER(C.POINTER(C.c_uint8)),

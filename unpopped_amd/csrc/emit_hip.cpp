@@ -81,6 +81,8 @@ const char* lower_name(int32_t kind) {
     case UNP_F16: return "f16";
     case UNP_U4: return "u4";
     case UNP_I4: return "i4";
+    case UNP_I8: return "i8";
+    case UNP_U8: return "u8";
     default: return "x";
   }
 }
@@ -583,6 +585,86 @@ static int32_t lower_dequant(const unp_form& f, Lowered& L, std::string& why) {
   return UNP_OK;
 }
 
+// The dequantizing GEMM: the int8 MFMA entry when the group holds whole 32-deep MFMA steps, and
+// a serial entry for any other shape.  KC, the k-values staged in LDS per chunk, is the largest
+// multiple of 32 that divides the group within 512 bytes of an I8 column or 128 of an I32's.
+static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& why) {
+  if (f.q_kind != UNP_U4 && f.q_kind != UNP_I4) {
+    why = "dequant-GEMM weights must be U4 or I4";
+    return UNP_UNSUPPORTED_DTYPE;
+  }
+  if (f.dtype != UNP_I8 && f.dtype != UNP_I32) {
+    why = "dequant-GEMM activations must be I8 or I32";
+    return UNP_UNSUPPORTED_DTYPE;
+  }
+  if (f.group < 1) {
+    why = "a dequant group of zero columns";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  const bool qs = f.q_kind == UNP_I4;
+  const int xb = f.dtype == UNP_I32 ? 4 : 1;
+  const char* xt = xb == 4 ? "int" : "signed char";
+  int kc = 0;
+  for (int c = 32; c <= (xb == 4 ? 128 : 512); c += 32)
+    if (f.group % c == 0) kc = c;
+  std::ostringstream name;
+  name << "unp_dequant_gemm_" << lower_name(f.q_kind) << "_g" << f.group << "_" << lower_name(f.dtype) << "_i32";
+  L.name = name.str();
+  L.threads = 256;
+  L.blocks_per_cu = 8;
+  std::ostringstream src;
+  src << header(L.name, f);
+  const std::string sig = std::string("(const unsigned char* w, const int* zero, const int* scale, const ") + xt +
+                          "* x, int* out, long long R, long long K, long long C)";
+  if (kc) {
+    Entry e;
+    e.fast = true;
+    e.symbol = L.name + "_mfma";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << sig << " {\n  unp::dqgemm_mfma<"
+        << (qs ? "true" : "false") << ", " << xb << ", " << f.group << ", " << kc
+        << ">(w, zero, scale, x, out, R, K, C);\n}\n";
+    L.entries.push_back(e);
+  }
+  {
+    Entry e;
+    e.fast = false;
+    e.symbol = L.name + "_any";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << sig << " {\n  unp::dqgemm_any<"
+        << (qs ? "true" : "false") << ", " << xt << ", 256>(w, zero, scale, x, out, R, K, C, " << f.group
+        << ");\n}\n";
+    L.entries.push_back(e);
+  }
+  L.source = src.str();
+  std::ostringstream j;
+  j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"dequant_gemm\",\"w\":\"" << kind_name(f.q_kind)
+    << "\",\"zero\":\"I32\",\"scale\":\"I32\",\"x\":\"" << kind_name(f.dtype) << "\",\"out\":\"I32\",\"group\":"
+    << f.group << ",\"chunk\":" << kc
+    << ",\"params\":[{\"name\":\"w\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\"" << kind_name(f.q_kind)
+    << "\"},{\"name\":\"zero\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\"I32\"},{\"name\":\"scale\",\"kind\":"
+       "\"buffer\",\"role\":\"Read\",\"dtype\":\"I32\"},{\"name\":\"x\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\""
+    << kind_name(f.dtype)
+    << "\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\",\"dtype\":\"I32\"}"
+    << ",{\"name\":\"n0\",\"kind\":\"scalar\",\"dtype\":\"I32\"},{\"name\":\"n1\",\"kind\":\"scalar\",\"dtype\":\"I32\"},{"
+       "\"name\":\"n2\",\"kind\":\"scalar\",\"dtype\":\"I32\"}]"
+    << ",\"launch\":{\"block\":[256,1,1],\"grid_policy\":\"mfma: one block per 64 x 64 output tile; any: threads "
+       "stride over the outputs\"},\"entries\":[";
+  for (size_t i = 0; i < L.entries.size(); ++i)
+    j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"when\":\""
+      << (L.entries[i].fast ? "K % group == 0, C % 4 == 0, x aligned to 4 elements, w to 8 bytes "
+                              "(v_mfma_i32_32x32x32_i8)"
+                            : "otherwise")
+      << "\"}";
+  j << "],\"workspace\":null"
+    << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
+    << ",\"fidelity_notes\":["
+    << json_str("I32 arithmetic that wraps, regrouped in that ring as sum_g scale * (sum_k w * x - zero * sum_k x); "
+                "the sums of w * x run on the int8 MFMA, I32 activations as four signed byte digits: bit-exact "
+                "against the serial kernel for every input")
+    << "]}";
+  L.interface_json = j.str();
+  return UNP_OK;
+}
+
 // ---- Access::RowReduce ---------------------------------------------------------------------
 
 namespace {
@@ -1037,6 +1119,8 @@ int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail) {
       return lower_gather(f, out, detail);
     case UNP_FORM_DEQUANT4:
       return lower_dequant(f, out, detail);
+    case UNP_FORM_DEQUANT_GEMM:
+      return lower_dequant_gemm(f, out, detail);
     case UNP_FORM_ROW_REDUCE:
       detail = "a row reduction's expressions come only with its KernelFn (Backend::lower_kernel)";
       return UNP_UNSUPPORTED_KERNEL;

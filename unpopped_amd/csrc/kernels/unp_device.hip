@@ -1510,6 +1510,215 @@ UNP_DEV void dequant4_bf16_any(const u8* __restrict__ q, const u16* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------
+// The dequantizing GEMM (crates/unpopped/tests/support/dequant.rs:104-181):
+//   out[r][c] = sum_k (w[r][k] - zero[r][g]) * scale[r][g] * x[k][c],  g = k / G,
+// every operation an I32 that wraps, so the result is the sum in Z / 2^32.  In that ring it
+// regroups exactly as
+//   sum_g scale[r][g] * (P_g[r][c] - zero[r][g] * X_g[c]),
+//   P_g = sum_{k in g} w[r][k] * x[k][c],   X_g[c] = sum_{k in g} x[k][c].
+// With int8 activations P_g is an int8 x int8 product sum: the MFMA's.  An I32 activation is
+// split into four signed byte digits: the bytes of z = (x + 0x808080) ^ 0x808080, read as int8,
+// satisfy x = sum_b 2^(8 b) digit_b(z) mod 2^32 (the low three bytes are biased by 128 into
+// [0, 256) and unbiased as signed bytes; the top byte's sign extension is the wrap).  Then
+// P_g = sum_b 2^(8 b) P_g,b with one int8 MFMA per digit plane.
+// ---------------------------------------------------------------------------------------
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+// Eight packed bytes of 4-bit weights (element i in byte i / 2, low nibble first) as sixteen
+// int8 in element order, sign-extended for I4.
+template <bool QS> UNP_DEV i32x4 unpack16(u64 q) {
+  const u32 a = (u32)q, b = (u32)(q >> 32);
+  u32 lo0 = a & 0x0F0F0F0Fu, hi0 = (a >> 4) & 0x0F0F0F0Fu;
+  u32 lo1 = b & 0x0F0F0F0Fu, hi1 = (b >> 4) & 0x0F0F0F0Fu;
+  if constexpr (QS) {
+    // n | 0xF0 where bit 3 is set: (n & 8) * 0x1E is 0xF0 and never carries out of its byte.
+    lo0 |= ((lo0 & 0x08080808u) * 0x1Eu) & 0xF0F0F0F0u;
+    hi0 |= ((hi0 & 0x08080808u) * 0x1Eu) & 0xF0F0F0F0u;
+    lo1 |= ((lo1 & 0x08080808u) * 0x1Eu) & 0xF0F0F0F0u;
+    hi1 |= ((hi1 & 0x08080808u) * 0x1Eu) & 0xF0F0F0F0u;
+  }
+  i32x4 r;
+  r[0] = (int)__builtin_amdgcn_perm(hi0, lo0, 0x05010400u);
+  r[1] = (int)__builtin_amdgcn_perm(hi0, lo0, 0x07030602u);
+  r[2] = (int)__builtin_amdgcn_perm(hi1, lo1, 0x05010400u);
+  r[3] = (int)__builtin_amdgcn_perm(hi1, lo1, 0x07030602u);
+  return r;
+}
+
+// 4 x 4 byte transpose: byte i of out[j] is byte j of in[i].
+UNP_DEV void transpose4x4(const u32 in[4], u32 out[4]) {
+  const u32 t0 = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // in0.0 in1.0 in0.1 in1.1
+  const u32 t1 = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);  // in2.0 in3.0 in2.1 in3.1
+  const u32 t2 = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // in0.2 in1.2 in0.3 in1.3
+  const u32 t3 = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);  // in2.2 in3.2 in2.3 in3.3
+  out[0] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
+}
+
+template <bool QS> UNP_DEV i32 nibble_at(const u8* w, i64 e) {
+  const u32 b = w[e >> 1];
+  return nibble_value<QS>((e & 1) ? (b >> 4) : (b & 15u));
+}
+
+// Any shape and group: one thread per output element, k in order, u32 (wrapping) arithmetic.
+template <bool QS, class XT, int THREADS>
+UNP_DEV void dqgemm_any(const u8* __restrict__ w, const i32* __restrict__ zero, const i32* __restrict__ scale,
+                        const XT* __restrict__ x, i32* __restrict__ out, i64 R, i64 K, i64 C, i64 G) {
+  const i64 ng = (K + G - 1) / G;
+  for (i64 o = (i64)blockIdx.x * THREADS + threadIdx.x; o < R * C; o += (i64)gridDim.x * THREADS) {
+    const i64 r = o / C, c = o - r * C;
+    u32 acc = 0;
+    for (i64 k = 0; k < K; ++k) {
+      const i64 gi = r * ng + k / G;
+      const u32 d = (u32)nibble_at<QS>(w, r * K + k) - (u32)zero[gi];
+      acc += d * (u32)scale[gi] * (u32)(i32)x[k * C + c];
+    }
+    out[o] = (i32)acc;
+  }
+}
+
+// MFMA: a block computes 64 x 64 outputs, wave (wm, wn) the 32 x 32 tile at (32 wm, 32 wn),
+// with v_mfma_i32_32x32x32_i8.  XB is the activation's width in bytes (1: I8, 4: I32), G the
+// group, KC the k-values staged per chunk (G % KC == 0, KC % 32 == 0).  Per chunk:
+//   1. the x chunk (KC x 64 elements) is loaded coalesced, split into XB digit planes and
+//      transposed 4 x 4 bytes at a time into LDS as columns (xs[plane][c][k]), so a B operand
+//      is one 16-byte LDS read;
+//   2. the 64 columns' digit sums (sdot4) accumulate X_g; at a group's first chunk the rows'
+//      scale and zero * scale go to LDS;
+//   3. each MFMA step's A operand is 8 packed bytes of the lane's row unpacked to 16 int8, its B
+//      the lane's column's 16 bytes of a plane: lane group q of both holds k = 32 t + 16 q + i,
+//      which the MFMA pairs byte for byte.
+// At a group's end each lane rescales its 16 accumulators: total += scale * P - zero * scale * X_g.
+// Needs K % G == 0, C % 4 == 0, x aligned to 4 XB bytes and w to 8 bytes.
+template <bool QS, int XB, int G, int KC>
+UNP_DEV void dqgemm_mfma(const u8* __restrict__ w, const i32* __restrict__ zero, const i32* __restrict__ scale,
+                         const void* __restrict__ xv, i32* __restrict__ out, i64 R, i64 K, i64 C) {
+  static_assert(XB == 1 || XB == 4, "I8 or I32 activations");
+  static_assert(KC % 32 == 0 && G % KC == 0, "whole MFMA steps per chunk, whole chunks per group");
+  constexpr int BM = 64, BN = 64, LS = KC + 16;  // LDS row stride of a column, bytes
+  constexpr int NCH = G / KC;
+  __shared__ __attribute__((aligned(16))) u8 xs[XB * BN * LS];
+  __shared__ u32 xsum[2][BN];
+  __shared__ u32 srow[2][BM], zsrow[2][BM];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const i64 ntn = (C + BN - 1) / BN;
+  const i64 tile_r = ((i64)blockIdx.x / ntn) * BM, tile_c = ((i64)blockIdx.x % ntn) * BN;
+  const i64 ng = K / G;
+  const int q = lane >> 5;  // lane group of the MFMA operands
+  const i64 arow = tile_r + wm * 32 + (lane & 31);
+  const bool arow_live = arow < R;
+  const int bcol = wn * 32 + (lane & 31);  // local column of this lane's B operand
+  const int cq = tid & 15, kq = tid >> 4;  // loader: columns 4 cq .. + 4, rows 4 kq + 64 p .. + 4
+  const i64 c0 = tile_c + 4 * cq;
+  const bool c0_live = c0 < C;
+  u32 total[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) total[v] = 0;
+  for (i64 g = 0; g < ng; ++g) {
+    const int gb = (int)(g & 1);
+    i32x16 P[XB];
+#pragma unroll
+    for (int b = 0; b < XB; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) P[b][v] = 0;
+    u32 xacc = 0;
+#pragma unroll 1
+    for (int ch = 0; ch < NCH; ++ch) {
+      const i64 k0 = g * G + (i64)ch * KC;
+      // 1. x chunk -> digit planes, columns
+#pragma unroll
+      for (int kl = 4 * kq; kl < KC; kl += 64) {
+        u32 rows[XB][4];  // rows[j][i]: row i, column j (XB = 4) or the row's 4 bytes (XB = 1)
+        if constexpr (XB == 1) {
+          const signed char* x = static_cast<const signed char*>(xv);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            rows[0][i] = c0_live ? *reinterpret_cast<const u32*>(x + (k0 + kl + i) * C + c0) : 0u;
+          u32 cols[4];
+          transpose4x4(rows[0], cols);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) *reinterpret_cast<u32*>(xs + (4 * cq + j) * LS + kl) = cols[j];
+        } else {
+          const i32* x = static_cast<const i32*>(xv);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            vec<u32, 4> r4;
+            if (c0_live) r4 = *reinterpret_cast<const vec<u32, 4>*>(x + (k0 + kl + i) * C + c0);
+            else r4.e[0] = r4.e[1] = r4.e[2] = r4.e[3] = 0u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) rows[j][i] = (r4.e[j] + 0x00808080u) ^ 0x00808080u;
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            u32 planes[4];
+            transpose4x4(rows[j], planes);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) *reinterpret_cast<u32*>(xs + (b * BN + 4 * cq + j) * LS + kl) = planes[b];
+          }
+        }
+      }
+      // 2. the rows' scale and zero * scale (rows past R: 0), once per group
+      if (ch == 0 && tid < BM) {
+        const i64 r = tile_r + tid;
+        const u32 sv = r < R ? (u32)scale[r * ng + g] : 0u;
+        const u32 zv = r < R ? (u32)zero[r * ng + g] : 0u;
+        srow[gb][tid] = sv;
+        zsrow[gb][tid] = zv * sv;
+      }
+      __syncthreads();
+      if (tid < BN) {
+#pragma unroll
+        for (int b = 0; b < XB; ++b) {
+          const u32* col = reinterpret_cast<const u32*>(xs + (b * BN + tid) * LS);
+          int acc = 0;
+#pragma unroll 8
+          for (int i = 0; i < KC / 4; ++i) acc = __builtin_amdgcn_sdot4((int)col[i], 0x01010101, acc, false);
+          xacc += (u32)acc << (8 * b);
+        }
+        if (ch == NCH - 1) xsum[gb][tid] = xacc;
+      }
+      // 3. the chunk's MFMA steps
+      const u8* wrow = w + (arow * K + k0) / 2;
+#pragma unroll
+      for (int t = 0; t < KC / 32; ++t) {
+        const u64 packed = arow_live ? *reinterpret_cast<const u64*>(wrow + (32 * t + 16 * q) / 2) : 0ull;
+        const i32x4 a = unpack16<QS>(packed);
+#pragma unroll
+        for (int b = 0; b < XB; ++b) {
+          const i32x4 bv = *reinterpret_cast<const i32x4*>(xs + (b * BN + bcol) * LS + 32 * t + 16 * q);
+          P[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bv, P[b], 0, 0, 0);
+        }
+      }
+      __syncthreads();  // xs is free for the next chunk; xsum is written
+    }
+    // 4. rescale: lane's element v is row 8 (v / 4) + 4 q + v % 4 of the wave tile, column l % 32.
+    // srow, zsrow and xsum alternate between two buffers by group, so the next group's writes
+    // (before its first barrier) never meet this group's reads.
+    const u32 xc = xsum[gb][bcol];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int lr = wm * 32 + 8 * (v >> 2) + 4 * q + (v & 3);
+      u32 p = (u32)P[0][v];
+#pragma unroll
+      for (int b = 1; b < XB; ++b) p += (u32)P[b][v] << (8 * b);
+      total[v] += srow[gb][lr] * p - zsrow[gb][lr] * xc;
+    }
+  }
+  const i64 c = tile_c + bcol;
+  if (c < C) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const i64 r = tile_r + wm * 32 + 8 * (v >> 2) + 4 * q + (v & 3);
+      if (r < R) out[r * C + c] = (i32)total[v];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Access::RowReduce (crates/unpopped/src/ir.rs:2114-2125): per row, NS staged folds, each over
 // a pre expression that may read the inputs and the earlier stages, then a full-width epilogue
 // (softmax, RMSNorm, a centred quotient ...).

@@ -566,6 +566,50 @@ J dequant4(const std::string& name, int32_t qk, int32_t zk, int32_t group, uint3
   return k;
 }
 
+// The dequantizing GEMM of tests/support/dequant.rs:107-181 with the extents as scalars and int8
+// activations: for each row and column, the groups counted without division (as the dequant
+// kernel above), then `acc += (widen(w) - zero) * scale * widen(x)` over k, every operation an I32
+// that wraps, and one store.
+J dequant_gemm(const std::string& name, int32_t wk, int32_t xk, int32_t group, uint32_t block, uint32_t grid) {
+  if (wk != UNP_U4 && wk != UNP_I4) throw Decline{"UnsupportedForm: dequant-GEMM weights are U4 or I4"};
+  if (xk != UNP_I32 && xk != UNP_I8) throw Decline{"UnsupportedForm: dequant-GEMM activations are I32 or I8"};
+  if (group < 1) throw Decline{"UnsupportedForm: a dequant group of zero columns"};
+  const uint32_t Rn = 0, Kn = 1, Cn = 2, R = 3, Cc = 4, NG = 5, G = 6, KK = 7, K = 8, ACC = 9, W = 10, Z = 11, S = 12,
+                 X = 13;
+  const J gi = e_add(e_mul(loc(R), loc(NG)), loc(G));
+  std::vector<J> step = {
+      s_load(W, p_logical(0, {e_add(e_mul(loc(R), loc(Kn)), loc(K))})),
+      s_load(Z, p_logical(1, {gi})),
+      s_load(S, p_logical(2, {gi})),
+      s_load(X, p_logical(3, {e_add(e_mul(loc(K), loc(Cn)), loc(Cc))})),
+      s_assign(ACC, e_add(loc(ACC), e_mul(e_mul(e_sub(e_cast(loc(W), "I32"), loc(Z)), loc(S)), e_cast(loc(X), "I32")))),
+      s_assign(KK, e_add(loc(KK), int_(1))),
+      s_if(e_bin("CmpEq", loc(KK), int_(group)), {s_assign(KK, int_(0)), s_assign(G, e_add(loc(G), int_(1)))}, {}),
+  };
+  std::vector<J> col = {s_let(ACC, int_(0)), s_let(G, int_(0)), s_let(KK, int_(0)),
+                        s_for(K, int_(0), loc(Kn), int_(1), step),
+                        s_store(p_logical(4, {e_add(e_mul(loc(R), loc(Cn)), loc(Cc))}), loc(ACC))};
+  std::vector<J> row = {
+      s_let(NG, int_(0)),
+      s_while(e_bin("CmpLt", e_mul(loc(NG), int_(group)), loc(Kn)), {s_assign(NG, e_add(loc(NG), int_(1)))}),
+      s_for(Cc, int_(0), loc(Cn), int_(1), col),
+  };
+  std::vector<J> body = {s_for(R, int_(0), loc(Rn), int_(1), row)};
+  std::vector<J> params = {param_buffer("w", EK(wk), "Read", 1),   param_buffer("zero", "I32", "Read", 1),
+                           param_buffer("scale", "I32", "Read", 1), param_buffer("x", EK(xk), "Read", 1),
+                           param_buffer("out", "I32", "Write", 1),  param_scalar("n0", "I32", Rn),
+                           param_scalar("n1", "I32", Kn),           param_scalar("n2", "I32", Cn)};
+  std::vector<J> locals;
+  for (int i = 0; i < 10; ++i) locals.push_back(local_decl("I32"));
+  locals.push_back(local_decl(EK(wk)));
+  locals.push_back(local_decl("I32"));
+  locals.push_back(local_decl("I32"));
+  locals.push_back(local_decl(EK(xk)));
+  J k = kernel_fn(name, "I32", params, locals, body, J::null(), {});
+  if (block || grid) grid_stride(k, block, grid);
+  return k;
+}
+
 // ---- Access::RowReduce (kernel_lift/row_reduce.rs, kernel_lift/row_reduce_launched.rs) ------
 
 // The payload items of a ScalarExpr node (crates/unpopped/src/ir.rs:235-420) that are
@@ -1231,6 +1275,34 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
       return UNP_OK;
     }
   }
+  // The dequantizing GEMM: w (U4/I4), zero, scale (I32), x (I32/I8) Read, out (I32) Write, three
+  // I32 extents; the group read back from the in-group counter's wrap test.
+  if (np == 8 && ps[0].buffer && (ps[0].elem == UNP_U4 || ps[0].elem == UNP_I4) && ps[1].buffer &&
+      ps[1].elem == UNP_I32 && ps[2].buffer && ps[2].elem == UNP_I32 && ps[3].buffer &&
+      (ps[3].elem == UNP_I8 || ps[3].elem == UNP_I32) && ps[4].buffer && ps[4].elem == UNP_I32 &&
+      ps[4].role == "Write") {
+    int64_t group = 0;
+    const J* cmp = find_stmt(*k.get("body"), [&](const J& x) {
+      const J* i = x.get("If");
+      const J* cond = i ? i->get("cond") : nullptr;
+      const J* bin = cond ? cond->get("Binary") : nullptr;
+      return bin && bin->t == J::Arr && bin->a.size() == 3 && bin->a[0].t == J::Str && bin->a[0].s == "CmpEq";
+    });
+    if (cmp) {
+      const J* ci = cmp->get("If")->get("cond")->get("Binary")->a[2].get("ConstInt");
+      if (ci && ci->t == J::Arr && !ci->a.empty() && ci->a[0].is_int) group = ci->a[0].i;
+    }
+    if (group >= 1 && group <= (1 << 30) &&
+        attempt([&] { return dequant_gemm(name, ps[0].elem, ps[3].elem, (int32_t)group, block, grid); })) {
+      out.form.kind = UNP_FORM_DEQUANT_GEMM;
+      out.form.q_kind = ps[0].elem;
+      out.form.dtype = ps[3].elem;
+      out.form.out_kind = UNP_I32;
+      out.form.group = (int32_t)group;
+      out.lift = "dequant_gemm";
+      return UNP_OK;
+    }
+  }
   // Access::RowReduce: n inputs (Read, rank r), out (Write, rank r), r I32 extents.  The stage
   // count follows from the locals; each stage's pre and the epilogue are read back from the
   // tree (un-binding the loaded and stage-result locals), each stage's fold from its accumulate
@@ -1410,6 +1482,13 @@ int32_t unp_kernel_row_reduce2(const char* name, int32_t dtype, int32_t op0, int
 int32_t unp_kernel_dequant4(const char* name, int32_t q_kind, int32_t z_kind, int32_t group, uint32_t block,
                             uint32_t grid, char** json, unp_error* err) {
   return unp::lift_call(json, err, [&] { return unp::dequant4(name ? name : "dequant4", q_kind, z_kind, group, block, grid); });
+}
+
+int32_t unp_kernel_dequant_gemm(const char* name, int32_t w_kind, int32_t x_kind, int32_t group, uint32_t block,
+                                uint32_t grid, char** json, unp_error* err) {
+  return unp::lift_call(json, err, [&] {
+    return unp::dequant_gemm(name ? name : "dequant_gemm", w_kind, x_kind, group, block, grid);
+  });
 }
 
 int32_t unp_lift_row_reduce(const char* name, int32_t dtype, int32_t rank, int32_t n_inputs, const char* stages_json,

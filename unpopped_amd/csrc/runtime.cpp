@@ -760,6 +760,30 @@ int32_t run_dequant(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_
   return launch(x, entry, grid, params, s, err);
 }
 
+// The dequantizing GEMM: w, zero, scale, x, out, then R, K, C.  The MFMA entry takes whole
+// groups, 4-column rows of x and aligned operands; anything else runs the serial entry.
+int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  Args A;
+  int32_t rc = take_args(a, n, 5, 3, A, err);
+  if (rc == UNP_OK) rc = extents_i32(A, 3, err);
+  if (rc != UNP_OK) return rc;
+  long long R = A.ext[0], K = A.ext[1], C = A.ext[2];
+  if ((rc = need_buffers(A, R > 0 && C > 0, err)) != UNP_OK) return rc;
+  if (R == 0 || C == 0) return UNP_OK;
+  uint64_t w = A.buf[0], zp = A.buf[1], sc = A.buf[2], xa = A.buf[3], out = A.buf[4];
+  const long long group = x->l.form.group;
+  const uint64_t xalign = x->l.form.dtype == UNP_I32 ? 16 : 4;
+  const long long tiles = ((R + 63) / 64) * ((C + 63) / 64);
+  const bool fast_ok = K % group == 0 && C % 4 == 0 && xa % xalign == 0 && (w & 7) == 0 && (zp & 3) == 0 &&
+                       (sc & 3) == 0 && (out & 3) == 0 && tiles <= 0x7FFFFFFFLL;
+  size_t entry = pick(x, fast_ok);
+  if (x->l.entries[entry].fast && !fast_ok) entry = x->l.entries.size() - 1;
+  const uint32_t grid =
+      x->l.entries[entry].fast ? (uint32_t)tiles : (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+  void* params[] = {&w, &zp, &sc, &xa, &out, &R, &K, &C};
+  return launch(x, entry, grid, params, s, err);
+}
+
 }  // namespace
 
 extern "C" int32_t unp_hip_exec_launch(unp_exec* x, const unp_arg* args, size_t nargs, void* stream,
@@ -787,6 +811,8 @@ extern "C" int32_t unp_hip_exec_launch(unp_exec* x, const unp_arg* args, size_t 
       return run_row_reduce(x, args, nargs, s, err);
     case UNP_FORM_DEQUANT4:
       return run_dequant(x, args, nargs, s, err);
+    case UNP_FORM_DEQUANT_GEMM:
+      return run_dequant_gemm(x, args, nargs, s, err);
     default:
       set_error(err, UNP_UNSUPPORTED_KERNEL, "unknown form");
       return UNP_UNSUPPORTED_KERNEL;

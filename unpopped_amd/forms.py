@@ -34,10 +34,12 @@ def kernel_for(kind: str, dtype: str = "F32", rank: int = 1, op: str = "Sum", op
         return u.lift_gather("gather", dtype, rank, index_dtype, 0, oob, launch=CALLER_LAUNCH)
     if kind == "dequant4":
         return u.kernel_dequant4("dequant", q_kind, z_kind, group, launch=CALLER_LAUNCH)
+    if kind == "dequant_gemm":
+        return u.kernel_dequant_gemm("dequant_gemm", q_kind, dtype, group, launch=CALLER_LAUNCH)
     raise ValueError(kind)
 
 NP_KIND = {np.float32: "F32", np.float64: "F64", np.int32: "I32", np.int64: "I64", np.uint32: "U32",
-           np.uint16: "Bf16", np.uint8: "U8"}
+           np.uint16: "Bf16", np.uint8: "U8", np.int8: "I8"}
 
 
 def executor(**form) -> u.Executor:
@@ -169,6 +171,20 @@ def dequant4(q_packed, scales, zeros_packed, rows, cols, group, q_kind="U4", z_k
     ex.launch(dq, ds, dz, do, rows, cols)
     u.synchronize()
     return do.download(np.uint16, rows * cols).reshape(rows, cols)
+
+
+def dequant_gemm(w_packed, zero, scale, x, rows, k, cols, group, w_kind="U4") -> np.ndarray:
+    """out = sum_k (w - zero) * scale * x over I32 that wraps; x is I32 or I8 by its dtype."""
+    x = np.ascontiguousarray(x)
+    ex = executor(kind="dequant_gemm", q_kind=w_kind, dtype=NP_KIND.get(x.dtype.type, "I8"), group=group)
+    dw = u.DeviceBuffer.from_array(np.ascontiguousarray(w_packed, np.uint8))
+    dz = u.DeviceBuffer.from_array(np.ascontiguousarray(zero, np.int32))
+    ds = u.DeviceBuffer.from_array(np.ascontiguousarray(scale, np.int32))
+    dx = u.DeviceBuffer.from_array(x)
+    do = u.DeviceBuffer(max(rows * cols * 4, 1))
+    ex.launch(dw, dz, ds, dx, do, rows, k, cols)
+    u.synchronize()
+    return do.download(np.int32, rows * cols).reshape(rows, cols)
 
 
 def row_reduce_executor(dtype: str, rank: int, stages, epilogue, n_inputs: int = 1) -> u.Executor:
