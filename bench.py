@@ -362,6 +362,44 @@ def ceilings(u, cus: int, nbytes: int = 1 << 30, reps: int = 10) -> None:
                           "GBps": round(best[0], 1), "frac_of_peak": round(best[0] / PEAK_GBPS, 4)}), flush=True)
 
 
+def gemm_lines(u, synth, steps: int, warmup: int) -> None:
+    """The dequantizing GEMM (tests/support/dequant.rs:104-181) at a weight of LLM size: U4 w
+    8192 x 28672 with an I32 zero point and scale per 128 columns, times x of C columns (I8 and I32),
+    one JSON line per shape.  Bytes are w + zero + scale + x + out; operations 2 R K C."""
+    from unpopped_amd import forms as H
+
+    R, K, G = 8192, 28672, 128
+    ng = K // G
+    w = synth.nibbles(6, R * K)
+    zero = synth.int16_i32(61, R * ng)
+    scale = (synth.int16_i32(62, R * ng) - 8) * 97
+    dw, dz, ds = (u.DeviceBuffer.from_array(a) for a in (w, zero, scale))
+    for xk, xdt in (("I8", np.int8), ("I32", np.int32)):
+        ex = H.executor(kind="dequant_gemm", q_kind="U4", dtype=xk, group=G)
+        for C in (16, 64, 256, 1024):
+            x = (synth.int16_i32(63, K * C) * 13 - 100).astype(xdt)
+            dx, do = u.DeviceBuffer.from_array(x), u.DeviceBuffer(R * C * 4)
+            for _ in range(warmup):
+                ex.launch(dw, dz, ds, dx, do, R, K, C)
+            u.synchronize()
+            e0, e1 = u.Event(), u.Event()
+            e0.record()
+            for _ in range(steps):
+                ex.launch(dw, dz, ds, dx, do, R, K, C)
+            e1.record()
+            e1.synchronize()
+            us = e0.elapsed_ms(e1) * 1e3 / steps
+            nbytes = R * K // 2 + R * ng * 8 + K * C * x.itemsize + R * C * 4
+            ops = 2 * R * K * C
+            log(f"[bench] gemm x {xk} C {C}: {us:.1f} us")
+            print(json.dumps({"gemm": f"U4 {R}x{K} g{G} times {xk} {K}x{C}", "entry": ex.last_launch()["entry"],
+                              "us": round(us, 1), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
+                              "frac_of_hbm_peak": round(nbytes / us / 1e3 / PEAK_GBPS, 4),
+                              "TOPs": round(ops / us / 1e6, 1), "frac_of_int8_mfma_peak": round(ops / us / 1e6 / 5000, 4)}),
+                  flush=True)
+            del dx, do
+
+
 def attach_traffic(per) -> None:
     """HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE passes (each counter scaled
     by what it reads for a plain copy of known size), where a profile covers the kernel."""
@@ -388,6 +426,8 @@ def main() -> int:
                     help="only launch a plain 256 MiB copy (calibrates the HBM byte counters)")
     ap.add_argument("--ceilings", action="store_true",
                     help="only measure this device's streaming read / write / copy rates on 1 GiB")
+    ap.add_argument("--gemm", action="store_true",
+                    help="only time the dequantizing GEMM at LLM shapes (one JSON line per shape)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -406,6 +446,9 @@ def main() -> int:
         return 0
     if args.ceilings:
         ceilings(u, cus)
+        return 0
+    if args.gemm:
+        gemm_lines(u, synth, args.steps, args.warmup)
         return 0
     cases = build_cases(u, synth)
     if args.only:

@@ -376,16 +376,20 @@ def test_row_reduce_two_inputs_and_rank_three():
 
 
 def test_dequant_gemm_entries_follow_the_group():
-    """The MFMA entry exists when the group holds whole 32-deep steps; the serial entry always.
-    The chunk staged per LDS pass divides the group."""
+    """The streaming entry and its prep exist when the group holds whole 64-value chunks, the
+    LDS-transpose MFMA entry when it holds whole 32-deep steps, the serial entry always; each
+    staged chunk divides the group."""
     b = u.HipBackend()
-    for w_kind, x_kind, group, chunk in (("I4", "I32", 128, 128), ("U4", "I32", 512, 128), ("U4", "I8", 1024, 512),
-                                         ("U4", "I8", 96, 96), ("I4", "I32", 7, 0), ("U4", "I8", 48, 0)):
+    for w_kind, x_kind, group, chunk, stream in (("I4", "I32", 128, 128, 64), ("U4", "I32", 512, 128, 64),
+                                                 ("U4", "I8", 1024, 512, 128), ("U4", "I8", 64, 64, 64),
+                                                 ("U4", "I8", 96, 96, 0), ("I4", "I32", 7, 0, 0), ("U4", "I8", 48, 0, 0)):
         g = b.lower_kernel(u.kernel_dequant_gemm("m", w_kind, x_kind, group))
         assert g.interface["form"] == "dequant_gemm" and g.interface["group"] == group
         assert g.interface["chunk"] == chunk and (chunk == 0 or group % chunk == 0)
-        syms = [e["symbol"] for e in g.interface["entries"]]
-        assert syms[-1].endswith("_any") and (syms[0].endswith("_mfma") == (chunk > 0))
+        assert g.interface["stream_chunk"] == stream and (stream == 0 or group % stream == 0)
+        syms = [e["symbol"].rsplit("_", 1)[1] for e in g.interface["entries"]]
+        want = (["stream"] if stream else []) + (["mfma"] if chunk else []) + ["any"] + (["prep"] if stream else [])
+        assert syms == want
 
 
 def test_dequant_gemm_refuses_other_element_types():

@@ -432,16 +432,20 @@ def test_dequant_gemm_reference_fixture(hip_device):
 
 
 GEMM_MFMA_CASES = [
-    # (R, K, C, group, x dtype): whole groups, C % 4 == 0 -> the MFMA entry
+    # (R, K, C, group, x dtype): whole groups.  A group of 64-multiples takes the streaming
+    # entry (split-K with atomics when the tiles are few), another 32-multiple the LDS-transpose
+    # MFMA entry.
     (64, 128, 64, 128, np.int32),
     (130, 384, 132, 128, np.int32),   # ragged row and column tiles
     (70, 96, 68, 32, np.int32),       # one 32-deep step per group
-    (65, 512, 36, 256, np.int32),     # two chunks per group
+    (65, 512, 36, 256, np.int32),     # several chunks per group
     (1, 256, 4, 64, np.int32),
     (130, 384, 132, 128, np.int8),
-    (33, 2048, 12, 1024, np.int8),    # two 512-deep chunks per group
+    (33, 2048, 12, 1024, np.int8),    # eight 128-deep chunks per group
     (200, 1152, 260, 96, np.int8),    # a 96-deep group: three steps
-    (300, 4096, 64, 128, np.int32),
+    (300, 4096, 64, 128, np.int32),   # split-K
+    (257, 8192, 70, 128, np.int8),    # split-K, ragged columns
+    (129, 6144, 33, 64, np.int32),    # split-K, 64-deep groups
 ]
 
 
@@ -451,14 +455,24 @@ def test_dequant_gemm_mfma_bit_exact(hip_device, R, K, C, group, xdt, w_kind):
     H.say(f"[case] dequant GEMM mfma {w_kind} x {np.dtype(xdt).name} {R}x{K}x{C} g{group}")
     w, zero, scale, x = _gemm_data(R * 7 + K + C, R, K, C, group, xdt)
     got = H.dequant_gemm(w, zero, scale, x, R, K, C, group, w_kind=w_kind)
-    assert _gemm_entry(w_kind, xdt, group).endswith("_mfma")
+    assert _gemm_entry(w_kind, xdt, group).endswith("_stream" if group % 64 == 0 else "_mfma")
     want = oracle.dequant_gemm_i32(w, zero, scale, x, R, K, C, group, w_signed=w_kind == "I4")
     assert np.array_equal(got, want)
 
 
+def test_dequant_gemm_repeated_launches_reuse_the_workspace(hip_device):
+    """Two shapes in a row on one executor (the workspace grows, the split-K output is zeroed
+    afresh each launch), then the first shape again."""
+    H.say("[case] dequant GEMM repeated launches")
+    for R, K, C in ((96, 2048, 16), (160, 4096, 96), (96, 2048, 16)):
+        w, zero, scale, x = _gemm_data(R + K + C, R, K, C, 128, np.int8)
+        got = H.dequant_gemm(w, zero, scale, x, R, K, C, 128, w_kind="I4")
+        assert np.array_equal(got, oracle.dequant_gemm_i32(w, zero, scale, x, R, K, C, 128, w_signed=True))
+
+
 @pytest.mark.parametrize("R,K,C,group,xdt", [
     (9, 100, 8, 32, np.int32),   # a ragged last group
-    (17, 128, 5, 64, np.int32),  # C % 4 != 0
+    (17, 128, 5, 32, np.int32),  # C % 4 != 0 with 32-deep groups (64-multiples stream)
     (6, 70, 3, 7, np.int8),      # a group of 7: no MFMA entry
     (3, 0, 8, 64, np.int32),     # K = 0: all zeros
 ])
@@ -475,22 +489,26 @@ def test_dequant_gemm_serial_entry_bit_exact(hip_device, R, K, C, group, xdt):
     assert np.array_equal(got, want)
 
 
-def test_dequant_gemm_mfma_matches_serial_entry_on_unaligned_x(hip_device):
-    """x one element off its alignment forces the serial entry on a shape the MFMA takes; both agree."""
-    H.say("[case] dequant GEMM unaligned x")
+def test_dequant_gemm_entries_agree_by_alignment(hip_device):
+    """One shape through each entry: aligned operands stream; w 8 bytes off a 16-byte boundary
+    takes the LDS-transpose MFMA entry; x one element off its 16-byte boundary as well, the
+    serial entry.  All equal the oracle."""
+    H.say("[case] dequant GEMM entries by alignment")
     R, K, C, G = 64, 256, 64, 64
     w, zero, scale, x = _gemm_data(11, R, K, C, G, np.int32)
-    ex = H.executor(kind="dequant_gemm", q_kind="U4", dtype="I32", group=G)
-    dw, dz, ds = (u.DeviceBuffer.from_array(a) for a in (w, zero, scale))
-    dx = u.DeviceBuffer.from_array(np.concatenate([np.zeros(1, np.int32), x]))
-    do = u.DeviceBuffer(R * C * 4)
-    ex.launch(dw, dz, ds, dx.at(4), do, R, K, C)
-    u.synchronize()
-    assert ex.last_launch()["entry"].endswith("_any")
-    got = do.download(np.int32, R * C).reshape(R, C)
     want = oracle.dequant_gemm_i32(w, zero, scale, x, R, K, C, G)
-    assert np.array_equal(got, want)
-    assert np.array_equal(H.dequant_gemm(w, zero, scale, x, R, K, C, G), want)
+    ex = H.executor(kind="dequant_gemm", q_kind="U4", dtype="I32", group=G)
+    dz, ds = (u.DeviceBuffer.from_array(a) for a in (zero, scale))
+    dw, dx = u.DeviceBuffer.from_array(w), u.DeviceBuffer.from_array(x)
+    dw8 = u.DeviceBuffer.from_array(np.concatenate([np.zeros(8, np.uint8), w]))
+    dx4 = u.DeviceBuffer.from_array(np.concatenate([np.zeros(1, np.int32), x]))
+    for wb, xb, entry in ((dw, dx, "_stream"), (dw8.at(8), dx, "_mfma"), (dw8.at(8), dx4.at(4), "_any")):
+        do = u.DeviceBuffer(R * C * 4)
+        do.fill(0x5A)
+        ex.launch(wb, dz, ds, xb, do, R, K, C)
+        u.synchronize()
+        assert ex.last_launch()["entry"].endswith(entry)
+        assert np.array_equal(do.download(np.int32, R * C).reshape(R, C), want), entry
 
 
 # ---------------------------------------------------------------------------------------

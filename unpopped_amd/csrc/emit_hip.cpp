@@ -607,6 +607,10 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
   int kc = 0;
   for (int c = 32; c <= (xb == 4 ? 128 : 512); c += 32)
     if (f.group % c == 0) kc = c;
+  // The streaming schedule: groups of whole 64-value chunks.  Stage chunk 128 (I8, when it
+  // divides the group) or 64; four waves stacked over 128 rows and 32 columns; NS stages.
+  const int skc = f.group % 64 != 0 ? 0 : (xb == 1 && f.group % 128 == 0 ? 128 : 64);
+  const int swr = 4, swc = 1, sns = 4;
   std::ostringstream name;
   name << "unp_dequant_gemm_" << lower_name(f.q_kind) << "_g" << f.group << "_" << lower_name(f.dtype) << "_i32";
   L.name = name.str();
@@ -616,6 +620,19 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
   src << header(L.name, f);
   const std::string sig = std::string("(const unsigned char* w, const int* zero, const int* scale, const ") + xt +
                           "* x, int* out, long long R, long long K, long long C)";
+  if (skc) {
+    Entry e;
+    e.fast = true;
+    e.symbol = L.name + "_stream";
+    e.vec = 32 * swr;  // rows per block
+    e.k = 32 * swc;    // columns per block
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol
+        << "(const unsigned char* w, const int* zero, const int* scale, const unsigned char* xp, const unsigned* xsum, "
+           "int* out, long long R, long long K, long long C, long long Cp, long long S) {\n  unp::dqg_stream<"
+        << (qs ? "true" : "false") << ", " << xb << ", " << f.group << ", " << skc << ", " << swr << ", " << swc << ", "
+        << sns << ">(w, zero, scale, xp, xsum, out, R, K, C, Cp, S);\n}\n";
+    L.entries.push_back(e);
+  }
   if (kc) {
     Entry e;
     e.fast = true;
@@ -634,11 +651,21 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
         << ");\n}\n";
     L.entries.push_back(e);
   }
+  if (skc) {
+    Entry e;
+    e.fast = false;
+    e.symbol = L.name + "_prep";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(const " << xt
+        << "* x, unsigned char* xp, unsigned* xsum, long long K, long long C, long long Cp, long long G, int* out, "
+           "long long n_out) {\n  unp::dqg_prep<"
+        << xt << ", " << xb << ", " << skc << ">(x, xp, xsum, K, C, Cp, G, out, n_out);\n}\n";
+    L.entries.push_back(e);
+  }
   L.source = src.str();
   std::ostringstream j;
   j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"dequant_gemm\",\"w\":\"" << kind_name(f.q_kind)
     << "\",\"zero\":\"I32\",\"scale\":\"I32\",\"x\":\"" << kind_name(f.dtype) << "\",\"out\":\"I32\",\"group\":"
-    << f.group << ",\"chunk\":" << kc
+    << f.group << ",\"chunk\":" << kc << ",\"stream_chunk\":" << skc
     << ",\"params\":[{\"name\":\"w\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\"" << kind_name(f.q_kind)
     << "\"},{\"name\":\"zero\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\"I32\"},{\"name\":\"scale\",\"kind\":"
        "\"buffer\",\"role\":\"Read\",\"dtype\":\"I32\"},{\"name\":\"x\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\""
@@ -646,15 +673,25 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
     << "\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\",\"dtype\":\"I32\"}"
     << ",{\"name\":\"n0\",\"kind\":\"scalar\",\"dtype\":\"I32\"},{\"name\":\"n1\",\"kind\":\"scalar\",\"dtype\":\"I32\"},{"
        "\"name\":\"n2\",\"kind\":\"scalar\",\"dtype\":\"I32\"}]"
-    << ",\"launch\":{\"block\":[256,1,1],\"grid_policy\":\"mfma: one block per 64 x 64 output tile; any: threads "
-       "stride over the outputs\"},\"entries\":[";
-  for (size_t i = 0; i < L.entries.size(); ++i)
-    j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"when\":\""
-      << (L.entries[i].fast ? "K % group == 0, C % 4 == 0, x aligned to 4 elements, w to 8 bytes "
-                              "(v_mfma_i32_32x32x32_i8)"
-                            : "otherwise")
+    << ",\"launch\":{\"block\":[256,1,1],\"grid_policy\":\"stream: a prep launch over (group, 64 columns), then "
+       "(row tiles x splits, rounded up to 8) x column tiles blocks of 128 x 32 outputs, the splits adding into out "
+       "with atomics; mfma: one block per 64 x 64 output tile; any: threads stride over the outputs\"},\"entries\":[";
+  for (size_t i = 0; i < L.entries.size(); ++i) {
+    const std::string& sym = L.entries[i].symbol;
+    const bool is_stream = sym.size() > 7 && sym.compare(sym.size() - 7, 7, "_stream") == 0;
+    const bool is_prep = sym.size() > 5 && sym.compare(sym.size() - 5, 5, "_prep") == 0;
+    j << (i ? "," : "") << "{\"symbol\":\"" << sym << "\",\"when\":\""
+      << (is_stream ? "K % group == 0, w 16-byte aligned; after the prep launch (LDS-staged DMA, "
+                      "v_mfma_i32_32x32x32_i8)"
+                    : is_prep ? "before the stream entry: x repacked into digit planes and group column sums"
+                              : L.entries[i].fast ? "K % group == 0, C % 4 == 0, x aligned to 4 elements, w to 8 "
+                                                    "bytes (v_mfma_i32_32x32x32_i8)"
+                                                  : "otherwise")
       << "\"}";
-  j << "],\"workspace\":null"
+  }
+  j << "],\"workspace\":" << (skc ? "\"stream: K x Cp x planes bytes of repacked x, then (K / group x Cp + 64) u32 column "
+                                    "sums (Cp = C rounded up to 64)\""
+                                  : "null")
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["
     << json_str("I32 arithmetic that wraps, regrouped in that ring as sum_g scale * (sum_k w * x - zero * sum_k x); "

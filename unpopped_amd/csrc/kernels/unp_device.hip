@@ -1719,6 +1719,231 @@ UNP_DEV void dqgemm_mfma(const u8* __restrict__ w, const i32* __restrict__ zero,
 }
 
 // ---------------------------------------------------------------------------------------
+// The streaming schedule for whole groups of 64-multiples (G % KC == 0, KC % 64 == 0).
+//
+// A pre-pass repacks x once into x' (MFMA-ready digit planes) and the group column sums:
+//   x'[kc][b][kseg][c][16 bytes]: digit plane b of x[kc KC + 16 kseg + i][c], i < 16, for
+//     chunk kc (KC k-values), columns c < Cp (a multiple of 64; columns past C are 0);
+//   xsum[g][c] = sum_{k in g} x[k][c] (wrapping), Cp entries per group and 64 spare at the end.
+// It also zeroes out when the main kernel accumulates split-K parts with atomics.
+//
+// The main kernel: a block owns BM = 32 WR rows x BN = 32 WC columns, one 32 x 32 MFMA tile per
+// wave, and a range of whole groups (split-K: parts add into out with u32 atomics, which are
+// exact and order-free in Z / 2^32).  It streams the chunks of its range through NS LDS stages
+// with global->LDS DMA: per chunk the w rows (16-byte segments, segment-major so a wave's A
+// reads are contiguous), the x' columns, the rows' scales and zero points and the group's
+// column sums.  Each wave issues a fixed share of a stage's DMA ops; at the top of chunk i it
+// waits until only its ops of the NS - 2 younger stages are outstanding, a barrier makes the
+// whole stage visible and retires the stage read last, and the wave refills that stage with
+// chunk i + NS - 1 (clamped to the range, so every pass issues the same ops).  No other
+// vector memory operation is in flight inside the loop, so the wait counts are exact.  The
+// stages are distinct __shared__ objects and the loop has no branch between a DMA and the
+// reads of its stage: the compiler can then tell that a read of one stage does not depend on
+// the DMA into another and inserts no wait of its own (a branch, such as waits that differ
+// by wave, makes it drain every DMA once per pass of the unrolled loop).
+// ---------------------------------------------------------------------------------------
+template <class XT, int XB, int KC>
+UNP_DEV void dqg_prep(const XT* __restrict__ x, u8* __restrict__ xp, u32* __restrict__ xsum, i64 K, i64 C,
+                      i64 Cp, i64 G, i32* __restrict__ out, i64 n_out) {
+  static_assert(KC % 64 == 0, "chunks of whole 16-value segments and MFMA step pairs");
+  __shared__ u32 part[4][64];
+  const int tid = threadIdx.x, cl = tid & 63, t4 = tid >> 6;
+  const i64 slabs = Cp / 64;
+  const i64 g = (i64)blockIdx.x / slabs, c = ((i64)blockIdx.x % slabs) * 64 + cl;
+  const bool live = c < C;
+  u32 sum = 0;
+  for (i64 ks = t4; ks < G / 16; ks += 4) {
+    const i64 k0 = g * G + ks * 16;
+    u32 wd[XB][4];
+#pragma unroll
+    for (int b = 0; b < XB; ++b)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wd[b][e] = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const u32 v = live ? (u32)(i32)x[(k0 + i) * C + c] : 0u;
+      sum += v;
+      const u32 z = XB == 4 ? ((v + 0x00808080u) ^ 0x00808080u) : (v & 0xFFu);
+#pragma unroll
+      for (int b = 0; b < XB; ++b) wd[b][i >> 2] |= ((z >> (8 * b)) & 0xFFu) << (8 * (i & 3));
+    }
+    const i64 kc = k0 / KC, kseg = (k0 % KC) / 16;
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+      vec<u32, 4> o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o.e[e] = wd[b][e];
+      *reinterpret_cast<vec<u32, 4>*>(xp + (((kc * XB + b) * (KC / 16) + kseg) * Cp + c) * 16) = o;
+    }
+  }
+  part[t4][cl] = sum;
+  __syncthreads();
+  if (t4 == 0) xsum[g * Cp + c] = part[0][cl] + part[1][cl] + part[2][cl] + part[3][cl];
+  for (i64 o = (i64)blockIdx.x * 256 + tid; o < n_out; o += (i64)gridDim.x * 256) out[o] = 0;
+}
+
+// A block barrier for LDS stages filled by DMA: s_barrier as a compiler memory barrier and no
+// fence.  A fence would make every wave wait for all of its DMA (vmcnt(0)), including the
+// stages still meant to be in flight; the caller has already waited for the stage it reads,
+// and its earlier LDS reads have all returned (their values were consumed).
+UNP_DEV void dma_stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int BM, int BN, int KC, int XB> struct dqg_stage {
+  u8 a[BM * KC / 2];  // w: segment s of row r (16 bytes) at (s * BM + r) * 16
+  u8 b[XB * KC * BN];  // x': plane p, segment ks, column c at ((p * KC / 16 + ks) * BN + c) * 16
+  u32 s[BM];           // the rows' scales
+  u32 z[BM];           // the rows' zero points
+  u32 x[64];           // the group's column sums (BN used)
+};
+
+template <bool QS, int XB, int G, int KC, int WR, int WC, int NS>
+UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, const i32* __restrict__ scale,
+                        const u8* __restrict__ xp, const u32* __restrict__ xsum, i32* __restrict__ out, i64 R,
+                        i64 K, i64 C, i64 Cp, i64 S) {
+  static_assert(WR * WC == 4 && KC % 64 == 0 && G % KC == 0 && NS >= 3, "four waves, whole chunks");
+  constexpr int BM = 32 * WR, BN = 32 * WC;
+  typedef dqg_stage<BM, BN, KC, XB> St;
+  constexpr int NA = BM * KC / 2 / 1024, NB = XB * KC * BN / 1024, NSZ = BM / 64;
+  static_assert(NA * 1024 == BM * KC / 2 && NB * 1024 == XB * KC * BN && NSZ * 64 == BM, "whole 64-lane ops");
+  constexpr int OA = (NA + 3) / 4, OB = (NB + 3) / 4, OS = (2 * NSZ + 3) / 4;
+  constexpr int OPW = OA + OB + OS + 1;  // DMA ops per wave per stage
+  static_assert((NS - 2) * OPW < 64, "the wait count fits vmcnt");
+  __shared__ __attribute__((aligned(16))) St st0;
+  __shared__ __attribute__((aligned(16))) St st1;
+  __shared__ __attribute__((aligned(16))) St st2;
+  __shared__ __attribute__((aligned(16))) St st3;
+  __shared__ __attribute__((aligned(16))) St st4;
+  __shared__ __attribute__((aligned(16))) St st5;
+  static_assert(NS <= 6, "at most six stages");
+  St* const stages[6] = {&st0, &st1, &st2, &st3, &st4, &st5};
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave / WC, wc = wave % WC, q = lane >> 5, l32 = lane & 31;
+  const i64 ng = K / G;
+  const i64 tiles_r = (R + BM - 1) / BM, tiles_c = (C + BN - 1) / BN;
+  const i64 units = tiles_r * S;
+  // XCD-aware: consecutive blocks go to the eight XCDs in turn; the column tiles of one
+  // (row tile, split) unit take consecutive slots of one XCD, so they share its L2 for w.
+  const i64 xcd = (i64)blockIdx.x % 8, slot = (i64)blockIdx.x / 8;
+  const i64 u = (slot / tiles_c) * 8 + xcd, ct = slot % tiles_c;
+  if (u >= units) return;
+  const i64 rt = u / S, split = u % S;
+  const i64 tile_r = rt * BM, tile_c = ct * BN;
+  const i64 g0 = ng * split / S, g1 = ng * (split + 1) / S;
+  const i64 cpg = G / KC;                        // chunks per group
+  const i64 c0 = g0 * cpg, n = (g1 - g0) * cpg;  // this block's chunks
+  const i64 wbytes_row = K / 2;
+
+  // A stage's DMA: every wave issues the same sequence, OA ops of w rows, OB of x' columns, OS
+  // of scales or zero points (16-byte ops move 1 KiB, 4-byte ops 256 B) and one of the column
+  // sums, so every wave waits on the same count with no branch.  Where a kind has fewer ops
+  // than waves the extra ones repeat an op of that kind: both DMAs write the same bytes.
+  auto issue_stage = [&](St* stp, i64 i) {
+    const i64 chunk = c0 + (i < n ? i : n - 1);
+    const i64 k0 = chunk * KC, g = k0 / G;
+#pragma unroll
+    for (int m = 0; m < OA; ++m) {
+      const int o = (wave + 4 * m) % NA, sl = o * 64 + lane, seg = sl / BM, r = sl % BM;
+      const i64 row = tile_r + r < R ? tile_r + r : R - 1;
+      __builtin_amdgcn_global_load_lds(w + row * wbytes_row + k0 / 2 + 16 * seg, (lds_void*)(stp->a + o * 1024), 16, 0, 0);
+    }
+#pragma unroll
+    for (int m = 0; m < OB; ++m) {
+      const int o = (wave + 4 * m) % NB, sl = o * 64 + lane, c = sl % BN, rest = sl / BN;
+      const int pl = rest / (KC / 16), ks = rest % (KC / 16);
+      __builtin_amdgcn_global_load_lds(xp + (((chunk * XB + pl) * (KC / 16) + ks) * Cp + tile_c + c) * 16,
+                                       (lds_void*)(stp->b + o * 1024), 16, 0, 0);
+    }
+#pragma unroll
+    for (int m = 0; m < OS; ++m) {
+      const int o = (wave + 4 * m) % (2 * NSZ), which = o / NSZ, part = o % NSZ;
+      const i64 r = tile_r + part * 64 + lane;
+      const i64 row = r < R ? r : R - 1;
+      __builtin_amdgcn_global_load_lds((which == 0 ? scale : zero) + row * ng + g,
+                                       (lds_void*)((which == 0 ? stp->s : stp->z) + part * 64), 4, 0, 0);
+    }
+    __builtin_amdgcn_global_load_lds(xsum + g * Cp + tile_c + lane, (lds_void*)stp->x, 4, 0, 0);
+  };
+
+  i32x16 P[XB];
+#pragma unroll
+  for (int b = 0; b < XB; ++b)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) P[b][v] = 0;
+  u32 total[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) total[v] = 0;
+
+  auto compute = [&](const St* stp, i64 i) {
+#pragma unroll
+    for (int j = 0; j < KC / 64; ++j) {
+      const vec<u32, 4> araw = *reinterpret_cast<const vec<u32, 4>*>(stp->a + ((2 * j + q) * BM + 32 * wr + l32) * 16);
+      const i32x4 a0 = unpack16<QS>((u64)araw.e[0] | ((u64)araw.e[1] << 32));
+      const i32x4 a1 = unpack16<QS>((u64)araw.e[2] | ((u64)araw.e[3] << 32));
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int ks = 4 * j + 2 * q + h;
+#pragma unroll
+        for (int b = 0; b < XB; ++b) {
+          const i32x4 bv = *reinterpret_cast<const i32x4*>(stp->b + ((b * (KC / 16) + ks) * BN + 32 * wc + l32) * 16);
+          P[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? a1 : a0, bv, P[b], 0, 0, 0);
+        }
+      }
+    }
+    if (cpg == 1 || (i + 1) % cpg == 0) {
+      // The group ends: lane element v is row 8 (v / 4) + 4 q + v % 4 of the wave tile.
+      const u32 xc = stp->x[32 * wc + l32];
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int lr = 32 * wr + 8 * i4 + 4 * q;
+        const vec<u32, 4> s4 = *reinterpret_cast<const vec<u32, 4>*>(stp->s + lr);
+        const vec<u32, 4> z4 = *reinterpret_cast<const vec<u32, 4>*>(stp->z + lr);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = 4 * i4 + e;
+          u32 p = (u32)P[0][v];
+#pragma unroll
+          for (int b = 1; b < XB; ++b) p += (u32)P[b][v] << (8 * b);
+          total[v] += s4.e[e] * p - (z4.e[e] * s4.e[e]) * xc;
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < XB; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) P[b][v] = 0;
+    }
+  };
+
+  // Prologue: chunks 0 .. NS - 2.
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p) issue_stage(stages[p], p);
+  for (i64 i0 = 0; i0 < n; i0 += NS) {
+#pragma unroll
+    for (int I = 0; I < NS; ++I) {
+      // Past the range the wait, the barrier and the (clamped) DMA still run, so every pass of
+      // the loop issues the same memory operations and only the compute is conditional.
+      const i64 i = i0 + I;
+      wait_vm<(NS - 2) * OPW>();
+      dma_stage_barrier();
+      issue_stage(stages[(I + NS - 1) % NS], i + NS - 1);
+      if (i < n) compute(stages[I], i);
+    }
+  }
+  const i64 c = tile_c + 32 * wc + l32;
+  if (c < C) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const i64 r = tile_r + 32 * wr + 8 * (v >> 2) + 4 * q + (v & 3);
+      if (r < R) {
+        if (S == 1) out[r * C + c] = (i32)total[v];
+        else __hip_atomic_fetch_add(reinterpret_cast<u32*>(out) + r * C + c, total[v], __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Access::RowReduce (crates/unpopped/src/ir.rs:2114-2125): per row, NS staged folds, each over
 // a pre expression that may read the inputs and the earlier stages, then a full-width epilogue
 // (softmax, RMSNorm, a centred quotient ...).

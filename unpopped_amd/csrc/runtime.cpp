@@ -772,14 +772,52 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
   if (R == 0 || C == 0) return UNP_OK;
   uint64_t w = A.buf[0], zp = A.buf[1], sc = A.buf[2], xa = A.buf[3], out = A.buf[4];
   const long long group = x->l.form.group;
-  const uint64_t xalign = x->l.form.dtype == UNP_I32 ? 16 : 4;
+  const bool x32 = x->l.form.dtype == UNP_I32;
+  size_t stream = SIZE_MAX, prep = SIZE_MAX;
+  for (size_t i = 0; i < x->l.entries.size(); ++i) {
+    const std::string& sym = x->l.entries[i].symbol;
+    if (sym.size() > 7 && sym.compare(sym.size() - 7, 7, "_stream") == 0) stream = i;
+    if (sym.size() > 5 && sym.compare(sym.size() - 5, 5, "_prep") == 0) prep = i;
+  }
+  if (stream != SIZE_MAX && prep != SIZE_MAX && K > 0 && K % group == 0 && (w & 15) == 0 && (zp & 3) == 0 &&
+      (sc & 3) == 0 && (out & 3) == 0 && (xa & (x32 ? 3 : 0)) == 0) {
+    // Streaming: repack x, then the LDS-staged MFMA kernel over (row tile, split) x column tiles.
+    const long long bm = x->l.entries[stream].vec, bn = x->l.entries[stream].k;
+    const long long ng = K / group, Cp = (C + 63) / 64 * 64;
+    const long long tiles_r = (R + bm - 1) / bm, tiles_c = (C + bn - 1) / bn;
+    // Splits of K: enough blocks for two per CU, at least four groups per split.
+    const long long target = 2LL * x->cu_count;
+    long long S = (target + tiles_r * tiles_c - 1) / (tiles_r * tiles_c);
+    S = std::max(1LL, std::min(S, ng / 4));
+    const long long units = tiles_r * S;
+    const long long blocks = (units + 7) / 8 * 8 * tiles_c;
+    if (blocks > 0x7FFFFFFFLL || ng * (Cp / 64) > 0x7FFFFFFFLL) {
+      set_error(err, UNP_INVALID_ARGUMENT, "dequant GEMM shape too large for one launch");
+      return UNP_INVALID_ARGUMENT;
+    }
+    const size_t xp_bytes = (size_t)K * (size_t)Cp * (x32 ? 4 : 1);
+    const size_t ws_bytes = xp_bytes + ((size_t)ng * (size_t)Cp + 64) * 4;
+    if ((rc = ensure_ws(x, ws_bytes, false, err)) != UNP_OK) return rc;
+    uint64_t xp = (uint64_t)x->ws, xs = xp + xp_bytes;
+    long long Kp = K, Cc = C, Cpp = Cp, G = group, n_out = S > 1 ? R * C : 0;
+    void* pparams[] = {&xa, &xp, &xs, &Kp, &Cc, &Cpp, &G, &out, &n_out};
+    if ((rc = launch(x, prep, (uint32_t)(ng * (Cp / 64)), pparams, s, err)) != UNP_OK) return rc;
+    void* mparams[] = {&w, &zp, &sc, &xp, &xs, &out, &R, &K, &C, &Cpp, &S};
+    return launch(x, stream, (uint32_t)blocks, mparams, s, err);
+  }
+  const uint64_t xalign = x32 ? 16 : 4;
   const long long tiles = ((R + 63) / 64) * ((C + 63) / 64);
   const bool fast_ok = K % group == 0 && C % 4 == 0 && xa % xalign == 0 && (w & 7) == 0 && (zp & 3) == 0 &&
                        (sc & 3) == 0 && (out & 3) == 0 && tiles <= 0x7FFFFFFFLL;
-  size_t entry = pick(x, fast_ok);
-  if (x->l.entries[entry].fast && !fast_ok) entry = x->l.entries.size() - 1;
-  const uint32_t grid =
-      x->l.entries[entry].fast ? (uint32_t)tiles : (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+  size_t entry = SIZE_MAX;
+  for (size_t i = 0; i < x->l.entries.size(); ++i) {
+    const std::string& sym = x->l.entries[i].symbol;
+    const bool is_mfma = sym.size() > 5 && sym.compare(sym.size() - 5, 5, "_mfma") == 0;
+    const bool is_any = sym.size() > 4 && sym.compare(sym.size() - 4, 4, "_any") == 0;
+    if ((is_mfma && fast_ok && entry == SIZE_MAX) || (is_any && (entry == SIZE_MAX || !fast_ok))) entry = i;
+  }
+  const bool mfma = x->l.entries[entry].fast;
+  const uint32_t grid = mfma ? (uint32_t)tiles : (uint32_t)(x->cu_count * x->l.blocks_per_cu);
   void* params[] = {&w, &zp, &sc, &xa, &out, &R, &K, &C};
   return launch(x, entry, grid, params, s, err);
 }
