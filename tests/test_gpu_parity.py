@@ -446,7 +446,24 @@ GEMM_MFMA_CASES = [
     (300, 4096, 64, 128, np.int32),   # split-K
     (257, 8192, 70, 128, np.int8),    # split-K, ragged columns
     (129, 6144, 33, 64, np.int32),    # split-K, 64-deep groups
+    # C <= 32 with groups of 1..4 128-deep steps (1..2 for I32) take the decode entry.
+    (64, 128, 16, 128, np.int8),      # one group: one split, plain stores
+    (130, 384, 13, 128, np.int32),    # ragged rows, C not a multiple of 16
+    (257, 8192, 32, 128, np.int8),    # split-K, two column tiles
+    (300, 4096, 1, 256, np.int32),    # one column, two steps per group
+    (129, 6144, 20, 512, np.int8),    # four steps per group
+    (70, 1152, 17, 384, np.int8),     # three steps per group
+    (1100, 2048, 16, 128, np.int8),   # row tiles not a multiple of the eight XCDs
 ]
+
+
+def _expected_gemm_entry(xdt, C, group):
+    """The entry the executor takes for aligned operands: decode for C <= 32 and groups of 1..4
+    whole 128-deep steps (1..2 for I32), then streaming for 64-multiples, then the MFMA entry."""
+    spg = group // 128 if group % 128 == 0 else 0
+    if C <= 32 and 1 <= spg <= (4 if xdt == np.int8 else 2):
+        return "_dec"
+    return "_stream" if group % 64 == 0 else "_mfma"
 
 
 @pytest.mark.parametrize("R,K,C,group,xdt", GEMM_MFMA_CASES)
@@ -455,16 +472,16 @@ def test_dequant_gemm_mfma_bit_exact(hip_device, R, K, C, group, xdt, w_kind):
     H.say(f"[case] dequant GEMM mfma {w_kind} x {np.dtype(xdt).name} {R}x{K}x{C} g{group}")
     w, zero, scale, x = _gemm_data(R * 7 + K + C, R, K, C, group, xdt)
     got = H.dequant_gemm(w, zero, scale, x, R, K, C, group, w_kind=w_kind)
-    assert _gemm_entry(w_kind, xdt, group).endswith("_stream" if group % 64 == 0 else "_mfma")
+    assert _gemm_entry(w_kind, xdt, group).endswith(_expected_gemm_entry(xdt, C, group))
     want = oracle.dequant_gemm_i32(w, zero, scale, x, R, K, C, group, w_signed=w_kind == "I4")
     assert np.array_equal(got, want)
 
 
 def test_dequant_gemm_repeated_launches_reuse_the_workspace(hip_device):
-    """Two shapes in a row on one executor (the workspace grows, the split-K output is zeroed
-    afresh each launch), then the first shape again."""
+    """Shapes in a row on one executor, switching between the decode and streaming entries (the
+    workspace grows, the split-K output is zeroed afresh each launch), then the first shape again."""
     H.say("[case] dequant GEMM repeated launches")
-    for R, K, C in ((96, 2048, 16), (160, 4096, 96), (96, 2048, 16)):
+    for R, K, C in ((96, 2048, 16), (160, 4096, 96), (96, 2048, 16), (300, 8192, 24)):
         w, zero, scale, x = _gemm_data(R + K + C, R, K, C, 128, np.int8)
         got = H.dequant_gemm(w, zero, scale, x, R, K, C, 128, w_kind="I4")
         assert np.array_equal(got, oracle.dequant_gemm_i32(w, zero, scale, x, R, K, C, 128, w_signed=True))

@@ -1944,6 +1944,220 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
 }
 
 // ---------------------------------------------------------------------------------------
+// The decode schedule for few columns (C up to 32) and groups of whole 128-value steps: the
+// weight stream dominates, so every wave streams its own rows straight into VGPRs and no block
+// barrier sits in the main loop.
+//
+// dqg_prep16 repacks x once for 16-column tiles, with the layout dqg_prep writes for 64-value
+// chunks: x'[kc][b][kseg][c][16 bytes] = digit plane b of x[64 kc + 16 kseg + i][c], i < 16, for
+// columns c < Cp (a multiple of 16; columns past C are 0), and xsum[g][c] = sum over group g of
+// x[k][c] (wrapping).  It also zeroes out for the split-K atomics.  One block per (group, 16
+// columns); thread (kseg slot, column).
+//
+// dqg_dec: a block owns BM = 64 MT rows (MT 16-row m-tiles per wave), 16 columns and a range of
+// whole groups (a split of K).  Per 128-deep step a lane loads 16 bytes of w for each m-tile
+// (row 16 m + lane % 16, k-block lane / 16) and 16 bytes of x' for each half step and digit
+// plane, D steps ahead, through buffer loads (a per-lane 32-bit offset plus a uniform step
+// offset: no 64-bit address arithmetic in the loop).  The int4 pairs become two
+// v_mfma_i32_16x16x64_i8 per m-tile and plane; the first MFMA of a group starts from a zero
+// accumulator.  Every refill is unconditional (clamped to the last step), so each pass of the
+// unrolled loop issues the same loads and the compiler's load counting stays exact across the
+// back edge: a conditional refill makes it drain every load once per pass.  At a group's end
+// total += scale * P - (scale * zero) * xsum, from LDS, where the block preloaded its rows'
+// scales and products scale * zero and its columns' group sums.  All splits of a row tile run
+// on one XCD, so their shared scale and zero-point cache lines come from that XCD's L2 once.
+// Splits add into out with u32 atomics, exact and order-free in Z / 2^32.
+// ---------------------------------------------------------------------------------------
+template <class XT, int XB>
+UNP_DEV void dqg_prep16(const XT* __restrict__ x, u8* __restrict__ xp, u32* __restrict__ xsum, i64 K, i64 C,
+                        i64 Cp, i64 G, i32* __restrict__ out, i64 n_out) {
+  __shared__ u32 part[16][16];
+  const int tid = threadIdx.x, cl = tid & 15, t16 = tid >> 4;
+  const i64 tiles = Cp / 16;
+  const i64 g = (i64)blockIdx.x / tiles, c = ((i64)blockIdx.x % tiles) * 16 + cl;
+  const bool live = c < C;
+  u32 sum = 0;
+  for (i64 ks = t16; ks < G / 16; ks += 16) {
+    const i64 k0 = g * G + ks * 16;
+    u32 wd[XB][4];
+#pragma unroll
+    for (int b = 0; b < XB; ++b)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wd[b][e] = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const u32 v = live ? (u32)(i32)x[(k0 + i) * C + c] : 0u;
+      sum += v;
+      // Signed byte digits of v (x = sum_b d_b 256^b, d_b in [-128, 127]) for I32; the byte for I8.
+      const u32 z = XB == 4 ? ((v + 0x00808080u) ^ 0x00808080u) : (v & 0xFFu);
+#pragma unroll
+      for (int b = 0; b < XB; ++b) wd[b][i >> 2] |= ((z >> (8 * b)) & 0xFFu) << (8 * (i & 3));
+    }
+    const i64 kc = k0 / 64, kseg = (k0 % 64) / 16;
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+      vec<u32, 4> o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o.e[e] = wd[b][e];
+      *reinterpret_cast<vec<u32, 4>*>(xp + (((kc * XB + b) * 4 + kseg) * Cp + c) * 16) = o;
+    }
+  }
+  part[t16][cl] = sum;
+  __syncthreads();
+  if (t16 == 0) {
+    u32 t = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) t += part[j][cl];
+    xsum[g * Cp + c] = t;
+  }
+  for (i64 o = (i64)blockIdx.x * 256 + tid; o < n_out; o += (i64)gridDim.x * 256) out[o] = 0;
+}
+
+typedef unsigned int u32x4b __attribute__((ext_vector_type(4)));
+
+template <bool QS, int XB, int G, int MT, int D, int MAXG>
+UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, const i32* __restrict__ scale,
+                     const u8* __restrict__ xp, const u32* __restrict__ xsum, i32* __restrict__ out, i64 R, i64 K,
+                     i64 C, i64 Cp, i64 S) {
+  constexpr int BM = 64 * MT, BN = 16, SPG = G / 128;
+  static_assert(G % 128 == 0 && D % SPG == 0, "whole steps per group, whole groups per unrolled pass");
+  __shared__ __attribute__((aligned(16))) u32 ss[MAXG][BM + 4];
+  __shared__ __attribute__((aligned(16))) u32 zs[MAXG][BM + 4];
+  __shared__ u32 xs[MAXG][BN];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kq = lane >> 4, r16 = lane & 15;
+  const i64 ng = K / G;
+  const i64 tiles_r = (R + BM - 1) / BM, tiles_c = (C + BN - 1) / BN;
+  // Block b: XCD b % 8; its slot b / 8 names (row tile of that XCD, split, column tile).
+  const i64 xcd = (i64)blockIdx.x % 8, slot = (i64)blockIdx.x / 8, per = S * tiles_c;
+  const i64 rt = (slot / per) * 8 + xcd, split = (slot % per) / tiles_c, ct = slot % tiles_c;
+  if (rt >= tiles_r) return;
+  const i64 tile_r = rt * BM, tile_c = ct * BN;
+  const i64 g0 = ng * split / S, g1 = ng * (split + 1) / S;
+  const int ngr = (int)(g1 - g0);  // at most MAXG: the host picks S
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)(u32)(R * (K / 2)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xp, (short)0, (int)(u32)(K * Cp * XB), 0x00020000);
+  const i64 kb = g0 * G, nsteps = (i64)ngr * SPG;
+  u32 wofs[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const i64 row = tile_r + wave * 16 * MT + 16 * m + r16;
+    wofs[m] = (u32)((row < R ? row : R - 1) * (K / 2) + kb / 2 + 16 * kq);
+  }
+  // Half step h of lane (kq, c) covers k = 32 kq + 16 h + [0, 16) of the step: x' segment 2 kq + h.
+  u32 xofs[XB][2];
+#pragma unroll
+  for (int b = 0; b < XB; ++b)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int e = 2 * kq + h;
+      xofs[b][h] = (u32)((((kb / 64 + e / 4) * XB * 4 + b * 4 + e % 4) * Cp + tile_c + r16) * 16);
+    }
+  u32x4b wv[D][MT];
+  i32x4 xv[D][XB][2];
+  auto load = [&](int sl, i64 i) {
+    const int sw = (int)(64 * i), sx = (int)(128 * XB * Cp * i);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) wv[sl][m] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)wofs[m], sw, 0);
+#pragma unroll
+    for (int b = 0; b < XB; ++b)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        xv[sl][b][h] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xofs[b][h], sx, 0));
+  };
+#pragma unroll
+  for (int p = 0; p < D; ++p) load(p, p < nsteps ? p : nsteps - 1);
+  // The preload: every load issued at once, while the first steps are in flight.
+  constexpr int PL = (BM * MAXG + 255) / 256, PX = (BN * MAXG + 255) / 256;
+  u32 sv[PL], zv[PL], cv[PX];
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int idx = tid + 256 * j, r = idx / MAXG, gg = idx % MAXG;
+    const i64 row = tile_r + r < R ? tile_r + r : R - 1;
+    const bool ok = r < BM && gg < ngr;
+    sv[j] = ok ? (u32)scale[row * ng + g0 + gg] : 0u;
+    zv[j] = ok ? (u32)zero[row * ng + g0 + gg] : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < PX; ++j) {
+    const int idx = tid + 256 * j, gg = idx / BN, c = idx % BN;
+    cv[j] = gg < ngr ? xsum[(g0 + gg) * Cp + tile_c + c] : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int idx = tid + 256 * j, r = idx / MAXG, gg = idx % MAXG;
+    if (r < BM) {
+      ss[gg][r] = sv[j];
+      zs[gg][r] = sv[j] * zv[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < PX; ++j) {
+    const int idx = tid + 256 * j, gg = idx / BN, c = idx % BN;
+    if (gg < MAXG) xs[gg][c] = cv[j];
+  }
+  __syncthreads();
+  i32x4 P[MT][XB];
+  u32 total[MT][4];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) total[m][v] = 0;
+  const i32x4 Z = {0, 0, 0, 0};
+  for (i64 i0 = 0; i0 < nsteps; i0 += D) {
+#pragma unroll
+    for (int I = 0; I < D; ++I) {
+      const i64 i = i0 + I;
+      if (i < nsteps) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const i32x4 a0 = unpack16<QS>((u64)wv[I][m][0] | ((u64)wv[I][m][1] << 32));
+          const i32x4 a1 = unpack16<QS>((u64)wv[I][m][2] | ((u64)wv[I][m][3] << 32));
+#pragma unroll
+          for (int b = 0; b < XB; ++b) {
+            P[m][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, xv[I][b][0], I % SPG == 0 ? Z : P[m][b], 0, 0, 0);
+            P[m][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, xv[I][b][1], P[m][b], 0, 0, 0);
+          }
+        }
+        if ((I + 1) % SPG == 0) {
+          // Lane (kq, c) holds rows 4 kq + v of each m-tile, column c.
+          const int gg = (int)(i / SPG);
+          const u32 xc = xs[gg][r16];
+#pragma unroll
+          for (int m = 0; m < MT; ++m) {
+            const int lr = wave * 16 * MT + 16 * m + 4 * kq;
+            const vec<u32, 4> s4 = *reinterpret_cast<const vec<u32, 4>*>(&ss[gg][lr]);
+            const vec<u32, 4> z4 = *reinterpret_cast<const vec<u32, 4>*>(&zs[gg][lr]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              u32 p = (u32)P[m][0][v];
+#pragma unroll
+              for (int b = 1; b < XB; ++b) p += (u32)P[m][b][v] << (8 * b);
+              total[m][v] += s4.e[v] * p - z4.e[v] * xc;
+            }
+          }
+        }
+      }
+      load(I, i + D < nsteps ? i + D : nsteps - 1);
+    }
+  }
+  const i64 c = tile_c + r16;
+  if (c < C) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const i64 r = tile_r + wave * 16 * MT + 16 * m + 4 * kq + v;
+        if (r < R) {
+          if (S == 1) out[r * C + c] = (i32)total[m][v];
+          else __hip_atomic_fetch_add(reinterpret_cast<u32*>(out) + r * C + c, total[m][v], __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Access::RowReduce (crates/unpopped/src/ir.rs:2114-2125): per row, NS staged folds, each over
 // a pre expression that may read the inputs and the earlier stages, then a full-width epilogue
 // (softmax, RMSNorm, a centred quotient ...).
