@@ -376,7 +376,7 @@ def gemm_lines(u, synth, steps: int, warmup: int) -> None:
     dw, dz, ds = (u.DeviceBuffer.from_array(a) for a in (w, zero, scale))
     for xk, xdt in (("I8", np.int8), ("I32", np.int32)):
         ex = H.executor(kind="dequant_gemm", q_kind="U4", dtype=xk, group=G)
-        for C in (16, 32, 64, 256, 1024):
+        for C in (16, 32, 64, 128, 256, 1024):
             x = (synth.int16_i32(63, K * C) * 13 - 100).astype(xdt)
             dx, do = u.DeviceBuffer.from_array(x), u.DeviceBuffer(R * C * 4)
             for _ in range(warmup):

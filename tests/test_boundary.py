@@ -376,15 +376,16 @@ def test_row_reduce_two_inputs_and_rank_three():
 
 
 def test_dequant_gemm_entries_follow_the_group():
-    """The decode entry and its prep exist when the group holds 1..4 whole 128-value steps (1..2
-    for I32 activations), the streaming entry and its prep when it holds whole 64-value chunks,
-    the LDS-transpose MFMA entry when it holds whole 32-deep steps, the serial entry always; each
-    staged chunk divides the group."""
+    """The decode entries (1, 2 and 4 column tiles for I8 activations, one for I32) and their prep
+    exist when the group holds 1..4 whole 128-value steps (1..2 for I32), the streaming entry and
+    its prep when it holds whole 64-value chunks, the LDS-transpose MFMA entry when it holds whole
+    32-deep steps, the serial entry always; each staged chunk divides the group."""
     b = u.HipBackend()
     for w_kind, x_kind, group, chunk, stream, dec in (
-            ("I4", "I32", 128, 128, 64, 2), ("I4", "I32", 256, 128, 64, 2), ("U4", "I32", 512, 128, 64, 0),
-            ("U4", "I8", 512, 512, 128, 4), ("U4", "I8", 384, 384, 128, 3), ("U4", "I8", 1024, 512, 128, 0),
-            ("U4", "I8", 64, 64, 64, 0), ("U4", "I8", 96, 96, 0, 0), ("I4", "I32", 7, 0, 0, 0), ("U4", "I8", 48, 0, 0, 0)):
+            ("I4", "I32", 128, 128, 64, 1), ("I4", "I32", 256, 128, 64, 2), ("U4", "I32", 512, 128, 64, 0),
+            ("U4", "I8", 128, 128, 128, 2), ("U4", "I8", 512, 512, 128, 4), ("U4", "I8", 384, 384, 128, 3),
+            ("U4", "I8", 1024, 512, 128, 0), ("U4", "I8", 64, 64, 64, 0), ("U4", "I8", 96, 96, 0, 0),
+            ("I4", "I32", 7, 0, 0, 0), ("U4", "I8", 48, 0, 0, 0)):
         g = b.lower_kernel(u.kernel_dequant_gemm("m", w_kind, x_kind, group))
         assert g.interface["form"] == "dequant_gemm" and g.interface["group"] == group
         assert g.interface["chunk"] == chunk and (chunk == 0 or group % chunk == 0)
@@ -392,7 +393,8 @@ def test_dequant_gemm_entries_follow_the_group():
         # The decode entry keeps a whole number of groups in flight.
         assert g.interface["decode_steps"] == dec and (dec == 0 or dec % (group // 128) == 0)
         syms = [e["symbol"].rsplit("_", 1)[1] for e in g.interface["entries"]]
-        want = ((["dec"] if dec else []) + (["stream"] if stream else []) + (["mfma"] if chunk else []) + ["any"]
+        decs = (["dec1", "dec2", "dec4"] if x_kind == "I8" else ["dec1"]) if dec else []
+        want = (decs + (["stream"] if stream else []) + (["mfma"] if chunk else []) + ["any"]
                 + (["prep"] if stream else []) + (["prep16"] if dec else []))
         assert syms == want
 

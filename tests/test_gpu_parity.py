@@ -446,23 +446,29 @@ GEMM_MFMA_CASES = [
     (300, 4096, 64, 128, np.int32),   # split-K
     (257, 8192, 70, 128, np.int8),    # split-K, ragged columns
     (129, 6144, 33, 64, np.int32),    # split-K, 64-deep groups
-    # C <= 32 with groups of 1..4 128-deep steps (1..2 for I32) take the decode entry.
+    (257, 8192, 200, 128, np.int8),   # C > 128: streaming split-K
+    # C <= 128 with groups of 1..4 128-deep steps (1..2 for I32) take a decode entry.
     (64, 128, 16, 128, np.int8),      # one group: one split, plain stores
     (130, 384, 13, 128, np.int32),    # ragged rows, C not a multiple of 16
-    (257, 8192, 32, 128, np.int8),    # split-K, two column tiles
+    (257, 8192, 32, 128, np.int8),    # split-K, two column tiles per block
     (300, 4096, 1, 256, np.int32),    # one column, two steps per group
     (129, 6144, 20, 512, np.int8),    # four steps per group
     (70, 1152, 17, 384, np.int8),     # three steps per group
     (1100, 2048, 16, 128, np.int8),   # row tiles not a multiple of the eight XCDs
+    (200, 4096, 100, 128, np.int8),   # four column tiles per block, two blocks across
+    (96, 2048, 128, 256, np.int8),    # the widest decode shape
 ]
 
 
 def _expected_gemm_entry(xdt, C, group):
-    """The entry the executor takes for aligned operands: decode for C <= 32 and groups of 1..4
-    whole 128-deep steps (1..2 for I32), then streaming for 64-multiples, then the MFMA entry."""
+    """The entry the executor takes for aligned operands: decode for C <= 128 and groups of 1..4
+    whole 128-deep steps (1..2 for I32) -- for I8 the entry with 1, 2 or 4 column tiles that first
+    covers C, for I32 the one-tile entry -- then streaming for 64-multiples, then the MFMA entry."""
     spg = group // 128 if group % 128 == 0 else 0
-    if C <= 32 and 1 <= spg <= (4 if xdt == np.int8 else 2):
-        return "_dec"
+    if C <= 128 and 1 <= spg <= (4 if xdt == np.int8 else 2):
+        if xdt != np.int8:
+            return "_dec1"
+        return "_dec1" if C <= 16 else "_dec2" if C <= 32 else "_dec4"
     return "_stream" if group % 64 == 0 else "_mfma"
 
 

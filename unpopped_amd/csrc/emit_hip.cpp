@@ -611,12 +611,13 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
   // divides the group) or 64; four waves stacked over 128 rows and 32 columns; NS stages.
   const int skc = f.group % 64 != 0 ? 0 : (xb == 1 && f.group % 128 == 0 ? 128 : 64);
   const int swr = 4, swc = 1, sns = 4;
-  // The decode schedule (few columns): groups of 1..4 whole 128-value steps (1..2 for I32
-  // activations, whose four digit planes take four times the x registers); D steps in flight,
-  // a whole number of groups.
+  // The decode schedule (up to 128 columns): groups of 1..4 whole 128-value steps (1..2 for I32
+  // activations, whose four digit planes take four times the x registers).  I8: two m-tiles per
+  // wave, 1, 2 or 4 column tiles of 16 sharing each unpacked w operand, two steps in flight (or
+  // one group); I32: four m-tiles, one column tile, one group in flight.
   const int spg = f.group % 128 == 0 ? f.group / 128 : 0;
   const bool dec = spg >= 1 && spg <= (xb == 1 ? 4 : 2);
-  const int dmt = 2, dd = spg <= 1 ? 2 : spg, dmaxg = 32;
+  const int dmt = xb == 1 ? 2 : 4, dd = xb == 1 ? (spg <= 1 ? 2 : spg) : spg, dmaxg = 32;
   std::ostringstream name;
   name << "unp_dequant_gemm_" << lower_name(f.q_kind) << "_g" << f.group << "_" << lower_name(f.dtype) << "_i32";
   L.name = name.str();
@@ -626,17 +627,18 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
   src << header(L.name, f);
   const std::string sig = std::string("(const unsigned char* w, const int* zero, const int* scale, const ") + xt +
                           "* x, int* out, long long R, long long K, long long C)";
-  if (dec) {
+  for (int nc = 1; dec && nc <= (xb == 1 ? 4 : 1); nc *= 2) {
     Entry e;
     e.fast = true;
-    e.symbol = L.name + "_dec";
+    e.symbol = L.name + "_dec" + std::to_string(nc);
     e.vec = 64 * dmt;  // rows per block
+    e.cols = 16 * nc;  // columns per block
     e.k = dmaxg;       // groups per split at most
     src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol
         << "(const unsigned char* w, const int* zero, const int* scale, const unsigned char* xp, const unsigned* xsum, "
            "int* out, long long R, long long K, long long C, long long Cp, long long S) {\n  unp::dqg_dec<"
-        << (qs ? "true" : "false") << ", " << xb << ", " << f.group << ", " << dmt << ", " << dd << ", " << dmaxg
-        << ">(w, zero, scale, xp, xsum, out, R, K, C, Cp, S);\n}\n";
+        << (qs ? "true" : "false") << ", " << xb << ", " << f.group << ", " << dmt << ", " << nc << ", " << dd << ", "
+        << dmaxg << ">(w, zero, scale, xp, xsum, out, R, K, C, Cp, S);\n}\n";
     L.entries.push_back(e);
   }
   if (skc) {
@@ -703,7 +705,8 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
     << ",{\"name\":\"n0\",\"kind\":\"scalar\",\"dtype\":\"I32\"},{\"name\":\"n1\",\"kind\":\"scalar\",\"dtype\":\"I32\"},{"
        "\"name\":\"n2\",\"kind\":\"scalar\",\"dtype\":\"I32\"}]"
     << ",\"launch\":{\"block\":[256,1,1],\"grid_policy\":\"dec: a prep launch over (group, 16 columns), then "
-       "(row tiles rounded up to 8) x splits x column tiles blocks of 128 x 16 outputs, a split's groups at most 32 "
+       "(row tiles rounded up to 8) x splits x column tiles blocks of 128 (I8) or 256 (I32) rows x 16, 32 or 64 "
+       "columns, about two blocks per CU, a split's groups at most 32 "
        "and the splits adding into out with atomics; stream: a prep launch over (group, 64 columns), then "
        "(row tiles x splits, rounded up to 8) x column tiles blocks of 128 x 32 outputs, the splits adding into out "
        "with atomics; mfma: one block per 64 x 64 output tile; any: threads stride over the outputs\"},\"entries\":[";
@@ -711,11 +714,12 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
     const std::string& sym = L.entries[i].symbol;
     const bool is_stream = sym.size() > 7 && sym.compare(sym.size() - 7, 7, "_stream") == 0;
     const bool is_prep = sym.size() > 5 && sym.compare(sym.size() - 5, 5, "_prep") == 0;
-    const bool is_dec = sym.size() > 4 && sym.compare(sym.size() - 4, 4, "_dec") == 0;
+    const bool is_dec = L.entries[i].cols > 0;
     const bool is_prep16 = sym.size() > 7 && sym.compare(sym.size() - 7, 7, "_prep16") == 0;
     j << (i ? "," : "") << "{\"symbol\":\"" << sym << "\",\"when\":\""
-      << (is_dec ? "C <= 32, K % group == 0, w 16-byte aligned, w and repacked x under 2 GiB; after the prep16 launch "
-                   "(buffer loads into VGPRs, v_mfma_i32_16x16x64_i8)"
+      << (is_dec ? "C <= 128 (the entry whose column tiles cover C, or the widest), K % group == 0, w 16-byte aligned, "
+                   "w and repacked x under 2 GiB; after the prep16 launch (buffer loads into VGPRs, "
+                   "v_mfma_i32_16x16x64_i8)"
           : is_prep16 ? "before the dec entry: x repacked for 16-column tiles, group column sums, out zeroed"
           : is_stream ? "K % group == 0, w 16-byte aligned; after the prep launch (LDS-staged DMA, "
                       "v_mfma_i32_32x32x32_i8)"
@@ -726,7 +730,7 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
       << "\"}";
   }
   j << "],\"workspace\":" << (skc ? "\"dec and stream: K x Cp x planes bytes of repacked x, then (K / group x Cp + 64) "
-                                    "u32 column sums (Cp = C rounded up to 16 for dec, to 64 for stream)\""
+                                    "u32 column sums (Cp = C rounded up to the decode entry's columns per block, or to 64 for stream)\""
                                   : "null")
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["

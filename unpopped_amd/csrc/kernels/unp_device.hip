@@ -1954,10 +1954,10 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
 // x[k][c] (wrapping).  It also zeroes out for the split-K atomics.  One block per (group, 16
 // columns); thread (kseg slot, column).
 //
-// dqg_dec: a block owns BM = 64 MT rows (MT 16-row m-tiles per wave), 16 columns and a range of
-// whole groups (a split of K).  Per 128-deep step a lane loads 16 bytes of w for each m-tile
-// (row 16 m + lane % 16, k-block lane / 16) and 16 bytes of x' for each half step and digit
-// plane, D steps ahead, through buffer loads (a per-lane 32-bit offset plus a uniform step
+// dqg_dec: a block owns BM = 64 MT rows (MT 16-row m-tiles per wave), 16 NC columns (NC column
+// tiles sharing each unpacked w operand) and a range of whole groups (a split of K).  Per
+// 128-deep step a lane loads 16 bytes of w for each m-tile (row 16 m + lane % 16, k-block
+// lane / 16) and 16 bytes of x' for each column tile, half step and digit plane, D steps ahead, through buffer loads (a per-lane 32-bit offset plus a uniform step
 // offset: no 64-bit address arithmetic in the loop).  The int4 pairs become two
 // v_mfma_i32_16x16x64_i8 per m-tile and plane; the first MFMA of a group starts from a zero
 // accumulator.  Every refill is unconditional (clamped to the last step), so each pass of the
@@ -2015,11 +2015,11 @@ UNP_DEV void dqg_prep16(const XT* __restrict__ x, u8* __restrict__ xp, u32* __re
 
 typedef unsigned int u32x4b __attribute__((ext_vector_type(4)));
 
-template <bool QS, int XB, int G, int MT, int D, int MAXG>
+template <bool QS, int XB, int G, int MT, int NC, int D, int MAXG>
 UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, const i32* __restrict__ scale,
                      const u8* __restrict__ xp, const u32* __restrict__ xsum, i32* __restrict__ out, i64 R, i64 K,
                      i64 C, i64 Cp, i64 S) {
-  constexpr int BM = 64 * MT, BN = 16, SPG = G / 128;
+  constexpr int BM = 64 * MT, BN = 16 * NC, SPG = G / 128;
   static_assert(G % 128 == 0 && D % SPG == 0, "whole steps per group, whole groups per unrolled pass");
   __shared__ __attribute__((aligned(16))) u32 ss[MAXG][BM + 4];
   __shared__ __attribute__((aligned(16))) u32 zs[MAXG][BM + 4];
@@ -2045,25 +2045,30 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
     wofs[m] = (u32)((row < R ? row : R - 1) * (K / 2) + kb / 2 + 16 * kq);
   }
   // Half step h of lane (kq, c) covers k = 32 kq + 16 h + [0, 16) of the step: x' segment 2 kq + h.
-  u32 xofs[XB][2];
+  u32 xofs[NC][XB][2];
 #pragma unroll
-  for (int b = 0; b < XB; ++b)
+  for (int t = 0; t < NC; ++t)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int e = 2 * kq + h;
-      xofs[b][h] = (u32)((((kb / 64 + e / 4) * XB * 4 + b * 4 + e % 4) * Cp + tile_c + r16) * 16);
-    }
+    for (int b = 0; b < XB; ++b)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int e = 2 * kq + h;
+        xofs[t][b][h] = (u32)((((kb / 64 + e / 4) * XB * 4 + b * 4 + e % 4) * Cp + tile_c + 16 * t + r16) * 16);
+      }
   u32x4b wv[D][MT];
-  i32x4 xv[D][XB][2];
+  i32x4 xv[D][NC][XB][2];
   auto load = [&](int sl, i64 i) {
     const int sw = (int)(64 * i), sx = (int)(128 * XB * Cp * i);
 #pragma unroll
     for (int m = 0; m < MT; ++m) wv[sl][m] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)wofs[m], sw, 0);
 #pragma unroll
-    for (int b = 0; b < XB; ++b)
+    for (int t = 0; t < NC; ++t)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        xv[sl][b][h] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xofs[b][h], sx, 0));
+      for (int b = 0; b < XB; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          xv[sl][t][b][h] =
+              __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xofs[t][b][h], sx, 0));
   };
 #pragma unroll
   for (int p = 0; p < D; ++p) load(p, p < nsteps ? p : nsteps - 1);
@@ -2097,12 +2102,14 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
     if (gg < MAXG) xs[gg][c] = cv[j];
   }
   __syncthreads();
-  i32x4 P[MT][XB];
-  u32 total[MT][4];
+  i32x4 P[MT][NC][XB];
+  u32 total[MT][NC][4];
 #pragma unroll
   for (int m = 0; m < MT; ++m)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) total[m][v] = 0;
+    for (int t = 0; t < NC; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) total[m][t][v] = 0;
   const i32x4 Z = {0, 0, 0, 0};
   for (i64 i0 = 0; i0 < nsteps; i0 += D) {
 #pragma unroll
@@ -2114,26 +2121,32 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
           const i32x4 a0 = unpack16<QS>((u64)wv[I][m][0] | ((u64)wv[I][m][1] << 32));
           const i32x4 a1 = unpack16<QS>((u64)wv[I][m][2] | ((u64)wv[I][m][3] << 32));
 #pragma unroll
-          for (int b = 0; b < XB; ++b) {
-            P[m][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, xv[I][b][0], I % SPG == 0 ? Z : P[m][b], 0, 0, 0);
-            P[m][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, xv[I][b][1], P[m][b], 0, 0, 0);
-          }
+          for (int t = 0; t < NC; ++t)
+#pragma unroll
+            for (int b = 0; b < XB; ++b) {
+              P[m][t][b] =
+                  __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, xv[I][t][b][0], I % SPG == 0 ? Z : P[m][t][b], 0, 0, 0);
+              P[m][t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, xv[I][t][b][1], P[m][t][b], 0, 0, 0);
+            }
         }
         if ((I + 1) % SPG == 0) {
           // Lane (kq, c) holds rows 4 kq + v of each m-tile, column c.
           const int gg = (int)(i / SPG);
-          const u32 xc = xs[gg][r16];
 #pragma unroll
           for (int m = 0; m < MT; ++m) {
             const int lr = wave * 16 * MT + 16 * m + 4 * kq;
             const vec<u32, 4> s4 = *reinterpret_cast<const vec<u32, 4>*>(&ss[gg][lr]);
             const vec<u32, 4> z4 = *reinterpret_cast<const vec<u32, 4>*>(&zs[gg][lr]);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              u32 p = (u32)P[m][0][v];
+            for (int t = 0; t < NC; ++t) {
+              const u32 xc = xs[gg][16 * t + r16];
 #pragma unroll
-              for (int b = 1; b < XB; ++b) p += (u32)P[m][b][v] << (8 * b);
-              total[m][v] += s4.e[v] * p - z4.e[v] * xc;
+              for (int v = 0; v < 4; ++v) {
+                u32 p = (u32)P[m][t][0][v];
+#pragma unroll
+                for (int b = 1; b < XB; ++b) p += (u32)P[m][t][b][v] << (8 * b);
+                total[m][t][v] += s4.e[v] * p - z4.e[v] * xc;
+              }
             }
           }
         }
@@ -2141,19 +2154,22 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
       load(I, i + D < nsteps ? i + D : nsteps - 1);
     }
   }
-  const i64 c = tile_c + r16;
-  if (c < C) {
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
+  for (int t = 0; t < NC; ++t) {
+    const i64 c = tile_c + 16 * t + r16;
+    if (c < C) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const i64 r = tile_r + wave * 16 * MT + 16 * m + 4 * kq + v;
-        if (r < R) {
-          if (S == 1) out[r * C + c] = (i32)total[m][v];
-          else __hip_atomic_fetch_add(reinterpret_cast<u32*>(out) + r * C + c, total[m][v], __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const i64 r = tile_r + wave * 16 * MT + 16 * m + 4 * kq + v;
+          if (r < R) {
+            if (S == 1) out[r * C + c] = (i32)total[m][t][v];
+            else __hip_atomic_fetch_add(reinterpret_cast<u32*>(out) + r * C + c, total[m][t][v], __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+          }
         }
-      }
+    }
   }
 }
 

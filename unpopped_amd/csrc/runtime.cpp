@@ -778,23 +778,27 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
     const std::string& sym = x->l.entries[i].symbol;
     if (sym.size() > 7 && sym.compare(sym.size() - 7, 7, "_stream") == 0) stream = i;
     if (sym.size() > 5 && sym.compare(sym.size() - 5, 5, "_prep") == 0) prep = i;
-    if (sym.size() > 4 && sym.compare(sym.size() - 4, 4, "_dec") == 0) dec = i;
     if (sym.size() > 7 && sym.compare(sym.size() - 7, 7, "_prep16") == 0) prep16 = i;
+    // The decode entry whose column tiles first cover C, else the widest (entries ascend).
+    const int cols = x->l.entries[i].cols;
+    if (cols > 0 && (dec == SIZE_MAX || x->l.entries[dec].cols < C)) dec = i;
   }
   const long long xbytes = x32 ? 4 : 1;
-  if (dec != SIZE_MAX && prep16 != SIZE_MAX && C <= 32 && K > 0 && K % group == 0 && (w & 15) == 0 &&
+  const long long bn = dec != SIZE_MAX ? x->l.entries[dec].cols : 16, Cpd = (C + bn - 1) / bn * bn;
+  if (dec != SIZE_MAX && prep16 != SIZE_MAX && C <= 128 && K > 0 && K % group == 0 && (w & 15) == 0 &&
       (zp & 3) == 0 && (sc & 3) == 0 && (out & 3) == 0 && (xa & (x32 ? 3 : 0)) == 0 &&
-      R * (K / 2) < 0x7FFFFFFFLL && K * ((C + 15) / 16 * 16) * xbytes < 0x7FFFFFFFLL) {
-    // Decode: repack x for 16-column tiles, then blocks of 128 rows x 16 columns x a split of K.
+      R * (K / 2) < 0x7FFFFFFFLL && K * Cpd * xbytes < 0x7FFFFFFFLL) {
+    // Decode: repack x for 16-column tiles (Cp a whole number of the entry's column tiles), then
+    // blocks of bm rows x bn columns x a split of K.
     const long long bm = x->l.entries[dec].vec, maxg = x->l.entries[dec].k;
-    const long long ng = K / group, Cp = (C + 15) / 16 * 16;
-    const long long tiles_r = (R + bm - 1) / bm, tiles_c = Cp / 16;
+    const long long ng = K / group, Cp = Cpd;
+    const long long tiles_r = (R + bm - 1) / bm, tiles_c = Cp / bn;
     // Splits of K: about two blocks per CU, at most maxg groups per split, at least one.
     long long S = (2LL * x->cu_count + tiles_r * tiles_c - 1) / (tiles_r * tiles_c);
     S = std::max(S, (ng + maxg - 1) / maxg);
     S = std::max(1LL, std::min(S, ng));
     const long long blocks = (tiles_r + 7) / 8 * 8 * S * tiles_c;
-    if (blocks > 0x7FFFFFFFLL || ng * tiles_c > 0x7FFFFFFFLL) {
+    if (blocks > 0x7FFFFFFFLL || ng * (Cp / 16) > 0x7FFFFFFFLL) {
       set_error(err, UNP_INVALID_ARGUMENT, "dequant GEMM shape too large for one launch");
       return UNP_INVALID_ARGUMENT;
     }
@@ -804,7 +808,7 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
     uint64_t xp = (uint64_t)x->ws, xs = xp + xp_bytes;
     long long Kp = K, Cc = C, Cpp = Cp, G = group, n_out = S > 1 ? R * C : 0;
     void* pparams[] = {&xa, &xp, &xs, &Kp, &Cc, &Cpp, &G, &out, &n_out};
-    if ((rc = launch(x, prep16, (uint32_t)(ng * tiles_c), pparams, s, err)) != UNP_OK) return rc;
+    if ((rc = launch(x, prep16, (uint32_t)(ng * (Cp / 16)), pparams, s, err)) != UNP_OK) return rc;
     void* mparams[] = {&w, &zp, &sc, &xp, &xs, &out, &R, &K, &C, &Cpp, &S};
     return launch(x, dec, (uint32_t)blocks, mparams, s, err);
   }

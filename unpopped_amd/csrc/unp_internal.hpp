@@ -30,6 +30,7 @@ struct Entry {
   bool wide = false;  // reduction: the block-per-row schedule (long rows)
   int threads = 0;    // block size of this entry (0: the form's)
   int blocks_per_cu = 0;  // persistent blocks per CU of this entry (0: the form's)
+  int cols = 0;           // output columns per block (dequant GEMM decode entries)
 };
 
 // Scan tile status: words per tile (a 256-byte stride: the status of consecutive tiles, which
