@@ -455,17 +455,20 @@ GEMM_MFMA_CASES = [
     (129, 6144, 20, 512, np.int8),    # four steps per group
     (70, 1152, 17, 384, np.int8),     # three steps per group
     (1100, 2048, 16, 128, np.int8),   # row tiles not a multiple of the eight XCDs
-    (200, 4096, 100, 128, np.int8),   # four column tiles per block, two blocks across
-    (96, 2048, 128, 256, np.int8),    # the widest decode shape
+    (200, 4096, 60, 128, np.int8),    # four column tiles per block
+    (96, 2048, 100, 256, np.int32),   # I32 decode past 64 columns
+    (200, 4096, 100, 128, np.int8),   # I8 past 64 columns: streaming, two column tiles per wave
+    (96, 2048, 128, 256, np.int8),
 ]
 
 
 def _expected_gemm_entry(xdt, C, group):
-    """The entry the executor takes for aligned operands: decode for C <= 128 and groups of 1..4
-    whole 128-deep steps (1..2 for I32) -- for I8 the entry with 1, 2 or 4 column tiles that first
-    covers C, for I32 the one-tile entry -- then streaming for 64-multiples, then the MFMA entry."""
+    """The entry the executor takes for aligned operands: decode for groups of 1..4 whole
+    128-deep steps (1..2 for I32) and C <= 64 (I8: the entry with 1, 2 or 4 column tiles that
+    first covers C) or C <= 128 (I32: the one-tile entry), then streaming for 64-multiples, then
+    the MFMA entry."""
     spg = group // 128 if group % 128 == 0 else 0
-    if C <= 128 and 1 <= spg <= (4 if xdt == np.int8 else 2):
+    if C <= (64 if xdt == np.int8 else 128) and 1 <= spg <= (4 if xdt == np.int8 else 2):
         if xdt != np.int8:
             return "_dec1"
         return "_dec1" if C <= 16 else "_dec2" if C <= 32 else "_dec4"

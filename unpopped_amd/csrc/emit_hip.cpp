@@ -608,10 +608,12 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
   for (int c = 32; c <= (xb == 4 ? 128 : 512); c += 32)
     if (f.group % c == 0) kc = c;
   // The streaming schedule: groups of whole 64-value chunks.  Stage chunk 128 (I8, when it
-  // divides the group) or 64; four waves stacked over 128 rows and 32 columns; NS stages.
+  // divides the group) or 64; four waves stacked over 128 rows, each with one 32 x 32 tile row
+  // and two column tiles (I8, 128-value chunks: 64 columns per block, three stages) or one (32
+  // columns, four stages).
   const int skc = f.group % 64 != 0 ? 0 : (xb == 1 && f.group % 128 == 0 ? 128 : 64);
-  const int swr = 4, swc = 1, sns = 4;
-  // The decode schedule (up to 128 columns): groups of 1..4 whole 128-value steps (1..2 for I32
+  const int swr = 4, swc = 1, stn = xb == 1 && skc == 128 ? 2 : 1, sns = stn == 2 ? 3 : 4;
+  // The decode schedule (up to 64 columns for I8, 128 for I32): groups of 1..4 whole 128-value steps (1..2 for I32
   // activations, whose four digit planes take four times the x registers).  I8: two m-tiles per
   // wave, 1, 2 or 4 column tiles of 16 sharing each unpacked w operand, two steps in flight (or
   // one group); I32: four m-tiles, one column tile, one group in flight.
@@ -645,13 +647,13 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
     Entry e;
     e.fast = true;
     e.symbol = L.name + "_stream";
-    e.vec = 32 * swr;  // rows per block
-    e.k = 32 * swc;    // columns per block
+    e.vec = 32 * swr;        // rows per block
+    e.k = 32 * swc * stn;    // columns per block
     src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol
         << "(const unsigned char* w, const int* zero, const int* scale, const unsigned char* xp, const unsigned* xsum, "
            "int* out, long long R, long long K, long long C, long long Cp, long long S) {\n  unp::dqg_stream<"
-        << (qs ? "true" : "false") << ", " << xb << ", " << f.group << ", " << skc << ", " << swr << ", " << swc << ", "
-        << sns << ">(w, zero, scale, xp, xsum, out, R, K, C, Cp, S);\n}\n";
+        << (qs ? "true" : "false") << ", " << xb << ", " << f.group << ", " << skc << ", " << swr << ", " << swc
+        << ", 1, " << stn << ", " << sns << ">(w, zero, scale, xp, xsum, out, R, K, C, Cp, S);\n}\n";
     L.entries.push_back(e);
   }
   if (kc) {
@@ -708,7 +710,7 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
        "(row tiles rounded up to 8) x splits x column tiles blocks of 128 (I8) or 256 (I32) rows x 16, 32 or 64 "
        "columns, about two blocks per CU, a split's groups at most 32 "
        "and the splits adding into out with atomics; stream: a prep launch over (group, 64 columns), then "
-       "(row tiles x splits, rounded up to 8) x column tiles blocks of 128 x 32 outputs, the splits adding into out "
+       "(row tiles x splits, rounded up to 8) x column tiles blocks of 128 x 64 (I8) or 128 x 32 outputs, the splits adding into out "
        "with atomics; mfma: one block per 64 x 64 output tile; any: threads stride over the outputs\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i) {
     const std::string& sym = L.entries[i].symbol;
@@ -717,7 +719,8 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
     const bool is_dec = L.entries[i].cols > 0;
     const bool is_prep16 = sym.size() > 7 && sym.compare(sym.size() - 7, 7, "_prep16") == 0;
     j << (i ? "," : "") << "{\"symbol\":\"" << sym << "\",\"when\":\""
-      << (is_dec ? "C <= 128 (the entry whose column tiles cover C, or the widest), K % group == 0, w 16-byte aligned, "
+      << (is_dec ? "C <= 64 for I8, C <= 128 for I32 (the entry whose column tiles cover C, or the widest), "
+                   "K % group == 0, w 16-byte aligned, "
                    "w and repacked x under 2 GiB; after the prep16 launch (buffer loads into VGPRs, "
                    "v_mfma_i32_16x16x64_i8)"
           : is_prep16 ? "before the dec entry: x repacked for 16-column tiles, group column sums, out zeroed"

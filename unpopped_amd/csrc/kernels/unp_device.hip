@@ -1727,12 +1727,12 @@ UNP_DEV void dqgemm_mfma(const u8* __restrict__ w, const i32* __restrict__ zero,
 //   xsum[g][c] = sum_{k in g} x[k][c] (wrapping), Cp entries per group and 64 spare at the end.
 // It also zeroes out when the main kernel accumulates split-K parts with atomics.
 //
-// The main kernel: a block owns BM = 32 WR rows x BN = 32 WC columns, one 32 x 32 MFMA tile per
-// wave, and a range of whole groups (split-K: parts add into out with u32 atomics, which are
-// exact and order-free in Z / 2^32).  It streams the chunks of its range through NS LDS stages
-// with global->LDS DMA: per chunk the w rows (16-byte segments, segment-major so a wave's A
-// reads are contiguous), the x' columns, the rows' scales and zero points and the group's
-// column sums.  Each wave issues a fixed share of a stage's DMA ops; at the top of chunk i it
+// The main kernel: a block owns BM = 32 WR TM rows x BN = 32 WC TN columns, TM x TN 32 x 32
+// MFMA tiles per wave (a tile row's unpacked w operand serves its TN column tiles), and a range
+// of whole groups (split-K: parts add into out with u32 atomics, which are exact and order-free
+// in Z / 2^32).  It streams the chunks of its range through NS LDS stages with global->LDS DMA:
+// per chunk the w rows (each op RPO rows x SPR contiguous 16-byte segments, XOR-swizzled in
+// LDS), the x' columns, the rows' scales and zero points and the group's column sums.  Each wave issues a fixed share of a stage's DMA ops; at the top of chunk i it
 // waits until only its ops of the NS - 2 younger stages are outstanding, a barrier makes the
 // whole stage visible and retires the stage read last, and the wave refills that stage with
 // chunk i + NS - 1 (clamped to the range, so every pass issues the same ops).  No other
@@ -1789,33 +1789,35 @@ UNP_DEV void dqg_prep(const XT* __restrict__ x, u8* __restrict__ xp, u32* __rest
 UNP_DEV void dma_stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 template <int BM, int BN, int KC, int XB> struct dqg_stage {
-  u8 a[BM * KC / 2];  // w: segment s of row r (16 bytes) at (s * BM + r) * 16
+  u8 a[BM * KC / 2];   // w: row r's 16-byte segment s at r * KC / 2 + 16 * (s ^ swz(r))
   u8 b[XB * KC * BN];  // x': plane p, segment ks, column c at ((p * KC / 16 + ks) * BN + c) * 16
   u32 s[BM];           // the rows' scales
   u32 z[BM];           // the rows' zero points
-  u32 x[64];           // the group's column sums (BN used)
+  u32 x[BN < 64 ? 64 : BN];  // the group's column sums (whole 64-lane DMA ops)
 };
 
-template <bool QS, int XB, int G, int KC, int WR, int WC, int NS>
+template <bool QS, int XB, int G, int KC, int WR, int WC, int TM, int TN, int NS>
 UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, const i32* __restrict__ scale,
                         const u8* __restrict__ xp, const u32* __restrict__ xsum, i32* __restrict__ out, i64 R,
                         i64 K, i64 C, i64 Cp, i64 S) {
-  static_assert(WR * WC == 4 && KC % 64 == 0 && G % KC == 0 && NS >= 3, "four waves, whole chunks");
-  constexpr int BM = 32 * WR, BN = 32 * WC;
+  constexpr int NW = WR * WC;
+  static_assert(NW == 4 && KC % 64 == 0 && G % KC == 0 && NS >= 3 && NS <= 4, "four waves, whole chunks");
+  constexpr int BM = 32 * WR * TM, BN = 32 * WC * TN;
   typedef dqg_stage<BM, BN, KC, XB> St;
-  constexpr int NA = BM * KC / 2 / 1024, NB = XB * KC * BN / 1024, NSZ = BM / 64;
+  // w DMA: an op moves RPO rows x SPR contiguous 16-byte segments; the segment order inside a
+  // row is XOR-swizzled by (row / FD) % SPR so that eight consecutive rows' reads of one
+  // segment fall in eight distinct LDS bank groups.
+  constexpr int SPR = KC / 32, RPO = 64 / SPR, FD = 16 / SPR;
+  constexpr int NA = BM * KC / 2 / 1024, NB = XB * KC * BN / 1024, NSZ = BM / 64, NX = (BN + 63) / 64;
   static_assert(NA * 1024 == BM * KC / 2 && NB * 1024 == XB * KC * BN && NSZ * 64 == BM, "whole 64-lane ops");
-  constexpr int OA = (NA + 3) / 4, OB = (NB + 3) / 4, OS = (2 * NSZ + 3) / 4;
-  constexpr int OPW = OA + OB + OS + 1;  // DMA ops per wave per stage
+  constexpr int OA = (NA + NW - 1) / NW, OB = (NB + NW - 1) / NW, OS = (2 * NSZ + NW - 1) / NW, OX = (NX + NW - 1) / NW;
+  constexpr int OPW = OA + OB + OS + OX;  // DMA ops per wave per stage
   static_assert((NS - 2) * OPW < 64, "the wait count fits vmcnt");
   __shared__ __attribute__((aligned(16))) St st0;
   __shared__ __attribute__((aligned(16))) St st1;
   __shared__ __attribute__((aligned(16))) St st2;
   __shared__ __attribute__((aligned(16))) St st3;
-  __shared__ __attribute__((aligned(16))) St st4;
-  __shared__ __attribute__((aligned(16))) St st5;
-  static_assert(NS <= 6, "at most six stages");
-  St* const stages[6] = {&st0, &st1, &st2, &st3, &st4, &st5};
+  St* const stages[4] = {&st0, &st1, &st2, &st3};
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave / WC, wc = wave % WC, q = lane >> 5, l32 = lane & 31;
@@ -1835,7 +1837,7 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
   const i64 wbytes_row = K / 2;
 
   // A stage's DMA: every wave issues the same sequence, OA ops of w rows, OB of x' columns, OS
-  // of scales or zero points (16-byte ops move 1 KiB, 4-byte ops 256 B) and one of the column
+  // of scales or zero points (16-byte ops move 1 KiB, 4-byte ops 256 B) and OX of the column
   // sums, so every wave waits on the same count with no branch.  Where a kind has fewer ops
   // than waves the extra ones repeat an op of that kind: both DMAs write the same bytes.
   auto issue_stage = [&](St* stp, i64 i) {
@@ -1843,74 +1845,99 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
     const i64 k0 = chunk * KC, g = k0 / G;
 #pragma unroll
     for (int m = 0; m < OA; ++m) {
-      const int o = (wave + 4 * m) % NA, sl = o * 64 + lane, seg = sl / BM, r = sl % BM;
+      const int o = (wave + NW * m) % NA;
+      const int r = o * RPO + lane / SPR, seg = (lane % SPR) ^ ((r / FD) % SPR);
       const i64 row = tile_r + r < R ? tile_r + r : R - 1;
       __builtin_amdgcn_global_load_lds(w + row * wbytes_row + k0 / 2 + 16 * seg, (lds_void*)(stp->a + o * 1024), 16, 0, 0);
     }
 #pragma unroll
     for (int m = 0; m < OB; ++m) {
-      const int o = (wave + 4 * m) % NB, sl = o * 64 + lane, c = sl % BN, rest = sl / BN;
+      const int o = (wave + NW * m) % NB, sl = o * 64 + lane, c = sl % BN, rest = sl / BN;
       const int pl = rest / (KC / 16), ks = rest % (KC / 16);
       __builtin_amdgcn_global_load_lds(xp + (((chunk * XB + pl) * (KC / 16) + ks) * Cp + tile_c + c) * 16,
                                        (lds_void*)(stp->b + o * 1024), 16, 0, 0);
     }
 #pragma unroll
     for (int m = 0; m < OS; ++m) {
-      const int o = (wave + 4 * m) % (2 * NSZ), which = o / NSZ, part = o % NSZ;
+      const int o = (wave + NW * m) % (2 * NSZ), which = o / NSZ, part = o % NSZ;
       const i64 r = tile_r + part * 64 + lane;
       const i64 row = r < R ? r : R - 1;
       __builtin_amdgcn_global_load_lds((which == 0 ? scale : zero) + row * ng + g,
                                        (lds_void*)((which == 0 ? stp->s : stp->z) + part * 64), 4, 0, 0);
     }
-    __builtin_amdgcn_global_load_lds(xsum + g * Cp + tile_c + lane, (lds_void*)stp->x, 4, 0, 0);
+#pragma unroll
+    for (int m = 0; m < OX; ++m) {
+      const int o = (wave + NW * m) % NX;
+      __builtin_amdgcn_global_load_lds(xsum + g * Cp + tile_c + 64 * o + lane, (lds_void*)(stp->x + 64 * o), 4, 0, 0);
+    }
   };
 
-  i32x16 P[XB];
+  i32x16 P[TM][TN][XB];
+  u32 total[TM][TN][16];
 #pragma unroll
-  for (int b = 0; b < XB; ++b)
+  for (int a = 0; a < TM; ++a)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) P[b][v] = 0;
-  u32 total[16];
+    for (int t = 0; t < TN; ++t)
 #pragma unroll
-  for (int v = 0; v < 16; ++v) total[v] = 0;
+      for (int v = 0; v < 16; ++v) total[a][t][v] = 0;
+  i32x16 Z;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) Z[v] = 0;
 
   auto compute = [&](const St* stp, i64 i) {
+    const bool first = cpg == 1 || i % cpg == 0;  // the group's first chunk: accumulators start at 0
 #pragma unroll
     for (int j = 0; j < KC / 64; ++j) {
-      const vec<u32, 4> araw = *reinterpret_cast<const vec<u32, 4>*>(stp->a + ((2 * j + q) * BM + 32 * wr + l32) * 16);
-      const i32x4 a0 = unpack16<QS>((u64)araw.e[0] | ((u64)araw.e[1] << 32));
-      const i32x4 a1 = unpack16<QS>((u64)araw.e[2] | ((u64)araw.e[3] << 32));
+      i32x4 a0[TM], a1[TM];
+#pragma unroll
+      for (int a = 0; a < TM; ++a) {
+        const int r = 32 * (wr * TM + a) + l32, sg = 2 * j + q;
+        const vec<u32, 4> araw =
+            *reinterpret_cast<const vec<u32, 4>*>(stp->a + r * (KC / 2) + 16 * (sg ^ ((r / FD) % SPR)));
+        a0[a] = unpack16<QS>((u64)araw.e[0] | ((u64)araw.e[1] << 32));
+        a1[a] = unpack16<QS>((u64)araw.e[2] | ((u64)araw.e[3] << 32));
+      }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int ks = 4 * j + 2 * q + h;
 #pragma unroll
-        for (int b = 0; b < XB; ++b) {
-          const i32x4 bv = *reinterpret_cast<const i32x4*>(stp->b + ((b * (KC / 16) + ks) * BN + 32 * wc + l32) * 16);
-          P[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? a1 : a0, bv, P[b], 0, 0, 0);
-        }
+        for (int t = 0; t < TN; ++t)
+#pragma unroll
+          for (int b = 0; b < XB; ++b) {
+            const i32x4 bv =
+                *reinterpret_cast<const i32x4*>(stp->b + ((b * (KC / 16) + ks) * BN + 32 * (wc * TN + t) + l32) * 16);
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+              P[a][t][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? a1[a] : a0[a], bv,
+                                                                 (j == 0 && h == 0 && first) ? Z : P[a][t][b], 0, 0, 0);
+          }
       }
     }
     if (cpg == 1 || (i + 1) % cpg == 0) {
-      // The group ends: lane element v is row 8 (v / 4) + 4 q + v % 4 of the wave tile.
-      const u32 xc = stp->x[32 * wc + l32];
+      // The group ends: lane element v is row 8 (v / 4) + 4 q + v % 4 of its 32 x 32 tile.
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int lr = 32 * wr + 8 * i4 + 4 * q;
-        const vec<u32, 4> s4 = *reinterpret_cast<const vec<u32, 4>*>(stp->s + lr);
-        const vec<u32, 4> z4 = *reinterpret_cast<const vec<u32, 4>*>(stp->z + lr);
+      for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int v = 4 * i4 + e;
-          u32 p = (u32)P[0][v];
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const int lr = 32 * (wr * TM + a) + 8 * i4 + 4 * q;
+          const vec<u32, 4> s4 = *reinterpret_cast<const vec<u32, 4>*>(stp->s + lr);
+          const vec<u32, 4> z4 = *reinterpret_cast<const vec<u32, 4>*>(stp->z + lr);
+          u32 zs[4];
 #pragma unroll
-          for (int b = 1; b < XB; ++b) p += (u32)P[b][v] << (8 * b);
-          total[v] += s4.e[e] * p - (z4.e[e] * s4.e[e]) * xc;
+          for (int e = 0; e < 4; ++e) zs[e] = z4.e[e] * s4.e[e];
+#pragma unroll
+          for (int t = 0; t < TN; ++t) {
+            const u32 xc = stp->x[32 * (wc * TN + t) + l32];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int v = 4 * i4 + e;
+              u32 p = (u32)P[a][t][0][v];
+#pragma unroll
+              for (int b = 1; b < XB; ++b) p += (u32)P[a][t][b][v] << (8 * b);
+              total[a][t][v] += s4.e[e] * p - zs[e] * xc;
+            }
+          }
         }
-      }
-#pragma unroll
-      for (int b = 0; b < XB; ++b)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) P[b][v] = 0;
     }
   };
 
@@ -1929,16 +1956,21 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
       if (i < n) compute(stages[I], i);
     }
   }
-  const i64 c = tile_c + 32 * wc + l32;
-  if (c < C) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const i64 r = tile_r + 32 * wr + 8 * (v >> 2) + 4 * q + (v & 3);
-      if (r < R) {
-        if (S == 1) out[r * C + c] = (i32)total[v];
-        else __hip_atomic_fetch_add(reinterpret_cast<u32*>(out) + r * C + c, total[v], __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-      }
+  for (int t = 0; t < TN; ++t) {
+    const i64 c = tile_c + 32 * (wc * TN + t) + l32;
+    if (c < C) {
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const i64 r = tile_r + 32 * (wr * TM + a) + 8 * (v >> 2) + 4 * q + (v & 3);
+          if (r < R) {
+            if (S == 1) out[r * C + c] = (i32)total[a][t][v];
+            else __hip_atomic_fetch_add(reinterpret_cast<u32*>(out) + r * C + c, total[a][t][v], __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
     }
   }
 }

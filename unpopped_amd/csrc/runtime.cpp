@@ -785,7 +785,9 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
   }
   const long long xbytes = x32 ? 4 : 1;
   const long long bn = dec != SIZE_MAX ? x->l.entries[dec].cols : 16, Cpd = (C + bn - 1) / bn * bn;
-  if (dec != SIZE_MAX && prep16 != SIZE_MAX && C <= 128 && K > 0 && K % group == 0 && (w & 15) == 0 &&
+  // Decode up to 64 columns for I8 activations (the streaming entry's 128 x 64 tiles win beyond),
+  // up to 128 for I32.
+  if (dec != SIZE_MAX && prep16 != SIZE_MAX && C <= (x32 ? 128 : 64) && K > 0 && K % group == 0 && (w & 15) == 0 &&
       (zp & 3) == 0 && (sc & 3) == 0 && (out & 3) == 0 && (xa & (x32 ? 3 : 0)) == 0 &&
       R * (K / 2) < 0x7FFFFFFFLL && K * Cpd * xbytes < 0x7FFFFFFFLL) {
     // Decode: repack x for 16-column tiles (Cp a whole number of the entry's column tiles), then
