@@ -881,6 +881,32 @@ def test_config4_gather_full(hip_device, dist):
     assert np.array_equal(got, table[ids])
 
 
+@pytest.mark.parametrize("C,xdt,entry", [(16, np.int8, "_dec1"), (64, np.int8, "_dec4"), (1024, np.int8, "_stream"),
+                                          (16, np.int32, "_dec1")])
+def test_dequant_gemm_full_size(hip_device, C, xdt, entry):
+    """The dequantizing GEMM at the bench's LLM shape (U4 w 8192 x 28672, full-range I32 zero
+    points and scales per 128 columns), with sampled rows against the oracle: rows are
+    independent, so the oracle runs on the sampled rows alone.  The samples include both edges
+    of every 128-row tile and a spread inside."""
+    R, K, G = 8192, 28672, 128
+    ng = K // G
+    H.say(f"[case] dequant GEMM full size U4 {R}x{K} g{G} times {np.dtype(xdt).name} {K}x{C}")
+    r = np.random.default_rng(C * 7 + np.dtype(xdt).itemsize)
+    w = synth.nibbles(6, R * K)
+    zero = r.integers(-2 ** 31, 2 ** 31, size=R * ng, dtype=np.int64).astype(np.int32)
+    scale = r.integers(-2 ** 31, 2 ** 31, size=R * ng, dtype=np.int64).astype(np.int32)
+    info = np.iinfo(xdt)
+    x = r.integers(int(info.min), int(info.max) + 1, size=K * C, dtype=np.int64).astype(xdt)
+    got = H.dequant_gemm(w, zero, scale, x, R, K, C, G)
+    assert _gemm_entry("U4", xdt, G).endswith(entry)
+    rows = sorted({0, R - 1, *range(127, R, 1024), *range(128, R, 1024), *r.integers(0, R, size=24).tolist()})
+    half = K // 2
+    for row in rows:
+        want = oracle.dequant_gemm_i32(w[row * half:(row + 1) * half], zero[row * ng:(row + 1) * ng],
+                                       scale[row * ng:(row + 1) * ng], x, 1, K, C, G)
+        assert np.array_equal(got[row], want[0]), row
+
+
 def test_config5_dequant_full(hip_device):
     H.say("[case] config 5: dequant 8192x28672 g128")
     R, Cc, G = 8192, 28672, 128
