@@ -270,6 +270,30 @@ typedef struct unp_arg {
 int32_t unp_hip_exec_create(const unp_generated* g, unp_exec** out, unp_error* err);
 int32_t unp_hip_exec_launch(unp_exec* e, const unp_arg* args, size_t nargs, void* stream,
                             unp_error* err);
+/* One buffer as the reference's storage image (TypedBuffer, crates/unpopped/src/oracle/
+ * buffers.rs:16-42; the C leg passes the same per buffer, unpopped-cpu-c/src/base.rs:65-103):
+ * the device address of the allocation, the view's rank, shape and signed element strides, and
+ * its base offset in elements.  Sub-byte kinds (U4, I4) count elements, two to a byte. */
+#define UNP_MAX_RANK 8
+typedef struct unp_view {
+  uint64_t data;
+  int32_t rank;
+  int32_t pad;
+  int64_t shape[UNP_MAX_RANK];
+  int64_t stride[UNP_MAX_RANK];
+  int64_t base;
+} unp_view;
+
+/* unp_hip_exec_launch with the buffers as storage images, in the KernelFn's parameter order
+ * (views for the buffer parameters, then the scalars).  This backend's kernels read dense
+ * row-major storage: a view is taken at data + base elements when every axis longer than one
+ * has the row-major stride, and, for the gather's index buffer, also as the reference's
+ * broadcast [n, d] with strides [1, 0] (tests/kernel_parallel_gather_agrees.rs:80-84).  Any
+ * other view (transposed, strided, negative strides, a sub-byte view starting mid-byte) is
+ * refused with UNP_INVALID_ARGUMENT before anything launches: refuse rather than approximate
+ * (backend.rs:703-707). */
+int32_t unp_hip_exec_launch_views(unp_exec* e, const unp_view* views, size_t nviews, const int64_t* scalars,
+                                  size_t nscalars, void* stream, unp_error* err);
 /* The last launch's geometry and chosen entry point (for reports). */
 int32_t unp_hip_exec_last_launch(const unp_exec* e, uint32_t grid[3], uint32_t block[3],
                                  char* entry, size_t entry_len);

@@ -916,3 +916,70 @@ def test_config5_dequant_full(hip_device):
     got = H.dequant4(q, s, z, R, Cc, G)
     want = oracle.dequant4_bf16(q, s, z, R, Cc, G)
     assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------------------------------
+# Buffers as storage images (unp_hip_exec_launch_views; TypedBuffer, oracle/buffers.rs:16-42)
+# ---------------------------------------------------------------------------------------
+
+def test_views_dense_with_base_match_the_pointer_launch(hip_device):
+    """Dense row-major views at a base offset launch the kernel on data + base; an axis of extent
+    one may carry any stride.  The results equal the pointer launch bit for bit."""
+    H.say("[case] views: dense, base offset")
+    R, Cc = 37, 300
+    x = synth.normal_f32(11, R * Cc + 5)
+    ex = H.executor(kind="row_reduce2", dtype="F32", rank=2, op="Sum", op1="Max")
+    din = u.DeviceBuffer.from_array(x)
+    a0, a1, b0, b1 = (u.DeviceBuffer(R * 4) for _ in range(4))
+    ex.launch(din.at(20), a0, a1, R, Cc)
+    ex.launch_views([(din, (R, Cc), None, 5), (b0, (R,), None, 0), (b1, (1, R), (977, 1), 0)], [R, Cc])
+    u.synchronize()
+    assert np.array_equal(a0.download(np.float32, R), b0.download(np.float32, R))
+    assert np.array_equal(a1.download(np.float32, R), b1.download(np.float32, R))
+    assert np.array_equal(b1.download(np.float32, R), oracle.reduce_rows(x[5:].reshape(R, Cc), "Max"))
+
+
+def test_views_gather_index_broadcast(hip_device):
+    """The reference's embedding passes the ids as a broadcast [n, d] view with strides [1, 0]
+    (tests/kernel_parallel_gather_agrees.rs:80-84); the table and the output are dense."""
+    H.say("[case] views: gather index broadcast")
+    V, D, n = 50, 64, 33
+    table = (np.arange(V * D, dtype=np.uint16) * 7).reshape(V, D)
+    ids = synth.uniform_ids_i32(12, n, V)
+    ex = H.executor(kind="gather", dtype="Bf16", rank=2, index_dtype="I32", oob="ZeroFill")
+    dt, di, do = u.DeviceBuffer.from_array(table), u.DeviceBuffer.from_array(ids), u.DeviceBuffer(n * D * 2)
+    ex.launch_views([(dt, (V, D), None, 0), (di, (n, D), (1, 0), 0), (do, (n, D), None, 0)], [n, D, V])
+    u.synchronize()
+    assert np.array_equal(do.download(np.uint16, n * D).reshape(n, D), table[ids])
+
+
+@pytest.mark.parametrize("what", ["transposed", "negative", "broadcast data", "odd u4 base"])
+def test_views_the_kernels_cannot_read_are_refused(hip_device, what):
+    """A view other than dense row-major (or the gather index broadcast) is refused with
+    INVALID_ARGUMENT before anything launches, and the output is untouched."""
+    H.say(f"[case] views refused: {what}")
+    if what == "odd u4 base":
+        R, Cc, G = 4, 256, 128
+        ex = H.executor(kind="dequant4", q_kind="U4", z_kind="U4", group=G, out_kind="Bf16")
+        q, s, z = u.DeviceBuffer(R * Cc), u.DeviceBuffer(R * 2 * 2), u.DeviceBuffer(R)
+        out = u.DeviceBuffer(R * Cc * 2)
+        out.fill(0x5A)
+        views = [(q, (R, Cc), None, 1), (s, (R, Cc // G), None, 0), (z, (R, Cc // G), None, 0), (out, (R, Cc), None, 0)]
+        scalars = [R, Cc]
+        check, count, dt = out, R * Cc, np.uint16
+    else:
+        R, Cc = 16, 64
+        ex = H.executor(kind="row_reduce2", dtype="F32", rank=2, op="Sum", op1="Max")
+        din = u.DeviceBuffer.from_array(synth.normal_f32(13, R * Cc))
+        o0, o1 = u.DeviceBuffer(R * 4), u.DeviceBuffer(R * 4)
+        o0.fill(0x5A)
+        strides = {"transposed": (1, R), "negative": (-Cc, 1), "broadcast data": (0, 1)}[what]
+        views = [(din, (R, Cc), strides, (R - 1) * Cc if what == "negative" else 0), (o0, (R,), None, 0),
+                 (o1, (R,), None, 0)]
+        scalars = [R, Cc]
+        check, count, dt = o0, R, np.float32
+    with pytest.raises(u.UnpError) as e:
+        ex.launch_views(views, scalars)
+    assert e.value.kind == "InvalidArgument", e.value
+    u.synchronize()
+    assert np.all(check.download(np.uint8, count * np.dtype(dt).itemsize) == 0x5A)

@@ -318,6 +318,25 @@ class Executor:
         err = _lib.Error()
         check(_lib.lib().unp_hip_exec_launch(self._h, arr, len(args), stream, C.byref(err)), err)
 
+    def launch_views(self, views, scalars, stream: int = 0) -> None:
+        """The buffers as storage images: ``views`` is a list of ``(buffer, shape, strides, base)``
+        in the KernelFn's buffer order (strides None: dense row-major; strides and base in
+        elements), ``scalars`` the integer parameters after them."""
+        arr = (_lib.View * len(views))()
+        for i, (buf, shape, strides, base) in enumerate(views):
+            shape = list(shape)
+            if strides is None:
+                strides, acc = [0] * len(shape), 1
+                for d in range(len(shape) - 1, -1, -1):
+                    strides[d], acc = acc, acc * shape[d]
+            arr[i].data, arr[i].rank, arr[i].base = buf.ptr, len(shape), int(base)
+            for d, (n, st) in enumerate(zip(shape, strides)):
+                arr[i].shape[d], arr[i].stride[d] = int(n), int(st)
+        sc = (C.c_int64 * max(len(scalars), 1))(*[int(v) for v in scalars])
+        err = _lib.Error()
+        check(_lib.lib().unp_hip_exec_launch_views(self._h, arr, len(views), sc, len(scalars), stream, C.byref(err)),
+              err)
+
     def last_launch(self) -> dict:
         g = (C.c_uint32 * 3)()
         b = (C.c_uint32 * 3)()

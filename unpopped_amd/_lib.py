@@ -47,6 +47,16 @@ class Arg(C.Structure):
     _fields_ = [("is_buffer", C.c_int32), ("pad", C.c_int32), ("value", C.c_uint64)]
 
 
+MAX_RANK = 8
+
+
+class View(C.Structure):
+    """unp_view: a buffer as the reference's storage image (device address, rank, shape, signed
+    element strides, base offset in elements)."""
+    _fields_ = [("data", C.c_uint64), ("rank", C.c_int32), ("pad", C.c_int32), ("shape", C.c_int64 * MAX_RANK),
+                ("stride", C.c_int64 * MAX_RANK), ("base", C.c_int64)]
+
+
 _lib = None
 
 
@@ -109,6 +119,7 @@ def lib() -> C.CDLL:
         "unp_hip_event_elapsed_ms": (i32, [P, P, C.POINTER(C.c_float)]),
         "unp_hip_exec_create": (i32, [P, C.POINTER(P), E]),
         "unp_hip_exec_launch": (i32, [P, C.POINTER(Arg), sz, P, E]),
+        "unp_hip_exec_launch_views": (i32, [P, C.POINTER(View), sz, C.POINTER(C.c_int64), sz, P, E]),
         "unp_hip_exec_last_launch": (i32, [P, C.POINTER(u32), C.POINTER(u32), C.c_char_p, sz]),
         "unp_hip_exec_destroy": (None, [P]),
     }

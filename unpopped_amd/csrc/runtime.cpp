@@ -859,6 +859,79 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
 
 }  // namespace
 
+// Element bits of buffer parameter b of a form: the element kinds of its storage images.
+static int view_elem_bits(const unp_form& f, size_t b) {
+  int32_t k = f.dtype;
+  if (f.kind == UNP_FORM_GATHER) {
+    k = (b == 2 || (int)b == f.data_slot) ? f.dtype : f.index_dtype;
+  } else if (f.kind == UNP_FORM_DEQUANT4) {
+    const int32_t ks[4] = {f.q_kind, UNP_F16, f.z_kind, f.out_kind};
+    if (b < 4) k = ks[b];
+  } else if (f.kind == UNP_FORM_DEQUANT_GEMM) {
+    const int32_t ks[5] = {f.q_kind, UNP_I32, UNP_I32, f.dtype, UNP_I32};
+    if (b < 5) k = ks[b];
+  }
+  const size_t by = unp::kind_bytes(k);
+  return by ? (int)(8 * by) : 4;  // the sub-byte kinds this backend reads are 4-bit
+}
+
+// A view the kernels can read: dense row-major from its base (an axis of extent 0 or 1 may carry
+// any stride), or the gather index's column broadcast [n, d] with strides [1, 0].
+static bool view_readable(const unp_view& v, bool index_broadcast_ok) {
+  for (int d = 0; d < v.rank; ++d)
+    if (v.shape[d] == 0) return true;  // empty: nothing is read
+  if (index_broadcast_ok && v.rank == 2 && v.stride[0] == 1 && v.stride[1] == 0) return true;
+  int64_t expect = 1;
+  for (int d = v.rank - 1; d >= 0; --d) {
+    if (v.shape[d] < 0) return false;
+    if (v.shape[d] > 1 && v.stride[d] != expect) return false;
+    expect *= v.shape[d];
+  }
+  return true;
+}
+
+extern "C" int32_t unp_hip_exec_launch_views(unp_exec* x, const unp_view* views, size_t nviews,
+                                             const int64_t* scalars, size_t nscalars, void* stream,
+                                             unp_error* err) {
+  if (!x) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null executor");
+    return UNP_INVALID_ARGUMENT;
+  }
+  if ((nviews && !views) || (nscalars && !scalars)) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null views or scalars");
+    return UNP_INVALID_ARGUMENT;
+  }
+  std::vector<unp_arg> args(nviews + nscalars);
+  for (size_t b = 0; b < nviews; ++b) {
+    const unp_view& v = views[b];
+    if (v.rank < 0 || v.rank > UNP_MAX_RANK) {
+      set_error(err, UNP_INVALID_ARGUMENT, "buffer " + std::to_string(b) + ": rank out of range");
+      return UNP_INVALID_ARGUMENT;
+    }
+    const bool index_buffer = x->l.form.kind == UNP_FORM_GATHER && b < 2 && (int)b != x->l.form.data_slot;
+    if (!view_readable(v, index_buffer)) {
+      set_error(err, UNP_INVALID_ARGUMENT,
+                "buffer " + std::to_string(b) +
+                    ": a strided view; this backend's kernels read dense row-major storage, so make the view "
+                    "contiguous first");
+      return UNP_INVALID_ARGUMENT;
+    }
+    const int bits = view_elem_bits(x->l.form, b);
+    if (v.base < 0 || (v.base * bits) % 8 != 0) {
+      set_error(err, UNP_INVALID_ARGUMENT,
+                "buffer " + std::to_string(b) + ": the base offset must be a whole byte and not negative");
+      return UNP_INVALID_ARGUMENT;
+    }
+    args[b].is_buffer = 1;
+    args[b].value = v.data + (uint64_t)(v.base * bits / 8);
+  }
+  for (size_t i = 0; i < nscalars; ++i) {
+    args[nviews + i].is_buffer = 0;
+    args[nviews + i].value = (uint64_t)scalars[i];
+  }
+  return unp_hip_exec_launch(x, args.data(), args.size(), stream, err);
+}
+
 extern "C" int32_t unp_hip_exec_launch(unp_exec* x, const unp_arg* args, size_t nargs, void* stream,
                                        unp_error* err) {
   if (!x) {
