@@ -37,8 +37,9 @@ def log(msg: str) -> None:
 
 
 class Case:
-    def __init__(self, name, what, nbytes, elements, setup):
+    def __init__(self, name, what, nbytes, elements, setup, ops=0):
         self.name, self.what, self.nbytes, self.elements, self.setup = name, what, nbytes, elements, setup
+        self.ops = ops  # integer operations per launch, for the lines that run on MFMA
         self.launch = None
 
 
@@ -152,6 +153,30 @@ def build_extras(u, synth):
                        8192 * 4096, row_reduce("softmax")))
     extras.append(Case("rr_rmsnorm", "f32 8192x4096 RowReduce RMS norm (Mean of squares, scale)", rr_bytes,
                        8192 * 4096, row_reduce("rms_norm")))
+
+    # The dequantizing GEMM (tests/support/dequant.rs:104-181) at a weight of LLM size, for a
+    # decode width and a prefill width: U4 w 8192 x 28672, I32 zero point and scale per 128
+    # columns, I8 activations.  Each launch is the x repack plus the main kernel.
+    R, K, G = 8192, 28672, 128
+    ng = K // G
+
+    def gemm(C):
+        def setup():
+            w = synth.nibbles(6, R * K)
+            zero = synth.int16_i32(61, R * ng)
+            scale = (synth.int16_i32(62, R * ng) - 8) * 97
+            x = (synth.int16_i32(63, K * C) * 13 - 100).astype(np.int8)
+            # An executor of its own, so that its last launch names this case's entry.
+            ex = u.Executor(u.HipBackend().lower_kernel(H.kernel_for(kind="dequant_gemm", q_kind="U4", dtype="I8",
+                                                                     group=G)))
+            dw, dz, ds, dx = (u.DeviceBuffer.from_array(a) for a in (w, zero, scale, x))
+            do = u.DeviceBuffer(R * C * 4)
+            return lambda: ex.launch(dw, dz, ds, dx, do, R, K, C), ex
+        return setup
+    for C, tag in ((16, "decode"), (1024, "prefill")):
+        nbytes = R * K // 2 + R * ng * 8 + K * C + R * C * 4
+        extras.append(Case(f"gemm_{tag}", f"dequant GEMM U4 {R}x{K} g{G} times I8 {K}x{C} (I32 out)", nbytes, R * C,
+                           gemm(C), ops=2 * R * K * C))
     return extras
 
 
@@ -177,6 +202,9 @@ def time_cases(u, cases, steps):
             "GBps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_GBPS, 4),
             "elements_per_s": round(c.elements / (ms * 1e-3), 1),
         })
+        if c.ops:
+            per[-1]["TOPs"] = round(c.ops / (ms * 1e-3) / 1e12, 1)
+            per[-1]["frac_of_int8_mfma_peak"] = round(c.ops / (ms * 1e-3) / 1e12 / 5000, 4)
         log(f"[bench] {c.name}: {ms * 1e3:.1f} us, {gbps:.0f} GB/s ({100 * gbps / PEAK_GBPS:.1f}% of peak)")
     return per
 
@@ -362,14 +390,59 @@ def ceilings(u, cus: int, nbytes: int = 1 << 30, reps: int = 10) -> None:
                           "GBps": round(best[0], 1), "frac_of_peak": round(best[0] / PEAK_GBPS, 4)}), flush=True)
 
 
+FLUSH_SRC = r"""
+typedef unsigned int u32;
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+// Plain (cached) loads over a buffer larger than the MALL: evicts what earlier launches left
+// there with clean lines, so the next timed launch reads its inputs from HBM.
+extern "C" __global__ void __launch_bounds__(256) unp_mall_flush(const u32x4* __restrict__ s, u32* __restrict__ sink,
+                                                                  long long n) {
+  const long long st = (long long)gridDim.x * 256;
+  u32 acc = 0;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += st) acc ^= s[i].x ^ s[i].w;
+  if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+"""
+
+
+class MallFlush:
+    """Reads 512 MiB with plain loads; launched between timed launches of one kernel."""
+
+    def __init__(self, u, cus: int):
+        import ctypes as C
+
+        from unpopped_amd import _lib
+
+        self.C, self._lib, self.L = C, _lib, _lib.lib()
+        co = u.HipCompiler().compile(FLUSH_SRC, "unp_mall_flush")
+        self.img = C.create_string_buffer(co, len(co))
+        self.m, self.f, err = C.c_void_p(), C.c_void_p(), _lib.Error()
+        _lib.check(self.L.unp_hip_module_load(self.img, len(co), C.byref(self.m), C.byref(err)), err)
+        _lib.check(self.L.unp_hip_get_function(self.m, b"unp_mall_flush", C.byref(self.f), C.byref(err)), err)
+        self.buf, self.sink = u.DeviceBuffer(512 << 20), u.DeviceBuffer(64)
+        self.buf.fill(1)
+        self.args = (C.c_uint64 * 3)(self.buf.ptr, self.sink.ptr, (512 << 20) // 16)
+        self.grid, self.block = (C.c_uint32 * 3)(cus * 4, 1, 1), (C.c_uint32 * 3)(256, 1, 1)
+
+    def run(self) -> None:
+        err = self._lib.Error()
+        self._lib.check(self.L.unp_hip_launch(self.f, self.grid, self.block, 0, None, self.args,
+                                              self.C.sizeof(self.args), self.C.byref(err)), err)
+
+
 def gemm_lines(u, synth, steps: int, warmup: int) -> None:
     """The dequantizing GEMM (tests/support/dequant.rs:104-181) at a weight of LLM size: U4 w
     8192 x 28672 with an I32 zero point and scale per 128 columns, times x of C columns (I8 and I32),
-    one JSON line per shape.  Bytes are w + zero + scale + x + out; operations 2 R K C."""
+    one JSON line per shape: the median of `steps` launches, each timed alone with HIP events after
+    a 512 MiB read with plain loads has evicted the weight from the MALL.  Bytes are w + zero + scale + x + out;
+    operations 2 R K C."""
     from unpopped_amd import forms as H
 
     R, K, G = 8192, 28672, 128
     ng = K // G
+    # Streamed between timed launches so that no launch finds the weight in the 256 MB MALL
+    # from the one before, as consecutive layers of a model would not.
+    flush = MallFlush(u, u.device_info()[1])
     w = synth.nibbles(6, R * K)
     zero = synth.int16_i32(61, R * ng)
     scale = (synth.int16_i32(62, R * ng) - 8) * 97
@@ -382,13 +455,16 @@ def gemm_lines(u, synth, steps: int, warmup: int) -> None:
             for _ in range(warmup):
                 ex.launch(dw, dz, ds, dx, do, R, K, C)
             u.synchronize()
-            e0, e1 = u.Event(), u.Event()
-            e0.record()
-            for _ in range(steps):
+            ts = []
+            for i in range(steps):
+                flush.run()
+                e0, e1 = u.Event(), u.Event()
+                e0.record()
                 ex.launch(dw, dz, ds, dx, do, R, K, C)
-            e1.record()
-            e1.synchronize()
-            us = e0.elapsed_ms(e1) * 1e3 / steps
+                e1.record()
+                e1.synchronize()
+                ts.append(e0.elapsed_ms(e1) * 1e3)
+            us = float(np.median(ts))
             nbytes = R * K // 2 + R * ng * 8 + K * C * x.itemsize + R * C * 4
             ops = 2 * R * K * C
             log(f"[bench] gemm x {xk} C {C}: {us:.1f} us")
