@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 
 #include "kernel_ir.hpp"
 #include "unp_internal.hpp"
@@ -762,6 +763,34 @@ int32_t run_dequant(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_
 
 // The dequantizing GEMM: w, zero, scale, x, out, then R, K, C.  The MFMA entry takes whole
 // groups, 4-column rows of x and aligned operands; anything else runs the serial entry.
+bool ends_with(const std::string& s, const char* tail) {
+  const size_t n = std::strlen(tail);
+  return s.size() > n && s.compare(s.size() - n, n, tail) == 0;
+}
+
+// The two-launch dequant-GEMM schedules: the prep entry repacks x into the workspace (Cp columns,
+// its grid covering groups x (Cp / cols_per_prep_block)) and zeroes out when K is split; then the
+// main entry runs over `blocks` blocks with S splits of K.
+int32_t run_repacked(unp_exec* x, size_t prep, size_t main, uint64_t w, uint64_t zp, uint64_t sc, uint64_t xa,
+                     uint64_t out, long long R, long long K, long long C, long long Cp, long long prep_cols,
+                     long long S, long long blocks, hipStream_t s, unp_error* err) {
+  const long long group = x->l.form.group, ng = K / group, xbytes = x->l.form.dtype == UNP_I32 ? 4 : 1;
+  if (blocks > 0x7FFFFFFFLL || ng * (Cp / prep_cols) > 0x7FFFFFFFLL) {
+    set_error(err, UNP_INVALID_ARGUMENT, "dequant GEMM shape too large for one launch");
+    return UNP_INVALID_ARGUMENT;
+  }
+  // x' (K x Cp x digit planes bytes), then the group column sums (ng x Cp u32, 64 spare).
+  const size_t xp_bytes = (size_t)K * (size_t)Cp * (size_t)xbytes;
+  int32_t rc = ensure_ws(x, xp_bytes + ((size_t)ng * (size_t)Cp + 64) * 4, false, err);
+  if (rc != UNP_OK) return rc;
+  uint64_t xp = (uint64_t)x->ws, xs = xp + xp_bytes;
+  long long Kp = K, Cc = C, Cpp = Cp, G = group, n_out = S > 1 ? R * C : 0;
+  void* pparams[] = {&xa, &xp, &xs, &Kp, &Cc, &Cpp, &G, &out, &n_out};
+  if ((rc = launch(x, prep, (uint32_t)(ng * (Cp / prep_cols)), pparams, s, err)) != UNP_OK) return rc;
+  void* mparams[] = {&w, &zp, &sc, &xp, &xs, &out, &R, &K, &C, &Cpp, &S};
+  return launch(x, main, (uint32_t)blocks, mparams, s, err);
+}
+
 int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
   Args A;
   int32_t rc = take_args(a, n, 5, 3, A, err);
@@ -773,86 +802,54 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
   uint64_t w = A.buf[0], zp = A.buf[1], sc = A.buf[2], xa = A.buf[3], out = A.buf[4];
   const long long group = x->l.form.group;
   const bool x32 = x->l.form.dtype == UNP_I32;
-  size_t stream = SIZE_MAX, prep = SIZE_MAX, dec = SIZE_MAX, prep16 = SIZE_MAX;
+  const long long xbytes = x32 ? 4 : 1;
+  size_t stream = SIZE_MAX, prep = SIZE_MAX, dec = SIZE_MAX, prep16 = SIZE_MAX, mfma = SIZE_MAX, any = SIZE_MAX;
   for (size_t i = 0; i < x->l.entries.size(); ++i) {
     const std::string& sym = x->l.entries[i].symbol;
-    if (sym.size() > 7 && sym.compare(sym.size() - 7, 7, "_stream") == 0) stream = i;
-    if (sym.size() > 5 && sym.compare(sym.size() - 5, 5, "_prep") == 0) prep = i;
-    if (sym.size() > 7 && sym.compare(sym.size() - 7, 7, "_prep16") == 0) prep16 = i;
+    if (ends_with(sym, "_stream")) stream = i;
+    if (ends_with(sym, "_prep")) prep = i;
+    if (ends_with(sym, "_prep16")) prep16 = i;
+    if (ends_with(sym, "_mfma")) mfma = i;
+    if (ends_with(sym, "_any")) any = i;
     // The decode entry whose column tiles first cover C, else the widest (entries ascend).
     const int cols = x->l.entries[i].cols;
     if (cols > 0 && (dec == SIZE_MAX || x->l.entries[dec].cols < C)) dec = i;
   }
-  const long long xbytes = x32 ? 4 : 1;
-  const long long bn = dec != SIZE_MAX ? x->l.entries[dec].cols : 16, Cpd = (C + bn - 1) / bn * bn;
+  // The two-launch schedules need whole groups, a 16-byte aligned w and aligned operands.
+  const bool whole = K > 0 && K % group == 0 && (w & 15) == 0 && (zp & 3) == 0 && (sc & 3) == 0 &&
+                     (out & 3) == 0 && (xa & (x32 ? 3 : 0)) == 0;
   // Decode up to 64 columns for I8 activations (the streaming entry's 128 x 64 tiles win beyond),
-  // up to 128 for I32.
-  if (dec != SIZE_MAX && prep16 != SIZE_MAX && C <= (x32 ? 128 : 64) && K > 0 && K % group == 0 && (w & 15) == 0 &&
-      (zp & 3) == 0 && (sc & 3) == 0 && (out & 3) == 0 && (xa & (x32 ? 3 : 0)) == 0 &&
-      R * (K / 2) < 0x7FFFFFFFLL && K * Cpd * xbytes < 0x7FFFFFFFLL) {
-    // Decode: repack x for 16-column tiles (Cp a whole number of the entry's column tiles), then
-    // blocks of bm rows x bn columns x a split of K.
-    const long long bm = x->l.entries[dec].vec, maxg = x->l.entries[dec].k;
-    const long long ng = K / group, Cp = Cpd;
-    const long long tiles_r = (R + bm - 1) / bm, tiles_c = Cp / bn;
-    // Splits of K: about two blocks per CU, at most maxg groups per split, at least one.
-    long long S = (2LL * x->cu_count + tiles_r * tiles_c - 1) / (tiles_r * tiles_c);
-    S = std::max(S, (ng + maxg - 1) / maxg);
-    S = std::max(1LL, std::min(S, ng));
-    const long long blocks = (tiles_r + 7) / 8 * 8 * S * tiles_c;
-    if (blocks > 0x7FFFFFFFLL || ng * (Cp / 16) > 0x7FFFFFFFLL) {
-      set_error(err, UNP_INVALID_ARGUMENT, "dequant GEMM shape too large for one launch");
-      return UNP_INVALID_ARGUMENT;
+  // up to 128 for I32; its buffer loads take 32-bit offsets.
+  if (dec != SIZE_MAX && prep16 != SIZE_MAX && whole && C <= (x32 ? 128 : 64)) {
+    const long long bm = x->l.entries[dec].vec, bn = x->l.entries[dec].cols, maxg = x->l.entries[dec].k;
+    const long long ng = K / group, Cp = (C + bn - 1) / bn * bn;  // whole column tiles of the entry
+    if (R * (K / 2) < 0x7FFFFFFFLL && K * Cp * xbytes < 0x7FFFFFFFLL) {
+      const long long tiles_r = (R + bm - 1) / bm, tiles_c = Cp / bn;
+      // Splits of K: about two blocks per CU, at most maxg groups per split, at least one.
+      long long S = (2LL * x->cu_count + tiles_r * tiles_c - 1) / (tiles_r * tiles_c);
+      S = std::max(S, (ng + maxg - 1) / maxg);
+      S = std::max(1LL, std::min(S, ng));
+      const long long blocks = (tiles_r + 7) / 8 * 8 * S * tiles_c;
+      return run_repacked(x, prep16, dec, w, zp, sc, xa, out, R, K, C, Cp, 16, S, blocks, s, err);
     }
-    const size_t xp_bytes = (size_t)K * (size_t)Cp * (size_t)xbytes;
-    const size_t ws_bytes = xp_bytes + ((size_t)ng * (size_t)Cp + 64) * 4;
-    if ((rc = ensure_ws(x, ws_bytes, false, err)) != UNP_OK) return rc;
-    uint64_t xp = (uint64_t)x->ws, xs = xp + xp_bytes;
-    long long Kp = K, Cc = C, Cpp = Cp, G = group, n_out = S > 1 ? R * C : 0;
-    void* pparams[] = {&xa, &xp, &xs, &Kp, &Cc, &Cpp, &G, &out, &n_out};
-    if ((rc = launch(x, prep16, (uint32_t)(ng * (Cp / 16)), pparams, s, err)) != UNP_OK) return rc;
-    void* mparams[] = {&w, &zp, &sc, &xp, &xs, &out, &R, &K, &C, &Cpp, &S};
-    return launch(x, dec, (uint32_t)blocks, mparams, s, err);
   }
-  if (stream != SIZE_MAX && prep != SIZE_MAX && K > 0 && K % group == 0 && (w & 15) == 0 && (zp & 3) == 0 &&
-      (sc & 3) == 0 && (out & 3) == 0 && (xa & (x32 ? 3 : 0)) == 0) {
-    // Streaming: repack x, then the LDS-staged MFMA kernel over (row tile, split) x column tiles.
+  if (stream != SIZE_MAX && prep != SIZE_MAX && whole) {
+    // Streaming: the LDS-staged MFMA kernel over (row tile, split) x column tiles.
     const long long bm = x->l.entries[stream].vec, bn = x->l.entries[stream].k;
     const long long ng = K / group, Cp = (C + 63) / 64 * 64;
     const long long tiles_r = (R + bm - 1) / bm, tiles_c = (C + bn - 1) / bn;
     // Splits of K: enough blocks for two per CU, at least four groups per split.
-    const long long target = 2LL * x->cu_count;
-    long long S = (target + tiles_r * tiles_c - 1) / (tiles_r * tiles_c);
+    long long S = (2LL * x->cu_count + tiles_r * tiles_c - 1) / (tiles_r * tiles_c);
     S = std::max(1LL, std::min(S, ng / 4));
-    const long long units = tiles_r * S;
-    const long long blocks = (units + 7) / 8 * 8 * tiles_c;
-    if (blocks > 0x7FFFFFFFLL || ng * (Cp / 64) > 0x7FFFFFFFLL) {
-      set_error(err, UNP_INVALID_ARGUMENT, "dequant GEMM shape too large for one launch");
-      return UNP_INVALID_ARGUMENT;
-    }
-    const size_t xp_bytes = (size_t)K * (size_t)Cp * (x32 ? 4 : 1);
-    const size_t ws_bytes = xp_bytes + ((size_t)ng * (size_t)Cp + 64) * 4;
-    if ((rc = ensure_ws(x, ws_bytes, false, err)) != UNP_OK) return rc;
-    uint64_t xp = (uint64_t)x->ws, xs = xp + xp_bytes;
-    long long Kp = K, Cc = C, Cpp = Cp, G = group, n_out = S > 1 ? R * C : 0;
-    void* pparams[] = {&xa, &xp, &xs, &Kp, &Cc, &Cpp, &G, &out, &n_out};
-    if ((rc = launch(x, prep, (uint32_t)(ng * (Cp / 64)), pparams, s, err)) != UNP_OK) return rc;
-    void* mparams[] = {&w, &zp, &sc, &xp, &xs, &out, &R, &K, &C, &Cpp, &S};
-    return launch(x, stream, (uint32_t)blocks, mparams, s, err);
+    const long long blocks = (tiles_r * S + 7) / 8 * 8 * tiles_c;
+    return run_repacked(x, prep, stream, w, zp, sc, xa, out, R, K, C, Cp, 64, S, blocks, s, err);
   }
-  const uint64_t xalign = x32 ? 16 : 4;
+  // One launch: the LDS-transpose MFMA entry when its operands line up, else the serial entry.
   const long long tiles = ((R + 63) / 64) * ((C + 63) / 64);
-  const bool fast_ok = K % group == 0 && C % 4 == 0 && xa % xalign == 0 && (w & 7) == 0 && (zp & 3) == 0 &&
-                       (sc & 3) == 0 && (out & 3) == 0 && tiles <= 0x7FFFFFFFLL;
-  size_t entry = SIZE_MAX;
-  for (size_t i = 0; i < x->l.entries.size(); ++i) {
-    const std::string& sym = x->l.entries[i].symbol;
-    const bool is_mfma = sym.size() > 5 && sym.compare(sym.size() - 5, 5, "_mfma") == 0;
-    const bool is_any = sym.size() > 4 && sym.compare(sym.size() - 4, 4, "_any") == 0;
-    if ((is_mfma && fast_ok && entry == SIZE_MAX) || (is_any && (entry == SIZE_MAX || !fast_ok))) entry = i;
-  }
-  const bool mfma = x->l.entries[entry].fast;
-  const uint32_t grid = mfma ? (uint32_t)tiles : (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+  const bool mfma_ok = mfma != SIZE_MAX && K % group == 0 && C % 4 == 0 && xa % (x32 ? 16 : 4) == 0 &&
+                       (w & 7) == 0 && (zp & 3) == 0 && (sc & 3) == 0 && (out & 3) == 0 && tiles <= 0x7FFFFFFFLL;
+  const size_t entry = mfma_ok ? mfma : any;
+  const uint32_t grid = mfma_ok ? (uint32_t)tiles : (uint32_t)(x->cu_count * x->l.blocks_per_cu);
   void* params[] = {&w, &zp, &sc, &xa, &out, &R, &K, &C};
   return launch(x, entry, grid, params, s, err);
 }
