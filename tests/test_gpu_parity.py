@@ -457,7 +457,9 @@ GEMM_MFMA_CASES = [
     (1100, 2048, 16, 128, np.int8),   # row tiles not a multiple of the eight XCDs
     (200, 4096, 60, 128, np.int8),    # four column tiles per block
     (96, 2048, 100, 256, np.int32),   # I32 decode past 64 columns
-    (200, 4096, 100, 128, np.int8),   # I8 past 64 columns: streaming, two column tiles per wave
+    (200, 4096, 100, 128, np.int8),   # I8 past 64 columns: streaming, 2 x 2 tiles per wave
+    (300, 8192, 300, 256, np.int8),   # three 128-column tiles, the last partly padding
+    (130, 4096, 150, 64, np.int8),    # 64-value chunks: four waves of one tile over 128 x 32
     (96, 2048, 128, 256, np.int8),
 ]
 

@@ -1728,7 +1728,8 @@ UNP_DEV void dqgemm_mfma(const u8* __restrict__ w, const i32* __restrict__ zero,
 // It also zeroes out when the main kernel accumulates split-K parts with atomics.
 //
 // The main kernel: a block owns BM = 32 WR TM rows x BN = 32 WC TN columns, TM x TN 32 x 32
-// MFMA tiles per wave (a tile row's unpacked w operand serves its TN column tiles), and a range
+// MFMA tiles per wave (a tile row's unpacked w operand serves its TN column tiles, a tile
+// column's x' operand its TM row tiles), and a range
 // of whole groups (split-K: parts add into out with u32 atomics, which are exact and order-free
 // in Z / 2^32).  It streams the chunks of its range through NS LDS stages with global->LDS DMA:
 // per chunk the w rows (each op RPO rows x SPR contiguous 16-byte segments, XOR-swizzled in

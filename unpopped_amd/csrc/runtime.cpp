@@ -818,7 +818,7 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
   // The two-launch schedules need whole groups, a 16-byte aligned w and aligned operands.
   const bool whole = K > 0 && K % group == 0 && (w & 15) == 0 && (zp & 3) == 0 && (sc & 3) == 0 &&
                      (out & 3) == 0 && (xa & (x32 ? 3 : 0)) == 0;
-  // Decode up to 64 columns for I8 activations (the streaming entry's 128 x 64 tiles win beyond),
+  // Decode up to 64 columns for I8 activations (the streaming entry's 128 x 128 tiles win beyond),
   // up to 128 for I32; its buffer loads take 32-bit offsets.
   if (dec != SIZE_MAX && prep16 != SIZE_MAX && whole && C <= (x32 ? 128 : 64)) {
     const long long bm = x->l.entries[dec].vec, bn = x->l.entries[dec].cols, maxg = x->l.entries[dec].k;
@@ -836,7 +836,8 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
   if (stream != SIZE_MAX && prep != SIZE_MAX && whole) {
     // Streaming: the LDS-staged MFMA kernel over (row tile, split) x column tiles.
     const long long bm = x->l.entries[stream].vec, bn = x->l.entries[stream].k;
-    const long long ng = K / group, Cp = (C + 63) / 64 * 64;
+    // Whole column tiles of the entry and whole 64-column prep slabs (bn is 32 or 128).
+    const long long cw = std::max(bn, 64LL), ng = K / group, Cp = (C + cw - 1) / cw * cw;
     const long long tiles_r = (R + bm - 1) / bm, tiles_c = (C + bn - 1) / bn;
     // Splits of K: enough blocks for two per CU, at least four groups per split.
     long long S = (2LL * x->cu_count + tiles_r * tiles_c - 1) / (tiles_r * tiles_c);
