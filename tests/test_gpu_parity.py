@@ -460,6 +460,7 @@ GEMM_MFMA_CASES = [
     (200, 4096, 100, 128, np.int8),   # I8 past 64 columns: streaming, 2 x 2 tiles per wave
     (300, 8192, 300, 256, np.int8),   # three 128-column tiles, the last partly padding
     (130, 4096, 150, 64, np.int8),    # 64-value chunks: four waves of one tile over 128 x 32
+    (257, 8192, 200, 128, np.int32),  # I32 streaming: 1 x 2 tiles per wave, split-K, ragged last tile
     (96, 2048, 128, 256, np.int8),
 ]
 

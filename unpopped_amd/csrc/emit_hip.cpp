@@ -609,11 +609,12 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
     if (f.group % c == 0) kc = c;
   // The streaming schedule: groups of whole 64-value chunks.  Stage chunk 128 (I8, when it
   // divides the group) or 64.  I8 with 128-value chunks: 2 x 2 waves, each with 2 x 2 tiles of
-  // 32 x 32 (128 x 128 per block), three stages, two blocks per CU; otherwise four waves
-  // stacked over 128 rows with one 32 x 32 tile each (128 x 32), four stages.
+  // 32 x 32 (128 x 128 per block); I32: four waves stacked over 128 rows with 1 x 2 tiles each
+  // (128 x 64); both with three stages and two blocks per CU.  I8 with 64-value chunks: four
+  // waves of one tile (128 x 32), four stages.
   const int skc = f.group % 64 != 0 ? 0 : (xb == 1 && f.group % 128 == 0 ? 128 : 64);
-  const bool big = xb == 1 && skc == 128;
-  const int swr = big ? 2 : 4, swc = big ? 2 : 1, stm = big ? 2 : 1, stn = big ? 2 : 1, sns = big ? 3 : 4;
+  const bool big = xb == 1 && skc == 128, two = big || xb == 4;
+  const int swr = big ? 2 : 4, swc = big ? 2 : 1, stm = big ? 2 : 1, stn = two ? 2 : 1, sns = two ? 3 : 4;
   // The decode schedule (up to 64 columns for I8, 128 for I32): groups of 1..4 whole 128-value steps (1..2 for I32
   // activations, whose four digit planes take four times the x registers).  I8: two m-tiles per
   // wave, 1, 2 or 4 column tiles of 16 sharing each unpacked w operand, two steps in flight (or
@@ -650,7 +651,7 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
     e.symbol = L.name + "_stream";
     e.vec = 32 * swr * stm;  // rows per block
     e.k = 32 * swc * stn;    // columns per block
-    src << "extern \"C\" __global__ void __launch_bounds__(256" << (big ? ", 2" : "") << ") " << e.symbol
+    src << "extern \"C\" __global__ void __launch_bounds__(256" << (two ? ", 2" : "") << ") " << e.symbol
         << "(const unsigned char* w, const int* zero, const int* scale, const unsigned char* xp, const unsigned* xsum, "
            "int* out, long long R, long long K, long long C, long long Cp, long long S) {\n  unp::dqg_stream<"
         << (qs ? "true" : "false") << ", " << xb << ", " << f.group << ", " << skc << ", " << swr << ", " << swc
@@ -711,7 +712,7 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
        "(row tiles rounded up to 8) x splits x column tiles blocks of 128 (I8) or 256 (I32) rows x 16, 32 or 64 "
        "columns, about two blocks per CU, a split's groups at most 32 "
        "and the splits adding into out with atomics; stream: a prep launch over (group, 64 columns), then "
-       "(row tiles x splits, rounded up to 8) x column tiles blocks of 128 x 128 (I8) or 128 x 32 outputs, the splits adding into out "
+       "(row tiles x splits, rounded up to 8) x column tiles blocks of 128 x 128 (I8, 128-value chunks), 128 x 64 (I32) or 128 x 32 outputs, the splits adding into out "
        "with atomics; mfma: one block per 64 x 64 output tile; any: threads stride over the outputs\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i) {
     const std::string& sym = L.entries[i].symbol;

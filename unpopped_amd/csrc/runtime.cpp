@@ -836,7 +836,7 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
   if (stream != SIZE_MAX && prep != SIZE_MAX && whole) {
     // Streaming: the LDS-staged MFMA kernel over (row tile, split) x column tiles.
     const long long bm = x->l.entries[stream].vec, bn = x->l.entries[stream].k;
-    // Whole column tiles of the entry and whole 64-column prep slabs (bn is 32 or 128).
+    // Whole column tiles of the entry and whole 64-column prep slabs (bn is 32, 64 or 128).
     const long long cw = std::max(bn, 64LL), ng = K / group, Cp = (C + cw - 1) / cw * cw;
     const long long tiles_r = (R + bm - 1) / bm, tiles_c = (C + bn - 1) / bn;
     // Splits of K: enough blocks for two per CU, at least four groups per split.
