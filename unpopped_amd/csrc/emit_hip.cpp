@@ -726,8 +726,9 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
                    "w and repacked x under 2 GiB; after the prep16 launch (buffer loads into VGPRs, "
                    "v_mfma_i32_16x16x64_i8)"
           : is_prep16 ? "before the dec entry: x repacked for 16-column tiles, group column sums, out zeroed"
-          : is_stream ? "K % group == 0, w 16-byte aligned; after the prep launch (LDS-staged DMA, "
-                      "v_mfma_i32_32x32x32_i8)"
+          : is_stream ? "K % group == 0, w 16-byte aligned, scales and column sums under 2 GiB; after the prep "
+                      "launch (LDS-staged DMA, v_mfma_i32_32x32x32_i8, the zero-point term on the MFMA in "
+                      "byte digits after the loop)"
                     : is_prep ? "before the stream entry: x repacked into digit planes and group column sums"
                               : L.entries[i].fast ? "K % group == 0, C % 4 == 0, x aligned to 4 elements, w to 8 "
                                                     "bytes (v_mfma_i32_32x32x32_i8)"

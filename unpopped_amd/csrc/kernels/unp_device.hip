@@ -1793,8 +1793,6 @@ template <int BM, int BN, int KC, int XB> struct dqg_stage {
   u8 a[BM * KC / 2];   // w: row r's 16-byte segment s at r * KC / 2 + 16 * (s ^ swz(r))
   u8 b[XB * KC * BN];  // x': plane p, segment ks, column c at ((p * KC / 16 + ks) * BN + c) * 16
   u32 s[BM];           // the rows' scales
-  u32 z[BM];           // the rows' zero points
-  u32 x[BN < 64 ? 64 : BN];  // the group's column sums (whole 64-lane DMA ops)
 };
 
 template <bool QS, int XB, int G, int KC, int WR, int WC, int TM, int TN, int NS>
@@ -1809,10 +1807,10 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
   // row is XOR-swizzled by (row / FD) % SPR so that eight consecutive rows' reads of one
   // segment fall in eight distinct LDS bank groups.
   constexpr int SPR = KC / 32, RPO = 64 / SPR, FD = 16 / SPR;
-  constexpr int NA = BM * KC / 2 / 1024, NB = XB * KC * BN / 1024, NSZ = BM / 64, NX = (BN + 63) / 64;
+  constexpr int NA = BM * KC / 2 / 1024, NB = XB * KC * BN / 1024, NSZ = BM / 64;
   static_assert(NA * 1024 == BM * KC / 2 && NB * 1024 == XB * KC * BN && NSZ * 64 == BM, "whole 64-lane ops");
-  constexpr int OA = (NA + NW - 1) / NW, OB = (NB + NW - 1) / NW, OS = (2 * NSZ + NW - 1) / NW, OX = (NX + NW - 1) / NW;
-  constexpr int OPW = OA + OB + OS + OX;  // DMA ops per wave per stage
+  constexpr int OA = (NA + NW - 1) / NW, OB = (NB + NW - 1) / NW, OS = (NSZ + NW - 1) / NW;
+  constexpr int OPW = OA + OB + OS;  // DMA ops per wave per stage
   static_assert((NS - 2) * OPW < 64, "the wait count fits vmcnt");
   __shared__ __attribute__((aligned(16))) St st0;
   __shared__ __attribute__((aligned(16))) St st1;
@@ -1837,9 +1835,9 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
   const i64 c0 = g0 * cpg, n = (g1 - g0) * cpg;  // this block's chunks
   const i64 wbytes_row = K / 2;
 
-  // A stage's DMA: every wave issues the same sequence, OA ops of w rows, OB of x' columns, OS
-  // of scales or zero points (16-byte ops move 1 KiB, 4-byte ops 256 B) and OX of the column
-  // sums, so every wave waits on the same count with no branch.  Where a kind has fewer ops
+  // A stage's DMA: every wave issues the same sequence, OA ops of w rows, OB of x' columns and
+  // OS of scales (16-byte ops move 1 KiB, 4-byte ops 256 B), so every wave waits on the same
+  // count with no branch.  Where a kind has fewer ops
   // than waves the extra ones repeat an op of that kind: both DMAs write the same bytes.
   auto issue_stage = [&](St* stp, i64 i) {
     const i64 chunk = c0 + (i < n ? i : n - 1);
@@ -1860,16 +1858,10 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
     }
 #pragma unroll
     for (int m = 0; m < OS; ++m) {
-      const int o = (wave + NW * m) % (2 * NSZ), which = o / NSZ, part = o % NSZ;
-      const i64 r = tile_r + part * 64 + lane;
+      const int o = (wave + NW * m) % NSZ;
+      const i64 r = tile_r + o * 64 + lane;
       const i64 row = r < R ? r : R - 1;
-      __builtin_amdgcn_global_load_lds((which == 0 ? scale : zero) + row * ng + g,
-                                       (lds_void*)((which == 0 ? stp->s : stp->z) + part * 64), 4, 0, 0);
-    }
-#pragma unroll
-    for (int m = 0; m < OX; ++m) {
-      const int o = (wave + NW * m) % NX;
-      __builtin_amdgcn_global_load_lds(xsum + g * Cp + tile_c + 64 * o + lane, (lds_void*)(stp->x + 64 * o), 4, 0, 0);
+      __builtin_amdgcn_global_load_lds(scale + row * ng + g, (lds_void*)(stp->s + o * 64), 4, 0, 0);
     }
   };
 
@@ -1916,28 +1908,23 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
     }
     if (cpg == 1 || (i + 1) % cpg == 0) {
       // The group ends: lane element v is row 8 (v / 4) + 4 q + v % 4 of its 32 x 32 tile.
+      // The zero-point term is left to the pass after the loop.
 #pragma unroll
       for (int a = 0; a < TM; ++a)
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
           const int lr = 32 * (wr * TM + a) + 8 * i4 + 4 * q;
           const vec<u32, 4> s4 = *reinterpret_cast<const vec<u32, 4>*>(stp->s + lr);
-          const vec<u32, 4> z4 = *reinterpret_cast<const vec<u32, 4>*>(stp->z + lr);
-          u32 zs[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) zs[e] = z4.e[e] * s4.e[e];
-#pragma unroll
-          for (int t = 0; t < TN; ++t) {
-            const u32 xc = stp->x[32 * (wc * TN + t) + l32];
+          for (int t = 0; t < TN; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int v = 4 * i4 + e;
               u32 p = (u32)P[a][t][0][v];
 #pragma unroll
               for (int b = 1; b < XB; ++b) p += (u32)P[a][t][b][v] << (8 * b);
-              total[a][t][v] += s4.e[e] * p - zs[e] * xc;
+              total[a][t][v] += s4.e[e] * p;
             }
-          }
         }
     }
   };
@@ -1957,6 +1944,89 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
       if (i < n) compute(stages[I], i);
     }
   }
+
+  // The zero-point term, minus the sum over the block's groups of (scale zero)[r, g] xsum[g, c],
+  // on the MFMA with 32 groups per instruction: lane (l32, q) holds groups 16 q .. 16 q + 15 of
+  // its row (A) or column (B).  Both factors are split into signed byte digits: the bytes of
+  // (v + 0x80808080) ^ 0x80808080 are digits d_i in [-128, 127] with sum d_i 256^i = v modulo
+  // 2^32.  The digit pairs i + j = sh add into one accumulator (at most 4 x 32 products of
+  // 2^14, exact), which then enters the total shifted left by 8 sh bits.
+  // The loads go through buffer resources with 32-bit offsets (byte counts under 2^31, which
+  // the launcher checks); rows past R lie past the end and read 0.  A step's products
+  // scale * zero for the block's BM rows x 32 groups are loaded coalesced (a wave instruction
+  // covers two rows' 32 groups) into LDS rows of 36 words, groups past the block's last zeroed,
+  // then each lane reads its row's 16 groups.  The LDS is stage memory, free once every DMA
+  // has landed and every wave has left the loop.
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scale, (short)0, (int)(u32)(R * ng * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)zero, (short)0, (int)(u32)(R * ng * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc((void*)xsum, (short)0, (int)(u32)(ng * Cp * 4), 0x00020000);
+  constexpr int SZW = 36, SZN = BM * 32 / (64 * NW);  // LDS row words; loads per thread per step
+  constexpr bool SZ_IN_STAGE = sizeof(St) >= sizeof(u32) * BM * SZW;
+  __shared__ __attribute__((aligned(16))) u32 szx[SZ_IN_STAGE ? 4 : BM * SZW];
+  u32* const szs = SZ_IN_STAGE ? reinterpret_cast<u32*>(&st0) : szx;
+  wait_vm<0>();
+  __syncthreads();
+  const int srow = tid / 32, sg = tid % 32;
+  const int sofs = (int)(((tile_r + srow) * ng + sg) * 4);  // rows past R read 0 (past the end)
+#pragma unroll 1
+  for (i64 gc = g0; gc < g1; gc += 32) {
+    const int gl = (int)(g1 - gc < 32 ? g1 - gc : 32);  // groups of this step in range
+    const u32 gmask = 0u - (u32)(sg < gl);
+#pragma unroll
+    for (int m = 0; m < SZN; ++m) {
+      const int so = (int)((gc + (i64)m * (64 * NW / 32) * ng) * 4);
+      const u32 v = (u32)__builtin_amdgcn_raw_buffer_load_b32(rs, sofs, so, 0) *
+                    (u32)__builtin_amdgcn_raw_buffer_load_b32(rz, sofs, so, 0);
+      szs[(m * (64 * NW / 32) + srow) * SZW + sg] = v & gmask;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+      const int lr = 32 * (wr * TM + a) + l32;
+      i32x4 ad[4];
+#pragma unroll
+      for (int wd = 0; wd < 4; ++wd) {
+        const vec<u32, 4> v4 = *reinterpret_cast<const vec<u32, 4>*>(szs + lr * SZW + 16 * q + 4 * wd);
+        u32 vb[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vb[e] = (v4.e[e] + 0x80808080u) ^ 0x80808080u;
+#pragma unroll
+        for (int pl = 0; pl < 4; ++pl)
+          ad[pl][wd] = (i32)(((vb[0] >> (8 * pl)) & 0xffu) | (((vb[1] >> (8 * pl)) & 0xffu) << 8) |
+                             (((vb[2] >> (8 * pl)) & 0xffu) << 16) | ((vb[3] >> (8 * pl)) << 24));
+      }
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        // Column below Cp (whole column tiles); group gc + 16 q + k' at (16 q Cp + c) 4 + (gc + k') Cp 4.
+        const int cofs = (int)((16 * q * Cp + tile_c + 32 * (wc * TN + t) + l32) * 4);
+        i32x4 bd[4];
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+          u32 vb[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int k = 16 * q + 4 * wd + e, so = (int)((gc + 4 * wd + e) * Cp * 4);
+            const u32 v = (u32)__builtin_amdgcn_raw_buffer_load_b32(rc, cofs, so, 0);
+            vb[e] = ((v & (0u - (u32)(k < gl))) + 0x80808080u) ^ 0x80808080u;
+          }
+#pragma unroll
+          for (int pl = 0; pl < 4; ++pl)
+            bd[pl][wd] = (i32)(((vb[0] >> (8 * pl)) & 0xffu) | (((vb[1] >> (8 * pl)) & 0xffu) << 8) |
+                               (((vb[2] >> (8 * pl)) & 0xffu) << 16) | ((vb[3] >> (8 * pl)) << 24));
+        }
+#pragma unroll
+        for (int sh = 0; sh < 4; ++sh) {
+          i32x16 acc = Z;
+#pragma unroll
+          for (int i = 0; i <= sh; ++i) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ad[i], bd[sh - i], acc, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) total[a][t][v] -= (u32)acc[v] << (8 * sh);
+        }
+      }
+    }
+    __syncthreads();  // every wave has read the step's products before the next step's writes
+  }
+
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
     const i64 c = tile_c + 32 * (wc * TN + t) + l32;

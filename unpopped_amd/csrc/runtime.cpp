@@ -838,12 +838,16 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
     const long long bm = x->l.entries[stream].vec, bn = x->l.entries[stream].k;
     // Whole column tiles of the entry and whole 64-column prep slabs (bn is 32, 64 or 128).
     const long long cw = std::max(bn, 64LL), ng = K / group, Cp = (C + cw - 1) / cw * cw;
-    const long long tiles_r = (R + bm - 1) / bm, tiles_c = (C + bn - 1) / bn;
-    // Splits of K: enough blocks for two per CU, at least four groups per split.
-    long long S = (2LL * x->cu_count + tiles_r * tiles_c - 1) / (tiles_r * tiles_c);
-    S = std::max(1LL, std::min(S, ng / 4));
-    const long long blocks = (tiles_r * S + 7) / 8 * 8 * tiles_c;
-    return run_repacked(x, prep, stream, w, zp, sc, xa, out, R, K, C, Cp, 64, S, blocks, s, err);
+    // Its zero-point pass reads scales, zero points and column sums by 32-bit byte offsets,
+    // up to a row tile and a 32-group step past their ends.
+    if ((R + 256) * ng * 4 < 0x7FFFFFFFLL && (ng + 32) * Cp * 4 < 0x7FFFFFFFLL) {
+      const long long tiles_r = (R + bm - 1) / bm, tiles_c = (C + bn - 1) / bn;
+      // Splits of K: enough blocks for two per CU, at least four groups per split.
+      long long S = (2LL * x->cu_count + tiles_r * tiles_c - 1) / (tiles_r * tiles_c);
+      S = std::max(1LL, std::min(S, ng / 4));
+      const long long blocks = (tiles_r * S + 7) / 8 * 8 * tiles_c;
+      return run_repacked(x, prep, stream, w, zp, sc, xa, out, R, K, C, Cp, 64, S, blocks, s, err);
+    }
   }
   // One launch: the LDS-transpose MFMA entry when its operands line up, else the serial entry.
   const long long tiles = ((R + 63) / 64) * ((C + 63) / 64);
