@@ -1961,25 +1961,37 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
   const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)zero, (short)0, (int)(u32)(R * ng * 4), 0x00020000);
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc((void*)xsum, (short)0, (int)(u32)(ng * Cp * 4), 0x00020000);
   constexpr int SZW = 36, SZN = BM * 32 / (64 * NW);  // LDS row words; loads per thread per step
+  // Two step buffers: the loads of the next step are issued before the current step's MFMAs.
   constexpr bool SZ_IN_STAGE = sizeof(St) >= sizeof(u32) * BM * SZW;
-  __shared__ __attribute__((aligned(16))) u32 szx[SZ_IN_STAGE ? 4 : BM * SZW];
-  u32* const szs = SZ_IN_STAGE ? reinterpret_cast<u32*>(&st0) : szx;
+  __shared__ __attribute__((aligned(16))) u32 szx[SZ_IN_STAGE ? 4 : 2 * BM * SZW];
+  u32* const szb0 = SZ_IN_STAGE ? reinterpret_cast<u32*>(&st0) : szx;
+  u32* const szb1 = SZ_IN_STAGE ? reinterpret_cast<u32*>(&st1) : szx + BM * SZW;
   wait_vm<0>();
   __syncthreads();
   const int srow = tid / 32, sg = tid % 32;
   const int sofs = (int)(((tile_r + srow) * ng + sg) * 4);  // rows past R read 0 (past the end)
-#pragma unroll 1
-  for (i64 gc = g0; gc < g1; gc += 32) {
-    const int gl = (int)(g1 - gc < 32 ? g1 - gc : 32);  // groups of this step in range
-    const u32 gmask = 0u - (u32)(sg < gl);
+  u32 sv[SZN], zv[SZN];
+  auto load_step = [&](i64 gs) {
 #pragma unroll
     for (int m = 0; m < SZN; ++m) {
-      const int so = (int)((gc + (i64)m * (64 * NW / 32) * ng) * 4);
-      const u32 v = (u32)__builtin_amdgcn_raw_buffer_load_b32(rs, sofs, so, 0) *
-                    (u32)__builtin_amdgcn_raw_buffer_load_b32(rz, sofs, so, 0);
-      szs[(m * (64 * NW / 32) + srow) * SZW + sg] = v & gmask;
+      const int so = (int)((gs + (i64)m * (64 * NW / 32) * ng) * 4);
+      sv[m] = (u32)__builtin_amdgcn_raw_buffer_load_b32(rs, sofs, so, 0);
+      zv[m] = (u32)__builtin_amdgcn_raw_buffer_load_b32(rz, sofs, so, 0);
     }
+  };
+  if (g0 < g1) load_step(g0);
+  int buf = 0;
+#pragma unroll 1
+  for (i64 gc = g0; gc < g1; gc += 32, buf ^= 1) {
+    const int gl = (int)(g1 - gc < 32 ? g1 - gc : 32);  // groups of this step in range
+    const u32 gmask = 0u - (u32)(sg < gl);
+    u32* const szs = buf ? szb1 : szb0;
+#pragma unroll
+    for (int m = 0; m < SZN; ++m) szs[(m * (64 * NW / 32) + srow) * SZW + sg] = (sv[m] * zv[m]) & gmask;
+    // The other buffer was last read before the previous step's barrier; this one is whole
+    // after this barrier.
     __syncthreads();
+    if (gc + 32 < g1) load_step(gc + 32);
 #pragma unroll
     for (int a = 0; a < TM; ++a) {
       const int lr = 32 * (wr * TM + a) + l32;
@@ -2024,7 +2036,6 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
         }
       }
     }
-    __syncthreads();  // every wave has read the step's products before the next step's writes
   }
 
 #pragma unroll
