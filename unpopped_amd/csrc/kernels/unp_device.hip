@@ -1970,7 +1970,12 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
   __syncthreads();
   const int srow = tid / 32, sg = tid % 32;
   const int sofs = (int)(((tile_r + srow) * ng + sg) * 4);  // rows past R read 0 (past the end)
-  u32 sv[SZN], zv[SZN];
+  // Column sums: lane (l32, q) of column tile t reads groups 16 q .. 16 q + 15 of its column
+  // (below Cp: whole column tiles) at (16 q Cp + c) 4 + (gs + k) Cp 4.
+  int cofs[TN];
+#pragma unroll
+  for (int t = 0; t < TN; ++t) cofs[t] = (int)((16 * q * Cp + tile_c + 32 * (wc * TN + t) + l32) * 4);
+  u32 sv[SZN], zv[SZN], xv[TN][16];
   auto load_step = [&](i64 gs) {
 #pragma unroll
     for (int m = 0; m < SZN; ++m) {
@@ -1978,6 +1983,10 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
       sv[m] = (u32)__builtin_amdgcn_raw_buffer_load_b32(rs, sofs, so, 0);
       zv[m] = (u32)__builtin_amdgcn_raw_buffer_load_b32(rz, sofs, so, 0);
     }
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int k = 0; k < 16; ++k) xv[t][k] = (u32)__builtin_amdgcn_raw_buffer_load_b32(rc, cofs[t], (int)((gs + k) * Cp * 4), 0);
   };
   if (g0 < g1) load_step(g0);
   int buf = 0;
@@ -1991,6 +2000,21 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
     // The other buffer was last read before the previous step's barrier; this one is whole
     // after this barrier.
     __syncthreads();
+    // This step's column-sum digits, before the next step's loads take over xv.
+    i32x4 bd[TN][4];
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int wd = 0; wd < 4; ++wd) {
+        u32 vb[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          vb[e] = ((xv[t][4 * wd + e] & (0u - (u32)(16 * q + 4 * wd + e < gl))) + 0x80808080u) ^ 0x80808080u;
+#pragma unroll
+        for (int pl = 0; pl < 4; ++pl)
+          bd[t][pl][wd] = (i32)(((vb[0] >> (8 * pl)) & 0xffu) | (((vb[1] >> (8 * pl)) & 0xffu) << 8) |
+                                (((vb[2] >> (8 * pl)) & 0xffu) << 16) | ((vb[3] >> (8 * pl)) << 24));
+      }
     if (gc + 32 < g1) load_step(gc + 32);
 #pragma unroll
     for (int a = 0; a < TM; ++a) {
@@ -2009,28 +2033,11 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
       }
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
-        // Column below Cp (whole column tiles); group gc + 16 q + k' at (16 q Cp + c) 4 + (gc + k') Cp 4.
-        const int cofs = (int)((16 * q * Cp + tile_c + 32 * (wc * TN + t) + l32) * 4);
-        i32x4 bd[4];
-#pragma unroll
-        for (int wd = 0; wd < 4; ++wd) {
-          u32 vb[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int k = 16 * q + 4 * wd + e, so = (int)((gc + 4 * wd + e) * Cp * 4);
-            const u32 v = (u32)__builtin_amdgcn_raw_buffer_load_b32(rc, cofs, so, 0);
-            vb[e] = ((v & (0u - (u32)(k < gl))) + 0x80808080u) ^ 0x80808080u;
-          }
-#pragma unroll
-          for (int pl = 0; pl < 4; ++pl)
-            bd[pl][wd] = (i32)(((vb[0] >> (8 * pl)) & 0xffu) | (((vb[1] >> (8 * pl)) & 0xffu) << 8) |
-                               (((vb[2] >> (8 * pl)) & 0xffu) << 16) | ((vb[3] >> (8 * pl)) << 24));
-        }
 #pragma unroll
         for (int sh = 0; sh < 4; ++sh) {
           i32x16 acc = Z;
 #pragma unroll
-          for (int i = 0; i <= sh; ++i) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ad[i], bd[sh - i], acc, 0, 0, 0);
+          for (int i = 0; i <= sh; ++i) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ad[i], bd[t][sh - i], acc, 0, 0, 0);
 #pragma unroll
           for (int v = 0; v < 16; ++v) total[a][t][v] -= (u32)acc[v] << (8 * sh);
         }
