@@ -1951,8 +1951,10 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
   // (v + 0x80808080) ^ 0x80808080 are digits d_i in [-128, 127] with sum d_i 256^i = v modulo
   // 2^32.  The digit pairs i + j = sh add into one accumulator (at most 4 x 32 products of
   // 2^14, exact), which then enters the total shifted left by 8 sh bits.
-  // The loads go through buffer resources with 32-bit offsets (byte counts under 2^31, which
-  // the launcher checks); rows past R lie past the end and read 0.  A step's products
+  // The loads go through buffer resources with the whole 32-bit byte offset in the range-checked
+  // vector offset (the scalar offset is not range-checked, so it stays 0); the launcher checks that
+  // every offset, a row tile and a 32-group step past the ends included, stays under 2^31.  Rows
+  // past R and groups past ng lie past num_records and read 0.  A step's products
   // scale * zero for the block's BM rows x 32 groups are loaded coalesced (a wave instruction
   // covers two rows' 32 groups) into LDS rows of 36 words, groups past the block's last zeroed,
   // then each lane reads its row's 16 groups.  The LDS is stage memory, free once every DMA
@@ -1980,13 +1982,13 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
 #pragma unroll
     for (int m = 0; m < SZN; ++m) {
       const int so = (int)((gs + (i64)m * (64 * NW / 32) * ng) * 4);
-      sv[m] = (u32)__builtin_amdgcn_raw_buffer_load_b32(rs, sofs, so, 0);
-      zv[m] = (u32)__builtin_amdgcn_raw_buffer_load_b32(rz, sofs, so, 0);
+      sv[m] = (u32)__builtin_amdgcn_raw_buffer_load_b32(rs, sofs + so, 0, 0);
+      zv[m] = (u32)__builtin_amdgcn_raw_buffer_load_b32(rz, sofs + so, 0, 0);
     }
 #pragma unroll
     for (int t = 0; t < TN; ++t)
 #pragma unroll
-      for (int k = 0; k < 16; ++k) xv[t][k] = (u32)__builtin_amdgcn_raw_buffer_load_b32(rc, cofs[t], (int)((gs + k) * Cp * 4), 0);
+      for (int k = 0; k < 16; ++k) xv[t][k] = (u32)__builtin_amdgcn_raw_buffer_load_b32(rc, cofs[t] + (int)((gs + k) * Cp * 4), 0, 0);
   };
   if (g0 < g1) load_step(g0);
   int buf = 0;
