@@ -10,9 +10,9 @@ One step is one pass of the suite over the seeded synthetic inputs, each kernel 
   cfg5   U4 8192 x 28672 dequant, f16 scales and U4 zeros per 128 columns, bf16 out (seed 4)
 Inputs are resident in HBM before the timed region.  Each kernel's time is the average over the
 timed steps of the HIP-event interval around its launch on the launch stream; `value` is the
-suite's algorithmic bytes over the suite's kernel time.  The CPU baseline is the oracle (the
-C restatement of the reference's serial algorithms, one thread) on a bounded sample of each
-configuration.
+suite's algorithmic bytes over the suite's kernel time.  The CPU baseline is the reference's
+cpu-c C99 leg (restated in oracle/cpuc.*) for the same lifted kernels, one pinned core, on bounded
+samples; it also runs config 1 (the CPU-only configuration) in full.
 """
 from __future__ import annotations
 
@@ -219,53 +219,92 @@ def cpu_model() -> str:
     return "unknown CPU"
 
 
-def cpu_baseline(synth, budget_s: float = 20.0) -> dict:
-    """The oracle (single-threaded C, -O2 -ffp-contract=off) on a bounded sample of each
-    configuration, pinned to one host core: the median of up to 5 runs after a warm-up."""
-    import oracle
+def cpu_baseline(synth, budget_s: float = 30.0) -> dict:
+    """The unpopped-cpu-c C99 leg, restated (oracle/cpuc.*: the reference emitter's serialized thread
+    loop, bounds-checked, compiled with its flags -O2 -ffp-contract=off), run on the same launched
+    KernelFns the GPU lowers (the caller's (256, 64) lifts), pinned to one host core: the median of
+    up to 5 runs after a warm-up.  cfg2 runs in full; the scans, the gather and the dequant on bounded
+    samples.  cfg1, the CPU-only configuration, runs in full through the serial and the launched lift
+    and is checked against RN32 of its exact sum; it is reported apart from the aggregate."""
+    import unpopped_amd as u
+    from oracle import cpuc
+    from oracle.cpuc import View
+    from unpopped_amd import forms as H
 
     legs = []
 
-    def timed(fn, nbytes, what):
-        fn()  # warm-up
+    def timed(name, k, args, nbytes, what):
+        ck = cpuc.kernel(k)
+        ck.time(*args, reps=0, warmup=1)
         runs, t0 = [], time.perf_counter()
-        while len(runs) < 5 and time.perf_counter() - t0 < budget_s / 5:
-            t1 = time.perf_counter()
-            fn()
-            runs.append(time.perf_counter() - t1)
-        legs.append({"sample": what, "bytes": nbytes, "s": float(np.median(runs))})
+        while len(runs) < 5 and time.perf_counter() - t0 < budget_s / 6:
+            ts, rc = ck.time(*args, reps=1, warmup=0)
+            if rc != cpuc.OK:
+                raise RuntimeError(f"the C99 of {name} returned status {rc}")
+            runs.append(ts[0])
+        s = float(np.median(runs))
+        legs.append({"name": name, "sample": what, "bytes": nbytes, "s": s, "runs": len(runs),
+                     "GBps": round(nbytes / s / 1e9, 4)})
+        log(f"[bench] cpu-c {name}: {what}: {s * 1e3:.1f} ms, {nbytes / s / 1e9:.3f} GB/s")
 
     saved = os.sched_getaffinity(0)
-    os.sched_setaffinity(0, {min(saved)})
+    core = min(saved)
+    os.sched_setaffinity(0, {core})
     try:
-        x2 = synth.normal_f32(1, 1024 * 4096).reshape(1024, 4096)
-        timed(lambda: (oracle.reduce_rows(x2, "Sum"), oracle.reduce_rows(x2, "Max")), x2.nbytes + 2 * 1024 * 4,
-              "cfg2 1024 of 8192 rows")
-        x3 = synth.int16_i32(2, 1 << 24).reshape(1, -1)
-        timed(lambda: oracle.scan_rows(x3, "Sum"), 2 * x3.nbytes, "cfg3a 2^24 of 2^28")
-        x3b = synth.uniform_01_f32(2, 1 << 24).reshape(1, -1)
-        timed(lambda: oracle.scan_rows(x3b, "Sum"), 2 * x3b.nbytes, "cfg3b 2^24 of 2^26")
+        R, Cc = 8192, 4096
+        x2 = synth.normal_f32(1, R * Cc).reshape(R, Cc)
+        timed("cfg2", H.kernel_for(kind="row_reduce2", dtype="F32", rank=2),
+              (x2, np.zeros(R, np.float32), np.zeros(R, np.float32), R, Cc), x2.nbytes + 2 * R * 4, "full 8192x4096")
+        del x2
+        n = 1 << 24
+        x3 = synth.int16_i32(2, n)
+        timed("cfg3a", H.kernel_for(kind="scan", dtype="I32"), (x3, np.empty(n, np.int32), n), 8 * n, "2^24 of 2^28")
+        x3b = synth.uniform_01_f32(2, n)
+        timed("cfg3b", H.kernel_for(kind="scan", dtype="F32"), (x3b, np.empty(n, np.float32), n), 8 * n,
+              "2^24 of 2^26")
+        del x3, x3b
         V, D, N = 16384, 4096, 4096
         t = synth.normal_bf16_bits(3, V * D, 0.02).reshape(V, D)
         ids = synth.uniform_ids_i32(3, N, V)
-        timed(lambda: oracle.gather_rows(t, ids, "ZeroFill"), 2 * N * D * 2 + N * 4,
-              "cfg4 4096 rows from a 16384-row table")
+        timed("cfg4", H.kernel_for(kind="gather", dtype="Bf16", rank=2),
+              (t, View(ids, (N, D), (1, 0)), np.empty((N, D), np.uint16), N, D, V), 2 * N * D * 2 + N * 4,
+              "4096 uniform ids into a 16384-row table")
+        del t
         R, Cc, G = 256, 28672, 128
         q, z = synth.nibbles(4, R * Cc), synth.nibbles(41, R * (Cc // G))
-        s = synth.uniform_f16_bits(42, R * (Cc // G), 0.001, 0.02)
-        timed(lambda: oracle.dequant4_bf16(q, s, z, R, Cc, G), R * Cc // 2 + R * 224 * 3 + R * Cc * 2,
-              "cfg5 256 of 8192 rows")
+        sc = synth.uniform_f16_bits(42, R * (Cc // G), 0.001, 0.02)
+        timed("cfg5", H.kernel_for(kind="dequant4"),
+              (View(q, (R * Cc,), (1,)), sc, View(z, (R * Cc // G,), (1,)), np.empty(R * Cc, np.uint16), R, Cc),
+              R * Cc // 2 + R * (Cc // G) * 3 + R * Cc * 2, "256 of 8192 rows")
+        # cfg1: the CPU configuration in full, lift -> C99 -> checked against RN32(exact sum).
+        n1 = 1 << 24
+        x1 = synth.uniform_pm1_f32(0, n1)
+        exact = np.float32(float(int(np.round(x1.astype(np.float64) * 2.0**24).astype(np.int64).sum())) * 2.0**-24)
+        cfg1 = {}
+        for tag, launch in (("serial", None), ("launched_256x64", (256, 64))):
+            k = u.lift_reduction("cfg1", "F32", 1, "Sum", launch=launch)
+            out = np.zeros(1, np.float32)
+            ck = cpuc.kernel(k)
+            ts, rc = ck.time(x1, View(out.reshape(()), (), ()), n1, reps=5, warmup=1)
+            s = float(np.median(ts))
+            cfg1[tag] = {"s": round(s, 6), "GBps": round(4 * n1 / s / 1e9, 4), "status": rc,
+                         "equals_rn32_exact": bool(out[0] == exact)}
+            log(f"[bench] cpu-c cfg1 {tag}: {s * 1e3:.1f} ms, sum {out[0]!r} (exact {exact!r})")
     finally:
         os.sched_setaffinity(0, saved)
     total_b = sum(l["bytes"] for l in legs)
     total_s = sum(l["s"] for l in legs)
     return {
-        "value": round(total_b / total_s / 1e9, 3),
+        "value": round(total_b / total_s / 1e9, 4),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"one core of {os.cpu_count()} ({cpu_model()}), median of up to 5 runs; "
-                  + "; ".join(f"{l['sample']}: {l['bytes'] / l['s'] / 1e9:.3f} GB/s" for l in legs),
+        "emitter": "unpopped-cpu-c C99 (restated: oracle/cpuc.cpp), cc -O2 -ffp-contract=off",
+        "host": f"core {core} of {os.cpu_count()} ({cpu_model()})",
+        "sample": "; ".join(f"{l['name']} {l['sample']}: {l['GBps']:.3f} GB/s" for l in legs)
+                  + "; median of up to 5 runs after a warm-up, the (256, 64) launched lifts",
+        "legs": legs,
+        "cfg1": cfg1,
     }
 
 
@@ -568,7 +607,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        log("[bench] CPU baseline (oracle, 1 thread)")
+        log("[bench] CPU baseline (the cpu-c C99 leg, 1 thread)")
         cpu = cpu_baseline(synth)
 
     line = {

@@ -36,3 +36,25 @@ def float_sum_bound_corpus(rows: int = 5, cols: int = 96) -> np.ndarray:
         v.append((lcg() - 0.5) * 2.0e5)
     a = np.array(v, dtype=np.float64).reshape(cols, rows)  # pushed column by column
     return np.ascontiguousarray(a.T)
+
+
+def dequant_gemm_fixture(signed: bool = True) -> dict:
+    """The dequant-GEMM fixture of crates/unpopped/tests/support/dequant.rs:145-181 (R=4, K=8, C=4,
+    GROUP=4): its data generators and its host answer, the fixture's own triple loop."""
+    R, K, C, GROUP = 4, 8, 4, 4
+    G = K // GROUP
+    nib = [(r * 5 + k * 3 + 1) % 16 for r in range(R) for k in range(K)]
+    packed = np.array([nib[i] | nib[i + 1] << 4 for i in range(0, len(nib), 2)], np.uint8)
+    zero = np.array([(i % 3) - 1 for i in range(R * G)], np.int32)
+    scale = np.array([1 + (i * 2 % 3) for i in range(R * G)], np.int32)
+    x = np.array([(i * 7 % 9) - 4 for i in range(K * C)], np.int32)
+    want = np.zeros((R, C), np.int64)
+    for r in range(R):
+        for c in range(C):
+            for k in range(K):
+                n = nib[r * K + k]
+                n = n - 16 if signed and n >= 8 else n
+                g = r * G + k // GROUP
+                want[r, c] += (n - int(zero[g])) * int(scale[g]) * int(x[k * C + c])
+    return {"rows": R, "k": K, "cols": C, "group": GROUP, "w_packed": packed, "zero": zero, "scale": scale,
+            "x": x, "expected": want.astype(np.int32)}
