@@ -294,6 +294,16 @@ typedef struct unp_view {
  * (backend.rs:703-707). */
 int32_t unp_hip_exec_launch_views(unp_exec* e, const unp_view* views, size_t nviews, const int64_t* scalars,
                                   size_t nscalars, void* stream, unp_error* err);
+/* No reference counterpart: it exists for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  unp_hip_exec_launch with every
+ * workspace the executor would allocate (scan tile status and ticket counter, reduction partials and
+ * counters, the dequant GEMM's repacked activations) taken from one static device array of
+ * UNP_STATIC_SCRATCH_BYTES per GPU instead; the call allocates and frees nothing.  A launch whose
+ * workspace does not fit is refused with UNP_INVALID_ARGUMENT before anything runs.  Each call
+ * clears the part of the array it uses on its stream first; calls that overlap on one GPU share the
+ * array and race, so a caller serialises them. */
+#define UNP_STATIC_SCRATCH_BYTES (4u << 20)
+int32_t unp_hip_exec_launch_static(unp_exec* e, const unp_arg* args, size_t nargs, void* stream, unp_error* err);
 /* The last launch's geometry and chosen entry point (for reports). */
 int32_t unp_hip_exec_last_launch(const unp_exec* e, uint32_t grid[3], uint32_t block[3],
                                  char* entry, size_t entry_len);

@@ -307,16 +307,28 @@ class Executor:
         check(_lib.lib().unp_hip_exec_create(kernel._handle, C.byref(h), C.byref(err)), err)
         self._h = h
 
-    def launch(self, *args, stream: int = 0) -> None:
-        """Arguments in the KernelFn's parameter order: buffers, then integer scalars."""
+    @staticmethod
+    def _args(args):
         arr = (_lib.Arg * len(args))()
         for i, a in enumerate(args):
             if isinstance(a, DeviceBuffer):
                 arr[i].is_buffer, arr[i].value = 1, a.ptr
             else:
                 arr[i].is_buffer, arr[i].value = 0, int(a) & 0xFFFFFFFFFFFFFFFF
+        return arr
+
+    def launch(self, *args, stream: int = 0) -> None:
+        """Arguments in the KernelFn's parameter order: buffers, then integer scalars."""
         err = _lib.Error()
-        check(_lib.lib().unp_hip_exec_launch(self._h, arr, len(args), stream, C.byref(err)), err)
+        check(_lib.lib().unp_hip_exec_launch(self._h, self._args(args), len(args), stream, C.byref(err)), err)
+
+    def launch_static(self, *args, stream: int = 0) -> None:
+        """``launch`` with every workspace in the library's static device scratch
+        (``unp_hip_exec_launch_static``): no allocation; a launch whose workspace does not fit is an
+        INVALID_ARGUMENT error.  Calls that overlap on one GPU share the scratch and race."""
+        err = _lib.Error()
+        check(_lib.lib().unp_hip_exec_launch_static(self._h, self._args(args), len(args), stream, C.byref(err)),
+              err)
 
     def launch_views(self, views, scalars, stream: int = 0) -> None:
         """The buffers as storage images: ``views`` is a list of ``(buffer, shape, strides, base)``

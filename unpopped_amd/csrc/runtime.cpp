@@ -64,6 +64,9 @@ struct unp_exec {
   size_t n_counters = 0;
   uint32_t epoch = 0;
   uint32_t ticket_base = 0;
+  // Set for the duration of a no-allocation launch: every workspace is carved from this region
+  // (cleared first) instead of the executor's own allocations.
+  const unp::Scratch* fixed = nullptr;
   uint32_t grid[3] = {0, 0, 0};
   uint32_t block[3] = {0, 0, 0};
   std::string last_entry;
@@ -428,6 +431,54 @@ int32_t ensure_ws(unp_exec* x, size_t bytes, bool need_counter, unp_error* err) 
   return UNP_OK;
 }
 
+// The workspaces of one launch: the executor's own allocations, or, in a no-allocation launch,
+// 256-byte-aligned pieces of the caller's scratch region (a ticket counter, then the counters,
+// then the workspace), cleared on the launch stream before the kernel runs.
+struct Ws {
+  void* ws = nullptr;
+  uint32_t* counter = nullptr;
+  uint32_t* counters = nullptr;
+};
+
+int32_t ensure_counters(unp_exec* x, size_t n, unp_error* err);
+
+int32_t workspace(unp_exec* x, size_t bytes, bool need_counter, size_t n_counters, hipStream_t s, Ws& w,
+                  unp_error* err) {
+  if (x->fixed) {
+    const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    const size_t need = (need_counter ? 256 : 0) + up(n_counters * sizeof(uint32_t)) + up(bytes);
+    // The last 256 bytes stay unused, so no piece ends at the region's very end.
+    if (x->fixed->cap < 256 || need > x->fixed->cap - 256) {
+      set_error(err, UNP_INVALID_ARGUMENT,
+                "this launch needs " + std::to_string(need) + " bytes of workspace; the static scratch holds " +
+                    std::to_string(x->fixed->cap) + " (" + std::to_string(x->fixed->cap - 256) + " usable)");
+      return UNP_INVALID_ARGUMENT;
+    }
+    uint8_t* p = static_cast<uint8_t*>(x->fixed->base);
+    if (need_counter) {
+      w.counter = reinterpret_cast<uint32_t*>(p);
+      p += 256;
+    }
+    if (n_counters) {
+      w.counters = reinterpret_cast<uint32_t*>(p);
+      p += up(n_counters * sizeof(uint32_t));
+    }
+    if (bytes) w.ws = p;
+    if (need) {
+      const hipError_t e = hipMemsetAsync(x->fixed->base, 0, need, s);
+      if (e != hipSuccess) return hip_fail(err, "hipMemsetAsync(scratch)", e);
+    }
+    return UNP_OK;
+  }
+  int32_t rc = ensure_ws(x, bytes, need_counter, err);
+  if (rc == UNP_OK && n_counters) rc = ensure_counters(x, n_counters, err);
+  if (rc != UNP_OK) return rc;
+  w.ws = x->ws;
+  w.counter = x->counter;
+  w.counters = x->counters;
+  return UNP_OK;
+}
+
 // The kept and the reduced axes of a row-major input with their element strides, outermost
 // first, adjacent axes of a kind merged (a merged run's stride is its innermost axis's).
 void fill_axes_desc(const std::vector<int64_t>& ext, int32_t rank, uint32_t mask, unp::axes_desc_host& d) {
@@ -528,10 +579,11 @@ int32_t run_xreduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, u
   }
   if (sched == 'a') {
     const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
-    if ((rc = ensure_ws(x, (size_t)grid * 8, true, err)) != UNP_OK) return rc;
+    Ws w;
+    if ((rc = workspace(x, (size_t)grid * 8, true, 0, s, w, err)) != UNP_OK) return rc;
     long long nn = count;
-    void* ws = x->ws;
-    void* cnt = x->counter;
+    void* ws = w.ws;
+    void* cnt = w.counter;
     params.push_back(&nn);
     params.push_back(&ws);
     params.push_back(&cnt);
@@ -592,10 +644,11 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
       void* ws = nullptr;
       void* cnt = nullptr;
       if (S > 1) {
-        if ((rc = ensure_ws(x, (size_t)(strips * S * cw) * acc_bytes, false, err)) != UNP_OK) return rc;
-        if ((rc = ensure_counters(x, (size_t)strips, err)) != UNP_OK) return rc;
-        ws = x->ws;
-        cnt = x->counters;
+        Ws w;
+        if ((rc = workspace(x, (size_t)(strips * S * cw) * acc_bytes, false, (size_t)strips, s, w, err)) != UNP_OK)
+          return rc;
+        ws = w.ws;
+        cnt = w.counters;
       }
       void* params[] = {&in, &out, &a, &r, &b, &S, &ws, &cnt};
       return launch(x, entry, (uint32_t)grid, params, s, err);
@@ -620,10 +673,11 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
   const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
   if (x->l.reduce_all) {
     const size_t acc_bytes = 8;
-    if ((rc = ensure_ws(x, grid * acc_bytes, true, err)) != UNP_OK) return rc;
+    Ws w;
+    if ((rc = workspace(x, grid * acc_bytes, true, 0, s, w, err)) != UNP_OK) return rc;
     long long nn = cols;
-    void* ws = x->ws;
-    void* cnt = x->counter;
+    void* ws = w.ws;
+    void* cnt = w.counter;
     void* params[] = {&in, &o0, &nn, &ws, &cnt};
     return launch(x, entry, grid, params, s, err);
   }
@@ -654,7 +708,16 @@ int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_err
     set_error(err, UNP_INVALID_ARGUMENT, "too many scan tiles for one launch");
     return UNP_INVALID_ARGUMENT;
   }
-  if ((rc = ensure_ws(x, (size_t)tiles * unp::kScanStatusWords * 8, true, err)) != UNP_OK) return rc;
+  Ws w;
+  if ((rc = workspace(x, (size_t)tiles * unp::kScanStatusWords * 8, true, 0, s, w, err)) != UNP_OK) return rc;
+  if (x->fixed) {
+    // The scratch was just cleared: epoch 1 and tickets from 0, and no state kept for the next call.
+    uint32_t tb = 0, ep = 1;
+    void* st = w.ws;
+    void* cnt = w.counter;
+    void* params[] = {&in, &out, &rows, &cols, &st, &cnt, &tb, &ep};
+    return launch(x, entry, grid, params, s, err);
+  }
   if (x->epoch == 0x7fffffffu) {
     // The status words hold a 31-bit epoch: after 2^31 - 1 launches the tags would repeat, so
     // clear the words and restart at epoch 1.
@@ -664,8 +727,8 @@ int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_err
   }
   x->epoch += 1;  // the words start zeroed, so epoch 1 is never seen before the first launch
   uint32_t tb = x->ticket_base, ep = x->epoch;
-  void* st = x->ws;
-  void* cnt = x->counter;
+  void* st = w.ws;
+  void* cnt = w.counter;
   void* params[] = {&in, &out, &rows, &cols, &st, &cnt, &tb, &ep};
   rc = launch(x, entry, grid, params, s, err);
   // One ticket per tile, plus the one failing draw that ends each block.
@@ -781,9 +844,10 @@ int32_t run_repacked(unp_exec* x, size_t prep, size_t main, uint64_t w, uint64_t
   }
   // x' (K x Cp x digit planes bytes), then the group column sums (ng x Cp u32, 64 spare).
   const size_t xp_bytes = (size_t)K * (size_t)Cp * (size_t)xbytes;
-  int32_t rc = ensure_ws(x, xp_bytes + ((size_t)ng * (size_t)Cp + 64) * 4, false, err);
+  Ws wsp;
+  int32_t rc = workspace(x, xp_bytes + ((size_t)ng * (size_t)Cp + 64) * 4, false, 0, s, wsp, err);
   if (rc != UNP_OK) return rc;
-  uint64_t xp = (uint64_t)x->ws, xs = xp + xp_bytes;
+  uint64_t xp = (uint64_t)wsp.ws, xs = xp + xp_bytes;
   long long Kp = K, Cc = C, Cpp = Cp, G = group, n_out = S > 1 ? R * C : 0;
   void* pparams[] = {&xa, &xp, &xs, &Kp, &Cc, &Cpp, &G, &out, &n_out};
   if ((rc = launch(x, prep, (uint32_t)(ng * (Cp / prep_cols)), pparams, s, err)) != UNP_OK) return rc;
@@ -966,3 +1030,20 @@ extern "C" int32_t unp_hip_exec_launch(unp_exec* x, const unp_arg* args, size_t 
       return UNP_UNSUPPORTED_KERNEL;
   }
 }
+
+namespace unp {
+
+int32_t exec_launch_in(unp_exec* x, const unp_arg* args, size_t nargs, void* stream, void* scratch, size_t cap,
+                       unp_error* err) {
+  if (!x || !scratch) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null executor or scratch");
+    return UNP_INVALID_ARGUMENT;
+  }
+  const Scratch sc{scratch, cap};
+  x->fixed = &sc;
+  const int32_t rc = unp_hip_exec_launch(x, args, nargs, stream, err);
+  x->fixed = nullptr;
+  return rc;
+}
+
+}  // namespace unp

@@ -125,6 +125,17 @@ uint64_t fnv1a64(const std::string& s);
 
 void set_error(unp_error* err, int32_t code, const std::string& detail);
 
+// A caller-provided device region that a no-allocation launch carves its workspaces from.
+struct Scratch {
+  void* base;
+  size_t cap;
+};
+// unp_hip_exec_launch with every workspace taken from [scratch, scratch + cap) and cleared on the
+// launch stream first: it calls no allocator, and refuses a launch whose workspace does not fit
+// with UNP_INVALID_ARGUMENT before anything runs.
+int32_t exec_launch_in(unp_exec* x, const unp_arg* args, size_t nargs, void* stream, void* scratch, size_t cap,
+                       unp_error* err);
+
 }  // namespace unp
 
 struct unp_generated {
