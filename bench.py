@@ -9,8 +9,11 @@ One step is one pass of the suite over the seeded synthetic inputs, each kernel 
   cfg4z  the same gather with Zipf(1.1) ids (seed 3)
   cfg5   U4 8192 x 28672 dequant, f16 scales and U4 zeros per 128 columns, bf16 out (seed 4)
 Inputs are resident in HBM before the timed region.  Each kernel's time is the average over the
-timed steps of the HIP-event interval around its launch on the launch stream; `value` is the
-suite's algorithmic bytes over the suite's kernel time.  The CPU baseline is the reference's
+timed steps of the interval between two HIP events that take its own dispatch start and end
+timestamps on the launch stream (hipExtModuleLaunchKernel); `value` is the algorithmic bytes of
+the cases whose algorithmic bytes are HBM bytes (all but cfg4z, whose repeated rows come from L2
+and the MALL; it runs in the same steps and is reported beside the aggregate) over their kernel
+time.  The CPU baseline is the reference's
 cpu-c C99 leg (restated in oracle/cpuc.*) for the same lifted kernels, one pinned core, on bounded
 samples; it also runs config 1 (the CPU-only configuration) in full.
 """
@@ -37,9 +40,12 @@ def log(msg: str) -> None:
 
 
 class Case:
-    def __init__(self, name, what, nbytes, elements, setup, ops=0):
+    def __init__(self, name, what, nbytes, elements, setup, ops=0, in_value=True):
         self.name, self.what, self.nbytes, self.elements, self.setup = name, what, nbytes, elements, setup
         self.ops = ops  # integer operations per launch, for the lines that run on MFMA
+        # Whether the case's algorithmic bytes are HBM bytes and so count in `value`: the Zipf
+        # gather's repeated rows come from L2 and the MALL, so it is reported beside the aggregate.
+        self.in_value = in_value
         self.launch = None
 
 
@@ -95,7 +101,8 @@ def build_cases(u, synth):
         return setup
     gbytes = 65536 * 4096 * 2 * 2 + 65536 * 4
     cases.append(Case("cfg4u", "bf16 262144x4096 gather, 65536 uniform ids", gbytes, 65536 * 4096, gather("uniform")))
-    cases.append(Case("cfg4z", "bf16 262144x4096 gather, 65536 Zipf(1.1) ids", gbytes, 65536 * 4096, gather("zipf")))
+    cases.append(Case("cfg4z", "bf16 262144x4096 gather, 65536 Zipf(1.1) ids", gbytes, 65536 * 4096, gather("zipf"),
+                      in_value=False))
 
     def cfg5():
         R, Cc, G = 8192, 28672, 128
@@ -181,20 +188,22 @@ def build_extras(u, synth):
 
 
 def time_cases(u, cases, steps):
-    """Average HIP-event time of each case's launch over `steps` rounds (one launch per case per
-    round, on the launch stream)."""
-    events = [[u.Event() for _ in range(len(cases) + 1)] for _ in range(steps)]
+    """Average kernel time of each case's launch over `steps` rounds (one launch per case per round,
+    on the launch stream).  Each launch carries a pair of HIP events that take the first and the last
+    kernel's own dispatch timestamps (unp_hip_exec_set_timing, hipExtModuleLaunchKernel), so the time
+    is the kernels' and not the queueing gap around them, as in a rocprofv3 kernel trace."""
+    events = [[(u.Event(), u.Event()) for _ in cases] for _ in range(steps)]
     u.synchronize()
     for s in range(steps):
-        ev = events[s]
-        ev[0].record()
         for i, c in enumerate(cases):
+            c.exec.set_timing(*events[s][i])
             c.launch()
-            ev[i + 1].record()
     u.synchronize()
+    for c in cases:
+        c.exec.set_timing(None, None)
     per = []
     for i, c in enumerate(cases):
-        ms = sum(events[s][i].elapsed_ms(events[s][i + 1]) for s in range(steps)) / steps
+        ms = sum(events[s][i][0].elapsed_ms(events[s][i][1]) for s in range(steps)) / steps
         gbps = c.nbytes / (ms * 1e-3) / 1e9
         per.append({
             "name": c.name, "what": c.what, "entry": c.exec.last_launch()["entry"],
@@ -515,17 +524,21 @@ def gemm_lines(u, synth, steps: int, warmup: int) -> None:
             del dx, do
 
 
-def attach_traffic(per) -> None:
-    """HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE passes (each counter scaled
-    by what it reads for a plain copy of known size), where a profile covers the kernel."""
+def attach_traffic(per, cases) -> None:
+    """HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE profile (each counter scaled by
+    what it reads for a plain copy of known size), attached only to a case whose running kernel has
+    the source revision (FNV-1a of the generated source) that was profiled, and labelled with the
+    file it comes from; a kernel changed since its profile gets no figure."""
     tf = ROOT / "profiles" / "traffic.json"
     if not tf.exists():
         return
     known = json.loads(tf.read_text()).get("cases", {})
-    for p in per:
+    for p, c in zip(per, cases):
         t = known.get(p["name"])
-        if t and t.get("kernel") == p["entry"]:
+        rev = f"{c.exec.kernel.revision_hash():016x}"
+        if t and t.get("kernel") == p["entry"] and t.get("revision") == rev:
             p["traffic"] = t["traffic_bytes"]
+            p["traffic_source"] = f"profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; revision {rev})"
 
 
 def main() -> int:
@@ -583,14 +596,17 @@ def main() -> int:
     t0 = time.perf_counter()
     per = time_cases(u, cases, args.steps)
     wall = time.perf_counter() - t0
-    total_bytes = sum(c.nbytes for c in cases)
+    for p, c in zip(per, cases):
+        p["in_value"] = c.in_value
+    hbm = [(p, c) for p, c in zip(per, cases) if c.in_value]
+    total_bytes = sum(c.nbytes for _, c in hbm)
     ms_step = sum(p["us"] for p in per) / 1e3
-    value = total_bytes / (ms_step * 1e-3) / 1e9
+    value = total_bytes / (sum(p["us"] for p, _ in hbm) * 1e-6) / 1e9 if hbm else 0.0
     dom = max(per, key=lambda p: p["us"])
 
-    # HBM bytes per launch from the committed FETCH_SIZE/WRITE_SIZE passes (each scaled by what
-    # the counter reads for a plain copy of known size); null when no profile covers the kernel.
-    attach_traffic(per)
+    # HBM bytes per launch from the committed FETCH_SIZE/WRITE_SIZE passes, for kernels whose source
+    # is the profiled one; null otherwise.
+    attach_traffic(per, cases)
     traffic = dom.get("traffic")
 
     extra = None
@@ -603,7 +619,7 @@ def main() -> int:
                 c.launch()
         log(f"[bench] timing {args.steps} steps of the extra lines")
         extra = time_cases(u, xs, args.steps)
-        attach_traffic(extra)
+        attach_traffic(extra, xs)
 
     cpu = None
     if not args.no_cpu:
@@ -625,6 +641,10 @@ def main() -> int:
         "data": "synthetic: seeded LCG streams (dyadic uniforms, Box-Muller normals, Zipf ids)",
         "config": {
             "workload": "suite: " + ", ".join(c.name for c in cases),
+            "value_counts": ", ".join(c.name for _, c in hbm) + " (algorithmic bytes = HBM bytes); "
+                            + ", ".join(c.name for c in cases if not c.in_value)
+                            + " timed in the same steps and reported beside it (cache-served rows)",
+            "timing": "per-kernel dispatch timestamps (HIP events via hipExtModuleLaunchKernel) on the launch stream",
             "device": arch,
             "cu_count": cus,
             "wall_s_timed_region": round(wall, 4),
@@ -638,6 +658,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(dom["GBps"] / PEAK_GBPS, 4),
             "traffic": traffic,
+            "traffic_source": dom.get("traffic_source"),
         },
         "cpu_baseline": cpu,
         "extra_kernels": extra,

@@ -304,6 +304,12 @@ int32_t unp_hip_exec_launch_views(unp_exec* e, const unp_view* views, size_t nvi
  * array and race, so a caller serialises them. */
 #define UNP_STATIC_SCRATCH_BYTES (4u << 20)
 int32_t unp_hip_exec_launch_static(unp_exec* e, const unp_arg* args, size_t nargs, void* stream, unp_error* err);
+/* Kernel timing for reports (no reference counterpart): after this call every launch of `e` records
+ * `start` at the beginning of its first kernel and `stop` at the end of its last, from the kernels'
+ * own dispatch timestamps (hipExtModuleLaunchKernel), so unp_hip_event_elapsed_ms(start, stop) is
+ * the launch's kernel time without the queueing gap around it.  NULL, NULL restores plain launches;
+ * the events must stay alive while they are set. */
+int32_t unp_hip_exec_set_timing(unp_exec* e, unp_event* start, unp_event* stop);
 /* The last launch's geometry and chosen entry point (for reports). */
 int32_t unp_hip_exec_last_launch(const unp_exec* e, uint32_t grid[3], uint32_t block[3],
                                  char* entry, size_t entry_len);

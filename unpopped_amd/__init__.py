@@ -349,6 +349,12 @@ class Executor:
         check(_lib.lib().unp_hip_exec_launch_views(self._h, arr, len(views), sc, len(scalars), stream, C.byref(err)),
               err)
 
+    def set_timing(self, start: "Event | None", end: "Event | None") -> None:
+        """Record ``start``/``end`` from the first and last kernel's own dispatch timestamps on every
+        later launch (``None, None`` stops)."""
+        check(_lib.lib().unp_hip_exec_set_timing(self._h, start._h if start else None, end._h if end else None),
+              what="set_timing")
+
     def last_launch(self) -> dict:
         g = (C.c_uint32 * 3)()
         b = (C.c_uint32 * 3)()

@@ -121,6 +121,7 @@ def lib() -> C.CDLL:
         "unp_hip_exec_launch": (i32, [P, C.POINTER(Arg), sz, P, E]),
         "unp_hip_exec_launch_views": (i32, [P, C.POINTER(View), sz, C.POINTER(C.c_int64), sz, P, E]),
         "unp_hip_exec_launch_static": (i32, [P, C.POINTER(Arg), sz, P, E]),
+        "unp_hip_exec_set_timing": (i32, [P, P, P]),
         "unp_hip_exec_last_launch": (i32, [P, C.POINTER(u32), C.POINTER(u32), C.c_char_p, sz]),
         "unp_hip_exec_destroy": (None, [P]),
     }

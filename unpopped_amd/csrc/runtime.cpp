@@ -15,6 +15,14 @@
 #include "kernel_ir.hpp"
 #include "unp_internal.hpp"
 
+// libamdhip64's launch with kernel-timestamp events (declared in hip/hip_ext.h, whose C++ helpers
+// need the HIP compiler; this file is compiled by the host compiler).
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX, uint32_t globalWorkSizeY,
+                                               uint32_t globalWorkSizeZ, uint32_t localWorkSizeX,
+                                               uint32_t localWorkSizeY, uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void** kernelParams, void** extra,
+                                               hipEvent_t startEvent, hipEvent_t stopEvent, uint32_t flags);
+
 using unp::set_error;
 
 namespace {
@@ -67,6 +75,10 @@ struct unp_exec {
   // Set for the duration of a no-allocation launch: every workspace is carved from this region
   // (cleared first) instead of the executor's own allocations.
   const unp::Scratch* fixed = nullptr;
+  // Kernel timing for reports: the first kernel of a launch records t_start at its beginning and
+  // every kernel records t_stop at its end (their own dispatch timestamps).
+  hipEvent_t t_start = nullptr, t_stop = nullptr;
+  bool t_first = false;
   uint32_t grid[3] = {0, 0, 0};
   uint32_t block[3] = {0, 0, 0};
   std::string last_entry;
@@ -344,6 +356,13 @@ void unp_hip_exec_destroy(unp_exec* x) {
   delete x;
 }
 
+int32_t unp_hip_exec_set_timing(unp_exec* x, unp_event* start, unp_event* stop) {
+  if (!x || (start == nullptr) != (stop == nullptr)) return UNP_INVALID_ARGUMENT;
+  x->t_start = start ? start->e : nullptr;
+  x->t_stop = stop ? stop->e : nullptr;
+  return UNP_OK;
+}
+
 int32_t unp_hip_exec_last_launch(const unp_exec* x, uint32_t grid[3], uint32_t block[3], char* entry,
                                  size_t entry_len) {
   if (!x) return UNP_INVALID_ARGUMENT;
@@ -529,6 +548,18 @@ int32_t launch(unp_exec* x, size_t entry, uint32_t grid, void** params, hipStrea
   x->block[0] = threads;
   x->block[1] = x->block[2] = 1;
   x->last_entry = x->l.entries[entry].symbol;
+  if (x->t_stop) {
+    if ((uint64_t)grid * threads > 0xFFFFFFFFull) {
+      set_error(err, UNP_INVALID_ARGUMENT, "a timed launch takes at most 2^32 - 1 work-items");
+      return UNP_INVALID_ARGUMENT;
+    }
+    hipEvent_t start = x->t_first ? x->t_start : nullptr;
+    x->t_first = false;
+    const hipError_t e = hipExtModuleLaunchKernel(x->fns[entry], grid * threads, 1, 1, threads, 1, 1, 0, s, params,
+                                                  nullptr, start, x->t_stop, 0);
+    if (e != hipSuccess) return hip_fail(err, "hipExtModuleLaunchKernel", e);
+    return UNP_OK;
+  }
   const hipError_t e = hipModuleLaunchKernel(x->fns[entry], grid, 1, 1, threads, 1, 1, 0, s, params, nullptr);
   if (e != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel", e);
   return UNP_OK;
@@ -1005,6 +1036,7 @@ extern "C" int32_t unp_hip_exec_launch(unp_exec* x, const unp_arg* args, size_t 
     return UNP_INVALID_ARGUMENT;
   }
   set_error(err, UNP_OK, "");
+  x->t_first = true;
   int cur = -1;
   if (hipGetDevice(&cur) != hipSuccess || cur != x->device) {
     set_error(err, UNP_INVALID_ARGUMENT, "the executor was created on another device");
