@@ -115,8 +115,13 @@ enum unp_form_kind {
                                weights, I32 zero and scale per group, I32 or I8 activations,
                                I32 out, all wrapping */
 };
-/* ReduceOp subset (crates/unpopped/src/ir.rs:1700). */
-enum unp_reduce_op { UNP_OP_SUM = 0, UNP_OP_PROD = 1, UNP_OP_MAX = 2, UNP_OP_MIN = 3, UNP_OP_MEAN = 4 };
+/* ReduceOp subset (crates/unpopped/src/ir.rs:1700-1735).  And/Or/Xor fold integers bitwise;
+ * MaxNum/MinNum ignore NaN (a run of only NaN gives NaN); the reference lifts these five as
+ * sequential reductions only (kernel_lift.rs:763-800, block_reduce.rs:97-133). */
+enum unp_reduce_op {
+  UNP_OP_SUM = 0, UNP_OP_PROD = 1, UNP_OP_MAX = 2, UNP_OP_MIN = 3, UNP_OP_MEAN = 4,
+  UNP_OP_AND = 5, UNP_OP_OR = 6, UNP_OP_XOR = 7, UNP_OP_MAXNUM = 8, UNP_OP_MINNUM = 9
+};
 /* OobPolicy (ir.rs:2582). */
 enum unp_oob_policy { UNP_OOB_SKIP = 0, UNP_OOB_ZEROFILL = 1, UNP_OOB_CLAMP = 2 };
 

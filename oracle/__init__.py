@@ -20,8 +20,9 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "liboracle.so"
 
-SUM, PROD, MAX, MIN, MEAN = 0, 1, 2, 3, 4
-OPS = {"Sum": SUM, "Prod": PROD, "Max": MAX, "Min": MIN, "Mean": MEAN}
+SUM, PROD, MAX, MIN, MEAN, AND, OR, XOR, MAXNUM, MINNUM = range(10)
+OPS = {"Sum": SUM, "Prod": PROD, "Max": MAX, "Min": MIN, "Mean": MEAN, "And": AND, "Or": OR, "Xor": XOR,
+       "MaxNum": MAXNUM, "MinNum": MINNUM}
 SKIP, ZEROFILL, CLAMP = 0, 1, 2
 POLICIES = {"Skip": SKIP, "ZeroFill": ZEROFILL, "Clamp": CLAMP}
 IDX_KINDS = {"I32": 9, "I64": 10, "U32": 23}

@@ -118,8 +118,10 @@ void orc_sub4_store(uint8_t* p, int64_t i, int32_t v) {
  * Reductions: lift_reduction_opdef's order (crates/unpopped/src/kernel_lift.rs:447-484,
  * ReductionShape :838-1025): per kept row, the reduced elements ascending into an
  * accumulator (f64 for a float, the dtype itself for an integer), Max/Min with a `have` flag
- * that keeps a NaN once seen (extremum_step :1097-1160), Mean divides by the reduced extent,
- * and one cast down at the store (:965-983).  An empty fold stores the starting value.
+ * that keeps a NaN once seen (extremum_step :1097-1160), MaxNum/MinNum that skip a NaN element
+ * and replace a NaN accumulator (nan_arm :1129-1160), And/Or/Xor seeded by the first element
+ * (bit_step :1071-1095), Mean divides by the reduced extent, and one cast down at the store
+ * (:965-983).  An empty fold stores the starting value.
  * ==================================================================================== */
 
 static double fold_f64(int op, double acc, double v, int* have) {
@@ -135,6 +137,15 @@ static double fold_f64(int op, double acc, double v, int* have) {
       if (!*have) r = v;
       else if (v != v) r = v;
       else if (op == ORC_MAX ? v > acc : v < acc) r = v;
+      *have = 1;
+      return r;
+    }
+    case ORC_MAXNUM:
+    case ORC_MINNUM: {
+      double r = acc;
+      if (!*have) r = v;
+      else if (acc != acc) r = v;
+      else if (v == v && (op == ORC_MAXNUM ? v > acc : v < acc)) r = v;
       *have = 1;
       return r;
     }
@@ -173,7 +184,12 @@ void orc_reduce_rows_f64(const double* in, int64_t rows, int64_t cols, int op, d
         const T v = in[r * cols + c];                                              \
         if (op == ORC_SUM) acc = acc + (U)v;                                       \
         else if (op == ORC_PROD) acc = acc * (U)v;                                 \
-        else if (!have || (op == ORC_MAX ? v > (T)acc : v < (T)acc)) acc = (U)v;   \
+        else if (op == ORC_AND) acc = have ? (acc & (U)v) : (U)v;                  \
+        else if (op == ORC_OR) acc = have ? (acc | (U)v) : (U)v;                   \
+        else if (op == ORC_XOR) acc = have ? (acc ^ (U)v) : (U)v;                  \
+        else if (!have || ((op == ORC_MAX || op == ORC_MAXNUM) ? v > (T)acc        \
+                                                                : v < (T)acc))     \
+          acc = (U)v;                                                              \
         have = 1;                                                                  \
       }                                                                            \
       out[r] = (T)acc;                                                             \

@@ -15,7 +15,10 @@
 #include <stdint.h>
 
 /* ReduceOp subset and OobPolicy codes (as include/unpopped_hip.h). */
-enum { ORC_SUM = 0, ORC_PROD = 1, ORC_MAX = 2, ORC_MIN = 3, ORC_MEAN = 4 };
+enum {
+  ORC_SUM = 0, ORC_PROD = 1, ORC_MAX = 2, ORC_MIN = 3, ORC_MEAN = 4,
+  ORC_AND = 5, ORC_OR = 6, ORC_XOR = 7, ORC_MAXNUM = 8, ORC_MINNUM = 9
+};
 enum { ORC_SKIP = 0, ORC_ZEROFILL = 1, ORC_CLAMP = 2 };
 enum { ORC_IDX_I32 = 9, ORC_IDX_I64 = 10, ORC_IDX_U32 = 23 };
 

@@ -231,8 +231,12 @@ def test_lower_kernel_refuses_anything_else():
     refused(json.dumps([1, 2, 3]), "ParseError")
     # a gather along axis 1 is recognised and refused by name
     assert "axis 1" in refused(u.lift_gather("g", "F32", 2, axis=1))
-    # a float Prod (serial lift exists; this backend has no kernel for it)
-    refused(u.lift_reduction("r", "F32", 2, "Prod"))
+    # a float Prod: the serial lift is lowered to the entry that multiplies in the serial order; the
+    # launched lift declines it (block_reduce.rs:97-133)
+    assert b.lower_kernel(u.lift_reduction("r", "F32", 2, "Prod")).name.startswith("unp_reduce_serial_prod_f32")
+    with pytest.raises(_lib.UnpError) as e:
+        u.lift_reduction("r", "F32", 2, "Prod", launch=(256, 64))
+    assert e.value.kind == "LiftDecline" and "float Prod" in e.value.detail
     # a scan along a non-innermost axis
     refused(u.lift_scan("s", "F32", 2, "Sum", axis=0))
     # a pre-map body (x * x) is the lift of OpDef::reduction with that body: recognised, and
@@ -252,7 +256,7 @@ def test_lower_kernel_refuses_anything_else():
 def test_lower_form_declines_unsupported_forms():
     b = u.HipBackend()
     for form, kind in [
-        (dict(kind="reduction", dtype="F32", op="Prod", rank=1, reduced_from=0), "UnsupportedKernel"),
+        (dict(kind="reduction", dtype="F32", op="And", rank=1, reduced_from=0), "UnsupportedKernel"),
         (dict(kind="reduction", dtype="I32", op="Mean", rank=1, reduced_from=0), "UnsupportedKernel"),
         (dict(kind="scan", dtype="F32", op="Mean"), "UnsupportedKernel"),
         (dict(kind="gather", dtype="U4", rank=2), "UnsupportedDtype"),
@@ -406,3 +410,23 @@ def test_dequant_gemm_refuses_other_element_types():
     k["params"][3]["kind"]["Buffer"]["elem"] = "I16"
     with pytest.raises(_lib.UnpError):
         u.HipBackend().lower_kernel(k)
+
+
+def test_bit_and_nan_ignoring_folds_lift_only_sequentially():
+    """And/Or/Xor (integers) and MaxNum/MinNum lift as sequential reductions only
+    (kernel_lift.rs:763-800, block_reduce.rs:97-133): the serial lift is recognised and lowered, the
+    launched lift, a scan and a float bit fold are typed declines."""
+    be = u.HipBackend()
+    for dt, op in (("F32", "MaxNum"), ("F64", "MinNum"), ("I32", "And"), ("I64", "Or"), ("I32", "Xor")):
+        for axes in ((1,), (0,), (0, 1)):
+            g = be.lower_kernel(u.lift_reduction("r", dt, 2, op, axes=axes))
+            assert op.lower() in g.name, (dt, op, g.name)
+        with pytest.raises(_lib.UnpError) as e:
+            u.lift_reduction("r", dt, 2, op, launch=(256, 64))
+        assert e.value.kind == "LiftDecline" and "sequential lift only" in e.value.detail
+        with pytest.raises(_lib.UnpError):
+            u.lift_scan("s", dt, 1, op)
+    for op in ("And", "Or", "Xor"):
+        with pytest.raises(_lib.UnpError) as e:
+            u.lift_reduction("r", "F32", 2, op)
+        assert "bit reduction at a float dtype" in e.value.detail

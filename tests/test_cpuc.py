@@ -398,3 +398,15 @@ def test_refusals_are_typed():
     with pytest.raises(cpuc.Declined) as e:
         cpuc.lower("{not json")
     assert e.value.code == cpuc.PARSE_ERROR
+
+
+@pytest.mark.parametrize("dtype,op", [("F32", "MaxNum"), ("F64", "MinNum"), ("I32", "And"), ("I64", "Or"),
+                                      ("I32", "Xor"), ("I64", "MaxNum")])
+def test_sequential_only_folds_equal_the_oracle(dtype, op):
+    x = data(dtype, (8, 29))
+    if dtype[0] == "F":
+        x[1, 0], x[2, :], x[3, 11] = np.nan, np.nan, np.nan
+    k = u.lift_reduction("so", dtype, 2, op)
+    out = np.zeros(8, NP[dtype])
+    assert cpuc.run(k, x, out, 8, 29) == cpuc.OK
+    assert np.array_equal(out, oracle.reduce_rows(x, op), equal_nan=dtype[0] == "F"), (dtype, op)

@@ -102,6 +102,36 @@ def test_rowreduce_nan_and_infinities(hip_device):
     assert np.isnan(s[4]) and np.isnan(want[4])
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64, np.int32, np.int64])
+@pytest.mark.parametrize("shape", [(3, 5), (7, 1000), (2, 70000), (1, 1 << 20)])
+def test_sequential_only_folds_on_rows_and_whole_arrays(hip_device, dtype, shape):
+    """The folds the reference lifts only sequentially: MaxNum/MinNum (NaN-ignoring) and, at the
+    integers, And/Or/Xor, bit-exact against the oracle on the row schedule and the whole-array
+    schedule; a float Prod in the serial lift's own order, bit-exact too."""
+    is_int = dtype in (np.int32, np.int64)
+    r = rng(47)
+    if is_int:
+        info = np.iinfo(dtype)
+        x = r.integers(info.min, info.max, size=shape, dtype=dtype, endpoint=True)
+        ops = ["And", "Or", "Xor", "MaxNum", "MinNum"]
+    else:
+        x = r.normal(size=shape).astype(dtype)
+        x.ravel()[::5] = np.nan
+        if shape[0] > 1:
+            x[1, :] = np.nan  # a row of only NaN folds to NaN
+        ops = ["MaxNum", "MinNum"] + (["Prod"] if x.size <= 70000 * 2 else [])
+    for op in ops:
+        H.say(f"[case] {op} rows {shape} {np.dtype(dtype).name}")
+        xp = np.abs(x) + 0.5 if op == "Prod" else x  # keep the products finite and away from 0
+        got = H.reduce_rows(xp, op)
+        assert np.array_equal(got, oracle.reduce_rows(xp, op), equal_nan=True), op
+        if x.size <= (1 << 20) and op != "Prod" or x.size <= 4096:
+            H.say(f"[case] {op} all {x.size} {np.dtype(dtype).name}")
+            got = H.reduce_all(np.ascontiguousarray(xp.ravel()), op)
+            want = oracle.reduce_rows(np.ascontiguousarray(xp.reshape(1, -1)), op)[0]
+            assert np.array_equal(np.array([got]), np.array([want]), equal_nan=True), op
+
+
 def test_rowreduce_sum_max_fused_matches_two_folds(hip_device):
     H.say("[case] row_reduce2 sum+max f32 (129, 4096)")
     x = synth.normal_f32(1, 129 * 4096).reshape(129, 4096)
@@ -563,19 +593,25 @@ AXES_CASES = [((64, 300), (0,)), ((4096, 1024), (0,)), ((1000, 37), (0,)), ((3, 
 
 @pytest.mark.parametrize("shape,axes", AXES_CASES)
 @pytest.mark.parametrize("dtype", [np.float32, np.float64, np.int32, np.int64])
-@pytest.mark.parametrize("op", ["Sum", "Max", "Min", "Mean", "Prod"])
+@pytest.mark.parametrize("op", ["Sum", "Max", "Min", "Mean", "Prod", "MaxNum", "MinNum", "And", "Or", "Xor"])
 def test_reduce_any_axes(hip_device, shape, axes, dtype, op):
-    if op == "Mean" and dtype in (np.int32, np.int64):
-        pytest.skip("an integer Mean has no lift (check_accumulated_dtype, kernel_lift.rs:763)")
-    if op == "Prod" and dtype in (np.float32, np.float64):
-        pytest.skip("a float Prod is refused (not order-independent, no declared bound)")
+    is_int = dtype in (np.int32, np.int64)
     H.say(f"[case] reduce axes {axes} of {shape} {np.dtype(dtype).name} {op}")
     r = rng(40)
-    if dtype in (np.int32, np.int64):
+    if is_int:
         info = np.iinfo(dtype)
         x = r.integers(info.min, info.max, size=shape, dtype=dtype, endpoint=True)
     else:
         x = r.normal(size=shape).astype(dtype)
+        if op in ("MaxNum", "MinNum") and x.size:
+            x.ravel()[::7] = np.nan  # skipped by the NaN-ignoring folds
+    if (op == "Mean" and is_int) or (op in ("And", "Or", "Xor") and not is_int):
+        # No lift: an integer Mean, a bit fold of a float (check_accumulated_dtype, kernel_lift.rs:763-800).
+        with pytest.raises(u.UnpError) as e:
+            H.reduce_axes(x, axes, op)
+        assert e.value.kind == "LiftDecline"
+        assert ("an integer Mean" if op == "Mean" else "a bit reduction at a float dtype") in e.value.detail
+        return
     got = H.reduce_axes(x, axes, op)
     x2d, want = oracle_axes(x, axes, op)
     want = want.reshape(got.shape)

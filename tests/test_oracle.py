@@ -580,3 +580,41 @@ def test_rx_program_ops_follow_the_host_libm():
     # Fma rounds once: 0.1 * 10 - 1 is exactly 2^-54 (0.1 is 0x1.999999999999ap-4), the two-step form gives 0
     assert oracle.rx_eval(X.fma(X.input(0), X.input(1), X.input(2)), [0.1, 10.0, -1.0]) == 2.0 ** -54
     assert oracle.rx_eval(X.input(0) * X.input(1) + X.input(2), [0.1, 10.0, -1.0]) == 0.0
+
+
+def test_nan_ignoring_folds_against_numpy():
+    """MaxNum/MinNum (kernel_lift.rs nan_arm: a NaN accumulator is replaced, a NaN element is
+    skipped) equal numpy's fmax/fmin reductions, which ignore NaN unless every element is NaN; an
+    empty row stores 0.  The NaN-keeping Max differs on every row holding a NaN."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((8, 33)).astype(np.float32)
+    x[1, 0] = np.nan
+    x[2, :] = np.nan
+    x[3, 17] = np.nan
+    x[4, -1] = np.nan
+    x[5, ::2] = np.nan
+    for op, f in (("MaxNum", np.fmax), ("MinNum", np.fmin)):
+        got = oracle.reduce_rows(x, op)
+        assert np.array_equal(got, f.reduce(x, axis=1), equal_nan=True), op
+        assert np.array_equal(oracle.reduce_rows(x.astype(np.float64), op), f.reduce(x.astype(np.float64), axis=1),
+                              equal_nan=True)
+        keep = oracle.reduce_rows(x, op[:3])
+        for r in (1, 3, 4, 5):
+            assert np.isnan(keep[r]) and not np.isnan(got[r]), (op, r)
+    assert np.array_equal(oracle.reduce_rows(np.zeros((3, 0), np.float32), "MaxNum"), np.zeros(3, np.float32))
+
+
+def test_bit_folds_against_numpy():
+    """And/Or/Xor (kernel_lift.rs bit_step, seeded by the first element) equal numpy's bitwise
+    reductions over full-range integers; an empty row stores 0 (not And's all-ones identity); at an
+    integer MaxNum/MinNum are Max/Min."""
+    rng = np.random.default_rng(12)
+    for nt in (np.int32, np.int64):
+        info = np.iinfo(nt)
+        x = rng.integers(info.min, info.max, (9, 21), dtype=np.int64).astype(nt)
+        x[0] = -1
+        for op, f in (("And", np.bitwise_and), ("Or", np.bitwise_or), ("Xor", np.bitwise_xor)):
+            assert np.array_equal(oracle.reduce_rows(x, op), f.reduce(x, axis=1)), (nt, op)
+            assert np.array_equal(oracle.reduce_rows(np.zeros((2, 0), nt), op), np.zeros(2, nt))
+        assert np.array_equal(oracle.reduce_rows(x, "MaxNum"), x.max(axis=1))
+        assert np.array_equal(oracle.reduce_rows(x, "MinNum"), x.min(axis=1))

@@ -28,7 +28,8 @@ ELEMENT_KINDS = {
     "Complex64": 21, "Complex128": 22, "U32": 23, "U64": 24, "F4E2M1": 25, "F6E2M3": 26,
     "F6E3M2": 27,
 }
-REDUCE_OPS = {"Sum": 0, "Prod": 1, "Max": 2, "Min": 3, "Mean": 4}
+REDUCE_OPS = {"Sum": 0, "Prod": 1, "Max": 2, "Min": 3, "Mean": 4, "And": 5, "Or": 6, "Xor": 7, "MaxNum": 8,
+              "MinNum": 9}
 OOB_POLICIES = {"Skip": 0, "ZeroFill": 1, "Clamp": 2}
 FORMS = {"reduction": 0, "scan": 1, "gather": 2, "dequant4": 3, "row_reduce2": 4, "row_reduce": 5, "dequant_gemm": 6}
 DTYPE_SUPPORT = {0: "Supported", 1: "Unsupported", 2: "NotExpressible"}

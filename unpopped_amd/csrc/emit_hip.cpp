@@ -45,6 +45,11 @@ const char* op_name(int32_t op) {
     case UNP_OP_MAX: return "max";
     case UNP_OP_MIN: return "min";
     case UNP_OP_MEAN: return "mean";
+    case UNP_OP_AND: return "and";
+    case UNP_OP_OR: return "or";
+    case UNP_OP_XOR: return "xor";
+    case UNP_OP_MAXNUM: return "maxnum";
+    case UNP_OP_MINNUM: return "minnum";
     default: return nullptr;
   }
 }
@@ -102,9 +107,11 @@ std::string json_str(const std::string& s) {
   return o + "\"";
 }
 
-// The folds the reduction forms accept: those of lift_reduction_opdef_launched
-// (crates/unpopped/src/kernel_lift/block_reduce.rs:97-133) at F32/F64/I32/I64
-// (kernel_lift.rs:763-803): float Sum/Mean/Max/Min, integer Sum/Prod/Max/Min.
+// The folds the reduction forms accept at F32/F64/I32/I64 (kernel_lift.rs:763-803): those of
+// lift_reduction_opdef_launched (crates/unpopped/src/kernel_lift/block_reduce.rs:97-133), float
+// Sum/Mean/Max/Min and integer Sum/Prod/Max/Min, and the sequential lift's MaxNum/MinNum and integer
+// And/Or/Xor, whose results do not depend on the fold's order (NaN payload and the sign of a zero
+// tie aside, as for Max/Min).
 bool reduction_ok(int32_t dtype, int32_t op, std::string& why) {
   if (!ctype(dtype) || dtype == UNP_U32) {
     why = "a reduction outside F32, F64, I32 and I64";
@@ -119,8 +126,8 @@ bool reduction_ok(int32_t dtype, int32_t op, std::string& why) {
     why = "an integer Mean";
     return false;
   }
-  if (!is_int && op == UNP_OP_PROD) {
-    why = "a float Prod in a launched reduction (not order-independent, and no declared bound)";
+  if (!is_int && (op == UNP_OP_AND || op == UNP_OP_OR || op == UNP_OP_XOR)) {
+    why = "a bit reduction at a float dtype";
     return false;
   }
   return true;
@@ -211,9 +218,16 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
     why = "a reduced axis outside the rank";
     return UNP_LIFT_DECLINE;
   }
-  const char sched = reduction_schedule(mask, f.rank);
+  // A float Prod has no order-free form and no declared bound: it runs in the serial lift's own
+  // order (the launched lift refuses it, block_reduce.rs:97-133).
+  const bool serial = kind_is_float(f.dtype) && f.op0 == UNP_OP_PROD;
+  const char sched = serial ? 'q' : reduction_schedule(mask, f.rank);
   if (two && sched != 'r') {
     why = "the fused row fold reduces the trailing axis";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (two && kind_is_float(f.dtype) && f.op1 == UNP_OP_PROD) {
+    why = "a float Prod in the fused row fold (not order-independent, and no declared bound)";
     return UNP_UNSUPPORTED_KERNEL;
   }
   if (!reduction_ok(f.dtype, f.op0, why) || (two && !reduction_ok(f.dtype, f.op1, why)))
@@ -226,8 +240,11 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
   L.form.reduced_from = f.rank;
   for (int32_t d = f.rank - 1; d >= 0 && ((mask >> d) & 1u); --d) L.form.reduced_from = d;
   std::ostringstream name;
-  name << (sched == 'a' ? "unp_reduce_all_" : sched == 'm' ? "unp_reduce_mid_" : sched == 'g' ? "unp_reduce_axes_"
-                                                                                            : "unp_rowreduce_")
+  name << (sched == 'a'   ? "unp_reduce_all_"
+           : sched == 'm' ? "unp_reduce_mid_"
+           : sched == 'g' ? "unp_reduce_axes_"
+           : sched == 'q' ? "unp_reduce_serial_"
+                          : "unp_rowreduce_")
        << op_name(f.op0);
   if (two) name << "_" << op_name(f.op1);
   name << "_" << lower_name(f.dtype);
@@ -252,6 +269,16 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
           << ", 512, 8>(in, out, A, R, B, S, partials, counters);\n}\n";
       L.entries.push_back(e);
     }
+  } else if (sched == 'q') {
+    L.threads = 256;
+    L.blocks_per_cu = 8;
+    Entry e;
+    e.fast = false;
+    e.vec = 1;
+    e.symbol = L.name + "_q";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(const " << T << "* in, " << T
+        << "* out, unp::axes_desc d) {\n  unp::reduce_serial_prod<" << T << ", 256>(in, out, d);\n}\n";
+    L.entries.push_back(e);
   } else if (sched == 'g') {
     L.threads = 256;
     L.blocks_per_cu = 8;
@@ -308,7 +335,8 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
   for (int32_t d = 0, n = 0; d < f.rank; ++d)
     if ((mask >> d) & 1u) j << (n++ ? "," : "") << d;
   j << "],\"schedule\":\""
-    << (sched == 'a' ? "all" : sched == 'r' ? "rows" : sched == 'm' ? "mid" : "generic") << "\""
+    << (sched == 'a' ? "all" : sched == 'r' ? "rows" : sched == 'm' ? "mid" : sched == 'q' ? "serial" : "generic")
+    << "\""
     << ",\"params\":[{\"name\":\"in0\",\"kind\":\"buffer\",\"role\":\"Read\"},"
     << (two ? "{\"name\":\"out0\",\"kind\":\"buffer\",\"role\":\"Write\"},{\"name\":\"out1\",\"kind\":\"buffer\",\"role\":\"Write\"}"
             : "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}");
@@ -319,12 +347,14 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
         : sched == 'm' ? "the input as A x R x B: a wave per 64 x vec columns, blocks split R into chunks, the "
                          "last-ticket block of a column strip folds the chunk partials in chunk order"
         : sched == 'g' ? "one wave per output element, lanes stride over the reduced positions"
+        : sched == 'q' ? "one lane per output element, the reduced positions multiplied in the serial lift's "
+                         "order (f64, row-major over the reduced axes)"
                        : "waves stride over rows (one wave per row); rows longer than 32768 elements: one block per row")
     << "\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
       << ",\"when\":\"" << (L.entries[i].wide ? "reduced extent > 32768; " : "")
-      << (sched == 'g'   ? "always"
+      << ((sched == 'g' || sched == 'q') ? "always"
           : sched == 'm' ? (L.entries[i].fast ? "B % vec == 0 and in0 16-byte aligned" : "otherwise")
                          : (L.entries[i].fast ? "reduced extent % vec == 0 and in0 16-byte aligned" : "otherwise"))
       << "\"}";
@@ -1067,6 +1097,10 @@ int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L
     return UNP_UNSUPPORTED_KERNEL;
   }
   if (!reduction_ok(f.dtype, f.op0, why)) return UNP_UNSUPPORTED_KERNEL;
+  if (f.op0 == UNP_OP_PROD) {
+    why = "a float Prod with a pre-map body or a fused post (not order-independent, and no declared bound)";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
   const uint32_t mask = reduction_mask(f);
   if (mask == 0 || (mask >> f.rank) != 0) {
     why = "a reduced axis outside the rank";

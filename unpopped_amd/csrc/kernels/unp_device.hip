@@ -39,7 +39,10 @@ typedef long long i64;
 
 #define UNP_DEV __device__ __forceinline__
 
-enum : int { OP_SUM = 0, OP_PROD = 1, OP_MAX = 2, OP_MIN = 3, OP_MEAN = 4 };
+enum : int {
+  OP_SUM = 0, OP_PROD = 1, OP_MAX = 2, OP_MIN = 3, OP_MEAN = 4,
+  OP_AND = 5, OP_OR = 6, OP_XOR = 7, OP_MAXNUM = 8, OP_MINNUM = 9
+};
 enum : int { OOB_SKIP = 0, OOB_ZEROFILL = 1, OOB_CLAMP = 2 };
 
 template <class T> struct traits;
@@ -121,11 +124,49 @@ template <class A> struct fold<A, OP_MIN> {
   }
 };
 
-// The value stored for a finished fold over `n` elements.
+// MaxNum / MinNum ignore NaN: the quiet NaN is their identity (any value replaces it), so a run
+// of only NaN folds to NaN.  On integers they are Max / Min.
+template <class A> struct fold<A, OP_MAXNUM> {
+  static UNP_DEV A identity() {
+    if constexpr (traits<A>::is_float) return A(__builtin_nan(""));
+    else return traits<A>::lo;
+  }
+  static UNP_DEV A apply(A a, A b) {
+    if constexpr (traits<A>::is_float) return a != a ? b : ((b == b && b > a) ? b : a);
+    else return b > a ? b : a;
+  }
+};
+template <class A> struct fold<A, OP_MINNUM> {
+  static UNP_DEV A identity() {
+    if constexpr (traits<A>::is_float) return A(__builtin_nan(""));
+    else return traits<A>::hi;
+  }
+  static UNP_DEV A apply(A a, A b) {
+    if constexpr (traits<A>::is_float) return a != a ? b : ((b == b && b < a) ? b : a);
+    else return b < a ? b : a;
+  }
+};
+
+// Bitwise folds of the integers (associative and commutative: every order gives the same bits).
+template <class A> struct fold<A, OP_AND> {
+  static UNP_DEV A identity() { return (A)~(typename traits<A>::uns)0; }
+  static UNP_DEV A apply(A a, A b) { return a & b; }
+};
+template <class A> struct fold<A, OP_OR> {
+  static UNP_DEV A identity() { return A(0); }
+  static UNP_DEV A apply(A a, A b) { return a | b; }
+};
+template <class A> struct fold<A, OP_XOR> {
+  static UNP_DEV A identity() { return A(0); }
+  static UNP_DEV A apply(A a, A b) { return a ^ b; }
+};
+
+// The value stored for a finished fold over `n` elements: an empty fold stores the lift's
+// starting value 0 (kernel_lift.rs:899-906), whatever the fold's identity.
 template <class T, int OP, class A> UNP_DEV T finish(A a, i64 n) {
   if constexpr (OP == OP_MEAN) {
     return (T)(a / (double)n);
-  } else if constexpr (OP == OP_MAX || OP == OP_MIN) {
+  } else if constexpr (OP == OP_MAX || OP == OP_MIN || OP == OP_MAXNUM || OP == OP_MINNUM || OP == OP_AND) {
     return n == 0 ? T(0) : (T)a;
   } else {
     return (T)a;
@@ -636,6 +677,40 @@ UNP_DEV void reduce_generic(const T* __restrict__ in, T* __restrict__ out, const
     }
     a = wave_reduce<Ac, OP>(a);
     if (lane == 0) out[o] = finish<T, OP>(a, d.count);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// A fold whose result depends on its order and has no declared bound (a float Prod: every f64
+// product rounds): the serial lift's order itself (kernel_lift.rs:919-941), one lane per output,
+// the reduced positions ascending in row-major order over the reduced axes into an f64
+// accumulator seeded with 1, one rounding to T at the store.  Bit-exact to the serial lift; not a
+// fast schedule (the dependent multiplies are the critical path).
+// ---------------------------------------------------------------------------------------
+template <class T, int THREADS>
+UNP_DEV void reduce_serial_prod(const T* __restrict__ in, T* __restrict__ out, const axes_desc& d) {
+  const i64 stride = (i64)gridDim.x * THREADS;
+  for (i64 o = (i64)blockIdx.x * THREADS + threadIdx.x; o < d.outs; o += stride) {
+    i64 off = 0, q = o;
+    for (i64 k = d.nk - 1; k >= 0; --k) {
+      const i64 c = q % d.kext[k];
+      q /= d.kext[k];
+      off += c * d.kstr[k];
+    }
+    i64 ctr[8];
+    for (i64 k = 0; k < d.nr; ++k) ctr[k] = 0;
+    double a = 1.0;
+    for (i64 t = 0; t < d.count; ++t) {
+      a = a * (double)in[off];
+      // Advance the odometer over the reduced axes (innermost fastest).
+      for (i64 k = d.nr - 1; k >= 0; --k) {
+        off += d.rstr[k];
+        if (++ctr[k] < d.rext[k]) break;
+        off -= d.rext[k] * d.rstr[k];
+        ctr[k] = 0;
+      }
+    }
+    out[o] = (T)a;
   }
 }
 

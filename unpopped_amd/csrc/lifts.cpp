@@ -44,25 +44,49 @@ const char* reduce_op_name(int32_t op) {
     case UNP_OP_MAX: return "Max";
     case UNP_OP_MIN: return "Min";
     case UNP_OP_MEAN: return "Mean";
+    case UNP_OP_AND: return "And";
+    case UNP_OP_OR: return "Or";
+    case UNP_OP_XOR: return "Xor";
+    case UNP_OP_MAXNUM: return "MaxNum";
+    case UNP_OP_MINNUM: return "MinNum";
     default: return nullptr;
   }
 }
+bool is_bit_op(int32_t op) { return op == UNP_OP_AND || op == UNP_OP_OR || op == UNP_OP_XOR; }
+bool is_num_op(int32_t op) { return op == UNP_OP_MAXNUM || op == UNP_OP_MINNUM; }
 
 // `for counter(d) in 0..extent(d) { inner }` (kernel_lift.rs:1037-1047).
 std::vector<J> for_axis(uint32_t d, uint32_t r, std::vector<J> inner) {
   return {s_for(r + d, int_(0), loc(d), int_(1), std::move(inner))};
 }
 
-// The Max/Min step with the NaN rule (kernel_lift.rs:1097-1160).
+// The Max/Min/MaxNum/MinNum step (kernel_lift.rs:1097-1127): `if !have { acc = v }` else the NaN
+// arm, then `have = 1`.  The NaN arm (nan_arm, :1129-1160): an integer just compares; Max/Min take
+// a NaN element (`v != v`); MaxNum/MinNum replace a NaN accumulator (`acc != acc`) and compare only
+// a non-NaN element (`v == v`).
 std::vector<J> extremum_step(int32_t rop, uint32_t acc, uint32_t have, uint32_t val, bool is_int) {
-  const char* better = rop == UNP_OP_MAX ? "CmpGt" : "CmpLt";
+  const char* better = (rop == UNP_OP_MAX || rop == UNP_OP_MAXNUM) ? "CmpGt" : "CmpLt";
   J keep_going = s_if(e_bin(better, loc(val), loc(acc)), {s_assign(acc, loc(val))}, {});
-  J nan_check = is_int ? keep_going
-                       : s_if(e_bin("CmpNe", loc(val), loc(val)), {s_assign(acc, loc(val))}, {keep_going});
+  J nan_check;
+  if (is_int)
+    nan_check = keep_going;
+  else if (is_num_op(rop))
+    nan_check = s_if(e_bin("CmpNe", loc(acc), loc(acc)), {s_assign(acc, loc(val))},
+                     {s_if(e_bin("CmpEq", loc(val), loc(val)), {keep_going}, {})});
+  else
+    nan_check = s_if(e_bin("CmpNe", loc(val), loc(val)), {s_assign(acc, loc(val))}, {keep_going});
   return {s_if(loc(have), {nan_check}, {s_assign(acc, loc(val))}), s_assign(have, int_(1))};
 }
 
-// The fold step (kernel_lift.rs:1049-1069) for the ops lowered here.
+// The And/Or/Xor step of an integer fold, seeded by the first element (bit_step,
+// kernel_lift.rs:1071-1095): `if have { acc = acc OP v } else { acc = v }`, then `have = 1`.
+std::vector<J> bit_step(int32_t rop, uint32_t acc, uint32_t have, uint32_t val) {
+  const char* op = rop == UNP_OP_AND ? "BitAnd" : rop == UNP_OP_OR ? "BitOr" : "BitXor";
+  return {s_if(loc(have), {s_assign(acc, e_bin(op, loc(acc), loc(val)))}, {s_assign(acc, loc(val))}),
+          s_assign(have, int_(1))};
+}
+
+// The fold step (kernel_lift.rs:1049-1069).
 std::vector<J> fold_step(int32_t rop, uint32_t acc, uint32_t have, uint32_t val, bool is_int) {
   switch (rop) {
     case UNP_OP_SUM:
@@ -70,6 +94,10 @@ std::vector<J> fold_step(int32_t rop, uint32_t acc, uint32_t have, uint32_t val,
       return {s_assign(acc, e_add(loc(acc), loc(val)))};
     case UNP_OP_PROD:
       return {s_assign(acc, e_mul(loc(acc), loc(val)))};
+    case UNP_OP_AND:
+    case UNP_OP_OR:
+    case UNP_OP_XOR:
+      return bit_step(rop, acc, have, val);
     default:
       return extremum_step(rop, acc, have, val, is_int);
   }
@@ -164,9 +192,14 @@ struct Shape {
   }
 };
 
-// check_accumulated_dtype (kernel_lift.rs:763-803) for the ops lifted here.
+// check_accumulated_dtype (kernel_lift.rs:763-803) for the ops lifted here: a bit or NaN-ignoring
+// fold only in a plain reduction, a bit fold only at an integer dtype.
 void check_accumulated(int32_t dtype, int32_t rop, const char* what) {
-  if (!reduce_op_name(rop)) throw Decline{"UnsupportedForm: a reduce op outside Sum, Prod, Max, Min and Mean"};
+  if (!reduce_op_name(rop)) throw Decline{"UnsupportedForm: a reduce op this restatement does not name"};
+  if (((is_bit_op(rop) || is_num_op(rop)) && std::strcmp(what, "a reduction") != 0) ||
+      (is_bit_op(rop) && !is_int_kernel_dtype(dtype)))
+    throw Decline{"UnsupportedForm: a bit or NaN-ignoring reduction outside a plain reduction, or a bit reduction "
+                  "at a float dtype"};
   if (dtype == UNP_F32 || dtype == UNP_F64) return;
   if (!is_int_kernel_dtype(dtype))
     throw Decline{std::string("UnsupportedForm: ") + what + " outside F32, F64, I32 and I64"};
@@ -211,6 +244,9 @@ J lift_reduction(const std::string& name, int32_t dtype, int32_t rank, int32_t r
   }
   if (grid == 0 || !pow2(block)) throw Decline{"BadLaunch"};
   // check_order_independent (block_reduce.rs:97-133)
+  if (is_bit_op(rop) || is_num_op(rop))
+    throw Decline{"UnsupportedForm: a bit or NaN-ignoring reduction in a launched reduction (the sequential lift "
+                  "only)"};
   if ((rop == UNP_OP_PROD && !sh.is_int()) || (rop == UNP_OP_MEAN && sh.is_int()))
     throw Decline{"UnsupportedForm: an integer Mean or a float Prod in a launched reduction"};
   const bool flag = rop == UNP_OP_MAX || rop == UNP_OP_MIN;
@@ -497,6 +533,8 @@ J lift_gather(const std::string& name, int32_t dtype, int32_t rank, int32_t idx,
 J row_reduce2(const std::string& name, int32_t dtype, int32_t op0, int32_t op1, uint32_t block, uint32_t grid) {
   check_accumulated(dtype, op0, "a reduction");
   check_accumulated(dtype, op1, "a reduction");
+  if (op0 > UNP_OP_MEAN || op1 > UNP_OP_MEAN)
+    throw Decline{"UnsupportedForm: the fused row fold takes Sum, Prod, Max, Min and Mean"};
   const Shape sh(dtype, 2, 0);
   const uint32_t x = 4, a0 = 5, h0 = 6, a1 = 7, h1 = 8, v = 9;
   auto stored = [&](int32_t op, uint32_t acc) {
@@ -1156,7 +1194,8 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
         }
       }
     }
-    static const int32_t ops[] = {UNP_OP_SUM, UNP_OP_PROD, UNP_OP_MAX, UNP_OP_MIN, UNP_OP_MEAN};
+    static const int32_t ops[] = {UNP_OP_SUM,    UNP_OP_PROD, UNP_OP_MAX, UNP_OP_MIN, UNP_OP_MEAN,
+                                  UNP_OP_MAXNUM, UNP_OP_MINNUM, UNP_OP_AND, UNP_OP_OR, UNP_OP_XOR};
     // Every reduced-axis set whose output rank matches (ReductionShape::new,
     // kernel_lift.rs:854-870), trailing runs first: the reduction most often asked for.
     std::vector<uint32_t> masks;

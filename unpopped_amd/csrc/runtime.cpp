@@ -641,7 +641,7 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
   const int vec = 16 / (int)unp::kind_bytes(f.dtype);
   const char sched = x->l.red_schedule;
   const uint32_t mask = x->l.axes_mask;
-  if (sched == 'm' || sched == 'g') {
+  if (sched == 'm' || sched == 'g' || sched == 'q') {
     // Output elements and reduced positions per output.
     long long outs = 1, count = 1;
     for (int32_t d = 0; d < f.rank; ++d) ((mask >> d) & 1u ? count : outs) *= A.ext[(size_t)d];
@@ -684,13 +684,13 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
       void* params[] = {&in, &out, &a, &r, &b, &S, &ws, &cnt};
       return launch(x, entry, (uint32_t)grid, params, s, err);
     }
-    // Any other mask.
+    // Any other mask (a wave per output), or the serial product (a lane per output).
     unp::axes_desc_host d{};
     fill_axes_desc(A.ext, f.rank, mask, d);
     d.outs = outs;
     d.count = count;
     const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
-    const long long want = (outs + 3) / 4;
+    const long long want = sched == 'q' ? (outs + 255) / 256 : (outs + 3) / 4;
     const uint32_t grid = (uint32_t)(want < cap ? want : cap);
     void* params[] = {&in, &out, &d};
     return launch(x, 0, grid, params, s, err);

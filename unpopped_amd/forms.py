@@ -15,6 +15,7 @@ _execs: dict = {}
 # The KernelFn a caller hands the backend: the reference's launched lift at a caller-chosen
 # geometry (the backend substitutes its own device-class launch and says so in the interface).
 CALLER_LAUNCH = (256, 64)
+SEQUENTIAL_ONLY = ("And", "Or", "Xor", "MaxNum", "MinNum")
 
 
 def kernel_for(kind: str, dtype: str = "F32", rank: int = 1, op: str = "Sum", op1: str = "Max",
@@ -25,7 +26,11 @@ def kernel_for(kind: str, dtype: str = "F32", rank: int = 1, op: str = "Sum", op
     if kind == "reduction":
         k = rank - 1 if reduced_from is None else reduced_from
         ax = tuple(range(k, rank)) if axes is None else tuple(axes)
-        return u.lift_reduction("reduce", dtype, rank, op, axes=ax, keepdim=keepdim, launch=CALLER_LAUNCH)
+        # The bit and NaN-ignoring folds, and a float Prod, lift only sequentially
+        # (kernel_lift/block_reduce.rs:97-133).
+        serial = op in SEQUENTIAL_ONLY or (op == "Prod" and dtype in ("F32", "F64"))
+        launch = None if serial else CALLER_LAUNCH
+        return u.lift_reduction("reduce", dtype, rank, op, axes=ax, keepdim=keepdim, launch=launch)
     if kind == "row_reduce2":
         return u.kernel_row_reduce2("row_fold", dtype, op, op1, launch=CALLER_LAUNCH)
     if kind == "scan":
