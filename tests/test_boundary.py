@@ -237,8 +237,13 @@ def test_lower_kernel_refuses_anything_else():
     with pytest.raises(_lib.UnpError) as e:
         u.lift_reduction("r", "F32", 2, "Prod", launch=(256, 64))
     assert e.value.kind == "LiftDecline" and "float Prod" in e.value.detail
-    # a scan along a non-innermost axis
-    refused(u.lift_scan("s", "F32", 2, "Sum", axis=0))
+    # a scan along a non-innermost axis: the serial lift, lowered to the serial-order scan; the
+    # launched lift declines it (kernel_lift.rs:689-695)
+    g = b.lower_kernel(u.lift_scan("s", "F32", 2, "Sum", axis=0))
+    assert g.interface["schedule"] == "serial" and g.interface["axis"] == 0
+    with pytest.raises(_lib.UnpError) as e:
+        u.lift_scan("s", "F32", 2, "Sum", axis=0, launch=(256, 64))
+    assert "non-innermost" in e.value.detail
     # a pre-map body (x * x) is the lift of OpDef::reduction with that body: recognised, and
     # spelled into the kernel (kernel_lift.rs:919-941)
     sq = json.dumps(u.lift_reduction("r", "F64", 1, "Sum")).replace(
@@ -258,7 +263,7 @@ def test_lower_form_declines_unsupported_forms():
     for form, kind in [
         (dict(kind="reduction", dtype="F32", op="And", rank=1, reduced_from=0), "UnsupportedKernel"),
         (dict(kind="reduction", dtype="I32", op="Mean", rank=1, reduced_from=0), "UnsupportedKernel"),
-        (dict(kind="scan", dtype="F32", op="Mean"), "UnsupportedKernel"),
+        (dict(kind="scan", dtype="I32", op="Mean"), "UnsupportedKernel"),
         (dict(kind="gather", dtype="U4", rank=2), "UnsupportedDtype"),
         (dict(kind="dequant4", out_kind="F32"), "UnsupportedDtype"),
         (dict(kind="dequant4", group=0), "UnsupportedKernel"),
@@ -430,3 +435,19 @@ def test_bit_and_nan_ignoring_folds_lift_only_sequentially():
         with pytest.raises(_lib.UnpError) as e:
             u.lift_reduction("r", "F32", 2, op)
         assert "bit reduction at a float dtype" in e.value.detail
+
+
+def test_mean_and_float_prod_scans_lift_only_sequentially():
+    """A Mean scan and a float Prod scan have serial lifts only (kernel_lift/scan_launched.rs:66-75):
+    the serial lift is lowered (Mean on the look-back scan with the division at the store, a float
+    Prod in the serial order), the launched lift declines, and an integer Mean declines."""
+    b = u.HipBackend()
+    assert b.lower_kernel(u.lift_scan("s", "F32", 1, "Mean")).name.startswith("unp_scan_incl_mean_f32")
+    assert b.lower_kernel(u.lift_scan("s", "F64", 1, "Prod", exclusive=True)).name.startswith("unp_scan_seq_excl_prod")
+    for op in ("Mean", "Prod"):
+        with pytest.raises(_lib.UnpError) as e:
+            u.lift_scan("s", "F32", 1, op, launch=(256, 64))
+        assert e.value.kind == "LiftDecline"
+    with pytest.raises(_lib.UnpError) as e:
+        u.lift_scan("s", "I32", 1, "Mean")
+    assert "integer Mean" in e.value.detail

@@ -410,3 +410,21 @@ def test_sequential_only_folds_equal_the_oracle(dtype, op):
     out = np.zeros(8, NP[dtype])
     assert cpuc.run(k, x, out, 8, 29) == cpuc.OK
     assert np.array_equal(out, oracle.reduce_rows(x, op), equal_nan=dtype[0] == "F"), (dtype, op)
+
+
+@pytest.mark.parametrize("dtype", ["F32", "F64", "I64"])
+@pytest.mark.parametrize("axis", [0, 1, 2])
+def test_scans_along_any_axis_equal_the_oracle(dtype, axis):
+    """The serial scan lift along each axis of a rank-3 input (lift_scan_opdef, kernel_lift.rs:504-519):
+    the oracle scans the same elements with that axis moved last."""
+    x = data(dtype, (3, 4, 5))
+    ops = ("Sum", "Max", "Min", "Prod") + (("Mean",) if dtype[0] == "F" else ())
+    for op in ops:
+        for exclusive, reverse in ((False, False), (True, True)):
+            k = u.lift_scan("sa", dtype, 3, op, axis=axis, exclusive=exclusive, reverse=reverse)
+            out = np.zeros_like(x)
+            assert cpuc.run(k, x, out, 3, 4, 5) == cpuc.OK
+            xm = np.ascontiguousarray(np.moveaxis(x, axis, -1))
+            want = np.moveaxis(oracle.scan_rows(xm.reshape(-1, xm.shape[-1]), op, exclusive, reverse).reshape(xm.shape),
+                               -1, axis)
+            assert out.tobytes() == np.ascontiguousarray(want).tobytes(), (op, exclusive, reverse)

@@ -299,6 +299,67 @@ def test_scan_eight_byte_staged(hip_device, op):
         assert np.array_equal(H.scan_rows(xf, op, excl, rev), oracle.scan_rows(xf, op, excl, rev)), (excl, rev)
 
 
+SCAN_AXES_CASES = [((64, 300), 0), ((3, 1000, 5), 1), ((5, 7, 300), 0), ((2, 3, 4, 5), 2), ((1000, 2), 0),
+                   ((1, 4096, 64), 1), ((3, 0, 4), 1), ((6, 5), 1)]
+
+
+@pytest.mark.parametrize("shape,axis", SCAN_AXES_CASES)
+@pytest.mark.parametrize("dtype", [np.float32, np.float64, np.int32, np.int64])
+def test_scan_any_axis_bit_exact(hip_device, shape, axis, dtype):
+    """The serial scan lift along any axis (lift_scan_opdef, kernel_lift.rs:504-519): a non-innermost
+    axis, and a float Prod on any axis, run in the serial lift's own order and are bit-exact for every
+    op, float Sum and Mean included; the innermost axis of the other folds takes the look-back scan."""
+    is_int = dtype in (np.int32, np.int64)
+    r = rng(48)
+    if is_int:
+        x = r.integers(-1000, 1000, size=shape, dtype=dtype)
+    else:
+        x = r.normal(size=shape).astype(dtype)
+    inner = axis == len(shape) - 1
+    for op in ("Sum", "Max", "Min", "Prod") + (() if is_int else ("Mean",)):
+        for exclusive, reverse in ((False, False), (True, False), (False, True)):
+            H.say(f"[case] scan axis {axis} of {shape} {np.dtype(dtype).name} {op} excl={exclusive} rev={reverse}")
+            xs = (np.abs(x) * 0.5 + 0.75).astype(dtype) if op == "Prod" and not is_int else x
+            got = H.scan_axis(xs, axis, op, exclusive, reverse)
+            xm = np.ascontiguousarray(np.moveaxis(xs, axis, -1))
+            rows = xm.reshape(-1, xm.shape[-1]) if xm.size else xm.reshape(0, max(xm.shape[-1], 0))
+            want = np.moveaxis(oracle.scan_rows(rows, op, exclusive, reverse).reshape(xm.shape), -1, axis)
+            if inner and not is_int and op in ("Sum", "Mean"):
+                # the look-back scan: every prefix within the declared bound
+                cols = xm.shape[-1]
+                g2 = np.moveaxis(got, axis, -1).reshape(-1, cols).astype(np.float64)
+                w2 = rows.astype(np.float64)
+                for i in range(g2.shape[0]):
+                    pre = np.cumsum(np.abs(w2[i][::-1] if reverse else w2[i]))
+                    if exclusive:
+                        pre = np.concatenate([[0.0], pre[:-1]])
+                    n = np.arange(1, cols + 1, dtype=np.float64)
+                    cnt = (n - 1 if exclusive else n) if op == "Mean" else np.ones(cols)
+                    g = g2[i][::-1] if reverse else g2[i]
+                    wv = np.moveaxis(want, axis, -1).reshape(-1, cols)[i].astype(np.float64)
+                    wv = wv[::-1] if reverse else wv
+                    tol = (2 * n * 2.0**-53 * pre) / np.maximum(cnt, 1) + np.spacing(np.abs(wv).astype(dtype))
+                    ok = np.isnan(wv) | (np.abs(g - wv) <= tol)
+                    assert ok.all(), (op, i)
+            else:
+                assert np.array_equal(got, want, equal_nan=True), op
+
+
+def test_mean_scan_dyadic_is_bit_exact(hip_device):
+    """A Mean scan on the innermost axis (the look-back scan, divided at the store): on dyadic data
+    every f64 prefix is exact, so each output is the oracle's (prefix / count) rounded, bit for bit;
+    an exclusive scan's first output is 0 / 0."""
+    for n in (1, 4096, 50000, (1 << 20) + 3):
+        x = dyadic(49, (n,), np.float32)
+        for exclusive in (False, True):
+            H.say(f"[case] mean scan n={n} excl={exclusive}")
+            got = H.scan_rows(x, "Mean", exclusive)
+            want = oracle.scan_rows(x.reshape(1, -1), "Mean", exclusive).ravel()
+            assert np.array_equal(got, want, equal_nan=True)
+            if exclusive:
+                assert np.isnan(got[0])
+
+
 def test_scan_unaligned_takes_the_register_path(hip_device):
     """A row whose extent is not a multiple of 16 bytes runs the register entry at size."""
     H.say("[case] scan i32 unaligned (1, 1000003)")

@@ -383,19 +383,68 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     why = "a scan outside F32, F64, I32 and I64";
     return UNP_UNSUPPORTED_KERNEL;
   }
-  if (f.op0 != UNP_OP_SUM && f.op0 != UNP_OP_MAX && f.op0 != UNP_OP_MIN && f.op0 != UNP_OP_PROD) {
-    why = "a Mean scan in a launched scan (a running mean has no declared bound)";
+  if (f.op0 != UNP_OP_SUM && f.op0 != UNP_OP_MAX && f.op0 != UNP_OP_MIN && f.op0 != UNP_OP_PROD &&
+      f.op0 != UNP_OP_MEAN) {
+    why = "a scan folds Sum, Prod, Max, Min or Mean";
     return UNP_UNSUPPORTED_KERNEL;
   }
-  if (f.op0 == UNP_OP_PROD && kind_is_float(f.dtype)) {
-    why = "a float Prod scan in a launched scan (not order-independent, and no declared bound)";
+  if (f.op0 == UNP_OP_MEAN && !kind_is_float(f.dtype)) {
+    why = "an integer Mean";
     return UNP_UNSUPPORTED_KERNEL;
   }
+  // The scanned axis: axes_mask's one bit, or the innermost axis.
+  int32_t axis = f.rank - 1;
+  if (f.axes_mask) {
+    if ((f.axes_mask & (f.axes_mask - 1)) != 0 || (f.axes_mask >> f.rank) != 0) {
+      why = "a scan scans exactly one axis inside the rank";
+      return UNP_LIFT_DECLINE;
+    }
+    axis = __builtin_ctz(f.axes_mask);
+  }
+  // A non-innermost axis, or a float Prod (every product rounds, no declared bound), runs in the
+  // serial lift's own order.
+  const bool serial = axis != f.rank - 1 || (f.op0 == UNP_OP_PROD && kind_is_float(f.dtype));
+  L.serial_scan = serial;
+  L.scan_axis = axis;
   const char* T = ctype(f.dtype);
   std::ostringstream name;
-  name << "unp_scan_" << (f.exclusive ? "excl_" : "incl_") << (f.reverse ? "rev_" : "") << op_name(f.op0)
-       << "_" << lower_name(f.dtype);
+  name << "unp_scan_" << (serial ? "seq_" : "") << (f.exclusive ? "excl_" : "incl_") << (f.reverse ? "rev_" : "")
+       << op_name(f.op0) << "_" << lower_name(f.dtype);
   L.name = name.str();
+  if (serial) {
+    Entry e;
+    e.fast = false;
+    e.vec = 1;
+    e.threads = 256;
+    e.blocks_per_cu = 8;
+    e.symbol = L.name + "_q";
+    std::ostringstream src;
+    src << header(L.name, f);
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(const " << T << "* in, " << T
+        << "* out, long long A, long long S, long long B) {\n  unp::scan_seq<" << T << ", " << f.op0 << ", "
+        << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false") << ", 8>(in, out, A, S, B);\n}\n";
+    L.entries.push_back(e);
+    L.threads = 256;
+    L.blocks_per_cu = 8;
+    L.source = src.str();
+    std::ostringstream j;
+    j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"scan\",\"dtype\":\"" << kind_name(f.dtype)
+      << "\",\"op\":\"" << op_name(f.op0) << "\",\"exclusive\":" << (f.exclusive ? "true" : "false")
+      << ",\"reverse\":" << (f.reverse ? "true" : "false") << ",\"rank\":" << f.rank << ",\"axis\":" << axis
+      << ",\"schedule\":\"serial\",\"params\":[{\"name\":\"in0\",\"kind\":\"buffer\",\"role\":\"Read\"},"
+      << "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
+    for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
+    j << "],\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*8\",\"grid_policy\":\"device-class constant; one "
+      << "lane per column of the input seen as A x S x B around the scanned axis, lanes stride over columns\"},"
+      << "\"entries\":[{\"symbol\":\"" << e.symbol << "\",\"when\":\"always\"}],\"workspace\":null"
+      << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
+      << ",\"fidelity_notes\":[" << json_str("the serial lift's own order: each column's prefix folds ascending (descending "
+                                             "for a reverse scan) in the serial accumulator and rounds once per output; "
+                                             "bit-exact against the serial scan")
+      << "]}";
+    L.interface_json = j.str();
+    return UNP_OK;
+  }
   // Two schedules, one ticket per block tile per round:
   //  _v  rows of a multiple of 16 bytes, 16-byte aligned: the LDS-staged scan, one producer
   //      wave streaming the next tile into LDS by DMA plus NC consumer waves, one block per
@@ -462,10 +511,10 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     << " bytes, zeroed once\",\"counter\":4,\"host_state\":[\"epoch\",\"ticket_base\"]}"
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["
-    << json_str(kind_is_float(f.dtype) && f.op0 == UNP_OP_SUM
-                    ? "float Sum: every prefix is an f64 fold of the same elements in a different order (tile-local "
-                      "striped scan plus decoupled look-back); within the declared per-prefix bound "
-                      "gamma_(n-1)*sum|x| + 1/2 ulp; bit-equal whenever the f64 partial sums are exact"
+    << json_str(kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN)
+                    ? "float Sum / Mean: every prefix is an f64 fold of the same elements in a different order (tile-local "
+                      "striped scan plus decoupled look-back; a Mean divides it by the count once); within the declared "
+                      "per-prefix bound gamma_(n-1)*sum|x| + 1/2 ulp; bit-equal whenever the f64 partial sums are exact"
                     : "order-independent fold: bit-exact against the serial scan except NaN payload and the sign of a zero in Max/Min")
     << "," << json_str("one single-pass decoupled look-back launch replaces the KernelFn's block-per-row three-phase schedule")
     << "]}";

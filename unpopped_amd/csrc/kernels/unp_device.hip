@@ -856,6 +856,68 @@ UNP_DEV void xreduce_generic(const T* const* __restrict__ in, T* __restrict__ ou
   }
 }
 
+// A scan's stored prefix: the fold rounded once to T, or for a running Mean the f64 sum divided by
+// the count folded so far (scan_stored, kernel_lift.rs:604-619; an exclusive first prefix is 0 / 0).
+template <class T, int OP, class A> UNP_DEV T scan_out(A v, i64 count) {
+  if constexpr (OP == OP_MEAN) return (T)(v / (double)count);
+  else return (T)v;
+}
+
+// The serial scan lift's accumulator: f64 for every float op (kernel_lift.rs:883-896), the dtype
+// itself for an integer.
+template <class T> struct serial_acc { typedef T type; };
+template <> struct serial_acc<float> { typedef double type; };
+
+// ---------------------------------------------------------------------------------------
+// A scan in the serial lift's own order (lift_scan_opdef, kernel_lift.rs:504-700): along a
+// non-innermost axis of A x S x B, or a float Prod (every product rounds; no declared bound).
+// One lane per column (a, b), lanes of a wave on consecutive b so that a wave's loads and stores
+// of one step are contiguous; the scanned axis walked ascending (descending for a reverse scan),
+// the prefix folded in the serial accumulator, a Mean divided by the count so far, each prefix
+// rounded once at its store.  Bit-exact to the serial lift for every op and dtype.  U loads of a
+// column are issued before its U stores, so one wait covers them.
+// ---------------------------------------------------------------------------------------
+template <class T, int OP, bool EXCL, bool REV, int U>
+UNP_DEV void scan_seq(const T* __restrict__ in, T* __restrict__ out, i64 A, i64 S, i64 B) {
+  typedef typename serial_acc<T>::type Ac;
+  typedef fold<Ac, OP> F;
+  const i64 cols = A * B;
+  const i64 stride = (i64)gridDim.x * blockDim.x;
+  for (i64 c = (i64)blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += stride) {
+    const i64 a = c / B, b = c - a * B;
+    const i64 base = a * S * B + b;
+    Ac v = F::identity();
+    i64 i = 0;
+    for (; i + U <= S; i += U) {
+      T x[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) x[u] = in[base + (REV ? S - 1 - (i + u) : i + u) * B];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const i64 off = base + (REV ? S - 1 - (i + u) : i + u) * B;
+        if constexpr (EXCL) {
+          out[off] = scan_out<T, OP>(v, i + u);
+          v = F::apply(v, (Ac)x[u]);
+        } else {
+          v = F::apply(v, (Ac)x[u]);
+          out[off] = scan_out<T, OP>(v, i + u + 1);
+        }
+      }
+    }
+    for (; i < S; ++i) {
+      const i64 off = base + (REV ? S - 1 - i : i) * B;
+      const T xv = in[off];
+      if constexpr (EXCL) {
+        out[off] = scan_out<T, OP>(v, i);
+        v = F::apply(v, (Ac)xv);
+      } else {
+        v = F::apply(v, (Ac)xv);
+        out[off] = scan_out<T, OP>(v, i + 1);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Single-pass scan with decoupled look-back, along the innermost axis of rows x cols.
 //
@@ -1064,17 +1126,17 @@ UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 ro
     for (int k = 0; k < K; ++k) {
       A v = F::apply(base, pre[k]);
       vec<T, VEC> o;
+      const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;  // scan-order index of element 0
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         if constexpr (EXCL) {
-          o.e[e] = (T)v;
+          o.e[e] = scan_out<T, OP>(v, pos + e);
           v = F::apply(v, (A)x[k].e[e]);
         } else {
           v = F::apply(v, (A)x[k].e[e]);
-          o.e[e] = (T)v;
+          o.e[e] = scan_out<T, OP>(v, pos + e + 1);
         }
       }
-      const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
       if (full || pos + VEC <= cols) {
         if constexpr (REV) {
           vec<T, VEC> v2;
@@ -1297,17 +1359,17 @@ UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows
     for (int k = 0; k < K; ++k) {
       A v = F::apply(base, pre[k]);
       vec<T, VEC> o;
+      const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;  // scan-order index of element 0
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         if constexpr (EXCL) {
-          o.e[e] = (T)v;
+          o.e[e] = scan_out<T, OP>(v, pos + e);
           v = F::apply(v, (A)x[k].e[e]);
         } else {
           v = F::apply(v, (A)x[k].e[e]);
-          o.e[e] = (T)v;
+          o.e[e] = scan_out<T, OP>(v, pos + e + 1);
         }
       }
-      const i64 pos = p0 + ((i64)k * 64 + lane) * VEC;
       if (full || pos + VEC <= cols) {
         if constexpr (REV) {
           vec<T, VEC> v2;

@@ -1229,18 +1229,23 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
         }
       }
       if (orank == r && n == 1) {
-        for (int ex = 0; ex <= 1; ++ex)
-          for (int rev = 0; rev <= 1; ++rev)
-            if (attempt([&] { return lift_scan(name, dt, r, op, r - 1, ex, rev, block, grid); })) {
-              out.form.kind = UNP_FORM_SCAN;
-              out.form.dtype = dt;
-              out.form.rank = r;
-              out.form.op0 = op;
-              out.form.exclusive = ex;
-              out.form.reverse = rev;
-              out.lift = block ? "lift_scan_opdef_launched" : "lift_scan_opdef";
-              return UNP_OK;
-            }
+        // The innermost axis first (the only one a launched scan takes), then the others.
+        for (int32_t ai = 0; ai < r; ++ai) {
+          const int32_t axis = ai == 0 ? r - 1 : ai - 1;
+          for (int ex = 0; ex <= 1; ++ex)
+            for (int rev = 0; rev <= 1; ++rev)
+              if (attempt([&] { return lift_scan(name, dt, r, op, axis, ex, rev, block, grid); })) {
+                out.form.kind = UNP_FORM_SCAN;
+                out.form.dtype = dt;
+                out.form.rank = r;
+                out.form.op0 = op;
+                out.form.exclusive = ex;
+                out.form.reverse = rev;
+                out.form.axes_mask = axis == r - 1 ? 0u : (1u << axis);
+                out.lift = block ? "lift_scan_opdef_launched" : "lift_scan_opdef";
+                return UNP_OK;
+              }
+        }
       }
     }
   }

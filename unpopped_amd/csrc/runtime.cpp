@@ -723,6 +723,18 @@ int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_err
   int32_t rc = take_args(a, n, 2, (size_t)f.rank, A, err);
   if (rc == UNP_OK) rc = extents_i32(A, (size_t)f.rank, err);
   if (rc != UNP_OK) return rc;
+  if (x->l.serial_scan) {
+    // The input as A x S x B around the scanned axis; one lane per column.
+    const size_t ax = (size_t)x->l.scan_axis;
+    long long a0 = product(A.ext, 0, ax), S = A.ext[ax], b0 = product(A.ext, ax + 1, (size_t)f.rank);
+    if ((rc = need_buffers(A, a0 > 0 && S > 0 && b0 > 0, err)) != UNP_OK) return rc;
+    if (a0 == 0 || S == 0 || b0 == 0) return UNP_OK;
+    uint64_t in = A.buf[0], out = A.buf[1];
+    const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
+    const long long want = (a0 * b0 + 255) / 256;
+    void* params[] = {&in, &out, &a0, &S, &b0};
+    return launch(x, 0, (uint32_t)(want < cap ? want : cap), params, s, err);
+  }
   long long rows = product(A.ext, 0, (size_t)f.rank - 1);
   long long cols = A.ext[(size_t)f.rank - 1];
   if ((rc = need_buffers(A, rows > 0 && cols > 0, err)) != UNP_OK) return rc;

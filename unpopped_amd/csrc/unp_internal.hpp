@@ -90,6 +90,10 @@ struct Lowered {
   uint32_t axes_mask = 0;  // the reduced axes, bit d = axis d
   int threads = 256;
   int blocks_per_cu = 8;
+  // A scan in the serial lift's own order (a non-innermost axis, or a float Prod): the scanned
+  // axis, and the input seen as A x S x B around it.
+  bool serial_scan = false;
+  int32_t scan_axis = 0;
   RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only
   ReductionExpr rx;  // UNP_FORM_REDUCTION: the body and post
 };

@@ -21,7 +21,8 @@ SEQUENTIAL_ONLY = ("And", "Or", "Xor", "MaxNum", "MinNum")
 def kernel_for(kind: str, dtype: str = "F32", rank: int = 1, op: str = "Sum", op1: str = "Max",
                reduced_from: int | None = None, exclusive: bool = False, reverse: bool = False,
                index_dtype: str = "I32", oob: str = "ZeroFill", q_kind: str = "U4", z_kind: str = "U4",
-               group: int = 128, axes: tuple | None = None, keepdim: bool = False, **_ignored) -> dict:
+               group: int = 128, axes: tuple | None = None, keepdim: bool = False, axis: int | None = None,
+               **_ignored) -> dict:
     """The KernelFn (as its serde JSON dict) of the lift or authored kernel for a form."""
     if kind == "reduction":
         k = rank - 1 if reduced_from is None else reduced_from
@@ -34,7 +35,12 @@ def kernel_for(kind: str, dtype: str = "F32", rank: int = 1, op: str = "Sum", op
     if kind == "row_reduce2":
         return u.kernel_row_reduce2("row_fold", dtype, op, op1, launch=CALLER_LAUNCH)
     if kind == "scan":
-        return u.lift_scan("scan", dtype, rank, op, exclusive=exclusive, reverse=reverse, launch=CALLER_LAUNCH)
+        # A scan along a non-innermost axis, a Mean scan and a float Prod scan lift only sequentially
+        # (kernel_lift.rs:689-695, kernel_lift/scan_launched.rs:66-75).
+        ax = rank - 1 if axis is None else axis
+        serial = ax != rank - 1 or op == "Mean" or (op == "Prod" and dtype in ("F32", "F64"))
+        return u.lift_scan("scan", dtype, rank, op, axis=ax, exclusive=exclusive, reverse=reverse,
+                           launch=None if serial else CALLER_LAUNCH)
     if kind == "gather":
         return u.lift_gather("gather", dtype, rank, index_dtype, 0, oob, launch=CALLER_LAUNCH)
     if kind == "dequant4":
@@ -146,6 +152,17 @@ def scan_rows(x: np.ndarray, op: str, exclusive=False, reverse=False) -> np.ndar
     ex.launch(din, dout, rows, cols)
     u.synchronize()
     return dout.download(x.dtype, rows * cols).reshape(x.shape)
+
+
+def scan_axis(x: np.ndarray, axis: int, op: str, exclusive=False, reverse=False) -> np.ndarray:
+    """Scan ``x`` (any rank) along ``axis`` with the lift of that axis."""
+    ex = executor(kind="scan", dtype=NP_KIND[x.dtype.type], rank=x.ndim, op=op, exclusive=exclusive,
+                  reverse=reverse, axis=axis)
+    din = u.DeviceBuffer.from_array(np.ascontiguousarray(x))
+    dout = u.DeviceBuffer(max(x.nbytes, 1))
+    ex.launch(din, dout, *x.shape)
+    u.synchronize()
+    return dout.download(x.dtype, x.size).reshape(x.shape)
 
 
 def gather_rows(table: np.ndarray, ids: np.ndarray, oob: str, out_init: np.ndarray | None = None,
