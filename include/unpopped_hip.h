@@ -142,7 +142,8 @@ typedef struct unp_form {
   int32_t out_kind;    /* dequant: Bf16 */
   uint32_t axes_mask;  /* reduction: the reduced axes, bit d = axis d (ReductionShape::new,
                           kernel_lift.rs:854-870); 0 means axes reduced_from..rank-1.
-                          scan: the scanned axis as its one bit; 0 means the innermost axis */
+                          scan: the scanned axis as its one bit; 0 means the innermost axis.
+                          gather: the gathered axis as its one bit; 0 means axis 0 */
 } unp_form;
 
 /* Lower one form to HIP source (the work Backend::lower_kernel does once it has recognised

@@ -169,6 +169,24 @@ def gather_rows(table: np.ndarray, ids: np.ndarray, policy: str, out_init: np.nd
     return out
 
 
+def gather_axis(table: np.ndarray, ids: np.ndarray, axis: int, policy: str,
+                out_init: np.ndarray | None = None) -> np.ndarray:
+    """index_select along ``axis`` with a 1-D index (the gather lift's cell, kernel_lift/gather.rs:184-232,
+    at every coordinate of the other axes): the table seen as A x V x B, each of the A slices a row
+    gather of B-element rows."""
+    table = np.ascontiguousarray(table)
+    V = table.shape[axis]
+    A = int(np.prod(table.shape[:axis], dtype=np.int64))
+    B = int(np.prod(table.shape[axis + 1:], dtype=np.int64))
+    out_shape = table.shape[:axis] + (ids.shape[0],) + table.shape[axis + 1:]
+    out = (np.zeros(out_shape, table.dtype) if out_init is None else np.array(out_init, copy=True)).reshape(
+        A, ids.shape[0], B)
+    t3 = table.reshape(A, V, B)
+    for a in range(A):
+        out[a] = gather_rows(t3[a], ids, policy, out_init=out[a], src_extent=V)
+    return out.reshape(out_shape)
+
+
 # ---- dequant --------------------------------------------------------------------------
 
 def dequant4_bf16(q_packed: np.ndarray, scales_f16_bits: np.ndarray, zeros_packed: np.ndarray, rows: int,

@@ -229,8 +229,8 @@ def test_lower_kernel_refuses_anything_else():
     # not JSON, not a KernelFn
     refused("{not json", "ParseError")
     refused(json.dumps([1, 2, 3]), "ParseError")
-    # a gather along axis 1 is recognised and refused by name
-    assert "axis 1" in refused(u.lift_gather("g", "F32", 2, axis=1))
+    # a gather along axis 1 (index_select) is recognised and lowered to the batched row gather
+    assert b.lower_kernel(u.lift_gather("g", "F32", 2, axis=1)).interface["axis"] == 1
     # a float Prod: the serial lift is lowered to the entry that multiplies in the serial order; the
     # launched lift declines it (block_reduce.rs:97-133)
     assert b.lower_kernel(u.lift_reduction("r", "F32", 2, "Prod")).name.startswith("unp_reduce_serial_prod_f32")

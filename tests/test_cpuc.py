@@ -428,3 +428,19 @@ def test_scans_along_any_axis_equal_the_oracle(dtype, axis):
             want = np.moveaxis(oracle.scan_rows(xm.reshape(-1, xm.shape[-1]), op, exclusive, reverse).reshape(xm.shape),
                                -1, axis)
             assert out.tobytes() == np.ascontiguousarray(want).tobytes(), (op, exclusive, reverse)
+
+
+@pytest.mark.parametrize("axis", [0, 1, 2])
+@pytest.mark.parametrize("oob", ["Skip", "ZeroFill", "Clamp"])
+def test_gather_along_any_axis_equals_the_oracle(axis, oob):
+    t = RNG.integers(0, 2**16, (3, 8, 5), dtype=np.uint16)
+    V = t.shape[axis]
+    ids = RNG.integers(-2, V + 2, 6).astype(np.int32)
+    osh = t.shape[:axis] + (6,) + t.shape[axis + 1:]
+    strides = tuple(1 if d == axis else 0 for d in range(3))
+    init = RNG.integers(0, 2**16, osh, dtype=np.uint16)
+    for launch in (None, (32, 2)):
+        out = init.copy()
+        k = u.lift_gather("ga", "Bf16", 3, "I32", axis, oob, launch=launch)
+        assert cpuc.run(k, t, View(ids, osh, strides), out, *osh, V) == cpuc.OK
+        assert np.array_equal(out, oracle.gather_axis(t, ids, axis, oob, out_init=init)), launch

@@ -429,6 +429,27 @@ def test_gather_many_rows_whole_row_path(hip_device, oob):
     assert np.array_equal(got, oracle.gather_rows(table, ids, oob, out_init=init))
 
 
+@pytest.mark.parametrize("shape,axis", [((4, 300, 16), 1), ((3, 5, 4096), 1), ((8, 100), 1), ((2, 3, 50, 7), 2),
+                                        ((64, 1000), 0), ((5, 9, 2048), 1), ((3, 40, 1), 1)])
+@pytest.mark.parametrize("oob", ["Skip", "ZeroFill", "Clamp"])
+@pytest.mark.parametrize("idx", [np.int32, np.int64, np.uint32])
+def test_gather_along_any_axis(hip_device, shape, axis, oob, idx):
+    """index_select along any axis (OpDef::gather with a 1-D index, ir.rs:3838-3876; the gather lift's
+    cell, gather.rs:184-232): bit-exact against the oracle, out-of-range ids under each policy."""
+    H.say(f"[case] gather axis {axis} of {shape} {oob} {np.dtype(idx).name}")
+    r = rng(50)
+    t = r.integers(0, 2**16, size=shape, dtype=np.uint16)
+    V = shape[axis]
+    ids = r.integers(-3 if idx != np.uint32 else 0, V + 3, 37).astype(idx)
+    out_shape = shape[:axis] + (37,) + shape[axis + 1:]
+    init = r.integers(0, 2**16, size=out_shape, dtype=np.uint16)
+    got = H.gather_axis(t, ids, axis, oob, out_init=init, elem_kind="Bf16")
+    assert np.array_equal(got, oracle.gather_axis(t, ids, axis, oob, out_init=init))
+    tf = r.normal(size=shape).astype(np.float32)
+    got = H.gather_axis(tf, ids, axis, oob, out_init=init.astype(np.float32))
+    assert np.array_equal(got, oracle.gather_axis(tf, ids, axis, oob, out_init=init.astype(np.float32)))
+
+
 def test_gather_empty_source_zero_fills(hip_device):
     H.say("[case] gather empty source")
     table = np.zeros((1, 8), np.uint16)

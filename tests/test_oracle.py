@@ -618,3 +618,23 @@ def test_bit_folds_against_numpy():
             assert np.array_equal(oracle.reduce_rows(np.zeros((2, 0), nt), op), np.zeros(2, nt))
         assert np.array_equal(oracle.reduce_rows(x, "MaxNum"), x.max(axis=1))
         assert np.array_equal(oracle.reduce_rows(x, "MinNum"), x.min(axis=1))
+
+
+def test_gather_along_any_axis_against_numpy():
+    """index_select along each axis: numpy's take of the clamped index, with the policy applied to the
+    stored cells (Skip leaves them, ZeroFill zeroes them, Clamp keeps the clamped read)."""
+    rng = np.random.default_rng(13)
+    t = rng.integers(0, 2**16, (4, 6, 5), dtype=np.uint16)
+    for axis in range(3):
+        V = t.shape[axis]
+        ids = rng.integers(-3, V + 3, 7).astype(np.int64)
+        init = rng.integers(0, 2**16, t.shape[:axis] + (7,) + t.shape[axis + 1:], dtype=np.uint16)
+        taken = np.take(t, np.clip(ids, 0, V - 1), axis=axis)
+        oob = (ids < 0) | (ids >= V)
+        shape = [1, 1, 1]
+        shape[axis] = 7
+        mask = np.broadcast_to(oob.reshape(shape), taken.shape)
+        for policy, want in (("Clamp", taken), ("ZeroFill", np.where(mask, 0, taken)),
+                             ("Skip", np.where(mask, init, taken))):
+            got = oracle.gather_axis(t, ids, axis, policy, out_init=init)
+            assert np.array_equal(got, want), (axis, policy)

@@ -544,10 +544,21 @@ static int32_t lower_gather(const unp_form& f, Lowered& L, std::string& why) {
     why = "an ill-formed gather";
     return UNP_LIFT_DECLINE;
   }
+  // The gathered axis: axes_mask's one bit, or axis 0 (the row gather of an embedding).
+  int32_t axis = 0;
+  if (f.axes_mask) {
+    if ((f.axes_mask & (f.axes_mask - 1)) != 0 || (f.axes_mask >> f.rank) != 0) {
+      why = "a gather gathers exactly one axis inside the rank";
+      return UNP_LIFT_DECLINE;
+    }
+    axis = __builtin_ctz(f.axes_mask);
+  }
+  L.scan_axis = axis;  // the gathered axis (the executor sees the output as A x NI rows)
+  const bool batch = axis > 0;
   const char* I = ctype(f.index_dtype);
   std::ostringstream name;
-  name << "unp_gather_rows_" << lower_name(f.dtype) << "_by_" << lower_name(f.index_dtype) << "_"
-       << oob_name(f.oob);
+  name << "unp_gather_" << (batch ? "select_" : "rows_") << lower_name(f.dtype) << "_by_" << lower_name(f.index_dtype)
+       << "_" << oob_name(f.oob);
   L.name = name.str();
   L.threads = 256;
   L.blocks_per_cu = 1;
@@ -567,15 +578,17 @@ static int32_t lower_gather(const unp_form& f, Lowered& L, std::string& why) {
     e.blocks_per_cu = units[i] == 16 ? 2 : 1;
     src << "extern \"C\" __global__ void __launch_bounds__(" << e.threads << ") " << e.symbol
         << "(const unsigned char* table, const " << I << "* ids, unsigned char* out, long long n_rows, "
-        << "long long row_bytes, " << I << " src_extent) {\n  unp::gather_rows<" << I << ", " << f.oob << ", "
-        << units[i] << ", " << e.threads << ", " << U << ", 2>(table, ids, out, n_rows, row_bytes, src_extent);\n}\n";
+        << "long long row_bytes, " << I << " src_extent" << (batch ? ", long long ni" : "")
+        << ") {\n  unp::gather_rows<" << I << ", " << f.oob << ", " << units[i] << ", " << e.threads << ", " << U
+        << ", 2" << (batch ? ", true" : "") << ">(table, ids, out, n_rows, row_bytes, src_extent"
+        << (batch ? ", ni" : "") << ");\n}\n";
     L.entries.push_back(e);
   }
   L.source = src.str();
   std::ostringstream j;
   j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"gather\",\"dtype\":\"" << kind_name(f.dtype)
     << "\",\"index_dtype\":\"" << kind_name(f.index_dtype) << "\",\"oob\":\"" << oob_name(f.oob)
-    << "\",\"axis\":0,\"rank\":" << f.rank << ",\"params\":[{\"name\":\"in0\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\""
+    << "\",\"axis\":" << axis << ",\"rank\":" << f.rank << ",\"params\":[{\"name\":\"in0\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\""
     << kind_name(f.data_slot == 0 ? f.dtype : f.index_dtype) << "\"},{\"name\":\"in1\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\""
     << kind_name(f.data_slot == 1 ? f.dtype : f.index_dtype)
     << "\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
@@ -583,7 +596,8 @@ static int32_t lower_gather(const unp_form& f, Lowered& L, std::string& why) {
   j << ",{\"name\":\"src_extent\",\"kind\":\"scalar\",\"dtype\":\"" << kind_name(f.index_dtype)
     << "\"}],\"launch\":{\"block\":[" << L.entries[0].threads << ",1,1],\"grid\":\"cu_count*"
     << L.entries[0].blocks_per_cu
-    << "\",\"grid_policy\":\"waves stride over output rows; whole rows of 64 x 8 units two at a time per wave\"},\"entries\":[";
+    << "\",\"grid_policy\":\"waves stride over output rows (the output seen as A x NI rows of the axes after the "
+       "gathered one, the index 1-D over NI); whole rows of 64 x 8 units two at a time per wave\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"unit_bytes\":" << L.entries[i].vec
       << ",\"when\":\"" << (L.entries[i].fast ? "row bytes % 16 == 0 and table/out 16-byte aligned" : "otherwise")

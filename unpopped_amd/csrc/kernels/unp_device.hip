@@ -1409,15 +1409,29 @@ template <class IDX> UNP_DEV bool below_zero(IDX v) {
   else return false;
 }
 
-template <class IDX, int POLICY, int UNIT, int THREADS, int U, int RPW>
+//
+// BATCH: a gather along an axis after the first (index_select, OpDef::gather with a 1-D index,
+// ir.rs:3838-3876).  The output is A x NI rows of row_bytes (the axes before the gathered one, the
+// gathered one, the rest as one row), the table A x src_extent rows: output row r = a * NI + i
+// takes the table row a * src_extent + clamp(ids[i]).  Without BATCH, A = 1 and NI = n_rows.
+template <class IDX, int POLICY, int UNIT, int THREADS, int U, int RPW, bool BATCH = false>
 UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ ids, u8* __restrict__ out,
-                         i64 n_rows, i64 row_bytes, IDX src_extent) {
+                         i64 n_rows, i64 row_bytes, IDX src_extent, i64 NI = 0) {
   typedef typename unit_type<UNIT>::elem E;
   constexpr int N = unit_type<UNIT>::n;
   typedef vec<E, N> V;
   constexpr int WAVES = THREADS / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const i64 units = row_bytes / UNIT;
+  // The id of output row r, and the table row its clamped id `cl` names.
+  auto id_at = [&](i64 r) -> IDX {
+    if constexpr (BATCH) return ids[r % NI];
+    else return ids[r];
+  };
+  auto src_row = [&](i64 r, IDX cl) -> i64 {
+    if constexpr (BATCH) return (r / NI) * (i64)src_extent + (i64)cl;
+    else return (i64)cl;
+  };
   if (units == 64 * U) {
     // Whole rows of 64 * U units: RPW rows of a wave in flight at once (every load of the
     // RPW rows, then the next ids, then every store).  Table rows are read through the
@@ -1426,7 +1440,7 @@ UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ i
     i64 r0 = ((i64)blockIdx.x * WAVES + wave) * RPW;
     IDX nxt[RPW];
 #pragma unroll
-    for (int j = 0; j < RPW; ++j) nxt[j] = r0 + j < n_rows ? ids[r0 + j] : (IDX)0;
+    for (int j = 0; j < RPW; ++j) nxt[j] = r0 + j < n_rows ? id_at(r0 + j) : (IDX)0;
     for (; r0 < n_rows; r0 += rstride) {
       V v[RPW][U];
       bool take[RPW], zero[RPW];
@@ -1440,13 +1454,13 @@ UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ i
         zero[j] = live && oob && POLICY == OOB_ZEROFILL;
         if (take[j]) {
           const IDX cl = below ? (IDX)0 : (oob ? (IDX)(src_extent - (IDX)1) : raw);
-          const E* __restrict__ src = reinterpret_cast<const E*>(table + (i64)cl * row_bytes);
+          const E* __restrict__ src = reinterpret_cast<const E*>(table + src_row(r0 + j, cl) * row_bytes);
 #pragma unroll
           for (int k = 0; k < U; ++k) v[j][k] = ld<E, N>(src + ((i64)lane + 64 * k) * N);
         }
       }
 #pragma unroll
-      for (int j = 0; j < RPW; ++j) nxt[j] = r0 + rstride + j < n_rows ? ids[r0 + rstride + j] : (IDX)0;
+      for (int j = 0; j < RPW; ++j) nxt[j] = r0 + rstride + j < n_rows ? id_at(r0 + rstride + j) : (IDX)0;
 #pragma unroll
       for (int j = 0; j < RPW; ++j) {
         E* __restrict__ dst = reinterpret_cast<E*>(out + (r0 + j) * row_bytes);
@@ -1466,7 +1480,7 @@ UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ i
   // Any other row width: a row per wave step, U units of each lane in flight.
   const i64 rstride = (i64)gridDim.x * WAVES;
   i64 r = (i64)blockIdx.x * WAVES + wave;
-  IDX next = r < n_rows ? ids[r] : (IDX)0;
+  IDX next = r < n_rows ? id_at(r) : (IDX)0;
   for (; r < n_rows; r += rstride) {
     const IDX raw = next;
     const i64 rn = r + rstride;
@@ -1474,7 +1488,7 @@ UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ i
     const bool oob = below || !(raw < src_extent);
     E* __restrict__ dst = reinterpret_cast<E*>(out + r * row_bytes);
     if (oob && POLICY != OOB_CLAMP) {
-      if (rn < n_rows) next = ids[rn];
+      if (rn < n_rows) next = id_at(rn);
       if constexpr (POLICY == OOB_ZEROFILL) {
         V z;
         __builtin_memset(&z, 0, sizeof(V));
@@ -1483,8 +1497,8 @@ UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ i
       continue;
     }
     const IDX cl = below ? (IDX)0 : (oob ? (IDX)(src_extent - (IDX)1) : raw);
-    const E* __restrict__ src = reinterpret_cast<const E*>(table + (i64)cl * row_bytes);
-    if (rn < n_rows) next = ids[rn];
+    const E* __restrict__ src = reinterpret_cast<const E*>(table + src_row(r, cl) * row_bytes);
+    if (rn < n_rows) next = id_at(rn);
     for (i64 u = lane; u < units; u += 64 * U) {
       V v[U];
 #pragma unroll

@@ -1273,11 +1273,8 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
     for (int32_t axis = 0; axis < r; ++axis)
       for (int32_t pol : pols)
         if (attempt([&] { return lift_gather(name, ps[0].elem, r, ps[1].elem, axis, pol, block, grid); })) {
-          if (axis != 0) {
-            why = "a gather along axis " + std::to_string(axis) + " (this backend lowers row gathers, axis 0)";
-            return UNP_UNSUPPORTED_KERNEL;
-          }
           out.form.kind = UNP_FORM_GATHER;
+          out.form.axes_mask = axis == 0 ? 0u : (1u << axis);
           out.form.dtype = ps[0].elem;
           out.form.rank = r;
           out.form.index_dtype = ps[1].elem;

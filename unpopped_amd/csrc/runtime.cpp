@@ -812,8 +812,11 @@ int32_t run_gather(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_e
   int32_t rc = take_args(a, n, 3, (size_t)f.rank + 1, A, err);
   if (rc == UNP_OK) rc = extents_i32(A, (size_t)f.rank, err);
   if (rc != UNP_OK) return rc;
-  const long long n_rows = A.ext[0];
-  const long long row_elems = product(A.ext, 1, (size_t)f.rank);
+  // The output as A x NI rows around the gathered axis (A = 1 for axis 0).
+  const size_t ax = (size_t)x->l.scan_axis;
+  const long long ni = A.ext[ax];
+  const long long n_rows = product(A.ext, 0, ax + 1);
+  const long long row_elems = product(A.ext, ax + 1, (size_t)f.rank);
   const long long row_bytes = row_elems * (long long)unp::kind_bytes(f.dtype);
   if ((rc = need_buffers(A, n_rows > 0 && row_bytes > 0, err)) != UNP_OK) return rc;
   if (n_rows == 0 || row_bytes == 0) return UNP_OK;
@@ -843,9 +846,9 @@ int32_t run_gather(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_e
   const size_t entry = pick(x, row_bytes % 16 == 0 && aligned16(table) && aligned16(out));
   const int bpc = x->l.entries[entry].blocks_per_cu ? x->l.entries[entry].blocks_per_cu : x->l.blocks_per_cu;
   const uint32_t grid = (uint32_t)(x->cu_count * bpc);
-  long long nr = n_rows, rb = row_bytes;
+  long long nr = n_rows, rb = row_bytes, nib = ni;
   void* ext_arg = f.index_dtype == UNP_I32 ? (void*)&ext32 : (f.index_dtype == UNP_U32 ? (void*)&extu32 : (void*)&ext64);
-  void* params[] = {&table, &ids, &out, &nr, &rb, ext_arg};
+  void* params[] = {&table, &ids, &out, &nr, &rb, ext_arg, &nib};
   return launch(x, entry, grid, params, s, err);
 }
 

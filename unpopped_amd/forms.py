@@ -42,7 +42,7 @@ def kernel_for(kind: str, dtype: str = "F32", rank: int = 1, op: str = "Sum", op
         return u.lift_scan("scan", dtype, rank, op, axis=ax, exclusive=exclusive, reverse=reverse,
                            launch=None if serial else CALLER_LAUNCH)
     if kind == "gather":
-        return u.lift_gather("gather", dtype, rank, index_dtype, 0, oob, launch=CALLER_LAUNCH)
+        return u.lift_gather("gather", dtype, rank, index_dtype, 0 if axis is None else axis, oob, launch=CALLER_LAUNCH)
     if kind == "dequant4":
         return u.kernel_dequant4("dequant", q_kind, z_kind, group, launch=CALLER_LAUNCH)
     if kind == "dequant_gemm":
@@ -180,6 +180,20 @@ def gather_rows(table: np.ndarray, ids: np.ndarray, oob: str, out_init: np.ndarr
     do = u.DeviceBuffer.from_array(out0)
     ext = table.shape[0] if src_extent is None else src_extent
     ex.launch(dt, di, do, n, *inner, ext)
+    u.synchronize()
+    return do.download(table.dtype, int(np.prod(out_shape))).reshape(out_shape)
+
+
+def gather_axis(table: np.ndarray, ids: np.ndarray, axis: int, oob: str, out_init: np.ndarray | None = None,
+                elem_kind: str | None = None) -> np.ndarray:
+    """index_select: ``out`` takes ``table``'s shape with ``axis`` replaced by ``len(ids)``, and
+    ``out[.., i, ..] = table[.., clamp(ids[i]), ..]`` under the policy (1-D ``ids``)."""
+    kind = elem_kind or NP_KIND[table.dtype.type]
+    ex = executor(kind="gather", dtype=kind, rank=table.ndim, index_dtype=NP_KIND[ids.dtype.type], oob=oob, axis=axis)
+    out_shape = table.shape[:axis] + (ids.shape[0],) + table.shape[axis + 1:]
+    out0 = np.zeros(out_shape, table.dtype) if out_init is None else out_init
+    dt, di, do = (u.DeviceBuffer.from_array(np.ascontiguousarray(a)) for a in (table, ids, out0))
+    ex.launch(dt, di, do, *out_shape, table.shape[axis])
     u.synchronize()
     return do.download(table.dtype, int(np.prod(out_shape))).reshape(out_shape)
 
