@@ -292,13 +292,21 @@ typedef struct unp_view {
 } unp_view;
 
 /* unp_hip_exec_launch with the buffers as storage images, in the KernelFn's parameter order
- * (views for the buffer parameters, then the scalars).  This backend's kernels read dense
- * row-major storage: a view is taken at data + base elements when every axis longer than one
- * has the row-major stride, and, for the gather's index buffer, also as the reference's
- * broadcast [n, d] with strides [1, 0] (tests/kernel_parallel_gather_agrees.rs:80-84).  Any
- * other view (transposed, strided, negative strides, a sub-byte view starting mid-byte) is
- * refused with UNP_INVALID_ARGUMENT before anything launches: refuse rather than approximate
- * (backend.rs:703-707). */
+ * (views for the buffer parameters, then the scalars).  The shape is authoritative, as in the
+ * reference's TypedBuffer: each view must have exactly the shape the extent scalars give its
+ * parameter (a reduction's output: the kept extents, or the keepdim shape with the reduced axes
+ * of extent 1; a gather's table: the output's extents except along the gathered axis, where it
+ * holds at least src_extent rows), must not reach below its storage (base plus every negative
+ * stride times its extent less one), and a 4-bit view starts on a whole byte; anything else is
+ * UNP_INVALID_ARGUMENT before anything launches.
+ * Dense row-major views (any stride on an axis of extent one; the gather index broadcast along
+ * every axis but the gathered one, e.g. [n, d] with strides [1, 0],
+ * tests/kernel_parallel_gather_agrees.rs:80-84) launch the pointer kernels at data + base.  Any
+ * other view -- transposed, strided, negative strides, a full-shape gather index -- is read and
+ * written through its strides by the reduction (plain body), fused row fold, scan and gather
+ * forms (their "strided" interface entries); the row-reduce, pre-map reduction and dequant forms
+ * read dense storage only and refuse it with UNP_INVALID_ARGUMENT (backend.rs:703-707).  The
+ * storage behind a view is the caller's: every element the view names must lie inside it. */
 int32_t unp_hip_exec_launch_views(unp_exec* e, const unp_view* views, size_t nviews, const int64_t* scalars,
                                   size_t nscalars, void* stream, unp_error* err);
 /* No reference counterpart: it exists for callers that cannot allocate (code under HIP graph

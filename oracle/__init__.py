@@ -187,6 +187,37 @@ def gather_axis(table: np.ndarray, ids: np.ndarray, axis: int, policy: str,
     return out.reshape(out_shape)
 
 
+def gather_cells(table: np.ndarray, ids: np.ndarray, axis: int, policy: str, out_init: np.ndarray | None = None,
+                 src_extent: int | None = None) -> np.ndarray:
+    """The gather lift's cell at every output coordinate c (kernel_lift/gather.rs:184-232), with an
+    index of the output's own shape (a storage image of any strides, not only the broadcast 1-D
+    index): ``raw = ids[c]``; when ``0 <= raw < src_extent`` the cell stores ``table[c with axis :=
+    raw]``; otherwise Skip leaves it, ZeroFill stores 0 and Clamp stores the row clamped into
+    ``[0, src_extent - 1]``.  ``table`` has the output's extents except along ``axis``."""
+    ids = np.asarray(ids)
+    ext = table.shape[axis] if src_extent is None else int(src_extent)
+    raw = ids.astype(np.int64)
+    below = raw < 0
+    oob = below | (raw >= ext)
+    out = np.zeros(ids.shape, table.dtype) if out_init is None else np.array(out_init, copy=True)
+    if policy == "Clamp":
+        if ext < 1:
+            raise ValueError("a Clamp gather needs a source extent of at least 1")
+        take = np.ones(ids.shape, bool)
+    else:
+        take = ~oob
+    cl = np.where(below, 0, np.where(oob, max(ext - 1, 0), raw))
+    cl = np.where(take, cl, 0)
+    if table.shape[axis] == 0:
+        got = np.zeros(ids.shape, table.dtype)
+    else:
+        got = np.take_along_axis(table, cl, axis)
+    out[take] = got[take]
+    if policy == "ZeroFill":
+        out[oob] = 0
+    return out
+
+
 # ---- dequant --------------------------------------------------------------------------
 
 def dequant4_bf16(q_packed: np.ndarray, scales_f16_bits: np.ndarray, zeros_packed: np.ndarray, rows: int,

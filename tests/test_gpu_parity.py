@@ -14,8 +14,11 @@ import pytest
 
 import oracle
 import unpopped_amd as u
+from oracle import cpuc
 from unpopped_amd import forms as H
 from unpopped_amd import synth
+
+RNG = np.random.default_rng(4242)
 
 pytestmark = pytest.mark.gpu
 
@@ -1044,8 +1047,8 @@ def test_config5_dequant_full(hip_device):
 # ---------------------------------------------------------------------------------------
 
 def test_views_dense_with_base_match_the_pointer_launch(hip_device):
-    """Dense row-major views at a base offset launch the kernel on data + base; an axis of extent
-    one may carry any stride.  The results equal the pointer launch bit for bit."""
+    """Dense row-major views at a base offset launch the kernel on data + base.  The results equal the
+    pointer launch bit for bit."""
     H.say("[case] views: dense, base offset")
     R, Cc = 37, 300
     x = synth.normal_f32(11, R * Cc + 5)
@@ -1053,7 +1056,7 @@ def test_views_dense_with_base_match_the_pointer_launch(hip_device):
     din = u.DeviceBuffer.from_array(x)
     a0, a1, b0, b1 = (u.DeviceBuffer(R * 4) for _ in range(4))
     ex.launch(din.at(20), a0, a1, R, Cc)
-    ex.launch_views([(din, (R, Cc), None, 5), (b0, (R,), None, 0), (b1, (1, R), (977, 1), 0)], [R, Cc])
+    ex.launch_views([(din, (R, Cc), None, 5), (b0, (R,), None, 0), (b1, (R,), (1,), 0)], [R, Cc])
     u.synchronize()
     assert np.array_equal(a0.download(np.float32, R), b0.download(np.float32, R))
     assert np.array_equal(a1.download(np.float32, R), b1.download(np.float32, R))
@@ -1074,33 +1077,266 @@ def test_views_gather_index_broadcast(hip_device):
     assert np.array_equal(do.download(np.uint16, n * D).reshape(n, D), table[ids])
 
 
-@pytest.mark.parametrize("what", ["transposed", "negative", "broadcast data", "odd u4 base"])
-def test_views_the_kernels_cannot_read_are_refused(hip_device, what):
-    """A view other than dense row-major (or the gather index broadcast) is refused with
-    INVALID_ARGUMENT before anything launches, and the output is untouched."""
+def _logical(storage: np.ndarray, shape, strides, base: int = 0) -> np.ndarray:
+    """The numpy view a storage image names: ``storage``'s elements from ``base`` on, at the given
+    extents and signed element strides (oracle/buffers.rs:16-42)."""
+    flat = storage.reshape(-1)
+    it = flat.itemsize
+    return np.lib.stride_tricks.as_strided(flat[base:], shape=tuple(shape), strides=tuple(st * it for st in strides))
+
+
+def _run_images(ex, images, scalars):
+    """Upload each image's storage, launch through unp_hip_exec_launch_views, download every
+    storage array (the outputs with whatever the launch left outside their views)."""
+    bufs = [u.DeviceBuffer.from_array(st) for st, _, _, _ in images]
+    ex.launch_views([(b, shape, strides, base) for b, (_, shape, strides, base) in zip(bufs, images)], scalars)
+    u.synchronize()
+    return [b.download(st.dtype, st.size).reshape(st.shape) for b, (st, _, _, _) in zip(bufs, images)]
+
+
+def _expect(storage: np.ndarray, shape, strides, base, values) -> np.ndarray:
+    """``storage`` with ``values`` written through the view (every other element unchanged)."""
+    want = storage.copy()
+    _logical(want, shape, strides, base)[...] = values
+    return want
+
+
+def _fold_axes(x: np.ndarray, axes, op: str) -> np.ndarray:
+    """The oracle's fold of ``x`` over ``axes`` (row-major over the reduced axes), kept shape."""
+    kept = [d for d in range(x.ndim) if d not in axes]
+    m = np.ascontiguousarray(np.transpose(x, kept + list(axes)))
+    outs = int(np.prod([x.shape[d] for d in kept], dtype=np.int64))
+    return oracle.reduce_rows(m.reshape(outs, -1), op).reshape([x.shape[d] for d in kept])
+
+
+STRIDED_REDUCTIONS = [
+    # (dtype, op, storage shape, view shape, view strides, base, reduced axes)
+    ("F32", "Sum", (300, 40), (40, 300), (1, 40), 0, (1,)),           # transposed
+    ("F32", "Max", (300, 40), (40, 300), (1, 40), 0, (0,)),
+    ("I64", "Sum", (12, 10, 18), (12, 10, 9), (180, -18, 2), 162, (0, 2)),  # reversed axis 1, every 2nd of axis 2
+    ("I32", "Min", (12, 10, 18), (10, 12), (1, 180), 0, (1,)),        # a transposed slice
+    ("F64", "Mean", (64, 33), (33, 64), (1, 33), 0, (0,)),
+    ("F32", "Prod", (50, 21), (21, 50), (-1, 21), 20, (1,)),          # the serial product, reversed rows
+    ("F32", "MaxNum", (40, 64), (40, 32), (64, -2), 63, (1,)),
+    ("I64", "Xor", (16, 30), (30, 16), (1, 16), 0, (1,)),
+]
+
+
+@pytest.mark.parametrize("case", STRIDED_REDUCTIONS, ids=lambda c: f"{c[0]}-{c[1]}-{c[3]}-{c[4]}")
+def test_reductions_read_through_view_strides(hip_device, case):
+    """A reduction over a transposed, reversed or strided storage image reads through its strides: the
+    result equals the oracle's fold of the logical array (bit for bit for integers, Max/Min/MaxNum, the
+    serial Prod and dyadic data; float Sum/Mean within the declared bound on normal data), and the
+    output, itself a strided view, leaves every other element of its storage untouched."""
+    dtype, op, sshape, vshape, vstrides, base, axes = case
+    H.say(f"[case] strided reduction {dtype} {op} view {vshape} strides {vstrides} base {base} axes {axes}")
+    nt = {"F32": np.float32, "F64": np.float64, "I32": np.int32, "I64": np.int64}[dtype]
+    n = int(np.prod(sshape))
+    if dtype.startswith("F"):
+        data = (synth.uniform_pm1_f32(17, n).astype(nt) if op != "Prod" else
+                (1 + synth.uniform_pm1_f32(17, n) / 64).astype(nt))
+        if op == "MaxNum":
+            data[::5] = np.nan
+    else:
+        info = np.iinfo(nt)
+        data = RNG.integers(info.min // 2, info.max // 2, n, dtype=np.int64).astype(nt)
+    storage = data.reshape(sshape)
+    x = _logical(storage, vshape, vstrides, base).copy()
+    kept = [vshape[d] for d in range(len(vshape)) if d not in axes]
+    want_vals = _fold_axes(x, axes, op)
+    # The output: every 3rd element of a larger buffer, from element 1, reversed.
+    outs = int(np.prod(kept, dtype=np.int64))
+    ostore = np.full(3 * outs + 2, 7, nt)
+    ostrides = [0] * len(kept)
+    acc = -3
+    for d in range(len(kept) - 1, -1, -1):
+        ostrides[d], acc = acc, acc * kept[d]
+    obase = 1 + 3 * (outs - 1)
+    ex = H.executor(kind="reduction", dtype=dtype, rank=len(vshape), op=op, axes=axes)
+    _, got = _run_images(ex, [(storage, vshape, vstrides, base), (ostore, kept, ostrides, obase)], list(vshape))
+    want = _expect(ostore, kept, ostrides, obase, want_vals)
+    if dtype.startswith("F") and op in ("Sum", "Mean"):
+        # Dyadic data: every order of the f64 fold is exact, so the bits match.
+        assert got.tobytes() == want.tobytes()
+        xn = synth.normal_f32(18, n).astype(nt).reshape(sshape)
+        _, got = _run_images(ex, [(xn, vshape, vstrides, base), (ostore, kept, ostrides, obase)], list(vshape))
+        xl = _logical(xn, vshape, vstrides, base)
+        g = _logical(got, kept, ostrides, obase)
+        rows = np.transpose(xl, [d for d in range(len(vshape)) if d not in axes] + list(axes)).reshape(outs, -1)
+        for r, gv in zip(rows, g.reshape(-1)):
+            assert abs(float(gv) - oracle.neumaier(r) / (len(r) if op == "Mean" else 1)) <= \
+                oracle.sum_bound(r, float(gv), mean=op == "Mean", f32=dtype == "F32")
+        mask = np.ones(ostore.size, bool)
+        _logical(mask, kept, ostrides, obase)[...] = False
+        assert np.array_equal(got[mask], ostore[mask])
+    else:
+        assert got.tobytes() == want.tobytes()
+
+
+def test_keepdim_output_and_fused_row_fold_through_strides(hip_device):
+    """The keepdim output shape is accepted; the fused row fold (Sum + Max) reads a transposed input
+    and writes both outputs through their own strides."""
+    H.say("[case] strided keepdim reduction and row fold")
+    R, Cc = 48, 96
+    st = synth.uniform_pm1_f32(19, R * Cc).reshape(Cc, R)   # the view (R, Cc) is its transpose
+    x = st.T.copy()
+    ex = H.executor(kind="reduction", dtype="F32", rank=2, op="Max", axes=(1,), keepdim=True)
+    o = np.zeros(2 * R, np.float32)
+    _, got = _run_images(ex, [(st, (R, Cc), (1, R), 0), (o, (R, 1), (2, 5), 0)], [R, Cc])
+    assert got.tobytes() == _expect(o, (R, 1), (2, 5), 0, oracle.reduce_rows(x, "Max").reshape(R, 1)).tobytes()
+    ex2 = H.executor(kind="row_reduce2", dtype="F32", rank=2, op="Sum", op1="Max")
+    o0, o1 = np.full(R, 3, np.float32), np.full(2 * R, 3, np.float32)
+    _, g0, g1 = _run_images(ex2, [(st, (R, Cc), (1, R), 0), (o0, (R,), (-1,), R - 1), (o1, (R,), (2,), 1)], [R, Cc])
+    assert g0.tobytes() == oracle.reduce_rows(x, "Sum")[::-1].tobytes()  # dyadic: exact
+    assert g1.tobytes() == _expect(o1, (R,), (2,), 1, oracle.reduce_rows(x, "Max")).tobytes()
+
+
+STRIDED_SCANS = [
+    # (dtype, op, exclusive, reverse, storage shape, view shape, strides, base, axis)
+    ("I32", "Sum", False, False, (500, 24), (24, 500), (1, 24), 0, 1),      # transposed, scan the long axis
+    ("I64", "Max", True, False, (30, 200), (30, 200), (200, -1), 199, 1),   # reversed rows
+    ("F32", "Sum", True, True, (8, 6, 70), (8, 70, 6), (420, 1, 70), 0, 1),  # non-innermost, transposed
+    ("F64", "Mean", False, False, (40, 90), (45, 40), (2, 90), 0, 0),       # every 2nd of axis 0, transposed
+    ("F32", "Prod", False, True, (64, 32), (32, 64), (1, 32), 0, 1),
+]
+
+
+@pytest.mark.parametrize("case", STRIDED_SCANS, ids=lambda c: f"{c[0]}-{c[1]}-{c[5]}-{c[6]}-ax{c[8]}")
+def test_scans_read_through_view_strides(hip_device, case):
+    """A scan over a transposed, reversed or strided storage image walks the scanned axis in the serial
+    lift's order through the strides: bit-exact against the oracle's serial scan of the logical array for
+    every op (float Sum too), the output written through its own strides."""
+    dtype, op, excl, rev, sshape, vshape, vstrides, base, axis = case
+    H.say(f"[case] strided scan {dtype} {op} excl={excl} rev={rev} view {vshape} strides {vstrides} axis {axis}")
+    nt = {"F32": np.float32, "F64": np.float64, "I32": np.int32, "I64": np.int64}[dtype]
+    n = int(np.prod(sshape))
+    if op == "Prod":
+        data = (1 + synth.normal_f32(21, n) / 32).astype(nt)
+    elif dtype.startswith("F"):
+        data = synth.normal_f32(21, n).astype(nt)
+    else:
+        data = RNG.integers(-2**20, 2**20, n).astype(nt)
+    storage = data.reshape(sshape)
+    x = _logical(storage, vshape, vstrides, base).copy()
+    moved = np.ascontiguousarray(np.moveaxis(x, axis, -1))
+    want_vals = np.moveaxis(oracle.scan_rows(moved.reshape(-1, moved.shape[-1]), op, excl, rev).reshape(moved.shape),
+                            -1, axis)
+    # The output: the transpose of a dense buffer of the view's reversed shape.
+    ostore = np.full(vshape[::-1], 5, nt)
+    ostrides = [int(np.prod(vshape[:d], dtype=np.int64)) for d in range(len(vshape))]
+    ex = H.executor(kind="scan", dtype=dtype, rank=len(vshape), op=op, exclusive=excl, reverse=rev, axis=axis)
+    _, got = _run_images(ex, [(storage, vshape, vstrides, base), (ostore, vshape, ostrides, 0)], list(vshape))
+    assert got.tobytes() == _expect(ostore, vshape, ostrides, 0, want_vals).tobytes()
+
+
+@pytest.mark.parametrize("index_dtype", ["I32", "I64", "U32"])
+@pytest.mark.parametrize("oob", ["Skip", "ZeroFill", "Clamp"])
+def test_gather_with_a_full_shape_index_view(hip_device, index_dtype, oob):
+    """The gather lift reads its index at every output coordinate (kernel_lift/gather.rs:184-232): a
+    full-shape index view with a different id in every cell gathers element by element, equal to the
+    oracle's per-cell gather and to the C99 leg on the same storage images."""
+    H.say(f"[case] strided gather, full-shape index {index_dtype} {oob}")
+    V, D, N = 40, 24, 33
+    nt = {"I32": np.int32, "I64": np.int64, "U32": np.uint32}[index_dtype]
+    table = synth.normal_bf16_bits(23, V * D, 0.02).reshape(V, D)
+    lo = 0 if index_dtype == "U32" else -5
+    ids = RNG.integers(lo, V + 5, (N, D)).astype(nt)
+    init = np.full((N, D), 0x3C00, np.uint16)
+    ex = H.executor(kind="gather", dtype="Bf16", rank=2, index_dtype=index_dtype, oob=oob)
+    _, _, got = _run_images(ex, [(table, (V, D), (D, 1), 0), (ids, (N, D), (D, 1), 0), (init, (N, D), (D, 1), 0)],
+                            [N, D, V])
+    want = oracle.gather_cells(table, ids, 0, oob, out_init=init)
+    assert np.array_equal(got, want)
+    c = init.copy()
+    assert cpuc.run(H.kernel_for(kind="gather", dtype="Bf16", rank=2, index_dtype=index_dtype, oob=oob), table, ids,
+                    c, N, D, V) == cpuc.OK
+    assert np.array_equal(got, c)
+
+
+def test_gather_through_transposed_table_and_reversed_output(hip_device):
+    """A transposed table, the broadcast index and a reversed output: read through the strides."""
+    H.say("[case] strided gather, transposed table")
+    V, D, N = 64, 48, 50
+    tstore = synth.normal_bf16_bits(24, V * D, 0.02).reshape(D, V)  # the (V, D) table is its transpose
+    ids = RNG.integers(-3, V + 3, N).astype(np.int64)
+    init = np.full((N, D), 0x1111, np.uint16)
+    for oob in ("Skip", "ZeroFill", "Clamp"):
+        ex = H.executor(kind="gather", dtype="Bf16", rank=2, index_dtype="I64", oob=oob)
+        _, _, got = _run_images(ex, [(tstore, (V, D), (1, V), 0), (ids, (N, D), (1, 0), 0),
+                                     (init, (N, D), (-D, 1), (N - 1) * D)], [N, D, V])
+        want = oracle.gather_rows(tstore.T.copy(), ids, oob, out_init=init[::-1].copy())[::-1]
+        assert np.array_equal(got, want), oob
+
+
+def test_gather_along_an_axis_of_a_longer_table(hip_device):
+    """index_select along axis 1 from a table holding more rows along that axis than src_extent: the
+    dense kernels step src_extent rows per slice, so the launch reads through the table's strides."""
+    H.say("[case] strided gather, axis 1, table longer than src_extent")
+    A, Vt, B, N, src = 6, 20, 10, 9, 15
+    table = RNG.integers(0, 2**31, (A, Vt, B)).astype(np.int32)
+    ids = RNG.integers(-2, src + 3, N).astype(np.int32)
+    init = np.full((A, N, B), -7, np.int32)
+    ex = H.executor(kind="gather", dtype="I32", rank=3, index_dtype="I32", oob="ZeroFill", axis=1)
+    _, _, got = _run_images(ex, [(table, (A, Vt, B), (Vt * B, B, 1), 0), (ids, (A, N, B), (0, 1, 0), 0),
+                                 (init, (A, N, B), (N * B, B, 1), 0)], [A, N, B, src])
+    full = np.broadcast_to(ids.reshape(1, N, 1), (A, N, B))
+    assert np.array_equal(got, oracle.gather_cells(table, full, 1, "ZeroFill", out_init=init, src_extent=src))
+
+
+REFUSED_VIEWS = ["output shorter than the extents", "input of another shape", "wrong rank", "below the storage",
+                 "odd u4 base", "strided dequant output", "table shorter than src_extent", "view count"]
+
+
+@pytest.mark.parametrize("what", REFUSED_VIEWS)
+def test_views_that_do_not_fit_are_refused(hip_device, what):
+    """A view whose shape differs from what the form's extents ask for, that reaches below its storage,
+    that starts mid-byte, or that is strided for a form that reads dense storage only, is refused with
+    INVALID_ARGUMENT before anything launches, and the output storage is untouched."""
     H.say(f"[case] views refused: {what}")
-    if what == "odd u4 base":
+    if what in ("odd u4 base", "strided dequant output"):
         R, Cc, G = 4, 256, 128
-        ex = H.executor(kind="dequant4", q_kind="U4", z_kind="U4", group=G, out_kind="Bf16")
+        ex = H.executor(kind="dequant4", q_kind="U4", z_kind="U4", group=G)
         q, s, z = u.DeviceBuffer(R * Cc), u.DeviceBuffer(R * 2 * 2), u.DeviceBuffer(R)
-        out = u.DeviceBuffer(R * Cc * 2)
+        out = u.DeviceBuffer(2 * R * Cc * 2)
         out.fill(0x5A)
-        views = [(q, (R, Cc), None, 1), (s, (R, Cc // G), None, 0), (z, (R, Cc // G), None, 0), (out, (R, Cc), None, 0)]
+        qbase = 1 if what == "odd u4 base" else 0
+        ostride = 2 if what == "strided dequant output" else 1
+        views = [(q, (R * Cc,), None, qbase), (s, (R * 2,), None, 0), (z, (R * 2,), None, 0),
+                 (out, (R * Cc,), (ostride,), 0)]
         scalars = [R, Cc]
-        check, count, dt = out, R * Cc, np.uint16
+        check, nbytes = out, 2 * R * Cc * 2
+    elif what == "table shorter than src_extent":
+        V, D, n = 10, 16, 5
+        ex = H.executor(kind="gather", dtype="Bf16", rank=2, index_dtype="I32", oob="Clamp")
+        t, i = u.DeviceBuffer(V * D * 2), u.DeviceBuffer(n * 4)
+        out = u.DeviceBuffer(n * D * 2)
+        out.fill(0x5A)
+        views = [(t, (V, D), None, 0), (i, (n, D), (1, 0), 0), (out, (n, D), None, 0)]
+        scalars = [n, D, V + 1]
+        check, nbytes = out, n * D * 2
     else:
         R, Cc = 16, 64
         ex = H.executor(kind="row_reduce2", dtype="F32", rank=2, op="Sum", op1="Max")
         din = u.DeviceBuffer.from_array(synth.normal_f32(13, R * Cc))
         o0, o1 = u.DeviceBuffer(R * 4), u.DeviceBuffer(R * 4)
         o0.fill(0x5A)
-        strides = {"transposed": (1, R), "negative": (-Cc, 1), "broadcast data": (0, 1)}[what]
-        views = [(din, (R, Cc), strides, (R - 1) * Cc if what == "negative" else 0), (o0, (R,), None, 0),
-                 (o1, (R,), None, 0)]
+        o1.fill(0x5A)
+        iv, v0 = (din, (R, Cc), None, 0), (o0, (R,), None, 0)
+        if what == "output shorter than the extents":
+            v0 = (o0, (R - 1,), None, 0)
+        elif what == "input of another shape":
+            iv = (din, (R, Cc - 1), None, 0)
+        elif what == "wrong rank":
+            v0 = (o0, (1, R), None, 0)
+        elif what == "below the storage":
+            iv = (din, (R, Cc), (-Cc, 1), 0)
+        views = [iv, v0, (o1, (R,), None, 0)]
+        if what == "view count":
+            views = views[:2]
         scalars = [R, Cc]
-        check, count, dt = o0, R, np.float32
+        check, nbytes = o0, R * 4
     with pytest.raises(u.UnpError) as e:
         ex.launch_views(views, scalars)
     assert e.value.kind == "InvalidArgument", e.value
     u.synchronize()
-    assert np.all(check.download(np.uint8, count * np.dtype(dt).itemsize) == 0x5A)
+    assert np.all(check.download(np.uint8, nbytes) == 0x5A)

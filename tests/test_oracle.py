@@ -638,3 +638,40 @@ def test_gather_along_any_axis_against_numpy():
                              ("Skip", np.where(mask, init, taken))):
             got = oracle.gather_axis(t, ids, axis, policy, out_init=init)
             assert np.array_equal(got, want), (axis, policy)
+
+
+def test_gather_cells_pins():
+    """The per-cell gather (an index of the output's own shape) against: the index_select oracle when
+    the index is the same along every other axis; the C99 leg running the gather lift on the same
+    storage images; the identity index reproducing the table."""
+    from unpopped_amd import forms as H
+    from oracle import cpuc
+    from oracle.cpuc import View
+
+    rng_ = np.random.default_rng(23)
+    t = rng_.integers(0, 2**16, (5, 6, 4), dtype=np.uint16)
+    for axis in range(3):
+        V = t.shape[axis]
+        n = 7
+        out_shape = t.shape[:axis] + (n,) + t.shape[axis + 1:]
+        ids1 = rng_.integers(-3, V + 3, n).astype(np.int64)
+        shape = [1, 1, 1]
+        shape[axis] = n
+        full = np.broadcast_to(ids1.reshape(shape), out_shape)
+        init = rng_.integers(0, 2**16, out_shape, dtype=np.uint16)
+        for policy in ("Skip", "ZeroFill", "Clamp"):
+            want = oracle.gather_axis(t, ids1, axis, policy, out_init=init)
+            assert np.array_equal(oracle.gather_cells(t, full, axis, policy, out_init=init), want), (axis, policy)
+        # A different index in every cell: the C99 leg of the lift reads it through the view.
+        ids = rng_.integers(-2, V + 2, out_shape).astype(np.int32)
+        k = H.kernel_for(kind="gather", dtype="Bf16", rank=3, index_dtype="I32", oob="ZeroFill", axis=axis)
+        got = init.copy()
+        assert cpuc.run(k, t, View(ids), got, *out_shape, V) == cpuc.OK
+        assert np.array_equal(oracle.gather_cells(t, ids, axis, "ZeroFill", out_init=init), got), axis
+    ident = np.broadcast_to(np.arange(5).reshape(5, 1, 1), t.shape)
+    assert np.array_equal(oracle.gather_cells(t, ident, 0, "Skip"), t)
+    # A planted mistake (the index read at the transposed cell) fails the C99 comparison.
+    ids = rng_.integers(0, 5, (5, 5)).astype(np.int32)
+    t2 = rng_.integers(0, 2**16, (5, 5), dtype=np.uint16)
+    good = oracle.gather_cells(t2, ids, 0, "Skip")
+    assert not np.array_equal(oracle.gather_cells(t2, ids.T.copy(), 0, "Skip"), good)

@@ -207,6 +207,10 @@ char reduction_schedule(uint32_t mask, int32_t rank) {
   return 'g';
 }
 
+// When the executor picks an entry that reads through storage-image strides.
+static const char* const kStridedWhen =
+    "a storage image that is not dense row-major (unp_hip_exec_launch_views): the view's strides";
+
 static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) {
   const bool two = f.kind == UNP_FORM_ROW_REDUCE2;
   if (f.rank < 1 || f.rank > 8) {
@@ -277,7 +281,7 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
     e.vec = 1;
     e.symbol = L.name + "_q";
     src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(const " << T << "* in, " << T
-        << "* out, unp::axes_desc d) {\n  unp::reduce_serial_prod<" << T << ", 256>(in, out, d);\n}\n";
+        << "* out, unp::red_view d) {\n  unp::reduce_serial_prod<" << T << ", 256>(in, out, d);\n}\n";
     L.entries.push_back(e);
   } else if (sched == 'g') {
     L.threads = 256;
@@ -326,6 +330,22 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
       }
     }
   }
+  // Storage images that are not dense row-major (transposed, strided, reversed): one wave per
+  // output reading through the view's strides (the serial product: one lane per output, its own
+  // order); the fused row fold runs one launch per fold.
+  for (int o = 0; o < (two ? 2 : 1); ++o) {
+    Entry e;
+    e.strided = true;
+    e.vec = 1;
+    e.threads = 256;
+    e.blocks_per_cu = 8;
+    e.symbol = L.name + (o ? "_x1" : "_x");
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(const " << T << "* in, " << T
+        << "* out, unp::red_view v) {\n  unp::";
+    if (sched == 'q') src << "reduce_serial_prod<" << T << ", 256>(in, out, v);\n}\n";
+    else src << "reduce_strided<" << T << ", " << (o ? f.op1 : f.op0) << ", 256>(in, out, v);\n}\n";
+    L.entries.push_back(e);
+  }
   L.source = src.str();
   std::ostringstream j;
   j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":"
@@ -354,7 +374,8 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
       << ",\"when\":\"" << (L.entries[i].wide ? "reduced extent > 32768; " : "")
-      << ((sched == 'g' || sched == 'q') ? "always"
+      << (L.entries[i].strided ? kStridedWhen
+          : (sched == 'g' || sched == 'q') ? "always"
           : sched == 'm' ? (L.entries[i].fast ? "B % vec == 0 and in0 16-byte aligned" : "otherwise")
                          : (L.entries[i].fast ? "reduced extent % vec == 0 and in0 16-byte aligned" : "otherwise"))
       << "\"}";
@@ -372,6 +393,24 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
     << "]}";
   L.interface_json = j.str();
   return UNP_OK;
+}
+
+// A scan's entry over storage images: one lane per column, the scanned axis walked in the serial
+// lift's order through the views' strides.
+static std::string scan_strided_entry(const unp_form& f, Lowered& L) {
+  Entry e;
+  e.strided = true;
+  e.vec = 1;
+  e.threads = 256;
+  e.blocks_per_cu = 8;
+  e.symbol = L.name + "_x";
+  const char* T = ctype(f.dtype);
+  std::ostringstream src;
+  src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(const " << T << "* in, " << T
+      << "* out, unp::scan_view v) {\n  unp::scan_strided<" << T << ", " << f.op0 << ", "
+      << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false") << ">(in, out, v);\n}\n";
+  L.entries.push_back(e);
+  return src.str();
 }
 
 static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
@@ -424,6 +463,7 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
         << "* out, long long A, long long S, long long B) {\n  unp::scan_seq<" << T << ", " << f.op0 << ", "
         << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false") << ", 8>(in, out, A, S, B);\n}\n";
     L.entries.push_back(e);
+    src << scan_strided_entry(f, L);
     L.threads = 256;
     L.blocks_per_cu = 8;
     L.source = src.str();
@@ -436,7 +476,8 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
     j << "],\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*8\",\"grid_policy\":\"device-class constant; one "
       << "lane per column of the input seen as A x S x B around the scanned axis, lanes stride over columns\"},"
-      << "\"entries\":[{\"symbol\":\"" << e.symbol << "\",\"when\":\"always\"}],\"workspace\":null"
+      << "\"entries\":[{\"symbol\":\"" << e.symbol << "\",\"when\":\"always\"},{\"symbol\":\""
+      << L.entries.back().symbol << "\",\"when\":\"" << kStridedWhen << "\"}],\"workspace\":null"
       << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
       << ",\"fidelity_notes\":[" << json_str("the serial lift's own order: each column's prefix folds ascending (descending "
                                              "for a reverse scan) in the serial accumulator and rounds once per output; "
@@ -490,6 +531,7 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
         << ">(in, out, rows, cols, status, counter, ticket_base, epoch);\n}\n";
     L.entries.push_back(e);
   }
+  src << scan_strided_entry(f, L);
   L.threads = L.entries[0].threads;
   L.blocks_per_cu = 1;
   L.source = src.str();
@@ -506,7 +548,10 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
       << ",\"k\":" << L.entries[i].k << ",\"waves\":" << L.entries[i].wpb
       << ",\"block\":" << L.entries[i].threads << ",\"blocks_per_cu\":" << L.entries[i].blocks_per_cu
       << ",\"block_tile\":" << 64 * L.entries[i].vec * L.entries[i].k * L.entries[i].wpb << ",\"when\":\""
-      << (L.entries[i].fast ? "scanned extent % vec == 0 and in0/out 16-byte aligned" : "otherwise") << "\"}";
+      << (L.entries[i].strided ? kStridedWhen
+          : L.entries[i].fast  ? "scanned extent % vec == 0 and in0/out 16-byte aligned"
+                               : "otherwise")
+      << "\"}";
   j << "],\"workspace\":{\"status\":\"tiles * " << kScanStatusWords * 8
     << " bytes, zeroed once\",\"counter\":4,\"host_state\":[\"epoch\",\"ticket_base\"]}"
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
@@ -584,6 +629,21 @@ static int32_t lower_gather(const unp_form& f, Lowered& L, std::string& why) {
         << (batch ? ", ni" : "") << ");\n}\n";
     L.entries.push_back(e);
   }
+  {
+    // Storage images that are not the dense layout above: one lane per output element, the table,
+    // index and output addressed through their strides, the element moved as raw bits.
+    Entry e;
+    e.strided = true;
+    e.vec = (int)eb;
+    e.threads = 256;
+    e.blocks_per_cu = 8;
+    e.symbol = L.name + "_x";
+    const char* E = eb == 1 ? "unsigned char" : eb == 2 ? "unsigned short" : eb == 4 ? "unsigned int" : "unsigned long long";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(const " << E << "* table, const "
+        << I << "* ids, " << E << "* out, unp::gather_view v, " << I << " src_extent) {\n  unp::gather_strided<" << E
+        << ", " << I << ", " << f.oob << ">(table, ids, out, v, src_extent);\n}\n";
+    L.entries.push_back(e);
+  }
   L.source = src.str();
   std::ostringstream j;
   j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"gather\",\"dtype\":\"" << kind_name(f.dtype)
@@ -600,7 +660,10 @@ static int32_t lower_gather(const unp_form& f, Lowered& L, std::string& why) {
        "gathered one, the index 1-D over NI); whole rows of 64 x 8 units two at a time per wave\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"unit_bytes\":" << L.entries[i].vec
-      << ",\"when\":\"" << (L.entries[i].fast ? "row bytes % 16 == 0 and table/out 16-byte aligned" : "otherwise")
+      << ",\"when\":\""
+      << (L.entries[i].strided ? kStridedWhen
+          : L.entries[i].fast  ? "row bytes % 16 == 0 and table/out 16-byte aligned"
+                               : "otherwise")
       << "\"}";
   j << "],\"workspace\":null,\"fidelity_notes\":[" << json_str("a raw bit move: bit-exact for every grid and block")
     << "]}";

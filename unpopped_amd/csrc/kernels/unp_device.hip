@@ -680,6 +680,16 @@ UNP_DEV void reduce_generic(const T* __restrict__ in, T* __restrict__ out, const
   }
 }
 
+// A reduction over storage images (oracle/buffers.rs:16-42): the kept axes with their input and
+// output element strides, the reduced axes with their input strides, any signs.  A dense
+// row-major reduction is the special case of row-major strides.
+struct red_view {
+  i64 nk, nr;
+  i64 kext[8], kstr[8], kost[8];
+  i64 rext[8], rstr[8];
+  i64 outs, count;
+};
+
 // ---------------------------------------------------------------------------------------
 // A fold whose result depends on its order and has no declared bound (a float Prod: every f64
 // product rounds): the serial lift's order itself (kernel_lift.rs:919-941), one lane per output,
@@ -687,15 +697,17 @@ UNP_DEV void reduce_generic(const T* __restrict__ in, T* __restrict__ out, const
 // accumulator seeded with 1, one rounding to T at the store.  Bit-exact to the serial lift; not a
 // fast schedule (the dependent multiplies are the critical path).
 // ---------------------------------------------------------------------------------------
+
 template <class T, int THREADS>
-UNP_DEV void reduce_serial_prod(const T* __restrict__ in, T* __restrict__ out, const axes_desc& d) {
+UNP_DEV void reduce_serial_prod(const T* __restrict__ in, T* __restrict__ out, const red_view d) {
   const i64 stride = (i64)gridDim.x * THREADS;
   for (i64 o = (i64)blockIdx.x * THREADS + threadIdx.x; o < d.outs; o += stride) {
-    i64 off = 0, q = o;
+    i64 off = 0, oo = 0, q = o;
     for (i64 k = d.nk - 1; k >= 0; --k) {
       const i64 c = q % d.kext[k];
       q /= d.kext[k];
       off += c * d.kstr[k];
+      oo += c * d.kost[k];
     }
     i64 ctr[8];
     for (i64 k = 0; k < d.nr; ++k) ctr[k] = 0;
@@ -710,7 +722,38 @@ UNP_DEV void reduce_serial_prod(const T* __restrict__ in, T* __restrict__ out, c
         ctr[k] = 0;
       }
     }
-    out[o] = (T)a;
+    out[oo] = (T)a;
+  }
+}
+
+// Any order-free fold over storage images: one wave per output (as reduce_generic), the input and
+// the output read and written through their strides.
+template <class T, int OP, int THREADS>
+UNP_DEV void reduce_strided(const T* __restrict__ in, T* __restrict__ out, const red_view d) {
+  typedef typename acc<T, OP>::type Ac;
+  typedef fold<Ac, OP> F;
+  const int lane = threadIdx.x & 63;
+  const i64 nw = (i64)gridDim.x * (THREADS / 64);
+  for (i64 o = (i64)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6); o < d.outs; o += nw) {
+    i64 base = 0, oo = 0, q = o;
+    for (i64 k = d.nk - 1; k >= 0; --k) {
+      const i64 c = q % d.kext[k];
+      q /= d.kext[k];
+      base += c * d.kstr[k];
+      oo += c * d.kost[k];
+    }
+    Ac a = F::identity();
+    for (i64 t = lane; t < d.count; t += 64) {
+      i64 off = base, u = t;
+      for (i64 k = d.nr - 1; k >= 0; --k) {
+        const i64 c = u % d.rext[k];
+        u /= d.rext[k];
+        off += c * d.rstr[k];
+      }
+      a = F::apply(a, (Ac)in[off]);
+    }
+    a = wave_reduce<Ac, OP>(a);
+    if (lane == 0) out[oo] = finish<T, OP>(a, d.count);
   }
 }
 
@@ -913,6 +956,45 @@ UNP_DEV void scan_seq(const T* __restrict__ in, T* __restrict__ out, i64 A, i64 
       } else {
         v = F::apply(v, (Ac)xv);
         out[off] = scan_out<T, OP>(v, i + 1);
+      }
+    }
+  }
+}
+
+// A scan over storage images: the non-scanned axes (extents, input and output strides) and the
+// scanned axis (extent, input and output strides), any signs.  One lane per column, the serial
+// lift's order (as scan_seq): bit-exact for every op.
+struct scan_view {
+  i64 nc;
+  i64 cext[8], cin[8], cout[8];
+  i64 S, sin, sout;
+  i64 cols;
+};
+
+template <class T, int OP, bool EXCL, bool REV>
+UNP_DEV void scan_strided(const T* __restrict__ in, T* __restrict__ out, const scan_view v) {
+  typedef typename serial_acc<T>::type Ac;
+  typedef fold<Ac, OP> F;
+  const i64 stride = (i64)gridDim.x * blockDim.x;
+  for (i64 c = (i64)blockIdx.x * blockDim.x + threadIdx.x; c < v.cols; c += stride) {
+    i64 bi = 0, bo = 0, q = c;
+    for (i64 k = v.nc - 1; k >= 0; --k) {
+      const i64 x = q % v.cext[k];
+      q /= v.cext[k];
+      bi += x * v.cin[k];
+      bo += x * v.cout[k];
+    }
+    Ac acc_ = F::identity();
+    for (i64 i = 0; i < v.S; ++i) {
+      const i64 s = REV ? v.S - 1 - i : i;
+      const T x = in[bi + s * v.sin];
+      T* o = out + bo + s * v.sout;
+      if constexpr (EXCL) {
+        *o = scan_out<T, OP>(acc_, i);
+        acc_ = F::apply(acc_, (Ac)x);
+      } else {
+        acc_ = F::apply(acc_, (Ac)x);
+        *o = scan_out<T, OP>(acc_, i + 1);
       }
     }
   }
@@ -1512,6 +1594,42 @@ UNP_DEV void gather_rows(const u8* __restrict__ table, const IDX* __restrict__ i
         if (uu < units) st_nt<E, N>(dst + uu * N, v[k]);
       }
     }
+  }
+}
+
+// A gather over storage images (the gather lift's cell, gather.rs:184-232, at every output
+// coordinate): the output extents, the table's strides (its stride along the gathered axis applies
+// to the clamped index), the index's strides over the output coordinates (a full-shape index, or a
+// 1-D one broadcast with zero strides), the output's strides.  One lane per output element; the
+// element moves as raw bits of E.
+struct gather_view {
+  i64 rank, axis;
+  i64 ext[8], tstr[8], istr[8], ostr[8];
+  i64 outs;
+};
+
+template <class E, class IDX, int POLICY>
+UNP_DEV void gather_strided(const E* __restrict__ table, const IDX* __restrict__ ids, E* __restrict__ out,
+                            const gather_view v, IDX src_extent) {
+  const i64 stride = (i64)gridDim.x * blockDim.x;
+  for (i64 o = (i64)blockIdx.x * blockDim.x + threadIdx.x; o < v.outs; o += stride) {
+    i64 t = 0, ix = 0, oo = 0, q = o;
+    for (i64 k = v.rank - 1; k >= 0; --k) {
+      const i64 c = q % v.ext[k];
+      q /= v.ext[k];
+      if (k != v.axis) t += c * v.tstr[k];
+      ix += c * v.istr[k];
+      oo += c * v.ostr[k];
+    }
+    const IDX raw = ids[ix];
+    const bool below = below_zero(raw);
+    const bool oob = below || !(raw < src_extent);
+    if (oob && POLICY != OOB_CLAMP) {
+      if constexpr (POLICY == OOB_ZEROFILL) out[oo] = (E)0;
+      continue;
+    }
+    const IDX cl = below ? (IDX)0 : (oob ? (IDX)(src_extent - (IDX)1) : raw);
+    out[oo] = table[t + (i64)cl * v.tstr[v.axis]];
   }
 }
 

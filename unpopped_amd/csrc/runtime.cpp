@@ -524,6 +524,48 @@ void fill_axes_desc(const std::vector<int64_t>& ext, int32_t rank, uint32_t mask
   }
 }
 
+// Appends axis (e, is, os) to a descriptor's list, merged into the previous axis when the two
+// walk storage as one (the previous stride is this axis's extent times its stride, in every
+// buffer); axes of extent 1 add nothing.
+template <int NS>
+void add_axis(long long* ext, long long* const (&str)[NS], long long& n, long long e, const long long (&st)[NS]) {
+  if (e == 1) return;
+  if (n > 0) {
+    bool merge = true;
+    for (int k = 0; k < NS; ++k) merge = merge && str[k][n - 1] == e * st[k];
+    if (merge) {
+      ext[n - 1] *= e;
+      for (int k = 0; k < NS; ++k) str[k][n - 1] = st[k];
+      return;
+    }
+  }
+  ext[n] = e;
+  for (int k = 0; k < NS; ++k) str[k][n] = st[k];
+  ++n;
+}
+
+// The kept and reduced axes of a reduction over storage images: in_str[a] is the input's element
+// stride along axis a, out_str[a] the output's along kept axis a (ignored for reduced axes).
+void fill_red_view(const std::vector<int64_t>& ext, int32_t rank, uint32_t mask, const long long* in_str,
+                   const long long* out_str, unp::red_view_host& d) {
+  long long* const kstrs[2] = {d.kstr, d.kost};
+  long long* const rstrs[1] = {d.rstr};
+  for (int32_t a = 0; a < rank; ++a) {
+    if ((mask >> a) & 1u) {
+      const long long st[1] = {in_str[a]};
+      add_axis<1>(d.rext, rstrs, d.nr, ext[(size_t)a], st);
+    } else {
+      const long long st[2] = {in_str[a], out_str[a]};
+      add_axis<2>(d.kext, kstrs, d.nk, ext[(size_t)a], st);
+    }
+  }
+}
+
+static_assert(sizeof(unp::red_view_host) == 44 * 8, "red_view_host mirrors the device's red_view");
+static_assert(sizeof(unp::scan_view_host) == 29 * 8, "scan_view_host mirrors the device's scan_view");
+static_assert(sizeof(unp::gather_view_host) == 35 * 8, "gather_view_host mirrors the device's gather_view");
+static_assert(sizeof(unp::axes_desc_host) == 36 * 8, "axes_desc_host mirrors the device's axes_desc");
+
 // At least n zeroed ticket counters.  Kernels leave every counter they use at zero, so a
 // larger array is allocated afresh (and zeroed) only when a launch needs more strips.
 int32_t ensure_counters(unp_exec* x, size_t n, unp_error* err) {
@@ -565,12 +607,18 @@ int32_t launch(unp_exec* x, size_t entry, uint32_t grid, void** params, hipStrea
   return UNP_OK;
 }
 
+// The pointer-launch entry for the arguments' alignment and row length (entries that read
+// through storage-image strides are never picked here).
 size_t pick(const unp_exec* x, bool fast_ok, bool wide = false) {
-  for (size_t i = 0; i < x->l.entries.size(); ++i)
-    if (x->l.entries[i].fast == fast_ok && x->l.entries[i].wide == wide) return i;
-  for (size_t i = 0; i < x->l.entries.size(); ++i)
-    if (!x->l.entries[i].fast && x->l.entries[i].wide == wide) return i;
-  return x->l.entries.size() - 1;
+  const std::vector<unp::Entry>& es = x->l.entries;
+  for (size_t i = 0; i < es.size(); ++i)
+    if (!es[i].strided && es[i].fast == fast_ok && es[i].wide == wide) return i;
+  for (size_t i = 0; i < es.size(); ++i)
+    if (!es[i].strided && !es[i].fast && es[i].wide == wide) return i;
+  size_t last = 0;
+  for (size_t i = 0; i < es.size(); ++i)
+    if (!es[i].strided) last = i;
+  return last;
 }
 
 int64_t product(const std::vector<int64_t>& v, size_t from, size_t to) {
@@ -684,16 +732,36 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
       void* params[] = {&in, &out, &a, &r, &b, &S, &ws, &cnt};
       return launch(x, entry, (uint32_t)grid, params, s, err);
     }
-    // Any other mask (a wave per output), or the serial product (a lane per output).
+    const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
+    if (sched == 'q') {
+      // The serial product (a lane per output) takes the storage-image descriptor, here with the
+      // row-major strides of the input and of the kept-axes output.
+      std::vector<long long> in_str((size_t)f.rank), out_str((size_t)f.rank, 0);
+      long long si = 1, so = 1;
+      for (int32_t k = f.rank - 1; k >= 0; --k) {
+        in_str[(size_t)k] = si;
+        si *= A.ext[(size_t)k];
+        if (!((mask >> k) & 1u)) {
+          out_str[(size_t)k] = so;
+          so *= A.ext[(size_t)k];
+        }
+      }
+      unp::red_view_host d{};
+      fill_red_view(A.ext, f.rank, mask, in_str.data(), out_str.data(), d);
+      d.outs = outs;
+      d.count = count;
+      const long long want = (outs + 255) / 256;
+      void* params[] = {&in, &out, &d};
+      return launch(x, 0, (uint32_t)(want < cap ? want : cap), params, s, err);
+    }
+    // Any other mask: a wave per output.
     unp::axes_desc_host d{};
     fill_axes_desc(A.ext, f.rank, mask, d);
     d.outs = outs;
     d.count = count;
-    const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
-    const long long want = sched == 'q' ? (outs + 255) / 256 : (outs + 3) / 4;
-    const uint32_t grid = (uint32_t)(want < cap ? want : cap);
+    const long long want = (outs + 3) / 4;
     void* params[] = {&in, &out, &d};
-    return launch(x, 0, grid, params, s, err);
+    return launch(x, 0, (uint32_t)(want < cap ? want : cap), params, s, err);
   }
   const long long rows = product(A.ext, 0, (size_t)f.reduced_from);
   const long long cols = product(A.ext, (size_t)f.reduced_from, (size_t)f.rank);
@@ -987,61 +1055,389 @@ static int view_elem_bits(const unp_form& f, size_t b) {
   return by ? (int)(8 * by) : 4;  // the sub-byte kinds this backend reads are 4-bit
 }
 
-// A view the kernels can read: dense row-major from its base (an axis of extent 0 or 1 may carry
-// any stride), or the gather index's column broadcast [n, d] with strides [1, 0].
-static bool view_readable(const unp_view& v, bool index_broadcast_ok) {
+namespace {
+
+int64_t low_i32(int64_t v) { return (int64_t)(int32_t)(uint32_t)(uint64_t)v; }
+
+// The buffer and scalar parameters of a lowered form's KernelFn.
+void param_counts(const unp_exec* x, size_t& nbuf, size_t& nscal) {
+  const unp_form& f = x->l.form;
+  nbuf = nscal = 0;
+  switch (f.kind) {
+    case UNP_FORM_REDUCTION: nbuf = (size_t)x->l.rx.n_inputs + 1; nscal = (size_t)f.rank; break;
+    case UNP_FORM_ROW_REDUCE2: nbuf = 3; nscal = 2; break;
+    case UNP_FORM_SCAN: nbuf = 2; nscal = (size_t)f.rank; break;
+    case UNP_FORM_GATHER: nbuf = 3; nscal = (size_t)f.rank + 1; break;
+    case UNP_FORM_ROW_REDUCE: nbuf = (size_t)x->l.rr.n_inputs + 1; nscal = (size_t)x->l.rr.rank; break;
+    case UNP_FORM_DEQUANT4: nbuf = 4; nscal = 2; break;
+    case UNP_FORM_DEQUANT_GEMM: nbuf = 5; nscal = 3; break;
+    default: break;
+  }
+}
+
+// The shape a buffer parameter's view must have, from the form and the extent scalars (the
+// extents every access of the KernelFn ranges over).  A reduction's output may also take the
+// keepdim shape (the input's rank, its reduced axes of extent 1); a gather's table has the
+// output's extents except along the gathered axis, where it holds at least src_extent rows.
+struct Want {
+  std::vector<int64_t> shape;
+  std::vector<int64_t> keepdim;  // empty: no alternative
+  int table_axis = -1;
+  int64_t table_rows = 0;
+};
+
+int64_t ceil_div(int64_t a, int64_t b) { return b > 0 ? (a + b - 1) / b : 0; }
+
+// The gather's source extent as its index type reads it (negative: no row is ever read).
+int64_t gather_src_extent(const unp_form& f, int64_t raw) {
+  if (f.index_dtype == UNP_I32) return low_i32(raw);
+  if (f.index_dtype == UNP_U32) return (int64_t)(uint32_t)(uint64_t)raw;
+  return raw;
+}
+
+std::vector<Want> wanted_shapes(const unp_exec* x, const std::vector<int64_t>& ext, const int64_t* sc) {
+  const unp_form& f = x->l.form;
+  std::vector<Want> w;
+  auto one = [&](std::vector<int64_t> s) {
+    Want a;
+    a.shape = std::move(s);
+    w.push_back(a);
+  };
+  switch (f.kind) {
+    case UNP_FORM_REDUCTION:
+    case UNP_FORM_ROW_REDUCE2: {
+      const bool two = f.kind == UNP_FORM_ROW_REDUCE2;
+      const size_t nin = two ? 1 : (size_t)x->l.rx.n_inputs;
+      for (size_t k = 0; k < nin; ++k) one(ext);
+      Want o;
+      std::vector<int64_t> kd(ext);
+      for (int32_t d = 0; d < f.rank; ++d) {
+        if ((x->l.axes_mask >> d) & 1u) kd[(size_t)d] = 1;
+        else o.shape.push_back(ext[(size_t)d]);
+      }
+      if (!two) o.keepdim = kd;
+      w.push_back(o);
+      if (two) w.push_back(o);
+      break;
+    }
+    case UNP_FORM_SCAN:
+      one(ext);
+      one(ext);
+      break;
+    case UNP_FORM_GATHER: {
+      Want t;
+      t.shape = ext;
+      t.table_axis = x->l.scan_axis;
+      t.table_rows = std::max<int64_t>(0, gather_src_extent(f, sc[f.rank]));
+      Want i;
+      i.shape = ext;
+      w.push_back(f.data_slot == 0 ? t : i);
+      w.push_back(f.data_slot == 0 ? i : t);
+      one(ext);
+      break;
+    }
+    case UNP_FORM_ROW_REDUCE:
+      for (int32_t k = 0; k <= x->l.rr.n_inputs; ++k) one(ext);
+      break;
+    case UNP_FORM_DEQUANT4: {
+      const int64_t R = ext[0], C = ext[1], ng = ceil_div(C, f.group);
+      one({R * C});
+      one({R * ng});
+      one({R * ng});
+      one({R * C});
+      break;
+    }
+    case UNP_FORM_DEQUANT_GEMM: {
+      const int64_t R = ext[0], K = ext[1], C = ext[2], ng = ceil_div(K, f.group);
+      one({R * K});
+      one({R * ng});
+      one({R * ng});
+      one({K * C});
+      one({R * C});
+      break;
+    }
+    default:
+      break;
+  }
+  return w;
+}
+
+std::string shape_text(const int64_t* s, size_t n) {
+  std::string t = "[";
+  for (size_t d = 0; d < n; ++d) t += (d ? ", " : "") + std::to_string(s[d]);
+  return t + "]";
+}
+
+bool shape_is(const unp_view& v, const std::vector<int64_t>& s) {
+  if ((size_t)v.rank != s.size()) return false;
+  for (size_t d = 0; d < s.size(); ++d)
+    if (v.shape[d] != s[d]) return false;
+  return true;
+}
+
+// Whether view v has the shape `want` asks for; `why` says how it differs.
+bool shape_ok(const unp_view& v, const Want& want, std::string& why) {
+  if (want.table_axis >= 0) {
+    bool ok = (size_t)v.rank == want.shape.size();
+    for (size_t d = 0; ok && d < want.shape.size(); ++d)
+      ok = (int)d == want.table_axis ? v.shape[d] >= want.table_rows : v.shape[d] == want.shape[d];
+    if (!ok) {
+      std::vector<int64_t> t(want.shape);
+      t[(size_t)want.table_axis] = want.table_rows;
+      why = "the table view has shape " + shape_text(v.shape, (size_t)v.rank) + "; the extents ask for " +
+            shape_text(t.data(), t.size()) + " (at least " + std::to_string(want.table_rows) + " along axis " +
+            std::to_string(want.table_axis) + ")";
+    }
+    return ok;
+  }
+  if (shape_is(v, want.shape) || (!want.keepdim.empty() && shape_is(v, want.keepdim))) return true;
+  why = "the view has shape " + shape_text(v.shape, (size_t)v.rank) + "; the extents ask for " +
+        shape_text(want.shape.data(), want.shape.size()) +
+        (want.keepdim.empty() ? std::string() : " or " + shape_text(want.keepdim.data(), want.keepdim.size()));
+  return false;
+}
+
+bool view_empty(const unp_view& v) {
   for (int d = 0; d < v.rank; ++d)
-    if (v.shape[d] == 0) return true;  // empty: nothing is read
-  if (index_broadcast_ok && v.rank == 2 && v.stride[0] == 1 && v.stride[1] == 0) return true;
+    if (v.shape[d] == 0) return true;
+  return false;
+}
+
+// Dense row-major from its base: every axis longer than one has the row-major stride.
+bool row_major(const unp_view& v) {
   int64_t expect = 1;
   for (int d = v.rank - 1; d >= 0; --d) {
-    if (v.shape[d] < 0) return false;
     if (v.shape[d] > 1 && v.stride[d] != expect) return false;
     expect *= v.shape[d];
   }
   return true;
 }
 
+// The gather index as the dense kernels read it: one id per position of the gathered axis, the
+// other axes broadcast (stride 0), e.g. the embedding's [n, d] ids with strides [1, 0]
+// (tests/kernel_parallel_gather_agrees.rs:80-84).
+bool index_broadcast(const unp_view& v, int axis) {
+  for (int d = 0; d < v.rank; ++d) {
+    if (v.shape[d] <= 1) continue;
+    if (d == axis ? v.stride[d] != 1 : v.stride[d] != 0) return false;
+  }
+  return true;
+}
+
+// Whether every view suits the pointer-launch kernels (dense row-major storage from the base).
+bool views_dense(const unp_exec* x, const unp_view* v, size_t n, int64_t src_extent) {
+  const unp_form& f = x->l.form;
+  for (size_t b = 0; b < n; ++b) {
+    if (view_empty(v[b])) continue;
+    if (f.kind == UNP_FORM_GATHER && b < 2) {
+      const int ax = x->l.scan_axis;
+      if ((int)b == f.data_slot) {
+        if (!row_major(v[b])) return false;
+        // The dense kernels step A x src_extent rows: a table longer along a gathered axis
+        // after the first needs the strides.
+        if (ax > 0 && v[b].shape[ax] != src_extent) return false;
+      } else if (!index_broadcast(v[b], ax)) {
+        return false;
+      }
+      continue;
+    }
+    if (!row_major(v[b])) return false;
+  }
+  return true;
+}
+
+int32_t invalid(unp_error* err, const std::string& what) {
+  set_error(err, UNP_INVALID_ARGUMENT, what);
+  return UNP_INVALID_ARGUMENT;
+}
+
+// Checks shared by every launch of an executor: the device, the error, the timing state.
+int32_t begin_launch(unp_exec* x, unp_error* err) {
+  set_error(err, UNP_OK, "");
+  x->t_first = true;
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur != x->device)
+    return invalid(err, "the executor was created on another device");
+  return UNP_OK;
+}
+
+uint32_t lanes_grid(const unp_exec* x, long long items, long long per_block) {
+  const long long cap = (long long)x->cu_count * 8;
+  const long long want = (items + per_block - 1) / per_block;
+  return (uint32_t)(want < cap ? want : cap);
+}
+
+size_t strided_entry(const unp_exec* x, int which) {
+  for (size_t i = 0; i < x->l.entries.size(); ++i)
+    if (x->l.entries[i].strided && which-- == 0) return i;
+  return SIZE_MAX;
+}
+
+uint64_t view_ptr(const unp_view& v, size_t elem_bytes) { return v.data + (uint64_t)(v.base * (int64_t)elem_bytes); }
+
+// A plain reduction (or the fused row fold) over storage images: one launch per output.
+int32_t strided_reduction(unp_exec* x, const unp_view* v, const std::vector<int64_t>& ext, hipStream_t s,
+                          unp_error* err) {
+  const unp_form& f = x->l.form;
+  const bool two = f.kind == UNP_FORM_ROW_REDUCE2;
+  const uint32_t mask = x->l.axes_mask;
+  long long outs = 1, count = 1;
+  for (int32_t d = 0; d < f.rank; ++d) ((mask >> d) & 1u ? count : outs) *= ext[(size_t)d];
+  if (outs == 0) return UNP_OK;
+  const size_t eb = unp::kind_bytes(f.dtype);
+  for (int o = 0; o < (two ? 2 : 1); ++o) {
+    const unp_view& in = v[0];
+    const unp_view& ov = v[1 + o];
+    const bool keepdim = ov.rank == f.rank;
+    long long in_str[UNP_MAX_RANK], out_str[UNP_MAX_RANK];
+    for (int32_t a = 0, kept = 0; a < f.rank; ++a) {
+      in_str[a] = in.stride[a];
+      out_str[a] = 0;
+      if (!((mask >> a) & 1u)) out_str[a] = keepdim ? ov.stride[a] : ov.stride[kept++];
+    }
+    unp::red_view_host d{};
+    fill_red_view(ext, f.rank, mask, in_str, out_str, d);
+    d.outs = outs;
+    d.count = count;
+    const size_t entry = strided_entry(x, o);
+    uint64_t ip = view_ptr(in, eb), op = view_ptr(ov, eb);
+    void* params[] = {&ip, &op, &d};
+    const uint32_t grid = lanes_grid(x, outs, x->l.red_schedule == 'q' ? 256 : 4);
+    const int32_t rc = launch(x, entry, grid, params, s, err);
+    if (rc != UNP_OK) return rc;
+  }
+  return UNP_OK;
+}
+
+// A scan over storage images: one lane per column, the scanned axis walked through its strides.
+int32_t strided_scan(unp_exec* x, const unp_view* v, const std::vector<int64_t>& ext, hipStream_t s, unp_error* err) {
+  const unp_form& f = x->l.form;
+  const int ax = x->l.scan_axis;
+  unp::scan_view_host d{};
+  long long* const strs[2] = {d.cin, d.cout};
+  long long cols = 1;
+  for (int a = 0; a < f.rank; ++a) {
+    if (a == ax) continue;
+    cols *= ext[(size_t)a];
+    const long long st[2] = {v[0].stride[a], v[1].stride[a]};
+    add_axis<2>(d.cext, strs, d.nc, ext[(size_t)a], st);
+  }
+  d.S = ext[(size_t)ax];
+  d.sin = v[0].stride[ax];
+  d.sout = v[1].stride[ax];
+  d.cols = cols;
+  if (cols == 0 || d.S == 0) return UNP_OK;
+  const size_t eb = unp::kind_bytes(f.dtype);
+  uint64_t ip = view_ptr(v[0], eb), op = view_ptr(v[1], eb);
+  void* params[] = {&ip, &op, &d};
+  return launch(x, strided_entry(x, 0), lanes_grid(x, cols, 256), params, s, err);
+}
+
+// A gather over storage images: one lane per output element.
+int32_t strided_gather(unp_exec* x, const unp_view* v, const std::vector<int64_t>& ext, int64_t raw_src,
+                       hipStream_t s, unp_error* err) {
+  const unp_form& f = x->l.form;
+  const unp_view& tv = v[f.data_slot == 0 ? 0 : 1];
+  const unp_view& iv = v[f.data_slot == 0 ? 1 : 0];
+  const unp_view& ov = v[2];
+  unp::gather_view_host d{};
+  d.rank = f.rank;
+  d.axis = x->l.scan_axis;
+  long long outs = 1;
+  for (int a = 0; a < f.rank; ++a) {
+    d.ext[a] = ext[(size_t)a];
+    d.tstr[a] = tv.stride[a];
+    d.istr[a] = iv.stride[a];
+    d.ostr[a] = ov.stride[a];
+    outs *= ext[(size_t)a];
+  }
+  d.outs = outs;
+  if (outs == 0) return UNP_OK;
+  const int64_t src = gather_src_extent(f, raw_src);
+  if (src <= 0 && f.oob == UNP_OOB_CLAMP) return invalid(err, "a Clamp gather needs a source extent of at least 1");
+  const size_t eb = unp::kind_bytes(f.dtype), ib = unp::kind_bytes(f.index_dtype);
+  uint64_t tp = view_ptr(tv, eb), ip = view_ptr(iv, ib), op = view_ptr(ov, eb);
+  int32_t e32 = (int32_t)src;
+  uint32_t eu32 = (uint32_t)src;
+  long long e64 = src;
+  void* ext_arg = f.index_dtype == UNP_I32 ? (void*)&e32 : (f.index_dtype == UNP_U32 ? (void*)&eu32 : (void*)&e64);
+  void* params[] = {&tp, &ip, &op, &d, ext_arg};
+  return launch(x, strided_entry(x, 0), lanes_grid(x, outs, 256), params, s, err);
+}
+
+}  // namespace
+
 extern "C" int32_t unp_hip_exec_launch_views(unp_exec* x, const unp_view* views, size_t nviews,
                                              const int64_t* scalars, size_t nscalars, void* stream,
                                              unp_error* err) {
-  if (!x) {
-    set_error(err, UNP_INVALID_ARGUMENT, "null executor");
-    return UNP_INVALID_ARGUMENT;
+  if (!x) return invalid(err, "null executor");
+  if ((nviews && !views) || (nscalars && !scalars)) return invalid(err, "null views or scalars");
+  const unp_form& f = x->l.form;
+  size_t nbuf = 0, nscal = 0;
+  param_counts(x, nbuf, nscal);
+  if (nviews != nbuf || nscalars != nscal)
+    return invalid(err, "expected " + std::to_string(nbuf) + " views and " + std::to_string(nscal) + " scalars, got " +
+                            std::to_string(nviews) + " and " + std::to_string(nscalars));
+  // The extents: the leading scalars, I32 as the KernelFn declares them.
+  const size_t n_ext = f.kind == UNP_FORM_ROW_REDUCE ? (size_t)x->l.rr.rank
+                       : f.kind == UNP_FORM_GATHER   ? (size_t)f.rank
+                                                     : nscal;
+  std::vector<int64_t> ext(n_ext);
+  for (size_t i = 0; i < n_ext; ++i) {
+    ext[i] = low_i32(scalars[i]);
+    if (ext[i] < 0) return invalid(err, "extent n" + std::to_string(i) + " is negative");
   }
-  if ((nviews && !views) || (nscalars && !scalars)) {
-    set_error(err, UNP_INVALID_ARGUMENT, "null views or scalars");
-    return UNP_INVALID_ARGUMENT;
-  }
-  std::vector<unp_arg> args(nviews + nscalars);
+  const std::vector<Want> want = wanted_shapes(x, ext, scalars);
+  if (want.size() != nbuf) return invalid(err, "unknown form");
   for (size_t b = 0; b < nviews; ++b) {
     const unp_view& v = views[b];
-    if (v.rank < 0 || v.rank > UNP_MAX_RANK) {
-      set_error(err, UNP_INVALID_ARGUMENT, "buffer " + std::to_string(b) + ": rank out of range");
-      return UNP_INVALID_ARGUMENT;
+    const std::string at = "buffer " + std::to_string(b) + ": ";
+    if (v.rank < 0 || v.rank > UNP_MAX_RANK) return invalid(err, at + "rank out of range");
+    std::string why;
+    if (!shape_ok(v, want[b], why)) return invalid(err, at + why);
+    if (view_empty(v)) continue;
+    // Every element the view names must lie at or above the storage start, and its offsets must
+    // stay well inside the kernels' 64-bit index arithmetic.
+    const int bits = view_elem_bits(f, b);
+    __int128 lo = v.base, hi = v.base;
+    for (int d = 0; d < v.rank; ++d) {
+      const __int128 span = (__int128)v.stride[d] * (v.shape[d] - 1);
+      (span < 0 ? lo : hi) += span;
     }
-    const bool index_buffer = x->l.form.kind == UNP_FORM_GATHER && b < 2 && (int)b != x->l.form.data_slot;
-    if (!view_readable(v, index_buffer)) {
-      set_error(err, UNP_INVALID_ARGUMENT,
-                "buffer " + std::to_string(b) +
-                    ": a strided view; this backend's kernels read dense row-major storage, so make the view "
-                    "contiguous first");
-      return UNP_INVALID_ARGUMENT;
-    }
-    const int bits = view_elem_bits(x->l.form, b);
-    if (v.base < 0 || (v.base * bits) % 8 != 0) {
-      set_error(err, UNP_INVALID_ARGUMENT,
-                "buffer " + std::to_string(b) + ": the base offset must be a whole byte and not negative");
-      return UNP_INVALID_ARGUMENT;
-    }
-    args[b].is_buffer = 1;
-    args[b].value = v.data + (uint64_t)(v.base * bits / 8);
+    if (lo < 0) return invalid(err, at + "the view reaches below its storage (base plus its negative strides < 0)");
+    if (hi > ((__int128)1 << 60)) return invalid(err, at + "the view's offsets exceed 2^60 elements");
+    if (bits < 8 && (v.base * bits) % 8 != 0)
+      return invalid(err, at + "a 4-bit view must start on a whole byte (an even base)");
+    if (!v.data) return invalid(err, at + "null storage");
   }
-  for (size_t i = 0; i < nscalars; ++i) {
-    args[nviews + i].is_buffer = 0;
-    args[nviews + i].value = (uint64_t)scalars[i];
+  const int64_t raw_src = f.kind == UNP_FORM_GATHER ? scalars[f.rank] : 0;
+  const int64_t src = f.kind == UNP_FORM_GATHER ? gather_src_extent(f, raw_src) : 0;
+  if (views_dense(x, views, nviews, src)) {
+    std::vector<unp_arg> args(nviews + nscalars);
+    for (size_t b = 0; b < nviews; ++b) {
+      const int bits = view_elem_bits(f, b);
+      args[b].is_buffer = 1;
+      args[b].value = views[b].data + (uint64_t)(views[b].base * bits / 8);
+    }
+    for (size_t i = 0; i < nscalars; ++i) {
+      args[nviews + i].is_buffer = 0;
+      args[nviews + i].value = (uint64_t)scalars[i];
+    }
+    return unp_hip_exec_launch(x, args.data(), args.size(), stream, err);
   }
-  return unp_hip_exec_launch(x, args.data(), args.size(), stream, err);
+  // Some view is transposed, strided, reversed or broadcast: the forms with a strided entry read
+  // through the strides; the others read dense storage only.
+  const bool plain_reduction = (f.kind == UNP_FORM_REDUCTION && x->l.rx.plain) || f.kind == UNP_FORM_ROW_REDUCE2;
+  if (!plain_reduction && f.kind != UNP_FORM_SCAN && f.kind != UNP_FORM_GATHER)
+    return invalid(err,
+                   "a view that is not dense row-major: this form reads dense storage (the plain reduction, scan "
+                   "and gather forms read any strides), so make the view contiguous first");
+  const int32_t rc = begin_launch(x, err);
+  if (rc != UNP_OK) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  if (plain_reduction) return strided_reduction(x, views, ext, s, err);
+  if (f.kind == UNP_FORM_SCAN) return strided_scan(x, views, ext, s, err);
+  return strided_gather(x, views, ext, raw_src, s, err);
 }
 
 extern "C" int32_t unp_hip_exec_launch(unp_exec* x, const unp_arg* args, size_t nargs, void* stream,
@@ -1050,13 +1446,8 @@ extern "C" int32_t unp_hip_exec_launch(unp_exec* x, const unp_arg* args, size_t 
     set_error(err, UNP_INVALID_ARGUMENT, "null executor");
     return UNP_INVALID_ARGUMENT;
   }
-  set_error(err, UNP_OK, "");
-  x->t_first = true;
-  int cur = -1;
-  if (hipGetDevice(&cur) != hipSuccess || cur != x->device) {
-    set_error(err, UNP_INVALID_ARGUMENT, "the executor was created on another device");
-    return UNP_INVALID_ARGUMENT;
-  }
+  const int32_t rc = begin_launch(x, err);
+  if (rc != UNP_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   switch (x->l.form.kind) {
     case UNP_FORM_REDUCTION:

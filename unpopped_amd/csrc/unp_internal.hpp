@@ -31,6 +31,9 @@ struct Entry {
   int threads = 0;    // block size of this entry (0: the form's)
   int blocks_per_cu = 0;  // persistent blocks per CU of this entry (0: the form's)
   int cols = 0;           // output columns per block (dequant GEMM decode entries)
+  // Reads and writes its buffers through storage-image strides (unp_hip_exec_launch_views with a
+  // view that is not dense row-major); never picked for a pointer launch.
+  bool strided = false;
 };
 
 // Scan tile status: words per tile (a 256-byte stride: the status of consecutive tiles, which
@@ -51,6 +54,26 @@ struct axes_desc_host {
   long long kext[8], kstr[8];
   long long rext[8], rstr[8];
   long long outs, count;
+};
+
+// Host images of the storage-image descriptors (red_view, scan_view, gather_view; passed by
+// value): extents and signed element strides of the views, axes outermost first.
+struct red_view_host {
+  long long nk, nr;
+  long long kext[8], kstr[8], kost[8];
+  long long rext[8], rstr[8];
+  long long outs, count;
+};
+struct scan_view_host {
+  long long nc;
+  long long cext[8], cin[8], cout[8];
+  long long S, sin, sout;
+  long long cols;
+};
+struct gather_view_host {
+  long long rank, axis;
+  long long ext[8], tstr[8], istr[8], ostr[8];
+  long long outs;
 };
 
 // An Access::RowReduce (crates/unpopped/src/ir.rs:2114-2125): the stages' pre expressions and
