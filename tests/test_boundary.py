@@ -451,3 +451,344 @@ def test_mean_and_float_prod_scans_lift_only_sequentially():
     with pytest.raises(_lib.UnpError) as e:
         u.lift_scan("s", "I32", 1, "Mean")
     assert "integer Mean" in e.value.detail
+
+
+# ---------------------------------------------------------------------------------------
+# Recognition up to a consistent renumbering of locals and any key order
+# ---------------------------------------------------------------------------------------
+
+def renumber_locals(k: dict, perm: list[int]) -> dict:
+    """``k`` with local i renamed perm[i] everywhere it is referenced (the ScalarExpr leaf Local(n), the
+    ``local`` of Let/Load/Assign/For and of a Scalar parameter) and its locals list permuted to match."""
+    k = copy.deepcopy(k)
+
+    def walk(x):
+        if isinstance(x, dict):
+            if len(x) == 1 and isinstance(x.get("Local"), int):
+                x["Local"] = perm[x["Local"]]
+                return
+            for key, v in x.items():
+                if key == "local" and isinstance(v, int):
+                    x[key] = perm[v]
+                else:
+                    walk(v)
+        elif isinstance(x, list):
+            for v in x:
+                walk(v)
+
+    walk(k["params"])
+    walk(k["body"])
+    locs = [None] * len(k["locals"])
+    for old, new in enumerate(perm):
+        locs[new] = k["locals"][old]
+    k["locals"] = locs
+    return k
+
+
+def shuffle_keys(x, rng):
+    """The same JSON value with every object's keys in a random order."""
+    if isinstance(x, dict):
+        items = list(x.items())
+        rng.shuffle(items)
+        return {key: shuffle_keys(v, rng) for key, v in items}
+    if isinstance(x, list):
+        return [shuffle_keys(v, rng) for v in x]
+    return x
+
+
+def _renumber_cases():
+    from unpopped_amd import expr as X
+
+    x0, x1, r0 = X.input(0), X.input(1), X.reduced(0)
+    stages, epi = X.softmax()
+    out = [make for make, _, _ in CASES]
+    out += [
+        lambda: u.lift_reduction("xr", "F32", 2, "Sum", axes=(1,), launch=(256, 64), n_inputs=2, body=x0 * x1,
+                                 post=r0.sqrt()),
+        lambda: u.lift_reduction("xr", "F64", 3, "Max", axes=(0, 2), n_inputs=2, body=x0 - x1),
+        lambda: u.lift_reduction("mn", "F32", 2, "MaxNum", axes=(0,)),
+        lambda: u.lift_scan("s", "F64", 3, "Mean", axis=1, exclusive=True),
+        lambda: u.lift_gather("g", "I32", 3, "U32", axis=2, oob="Skip", launch=(64, 3)),
+        lambda: u.lift_row_reduce("softmax", "F32", 2, stages, epi, launch=(256, 64)),
+        lambda: u.lift_row_reduce("softmax", "F64", 3, stages, epi),
+    ]
+    return out
+
+
+@pytest.mark.parametrize("i", range(len(_renumber_cases())))
+def test_lower_kernel_tolerates_renumbered_locals_and_key_order(i):
+    """A kernel equal to a lift up to a consistent renumbering of its locals, with its object keys in any
+    order, is recognised as that lift and lowers to the same HIP source."""
+    import random
+
+    k = _renumber_cases()[i]()
+    b = u.HipBackend()
+    want = b.lower_kernel(k)
+    rng = random.Random(1000 + i)
+    for _ in range(3):
+        perm = list(range(len(k["locals"])))
+        rng.shuffle(perm)
+        moved = shuffle_keys(renumber_locals(k, perm), rng)
+        assert moved != k
+        g = b.lower_kernel(json.dumps(moved))
+        assert g.name == want.name and g.source == want.source
+        assert g.interface["lift"] == want.interface["lift"]
+    # the reverse numbering too (every id moves)
+    g = b.lower_kernel(renumber_locals(k, list(range(len(k["locals"])))[::-1]))
+    assert g.source == want.source
+
+
+def test_inconsistent_renumbering_is_refused():
+    """Renaming one reference of a local (not all of them) changes the kernel: refused."""
+    k = u.lift_reduction("r", "F32", 2, "Sum", launch=(256, 64))
+    text = json.dumps(k)
+    # the accumulator (local 5) renamed in its Let only: its folds still read local 5
+    bad = text.replace('{"Let": {"local": 5, "init"', '{"Let": {"local": 7, "init"', 1)
+    assert bad != text
+    with pytest.raises(_lib.UnpError) as e:
+        u.HipBackend().lower_kernel(bad)
+    assert e.value.kind == "UnsupportedKernel"
+    # a permuted locals list without renaming the references: the declared types no longer line up
+    k2 = copy.deepcopy(k)
+    k2["locals"] = k2["locals"][::-1]
+    with pytest.raises(_lib.UnpError) as e:
+        u.HipBackend().lower_kernel(k2)
+    assert e.value.kind == "UnsupportedKernel"
+
+
+# ---------------------------------------------------------------------------------------
+# The lifts' parameter names, local layout and statement skeletons, pinned to the reference
+# ---------------------------------------------------------------------------------------
+
+def _place(p):
+    (kind, b), = p.items()
+    return ("buf", b["buffer"]) if kind == "Logical" else ("shared", b["alloc"])
+
+
+def skeleton(block):
+    """Statement kinds with the locals and places they name, nested as in the body."""
+    out = []
+    for st in block:
+        (kind, b), = st.items()
+        if kind == "For":
+            out.append(("For", b["local"], skeleton(b["body"])))
+        elif kind == "Let":
+            out.append(("Let", b["local"]))
+        elif kind == "Load":
+            out.append(("Load", b["local"], _place(b["place"])))
+        elif kind == "Assign":
+            out.append(("Assign", b["local"]))
+        elif kind == "Store":
+            out.append(("Store", _place(b["place"])))
+        elif kind == "If":
+            out.append(("If", skeleton(b["then"]), skeleton(b["els"])))
+        elif kind == "While":
+            out.append(("While", skeleton(b["body"])))
+        else:
+            out.append((kind,))
+    return out
+
+
+def _sig(k):
+    params = []
+    for p in k["params"]:
+        (kind, b), = p["kind"].items()
+        params.append((p["name"], kind, b.get("rank") if kind == "Buffer" else b["local"]))
+    return params, [loc["elem"] for loc in k["locals"]]
+
+
+# extremum_step (kernel_lift.rs:1097-1129) with nan_arm (:1134-1160) for a float Max/Min:
+#   if have { if v != v { acc = v } else { if better(v, acc) { acc = v } } } else { acc = v }; have = 1
+def _float_extremum(acc, have):
+    return [("If", [("If", [("Assign", acc)], [("If", [("Assign", acc)], [])])], [("Assign", acc)]),
+            ("Assign", have)]
+
+
+# ... and for MaxNum/MinNum: if acc != acc { acc = v } else { if v == v { if better { acc = v } } }
+def _num_extremum(acc, have):
+    return [("If", [("If", [("Assign", acc)], [("If", [("If", [("Assign", acc)], [])], [])])], [("Assign", acc)]),
+            ("Assign", have)]
+
+
+def test_serial_reduction_skeleton_follows_kernel_lift():
+    """lift_reduction_opdef (kernel_lift.rs:447-484): locals extents 0..r, counters r..2r, loaded inputs
+    2r..2r+n, then acc, have, val (:440-442, signature :1006-1024); per kept row `acc`/`have` Lets, the
+    reduced loops around the loads, `val` and the fold step (reduce_loop :919-941), one Store."""
+    k = u.lift_reduction("r", "F32", 2, "Max", axes=(1,))
+    params, locals_ = _sig(k)
+    assert params == [("in0", "Buffer", 2), ("out", "Buffer", 1), ("n0", "Scalar", 0), ("n1", "Scalar", 1)]
+    assert locals_ == ["I32"] * 4 + ["F32", "F64", "I32", "F64"]
+    assert skeleton(k["body"]) == [
+        ("For", 2, [("Let", 5), ("Let", 6),
+                    ("For", 3, [("Load", 4, ("buf", 0)), ("Let", 7), *_float_extremum(5, 6)]),
+                    ("Store", ("buf", 1))])]
+    # Sum: one Assign acc = acc + val (fold_step :1049-1060); the reduced axis 0 nests inside kept axis 1
+    s = u.lift_reduction("r", "I64", 2, "Sum", axes=(0,))
+    assert skeleton(s["body"]) == [
+        ("For", 3, [("Let", 5), ("Let", 6), ("For", 2, [("Load", 4, ("buf", 0)), ("Let", 7), ("Assign", 5)]),
+                    ("Store", ("buf", 1))])]
+    assert s["body"][0]["For"]["end"] == {"Local": 1}  # for_axis (:1037-1047): counter r + d to extent d
+    m = u.lift_reduction("r", "F64", 1, "MaxNum")
+    assert skeleton(m["body"]) == [("Let", 3), ("Let", 4), ("For", 1, [("Load", 2, ("buf", 0)), ("Let", 5),
+                                                                      *_num_extremum(3, 4)]),
+                                   ("Store", ("buf", 1))]
+
+
+def test_launched_reduction_skeleton_follows_block_reduce():
+    """lift_reduction_opdef_launched (block_reduce.rs:50-93): the row's Lets, the thread's strided slice
+    of the reduced axis (:278-288), publish (:191-206), a Barrier, log2(block) rounds of `If tid < s`
+    (load the partner's partial and flag, fold, publish) each followed by a Barrier (:210-247), thread
+    0's store (:292-307), inside the block-strided kept loop (:312-338); locals red and partner_have
+    after the serial layout."""
+    k = u.lift_reduction("r", "F32", 2, "Max", axes=(1,), launch=(4, 2))
+    params, locals_ = _sig(k)
+    assert locals_ == ["I32"] * 4 + ["F32", "F64", "I32", "F64", "F32", "I32"]
+    rnd = ("If", [("Load", 7, ("shared", 0)), ("Load", 9, ("shared", 1)), ("If", _float_extremum(5, 6), []),
+                  ("Store", ("shared", 0)), ("Store", ("shared", 1))], [])
+    row = [("Let", 5), ("Let", 6),
+           ("For", 3, [("Load", 4, ("buf", 0)), ("Let", 7), *_float_extremum(5, 6)]),
+           ("Store", ("shared", 0)), ("Store", ("shared", 1)), ("Barrier",),
+           rnd, ("Barrier",), rnd, ("Barrier",),
+           ("If", [("Store", ("buf", 1))], [])]
+    assert skeleton(k["body"]) == [("For", 2, row)]
+    outer = k["body"][0]["For"]
+    assert outer["start"] == {"Cast": [{"Exec": {"BlockIdx": 0}}, {"to": "I32", "round": "NearestEven", "sat": "Wrap"}]}
+    inner = outer["body"][2]["For"]
+    assert inner["start"]["Cast"][0] == {"Exec": {"ThreadIdx": 0}}
+    assert inner["step"]["Cast"][0] == {"Exec": {"BlockDim": 0}}
+    # no kept axis: the row under `if BlockIdx == 0` (:314-323); Sum publishes no flag
+    a = u.lift_reduction("r", "F32", 1, "Sum", launch=(2, 3))
+    sk = skeleton(a["body"])
+    assert len(sk) == 1 and sk[0][0] == "If"
+    assert sk[0][1][:3] == [("Let", 3), ("Let", 4), ("For", 1, [("Load", 2, ("buf", 0)), ("Let", 5), ("Assign", 3)])]
+    assert sk[0][1][3:] == [("Store", ("shared", 0)), ("Barrier",),
+                            ("If", [("Load", 5, ("shared", 0)), ("Assign", 3), ("Store", ("shared", 0))], []),
+                            ("Barrier",), ("If", [("Store", ("buf", 1))], [])]
+
+
+def test_serial_scan_skeleton_follows_kernel_lift():
+    """lift_scan_opdef (kernel_lift.rs:504-519): the kept loops around scan_row (:631-660: Let acc, Let
+    have, the scanned loop) around scan_pass (:548-576: loads, val, then the fold and the write, the
+    write first for an exclusive scan; a Mean also counts in `have`)."""
+    inc = u.lift_scan("s", "I32", 2, "Sum")
+    assert skeleton(inc["body"]) == [
+        ("For", 2, [("Let", 5), ("Let", 6),
+                    ("For", 3, [("Load", 4, ("buf", 0)), ("Let", 7), ("Assign", 5), ("Store", ("buf", 1))])])]
+    exc = u.lift_scan("s", "F64", 2, "Mean", axis=0, exclusive=True, reverse=True)
+    assert skeleton(exc["body"]) == [
+        ("For", 3, [("Let", 5), ("Let", 6),
+                    ("For", 2, [("Load", 4, ("buf", 0)), ("Let", 7), ("Store", ("buf", 1)), ("Assign", 5),
+                                ("Assign", 6)])])]
+    f = exc["body"][0]["For"]["body"][2]["For"]
+    i32 = lambda v: {"ConstInt": [v, "I32"]}  # noqa: E731
+    assert f["start"] == {"Sub": [{"Local": 0}, i32(1)]} and f["end"] == i32(-1) and f["step"] == i32(-1)
+
+
+def test_gather_skeleton_follows_the_gather_lift():
+    """lift_gather_opdef (gather.rs:184-232): locals extents, counters, the loaded data and index, the
+    source extent (a Scalar parameter) and the clamped index; each cell loads its index, lets the
+    clamp, and guards the data load and store by `raw < 0` then `raw >= extent` (ZeroFill stores zero
+    in both out-of-range arms, Skip nothing, Clamp is unguarded)."""
+    k = u.lift_gather("g", "Bf16", 2, "I32", oob="ZeroFill")
+    params, locals_ = _sig(k)
+    assert params == [("in0", "Buffer", 2), ("in1", "Buffer", 2), ("out", "Buffer", 2), ("n0", "Scalar", 0),
+                      ("n1", "Scalar", 1), ("src_extent", "Scalar", 6)]
+    assert locals_ == ["I32"] * 4 + ["Bf16", "I32", "I32", "I32"]
+    compute = [("Load", 4, ("buf", 0)), ("Store", ("buf", 2))]
+    zero = [("Store", ("buf", 2))]
+    cell = [("Load", 5, ("buf", 1)), ("Let", 6 + 1), ("If", zero, [("If", zero, compute)])]
+    assert skeleton(k["body"]) == [("For", 2, [("For", 3, cell)])]
+    load = k["body"][0]["For"]["body"][0]["For"]["body"][2]["If"]["els"][0]["If"]["els"][0]["Load"]
+    assert load["place"]["Logical"]["coords"] == [{"Local": 7}, {"Local": 3}]  # place_at (:103-113)
+    c = u.lift_gather("g", "Bf16", 2, "I32", oob="Clamp", axis=1)
+    cl = c["body"][0]["For"]["body"][0]["For"]["body"]
+    assert skeleton(cl) == [("Load", 5, ("buf", 1)), ("Let", 7), *compute]
+    assert cl[2]["Load"]["place"]["Logical"]["coords"] == [{"Local": 2}, {"Local": 7}]
+
+
+# ---------------------------------------------------------------------------------------
+# The shared launch_cases() corpus (launch_cases.rs:137-180)
+# ---------------------------------------------------------------------------------------
+
+def elementwise_launched(name: str, dtype: str, rank: int, body: dict, block: int, grid: int) -> dict:
+    """lift_elementwise_opdef_launched (kernel_lift.rs:96-128, grid_stride_outermost :256-285) for two
+    inputs: loads of in0/in1 at the counters, the body stored to out, the outermost loop grid-strided."""
+    r = rank
+    i32 = lambda v: {"ConstInt": [v, "I32"]}  # noqa: E731
+    coords = [{"Local": r + d} for d in range(r)]
+    inner = [{"Load": {"local": 2 * r + k, "place": {"Logical": {"buffer": k, "coords": coords}}}} for k in range(2)]
+    inner.append({"Store": {"place": {"Logical": {"buffer": 2, "coords": coords}}, "value": body}})
+    blk = inner
+    for d in reversed(range(r)):
+        blk = [{"For": {"local": r + d, "start": i32(0), "end": {"Local": d}, "step": i32(1), "unroll": "None",
+                        "body": blk}}]
+    cast = lambda e: {"Cast": [e, {"to": "I32", "round": "NearestEven", "sat": "Wrap"}]}  # noqa: E731
+    ex = lambda i: {"Exec": {i: 0}}  # noqa: E731
+    blk[0]["For"]["start"] = cast({"Add": [{"Mul": [ex("BlockIdx"), ex("BlockDim")]}, ex("ThreadIdx")]})
+    blk[0]["For"]["step"] = cast({"Mul": [ex("GridDim"), ex("BlockDim")]})
+    params = [{"name": f"in{k}", "kind": {"Buffer": {"elem": dtype, "role": "Read", "rank": r}}} for k in range(2)]
+    params.append({"name": "out", "kind": {"Buffer": {"elem": dtype, "role": "Write", "rank": r}}})
+    params += [{"name": f"n{d}", "kind": {"Scalar": {"ty": "I32", "local": d}}} for d in range(r)]
+    locals_ = [{"elem": "I32", "lanes": 1}] * (2 * r) + [{"elem": dtype, "lanes": 1}] * 2
+    return {"name": name, "compute": dtype, "params": params, "locals": locals_, "body": blk,
+            "launch": {"block": [block, 1, 1], "grid": [grid, 1, 1], "subgroup": None, "cluster": None,
+                       "devices": 1, "grid_dims": None},
+            "allocs": [], "result": None, "results": []}
+
+
+def launch_cases():
+    """The corpus's four cases: (name, dtype, shape, (block, grid), ulps, body, numpy reference)."""
+    a, b = {"Local": None}, None  # placeholders replaced per rank below
+    del a, b
+
+    def case(name, dtype, shape, launch, ulps, body, ref):
+        r = len(shape)
+        la, lb = {"Local": 2 * r}, {"Local": 2 * r + 1}
+        return name, dtype, shape, launch, ulps, body(la, lb), ref
+
+    ab = lambda x: {"Unary": ["Abs", x]}  # noqa: E731
+    return [
+        case("fma_shape", "F32", (5, 7), (4, 2), 3, lambda x, y: {"Add": [{"Mul": [ab(x), ab(y)]}, ab(x)]},
+             lambda x, y: np.abs(x.astype(np.float64)) * np.abs(y) + np.abs(x)),
+        case("div", "F32", (6, 5), (8, 2), 0, lambda x, y: {"Div": [x, y]}, lambda x, y: x.astype(np.float64) / y),
+        case("sub", "I32", (3, 11), (8, 1), 0, lambda x, y: {"Sub": [x, y]}, lambda x, y: x - y),
+        case("add", "U32", (37,), (16, 3), 0, lambda x, y: {"Add": [x, y]}, lambda x, y: x + y),
+    ]
+
+
+import numpy as np  # noqa: E402
+
+
+@pytest.mark.parametrize("case", launch_cases(), ids=lambda c: c[0])
+def test_launch_cases_corpus_is_refused_typed_and_runs_on_the_c_leg(case):
+    """Each launch_cases() kernel (a launched elementwise lift) is outside this backend's path: lower_kernel
+    refuses it with a typed UnsupportedKernel.  The C99 leg runs it within the corpus's stated ulps of the
+    f64-evaluated result (launch_cases.rs:14-27)."""
+    from oracle import cpuc
+
+    name, dtype, shape, (block, grid), ulps, body, ref = case
+    k = elementwise_launched(name, dtype, len(shape), body, block, grid)
+    with pytest.raises(_lib.UnpError) as e:
+        u.HipBackend().lower_kernel(k)
+    assert e.value.kind == "UnsupportedKernel"
+    rng = np.random.default_rng(7)
+    nt = {"F32": np.float32, "I32": np.int32, "U32": np.uint32}[dtype]
+    if dtype == "F32":
+        x = rng.normal(size=shape).astype(nt)
+        y = rng.normal(size=shape).astype(nt)
+        y.ravel()[::4] = 0  # zero denominators: inf and NaN agree
+    else:
+        info = np.iinfo(nt)
+        x = rng.integers(info.min, info.max, shape, dtype=np.int64, endpoint=True).astype(nt)
+        y = rng.integers(info.min, info.max, shape, dtype=np.int64, endpoint=True).astype(nt)
+    out = np.zeros(shape, nt)
+    assert cpuc.run(k, x, y, out, *shape) == cpuc.OK
+    with np.errstate(all="ignore"):
+        want = ref(x, y)
+    if dtype == "F32":
+        w32 = want.astype(np.float32)
+        same = (out == w32) | (np.isnan(out) & np.isnan(w32))
+        ia, ib = out.view(np.int32).astype(np.int64), w32.view(np.int32).astype(np.int64)
+        assert (same | (np.abs(ia - ib) <= ulps)).all()
+    else:
+        assert np.array_equal(out, want.astype(nt))

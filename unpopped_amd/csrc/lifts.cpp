@@ -1033,6 +1033,125 @@ void normalize(J& j, bool top) {
     if (!(top && kv.first == "launch")) normalize(kv.second, false);
 }
 
+// ---- local renumbering ----------------------------------------------------------------------
+// A KernelFn names its locals by index (LocalId, kernel.rs): the ScalarExpr leaf Local(n) and the
+// `local` of Let, Load, Assign, For and a Scalar parameter.  Two kernels that differ only by a
+// consistent renumbering of their locals (the locals list permuted to match) are the same kernel.
+
+// Every local-id reference of `j`, each object's keys in sorted order (so that the visit does not
+// depend on the order a writer put the keys in).
+template <class F>
+void visit_local_refs(J& j, F& f) {
+  if (j.t == J::Arr) {
+    for (auto& x : j.a) visit_local_refs(x, f);
+    return;
+  }
+  if (j.t != J::Obj) return;
+  if (j.o.size() == 1 && j.o[0].first == "Local" && j.o[0].second.t == J::Num && j.o[0].second.is_int) {
+    f(j.o[0].second);
+    return;
+  }
+  std::vector<size_t> order(j.o.size());
+  for (size_t i = 0; i < order.size(); ++i) order[i] = i;
+  std::sort(order.begin(), order.end(), [&](size_t a, size_t b) { return j.o[a].first < j.o[b].first; });
+  for (size_t i : order) {
+    auto& kv = j.o[i];
+    if (kv.first == "local" && kv.second.t == J::Num && kv.second.is_int) f(kv.second);
+    else visit_local_refs(kv.second, f);
+  }
+}
+
+// The references of a KernelFn: its parameters, then its body.
+template <class F>
+void visit_kernel_locals(J& k, F& f) {
+  for (auto& kv : k.o)
+    if (kv.first == "params") visit_local_refs(kv.second, f);
+  for (auto& kv : k.o)
+    if (kv.first == "body") visit_local_refs(kv.second, f);
+}
+
+// A JSON value with every object's keys sorted (the same text whatever order a writer used).
+J sorted_keys(const J& j) {
+  J c = j;
+  if (c.t == J::Arr) {
+    for (auto& x : c.a) x = sorted_keys(x);
+  } else if (c.t == J::Obj) {
+    for (auto& kv : c.o) kv.second = sorted_keys(kv.second);
+    std::sort(c.o.begin(), c.o.end(), [](const std::pair<std::string, J>& a, const std::pair<std::string, J>& b) {
+      return a.first < b.first;
+    });
+  }
+  return c;
+}
+
+size_t local_count(const J& k) {
+  const J* l = k.get("locals");
+  return (l && l->t == J::Arr) ? l->a.size() : 0;
+}
+
+// The canonical numbering of k's locals: in order of first reference, then the unreferenced ones
+// ordered by their declarations (which alone tell them apart).  False when a reference names no
+// declared local.
+bool canonical_order(const J& k, std::vector<int64_t>& to) {
+  const size_t m = local_count(k);
+  to.assign(m, -1);
+  int64_t next = 0;
+  bool ok = true;
+  J copy = k;
+  auto first = [&](J& id) {
+    if (id.i < 0 || (size_t)id.i >= m) {
+      ok = false;
+      return;
+    }
+    if (to[(size_t)id.i] < 0) to[(size_t)id.i] = next++;
+  };
+  visit_kernel_locals(copy, first);
+  std::vector<std::pair<std::string, size_t>> rest;
+  const J* decls = k.get("locals");
+  for (size_t i = 0; i < m; ++i)
+    if (to[i] < 0) rest.emplace_back(kir::write(sorted_keys(decls->a[i])), i);
+  std::stable_sort(rest.begin(), rest.end(),
+                   [](const std::pair<std::string, size_t>& a, const std::pair<std::string, size_t>& b) {
+                     return a.first < b.first;
+                   });
+  for (const auto& r : rest) to[r.second] = next++;
+  return ok;
+}
+
+// k with local i renamed to[i] (a permutation) and its locals list permuted to match.
+J renumbered(const J& k, const std::vector<int64_t>& to) {
+  J c = k;
+  auto rename = [&](J& id) {
+    if (id.i >= 0 && (size_t)id.i < to.size()) id.i = to[(size_t)id.i];
+  };
+  visit_kernel_locals(c, rename);
+  for (auto& kv : c.o)
+    if (kv.first == "locals" && kv.second.t == J::Arr && kv.second.a.size() == to.size()) {
+      std::vector<J> perm(to.size());
+      for (size_t i = 0; i < to.size(); ++i) perm[(size_t)to[i]] = kv.second.a[i];
+      kv.second.a = std::move(perm);
+    }
+  return c;
+}
+
+// k in its canonical numbering (unchanged when a reference names no declared local).
+J canonical(const J& k) {
+  std::vector<int64_t> to;
+  return canonical_order(k, to) ? renumbered(k, to) : k;
+}
+
+// The canonical kernel `kc` renumbered into the numbering of `proto`: the kernel as the lift that
+// produced `proto` would number it, when the two share a statement skeleton (the expressions a
+// caller supplies read only locals defined before them, so they do not move a first reference).
+bool into_numbering_of(const J& proto, const J& kc, J& out) {
+  std::vector<int64_t> to;
+  if (!canonical_order(proto, to) || to.size() != local_count(kc)) return false;
+  std::vector<int64_t> back(to.size());
+  for (size_t i = 0; i < to.size(); ++i) back[(size_t)to[i]] = (int64_t)i;
+  out = renumbered(kc, back);
+  return true;
+}
+
 struct ParamInfo {
   bool buffer = false;
   int32_t elem = -1;
@@ -1082,6 +1201,7 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
     return UNP_PARSE_ERROR;
   }
   normalize(k, true);
+  const J kc = canonical(k);  // compared in the canonical numbering of locals
   const std::string name = k.get("name")->s;
   std::vector<ParamInfo> ps;
   if (!read_params(k, ps)) {
@@ -1107,7 +1227,7 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
     J c = cand;
     for (auto& kv : c.o)
       if (kv.first == "name") kv.second = J::str(name);
-    return c == k;
+    return canonical(c) == kc;
   };
   auto attempt = [&](auto&& make) {
     try {
@@ -1133,9 +1253,14 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
   if (nin >= 1 && nin <= 8) {
     const int32_t dt = ps[0].elem, r = ps[0].rank, orank = ps[nin].rank;
     const uint32_t n = (uint32_t)nin;
-    J xbody = input_leaf(0), xpost;
-    bool has_post = false, exprs_ok = true;
-    {
+    // The pre-map body read back from the `val` Let (the up-cast stripped, the loaded locals
+    // unbound to Input(k)) and a fused post from the output store (Local(red) unbound to
+    // Reduced(0)), in the lift's numbering of locals; false when they read any other local.
+    auto extract = [&](const J& kk, J& xbody, J& xpost, bool& has_post) {
+      xbody = input_leaf(0);
+      xpost = J();
+      has_post = false;
+      bool exprs_ok = true;
       const uint32_t val = 2 * (uint32_t)r + n + 2, red = val + 1;
       auto unbind_locals = [&](const J& e, J& o) {
         bool ok = true;
@@ -1156,7 +1281,7 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
         }
         return ok;
       };
-      const J& kb = *k.get("body");
+      const J& kb = *kk.get("body");
       const J* let = find_stmt(kb, [&](const J& x) {
         const J* l = x.get("Let");
         return l && l->get("local") && l->get("local")->is_int && l->get("local")->i == (int64_t)val;
@@ -1193,7 +1318,27 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
           if (!has_post) exprs_ok = false;
         }
       }
-    }
+      return exprs_ok;
+    };
+    J xbody, xpost;
+    bool has_post = false;
+    const bool exprs_ok = extract(k, xbody, xpost, has_post);
+    auto take_reduction = [&](int32_t op, uint32_t mask, const J& b, const J& p, bool hp) {
+      out.form.kind = UNP_FORM_REDUCTION;
+      out.form.dtype = dt;
+      out.form.rank = r;
+      out.form.op0 = op;
+      out.form.axes_mask = mask;
+      out.rx.n_inputs = (int32_t)n;
+      out.rx.body = b;
+      out.rx.has_post = hp;
+      out.rx.post = p;
+      out.rx.plain = n == 1 && b == input_leaf(0) && !hp;
+      out.form.reduced_from = r;
+      for (int32_t d = r - 1; d >= 0 && ((mask >> d) & 1u); --d) out.form.reduced_from = d;
+      out.lift = block ? "lift_reduction_opdef_launched" : "lift_reduction_opdef";
+      return UNP_OK;
+    };
     static const int32_t ops[] = {UNP_OP_SUM,    UNP_OP_PROD, UNP_OP_MAX, UNP_OP_MIN, UNP_OP_MEAN,
                                   UNP_OP_MAXNUM, UNP_OP_MINNUM, UNP_OP_AND, UNP_OP_OR, UNP_OP_XOR};
     // Every reduced-axis set whose output rank matches (ReductionShape::new,
@@ -1210,22 +1355,8 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
           if (orank != want) continue;
           if (exprs_ok && attempt([&] {
                 return lift_reduction(name, dt, r, op, mask, keep, block, grid, n, &xbody, has_post ? &xpost : nullptr);
-              })) {
-            out.form.kind = UNP_FORM_REDUCTION;
-            out.form.dtype = dt;
-            out.form.rank = r;
-            out.form.op0 = op;
-            out.form.axes_mask = mask;
-            out.rx.n_inputs = (int32_t)n;
-            out.rx.body = xbody;
-            out.rx.has_post = has_post;
-            out.rx.post = xpost;
-            out.rx.plain = n == 1 && xbody == input_leaf(0) && !has_post;
-            out.form.reduced_from = r;
-            for (int32_t d = r - 1; d >= 0 && ((mask >> d) & 1u); --d) out.form.reduced_from = d;
-            out.lift = block ? "lift_reduction_opdef_launched" : "lift_reduction_opdef";
-            return UNP_OK;
-          }
+              }))
+            return take_reduction(op, mask, xbody, xpost, has_post);
         }
       }
       if (orank == r && n == 1) {
@@ -1248,6 +1379,29 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
         }
       }
     }
+    // A kernel whose locals are numbered otherwise: renumbered into each candidate skeleton's own
+    // numbering (the lift with the plain body, with and without a fused post), its body and post
+    // read back there, and the candidate re-lifted with them and compared.
+    const J probe_post = e_add(reduced_leaf(0), reduced_leaf(0));
+    for (int32_t op : ops)
+      for (uint32_t mask : masks) {
+        const int32_t kept = r - __builtin_popcount(mask);
+        for (int keep = 0; keep <= 1; ++keep) {
+          if (orank != (keep ? r : kept)) continue;
+          for (int pm = 0; pm <= 1; ++pm) {
+            J proto, kr, b, p;
+            bool hp = false;
+            try {
+              proto = lift_reduction(name, dt, r, op, mask, keep, block, grid, n, nullptr, pm ? &probe_post : nullptr);
+            } catch (const Decline&) {
+              continue;
+            }
+            if (!into_numbering_of(proto, kc, kr) || !extract(kr, b, p, hp) || hp != (pm == 1)) continue;
+            if (attempt([&] { return lift_reduction(name, dt, r, op, mask, keep, block, grid, n, &b, hp ? &p : nullptr); }))
+              return take_reduction(op, mask, b, p, hp);
+          }
+        }
+      }
   }
   // Fused row fold: in0 Read rank 2, out0 / out1 Write rank 1, two I32 extents.
   if (np == 5 && ps[0].buffer && ps[0].rank == 2 && ps[1].buffer && ps[2].buffer && !ps[3].buffer && !ps[4].buffer) {
@@ -1363,72 +1517,103 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
     const uint32_t S = (uint32_t)(L / (int64_t)(n + 4));
     if (S > 8) continue;
     const Row w{ps[0].elem, (uint32_t)r, (uint32_t)n, S};
-    const J& body = *k.get("body");
     RowReduceSpec sp;
     sp.dtype = ps[0].elem;
     sp.rank = (int32_t)r;
     sp.n_inputs = (int32_t)n;
-    bool ok = true;
-    std::vector<std::vector<int32_t>> cand;
-    for (uint32_t st = 0; ok && st < S; ++st) {
-      const uint32_t val = w.stage_base(st) + 2, acc = w.stage_base(st);
-      const J* let = find_stmt(body, [&](const J& x) {
-        const J* l = x.get("Let");
-        return l && l->get("local") && l->get("local")->is_int && l->get("local")->i == (int64_t)val;
-      });
-      if (!let) {
-        ok = false;
-        break;
-      }
-      J init = *let->get("Let")->get("init");
-      if (w.dtype != UNP_F64) {
-        const J* c = init.get("Cast");
-        if (!c || c->t != J::Arr || c->a.size() != 2) {
+    // Reads the stages' pres, folds and the epilogue back from `kk` (in the lift's numbering of
+    // locals) and tries every combination of the candidate folds.
+    auto try_row_reduce = [&](const J& kk) {
+      const J& body = *kk.get("body");
+      sp.pres.clear();
+      sp.ops.clear();
+      bool ok = true;
+      std::vector<std::vector<int32_t>> cand;
+      for (uint32_t st = 0; ok && st < S; ++st) {
+        const uint32_t val = w.stage_base(st) + 2, acc = w.stage_base(st);
+        const J* let = find_stmt(body, [&](const J& x) {
+          const J* l = x.get("Let");
+          return l && l->get("local") && l->get("local")->is_int && l->get("local")->i == (int64_t)val;
+        });
+        if (!let) {
           ok = false;
           break;
         }
-        J operand = c->a[0];  // copied out before `init` (which owns it) is replaced
-        init = std::move(operand);
+        J init = *let->get("Let")->get("init");
+        if (w.dtype != UNP_F64) {
+          const J* c = init.get("Cast");
+          if (!c || c->t != J::Arr || c->a.size() != 2) {
+            ok = false;
+            break;
+          }
+          J operand = c->a[0];  // copied out before `init` (which owns it) is replaced
+          init = std::move(operand);
+        }
+        J pre;
+        if (!unbind(w, init, st, pre)) {
+          ok = false;
+          break;
+        }
+        sp.pres.push_back(pre);
+        const J* asg = find_stmt(body, [&](const J& x) {
+          const J* a = x.get("Assign");
+          return a && a->get("local") && a->get("local")->is_int && a->get("local")->i == (int64_t)acc;
+        });
+        const J* value = asg ? asg->get("Assign")->get("value") : nullptr;
+        if (value && value->get("Add")) cand.push_back({UNP_OP_SUM, UNP_OP_MEAN});
+        else if (value && value->get("Mul")) cand.push_back({UNP_OP_PROD});
+        else cand.push_back({UNP_OP_MAX, UNP_OP_MIN});
       }
-      J pre;
-      if (!unbind(w, init, st, pre)) {
-        ok = false;
-        break;
+      const J* store = ok ? find_stmt(body, [&](const J& x) {
+        const J* st = x.get("Store");
+        const J* pl = st ? st->get("place") : nullptr;
+        const J* lg = pl ? pl->get("Logical") : nullptr;
+        return lg && lg->get("buffer") && lg->get("buffer")->is_int && lg->get("buffer")->i == (int64_t)n;
+      })
+                          : nullptr;
+      if (!store || !unbind(w, *store->get("Store")->get("value"), S, sp.epilogue)) return false;
+      // every combination of the candidate folds
+      std::vector<size_t> pick(S, 0);
+      for (;;) {
+        sp.ops.clear();
+        for (uint32_t st = 0; st < S; ++st) sp.ops.push_back(cand[st][pick[st]]);
+        if (attempt([&] { return lift_row_reduce(name, sp, block, grid); })) return true;
+        uint32_t st = 0;
+        while (st < S && ++pick[st] == cand[st].size()) pick[st++] = 0;
+        if (st == S) break;
       }
-      sp.pres.push_back(pre);
-      const J* asg = find_stmt(body, [&](const J& x) {
-        const J* a = x.get("Assign");
-        return a && a->get("local") && a->get("local")->is_int && a->get("local")->i == (int64_t)acc;
-      });
-      const J* value = asg ? asg->get("Assign")->get("value") : nullptr;
-      if (value && value->get("Add")) cand.push_back({UNP_OP_SUM, UNP_OP_MEAN});
-      else if (value && value->get("Mul")) cand.push_back({UNP_OP_PROD});
-      else cand.push_back({UNP_OP_MAX, UNP_OP_MIN});
+      return false;
+    };
+    bool found = try_row_reduce(k);
+    // A kernel whose locals are numbered otherwise: renumbered into the numbering of each
+    // candidate skeleton (the lift of every fold combination with Input(0) pres and epilogue;
+    // at most 625 combinations, i.e. up to four stages).
+    uint32_t combos = 1;
+    for (uint32_t st = 0; st < S; ++st) combos *= 5;
+    if (!found && S <= 4) {
+      static const int32_t rops[] = {UNP_OP_SUM, UNP_OP_PROD, UNP_OP_MAX, UNP_OP_MIN, UNP_OP_MEAN};
+      for (uint32_t c = 0; !found && c < combos; ++c) {
+        RowReduceSpec proto_sp = sp;
+        proto_sp.ops.clear();
+        proto_sp.pres.assign(S, input_leaf(0));
+        proto_sp.epilogue = input_leaf(0);
+        for (uint32_t st = 0, q = c; st < S; ++st, q /= 5) proto_sp.ops.push_back(rops[q % 5]);
+        J proto, kr;
+        try {
+          proto = lift_row_reduce(name, proto_sp, block, grid);
+        } catch (const Decline&) {
+          continue;
+        }
+        if (into_numbering_of(proto, kc, kr)) found = try_row_reduce(kr);
+      }
     }
-    const J* store = ok ? find_stmt(body, [&](const J& x) {
-      const J* st = x.get("Store");
-      const J* pl = st ? st->get("place") : nullptr;
-      const J* lg = pl ? pl->get("Logical") : nullptr;
-      return lg && lg->get("buffer") && lg->get("buffer")->is_int && lg->get("buffer")->i == (int64_t)n;
-    })
-                        : nullptr;
-    if (!store || !unbind(w, *store->get("Store")->get("value"), S, sp.epilogue)) continue;
-    // every combination of the candidate folds
-    std::vector<size_t> pick(S, 0);
-    for (;;) {
-      sp.ops.clear();
-      for (uint32_t st = 0; st < S; ++st) sp.ops.push_back(cand[st][pick[st]]);
-      if (attempt([&] { return lift_row_reduce(name, sp, block, grid); })) {
-        out.form.kind = UNP_FORM_ROW_REDUCE;
-        out.form.dtype = sp.dtype;
-        out.form.rank = sp.rank;
-        out.rr = sp;
-        out.lift = block ? "lift_row_reduce_opdef_launched" : "lift_row_reduce_opdef";
-        return UNP_OK;
-      }
-      uint32_t st = 0;
-      while (st < S && ++pick[st] == cand[st].size()) pick[st++] = 0;
-      if (st == S) break;
+    if (found) {
+      out.form.kind = UNP_FORM_ROW_REDUCE;
+      out.form.dtype = sp.dtype;
+      out.form.rank = sp.rank;
+      out.rr = sp;
+      out.lift = block ? "lift_row_reduce_opdef_launched" : "lift_row_reduce_opdef";
+      return UNP_OK;
     }
   }
   why = "kernel `" + name +
