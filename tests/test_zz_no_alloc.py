@@ -106,7 +106,9 @@ def test_column_reduction_matches_the_allocating_launch(hip_device):
             return din, u.DeviceBuffer(c * 4), r, c
         got, want = both(ex, make, lambda a: a[1].download(np.float32, c))
         assert got.tobytes() == want.tobytes()
-        assert ex.last_launch()["grid"][0] > c // 256  # the schedule splits R: a workspace is in use
+        # a device-class grid; with c / 256 column strips the schedule splits R into chunks whose
+        # partials live in the workspace
+        assert ex.last_launch()["grid"][0] == u.device_info()[1]
 
 
 def test_dequant_gemm_matches_the_allocating_launch(hip_device):

@@ -559,7 +559,9 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     << json_str(kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN)
                     ? "float Sum / Mean: every prefix is an f64 fold of the same elements in a different order (tile-local "
                       "striped scan plus decoupled look-back; a Mean divides it by the count once); within the declared "
-                      "per-prefix bound gamma_(n-1)*sum|x| + 1/2 ulp; bit-equal whenever the f64 partial sums are exact"
+                      "per-prefix bound gamma_(n-1)*sum|x| + 1/2 ulp; bit-equal whenever the f64 partial sums are exact. "
+                      "Not reproducible run to run: the carry's association depends on how many tiles each look-back "
+                      "folded before it met an inclusive prefix, which depends on timing; every launch is within the bound"
                     : "order-independent fold: bit-exact against the serial scan except NaN payload and the sign of a zero in Max/Min")
     << "," << json_str("one single-pass decoupled look-back launch replaces the KernelFn's block-per-row three-phase schedule")
     << "]}";

@@ -534,8 +534,9 @@ UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
 //
 // A wave covers 64 * VEC consecutive columns b of one a; the block's WAVES waves split the
 // block's run of rows into WAVES consecutive pieces; the blocks of one column strip split R
-// into S consecutive chunks.  Consecutive blocks take consecutive strips of one chunk, so the
-// blocks in flight together read whole rows.  Lane l folds its VEC columns down its rows in ascending order
+// into S consecutive chunks.  The (strip, chunk) items are numbered chunk-major and blocks stride
+// over them (a device-class grid), so consecutive blocks take consecutive strips of one chunk and
+// the blocks in flight together read whole rows.  Lane l folds its VEC columns down its rows in ascending order
 // (16-byte loads, every load of a wave instruction contiguous, U rows in flight); the waves
 // meet in LDS in wave order; with S > 1 each block publishes its partials and the block that
 // draws the strip's last ticket folds the S partials in chunk order and stores.  The order is
@@ -554,88 +555,94 @@ UNP_DEV void reduce_mid(const T* __restrict__ in, T* __restrict__ out, i64 A, i6
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const i64 ncb = (B + CW - 1) / CW;
   const i64 nstrips = A * ncb;
-  const i64 strip = (i64)blockIdx.x % nstrips;  // a * ncb + cb
-  const i64 s = (i64)blockIdx.x / nstrips;
-  const i64 a = strip / ncb, cb = strip - a * ncb;
-  const i64 b0 = cb * CW + (i64)lane * VEC;
-  const bool live = b0 < B;  // VEC divides B (the host picks VEC = 1 otherwise)
-  // This block's rows [i0, i1), then this wave's piece of them.
-  const i64 i0 = (R * s) / S, i1 = (R * (s + 1)) / S;
-  const i64 w0 = i0 + ((i1 - i0) * wave) / WAVES, w1 = i0 + ((i1 - i0) * (wave + 1)) / WAVES;
-  Ac acc_[VEC];
+  // Items (strip, chunk), item = s * nstrips + strip; blocks stride over them.
+  for (i64 item = blockIdx.x; item < nstrips * S; item += gridDim.x) {
+    const i64 strip = item % nstrips;  // a * ncb + cb
+    const i64 s = item / nstrips;
+    const i64 a = strip / ncb, cb = strip - a * ncb;
+    const i64 b0 = cb * CW + (i64)lane * VEC;
+    const bool live = b0 < B;  // VEC divides B (the host picks VEC = 1 otherwise)
+    // This item's rows [i0, i1), then this wave's piece of them.
+    const i64 i0 = (R * s) / S, i1 = (R * (s + 1)) / S;
+    const i64 w0 = i0 + ((i1 - i0) * wave) / WAVES, w1 = i0 + ((i1 - i0) * (wave + 1)) / WAVES;
+    Ac acc_[VEC];
 #pragma unroll
-  for (int e = 0; e < VEC; ++e) acc_[e] = F::identity();
-  if (live) {
-    const T* __restrict__ p = in + (a * R) * B + b0;
-    i64 i = w0;
-    for (; i + U <= w1; i += U) {
-      vec<T, VEC> v[U];
+    for (int e = 0; e < VEC; ++e) acc_[e] = F::identity();
+    if (live) {
+      const T* __restrict__ p = in + (a * R) * B + b0;
+      i64 i = w0;
+      for (; i + U <= w1; i += U) {
+        vec<T, VEC> v[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = ld_nt<T, VEC>(p + (i + u) * B);
+        for (int u = 0; u < U; ++u) v[u] = ld_nt<T, VEC>(p + (i + u) * B);
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) acc_[e] = F::apply(acc_[e], (Ac)v[u].e[e]);
-    }
-    for (; i < w1; ++i) {
-      const vec<T, VEC> v = ld_nt<T, VEC>(p + i * B);
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) acc_[e] = F::apply(acc_[e], (Ac)v.e[e]);
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) sh[wave][lane * VEC + e] = acc_[e];
-  __syncthreads();
-  // Wave 0 folds the waves' partials in wave order.
-  if (wave == 0) {
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      Ac r = sh[0][lane * VEC + e];
-#pragma unroll
-      for (int w = 1; w < WAVES; ++w) r = F::apply(r, sh[w][lane * VEC + e]);
-      acc_[e] = r;
-    }
-    if (S == 1) {
-      if (live) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) out[a * B + b0 + e] = finish<T, OP>(acc_[e], R);
+          for (int e = 0; e < VEC; ++e) acc_[e] = F::apply(acc_[e], (Ac)v[u].e[e]);
       }
-      return;
+      for (; i < w1; ++i) {
+        const vec<T, VEC> v = ld_nt<T, VEC>(p + i * B);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc_[e] = F::apply(acc_[e], (Ac)v.e[e]);
+      }
     }
-    Ac* __restrict__ mine = partials + (strip * S + s) * CW + (i64)lane * VEC;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) store_agent(&mine[e], acc_[e]);
-    if (lane == 0) last = (arrive_after_stores(&counters[strip]) == (u32)(S - 1)) ? 1u : 0u;
+    for (int e = 0; e < VEC; ++e) sh[wave][lane * VEC + e] = acc_[e];
+    __syncthreads();
+    // Wave 0 folds the waves' partials in wave order.
+    if (wave == 0) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        Ac r = sh[0][lane * VEC + e];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) r = F::apply(r, sh[w][lane * VEC + e]);
+        acc_[e] = r;
+      }
+      if (S == 1) {
+        if (live) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) out[a * B + b0 + e] = finish<T, OP>(acc_[e], R);
+        }
+      } else {
+        Ac* __restrict__ mine = partials + (strip * S + s) * CW + (i64)lane * VEC;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) store_agent(&mine[e], acc_[e]);
+        if (lane == 0) last = (arrive_after_stores(&counters[strip]) == (u32)(S - 1)) ? 1u : 0u;
+      }
+    }
+    if (S > 1) {
+      __syncthreads();
+      if (last != 0u && wave == 0) {
+        // Every other item's partials were complete before its arrival; the device-coherent
+        // loads see them, 8 chunks in flight at a time.
+        Ac r[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) r[e] = F::identity();
+        const Ac* __restrict__ col = partials + strip * S * CW + (i64)lane * VEC;
+        i64 k = 0;
+        for (; k + 8 <= S; k += 8) {
+          Ac v[8][VEC];
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) v[t][e] = load_agent(&col[(k + t) * CW + e]);
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) r[e] = F::apply(r[e], v[t][e]);
+        }
+        for (; k < S; ++k)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) r[e] = F::apply(r[e], load_agent(&col[k * CW + e]));
+        if (live) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) out[a * B + b0 + e] = finish<T, OP>(r[e], R);
+        }
+        if (lane == 0) __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __syncthreads();  // sh and last are the next item's
   }
-  if (S == 1) return;
-  __syncthreads();
-  if (last == 0u || wave != 0) return;
-  // Every other block's partials were complete before its arrival; the device-coherent loads
-  // see them, 8 chunks in flight at a time.
-  Ac r[VEC];
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) r[e] = F::identity();
-  const Ac* __restrict__ col = partials + strip * S * CW + (i64)lane * VEC;
-  i64 k = 0;
-  for (; k + 8 <= S; k += 8) {
-    Ac v[8][VEC];
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) v[t][e] = load_agent(&col[(k + t) * CW + e]);
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) r[e] = F::apply(r[e], v[t][e]);
-  }
-  for (; k < S; ++k)
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) r[e] = F::apply(r[e], load_agent(&col[k * CW + e]));
-  if (live) {
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) out[a * B + b0 + e] = finish<T, OP>(r[e], R);
-  }
-  if (lane == 0) __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------------------

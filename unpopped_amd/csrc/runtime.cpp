@@ -3,9 +3,18 @@
 // The executor is the consumer-side launch layer the reference leaves out by rule
 // (docs/PATENT-SWEEP.md:265-272): it compiles a lowered kernel's source once, loads it with
 // hipModuleLoadData, picks the entry point whose alignment preconditions the arguments meet,
-// sizes the grid from the device (a device-class constant, never from an extent), owns the
-// scan's tile-status and the full reduction's partials workspaces, and launches with
+// owns the scan's tile-status and the full reduction's partials workspaces, and launches with
 // hipModuleLaunchKernel.
+//
+// Launch geometry follows the reference's rule that no block, grid or thread count is derived
+// from a loop bound (docs/PATENT-SWEEP.md:269): every reduction, scan, gather, row-reduce and
+// dequant launch takes a device-class grid (cu_count times the entry's blocks per CU) and its
+// blocks stride over the work, the surplus exiting.  The work decomposition itself (the column
+// reduction's chunks of the reduced axis, the scan's tiles) is sized from the extents; it sets
+// how many items the fixed grid strides over, not how many blocks run.  One path departs from
+// the rule: the dequantizing GEMM launches one block per (row tile, split of K, column tile)
+// item of its MFMA schedules and one prep block per (group, column slab), i.e. a grid that is
+// the item count.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -653,8 +662,7 @@ int32_t run_xreduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, u
     params.push_back(&rows);
     params.push_back(&cols);
     const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
-    const long long want = (rows + 3) / 4;
-    return launch(x, aligned ? 0 : 1, (uint32_t)(want < cap ? want : cap), params.data(), s, err);
+    return launch(x, aligned ? 0 : 1, (uint32_t)cap, params.data(), s, err);
   }
   if (sched == 'a') {
     const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
@@ -674,8 +682,7 @@ int32_t run_xreduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, u
   d.count = count;
   params.push_back(&d);
   const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
-  const long long want = (outs + 3) / 4;
-  return launch(x, 0, (uint32_t)(want < cap ? want : cap), params.data(), s, err);
+  return launch(x, 0, (uint32_t)cap, params.data(), s, err);
 }
 
 int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
@@ -706,17 +713,13 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
       const size_t entry = (b % vec == 0 && aligned16(in)) ? 0 : 1;
       const long long cw = 64LL * x->l.entries[entry].vec;
       const long long strips = a * ((b + cw - 1) / cw);
-      // Chunks of R: about cu_count * blocks_per_cu blocks in all, at least 16 rows per chunk,
-      // at most 1024 chunks.
-      const long long target = (long long)x->cu_count * x->l.blocks_per_cu;
-      long long S = (target + strips - 1) / strips;
+      // The grid is the device-class constant (cu_count * blocks_per_cu); the work is strips x S
+      // items, S chunks of R: about one item per block, at least 16 rows per chunk, at most 1024
+      // chunks.  Blocks stride over the items.
+      const long long grid = (long long)x->cu_count * x->l.blocks_per_cu;
+      long long S = (grid + strips - 1) / strips;
       S = std::min(S, std::max(1LL, r / 16));
       S = std::max(1LL, std::min(S, 1024LL));
-      const long long grid = strips * S;
-      if (grid > 0x7fffffffLL) {
-        set_error(err, UNP_INVALID_ARGUMENT, "too many column strips for one launch");
-        return UNP_INVALID_ARGUMENT;
-      }
       const size_t acc_bytes = (unp::kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN))
                                    ? 8
                                    : unp::kind_bytes(f.dtype);
@@ -750,18 +753,16 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
       fill_red_view(A.ext, f.rank, mask, in_str.data(), out_str.data(), d);
       d.outs = outs;
       d.count = count;
-      const long long want = (outs + 255) / 256;
       void* params[] = {&in, &out, &d};
-      return launch(x, 0, (uint32_t)(want < cap ? want : cap), params, s, err);
+      return launch(x, 0, (uint32_t)cap, params, s, err);
     }
     // Any other mask: a wave per output.
     unp::axes_desc_host d{};
     fill_axes_desc(A.ext, f.rank, mask, d);
     d.outs = outs;
     d.count = count;
-    const long long want = (outs + 3) / 4;
     void* params[] = {&in, &out, &d};
-    return launch(x, 0, (uint32_t)(want < cap ? want : cap), params, s, err);
+    return launch(x, 0, (uint32_t)cap, params, s, err);
   }
   const long long rows = product(A.ext, 0, (size_t)f.reduced_from);
   const long long cols = product(A.ext, (size_t)f.reduced_from, (size_t)f.rank);
@@ -798,10 +799,8 @@ int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_err
     if ((rc = need_buffers(A, a0 > 0 && S > 0 && b0 > 0, err)) != UNP_OK) return rc;
     if (a0 == 0 || S == 0 || b0 == 0) return UNP_OK;
     uint64_t in = A.buf[0], out = A.buf[1];
-    const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
-    const long long want = (a0 * b0 + 255) / 256;
     void* params[] = {&in, &out, &a0, &S, &b0};
-    return launch(x, 0, (uint32_t)(want < cap ? want : cap), params, s, err);
+    return launch(x, 0, (uint32_t)(x->cu_count * x->l.blocks_per_cu), params, s, err);
   }
   long long rows = product(A.ext, 0, (size_t)f.rank - 1);
   long long cols = A.ext[(size_t)f.rank - 1];
@@ -865,7 +864,7 @@ int32_t run_row_reduce(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, u
   // thread), 2 vector passes, 3 scalar passes
   const size_t entry = !aligned ? 3 : (cols <= 256LL * vec * 4 ? 0 : (cols <= 256LL * vec * 8 ? 1 : 2));
   const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
-  const uint32_t grid = (uint32_t)(rows < cap ? rows : cap);
+  const uint32_t grid = (uint32_t)cap;
   std::vector<void*> params;
   std::vector<uint64_t> ptrs(A.buf.begin(), A.buf.end());
   for (size_t i = 0; i < ptrs.size(); ++i) params.push_back(&ptrs[i]);
@@ -1261,11 +1260,9 @@ int32_t begin_launch(unp_exec* x, unp_error* err) {
   return UNP_OK;
 }
 
-uint32_t lanes_grid(const unp_exec* x, long long items, long long per_block) {
-  const long long cap = (long long)x->cu_count * 8;
-  const long long want = (items + per_block - 1) / per_block;
-  return (uint32_t)(want < cap ? want : cap);
-}
+// The strided entries' grid: a device-class constant (8 blocks of 256 per CU); blocks stride
+// over the work and those past it exit.
+uint32_t strided_grid(const unp_exec* x) { return (uint32_t)(x->cu_count * 8); }
 
 size_t strided_entry(const unp_exec* x, int which) {
   for (size_t i = 0; i < x->l.entries.size(); ++i)
@@ -1302,7 +1299,7 @@ int32_t strided_reduction(unp_exec* x, const unp_view* v, const std::vector<int6
     const size_t entry = strided_entry(x, o);
     uint64_t ip = view_ptr(in, eb), op = view_ptr(ov, eb);
     void* params[] = {&ip, &op, &d};
-    const uint32_t grid = lanes_grid(x, outs, x->l.red_schedule == 'q' ? 256 : 4);
+    const uint32_t grid = strided_grid(x);
     const int32_t rc = launch(x, entry, grid, params, s, err);
     if (rc != UNP_OK) return rc;
   }
@@ -1330,7 +1327,7 @@ int32_t strided_scan(unp_exec* x, const unp_view* v, const std::vector<int64_t>&
   const size_t eb = unp::kind_bytes(f.dtype);
   uint64_t ip = view_ptr(v[0], eb), op = view_ptr(v[1], eb);
   void* params[] = {&ip, &op, &d};
-  return launch(x, strided_entry(x, 0), lanes_grid(x, cols, 256), params, s, err);
+  return launch(x, strided_entry(x, 0), strided_grid(x), params, s, err);
 }
 
 // A gather over storage images: one lane per output element.
@@ -1362,7 +1359,7 @@ int32_t strided_gather(unp_exec* x, const unp_view* v, const std::vector<int64_t
   long long e64 = src;
   void* ext_arg = f.index_dtype == UNP_I32 ? (void*)&e32 : (f.index_dtype == UNP_U32 ? (void*)&eu32 : (void*)&e64);
   void* params[] = {&tp, &ip, &op, &d, ext_arg};
-  return launch(x, strided_entry(x, 0), lanes_grid(x, outs, 256), params, s, err);
+  return launch(x, strided_entry(x, 0), strided_grid(x), params, s, err);
 }
 
 }  // namespace
