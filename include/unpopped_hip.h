@@ -124,6 +124,20 @@ enum unp_reduce_op {
 };
 /* OobPolicy (ir.rs:2582). */
 enum unp_oob_policy { UNP_OOB_SKIP = 0, UNP_OOB_ZEROFILL = 1, UNP_OOB_CLAMP = 2 };
+/* The schedule a form lowers to.  SERIAL is the serial lift's own order (one lane per output of a
+ * reduction, per column of a scan): the bits of the sequential fold the reference's
+ * Schedule::Reduction and Schedule::Scan { block: false } name (plan/types.rs:30-75).  DEVICE is
+ * this backend's device-class schedule.  Forms whose every schedule gives the same bits (the
+ * gather, the dequants, integer folds) lower the same kernels either way. */
+enum unp_schedule { UNP_SCHEDULE_DEVICE = 0, UNP_SCHEDULE_SERIAL = 1 };
+/* VariantFidelity (backend.rs:204-309) in declaration order: a variant's bits against the cell's
+ * default lowering (here the SERIAL schedule, the sequential fold's bits). */
+enum unp_fidelity {
+  UNP_BIT_IDENTICAL = 0,
+  UNP_DETERMINISTICALLY_DIVERGENT = 1,
+  UNP_NONDETERMINISTIC = 2,
+  UNP_MORE_PRECISE = 3
+};
 
 typedef struct unp_form {
   int32_t kind;        /* unp_form_kind */
@@ -144,11 +158,27 @@ typedef struct unp_form {
                           kernel_lift.rs:854-870); 0 means axes reduced_from..rank-1.
                           scan: the scanned axis as its one bit; 0 means the innermost axis.
                           gather: the gathered axis as its one bit; 0 means axis 0 */
+  int32_t schedule;    /* unp_schedule; 0 (DEVICE) for every form lowered before it existed */
 } unp_form;
 
 /* Lower one form to HIP source (the work Backend::lower_kernel does once it has recognised
- * the lifted kernel).  *out is owned by the caller (unp_generated_free). */
+ * the lifted kernel, and Backend::lower does for a plan the binding maps to a form).  *out is
+ * owned by the caller (unp_generated_free).  A schedule a form does not have is
+ * UNP_UNSUPPORTED_SCHEDULE. */
 int32_t unp_hip_lower_form(const unp_form* form, unp_generated** out, unp_error* err);
+
+/* Variant (backend.rs:313-353): a tag, the form to lower (unp_hip_lower_form) and its fidelity
+ * against the cell's default lowering, the SERIAL schedule. */
+typedef struct unp_variant {
+  char tag[32];
+  int32_t fidelity; /* unp_fidelity */
+  unp_form form;
+  char launch_note[256];
+} unp_variant;
+/* Backend::lower_variants (backend.rs:786-807): every schedule this backend has for the form's
+ * cell, the default (SERIAL) first.  Fills up to `cap` entries of `out` and sets *count to the
+ * number there are; a form with no lowering is refused as unp_hip_lower_form refuses it. */
+int32_t unp_hip_form_variants(const unp_form* form, unp_variant* out, size_t cap, size_t* count, unp_error* err);
 
 /* Backend::lower_kernel (backend.rs:726-737): lower a kernel-layer KernelFn, given as the JSON
  * serde writes for the reference's `KernelFn` (crates/unpopped/src/kernel.rs:1223-1250; element

@@ -792,3 +792,53 @@ def test_launch_cases_corpus_is_refused_typed_and_runs_on_the_c_leg(case):
         assert (same | (np.abs(ia - ib) <= ulps)).all()
     else:
         assert np.array_equal(out, want.astype(nt))
+
+
+# ---------------------------------------------------------------------------------------
+# Schedules and Backend::lower_variants (backend.rs:204-309, 786-807)
+# ---------------------------------------------------------------------------------------
+
+def test_form_variants_name_the_schedules_and_their_fidelity():
+    """Each cell's default is the serial schedule (the sequential fold's bits); the device schedule
+    follows with its honest fidelity: bit-identical for integer folds, deterministically divergent for a
+    float reduction (a fixed device order), nondeterministic for a float look-back scan (the carry's
+    association depends on timing).  Forms whose schedules agree list one."""
+    b = u.HipBackend()
+
+    def summary(**form):
+        return [(v["tag"], v["fidelity"], v["schedule"]) for v in b.form_variants(**form)]
+
+    assert summary(kind="reduction", dtype="F32", rank=2, op="Sum", axes=(1,)) == [
+        ("serial", "BitIdentical", "serial"), ("device", "DeterministicallyDivergent", "device")]
+    assert summary(kind="reduction", dtype="I64", rank=3, op="Xor", axes=(0, 2)) == [
+        ("serial", "BitIdentical", "serial"), ("device", "BitIdentical", "device")]
+    assert summary(kind="reduction", dtype="F32", rank=2, op="Prod", axes=(1,)) == [("serial", "BitIdentical", "serial")]
+    assert summary(kind="scan", dtype="F32", rank=1, op="Sum") == [
+        ("serial", "BitIdentical", "serial"), ("device", "Nondeterministic", "device")]
+    assert summary(kind="scan", dtype="I32", rank=1, op="Sum") == [
+        ("serial", "BitIdentical", "serial"), ("device", "BitIdentical", "device")]
+    assert summary(kind="scan", dtype="F64", rank=2, op="Sum", axes=(0,)) == [("serial", "BitIdentical", "serial")]
+    for form in (dict(kind="gather", dtype="Bf16", rank=2), dict(kind="dequant4"),
+                 dict(kind="row_reduce2", dtype="F32", rank=2), dict(kind="dequant_gemm", dtype="I8", group=128)):
+        assert summary(**form) == [("device", "BitIdentical", "device")], form
+    vs = b.form_variants(kind="reduction", dtype="F32", rank=2, op="Sum", axes=(1,))
+    assert vs[0]["kernel"].interface["schedule"] == "serial"
+    assert "serial lift's own order" in vs[0]["kernel"].interface["fidelity_notes"][0]
+    # refusals are those of lower_form
+    with pytest.raises(_lib.UnpError) as e:
+        b.form_variants(kind="reduction", dtype="F32", rank=2, op="Xor")
+    assert e.value.kind == "UnsupportedOp" or e.value.kind == "UnsupportedKernel"
+
+
+def test_schedules_a_form_does_not_have_are_refused():
+    b = u.HipBackend()
+    with pytest.raises(_lib.UnpError) as e:
+        b.lower_form("row_reduce2", "F32", 2, schedule="serial")
+    assert e.value.kind == "UnsupportedSchedule"
+    f = b.form("reduction", "F32", 2, "Sum")
+    f.schedule = 7
+    out, err = C.c_void_p(), _lib.Error()
+    assert _lib.lib().unp_hip_lower_form(C.byref(f), C.byref(out), C.byref(err)) == 2  # UNSUPPORTED_SCHEDULE
+    # the serial schedule of a gather or a dequant is its one kernel
+    assert (b.lower_form("gather", "Bf16", 2, schedule="serial").source
+            == b.lower_form("gather", "Bf16", 2).source)

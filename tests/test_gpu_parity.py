@@ -1404,3 +1404,69 @@ def test_grids_do_not_follow_the_extents(hip_device):
             grids.add(ex.last_launch()["grid"][0])
         assert len(grids) == 1, (form, grids)
         assert next(iter(grids)) % cus == 0, (form, grids)
+
+
+# ---------------------------------------------------------------------------------------
+# The serial schedule: the sequential fold's bits (the cell's default, Backend::lower)
+# ---------------------------------------------------------------------------------------
+
+_serial_execs: dict = {}
+
+
+def _serial_executor(**form):
+    key = tuple(sorted(form.items()))
+    if key not in _serial_execs:
+        _serial_execs[key] = u.Executor(u.HipBackend().lower_form(schedule="serial", **form))
+    return _serial_execs[key]
+
+
+@pytest.mark.parametrize("dtype,op", [("F32", "Sum"), ("F32", "Mean"), ("F32", "Max"), ("F32", "MinNum"),
+                                      ("F64", "Sum"), ("F64", "Min"), ("I32", "Sum"), ("I64", "Prod"),
+                                      ("I32", "And")])
+@pytest.mark.parametrize("axes", [(1,), (0,), (0, 2)])
+def test_serial_reduction_schedule_is_the_serial_lift_bit_for_bit(hip_device, dtype, op, axes):
+    """The serial schedule folds in the serial lift's order and accumulator: equal, bit for bit, to the
+    oracle's serial fold and to the C99 leg of the serial lift, NaN payloads and signed zeros included,
+    on normal (non-dyadic) data where any other order would round differently."""
+    rank = 3 if 2 in axes else 2
+    shape = (6, 700, 5) if rank == 3 else (37, 900)
+    H.say(f"[case] serial reduction {dtype} {op} axes {axes} {shape}")
+    nt = {"F32": np.float32, "F64": np.float64, "I32": np.int32, "I64": np.int64}[dtype]
+    r = rng(61)
+    if dtype.startswith("F"):
+        x = r.normal(size=shape).astype(nt)
+        flat = x.reshape(-1)
+        flat[::97] = np.nan
+        flat[1::89] = -0.0
+        flat[2::83] = 0.0
+        if op == "Sum":
+            flat[::97] = 1.0  # keep the sums finite and comparable
+    else:
+        info = np.iinfo(nt)
+        x = r.integers(info.min, info.max, size=shape, dtype=np.int64, endpoint=True).astype(nt)
+    kept = [n for d, n in enumerate(shape) if d not in axes]
+    ex = _serial_executor(kind="reduction", dtype=dtype, rank=rank, op=op, axes=axes)
+    din = u.DeviceBuffer.from_array(x)
+    dout = u.DeviceBuffer(int(np.prod(kept)) * x.itemsize)
+    ex.launch(din, dout, *shape)
+    u.synchronize()
+    got = dout.download(nt, int(np.prod(kept))).reshape(kept)
+    assert got.tobytes() == _fold_axes(x, axes, op).tobytes()
+    want = np.zeros(kept, nt)
+    assert cpuc.run(u.lift_reduction("serial", dtype, rank, op, axes=axes), x, want, *shape) == cpuc.OK
+    assert got.tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("dtype,op", [("F32", "Sum"), ("F32", "Max"), ("F64", "Mean"), ("I64", "Sum")])
+def test_serial_scan_schedule_is_the_serial_lift_bit_for_bit(hip_device, dtype, op):
+    """The innermost-axis scan on the serial schedule: bit-exact to the oracle's serial scan on normal
+    data (the device look-back schedule is only within the bound there)."""
+    H.say(f"[case] serial scan {dtype} {op}")
+    nt = {"F32": np.float32, "F64": np.float64, "I64": np.int64}[dtype]
+    x = (rng(62).normal(size=(9, 5000)) * 1000).astype(nt)
+    ex = _serial_executor(kind="scan", dtype=dtype, rank=2, op=op, exclusive=True)
+    din, dout = u.DeviceBuffer.from_array(x), u.DeviceBuffer(x.nbytes)
+    ex.launch(din, dout, *x.shape)
+    u.synchronize()
+    got = dout.download(nt, x.size).reshape(x.shape)
+    assert got.tobytes() == oracle.scan_rows(x, op, True, False).tobytes()

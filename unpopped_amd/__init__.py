@@ -31,6 +31,9 @@ ELEMENT_KINDS = {
 REDUCE_OPS = {"Sum": 0, "Prod": 1, "Max": 2, "Min": 3, "Mean": 4, "And": 5, "Or": 6, "Xor": 7, "MaxNum": 8,
               "MinNum": 9}
 OOB_POLICIES = {"Skip": 0, "ZeroFill": 1, "Clamp": 2}
+SCHEDULES = {"device": 0, "serial": 1}
+# VariantFidelity (backend.rs:204-309), in declaration order.
+FIDELITIES = ["BitIdentical", "DeterministicallyDivergent", "Nondeterministic", "MorePrecise"]
 FORMS = {"reduction": 0, "scan": 1, "gather": 2, "dequant4": 3, "row_reduce2": 4, "row_reduce": 5, "dequant_gemm": 6}
 DTYPE_SUPPORT = {0: "Supported", 1: "Unsupported", 2: "NotExpressible"}
 ARTIFACT_KINDS = {0: "Ptx", 1: "Cubin", 2: "HipCodeObject", 3: "SpirV", 4: "Stub"}
@@ -75,7 +78,20 @@ class HipBackend:
                    op1: str = "Max", reduced_from: int | None = None, exclusive: bool = False,
                    reverse: bool = False, index_dtype: str = "I32", oob: str = "ZeroFill",
                    data_slot: int = 0, q_kind: str = "U4", z_kind: str = "U4", group: int = 128,
-                   out_kind: str = "Bf16", axes: tuple | None = None) -> GeneratedKernel:
+                   out_kind: str = "Bf16", axes: tuple | None = None, schedule: str = "device") -> GeneratedKernel:
+        """Lower one form (``unp_hip_lower_form``); ``schedule`` is ``"device"`` (this backend's
+        device-class schedule) or ``"serial"`` (the serial lift's own order)."""
+        return self._wrap(lambda out, err: _lib.lib().unp_hip_lower_form(
+            C.byref(self.form(kind, dtype, rank, op, op1, reduced_from, exclusive, reverse, index_dtype, oob,
+                              data_slot, q_kind, z_kind, group, out_kind, axes, schedule)), out, err))
+
+    @staticmethod
+    def form(kind: str, dtype: str = "F32", rank: int = 1, op: str = "Sum", op1: str = "Max",
+             reduced_from: int | None = None, exclusive: bool = False, reverse: bool = False,
+             index_dtype: str = "I32", oob: str = "ZeroFill", data_slot: int = 0, q_kind: str = "U4",
+             z_kind: str = "U4", group: int = 128, out_kind: str = "Bf16", axes: tuple | None = None,
+             schedule: str = "device") -> "_lib.Form":
+        """The C ABI's unp_form for these fields."""
         f = _lib.Form()
         f.kind = FORMS[kind]
         f.dtype = ELEMENT_KINDS[dtype]
@@ -93,7 +109,26 @@ class HipBackend:
         f.group = group
         f.out_kind = ELEMENT_KINDS[out_kind]
         f.axes_mask = sum(1 << d for d in axes) if axes else 0
-        return self._wrap(lambda out, err: _lib.lib().unp_hip_lower_form(C.byref(f), out, err))
+        f.schedule = SCHEDULES[schedule]
+        return f
+
+    def form_variants(self, **form) -> list[dict]:
+        """Backend::lower_variants for a form (``unp_hip_form_variants``): each schedule this backend
+        has for the cell, the default first, with its fidelity and the GeneratedKernel it lowers to."""
+        f = self.form(**form)
+        cap = 8
+        arr = (_lib.Variant * cap)()
+        n = C.c_size_t()
+        err = _lib.Error()
+        check(_lib.lib().unp_hip_form_variants(C.byref(f), arr, cap, C.byref(n), C.byref(err)), err)
+        out = []
+        for v in arr[:min(n.value, cap)]:
+            fv = _lib.Form.from_buffer_copy(v.form)
+            g = self._wrap(lambda o, e, fv=fv: _lib.lib().unp_hip_lower_form(C.byref(fv), o, e))
+            out.append({"tag": v.tag.decode(), "fidelity": FIDELITIES[v.fidelity],
+                        "schedule": [k for k, s in SCHEDULES.items() if s == v.form.schedule][0],
+                        "launch_note": v.launch_note.decode(), "kernel": g})
+        return out
 
     def lower_kernel(self, kernel) -> GeneratedKernel:
         """``Backend::lower_kernel`` (backend.rs:726-737): ``kernel`` is a KernelFn as its serde

@@ -40,7 +40,14 @@ class Error(C.Structure):
 class Form(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "kind", "dtype", "rank", "op0", "op1", "reduced_from", "exclusive", "reverse",
-        "index_dtype", "oob", "data_slot", "q_kind", "z_kind", "group", "out_kind")] + [("axes_mask", C.c_uint32)]
+        "index_dtype", "oob", "data_slot", "q_kind", "z_kind", "group", "out_kind")] + [
+        ("axes_mask", C.c_uint32), ("schedule", C.c_int32)]
+
+
+class Variant(C.Structure):
+    """unp_variant: Variant (backend.rs:313-353) as the backend describes it: a tag, a fidelity
+    (VariantFidelity order), the form to lower and a launch note."""
+    _fields_ = [("tag", C.c_char * 32), ("fidelity", C.c_int32), ("form", Form), ("launch_note", C.c_char * 256)]
 
 
 class Arg(C.Structure):
@@ -83,6 +90,7 @@ def lib() -> C.CDLL:
         "unp_generated_revision_hash": (u64, [P]),
         "unp_generated_free": (None, [P]),
         "unp_hip_lower_form": (i32, [C.POINTER(Form), C.POINTER(P), E]),
+        "unp_hip_form_variants": (i32, [C.POINTER(Form), C.POINTER(Variant), sz, C.POINTER(sz), E]),
         "unp_hip_lower_kernel": (i32, [C.c_char_p, C.POINTER(P), E]),
         "unp_lift_reduction": (i32, [C.c_char_p, i32, i32, i32, u32, i32, u32, u32, C.POINTER(C.c_void_p), E]),
         "unp_lift_reduction_x": (i32, [C.c_char_p, i32, i32, i32, u32, i32, i32, C.c_char_p, C.c_char_p, u32, u32,

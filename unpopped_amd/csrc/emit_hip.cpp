@@ -223,8 +223,13 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
     return UNP_LIFT_DECLINE;
   }
   // A float Prod has no order-free form and no declared bound: it runs in the serial lift's own
-  // order (the launched lift refuses it, block_reduce.rs:97-133).
-  const bool serial = kind_is_float(f.dtype) && f.op0 == UNP_OP_PROD;
+  // order (the launched lift refuses it, block_reduce.rs:97-133); so does every reduction asked
+  // for on the serial schedule.
+  if (two && f.schedule == UNP_SCHEDULE_SERIAL) {
+    why = "the fused row fold has no serial schedule (its default is the device schedule)";
+    return UNP_UNSUPPORTED_SCHEDULE;
+  }
+  const bool serial = (kind_is_float(f.dtype) && f.op0 == UNP_OP_PROD) || f.schedule == UNP_SCHEDULE_SERIAL;
   const char sched = serial ? 'q' : reduction_schedule(mask, f.rank);
   if (two && sched != 'r') {
     why = "the fused row fold reduces the trailing axis";
@@ -281,7 +286,7 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
     e.vec = 1;
     e.symbol = L.name + "_q";
     src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(const " << T << "* in, " << T
-        << "* out, unp::red_view d) {\n  unp::reduce_serial_prod<" << T << ", 256>(in, out, d);\n}\n";
+        << "* out, unp::red_view d) {\n  unp::reduce_serial<" << T << ", " << f.op0 << ", 256>(in, out, d);\n}\n";
     L.entries.push_back(e);
   } else if (sched == 'g') {
     L.threads = 256;
@@ -342,7 +347,7 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
     e.symbol = L.name + (o ? "_x1" : "_x");
     src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(const " << T << "* in, " << T
         << "* out, unp::red_view v) {\n  unp::";
-    if (sched == 'q') src << "reduce_serial_prod<" << T << ", 256>(in, out, v);\n}\n";
+    if (sched == 'q') src << "reduce_serial<" << T << ", " << f.op0 << ", 256>(in, out, v);\n}\n";
     else src << "reduce_strided<" << T << ", " << (o ? f.op1 : f.op0) << ", 256>(in, out, v);\n}\n";
     L.entries.push_back(e);
   }
@@ -367,8 +372,8 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
         : sched == 'm' ? "the input as A x R x B: a wave per 64 x vec columns, blocks split R into chunks, the "
                          "last-ticket block of a column strip folds the chunk partials in chunk order"
         : sched == 'g' ? "one wave per output element, lanes stride over the reduced positions"
-        : sched == 'q' ? "one lane per output element, the reduced positions multiplied in the serial lift's "
-                         "order (f64, row-major over the reduced axes)"
+        : sched == 'q' ? "one lane per output element, the reduced positions folded in the serial lift's "
+                         "order (the serial accumulator, row-major over the reduced axes)"
                        : "waves stride over rows (one wave per row); rows longer than 32768 elements: one block per row")
     << "\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i)
@@ -385,7 +390,8 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
                        : "null")
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["
-    << json_str(kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN || (two && (f.op1 == UNP_OP_SUM || f.op1 == UNP_OP_MEAN)))
+    << json_str(sched == 'q' ? "the serial lift's own order and accumulator: bit-exact against the serial kernel for every op"
+                : kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN || (two && (f.op1 == UNP_OP_SUM || f.op1 == UNP_OP_MEAN)))
                     ? "float Sum/Mean: f64 accumulation in an order fixed by (grid, block=256, vector width); "
                       "within the declared bound gamma_(n-1)*sum|x| + 1/2 ulp, not the KernelFn's (block, grid) order"
                     : "order-independent fold: bit-exact against the serial kernel except NaN payload and the sign of a zero in Max/Min")
@@ -441,8 +447,9 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     axis = __builtin_ctz(f.axes_mask);
   }
   // A non-innermost axis, or a float Prod (every product rounds, no declared bound), runs in the
-  // serial lift's own order.
-  const bool serial = axis != f.rank - 1 || (f.op0 == UNP_OP_PROD && kind_is_float(f.dtype));
+  // serial lift's own order; so does every scan asked for on the serial schedule.
+  const bool serial = axis != f.rank - 1 || (f.op0 == UNP_OP_PROD && kind_is_float(f.dtype)) ||
+                      f.schedule == UNP_SCHEDULE_SERIAL;
   L.serial_scan = serial;
   L.scan_axis = axis;
   const char* T = ctype(f.dtype);
@@ -1354,6 +1361,10 @@ int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L
 int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail) {
   out = Lowered{};
   out.form = f;
+  if (f.schedule != UNP_SCHEDULE_DEVICE && f.schedule != UNP_SCHEDULE_SERIAL) {
+    detail = "an unknown schedule";
+    return UNP_UNSUPPORTED_SCHEDULE;
+  }
   switch (f.kind) {
     case UNP_FORM_REDUCTION:
     case UNP_FORM_ROW_REDUCE2:
@@ -1373,6 +1384,57 @@ int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail) {
       detail = "an unknown form";
       return UNP_UNSUPPORTED_KERNEL;
   }
+}
+
+// Backend::lower_variants for a form: the serial schedule (the cell's default: the sequential
+// fold's bits) and the device schedule with its fidelity against it.  Forms whose schedules all
+// give the same bits list one variant; the fused row fold, which has no serial schedule, lists
+// its device schedule as its default.
+int32_t form_variants(const unp_form& f, std::vector<unp_variant>& out, std::string& detail) {
+  out.clear();
+  unp_form dev = f, ser = f;
+  dev.schedule = UNP_SCHEDULE_DEVICE;
+  ser.schedule = UNP_SCHEDULE_SERIAL;
+  Lowered L;
+  const int32_t rc = lower_form(dev, L, detail);
+  if (rc != UNP_OK) return rc;
+  auto add = [&](const char* tag, int32_t fid, const unp_form& form, const std::string& note) {
+    unp_variant v{};
+    std::snprintf(v.tag, sizeof(v.tag), "%s", tag);
+    v.fidelity = fid;
+    v.form = form;
+    std::snprintf(v.launch_note, sizeof(v.launch_note), "%s", note.c_str());
+    out.push_back(v);
+  };
+  const bool fl = kind_is_float(f.dtype);
+  if (f.kind == UNP_FORM_REDUCTION) {
+    add("serial", UNP_BIT_IDENTICAL, ser, "one lane per output, the serial lift's order and accumulator");
+    if (L.red_schedule != 'q') {
+      // Order-free integer folds give the same bits in any order; a float fold's device order is
+      // fixed for a device class but not the serial one (Sum/Mean round differently; Max/Min/
+      // MaxNum/MinNum may keep another NaN payload or zero sign).
+      add("device", fl ? UNP_DETERMINISTICALLY_DIVERGENT : UNP_BIT_IDENTICAL, dev,
+          "cu_count x blocks_per_cu blocks; one launch (the full reduction and the split column "
+          "reduction fold their partials in a last-ticket block)");
+    }
+    return UNP_OK;
+  }
+  if (f.kind == UNP_FORM_SCAN) {
+    add("serial", UNP_BIT_IDENTICAL, ser, "one lane per column, the serial lift's order and accumulator");
+    if (!L.serial_scan) {
+      // The look-back carry's association depends on how far each look-back walked, which
+      // depends on timing: a float result can differ from launch to launch.
+      add("device", fl ? UNP_NONDETERMINISTIC : UNP_BIT_IDENTICAL, dev,
+          "one persistent block per CU drawing tile tickets; decoupled look-back over a tile-status "
+          "workspace tagged with a launch epoch");
+    }
+    return UNP_OK;
+  }
+  // The gather, the dequants and the fused row fold: one schedule.
+  std::string note = "entries picked per launch by alignment and shape:";
+  for (const Entry& e : L.entries) note += " " + e.symbol.substr(L.name.size());
+  add("device", UNP_BIT_IDENTICAL, dev, note);
+  return UNP_OK;
 }
 
 }  // namespace unp

@@ -697,16 +697,25 @@ struct red_view {
   i64 outs, count;
 };
 
-// ---------------------------------------------------------------------------------------
-// A fold whose result depends on its order and has no declared bound (a float Prod: every f64
-// product rounds): the serial lift's order itself (kernel_lift.rs:919-941), one lane per output,
-// the reduced positions ascending in row-major order over the reduced axes into an f64
-// accumulator seeded with 1, one rounding to T at the store.  Bit-exact to the serial lift; not a
-// fast schedule (the dependent multiplies are the critical path).
-// ---------------------------------------------------------------------------------------
+// The serial lifts' accumulator: f64 for every float op (kernel_lift.rs:883-896), the dtype
+// itself for an integer.
+template <class T> struct serial_acc { typedef T type; };
+template <> struct serial_acc<float> { typedef double type; };
 
-template <class T, int THREADS>
-UNP_DEV void reduce_serial_prod(const T* __restrict__ in, T* __restrict__ out, const red_view d) {
+// ---------------------------------------------------------------------------------------
+// The serial lift's own order (kernel_lift.rs:447-484, reduce_loop :919-941): one lane per
+// output, the reduced positions ascending in row-major order over the reduced axes folded into
+// the serial accumulator (f64 for a float, the dtype itself for an integer), one rounding at the
+// store.  The fold functors applied from their identity in this order make exactly the serial
+// lift's steps (the `have` flag's first assignment included: kernel_lift.rs:1097-1160), so this is
+// bit-exact to the serial kernel for every op, NaN payloads and signed zeros included.  The
+// schedule of a float Prod (every product rounds; no declared bound) and the serial schedule of
+// every reduction; not fast (each lane's fold is a dependent chain).
+// ---------------------------------------------------------------------------------------
+template <class T, int OP, int THREADS>
+UNP_DEV void reduce_serial(const T* __restrict__ in, T* __restrict__ out, const red_view d) {
+  typedef typename serial_acc<T>::type Ac;
+  typedef fold<Ac, OP> F;
   const i64 stride = (i64)gridDim.x * THREADS;
   for (i64 o = (i64)blockIdx.x * THREADS + threadIdx.x; o < d.outs; o += stride) {
     i64 off = 0, oo = 0, q = o;
@@ -718,9 +727,9 @@ UNP_DEV void reduce_serial_prod(const T* __restrict__ in, T* __restrict__ out, c
     }
     i64 ctr[8];
     for (i64 k = 0; k < d.nr; ++k) ctr[k] = 0;
-    double a = 1.0;
+    Ac a = F::identity();
     for (i64 t = 0; t < d.count; ++t) {
-      a = a * (double)in[off];
+      a = F::apply(a, (Ac)in[off]);
       // Advance the odometer over the reduced axes (innermost fastest).
       for (i64 k = d.nr - 1; k >= 0; --k) {
         off += d.rstr[k];
@@ -729,7 +738,7 @@ UNP_DEV void reduce_serial_prod(const T* __restrict__ in, T* __restrict__ out, c
         ctr[k] = 0;
       }
     }
-    out[oo] = (T)a;
+    out[oo] = finish<T, OP>(a, d.count);
   }
 }
 
@@ -913,10 +922,6 @@ template <class T, int OP, class A> UNP_DEV T scan_out(A v, i64 count) {
   else return (T)v;
 }
 
-// The serial scan lift's accumulator: f64 for every float op (kernel_lift.rs:883-896), the dtype
-// itself for an integer.
-template <class T> struct serial_acc { typedef T type; };
-template <> struct serial_acc<float> { typedef double type; };
 
 // ---------------------------------------------------------------------------------------
 // A scan in the serial lift's own order (lift_scan_opdef, kernel_lift.rs:504-700): along a

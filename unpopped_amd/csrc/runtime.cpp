@@ -136,6 +136,25 @@ int32_t unp_hip_lower_form(const unp_form* form, unp_generated** out, unp_error*
   return UNP_OK;
 }
 
+int32_t unp_hip_form_variants(const unp_form* form, unp_variant* out, size_t cap, size_t* count, unp_error* err) {
+  if (count) *count = 0;
+  if (!form || !count || (cap && !out)) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null form, output or count");
+    return UNP_INVALID_ARGUMENT;
+  }
+  std::vector<unp_variant> vs;
+  std::string why;
+  const int32_t rc = unp::form_variants(*form, vs, why);
+  if (rc != UNP_OK) {
+    set_error(err, rc, why);
+    return rc;
+  }
+  for (size_t i = 0; i < vs.size() && i < cap; ++i) out[i] = vs[i];
+  *count = vs.size();
+  set_error(err, UNP_OK, "");
+  return UNP_OK;
+}
+
 int32_t unp_hip_lower_kernel(const char* kernel_json, unp_generated** out, unp_error* err) {
   if (out) *out = nullptr;
   if (!kernel_json || !out) {

@@ -124,6 +124,8 @@ struct Lowered {
 // Emit the HIP source and interface for `f`; on refusal returns a nonzero unp_status and
 // fills `detail`.
 int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail);
+// Backend::lower_variants for a form: its schedules with their fidelity, the default first.
+int32_t form_variants(const unp_form& f, std::vector<unp_variant>& out, std::string& detail);
 // A recognised reduction with its body and post (the plain ones go to lower_form).
 int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& out, std::string& detail);
 // The same for a recognised Access::RowReduce.
