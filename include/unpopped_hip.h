@@ -215,6 +215,13 @@ int32_t unp_lift_scan(const char* name, int32_t dtype, int32_t rank, int32_t op,
  * OpDef::embedding is axis 0 with ZeroFill (ir.rs:3884-3886). */
 int32_t unp_lift_gather(const char* name, int32_t dtype, int32_t rank, int32_t index_dtype, int32_t axis,
                         int32_t oob, uint32_t block, uint32_t grid, char** json, unp_error* err);
+/* The gather lift in general (kernel_lift/gather.rs:35-101): n_inputs (2..8) inputs, input
+ * index_slot the integer index, input data_slot the gathered one, the others read at the output
+ * coordinate, and body_json (a ScalarExpr over Input(0..n_inputs), constants allowed) stored at the
+ * output coordinate. */
+int32_t unp_lift_gather_x(const char* name, int32_t dtype, int32_t rank, int32_t index_dtype, int32_t axis,
+                          int32_t oob, int32_t n_inputs, int32_t data_slot, int32_t index_slot, const char* body_json,
+                          uint32_t block, uint32_t grid, char** json, unp_error* err);
 /* No reference lift: the fused two-fold row reduction (softmax prologue) this backend authors,
  * each fold exactly a serial lifted reduction's; launched, rows grid-strided. */
 int32_t unp_kernel_row_reduce2(const char* name, int32_t dtype, int32_t op0, int32_t op1, uint32_t block,

@@ -218,6 +218,42 @@ def gather_cells(table: np.ndarray, ids: np.ndarray, axis: int, policy: str, out
     return out
 
 
+def gather_expr(inputs, index: int, data: int, axis: int, policy: str, body, out_init: np.ndarray,
+                src_extent: int) -> np.ndarray:
+    """The gather lift's cell in general (kernel_lift/gather.rs:35-101, 184-232), one output cell at a
+    time (small cases only): ``raw = inputs[index][c]``; out of ``[0, src_extent)`` Skip leaves the cell
+    and ZeroFill stores 0; otherwise (and always under Clamp) every other input is read at ``c``, the
+    gathered one with ``c[axis]`` replaced by the clamped index, and the body is evaluated on them
+    (the index input as its value) at f64, rounded once to the output's dtype (rx_eval)."""
+    out = np.array(out_init, copy=True)
+    f32 = out.dtype == np.float32
+    leaf = isinstance(body, dict) and list(body) == ["Input"]
+    for c in np.ndindex(out.shape):
+        raw = int(inputs[index][c])
+        below = raw < 0
+        oob = below or raw >= src_extent
+        if oob and policy != "Clamp":
+            if policy == "ZeroFill":
+                out[c] = 0
+            continue
+        cl = 0 if below else (src_extent - 1 if oob else raw)
+        vals = []
+        for k, a in enumerate(inputs):
+            if k == index:
+                vals.append(raw)
+            elif k == data:
+                cc = list(c)
+                cc[axis] = cl
+                vals.append(a[tuple(cc)])
+            else:
+                vals.append(a[c])
+        if leaf:
+            out[c] = vals[int(body["Input"])]
+        else:
+            out[c] = rx_eval(body, np.array(vals, np.float64), f32=f32)
+    return out
+
+
 # ---- dequant --------------------------------------------------------------------------
 
 def dequant4_bf16(q_packed: np.ndarray, scales_f16_bits: np.ndarray, zeros_packed: np.ndarray, rows: int,

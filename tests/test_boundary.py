@@ -511,6 +511,10 @@ def _renumber_cases():
         lambda: u.lift_gather("g", "I32", 3, "U32", axis=2, oob="Skip", launch=(64, 3)),
         lambda: u.lift_row_reduce("softmax", "F32", 2, stages, epi, launch=(256, 64)),
         lambda: u.lift_row_reduce("softmax", "F64", 3, stages, epi),
+        lambda: u.lift_gather("gx", "F32", 2, "I32", oob="ZeroFill", n_inputs=3, data=2, index=0,
+                              body=X.input(2) * X.input(1) + 0.5, launch=(64, 4)),
+        lambda: u.lift_gather("gx", "I64", 3, "U32", axis=1, oob="Skip", n_inputs=3, data=0, index=2,
+                              body=X.input(0)),
     ]
     return out
 
@@ -842,3 +846,37 @@ def test_schedules_a_form_does_not_have_are_refused():
     # the serial schedule of a gather or a dequant is its one kernel
     assert (b.lower_form("gather", "Bf16", 2, schedule="serial").source
             == b.lower_form("gather", "Bf16", 2).source)
+
+
+def test_general_gather_lift_follows_the_gather_lift():
+    """lift_gather_opdef in general (gather.rs:35-101, signature :239-258, cell :184-232): the index
+    input's own dtype, src_extent after the extents, locals per input then src_extent and the clamp;
+    the cell loads the index, lets the clamp, and under the guards loads every other input (the
+    gathered one at the clamped coordinate) before the store of the body."""
+    from unpopped_amd import expr as X
+
+    k = u.lift_gather("g", "F32", 2, "I64", oob="ZeroFill", n_inputs=3, data=2, index=0,
+                      body=X.input(2) * X.input(1))
+    params, locals_ = _sig(k)
+    assert params == [("in0", "Buffer", 2), ("in1", "Buffer", 2), ("in2", "Buffer", 2), ("out", "Buffer", 2),
+                      ("n0", "Scalar", 0), ("n1", "Scalar", 1), ("src_extent", "Scalar", 7)]
+    assert [p["kind"]["Buffer"]["elem"] for p in k["params"][:3]] == ["I64", "F32", "F32"]
+    assert locals_ == ["I32"] * 4 + ["I64", "F32", "F32", "I64", "I64"]
+    compute = [("Load", 5, ("buf", 1)), ("Load", 6, ("buf", 2)), ("Store", ("buf", 3))]
+    zero = [("Store", ("buf", 3))]
+    cell = [("Load", 4, ("buf", 0)), ("Let", 8), ("If", zero, [("If", zero, compute)])]
+    assert skeleton(k["body"]) == [("For", 2, [("For", 3, cell)])]
+    inner = k["body"][0]["For"]["body"][0]["For"]["body"][2]["If"]["els"][0]["If"]["els"]
+    assert inner[1]["Load"]["place"]["Logical"]["coords"] == [{"Local": 8}, {"Local": 3}]
+    assert inner[2]["Store"]["value"] == {"Mul": [{"Local": 6}, {"Local": 5}]}
+    g = u.HipBackend().lower_kernel(k)
+    assert g.interface["inputs"] == 3 and g.interface["index_slot"] == 0 and g.interface["data_slot"] == 2
+    # a body reading a local that is no input, or a body at an integer dtype, is refused
+    bad = json.dumps(k).replace('{"Mul": [{"Local": 6}, {"Local": 5}]}', '{"Mul": [{"Local": 6}, {"Local": 1}]}')
+    with pytest.raises(_lib.UnpError) as e:
+        u.HipBackend().lower_kernel(bad)
+    assert e.value.kind == "UnsupportedKernel"
+    ki = u.lift_gather("g", "I32", 2, "I32", n_inputs=3, body=X.input(0) * X.input(2))
+    with pytest.raises(_lib.UnpError) as e:
+        u.HipBackend().lower_kernel(ki)
+    assert e.value.kind == "UnsupportedKernel"

@@ -1470,3 +1470,90 @@ def test_serial_scan_schedule_is_the_serial_lift_bit_for_bit(hip_device, dtype, 
     u.synchronize()
     got = dout.download(nt, x.size).reshape(x.shape)
     assert got.tobytes() == oracle.scan_rows(x, op, True, False).tobytes()
+
+
+# ---------------------------------------------------------------------------------------
+# The gather lift in general: n inputs, the index and the gathered one anywhere, a body
+# (kernel_lift/gather.rs:35-101)
+# ---------------------------------------------------------------------------------------
+
+_gx_execs: dict = {}
+
+
+def _gx_executor(key, make):
+    if key not in _gx_execs:
+        _gx_execs[key] = u.Executor(u.HipBackend().lower_kernel(make()))
+    return _gx_execs[key]
+
+
+@pytest.mark.parametrize("index_dtype", ["I32", "I64", "U32"])
+@pytest.mark.parametrize("oob", ["Skip", "ZeroFill", "Clamp"])
+def test_gather_with_a_body_and_three_inputs(hip_device, index_dtype, oob):
+    """out[n, d] = table[clamp(ids[n]), d] * scale[n, d] + 0.5 with the ids first and the table last:
+    equal to the oracle's cell (f64, one rounding) and, on these dyadic values, to the C99 leg."""
+    from unpopped_amd import expr as X
+
+    H.say(f"[case] gather with a body, 3 inputs, {index_dtype} {oob}")
+    V, D, N = 40, 48, 33
+    nt = {"I32": np.int32, "I64": np.int64, "U32": np.uint32}[index_dtype]
+    r = rng(81)
+    table = (r.integers(-1000, 1000, (V, D)) / 64).astype(np.float32)
+    scale = (r.integers(-64, 64, (N, D)) / 16).astype(np.float32)
+    ids1 = r.integers(0 if index_dtype == "U32" else -4, V + 4, N).astype(nt)
+    ids = np.broadcast_to(ids1.reshape(N, 1), (N, D)).copy()
+    init = np.full((N, D), 7.0, np.float32)
+    body = X.input(2) * X.input(1) + 0.5
+    make = lambda: u.lift_gather("gx", "F32", 2, index_dtype, oob=oob, n_inputs=3, data=2, index=0,  # noqa: E731
+                                 body=body, launch=(256, 64))
+    ex = _gx_executor(("gx3", index_dtype, oob), make)
+    bufs = [u.DeviceBuffer.from_array(a) for a in (ids1, scale, table, init)]
+    ex.launch(*bufs, N, D, V)
+    u.synchronize()
+    got = bufs[3].download(np.float32, N * D).reshape(N, D)
+    want = oracle.gather_expr([ids, scale, table], 0, 2, 0, oob, body.j, init, V)
+    assert got.tobytes() == want.tobytes()
+    c = init.copy()
+    assert cpuc.run(make(), ids, scale, table, c, N, D, V) == cpuc.OK
+    assert got.tobytes() == c.tobytes()
+
+
+def test_gather_with_a_body_along_an_axis_reading_the_index(hip_device):
+    """F64, rank 3, gathered along axis 1, the body reading the index value itself:
+    out = table[a, clamp(i), b] + 0.25 * ids; every output cell equals the oracle's."""
+    from unpopped_amd import expr as X
+
+    H.say("[case] gather with a body along axis 1, F64")
+    A, Vt, B, N = 3, 11, 6, 9
+    r = rng(82)
+    table = r.normal(size=(A, Vt, B))
+    ids1 = r.integers(-2, Vt + 2, N).astype(np.int32)
+    ids = np.broadcast_to(ids1.reshape(1, N, 1), (A, N, B)).copy()
+    init = np.zeros((A, N, B))
+    body = X.input(1) + X.input(0) * 0.25
+    ex = _gx_executor(("gxa",), lambda: u.lift_gather("gx", "F64", 3, "I32", axis=1, oob="Clamp", n_inputs=2, data=1,
+                                                      index=0, body=body))
+    bufs = [u.DeviceBuffer.from_array(a) for a in (ids1, table, init)]
+    ex.launch(*bufs, A, N, B, Vt)
+    u.synchronize()
+    got = bufs[2].download(np.float64, A * N * B).reshape(A, N, B)
+    assert got.tobytes() == oracle.gather_expr([ids, table], 0, 1, 1, "Clamp", body.j, init, Vt).tobytes()
+
+
+def test_gather_moving_one_input_of_three_through_views(hip_device):
+    """A leaf body over three inputs moves bits (I64 here); through storage images: a full-shape index
+    with a different id in every cell and a transposed table."""
+    from unpopped_amd import expr as X
+
+    H.say("[case] gather leaf body, 3 inputs, views")
+    V, D, N = 20, 12, 15
+    r = rng(83)
+    tstore = r.integers(-2**62, 2**62, (D, V)).astype(np.int64)  # the (V, D) table is its transpose
+    other = r.integers(0, 9, (N, D)).astype(np.int64)
+    ids = r.integers(-3, V + 3, (N, D)).astype(np.int64)
+    init = np.full((N, D), -1, np.int64)
+    ex = _gx_executor(("gxv",), lambda: u.lift_gather("gx", "I64", 2, "I64", oob="ZeroFill", n_inputs=3, data=0,
+                                                      index=2, body=X.input(0)))
+    _, _, _, got = _run_images(ex, [(tstore, (V, D), (1, V), 0), (other, (N, D), (D, 1), 0), (ids, (N, D), (D, 1), 0),
+                                    (init, (N, D), (D, 1), 0)], [N, D, V])
+    want = oracle.gather_expr([tstore.T.copy(), other, ids], 2, 0, 0, "ZeroFill", {"Input": 0}, init, V)
+    assert np.array_equal(got, want)

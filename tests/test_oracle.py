@@ -675,3 +675,38 @@ def test_gather_cells_pins():
     t2 = rng_.integers(0, 2**16, (5, 5), dtype=np.uint16)
     good = oracle.gather_cells(t2, ids, 0, "Skip")
     assert not np.array_equal(oracle.gather_cells(t2, ids.T.copy(), 0, "Skip"), good)
+
+
+def test_general_gather_cell_pins():
+    """The general gather cell (any input order, a body over the gathered element and the other inputs):
+    with the identity body and two inputs it is the per-cell gather; with a body it equals the C99 leg
+    of the same lift on the same inputs within the C leg's per-operation rounding (one rounding at f64
+    here, one per float operation there), and exactly on dyadic data where both are exact."""
+    from unpopped_amd import expr as X
+    from unpopped_amd import forms as H  # noqa: F401  (loads the library)
+    import unpopped_amd as u
+    from oracle import cpuc
+
+    r = np.random.default_rng(71)
+    t = r.integers(-100, 100, (7, 5)).astype(np.float32) / 8  # 7 rows, src_extent 6
+    ids = np.broadcast_to(r.integers(-2, 9, 7).reshape(7, 1), (7, 5)).astype(np.int32).copy()
+    init = np.full((7, 5), 3.0, np.float32)
+    for policy in ("Skip", "ZeroFill", "Clamp"):
+        want = oracle.gather_cells(t, ids, 0, policy, out_init=init, src_extent=6)
+        got = oracle.gather_expr([t, ids], 1, 0, 0, policy, {"Input": 0}, init, 6)
+        assert np.array_equal(got, want), policy
+    # three inputs: ids first, a scale at the output coordinate, the table last; body table * scale + 0.5
+    scale = r.integers(-16, 16, (7, 5)).astype(np.float32) / 4
+    body = X.input(2) * X.input(1) + 0.5
+    for policy in ("Skip", "ZeroFill", "Clamp"):
+        got = oracle.gather_expr([ids, scale, t], 0, 2, 0, policy, body.j, init, 6)
+        k = u.lift_gather("g", "F32", 2, "I32", axis=0, oob=policy, n_inputs=3, data=2, index=0, body=body)
+        c = init.copy()
+        assert cpuc.run(k, ids, scale, t, c, 7, 5, 6) == cpuc.OK
+        assert np.array_equal(got, c), policy  # dyadic: both exact
+    # a planted mistake (the clamped index applied to the wrong input) fails the C99 comparison
+    bad = oracle.gather_expr([ids, scale, t], 0, 1, 0, "Clamp", body.j, init, 6)
+    k = u.lift_gather("g", "F32", 2, "I32", axis=0, oob="Clamp", n_inputs=3, data=2, index=0, body=body)
+    c = init.copy()
+    assert cpuc.run(k, ids, scale, t, c, 7, 5, 6) == cpuc.OK
+    assert not np.array_equal(bad, c)

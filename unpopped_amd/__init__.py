@@ -194,8 +194,18 @@ def lift_scan(name: str, dtype: str, rank: int, op: str, axis: int | None = None
 
 
 def lift_gather(name: str, dtype: str, rank: int, index_dtype: str = "I32", axis: int = 0, oob: str = "ZeroFill",
-                launch: tuple | None = None) -> dict:
+                launch: tuple | None = None, n_inputs: int = 2, data: int = 0, index: int = 1, body=None) -> dict:
+    """The gather lift as a KernelFn dict: by default OpDef::gather (data Input(0), index Input(1), the
+    identity body); in general ``n_inputs`` inputs with the ``data`` and ``index`` slots and ``body`` an
+    elementwise expression over them (an ``expr.Expr`` or its serde dict)."""
     b, g = _geom(launch)
+    if body is not None or n_inputs != 2 or data != 0 or index != 1:
+        from . import expr as X
+
+        bj = json.dumps(X.as_json(X.input(data) if body is None else body)).encode()
+        return _lifted(lambda o, e: _lib.lib().unp_lift_gather_x(
+            name.encode(), ELEMENT_KINDS[dtype], rank, ELEMENT_KINDS[index_dtype], axis, OOB_POLICIES[oob],
+            n_inputs, data, index, bj, b, g, o, e))
     return _lifted(lambda o, e: _lib.lib().unp_lift_gather(name.encode(), ELEMENT_KINDS[dtype], rank,
                                                           ELEMENT_KINDS[index_dtype], axis, OOB_POLICIES[oob],
                                                           b, g, o, e))

@@ -1087,6 +1087,136 @@ bool contains(const kir::J& e, const kir::J& sub) {
 
 }  // namespace
 
+// A gather beyond OpDef::gather (kernel_lift/gather.rs:35-101): n inputs, the index and the
+// gathered data among them, an elementwise body.  One lane per output element: the index at the
+// output coordinate, its clamp and the policy as the cell does (:184-232), every other input read
+// at the output coordinate (the gathered one at the clamped coordinate on the axis), the body
+// evaluated in f64 and rounded once at the store, as the oracle evaluates a statement; a body that
+// is a single input moves its bits.  Every buffer is addressed through its strides (dense ones
+// with their row-major strides), so one entry serves pointer and storage-image launches.
+int32_t lower_gather_x(const unp_form& f, const GatherExpr& gx, Lowered& L, std::string& why) {
+  L = Lowered{};
+  L.form = f;
+  L.gx = gx;
+  const int32_t n = gx.n_inputs, ix = gx.index_slot, data = f.data_slot;
+  if (f.rank < 1 || f.rank > 8 || n < 2 || n > 8 || ix < 0 || ix >= n || data < 0 || data >= n || ix == data) {
+    why = "an ill-formed gather";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (!oob_name(f.oob) || (f.index_dtype != UNP_I32 && f.index_dtype != UNP_I64 && f.index_dtype != UNP_U32)) {
+    why = "an unknown out-of-range policy or a non-integer index";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  const kir::J& b = gx.body;
+  const bool leaf = b.t == kir::J::Obj && b.o.size() == 1 && b.o[0].first == "Input" && b.o[0].second.is_int;
+  const size_t eb = kind_bytes(f.dtype);
+  const char* T = ctype(f.dtype);
+  std::string value;
+  if (leaf) {
+    const int64_t k = b.o[0].second.i;
+    if (k == ix) {
+      why = "a gather whose body is its index";
+      return UNP_UNSUPPORTED_KERNEL;
+    }
+    if (eb == 0) {
+      why = "a gather of a sub-byte element kind";
+      return UNP_UNSUPPORTED_DTYPE;
+    }
+    value = "v" + std::to_string(k);  // the raw element, moved as bits
+  } else {
+    if (f.dtype != UNP_F32 && f.dtype != UNP_F64) {
+      why = "a gather body at " + std::string(kind_name(f.dtype)) + " (bodies are spelled at F32 and F64)";
+      return UNP_UNSUPPORTED_DTYPE;
+    }
+    std::string e;
+    if (!expr_cpp(b, T, e, why)) {
+      why = "body: " + why + " has no spelling here";
+      return UNP_UNSUPPORTED_OP;
+    }
+    value = "(" + std::string(T) + ")(" + e + ")";
+  }
+  const char* E = eb == 1 ? "unsigned char" : eb == 2 ? "unsigned short" : eb == 4 ? "unsigned int" : "unsigned long long";
+  const char* I = ctype(f.index_dtype);
+  std::ostringstream name;
+  name << "unp_gather_x" << n << "_" << lower_name(f.dtype) << "_by_" << lower_name(f.index_dtype) << "_"
+       << oob_name(f.oob) << "_" << std::hex << (fnv1a64(kir::write(b) + std::to_string(ix) + std::to_string(data)) & 0xffffffffu);
+  L.name = name.str();
+  L.threads = 256;
+  L.blocks_per_cu = 8;
+  L.scan_axis = 0;
+  for (int32_t d = 0; d < f.rank; ++d)
+    if ((f.axes_mask >> d) & 1u) L.scan_axis = d;
+  std::ostringstream src;
+  src << header(L.name, f);
+  Entry e;
+  e.fast = false;
+  e.strided = false;
+  e.vec = (int)eb;
+  e.symbol = L.name + "_e";
+  src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(";
+  for (int k = 0; k < n; ++k) src << "const void* in" << k << ", ";
+  src << "void* out, unp::gather_x_view v, " << I << " src_extent) {\n"
+      << "  const long long stride = (long long)gridDim.x * blockDim.x;\n"
+      << "  for (long long o = (long long)blockIdx.x * blockDim.x + threadIdx.x; o < v.outs; o += stride) {\n"
+      << "    long long c[8], q = o, oo = 0;\n"
+      << "    for (long long d = v.rank - 1; d >= 0; --d) { c[d] = q % v.ext[d]; q /= v.ext[d]; oo += c[d] * v.ostr[d]; }\n"
+      << "    auto at = [&](int k) { long long s = 0; for (long long d = 0; d < v.rank; ++d) s += c[d] * v.istr[k][d]; return s; };\n"
+      << "    const " << I << " raw = static_cast<const " << I << "*>(in" << ix << ")[at(" << ix << ")];\n"
+      << "    const bool below = unp::below_zero(raw);\n"
+      << "    const bool oob = below || !(raw < src_extent);\n";
+  if (f.oob != UNP_OOB_CLAMP) {
+    src << "    if (oob) {\n";
+    if (f.oob == UNP_OOB_ZEROFILL) src << "      static_cast<" << E << "*>(out)[oo] = 0;\n";
+    src << "      continue;\n    }\n";
+  }
+  src << "    const " << I << " cl = below ? (" << I << ")0 : (oob ? (" << I << ")(src_extent - (" << I << ")1) : raw);\n";
+  for (int k = 0; k < n; ++k) {
+    if (k == ix) continue;
+    src << "    const long long off" << k << " = at(" << k << ")"
+        << (k == data ? " + ((long long)cl - c[v.axis]) * v.istr[" + std::to_string(k) + "][v.axis]" : std::string())
+        << ";\n";
+    if (leaf) src << "    const " << E << " v" << k << " = static_cast<const " << E << "*>(in" << k << ")[off" << k << "];\n";
+  }
+  if (leaf) {
+    src << "    static_cast<" << E << "*>(out)[oo] = " << value << ";\n";
+  } else {
+    src << "    double x[" << n << "];\n";
+    for (int k = 0; k < n; ++k) {
+      if (k == ix) src << "    x[" << k << "] = (double)raw;\n";
+      else src << "    x[" << k << "] = (double)static_cast<const " << T << "*>(in" << k << ")[off" << k << "];\n";
+    }
+    src << "    static_cast<" << T << "*>(out)[oo] = " << value << ";\n";
+  }
+  src << "  }\n}\n";
+  L.entries.push_back(e);
+  Entry x = e;
+  x.strided = true;  // the same entry reads storage images
+  L.entries.push_back(x);
+  L.source = src.str();
+  std::ostringstream j;
+  j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"gather\",\"dtype\":\"" << kind_name(f.dtype)
+    << "\",\"index_dtype\":\"" << kind_name(f.index_dtype) << "\",\"oob\":\"" << oob_name(f.oob)
+    << "\",\"axis\":" << L.scan_axis << ",\"rank\":" << f.rank << ",\"inputs\":" << n << ",\"index_slot\":" << ix
+    << ",\"data_slot\":" << data << ",\"body\":" << json_str(kir::write(b)) << ",\"params\":[";
+  for (int k = 0; k < n; ++k)
+    j << "{\"name\":\"in" << k << "\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\""
+      << kind_name(k == ix ? f.index_dtype : f.dtype) << "\"},";
+  j << "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
+  for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
+  j << ",{\"name\":\"src_extent\",\"kind\":\"scalar\",\"dtype\":\"" << kind_name(f.index_dtype)
+    << "\"}],\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*8\",\"grid_policy\":\"one lane per output "
+       "element, lanes stride over the outputs\"},\"entries\":[{\"symbol\":\""
+    << e.symbol << "\",\"when\":\"always (dense buffers with their row-major strides, storage images with theirs)\"}]"
+    << ",\"workspace\":null,\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
+    << ",\"fidelity_notes\":["
+    << json_str(leaf ? "a raw bit move: bit-exact for every grid and block"
+                     : "the body evaluated in f64 and rounded once at the store, as the oracle evaluates a statement; "
+                       "bit-exact against the oracle")
+    << "]}";
+  L.interface_json = j.str();
+  return UNP_OK;
+}
+
 int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) {
   L = Lowered{};
   L.form.kind = UNP_FORM_ROW_REDUCE;

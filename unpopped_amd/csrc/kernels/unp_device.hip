@@ -1620,6 +1620,16 @@ struct gather_view {
   i64 outs;
 };
 
+// The general gather's storage images (kernel_lift/gather.rs:35-101): the output's extents and
+// strides, and every input's strides over the output coordinates (the gathered input's stride
+// along `axis` applies to the clamped index); the emitted kernel evaluates the body.
+struct gather_x_view {
+  i64 rank, axis;
+  i64 ext[8], ostr[8];
+  i64 istr[8][8];
+  i64 outs;
+};
+
 template <class E, class IDX, int POLICY>
 UNP_DEV void gather_strided(const E* __restrict__ table, const IDX* __restrict__ ids, E* __restrict__ out,
                             const gather_view v, IDX src_extent) {

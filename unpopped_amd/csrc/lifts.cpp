@@ -476,34 +476,59 @@ void grid_stride(J& k, uint32_t block, uint32_t grid) {
     if (kv.first == "launch") kv.second = launch_shape(block, grid);
 }
 
-// lift_gather_opdef (kernel_lift/gather.rs:35-55, cell :184-232) for OpDef::gather's inputs:
-// Input(0) the data, Input(1) the index, the identity copy body; launched by grid_stride.
+void check_post(const J& e, int64_t available, int64_t n_inputs);
+J input_leaf(uint32_t k);
+int64_t leaf_index(const J& e);
+template <class F> J map_leaves(const J& e, const F& leaf);
+
+// lift_gather_opdef (kernel_lift/gather.rs:35-55, check_gather :64-101, cell :184-232): n inputs,
+// input `index` the integer index (read at the output coordinate), input `data` the gathered one
+// (read with its `axis` coordinate replaced by the clamped index), the others read at the output
+// coordinate, and `body` an elementwise expression over Input(0..n) stored at the output
+// coordinate (OpDef::gather is n = 2, data 0, index 1 and the identity body Input(0),
+// ir.rs:3838-3855).  Launched by grid_stride.
 J lift_gather(const std::string& name, int32_t dtype, int32_t rank, int32_t idx, int32_t axis, int32_t oob,
-              uint32_t block, uint32_t grid) {
+              uint32_t block, uint32_t grid, uint32_t n = 2, uint32_t data = 0, uint32_t index = 1,
+              const J* body_expr = nullptr) {
   check_rank(rank);
   if (idx != UNP_I32 && idx != UNP_I64 && idx != UNP_U32) throw Decline{"UnsupportedForm: a non-integer gather index"};
-  if (axis < 0 || axis >= rank) throw Decline{"UnsupportedForm: an ill-formed gather"};
+  if (axis < 0 || axis >= rank || n < 2 || n > 8 || data >= n || index >= n || data == index)
+    throw Decline{"UnsupportedForm: an ill-formed gather"};
   if (!kind_name(dtype) || kind_bytes(dtype) == 0) throw Decline{"UnsupportedForm: a gather of a sub-byte dtype"};
-  const uint32_t r = (uint32_t)rank, n = 2, data = 0, index = 1;
-  const uint32_t loaded0 = 2 * r, loaded1 = 2 * r + 1, extent = 2 * r + n, clamped = extent + 1;
+  const J plain = input_leaf(data);
+  const J& bexpr = body_expr ? *body_expr : plain;
+  check_post(bexpr, 0, (int64_t)n);  // leaves_ok: the inputs and constants only
+  const uint32_t r = (uint32_t)rank;
+  auto loaded = [&](uint32_t k) { return 2 * r + k; };
+  const uint32_t extent = 2 * r + n, clamped = extent + 1;
   auto at = [&](uint32_t buffer, int via_axis, uint32_t via) {
     std::vector<J> c;
     for (uint32_t d = 0; d < r; ++d) c.push_back(((int)d == via_axis) ? loc(via) : loc(r + d));
     return p_logical(buffer, c);
   };
   auto ic = [&](int64_t v) { return e_int(v, EK(idx)); };
-  J raw = loc(loaded1);
+  J raw = loc(loaded(index));
   J clamp = e_bin("Min", e_bin("Max", raw, ic(0)), e_sub(loc(extent), ic(1)));
   J zero = (dtype == UNP_I32 || dtype == UNP_I64 || dtype == UNP_U32 || dtype == UNP_I8 || dtype == UNP_I16 ||
             dtype == UNP_U8 || dtype == UNP_U16 || dtype == UNP_U64)
                ? e_int(0, EK(dtype))
                : e_const(0.0);
-  std::vector<J> compute = {s_load(loaded0, at(data, axis, clamped)), s_store(at(n, -1, 0), loc(loaded0))};
+  std::vector<J> compute;
+  for (uint32_t k = 0; k < n; ++k)
+    if (k != index) compute.push_back(s_load(loaded(k), k == data ? at(k, axis, clamped) : at(k, -1, 0)));
+  const J value = map_leaves(bexpr, [&](const J& x, J& o) {
+    if (x.t == J::Obj && x.o.size() == 1 && x.o[0].first == "Input") {
+      o = loc(loaded((uint32_t)leaf_index(x)));
+      return true;
+    }
+    return false;
+  });
+  compute.push_back(s_store(at(n, -1, 0), value));
   auto guarded = [&](std::vector<J> oobb) {
     J upper = s_if(e_bin("CmpGe", raw, loc(extent)), oobb, compute);
     return s_if(e_bin("CmpLt", raw, ic(0)), oobb, {upper});
   };
-  std::vector<J> cell = {s_load(loaded1, at(index, -1, 0)), s_let(clamped, clamp)};
+  std::vector<J> cell = {s_load(loaded(index), at(index, -1, 0)), s_let(clamped, clamp)};
   if (oob == UNP_OOB_SKIP) cell.push_back(guarded({}));
   else if (oob == UNP_OOB_ZEROFILL) cell.push_back(guarded({s_store(at(n, -1, 0), zero)}));
   else if (oob == UNP_OOB_CLAMP)
@@ -511,16 +536,17 @@ J lift_gather(const std::string& name, int32_t dtype, int32_t rank, int32_t idx,
   else throw Decline{"UnsupportedForm: an unknown out-of-range policy"};
   std::vector<J> body = cell;
   for (int d = (int)r - 1; d >= 0; --d) body = {s_for(r + d, int_(0), loc((uint32_t)d), int_(1), body)};
-  std::vector<J> params = {param_buffer("in0", EK(dtype), "Read", rank), param_buffer("in1", EK(idx), "Read", rank),
-                           param_buffer("out", EK(dtype), "Write", rank)};
+  auto elem = [&](uint32_t k) { return k == index ? EK(idx) : EK(dtype); };
+  std::vector<J> params;
+  for (uint32_t k = 0; k < n; ++k) params.push_back(param_buffer("in" + std::to_string(k), elem(k), "Read", rank));
+  params.push_back(param_buffer("out", EK(dtype), "Write", rank));
   for (uint32_t d = 0; d < r; ++d) params.push_back(param_scalar("n" + std::to_string(d), "I32", d));
   params.push_back(param_scalar("src_extent", EK(idx), extent));
   std::vector<J> locals;
   for (uint32_t i = 0; i < 2 * r; ++i) locals.push_back(local_decl("I32"));
-  locals.push_back(local_decl(EK(dtype)));
-  locals.push_back(local_decl(EK(idx)));
-  locals.push_back(local_decl(EK(idx)));
-  locals.push_back(local_decl(EK(idx)));
+  for (uint32_t k = 0; k < n; ++k) locals.push_back(local_decl(elem(k)));
+  locals.push_back(local_decl(EK(idx)));  // src_extent
+  locals.push_back(local_decl(EK(idx)));  // clamped index
   J k = kernel_fn(name, EK(dtype), params, locals, body, J::null(), {});
   if (block || grid) grid_stride(k, block, grid);
   return k;
@@ -1419,24 +1445,94 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
           return UNP_OK;
         }
   }
-  // Gather: in0 data, in1 index, out, r I32 extents, src_extent.
-  if (np >= 5 && ps[0].buffer && ps[1].buffer && ps[2].buffer && ps[2].role == "Write" && ps[0].rank >= 1 &&
-      (size_t)ps[0].rank + 4 == np) {
-    const int32_t r = ps[0].rank;
+  // Gather: n inputs (one the integer index), out (Write), r I32 extents, src_extent of the index
+  // dtype.  The body is read back from the cell's last store (the loaded locals unbound to
+  // Input(k)); each candidate (index slot, data slot, axis, policy) is re-lifted and compared.
+  {
+    size_t nb = 0;
+    while (nb < np && ps[nb].buffer) ++nb;
+    const size_t n = nb >= 3 ? nb - 1 : 0;
+    const int32_t r = n ? ps[n].rank : 0;
+    const bool shape = n >= 2 && n <= 8 && ps[n].role == "Write" && r >= 1 && r <= 8 && np == nb + (size_t)r + 1 &&
+                       (ps[np - 1].elem == UNP_I32 || ps[np - 1].elem == UNP_I64 || ps[np - 1].elem == UNP_U32);
+    bool sig_ok = shape;
+    for (size_t i = nb; sig_ok && i + 1 < np; ++i) sig_ok = ps[i].elem == UNP_I32;
+    for (size_t i = 0; sig_ok && i < n; ++i) sig_ok = ps[i].role == "Read" && ps[i].rank == r;
+    const int32_t idx = sig_ok ? ps[np - 1].elem : -1, dt = sig_ok ? ps[n].elem : -1;
     static const int32_t pols[] = {UNP_OOB_SKIP, UNP_OOB_ZEROFILL, UNP_OOB_CLAMP};
-    for (int32_t axis = 0; axis < r; ++axis)
-      for (int32_t pol : pols)
-        if (attempt([&] { return lift_gather(name, ps[0].elem, r, ps[1].elem, axis, pol, block, grid); })) {
-          out.form.kind = UNP_FORM_GATHER;
-          out.form.axes_mask = axis == 0 ? 0u : (1u << axis);
-          out.form.dtype = ps[0].elem;
-          out.form.rank = r;
-          out.form.index_dtype = ps[1].elem;
-          out.form.oob = pol;
-          out.form.data_slot = 0;
-          out.lift = block ? "lift_gather_opdef_launched" : "lift_gather_opdef";
-          return UNP_OK;
+    // The body of the kernel `kk` in the lift's numbering: the last store to the output.
+    auto gather_body = [&](const J& kk, J& body) {
+      const J* last = nullptr;
+      find_stmt(*kk.get("body"), [&](const J& x) {
+        const J* st = x.get("Store");
+        const J* pl = st ? st->get("place") : nullptr;
+        const J* lg = pl ? pl->get("Logical") : nullptr;
+        if (lg && lg->get("buffer") && lg->get("buffer")->is_int && lg->get("buffer")->i == (int64_t)n) last = &x;
+        return false;
+      });
+      if (!last) return false;
+      bool ok = true;
+      try {
+        body = map_leaves(*last->get("Store")->get("value"), [&](const J& x, J& o) {
+          if (x.t != J::Obj || x.o.size() != 1 || x.o[0].first != "Local") return false;
+          const int64_t l = leaf_index(x);
+          if (l >= 2 * (int64_t)r && l < 2 * (int64_t)r + (int64_t)n) o = input_leaf((uint32_t)(l - 2 * r));
+          else {
+            ok = false;
+            o = x;
+          }
+          return true;
+        });
+      } catch (const Decline&) {
+        return false;
+      }
+      return ok;
+    };
+    auto take_gather = [&](uint32_t index, uint32_t data, int32_t axis, int32_t pol, const J& body) {
+      out.form.kind = UNP_FORM_GATHER;
+      out.form.axes_mask = axis == 0 ? 0u : (1u << axis);
+      out.form.dtype = dt;
+      out.form.rank = r;
+      out.form.index_dtype = idx;
+      out.form.oob = pol;
+      out.form.data_slot = (int32_t)data;
+      out.gx.n_inputs = (int32_t)n;
+      out.gx.index_slot = (int32_t)index;
+      out.gx.body = body;
+      out.gx.plain = n == 2 && body == input_leaf(data);
+      out.lift = block ? "lift_gather_opdef_launched" : "lift_gather_opdef";
+      return UNP_OK;
+    };
+    for (int pass = 0; sig_ok && pass < 2; ++pass) {
+      for (uint32_t index = 0; index < n; ++index) {
+        if (ps[index].elem != idx) continue;
+        bool others = true;
+        for (uint32_t k = 0; k < n; ++k)
+          if (k != index && ps[k].elem != dt) others = false;
+        if (!others) continue;
+        J body;
+        const bool fast_body = pass == 0 && gather_body(k, body);
+        if (pass == 0 && !fast_body) continue;
+        for (uint32_t data = 0; data < n; ++data) {
+          if (data == index) continue;
+          for (int32_t axis = 0; axis < r; ++axis)
+            for (int32_t pol : pols) {
+              if (pass == 1) {
+                // Locals numbered otherwise: renumber into the candidate's numbering first.
+                J proto, kr;
+                try {
+                  proto = lift_gather(name, dt, r, idx, axis, pol, block, grid, (uint32_t)n, data, index);
+                } catch (const Decline&) {
+                  continue;
+                }
+                if (!into_numbering_of(proto, kc, kr) || !gather_body(kr, body)) continue;
+              }
+              if (attempt([&] { return lift_gather(name, dt, r, idx, axis, pol, block, grid, (uint32_t)n, data, index, &body); }))
+                return take_gather(index, data, axis, pol, body);
+            }
         }
+      }
+    }
   }
   // Dequant: w (U4/I4), scale (F16), zero (U4/I4), out (Bf16), two I32 extents; the group is
   // the constant of the column-group counting loop.
@@ -1697,6 +1793,26 @@ int32_t unp_lift_gather(const char* name, int32_t dtype, int32_t rank, int32_t i
                         int32_t oob, uint32_t block, uint32_t grid, char** json, unp_error* err) {
   return unp::lift_call(json, err, [&] {
     return unp::lift_gather(name ? name : "gather", dtype, rank, index_dtype, axis, oob, block, grid);
+  });
+}
+
+int32_t unp_lift_gather_x(const char* name, int32_t dtype, int32_t rank, int32_t index_dtype, int32_t axis,
+                          int32_t oob, int32_t n_inputs, int32_t data_slot, int32_t index_slot, const char* body_json,
+                          uint32_t block, uint32_t grid, char** json, unp_error* err) {
+  using unp::kir::J;
+  J body;
+  std::string why;
+  if (!body_json || !unp::kir::parse(body_json, body, why)) {
+    unp::set_error(err, UNP_PARSE_ERROR, "body: a ScalarExpr expected " + why);
+    return UNP_PARSE_ERROR;
+  }
+  if (n_inputs < 2 || n_inputs > 8 || data_slot < 0 || index_slot < 0) {
+    unp::set_error(err, UNP_LIFT_DECLINE, "UnsupportedForm: an ill-formed gather");
+    return UNP_LIFT_DECLINE;
+  }
+  return unp::lift_call(json, err, [&] {
+    return unp::lift_gather(name ? name : "gather", dtype, rank, index_dtype, axis, oob, block, grid,
+                            (uint32_t)n_inputs, (uint32_t)data_slot, (uint32_t)index_slot, &body);
   });
 }
 

@@ -180,8 +180,9 @@ int32_t unp_hip_lower_kernel(const char* kernel_json, unp_generated** out, unp_e
       return rc;
     }
   } else {
-    rc = rec.form.kind == UNP_FORM_REDUCTION ? unp::lower_reduction_x(rec.form, rec.rx, g->l, why)
-                                            : unp::lower_form(rec.form, g->l, why);
+    rc = rec.form.kind == UNP_FORM_REDUCTION                       ? unp::lower_reduction_x(rec.form, rec.rx, g->l, why)
+         : (rec.form.kind == UNP_FORM_GATHER && !rec.gx.plain) ? unp::lower_gather_x(rec.form, rec.gx, g->l, why)
+                                                               : unp::lower_form(rec.form, g->l, why);
     if (rc != UNP_OK) {
       delete g;
       // A recognised lift whose form this backend has no kernel for is a refusal of the kernel.
@@ -892,7 +893,71 @@ int32_t run_row_reduce(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, u
   return launch(x, entry, grid, params.data(), s, err);
 }
 
+// The general gather's launch: the descriptor from each input's strides (istr[k][d] over the output
+// coordinates), the output's, and the source extent.
+int32_t launch_gather_x(unp_exec* x, const std::vector<uint64_t>& ptrs, const unp::gather_x_view_host& v,
+                        int64_t raw_src, hipStream_t s, unp_error* err) {
+  const unp_form& f = x->l.form;
+  if (v.outs == 0) return UNP_OK;
+  int64_t src = raw_src;
+  if (f.index_dtype == UNP_I32) src = (int64_t)(int32_t)(uint32_t)(uint64_t)raw_src;
+  else if (f.index_dtype == UNP_U32) src = (int64_t)(uint32_t)(uint64_t)raw_src;
+  if (src <= 0 && f.oob == UNP_OOB_CLAMP) {
+    set_error(err, UNP_INVALID_ARGUMENT, "a Clamp gather needs a source extent of at least 1");
+    return UNP_INVALID_ARGUMENT;
+  }
+  int32_t e32 = (int32_t)src;
+  uint32_t eu32 = (uint32_t)src;
+  long long e64 = src;
+  std::vector<uint64_t> p(ptrs);
+  std::vector<void*> params;
+  for (auto& q : p) params.push_back(&q);
+  unp::gather_x_view_host vv = v;
+  params.push_back(&vv);
+  params.push_back(f.index_dtype == UNP_I32 ? (void*)&e32 : (f.index_dtype == UNP_U32 ? (void*)&eu32 : (void*)&e64));
+  return launch(x, 0, (uint32_t)(x->cu_count * x->l.blocks_per_cu), params.data(), s, err);
+}
+
+// A general gather from device addresses: every input dense over the output's shape, the
+// gathered one with src_extent along the axis, the index 1-D along the axis (broadcast over the
+// others, as the row gather reads it).
+int32_t run_gather_x(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  const unp_form& f = x->l.form;
+  const size_t NI = (size_t)x->l.gx.n_inputs;
+  Args A;
+  int32_t rc = take_args(a, n, NI + 1, (size_t)f.rank + 1, A, err);
+  if (rc == UNP_OK) rc = extents_i32(A, (size_t)f.rank, err);
+  if (rc != UNP_OK) return rc;
+  const int ax = x->l.scan_axis, ix = x->l.gx.index_slot, data = f.data_slot;
+  unp::gather_x_view_host v{};
+  v.rank = f.rank;
+  v.axis = ax;
+  v.outs = 1;
+  for (int d = 0; d < f.rank; ++d) {
+    v.ext[d] = A.ext[(size_t)d];
+    v.outs *= v.ext[d];
+  }
+  if ((rc = need_buffers(A, v.outs > 0, err)) != UNP_OK) return rc;
+  int64_t src = (int64_t)A.ext[(size_t)f.rank];
+  if (f.index_dtype == UNP_I32) src = (int64_t)(int32_t)(uint32_t)(uint64_t)src;
+  else if (f.index_dtype == UNP_U32) src = (int64_t)(uint32_t)(uint64_t)src;
+  for (size_t k = 0; k <= NI; ++k) {
+    long long st = 1;
+    for (int d = f.rank - 1; d >= 0; --d) {
+      long long e = v.ext[d];
+      if ((int)k == data && d == ax) e = src > 0 ? src : 0;
+      if (k == NI) v.ostr[d] = st;
+      else if ((int)k == ix) v.istr[k][d] = d == ax ? 1 : 0;
+      else v.istr[k][d] = st;
+      st *= e;
+    }
+  }
+  std::vector<uint64_t> ptrs(A.buf.begin(), A.buf.end());
+  return launch_gather_x(x, ptrs, v, (int64_t)A.ext[(size_t)f.rank], s, err);
+}
+
 int32_t run_gather(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  if (!x->l.gx.plain) return run_gather_x(x, a, n, s, err);
   const unp_form& f = x->l.form;
   Args A;
   int32_t rc = take_args(a, n, 3, (size_t)f.rank + 1, A, err);
@@ -1058,10 +1123,14 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
 }  // namespace
 
 // Element bits of buffer parameter b of a form: the element kinds of its storage images.
-static int view_elem_bits(const unp_form& f, size_t b) {
+static int view_elem_bits(const unp::Lowered& l, size_t b) {
+  const unp_form& f = l.form;
   int32_t k = f.dtype;
   if (f.kind == UNP_FORM_GATHER) {
-    k = (b == 2 || (int)b == f.data_slot) ? f.dtype : f.index_dtype;
+    // buffer b of a gather: the index slot carries the index kind, every other buffer the data's
+    // (the plain gather's index is the input that is not data_slot)
+    const bool index = l.gx.plain ? ((b == 0 || b == 1) && (int)b != f.data_slot) : (int)b == l.gx.index_slot;
+    k = index ? f.index_dtype : f.dtype;
   } else if (f.kind == UNP_FORM_DEQUANT4) {
     const int32_t ks[4] = {f.q_kind, UNP_F16, f.z_kind, f.out_kind};
     if (b < 4) k = ks[b];
@@ -1085,7 +1154,7 @@ void param_counts(const unp_exec* x, size_t& nbuf, size_t& nscal) {
     case UNP_FORM_REDUCTION: nbuf = (size_t)x->l.rx.n_inputs + 1; nscal = (size_t)f.rank; break;
     case UNP_FORM_ROW_REDUCE2: nbuf = 3; nscal = 2; break;
     case UNP_FORM_SCAN: nbuf = 2; nscal = (size_t)f.rank; break;
-    case UNP_FORM_GATHER: nbuf = 3; nscal = (size_t)f.rank + 1; break;
+    case UNP_FORM_GATHER: nbuf = (size_t)x->l.gx.n_inputs + 1; nscal = (size_t)f.rank + 1; break;
     case UNP_FORM_ROW_REDUCE: nbuf = (size_t)x->l.rr.n_inputs + 1; nscal = (size_t)x->l.rr.rank; break;
     case UNP_FORM_DEQUANT4: nbuf = 4; nscal = 2; break;
     case UNP_FORM_DEQUANT_GEMM: nbuf = 5; nscal = 3; break;
@@ -1143,14 +1212,16 @@ std::vector<Want> wanted_shapes(const unp_exec* x, const std::vector<int64_t>& e
       one(ext);
       break;
     case UNP_FORM_GATHER: {
+      // The gathered input (data_slot) is the table; every other input, the index among them,
+      // has the output's shape.
       Want t;
       t.shape = ext;
       t.table_axis = x->l.scan_axis;
       t.table_rows = std::max<int64_t>(0, gather_src_extent(f, sc[f.rank]));
-      Want i;
-      i.shape = ext;
-      w.push_back(f.data_slot == 0 ? t : i);
-      w.push_back(f.data_slot == 0 ? i : t);
+      for (int32_t k = 0; k < x->l.gx.n_inputs; ++k) {
+        if (k == f.data_slot) w.push_back(t);
+        else one(ext);
+      }
       one(ext);
       break;
     }
@@ -1247,6 +1318,7 @@ bool views_dense(const unp_exec* x, const unp_view* v, size_t n, int64_t src_ext
   const unp_form& f = x->l.form;
   for (size_t b = 0; b < n; ++b) {
     if (view_empty(v[b])) continue;
+    if (f.kind == UNP_FORM_GATHER && !x->l.gx.plain) return false;  // one entry reads every layout
     if (f.kind == UNP_FORM_GATHER && b < 2) {
       const int ax = x->l.scan_axis;
       if ((int)b == f.data_slot) {
@@ -1353,6 +1425,25 @@ int32_t strided_scan(unp_exec* x, const unp_view* v, const std::vector<int64_t>&
 int32_t strided_gather(unp_exec* x, const unp_view* v, const std::vector<int64_t>& ext, int64_t raw_src,
                        hipStream_t s, unp_error* err) {
   const unp_form& f = x->l.form;
+  if (!x->l.gx.plain) {
+    const size_t NI = (size_t)x->l.gx.n_inputs;
+    unp::gather_x_view_host d{};
+    d.rank = f.rank;
+    d.axis = x->l.scan_axis;
+    d.outs = 1;
+    for (int a = 0; a < f.rank; ++a) {
+      d.ext[a] = ext[(size_t)a];
+      d.ostr[a] = v[NI].stride[a];
+      d.outs *= ext[(size_t)a];
+      for (size_t k = 0; k < NI; ++k) d.istr[k][a] = v[k].stride[a];
+    }
+    std::vector<uint64_t> ptrs;
+    for (size_t k = 0; k <= NI; ++k) {
+      const int32_t kind = (int)k == x->l.gx.index_slot ? f.index_dtype : f.dtype;
+      ptrs.push_back(view_ptr(v[k], unp::kind_bytes(kind)));
+    }
+    return launch_gather_x(x, ptrs, d, raw_src, s, err);
+  }
   const unp_view& tv = v[f.data_slot == 0 ? 0 : 1];
   const unp_view& iv = v[f.data_slot == 0 ? 1 : 0];
   const unp_view& ov = v[2];
@@ -1414,7 +1505,7 @@ extern "C" int32_t unp_hip_exec_launch_views(unp_exec* x, const unp_view* views,
     if (view_empty(v)) continue;
     // Every element the view names must lie at or above the storage start, and its offsets must
     // stay well inside the kernels' 64-bit index arithmetic.
-    const int bits = view_elem_bits(f, b);
+    const int bits = view_elem_bits(x->l, b);
     __int128 lo = v.base, hi = v.base;
     for (int d = 0; d < v.rank; ++d) {
       const __int128 span = (__int128)v.stride[d] * (v.shape[d] - 1);
@@ -1431,7 +1522,7 @@ extern "C" int32_t unp_hip_exec_launch_views(unp_exec* x, const unp_view* views,
   if (views_dense(x, views, nviews, src)) {
     std::vector<unp_arg> args(nviews + nscalars);
     for (size_t b = 0; b < nviews; ++b) {
-      const int bits = view_elem_bits(f, b);
+      const int bits = view_elem_bits(x->l, b);
       args[b].is_buffer = 1;
       args[b].value = views[b].data + (uint64_t)(views[b].base * bits / 8);
     }

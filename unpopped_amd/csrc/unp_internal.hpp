@@ -75,6 +75,12 @@ struct gather_view_host {
   long long ext[8], tstr[8], istr[8], ostr[8];
   long long outs;
 };
+struct gather_x_view_host {
+  long long rank, axis;
+  long long ext[8], ostr[8];
+  long long istr[8][8];
+  long long outs;
+};
 
 // An Access::RowReduce (crates/unpopped/src/ir.rs:2114-2125): the stages' pre expressions and
 // folds, then the full-width epilogue, as ScalarExpr JSON over Input(k) and Reduced(t) leaves.
@@ -98,6 +104,16 @@ struct ReductionExpr {
   kir::J post;  // ScalarExpr over Reduced(0)
 };
 
+// A recognised gather beyond OpDef::gather (kernel_lift/gather.rs:35-101): n inputs, the index and
+// the gathered data among them (form.data_slot), and an elementwise body over Input(0..n).  plain:
+// the two-input identity gather the row kernels move.
+struct GatherExpr {
+  bool plain = true;
+  int32_t n_inputs = 2;
+  int32_t index_slot = 1;
+  kir::J body;  // ScalarExpr over Input(k)
+};
+
 // A lowered form: what the executor needs to launch it.
 struct Lowered {
   unp_form form{};
@@ -119,6 +135,7 @@ struct Lowered {
   int32_t scan_axis = 0;
   RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only
   ReductionExpr rx;  // UNP_FORM_REDUCTION: the body and post
+  GatherExpr gx;     // UNP_FORM_GATHER: the inputs and body
 };
 
 // Emit the HIP source and interface for `f`; on refusal returns a nonzero unp_status and
@@ -128,6 +145,8 @@ int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail);
 int32_t form_variants(const unp_form& f, std::vector<unp_variant>& out, std::string& detail);
 // A recognised reduction with its body and post (the plain ones go to lower_form).
 int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& out, std::string& detail);
+// A recognised gather with more inputs or a body (the plain ones go to lower_form).
+int32_t lower_gather_x(const unp_form& f, const GatherExpr& gx, Lowered& out, std::string& detail);
 // The same for a recognised Access::RowReduce.
 int32_t lower_row_reduce(const RowReduceSpec& spec, Lowered& out, std::string& detail);
 
@@ -138,6 +157,7 @@ struct Recognized {
   unp_form form{};
   RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only
   ReductionExpr rx;  // UNP_FORM_REDUCTION only
+  GatherExpr gx;     // UNP_FORM_GATHER only
   std::string lift;
   kir::J launch;
   kir::J params;
