@@ -478,14 +478,15 @@ class MallFlush:
                                               self.C.sizeof(self.args), self.C.byref(err)), err)
 
 
-def gemm_lines(u, synth, steps: int, warmup: int) -> None:
+def gemm_lines(u, synth, steps: int, warmup: int, shapes: str = "") -> None:
     """The dequantizing GEMM (tests/support/dequant.rs:104-181) at a weight of LLM size: U4 w
     8192 x 28672 with an I32 zero point and scale per 128 columns, times x of C columns (I8 and I32),
     one JSON line per shape: the median of `steps` launches, each timed alone with HIP events after
     a 512 MiB read with plain loads has evicted the weight from the MALL.  Bytes are w + zero + scale + x + out;
-    operations 2 R K C."""
+    operations 2 R K C.  ``shapes`` ("I8:16,I32:1024") keeps only those (activation, C) pairs."""
     from unpopped_amd import forms as H
 
+    keep = {tuple(s.split(":")) for s in shapes.split(",") if s}
     R, K, G = 8192, 28672, 128
     ng = K // G
     # Streamed between timed launches so that no launch finds the weight in the 256 MB MALL
@@ -498,6 +499,8 @@ def gemm_lines(u, synth, steps: int, warmup: int) -> None:
     for xk, xdt in (("I8", np.int8), ("I32", np.int32)):
         ex = H.executor(kind="dequant_gemm", q_kind="U4", dtype=xk, group=G)
         for C in (16, 32, 64, 128, 256, 1024):
+            if keep and (xk, str(C)) not in keep:
+                continue
             x = (synth.int16_i32(63, K * C) * 13 - 100).astype(xdt)
             dx, do = u.DeviceBuffer.from_array(x), u.DeviceBuffer(R * C * 4)
             for _ in range(warmup):
@@ -556,6 +559,7 @@ def main() -> int:
                     help="only measure this device's streaming read / write / copy rates on 1 GiB")
     ap.add_argument("--gemm", action="store_true",
                     help="only time the dequantizing GEMM at LLM shapes (one JSON line per shape)")
+    ap.add_argument("--gemm-shapes", default="", help='with --gemm: only these "I8:16,I32:1024" (activation:C) pairs')
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -576,7 +580,7 @@ def main() -> int:
         ceilings(u, cus)
         return 0
     if args.gemm:
-        gemm_lines(u, synth, args.steps, args.warmup)
+        gemm_lines(u, synth, args.steps, args.warmup, args.gemm_shapes)
         return 0
     cases = build_cases(u, synth)
     if args.only:
