@@ -533,12 +533,11 @@ def attach_traffic(per, cases) -> None:
     the source revision (FNV-1a of the generated source) that was profiled, and labelled with the
     file it comes from; a kernel changed since its profile gets no figure."""
     tf = ROOT / "profiles" / "traffic.json"
-    if not tf.exists():
-        return
-    known = json.loads(tf.read_text()).get("cases", {})
+    known = json.loads(tf.read_text()).get("cases", {}) if tf.exists() else {}
     for p, c in zip(per, cases):
         t = known.get(p["name"])
         rev = f"{c.exec.kernel.revision_hash():016x}"
+        p["revision"] = rev
         if t and t.get("kernel") == p["entry"] and t.get("revision") == rev:
             p["traffic"] = t["traffic_bytes"]
             p["traffic_source"] = f"profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; revision {rev})"

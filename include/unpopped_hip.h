@@ -45,6 +45,8 @@ enum unp_status {
   UNP_LIFT_DECLINE = 10,          /* LiftDecline (kernel_lift.rs:48-85); detail names it */
   UNP_COMPILE_ERROR = 20,         /* Compiler::compile Err(String)     jit.rs:278 */
   UNP_HIP_ERROR = 30,             /* a HIP runtime call failed; detail has hipGetErrorString */
+  UNP_STALLED = 31,               /* a launch gave up waiting for another block (no reference
+                                     counterpart: unp_hip_exec_check) */
   UNP_INVALID_ARGUMENT = 40,      /* a launch argument does not fit the kernel's interface */
   UNP_PARSE_ERROR = 50            /* kernel JSON text that is not a KernelFn */
 };
@@ -362,6 +364,18 @@ int32_t unp_hip_exec_launch_static(unp_exec* e, const unp_arg* args, size_t narg
  * the launch's kernel time without the queueing gap around it.  NULL, NULL restores plain launches;
  * the events must stay alive while they are set. */
 int32_t unp_hip_exec_set_timing(unp_exec* e, unp_event* start, unp_event* stop);
+/* Bounded waits (no reference counterpart: the reference's CPU launches never wait on another
+ * thread).  A kernel that waits for another block of its launch -- a scan tile for its
+ * predecessors' status, a full or column reduction's folding block for the other blocks' partials,
+ * a staged scan's waves for their tile's look-back -- gives up once one wait has lasted `wait_us`
+ * microseconds of the device's wall clock (default 1 s; 0 gives up at the first unanswered probe),
+ * goes on with the fold's identity in place of the missing value, and counts the give-up in a word
+ * of the executor.  Every block still finishes, so a lost predecessor ends the launch with wrong
+ * outputs instead of hanging the device.  unp_hip_exec_check waits for the device and returns
+ * UNP_STALLED, and clears the count, when any launch of `e` since the last check gave up; else
+ * UNP_OK. */
+int32_t unp_hip_exec_set_wait_limit(unp_exec* e, uint32_t wait_us);
+int32_t unp_hip_exec_check(unp_exec* e, unp_error* err);
 /* The last launch's geometry and chosen entry point (for reports). */
 int32_t unp_hip_exec_last_launch(const unp_exec* e, uint32_t grid[3], uint32_t block[3],
                                  char* entry, size_t entry_len);

@@ -407,6 +407,58 @@ def test_scan_unaligned_takes_the_register_path(hip_device):
     assert np.array_equal(dout.download(np.int32, x.size).reshape(x.shape), oracle.scan_rows(x, "Sum"))
 
 
+WAIT_CASES = {
+    # form, input, launch scalars from the input's shape; one launch spans every CU
+    "scan_i32_staged": (dict(kind="scan", dtype="I32", rank=2, op="Sum"), lambda: rng(41).integers(
+        -50, 50, size=(1, 1 << 24), dtype=np.int32), lambda x: oracle.scan_rows(x, "Sum")),
+    "scan_i32_register": (dict(kind="scan", dtype="I32", rank=2, op="Max"), lambda: rng(42).integers(
+        -1000, 1000, size=(1, (1 << 23) + 1), dtype=np.int32), lambda x: oracle.scan_rows(x, "Max")),
+    "scan_f32_staged": (dict(kind="scan", dtype="F32", rank=2, op="Sum"),
+                        lambda: synth.uniform_pm1_f32(43, 1 << 24).reshape(1, -1), lambda x: oracle.scan_rows(x, "Sum")),
+    "reduce_all": (dict(kind="reduction", dtype="I64", rank=1, op="Sum", reduced_from=0), lambda: rng(44).integers(
+        -1 << 40, 1 << 40, size=1 << 22, dtype=np.int64), lambda x: np.array([oracle.reduce_rows(x.reshape(1, -1), "Sum")[0]])),
+    "reduce_columns": (dict(kind="reduction", dtype="F32", rank=2, op="Max", axes=(0,)), lambda: rng(45).normal(
+        size=(8192, 512)).astype(np.float32), lambda x: x.max(axis=0)),
+}
+
+
+@pytest.mark.parametrize("case", sorted(WAIT_CASES))
+def test_a_wait_that_runs_out_is_reported_not_hung(hip_device, case):
+    """Every wait of a kernel for another block is bounded.  With the bound at 0 a wait gives up at
+    its first unanswered probe, so the launch still ends on the device; a launch whose output then
+    differs from the oracle must have said so (``check`` raises Stalled).  With the default bound
+    restored, the same executor is exact again and reports nothing."""
+    form, make, want_of = WAIT_CASES[case]
+    x = make()
+    want = want_of(x)
+    ex = u.Executor(H._backend.lower_kernel(H.kernel_for(**form)))
+    din = u.DeviceBuffer.from_array(x)
+    dout = u.DeviceBuffer(x.nbytes)
+    outs = want.size
+
+    def run():
+        ex.launch(din, dout, *x.shape)
+        u.synchronize()
+        return dout.download(x.dtype, outs).reshape(want.shape)
+
+    H.say(f"[case] wait bound 0: {case} {x.shape}")
+    ex.set_wait_limit(0)
+    for i in range(3):
+        got = run()
+        try:
+            ex.check()
+            stalled = False
+        except u.UnpError as e:
+            assert e.kind == "Stalled", e
+            stalled = True
+        exact = np.array_equal(got, want)
+        H.say(f"[case] launch {i}: stalled={stalled} exact={exact}")
+        assert stalled or exact
+    ex.set_wait_limit(1_000_000)
+    assert np.array_equal(run(), want)
+    ex.check()
+
+
 def test_scan_repeated_launches_reuse_state(hip_device):
     """The look-back state is reused across launches (epoch tags): results stay exact."""
     H.say("[case] scan repeated launches")

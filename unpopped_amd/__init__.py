@@ -401,6 +401,18 @@ class Executor:
         check(_lib.lib().unp_hip_exec_set_timing(self._h, start._h if start else None, end._h if end else None),
               what="set_timing")
 
+    def set_wait_limit(self, wait_us: int) -> None:
+        """Bound every wait of a kernel for another block of its launch to ``wait_us`` microseconds
+        (default 1 s; 0 gives up at the first unanswered probe): a wait that runs out goes on with the
+        fold's identity and is counted for ``check``."""
+        check(_lib.lib().unp_hip_exec_set_wait_limit(self._h, int(wait_us)), what="set_wait_limit")
+
+    def check(self) -> None:
+        """Wait for the device; raise ``UnpError`` ("Stalled") when a launch since the last check
+        gave up a wait, so its outputs are not valid (the count is then cleared)."""
+        err = _lib.Error()
+        check(_lib.lib().unp_hip_exec_check(self._h, C.byref(err)), err)
+
     def last_launch(self) -> dict:
         g = (C.c_uint32 * 3)()
         b = (C.c_uint32 * 3)()

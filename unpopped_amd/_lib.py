@@ -21,6 +21,7 @@ UNSUPPORTED_KERNEL = 6
 LIFT_DECLINE = 10
 COMPILE_ERROR = 20
 HIP_ERROR = 30
+STALLED = 31
 INVALID_ARGUMENT = 40
 PARSE_ERROR = 50
 
@@ -28,7 +29,7 @@ STATUS_NAMES = {
     OK: "Ok", UNSUPPORTED_DTYPE: "UnsupportedDtype", UNSUPPORTED_SCHEDULE: "UnsupportedSchedule",
     UNSUPPORTED_OP: "UnsupportedOp", UNSUPPORTED_PLAN_SHAPE: "UnsupportedPlanShape",
     INADMISSIBLE_PLAN: "InadmissiblePlan", UNSUPPORTED_KERNEL: "UnsupportedKernel",
-    LIFT_DECLINE: "LiftDecline", COMPILE_ERROR: "CompileError", HIP_ERROR: "HipError",
+    LIFT_DECLINE: "LiftDecline", COMPILE_ERROR: "CompileError", HIP_ERROR: "HipError", STALLED: "Stalled",
     INVALID_ARGUMENT: "InvalidArgument", PARSE_ERROR: "ParseError",
 }
 
@@ -132,6 +133,8 @@ def lib() -> C.CDLL:
         "unp_hip_exec_launch_views": (i32, [P, C.POINTER(View), sz, C.POINTER(C.c_int64), sz, P, E]),
         "unp_hip_exec_launch_static": (i32, [P, C.POINTER(Arg), sz, P, E]),
         "unp_hip_exec_set_timing": (i32, [P, P, P]),
+        "unp_hip_exec_set_wait_limit": (i32, [P, u32]),
+        "unp_hip_exec_check": (i32, [P, E]),
         "unp_hip_exec_last_launch": (i32, [P, C.POINTER(u32), C.POINTER(u32), C.c_char_p, sz]),
         "unp_hip_exec_destroy": (None, [P]),
     }

@@ -273,9 +273,9 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
       e.vec = fast ? V : 1;
       e.symbol = L.name + (fast ? "_mv" : "_ms");
       src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol << "(const " << T << "* in, " << T
-          << "* out, long long A, long long R, long long B, long long S, typename unp::acc<" << T << ", " << f.op0
-          << ">::type* partials, unsigned* counters) {\n  unp::reduce_mid<" << T << ", " << f.op0 << ", " << e.vec
-          << ", 512, 8>(in, out, A, R, B, S, partials, counters);\n}\n";
+          << "* out, long long A, long long R, long long B, long long S, "
+          << "unsigned long long* partials, unsigned* counters, unsigned epoch, unp::waits wt) {\n  unp::reduce_mid<" << T
+          << ", " << f.op0 << ", " << e.vec << ", 512, 8>(in, out, A, R, B, S, partials, counters, epoch, wt);\n}\n";
       L.entries.push_back(e);
     }
   } else if (sched == 'q') {
@@ -308,9 +308,9 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
       e.vec = fast ? V : 1;
       e.symbol = L.name + (fast ? "_v" : "_s");
       src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol << "(const " << T << "* in, " << T
-          << "* out, long long n, typename unp::acc<" << T << ", " << f.op0
-          << ">::type* partials, unsigned* counter) {\n  unp::reduce_all<" << T << ", " << f.op0 << ", " << e.vec
-          << ", 512, " << (fast ? 16 : 8) << ">(in, out, n, partials, counter);\n}\n";
+          << "* out, long long n, unsigned long long* partials, unsigned* counter, unsigned epoch, unp::waits wt) {\n"
+          << "  unp::reduce_all<" << T << ", " << f.op0 << ", " << e.vec << ", 512, " << (fast ? 16 : 8)
+          << ">(in, out, n, partials, counter, epoch, wt);\n}\n";
       L.entries.push_back(e);
     }
   } else {
@@ -385,8 +385,8 @@ static int32_t lower_reduction(const unp_form& f, Lowered& L, std::string& why) 
                          : (L.entries[i].fast ? "reduced extent % vec == 0 and in0 16-byte aligned" : "otherwise"))
       << "\"}";
   j << "],\"workspace\":"
-    << (L.reduce_all   ? "{\"partials\":\"grid * accumulator bytes\",\"counter\":4}"
-        : sched == 'm' ? "{\"partials\":\"strips * chunks * 64 * vec * accumulator bytes\",\"counters\":\"strips * 4\"}"
+    << (L.reduce_all   ? "{\"partials\":\"grid * 8 bytes per 4-byte accumulator word (tagged with the launch epoch)\",\"counter\":4,\"stall\":4,\"host_state\":[\"epoch\"]}"
+        : sched == 'm' ? "{\"partials\":\"strips * chunks * 64 * vec * 8 bytes per 4-byte accumulator word (tagged with the launch epoch)\",\"counters\":\"strips * 4\",\"stall\":4,\"host_state\":[\"epoch\"]}"
                        : "null")
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["
@@ -515,10 +515,10 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     e.symbol = L.name + "_v";
     src << "extern \"C\" __global__ void __launch_bounds__(" << e.threads << ") " << e.symbol << "(const " << T
         << "* in, " << T << "* out, long long rows, long long cols, unsigned long long* status, "
-        << "unsigned* counter, unsigned ticket_base, unsigned epoch) {\n  unp::scan_staged<" << T << ", " << f.op0
+        << "unsigned* counter, unsigned ticket_base, unsigned epoch, unp::waits wt) {\n  unp::scan_staged<" << T << ", " << f.op0
         << ", " << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false") << ", " << e.vec << ", "
         << e.k << ", " << e.wpb << ", " << kScanStatusWords
-        << ">(in, out, rows, cols, status, counter, ticket_base, epoch);\n}\n";
+        << ">(in, out, rows, cols, status, counter, ticket_base, epoch, wt);\n}\n";
     L.entries.push_back(e);
   }
   {
@@ -532,10 +532,10 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     e.symbol = L.name + "_s";
     src << "extern \"C\" __global__ void __launch_bounds__(" << e.threads << ") " << e.symbol << "(const " << T
         << "* in, " << T << "* out, long long rows, long long cols, unsigned long long* status, "
-        << "unsigned* counter, unsigned ticket_base, unsigned epoch) {\n  unp::scan_lookback<" << T << ", " << f.op0
+        << "unsigned* counter, unsigned ticket_base, unsigned epoch, unp::waits wt) {\n  unp::scan_lookback<" << T << ", " << f.op0
         << ", " << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false") << ", 1, " << e.k
         << ", " << e.wpb << ", " << kScanStatusWords
-        << ">(in, out, rows, cols, status, counter, ticket_base, epoch);\n}\n";
+        << ">(in, out, rows, cols, status, counter, ticket_base, epoch, wt);\n}\n";
     L.entries.push_back(e);
   }
   src << scan_strided_entry(f, L);
@@ -560,7 +560,7 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
                                : "otherwise")
       << "\"}";
   j << "],\"workspace\":{\"status\":\"tiles * " << kScanStatusWords * 8
-    << " bytes, zeroed once\",\"counter\":4,\"host_state\":[\"epoch\",\"ticket_base\"]}"
+    << " bytes, zeroed once\",\"counter\":4,\"stall\":4,\"host_state\":[\"epoch\",\"ticket_base\"]}"
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["
     << json_str(kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN)
@@ -1435,10 +1435,10 @@ int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L
       e.symbol = L.name + (fast ? "_xav" : "_xas");
       src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol << "(";
       sig(src);
-      src << ", long long n, double* partials, unsigned* counter) {\n";
+      src << ", long long n, unsigned long long* partials, unsigned* counter, unsigned epoch, unp::waits wt) {\n";
       ins(src);
       src << "  unp::xreduce_all<" << T << ", " << NI << ", " << f.op0 << ", " << ops << ", " << e.vec << ", 512, "
-          << (fast ? 8 : 8) << ">(in, out, n, partials, counter);\n}\n";
+          << (fast ? 8 : 8) << ">(in, out, n, partials, counter, epoch, wt);\n}\n";
       L.entries.push_back(e);
     }
   } else {
@@ -1477,7 +1477,7 @@ int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L
           : L.entries[i].fast         ? "reduced extent % vec == 0 and every input 16-byte aligned"
                                       : "otherwise")
       << "\"}";
-  j << "],\"workspace\":" << (sched == 'a' ? "{\"partials\":\"grid * 8\",\"counter\":4}" : "null")
+  j << "],\"workspace\":" << (sched == 'a' ? "{\"partials\":\"grid * 16 (f64, tagged with the launch epoch)\",\"counter\":4,\"stall\":4,\"host_state\":[\"epoch\"]}" : "null")
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["
     << json_str("the body and the post evaluate in f64 and round once per statement, as the kernel evaluator runs the "

@@ -313,33 +313,10 @@ template <class A, int OP, int THREADS> UNP_DEV A block_reduce(A x, A* s) {
   return r;
 }
 
-// Device-scope (all XCDs) coherent scalar accesses: relaxed agent-scope atomics bypass the
-// non-coherent part of the cache hierarchy on gfx950.
-template <class X> UNP_DEV void store_agent(X* p, X v) {
-  if constexpr (sizeof(X) == 4) {
-    __hip_atomic_store(reinterpret_cast<u32*>(p), __builtin_bit_cast(u32, v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  } else {
-    __hip_atomic_store(reinterpret_cast<u64*>(p), __builtin_bit_cast(u64, v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-template <class X> UNP_DEV X load_agent(const X* p) {
-  if constexpr (sizeof(X) == 4) {
-    return __builtin_bit_cast(X, __hip_atomic_load(reinterpret_cast<const u32*>(p), __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT));
-  } else {
-    return __builtin_bit_cast(X, __hip_atomic_load(reinterpret_cast<const u64*>(p), __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT));
-  }
-}
-
-// Arrive at a device-scope counter after this wave's agent-scope stores (store_agent) are
-// complete: the stores are written through to the device-coherent level, so waiting for
-// them (vmcnt) is all the ordering a reader that loads with load_agent needs.  An acq_rel
-// atomic would also write back and invalidate this XCD's whole L2 (buffer_wbl2 / buffer_inv),
-// which costs more than the reduction when every block of a launch does it.  Returns the
-// counter's previous value.
+// Arrive at a device-scope counter once this wave's stores have completed (vmcnt), so that the
+// block drawing the last arrival usually finds every tagged partial already in place.  This
+// only shortens the reader's wait: the reader checks each partial's tag itself (tagged<A>),
+// and nothing here is needed for its correctness.  Returns the counter's previous value.
 UNP_DEV u32 arrive_after_stores(u32* counter) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): expcnt and lgkmcnt left at their maximum
@@ -354,6 +331,74 @@ UNP_DEV u32 arrive_after_stores(u32* counter) {
 UNP_DEV u32 draw_ticket(u32* counter) {
   return __builtin_amdgcn_atomic_inc32(counter, 0xffffffffu, __ATOMIC_RELAXED, "agent");
 }
+
+// ---------------------------------------------------------------------------------------
+// Bounded waits.  A wave that waits for another block (a scan tile for its predecessors'
+// status, a full reduction's folding block for the other blocks' partials, a staged scan's
+// consumer waves for their tile's look-back) gives up once `ticks` of the device's constant
+// wall clock (wall_clock64) have passed since its wait began, adds one to `*stall`, and goes
+// on with the identity in place of what it waited for.  Every wave still reaches the end of
+// the kernel, and the host reads the stall word to report the launch's outputs invalid instead
+// of the device hanging on a lost predecessor.  With ticks = 0 a wait gives up at its first
+// unanswered probe.
+// ---------------------------------------------------------------------------------------
+struct waits {
+  u32* stall;
+  u32 ticks;
+};
+static_assert(sizeof(waits) == 16, "the host passes a 16-byte waits argument");
+UNP_DEV void note_stall(const waits& wt) {
+  __hip_atomic_fetch_add(wt.stall, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// True once a wait that began at t0 has run out.
+UNP_DEV bool wait_over(u64 t0, const waits& wt) { return wall_clock64() - t0 >= (u64)wt.ticks; }
+
+// A value one block publishes for another, as W 64-bit words [launch epoch: 32 bits | 32 bits of
+// the value].  The reader takes the value only when every word carries this launch's epoch, so
+// the value arrives in the same atomic word as the tag that says it is complete: per-location
+// coherence of the relaxed agent-scope accesses is all the hand-off relies on, and no ordering
+// between different locations is needed (an agent-scope release / acquire pair would write back
+// and invalidate the XCD's whole L2).  The host advances the epoch per launch and clears the
+// words before the epoch wraps, so no reset is needed between launches.
+// Word i of a value lies at p + i * stride: callers lay the words out in planes, so that the
+// lanes of a wave store and load whole contiguous runs.
+template <class A> struct tagged {
+  static_assert(sizeof(A) == 4 || sizeof(A) == 8, "4- or 8-byte values");
+  static constexpr int W = sizeof(A) == 4 ? 1 : 2;
+  static UNP_DEV void put(u64* p, i64 stride, A v, u32 epoch) {
+    const u64 b = to_bits64(v), tag = (u64)epoch << 32;
+    __hip_atomic_store(p, tag | (b & 0xffffffffull), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (W == 2)
+      __hip_atomic_store(p + stride, tag | (b >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  static UNP_DEV bool take(const u64* p, i64 stride, u32 epoch, A& v) {
+    u64 w[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[i] = __hip_atomic_load(p + i * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool ok = (u32)(w[0] >> 32) == epoch;
+    u64 b = w[0] & 0xffffffffull;
+    if constexpr (W == 2) {
+      ok = ok && (u32)(w[1] >> 32) == epoch;
+      b |= w[1] << 32;
+    }
+    v = from_bits64<A>(b);
+    return ok;
+  }
+  // The value at p, waiting for it (bounded); `ident` after a give-up.
+  static UNP_DEV A wait(const u64* p, i64 stride, u32 epoch, A ident, const waits& wt) {
+    A v;
+    if (take(p, stride, epoch, v)) return v;
+    const u64 t0 = wall_clock64();
+    for (;;) {
+      __builtin_amdgcn_s_sleep(1);
+      if (take(p, stride, epoch, v)) return v;
+      if (wait_over(t0, wt)) {
+        note_stall(wt);
+        return ident;
+      }
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------------------
 // Row reduction, one wave per row: waves stride over rows (the outermost kept axis, as
@@ -482,11 +527,12 @@ UNP_DEV void rowreduce(const T* __restrict__ in, T* __restrict__ out0, T* __rest
 // folds a grid-strided slice, publishes its partial, and the block that draws the last
 // ticket folds the partials in block order and stores.  The order depends on
 // (gridDim.x, THREADS, VEC, UNROLL) only, so the result is reproducible run to run.
-// `counter` is zero on entry and is left zero.
+// `counter` is zero on entry and is left zero; the partials are tagged with the launch's `epoch`
+// and the folding block waits for each (bounded by `wt`).
 // ---------------------------------------------------------------------------------------
 template <class T, int OP, int VEC, int THREADS, int UNROLL>
-UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
-                        typename acc<T, OP>::type* __restrict__ partials, u32* __restrict__ counter) {
+UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n, u64* __restrict__ partials,
+                        u32* __restrict__ counter, u32 epoch, waits wt) {
   typedef typename acc<T, OP>::type A;
   typedef fold<A, OP> F;
   constexpr int WAVES = THREADS / 64;
@@ -512,14 +558,15 @@ UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
     for (int e = 0; e < VEC; ++e) a = F::apply(a, (A)v.e[e]);
   }
   a = block_reduce<A, OP, THREADS>(a, s);
+  typedef tagged<A> P;
   if (tid == 0) {
-    store_agent(&partials[blockIdx.x], a);
+    P::put(partials + blockIdx.x, gridDim.x, a, epoch);
     last = (arrive_after_stores(counter) == gridDim.x - 1) ? 1u : 0u;
   }
   __syncthreads();
   if (last == 0u) return;
   A b = F::identity();
-  for (u32 i = tid; i < gridDim.x; i += THREADS) b = F::apply(b, load_agent(&partials[i]));
+  for (u32 i = tid; i < gridDim.x; i += THREADS) b = F::apply(b, P::wait(partials + i, gridDim.x, epoch, F::identity(), wt));
   b = block_reduce<A, OP, THREADS>(b, s);
   if (tid == 0) {
     out[0] = finish<T, OP>(b, n);
@@ -541,14 +588,15 @@ UNP_DEV void reduce_all(const T* __restrict__ in, T* __restrict__ out, i64 n,
 // meet in LDS in wave order; with S > 1 each block publishes its partials and the block that
 // draws the strip's last ticket folds the S partials in chunk order and stores.  The order is
 // fixed by (S, WAVES, U), so the result is reproducible.  counters[strip] is zero on entry and
-// left zero.
+// left zero; the chunk partials are tagged with the launch's `epoch` (tagged<A>).
 // ---------------------------------------------------------------------------------------
 template <class T, int OP, int VEC, int THREADS, int U>
 UNP_DEV void reduce_mid(const T* __restrict__ in, T* __restrict__ out, i64 A, i64 R, i64 B, i64 S,
-                        typename acc<T, OP>::type* __restrict__ partials, u32* __restrict__ counters) {
+                        u64* __restrict__ partials, u32* __restrict__ counters, u32 epoch, waits wt) {
   typedef typename acc<T, OP>::type Ac;
   typedef fold<Ac, OP> F;
   constexpr int WAVES = THREADS / 64;
+  typedef tagged<Ac> P;
   constexpr i64 CW = (i64)64 * VEC;  // columns per strip
   __shared__ Ac sh[WAVES][64 * VEC];
   __shared__ u32 last;
@@ -604,28 +652,38 @@ UNP_DEV void reduce_mid(const T* __restrict__ in, T* __restrict__ out, i64 A, i6
           for (int e = 0; e < VEC; ++e) out[a * B + b0 + e] = finish<T, OP>(acc_[e], R);
         }
       } else {
-        Ac* __restrict__ mine = partials + (strip * S + s) * CW + (i64)lane * VEC;
+        // An item's partials: VEC x W planes of 64 words, word (e, i) of lane l at (e W + i) 64 + l.
+        u64* __restrict__ mine = partials + (strip * S + s) * CW * P::W + lane;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) store_agent(&mine[e], acc_[e]);
+        for (int e = 0; e < VEC; ++e) P::put(mine + e * P::W * 64, 64, acc_[e], epoch);
         if (lane == 0) last = (arrive_after_stores(&counters[strip]) == (u32)(S - 1)) ? 1u : 0u;
       }
     }
     if (S > 1) {
       __syncthreads();
       if (last != 0u && wave == 0) {
-        // Every other item's partials were complete before its arrival; the device-coherent
-        // loads see them, 8 chunks in flight at a time.
+        // The strip's chunk partials, 8 chunks in flight at a time, each taken once its tag
+        // shows this launch's epoch.
         Ac r[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) r[e] = F::identity();
-        const Ac* __restrict__ col = partials + strip * S * CW + (i64)lane * VEC;
+        const u64* __restrict__ col = partials + strip * S * CW * P::W + lane;
+        const i64 ITEM = CW * P::W;  // words from one chunk's partials to the next
         i64 k = 0;
         for (; k + 8 <= S; k += 8) {
           Ac v[8][VEC];
+          bool ok = true;
 #pragma unroll
           for (int t = 0; t < 8; ++t)
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) v[t][e] = load_agent(&col[(k + t) * CW + e]);
+            for (int e = 0; e < VEC; ++e) ok = P::take(col + (k + t) * ITEM + e * P::W * 64, 64, epoch, v[t][e]) && ok;
+          if (!ok) {  // a partial not yet visible: wait for each in turn
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+              for (int e = 0; e < VEC; ++e)
+                v[t][e] = P::wait(col + (k + t) * ITEM + e * P::W * 64, 64, epoch, F::identity(), wt);
+          }
 #pragma unroll
           for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -633,7 +691,8 @@ UNP_DEV void reduce_mid(const T* __restrict__ in, T* __restrict__ out, i64 A, i6
         }
         for (; k < S; ++k)
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) r[e] = F::apply(r[e], load_agent(&col[k * CW + e]));
+          for (int e = 0; e < VEC; ++e)
+            r[e] = F::apply(r[e], P::wait(col + k * ITEM + e * P::W * 64, 64, epoch, F::identity(), wt));
         if (live) {
 #pragma unroll
           for (int e = 0; e < VEC; ++e) out[a * B + b0 + e] = finish<T, OP>(r[e], R);
@@ -833,8 +892,8 @@ UNP_DEV void xreduce_rows(const T* const* __restrict__ in, T* __restrict__ out, 
 // No kept axis: blocks fold grid-strided slices, the last block to arrive folds the partials
 // in block order (the full reduction's protocol; `counter` zero on entry, left zero).
 template <class T, int NI, int OP, class OPS, int VEC, int THREADS, int UNROLL>
-UNP_DEV void xreduce_all(const T* const* __restrict__ in, T* __restrict__ out, i64 n, double* __restrict__ partials,
-                         u32* __restrict__ counter) {
+UNP_DEV void xreduce_all(const T* const* __restrict__ in, T* __restrict__ out, i64 n, u64* __restrict__ partials,
+                         u32* __restrict__ counter, u32 epoch, waits wt) {
   typedef fold<double, OP> F;
   constexpr int WAVES = THREADS / 64;
   __shared__ double sh[WAVES];
@@ -868,14 +927,16 @@ UNP_DEV void xreduce_all(const T* const* __restrict__ in, T* __restrict__ out, i
     take(v);
   }
   a = block_reduce<double, OP, THREADS>(a, sh);
+  typedef tagged<double> P;
   if (tid == 0) {
-    store_agent(&partials[blockIdx.x], a);
+    P::put(partials + blockIdx.x, gridDim.x, a, epoch);
     last = (arrive_after_stores(counter) == gridDim.x - 1) ? 1u : 0u;
   }
   __syncthreads();
   if (last == 0u) return;
   double b = F::identity();
-  for (u32 i = tid; i < gridDim.x; i += THREADS) b = F::apply(b, load_agent(&partials[i]));
+  for (u32 i = tid; i < gridDim.x; i += THREADS)
+    b = F::apply(b, P::wait(partials + i, gridDim.x, epoch, F::identity(), wt));
   b = block_reduce<double, OP, THREADS>(b, sh);
   if (tid == 0) {
     out[0] = xfinish<T, OP, OPS>(b, n);
@@ -1078,8 +1139,10 @@ template <class A, int SP = 0> struct tile_status {
 // The fold of every earlier tile of this row (j = tile's index in its row, j >= 1).
 // Lane l inspects the tiles l + 1, l + 65, ... back, P windows of 64 per round trip (the
 // probes of all P are in flight together); the walk stops at the first inclusive prefix.
+// A lane whose tile stays unpublished past the wait bound takes it as an inclusive identity,
+// which ends the walk (the stall is counted; the result is then not the prefix).
 template <class A, int OP, int P = 1, int SP = 0>
-UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch) {
+UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch, const waits& wt) {
   typedef fold<A, OP> F;
   typedef tile_status<A, SP> S;
   const A I = F::identity();
@@ -1106,9 +1169,17 @@ UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch) {
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const i64 pj = near - 64 * p;
-      while (state[p] == 0) {
-        __builtin_amdgcn_s_sleep(1);
-        state[p] = S::probe(st, tile - (u64)(j - pj), epoch, v[p]);
+      if (state[p] == 0) {
+        const u64 t0 = wall_clock64();
+        do {
+          __builtin_amdgcn_s_sleep(1);
+          state[p] = S::probe(st, tile - (u64)(j - pj), epoch, v[p]);
+          if (state[p] == 0 && wait_over(t0, wt)) {
+            note_stall(wt);
+            v[p] = I;
+            state[p] = 2;
+          }
+        } while (state[p] == 0);
       }
       const u64 incl = __ballot(state[p] == 2);
       const int f = incl ? __builtin_ctzll(incl) : 63;
@@ -1127,7 +1198,7 @@ UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch) {
 template <class T, int OP, bool EXCL, bool REV, int VEC, int K, int WPB, int SP>
 UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
                            u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base,
-                           u32 epoch) {
+                           u32 epoch, waits wt) {
   typedef typename acc<T, OP>::type A;
   typedef fold<A, OP> F;
   typedef tile_status<A, SP> S;
@@ -1205,7 +1276,7 @@ UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 ro
         if (lane == 0) S::publish(st, g, 1, agg, epoch);
       } else {
         if (lane == 0) S::publish(st, g, 0, agg, epoch);
-        gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch);
+        gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch, wt);
         if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
       }
       if (lane == 0) {
@@ -1301,7 +1372,7 @@ UNP_DEV void lds_barrier() {
 template <class T, int OP, bool EXCL, bool REV, int VEC, int K, int NC, int SP>
 UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
                          u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base,
-                         u32 epoch) {
+                         u32 epoch, waits wt) {
   typedef typename acc<T, OP>::type A;
   typedef fold<A, OP> F;
   typedef tile_status<A, SP> S;
@@ -1433,7 +1504,7 @@ UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows
         A agg = wagg[r & 1][0];
 #pragma unroll
         for (int w = 1; w < NC; ++w) agg = F::apply(agg, wagg[r & 1][w]);
-        gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch);
+        gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch, wt);
         if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
       }
       if (lane == 0) {
@@ -1442,8 +1513,17 @@ UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows
         __hip_atomic_store(&ready, (u32)r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
     } else {
-      while (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (u32)r + 1)
-        __builtin_amdgcn_s_sleep(1);
+      // Wave 0's look-back is itself bounded by the wait limit: this wait allows twice that.
+      if (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (u32)r + 1) {
+        const u64 t0 = wall_clock64();
+        while (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (u32)r + 1) {
+          __builtin_amdgcn_s_sleep(1);
+          if (wall_clock64() - t0 >= 2 * (u64)wt.ticks) {
+            if (lane == 0) note_stall(wt);
+            break;
+          }
+        }
+      }
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
       gex = gbase;
     }

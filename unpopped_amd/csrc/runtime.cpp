@@ -56,6 +56,23 @@ bool valid_target(const char* t) {
   return colons == 1 && at > 0 && at + 1 < n;
 }
 
+// How long one wait of a kernel for another block may last before the kernel gives up on it
+// (unp_hip_exec_set_wait_limit): a wait that the hardware serves takes microseconds.
+constexpr uint32_t kDefaultWaitUs = 1000000;
+
+uint32_t wait_ticks_for(int khz, uint32_t us) {
+  const unsigned long long t = (unsigned long long)khz * us / 1000ull;
+  return t > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)t;
+}
+
+// The device's `waits` kernel argument: the stall word and the bound in wall-clock ticks.
+struct waits_host {
+  uint32_t* stall;
+  uint32_t ticks;
+  uint32_t pad;
+};
+static_assert(sizeof(waits_host) == 16, "waits_host mirrors the device's waits");
+
 }  // namespace
 
 struct unp_module {
@@ -81,6 +98,11 @@ struct unp_exec {
   size_t n_counters = 0;
   uint32_t epoch = 0;
   uint32_t ticket_base = 0;
+  // Bounded waits: the word a kernel that gave up waiting counts into, read and cleared by
+  // unp_hip_exec_check, and the bound in ticks of the device's wall clock (wall_clock_khz kHz).
+  uint32_t* stall = nullptr;
+  uint32_t wait_ticks = 0;
+  int wall_clock_khz = 0;
   // Set for the duration of a no-allocation launch: every workspace is carved from this region
   // (cleared first) instead of the executor's own allocations.
   const unp::Scratch* fixed = nullptr;
@@ -348,25 +370,38 @@ int32_t unp_hip_exec_create(const unp_generated* g, unp_exec** out, unp_error* e
     return hip_fail(err, "hipGetDeviceProperties", e);
   }
   x->cu_count = p.multiProcessorCount;
+  e = hipDeviceGetAttribute(&x->wall_clock_khz, hipDeviceAttributeWallClockRate, x->device);
+  if (e != hipSuccess || x->wall_clock_khz <= 0) {
+    delete x;
+    return hip_fail(err, "hipDeviceGetAttribute(wall clock rate)", e != hipSuccess ? e : hipErrorInvalidValue);
+  }
+  x->wait_ticks = wait_ticks_for(x->wall_clock_khz, kDefaultWaitUs);
+  e = hipMalloc((void**)&x->stall, sizeof(uint32_t));
+  if (e == hipSuccess) e = hipMemset(x->stall, 0, sizeof(uint32_t));
+  if (e != hipSuccess) {
+    if (x->stall) hipFree(x->stall);
+    delete x;
+    return hip_fail(err, "hipMalloc(stall word)", e);
+  }
   std::vector<uint8_t> code;
   std::string log;
   const int32_t rc = unp::compile_source(x->l.source, x->l.name, 0, code, log);
   if (rc != UNP_OK) {
-    delete x;
+    unp_hip_exec_destroy(x);
     set_error(err, rc, log);
     return rc;
   }
   e = hipModuleLoadData(&x->mod, code.data());
   if (e != hipSuccess) {
-    delete x;
+    x->mod = nullptr;
+    unp_hip_exec_destroy(x);
     return hip_fail(err, "hipModuleLoadData", e);
   }
   for (const auto& en : x->l.entries) {
     hipFunction_t f = nullptr;
     e = hipModuleGetFunction(&f, x->mod, en.symbol.c_str());
     if (e != hipSuccess) {
-      hipModuleUnload(x->mod);
-      delete x;
+      unp_hip_exec_destroy(x);
       return hip_fail(err, ("hipModuleGetFunction " + en.symbol).c_str(), e);
     }
     x->fns.push_back(f);
@@ -381,8 +416,38 @@ void unp_hip_exec_destroy(unp_exec* x) {
   if (x->ws) hipFree(x->ws);
   if (x->counter) hipFree(x->counter);
   if (x->counters) hipFree(x->counters);
+  if (x->stall) hipFree(x->stall);
   if (x->mod) hipModuleUnload(x->mod);
   delete x;
+}
+
+int32_t unp_hip_exec_set_wait_limit(unp_exec* x, uint32_t wait_us) {
+  if (!x) return UNP_INVALID_ARGUMENT;
+  x->wait_ticks = wait_ticks_for(x->wall_clock_khz, wait_us);
+  return UNP_OK;
+}
+
+int32_t unp_hip_exec_check(unp_exec* x, unp_error* err) {
+  if (!x) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null executor");
+    return UNP_INVALID_ARGUMENT;
+  }
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(err, "hipDeviceSynchronize", e);
+  uint32_t n = 0;
+  e = hipMemcpy(&n, x->stall, sizeof n, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(err, "hipMemcpy(stall word)", e);
+  if (n == 0) {
+    set_error(err, UNP_OK, "");
+    return UNP_OK;
+  }
+  e = hipMemset(x->stall, 0, sizeof n);
+  if (e != hipSuccess) return hip_fail(err, "hipMemset(stall word)", e);
+  set_error(err, UNP_STALLED,
+            std::to_string(n) + " wait(s) in launches of `" + x->l.name + "` gave up after " +
+                std::to_string((unsigned long long)x->wait_ticks * 1000ull / (unsigned long long)x->wall_clock_khz) +
+                " us without the block they waited for; those launches' outputs are not valid");
+  return UNP_STALLED;
 }
 
 int32_t unp_hip_exec_set_timing(unp_exec* x, unp_event* start, unp_event* stop) {
@@ -526,6 +591,26 @@ int32_t workspace(unp_exec* x, size_t bytes, bool need_counter, size_t n_counter
   w.counters = x->counters;
   return UNP_OK;
 }
+
+// The epoch of a launch whose kernels tag their hand-off words (scan tile status, reduction
+// partials): 1 in a no-allocation launch, whose scratch was just cleared; else the executor's
+// next, after clearing its words when the 31-bit epoch would wrap (the scan's status words keep
+// 31 bits of it), so that no word is ever taken for one an earlier launch wrote.
+int32_t next_epoch(unp_exec* x, hipStream_t s, uint32_t& ep, unp_error* err) {
+  if (x->fixed) {
+    ep = 1;
+    return UNP_OK;
+  }
+  if (x->epoch == 0x7fffffffu) {
+    const hipError_t e = hipMemsetAsync(x->ws, 0, x->ws_bytes, s);
+    if (e != hipSuccess) return hip_fail(err, "hipMemsetAsync(tagged words)", e);
+    x->epoch = 0;
+  }
+  ep = ++x->epoch;  // the words start zeroed, so epoch 1 is never seen before the first launch
+  return UNP_OK;
+}
+
+waits_host waits_of(const unp_exec* x) { return waits_host{x->stall, x->wait_ticks, 0}; }
 
 // The kept and the reduced axes of a row-major input with their element strides, outermost
 // first, adjacent axes of a kind merged (a merged run's stride is its innermost axis's).
@@ -687,13 +772,18 @@ int32_t run_xreduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, u
   if (sched == 'a') {
     const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
     Ws w;
-    if ((rc = workspace(x, (size_t)grid * 8, true, 0, s, w, err)) != UNP_OK) return rc;
+    uint32_t ep = 0;
+    if ((rc = workspace(x, (size_t)grid * 16, true, 0, s, w, err)) != UNP_OK) return rc;
+    if ((rc = next_epoch(x, s, ep, err)) != UNP_OK) return rc;
     long long nn = count;
     void* ws = w.ws;
     void* cnt = w.counter;
+    waits_host wt = waits_of(x);
     params.push_back(&nn);
     params.push_back(&ws);
     params.push_back(&cnt);
+    params.push_back(&ep);
+    params.push_back(&wt);
     return launch(x, aligned ? 0 : 1, grid, params.data(), s, err);
   }
   unp::axes_desc_host d{};
@@ -740,19 +830,24 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
       long long S = (grid + strips - 1) / strips;
       S = std::min(S, std::max(1LL, r / 16));
       S = std::max(1LL, std::min(S, 1024LL));
+      // A partial is one 8-byte tagged word per 4 bytes of accumulator.
       const size_t acc_bytes = (unp::kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN))
                                    ? 8
                                    : unp::kind_bytes(f.dtype);
+      const size_t word_bytes = acc_bytes == 8 ? 16 : 8;
       void* ws = nullptr;
       void* cnt = nullptr;
+      uint32_t ep = 0;
       if (S > 1) {
         Ws w;
-        if ((rc = workspace(x, (size_t)(strips * S * cw) * acc_bytes, false, (size_t)strips, s, w, err)) != UNP_OK)
+        if ((rc = workspace(x, (size_t)(strips * S * cw) * word_bytes, false, (size_t)strips, s, w, err)) != UNP_OK)
           return rc;
+        if ((rc = next_epoch(x, s, ep, err)) != UNP_OK) return rc;
         ws = w.ws;
         cnt = w.counters;
       }
-      void* params[] = {&in, &out, &a, &r, &b, &S, &ws, &cnt};
+      waits_host wt = waits_of(x);
+      void* params[] = {&in, &out, &a, &r, &b, &S, &ws, &cnt, &ep, &wt};
       return launch(x, entry, (uint32_t)grid, params, s, err);
     }
     const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
@@ -792,13 +887,16 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
   const size_t entry = pick(x, cols % vec == 0 && aligned16(in), !x->l.reduce_all && cols > unp::kWideRow);
   const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
   if (x->l.reduce_all) {
-    const size_t acc_bytes = 8;
+    // Up to two 8-byte tagged words per block partial.
     Ws w;
-    if ((rc = workspace(x, grid * acc_bytes, true, 0, s, w, err)) != UNP_OK) return rc;
+    uint32_t ep = 0;
+    if ((rc = workspace(x, (size_t)grid * 16, true, 0, s, w, err)) != UNP_OK) return rc;
+    if ((rc = next_epoch(x, s, ep, err)) != UNP_OK) return rc;
     long long nn = cols;
     void* ws = w.ws;
     void* cnt = w.counter;
-    void* params[] = {&in, &o0, &nn, &ws, &cnt};
+    waits_host wt = waits_of(x);
+    void* params[] = {&in, &o0, &nn, &ws, &cnt, &ep, &wt};
     return launch(x, entry, grid, params, s, err);
   }
   long long r = rows, c = cols;
@@ -840,26 +938,21 @@ int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_err
   }
   Ws w;
   if ((rc = workspace(x, (size_t)tiles * unp::kScanStatusWords * 8, true, 0, s, w, err)) != UNP_OK) return rc;
+  waits_host wt = waits_of(x);
+  uint32_t ep = 0;
+  if ((rc = next_epoch(x, s, ep, err)) != UNP_OK) return rc;
   if (x->fixed) {
     // The scratch was just cleared: epoch 1 and tickets from 0, and no state kept for the next call.
-    uint32_t tb = 0, ep = 1;
+    uint32_t tb = 0;
     void* st = w.ws;
     void* cnt = w.counter;
-    void* params[] = {&in, &out, &rows, &cols, &st, &cnt, &tb, &ep};
+    void* params[] = {&in, &out, &rows, &cols, &st, &cnt, &tb, &ep, &wt};
     return launch(x, entry, grid, params, s, err);
   }
-  if (x->epoch == 0x7fffffffu) {
-    // The status words hold a 31-bit epoch: after 2^31 - 1 launches the tags would repeat, so
-    // clear the words and restart at epoch 1.
-    const hipError_t e = hipMemsetAsync(x->ws, 0, x->ws_bytes, s);
-    if (e != hipSuccess) return hip_fail(err, "hipMemsetAsync(status)", e);
-    x->epoch = 0;
-  }
-  x->epoch += 1;  // the words start zeroed, so epoch 1 is never seen before the first launch
-  uint32_t tb = x->ticket_base, ep = x->epoch;
+  uint32_t tb = x->ticket_base;
   void* st = w.ws;
   void* cnt = w.counter;
-  void* params[] = {&in, &out, &rows, &cols, &st, &cnt, &tb, &ep};
+  void* params[] = {&in, &out, &rows, &cols, &st, &cnt, &tb, &ep, &wt};
   rc = launch(x, entry, grid, params, s, err);
   // One ticket per tile, plus the one failing draw that ends each block.
   if (rc == UNP_OK) x->ticket_base = (uint32_t)(x->ticket_base + (uint32_t)(tiles + grid));

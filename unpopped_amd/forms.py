@@ -94,7 +94,7 @@ def reduce_axes(x: np.ndarray, axes: tuple, op: str, keepdim: bool = False) -> n
     din = u.DeviceBuffer.from_array(x)
     dout = u.DeviceBuffer(max(outs * x.itemsize, 1))
     ex.launch(din, dout, *x.shape)
-    u.synchronize()
+    ex.check()
     got = dout.download(x.dtype, outs)
     shape = tuple(1 if d in axes else n for d, n in enumerate(x.shape)) if keepdim else kept
     return got.reshape(shape)
@@ -127,7 +127,7 @@ def reduce_expr(inputs, axes: tuple, op: str, body, post=None, keepdim: bool = F
     dins = [u.DeviceBuffer.from_array(a) for a in xs]
     dout = u.DeviceBuffer(max(outs * x0.itemsize, 1))
     ex.launch(*dins, dout, *x0.shape)
-    u.synchronize()
+    ex.check()
     got = dout.download(x0.dtype, outs)
     return got.reshape(tuple(1 if d in axes else n for d, n in enumerate(x0.shape)) if keepdim else kept)
 
@@ -138,7 +138,7 @@ def reduce_all(x: np.ndarray, op: str):
     din = u.DeviceBuffer.from_array(x)
     out = u.DeviceBuffer(16)
     ex.launch(din, out, x.size)
-    u.synchronize()
+    ex.check()
     return out.download(x.dtype, 1)[0]
 
 
@@ -150,7 +150,7 @@ def scan_rows(x: np.ndarray, op: str, exclusive=False, reverse=False) -> np.ndar
     din = u.DeviceBuffer.from_array(x2)
     dout = u.DeviceBuffer(max(x2.nbytes, 1))
     ex.launch(din, dout, rows, cols)
-    u.synchronize()
+    ex.check()
     return dout.download(x.dtype, rows * cols).reshape(x.shape)
 
 
@@ -161,7 +161,7 @@ def scan_axis(x: np.ndarray, axis: int, op: str, exclusive=False, reverse=False)
     din = u.DeviceBuffer.from_array(np.ascontiguousarray(x))
     dout = u.DeviceBuffer(max(x.nbytes, 1))
     ex.launch(din, dout, *x.shape)
-    u.synchronize()
+    ex.check()
     return dout.download(x.dtype, x.size).reshape(x.shape)
 
 
