@@ -212,6 +212,13 @@ int32_t unp_lift_reduction_x(const char* name, int32_t dtype, int32_t rank, int3
  * :54-102) of OpDef::scan_simple (ir.rs:3422-3441): identity pre-map, no post. */
 int32_t unp_lift_scan(const char* name, int32_t dtype, int32_t rank, int32_t op, int32_t axis, int32_t exclusive,
                       int32_t reverse, uint32_t block, uint32_t grid, char** json, unp_error* err);
+/* The same lifts of an Access::Scan with n_inputs inputs, a pre-map over Input(0..n) and a fused
+ * post over Reduced(0) (the prefix rounded once) and Input(0..n) (the elements at the position)
+ * (kernel_lift.rs:530-602, :658-690; scan_launched.rs:140-160), both as ScalarExpr JSON; post_json
+ * NULL (or `{"Reduced":0}`) is the identity post. */
+int32_t unp_lift_scan_x(const char* name, int32_t dtype, int32_t rank, int32_t op, int32_t axis, int32_t exclusive,
+                        int32_t reverse, int32_t n_inputs, const char* pre_json, const char* post_json,
+                        uint32_t block, uint32_t grid, char** json, unp_error* err);
 /* lift_gather_opdef (kernel_lift/gather.rs:35-55) / lift_gather_opdef_launched (kernel_lift.rs
  * :183-191) of OpDef::gather(name, [dtype, index_dtype], axis, oob, index_dtype) (ir.rs:3838-3855);
  * OpDef::embedding is axis 0 with ZeroFill (ir.rs:3884-3886). */
@@ -343,7 +350,7 @@ typedef struct unp_view {
  * tests/kernel_parallel_gather_agrees.rs:80-84) launch the pointer kernels at data + base.  Any
  * other view -- transposed, strided, negative strides, a full-shape gather index -- is read and
  * written through its strides by the reduction (plain body), fused row fold, scan and gather
- * forms (their "strided" interface entries); the row-reduce, pre-map reduction and dequant forms
+ * forms (their "strided" interface entries); the row-reduce, pre-map reduction, pre-map scan and dequant forms
  * read dense storage only and refuse it with UNP_INVALID_ARGUMENT (backend.rs:703-707).  The
  * storage behind a view is the caller's: every element the view names must lie inside it. */
 int32_t unp_hip_exec_launch_views(unp_exec* e, const unp_view* views, size_t nviews, const int64_t* scalars,

@@ -61,6 +61,7 @@ def lib() -> C.CDLL:
             "orc_sum_launched_order": (d, [P, i64, i64, i32]),
             "orc_rx_eval": (d, [P, C.c_int32, P, P, i32]),
             "orc_row_reduce": (None, [P, C.c_int32, i64, i64, i32, C.c_int32, P, P, P, P, C.c_int32, P]),
+            "orc_scan_x": (None, [P, C.c_int32, i64, i64, i64, i32, i32, i32, i32, P, C.c_int32, P, C.c_int32, P]),
             "orc_sum_bound": (d, [P, i64, i32, i32, d]),
             "orc_neumaier": (d, [P, i64]),
             "orc_scan_rows_f32": (None, [P, i64, i64, i32, i32, i32, P]),
@@ -356,4 +357,24 @@ def row_reduce(inputs, stages, epilogue) -> np.ndarray:
     ins = (C.c_void_p * len(xs))(*[_p(a) for a in xs])
     lib().orc_row_reduce(ins, len(xs), rows, cols, int(dt == np.float64), len(stages), ops, pre_ptrs, pre_lens, epi,
                          epi_n, _p(out))
+    return out
+
+
+def scan_expr(inputs, axis: int, op: str, pre, post=None, exclusive: bool = False, reverse: bool = False) -> np.ndarray:
+    """The serial lifted scan of ``inputs`` (one shape, float32 or float64) along ``axis``: the
+    pre-map evaluated in f64 and rounded once per position, the prefix rounded once, and the post
+    (``None``: the identity) over that prefix and the position's inputs, rounded once at the store."""
+    xs = [np.ascontiguousarray(a) for a in inputs]
+    dt = xs[0].dtype
+    assert dt in (np.float32, np.float64) and all(a.dtype == dt and a.shape == xs[0].shape for a in xs)
+    assert 1 <= len(xs) <= 16
+    shape = xs[0].shape
+    a_ext = int(np.prod(shape[:axis], dtype=np.int64))
+    b_ext = int(np.prod(shape[axis + 1:], dtype=np.int64))
+    out = np.empty(shape, dt)
+    pre_arr, pre_n = _rx_array(pre)
+    post_arr, post_n = _rx_array(post) if post is not None else (None, 0)
+    ins = (C.c_void_p * len(xs))(*[_p(a) for a in xs])
+    lib().orc_scan_x(ins, len(xs), a_ext, shape[axis], b_ext, int(dt == np.float64), OPS[op], int(exclusive),
+                     int(reverse), pre_arr, pre_n, post_arr, post_n, _p(out))
     return out

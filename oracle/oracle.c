@@ -555,3 +555,48 @@ void orc_row_reduce(const void* const* ins, int32_t n_inputs, int64_t rows, int6
 #undef ORC_LOAD
 #undef ORC_ROUND
 }
+
+/* ======================================================================================
+ * Scan with a pre-map and a fused post: lift_scan_opdef (kernel_lift.rs:504-519) with
+ * scan_loads (:530-545, `val = up(pre)`), scan_pass (:548-576), scan_write (:578-602, the prefix
+ * rounded once into `red`, the post over it and the loaded elements) and scan_stored (:604-619).
+ * ==================================================================================== */
+
+void orc_scan_x(const void* const* ins, int32_t n_inputs, int64_t a_ext, int64_t s_ext, int64_t b_ext, int f64, int op,
+                int exclusive, int reverse, const orc_rx* pre, int32_t pre_len, const orc_rx* post, int32_t post_len,
+                void* out) {
+  double x[16], red[1] = {0.0};
+  const int f32 = !f64;
+#define ORC_LOAD(k, i) (f64 ? ((const double*)ins[k])[i] : (double)((const float*)ins[k])[i])
+#define ORC_ROUND(v) (f64 ? (v) : (double)(float)(v))
+#define ORC_STORE(i, v) (f64 ? (void)(((double*)out)[i] = (v)) : (void)(((float*)out)[i] = (float)(v)))
+  for (int64_t a = 0; a < a_ext; ++a)
+    for (int64_t b = 0; b < b_ext; ++b) {
+      double acc = scan_identity_f64(op);
+      int have = 0;
+      int64_t count = 0;
+      for (int64_t s = 0; s < s_ext; ++s) {
+        const int64_t i = reverse ? s_ext - 1 - s : s;
+        const int64_t off = (a * s_ext + i) * b_ext + b;
+        for (int32_t k = 0; k < n_inputs; ++k) x[k] = ORC_LOAD(k, off);
+        const double v = ORC_ROUND(orc_rx_eval(pre, pre_len, x, red, f32));
+        for (int pass = 0; pass < 2; ++pass) {
+          if (pass == (exclusive ? 1 : 0)) {
+            acc = fold_f64(op, acc, v, &have);
+            ++count;
+            continue;
+          }
+          const double r = ORC_ROUND(op == ORC_MEAN ? acc / (double)count : acc);
+          if (post_len > 0) {
+            red[0] = r;
+            ORC_STORE(off, orc_rx_eval(post, post_len, x, red, f32));
+          } else {
+            ORC_STORE(off, r);
+          }
+        }
+      }
+    }
+#undef ORC_LOAD
+#undef ORC_ROUND
+#undef ORC_STORE
+}

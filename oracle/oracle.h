@@ -94,5 +94,14 @@ double orc_rx_eval(const orc_rx* prog, int32_t len, const double* x, const doubl
 void orc_row_reduce(const void* const* ins, int32_t n_inputs, int64_t rows, int64_t cols, int f64, int32_t n_stages,
                     const int32_t* ops, const orc_rx* const* pres, const int32_t* pre_lens, const orc_rx* epi,
                     int32_t epi_len, void* out);
+/* The lifted serial scan with a pre-map and a fused post (lift_scan_opdef, kernel_lift.rs:504-619,
+ * as the kernel evaluator runs it): the inputs (n_inputs arrays of T, one shape) seen as A x S x B
+ * around the scanned axis; at each position the pre is evaluated in f64 over the position's inputs
+ * and rounded once to T, the fold takes it in f64 (fold_f64), the prefix is rounded once to T (a
+ * running Mean divided by the count folded so far), and a post (post_len > 0) is evaluated in f64
+ * over that prefix (Reduced(0)) and the position's inputs, rounded once at the store. */
+void orc_scan_x(const void* const* ins, int32_t n_inputs, int64_t a_ext, int64_t s_ext, int64_t b_ext, int f64, int op,
+                int exclusive, int reverse, const orc_rx* pre, int32_t pre_len, const orc_rx* post, int32_t post_len,
+                void* out);
 
 #endif

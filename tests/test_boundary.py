@@ -515,6 +515,10 @@ def _renumber_cases():
                               body=X.input(2) * X.input(1) + 0.5, launch=(64, 4)),
         lambda: u.lift_gather("gx", "I64", 3, "U32", axis=1, oob="Skip", n_inputs=3, data=0, index=2,
                               body=X.input(0)),
+        lambda: u.lift_scan("sx", "F32", 2, "Sum", n_inputs=2, pre=x0 * x1, post=r0 - x0, launch=(256, 64)),
+        lambda: u.lift_scan("sx", "F64", 3, "Mean", axis=0, exclusive=True, reverse=True, n_inputs=2,
+                            pre=x0 + x1, post=r0.sqrt()),
+        lambda: u.lift_scan("sx", "F32", 1, "Max", n_inputs=1, pre=x0 * x0),
     ]
     return out
 
@@ -686,6 +690,57 @@ def test_serial_scan_skeleton_follows_kernel_lift():
     f = exc["body"][0]["For"]["body"][2]["For"]
     i32 = lambda v: {"ConstInt": [v, "I32"]}  # noqa: E731
     assert f["start"] == {"Sub": [{"Local": 0}, i32(1)]} and f["end"] == i32(-1) and f["step"] == i32(-1)
+
+
+def test_scan_with_a_pre_and_a_post_follows_kernel_lift():
+    """lift_scan_opdef with a pre-map and a fused post: scan_loads (kernel_lift.rs:530-545) loads every
+    input, then `val = up(pre)` with Input(k) bound to loaded local 2r + k; scan_write (:578-602) lets
+    `red` (local 2r + n + 3) hold the prefix rounded once and stores the post with Reduced(0) bound to
+    `red` and Input(k) to the loaded locals; `red` is declared after the serial layout (:514-517).  The
+    launched lift's phase 1 (fold_only, scan_launched.rs:223-235) and phase 3 take the same loads and
+    pre, and only phase 3 writes."""
+    from unpopped_amd import expr as X
+
+    x0, x1, r0 = X.input(0), X.input(1), X.reduced(0)
+    k = u.lift_scan("s", "F32", 2, "Sum", n_inputs=2, pre=x0 * x1, post=r0 - x0)
+    params, locals_ = _sig(k)
+    assert params == [("in0", "Buffer", 2), ("in1", "Buffer", 2), ("out", "Buffer", 2), ("n0", "Scalar", 0),
+                      ("n1", "Scalar", 1)]
+    assert locals_ == ["I32"] * 4 + ["F32", "F32", "F64", "I32", "F64", "F32"]
+    assert skeleton(k["body"]) == [
+        ("For", 2, [("Let", 6), ("Let", 7),
+                    ("For", 3, [("Load", 4, ("buf", 0)), ("Load", 5, ("buf", 1)), ("Let", 8), ("Assign", 6),
+                                ("Let", 9), ("Store", ("buf", 2))])])]
+    inner = k["body"][0]["For"]["body"][2]["For"]["body"]
+    assert inner[2]["Let"]["init"] == {"Cast": [{"Mul": [{"Local": 4}, {"Local": 5}]},
+                                               {"to": "F64", "round": "NearestEven", "sat": "Wrap"}]}
+    assert inner[4]["Let"]["init"]["Cast"][0] == {"Local": 6}  # red: the F64 prefix cast down once
+    assert inner[5]["Store"]["value"] == {"Sub": [{"Local": 9}, {"Local": 4}]}
+    # exclusive: the write (Let red, Store) before the fold
+    e = u.lift_scan("s", "F64", 1, "Max", exclusive=True, n_inputs=2, pre=x0 - x1, post=r0 * 2.0)
+    body = skeleton(e["body"])
+    assert body[:2] == [("Let", 4), ("Let", 5)]
+    loop = body[2][2]
+    assert loop[:4] == [("Load", 2, ("buf", 0)), ("Load", 3, ("buf", 1)), ("Let", 6), ("Let", 7)]
+    assert loop[4] == ("Store", ("buf", 2))
+    # launched: phase 1 and phase 3 both load both inputs and take the same pre
+    la = u.lift_scan("s", "F32", 1, "Sum", n_inputs=2, pre=x0 * x1, post=r0 - x0, launch=(4, 2))
+    lets = []
+
+    def walk(x):
+        if isinstance(x, dict):
+            if "Let" in x and x["Let"]["local"] == 6:  # val = 2r + n + 2
+                lets.append(x["Let"]["init"])
+            for v in x.values():
+                walk(v)
+        elif isinstance(x, list):
+            for v in x:
+                walk(v)
+
+    walk(la["body"])
+    assert len(lets) == 2 and lets[0] == lets[1]
+    stores = json.dumps(la["body"]).count('"Logical": {"buffer": 2')
+    assert stores == 1
 
 
 def test_gather_skeleton_follows_the_gather_lift():

@@ -157,6 +157,39 @@ def test_launched_scan_is_the_written_order(block):
     assert np.array_equal(out, oracle.scan_rows(xi.reshape(1, -1), "Sum").ravel())
 
 
+@pytest.mark.parametrize("dtype", ["F32", "F64"])
+@pytest.mark.parametrize("axis", [0, 1])
+def test_scans_with_a_pre_and_a_post_equal_the_oracle(dtype, axis):
+    """A scan of two inputs with the pre-map `x * y` and the post `Reduced(0) - Input(0)` (one
+    operation each, so C's per-operation rounding and the kernel evaluator's per-statement rounding
+    agree): the C leg of the serial lift equals orc_scan_x bit for bit on every op, direction and
+    exclusivity; the launched lift's C leg (another association of the Sum) stays within the
+    per-prefix bound and is exact for Max / Min."""
+    a, b = data(dtype, (5, 37)), data(dtype, (5, 37))
+    pre, post = X.input(0) * X.input(1), X.reduced(0) - X.input(0)
+    for op in ("Sum", "Max", "Min", "Mean", "Prod"):
+        for exclusive in (False, True):
+            for reverse in (False, True):
+                k = u.lift_scan("sx", dtype, 2, op, axis=axis, exclusive=exclusive, reverse=reverse, n_inputs=2,
+                                pre=pre, post=post)
+                out = np.zeros_like(a)
+                assert cpuc.run(k, a, b, out, 5, 37) == cpuc.OK
+                want = oracle.scan_expr([a, b], axis, op, pre, post, exclusive, reverse)
+                assert out.tobytes() == want.tobytes(), (op, exclusive, reverse)
+    if axis == 1:
+        for op in ("Sum", "Max", "Min"):
+            k = u.lift_scan("sx", dtype, 2, op, n_inputs=2, pre=pre, post=post, launch=(8, 2))
+            out = np.zeros_like(a)
+            assert cpuc.run(k, a, b, out, 5, 37) == cpuc.OK
+            want = oracle.scan_expr([a, b], 1, op, pre, post)
+            if op == "Sum":
+                v = (a.astype(np.float64) * b).astype(a.dtype).astype(np.float64)
+                bound = 37 * 2.0 ** -52 * np.cumsum(np.abs(v), axis=1) + 2 * np.spacing(np.abs(want).astype(a.dtype))
+                assert np.all(np.abs(out.astype(np.float64) - want) <= bound)
+            else:
+                assert out.tobytes() == want.tobytes(), op
+
+
 # ---- gather --------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("index_dtype", ["I32", "I64", "U32"])

@@ -459,6 +459,77 @@ def test_a_wait_that_runs_out_is_reported_not_hung(hip_device, case):
     ex.check()
 
 
+# ---- scans with a pre-map and a fused post ---------------------------------------------
+
+def _eighths(seed, shape, dt=np.float32):
+    """Multiples of 1/8 in [-12.5, 12.5): every product, partial sum and prefix of these stays exact,
+    so every association of the fold gives the serial bits."""
+    return (rng(seed).integers(-100, 100, size=shape) / 8).astype(dt)
+
+
+def _scan_x_cases():
+    from unpopped_amd import expr as X
+
+    x0, x1, x2, r0 = X.input(0), X.input(1), X.input(2), X.reduced(0)
+    # name: (dtype, shape, axis, op, exclusive, reverse, n_inputs, pre, post, data)
+    return {
+        "dev_sum_prod": (np.float32, (4, 5000), 1, "Sum", False, False, 2, x0 * x1, None, "eighths"),
+        "dev_sum_excl_rev_post": (np.float32, (3, 70001), 1, "Sum", True, True, 2, x0 * x1, r0 - x0, "eighths"),
+        "dev_sum_full_row": (np.float32, (1, 1 << 22), 1, "Sum", False, False, 2, x0 * x1, r0 - x0, "eighths"),
+        "dev_max_three_inputs": (np.float64, (2, 33333), 1, "Max", False, False, 3, x0 * x1 + x2, r0 * x2, "normal"),
+        "dev_min_sqrt_post": (np.float32, (5, 4096), 1, "Min", True, False, 2, x0 - x1, (r0 * r0).sqrt(), "normal"),
+        "seq_mean_axis1": (np.float32, (6, 7, 9), 1, "Mean", False, False, 2, x0 + x1, r0 * 2.0, "normal"),
+        "seq_sum_axis0": (np.float32, (300, 17), 0, "Sum", False, True, 1, x0 * x0, None, "normal"),
+        "seq_prod": (np.float32, (4, 50), 1, "Prod", True, False, 1, x0 * 0.5 + 1.0, None, "normal"),
+        "seq_max_f64_axis0": (np.float64, (40, 3, 5), 0, "Max", False, False, 2, x0 / x1, r0 - x1, "normal"),
+    }
+
+
+@pytest.mark.parametrize("case", sorted(_scan_x_cases()))
+def test_scan_with_a_pre_and_a_post(hip_device, case):
+    """Scans of n inputs with a pre-map and a fused post against orc_scan_x: bit-exact on every
+    schedule (the data make every association of a Sum exact), Max/Min exact up to NaN payload; NaN and
+    infinity from the pre (x / y with zeros) included.  The small serial cases are checked against the
+    C99 leg of the same KernelFn too."""
+    dt, shape, axis, op, excl, rev, n, pre, post, data = _scan_x_cases()[case]
+    H.say(f"[case] scan with pre/post {case} {shape}")
+    if data == "eighths":
+        xs = [_eighths(60 + k, shape, dt) for k in range(n)]
+    else:
+        xs = [rng(60 + k).normal(size=shape).astype(dt) for k in range(n)]
+        if n >= 2:
+            xs[1].ravel()[::97] = 0.0  # x / 0: infinities and NaN from the pre
+    got = H.scan_expr(xs, axis, op, pre, post, excl, rev)
+    want = oracle.scan_expr(xs, axis, op, pre, post, excl, rev)
+    assert np.array_equal(got, want, equal_nan=True)
+    if case.startswith("seq") and int(np.prod(shape)) <= 4096:
+        k = u.lift_scan("s", H.NP_KIND[dt], len(shape), op, axis=axis, exclusive=excl, reverse=rev, n_inputs=n,
+                        pre=pre, post=post)
+        out = np.zeros(shape, dt)
+        assert cpuc.run(k, *xs, out, *shape) == cpuc.OK
+        # C rounds each operation of a statement; the kernel evaluator once per statement
+        close = np.isclose(out, want, rtol=4 * np.finfo(dt).eps, atol=0, equal_nan=True)
+        assert close.all()
+
+
+def test_scan_with_a_pre_within_the_bound_on_normal_data(hip_device):
+    """A device-schedule Sum of x * y over 2^22 normal values: every prefix within the declared
+    per-prefix bound of the serial lift's f64 scan of the pre-mapped values."""
+    from unpopped_amd import expr as X
+
+    n = 1 << 22
+    H.say(f"[case] scan with pre x*y, {n} normal values")
+    x = rng(71).normal(size=(1, n)).astype(np.float32)
+    y = rng(72).normal(size=(1, n)).astype(np.float32)
+    got = H.scan_expr([x, y], 1, "Sum", X.input(0) * X.input(1)).ravel().astype(np.float64)
+    want = oracle.scan_expr([x, y], 1, "Sum", X.input(0) * X.input(1)).ravel().astype(np.float64)
+    v = (x * y).ravel().astype(np.float64)
+    k = np.arange(n, dtype=np.float64)
+    gamma = k * 2.0 ** -53 / (1 - k * 2.0 ** -53)
+    ulp = np.spacing(np.abs(got).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 2 * gamma * np.cumsum(np.abs(v)) + ulp)
+
+
 def test_scan_repeated_launches_reuse_state(hip_device):
     """The look-back state is reused across launches (epoch tags): results stay exact."""
     H.say("[case] scan repeated launches")
@@ -1367,7 +1438,8 @@ def test_gather_along_an_axis_of_a_longer_table(hip_device):
 
 
 REFUSED_VIEWS = ["output shorter than the extents", "input of another shape", "wrong rank", "below the storage",
-                 "odd u4 base", "strided dequant output", "table shorter than src_extent", "view count"]
+                 "odd u4 base", "strided dequant output", "table shorter than src_extent", "view count",
+                 "transposed input of a pre-map scan"]
 
 
 @pytest.mark.parametrize("what", REFUSED_VIEWS)
@@ -1388,6 +1460,17 @@ def test_views_that_do_not_fit_are_refused(hip_device, what):
                  (out, (R * Cc,), (ostride,), 0)]
         scalars = [R, Cc]
         check, nbytes = out, 2 * R * Cc * 2
+    elif what == "transposed input of a pre-map scan":
+        from unpopped_amd import expr as X
+
+        R, Cc = 8, 32
+        ex = H.scan_expr_executor("F32", 2, "Sum", 1, X.input(0) * X.input(1), None, 2)
+        a, b = u.DeviceBuffer(R * Cc * 4), u.DeviceBuffer(R * Cc * 4)
+        out = u.DeviceBuffer(R * Cc * 4)
+        out.fill(0x5A)
+        views = [(a, (R, Cc), (1, R), 0), (b, (R, Cc), None, 0), (out, (R, Cc), None, 0)]
+        scalars = [R, Cc]
+        check, nbytes = out, R * Cc * 4
     elif what == "table shorter than src_extent":
         V, D, n = 10, 16, 5
         ex = H.executor(kind="gather", dtype="Bf16", rank=2, index_dtype="I32", oob="Clamp")

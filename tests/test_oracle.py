@@ -710,3 +710,100 @@ def test_general_gather_cell_pins():
     c = init.copy()
     assert cpuc.run(k, ids, scale, t, c, 7, 5, 6) == cpuc.OK
     assert not np.array_equal(bad, c)
+
+
+# ---- scans with a pre-map and a fused post (orc_scan_x) ---------------------------------
+
+SCAN_OPS = ["Sum", "Max", "Min", "Prod", "Mean"]
+
+
+@pytest.mark.parametrize("op", SCAN_OPS)
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_scan_x_identity_pre_equals_the_scan_oracle(op, dt):
+    """With the identity pre-map and no post the lifted scan is the plain one: orc_scan_x agrees
+    bit for bit with orc_scan_rows (pinned above) on every op, direction and exclusivity, NaN and
+    infinity included."""
+    x = np.random.default_rng(51).normal(size=(3, 37)).astype(dt)
+    x[0, 5] = np.nan
+    x[1, 9] = np.inf
+    x[2, 30] = -np.inf
+    for excl in (False, True):
+        for rev in (False, True):
+            got = oracle.scan_expr([x], 1, op, X.input(0), exclusive=excl, reverse=rev)
+            assert np.array_equal(got, oracle.scan_rows(x, op, excl, rev), equal_nan=True), (op, excl, rev)
+
+
+@pytest.mark.parametrize("axis", [0, 1, 2])
+def test_scan_x_along_any_axis_equals_the_moved_axis_scan(axis):
+    """The A x S x B indexing: a scan along `axis` equals the innermost-axis scan of the array with
+    that axis moved last."""
+    x = np.random.default_rng(52).normal(size=(4, 5, 6)).astype(np.float32)
+    for op in ("Sum", "Max", "Mean"):
+        got = oracle.scan_expr([x], axis, op, X.input(0), reverse=True)
+        moved = np.moveaxis(x, axis, -1)
+        want = oracle.scan_rows(moved.reshape(-1, moved.shape[-1]), op, False, True).reshape(moved.shape)
+        assert np.array_equal(got, np.moveaxis(want, -1, axis)), (axis, op)
+
+
+def test_scan_x_pre_rounds_once_before_the_fold():
+    """`val = up(pre)`: the pre-map is rounded once to the dtype before the f64 fold.  For f32 inputs
+    x * y rounded to f32 is numpy's f32 product, so the Sum scan is numpy's sequential f64 cumsum of
+    that product, rounded once per prefix.  The same data scanned without the rounding differs, so
+    the check sees a dropped rounding."""
+    r = np.random.default_rng(53)
+    x = r.normal(size=(2, 300)).astype(np.float32)
+    y = r.normal(size=(2, 300)).astype(np.float32)
+    got = oracle.scan_expr([x, y], 1, "Sum", X.input(0) * X.input(1))
+    prod = x * y
+    want = np.cumsum(prod.astype(np.float64), axis=1).astype(np.float32)
+    assert np.array_equal(got, want)
+    unrounded = np.cumsum(x.astype(np.float64) * y.astype(np.float64), axis=1).astype(np.float32)
+    assert not np.array_equal(unrounded, want)
+
+
+def test_scan_x_post_reads_the_rounded_prefix_and_the_position():
+    """scan_write: the post reads Reduced(0) as the prefix rounded once and Input(k) as the element at
+    the position.  On data whose every prefix is exact in f32 (multiples of 1/8 below 2^7)
+    `Reduced(0) - Input(0)` after an inclusive Sum is the exclusive prefix, and
+    `Reduced(0) * 2 + Input(1)` is that closed form too."""
+    r = np.random.default_rng(54)
+    x = (r.integers(-100, 100, size=(4, 257)) / 8).astype(np.float32)
+    y = (r.integers(-100, 100, size=(4, 257)) / 8).astype(np.float32)
+    incl = np.cumsum(x.astype(np.float64), axis=1)
+    got = oracle.scan_expr([x], 1, "Sum", X.input(0), post=X.reduced(0) - X.input(0))
+    assert np.array_equal(got, (incl - x).astype(np.float32))
+    assert np.array_equal(got, oracle.scan_rows(x, "Sum", True, False))
+    got2 = oracle.scan_expr([x, y], 1, "Sum", X.input(0), post=X.reduced(0) * 2.0 + X.input(1))
+    assert np.array_equal(got2, (incl.astype(np.float32).astype(np.float64) * 2 + y).astype(np.float32))
+
+
+def test_scan_x_post_rounds_the_prefix_before_it():
+    """The post sees the prefix rounded to f32, not the f64 fold: for `sqrt(Reduced(0))` the result
+    is sqrt of the f32 prefix rounded once; a post fed the unrounded f64 fold differs on this data."""
+    x = np.random.default_rng(56).random(size=(1, 2000)).astype(np.float32)
+    got = oracle.scan_expr([x], 1, "Sum", X.input(0), post=X.reduced(0).sqrt())
+    pref = np.cumsum(x.astype(np.float64), axis=1)
+    want = np.sqrt(pref.astype(np.float32).astype(np.float64)).astype(np.float32)
+    assert np.array_equal(got, want)
+    assert not np.array_equal(np.sqrt(pref).astype(np.float32), want)
+
+
+def test_scan_x_running_mean_and_nan_rules():
+    """A Mean scan divides the f64 sum by the count so far (an exclusive first prefix is 0 / 0, NaN);
+    a Max scan of a pre-map that makes NaN keeps it from there on (numpy's maximum.accumulate)."""
+    x = synth.uniform_pm1_f32(57, 3 * 64).reshape(3, 64)
+    y = synth.uniform_pm1_f32(58, 3 * 64).reshape(3, 64)
+    got = oracle.scan_expr([x, y], 1, "Mean", X.input(0) + X.input(1))
+    s = (x + y).astype(np.float64)
+    want = (np.cumsum(s, axis=1) / np.arange(1, 65)).astype(np.float32)
+    assert np.array_equal(got, want)
+    ex = oracle.scan_expr([x, y], 1, "Mean", X.input(0) + X.input(1), exclusive=True)
+    assert np.all(np.isnan(ex[:, 0])) and np.array_equal(ex[:, 1:], want[:, :-1])
+    d = y.copy()
+    d[1, 20] = 0.0
+    x2 = x.copy()
+    x2[1, 20] = 0.0  # 0 / 0: NaN from column 20 on
+    v = (x2.astype(np.float64) / d.astype(np.float64)).astype(np.float32)
+    got = oracle.scan_expr([x2, d], 1, "Max", X.input(0) / X.input(1))
+    assert np.array_equal(got, np.maximum.accumulate(v, axis=1), equal_nan=True)
+    assert np.isnan(got[1, 20:]).all() and not np.isnan(got[1, :20]).any()

@@ -186,11 +186,24 @@ def lift_reduction(name: str, dtype: str, rank: int, op: str, axes: tuple = (), 
 
 
 def lift_scan(name: str, dtype: str, rank: int, op: str, axis: int | None = None, exclusive: bool = False,
-              reverse: bool = False, launch: tuple | None = None) -> dict:
+              reverse: bool = False, launch: tuple | None = None, n_inputs: int = 1, pre=None, post=None) -> dict:
+    """The scan lift (serial, or launched on ``launch = (block, grid)``) as a KernelFn dict.  ``pre``
+    is the pre-map over ``Input(0..n_inputs)`` (default ``Input(0)``) and ``post`` a fused post over
+    ``Reduced(0)`` (the prefix rounded once) and the position's ``Input(k)`` (default the identity),
+    each an ``expr.Expr`` or its serde dict."""
     b, g = _geom(launch)
     ax = rank - 1 if axis is None else axis
-    return _lifted(lambda o, e: _lib.lib().unp_lift_scan(name.encode(), ELEMENT_KINDS[dtype], rank, REDUCE_OPS[op],
-                                                        ax, int(exclusive), int(reverse), b, g, o, e))
+    if pre is None and post is None and n_inputs == 1:
+        return _lifted(lambda o, e: _lib.lib().unp_lift_scan(name.encode(), ELEMENT_KINDS[dtype], rank,
+                                                            REDUCE_OPS[op], ax, int(exclusive), int(reverse), b, g,
+                                                            o, e))
+    from . import expr as X
+
+    pj = json.dumps(X.as_json(X.input(0) if pre is None else pre)).encode()
+    qj = None if post is None else json.dumps(X.as_json(post)).encode()
+    return _lifted(lambda o, e: _lib.lib().unp_lift_scan_x(name.encode(), ELEMENT_KINDS[dtype], rank, REDUCE_OPS[op],
+                                                          ax, int(exclusive), int(reverse), n_inputs, pj, qj, b, g,
+                                                          o, e))
 
 
 def lift_gather(name: str, dtype: str, rank: int, index_dtype: str = "I32", axis: int = 0, oob: str = "ZeroFill",

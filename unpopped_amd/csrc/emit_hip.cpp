@@ -1488,6 +1488,135 @@ int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L
   return UNP_OK;
 }
 
+// A scan with a pre-map body over n inputs and a fused post (lift_scan_opdef with pre and post,
+// kernel_lift.rs:504-602; scan_launched.rs:54-102).  Float dtypes only: the expressions are
+// spelled in f64.  The innermost axis with Sum / Max / Min runs the register look-back scan
+// (xscan_lookback); any other axis, a Mean, a float Prod and the serial schedule run xscan_seq
+// in the serial lift's order.
+int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std::string& why) {
+  if (rx.plain) return lower_form(f, L, why);
+  L = Lowered{};
+  L.form = f;
+  L.rx = rx;
+  if (f.rank < 1 || f.rank > 8) {
+    why = "rank is zero or more than 8";
+    return UNP_LIFT_DECLINE;
+  }
+  if (f.dtype != UNP_F32 && f.dtype != UNP_F64) {
+    why = "a scan with a pre-map body at an integer dtype (its integer expressions have no spelling here)";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (rx.n_inputs < 1 || rx.n_inputs > 8) {
+    why = "a scan reads 1 to 8 inputs";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (f.op0 != UNP_OP_SUM && f.op0 != UNP_OP_MAX && f.op0 != UNP_OP_MIN && f.op0 != UNP_OP_PROD &&
+      f.op0 != UNP_OP_MEAN) {
+    why = "a scan folds Sum, Prod, Max, Min or Mean";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  int32_t axis = f.rank - 1;
+  if (f.axes_mask) {
+    if ((f.axes_mask & (f.axes_mask - 1)) != 0 || (f.axes_mask >> f.rank) != 0) {
+      why = "a scan scans exactly one axis inside the rank";
+      return UNP_LIFT_DECLINE;
+    }
+    axis = __builtin_ctz(f.axes_mask);
+  }
+  const bool serial = axis != f.rank - 1 || f.op0 == UNP_OP_PROD || f.op0 == UNP_OP_MEAN ||
+                      f.schedule == UNP_SCHEDULE_SERIAL;
+  L.serial_scan = serial;
+  L.scan_axis = axis;
+  const char* T = ctype(f.dtype);
+  std::string pre, post = "r[0]";
+  if (!expr_cpp(rx.body, T, pre, why)) {
+    why = "pre: " + why + " has no spelling here";
+    return UNP_UNSUPPORTED_OP;
+  }
+  if (rx.has_post && !expr_cpp(rx.post, T, post, why)) {
+    why = "post: " + why + " has no spelling here";
+    return UNP_UNSUPPORTED_OP;
+  }
+  const int NI = rx.n_inputs;
+  const char* EX = f.exclusive ? "true" : "false";
+  const char* RV = f.reverse ? "true" : "false";
+  const std::string key = std::string(T) + "|" + std::to_string(NI) + "|" + std::to_string(f.op0) + "|" + EX + "|" +
+                          RV + "|" + (serial ? "q" : "d") + "|" + pre + "|" + (rx.has_post ? post : std::string("-"));
+  char hx[17];
+  std::snprintf(hx, sizeof hx, "%016llx", (unsigned long long)fnv1a64(key));
+  L.name = std::string("unp_xscan_") + (serial ? "seq_" : "") + (f.exclusive ? "excl_" : "incl_") +
+           (f.reverse ? "rev_" : "") + op_name(f.op0) + "_" + lower_name(f.dtype) + "_" + std::string(hx, 8);
+  const std::string ops = L.name + "_ops";
+  std::ostringstream src;
+  src << header(L.name, f);
+  src << "struct " << ops << " {\n  static constexpr bool has_post = " << (rx.has_post ? "true" : "false") << ";\n"
+      << "  static __device__ __forceinline__ double pre(const double* x) { (void)x; return " << pre << "; }\n"
+      << "  static __device__ __forceinline__ double post(const double* r, const double* x) { (void)r; (void)x; "
+      << "return " << post << "; }\n};\n";
+  std::ostringstream sig, ins;
+  for (int k = 0; k < NI; ++k) sig << "const " << T << "* in" << k << ", ";
+  sig << T << "* out";
+  ins << "  const " << T << "* in[" << NI << "] = {";
+  for (int k = 0; k < NI; ++k) ins << (k ? ", " : "") << "in" << k;
+  ins << "};\n";
+  Entry e;
+  e.fast = false;
+  e.vec = 1;
+  if (serial) {
+    e.threads = 256;
+    e.blocks_per_cu = 8;
+    e.symbol = L.name + "_xq";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol << "(" << sig.str()
+        << ", long long A, long long S, long long B) {\n" << ins.str() << "  unp::xscan_seq<" << T << ", " << NI
+        << ", " << f.op0 << ", " << ops << ", " << EX << ", " << RV << ">(in, out, A, S, B);\n}\n";
+  } else {
+    // 8 waves of K = 8 steps: a 4096-position block tile, the raw inputs of every step kept in
+    // registers for the post.
+    e.k = 8;
+    e.wpb = 8;
+    e.threads = 512;
+    e.blocks_per_cu = 2;
+    e.symbol = L.name + "_xs";
+    src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol << "(" << sig.str()
+        << ", long long rows, long long cols, unsigned long long* status, unsigned* counter, unsigned ticket_base, "
+        << "unsigned epoch, unp::waits wt) {\n" << ins.str() << "  unp::xscan_lookback<" << T << ", " << NI << ", "
+        << f.op0 << ", " << ops << ", " << EX << ", " << RV << ", " << e.k << ", " << e.wpb << ", " << kScanStatusWords
+        << ">(in, out, rows, cols, status, counter, ticket_base, epoch, wt);\n}\n";
+  }
+  L.entries.push_back(e);
+  L.threads = e.threads;
+  L.blocks_per_cu = e.blocks_per_cu;
+  L.source = src.str();
+  std::ostringstream j;
+  j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"scan\",\"dtype\":\"" << kind_name(f.dtype)
+    << "\",\"op\":\"" << op_name(f.op0) << "\",\"exclusive\":" << EX << ",\"reverse\":" << RV << ",\"rank\":" << f.rank
+    << ",\"axis\":" << axis << ",\"n_inputs\":" << NI << ",\"pre\":" << kir::write(rx.body)
+    << ",\"post\":" << (rx.has_post ? kir::write(rx.post) : std::string("null"))
+    << ",\"schedule\":\"" << (serial ? "serial" : "device") << "\",\"params\":[";
+  for (int k = 0; k < NI; ++k) j << "{\"name\":\"in" << k << "\",\"kind\":\"buffer\",\"role\":\"Read\"},";
+  j << "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
+  for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
+  j << "],\"launch\":{\"block\":[" << e.threads << ",1,1],\"grid\":\"cu_count*" << e.blocks_per_cu
+    << "\",\"grid_policy\":\""
+    << (serial ? "device-class constant; one lane per column of the inputs seen as A x S x B around the scanned axis"
+               : "device-class constant; block tiles of 4096 positions taken by ticket, decoupled look-back")
+    << "\"},\"entries\":[{\"symbol\":\"" << e.symbol << "\",\"when\":\"always\"}],\"workspace\":"
+    << (serial ? std::string("null")
+               : "{\"status\":\"tiles * " + std::to_string(kScanStatusWords * 8) +
+                     " bytes, zeroed once\",\"counter\":4,\"stall\":4,\"host_state\":[\"epoch\",\"ticket_base\"]}")
+    << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
+    << ",\"fidelity_notes\":["
+    << json_str(serial ? "the pre and the post evaluate in f64 and round once per statement, as the kernel evaluator runs "
+                         "the lifted kernel; the fold in the serial lift's own order: bit-exact against the serial kernel"
+                       : "the pre and the post evaluate in f64 and round once per statement; a Sum's prefixes are f64 "
+                         "folds of the pre-mapped elements in another order (wave-local scans and decoupled look-back), "
+                         "within the declared per-prefix bound gamma_(n-1)*sum|v| + 1/2 ulp before the post, and not "
+                         "reproducible run to run; Max/Min exact except NaN payload and the sign of a zero")
+    << "]}";
+  L.interface_json = j.str();
+  return UNP_OK;
+}
+
 int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail) {
   out = Lowered{};
   out.form = f;

@@ -1323,6 +1323,161 @@ UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 ro
 }
 
 // ---------------------------------------------------------------------------------------
+// Scans of NI inputs with a pre-map and a fused post (lift_scan_opdef with pre and post,
+// kernel_lift.rs:530-602; scan_launched.rs:140-160).  At each position OPS::pre evaluates in f64
+// over the position's inputs and rounds once to T, and that element is what the fold takes
+// (`val = up(pre)`).  The stored prefix is rounded once to T (`red`).  With a post, OPS::post
+// evaluates in f64 over `red` (r[0]) and the position's inputs (x[k]) and rounds once at the
+// store.  Float dtypes only.
+// ---------------------------------------------------------------------------------------
+template <class T, int NI, class OPS> UNP_DEV T xscan_elem(const T* const* __restrict__ in, i64 off, T (&raw)[NI]) {
+  double x[NI];
+#pragma unroll
+  for (int k = 0; k < NI; ++k) {
+    raw[k] = in[k][off];
+    x[k] = (double)raw[k];
+  }
+  return (T)OPS::pre(x);
+}
+template <class T, int NI, class OPS> UNP_DEV T xscan_store(T red, const T (&raw)[NI]) {
+  if constexpr (OPS::has_post) {
+    double x[NI], r[1] = {(double)red};
+#pragma unroll
+    for (int k = 0; k < NI; ++k) x[k] = (double)raw[k];
+    return (T)OPS::post(r, x);
+  } else {
+    return red;
+  }
+}
+
+// The serial lift's order (as scan_seq): one lane per column of A x S x B, bit-exact.
+template <class T, int NI, int OP, class OPS, bool EXCL, bool REV>
+UNP_DEV void xscan_seq(const T* const* __restrict__ in, T* __restrict__ out, i64 A, i64 S, i64 B) {
+  typedef typename serial_acc<T>::type Ac;
+  typedef fold<Ac, OP> F;
+  const i64 cols = A * B;
+  const i64 stride = (i64)gridDim.x * blockDim.x;
+  for (i64 c = (i64)blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += stride) {
+    const i64 a = c / B, b = c - a * B;
+    const i64 base = a * S * B + b;
+    Ac v = F::identity();
+    for (i64 i = 0; i < S; ++i) {
+      const i64 off = base + (REV ? S - 1 - i : i) * B;
+      T raw[NI];
+      const T e = xscan_elem<T, NI, OPS>(in, off, raw);
+      if constexpr (EXCL) {
+        out[off] = xscan_store<T, NI, OPS>(scan_out<T, OP>(v, i), raw);
+        v = F::apply(v, (Ac)e);
+      } else {
+        v = F::apply(v, (Ac)e);
+        out[off] = xscan_store<T, NI, OPS>(scan_out<T, OP>(v, i + 1), raw);
+      }
+    }
+  }
+}
+
+// The device schedule (innermost axis, Sum / Max / Min, as scan_lookback with one element per
+// lane per step): block tiles of WPB * 64 * K positions taken by ticket, a wave-local scan of
+// the pre-mapped elements, the block's aggregate published and the row's earlier tiles folded by
+// decoupled look-back, each prefix rounded once and passed through the post.  Lane l's step k
+// is position k * 64 + l of its wave's stripe, so every load and store of a step is contiguous.
+template <class T, int NI, int OP, class OPS, bool EXCL, bool REV, int K, int WPB, int SP>
+UNP_DEV void xscan_lookback(const T* const* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
+                            u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base, u32 epoch, waits wt) {
+  typedef typename acc<T, OP>::type A;
+  typedef fold<A, OP> F;
+  typedef tile_status<A, SP> S;
+  constexpr i64 WT = (i64)64 * K;
+  constexpr i64 BT = WT * WPB;
+  __shared__ u32 slot[2];
+  __shared__ A wagg[WPB];
+  __shared__ A gbase;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const A I = F::identity();
+  const T pad = (T)I;  // the identity, exactly representable at the element type
+  const i64 tpr = (cols + BT - 1) / BT;
+  const u64 total = (u64)rows * (u64)tpr;
+  if (tid == 0) slot[0] = draw_ticket(counter) - ticket_base;
+  __syncthreads();
+  for (int r = 0;; ++r) {
+    const u64 g = slot[r & 1];
+    if (g >= total) break;  // uniform across the block
+    u32 next = 0;
+    if (tid == 0) next = draw_ticket(counter);
+    const i64 row = (i64)(g / (u64)tpr);
+    const i64 j = (i64)g - row * tpr;
+    const i64 p0 = j * BT + (i64)wave * WT;
+
+    // This wave's elements in scan order, pre-mapped; the raw inputs kept for the post.
+    T x[K];
+    T raw[K][OPS::has_post ? NI : 1];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const i64 pos = p0 + (i64)k * 64 + lane;
+      if (pos < cols) {
+        T rk[NI];
+        x[k] = xscan_elem<T, NI, OPS>(in, row * cols + (REV ? cols - 1 - pos : pos), rk);
+        if constexpr (OPS::has_post) {
+#pragma unroll
+          for (int q = 0; q < NI; ++q) raw[k][q] = rk[q];
+        }
+      } else {
+        x[k] = pad;
+      }
+    }
+
+    // Wave-local prefixes: pre[k] is the fold of this wave's elements before lane's step k.
+    A pre[K];
+    A carry = I;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const A inc = wave_inclusive_scan<A, OP>((A)x[k], lane);
+      pre[k] = F::apply(carry, wave_shr1(inc, I));
+      carry = F::apply(carry, readlane(inc, 63));
+    }
+    if (lane == 0) wagg[wave] = carry;
+    __syncthreads();
+
+    A wex = I;
+    for (int w = 0; w < wave; ++w) wex = F::apply(wex, wagg[w]);
+    if (wave == 0) {
+      A agg = wagg[0];
+#pragma unroll
+      for (int w = 1; w < WPB; ++w) agg = F::apply(agg, wagg[w]);
+      A gex = I;
+      if (j == 0) {
+        if (lane == 0) S::publish(st, g, 1, agg, epoch);
+      } else {
+        if (lane == 0) S::publish(st, g, 0, agg, epoch);
+        gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch, wt);
+        if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
+      }
+      if (lane == 0) {
+        gbase = gex;
+        slot[(r + 1) & 1] = next - ticket_base;
+      }
+    }
+    __syncthreads();
+    const A base = F::apply(gbase, wex);
+
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const i64 pos = p0 + (i64)k * 64 + lane;  // scan-order index
+      if (pos < cols) {
+        const A before = F::apply(base, pre[k]);
+        const T red = EXCL ? scan_out<T, OP>(before, pos) : scan_out<T, OP>(F::apply(before, (A)x[k]), pos + 1);
+        T rk[NI];
+        if constexpr (OPS::has_post) {
+#pragma unroll
+          for (int q = 0; q < NI; ++q) rk[q] = raw[k][q];
+        }
+        out[row * cols + (REV ? cols - 1 - pos : pos)] = xscan_store<T, NI, OPS>(red, rk);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // LDS-staged single-pass scan with decoupled look-back, for rows whose scanned extent is a
 // multiple of VEC (in / out 16-byte aligned).
 //

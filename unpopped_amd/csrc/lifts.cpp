@@ -2,9 +2,9 @@
 // the recognizer behind Backend::lower_kernel.
 //
 // Each lift builds exactly the KernelFn the reference's lift builds (same statements, locals,
-// parameters, launch shape and shared allocations), for the op forms this backend lowers: a
-// reduction or scan of one input with the identity body and no fused post, and a gather whose
-// body is the identity copy of the data input.  lower_kernel recognises a kernel by lifting
+// parameters, launch shape and shared allocations), for the op forms this backend lowers:
+// reductions and scans of n inputs with a pre-map body and a fused post, the fused row folds,
+// RowReduce, gathers with a body, and the int4 dequant forms.  lower_kernel recognises a kernel by lifting
 // every candidate form its signature admits and comparing the trees: a kernel equal to a lift's
 // output is that form; anything else is refused with UnsupportedKernel (refuse rather than
 // approximate, crates/unpopped/src/backend.rs:703-707).
@@ -215,6 +215,9 @@ J launch_or_null(uint32_t block, uint32_t grid) { return (block || grid) ? launc
 J input_leaf(uint32_t k);
 J reduced_leaf(uint32_t t);
 void check_reduction_exprs(const J& body, const J* post, uint32_t n_inputs);
+void check_post(const J& e, int64_t available, int64_t n_inputs);
+int64_t leaf_index(const J& e);
+template <class F> J map_leaves(const J& e, const F& leaf);
 
 // lift_reduction_opdef (kernel_lift.rs:447-484) and lift_reduction_opdef_launched
 // (kernel_lift/block_reduce.rs:50-93): n inputs, a pre-map `body` over them (Input(0) for the
@@ -335,42 +338,91 @@ J scan_identity(int32_t rop, int32_t dtype) {
 
 bool dtype_is_f64(const Shape& sh) { return sh.dtype == UNP_F64; }
 
-// scan_pass (kernel_lift.rs:548-576) with the identity pre-map and no post.
-std::vector<J> scan_pass(const Shape& sh, int32_t rop, bool exclusive) {
-  std::vector<J> pass = {s_load(sh.loaded(0), p_logical(0, sh.counters())), s_let(sh.val, sh.up(loc(sh.loaded(0))))};
+// scan_loads (kernel_lift.rs:530-545): one load per input at the current position, then
+// `val = up(pre)` with each Input(k) bound to the k-th loaded local.
+std::vector<J> scan_loads(const Shape& sh, const J& pre) {
+  std::vector<J> pass;
+  for (uint32_t k = 0; k < sh.n; ++k) pass.push_back(s_load(sh.loaded(k), p_logical(k, sh.counters())));
+  pass.push_back(s_let(sh.val, sh.up(sh.subst_inputs(pre))));
+  return pass;
+}
+
+// scan_write (kernel_lift.rs:578-602): the prefix stored at the current position; with a fused
+// post, the prefix rounded once into `red` and the post over it, its Input(k) leaves bound to
+// the elements loaded for this position.
+std::vector<J> scan_write(const Shape& sh, int32_t rop, const J* post) {
   // scan_stored (kernel_lift.rs:604-619): a running Mean divides by the count folded so far.
   J stored = sh.stored(rop);
   if (rop == UNP_OP_MEAN) {
     J mean = e_div(loc(sh.acc), widen(loc(sh.have), "F64"));
     stored = dtype_is_f64(sh) ? mean : widen(mean, EK(sh.dtype));
   }
-  J write = s_store(p_logical(sh.n, sh.counters()), stored);
+  const J place = p_logical(sh.n, sh.counters());
+  if (!post) return {s_store(place, stored)};
+  const J value = map_leaves(*post, [&](const J& x, J& out) {
+    if (x.t != J::Obj || x.o.size() != 1) return false;
+    if (x.o[0].first == "Reduced") {
+      out = loc(sh.red);
+      return true;
+    }
+    if (x.o[0].first == "Input") {
+      out = loc(sh.loaded((uint32_t)leaf_index(x)));
+      return true;
+    }
+    return false;
+  });
+  return {s_let(sh.red, stored), s_store(place, value)};
+}
+
+// scan_pass (kernel_lift.rs:548-576): load and pre-map, fold, and write the prefix after the
+// fold (inclusive) or before it (exclusive).
+std::vector<J> scan_pass(const Shape& sh, int32_t rop, bool exclusive, const J& pre, const J* post) {
+  std::vector<J> pass = scan_loads(sh, pre);
+  const std::vector<J> write = scan_write(sh, rop, post);
   std::vector<J> fold = fold_step(rop, sh.acc, sh.have, sh.val, sh.is_int());
   if (rop == UNP_OP_MEAN) fold.push_back(s_assign(sh.have, e_add(loc(sh.have), int_(1))));
   if (exclusive) {
-    pass.push_back(write);
+    for (auto& s : write) pass.push_back(s);
     for (auto& s : fold) pass.push_back(s);
   } else {
     for (auto& s : fold) pass.push_back(s);
-    pass.push_back(write);
+    for (auto& s : write) pass.push_back(s);
   }
   return pass;
 }
 
+// check_scan (kernel_lift.rs:658-690) for the expressions: the pre-map reads only the op's
+// inputs (leaves_ok); a fused post reads Reduced(0) and the inputs (check_post with one stage),
+// and only at a float dtype (check_accumulated_dtype, kernel_lift.rs:796-801).
+void check_scan_exprs(int32_t dtype, const J& pre, const J* post, uint32_t n_inputs) {
+  check_post(pre, 0, (int64_t)n_inputs);
+  if (post) {
+    if (is_int_kernel_dtype(dtype)) throw Decline{"UnsupportedForm: a fused post at an integer dtype"};
+    check_post(*post, 1, (int64_t)n_inputs);
+  }
+}
+
 // lift_scan_opdef (kernel_lift.rs:504-519) and lift_scan_opdef_launched
-// (kernel_lift/scan_launched.rs:54-102), identity pre-map, no post.
+// (kernel_lift/scan_launched.rs:54-102): n inputs, a pre-map `pre_expr` over them (Input(0) for
+// the plain scan) and an optional fused `post` over Reduced(0) and the inputs (nullptr for the
+// identity post).
 J lift_scan(const std::string& name, int32_t dtype, int32_t rank, int32_t rop, int32_t axis, bool exclusive,
-            bool reverse, uint32_t block, uint32_t grid) {
+            bool reverse, uint32_t block, uint32_t grid, uint32_t n_inputs = 1, const J* pre_expr = nullptr,
+            const J* post = nullptr) {
   check_accumulated(dtype, rop, "a scan");
+  const J plain = input_leaf(0);
+  const J& pre = pre_expr ? *pre_expr : plain;
+  if (post && *post == reduced_leaf(0)) post = nullptr;  // the identity post
+  check_scan_exprs(dtype, pre, post, n_inputs);
   check_rank(rank);
   const bool launched = block || grid;
   if (axis < 0 || axis >= rank) throw Decline{"UnsupportedForm: a scan axis outside the rank"};
   if (launched && axis != rank - 1) throw Decline{"UnsupportedForm: a scan over a non-innermost axis in a launched scan"};
   if (rop == UNP_OP_MEAN && dtype != UNP_F32 && dtype != UNP_F64) throw Decline{"UnsupportedForm: an integer Mean"};
   if (!launched) {
-    const Shape sh(dtype, (uint32_t)rank, 1u << axis);
+    const Shape sh(dtype, (uint32_t)rank, 1u << axis, n_inputs);
     const uint32_t scanned = sh.reduced[0];
-    std::vector<J> pass = scan_pass(sh, rop, exclusive);
+    std::vector<J> pass = scan_pass(sh, rop, exclusive, pre, post);
     J start = reverse ? e_sub(loc(scanned), int_(1)) : int_(0);
     J end = reverse ? int_(-1) : loc(scanned);
     J step = reverse ? int_(-1) : int_(1);
@@ -379,10 +431,11 @@ J lift_scan(const std::string& name, int32_t dtype, int32_t rank, int32_t rop, i
     for (auto it = sh.kept.rbegin(); it != sh.kept.rend(); ++it) row = for_axis(*it, sh.r, row);
     std::vector<J> params, locals;
     sh.signature(sh.r, params, locals);
+    if (post) locals.push_back(local_decl(EK(dtype)));  // red: the prefix rounded to the compute dtype
     return kernel_fn(name, EK(dtype), params, locals, row, J::null(), {});
   }
   if (grid == 0 || !pow2(block)) throw Decline{"BadLaunch"};
-  const Shape sh(dtype, (uint32_t)rank, 0);
+  const Shape sh(dtype, (uint32_t)rank, 0, n_inputs);
   if (rop == UNP_OP_MEAN) throw Decline{"UnsupportedForm: a Mean scan in a launched scan"};
   if (rop == UNP_OP_PROD && !sh.is_int()) throw Decline{"UnsupportedForm: a float Prod scan in a launched scan"};
   const bool flag = rop == UNP_OP_MAX || rop == UNP_OP_MIN;
@@ -402,7 +455,7 @@ J lift_scan(const std::string& name, int32_t dtype, int32_t rank, int32_t rop, i
       return s_for(sh.counter(scanned), e_sub(e_sub(n, int_(1)), loc(lo)), e_sub(e_sub(n, int_(1)), loc(hi)), int_(-1), body);
     return s_for(sh.counter(scanned), loc(lo), loc(hi), int_(1), body);
   };
-  std::vector<J> fold_only = {s_load(sh.loaded(0), p_logical(0, sh.counters())), s_let(sh.val, sh.up(loc(sh.loaded(0))))};
+  std::vector<J> fold_only = scan_loads(sh, pre);
   for (auto& s : fold_step(rop, sh.acc, sh.have, sh.val, sh.is_int())) fold_only.push_back(s);
   std::vector<J> row = {s_let(sh.acc, identity()), s_let(sh.have, int_(0)), s_let(partner, identity()), walk(fold_only)};
   for (auto& s : publish()) row.push_back(s);
@@ -426,7 +479,7 @@ J lift_scan(const std::string& name, int32_t dtype, int32_t rank, int32_t rop, i
     }
     row.push_back(s_if(e_bin("CmpEq", thread(), uconst(0)), {s_assign(sh.acc, identity()), s_assign(sh.have, int_(0))}, load));
   }
-  row.push_back(walk(scan_pass(sh, rop, exclusive)));
+  row.push_back(walk(scan_pass(sh, rop, exclusive, pre, post)));
   row.push_back(s_barrier());
   std::vector<J> body;
   if (sh.kept.empty()) {
@@ -1365,6 +1418,22 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
       out.lift = block ? "lift_reduction_opdef_launched" : "lift_reduction_opdef";
       return UNP_OK;
     };
+    auto take_scan = [&](int32_t op, int32_t axis, int ex, int rev, const J& b, const J& p, bool hp) {
+      out.form.kind = UNP_FORM_SCAN;
+      out.form.dtype = dt;
+      out.form.rank = r;
+      out.form.op0 = op;
+      out.form.exclusive = ex;
+      out.form.reverse = rev;
+      out.form.axes_mask = axis == r - 1 ? 0u : (1u << axis);
+      out.rx.n_inputs = (int32_t)n;
+      out.rx.body = b;
+      out.rx.has_post = hp;
+      out.rx.post = p;
+      out.rx.plain = n == 1 && b == input_leaf(0) && !hp;
+      out.lift = block ? "lift_scan_opdef_launched" : "lift_scan_opdef";
+      return UNP_OK;
+    };
     static const int32_t ops[] = {UNP_OP_SUM,    UNP_OP_PROD, UNP_OP_MAX, UNP_OP_MIN, UNP_OP_MEAN,
                                   UNP_OP_MAXNUM, UNP_OP_MINNUM, UNP_OP_AND, UNP_OP_OR, UNP_OP_XOR};
     // Every reduced-axis set whose output rank matches (ReductionShape::new,
@@ -1385,23 +1454,16 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
             return take_reduction(op, mask, xbody, xpost, has_post);
         }
       }
-      if (orank == r && n == 1) {
+      if (orank == r && exprs_ok) {
         // The innermost axis first (the only one a launched scan takes), then the others.
         for (int32_t ai = 0; ai < r; ++ai) {
           const int32_t axis = ai == 0 ? r - 1 : ai - 1;
           for (int ex = 0; ex <= 1; ++ex)
             for (int rev = 0; rev <= 1; ++rev)
-              if (attempt([&] { return lift_scan(name, dt, r, op, axis, ex, rev, block, grid); })) {
-                out.form.kind = UNP_FORM_SCAN;
-                out.form.dtype = dt;
-                out.form.rank = r;
-                out.form.op0 = op;
-                out.form.exclusive = ex;
-                out.form.reverse = rev;
-                out.form.axes_mask = axis == r - 1 ? 0u : (1u << axis);
-                out.lift = block ? "lift_scan_opdef_launched" : "lift_scan_opdef";
-                return UNP_OK;
-              }
+              if (attempt([&] {
+                    return lift_scan(name, dt, r, op, axis, ex, rev, block, grid, n, &xbody, has_post ? &xpost : nullptr);
+                  }))
+                return take_scan(op, axis, ex, rev, xbody, xpost, has_post);
         }
       }
     }
@@ -1428,6 +1490,25 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
           }
         }
       }
+    if (orank == r)
+      for (int32_t op : ops)
+        for (int32_t axis = r - 1; axis >= 0; --axis)
+          for (int ex = 0; ex <= 1; ++ex)
+            for (int rev = 0; rev <= 1; ++rev)
+              for (int pm = 0; pm <= 1; ++pm) {
+                J proto, kr, b, p;
+                bool hp = false;
+                try {
+                  proto = lift_scan(name, dt, r, op, axis, ex, rev, block, grid, n, nullptr, pm ? &probe_post : nullptr);
+                } catch (const Decline&) {
+                  continue;
+                }
+                if (!into_numbering_of(proto, kc, kr) || !extract(kr, b, p, hp) || hp != (pm == 1)) continue;
+                if (attempt([&] {
+                      return lift_scan(name, dt, r, op, axis, ex, rev, block, grid, n, &b, hp ? &p : nullptr);
+                    }))
+                  return take_scan(op, axis, ex, rev, b, p, hp);
+              }
   }
   // Fused row fold: in0 Read rank 2, out0 / out1 Write rank 1, two I32 extents.
   if (np == 5 && ps[0].buffer && ps[0].rank == 2 && ps[1].buffer && ps[2].buffer && !ps[3].buffer && !ps[4].buffer) {
@@ -1786,6 +1867,30 @@ int32_t unp_lift_scan(const char* name, int32_t dtype, int32_t rank, int32_t op,
                       int32_t reverse, uint32_t block, uint32_t grid, char** json, unp_error* err) {
   return unp::lift_call(json, err, [&] {
     return unp::lift_scan(name ? name : "scan", dtype, rank, op, axis, exclusive != 0, reverse != 0, block, grid);
+  });
+}
+
+int32_t unp_lift_scan_x(const char* name, int32_t dtype, int32_t rank, int32_t op, int32_t axis, int32_t exclusive,
+                        int32_t reverse, int32_t n_inputs, const char* pre_json, const char* post_json, uint32_t block,
+                        uint32_t grid, char** json, unp_error* err) {
+  using unp::kir::J;
+  J pre, post;
+  std::string why;
+  if (n_inputs < 1 || n_inputs > 8) {
+    unp::set_error(err, UNP_INVALID_ARGUMENT, "a scan reads 1 to 8 inputs");
+    return UNP_INVALID_ARGUMENT;
+  }
+  if (!pre_json || !unp::kir::parse(pre_json, pre, why)) {
+    unp::set_error(err, UNP_PARSE_ERROR, "pre: a ScalarExpr expected " + why);
+    return UNP_PARSE_ERROR;
+  }
+  if (post_json && !unp::kir::parse(post_json, post, why)) {
+    unp::set_error(err, UNP_PARSE_ERROR, "post: a ScalarExpr expected " + why);
+    return UNP_PARSE_ERROR;
+  }
+  return unp::lift_call(json, err, [&] {
+    return unp::lift_scan(name ? name : "scan", dtype, rank, op, axis, exclusive != 0, reverse != 0, block, grid,
+                          (uint32_t)n_inputs, &pre, post_json ? &post : nullptr);
   });
 }
 

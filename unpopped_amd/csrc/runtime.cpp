@@ -203,6 +203,7 @@ int32_t unp_hip_lower_kernel(const char* kernel_json, unp_generated** out, unp_e
     }
   } else {
     rc = rec.form.kind == UNP_FORM_REDUCTION                       ? unp::lower_reduction_x(rec.form, rec.rx, g->l, why)
+         : rec.form.kind == UNP_FORM_SCAN                          ? unp::lower_scan_x(rec.form, rec.rx, g->l, why)
          : (rec.form.kind == UNP_FORM_GATHER && !rec.gx.plain) ? unp::lower_gather_x(rec.form, rec.gx, g->l, why)
                                                                : unp::lower_form(rec.form, g->l, why);
     if (rc != UNP_OK) {
@@ -904,7 +905,62 @@ int32_t run_reduction(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, un
   return launch(x, entry, grid, params, s, err);
 }
 
+// A scan with a pre-map body and a fused post: n inputs of one shape, then the output.
+int32_t run_xscan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  const unp_form& f = x->l.form;
+  const size_t NI = (size_t)x->l.rx.n_inputs;
+  Args A;
+  int32_t rc = take_args(a, n, NI + 1, (size_t)f.rank, A, err);
+  if (rc == UNP_OK) rc = extents_i32(A, (size_t)f.rank, err);
+  if (rc != UNP_OK) return rc;
+  std::vector<uint64_t> ptrs(A.buf.begin(), A.buf.end());
+  std::vector<void*> params;
+  for (size_t k = 0; k <= NI; ++k) params.push_back(&ptrs[k]);
+  const uint32_t grid = (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+  if (x->l.serial_scan) {
+    const size_t ax = (size_t)x->l.scan_axis;
+    long long a0 = product(A.ext, 0, ax), S = A.ext[ax], b0 = product(A.ext, ax + 1, (size_t)f.rank);
+    if ((rc = need_buffers(A, a0 > 0 && S > 0 && b0 > 0, err)) != UNP_OK) return rc;
+    if (a0 == 0 || S == 0 || b0 == 0) return UNP_OK;
+    params.push_back(&a0);
+    params.push_back(&S);
+    params.push_back(&b0);
+    return launch(x, 0, grid, params.data(), s, err);
+  }
+  long long rows = product(A.ext, 0, (size_t)f.rank - 1);
+  long long cols = A.ext[(size_t)f.rank - 1];
+  if ((rc = need_buffers(A, rows > 0 && cols > 0, err)) != UNP_OK) return rc;
+  if (rows == 0 || cols == 0) return UNP_OK;
+  const unp::Entry& en = x->l.entries[0];
+  const long long tile = 64LL * en.k * en.wpb;
+  const unsigned long long tiles = (unsigned long long)rows * (unsigned long long)((cols + tile - 1) / tile);
+  if (tiles + grid >= (1ull << 31)) {
+    set_error(err, UNP_INVALID_ARGUMENT, "too many scan tiles for one launch");
+    return UNP_INVALID_ARGUMENT;
+  }
+  Ws w;
+  if ((rc = workspace(x, (size_t)tiles * unp::kScanStatusWords * 8, true, 0, s, w, err)) != UNP_OK) return rc;
+  waits_host wt = waits_of(x);
+  uint32_t ep = 0;
+  if ((rc = next_epoch(x, s, ep, err)) != UNP_OK) return rc;
+  uint32_t tb = x->fixed ? 0 : x->ticket_base;
+  void* st = w.ws;
+  void* cnt = w.counter;
+  params.push_back(&rows);
+  params.push_back(&cols);
+  params.push_back(&st);
+  params.push_back(&cnt);
+  params.push_back(&tb);
+  params.push_back(&ep);
+  params.push_back(&wt);
+  rc = launch(x, 0, grid, params.data(), s, err);
+  // One ticket per tile, plus the one failing draw that ends each block.
+  if (rc == UNP_OK && !x->fixed) x->ticket_base = (uint32_t)(x->ticket_base + (uint32_t)(tiles + grid));
+  return rc;
+}
+
 int32_t run_scan(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  if (!x->l.rx.plain) return run_xscan(x, a, n, s, err);
   const unp_form& f = x->l.form;
   Args A;
   int32_t rc = take_args(a, n, 2, (size_t)f.rank, A, err);
@@ -1246,7 +1302,7 @@ void param_counts(const unp_exec* x, size_t& nbuf, size_t& nscal) {
   switch (f.kind) {
     case UNP_FORM_REDUCTION: nbuf = (size_t)x->l.rx.n_inputs + 1; nscal = (size_t)f.rank; break;
     case UNP_FORM_ROW_REDUCE2: nbuf = 3; nscal = 2; break;
-    case UNP_FORM_SCAN: nbuf = 2; nscal = (size_t)f.rank; break;
+    case UNP_FORM_SCAN: nbuf = (size_t)x->l.rx.n_inputs + 1; nscal = (size_t)f.rank; break;
     case UNP_FORM_GATHER: nbuf = (size_t)x->l.gx.n_inputs + 1; nscal = (size_t)f.rank + 1; break;
     case UNP_FORM_ROW_REDUCE: nbuf = (size_t)x->l.rr.n_inputs + 1; nscal = (size_t)x->l.rr.rank; break;
     case UNP_FORM_DEQUANT4: nbuf = 4; nscal = 2; break;
@@ -1301,8 +1357,7 @@ std::vector<Want> wanted_shapes(const unp_exec* x, const std::vector<int64_t>& e
       break;
     }
     case UNP_FORM_SCAN:
-      one(ext);
-      one(ext);
+      for (int32_t k = 0; k <= x->l.rx.n_inputs; ++k) one(ext);  // the inputs and the output
       break;
     case UNP_FORM_GATHER: {
       // The gathered input (data_slot) is the table; every other input, the index among them,
@@ -1628,10 +1683,11 @@ extern "C" int32_t unp_hip_exec_launch_views(unp_exec* x, const unp_view* views,
   // Some view is transposed, strided, reversed or broadcast: the forms with a strided entry read
   // through the strides; the others read dense storage only.
   const bool plain_reduction = (f.kind == UNP_FORM_REDUCTION && x->l.rx.plain) || f.kind == UNP_FORM_ROW_REDUCE2;
-  if (!plain_reduction && f.kind != UNP_FORM_SCAN && f.kind != UNP_FORM_GATHER)
+  const bool plain_scan = f.kind == UNP_FORM_SCAN && x->l.rx.plain;
+  if (!plain_reduction && !plain_scan && f.kind != UNP_FORM_GATHER)
     return invalid(err,
-                   "a view that is not dense row-major: this form reads dense storage (the plain reduction, scan "
-                   "and gather forms read any strides), so make the view contiguous first");
+                   "a view that is not dense row-major: this form reads dense storage (the plain reduction, plain "
+                   "scan and gather forms read any strides), so make the view contiguous first");
   const int32_t rc = begin_launch(x, err);
   if (rc != UNP_OK) return rc;
   hipStream_t s = (hipStream_t)stream;

@@ -134,7 +134,7 @@ struct Lowered {
   bool serial_scan = false;
   int32_t scan_axis = 0;
   RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only
-  ReductionExpr rx;  // UNP_FORM_REDUCTION: the body and post
+  ReductionExpr rx;  // UNP_FORM_REDUCTION and UNP_FORM_SCAN: the pre-map body and the post
   GatherExpr gx;     // UNP_FORM_GATHER: the inputs and body
 };
 
@@ -145,6 +145,7 @@ int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail);
 int32_t form_variants(const unp_form& f, std::vector<unp_variant>& out, std::string& detail);
 // A recognised reduction with its body and post (the plain ones go to lower_form).
 int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& out, std::string& detail);
+int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& out, std::string& detail);
 // A recognised gather with more inputs or a body (the plain ones go to lower_form).
 int32_t lower_gather_x(const unp_form& f, const GatherExpr& gx, Lowered& out, std::string& detail);
 // The same for a recognised Access::RowReduce.
@@ -156,7 +157,7 @@ int32_t lower_row_reduce(const RowReduceSpec& spec, Lowered& out, std::string& d
 struct Recognized {
   unp_form form{};
   RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only
-  ReductionExpr rx;  // UNP_FORM_REDUCTION only
+  ReductionExpr rx;  // UNP_FORM_REDUCTION and UNP_FORM_SCAN
   GatherExpr gx;     // UNP_FORM_GATHER only
   std::string lift;
   kir::J launch;

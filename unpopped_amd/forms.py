@@ -248,3 +248,34 @@ def row_reduce(inputs, stages, epilogue) -> np.ndarray:
     ex.launch(*dins, dout, *(x0.shape if x0.ndim else (1,)))
     u.synchronize()
     return dout.download(x0.dtype, x0.size).reshape(x0.shape)
+
+
+def scan_expr_executor(dtype: str, rank: int, op: str, axis: int, pre, post=None, n_inputs: int = 1,
+                       exclusive: bool = False, reverse: bool = False, launch=CALLER_LAUNCH) -> u.Executor:
+    """The scan lift with a pre-map and a fused post (launched on the innermost axis unless a Mean, a
+    float Prod or another axis makes it the serial lift), lowered, compiled and loaded."""
+    import json
+
+    from . import expr as X
+
+    serial = axis != rank - 1 or op in ("Mean", "Prod") or launch is None
+    key = ("scan_expr", dtype, rank, op, axis, n_inputs, exclusive, reverse, serial, json.dumps(X.as_json(pre)),
+           json.dumps(X.as_json(post)) if post is not None else None)
+    if key not in _execs:
+        k = u.lift_scan("scan", dtype, rank, op, axis=axis, exclusive=exclusive, reverse=reverse,
+                        launch=None if serial else launch, n_inputs=n_inputs, pre=pre, post=post)
+        _execs[key] = u.Executor(_backend.lower_kernel(k))
+    return _execs[key]
+
+
+def scan_expr(inputs, axis: int, op: str, pre, post=None, exclusive: bool = False, reverse: bool = False,
+              launch=CALLER_LAUNCH) -> np.ndarray:
+    """Scan `pre` over the inputs (one shape, float32/float64) along `axis`, then `post` per position."""
+    xs = [np.ascontiguousarray(a) for a in inputs]
+    x0 = xs[0]
+    ex = scan_expr_executor(NP_KIND[x0.dtype.type], x0.ndim, op, axis, pre, post, len(xs), exclusive, reverse, launch)
+    dins = [u.DeviceBuffer.from_array(a) for a in xs]
+    dout = u.DeviceBuffer(max(x0.nbytes, 1))
+    ex.launch(*dins, dout, *x0.shape)
+    ex.check()
+    return dout.download(x0.dtype, x0.size).reshape(x0.shape)
