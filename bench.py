@@ -391,10 +391,24 @@ extern "C" __global__ void __launch_bounds__(256) unp_ceiling_copy(const u32x4* 
 """
 
 
-def ceilings(u, cus: int, nbytes: int = 1 << 30, reps: int = 10) -> None:
-    """Streaming read / write / copy rates of this device on 1 GiB buffers (median of `reps`
-    launches, one block of 256 threads per CU per grid step): the practical ceilings that the
-    suite's kernels are read against, beside the 8 TB/s peak."""
+# Each suite kernel's own byte pattern and size: the ceiling it is read against.  The scans and the
+# gather read and write the same bytes (copy); the row reduce only reads; the dequant mostly writes.
+CEILING_SIZES = [
+    ("read", 1 << 30, "1 GiB"),
+    ("read", 128 << 20, "cfg2: 8192 x 4096 f32"),
+    ("write", 1 << 30, "1 GiB"),
+    ("write", 448 << 20, "cfg5's output: 8192 x 28672 bf16"),
+    ("copy", 1 << 30, "1 GiB, cfg3a: 2^28 i32"),
+    ("copy", 512 << 20, "cfg4: 65536 rows of 8 KiB"),
+    ("copy", 256 << 20, "cfg3b: 2^26 f32"),
+]
+
+
+def ceilings(u, cus: int, reps: int = 10) -> None:
+    """Streaming read / write / copy rates of this device (median of `reps` launches, the best of 1, 2
+    and 4 blocks of 256 threads per CU), on 1 GiB and at each suite kernel's own size: the practical
+    ceilings that the suite's kernels are read against, beside the 8 TB/s peak.  A copy of `size`
+    reads `size` bytes and writes `size` bytes."""
     import ctypes as C
 
     from unpopped_amd import _lib
@@ -409,13 +423,16 @@ def ceilings(u, cus: int, nbytes: int = 1 << 30, reps: int = 10) -> None:
         f = C.c_void_p()
         _lib.check(L.unp_hip_get_function(m, name.encode(), C.byref(f), C.byref(err)), err)
         fns[name] = f
-    a, b, sink = u.DeviceBuffer(nbytes), u.DeviceBuffer(nbytes), u.DeviceBuffer(64)
+    big = max(size for _, size, _ in CEILING_SIZES)
+    a, b, sink = u.DeviceBuffer(big), u.DeviceBuffer(big), u.DeviceBuffer(64)
     a.fill(1)
-    n = nbytes // 16
-    cases = [("read", "unp_ceiling_read", (a.ptr, sink.ptr, n), nbytes),
-             ("write", "unp_ceiling_write", (b.ptr, n), nbytes),
-             ("copy", "unp_ceiling_copy", (a.ptr, b.ptr, n), 2 * nbytes)]
-    for label, name, vals, moved in cases:
+    for label, size, what in CEILING_SIZES:
+        n = size // 16
+        name, vals, moved = {
+            "read": ("unp_ceiling_read", (a.ptr, sink.ptr, n), size),
+            "write": ("unp_ceiling_write", (b.ptr, n), size),
+            "copy": ("unp_ceiling_copy", (a.ptr, b.ptr, n), 2 * size),
+        }[label]
         args = (C.c_uint64 * len(vals))(*vals)
         best = None
         for bpc in (1, 2, 4):
@@ -431,11 +448,12 @@ def ceilings(u, cus: int, nbytes: int = 1 << 30, reps: int = 10) -> None:
                     ts.append(e0.elapsed_ms(e1))
             ms = float(np.median(ts))
             gbps = moved / (ms * 1e-3) / 1e9
-            log(f"[bench] ceiling {label}: {cus * bpc} blocks, {ms * 1e3:.1f} us, {gbps:.0f} GB/s")
+            log(f"[bench] ceiling {label} {size} B: {cus * bpc} blocks, {ms * 1e3:.1f} us, {gbps:.0f} GB/s")
             if best is None or gbps > best[0]:
                 best = (gbps, cus * bpc, ms)
-        print(json.dumps({"ceiling": label, "bytes": moved, "blocks": best[1], "us": round(best[2] * 1e3, 1),
-                          "GBps": round(best[0], 1), "frac_of_peak": round(best[0] / PEAK_GBPS, 4)}), flush=True)
+        print(json.dumps({"ceiling": label, "size": size, "what": what, "bytes": moved, "blocks": best[1],
+                          "us": round(best[2] * 1e3, 1), "GBps": round(best[0], 1),
+                          "frac_of_peak": round(best[0] / PEAK_GBPS, 4)}), flush=True)
 
 
 FLUSH_SRC = r"""
@@ -543,6 +561,86 @@ def attach_traffic(per, cases) -> None:
             p["traffic_source"] = f"profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; revision {rev})"
 
 
+def _pmc_dispatches(d: Path, counter: str) -> list:
+    """(kernel name, value) of every dispatch in one rocprofv3 --pmc pass under `d`, in dispatch order."""
+    import csv
+
+    files = sorted(d.rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                if r["Counter_Name"] == counter:
+                    name = r["Kernel_Name"].strip()
+                    name = name[:-3] if name.endswith(".kd") else name
+                    rows.append((int(r["Dispatch_Id"]), name, float(r["Counter_Value"])))
+    rows.sort()
+    return [(k, v) for _, k, v in rows]
+
+
+def _bench_line(path: Path) -> dict:
+    for line in reversed(path.read_text().splitlines()):
+        if line.startswith('{"metric"'):
+            return json.loads(line)
+    raise SystemExit(f"no bench JSON line in {path}")
+
+
+def _per_case(dispatches: list, line: dict) -> dict:
+    """Mean counter value per case.  The suite launches each case `warmup` times in order, then one
+    launch per case per step; the extra lines follow the same pattern.  A kernel that several cases
+    share (the gather: cfg4u, cfg4z) is split by that order."""
+    W, S = line["warmup"], line["steps"]
+    order: dict = {}
+    for group in (line["config"]["kernels"], line.get("extra_kernels") or []):
+        names = {}
+        for k in group:
+            names.setdefault(k["entry"], []).append(k["name"])
+        for entry, cs in names.items():
+            order.setdefault(entry, []).extend([c for c in cs for _ in range(W)] + cs * S)
+    seen: dict = {}
+    for name, v in dispatches:
+        seen.setdefault(name, []).append(v)
+    out: dict = {}
+    for entry, cs in order.items():
+        vals = seen.get(entry, [])
+        if len(vals) != len(cs):
+            log(f"[traffic] {entry}: {len(vals)} dispatches, expected {len(cs)}: skipped")
+            continue
+        for c, v in zip(cs, vals):
+            out.setdefault(c, []).append(v)
+    return {c: float(np.mean(v)) for c, v in out.items()}
+
+
+def assemble_traffic(d: Path) -> None:
+    """Writes profiles/traffic.json from four rocprofv3 --pmc passes under `d` (fetch/, write/: the
+    bench; cfetch/, cwrite/: the plain 256 MiB copy of --copy-probe) and the bench's JSON lines
+    (fetch.json, write.json: the stdout of the two bench passes).  FETCH_SIZE and WRITE_SIZE are KiB
+    per dispatch; each is scaled by what it reads for the copy of known size.  Every case carries the
+    source revision of the kernel that ran, so bench.py attaches the figure only to that kernel."""
+    fl, wl = _bench_line(d / "fetch.json"), _bench_line(d / "write.json")
+    kernels = {k["name"]: k for k in fl["config"]["kernels"] + (fl.get("extra_kernels") or [])}
+    wrev = {k["name"]: k.get("revision") for k in wl["config"]["kernels"] + (wl.get("extra_kernels") or [])}
+    probe_kib = (256 << 20) / 1024
+    cf = [v for k, v in _pmc_dispatches(d / "cfetch", "FETCH_SIZE") if k == "unp_copy_probe"]
+    cw = [v for k, v in _pmc_dispatches(d / "cwrite", "WRITE_SIZE") if k == "unp_copy_probe"]
+    fscale, wscale = probe_kib / float(np.mean(cf)), probe_kib / float(np.mean(cw))
+    fetch = _per_case(_pmc_dispatches(d / "fetch", "FETCH_SIZE"), fl)
+    write = _per_case(_pmc_dispatches(d / "write", "WRITE_SIZE"), wl)
+    cases = {}
+    for name, k in kernels.items():
+        if name not in fetch or name not in write or wrev.get(name) != k.get("revision"):
+            continue
+        fb, wb = fetch[name] * 1024 * fscale, write[name] * 1024 * wscale
+        cases[name] = {"kernel": k["entry"], "revision": k.get("revision"), "fetch_bytes": round(fb),
+                       "write_bytes": round(wb), "traffic_bytes": round(fb + wb), "algorithmic_bytes": k["bytes"],
+                       "ratio": round((fb + wb) / k["bytes"], 4)}
+        log(f"[traffic] {name}: fetch {fb / 1e6:.1f} MB, write {wb / 1e6:.1f} MB, ratio {(fb + wb) / k['bytes']:.4f}")
+    out = {"fetch_scale": round(fscale, 4), "write_scale": round(wscale, 4), "cases": cases}
+    (ROOT / "profiles" / "traffic.json").write_text(json.dumps(out, indent=1) + "\n")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -555,11 +653,16 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true",
                     help="only launch a plain 256 MiB copy (calibrates the HBM byte counters)")
     ap.add_argument("--ceilings", action="store_true",
-                    help="only measure this device's streaming read / write / copy rates on 1 GiB")
+                    help="only measure this device's streaming read / write / copy rates, on 1 GiB and at each suite kernel's size")
     ap.add_argument("--gemm", action="store_true",
                     help="only time the dequantizing GEMM at LLM shapes (one JSON line per shape)")
     ap.add_argument("--gemm-shapes", default="", help='with --gemm: only these "I8:16,I32:1024" (activation:C) pairs')
+    ap.add_argument("--traffic-from", default="",
+                    help="write profiles/traffic.json from the rocprofv3 --pmc passes under this folder (no GPU)")
     args = ap.parse_args()
+    if args.traffic_from:
+        assemble_traffic(Path(args.traffic_from))
+        return 0
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         return 2
