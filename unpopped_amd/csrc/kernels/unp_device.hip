@@ -1141,8 +1141,26 @@ template <class A, int SP = 0> struct tile_status {
 // probes of all P are in flight together); the walk stops at the first inclusive prefix.
 // A lane whose tile stays unpublished past the wait bound takes it as an inclusive identity,
 // which ends the walk (the stall is counted; the result is then not the prefix).
-template <class A, int OP, int P = 1, int SP = 0>
-UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch, const waits& wt) {
+//
+// The walk is split in two: lookback_issue loads the first P windows' words and returns at
+// once; lookback_finish decodes them and walks on.  A caller that has other work puts it
+// between the two, so the first round trip overlaps it; lookback does both back to back.
+// Lanes before the row's first tile read the current tile's own words (a valid address) and
+// take the identity.
+template <class A, int P, int SP>
+UNP_DEV void lookback_issue(const u64* st, u64 tile, i64 j, int lane,
+                            u64 (&w)[P][tile_status<A, SP>::W]) {
+  typedef tile_status<A, SP> S;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const i64 pj = j - 1 - lane - 64 * p;
+    S::fetch(st, pj >= 0 ? tile - (u64)(j - pj) : tile, w[p]);
+  }
+}
+
+template <class A, int OP, int P, int SP>
+UNP_DEV A lookback_finish(const u64* st, u64 tile, i64 j, int lane, u32 epoch, const waits& wt,
+                          u64 (&w)[P][tile_status<A, SP>::W]) {
   typedef fold<A, OP> F;
   typedef tile_status<A, SP> S;
   const A I = F::identity();
@@ -1151,14 +1169,6 @@ UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch, const wa
   for (;;) {
     A v[P];
     int state[P];
-    u64 w[P][S::W];
-    // Issue every probe of the P windows before decoding any: lanes before the row's first
-    // tile read the current tile's own words (a valid address) and take the identity.
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const i64 pj = near - 64 * p;
-      S::fetch(st, pj >= 0 ? tile - (u64)(j - pj) : tile, w[p]);
-    }
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const i64 pj = near - 64 * p;
@@ -1188,7 +1198,19 @@ UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch, const wa
       if (incl) return excl;
     }
     near -= 64 * P;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const i64 pj = near - 64 * p;
+      S::fetch(st, pj >= 0 ? tile - (u64)(j - pj) : tile, w[p]);
+    }
   }
+}
+
+template <class A, int OP, int P = 1, int SP = 0>
+UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch, const waits& wt) {
+  u64 w[P][tile_status<A, SP>::W];
+  lookback_issue<A, P, SP>(st, tile, j, lane, w);
+  return lookback_finish<A, OP, P, SP>(st, tile, j, lane, epoch, wt, w);
 }
 
 // One wave's tile: load, tile-local scan, publish, look back, store.
@@ -1630,6 +1652,14 @@ UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows
     T* __restrict__ rout = out + row * cols;
 
     const bool full = p0 + WT <= cols;  // uniform per wave
+    // With a 4-byte carry, wave 0 issues its look-back's first probes (four windows: a round of
+    // tiles back) before the in-tile scan, so their round trip overlaps the scan.  An 8-byte
+    // carry's probes would hold 16 more VGPRs across the scan, which then spills (measured
+    // slower), so it looks back after the scan.
+    constexpr int LP = sizeof(A) == 4 ? 4 : 1;
+    constexpr bool EARLY = sizeof(A) == 4;
+    u64 lw[LP][S::W];
+    if (EARLY && wave == 0 && j > 0) lookback_issue<A, LP, SP>(st, g, j, lane, lw);
     vec<T, VEC> x[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -1659,7 +1689,8 @@ UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows
         A agg = wagg[r & 1][0];
 #pragma unroll
         for (int w = 1; w < NC; ++w) agg = F::apply(agg, wagg[r & 1][w]);
-        gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch, wt);
+        if constexpr (EARLY) gex = lookback_finish<A, OP, LP, SP>(st, g, j, lane, epoch, wt, lw);
+        else gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch, wt);
         if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
       }
       if (lane == 0) {
