@@ -275,24 +275,35 @@ template <class A, int OP> UNP_DEV A row_inclusive_scan(A x) {
   return x;
 }
 
+// Wait states between an 8-byte VALU result and a v_readlane of it.  On gfx950 a v_readlane
+// issued one wait state after a v_add_f64 (all the compiler puts there) has returned the
+// register's value from before the add: a wave scan's row totals, read at lanes 15/31/47/63,
+// then lacked the last DPP steps.  The asm takes and returns the value, so its nops sit after
+// the value's producer and before every reader.  4-byte values are not affected.
+template <class X> UNP_DEV X settle(X x) {
+  if constexpr (sizeof(X) == 8) asm volatile("s_nop 4" : "+v"(x));
+  return x;
+}
+
 // The fold of all 64 lanes, the same value in every lane.
 template <class A, int OP> UNP_DEV A wave_reduce(A x) {
   typedef fold<A, OP> F;
-  x = row_inclusive_scan<A, OP>(x);
+  x = settle(row_inclusive_scan<A, OP>(x));
   return F::apply(F::apply(F::apply(readlane(x, 15), readlane(x, 31)), readlane(x, 47)),
                   readlane(x, 63));
 }
 
-// Inclusive scan over the 64 lanes (lane order = fold order).
+// Inclusive scan over the 64 lanes (lane order = fold order).  The result is settled, so a
+// caller may read it with readlane at once.
 template <class A, int OP> UNP_DEV A wave_inclusive_scan(A x, int lane) {
   typedef fold<A, OP> F;
-  x = row_inclusive_scan<A, OP>(x);
+  x = settle(row_inclusive_scan<A, OP>(x));
   const A r0 = readlane(x, 15);
   const A r01 = F::apply(r0, readlane(x, 31));
   const A r012 = F::apply(r01, readlane(x, 47));
   const int row = lane >> 4;
   const A pre = row == 1 ? r0 : (row == 2 ? r01 : r012);
-  return row == 0 ? x : F::apply(pre, x);
+  return settle(row == 0 ? x : F::apply(pre, x));
 }
 
 // Lane l receives lane l-1's value; lane 0 receives `fill`.
