@@ -155,6 +155,16 @@ def build_extras(u, synth):
         return lambda: ex.launch(din, dout, n), ex
     extras.append(Case("rd_all", "f32 2^24 full Sum (cfg1's data on the GPU; cfg1 itself is the CPU case)",
                        (1 << 24) * 4 + 4, 1 << 24, full_sum))
+    def scan_fixed():
+        # cfg3b on the fixed schedule: the same launch with the look-back's association fixed by the
+        # tiling, so the f32 result has the same bits on every launch.
+        n = 1 << 26
+        x = synth.uniform_01_f32(2, n)
+        ex = u.Executor(u.HipBackend().lower_form("scan", "F32", 1, "Sum", schedule="fixed"))
+        din, dout = u.DeviceBuffer.from_array(x), u.DeviceBuffer(n * 4)
+        return lambda: ex.launch(din, dout, n), ex
+    extras.append(Case("cfg3b_fixed", "f32 inclusive sum scan 2^26 on the fixed schedule (reproducible bits)",
+                       2 * (1 << 26) * 4, 1 << 26, scan_fixed))
     rr_bytes = 2 * 8192 * 4096 * 4
     extras.append(Case("rr_softmax", "f32 8192x4096 RowReduce softmax (Max, Sum of exp, divide)", rr_bytes,
                        8192 * 4096, row_reduce("softmax")))

@@ -129,9 +129,14 @@ enum unp_oob_policy { UNP_OOB_SKIP = 0, UNP_OOB_ZEROFILL = 1, UNP_OOB_CLAMP = 2 
 /* The schedule a form lowers to.  SERIAL is the serial lift's own order (one lane per output of a
  * reduction, per column of a scan): the bits of the sequential fold the reference's
  * Schedule::Reduction and Schedule::Scan { block: false } name (plan/types.rs:30-75).  DEVICE is
- * this backend's device-class schedule.  Forms whose every schedule gives the same bits (the
- * gather, the dequants, integer folds) lower the same kernels either way. */
-enum unp_schedule { UNP_SCHEDULE_DEVICE = 0, UNP_SCHEDULE_SERIAL = 1 };
+ * this backend's device-class schedule.  FIXED is the device schedule with every float
+ * association fixed by the launch's tiling, so a float result is the same on every launch (the
+ * reference's launched lifts fix theirs by geometry, kernel_lift/scan_launched.rs:19-26): a
+ * float scan's look-back folds tile aggregates in a fixed grouping; a scan with a pre-map runs
+ * its serial entry; every other form's device schedule is already fixed and lowers unchanged.
+ * Forms whose every schedule gives the same bits (the gather, the dequants, integer folds)
+ * lower the same kernels whichever is asked. */
+enum unp_schedule { UNP_SCHEDULE_DEVICE = 0, UNP_SCHEDULE_SERIAL = 1, UNP_SCHEDULE_FIXED = 2 };
 /* VariantFidelity (backend.rs:204-309) in declaration order: a variant's bits against the cell's
  * default lowering (here the SERIAL schedule, the sequential fold's bits). */
 enum unp_fidelity {

@@ -861,7 +861,8 @@ def test_form_variants_name_the_schedules_and_their_fidelity():
     """Each cell's default is the serial schedule (the sequential fold's bits); the device schedule
     follows with its honest fidelity: bit-identical for integer folds, deterministically divergent for a
     float reduction (a fixed device order), nondeterministic for a float look-back scan (the carry's
-    association depends on timing).  Forms whose schedules agree list one."""
+    association depends on timing), which also lists the fixed schedule (the look-back's association
+    fixed by the tiling).  Forms whose schedules agree list one."""
     b = u.HipBackend()
 
     def summary(**form):
@@ -873,7 +874,8 @@ def test_form_variants_name_the_schedules_and_their_fidelity():
         ("serial", "BitIdentical", "serial"), ("device", "BitIdentical", "device")]
     assert summary(kind="reduction", dtype="F32", rank=2, op="Prod", axes=(1,)) == [("serial", "BitIdentical", "serial")]
     assert summary(kind="scan", dtype="F32", rank=1, op="Sum") == [
-        ("serial", "BitIdentical", "serial"), ("device", "Nondeterministic", "device")]
+        ("serial", "BitIdentical", "serial"), ("device", "Nondeterministic", "device"),
+        ("fixed", "DeterministicallyDivergent", "fixed")]
     assert summary(kind="scan", dtype="I32", rank=1, op="Sum") == [
         ("serial", "BitIdentical", "serial"), ("device", "BitIdentical", "device")]
     assert summary(kind="scan", dtype="F64", rank=2, op="Sum", axes=(0,)) == [("serial", "BitIdentical", "serial")]
@@ -887,6 +889,22 @@ def test_form_variants_name_the_schedules_and_their_fidelity():
     with pytest.raises(_lib.UnpError) as e:
         b.form_variants(kind="reduction", dtype="F32", rank=2, op="Xor")
     assert e.value.kind == "UnsupportedOp" or e.value.kind == "UnsupportedKernel"
+
+
+def test_fixed_schedule_lowers_a_float_scan_apart_and_other_forms_unchanged():
+    """The fixed schedule changes only a float scan's look-back (the unp_scan_fix_ entries, fidelity
+    notes saying so); forms whose device schedule is already fixed lower the same source on it."""
+    b = u.HipBackend()
+    g = b.lower_form("scan", "F32", 1, "Sum", schedule="fixed")
+    assert g.name == "unp_scan_fix_incl_sum_f32" and g.interface["schedule"] == "fixed"
+    assert "same bits on every launch" in g.interface["fidelity_notes"][0]
+    flag = ", true>(in, out, rows, cols"  # the scan templates' FIXED argument
+    assert g.source.count(flag) == 2  # the staged and the register entry
+    assert flag not in b.lower_form("scan", "F32", 1, "Sum").source
+    for form in (dict(kind="reduction", dtype="F32", rank=2, op="Sum", axes=(1,)),
+                 dict(kind="scan", dtype="I32", rank=1, op="Sum"),
+                 dict(kind="gather", dtype="Bf16", rank=2)):
+        assert b.lower_form(schedule="fixed", **form).source == b.lower_form(**form).source, form
 
 
 def test_schedules_a_form_does_not_have_are_refused():

@@ -1608,6 +1608,90 @@ def test_serial_scan_schedule_is_the_serial_lift_bit_for_bit(hip_device, dtype, 
 
 
 # ---------------------------------------------------------------------------------------
+# The fixed schedule: the device launch with a float look-back's association fixed by the
+# tiling (tiles in groups of 64 per row): the same bits on every launch
+# ---------------------------------------------------------------------------------------
+
+_fixed_execs: dict = {}
+# Block tiles of an 8-byte carry (an f32 Sum folds in f64): the staged entry's 4 waves x 64 lanes x
+# 4 x 18 elements, the register entry's 16 waves x 64 lanes x 16.
+_TILE_V, _TILE_S = 4 * 64 * 4 * 18, 16 * 64 * 16
+
+
+def _fixed_scan(x: np.ndarray, op: str, exclusive=False, reverse=False):
+    rows, cols = x.shape
+    form = dict(kind="scan", dtype=H.NP_KIND[x.dtype.type], rank=2, op=op, exclusive=exclusive, reverse=reverse)
+    key = tuple(sorted(form.items()))
+    if key not in _fixed_execs:
+        _fixed_execs[key] = u.Executor(u.HipBackend().lower_form(schedule="fixed", **form))
+    ex = _fixed_execs[key]
+    din, dout = u.DeviceBuffer.from_array(x), u.DeviceBuffer(max(x.nbytes, 1))
+    ex.launch(din, dout, rows, cols)
+    ex.check()
+    return dout.download(x.dtype, x.size).reshape(x.shape), ex.last_launch()["entry"]
+
+
+@pytest.mark.parametrize("shape,entry", [
+    ((1, 64 * _TILE_V), "_v"),            # exactly one group: the next tile would start group 1
+    ((1, 130 * _TILE_V), "_v"),           # groups 0..2 of the staged entry
+    ((3, 66 * _TILE_V), "_v"),            # several rows, each with its own groups
+    ((1, 129 * _TILE_S + 3), "_s"),       # the register entry (rows not a multiple of 4)
+    ((2, 70 * _TILE_S + 1), "_s"),
+])
+@pytest.mark.parametrize("exclusive,reverse", [(False, False), (True, True)])
+def test_fixed_scan_schedule_dyadic_bit_exact(hip_device, shape, entry, exclusive, reverse):
+    """On the fixed schedule, dyadic data (every f64 partial exact) give RN32 of the exact prefix: the
+    oracle's bits, through the staged and the register entry, across group boundaries and rows."""
+    H.say(f"[case] fixed scan f32 Sum dyadic {shape} excl={exclusive} rev={reverse}")
+    x = synth.uniform_01_f32(31, shape[0] * shape[1]).reshape(shape)
+    got, ran = _fixed_scan(x, "Sum", exclusive, reverse)
+    assert ran.endswith(entry), ran
+    assert got.tobytes() == oracle.scan_rows(x, "Sum", exclusive, reverse).tobytes()
+
+
+@pytest.mark.parametrize("n", [1 << 24, (1 << 24) - 3])
+def test_fixed_scan_schedule_repeats_bit_for_bit(hip_device, n):
+    """Normal data, where every association rounds differently: eight launches (four on the register
+    entry) give the same bits, each within the declared per-prefix bound of the serial lift's f64 scan
+    (kernel_parallel_scan_agrees.rs:287-300)."""
+    H.say(f"[case] fixed scan f32 Sum normal n={n}, repeated launches")
+    x = rng(63).normal(size=(1, n)).astype(np.float32)
+    want = oracle.scan_rows(x, "Sum").ravel().astype(np.float64)
+    xs = x.ravel().astype(np.float64)
+    u53 = 2.0 ** -53
+    k = np.arange(n, dtype=np.float64)
+    bound = 2 * (k * u53 / (1 - k * u53)) * np.cumsum(np.abs(xs))
+    first, ran = _fixed_scan(x, "Sum")
+    assert ran.endswith("_v" if n % 4 == 0 else "_s"), ran
+    g = first.ravel()
+    assert np.all(np.abs(g.astype(np.float64) - want) <= bound + np.spacing(np.abs(g)).astype(np.float64))
+    for _ in range(7 if n % 4 == 0 else 3):
+        assert _fixed_scan(x, "Sum")[0].tobytes() == first.tobytes()
+
+
+@pytest.mark.parametrize("op", ["Max", "Min"])
+def test_fixed_scan_schedule_extremum(hip_device, op):
+    """Max/Min with NaN and infinities on the fixed schedule: the oracle's values (NaN wherever it has
+    NaN), and the same bits on a second launch."""
+    H.say(f"[case] fixed scan f32 {op} with NaN/inf")
+    x = rng(64).normal(size=(2, 70 * _TILE_V)).astype(np.float32)
+    x[0, 3 * _TILE_V + 17] = np.nan
+    x[1, 10] = np.inf
+    x[1, 65 * _TILE_V] = -np.inf
+    got, _ = _fixed_scan(x, op)
+    assert equal_extremum(got, oracle.scan_rows(x, op))
+    assert _fixed_scan(x, op)[0].tobytes() == got.tobytes()
+
+
+def test_fixed_scan_schedule_config3b_full(hip_device):
+    H.say("[case] config 3b on the fixed schedule: f32 inclusive scan 2^26")
+    n = 1 << 26
+    x = synth.uniform_01_f32(2, n).reshape(1, n)
+    got, _ = _fixed_scan(x, "Sum")
+    assert got.tobytes() == oracle.scan_rows(x, "Sum").tobytes()
+
+
+# ---------------------------------------------------------------------------------------
 # The gather lift in general: n inputs, the index and the gathered one anywhere, a body
 # (kernel_lift/gather.rs:35-101)
 # ---------------------------------------------------------------------------------------

@@ -31,7 +31,7 @@ ELEMENT_KINDS = {
 REDUCE_OPS = {"Sum": 0, "Prod": 1, "Max": 2, "Min": 3, "Mean": 4, "And": 5, "Or": 6, "Xor": 7, "MaxNum": 8,
               "MinNum": 9}
 OOB_POLICIES = {"Skip": 0, "ZeroFill": 1, "Clamp": 2}
-SCHEDULES = {"device": 0, "serial": 1}
+SCHEDULES = {"device": 0, "serial": 1, "fixed": 2}
 # VariantFidelity (backend.rs:204-309), in declaration order.
 FIDELITIES = ["BitIdentical", "DeterministicallyDivergent", "Nondeterministic", "MorePrecise"]
 FORMS = {"reduction": 0, "scan": 1, "gather": 2, "dequant4": 3, "row_reduce2": 4, "row_reduce": 5, "dequant_gemm": 6}
@@ -80,7 +80,8 @@ class HipBackend:
                    data_slot: int = 0, q_kind: str = "U4", z_kind: str = "U4", group: int = 128,
                    out_kind: str = "Bf16", axes: tuple | None = None, schedule: str = "device") -> GeneratedKernel:
         """Lower one form (``unp_hip_lower_form``); ``schedule`` is ``"device"`` (this backend's
-        device-class schedule) or ``"serial"`` (the serial lift's own order)."""
+        device-class schedule), ``"serial"`` (the serial lift's own order) or ``"fixed"`` (the device
+        schedule with every float association fixed by the tiling: the same bits on every launch)."""
         return self._wrap(lambda out, err: _lib.lib().unp_hip_lower_form(
             C.byref(self.form(kind, dtype, rank, op, op1, reduced_from, exclusive, reverse, index_dtype, oob,
                               data_slot, q_kind, z_kind, group, out_kind, axes, schedule)), out, err))

@@ -452,10 +452,14 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
                       f.schedule == UNP_SCHEDULE_SERIAL;
   L.serial_scan = serial;
   L.scan_axis = axis;
+  // The fixed schedule: a float fold's look-back combines tile aggregates in an association the
+  // tiling alone fixes (lookback_grouped), so every launch gives the same bits.  An integer fold
+  // gives the same bits in any order: its fixed schedule is the device schedule.
+  const bool fixed = !serial && f.schedule == UNP_SCHEDULE_FIXED && kind_is_float(f.dtype);
   const char* T = ctype(f.dtype);
   std::ostringstream name;
-  name << "unp_scan_" << (serial ? "seq_" : "") << (f.exclusive ? "excl_" : "incl_") << (f.reverse ? "rev_" : "")
-       << op_name(f.op0) << "_" << lower_name(f.dtype);
+  name << "unp_scan_" << (serial ? "seq_" : fixed ? "fix_" : "") << (f.exclusive ? "excl_" : "incl_")
+       << (f.reverse ? "rev_" : "") << op_name(f.op0) << "_" << lower_name(f.dtype);
   L.name = name.str();
   if (serial) {
     Entry e;
@@ -517,7 +521,7 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
         << "* in, " << T << "* out, long long rows, long long cols, unsigned long long* status, "
         << "unsigned* counter, unsigned ticket_base, unsigned epoch, unp::waits wt) {\n  unp::scan_staged<" << T << ", " << f.op0
         << ", " << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false") << ", " << e.vec << ", "
-        << e.k << ", " << e.wpb << ", " << kScanStatusWords
+        << e.k << ", " << e.wpb << ", " << kScanStatusWords << (fixed ? ", true" : "")
         << ">(in, out, rows, cols, status, counter, ticket_base, epoch, wt);\n}\n";
     L.entries.push_back(e);
   }
@@ -534,7 +538,7 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
         << "* in, " << T << "* out, long long rows, long long cols, unsigned long long* status, "
         << "unsigned* counter, unsigned ticket_base, unsigned epoch, unp::waits wt) {\n  unp::scan_lookback<" << T << ", " << f.op0
         << ", " << (f.exclusive ? "true" : "false") << ", " << (f.reverse ? "true" : "false") << ", 1, " << e.k
-        << ", " << e.wpb << ", " << kScanStatusWords
+        << ", " << e.wpb << ", " << kScanStatusWords << (fixed ? ", true" : "")
         << ">(in, out, rows, cols, status, counter, ticket_base, epoch, wt);\n}\n";
     L.entries.push_back(e);
   }
@@ -546,6 +550,7 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
   j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"scan\",\"dtype\":\"" << kind_name(f.dtype)
     << "\",\"op\":\"" << op_name(f.op0) << "\",\"exclusive\":" << (f.exclusive ? "true" : "false")
     << ",\"reverse\":" << (f.reverse ? "true" : "false") << ",\"rank\":" << f.rank
+    << ",\"schedule\":\"" << (fixed ? "fixed" : "device") << "\""
     << ",\"params\":[{\"name\":\"in0\",\"kind\":\"buffer\",\"role\":\"Read\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
   for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
   j << "],\"launch\":{\"block\":[" << L.threads << ",1,1],\"grid\":\"cu_count*" << L.blocks_per_cu
@@ -563,7 +568,13 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     << " bytes, zeroed once\",\"counter\":4,\"stall\":4,\"host_state\":[\"epoch\",\"ticket_base\"]}"
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["
-    << json_str(kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN)
+    << json_str(fixed
+                    ? "fixed schedule: a tile's carry is G(k-1) folded with the wave-tree prefix of its group's earlier tile "
+                      "aggregates (groups of 64 tiles per row, G(k) = G(k-1) folded with the group's wave-tree total), an "
+                      "association the tile size alone fixes: the same bits on every launch and any grid. Float Sum / Mean "
+                      "fold in f64 within the declared per-prefix bound gamma_(n-1)*sum|x| + 1/2 ulp; Max/Min keep one NaN "
+                      "payload and zero sign launch to launch"
+                : kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN)
                     ? "float Sum / Mean: every prefix is an f64 fold of the same elements in a different order (tile-local "
                       "striped scan plus decoupled look-back; a Mean divides it by the count once); within the declared "
                       "per-prefix bound gamma_(n-1)*sum|x| + 1/2 ulp; bit-equal whenever the f64 partial sums are exact. "
@@ -1523,8 +1534,10 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std
     }
     axis = __builtin_ctz(f.axes_mask);
   }
+  // The fixed schedule of a scan with a pre-map runs the serial entry: the register look-back
+  // here has no fixed-association form.
   const bool serial = axis != f.rank - 1 || f.op0 == UNP_OP_PROD || f.op0 == UNP_OP_MEAN ||
-                      f.schedule == UNP_SCHEDULE_SERIAL;
+                      f.schedule == UNP_SCHEDULE_SERIAL || f.schedule == UNP_SCHEDULE_FIXED;
   L.serial_scan = serial;
   L.scan_axis = axis;
   const char* T = ctype(f.dtype);
@@ -1620,7 +1633,7 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std
 int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail) {
   out = Lowered{};
   out.form = f;
-  if (f.schedule != UNP_SCHEDULE_DEVICE && f.schedule != UNP_SCHEDULE_SERIAL) {
+  if (f.schedule != UNP_SCHEDULE_DEVICE && f.schedule != UNP_SCHEDULE_SERIAL && f.schedule != UNP_SCHEDULE_FIXED) {
     detail = "an unknown schedule";
     return UNP_UNSUPPORTED_SCHEDULE;
   }
@@ -1686,6 +1699,15 @@ int32_t form_variants(const unp_form& f, std::vector<unp_variant>& out, std::str
       add("device", fl ? UNP_NONDETERMINISTIC : UNP_BIT_IDENTICAL, dev,
           "one persistent block per CU drawing tile tickets; decoupled look-back over a tile-status "
           "workspace tagged with a launch epoch");
+      if (fl) {
+        // The same launch with the look-back's association fixed by the tiling: reproducible,
+        // in a different order from the serial fold.
+        unp_form fix = f;
+        fix.schedule = UNP_SCHEDULE_FIXED;
+        add("fixed", UNP_DETERMINISTICALLY_DIVERGENT, fix,
+            "as device, the look-back folding tile aggregates in groups of 64 tiles in a fixed "
+            "association: the same bits every launch");
+      }
     }
     return UNP_OK;
   }

@@ -1224,11 +1224,84 @@ UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch, const wa
   return lookback_finish<A, OP, P, SP>(st, tile, j, lane, epoch, wt, w);
 }
 
+// The look-back of a float fold, with an association fixed by the tiling alone.
+//
+// A row's tiles form groups of 64 (tile j is lane j % 64 of group j / 64).  Group k's total
+// G(k) = fold(G(k-1), reduce(group k's aggregates)), with G(-1) the identity and reduce the
+// wave's fixed DPP tree (wave_reduce, which is also lane 63 of wave_inclusive_scan).  The carry
+// into tile j is fold(G(k-1), scan(aggregates of tiles 64k .. j-1)), scan the same tree.  No
+// value depends on which block computes it or when, so the result bits are fixed for a given
+// tile size, whatever the grid and the timing.
+//
+// G(k) is published in the status slot of the group's last tile (flag 1, over its aggregate);
+// a row's first tile carries flag 1 too, where the aggregate is its own prefix.  The look-back
+// probes its group's earlier tiles (window a), the previous group (window b) and the slot of
+// G(k-2).  With G(k-1) published it is done; with G(k-2) (or k = 1) and window b complete it
+// computes G(k-1) and publishes it; otherwise it probes again (the lowest group without a total
+// gets one from its own last tile, whose look-back waits only on lower tiles).  The last tile of
+// a group publishes G(k) itself.  `agg` is this tile's aggregate.
+template <class A, int OP, int SP>
+UNP_DEV A lookback_grouped(u64* st, u64 g, i64 j, int lane, u32 epoch, const waits& wt, A agg) {
+  typedef fold<A, OP> F;
+  typedef tile_status<A, SP> S;
+  constexpr int W = S::W;
+  const A I = F::identity();
+  const i64 k = j >> 6;
+  const int q = (int)(j & 63);
+  const u64 row0 = g - (u64)j;  // status index of the row's first tile
+  // Window a: lane l < q reads tile 64k + l; window b: lane l reads tile 64(k-1) + l; every
+  // lane reads the slot of G(k-2).  Lanes with nothing to read take the tile's own slot.
+  const u64 ia = lane < q ? row0 + (u64)(64 * k + lane) : g;
+  const u64 ib = k >= 1 ? row0 + (u64)(64 * (k - 1) + lane) : g;
+  const u64 ic = k >= 2 ? row0 + (u64)(64 * (k - 2) + 63) : g;
+  const u64 t0 = wall_clock64();
+  for (;;) {
+    u64 wa[W], wb[W], wc[W];
+    S::fetch(st, ia, wa);
+    S::fetch(st, ib, wb);
+    S::fetch(st, ic, wc);
+    A va = I, vb = I, vc = I;
+    const int sa = lane < q ? S::decode(wa, epoch, va) : 1;
+    if (lane >= q) va = lane == 63 ? agg : I;
+    const int sb = k >= 1 ? S::decode(wb, epoch, vb) : 0;
+    const int sc = k >= 2 ? S::decode(wc, epoch, vc) : 2;
+    // Every earlier tile of the group has published (an aggregate; flag 1 only on a row's
+    // first tile, where it is the aggregate too).
+    bool ok = __ballot(sa == 0) == 0;
+    A gprev = I;
+    bool have_prev = k == 0;
+    if (ok && k >= 1) {
+      const int sb63 = __builtin_amdgcn_readlane(sb, 63);
+      if (sb63 == 2) {
+        gprev = readlane(vb, 63);  // G(k-1) published
+        have_prev = true;
+      } else if (__ballot(sb == 0) == 0 && sc == 2) {
+        // G(k-1) from G(k-2) (the identity for k = 1) and the previous group's aggregates.
+        const A gpp = k >= 2 ? vc : I;
+        gprev = F::apply(gpp, wave_reduce<A, OP>(vb));
+        if (lane == 0) S::publish(st, row0 + (u64)(64 * (k - 1) + 63), 1, gprev, epoch);
+        have_prev = true;
+      }
+    }
+    if (ok && have_prev) {
+      const A sc_a = wave_inclusive_scan<A, OP>(va, lane);
+      const A inner = q > 0 ? readlane(sc_a, q - 1) : I;
+      if (q == 63 && lane == 0) S::publish(st, g, 1, F::apply(gprev, readlane(sc_a, 63)), epoch);
+      return q > 0 ? F::apply(gprev, inner) : gprev;
+    }
+    if (wait_over(t0, wt)) {
+      if (lane == 0) note_stall(wt);
+      return I;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
 // One wave's tile: load, tile-local scan, publish, look back, store.
 // One block tile: every wave loads and scans its stripe set (WT = 64 * VEC * K positions),
 // the waves' aggregates are combined in LDS, wave 0 publishes the block tile's aggregate,
 // looks back and publishes its inclusive prefix, and every wave stores its prefixes.
-template <class T, int OP, bool EXCL, bool REV, int VEC, int K, int WPB, int SP>
+template <class T, int OP, bool EXCL, bool REV, int VEC, int K, int WPB, int SP, bool FIXED = false>
 UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
                            u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base,
                            u32 epoch, waits wt) {
@@ -1309,8 +1382,12 @@ UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 ro
         if (lane == 0) S::publish(st, g, 1, agg, epoch);
       } else {
         if (lane == 0) S::publish(st, g, 0, agg, epoch);
-        gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch, wt);
-        if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
+        if constexpr (FIXED && traits<A>::is_float) {
+          gex = lookback_grouped<A, OP, SP>(st, g, j, lane, epoch, wt, agg);
+        } else {
+          gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch, wt);
+          if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
+        }
       }
       if (lane == 0) {
         gbase = gex;
@@ -1557,7 +1634,7 @@ UNP_DEV void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <class T, int OP, bool EXCL, bool REV, int VEC, int K, int NC, int SP>
+template <class T, int OP, bool EXCL, bool REV, int VEC, int K, int NC, int SP, bool FIXED = false>
 UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
                          u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base,
                          u32 epoch, waits wt) {
@@ -1667,8 +1744,10 @@ UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows
     // tiles back) before the in-tile scan, so their round trip overlaps the scan.  An 8-byte
     // carry's probes would hold 16 more VGPRs across the scan, which then spills (measured
     // slower), so it looks back after the scan.
+    // FIXED: a float fold takes lookback_grouped, whose association the tiling alone fixes.
+    constexpr bool GROUPED = FIXED && traits<A>::is_float;
     constexpr int LP = sizeof(A) == 4 ? 4 : 1;
-    constexpr bool EARLY = sizeof(A) == 4;
+    constexpr bool EARLY = sizeof(A) == 4 && !GROUPED;
     u64 lw[LP][S::W];
     if (EARLY && wave == 0 && j > 0) lookback_issue<A, LP, SP>(st, g, j, lane, lw);
     vec<T, VEC> x[K];
@@ -1697,12 +1776,17 @@ UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows
     A gex = I;
     if (wave == 0) {
       if (j > 0) {
-        A agg = wagg[r & 1][0];
+        // The tile's aggregate, folded as the producer folded it.
+        A agg = I;
 #pragma unroll
-        for (int w = 1; w < NC; ++w) agg = F::apply(agg, wagg[r & 1][w]);
-        if constexpr (EARLY) gex = lookback_finish<A, OP, LP, SP>(st, g, j, lane, epoch, wt, lw);
-        else gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch, wt);
-        if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
+        for (int w = 0; w < NC; ++w) agg = F::apply(agg, wagg[r & 1][w]);
+        if constexpr (GROUPED) {
+          gex = lookback_grouped<A, OP, SP>(st, g, j, lane, epoch, wt, agg);
+        } else {
+          if constexpr (EARLY) gex = lookback_finish<A, OP, LP, SP>(st, g, j, lane, epoch, wt, lw);
+          else gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch, wt);
+          if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
+        }
       }
       if (lane == 0) {
         gbase = gex;
