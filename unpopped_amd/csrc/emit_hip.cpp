@@ -1083,6 +1083,18 @@ bool costly(const kir::J& e) {
   return false;
 }
 
+// True when the expression node `tag` occurs anywhere in `e`.
+bool mentions(const kir::J& e, const char* tag) {
+  using kir::J;
+  if (e.t == J::Obj)
+    for (const auto& kv : e.o)
+      if (kv.first == tag || mentions(kv.second, tag)) return true;
+  if (e.t == J::Arr)
+    for (const J& x : e.a)
+      if (mentions(x, tag)) return true;
+  return false;
+}
+
 // True when `sub` occurs in `e` as a subtree.
 bool contains(const kir::J& e, const kir::J& sub) {
   using kir::J;
@@ -1275,6 +1287,30 @@ int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) 
       }
       cached = (int)st;
     }
+  // An f32 epilogue that is a quotient by a row value and reuses a costly stage value (softmax's
+  // exp(x - max) / sum, whose per-element f64 work bounds the kernel rather than HBM): the
+  // element multiplies by the row's reciprocal, which the compiler computes once per row, in
+  // place of an IEEE f64 division per element.  A memory-bound quotient (RMS norm, a centred
+  // quotient) keeps its division: the rewrite would buy it no time.  x * (1 / s) is within 2^-52 of x / s, so after the
+  // one rounding to f32 the output is the quotient's or its neighbour (1 ulp, only where the
+  // quotient lies that close to a rounding boundary), inside the 2-ulp tolerance of an f32
+  // epilogue (kernel_row_reduce_agrees.rs:25).  Zero, infinite and NaN divisors give the same
+  // results either way.  Only a division at the root, whose value goes straight to the store,
+  // is rewritten: under a comparison or another op, a 1-ulp change could move more than 1 ulp.
+  bool recip = false;
+  if (sp.dtype == UNP_F32 && cached >= 0 && sp.epilogue.t == kir::J::Obj && sp.epilogue.o.size() == 1 &&
+      sp.epilogue.o[0].first == "Div" && sp.epilogue.o[0].second.t == kir::J::Arr &&
+      sp.epilogue.o[0].second.a.size() == 2 && !mentions(sp.epilogue.o[0].second.a[1], "Input")) {
+    const kir::J& num = sp.epilogue.o[0].second.a[0];
+    const kir::J& den = sp.epilogue.o[0].second.a[1];
+    std::string a, b, ac, w2;
+    const kir::J* reuse = cached >= 0 ? &sp.pres[cached] : nullptr;
+    if (expr_cpp(num, T, a, w2) && expr_cpp(den, T, b, w2) && expr_cpp(num, T, ac, w2, reuse)) {
+      epi = "(" + a + " * (1.0 / " + b + "))";
+      epi_c = "(" + ac + " * (1.0 / " + b + "))";
+      recip = true;
+    }
+  }
   // The name carries a hash of the expressions: different row reductions never share a symbol.
   std::string key = std::string(T) + "|" + std::to_string(sp.n_inputs);
   for (size_t st = 0; st < NS; ++st) key += "|" + std::to_string(sp.ops[st]) + ":" + pre[st];
@@ -1348,8 +1384,12 @@ int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) 
                 "within an ulp of the host libm's")
     << "," << json_str("Sum/Mean stages fold in f64 in a geometry-fixed order: within the declared bound "
                        "gamma_(n-1)*sum|x| of the serial fold, then one rounding; Max/Min stages are exact except NaN "
-                       "payload and the sign of a zero")
-    << "]}";
+                       "payload and the sign of a zero");
+  if (recip)
+    j << "," << json_str("the f32 epilogue's quotient by a row value multiplies by the row's f64 reciprocal: "
+                         "within 2^-52 of the quotient, so the f32 output is the quotient's rounding or its "
+                         "neighbour, within the 2-ulp tolerance of an f32 epilogue");
+  j << "]}";
   L.interface_json = j.str();
   return UNP_OK;
 }
