@@ -316,7 +316,10 @@ def test_row_reduce_lifts_round_trip(which, dtype, launch):
     # subexpressions are not held.
     assert g.interface["epilogue_reuses_stage"] == (1 if which == "softmax" else -1)
     if which == "softmax":
-        assert "epi_c" in g.source and "c / r[1]" in g.source.replace("(", "").replace(")", "")
+        # An f32 output multiplies the kept value by the row's reciprocal; an f64 output divides.
+        flat = g.source.replace("(", "").replace(")", "")
+        assert "epi_c" in g.source and ("c * 1.0 / r[1]" if dtype == "F32" else "c / r[1]") in flat
+        assert ("reciprocal" in g.interface["fidelity_notes"][-1]) == (dtype == "F32")
 
 
 def test_row_reduce_launched_shape():
