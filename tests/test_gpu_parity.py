@@ -1683,6 +1683,22 @@ def test_fixed_scan_schedule_extremum(hip_device, op):
     assert _fixed_scan(x, op)[0].tobytes() == got.tobytes()
 
 
+@pytest.mark.parametrize("shape", [(1, 70 * 4 * 64 * 2 * 18), (2, 66 * 4 * 64 * 2 * 18 + 1), (3, 5000)])
+def test_fixed_scan_schedule_f64_and_mean_free_ops(hip_device, shape):
+    """F64 data on the fixed schedule (the staged entry's 2-element vectors, and the register entry):
+    a dyadic Sum bit-exact, Max/Min equal to the oracle's with NaN cells, a repeat identical."""
+    H.say(f"[case] fixed scan f64 {shape}")
+    x = (rng(65).integers(-2**20, 2**20, size=shape) / 1024.0).astype(np.float64)
+    got, _ = _fixed_scan(x, "Sum", True, False)
+    assert got.tobytes() == oracle.scan_rows(x, "Sum", True, False).tobytes()
+    y = rng(66).normal(size=shape)
+    y.ravel()[::5001] = np.nan
+    for op in ("Max", "Min"):
+        g1, _ = _fixed_scan(y, op, False, True)
+        assert equal_extremum(g1, oracle.scan_rows(y, op, False, True)), op
+        assert _fixed_scan(y, op, False, True)[0].tobytes() == g1.tobytes(), op
+
+
 def test_fixed_scan_schedule_config3b_full(hip_device):
     H.say("[case] config 3b on the fixed schedule: f32 inclusive scan 2^26")
     n = 1 << 26

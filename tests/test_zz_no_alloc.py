@@ -3,8 +3,8 @@
 row, the second smaller, for every form whose kernels use a workspace -- the scans (tile status and
 ticket counter), the full reduction (partials and counter), the column reduction (partials and strip
 counters) and the dequantizing GEMM (repacked activations and column sums).  Results are compared bit
-for bit: the integer forms and the fixed-order float reductions are deterministic, and the f32 scan
-runs on dyadic data, where every association is exact.  A launch whose workspace exceeds the static
+for bit: the integer forms and the fixed-order float reductions are deterministic, the f32 scan
+runs on dyadic data, where every association is exact, and on normal data on the fixed schedule.  A launch whose workspace exceeds the static
 scratch is refused before anything runs."""
 from __future__ import annotations
 
@@ -81,6 +81,17 @@ def test_scans_match_the_allocating_launch(hip_device):
         def make():
             return din, u.DeviceBuffer(n * 4), 1, n
         got, want = both(exf, make, lambda a: a[1].download(np.float32, n))
+        assert got.tobytes() == want.tobytes()
+    # The fixed schedule on normal data: only an association fixed by the tiling makes the two
+    # launches agree bit for bit here.
+    exx = u.Executor(u.HipBackend().lower_form("scan", "F32", 2, "Sum", schedule="fixed"))
+    for n in (1 << 24, 100003):
+        print(f"[no_alloc] f32 scan, fixed schedule, normal data n={n}", flush=True)
+        din = u.DeviceBuffer.from_array(synth.normal_f32(5, n))
+
+        def make():
+            return din, u.DeviceBuffer(n * 4), 1, n
+        got, want = both(exx, make, lambda a: a[1].download(np.float32, n))
         assert got.tobytes() == want.tobytes()
 
 
