@@ -1626,6 +1626,18 @@ template <int N> UNP_DEV void wait_vm() {
 }
 UNP_DEV void wait_vm_all() { wait_vm<0>(); }
 
+// fn(ic<0>{}), fn(ic<1>{}), ..., fn(ic<N - 1>{}): a loop whose index is a constant expression
+// in the body (for immediates such as a wait count).
+template <int V> struct ic {
+  static constexpr int value = V;
+};
+template <int N, int I = 0, class Fn> UNP_DEV void unroll_for(Fn&& fn) {
+  if constexpr (I < N) {
+    fn(ic<I>{});
+    unroll_for<N, I + 1>(fn);
+  }
+}
+
 // A block barrier that orders LDS only: no wait on outstanding global stores.  A wave with
 // global->LDS DMA in flight must wait for it first (the DMA counts as LDS writes).
 UNP_DEV void lds_barrier() {
@@ -1654,6 +1666,9 @@ UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows
   const u64 total = (u64)rows * (u64)tpr;
   const A I = F::identity();
   const T pad = (T)I;  // the identity, exactly representable at the element type
+  // The producer folds a full tile share by share as its loads land; vmcnt holds at most 63
+  // outstanding loads, so the per-share waits are exact only while (NC - 1) * K stays below it.
+  constexpr bool CHUNKED = (NC - 1) * K <= 63;
 
   if (wave == NC) {
     // ---- producer ----
@@ -1693,15 +1708,49 @@ UNP_DEV void scan_staged(const T* __restrict__ in, T* __restrict__ out, i64 rows
       const T* __restrict__ rin = in + row * cols;
       const i64 t0 = j * BT;
       const bool full = t0 + BT <= cols;
-      if (full) load(rin, t0, b, true);
-      else load(rin, t0, b, false);
-      wait_vm_all();
       A agg = I;
+      if (full && CHUNKED) {
+        // Loads complete in issue order, so once at most (NC - 1 - c) * K of this tile's
+        // NC * K loads are outstanding, wave c's share is in LDS: fold it while the rest
+        // of the tile is still arriving.  The share is read with ds_read_b128 from inline
+        // assembly: for an ordinary LDS read the compiler waits for every outstanding DMA load
+        // of the wave first.  The LDS stores of the shares' aggregates wait for the last share.
+        load(rin, t0, b, true);
+        A ws[NC];
+        unroll_for<NC>([&](auto cc) {
+          constexpr int c = decltype(cc)::value;
+          wait_vm<(NC - 1 - c) * K>();
+          const u32 at = (u32)(size_t)(lds_void*)&buf[b][c * WT + lane * VEC];
+          u32x4_t raw[K];
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const A w = wave_reduce<A, OP>(full ? share(t0, b, c, true) : share(t0, b, c, false));
-        if (lane == 0) wagg[b][c] = w;
-        agg = F::apply(agg, w);
+          for (int k = 0; k < K; ++k)
+            asm volatile("ds_read_b128 %0, %1" : "=v"(raw[k]) : "v"(at + (u32)(k * 64 * VEC * (int)sizeof(T))) : "memory");
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          A s = I;
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            asm volatile("" : "+v"(raw[k]));  // no use of raw[k] moves above the wait
+            const vec<T, VEC> v = __builtin_bit_cast(vec<T, VEC>, raw[k]);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) s = F::apply(s, (A)v.e[e]);
+          }
+          ws[c] = wave_reduce<A, OP>(s);
+          agg = F::apply(agg, ws[c]);
+        });
+        if (lane == 0) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) wagg[b][c] = ws[c];
+        }
+      } else {
+        if (full) load(rin, t0, b, true);
+        else load(rin, t0, b, false);
+        wait_vm_all();
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const A w = wave_reduce<A, OP>(full ? share(t0, b, c, true) : share(t0, b, c, false));
+          if (lane == 0) wagg[b][c] = w;
+          agg = F::apply(agg, w);
+        }
       }
       if (lane == 0) S::publish(st, g, j == 0 ? 1 : 0, agg, epoch);
     };
