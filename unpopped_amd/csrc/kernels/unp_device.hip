@@ -1235,12 +1235,16 @@ UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch, const wa
 //
 // G(k) is published in the status slot of the group's last tile (flag 1, over its aggregate);
 // a row's first tile carries flag 1 too, where the aggregate is its own prefix.  The look-back
-// probes its group's earlier tiles (window a), the previous group (window b) and the slot of
-// G(k-2).  With G(k-1) published it is done; with G(k-2) (or k = 1) and window b complete it
-// computes G(k-1) and publishes it; otherwise it probes again (the lowest group without a total
-// gets one from its own last tile, whose look-back waits only on lower tiles).  The last tile of
-// a group publishes G(k) itself.  `agg` is this tile's aggregate.
-template <class A, int OP, int SP>
+// probes its group's earlier tiles (window a) and the D groups before it (windows 1 .. D, all in
+// one round trip).  Walking back from group k-1, it stops at the first group whose total is
+// published (or past the row's first group, whose predecessor total is the identity); with every
+// aggregate of the groups walked over present, it refolds their totals in order,
+// G(m) = fold(G(m-1), reduce(group m)), which gives the same bits whoever computes them, and
+// publishes each.  Otherwise it probes again (the lowest group without a total gets one from its
+// own last tile, whose look-back waits only on lower tiles).  The last tile of a group publishes
+// G(k) itself.  `agg` is this tile's aggregate.  D = 2 measured best for the f32 scan: deeper
+// windows hold more status words across the probe and the staged consumer spills.
+template <class A, int OP, int SP, int D = 2>
 UNP_DEV A lookback_grouped(u64* st, u64 g, i64 j, int lane, u32 epoch, const waits& wt, A agg) {
   typedef fold<A, OP> F;
   typedef tile_status<A, SP> S;
@@ -1249,41 +1253,51 @@ UNP_DEV A lookback_grouped(u64* st, u64 g, i64 j, int lane, u32 epoch, const wai
   const i64 k = j >> 6;
   const int q = (int)(j & 63);
   const u64 row0 = g - (u64)j;  // status index of the row's first tile
-  // Window a: lane l < q reads tile 64k + l; window b: lane l reads tile 64(k-1) + l; every
-  // lane reads the slot of G(k-2).  Lanes with nothing to read take the tile's own slot.
+  // Window a: lane l < q reads tile 64k + l; window d: lane l reads tile 64(k-d) + l.  Lanes
+  // with nothing to read take the tile's own slot.
   const u64 ia = lane < q ? row0 + (u64)(64 * k + lane) : g;
-  const u64 ib = k >= 1 ? row0 + (u64)(64 * (k - 1) + lane) : g;
-  const u64 ic = k >= 2 ? row0 + (u64)(64 * (k - 2) + 63) : g;
   const u64 t0 = wall_clock64();
   for (;;) {
-    u64 wa[W], wb[W], wc[W];
+    u64 wa[W], wd[D][W];
     S::fetch(st, ia, wa);
-    S::fetch(st, ib, wb);
-    S::fetch(st, ic, wc);
-    A va = I, vb = I, vc = I;
+#pragma unroll
+    for (int d = 1; d <= D; ++d) S::fetch(st, k >= d ? row0 + (u64)(64 * (k - d) + lane) : g, wd[d - 1]);
+    A va = I;
     const int sa = lane < q ? S::decode(wa, epoch, va) : 1;
     if (lane >= q) va = lane == 63 ? agg : I;
-    const int sb = k >= 1 ? S::decode(wb, epoch, vb) : 0;
-    const int sc = k >= 2 ? S::decode(wc, epoch, vc) : 2;
     // Every earlier tile of the group has published (an aggregate; flag 1 only on a row's
     // first tile, where it is the aggregate too).
     bool ok = __ballot(sa == 0) == 0;
-    A gprev = I;
-    bool have_prev = k == 0;
-    if (ok && k >= 1) {
-      const int sb63 = __builtin_amdgcn_readlane(sb, 63);
-      if (sb63 == 2) {
-        gprev = readlane(vb, 63);  // G(k-1) published
-        have_prev = true;
-      } else if (__ballot(sb == 0) == 0 && sc == 2) {
-        // G(k-1) from G(k-2) (the identity for k = 1) and the previous group's aggregates.
-        const A gpp = k >= 2 ? vc : I;
-        gprev = F::apply(gpp, wave_reduce<A, OP>(vb));
-        if (lane == 0) S::publish(st, row0 + (u64)(64 * (k - 1) + 63), 1, gprev, epoch);
-        have_prev = true;
+    A vd[D];
+    int depth = 0;  // groups k-1 .. k-depth+1 are folded onto the total found at k-depth
+    A base = I;
+    if (ok) {
+#pragma unroll
+      for (int d = 1; d <= D; ++d) {
+        if (depth != 0) break;
+        if (k < d) {
+          depth = d;  // past the row's first group: G(-1) is the identity
+          break;
+        }
+        vd[d - 1] = I;
+        const int sd = S::decode(wd[d - 1], epoch, vd[d - 1]);
+        if (__builtin_amdgcn_readlane(sd, 63) == 2) {
+          base = readlane(vd[d - 1], 63);  // G(k-d) published
+          depth = d;
+        } else if (__ballot(sd == 0) != 0) {
+          break;  // an aggregate of group k-d is not out yet
+        }
       }
     }
-    if (ok && have_prev) {
+    if (ok && depth != 0) {
+      A gprev = base;
+#pragma unroll
+      for (int d = D; d >= 1; --d) {
+        if (d < depth) {
+          gprev = F::apply(gprev, wave_reduce<A, OP>(vd[d - 1]));
+          if (lane == 0) S::publish(st, row0 + (u64)(64 * (k - d) + 63), 1, gprev, epoch);
+        }
+      }
       const A sc_a = wave_inclusive_scan<A, OP>(va, lane);
       const A inner = q > 0 ? readlane(sc_a, q - 1) : I;
       if (q == 63 && lane == 0) S::publish(st, g, 1, F::apply(gprev, readlane(sc_a, 63)), epoch);
