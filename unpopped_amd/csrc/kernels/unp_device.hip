@@ -1243,7 +1243,7 @@ UNP_DEV A lookback(const u64* st, u64 tile, i64 j, int lane, u32 epoch, const wa
 // publishes each.  Otherwise it probes again (the lowest group without a total gets one from its
 // own last tile, whose look-back waits only on lower tiles).  The last tile of a group publishes
 // G(k) itself.  `agg` is this tile's aggregate.  D = 2 measured best for the f32 scan: deeper
-// windows hold more status words across the probe and the staged consumer spills.
+// windows cost more probe words per look-back than the waits they save.
 template <class A, int OP, int SP, int D = 2>
 UNP_DEV A lookback_grouped(u64* st, u64 g, i64 j, int lane, u32 epoch, const waits& wt, A agg) {
   typedef fold<A, OP> F;
