@@ -80,7 +80,8 @@ def build_cases(u, synth):
         din = u.DeviceBuffer.from_array(x)
         dout = u.DeviceBuffer(n * 4)
         return lambda: ex.launch(din, dout, n), ex
-    cases.append(Case("cfg3b", "f32 inclusive sum scan 2^26 (f64 carry)", 2 * (1 << 26) * 4, 1 << 26, cfg3b))
+    cases.append(Case("cfg3b", "f32 inclusive sum scan 2^26 (f64 carry, fixed schedule: reproducible bits)",
+                      2 * (1 << 26) * 4, 1 << 26, cfg3b))
 
     table_holder = {}
 
@@ -155,16 +156,17 @@ def build_extras(u, synth):
         return lambda: ex.launch(din, dout, n), ex
     extras.append(Case("rd_all", "f32 2^24 full Sum (cfg1's data on the GPU; cfg1 itself is the CPU case)",
                        (1 << 24) * 4 + 4, 1 << 24, full_sum))
-    def scan_fixed():
-        # cfg3b on the fixed schedule: the same launch with the look-back's association fixed by the
-        # tiling, so the f32 result has the same bits on every launch.
+    def scan_device():
+        # cfg3b on the device schedule, the Nondeterministic variant: the decoupled look-back folds
+        # however far each look-back walked, so the f32 bits can change from launch to launch.  The
+        # cfg3b line above runs what lower_kernel lowers, the fixed schedule (reproducible bits).
         n = 1 << 26
         x = synth.uniform_01_f32(2, n)
-        ex = u.Executor(u.HipBackend().lower_form("scan", "F32", 1, "Sum", schedule="fixed"))
+        ex = u.Executor(u.HipBackend().lower_form("scan", "F32", 1, "Sum", schedule="device"))
         din, dout = u.DeviceBuffer.from_array(x), u.DeviceBuffer(n * 4)
         return lambda: ex.launch(din, dout, n), ex
-    extras.append(Case("cfg3b_fixed", "f32 inclusive sum scan 2^26 on the fixed schedule (reproducible bits)",
-                       2 * (1 << 26) * 4, 1 << 26, scan_fixed))
+    extras.append(Case("cfg3b_device", "f32 inclusive sum scan 2^26 on the device schedule (bits vary run to run)",
+                       2 * (1 << 26) * 4, 1 << 26, scan_device))
     rr_bytes = 2 * 8192 * 4096 * 4
     extras.append(Case("rr_softmax", "f32 8192x4096 RowReduce softmax (Max, Sum of exp, divide)", rr_bytes,
                        8192 * 4096, row_reduce("softmax")))
@@ -211,6 +213,12 @@ def time_cases(u, cases, steps):
     u.synchronize()
     for c in cases:
         c.exec.set_timing(None, None)
+        # A wait that ran out leaves the launch's outputs invalid (unp_hip_exec_check); a timing of
+        # such a launch is no measurement, so the run stops here.
+        try:
+            c.exec.check()
+        except u.UnpError as e:
+            raise SystemExit(f"[bench] {c.name}: a timed launch reported {e.kind}: {e}; no line is printed")
     per = []
     for i, c in enumerate(cases):
         ms = sum(events[s][i][0].elapsed_ms(events[s][i][1]) for s in range(steps)) / steps

@@ -132,10 +132,12 @@ enum unp_oob_policy { UNP_OOB_SKIP = 0, UNP_OOB_ZEROFILL = 1, UNP_OOB_CLAMP = 2 
  * this backend's device-class schedule.  FIXED is the device schedule with every float
  * association fixed by the launch's tiling, so a float result is the same on every launch (the
  * reference's launched lifts fix theirs by geometry, kernel_lift/scan_launched.rs:19-26): a
- * float scan's look-back folds tile aggregates in a fixed grouping; a scan with a pre-map runs
- * its serial entry; every other form's device schedule is already fixed and lowers unchanged.
- * Forms whose every schedule gives the same bits (the gather, the dequants, integer folds)
- * lower the same kernels whichever is asked. */
+ * float scan's look-back (with or without a pre-map) folds tile aggregates in a fixed grouping;
+ * every other form's device schedule is already fixed and lowers unchanged.  A float scan's
+ * DEVICE look-back folds however far each look-back walked, which timing decides: its bits can
+ * change from launch to launch, so unp_hip_lower_kernel lowers a lifted float scan on FIXED and
+ * DEVICE is only a Nondeterministic variant.  Forms whose every schedule gives the same bits
+ * (the gather, the dequants, integer folds) lower the same kernels whichever is asked. */
 enum unp_schedule { UNP_SCHEDULE_DEVICE = 0, UNP_SCHEDULE_SERIAL = 1, UNP_SCHEDULE_FIXED = 2 };
 /* VariantFidelity (backend.rs:204-309) in declaration order: a variant's bits against the cell's
  * default lowering (here the SERIAL schedule, the sequential fold's bits). */
@@ -183,7 +185,7 @@ typedef struct unp_variant {
   char launch_note[256];
 } unp_variant;
 /* Backend::lower_variants (backend.rs:786-807): every schedule this backend has for the form's
- * cell, the default (SERIAL) first.  Fills up to `cap` entries of `out` and sets *count to the
+ * cell, the default (SERIAL) first, then the reproducible ones, then a Nondeterministic one.  Fills up to `cap` entries of `out` and sets *count to the
  * number there are; a form with no lowering is refused as unp_hip_lower_form refuses it. */
 int32_t unp_hip_form_variants(const unp_form* form, unp_variant* out, size_t cap, size_t* count, unp_error* err);
 
@@ -193,7 +195,8 @@ int32_t unp_hip_form_variants(const unp_form* form, unp_variant* out, size_t cap
  * the lifts below (or the two kernels this backend authors) by lifting each candidate form its
  * signature admits and comparing the trees; anything else is UNP_UNSUPPORTED_KERNEL, and text that
  * is not a KernelFn is UNP_PARSE_ERROR.  The interface JSON carries the kernel's declared launch
- * and parameters (KernelInterface::of, kernel_interface.rs:237-262) beside the HIP launch. */
+ * and parameters (KernelInterface::of, kernel_interface.rs:237-262) beside the HIP launch.  A
+ * float scan lowers the FIXED schedule (reproducible bits); every other form its DEVICE one. */
 int32_t unp_hip_lower_kernel(const char* kernel_json, unp_generated** out, unp_error* err);
 
 /* ---------------------------------------------------------------------------------------

@@ -149,7 +149,7 @@ CASES = [
     (lambda: u.lift_reduction("r", "I64", 2, "Prod", launch=(32, 3)), "lift_reduction_opdef_launched", "unp_rowreduce_prod_i64"),
     (lambda: u.lift_reduction("r", "I32", 2, "Min", axes=(0, 1)), "lift_reduction_opdef", "unp_reduce_all_min_i32"),
     (lambda: u.lift_scan("s", "I32", 1, "Sum", launch=(256, 1)), "lift_scan_opdef_launched", "unp_scan_incl_sum_i32"),
-    (lambda: u.lift_scan("s", "F32", 3, "Max", exclusive=True, reverse=True), "lift_scan_opdef", "unp_scan_excl_rev_max_f32"),
+    (lambda: u.lift_scan("s", "F32", 3, "Max", exclusive=True, reverse=True), "lift_scan_opdef", "unp_scan_fix_excl_rev_max_f32"),
     (lambda: u.lift_scan("s", "I64", 2, "Prod", exclusive=True, launch=(64, 8)), "lift_scan_opdef_launched", "unp_scan_excl_prod_i64"),
     (lambda: u.lift_gather("e", "Bf16", 2, "I32", launch=(256, 4096)), "lift_gather_opdef_launched", "unp_gather_rows_bf16_by_i32_ZeroFill"),
     (lambda: u.lift_gather("g", "U8", 3, "I64", oob="Skip"), "lift_gather_opdef", "unp_gather_rows_u8_by_i64_Skip"),
@@ -445,7 +445,7 @@ def test_mean_and_float_prod_scans_lift_only_sequentially():
     the serial lift is lowered (Mean on the look-back scan with the division at the store, a float
     Prod in the serial order), the launched lift declines, and an integer Mean declines."""
     b = u.HipBackend()
-    assert b.lower_kernel(u.lift_scan("s", "F32", 1, "Mean")).name.startswith("unp_scan_incl_mean_f32")
+    assert b.lower_kernel(u.lift_scan("s", "F32", 1, "Mean")).name.startswith("unp_scan_fix_incl_mean_f32")
     assert b.lower_kernel(u.lift_scan("s", "F64", 1, "Prod", exclusive=True)).name.startswith("unp_scan_seq_excl_prod")
     for op in ("Mean", "Prod"):
         with pytest.raises(_lib.UnpError) as e:
@@ -861,11 +861,11 @@ def test_launch_cases_corpus_is_refused_typed_and_runs_on_the_c_leg(case):
 # ---------------------------------------------------------------------------------------
 
 def test_form_variants_name_the_schedules_and_their_fidelity():
-    """Each cell's default is the serial schedule (the sequential fold's bits); the device schedule
-    follows with its honest fidelity: bit-identical for integer folds, deterministically divergent for a
-    float reduction (a fixed device order), nondeterministic for a float look-back scan (the carry's
-    association depends on timing), which also lists the fixed schedule (the look-back's association
-    fixed by the tiling).  Forms whose schedules agree list one."""
+    """Each cell's default is the serial schedule (the sequential fold's bits); the device schedules
+    follow with their honest fidelity: bit-identical for integer folds, deterministically divergent for
+    a float reduction (a fixed device order) and for a float scan's fixed schedule (the look-back's
+    association fixed by the tiling), which comes before the nondeterministic look-back (the carry's
+    association depends on timing).  Forms whose schedules agree list one."""
     b = u.HipBackend()
 
     def summary(**form):
@@ -877,8 +877,8 @@ def test_form_variants_name_the_schedules_and_their_fidelity():
         ("serial", "BitIdentical", "serial"), ("device", "BitIdentical", "device")]
     assert summary(kind="reduction", dtype="F32", rank=2, op="Prod", axes=(1,)) == [("serial", "BitIdentical", "serial")]
     assert summary(kind="scan", dtype="F32", rank=1, op="Sum") == [
-        ("serial", "BitIdentical", "serial"), ("device", "Nondeterministic", "device"),
-        ("fixed", "DeterministicallyDivergent", "fixed")]
+        ("serial", "BitIdentical", "serial"), ("fixed", "DeterministicallyDivergent", "fixed"),
+        ("device", "Nondeterministic", "device")]
     assert summary(kind="scan", dtype="I32", rank=1, op="Sum") == [
         ("serial", "BitIdentical", "serial"), ("device", "BitIdentical", "device")]
     assert summary(kind="scan", dtype="F64", rank=2, op="Sum", axes=(0,)) == [("serial", "BitIdentical", "serial")]
@@ -896,11 +896,13 @@ def test_form_variants_name_the_schedules_and_their_fidelity():
 
 def test_fixed_schedule_lowers_a_float_scan_apart_and_other_forms_unchanged():
     """The fixed schedule changes only a float scan's look-back (the unp_scan_fix_ entries, fidelity
-    notes saying so); forms whose device schedule is already fixed lower the same source on it."""
+    notes saying so, and that the entry, which the row length and alignment pick, fixes the tile size);
+    forms whose device schedule is already fixed lower the same source on it."""
     b = u.HipBackend()
     g = b.lower_form("scan", "F32", 1, "Sum", schedule="fixed")
     assert g.name == "unp_scan_fix_incl_sum_f32" and g.interface["schedule"] == "fixed"
     assert "same bits on every launch" in g.interface["fidelity_notes"][0]
+    assert "for one entry" in g.interface["fidelity_notes"][0]
     flag = ", true>(in, out, rows, cols"  # the scan templates' FIXED argument
     assert g.source.count(flag) == 2  # the staged and the register entry
     assert flag not in b.lower_form("scan", "F32", 1, "Sum").source
@@ -908,6 +910,26 @@ def test_fixed_schedule_lowers_a_float_scan_apart_and_other_forms_unchanged():
                  dict(kind="scan", dtype="I32", rank=1, op="Sum"),
                  dict(kind="gather", dtype="Bf16", rank=2)):
         assert b.lower_form(schedule="fixed", **form).source == b.lower_form(**form).source, form
+
+
+def test_lower_kernel_takes_the_fixed_schedule_for_float_scans():
+    """A lifted float scan lowers the fixed schedule (the reference's launched scan is reproducible,
+    kernel_lift/scan_launched.rs:22-27), with a pre-map too; an integer scan and a float reduction lower
+    their device schedule, which is already the same every launch.  The nondeterministic look-back is
+    reached only through lower_form(schedule="device")."""
+    from unpopped_amd import expr as X
+
+    b = u.HipBackend()
+    g = b.lower_kernel(u.lift_scan("s", "F32", 1, "Sum"))
+    assert g.interface["schedule"] == "fixed" and g.name.startswith("unp_scan_fix_")
+    assert "not reproducible" not in " ".join(g.interface["fidelity_notes"])
+    gx = b.lower_kernel(u.lift_scan("s", "F64", 2, "Sum", n_inputs=2, pre=X.input(0) * X.input(1)))
+    assert gx.interface["schedule"] == "fixed" and gx.name.startswith("unp_xscan_fix_")
+    assert "same bits on every launch" in gx.interface["fidelity_notes"][0]
+    assert ", true>(in, out, rows, cols" in gx.source
+    assert b.lower_kernel(u.lift_scan("s", "I32", 1, "Sum")).interface["schedule"] == "device"
+    dev = b.lower_form("scan", "F32", 1, "Sum", schedule="device")
+    assert dev.interface["schedule"] == "device" and "Not reproducible" in dev.interface["fidelity_notes"][0]
 
 
 def test_schedules_a_form_does_not_have_are_refused():

@@ -253,35 +253,88 @@ def test_scan_f32_sum_within_bound(hip_device):
     assert np.all(np.abs(got - want) <= 2 * bound)
 
 
-def test_scan_f32_repeat_launches_stay_within_the_bound(hip_device):
-    """The f32 Sum scan's carry across tiles is an f64 fold whose association depends on how far each
-    tile's look-back walked, which can change from launch to launch (the interface's fidelity notes say
-    so).  Eight launches on the same normal data, 910 tiles over every CU: each launch is within the
-    declared per-prefix bound of the serial lift's f64 scan (kernel_parallel_scan_agrees.rs:287-300); the
-    spread between launches is reported.  On dyadic data every association is exact: all launches agree
-    bit for bit."""
-    n = 1 << 24
-    H.say(f"[case] scan f32 Sum, {n} normal values, 8 launches")
-    x = rng(29).normal(size=(1, n)).astype(np.float32)
+def _repeat_within_bound(x, run, launches):
+    """`launches` results of `run()` on the normal f32 row `x`, each checked against the declared
+    per-prefix bound of the serial lift's f64 scan (kernel_parallel_scan_agrees.rs:287-300)."""
+    n = x.shape[1]
     want = oracle.scan_rows(x, "Sum").ravel().astype(np.float64)
     xs = x.ravel().astype(np.float64)
-    u = 2.0 ** -53
+    u53 = 2.0 ** -53
     k = np.arange(n, dtype=np.float64)
-    gamma = k * u / (1 - k * u)
+    gamma = k * u53 / (1 - k * u53)
     prefix_abs = np.cumsum(np.abs(xs))
     runs = []
-    for _ in range(8):
-        got = H.scan_rows(x, "Sum").ravel()
+    for _ in range(launches):
+        got = run().ravel()
         g = got.astype(np.float64)
         ulp = np.spacing(np.abs(got)).astype(np.float64)
         assert np.all(np.abs(g - want) <= 2 * gamma * prefix_abs + ulp)
         runs.append(got)
-    differ = max(int(np.count_nonzero(r != runs[0])) for r in runs)
-    H.say(f"[case] launches differ from the first in at most {differ} of {n} outputs")
+    return runs
+
+
+def test_scan_f32_repeat_launches_are_bit_identical(hip_device):
+    """A lifted f32 Sum scan lowers the fixed schedule, whose carries fold tile aggregates in an
+    association the tiling fixes: eight launches on the same normal data, over every CU, give the same
+    bits (the reference's launched scan is reproducible too, kernel_lift/scan_launched.rs:22-27), each
+    within the declared per-prefix bound.  On dyadic data every association is exact: the oracle's bits."""
+    n = 1 << 24
+    H.say(f"[case] scan f32 Sum (lower_kernel: fixed schedule), {n} normal values, 8 launches")
+    x = rng(29).normal(size=(1, n)).astype(np.float32)
+    runs = _repeat_within_bound(x, lambda: H.scan_rows(x, "Sum"), 8)
+    assert all(r.tobytes() == runs[0].tobytes() for r in runs)
     xd = synth.uniform_pm1_f32(30, n).reshape(1, n)
     first = H.scan_rows(xd, "Sum")
-    for _ in range(3):
+    assert first.tobytes() == oracle.scan_rows(xd, "Sum").tobytes()
+    for _ in range(2):
         assert H.scan_rows(xd, "Sum").tobytes() == first.tobytes()
+
+
+def test_scan_f32_device_schedule_stays_within_the_bound(hip_device):
+    """The device schedule, a Nondeterministic variant: its carry's association depends on how far
+    each tile's look-back walked, which can change from launch to launch.  Eight launches on normal
+    data are each within the declared per-prefix bound; the spread between launches is reported."""
+    n = 1 << 24
+    H.say(f"[case] scan f32 Sum on the device schedule, {n} normal values, 8 launches")
+    x = rng(29).normal(size=(1, n)).astype(np.float32)
+    ex = u.Executor(u.HipBackend().lower_form("scan", "F32", 2, "Sum", schedule="device"))
+    din, dout = u.DeviceBuffer.from_array(x), u.DeviceBuffer(x.nbytes)
+
+    def run():
+        ex.launch(din, dout, 1, n)
+        ex.check()
+        return dout.download(np.float32, n)
+
+    runs = _repeat_within_bound(x, run, 8)
+    differ = max(int(np.count_nonzero(r != runs[0])) for r in runs)
+    H.say(f"[case] device-schedule launches differ from the first in at most {differ} of {n} outputs")
+
+
+def test_scan_f32_fixed_bits_per_entry(hip_device):
+    """The fixed schedule's association is fixed by the entry's tile size, and the entry follows from
+    the row's length and the buffers' alignment: the same normal values at a 16-byte-aligned address
+    take the staged entry (18432-element tiles) and 4 bytes further on the register entry
+    (16384-element tiles).  Each gives the same bits on every launch and stays within the bound; the
+    two may differ from each other, and how many outputs do is reported."""
+    n = 3 * (1 << 20)
+    H.say(f"[case] fixed scan f32 Sum normal n={n}, aligned and at +4 bytes, two launches each")
+    x = rng(61).normal(size=(1, n)).astype(np.float32)
+    ex = H.executor(kind="scan", dtype="F32", rank=2, op="Sum")
+    din, dout = u.DeviceBuffer(x.nbytes + 16), u.DeviceBuffer(x.nbytes + 16)
+    got = {}
+    for off in (0, 4):
+        din.at(off).upload(x)
+
+        def run():
+            ex.launch(din.at(off), dout.at(off), 1, n)
+            ex.check()
+            return dout.at(off).download(np.float32, n)
+
+        runs = _repeat_within_bound(x, run, 2)
+        assert runs[0].tobytes() == runs[1].tobytes(), off
+        got[off] = (ex.last_launch()["entry"], runs[0])
+    assert got[0][0].endswith("_v") and got[4][0].endswith("_s"), (got[0][0], got[4][0])
+    H.say(f"[case] the two entries differ in {int(np.count_nonzero(got[0][1] != got[4][1]))} of {n} outputs")
 
 
 @pytest.mark.parametrize("op", ["Max", "Min"])
@@ -415,6 +468,11 @@ WAIT_CASES = {
         -1000, 1000, size=(1, (1 << 23) + 1), dtype=np.int32), lambda x: oracle.scan_rows(x, "Max")),
     "scan_f32_staged": (dict(kind="scan", dtype="F32", rank=2, op="Sum"),
                         lambda: synth.uniform_pm1_f32(43, 1 << 24).reshape(1, -1), lambda x: oracle.scan_rows(x, "Sum")),
+    "scan_f32_register": (dict(kind="scan", dtype="F32", rank=2, op="Sum"),
+                          lambda: synth.uniform_pm1_f32(47, (1 << 23) + 3).reshape(1, -1),
+                          lambda x: oracle.scan_rows(x, "Sum")),
+    "scan_f32_device": (dict(kind="scan", dtype="F32", rank=2, op="Sum", schedule="device"),
+                        lambda: synth.uniform_pm1_f32(48, 1 << 24).reshape(1, -1), lambda x: oracle.scan_rows(x, "Sum")),
     "reduce_all": (dict(kind="reduction", dtype="I64", rank=1, op="Sum", reduced_from=0), lambda: rng(44).integers(
         -1 << 40, 1 << 40, size=1 << 22, dtype=np.int64), lambda x: np.array([oracle.reduce_rows(x.reshape(1, -1), "Sum")[0]])),
     "reduce_columns": (dict(kind="reduction", dtype="F32", rank=2, op="Max", axes=(0,)), lambda: rng(45).normal(
@@ -431,7 +489,11 @@ def test_a_wait_that_runs_out_is_reported_not_hung(hip_device, case):
     form, make, want_of = WAIT_CASES[case]
     x = make()
     want = want_of(x)
-    ex = u.Executor(H._backend.lower_kernel(H.kernel_for(**form)))
+    if "schedule" in form:  # a schedule the lifted kernel does not lower by default
+        f = dict(form)
+        ex = u.Executor(u.HipBackend().lower_form(f.pop("kind"), f.pop("dtype"), f.pop("rank"), f.pop("op"), **f))
+    else:
+        ex = u.Executor(H._backend.lower_kernel(H.kernel_for(**form)))
     din = u.DeviceBuffer.from_array(x)
     dout = u.DeviceBuffer(x.nbytes)
     outs = want.size
@@ -513,21 +575,25 @@ def test_scan_with_a_pre_and_a_post(hip_device, case):
 
 
 def test_scan_with_a_pre_within_the_bound_on_normal_data(hip_device):
-    """A device-schedule Sum of x * y over 2^22 normal values: every prefix within the declared
-    per-prefix bound of the serial lift's f64 scan of the pre-mapped values."""
+    """A lifted Sum of x * y over 2^22 normal values (the fixed schedule, which lower_kernel takes for a
+    float scan): every prefix within the declared per-prefix bound of the serial lift's f64 scan of the
+    pre-mapped values, and four launches bit for bit the same."""
     from unpopped_amd import expr as X
 
     n = 1 << 22
-    H.say(f"[case] scan with pre x*y, {n} normal values")
+    H.say(f"[case] scan with pre x*y, {n} normal values, 4 launches")
     x = rng(71).normal(size=(1, n)).astype(np.float32)
     y = rng(72).normal(size=(1, n)).astype(np.float32)
-    got = H.scan_expr([x, y], 1, "Sum", X.input(0) * X.input(1)).ravel().astype(np.float64)
+    first = H.scan_expr([x, y], 1, "Sum", X.input(0) * X.input(1))
+    got = first.ravel().astype(np.float64)
     want = oracle.scan_expr([x, y], 1, "Sum", X.input(0) * X.input(1)).ravel().astype(np.float64)
     v = (x * y).ravel().astype(np.float64)
     k = np.arange(n, dtype=np.float64)
     gamma = k * 2.0 ** -53 / (1 - k * 2.0 ** -53)
     ulp = np.spacing(np.abs(got).astype(np.float32)).astype(np.float64)
     assert np.all(np.abs(got - want) <= 2 * gamma * np.cumsum(np.abs(v)) + ulp)
+    for _ in range(3):
+        assert H.scan_expr([x, y], 1, "Sum", X.input(0) * X.input(1)).tobytes() == first.tobytes()
 
 
 def test_scan_repeated_launches_reuse_state(hip_device):

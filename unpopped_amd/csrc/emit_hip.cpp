@@ -571,9 +571,12 @@ static int32_t lower_scan(const unp_form& f, Lowered& L, std::string& why) {
     << json_str(fixed
                     ? "fixed schedule: a tile's carry is G(k-1) folded with the wave-tree prefix of its group's earlier tile "
                       "aggregates (groups of 64 tiles per row, G(k) = G(k-1) folded with the group's wave-tree total), an "
-                      "association the tile size alone fixes: the same bits on every launch and any grid. Float Sum / Mean "
-                      "fold in f64 within the declared per-prefix bound gamma_(n-1)*sum|x| + 1/2 ulp; Max/Min keep one NaN "
-                      "payload and zero sign launch to launch"
+                      "association the tile size alone fixes: the same bits on every launch and any grid for one entry. "
+                      "The entry follows from the row length and the buffers' alignment: rows of whole 16-byte vectors at "
+                      "16-byte-aligned addresses take the staged entry (18432-element tiles), others the register entry "
+                      "(16384-element tiles), whose bits may differ; a strided view runs the serial order. Float Sum / "
+                      "Mean fold in f64 within the declared per-prefix bound gamma_(n-1)*sum|x| + 1/2 ulp; Max/Min keep one "
+                      "NaN payload and zero sign launch to launch"
                 : kind_is_float(f.dtype) && (f.op0 == UNP_OP_SUM || f.op0 == UNP_OP_MEAN)
                     ? "float Sum / Mean: every prefix is an f64 fold of the same elements in a different order (tile-local "
                       "striped scan plus decoupled look-back; a Mean divides it by the count once); within the declared "
@@ -1574,10 +1577,11 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std
     }
     axis = __builtin_ctz(f.axes_mask);
   }
-  // The fixed schedule of a scan with a pre-map runs the serial entry: the register look-back
-  // here has no fixed-association form.
+  // The fixed schedule folds the register look-back's carries in groups of 64 tiles in an order
+  // the tiling fixes (lookback_grouped), as the plain scan's does.
   const bool serial = axis != f.rank - 1 || f.op0 == UNP_OP_PROD || f.op0 == UNP_OP_MEAN ||
-                      f.schedule == UNP_SCHEDULE_SERIAL || f.schedule == UNP_SCHEDULE_FIXED;
+                      f.schedule == UNP_SCHEDULE_SERIAL;
+  const bool fixed = !serial && f.schedule == UNP_SCHEDULE_FIXED;
   L.serial_scan = serial;
   L.scan_axis = axis;
   const char* T = ctype(f.dtype);
@@ -1594,10 +1598,11 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std
   const char* EX = f.exclusive ? "true" : "false";
   const char* RV = f.reverse ? "true" : "false";
   const std::string key = std::string(T) + "|" + std::to_string(NI) + "|" + std::to_string(f.op0) + "|" + EX + "|" +
-                          RV + "|" + (serial ? "q" : "d") + "|" + pre + "|" + (rx.has_post ? post : std::string("-"));
+                          RV + "|" + (serial ? "q" : fixed ? "f" : "d") + "|" + pre + "|" +
+                          (rx.has_post ? post : std::string("-"));
   char hx[17];
   std::snprintf(hx, sizeof hx, "%016llx", (unsigned long long)fnv1a64(key));
-  L.name = std::string("unp_xscan_") + (serial ? "seq_" : "") + (f.exclusive ? "excl_" : "incl_") +
+  L.name = std::string("unp_xscan_") + (serial ? "seq_" : fixed ? "fix_" : "") + (f.exclusive ? "excl_" : "incl_") +
            (f.reverse ? "rev_" : "") + op_name(f.op0) + "_" + lower_name(f.dtype) + "_" + std::string(hx, 8);
   const std::string ops = L.name + "_ops";
   std::ostringstream src;
@@ -1634,7 +1639,7 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std
         << ", long long rows, long long cols, unsigned long long* status, unsigned* counter, unsigned ticket_base, "
         << "unsigned epoch, unp::waits wt) {\n" << ins.str() << "  unp::xscan_lookback<" << T << ", " << NI << ", "
         << f.op0 << ", " << ops << ", " << EX << ", " << RV << ", " << e.k << ", " << e.wpb << ", " << kScanStatusWords
-        << ">(in, out, rows, cols, status, counter, ticket_base, epoch, wt);\n}\n";
+        << (fixed ? ", true" : "") << ">(in, out, rows, cols, status, counter, ticket_base, epoch, wt);\n}\n";
   }
   L.entries.push_back(e);
   L.threads = e.threads;
@@ -1645,7 +1650,7 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std
     << "\",\"op\":\"" << op_name(f.op0) << "\",\"exclusive\":" << EX << ",\"reverse\":" << RV << ",\"rank\":" << f.rank
     << ",\"axis\":" << axis << ",\"n_inputs\":" << NI << ",\"pre\":" << kir::write(rx.body)
     << ",\"post\":" << (rx.has_post ? kir::write(rx.post) : std::string("null"))
-    << ",\"schedule\":\"" << (serial ? "serial" : "device") << "\",\"params\":[";
+    << ",\"schedule\":\"" << (serial ? "serial" : fixed ? "fixed" : "device") << "\",\"params\":[";
   for (int k = 0; k < NI; ++k) j << "{\"name\":\"in" << k << "\",\"kind\":\"buffer\",\"role\":\"Read\"},";
   j << "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
   for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
@@ -1661,10 +1666,16 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std
     << ",\"fidelity_notes\":["
     << json_str(serial ? "the pre and the post evaluate in f64 and round once per statement, as the kernel evaluator runs "
                          "the lifted kernel; the fold in the serial lift's own order: bit-exact against the serial kernel"
-                       : "the pre and the post evaluate in f64 and round once per statement; a Sum's prefixes are f64 "
-                         "folds of the pre-mapped elements in another order (wave-local scans and decoupled look-back), "
-                         "within the declared per-prefix bound gamma_(n-1)*sum|v| + 1/2 ulp before the post, and not "
-                         "reproducible run to run; Max/Min exact except NaN payload and the sign of a zero")
+                : fixed ? "the pre and the post evaluate in f64 and round once per statement; a Sum's prefixes are f64 "
+                          "folds of the pre-mapped elements in an order the 4096-position block tiles fix (wave-local "
+                          "scans; a tile's carry folds the totals of 64-tile groups, then the wave-tree prefix of its "
+                          "group's earlier aggregates): the same bits on every launch, within the declared per-prefix "
+                          "bound gamma_(n-1)*sum|v| + 1/2 ulp before the post; Max/Min exact except NaN payload and the "
+                          "sign of a zero, which the tiling fixes too"
+                        : "the pre and the post evaluate in f64 and round once per statement; a Sum's prefixes are f64 "
+                          "folds of the pre-mapped elements in another order (wave-local scans and decoupled look-back), "
+                          "within the declared per-prefix bound gamma_(n-1)*sum|v| + 1/2 ulp before the post, and not "
+                          "reproducible run to run; Max/Min exact except NaN payload and the sign of a zero")
     << "]}";
   L.interface_json = j.str();
   return UNP_OK;
@@ -1734,20 +1745,20 @@ int32_t form_variants(const unp_form& f, std::vector<unp_variant>& out, std::str
   if (f.kind == UNP_FORM_SCAN) {
     add("serial", UNP_BIT_IDENTICAL, ser, "one lane per column, the serial lift's order and accumulator");
     if (!L.serial_scan) {
+      if (fl) {
+        // The launch with the look-back's association fixed by the tiling (the default of a lifted
+        // float scan): reproducible, in a different order from the serial fold.
+        unp_form fix = f;
+        fix.schedule = UNP_SCHEDULE_FIXED;
+        add("fixed", UNP_DETERMINISTICALLY_DIVERGENT, fix,
+            "persistent blocks drawing tile tickets, the look-back folding tile aggregates in groups of 64 "
+            "tiles in a fixed association: the same bits every launch");
+      }
       // The look-back carry's association depends on how far each look-back walked, which
       // depends on timing: a float result can differ from launch to launch.
       add("device", fl ? UNP_NONDETERMINISTIC : UNP_BIT_IDENTICAL, dev,
           "one persistent block per CU drawing tile tickets; decoupled look-back over a tile-status "
           "workspace tagged with a launch epoch");
-      if (fl) {
-        // The same launch with the look-back's association fixed by the tiling: reproducible,
-        // in a different order from the serial fold.
-        unp_form fix = f;
-        fix.schedule = UNP_SCHEDULE_FIXED;
-        add("fixed", UNP_DETERMINISTICALLY_DIVERGENT, fix,
-            "as device, the look-back folding tile aggregates in groups of 64 tiles in a fixed "
-            "association: the same bits every launch");
-      }
     }
     return UNP_OK;
   }

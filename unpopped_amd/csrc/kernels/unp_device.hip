@@ -243,11 +243,15 @@ template <int CTRL, int ROW_MASK, class X> UNP_DEV X dpp(X old, X src) {
   }
 }
 
+template <class X> UNP_DEV X settle(X x);
+
+// v_readlane of a 4- or 8-byte value.  An 8-byte value is settled first (settle, below): the
+// readlane may follow the VALU op that produced it by fewer wait states than gfx950 needs.
 template <class X> UNP_DEV X readlane(X v, int lane) {
   if constexpr (sizeof(X) == 4) {
     return __builtin_bit_cast(X, (u32)__builtin_amdgcn_readlane((int)__builtin_bit_cast(u32, v), lane));
   } else {
-    const u64 b = __builtin_bit_cast(u64, v);
+    const u64 b = __builtin_bit_cast(u64, settle(v));
     const u32 lo = (u32)__builtin_amdgcn_readlane((int)(u32)b, lane);
     const u32 hi = (u32)__builtin_amdgcn_readlane((int)(u32)(b >> 32), lane);
     return __builtin_bit_cast(X, ((u64)hi << 32) | (u64)lo);
@@ -279,7 +283,8 @@ template <class A, int OP> UNP_DEV A row_inclusive_scan(A x) {
 // issued one wait state after a v_add_f64 (all the compiler puts there) has returned the
 // register's value from before the add: a wave scan's row totals, read at lanes 15/31/47/63,
 // then lacked the last DPP steps.  The asm takes and returns the value, so its nops sit after
-// the value's producer and before every reader.  4-byte values are not affected.
+// the value's producer and before every reader.  4-byte values are not affected.  readlane
+// settles every 8-byte value it reads, so no caller depends on doing it first.
 template <class X> UNP_DEV X settle(X x) {
   if constexpr (sizeof(X) == 8) asm volatile("s_nop 4" : "+v"(x));
   return x;
@@ -1305,6 +1310,13 @@ UNP_DEV A lookback_grouped(u64* st, u64 g, i64 j, int lane, u32 epoch, const wai
     }
     if (wait_over(t0, wt)) {
       if (lane == 0) note_stall(wt);
+      // A group's last tile publishes a total even after giving up (the fold of what it has, with
+      // no carry), so that the tiles after it stop there instead of each waiting out the bound;
+      // the stall count already marks the launch's outputs invalid.
+      if (q == 63) {
+        const A tot = wave_reduce<A, OP>(va);
+        if (lane == 0) S::publish(st, g, 1, tot, epoch);
+      }
       return I;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -1505,7 +1517,7 @@ UNP_DEV void xscan_seq(const T* const* __restrict__ in, T* __restrict__ out, i64
 // the pre-mapped elements, the block's aggregate published and the row's earlier tiles folded by
 // decoupled look-back, each prefix rounded once and passed through the post.  Lane l's step k
 // is position k * 64 + l of its wave's stripe, so every load and store of a step is contiguous.
-template <class T, int NI, int OP, class OPS, bool EXCL, bool REV, int K, int WPB, int SP>
+template <class T, int NI, int OP, class OPS, bool EXCL, bool REV, int K, int WPB, int SP, bool FIXED = false>
 UNP_DEV void xscan_lookback(const T* const* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols,
                             u64* __restrict__ st, u32* __restrict__ counter, u32 ticket_base, u32 epoch, waits wt) {
   typedef typename acc<T, OP>::type A;
@@ -1573,8 +1585,12 @@ UNP_DEV void xscan_lookback(const T* const* __restrict__ in, T* __restrict__ out
         if (lane == 0) S::publish(st, g, 1, agg, epoch);
       } else {
         if (lane == 0) S::publish(st, g, 0, agg, epoch);
-        gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch, wt);
-        if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
+        if constexpr (FIXED && traits<A>::is_float) {
+          gex = lookback_grouped<A, OP, SP>(st, g, j, lane, epoch, wt, agg);
+        } else {
+          gex = lookback<A, OP, 1, SP>(st, g, j, lane, epoch, wt);
+          if (lane == 0) S::publish(st, g, 1, F::apply(gex, agg), epoch);
+        }
       }
       if (lane == 0) {
         gbase = gex;

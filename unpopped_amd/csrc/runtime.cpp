@@ -190,6 +190,12 @@ int32_t unp_hip_lower_kernel(const char* kernel_json, unp_generated** out, unp_e
     set_error(err, rc, why);
     return rc;
   }
+  // A lifted float scan lowers the fixed schedule: its carries fold in an order the tiling
+  // fixes, so every launch gives the same bits, as the reference's launched scan lift promises
+  // (kernel_lift/scan_launched.rs:22-27).  The device schedule's look-back, whose float
+  // association depends on timing, is only a Nondeterministic variant (unp_hip_form_variants).
+  if (rec.form.kind == UNP_FORM_SCAN && unp::kind_is_float(rec.form.dtype) && rec.form.schedule == UNP_SCHEDULE_DEVICE)
+    rec.form.schedule = UNP_SCHEDULE_FIXED;
   auto* g = new unp_generated();
   if (rec.form.kind == UNP_FORM_ROW_REDUCE) {
     // A row reduction whose expressions hold a node this backend cannot spell is an
@@ -578,10 +584,8 @@ int32_t workspace(unp_exec* x, size_t bytes, bool need_counter, size_t n_counter
       p += up(n_counters * sizeof(uint32_t));
     }
     if (bytes) w.ws = p;
-    if (need) {
-      const hipError_t e = hipMemsetAsync(x->fixed->base, 0, need, s);
-      if (e != hipSuccess) return hip_fail(err, "hipMemsetAsync(scratch)", e);
-    }
+    // A kernel, not hipMemsetAsync: a call under graph capture then records no memset node.
+    if (need) return unp::scratch_clear(x->fixed->base, need, s, err);
     return UNP_OK;
   }
   int32_t rc = ensure_ws(x, bytes, need_counter, err);

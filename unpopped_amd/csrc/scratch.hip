@@ -8,8 +8,10 @@
 // held until the process ends.  Its device address is looked up once per device, with that device
 // current, through hipGetSymbolAddress; host code only ever uses that address, never the array's
 // name (which in host code is a stand-in, not a device pointer).  Every launch clears the part it
-// uses on its stream before its kernels run, so no call depends on what an earlier one left.  Calls
-// that overlap on one GPU share the array and race: a caller serialises them (one stream, or events).
+// uses on its stream before its kernels run, so no call depends on what an earlier one left; the
+// clear is a kernel (scratch_zero), not hipMemsetAsync, so a captured call records kernel nodes
+// only.  Calls that overlap on one GPU share the array and race: a caller serialises them (one
+// stream, or events).
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -17,6 +19,34 @@
 #include "unp_internal.hpp"
 
 static __device__ __align__(256) unsigned char scratch[UNP_STATIC_SCRATCH_BYTES];
+
+// Zero n 16-byte words at p (grid-strided).
+__global__ void __launch_bounds__(256) scratch_zero(uint4* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = uint4{0, 0, 0, 0};
+}
+
+namespace unp {
+
+int32_t scratch_clear(void* base, size_t bytes, void* stream, unp_error* err) {
+  if (bytes % 16 != 0) {
+    set_error(err, UNP_INVALID_ARGUMENT, "a scratch clear covers whole 16-byte words");
+    return UNP_INVALID_ARGUMENT;
+  }
+  const size_t n = bytes / 16;
+  if (n == 0) return UNP_OK;
+  const size_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(scratch_zero, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream),
+                     static_cast<uint4*>(base), n);
+  const hipError_t h = hipGetLastError();
+  if (h != hipSuccess) {
+    set_error(err, UNP_HIP_ERROR, std::string("scratch_zero launch: ") + hipGetErrorString(h));
+    return UNP_HIP_ERROR;
+  }
+  return UNP_OK;
+}
+
+}  // namespace unp
 
 namespace {
 

@@ -180,6 +180,9 @@ struct Scratch {
   void* base;
   size_t cap;
 };
+// Zero `bytes` (a multiple of 16) at the device address `base` with a kernel on `stream`
+// (scratch.hip): the static scratch's per-call clear, a kernel node under graph capture.
+int32_t scratch_clear(void* base, size_t bytes, void* stream, unp_error* err);
 // unp_hip_exec_launch with every workspace taken from [scratch, scratch + cap) and cleared on the
 // launch stream first: it calls no allocator, and refuses a launch whose workspace does not fit
 // with UNP_INVALID_ARGUMENT before anything runs.
