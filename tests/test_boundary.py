@@ -773,7 +773,7 @@ def test_gather_skeleton_follows_the_gather_lift():
 # ---------------------------------------------------------------------------------------
 
 def elementwise_launched(name: str, dtype: str, rank: int, body: dict, block: int, grid: int) -> dict:
-    """lift_elementwise_opdef_launched (kernel_lift.rs:96-128, grid_stride_outermost :256-285) for two
+    """lift_elementwise_opdef_launched (kernel_lift.rs:145, grid_stride_outermost :256-285) for two
     inputs: loads of in0/in1 at the counters, the body stored to out, the outermost loop grid-strided."""
     r = rank
     i32 = lambda v: {"ConstInt": [v, "I32"]}  # noqa: E731
