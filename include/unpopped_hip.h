@@ -86,7 +86,11 @@ enum unp_artifact_kind {
 const char* unp_hip_name(void);
 /* Backend::provider (backend.rs:681): "unpopped-hip". */
 const char* unp_hip_provider(void);
-/* Backend::total_integer_ops (backend.rs:692): 0, the default. */
+/* Backend::total_integer_ops (backend.rs:682-694): 1.  Integer Div, Shl, Shr and ConstInt at the
+ * I32, I64, U32 and U64 compute dtypes are spelled by the total rule of
+ * docs/int-div-shift-semantics.md (rules 1-3): a zero divisor gives the dividend, so does signed
+ * MIN / -1; a shift count is read as unsigned bits modulo 32 (modulo 64 for a 64-bit type); Shl
+ * wraps and Shr is arithmetic on signed types, logical on unsigned ones; Add, Sub and Mul wrap. */
 int32_t unp_hip_total_integer_ops(void);
 /* Backend::supports_dtype (backend.rs:779): one of unp_dtype_support for an element kind on
  * a target id such as "rocm:gfx950" (crates/unpopped-vocab/src/target.rs:188). */
@@ -113,9 +117,12 @@ enum unp_form_kind {
   UNP_FORM_ROW_REDUCE = 5,  /* Access::RowReduce: staged row folds, then a full-width epilogue
                                (kernel_lift/row_reduce.rs:31, row_reduce_launched.rs:47); its
                                expressions come only through unp_hip_lower_kernel */
-  UNP_FORM_DEQUANT_GEMM = 6 /* the dequantizing GEMM (tests/support/dequant.rs:104-181): U4/I4
+  UNP_FORM_DEQUANT_GEMM = 6, /* the dequantizing GEMM (tests/support/dequant.rs:104-181): U4/I4
                                weights, I32 zero and scale per group, I32 or I8 activations,
                                I32 out, all wrapping */
+  UNP_FORM_ELEMENTWISE = 7  /* Access::Elementwise, launched (kernel_lift.rs:96-153): a body over
+                               n inputs read at the output coordinate, each optionally through an
+                               axis permutation; its body comes only through unp_hip_lower_kernel */
 };
 /* ReduceOp subset (crates/unpopped/src/ir.rs:1700-1735).  And/Or/Xor fold integers bitwise;
  * MaxNum/MinNum ignore NaN (a run of only NaN gives NaN); the reference lifts these five as
@@ -239,6 +246,14 @@ int32_t unp_lift_gather(const char* name, int32_t dtype, int32_t rank, int32_t i
 int32_t unp_lift_gather_x(const char* name, int32_t dtype, int32_t rank, int32_t index_dtype, int32_t axis,
                           int32_t oob, int32_t n_inputs, int32_t data_slot, int32_t index_slot, const char* body_json,
                           uint32_t block, uint32_t grid, char** json, unp_error* err);
+/* lift_elementwise_opdef (kernel_lift.rs:96-130) / lift_elementwise_opdef_launched (:145-153): n_inputs
+ * (1..8) inputs of dtype read at the loop counters, body_json (a ScalarExpr over Input(0..n_inputs),
+ * constants allowed) stored at the output coordinate.  perms: NULL for identity reads, else
+ * n_inputs x rank axis indices, row k the View::Permute of input k (iteration axis d reads the
+ * input's axis perms[k * rank + d], counter_place, kernel_lift.rs:315-324); block and grid 0 for
+ * the serial lift. */
+int32_t unp_lift_elementwise(const char* name, int32_t dtype, int32_t rank, int32_t n_inputs, const char* body_json,
+                             const int32_t* perms, uint32_t block, uint32_t grid, char** json, unp_error* err);
 /* No reference lift: the fused two-fold row reduction (softmax prologue) this backend authors,
  * each fold exactly a serial lifted reduction's; launched, rows grid-strided. */
 int32_t unp_kernel_row_reduce2(const char* name, int32_t dtype, int32_t op0, int32_t op1, uint32_t block,

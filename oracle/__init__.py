@@ -72,6 +72,8 @@ def lib() -> C.CDLL:
             "orc_gather_rows": (None, [P, i64, i64, P, i32, i64, i32, P]),
             "orc_dequant4_bf16": (None, [P, i32, P, P, i32, i64, i64, i64, P]),
             "orc_dequant_gemm_i32": (None, [P, i32, P, P, P, i32, i64, i64, i64, i64, P]),
+            "orc_elementwise_f": (None, [P, C.c_int32, i64, i32, P, C.c_int32, P]),
+            "orc_elementwise_i": (None, [P, C.c_int32, i64, P, C.c_int32, C.c_int32, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -378,3 +380,111 @@ def scan_expr(inputs, axis: int, op: str, pre, post=None, exclusive: bool = Fals
     lib().orc_scan_x(ins, len(xs), a_ext, shape[axis], b_ext, int(dt == np.float64), OPS[op], int(exclusive),
                      int(reverse), pre_arr, pre_n, post_arr, post_n, _p(out))
     return out
+
+
+# ---- Access::Elementwise ---------------------------------------------------------------
+
+NP_KINDS = {"F32": np.float32, "F64": np.float64, "I32": np.int32, "I64": np.int64, "U32": np.uint32,
+            "U64": np.uint64, "I8": np.int8, "U8": np.uint8, "I16": np.int16, "U16": np.uint16,
+            "F16": np.float16, "Bf16": np.uint16}
+INT_KINDS = {"I32": 9, "I64": 10, "U32": 23, "U64": 24}
+MUT_DIV0, MUT_MINNEG1, MUT_CLAMP, MUT_LOGICAL, MUT_FLOOR = 1, 2, 4, 8, 16
+_IX = {"Input": 1, "ConstInt": 2, "Cast": 3, "Add": 4, "Sub": 5, "Mul": 6, "Div": 7, "Shl": 8, "Shr": 9,
+       "Min": 10, "Max": 11, "BitAnd": 12, "BitOr": 13, "BitXor": 14, "Cmp": 15, "Select": 16}
+_CMPS = ["CmpEq", "CmpNe", "CmpLt", "CmpLe", "CmpGt", "CmpGe"]
+
+
+class IX(C.Structure):
+    _fields_ = [("op", C.c_int32), ("arg", C.c_int32), ("kind", C.c_int32), ("pad", C.c_int32), ("v", C.c_int64)]
+
+
+def int_type(e, compute: str) -> str:
+    """The type of an integer expression node (crates/unpopped/src/types.rs:679-751 over the subset
+    eval_int takes): an Input is the compute dtype, a ConstInt its kind, a Cast its target,
+    arithmetic its operands' common type, a comparison the compute dtype, a Select its arms'."""
+    if hasattr(e, "j"):
+        e = e.j
+    (tag, p), = e.items()
+    if tag == "Input":
+        return compute
+    if tag == "ConstInt":
+        return p[1]
+    if tag == "Cast":
+        return p[1]["to"]
+    if tag in ("Add", "Sub", "Mul", "Div"):
+        a, b = int_type(p[0], compute), int_type(p[1], compute)
+    elif tag == "Binary":
+        a, b = int_type(p[1], compute), int_type(p[2], compute)
+        if a == b and p[0] in _CMPS:
+            return compute
+    elif tag == "Select":
+        a, b = int_type(p[1], compute), int_type(p[2], compute)
+    else:
+        raise ValueError(f"the integer evaluator has no {tag}")
+    if a != b:
+        raise ValueError(f"{tag} of {a} and {b}")
+    return a
+
+
+def int_program(e, t: str, compute: str) -> list[tuple[int, int, int, int]]:
+    """A ScalarExpr as the C oracle's typed postfix program (op, arg, kind, literal), each node at
+    the kind eval_int (oracle/kernel_eval.rs:809-848) evaluates it at: `t` for an operand, its own
+    type for a Cast's operand, a comparison's operands and a Select's condition."""
+    if hasattr(e, "j"):
+        e = e.j
+    (tag, p), = e.items()
+    k = INT_KINDS[t]
+    own = lambda x: int_program(x, int_type(x, compute), compute)  # noqa: E731
+    if tag == "Input":
+        return [(1, int(p), k, 0)]
+    if tag == "ConstInt":
+        return [(2, 0, k, int(p[0]))]
+    if tag == "Cast":
+        if p[1].get("sat", "Wrap") != "Wrap" or p[1]["to"] != t:
+            raise ValueError("only an integer wrap to the node's type")
+        return own(p[0]) + [(3, 0, k, 0)]
+    if tag in ("Add", "Sub", "Mul", "Div"):
+        return int_program(p[0], t, compute) + int_program(p[1], t, compute) + [(_IX[tag], 0, k, 0)]
+    if tag == "Binary":
+        if p[0] in _CMPS:
+            return own(p[1]) + own(p[2]) + [(15, _CMPS.index(p[0]), k, 0)]
+        return int_program(p[1], t, compute) + int_program(p[2], t, compute) + [(_IX[p[0]], 0, k, 0)]
+    if tag == "Select":
+        return own(p[0]) + int_program(p[1], t, compute) + int_program(p[2], t, compute) + [(16, 0, k, 0)]
+    raise ValueError(f"the integer evaluator has no {tag}")
+
+
+def elementwise(inputs, body, dtype: str, perms=None, mutant: int = 0) -> np.ndarray:
+    """The serial Access::Elementwise kernel (kernel_lift.rs:96-130) as the kernel evaluator runs it:
+    input k is read through its View::Permute (iteration axis d reads its axis ``perms[k][d]``,
+    counter_place :315-324), and the body is evaluated per output element -- in f64 and rounded once
+    at the store for F32/F64 (orc_elementwise_f), by eval_int's total rule for I32/I64/U32/U64
+    (orc_elementwise_i, ``mutant`` planting a mistake for the tests), or as a bit move of one input."""
+    if hasattr(body, "j"):
+        body = body.j
+    xs = [np.asarray(a) if perms is None else np.transpose(np.asarray(a), perms[k]) for k, a in enumerate(inputs)]
+    xs = [np.ascontiguousarray(a) for a in xs]
+    shape = xs[0].shape
+    if list(body) == ["Input"]:
+        return xs[int(body["Input"])].copy()
+    n = int(np.prod(shape, dtype=np.int64))
+    if dtype in ("F32", "F64"):
+        f64 = dtype == "F64"
+        ys = [np.ascontiguousarray(a, np.float64 if f64 else np.float32) for a in xs]
+        ptrs = (C.c_void_p * len(ys))(*[_p(a) for a in ys])
+        arr, ln = _rx_array(body)
+        out = np.empty(shape, np.float64 if f64 else np.float32)
+        lib().orc_elementwise_f(ptrs, len(ys), n, int(f64), arr, ln, _p(out))
+        return out
+    if dtype not in INT_KINDS:
+        raise ValueError(f"no elementwise body at {dtype}")
+    prog = int_program(body, dtype, dtype)
+    arr = (IX * len(prog))(*[IX(op, arg, kind, 0, v) for op, arg, kind, v in prog])
+    ys = [np.ascontiguousarray(a.astype(NP_KINDS[dtype]).view(np.uint64) if dtype == "U64" else
+                               a.astype(NP_KINDS[dtype]).astype(np.int64)).view(np.int64) for a in xs]
+    ptrs = (C.c_void_p * len(ys))(*[_p(a) for a in ys])
+    raw = np.empty(shape, np.int64)
+    lib().orc_elementwise_i(ptrs, len(ys), n, arr, len(prog), int(mutant), _p(raw))
+    if dtype == "U64":
+        return raw.view(np.uint64)
+    return raw.astype(NP_KINDS[dtype])

@@ -600,3 +600,150 @@ void orc_scan_x(const void* const* ins, int32_t n_inputs, int64_t a_ext, int64_t
 #undef ORC_ROUND
 #undef ORC_STORE
 }
+
+/* ======================================================================================
+ * Access::Elementwise: lift_elementwise_opdef (kernel_lift.rs:96-130) run by the kernel
+ * evaluator.  A float statement is evaluated in f64 and rounded once at the store
+ * (kernel_eval.rs:763-771); an integer one by eval_int (kernel_eval.rs:809-848) with int_div,
+ * int_binary, int_shift and wrap (:1114-1175).
+ * ==================================================================================== */
+
+void orc_elementwise_f(const void* const* ins, int32_t n_inputs, int64_t count, int f64, const orc_rx* prog,
+                       int32_t len, void* out) {
+  double x[16], red[1] = {0.0};
+  for (int64_t i = 0; i < count; ++i) {
+    for (int32_t k = 0; k < n_inputs; ++k)
+      x[k] = f64 ? ((const double*)ins[k])[i] : (double)((const float*)ins[k])[i];
+    const double v = orc_rx_eval(prog, len, x, red, !f64);
+    if (f64) ((double*)out)[i] = v;
+    else ((float*)out)[i] = (float)v;
+  }
+}
+
+typedef __int128 i128;
+
+/* The kind's value range (types.rs int_range). */
+static void int_range(int32_t kind, i128* lo, i128* hi) {
+  switch (kind) {
+    case ORC_K_I32: *lo = -((i128)1 << 31); *hi = ((i128)1 << 31) - 1; break;
+    case ORC_K_U32: *lo = 0; *hi = ((i128)1 << 32) - 1; break;
+    case ORC_K_I64: *lo = -((i128)1 << 63); *hi = ((i128)1 << 63) - 1; break;
+    default: *lo = 0; *hi = ((i128)1 << 64) - 1; break;
+  }
+}
+
+/* wrap (kernel_eval.rs:1165-1174): v taken into the kind's range modulo its size. */
+static i128 int_wrap(int32_t kind, i128 v) {
+  i128 lo, hi;
+  int_range(kind, &lo, &hi);
+  if (v >= lo && v <= hi) return v;
+  const i128 m = hi - lo + 1;
+  i128 r = (v - lo) % m;
+  if (r < 0) r += m;
+  return r + lo;
+}
+
+/* int_div (kernel_eval.rs:1114-1120): a zero divisor and signed MIN / -1 give the dividend;
+ * otherwise the quotient truncated toward zero (C's `/` on the 128-bit values). */
+static i128 int_div(int32_t kind, i128 x, i128 y, int32_t mutant) {
+  i128 lo, hi;
+  int_range(kind, &lo, &hi);
+  if (y == 0) return (mutant & ORC_MUT_DIV0) ? 0 : x;
+  if (lo < 0 && x == lo && y == -1) return (mutant & ORC_MUT_MINNEG1) ? hi : x;
+  i128 q = x / y;
+  if ((mutant & ORC_MUT_FLOOR) && (x % y != 0) && ((x < 0) != (y < 0))) q -= 1;
+  return q;
+}
+
+/* int_shift (kernel_eval.rs:1151-1163): the count's two's-complement bits modulo the width (64
+ * for a 64-bit kind, else 32); Shl wraps, Shr is arithmetic on the signed value (logical for an
+ * unsigned kind, whose values are non-negative). */
+static i128 int_shift(int32_t kind, int left, i128 x, i128 y, int32_t mutant) {
+  const int width = (kind == ORC_K_I64 || kind == ORC_K_U64) ? 64 : 32;
+  const unsigned __int128 ybits = (unsigned __int128)y;
+  unsigned k = (unsigned)(ybits & (unsigned __int128)(width - 1));
+  if ((mutant & ORC_MUT_CLAMP) && (y < 0 || y >= width)) {
+    /* a count past the width clamps to the width: every bit shifted out */
+    if (left) return 0;
+    return x < 0 ? -1 : 0;
+  }
+  if (left) return int_wrap(kind, x * ((i128)1 << k));
+  if ((mutant & ORC_MUT_LOGICAL) && x < 0) {
+    i128 lo, hi;
+    int_range(kind, &lo, &hi);
+    const i128 m = (hi - lo + 1);
+    return int_wrap(kind, (x + m) >> k);
+  }
+  return x >> k; /* gcc's >> of a negative __int128 is arithmetic */
+}
+
+static i128 ix_input(int32_t kind, int64_t raw) {
+  switch (kind) {
+    case ORC_K_I32: return (int32_t)(uint32_t)(uint64_t)raw;
+    case ORC_K_U32: return (uint32_t)(uint64_t)raw;
+    case ORC_K_I64: return raw;
+    default: return (uint64_t)raw;
+  }
+}
+
+void orc_elementwise_i(const int64_t* const* ins, int32_t n_inputs, int64_t count, const orc_ix* prog, int32_t len,
+                       int32_t mutant, int64_t* out) {
+  (void)n_inputs;
+  i128 st[64];
+  for (int64_t i = 0; i < count; ++i) {
+    int sp = 0;
+    for (int32_t j = 0; j < len; ++j) {
+      const orc_ix* p = &prog[j];
+      const int32_t t = p->kind;
+      i128 a = 0, b = 0, c = 0;
+      switch (p->op) {
+        case ORC_IX_INPUT: st[sp++] = ix_input(t, ins[p->arg][i]); continue;
+        case ORC_IX_CONST: st[sp++] = int_wrap(t, (i128)p->v); continue;
+        case ORC_IX_CAST: st[sp - 1] = int_wrap(t, st[sp - 1]); continue;
+        case ORC_IX_SELECT:
+          sp -= 2;
+          c = st[sp - 1];
+          st[sp - 1] = c != 0 ? st[sp] : st[sp + 1];
+          continue;
+        default: break;
+      }
+      sp--;
+      a = st[sp - 1];
+      b = st[sp];
+      i128 r = 0;
+      switch (p->op) {
+        case ORC_IX_ADD: r = int_wrap(t, a + b); break;
+        case ORC_IX_SUB: r = int_wrap(t, a - b); break;
+        case ORC_IX_MUL: {
+          /* the product of two 64-bit values can pass 2^127: wrap through the unsigned 128-bit
+           * product, whose low 64 bits are the product's */
+          const unsigned __int128 u = (unsigned __int128)a * (unsigned __int128)b;
+          r = int_wrap(t, (i128)(uint64_t)u);
+          if (t == ORC_K_I32 || t == ORC_K_U32) r = int_wrap(t, (i128)(uint32_t)(uint64_t)u);
+          break;
+        }
+        case ORC_IX_DIV: r = int_div(t, a, b, mutant); break;
+        case ORC_IX_SHL: r = int_shift(t, 1, a, b, mutant); break;
+        case ORC_IX_SHR: r = int_shift(t, 0, a, b, mutant); break;
+        case ORC_IX_MIN: r = a < b ? a : b; break;
+        case ORC_IX_MAX: r = a > b ? a : b; break;
+        case ORC_IX_AND: r = a & b; break;
+        case ORC_IX_OR: r = a | b; break;
+        case ORC_IX_XOR: r = a ^ b; break;
+        case ORC_IX_CMP:
+          switch (p->arg) {
+            case 0: r = a == b; break;
+            case 1: r = a != b; break;
+            case 2: r = a < b; break;
+            case 3: r = a <= b; break;
+            case 4: r = a > b; break;
+            default: r = a >= b; break;
+          }
+          break;
+        default: r = 0; break;
+      }
+      st[sp - 1] = r;
+    }
+    out[i] = (int64_t)(uint64_t)(unsigned __int128)st[0];
+  }
+}

@@ -104,4 +104,38 @@ void orc_scan_x(const void* const* ins, int32_t n_inputs, int64_t a_ext, int64_t
                 int exclusive, int reverse, const orc_rx* pre, int32_t pre_len, const orc_rx* post, int32_t post_len,
                 void* out);
 
+/* ---- Access::Elementwise (kernel_lift.rs:96-153 as the kernel evaluator runs it) ---------- */
+
+/* out[i] = round_T(program(x_0[i], ..., x_{n-1}[i])) for i < count: the body evaluated in f64 and
+ * rounded once at the store (the statement model, oracle/kernel_eval.rs:763-771; launch_cases.rs
+ * :14-27).  `ins` are n_inputs arrays of T already in the output's element order; `f64` picks T. */
+void orc_elementwise_f(const void* const* ins, int32_t n_inputs, int64_t count, int f64, const orc_rx* prog,
+                       int32_t len, void* out);
+
+/* An integer expression program (postfix): every node carries the integer kind it is evaluated
+ * at (ORC_K_*), as eval_int (oracle/kernel_eval.rs:809-848) passes the type down: an operand at the
+ * node's type, except a Cast's operand, a comparison's operands and a Select's condition, which
+ * the program compiler types by the operand's own type. */
+enum { ORC_K_I32 = 9, ORC_K_I64 = 10, ORC_K_U32 = 23, ORC_K_U64 = 24 };
+enum {
+  ORC_IX_INPUT = 1, ORC_IX_CONST, ORC_IX_CAST, ORC_IX_ADD, ORC_IX_SUB, ORC_IX_MUL, ORC_IX_DIV, ORC_IX_SHL,
+  ORC_IX_SHR, ORC_IX_MIN, ORC_IX_MAX, ORC_IX_AND, ORC_IX_OR, ORC_IX_XOR, ORC_IX_CMP, ORC_IX_SELECT
+};
+typedef struct orc_ix {
+  int32_t op;
+  int32_t arg;  /* INPUT: the input; CMP: 0 Eq, 1 Ne, 2 Lt, 3 Le, 4 Gt, 5 Ge */
+  int32_t kind; /* the kind the node's value is computed at */
+  int32_t pad;
+  int64_t v;    /* CONST: the literal */
+} orc_ix;
+/* Planted mistakes (tests only; 0 in every parity use): a zero divisor gives 0, MIN / -1
+ * saturates to MAX, a shift count at or past the width clamps (as PTX does) instead of wrapping,
+ * Shr is logical on a signed type, Div floors. */
+enum { ORC_MUT_DIV0 = 1, ORC_MUT_MINNEG1 = 2, ORC_MUT_CLAMP = 4, ORC_MUT_LOGICAL = 8, ORC_MUT_FLOOR = 16 };
+/* out[i] = program over the inputs' element i, each input an int64 array holding the compute
+ * kind's value (a U64 value as its bit pattern); the result is stored as the kind's value the same
+ * way. */
+void orc_elementwise_i(const int64_t* const* ins, int32_t n_inputs, int64_t count, const orc_ix* prog, int32_t len,
+                       int32_t mutant, int64_t* out);
+
 #endif

@@ -35,7 +35,7 @@ def test_backend_identity():
     b = u.HipBackend()
     assert b.name() == "hip"
     assert b.provider() == "unpopped-hip"
-    assert b.total_integer_ops() is False
+    assert b.total_integer_ops() is True
 
 
 def test_supports_dtype_is_target_conditional():
@@ -769,91 +769,46 @@ def test_gather_skeleton_follows_the_gather_lift():
 
 
 # ---------------------------------------------------------------------------------------
-# The shared launch_cases() corpus (launch_cases.rs:137-180)
+# The shared launch_cases() corpus (launch_cases.rs:137-180): launched elementwise lifts
 # ---------------------------------------------------------------------------------------
 
-def elementwise_launched(name: str, dtype: str, rank: int, body: dict, block: int, grid: int) -> dict:
-    """lift_elementwise_opdef_launched (kernel_lift.rs:145, grid_stride_outermost :256-285) for two
-    inputs: loads of in0/in1 at the counters, the body stored to out, the outermost loop grid-strided."""
-    r = rank
-    i32 = lambda v: {"ConstInt": [v, "I32"]}  # noqa: E731
-    coords = [{"Local": r + d} for d in range(r)]
-    inner = [{"Load": {"local": 2 * r + k, "place": {"Logical": {"buffer": k, "coords": coords}}}} for k in range(2)]
-    inner.append({"Store": {"place": {"Logical": {"buffer": 2, "coords": coords}}, "value": body}})
-    blk = inner
-    for d in reversed(range(r)):
-        blk = [{"For": {"local": r + d, "start": i32(0), "end": {"Local": d}, "step": i32(1), "unroll": "None",
-                        "body": blk}}]
-    cast = lambda e: {"Cast": [e, {"to": "I32", "round": "NearestEven", "sat": "Wrap"}]}  # noqa: E731
-    ex = lambda i: {"Exec": {i: 0}}  # noqa: E731
-    blk[0]["For"]["start"] = cast({"Add": [{"Mul": [ex("BlockIdx"), ex("BlockDim")]}, ex("ThreadIdx")]})
-    blk[0]["For"]["step"] = cast({"Mul": [ex("GridDim"), ex("BlockDim")]})
-    params = [{"name": f"in{k}", "kind": {"Buffer": {"elem": dtype, "role": "Read", "rank": r}}} for k in range(2)]
-    params.append({"name": "out", "kind": {"Buffer": {"elem": dtype, "role": "Write", "rank": r}}})
-    params += [{"name": f"n{d}", "kind": {"Scalar": {"ty": "I32", "local": d}}} for d in range(r)]
-    locals_ = [{"elem": "I32", "lanes": 1}] * (2 * r) + [{"elem": dtype, "lanes": 1}] * 2
-    return {"name": name, "compute": dtype, "params": params, "locals": locals_, "body": blk,
-            "launch": {"block": [block, 1, 1], "grid": [grid, 1, 1], "subgroup": None, "cluster": None,
-                       "devices": 1, "grid_dims": None},
-            "allocs": [], "result": None, "results": []}
+from tests.launch_corpus import corpus_args, elementwise_launched, launch_cases, over_inputs  # noqa: E402
 
 
-def launch_cases():
-    """The corpus's four cases: (name, dtype, shape, (block, grid), ulps, body, numpy reference)."""
-    a, b = {"Local": None}, None  # placeholders replaced per rank below
-    del a, b
+@pytest.mark.parametrize("case", launch_cases(), ids=lambda c: c[0])
+def test_launch_cases_corpus_lowers_and_runs_on_the_c_leg(case):
+    """Each launch_cases() kernel is lowered by lower_kernel as the launched elementwise lift: the lift
+    restated here builds the same tree (kernel_lift.rs:96-153), the interface names the lift and the
+    kernel's declared launch, and the source compiles for gfx950.  On the corpus's own inputs
+    (launch_cases.rs:72-99) the C99 leg agrees with the oracle within the case's ulps
+    (launch_cases.rs:14-27)."""
+    from oracle import cpuc
 
-    def case(name, dtype, shape, launch, ulps, body, ref):
-        r = len(shape)
-        la, lb = {"Local": 2 * r}, {"Local": 2 * r + 1}
-        return name, dtype, shape, launch, ulps, body(la, lb), ref
-
-    ab = lambda x: {"Unary": ["Abs", x]}  # noqa: E731
-    return [
-        case("fma_shape", "F32", (5, 7), (4, 2), 3, lambda x, y: {"Add": [{"Mul": [ab(x), ab(y)]}, ab(x)]},
-             lambda x, y: np.abs(x.astype(np.float64)) * np.abs(y) + np.abs(x)),
-        case("div", "F32", (6, 5), (8, 2), 0, lambda x, y: {"Div": [x, y]}, lambda x, y: x.astype(np.float64) / y),
-        case("sub", "I32", (3, 11), (8, 1), 0, lambda x, y: {"Sub": [x, y]}, lambda x, y: x - y),
-        case("add", "U32", (37,), (16, 3), 0, lambda x, y: {"Add": [x, y]}, lambda x, y: x + y),
-    ]
+    name, dtype, shape, (block, grid), ulps, body, _ = case
+    k = elementwise_launched(name, dtype, len(shape), body, block, grid)
+    r = len(shape)
+    b_in = over_inputs(body, r)
+    assert u.lift_elementwise(name, dtype, r, b_in, n_inputs=2, launch=(block, grid)) == k
+    g = u.HipBackend().lower_kernel(k)
+    assert g.interface["lift"] == "lift_elementwise_opdef_launched"
+    assert g.interface["form"] == "elementwise" and g.interface["dtype"] == dtype
+    assert g.interface["declared_launch"]["block"] == [block, 1, 1]
+    assert [e["symbol"][len(g.name):] for e in g.interface["entries"]] == ["_v", "_s", "_e"]
+    u.HipCompiler().compile(g.source, g.name)
+    x, y, out = corpus_args(dtype, shape)
+    want = oracle.elementwise([x, y], b_in, dtype)
+    assert want.any(), "the expected output is not the zeroed buffer (launch_cases.rs:196-203)"
+    assert cpuc.run(k, x, y, out, *shape) == cpuc.OK
+    if ulps == 0:
+        assert out.tobytes() == want.tobytes()
+    else:
+        ia, ib = out.view(np.int32).astype(np.int64), want.view(np.int32).astype(np.int64)
+        assert (np.abs(ia - ib) <= ulps).all()
 
 
 import numpy as np  # noqa: E402
 
-
-@pytest.mark.parametrize("case", launch_cases(), ids=lambda c: c[0])
-def test_launch_cases_corpus_is_refused_typed_and_runs_on_the_c_leg(case):
-    """Each launch_cases() kernel (a launched elementwise lift) is outside this backend's path: lower_kernel
-    refuses it with a typed UnsupportedKernel.  The C99 leg runs it within the corpus's stated ulps of the
-    f64-evaluated result (launch_cases.rs:14-27)."""
-    from oracle import cpuc
-
-    name, dtype, shape, (block, grid), ulps, body, ref = case
-    k = elementwise_launched(name, dtype, len(shape), body, block, grid)
-    with pytest.raises(_lib.UnpError) as e:
-        u.HipBackend().lower_kernel(k)
-    assert e.value.kind == "UnsupportedKernel"
-    rng = np.random.default_rng(7)
-    nt = {"F32": np.float32, "I32": np.int32, "U32": np.uint32}[dtype]
-    if dtype == "F32":
-        x = rng.normal(size=shape).astype(nt)
-        y = rng.normal(size=shape).astype(nt)
-        y.ravel()[::4] = 0  # zero denominators: inf and NaN agree
-    else:
-        info = np.iinfo(nt)
-        x = rng.integers(info.min, info.max, shape, dtype=np.int64, endpoint=True).astype(nt)
-        y = rng.integers(info.min, info.max, shape, dtype=np.int64, endpoint=True).astype(nt)
-    out = np.zeros(shape, nt)
-    assert cpuc.run(k, x, y, out, *shape) == cpuc.OK
-    with np.errstate(all="ignore"):
-        want = ref(x, y)
-    if dtype == "F32":
-        w32 = want.astype(np.float32)
-        same = (out == w32) | (np.isnan(out) & np.isnan(w32))
-        ia, ib = out.view(np.int32).astype(np.int64), w32.view(np.int32).astype(np.int64)
-        assert (same | (np.abs(ia - ib) <= ulps)).all()
-    else:
-        assert np.array_equal(out, want.astype(nt))
+import oracle  # noqa: E402
 
 
 # ---------------------------------------------------------------------------------------

@@ -225,6 +225,24 @@ def lift_gather(name: str, dtype: str, rank: int, index_dtype: str = "I32", axis
                                                           b, g, o, e))
 
 
+def lift_elementwise(name: str, dtype: str, rank: int, body, n_inputs: int = 1, perms=None,
+                     launch: tuple | None = None) -> dict:
+    """The Access::Elementwise lift (kernel_lift.rs:96-153; serial, or launched on ``launch = (block,
+    grid)``) as a KernelFn dict: ``body`` over ``Input(0..n_inputs)`` (an ``expr.Expr`` or its serde
+    dict) stored at the output coordinate.  ``perms`` (one axis list per input, or None) reads input k
+    through View::Permute: iteration axis d reads its axis ``perms[k][d]``."""
+    from . import expr as X
+
+    b, g = _geom(launch)
+    bj = json.dumps(X.as_json(body)).encode()
+    pp = None
+    if perms is not None:
+        flat = [int(a) for p in perms for a in p]
+        pp = (C.c_int32 * max(1, len(flat)))(*flat)
+    return _lifted(lambda o, e: _lib.lib().unp_lift_elementwise(name.encode(), ELEMENT_KINDS[dtype], rank, n_inputs,
+                                                               bj, pp, b, g, o, e))
+
+
 def kernel_row_reduce2(name: str, dtype: str, op0: str = "Sum", op1: str = "Max", launch: tuple | None = None) -> dict:
     b, g = _geom(launch)
     return _lifted(lambda o, e: _lib.lib().unp_kernel_row_reduce2(name.encode(), ELEMENT_KINDS[dtype],

@@ -100,6 +100,8 @@ def lib() -> C.CDLL:
         "unp_lift_scan_x": (i32, [C.c_char_p, i32, i32, i32, i32, i32, i32, i32, C.c_char_p, C.c_char_p, u32, u32,
                                   C.POINTER(C.c_void_p), E]),
         "unp_lift_gather": (i32, [C.c_char_p, i32, i32, i32, i32, i32, u32, u32, C.POINTER(C.c_void_p), E]),
+        "unp_lift_elementwise": (i32, [C.c_char_p, i32, i32, i32, C.c_char_p, C.POINTER(i32), u32, u32,
+                                       C.POINTER(C.c_void_p), E]),
         "unp_lift_gather_x": (i32, [C.c_char_p, i32, i32, i32, i32, i32, i32, i32, i32, C.c_char_p, u32, u32,
                                     C.POINTER(C.c_void_p), E]),
         "unp_kernel_row_reduce2": (i32, [C.c_char_p, i32, i32, i32, u32, u32, C.POINTER(C.c_void_p), E]),

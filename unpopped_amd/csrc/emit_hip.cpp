@@ -82,6 +82,9 @@ const char* lower_name(int32_t kind) {
     case UNP_I32: return "i32";
     case UNP_I64: return "i64";
     case UNP_U32: return "u32";
+    case UNP_U64: return "u64";
+    case UNP_I16: return "i16";
+    case UNP_U16: return "u16";
     case UNP_BF16: return "bf16";
     case UNP_F16: return "f16";
     case UNP_U4: return "u4";
@@ -1061,6 +1064,165 @@ bool expr_cpp(const kir::J& e, const char* T, std::string& out, std::string& why
   return false;
 }
 
+// ---- integer expressions (oracle/kernel_eval.rs:809-848, 1114-1175) ---------------------------
+
+// The C++ type of an integer compute kind this backend spells expressions at.
+const char* int_ctype(int32_t kind) {
+  switch (kind) {
+    case UNP_I32: return "int";
+    case UNP_I64: return "long long";
+    case UNP_U32: return "unsigned int";
+    case UNP_U64: return "unsigned long long";
+    default: return nullptr;
+  }
+}
+
+// The type of an expression node under an integer compute dtype (types.rs:679-751 for the nodes
+// the integer evaluator takes): an Input is the compute dtype, a ConstInt its own kind, a Cast its
+// target, arithmetic its operands' common type, a comparison the compute dtype's 0/1, a Select its
+// arms'.  -1 for a node outside that subset or operands of different types.
+int32_t int_node_type(const kir::J& e, int32_t compute) {
+  using kir::J;
+  if (e.t != J::Obj || e.o.size() != 1) return -1;
+  const std::string& tag = e.o[0].first;
+  const J& p = e.o[0].second;
+  if (tag == "Input") return compute;
+  if (tag == "ConstInt") return p.t == J::Arr && p.a.size() == 2 && p.a[1].t == J::Str ? kind_from_name(p.a[1].s) : -1;
+  if (tag == "Cast") {
+    const J* to = p.t == J::Arr && p.a.size() == 2 ? p.a[1].get("to") : nullptr;
+    return to && to->t == J::Str ? kind_from_name(to->s) : -1;
+  }
+  auto same = [&](const J& a, const J& b) {
+    const int32_t x = int_node_type(a, compute), y = int_node_type(b, compute);
+    return x == y ? x : -1;
+  };
+  if (tag == "Add" || tag == "Sub" || tag == "Mul" || tag == "Div")
+    return p.t == J::Arr && p.a.size() == 2 ? same(p.a[0], p.a[1]) : -1;
+  if (tag == "Binary") {
+    if (p.t != J::Arr || p.a.size() != 3 || p.a[0].t != J::Str) return -1;
+    const int32_t t = same(p.a[1], p.a[2]);
+    return t >= 0 && p.a[0].s.compare(0, 3, "Cmp") == 0 ? compute : t;
+  }
+  if (tag == "Select") return p.t == J::Arr && p.a.size() == 3 ? same(p.a[1], p.a[2]) : -1;
+  return -1;
+}
+
+// An integer expression spelled at the integer kind `t` as the reference's kernel evaluator
+// computes it (eval_int, kernel_eval.rs:809-848): every operand at `t` except a Cast's operand, a
+// comparison's operands and a Select's condition, which are read at their own type.  The total
+// rule of docs/int-div-shift-semantics.md (rules 1-3) is in the device library's unp::xi helpers:
+// Add/Sub/Mul wrap, a zero divisor and signed MIN / -1 give the dividend, shift counts are taken
+// modulo the width.  A ConstInt is its value wrapped to `t` (kernel_eval.rs:1165-1174).
+bool int_expr_cpp(const kir::J& e, int32_t t, int32_t compute, std::string& out, std::string& why) {
+  using kir::J;
+  const char* T = int_ctype(t);
+  if (!T) {
+    why = std::string("an integer expression at ") + (kind_name(t) ? kind_name(t) : "an unknown kind");
+    return false;
+  }
+  if (e.t != J::Obj || e.o.size() != 1) {
+    why = "a malformed ScalarExpr";
+    return false;
+  }
+  const std::string& tag = e.o[0].first;
+  const J& p = e.o[0].second;
+  auto at = [&](const J& x, int32_t ty, std::string& o) { return int_expr_cpp(x, ty, compute, o, why); };
+  auto own = [&](const J& x, std::string& o) {
+    const int32_t ty = int_node_type(x, compute);
+    if (!int_ctype(ty)) {
+      if (why.empty()) why = "an operand outside the integer kinds I32, I64, U32 and U64";
+      return false;
+    }
+    return at(x, ty, o);
+  };
+  if (tag == "Input") {
+    if (!p.is_int || p.i < 0 || t != compute) {
+      why = "a malformed Input";
+      return false;
+    }
+    out = "x[" + std::to_string(p.i) + "]";
+    return true;
+  }
+  if (tag == "ConstInt") {
+    if (p.t != J::Arr || p.a.size() != 2 || !p.a[0].is_int) {
+      why = "a ConstInt outside the 64-bit signed range";
+      return false;
+    }
+    const int64_t v = p.a[0].i;
+    char buf[64];
+    if (t == UNP_I32) std::snprintf(buf, sizeof buf, "(int)(%d)", (int)(int32_t)(uint32_t)(uint64_t)v);
+    else if (t == UNP_U32) std::snprintf(buf, sizeof buf, "(unsigned int)%uu", (unsigned)(uint32_t)(uint64_t)v);
+    else if (t == UNP_U64) std::snprintf(buf, sizeof buf, "(unsigned long long)%lluull", (unsigned long long)(uint64_t)v);
+    else if (v == INT64_MIN) std::snprintf(buf, sizeof buf, "(-9223372036854775807ll - 1ll)");
+    else std::snprintf(buf, sizeof buf, "(long long)(%lldll)", (long long)v);
+    out = buf;
+    return true;
+  }
+  if (tag == "Cast") {
+    // An integer-to-integer wrap to `t` (a Cast to another type is a mixed expression).
+    const J* sat = p.t == J::Arr && p.a.size() == 2 ? p.a[1].get("sat") : nullptr;
+    if (int_node_type(e, compute) != t || !sat || sat->t != J::Str || sat->s != "Wrap") {
+      why = "a Cast other than an integer wrap to the expression's type";
+      return false;
+    }
+    std::string a;
+    if (!own(p.a[0], a)) return false;
+    out = "(" + std::string(T) + ")(" + a + ")";
+    return true;
+  }
+  std::string a, b, c;
+  if (tag == "Add" || tag == "Sub" || tag == "Mul" || tag == "Div") {
+    if (p.t != J::Arr || p.a.size() != 2 || !at(p.a[0], t, a) || !at(p.a[1], t, b)) return false;
+    std::string fn = tag == "Add" ? "add" : tag == "Sub" ? "sub" : tag == "Mul" ? "mul" : "div";
+    out = "unp::xi::" + fn + "<" + T + ">(" + a + ", " + b + ")";
+    return true;
+  }
+  if (tag == "Binary") {
+    if (p.t != J::Arr || p.a.size() != 3 || p.a[0].t != J::Str) {
+      why = "a malformed Binary";
+      return false;
+    }
+    const std::string& op = p.a[0].s;
+    static const struct {
+      const char* op;
+      const char* fn;
+    } ib[] = {{"Shl", "shl"}, {"Shr", "shr"}, {"Min", "min"}, {"Max", "max"},
+              {"BitAnd", "bit_and"}, {"BitOr", "bit_or"}, {"BitXor", "bit_xor"}};
+    for (const auto& u : ib)
+      if (op == u.op) {
+        if (!at(p.a[1], t, a) || !at(p.a[2], t, b)) return false;
+        out = std::string("unp::xi::") + u.fn + "<" + T + ">(" + a + ", " + b + ")";
+        return true;
+      }
+    static const struct {
+      const char* op;
+      const char* c;
+    } cmp[] = {{"CmpEq", "=="}, {"CmpNe", "!="}, {"CmpLt", "<"}, {"CmpLe", "<="}, {"CmpGt", ">"}, {"CmpGe", ">="}};
+    for (const auto& u : cmp)
+      if (op == u.op) {
+        // eval_cmp (kernel_eval.rs:871-882): both operands at their own (common) type, 1 or 0.
+        if (int_node_type(p.a[1], compute) != int_node_type(p.a[2], compute)) {
+          why = "a comparison of operands of different types";
+          return false;
+        }
+        if (!own(p.a[1], a) || !own(p.a[2], b)) return false;
+        out = "(" + std::string(T) + ")((" + a + ") " + u.c + " (" + b + ") ? 1 : 0)";
+        return true;
+      }
+    why = "the integer binary op " + op;
+    return false;
+  }
+  if (tag == "Select") {
+    // eval_int_select (kernel_eval.rs:850-860): the condition at its own type tested != 0, then
+    // one arm evaluated at `t`.
+    if (p.t != J::Arr || p.a.size() != 3 || !own(p.a[0], c) || !at(p.a[1], t, a) || !at(p.a[2], t, b)) return false;
+    out = "((" + c + ") != 0 ? (" + a + ") : (" + b + "))";
+    return true;
+  }
+  why = "the integer expression node " + tag;
+  return false;
+}
+
 // True when evaluating `e` costs a library call or a division in f64: the per-element value
 // is then worth holding in registers between a stage and the epilogue.
 bool costly(const kir::J& e) {
@@ -1238,6 +1400,190 @@ int32_t lower_gather_x(const unp_form& f, const GatherExpr& gx, Lowered& L, std:
     << json_str(leaf ? "a raw bit move: bit-exact for every grid and block"
                      : "the body evaluated in f64 and rounded once at the store, as the oracle evaluates a statement; "
                        "bit-exact against the oracle")
+    << "]}";
+  L.interface_json = j.str();
+  return UNP_OK;
+}
+
+// An Access::Elementwise lift (kernel_lift.rs:96-153): out[c] = body(in0[c], ..., in(n-1)[c]) at
+// every output coordinate c, input k read through its axis permutation when it has one.  The cell
+// follows the oracle's statement model (launch_cases.rs:14-27): a float body is evaluated in f64 and
+// rounded once at the store (bit-exact against the oracle, so 0 ULPs on every corpus case, the
+// IEEE-rounded divide included); an integer body at I32/I64/U32/U64 by the total rule (unp::xi);
+// a body that is one input moves that input's bits at any element kind of whole bytes.
+// Entries: `_v` streams 16-byte packs when every buffer is dense, unpermuted and 16-byte aligned,
+// `_s` the same element by element at any alignment, and `_e` walks each buffer through its own
+// strides (a permuted input, or storage images that are not dense row-major).
+int32_t lower_elementwise(const unp_form& f, const ElementwiseExpr& ew, Lowered& L, std::string& why) {
+  L = Lowered{};
+  L.form = f;
+  L.form.kind = UNP_FORM_ELEMENTWISE;
+  L.ew = ew;
+  const int32_t n = ew.n_inputs;
+  if (f.rank < 1 || f.rank > 8 || n < 1 || n > 8) {
+    why = "an elementwise op of 1 to 8 inputs at rank 1 to 8";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (!ew.perms.empty() && ew.perms.size() != (size_t)n) {
+    why = "an ill-formed view";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  const kir::J& b = ew.body;
+  const bool leaf = b.t == kir::J::Obj && b.o.size() == 1 && b.o[0].first == "Input" && b.o[0].second.is_int;
+  const size_t eb = kind_bytes(f.dtype);
+  std::string T, cell;
+  const bool is_float = f.dtype == UNP_F32 || f.dtype == UNP_F64;
+  if (leaf) {
+    if (eb == 0) {
+      why = "an elementwise op over a sub-byte element kind";
+      return UNP_UNSUPPORTED_DTYPE;
+    }
+    T = eb == 1 ? "unsigned char" : eb == 2 ? "unsigned short" : eb == 4 ? "unsigned int" : eb == 8 ? "unsigned long long" : "uint4";
+    cell = "  return a[" + std::to_string(b.o[0].second.i) + "];\n";
+  } else if (is_float) {
+    T = ctype(f.dtype);
+    std::string e;
+    if (!expr_cpp(b, T.c_str(), e, why)) {
+      why = "body: " + why + " has no spelling here";
+      return UNP_UNSUPPORTED_OP;
+    }
+    cell = "  double x[" + std::to_string(n) + "];\n  for (int k = 0; k < " + std::to_string(n) +
+           "; ++k) x[k] = (double)a[k];\n  return (" + T + ")(" + e + ");\n";
+  } else if (int_ctype(f.dtype)) {
+    T = int_ctype(f.dtype);
+    std::string e;
+    if (int_node_type(b, f.dtype) != f.dtype) {
+      why = "body: an integer expression whose type is not the compute dtype (or a node outside the integer "
+            "evaluator's subset: ConstInt, Cast, Add, Sub, Mul, Div, Shl, Shr, Min, Max, BitAnd, BitOr, BitXor, "
+            "comparisons and Select)";
+      return UNP_UNSUPPORTED_OP;
+    }
+    if (!int_expr_cpp(b, f.dtype, f.dtype, e, why)) {
+      why = "body: " + why + " has no spelling here";
+      return UNP_UNSUPPORTED_OP;
+    }
+    cell = "  const " + T + "* x = a;\n  return " + e + ";\n";
+  } else {
+    why = std::string("an elementwise body at ") + (kind_name(f.dtype) ? kind_name(f.dtype) : "an unknown kind") +
+          " (bodies are spelled at F32, F64, I32, I64, U32 and U64; a single-input body at any whole-byte kind)";
+    return UNP_UNSUPPORTED_DTYPE;
+  }
+  std::string perm_text;
+  for (const auto& p : ew.perms) {
+    perm_text += "[";
+    for (size_t d = 0; d < p.size(); ++d) perm_text += (d ? "," : "") + std::to_string(p[d]);
+    perm_text += "]";
+  }
+  const int vec = eb && eb <= 16 ? (int)(16 / eb) : 1;
+  std::ostringstream name;
+  name << "unp_ew" << n << "_" << lower_name(f.dtype) << "_" << std::hex
+       << (fnv1a64(kir::write(b) + "|" + perm_text + "|" + std::to_string(f.rank)) & 0xffffffffu);
+  L.name = name.str();
+  L.threads = 256;
+  L.blocks_per_cu = 8;
+  const std::string N = std::to_string(n);
+  auto loads = [&](const std::string& idx_of_k) {
+    std::string s = "{";
+    for (int k = 0; k < n; ++k) {
+      std::string ix = idx_of_k;
+      for (size_t at = ix.find('#'); at != std::string::npos; at = ix.find('#')) ix.replace(at, 1, std::to_string(k));
+      s += (k ? ", " : "") + ix;
+    }
+    return s + "}";
+  };
+  auto params = [&]() {
+    std::string s;
+    for (int k = 0; k < n; ++k) s += "const void* in" + std::to_string(k) + ", ";
+    return s + "void* out";
+  };
+  std::ostringstream src;
+  src << header(L.name, L.form) << "namespace {\n"
+      << "using ew_t = " << T << ";\n"
+      << "__device__ __forceinline__ ew_t ew_cell(const ew_t (&a)[" << N << "]) {\n"
+      << cell << "}\n"
+      << "struct alignas(16) ew_pack { ew_t e[" << vec << "]; };\n"
+      << "}  // namespace\n";
+  const std::string V = L.name + "_v", S = L.name + "_s", E = L.name + "_e";
+  src << "extern \"C\" __global__ void " << kLaunchBounds << " " << V << "(" << params() << ", long long n) {\n"
+      << "  const long long stride = (long long)gridDim.x * blockDim.x;\n"
+      << "  const long long t0 = (long long)blockIdx.x * blockDim.x + threadIdx.x;\n"
+      << "  const long long np = n / " << vec << ";\n"
+      << "  for (long long i = t0; i < np; i += stride) {\n";
+  for (int k = 0; k < n; ++k)
+    src << "    const ew_pack p" << k << " = static_cast<const ew_pack*>(in" << k << ")[i];\n";
+  src << "    ew_pack o;\n"
+      << "#pragma unroll\n"
+      << "    for (int j = 0; j < " << vec << "; ++j) {\n"
+      << "      const ew_t a[" << N << "] = " << loads("p#.e[j]") << ";\n"
+      << "      o.e[j] = ew_cell(a);\n"
+      << "    }\n"
+      << "    static_cast<ew_pack*>(out)[i] = o;\n"
+      << "  }\n"
+      << "  for (long long i = np * " << vec << " + t0; i < n; i += stride) {\n"
+      << "    const ew_t a[" << N << "] = " << loads("static_cast<const ew_t*>(in#)[i]") << ";\n"
+      << "    static_cast<ew_t*>(out)[i] = ew_cell(a);\n"
+      << "  }\n}\n";
+  src << "extern \"C\" __global__ void " << kLaunchBounds << " " << S << "(" << params() << ", long long n) {\n"
+      << "  const long long stride = (long long)gridDim.x * blockDim.x;\n"
+      << "  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {\n"
+      << "    const ew_t a[" << N << "] = " << loads("static_cast<const ew_t*>(in#)[i]") << ";\n"
+      << "    static_cast<ew_t*>(out)[i] = ew_cell(a);\n"
+      << "  }\n}\n";
+  // The strided entry: v.ext the output's extents, v.ostr its strides, v.istr[k] input k's strides
+  // over the output's axes (a permuted input's strides already permuted by the host).
+  src << "extern \"C\" __global__ void " << kLaunchBounds << " " << E << "(" << params()
+      << ", unp::gather_x_view v) {\n"
+      << "  const long long stride = (long long)gridDim.x * blockDim.x;\n"
+      << "  for (long long o = (long long)blockIdx.x * blockDim.x + threadIdx.x; o < v.outs; o += stride) {\n"
+      << "    long long q = o, oo = 0, off[" << N << "] = {};\n"
+      << "    for (long long d = v.rank - 1; d >= 0; --d) {\n"
+      << "      const long long c = q % v.ext[d];\n"
+      << "      q /= v.ext[d];\n"
+      << "      oo += c * v.ostr[d];\n"
+      << "#pragma unroll\n"
+      << "      for (int k = 0; k < " << N << "; ++k) off[k] += c * v.istr[k][d];\n"
+      << "    }\n"
+      << "    const ew_t a[" << N << "] = " << loads("static_cast<const ew_t*>(in#)[off[#]]") << ";\n"
+      << "    static_cast<ew_t*>(out)[oo] = ew_cell(a);\n"
+      << "  }\n}\n";
+  Entry ev;
+  ev.symbol = V;
+  ev.fast = true;
+  ev.vec = vec;
+  Entry es = ev;
+  es.symbol = S;
+  es.fast = false;
+  es.vec = 1;
+  Entry ee = es;
+  ee.symbol = E;
+  ee.strided = true;
+  L.entries = {ev, es, ee};
+  L.source = src.str();
+  std::ostringstream j;
+  j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"elementwise\",\"dtype\":\"" << kind_name(f.dtype)
+    << "\",\"rank\":" << f.rank << ",\"inputs\":" << n << ",\"body\":" << json_str(kir::write(b)) << ",\"views\":[";
+  for (size_t k = 0; k < ew.perms.size(); ++k) {
+    j << (k ? "," : "") << "{\"Permute\":{\"perm\":[";
+    for (size_t d = 0; d < ew.perms[k].size(); ++d) j << (d ? "," : "") << ew.perms[k][d];
+    j << "]}}";
+  }
+  j << "],\"params\":[";
+  for (int k = 0; k < n; ++k)
+    j << "{\"name\":\"in" << k << "\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\"" << kind_name(f.dtype) << "\"},";
+  j << "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\",\"dtype\":\"" << kind_name(f.dtype) << "\"}";
+  for (int d = 0; d < f.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
+  j << "],\"launch\":{\"block\":[256,1,1],\"grid\":\"min(cu_count*8, the lanes the elements need)\",\"grid_policy\":"
+       "\"lanes stride over the elements (16-byte packs on the _v entry)\"},\"entries\":["
+    << "{\"symbol\":\"" << V << "\",\"when\":\"every buffer dense row-major, no permuted input, every base 16-byte aligned\"},"
+    << "{\"symbol\":\"" << S << "\",\"when\":\"every buffer dense row-major and no permuted input, any alignment\"},"
+    << "{\"symbol\":\"" << E << "\",\"when\":\"a permuted input, or storage images that are not dense row-major\"}]"
+    << ",\"workspace\":null,\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
+    << ",\"fidelity_notes\":["
+    << json_str(leaf ? "a raw bit move: bit-exact for every grid and block"
+                : is_float ? "the body evaluated in f64 and rounded once at the store, as the oracle evaluates a "
+                             "statement: bit-exact against the oracle (0 ULPs, the divide IEEE-rounded)"
+                           : "integer arithmetic by the total rule (Add/Sub/Mul wrap; a zero divisor and signed MIN / -1 "
+                             "give the dividend; shift counts modulo the width): bit-exact against the oracle")
     << "]}";
   L.interface_json = j.str();
   return UNP_OK;
@@ -1702,6 +2048,9 @@ int32_t lower_form(const unp_form& f, Lowered& out, std::string& detail) {
       return lower_dequant_gemm(f, out, detail);
     case UNP_FORM_ROW_REDUCE:
       detail = "a row reduction's expressions come only with its KernelFn (Backend::lower_kernel)";
+      return UNP_UNSUPPORTED_KERNEL;
+    case UNP_FORM_ELEMENTWISE:
+      detail = "an elementwise op's body comes only with its KernelFn (Backend::lower_kernel)";
       return UNP_UNSUPPORTED_KERNEL;
     default:
       detail = "an unknown form";

@@ -3075,6 +3075,45 @@ UNP_DEV double rem_floor(double a, double b) { return a - floor(a / b) * b; }
 UNP_DEV double select(double c, double a, double b) { return c != 0.0 ? a : b; }
 }  // namespace xf
 
+namespace xi {
+// Integer arithmetic at I32, I64, U32 and U64 by the total rule of the reference's kernel
+// evaluator (oracle/kernel_eval.rs:1114-1175, docs/int-div-shift-semantics.md rules 1-3).  Add,
+// Sub and Mul wrap: they run on the unsigned type of the width and convert back.  A zero divisor
+// gives the dividend; so does signed MIN / -1 (a signed divisor of -1 is the wrapping negation,
+// which is the quotient for every other dividend).  A shift count's bits are read as unsigned and
+// taken modulo the width (32, or 64 for a 64-bit type); Shl shifts the unsigned bits (no overflow
+// for a negative or large value), Shr is arithmetic on a signed type and logical on an unsigned
+// one.  Min, Max and the bitwise ops act on the type's values.
+template <class T> struct ibits;
+template <> struct ibits<int> { using U = unsigned int; static constexpr bool sgn = true; static constexpr unsigned w = 32; };
+template <> struct ibits<unsigned int> { using U = unsigned int; static constexpr bool sgn = false; static constexpr unsigned w = 32; };
+template <> struct ibits<long long> { using U = unsigned long long; static constexpr bool sgn = true; static constexpr unsigned w = 64; };
+template <> struct ibits<unsigned long long> {
+  using U = unsigned long long;
+  static constexpr bool sgn = false;
+  static constexpr unsigned w = 64;
+};
+template <class T> UNP_DEV T add(T a, T b) { using U = typename ibits<T>::U; return (T)((U)a + (U)b); }
+template <class T> UNP_DEV T sub(T a, T b) { using U = typename ibits<T>::U; return (T)((U)a - (U)b); }
+template <class T> UNP_DEV T mul(T a, T b) { using U = typename ibits<T>::U; return (T)((U)a * (U)b); }
+template <class T> UNP_DEV T div(T a, T b) {
+  using U = typename ibits<T>::U;
+  if (b == (T)0) return a;
+  if constexpr (ibits<T>::sgn) {
+    if (b == (T)-1) return (T)((U)0 - (U)a);
+  }
+  return (T)(a / b);
+}
+template <class T> UNP_DEV unsigned count(T c) { return (unsigned)((typename ibits<T>::U)c & (ibits<T>::w - 1u)); }
+template <class T> UNP_DEV T shl(T a, T c) { using U = typename ibits<T>::U; return (T)((U)a << count(c)); }
+template <class T> UNP_DEV T shr(T a, T c) { return (T)(a >> count(c)); }
+template <class T> UNP_DEV T min(T a, T b) { return a < b ? a : b; }
+template <class T> UNP_DEV T max(T a, T b) { return a > b ? a : b; }
+template <class T> UNP_DEV T bit_and(T a, T b) { return (T)(a & b); }
+template <class T> UNP_DEV T bit_or(T a, T b) { return (T)(a | b); }
+template <class T> UNP_DEV T bit_xor(T a, T b) { return (T)(a ^ b); }
+}  // namespace xi
+
 template <class T, int NI, int NS, class OPS, int THREADS, int VEC, int R, int S>
 UNP_DEV void rr_stage(const T* const* rin, const vec<T, VEC> (&xr)[NI][R > 0 ? R : 1], i64 cols, double (&red)[NS],
                       double* part, double* redsh, double (&cv)[R > 0 ? R : 1][VEC]) {

@@ -3,8 +3,9 @@
 //
 // Each lift builds exactly the KernelFn the reference's lift builds (same statements, locals,
 // parameters, launch shape and shared allocations), for the op forms this backend lowers:
-// reductions and scans of n inputs with a pre-map body and a fused post, the fused row folds,
-// RowReduce, gathers with a body, and the int4 dequant forms.  lower_kernel recognises a kernel by lifting
+// elementwise ops of n inputs (permuted reads included), reductions and scans of n inputs with a
+// pre-map body and a fused post, the fused row folds, RowReduce, gathers with a body, and the int4
+// dequant forms.  lower_kernel recognises a kernel by lifting
 // every candidate form its signature admits and comparing the trees: a kernel equal to a lift's
 // output is that form; anything else is refused with UnsupportedKernel (refuse rather than
 // approximate, crates/unpopped/src/backend.rs:703-707).
@@ -600,6 +601,60 @@ J lift_gather(const std::string& name, int32_t dtype, int32_t rank, int32_t idx,
   for (uint32_t k = 0; k < n; ++k) locals.push_back(local_decl(elem(k)));
   locals.push_back(local_decl(EK(idx)));  // src_extent
   locals.push_back(local_decl(EK(idx)));  // clamped index
+  J k = kernel_fn(name, EK(dtype), params, locals, body, J::null(), {});
+  if (block || grid) grid_stride(k, block, grid);
+  return k;
+}
+
+// lift_elementwise_opdef (kernel_lift.rs:96-130) and lift_elementwise_opdef_launched (:145-153):
+// n inputs loaded at the loop counters into locals 2r..2r+n (input k through its axis permutation
+// perms[k] when given: the counter of iteration axis d is the coordinate on the input's axis
+// perms[k][d], counter_place :315-324), then `body` with Input(k) bound to those locals stored at
+// the counters; the loops nest axis 0 outermost.  The signature (elementwise_signature :328-343):
+// the inputs, the output, one I32 extent per axis; locals: the extents, the counters, one loaded
+// value per input.  Launched by grid_stride.
+J lift_elementwise(const std::string& name, int32_t dtype, int32_t rank, uint32_t n, const J& body_expr,
+                   const std::vector<std::vector<int32_t>>& perms, uint32_t block, uint32_t grid) {
+  check_rank(rank);
+  if (n < 1 || n > 8) throw Decline{"UnsupportedForm: an elementwise op of 1 to 8 inputs"};
+  if (!kind_name(dtype)) throw Decline{"UnsupportedForm: an unknown element kind"};
+  check_post(body_expr, 0, (int64_t)n);  // leaves_ok: the inputs and constants only
+  const uint32_t r = (uint32_t)rank;
+  if (!perms.empty()) {
+    // check_plain_with (kernel_lift.rs:380-390): one view per input, each a permutation of the axes.
+    if (perms.size() != n) throw Decline{"UnsupportedForm: an ill-formed view"};
+    for (const auto& p : perms) {
+      if (p.size() != r) throw Decline{"UnsupportedForm: an ill-formed view"};
+      uint32_t seen = 0;
+      for (int32_t a : p) {
+        if (a < 0 || a >= rank || ((seen >> a) & 1u)) throw Decline{"UnsupportedForm: an ill-formed view"};
+        seen |= 1u << a;
+      }
+    }
+  }
+  auto counters = [&](uint32_t buffer, const std::vector<int32_t>* perm) {
+    std::vector<J> c(r);
+    for (uint32_t d = 0; d < r; ++d) c[perm ? (uint32_t)(*perm)[d] : d] = loc(r + d);
+    return p_logical(buffer, c);
+  };
+  std::vector<J> inner;
+  for (uint32_t k = 0; k < n; ++k) inner.push_back(s_load(2 * r + k, counters(k, perms.empty() ? nullptr : &perms[k])));
+  const J value = map_leaves(body_expr, [&](const J& x, J& o) {
+    if (x.t == J::Obj && x.o.size() == 1 && x.o[0].first == "Input") {
+      o = loc(2 * r + (uint32_t)leaf_index(x));
+      return true;
+    }
+    return false;
+  });
+  inner.push_back(s_store(counters(n, nullptr), value));
+  std::vector<J> body = inner;
+  for (int d = (int)r - 1; d >= 0; --d) body = {s_for(r + d, int_(0), loc((uint32_t)d), int_(1), body)};
+  std::vector<J> params, locals;
+  for (uint32_t k = 0; k < n; ++k) params.push_back(param_buffer("in" + std::to_string(k), EK(dtype), "Read", rank));
+  params.push_back(param_buffer("out", EK(dtype), "Write", rank));
+  for (uint32_t d = 0; d < r; ++d) params.push_back(param_scalar("n" + std::to_string(d), "I32", d));
+  for (uint32_t i = 0; i < 2 * r; ++i) locals.push_back(local_decl("I32"));
+  for (uint32_t k = 0; k < n; ++k) locals.push_back(local_decl(EK(dtype)));
   J k = kernel_fn(name, EK(dtype), params, locals, body, J::null(), {});
   if (block || grid) grid_stride(k, block, grid);
   return k;
@@ -1332,6 +1387,88 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
   if (nin >= 1 && nin <= 8) {
     const int32_t dt = ps[0].elem, r = ps[0].rank, orank = ps[nin].rank;
     const uint32_t n = (uint32_t)nin;
+    // Elementwise (kernel_lift.rs:96-153): the body read back from the output store (the loaded
+    // locals unbound to Input(k)) and each input's permutation from its load's coordinates, in the
+    // lift's numbering of locals; the lift re-run with them and compared as a whole.
+    if (orank == r && ps[nin].elem == dt) {
+      auto ew_extract = [&](const J& kk, J& body, std::vector<std::vector<int32_t>>& perms) {
+        const J& kb = *kk.get("body");
+        const J* store = find_stmt(kb, [&](const J& x) {
+          const J* st = x.get("Store");
+          const J* pl = st ? st->get("place") : nullptr;
+          const J* lg = pl ? pl->get("Logical") : nullptr;
+          return lg && lg->get("buffer") && lg->get("buffer")->is_int && lg->get("buffer")->i == (int64_t)n;
+        });
+        if (!store) return false;
+        bool ok = true;
+        try {
+          body = map_leaves(*store->get("Store")->get("value"), [&](const J& x, J& o) {
+            if (x.t != J::Obj || x.o.size() != 1 || x.o[0].first != "Local") return false;
+            const int64_t l = leaf_index(x);
+            if (l >= 2 * (int64_t)r && l < 2 * (int64_t)r + (int64_t)n) {
+              o = input_leaf((uint32_t)(l - 2 * r));
+            } else {
+              ok = false;
+              o = x;
+            }
+            return true;
+          });
+        } catch (const Decline&) {
+          return false;
+        }
+        if (!ok) return false;
+        perms.assign(n, std::vector<int32_t>());
+        bool any = false;
+        for (uint32_t kk2 = 0; kk2 < n; ++kk2) {
+          const J* ld = find_stmt(kb, [&](const J& x) {
+            const J* l = x.get("Load");
+            return l && l->get("local") && l->get("local")->is_int && l->get("local")->i == (int64_t)(2 * r + kk2);
+          });
+          const J* pl = ld ? ld->get("Load")->get("place") : nullptr;
+          const J* lg = pl ? pl->get("Logical") : nullptr;
+          const J* cs = lg ? lg->get("coords") : nullptr;
+          if (!cs || cs->t != J::Arr || cs->a.size() != (size_t)r) return false;
+          std::vector<int32_t> p((size_t)r, -1);
+          for (int32_t a = 0; a < r; ++a) {
+            const J& c = cs->a[(size_t)a];
+            if (c.t != J::Obj || c.o.size() != 1 || c.o[0].first != "Local") return false;
+            const int64_t d = leaf_index(c) - r;
+            if (d < 0 || d >= r || p[(size_t)d] != -1) return false;
+            p[(size_t)d] = a;
+          }
+          for (int32_t d = 0; d < r; ++d) any = any || p[(size_t)d] != d;
+          perms[kk2] = p;
+        }
+        if (!any) perms.clear();
+        return true;
+      };
+      auto take_elementwise = [&](const J& b, const std::vector<std::vector<int32_t>>& pm) {
+        out.form.kind = UNP_FORM_ELEMENTWISE;
+        out.form.dtype = dt;
+        out.form.rank = r;
+        out.ew.n_inputs = (int32_t)n;
+        out.ew.body = b;
+        out.ew.perms = pm;
+        out.lift = block ? "lift_elementwise_opdef_launched" : "lift_elementwise_opdef";
+        return UNP_OK;
+      };
+      J eb, kr;
+      std::vector<std::vector<int32_t>> ep;
+      if (ew_extract(k, eb, ep) && attempt([&] { return lift_elementwise(name, dt, r, n, eb, ep, block, grid); }))
+        return take_elementwise(eb, ep);
+      // Locals numbered otherwise: renumbered into the lift's own numbering first (the loads
+      // define the loaded locals in input order before the store reads them).
+      bool proto_ok = true;
+      J proto;
+      try {
+        proto = lift_elementwise(name, dt, r, n, input_leaf(0), {}, block, grid);
+      } catch (const Decline&) {
+        proto_ok = false;
+      }
+      if (proto_ok && into_numbering_of(proto, kc, kr) && ew_extract(kr, eb, ep) &&
+          attempt([&] { return lift_elementwise(name, dt, r, n, eb, ep, block, grid); }))
+        return take_elementwise(eb, ep);
+    }
     // The pre-map body read back from the `val` Let (the up-cast stripped, the loaded locals
     // unbound to Input(k)) and a fused post from the output store (Local(red) unbound to
     // Reduced(0)), in the lift's numbering of locals; false when they read any other local.
@@ -1794,8 +1931,8 @@ int32_t recognize_kernel(const std::string& text, Recognized& out, std::string& 
     }
   }
   why = "kernel `" + name +
-        "` is not one of the forms this backend lowers (a lifted reduction, scan, row reduction or row gather, "
-        "the fused row fold, or the int4 dequant)";
+        "` is not one of the forms this backend lowers (a lifted elementwise op, reduction, scan, row reduction or "
+        "gather, the fused row fold, or the int4 dequant)";
   return UNP_UNSUPPORTED_KERNEL;
 }
 
@@ -1918,6 +2055,27 @@ int32_t unp_lift_gather_x(const char* name, int32_t dtype, int32_t rank, int32_t
   return unp::lift_call(json, err, [&] {
     return unp::lift_gather(name ? name : "gather", dtype, rank, index_dtype, axis, oob, block, grid,
                             (uint32_t)n_inputs, (uint32_t)data_slot, (uint32_t)index_slot, &body);
+  });
+}
+
+int32_t unp_lift_elementwise(const char* name, int32_t dtype, int32_t rank, int32_t n_inputs, const char* body_json,
+                             const int32_t* perms, uint32_t block, uint32_t grid, char** json, unp_error* err) {
+  using unp::kir::J;
+  J body;
+  std::string why;
+  if (!body_json || !unp::kir::parse(body_json, body, why)) {
+    unp::set_error(err, UNP_PARSE_ERROR, "body: a ScalarExpr expected " + why);
+    return UNP_PARSE_ERROR;
+  }
+  if (n_inputs < 1 || n_inputs > 8 || rank < 0 || rank > 8) {
+    unp::set_error(err, UNP_LIFT_DECLINE, "UnsupportedForm: an elementwise op of 1 to 8 inputs at rank 1 to 8");
+    return UNP_LIFT_DECLINE;
+  }
+  std::vector<std::vector<int32_t>> pm;
+  if (perms)
+    for (int32_t k = 0; k < n_inputs; ++k) pm.emplace_back(perms + (size_t)k * (size_t)rank, perms + (size_t)(k + 1) * (size_t)rank);
+  return unp::lift_call(json, err, [&] {
+    return unp::lift_elementwise(name ? name : "elementwise", dtype, rank, (uint32_t)n_inputs, body, pm, block, grid);
   });
 }
 

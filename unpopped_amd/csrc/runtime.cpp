@@ -123,7 +123,8 @@ extern "C" {
 
 const char* unp_hip_name(void) { return "hip"; }
 const char* unp_hip_provider(void) { return "unpopped-hip"; }
-int32_t unp_hip_total_integer_ops(void) { return 0; }
+// Integer Div, Shl, Shr and ConstInt are spelled by the total rule (unp::xi in the device library).
+int32_t unp_hip_total_integer_ops(void) { return 1; }
 
 int32_t unp_hip_supports_dtype(int32_t kind, const char* target) {
   if (!valid_target(target)) return UNP_UNSUPPORTED;
@@ -197,10 +198,12 @@ int32_t unp_hip_lower_kernel(const char* kernel_json, unp_generated** out, unp_e
   if (rec.form.kind == UNP_FORM_SCAN && unp::kind_is_float(rec.form.dtype) && rec.form.schedule == UNP_SCHEDULE_DEVICE)
     rec.form.schedule = UNP_SCHEDULE_FIXED;
   auto* g = new unp_generated();
-  if (rec.form.kind == UNP_FORM_ROW_REDUCE) {
-    // A row reduction whose expressions hold a node this backend cannot spell is an
-    // UnsupportedOp (backend.rs:398-403), its other refusals an UnsupportedKernel.
-    rc = unp::lower_row_reduce(rec.rr, g->l, why);
+  if (rec.form.kind == UNP_FORM_ROW_REDUCE || rec.form.kind == UNP_FORM_ELEMENTWISE) {
+    // A row reduction or elementwise op whose expressions hold a node this backend cannot spell
+    // is an UnsupportedOp (backend.rs:398-403), one at a dtype it has no spelling for an
+    // UnsupportedDtype, its other refusals an UnsupportedKernel.
+    rc = rec.form.kind == UNP_FORM_ROW_REDUCE ? unp::lower_row_reduce(rec.rr, g->l, why)
+                                              : unp::lower_elementwise(rec.form, rec.ew, g->l, why);
     if (rc != UNP_OK) {
       delete g;
       if (rc != UNP_UNSUPPORTED_OP && rc != UNP_UNSUPPORTED_DTYPE) rc = UNP_UNSUPPORTED_KERNEL;
@@ -1156,6 +1159,75 @@ int32_t run_gather(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_e
   return launch(x, entry, grid, params, s, err);
 }
 
+// The elementwise op's strided launch: the descriptor holds the output's extents and strides and
+// every input's strides over the output's axes.
+int32_t launch_elementwise_strided(unp_exec* x, const std::vector<uint64_t>& ptrs, const unp::gather_x_view_host& v,
+                                   hipStream_t s, unp_error* err) {
+  if (v.outs == 0) return UNP_OK;
+  std::vector<uint64_t> p(ptrs);
+  std::vector<void*> params;
+  for (auto& q : p) params.push_back(&q);
+  unp::gather_x_view_host vv = v;
+  params.push_back(&vv);
+  const long long blocks = (v.outs + 255) / 256;
+  const uint32_t grid = (uint32_t)std::min<long long>(blocks, (long long)x->cu_count * x->l.blocks_per_cu);
+  size_t entry = 0;
+  while (entry + 1 < x->l.entries.size() && !x->l.entries[entry].strided) ++entry;
+  return launch(x, entry, grid, params.data(), s, err);
+}
+
+// An elementwise op from device addresses: every buffer dense row-major in its own shape, a
+// permuted input in its own axis order (the shape whose axis perm[d] has the output's extent d).
+int32_t run_elementwise(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
+  const unp_form& f = x->l.form;
+  const unp::ElementwiseExpr& ew = x->l.ew;
+  const size_t NI = (size_t)ew.n_inputs;
+  Args A;
+  int32_t rc = take_args(a, n, NI + 1, (size_t)f.rank, A, err);
+  if (rc == UNP_OK) rc = extents_i32(A, (size_t)f.rank, err);
+  if (rc != UNP_OK) return rc;
+  const long long total = product(A.ext, 0, (size_t)f.rank);
+  if ((rc = need_buffers(A, total > 0, err)) != UNP_OK) return rc;
+  if (total == 0) return UNP_OK;
+  std::vector<uint64_t> ptrs(A.buf.begin(), A.buf.end());
+  if (!ew.permuted()) {
+    bool al = true;
+    for (uint64_t q : ptrs) al = al && aligned16(q);
+    const size_t entry = pick(x, al);
+    const long long vec = x->l.entries[entry].vec, np = total / vec;
+    const long long lanes = std::max(np, total - np * vec);
+    const uint32_t grid =
+        (uint32_t)std::max<long long>(1, std::min<long long>((lanes + 255) / 256, (long long)x->cu_count * x->l.blocks_per_cu));
+    std::vector<void*> params;
+    for (auto& q : ptrs) params.push_back(&q);
+    long long nn = total;
+    params.push_back(&nn);
+    return launch(x, entry, grid, params.data(), s, err);
+  }
+  unp::gather_x_view_host v{};
+  v.rank = f.rank;
+  v.outs = total;
+  long long st = 1;
+  for (int d = f.rank - 1; d >= 0; --d) {
+    v.ext[d] = A.ext[(size_t)d];
+    v.ostr[d] = st;
+    st *= v.ext[d];
+  }
+  for (size_t k = 0; k < NI; ++k) {
+    // Input k's own shape and row-major strides, then the stride of iteration axis d is that of
+    // its axis perm[d].
+    long long shape[8], pstr[8];
+    for (int d = 0; d < f.rank; ++d) shape[ew.perms.empty() ? d : ew.perms[k][(size_t)d]] = v.ext[d];
+    long long ps = 1;
+    for (int a2 = f.rank - 1; a2 >= 0; --a2) {
+      pstr[a2] = ps;
+      ps *= shape[a2];
+    }
+    for (int d = 0; d < f.rank; ++d) v.istr[k][d] = pstr[ew.perms.empty() ? d : ew.perms[k][(size_t)d]];
+  }
+  return launch_elementwise_strided(x, ptrs, v, s, err);
+}
+
 int32_t run_dequant(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
   Args A;
   int32_t rc = take_args(a, n, 4, 2, A, err);
@@ -1311,6 +1383,7 @@ void param_counts(const unp_exec* x, size_t& nbuf, size_t& nscal) {
     case UNP_FORM_ROW_REDUCE: nbuf = (size_t)x->l.rr.n_inputs + 1; nscal = (size_t)x->l.rr.rank; break;
     case UNP_FORM_DEQUANT4: nbuf = 4; nscal = 2; break;
     case UNP_FORM_DEQUANT_GEMM: nbuf = 5; nscal = 3; break;
+    case UNP_FORM_ELEMENTWISE: nbuf = (size_t)x->l.ew.n_inputs + 1; nscal = (size_t)f.rank; break;
     default: break;
   }
 }
@@ -1386,6 +1459,17 @@ std::vector<Want> wanted_shapes(const unp_exec* x, const std::vector<int64_t>& e
       one({R * ng});
       one({R * ng});
       one({R * C});
+      break;
+    }
+    case UNP_FORM_ELEMENTWISE: {
+      // Input k in its own axis order: its axis perm[d] has the output's extent d.
+      for (int32_t k = 0; k < x->l.ew.n_inputs; ++k) {
+        std::vector<int64_t> s(ext);
+        if (!x->l.ew.perms.empty())
+          for (int32_t d = 0; d < f.rank; ++d) s[(size_t)x->l.ew.perms[(size_t)k][(size_t)d]] = ext[(size_t)d];
+        one(s);
+      }
+      one(ext);
       break;
     }
     case UNP_FORM_DEQUANT_GEMM: {
@@ -1471,6 +1555,7 @@ bool views_dense(const unp_exec* x, const unp_view* v, size_t n, int64_t src_ext
   for (size_t b = 0; b < n; ++b) {
     if (view_empty(v[b])) continue;
     if (f.kind == UNP_FORM_GATHER && !x->l.gx.plain) return false;  // one entry reads every layout
+    if (f.kind == UNP_FORM_ELEMENTWISE && x->l.ew.permuted()) return false;  // the strided entry
     if (f.kind == UNP_FORM_GATHER && b < 2) {
       const int ax = x->l.scan_axis;
       if ((int)b == f.data_slot) {
@@ -1624,6 +1709,27 @@ int32_t strided_gather(unp_exec* x, const unp_view* v, const std::vector<int64_t
   return launch(x, strided_entry(x, 0), strided_grid(x), params, s, err);
 }
 
+// An elementwise op over storage images: input k's stride along output axis d is its view's
+// stride along its axis perm[d].
+int32_t strided_elementwise(unp_exec* x, const unp_view* v, const std::vector<int64_t>& ext, hipStream_t s,
+                            unp_error* err) {
+  const unp_form& f = x->l.form;
+  const unp::ElementwiseExpr& ew = x->l.ew;
+  const size_t NI = (size_t)ew.n_inputs;
+  unp::gather_x_view_host d{};
+  d.rank = f.rank;
+  d.outs = 1;
+  for (int a = 0; a < f.rank; ++a) {
+    d.ext[a] = ext[(size_t)a];
+    d.ostr[a] = v[NI].stride[a];
+    d.outs *= ext[(size_t)a];
+    for (size_t k = 0; k < NI; ++k) d.istr[k][a] = v[k].stride[ew.perms.empty() ? a : ew.perms[k][(size_t)a]];
+  }
+  std::vector<uint64_t> ptrs;
+  for (size_t k = 0; k <= NI; ++k) ptrs.push_back(view_ptr(v[k], unp::kind_bytes(f.dtype)));
+  return launch_elementwise_strided(x, ptrs, d, s, err);
+}
+
 }  // namespace
 
 extern "C" int32_t unp_hip_exec_launch_views(unp_exec* x, const unp_view* views, size_t nviews,
@@ -1688,14 +1794,15 @@ extern "C" int32_t unp_hip_exec_launch_views(unp_exec* x, const unp_view* views,
   // through the strides; the others read dense storage only.
   const bool plain_reduction = (f.kind == UNP_FORM_REDUCTION && x->l.rx.plain) || f.kind == UNP_FORM_ROW_REDUCE2;
   const bool plain_scan = f.kind == UNP_FORM_SCAN && x->l.rx.plain;
-  if (!plain_reduction && !plain_scan && f.kind != UNP_FORM_GATHER)
+  if (!plain_reduction && !plain_scan && f.kind != UNP_FORM_GATHER && f.kind != UNP_FORM_ELEMENTWISE)
     return invalid(err,
                    "a view that is not dense row-major: this form reads dense storage (the plain reduction, plain "
-                   "scan and gather forms read any strides), so make the view contiguous first");
+                   "scan, gather and elementwise forms read any strides), so make the view contiguous first");
   const int32_t rc = begin_launch(x, err);
   if (rc != UNP_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   if (plain_reduction) return strided_reduction(x, views, ext, s, err);
+  if (f.kind == UNP_FORM_ELEMENTWISE) return strided_elementwise(x, views, ext, s, err);
   if (f.kind == UNP_FORM_SCAN) return strided_scan(x, views, ext, s, err);
   return strided_gather(x, views, ext, raw_src, s, err);
 }
@@ -1723,6 +1830,8 @@ extern "C" int32_t unp_hip_exec_launch(unp_exec* x, const unp_arg* args, size_t 
       return run_dequant(x, args, nargs, s, err);
     case UNP_FORM_DEQUANT_GEMM:
       return run_dequant_gemm(x, args, nargs, s, err);
+    case UNP_FORM_ELEMENTWISE:
+      return run_elementwise(x, args, nargs, s, err);
     default:
       set_error(err, UNP_UNSUPPORTED_KERNEL, "unknown form");
       return UNP_UNSUPPORTED_KERNEL;

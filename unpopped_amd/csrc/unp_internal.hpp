@@ -114,6 +114,22 @@ struct GatherExpr {
   kir::J body;  // ScalarExpr over Input(k)
 };
 
+// A recognised Access::Elementwise lift (kernel_lift.rs:96-130): n inputs read at the output
+// coordinate (input k through the axis permutation perms[k] when it is not empty: iteration axis d
+// reads the input's axis perms[k][d], kernel_lift.rs:315-324) and a body over Input(0..n) stored
+// at the output coordinate.
+struct ElementwiseExpr {
+  int32_t n_inputs = 1;
+  kir::J body;  // ScalarExpr over Input(k)
+  std::vector<std::vector<int32_t>> perms;
+  bool permuted() const {
+    for (const auto& p : perms)
+      for (size_t d = 0; d < p.size(); ++d)
+        if (p[d] != (int32_t)d) return true;
+    return false;
+  }
+};
+
 // A lowered form: what the executor needs to launch it.
 struct Lowered {
   unp_form form{};
@@ -136,6 +152,7 @@ struct Lowered {
   RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only
   ReductionExpr rx;  // UNP_FORM_REDUCTION and UNP_FORM_SCAN: the pre-map body and the post
   GatherExpr gx;     // UNP_FORM_GATHER: the inputs and body
+  ElementwiseExpr ew;  // UNP_FORM_ELEMENTWISE: the inputs, their permutations and the body
 };
 
 // Emit the HIP source and interface for `f`; on refusal returns a nonzero unp_status and
@@ -150,6 +167,8 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& out, s
 int32_t lower_gather_x(const unp_form& f, const GatherExpr& gx, Lowered& out, std::string& detail);
 // The same for a recognised Access::RowReduce.
 int32_t lower_row_reduce(const RowReduceSpec& spec, Lowered& out, std::string& detail);
+// A recognised Access::Elementwise (its body comes only with the KernelFn).
+int32_t lower_elementwise(const unp_form& f, const ElementwiseExpr& ew, Lowered& out, std::string& detail);
 
 // Backend::lower_kernel's recognizer (lifts.cpp): the form a KernelFn's JSON is, or a refusal.
 // A recognised kernel: the form to lower, the lift it matched, and the kernel's name, declared
@@ -159,6 +178,7 @@ struct Recognized {
   RowReduceSpec rr;  // UNP_FORM_ROW_REDUCE only
   ReductionExpr rx;  // UNP_FORM_REDUCTION and UNP_FORM_SCAN
   GatherExpr gx;     // UNP_FORM_GATHER only
+  ElementwiseExpr ew;  // UNP_FORM_ELEMENTWISE only
   std::string lift;
   kir::J launch;
   kir::J params;
