@@ -488,3 +488,27 @@ def elementwise(inputs, body, dtype: str, perms=None, mutant: int = 0) -> np.nda
     if dtype == "U64":
         return raw.view(np.uint64)
     return raw.astype(NP_KINDS[dtype])
+
+
+def int_reduce_expr(inputs, axes, op: str, body, dtype: str) -> np.ndarray:
+    """The serial lifted reduction of an integer body (I32/I64; kernel_lift.rs:919-941 with
+    `val = body`, no up-cast and no post): the body evaluated per position by eval_int's total rule
+    (``elementwise``), then folded at the element type (``reduce_rows`` over the reduced axes moved
+    last).  Integer folds wrap, so the fold's order does not change the bits."""
+    v = elementwise(inputs, body, dtype)
+    axes = tuple(sorted(axes))
+    kept = [d for d in range(v.ndim) if d not in axes]
+    t = np.ascontiguousarray(np.transpose(v, kept + list(axes)))
+    rows = int(np.prod([v.shape[d] for d in kept], dtype=np.int64))
+    cols = int(np.prod([v.shape[d] for d in axes], dtype=np.int64))
+    return reduce_rows(t.reshape(rows, cols), op).reshape([v.shape[d] for d in kept])
+
+
+def int_scan_expr(inputs, axis: int, op: str, pre, dtype: str, exclusive: bool = False,
+                  reverse: bool = False) -> np.ndarray:
+    """The serial lifted scan of an integer pre-map (I32/I64, identity post): the pre evaluated per
+    position by the total rule, then scanned along ``axis`` at the element type (``scan_rows``)."""
+    v = elementwise(inputs, pre, dtype)
+    m = np.ascontiguousarray(np.moveaxis(v, axis, -1))
+    out = scan_rows(m.reshape(-1, m.shape[-1]), op, exclusive, reverse).reshape(m.shape)
+    return np.ascontiguousarray(np.moveaxis(out, -1, axis))

@@ -281,3 +281,50 @@ def test_c99_leg_meets_the_oracle_on_the_boundary_vectors(dt, op):
     out = np.zeros_like(x)
     assert cpuc.run(k, x, y, out, x.size) == cpuc.OK
     assert out.tobytes() == oracle.elementwise([x, y], body, dt).tobytes()
+
+
+# ---- integer pre-map bodies of reductions and scans (kernel_lift.rs:755-800) --------------------
+
+@pytest.mark.parametrize("dt,nt", [("I32", np.int32), ("I64", np.int64)])
+@pytest.mark.parametrize("op", ["Sum", "Prod", "Max", "Min", "Xor"])
+def test_integer_body_reduction_oracle_meets_the_c99_leg(dt, nt, op):
+    """The oracle's integer-body reduction (the integer evaluator's values folded by the serial lift)
+    equals the C99 leg running the serial lifted kernel on boundary-heavy data."""
+    x, y = grid(dt)
+    side = int(round(np.sqrt(x.size)))
+    xs = [x.reshape(side, side), y.reshape(side, side)]
+    body = {"Add": [{"Div": [I(0), I(1)]}, B("Shl", I(1), I(0))]}
+    k = u.lift_reduction("r", dt, 2, op, axes=(1,), n_inputs=2, body=body)
+    out = np.zeros(side, nt)
+    assert cpuc.run(k, *xs, out, side, side) == cpuc.OK
+    assert out.tobytes() == oracle.int_reduce_expr(xs, (1,), op, body, dt).tobytes()
+
+
+@pytest.mark.parametrize("dt,nt", [("I32", np.int32), ("I64", np.int64)])
+@pytest.mark.parametrize("op", ["Sum", "Max"])
+def test_integer_pre_scan_oracle_meets_the_c99_leg(dt, nt, op):
+    x, y = grid(dt)
+    side = int(round(np.sqrt(x.size)))
+    xs = [x.reshape(side, side), y.reshape(side, side)]
+    pre = {"Sub": [{"Mul": [I(0), I(1)]}, B("Shr", I(0), I(1))]}
+    for excl, rev in ((False, False), (True, True)):
+        k = u.lift_scan("s", dt, 2, op, exclusive=excl, reverse=rev, n_inputs=2, pre=pre)
+        out = np.zeros((side, side), nt)
+        assert cpuc.run(k, *xs, out, side, side) == cpuc.OK
+        assert out.tobytes() == oracle.int_scan_expr(xs, 1, op, pre, dt, excl, rev).tobytes()
+
+
+def test_integer_bodies_lower_with_the_integer_rule_and_refuse_a_post():
+    b = u.HipBackend()
+    body = {"Div": [I(0), I(1)]}
+    g = b.lower_kernel(u.lift_reduction("r", "I64", 2, "Prod", axes=(1,), n_inputs=2, body=body, launch=(256, 4)))
+    assert "unp::xi::div<long long>" in g.source and "integer rule" in g.interface["fidelity_notes"][0]
+    s = b.lower_kernel(u.lift_scan("s", "I32", 1, "Sum", n_inputs=2, pre=body, launch=(256, 4)))
+    assert s.interface["schedule"] == "device" and "integer rule" in s.interface["fidelity_notes"][0]
+    with pytest.raises(_lib.UnpError) as e:
+        u.lift_reduction("r", "I32", 1, "Sum", n_inputs=2, body=body,
+                         post={"Add": [{"Reduced": 0}, {"ConstInt": [1, "I32"]}]})
+    assert "post" in str(e.value)
+    with pytest.raises(_lib.UnpError) as e:
+        u.lift_scan("s", "I32", 1, "Sum", n_inputs=2, pre=body, post={"Add": [{"Reduced": 0}, I(0)]})
+    assert "post" in str(e.value)

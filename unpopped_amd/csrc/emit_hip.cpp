@@ -1743,6 +1743,49 @@ int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) 
   return UNP_OK;
 }
 
+namespace {
+
+// The pre-map and post of a reduction or scan as C++ expressions over x[k] (the inputs) and r[0]
+// (the rounded fold): in f64 for F32/F64, at the element type by the total integer rule for
+// I32/I64 (no post there).  False, with `why` set, for a node that has no spelling.
+bool pre_ops_cpp(int32_t dtype, const ReductionExpr& rx, std::string& pre, std::string& post, std::string& why) {
+  if (dtype == UNP_I32 || dtype == UNP_I64) {
+    if (int_node_type(rx.body, dtype) != dtype || !int_expr_cpp(rx.body, dtype, dtype, pre, why)) {
+      if (why.empty()) why = "an integer expression whose type is not the compute dtype";
+      why = "body: " + why + " has no spelling here";
+      return false;
+    }
+    return true;
+  }
+  if (!expr_cpp(rx.body, ctype(dtype), pre, why)) {
+    why = "body: " + why + " has no spelling here";
+    return false;
+  }
+  if (rx.has_post && !expr_cpp(rx.post, ctype(dtype), post, why)) {
+    why = "post: " + why + " has no spelling here";
+    return false;
+  }
+  return true;
+}
+
+// The OPS struct the xreduce / xscan templates take: `arg` the type the expressions read their
+// inputs at and `acc` the fold's (double for a float, the element type for an integer).  A scan's
+// post also reads the position's inputs.
+std::string pre_ops_struct(const std::string& ops, int32_t dtype, bool has_post, const std::string& pre,
+                           const std::string& post, bool scan) {
+  const bool is_int = dtype == UNP_I32 || dtype == UNP_I64;
+  const std::string A = is_int ? ctype(dtype) : "double";
+  std::ostringstream s;
+  s << "struct " << ops << " {\n  typedef " << A << " arg;\n  typedef " << A << " acc;\n"
+    << "  static constexpr bool has_post = " << (has_post ? "true" : "false") << ";\n"
+    << "  static __device__ __forceinline__ " << A << " pre(const " << A << "* x) { (void)x; return " << pre << "; }\n"
+    << "  static __device__ __forceinline__ " << A << " post(const " << A << "* r" << (scan ? ", const " + A + "* x" : "")
+    << ") { (void)r; " << (scan ? "(void)x; " : "") << "return " << post << "; }\n};\n";
+  return s.str();
+}
+
+}  // namespace
+
 int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std::string& why) {
   if (rx.plain) return lower_form(f, L, why);
   L = Lowered{};
@@ -1752,9 +1795,15 @@ int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L
     why = "rank is zero or more than 8";
     return UNP_LIFT_DECLINE;
   }
-  if (f.dtype != UNP_F32 && f.dtype != UNP_F64) {
-    why = "a reduction with a pre-map body or a fused post at an integer dtype (its integer expressions have no "
-          "spelling here)";
+  // The integer kinds the reference lifts a body at (kernel_lift.rs:755-800): I32 and I64, with the
+  // identity post.
+  const bool int_body = f.dtype == UNP_I32 || f.dtype == UNP_I64;
+  if (f.dtype != UNP_F32 && f.dtype != UNP_F64 && !int_body) {
+    why = "a reduction with a pre-map body or a fused post outside F32, F64, I32 and I64";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (int_body && rx.has_post) {
+    why = "a fused post at an integer dtype";
     return UNP_UNSUPPORTED_KERNEL;
   }
   if (rx.n_inputs < 1 || rx.n_inputs > 8) {
@@ -1762,7 +1811,7 @@ int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L
     return UNP_UNSUPPORTED_KERNEL;
   }
   if (!reduction_ok(f.dtype, f.op0, why)) return UNP_UNSUPPORTED_KERNEL;
-  if (f.op0 == UNP_OP_PROD) {
+  if (f.op0 == UNP_OP_PROD && !int_body) {
     why = "a float Prod with a pre-map body or a fused post (not order-independent, and no declared bound)";
     return UNP_UNSUPPORTED_KERNEL;
   }
@@ -1779,14 +1828,7 @@ int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L
   for (int32_t d = f.rank - 1; d >= 0 && ((mask >> d) & 1u); --d) L.form.reduced_from = d;
   const char* T = ctype(f.dtype);
   std::string pre, post = "r[0]";
-  if (!expr_cpp(rx.body, T, pre, why)) {
-    why = "body: " + why + " has no spelling here";
-    return UNP_UNSUPPORTED_OP;
-  }
-  if (rx.has_post && !expr_cpp(rx.post, T, post, why)) {
-    why = "post: " + why + " has no spelling here";
-    return UNP_UNSUPPORTED_OP;
-  }
+  if (!pre_ops_cpp(f.dtype, rx, pre, post, why)) return UNP_UNSUPPORTED_OP;
   const int NI = rx.n_inputs;
   const std::string key = std::string(T) + "|" + std::to_string(NI) + "|" + std::to_string(f.op0) + "|" + sched +
                           "|" + pre + "|" + (rx.has_post ? post : std::string("-"));
@@ -1795,10 +1837,7 @@ int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L
   L.name = std::string("unp_xreduce_") + op_name(f.op0) + "_" + lower_name(f.dtype) + "_" + std::string(hx, 8);
   const std::string ops = L.name + "_ops";
   std::ostringstream src;
-  src << header(L.name, f);
-  src << "struct " << ops << " {\n  static constexpr bool has_post = " << (rx.has_post ? "true" : "false") << ";\n"
-      << "  static __device__ __forceinline__ double pre(const double* x) { (void)x; return " << pre << "; }\n"
-      << "  static __device__ __forceinline__ double post(const double* r) { (void)r; return " << post << "; }\n};\n";
+  src << header(L.name, f) << pre_ops_struct(ops, f.dtype, rx.has_post, pre, post, false);
   auto sig = [&](std::ostringstream& o) {
     for (int k = 0; k < NI; ++k) o << "const " << T << "* in" << k << ", ";
     o << T << "* out";
@@ -1880,9 +1919,13 @@ int32_t lower_reduction_x(const unp_form& f, const ReductionExpr& rx, Lowered& L
   j << "],\"workspace\":" << (sched == 'a' ? "{\"partials\":\"grid * 16 (f64, tagged with the launch epoch)\",\"counter\":4,\"stall\":4,\"host_state\":[\"epoch\"]}" : "null")
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["
-    << json_str("the body and the post evaluate in f64 and round once per statement, as the kernel evaluator runs the "
-                "lifted kernel; the fold is in f64 in a geometry-fixed order: a Sum/Mean within the declared bound "
-                "gamma_(n-1)*sum|x| of the serial fold, a Max/Min exact except NaN payload and the sign of a zero")
+    << json_str(int_body ? "the body evaluates at the element type by the total integer rule (Add/Sub/Mul wrap, a zero "
+                           "divisor and MIN / -1 give the dividend, shift counts modulo the width) and the fold wraps at "
+                           "the element type: every order gives the serial kernel's bits"
+                         : "the body and the post evaluate in f64 and round once per statement, as the kernel evaluator "
+                           "runs the lifted kernel; the fold is in f64 in a geometry-fixed order: a Sum/Mean within the "
+                           "declared bound gamma_(n-1)*sum|x| of the serial fold, a Max/Min exact except NaN payload and "
+                           "the sign of a zero")
     << "]}";
   L.interface_json = j.str();
   return UNP_OK;
@@ -1902,8 +1945,14 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std
     why = "rank is zero or more than 8";
     return UNP_LIFT_DECLINE;
   }
-  if (f.dtype != UNP_F32 && f.dtype != UNP_F64) {
-    why = "a scan with a pre-map body at an integer dtype (its integer expressions have no spelling here)";
+  // I32 and I64 take a pre-map with the identity post and no Mean (kernel_lift.rs:755-800).
+  const bool int_body = f.dtype == UNP_I32 || f.dtype == UNP_I64;
+  if (f.dtype != UNP_F32 && f.dtype != UNP_F64 && !int_body) {
+    why = "a scan with a pre-map body or a fused post outside F32, F64, I32 and I64";
+    return UNP_UNSUPPORTED_KERNEL;
+  }
+  if (int_body && (rx.has_post || f.op0 == UNP_OP_MEAN)) {
+    why = rx.has_post ? "a fused post at an integer dtype" : "an integer Mean";
     return UNP_UNSUPPORTED_KERNEL;
   }
   if (rx.n_inputs < 1 || rx.n_inputs > 8) {
@@ -1925,21 +1974,16 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std
   }
   // The fixed schedule folds the register look-back's carries in groups of 64 tiles in an order
   // the tiling fixes (lookback_grouped), as the plain scan's does.
-  const bool serial = axis != f.rank - 1 || f.op0 == UNP_OP_PROD || f.op0 == UNP_OP_MEAN ||
+  // An integer Prod wraps, so its look-back is exact in any order; a float Prod rounds at every
+  // step and runs the serial order.
+  const bool serial = axis != f.rank - 1 || (f.op0 == UNP_OP_PROD && !int_body) || f.op0 == UNP_OP_MEAN ||
                       f.schedule == UNP_SCHEDULE_SERIAL;
   const bool fixed = !serial && f.schedule == UNP_SCHEDULE_FIXED;
   L.serial_scan = serial;
   L.scan_axis = axis;
   const char* T = ctype(f.dtype);
   std::string pre, post = "r[0]";
-  if (!expr_cpp(rx.body, T, pre, why)) {
-    why = "pre: " + why + " has no spelling here";
-    return UNP_UNSUPPORTED_OP;
-  }
-  if (rx.has_post && !expr_cpp(rx.post, T, post, why)) {
-    why = "post: " + why + " has no spelling here";
-    return UNP_UNSUPPORTED_OP;
-  }
+  if (!pre_ops_cpp(f.dtype, rx, pre, post, why)) return UNP_UNSUPPORTED_OP;
   const int NI = rx.n_inputs;
   const char* EX = f.exclusive ? "true" : "false";
   const char* RV = f.reverse ? "true" : "false";
@@ -1952,11 +1996,7 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std
            (f.reverse ? "rev_" : "") + op_name(f.op0) + "_" + lower_name(f.dtype) + "_" + std::string(hx, 8);
   const std::string ops = L.name + "_ops";
   std::ostringstream src;
-  src << header(L.name, f);
-  src << "struct " << ops << " {\n  static constexpr bool has_post = " << (rx.has_post ? "true" : "false") << ";\n"
-      << "  static __device__ __forceinline__ double pre(const double* x) { (void)x; return " << pre << "; }\n"
-      << "  static __device__ __forceinline__ double post(const double* r, const double* x) { (void)r; (void)x; "
-      << "return " << post << "; }\n};\n";
+  src << header(L.name, f) << pre_ops_struct(ops, f.dtype, rx.has_post, pre, post, true);
   std::ostringstream sig, ins;
   for (int k = 0; k < NI; ++k) sig << "const " << T << "* in" << k << ", ";
   sig << T << "* out";
@@ -2010,7 +2050,10 @@ int32_t lower_scan_x(const unp_form& f, const ReductionExpr& rx, Lowered& L, std
                      " bytes, zeroed once\",\"counter\":4,\"stall\":4,\"host_state\":[\"epoch\",\"ticket_base\"]}")
     << ",\"compiler_args\":[\"--offload-arch=gfx950\",\"-O3\",\"-Xclang\",\"-target-feature\",\"-Xclang\",\"-packed-fp32-ops\"]"
     << ",\"fidelity_notes\":["
-    << json_str(serial ? "the pre and the post evaluate in f64 and round once per statement, as the kernel evaluator runs "
+    << json_str(int_body ? "the pre evaluates at the element type by the total integer rule (Add/Sub/Mul wrap, a zero "
+                           "divisor and MIN / -1 give the dividend, shift counts modulo the width) and the fold wraps at "
+                           "the element type: every order gives the serial kernel's bits"
+                : serial ? "the pre and the post evaluate in f64 and round once per statement, as the kernel evaluator runs "
                          "the lifted kernel; the fold in the serial lift's own order: bit-exact against the serial kernel"
                 : fixed ? "the pre and the post evaluate in f64 and round once per statement; a Sum's prefixes are f64 "
                           "folds of the pre-mapped elements in an order the 4096-position block tiles fix (wave-local "

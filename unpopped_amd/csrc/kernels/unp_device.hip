@@ -853,10 +853,13 @@ UNP_DEV void reduce_strided(const T* __restrict__ in, T* __restrict__ out, const
 // non-plain body or post: kernel_lift.rs:919-941, 987-1003).  Float compute dtypes: at each
 // position the body is evaluated in f64 over the inputs and rounded once to T, the fold runs in
 // f64, the finished fold (Mean divided) is rounded once to T, and the post is evaluated in f64
-// over that value and rounded once at the store.  The emitted source supplies OPS: `pre(x)`
-// over the NI input values and `post(r)` over r[0], both in doubles, and `has_post`.
+// over that value and rounded once at the store.  Integer compute dtypes (I32, I64; no post,
+// kernel_lift.rs:763-800): the body is evaluated at T by the total integer rule and the fold
+// wraps at T, so every order gives the serial kernel's bits.  The emitted source supplies OPS:
+// `arg` (the type the body reads its inputs at), `acc` (the fold's), `pre(x)` over the NI input
+// values, `post(r)` over r[0], and `has_post`.
 // ---------------------------------------------------------------------------------------
-template <class T, int OP, class OPS> UNP_DEV T xfinish(double a, i64 n) {
+template <class T, int OP, class OPS, class Ac> UNP_DEV T xfinish(Ac a, i64 n) {
   const T red = finish<T, OP>(a, n);
   if constexpr (OPS::has_post) {
     const double r[1] = {(double)red};
@@ -869,19 +872,21 @@ template <class T, int OP, class OPS> UNP_DEV T xfinish(double a, i64 n) {
 // The trailing run: rows x cols, one wave per row (U vectors of each input in flight per lane).
 template <class T, int NI, int OP, class OPS, int VEC, int THREADS, int U>
 UNP_DEV void xreduce_rows(const T* const* __restrict__ in, T* __restrict__ out, i64 rows, i64 cols) {
-  typedef fold<double, OP> F;
+  typedef typename OPS::acc Ac;
+  typedef typename OPS::arg X;
+  typedef fold<Ac, OP> F;
   constexpr i64 STEP = (i64)64 * VEC;
   const int lane = threadIdx.x & 63;
   const i64 nwaves = (i64)gridDim.x * (THREADS / 64);
   for (i64 row = (i64)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6); row < rows; row += nwaves) {
-    double a = F::identity();
+    Ac a = F::identity();
     auto take = [&](const vec<T, VEC> (&v)[NI]) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        double x[NI];
+        X x[NI];
 #pragma unroll
-        for (int k = 0; k < NI; ++k) x[k] = (double)v[k].e[e];
-        a = F::apply(a, (double)(T)OPS::pre(x));
+        for (int k = 0; k < NI; ++k) x[k] = (X)v[k].e[e];
+        a = F::apply(a, (Ac)(T)OPS::pre(x));
       }
     };
     i64 c = (i64)lane * VEC;
@@ -900,7 +905,7 @@ UNP_DEV void xreduce_rows(const T* const* __restrict__ in, T* __restrict__ out, 
       for (int k = 0; k < NI; ++k) v[k] = ld_nt<T, VEC>(in[k] + row * cols + c);
       take(v);
     }
-    a = wave_reduce<double, OP>(a);
+    a = wave_reduce<Ac, OP>(a);
     if (lane == 0) out[row] = xfinish<T, OP, OPS>(a, cols);
   }
 }
@@ -910,20 +915,22 @@ UNP_DEV void xreduce_rows(const T* const* __restrict__ in, T* __restrict__ out, 
 template <class T, int NI, int OP, class OPS, int VEC, int THREADS, int UNROLL>
 UNP_DEV void xreduce_all(const T* const* __restrict__ in, T* __restrict__ out, i64 n, u64* __restrict__ partials,
                          u32* __restrict__ counter, u32 epoch, waits wt) {
-  typedef fold<double, OP> F;
+  typedef typename OPS::acc Ac;
+  typedef typename OPS::arg X;
+  typedef fold<Ac, OP> F;
   constexpr int WAVES = THREADS / 64;
-  __shared__ double sh[WAVES];
+  __shared__ Ac sh[WAVES];
   __shared__ u32 last;
   const int tid = threadIdx.x;
   const i64 STEP = (i64)gridDim.x * THREADS * VEC;
-  double a = F::identity();
+  Ac a = F::identity();
   auto take = [&](const vec<T, VEC> (&v)[NI]) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      double x[NI];
+      X x[NI];
 #pragma unroll
-      for (int k = 0; k < NI; ++k) x[k] = (double)v[k].e[e];
-      a = F::apply(a, (double)(T)OPS::pre(x));
+      for (int k = 0; k < NI; ++k) x[k] = (X)v[k].e[e];
+      a = F::apply(a, (Ac)(T)OPS::pre(x));
     }
   };
   i64 c = ((i64)blockIdx.x * THREADS + tid) * VEC;
@@ -942,18 +949,18 @@ UNP_DEV void xreduce_all(const T* const* __restrict__ in, T* __restrict__ out, i
     for (int k = 0; k < NI; ++k) v[k] = ld_nt<T, VEC>(in[k] + c);
     take(v);
   }
-  a = block_reduce<double, OP, THREADS>(a, sh);
-  typedef tagged<double> P;
+  a = block_reduce<Ac, OP, THREADS>(a, sh);
+  typedef tagged<Ac> P;
   if (tid == 0) {
     P::put(partials + blockIdx.x, gridDim.x, a, epoch);
     last = (arrive_after_stores(counter) == gridDim.x - 1) ? 1u : 0u;
   }
   __syncthreads();
   if (last == 0u) return;
-  double b = F::identity();
+  Ac b = F::identity();
   for (u32 i = tid; i < gridDim.x; i += THREADS)
     b = F::apply(b, P::wait(partials + i, gridDim.x, epoch, F::identity(), wt));
-  b = block_reduce<double, OP, THREADS>(b, sh);
+  b = block_reduce<Ac, OP, THREADS>(b, sh);
   if (tid == 0) {
     out[0] = xfinish<T, OP, OPS>(b, n);
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -964,7 +971,9 @@ UNP_DEV void xreduce_all(const T* const* __restrict__ in, T* __restrict__ out, i
 // shape read at the same offsets.
 template <class T, int NI, int OP, class OPS, int THREADS>
 UNP_DEV void xreduce_generic(const T* const* __restrict__ in, T* __restrict__ out, const axes_desc& d) {
-  typedef fold<double, OP> F;
+  typedef typename OPS::acc Ac;
+  typedef typename OPS::arg X;
+  typedef fold<Ac, OP> F;
   const int lane = threadIdx.x & 63;
   const i64 nw = (i64)gridDim.x * (THREADS / 64);
   for (i64 o = (i64)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6); o < d.outs; o += nw) {
@@ -974,7 +983,7 @@ UNP_DEV void xreduce_generic(const T* const* __restrict__ in, T* __restrict__ ou
       q /= d.kext[k];
       base += c * d.kstr[k];
     }
-    double a = F::identity();
+    Ac a = F::identity();
     for (i64 t = lane; t < d.count; t += 64) {
       i64 off = base, u = t;
       for (i64 k = d.nr - 1; k >= 0; --k) {
@@ -982,12 +991,12 @@ UNP_DEV void xreduce_generic(const T* const* __restrict__ in, T* __restrict__ ou
         u /= d.rext[k];
         off += c * d.rstr[k];
       }
-      double x[NI];
+      X x[NI];
 #pragma unroll
-      for (int k = 0; k < NI; ++k) x[k] = (double)in[k][off];
-      a = F::apply(a, (double)(T)OPS::pre(x));
+      for (int k = 0; k < NI; ++k) x[k] = (X)in[k][off];
+      a = F::apply(a, (Ac)(T)OPS::pre(x));
     }
-    a = wave_reduce<double, OP>(a);
+    a = wave_reduce<Ac, OP>(a);
     if (lane == 0) out[o] = xfinish<T, OP, OPS>(a, d.count);
   }
 }
@@ -1464,14 +1473,15 @@ UNP_DEV void scan_lookback(const T* __restrict__ in, T* __restrict__ out, i64 ro
 // over the position's inputs and rounds once to T, and that element is what the fold takes
 // (`val = up(pre)`).  The stored prefix is rounded once to T (`red`).  With a post, OPS::post
 // evaluates in f64 over `red` (r[0]) and the position's inputs (x[k]) and rounds once at the
-// store.  Float dtypes only.
+// store.  At I32 and I64 (no post, no Mean) the pre is evaluated at T by the total integer rule
+// and the fold wraps at T.  OPS::arg is the type the expressions read their inputs at.
 // ---------------------------------------------------------------------------------------
 template <class T, int NI, class OPS> UNP_DEV T xscan_elem(const T* const* __restrict__ in, i64 off, T (&raw)[NI]) {
-  double x[NI];
+  typename OPS::arg x[NI];
 #pragma unroll
   for (int k = 0; k < NI; ++k) {
     raw[k] = in[k][off];
-    x[k] = (double)raw[k];
+    x[k] = (typename OPS::arg)raw[k];
   }
   return (T)OPS::pre(x);
 }

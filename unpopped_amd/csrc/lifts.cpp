@@ -194,8 +194,9 @@ struct Shape {
 };
 
 // check_accumulated_dtype (kernel_lift.rs:763-803) for the ops lifted here: a bit or NaN-ignoring
-// fold only in a plain reduction, a bit fold only at an integer dtype.
-void check_accumulated(int32_t dtype, int32_t rop, const char* what) {
+// fold only in a plain reduction, a bit fold only at an integer dtype, and at an integer dtype no
+// Mean and no fused post (`has_post`: the post is not the identity Reduced(0)).
+void check_accumulated(int32_t dtype, int32_t rop, const char* what, bool has_post = false) {
   if (!reduce_op_name(rop)) throw Decline{"UnsupportedForm: a reduce op this restatement does not name"};
   if (((is_bit_op(rop) || is_num_op(rop)) && std::strcmp(what, "a reduction") != 0) ||
       (is_bit_op(rop) && !is_int_kernel_dtype(dtype)))
@@ -205,6 +206,7 @@ void check_accumulated(int32_t dtype, int32_t rop, const char* what) {
   if (!is_int_kernel_dtype(dtype))
     throw Decline{std::string("UnsupportedForm: ") + what + " outside F32, F64, I32 and I64"};
   if (rop == UNP_OP_MEAN) throw Decline{"UnsupportedForm: an integer Mean"};
+  if (has_post) throw Decline{"UnsupportedForm: a fused post at an integer dtype"};
 }
 
 void check_rank(int32_t rank) {
@@ -226,7 +228,7 @@ template <class F> J map_leaves(const J& e, const F& leaf);
 J lift_reduction(const std::string& name, int32_t dtype, int32_t rank, int32_t rop, uint32_t axes, bool keepdim,
                  uint32_t block, uint32_t grid, uint32_t n_inputs = 1, const J* body_expr = nullptr,
                  const J* post = nullptr) {
-  check_accumulated(dtype, rop, "a reduction");
+  check_accumulated(dtype, rop, "a reduction", post && !(*post == reduced_leaf(0)));
   const J plain = input_leaf(0);
   const J& bexpr = body_expr ? *body_expr : plain;
   if (post && *post == reduced_leaf(0)) post = nullptr;  // the identity post
@@ -410,7 +412,7 @@ void check_scan_exprs(int32_t dtype, const J& pre, const J* post, uint32_t n_inp
 J lift_scan(const std::string& name, int32_t dtype, int32_t rank, int32_t rop, int32_t axis, bool exclusive,
             bool reverse, uint32_t block, uint32_t grid, uint32_t n_inputs = 1, const J* pre_expr = nullptr,
             const J* post = nullptr) {
-  check_accumulated(dtype, rop, "a scan");
+  check_accumulated(dtype, rop, "a scan", post && !(*post == reduced_leaf(0)));
   const J plain = input_leaf(0);
   const J& pre = pre_expr ? *pre_expr : plain;
   if (post && *post == reduced_leaf(0)) post = nullptr;  // the identity post
