@@ -366,15 +366,17 @@ typedef struct unp_view {
  * parameter (a reduction's output: the kept extents, or the keepdim shape with the reduced axes
  * of extent 1; a gather's table: the output's extents except along the gathered axis, where it
  * holds at least src_extent rows), must not reach below its storage (base plus every negative
- * stride times its extent less one), and a 4-bit view starts on a whole byte; anything else is
- * UNP_INVALID_ARGUMENT before anything launches.
- * Dense row-major views (any stride on an axis of extent one; the gather index broadcast along
- * every axis but the gathered one, e.g. [n, d] with strides [1, 0],
- * tests/kernel_parallel_gather_agrees.rs:80-84) launch the pointer kernels at data + base.  Any
- * other view -- transposed, strided, negative strides, a full-shape gather index -- is read and
- * written through its strides by the reduction (plain body), fused row fold, scan and gather
- * forms (their "strided" interface entries); the row-reduce, pre-map reduction, pre-map scan and dequant forms
- * read dense storage only and refuse it with UNP_INVALID_ARGUMENT (backend.rs:703-707).  The
+ * stride times its extent less one), and an output view must name each element once; anything else
+ * is UNP_INVALID_ARGUMENT before anything launches.
+ * Dense row-major views (any stride on an axis of extent one; a 4-bit view starting on a whole
+ * byte; the gather index broadcast along every axis but the gathered one, e.g. [n, d] with strides
+ * [1, 0], tests/kernel_parallel_gather_agrees.rs:80-84) launch the pointer kernels at data + base.
+ * Any other view -- transposed, strided, negative strides, broadcast, a full-shape gather index --
+ * is read and written through its strides by the reduction (plain body), fused row fold, scan,
+ * gather and elementwise forms (their "strided" interface entries).  The row-reduce, pre-map
+ * reduction, pre-map scan and dequant forms stage it: each such input view is packed into a dense
+ * copy the executor owns (allocated on first use), the pointer kernels run on the copies, and a
+ * staged output is unpacked into its view; elements outside the views are never touched.  The
  * storage behind a view is the caller's: every element the view names must lie inside it. */
 int32_t unp_hip_exec_launch_views(unp_exec* e, const unp_view* views, size_t nviews, const int64_t* scalars,
                                   size_t nscalars, void* stream, unp_error* err);

@@ -1504,29 +1504,27 @@ def test_gather_along_an_axis_of_a_longer_table(hip_device):
 
 
 REFUSED_VIEWS = ["output shorter than the extents", "input of another shape", "wrong rank", "below the storage",
-                 "odd u4 base", "strided dequant output", "table shorter than src_extent", "view count",
-                 "transposed input of a pre-map scan"]
+                 "overlapping dequant output", "table shorter than src_extent", "view count",
+                 "overlapping output of a pre-map scan"]
 
 
 @pytest.mark.parametrize("what", REFUSED_VIEWS)
 def test_views_that_do_not_fit_are_refused(hip_device, what):
     """A view whose shape differs from what the form's extents ask for, that reaches below its storage,
-    that starts mid-byte, or that is strided for a form that reads dense storage only, is refused with
-    INVALID_ARGUMENT before anything launches, and the output storage is untouched."""
+    or that names an output element twice (a staged output would be unpacked over itself), is refused
+    with INVALID_ARGUMENT before anything launches, and the output storage is untouched."""
     H.say(f"[case] views refused: {what}")
-    if what in ("odd u4 base", "strided dequant output"):
+    if what == "overlapping dequant output":
         R, Cc, G = 4, 256, 128
         ex = H.executor(kind="dequant4", q_kind="U4", z_kind="U4", group=G)
         q, s, z = u.DeviceBuffer(R * Cc), u.DeviceBuffer(R * 2 * 2), u.DeviceBuffer(R)
         out = u.DeviceBuffer(2 * R * Cc * 2)
         out.fill(0x5A)
-        qbase = 1 if what == "odd u4 base" else 0
-        ostride = 2 if what == "strided dequant output" else 1
-        views = [(q, (R * Cc,), None, qbase), (s, (R * 2,), None, 0), (z, (R * 2,), None, 0),
-                 (out, (R * Cc,), (ostride,), 0)]
+        views = [(q, (R * Cc,), None, 1), (s, (R * 2,), None, 0), (z, (R * 2,), None, 0),
+                 (out, (R * Cc,), (0,), 0)]
         scalars = [R, Cc]
         check, nbytes = out, 2 * R * Cc * 2
-    elif what == "transposed input of a pre-map scan":
+    elif what == "overlapping output of a pre-map scan":
         from unpopped_amd import expr as X
 
         R, Cc = 8, 32
@@ -1534,7 +1532,7 @@ def test_views_that_do_not_fit_are_refused(hip_device, what):
         a, b = u.DeviceBuffer(R * Cc * 4), u.DeviceBuffer(R * Cc * 4)
         out = u.DeviceBuffer(R * Cc * 4)
         out.fill(0x5A)
-        views = [(a, (R, Cc), (1, R), 0), (b, (R, Cc), None, 0), (out, (R, Cc), None, 0)]
+        views = [(a, (R, Cc), (1, R), 0), (b, (R, Cc), None, 0), (out, (R, Cc), (1, 1), 0)]
         scalars = [R, Cc]
         check, nbytes = out, R * Cc * 4
     elif what == "table shorter than src_extent":
@@ -1572,6 +1570,139 @@ def test_views_that_do_not_fit_are_refused(hip_device, what):
     assert e.value.kind == "InvalidArgument", e.value
     u.synchronize()
     assert np.all(check.download(np.uint8, nbytes) == 0x5A)
+
+# ---- staged storage images: the forms whose kernels read dense storage ------------------
+
+def _nibbles(storage_bytes: np.ndarray) -> np.ndarray:
+    """The 4-bit elements of packed bytes, element 2i in the low nibble of byte i."""
+    b = np.asarray(storage_bytes, np.uint8)
+    return np.stack([b & 15, b >> 4], axis=1).reshape(-1)
+
+
+def _pack(nib: np.ndarray) -> np.ndarray:
+    n = np.asarray(nib, np.uint8)
+    if n.size % 2:
+        n = np.concatenate([n, np.zeros(1, np.uint8)])
+    return (n[0::2] | (n[1::2] << 4)).astype(np.uint8)
+
+
+def test_staged_views_of_a_pre_map_reduction(hip_device):
+    """A float reduction with a body and a post over a transposed and a row-reversed input, into a
+    strided output; and an integer-body reduction over a strided input: each equals the oracle on the
+    logical arrays (dyadic data: bit for bit), with the output's other elements untouched."""
+    H.say("[case] staged views: pre-map reduction")
+    R, Cc = 33, 517
+    x0s = dyadic(301, (Cc, R), np.float32)           # storage of the transposed input
+    x1s = dyadic(302, (R, Cc), np.float32)           # rows reversed through a negative stride
+    outs = np.full(2 * R + 1, 9.0, np.float32)
+    body, post = X.input(0) * X.input(1) + X.input(0), X.reduced(0) * X.konst(0.5)
+    ex = H.reduce_expr_executor("F32", 2, "Sum", (1,), body, post, 2)
+    images = [(x0s, (R, Cc), (1, R), 0), (x1s, (R, Cc), (-Cc, 1), (R - 1) * Cc), (outs, (R,), (2,), 1)]
+    got = _run_images(ex, images, [R, Cc])
+    logical = [np.ascontiguousarray(_logical(st, sh, strd, b)) for st, sh, strd, b in images[:2]]
+    _, want = oracle_expr(logical, (1,), "Sum", body, post)
+    assert got[2].tobytes() == _expect(outs, (R,), (2,), 1, want).tobytes()
+    assert ex.last_launch()["entry"].startswith(ex.kernel.name)
+    # integer body, a strided input (every other column) and a reversed output
+    xi = rng(303).integers(-1000, 1000, (R, 2 * Cc)).astype(np.int64)
+    yi = rng(304).integers(-5, 5, (R, Cc)).astype(np.int64)
+    oi = np.full(R, 77, np.int64)
+    ibody = {"Div": [{"Mul": [{"Input": 0}, {"Input": 1}]}, {"Input": 1}]}
+    k = u.lift_reduction("r", "I64", 2, "Sum", axes=(1,), n_inputs=2, body=ibody, launch=(256, 4))
+    exi = u.Executor(u.HipBackend().lower_kernel(k))
+    images = [(xi, (R, Cc), (2 * Cc, 2), 1), (yi, (R, Cc), None, 0), (oi, (R,), (-1,), R - 1)]
+    got = _run_images(exi, images, [R, Cc])
+    logical = [np.ascontiguousarray(_logical(st, sh, strd if strd else (Cc, 1), b)) for st, sh, strd, b in images[:2]]
+    want = oracle.int_reduce_expr(logical, (1,), "Sum", ibody, "I64")
+    assert got[2].tobytes() == want[::-1].tobytes()
+
+
+def test_staged_views_of_a_pre_map_scan(hip_device):
+    """A scan with a pre and a post over a transposed input and a strided one, into an output whose
+    columns run backwards: the oracle's scan of the logical arrays (dyadic: bit for bit), the rest of
+    the output storage untouched."""
+    H.say("[case] staged views: pre-map scan")
+    R, Cc = 7, 3001
+    x0s = _eighths(311, (Cc, R))
+    x1s = _eighths(312, (R, 2 * Cc))
+    outs = np.full((R, Cc + 3), -4.0, np.float32)
+    pre, post = X.input(0) * X.input(1), X.reduced(0) - X.input(0)
+    ex = H.scan_expr_executor("F32", 2, "Sum", 1, pre, post, 2)
+    oview = ((R, Cc), (Cc + 3, -1), Cc + 1)
+    images = [(x0s, (R, Cc), (1, R), 0), (x1s, (R, Cc), (2 * Cc, 2), 0), (outs, *oview)]
+    got = _run_images(ex, images, [R, Cc])
+    logical = [np.ascontiguousarray(_logical(st, sh, strd, b)) for st, sh, strd, b in images[:2]]
+    want = oracle.scan_expr(logical, 1, "Sum", pre, post)
+    assert got[2].tobytes() == _expect(outs, *oview, want).tobytes()
+
+
+def test_staged_views_of_a_row_reduce(hip_device):
+    """Softmax over a transposed input into a row-strided output: bit for bit the dense launch on the
+    logical array (the same kernels on the staged copy), within the row-reduce bars of the oracle."""
+    H.say("[case] staged views: row reduce")
+    R, Cc = 19, 1000
+    xs = rng(321).normal(size=(Cc, R)).astype(np.float32)
+    x0, r0, r1 = X.input(0), X.reduced(0), X.reduced(1)
+    stages = [(x0, "Max"), ((x0 - r0).exp(), "Sum")]
+    epi = (x0 - r0).exp() / r1
+    ex = H.row_reduce_executor("F32", 2, stages, epi)
+    outs = np.full((R, Cc + 8), 3.0, np.float32)
+    images = [(xs, (R, Cc), (1, R), 0), (outs, (R, Cc), (Cc + 8, 1), 4)]
+    got = _run_images(ex, images, [R, Cc])
+    logical = np.ascontiguousarray(xs.T)
+    dense = H.row_reduce([logical], stages, epi)
+    assert got[1].tobytes() == _expect(outs, (R, Cc), (Cc + 8, 1), 4, dense).tobytes()
+    want = oracle.row_reduce([logical], stages, epi)
+    assert np.allclose(dense, want, rtol=1e-6, atol=0)
+
+
+def test_staged_views_of_the_dequant(hip_device):
+    """The int4 dequant with its weights every other nibble from an odd base, its scales reversed, its
+    zero points strided, into every other bf16 of the output: the oracle on the logical arrays, bit for
+    bit, and the output's other elements untouched."""
+    H.say("[case] staged views: dequant4")
+    R, Cc, G = 12, 384, 128
+    ng = Cc // G
+    r = rng(331)
+    qst = r.integers(0, 256, R * Cc, dtype=np.uint8)       # 2 R C nibbles; the view takes 1, 3, 5, ...
+    sst = np.array([0x3C00 + int(v) for v in r.integers(-600, 600, R * ng)], np.uint16)
+    zst = r.integers(0, 256, R * ng, dtype=np.uint8)       # 2 R ng nibbles; the view takes every other
+    outs = np.full(2 * R * Cc, 0x5A5A, np.uint16)
+    ex = H.executor(kind="dequant4", q_kind="U4", z_kind="U4", group=G)
+    dq, ds, dz, do = (u.DeviceBuffer.from_array(a) for a in (qst, sst, zst, outs))
+    ex.launch_views([(dq, (R * Cc,), (2,), 1), (ds, (R * ng,), (-1,), R * ng - 1), (dz, (R * ng,), (2,), 0),
+                     (do, (R * Cc,), (2,), 1)], [R, Cc])
+    u.synchronize()
+    got = do.download(np.uint16, outs.size)
+    q_log = _pack(_nibbles(qst)[1::2][: R * Cc])
+    s_log = sst[::-1].copy()
+    z_log = _pack(_nibbles(zst)[0::2][: R * ng])
+    want = oracle.dequant4_bf16(q_log, s_log, z_log, R, Cc, G)
+    assert got[1::2].tobytes() == want.tobytes()
+    assert np.all(got[0::2] == 0x5A5A)
+
+
+def test_staged_views_of_the_dequant_gemm(hip_device):
+    """The dequant GEMM with reversed weights (a negative stride over the nibbles), strided activations
+    and a strided output: the oracle on the logical arrays, bit for bit."""
+    H.say("[case] staged views: dequant GEMM")
+    R, K, C, G = 32, 256, 16, 64
+    w, zero, scale, x = _gemm_data(341, R, K, C, G, np.int32)
+    wn = _nibbles(w)[: R * K]
+    wst = _pack(wn[::-1])                                   # storage holds the nibbles backwards
+    xst = np.zeros(2 * K * C, np.int32)
+    xst[0::2] = x
+    outs = np.full(3 * R * C, 11, np.int32)
+    ex = H.executor(kind="dequant_gemm", q_kind="U4", dtype="I32", group=G)
+    dw, dz, ds, dx, do = (u.DeviceBuffer.from_array(a) for a in (wst, zero, scale, xst, outs))
+    ex.launch_views([(dw, (R * K,), (-1,), R * K - 1), (dz, (R * (K // G),), None, 0),
+                     (ds, (R * (K // G),), None, 0), (dx, (K * C,), (2,), 0), (do, (R * C,), (3,), 2)], [R, K, C])
+    u.synchronize()
+    got = do.download(np.int32, outs.size)
+    want = oracle.dequant_gemm_i32(w, zero, scale, x, R, K, C, G)
+    assert got[2::3].tobytes() == want.reshape(-1).tobytes()
+    assert np.all(got[0::3] == 11) and np.all(got[1::3] == 11)
+
 
 # ---------------------------------------------------------------------------------------
 # Launch geometry: a device-class grid, never derived from an extent (PATENT-SWEEP.md:269)

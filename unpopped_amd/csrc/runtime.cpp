@@ -113,6 +113,9 @@ struct unp_exec {
   uint32_t grid[3] = {0, 0, 0};
   uint32_t block[3] = {0, 0, 0};
   std::string last_entry;
+  // Dense copies of staged storage images, one per buffer parameter (grown on demand).
+  std::vector<void*> stage;
+  std::vector<size_t> stage_cap;
 };
 
 extern "C" {
@@ -427,6 +430,8 @@ void unp_hip_exec_destroy(unp_exec* x) {
   if (x->counter) hipFree(x->counter);
   if (x->counters) hipFree(x->counters);
   if (x->stall) hipFree(x->stall);
+  for (void* p : x->stage)
+    if (p) hipFree(p);
   if (x->mod) hipModuleUnload(x->mod);
   delete x;
 }
@@ -1554,6 +1559,7 @@ bool views_dense(const unp_exec* x, const unp_view* v, size_t n, int64_t src_ext
   const unp_form& f = x->l.form;
   for (size_t b = 0; b < n; ++b) {
     if (view_empty(v[b])) continue;
+    if (view_elem_bits(x->l, b) < 8 && v[b].base % 2 != 0) return false;  // a 4-bit view starting mid-byte
     if (f.kind == UNP_FORM_GATHER && !x->l.gx.plain) return false;  // one entry reads every layout
     if (f.kind == UNP_FORM_ELEMENTWISE && x->l.ew.permuted()) return false;  // the strided entry
     if (f.kind == UNP_FORM_GATHER && b < 2) {
@@ -1730,7 +1736,86 @@ int32_t strided_elementwise(unp_exec* x, const unp_view* v, const std::vector<in
   return launch_elementwise_strided(x, ptrs, d, s, err);
 }
 
+// Whether buffer parameter b of a lowered form is one it writes (an output).
+bool writes_buffer(const unp_exec* x, size_t b) {
+  switch (x->l.form.kind) {
+    case UNP_FORM_ROW_REDUCE2: return b == 1 || b == 2;
+    case UNP_FORM_DEQUANT4: return b == 3;
+    case UNP_FORM_DEQUANT_GEMM: return b == 4;
+    default: {
+      size_t nbuf = 0, nscal = 0;
+      param_counts(x, nbuf, nscal);
+      return b + 1 == nbuf;  // the output follows the inputs
+    }
+  }
+}
+
+// Whether the view's elements are pairwise distinct storage positions: with the axes of extent
+// above one ordered by |stride|, each stride exceeds the span of the smaller ones.
+bool view_injective(const unp_view& v) {
+  std::vector<std::pair<int64_t, int64_t>> ax;  // (|stride|, extent)
+  for (int d = 0; d < v.rank; ++d)
+    if (v.shape[d] > 1) ax.push_back({v.stride[d] < 0 ? -v.stride[d] : v.stride[d], v.shape[d]});
+  std::sort(ax.begin(), ax.end());
+  int64_t span = 0;
+  for (const auto& a : ax) {
+    if (a.first <= span) return false;
+    span += a.first * (a.second - 1);
+  }
+  return true;
+}
+
 }  // namespace
+
+// A form whose kernels read and write dense storage, over views some of which are not dense
+// row-major: each such input view is packed into a dense copy the executor owns, the form's
+// pointer launch runs on the copies, and a staged output is unpacked into its view afterwards
+// (views.hip).  Elements outside the views are never touched.  An output view must not name an
+// element twice.
+static int32_t staged_launch(unp_exec* x, const unp_view* v, size_t n, const int64_t* scalars, size_t nscalars,
+                             void* stream, unp_error* err) {
+  int32_t rc = begin_launch(x, err);
+  if (rc != UNP_OK) return rc;
+  auto is_out = [&](size_t b) { return writes_buffer(x, b); };
+  if (x->stage.size() < n) {
+    x->stage.resize(n, nullptr);
+    x->stage_cap.resize(n, 0);
+  }
+  std::vector<unp_arg> args(n + nscalars);
+  std::vector<char> staged(n, 0);
+  for (size_t b = 0; b < n; ++b) {
+    const int bits = view_elem_bits(x->l, b);
+    args[b].is_buffer = 1;
+    const bool dense = view_empty(v[b]) || (row_major(v[b]) && (bits >= 8 || v[b].base % 2 == 0));
+    if (dense) {
+      args[b].value = v[b].data + (uint64_t)(v[b].base * bits / 8);
+      continue;
+    }
+    if (is_out(b) && !view_injective(v[b]))
+      return invalid(err, "buffer " + std::to_string(b) + ": an output view that names an element twice");
+    const size_t bytes = (unp::view_stage_bytes(v[b], bits) + 255) & ~(size_t)255;
+    if (x->stage_cap[b] < bytes) {
+      if (x->stage[b]) hipFree(x->stage[b]);
+      x->stage[b] = nullptr;
+      x->stage_cap[b] = 0;
+      const hipError_t e = hipMalloc(&x->stage[b], bytes);
+      if (e != hipSuccess) return hip_fail(err, "hipMalloc(staged view)", e);
+      x->stage_cap[b] = bytes;
+    }
+    if (!is_out(b) && (rc = unp::view_stage_in(v[b], bits, x->stage[b], stream, err)) != UNP_OK) return rc;
+    args[b].value = (uint64_t)x->stage[b];
+    staged[b] = 1;
+  }
+  for (size_t i = 0; i < nscalars; ++i) {
+    args[n + i].is_buffer = 0;
+    args[n + i].value = (uint64_t)scalars[i];
+  }
+  if ((rc = unp_hip_exec_launch(x, args.data(), args.size(), stream, err)) != UNP_OK) return rc;
+  for (size_t b = 0; b < n; ++b)
+    if (staged[b] && is_out(b) && (rc = unp::view_stage_out(x->stage[b], v[b], view_elem_bits(x->l, b), stream, err)) != UNP_OK)
+      return rc;
+  return UNP_OK;
+}
 
 extern "C" int32_t unp_hip_exec_launch_views(unp_exec* x, const unp_view* views, size_t nviews,
                                              const int64_t* scalars, size_t nscalars, void* stream,
@@ -1771,8 +1856,7 @@ extern "C" int32_t unp_hip_exec_launch_views(unp_exec* x, const unp_view* views,
     }
     if (lo < 0) return invalid(err, at + "the view reaches below its storage (base plus its negative strides < 0)");
     if (hi > ((__int128)1 << 60)) return invalid(err, at + "the view's offsets exceed 2^60 elements");
-    if (bits < 8 && (v.base * bits) % 8 != 0)
-      return invalid(err, at + "a 4-bit view must start on a whole byte (an even base)");
+    if (bits < 8 && writes_buffer(x, b)) return invalid(err, at + "a 4-bit output view");
     if (!v.data) return invalid(err, at + "null storage");
   }
   const int64_t raw_src = f.kind == UNP_FORM_GATHER ? scalars[f.rank] : 0;
@@ -1791,13 +1875,11 @@ extern "C" int32_t unp_hip_exec_launch_views(unp_exec* x, const unp_view* views,
     return unp_hip_exec_launch(x, args.data(), args.size(), stream, err);
   }
   // Some view is transposed, strided, reversed or broadcast: the forms with a strided entry read
-  // through the strides; the others read dense storage only.
+  // through the strides; the others stage those views through dense copies.
   const bool plain_reduction = (f.kind == UNP_FORM_REDUCTION && x->l.rx.plain) || f.kind == UNP_FORM_ROW_REDUCE2;
   const bool plain_scan = f.kind == UNP_FORM_SCAN && x->l.rx.plain;
   if (!plain_reduction && !plain_scan && f.kind != UNP_FORM_GATHER && f.kind != UNP_FORM_ELEMENTWISE)
-    return invalid(err,
-                   "a view that is not dense row-major: this form reads dense storage (the plain reduction, plain "
-                   "scan, gather and elementwise forms read any strides), so make the view contiguous first");
+    return staged_launch(x, views, nviews, scalars, nscalars, stream, err);
   const int32_t rc = begin_launch(x, err);
   if (rc != UNP_OK) return rc;
   hipStream_t s = (hipStream_t)stream;

@@ -203,6 +203,13 @@ struct Scratch {
 // Zero `bytes` (a multiple of 16) at the device address `base` with a kernel on `stream`
 // (scratch.hip): the static scratch's per-call clear, a kernel node under graph capture.
 int32_t scratch_clear(void* base, size_t bytes, void* stream, unp_error* err);
+
+// Staged storage images (views.hip): the dense bytes a view of `bits`-bit elements packs into, the
+// pack of an input view into `dst` (row-major over its shape), and the unpack of a dense output into
+// its view, each as kernels on `stream`.
+size_t view_stage_bytes(const unp_view& v, int bits);
+int32_t view_stage_in(const unp_view& v, int bits, void* dst, void* stream, unp_error* err);
+int32_t view_stage_out(const void* src, const unp_view& v, int bits, void* stream, unp_error* err);
 // unp_hip_exec_launch with every workspace taken from [scratch, scratch + cap) and cleared on the
 // launch stream first: it calls no allocator, and refuses a launch whose workspace does not fit
 // with UNP_INVALID_ARGUMENT before anything runs.
