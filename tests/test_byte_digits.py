@@ -4,6 +4,7 @@ digits d_i in [-128, 127] with sum d_i 256^i = v modulo 2^32, and products of tw
 expansions, summed by digit class i + j < 4 and shifted by 8 (i + j) bits, equal the 32-bit
 wrapping product."""
 import numpy as np
+import pytest
 
 EDGES = np.array([0, 1, 127, 128, 255, 256, 0x7F7F7F7F, 0x80808080, 0x7FFFFFFF, 0x80000000, 0xFFFFFFFF,
                   0x00808080, 0x80000080, 0xFF00FF00], dtype=np.uint64)
@@ -165,3 +166,137 @@ def test_zero_point_pass_check_sees_planted_mistakes():
     assert not np.array_equal(_zero_point_pass(sz, xsum, 0, 45, masks=False), want)
     assert not np.array_equal(_zero_point_pass(sz, xsum, 0, 45, d_rows=lambda v, q: 8 * (v & 3) + 4 * q + (v >> 2)),
                               want)
+
+
+# ---------------------------------------------------------------------------------------
+# The zero-point pass's buffer addresses, lane by lane.  Its loads are raw buffer loads: the
+# resource holds num_records (R ng 4 bytes for scales and zero points, ng Cp 4 for the column
+# sums) and the whole byte offset is the 32-bit vector offset, so a load past num_records reads 0
+# and touches no memory.  What must hold: every offset the kernel forms (an int sum of ints)
+# stays in [0, 2^31), and every load whose value enters an output reads its own element inside
+# num_records.  A CPU restatement of the launcher's geometry (runtime.cpp run_dequant_gemm,
+# streaming branch) and of the pass's offsets (unp_device.hip dqg_stream: sofs, load_step, cofs),
+# for every thread of the blocks of the last row tile and of the last split.
+# ---------------------------------------------------------------------------------------
+
+LIMIT = 0x7FFFFFFF
+
+
+def _stream_geometry(x_bytes, group):
+    """The emitter's stream entry shape (emit_hip.cpp lower_dequant_gemm): waves WR x WC, tiles
+    TM x TN of 32 x 32 per wave."""
+    skc = 0 if group % 64 else (128 if x_bytes == 1 and group % 128 == 0 else 64)
+    big = x_bytes == 1 and skc == 128
+    two = big or x_bytes == 4
+    wr, wc = (2, 2) if big else (4, 1)
+    tm, tn = (2 if big else 1), (2 if two else 1)
+    return skc, wr, wc, tm, tn
+
+
+def _zero_point_offsets(R, K, C, group, x_bytes, cu=256):
+    """Yield, per examined block, the pass's loads: (kind, offsets, rows/cols, groups, used) arrays."""
+    skc, WR, WC, TM, TN = _stream_geometry(x_bytes, group)
+    assert skc, "a group of whole 64-value chunks"
+    BM, BN, NW = 32 * WR * TM, 32 * WC * TN, 4
+    ng = K // group
+    cw = max(BN, 64)
+    Cp = (C + cw - 1) // cw * cw
+    admitted = (R + 256) * ng * 4 < LIMIT and (ng + 32) * Cp * 4 < LIMIT
+    tiles_r, tiles_c = (R + BM - 1) // BM, (C + BN - 1) // BN
+    S = max(1, min((2 * cu + tiles_r * tiles_c - 1) // (tiles_r * tiles_c), ng // 4))
+    units = tiles_r * S
+    blocks = (units + 7) // 8 * 8 * tiles_c
+    tid = np.arange(256, dtype=np.int64)
+    lane, wave = tid & 63, tid >> 6
+    wc, q, l32 = wave % WC, lane >> 5, lane & 31
+    srow, sg = tid // 32, tid % 32
+    SZN = BM * 32 // (64 * NW)
+    # the units of the first and last row tiles (every split) and the last split of the last two
+    # row tiles, each at its first and last column tile; their block ids by inverting the
+    # XCD-aware mapping b -> (u, ct): slot = b / 8, u = (slot / tiles_c) 8 + b % 8, ct = slot % tiles_c
+    wanted = {(tiles_r - 1, sp) for sp in range(S)} | {(0, sp) for sp in range(S)}
+    wanted |= {(r, S - 1) for r in range(max(0, tiles_r - 2), tiles_r)}
+    picks = []
+    for rt, split in sorted(wanted):
+        u = rt * S + split
+        for ct in sorted({0, tiles_c - 1}):
+            b = ((u // 8) * tiles_c + ct) * 8 + u % 8
+            assert b < blocks
+            xcd, slot = b % 8, b // 8
+            assert ((slot // tiles_c) * 8 + xcd, slot % tiles_c) == (u, ct)
+            picks.append((u, ct))
+    out = []
+    for u, ct in picks:
+        rt, split = u // S, u % S
+        tile_r, tile_c = rt * BM, ct * BN
+        g0, g1 = ng * split // S, ng * (split + 1) // S
+        sofs = ((tile_r + srow) * ng + sg) * 4
+        steps = list(range(g0, g1, 32))
+        for gc in steps:
+            gl = min(g1 - gc, 32)
+            for m in range(SZN):
+                so = (gc + m * (64 * NW // 32) * ng) * 4
+                row = tile_r + srow + 8 * m
+                grp = sg + gc
+                out.append(("sz", sofs, so, row, grp, sg < gl))
+            for t in range(TN):
+                col = tile_c + 32 * (wc * TN + t) + l32
+                cofs = (16 * q * Cp + col) * 4
+                for k in range(16):
+                    grp = gc + 16 * q + k
+                    out.append(("cs", cofs, (gc + k) * Cp * 4, col, grp, (16 * q + k) < gl))
+    return admitted, ng, Cp, out
+
+
+SHAPES = [
+    # (R, K, C, group, activation bytes): ragged rows and columns, a few splits and the last one
+    (4096 + 17, 4096, 200, 128, 1),
+    (300, 8192, 96, 64, 4),
+    (129, 1024, 65, 128, 1),
+    (1000, 2048, 130, 256, 4),
+    (33, 512, 31, 64, 1),
+]
+
+
+@pytest.mark.parametrize("R,K,C,group,xb", SHAPES)
+def test_zero_point_pass_reads_its_own_elements_inside_num_records(R, K, C, group, xb):
+    admitted, ng, Cp, loads = _zero_point_offsets(R, K, C, group, xb)
+    assert admitted and loads
+    for kind, base, step, idx, grp, used in loads:
+        total = base + step  # the kernel adds the two ints
+        assert (base >= 0).all() and (base < LIMIT).all() and 0 <= step < LIMIT
+        assert (total >= 0).all() and (total < LIMIT).all(), kind
+        if kind == "sz":
+            rows = np.broadcast_to(idx, base.shape)
+            live = np.broadcast_to(used, base.shape) & (rows < R)
+            want = (rows * ng + grp) * 4
+            assert np.array_equal(total[live], want[live])
+            assert (total[live] < R * ng * 4).all()
+            # a row past R reads nothing: its offset lies past num_records
+            assert (total[rows >= R] >= R * ng * 4).all()
+        else:
+            cols = np.broadcast_to(idx, base.shape)
+            live = np.broadcast_to(used, base.shape) & (grp < ng)
+            want = (grp * Cp + cols) * 4
+            assert np.array_equal(total[live], want[live])
+            assert (cols < Cp).all() and (total[live] < ng * Cp * 4).all()
+
+
+@pytest.mark.parametrize("which", ["rows", "columns"])
+def test_zero_point_pass_offsets_fit_at_the_launchers_bound(which):
+    """Shapes just inside the launcher's admission bound ((R + 256) ng 4 and (ng + 32) Cp 4 under
+    2^31): the largest offset any lane forms still fits, and one step more is refused."""
+    K, group, xb = 8192, 128, 1
+    ng = K // group
+    if which == "rows":
+        R = LIMIT // (4 * ng) - 257
+        C = 64
+    else:
+        R = 128
+        C = LIMIT // (4 * (ng + 32)) // 128 * 128 - 128
+    admitted, ng2, Cp, loads = _zero_point_offsets(R, K, C, group, xb)
+    assert admitted
+    for _, base, step, *_ in loads:
+        assert ((base + step) < LIMIT).all() and ((base + step) >= 0).all()
+    R2, C2 = (R + 300, C) if which == "rows" else (R, C + 8 * 128)
+    assert not _zero_point_offsets(R2, K, C2, group, xb)[0]
