@@ -649,7 +649,7 @@ struct Emitter {
       std::string tt = t;
       for (char& ch : tt) ch = (char)tolower(ch);
       const std::string name = op == "Div" ? "div" : op == "Shl" ? "shl" : "shr";
-      return "unp_" + name + "_" + tt + "(" + x[0] + ", " + x[1] + ")";
+      return "leg_" + name + "_" + tt + "(" + x[0] + ", " + x[1] + ")";
     }
     refuse("the integer operation " + op);
   }
@@ -722,15 +722,15 @@ struct Emitter {
     if (is_narrow(to)) {
       if (spec.sat != "Wrap") refuse("a Cast to " + to + " with saturation " + spec.sat);
       if (rounding_matters(from, to) && spec.round != "NearestEven") refuse("a Cast to " + to + " rounding " + spec.round);
-      const std::string enc = to == "F16" ? "unp_f16_enc" : "unp_bf16_enc";
-      const std::string exact = to == "F16" ? "unp_d_to_f16" : "unp_d_to_bf16";
-      if (is_narrow(from)) return enc + "(" + std::string(from == "F16" ? "unpopped_f16_load" : "unpopped_bf16_load") + "(" + x + "))";
-      if (from == "F32" || from == "F32Strict") return enc + "(" + x + ")";
-      if (from == "I8" || from == "I16" || from == "U8" || from == "U16") return enc + "((float)(" + x + "))";
-      if (from == "F64" || from == "I32" || from == "U32" || from == "I64" || from == "U64") return exact + "((double)(" + x + "))";
+      // every source value is exact in a double, which the encoder rounds once
+      const std::string enc = to == "F16" ? "leg_to_f16" : "leg_to_bf16";
+      if (is_narrow(from)) return enc + "((double)" + std::string(from == "F16" ? "leg_f16_value" : "leg_bf16_value") + "(" + x + "))";
+      if (from == "F32" || from == "F32Strict" || from == "I8" || from == "I16" || from == "U8" || from == "U16" ||
+          from == "F64" || from == "I32" || from == "U32" || from == "I64" || from == "U64")
+        return enc + "((double)(" + x + "))";
       refuse("the Cast " + from + " -> " + to);
     }
-    const std::string dec = from == "F16" ? "unpopped_f16_load" : "unpopped_bf16_load";
+    const std::string dec = from == "F16" ? "leg_f16_value" : "leg_bf16_value";
     return cast(dec + "(" + x + ")", "F32", spec);
   }
 
@@ -762,13 +762,13 @@ struct Emitter {
       if (!rnd) refuse("the rounding mode " + r);
       long long lo, hi;
       int_range(to, lo, hi);
-      return "((" + t + ")unp_sat_f2ll(" + rnd + "((double)(" + x + ")), " + ll_lit(lo) + ", " + ll_lit(hi) + "))";
+      return "((" + t + ")leg_f2i_sat(" + rnd + "((double)(" + x + ")), " + ll_lit(lo) + ", " + ll_lit(hi) + "))";
     }
     if (!ff && tf) return "((" + t + ")(" + x + "))";
     if (spec.sat == "Clamp") {
       long long lo, hi;
       int_range(to, lo, hi);
-      return "((" + t + ")unp_clamp_ll((long long)(" + x + "), " + ll_lit(lo) + ", " + ll_lit(hi) + "))";
+      return "((" + t + ")leg_clamp((long long)(" + x + "), " + ll_lit(lo) + ", " + ll_lit(hi) + "))";
     }
     return "((" + t + ")(" + x + "))";
   }
@@ -1063,8 +1063,9 @@ struct Emitter {
     line("}");
   }
 
-  // Block-level statements: barrier-free runs become thread loops, a barrier ends one, and a
-  // construct holding a barrier is spelled once, its condition or bounds read at thread 0.
+  // A statement list at block level: each stretch of statements free of barriers is emitted as one
+  // loop over the block's threads; a statement containing a barrier closes the stretch and is
+  // emitted a single time, whatever condition or loop bounds it has evaluated as thread 0 sees them.
   void phases(const V& stmts) {
     std::vector<const V*> run;
     for (const V& s : stmts.a) {
@@ -1186,83 +1187,89 @@ struct Emitter {
 };
 
 // ---- the prelude: helpers the spellings call ------------------------------------------------------
-// Conversions and total integer operations (the semantics of typed.rs:27-76): float to integer
-// saturates with NaN to 0; integer division by zero, and MIN / -1, give the dividend; a shift count is
-// taken modulo the width and a right shift of a negative is arithmetic.
-const char* kTypedHelpers = R"(static long long unp_sat_f2ll(double y, long long lo, long long hi) {
-    long long v;
+// The semantics are the C leg's (typed.rs:27-76, narrow.rs, cfamily.rs:223-304); the text is this
+// file's own.  Float to integer: a NaN gives 0 and a value past either end of the kind the nearer
+// end (the caller has rounded it already).  Integer Div, Shl, Shr by the total rule: a zero divisor
+// gives the dividend, a signed divisor of -1 negates with wrap (MIN / -1 is MIN), a shift count's
+// bits are taken modulo the width, and >> on a signed kind fills with the sign bit.
+const char* kTypedHelpers = R"(static long long leg_f2i_sat(double y, long long lo, long long hi) {
     if (y != y) return 0;
-    if (y >= 9223372036854775808.0) return hi;
-    if (y < -9223372036854775808.0) return lo;
-    v = (long long)y;
-    return v > hi ? hi : (v < lo ? lo : v);
+    if (y <= (double)lo) return lo;
+    if (y >= (double)hi) return hi;
+    return (long long)y;
 }
-static long long unp_clamp_ll(long long v, long long lo, long long hi) { return v > hi ? hi : (v < lo ? lo : v); }
-static int unp_div_i32(int a, int b) { return (b == 0 || (b == -1 && a == -2147483647 - 1)) ? a : a / b; }
-static long long unp_div_i64(long long a, long long b) {
-    return (b == 0 || (b == -1 && a == -9223372036854775807LL - 1)) ? a : a / b;
+static long long leg_clamp(long long v, long long lo, long long hi) {
+    if (v < lo) return lo;
+    return v > hi ? hi : v;
 }
-static unsigned int unp_div_u32(unsigned int a, unsigned int b) { return b ? a / b : a; }
-static unsigned long long unp_div_u64(unsigned long long a, unsigned long long b) { return b ? a / b : a; }
-static int unp_shl_i32(int a, int c) { return (int)((unsigned int)a << ((unsigned int)c & 31u)); }
-static int unp_shr_i32(int a, int c) { unsigned int k = (unsigned int)c & 31u; return a >= 0 ? a >> k : ~(~a >> k); }
-static long long unp_shl_i64(long long a, long long c) {
-    return (long long)((unsigned long long)a << ((unsigned long long)c & 63ull));
+#define LEG_SIGNED_OPS(S, T, U, W) \
+static T leg_div_##S(T a, T b) { \
+    if (b == 0) return a; \
+    if (b == (T)-1) return (T)((U)0 - (U)a); \
+    return a / b; \
+} \
+static T leg_shl_##S(T a, T c) { return (T)((U)a << ((U)c & (U)(W - 1))); } \
+static T leg_shr_##S(T a, T c) { \
+    const U k = (U)c & (U)(W - 1); \
+    const U sign_fill = a < 0 ? ~(~(U)0 >> k) : (U)0; \
+    return (T)(((U)a >> k) | sign_fill); \
 }
-static long long unp_shr_i64(long long a, long long c) {
-    unsigned long long k = (unsigned long long)c & 63ull;
-    return a >= 0 ? a >> k : ~(~a >> k);
-}
-static unsigned int unp_shl_u32(unsigned int a, unsigned int c) { return a << (c & 31u); }
-static unsigned int unp_shr_u32(unsigned int a, unsigned int c) { return a >> (c & 31u); }
-static unsigned long long unp_shl_u64(unsigned long long a, unsigned long long c) { return a << (c & 63ull); }
-static unsigned long long unp_shr_u64(unsigned long long a, unsigned long long c) { return a >> (c & 63ull); }
+#define LEG_UNSIGNED_OPS(S, U, W) \
+static U leg_div_##S(U a, U b) { return b == 0 ? a : a / b; } \
+static U leg_shl_##S(U a, U c) { return a << (c & (U)(W - 1)); } \
+static U leg_shr_##S(U a, U c) { return a >> (c & (U)(W - 1)); }
+LEG_SIGNED_OPS(i32, int, unsigned int, 32)
+LEG_SIGNED_OPS(i64, long long, unsigned long long, 64)
+LEG_UNSIGNED_OPS(u32, unsigned int, 32)
+LEG_UNSIGNED_OPS(u64, unsigned long long, 64)
 )";
 
-// The F16/Bf16 codec: decode is exact; encode rounds a double once to nearest even, by scaling the
-// magnitude with powers of two (exact) and rounding the scaled significand, so the only rounding is the
-// one written out.  A NaN encodes as the quiet NaN with its sign.
-const char* kRoundHelper = R"(static double unp_rne_int(double q) {
-    double f = floor(q), r = q - f;
-    if (r > 0.5 || (r == 0.5 && fmod(f, 2.0) != 0.0)) f += 1.0;
+// The 16-bit float codec for a binary format of `eb` exponent bits and `mb` fraction bits (F16: 5, 10;
+// Bf16: 8, 7).  Decoding is exact.  Encoding rounds a double once, to nearest with ties to even: the
+// magnitude is scaled by a power of two (exact) to units of its binade's quantum (the subnormal
+// quantum below the normal range), rounded to an integer in the default rounding mode, and the
+// integer's bits become the fraction; a count reaching the next binade carries into the exponent
+// field, and past the largest finite value the result is infinity.  A NaN encodes as the quiet NaN
+// with its sign.
+const char* kCodec = R"(static unsigned leg_encode(double x, int eb, int mb) {
+    const unsigned sign = signbit(x) ? 1u << (eb + mb) : 0u, inf = ((1u << eb) - 1u) << mb;
+    const int bias = (1 << (eb - 1)) - 1, emin = 1 - bias;
+    double a = fabs(x), units;
+    unsigned long long n;
+    unsigned body;
+    int e;
+    if (a != a) return sign | inf | (1u << (mb - 1));
+    if (a == 0.0) return sign;
+    if (isinf(a)) return sign | inf;
+    (void)frexp(a, &e);
+    e -= 1;
+    if (e < emin) e = emin;
+    if (e > bias) return sign | inf;
+    units = nearbyint(ldexp(a, mb - e));
+    n = (unsigned long long)units;
+    if (e == emin && n < (1ull << mb)) body = (unsigned)n;
+    else body = ((unsigned)(e + bias) << mb) + (unsigned)(n - (1ull << mb));
+    return sign | (body >= inf ? inf : body);
+}
+static double leg_decode(unsigned h, int eb, int mb) {
+    const int bias = (1 << (eb - 1)) - 1;
+    const unsigned field = (h >> mb) & ((1u << eb) - 1u), frac = h & ((1u << mb) - 1u);
+    double v;
+    if (field == (1u << eb) - 1u) v = frac ? NAN : INFINITY;
+    else if (field == 0) v = ldexp((double)frac, 1 - bias - mb);
+    else v = ldexp((double)(frac | (1u << mb)), (int)field - bias - mb);
+    return (h >> (eb + mb)) & 1u ? -v : v;
+}
+static unsigned short leg_to_bf16(double x) { return (unsigned short)leg_encode(x, 8, 7); }
+static unsigned short leg_to_f16(double x) { return (unsigned short)leg_encode(x, 5, 10); }
+static float leg_bf16_value(unsigned short h) {
+    /* a Bf16 is the upper half of an F32: the bits move, NaN payloads included */
+    const unsigned int w = (unsigned int)h << 16;
+    float f;
+    memcpy(&f, &w, sizeof f);
     return f;
 }
-)";
-const char* kBf16Load = R"(static float unpopped_bf16_load(unsigned short h) {
-    union { unsigned int u; float f; } v;
-    v.u = (unsigned int)h << 16;
-    return v.f;
-}
-)";
-const char* kF16Load = R"(static float unpopped_f16_load(unsigned short h) {
-    int e = (h >> 10) & 31, m = h & 1023;
-    float v = e == 0 ? ldexpf((float)m, -24) : e == 31 ? (m ? NAN : INFINITY) : ldexpf((float)(m + 1024), e - 25);
-    return (h & 0x8000u) ? -v : v;
-}
-)";
-const char* kBf16Enc = R"(static unsigned short unp_d_to_bf16(double x) {
-    unsigned short s = signbit(x) ? 0x8000u : 0u;
-    double a = fabs(x), f;
-    int e;
-    if (a != a) return (unsigned short)(s | 0x7FC0u);
-    if (a >= 0x1.ffp127) return (unsigned short)(s | 0x7F80u);
-    if (a < 0x1p-126) return (unsigned short)(s | (unsigned short)unp_rne_int(ldexp(a, 133)));
-    f = unp_rne_int(ldexp(frexp(a, &e), 8));
-    return (unsigned short)(s | (unsigned short)(((e + 126) << 7) + ((int)f - 128)));
-}
-static unsigned short unp_bf16_enc(float x) { return unp_d_to_bf16((double)x); }
-)";
-const char* kF16Enc = R"(static unsigned short unp_d_to_f16(double x) {
-    unsigned short s = signbit(x) ? 0x8000u : 0u;
-    double a = fabs(x), f;
-    int e;
-    if (a != a) return (unsigned short)(s | 0x7E00u);
-    if (a >= 65520.0) return (unsigned short)(s | 0x7C00u);
-    if (a < 0x1p-14) return (unsigned short)(s | (unsigned short)unp_rne_int(ldexp(a, 24)));
-    f = unp_rne_int(ldexp(frexp(a, &e), 11));
-    return (unsigned short)(s | (unsigned short)(((e + 14) << 10) + ((int)f - 1024)));
-}
-static unsigned short unp_f16_enc(float x) { return unp_d_to_f16((double)x); }
+static float leg_f16_value(unsigned short h) { return (float)leg_decode(h, 5, 10); }
 )";
 
 std::string ident(const std::string& x) {
@@ -1283,15 +1290,9 @@ std::string lower(const V& k, std::string& entry) {
   entry = "unpopped_cpu_kernel_" + ident(K.name);
   const std::string body = em.signature(entry) + " {\n" + em.out + "    return 0;\n}\n";
   std::string src = "/* Generated by the cpu-c restatement (serial C99): do not edit. kernel: " + K.name + " */\n";
-  src += "#include <math.h>\n\n";
+  src += "#include <math.h>\n#include <string.h>\n\n";
   src += kTypedHelpers;
-  const bool bf_enc = body.find("unp_bf16_enc") != std::string::npos || body.find("unp_d_to_bf16") != std::string::npos;
-  const bool f_enc = body.find("unp_f16_enc") != std::string::npos || body.find("unp_d_to_f16") != std::string::npos;
-  if (bf_enc || f_enc) src += kRoundHelper;
-  if (body.find("unpopped_bf16_load") != std::string::npos) src += kBf16Load;
-  if (body.find("unpopped_f16_load") != std::string::npos) src += kF16Load;
-  if (bf_enc) src += kBf16Enc;
-  if (f_enc) src += kF16Enc;
+  if (body.find("leg_to_") != std::string::npos || body.find("_value(") != std::string::npos) src += kCodec;
   return src + "\n" + body;
 }
 
