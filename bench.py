@@ -414,11 +414,13 @@ extern "C" __global__ void __launch_bounds__(256) unp_ceiling_copy(const u32x4* 
 CEILING_SIZES = [
     ("read", 1 << 30, "1 GiB"),
     ("read", 128 << 20, "cfg2: 8192 x 4096 f32"),
+    ("read", 64 << 20, "the full sum: 2^24 f32"),
     ("write", 1 << 30, "1 GiB"),
     ("write", 448 << 20, "cfg5's output: 8192 x 28672 bf16"),
     ("copy", 1 << 30, "1 GiB, cfg3a: 2^28 i32"),
     ("copy", 512 << 20, "cfg4: 65536 rows of 8 KiB"),
     ("copy", 256 << 20, "cfg3b: 2^26 f32"),
+    ("copy", 128 << 20, "RowReduce: 8192 x 4096 f32 in and out"),
 ]
 
 

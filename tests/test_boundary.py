@@ -405,7 +405,7 @@ def test_dequant_gemm_entries_follow_the_group():
         # The decode entry keeps a whole number of groups in flight.
         assert g.interface["decode_steps"] == dec and (dec == 0 or dec % (group // 128) == 0)
         syms = [e["symbol"].rsplit("_", 1)[1] for e in g.interface["entries"]]
-        decs = (["dec1", "dec2", "dec4"] if x_kind == "I8" else ["dec1"]) if dec else []
+        decs = (["dec1", "dec2", "dec4", "dec1x"] if x_kind == "I8" else ["dec1"]) if dec else []
         want = (decs + (["stream"] if stream else []) + (["mfma"] if chunk else []) + ["any"]
                 + (["prep"] if stream else []) + (["prep16"] if dec else []))
         assert syms == want

@@ -797,19 +797,23 @@ GEMM_MFMA_CASES = [
     (130, 4096, 150, 64, np.int8),    # 64-value chunks: four waves of one tile over 128 x 32
     (257, 8192, 200, 128, np.int32),  # I32 streaming: 1 x 2 tiles per wave, split-K, ragged last tile
     (96, 2048, 128, 256, np.int8),
+    # I8 with C <= 16: eight waves of 256 rows per block with x' staged in LDS (32 steps at most).
+    (300, 24576, 9, 384, np.int8),    # three steps per group, ten groups per split at most
+    (513, 16384, 16, 512, np.int8),   # four steps per group, ragged 256-row tiles
+    (40, 256, 1, 256, np.int8),       # one column, one split of one group
 ]
 
 
 def _expected_gemm_entry(xdt, C, group):
     """The entry the executor takes for aligned operands: decode for groups of 1..4 whole
-    128-deep steps (1..2 for I32) and C <= 64 (I8: the entry with 1, 2 or 4 column tiles that
-    first covers C) or C <= 128 (I32: the one-tile entry), then streaming for 64-multiples, then
-    the MFMA entry."""
+    128-deep steps (1..2 for I32) and C <= 64 (I8: the one-tile entry that stages x' in LDS for
+    C <= 16, else the entry with 2 or 4 column tiles that first covers C) or C <= 128 (I32: the
+    one-tile entry), then streaming for 64-multiples, then the MFMA entry."""
     spg = group // 128 if group % 128 == 0 else 0
     if C <= (64 if xdt == np.int8 else 128) and 1 <= spg <= (4 if xdt == np.int8 else 2):
         if xdt != np.int8:
             return "_dec1"
-        return "_dec1" if C <= 16 else "_dec2" if C <= 32 else "_dec4"
+        return "_dec1x" if C <= 16 else "_dec2" if C <= 32 else "_dec4"
     return "_stream" if group % 64 == 0 else "_mfma"
 
 
@@ -1225,13 +1229,13 @@ def test_config4_gather_full(hip_device, dist):
     assert np.array_equal(got, table[ids])
 
 
-@pytest.mark.parametrize("C,xdt,entry", [(16, np.int8, "_dec1"), (64, np.int8, "_dec4"), (1024, np.int8, "_stream"),
+@pytest.mark.parametrize("C,xdt,entry", [(16, np.int8, "_dec1x"), (64, np.int8, "_dec4"), (1024, np.int8, "_stream"),
                                           (16, np.int32, "_dec1")])
 def test_dequant_gemm_full_size(hip_device, C, xdt, entry):
     """The dequantizing GEMM at the bench's LLM shape (U4 w 8192 x 28672, full-range I32 zero
     points and scales per 128 columns), with sampled rows against the oracle: rows are
     independent, so the oracle runs on the sampled rows alone.  The samples include both edges
-    of every 128-row tile and a spread inside."""
+    of every 128-row tile (256 rows for the entry that stages x' in LDS) and a spread inside."""
     R, K, G = 8192, 28672, 128
     ng = K // G
     H.say(f"[case] dequant GEMM full size U4 {R}x{K} g{G} times {np.dtype(xdt).name} {K}x{C}")

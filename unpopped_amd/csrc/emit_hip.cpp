@@ -830,6 +830,25 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
         << dmaxg << ">(w, zero, scale, xp, xsum, out, R, K, C, Cp, S);\n}\n";
     L.entries.push_back(e);
   }
+  if (dec && xb == 1) {
+    // One column tile with eight waves per block and the block's x' staged in LDS once (at most
+    // 32 steps: about 130 KiB of LDS with the scales, one block per CU), in place of every wave
+    // loading x' from L2 each step.
+    Entry e;
+    e.fast = true;
+    e.symbol = L.name + "_dec1x";
+    e.vec = 16 * dmt * 8;
+    e.cols = 16;
+    e.k = 32 / spg;
+    e.threads = 512;
+    e.blocks_per_cu = 1;
+    src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol
+        << "(const unsigned char* w, const int* zero, const int* scale, const unsigned char* xp, const unsigned* xsum, "
+           "int* out, long long R, long long K, long long C, long long Cp, long long S) {\n  unp::dqg_dec<"
+        << (qs ? "true" : "false") << ", 1, " << f.group << ", " << dmt << ", 1, " << dd << ", " << 32 / spg
+        << ", 8, true>(w, zero, scale, xp, xsum, out, R, K, C, Cp, S);\n}\n";
+    L.entries.push_back(e);
+  }
   if (skc) {
     Entry e;
     e.fast = true;
@@ -895,7 +914,8 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
        "\"name\":\"n2\",\"kind\":\"scalar\",\"dtype\":\"I32\"}]"
     << ",\"launch\":{\"block\":[256,1,1],\"grid_policy\":\"dec: a prep launch over (group, 16 columns), then "
        "(row tiles rounded up to 8) x splits x column tiles blocks of 128 (I8) or 256 (I32) rows x 16, 32 or 64 "
-       "columns, about two blocks per CU, a split's groups at most 32 "
+       "columns, about two blocks per CU, a split's groups at most 32 (I8 with C <= 16: blocks of 512 threads over "
+       "256 rows x 16 with the split's x' in LDS, one per CU, a split's steps at most 32) "
        "and the splits adding into out with atomics; stream: a prep launch over (group, 64 columns), then "
        "(row tiles x splits, rounded up to 8) x column tiles blocks of 128 x 128 (I8, 128-value chunks), 128 x 64 (I32) or 128 x 32 outputs, the splits adding into out "
        "with atomics; mfma: one block per 64 x 64 output tile; any: threads stride over the outputs\"},\"entries\":[";

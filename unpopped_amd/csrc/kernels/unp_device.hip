@@ -2831,6 +2831,12 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
 // scales and products scale * zero and its columns' group sums.  All splits of a row tile run
 // on one XCD, so their shared scale and zero-point cache lines come from that XCD's L2 once.
 // Splits add into out with u32 atomics, exact and order-free in Z / 2^32.
+//
+// WV waves per block (BM = 16 MT WV rows).  XL stages the x' of all of the block's steps in LDS
+// once, before the main loop (the host keeps a split within MAXG groups, MAXG * SPG steps), and
+// the waves read their x' operands from there: with one column tile the per-step x' is as many
+// bytes as a wave's w, and every wave loading it from L2 each step cost about an eighth of the
+// launch at C = 16.
 // ---------------------------------------------------------------------------------------
 template <class XT, int XB>
 UNP_DEV void dqg_prep16(const XT* __restrict__ x, u8* __restrict__ xp, u32* __restrict__ xsum, i64 K, i64 C,
@@ -2879,15 +2885,20 @@ UNP_DEV void dqg_prep16(const XT* __restrict__ x, u8* __restrict__ xp, u32* __re
 
 typedef unsigned int u32x4b __attribute__((ext_vector_type(4)));
 
-template <bool QS, int XB, int G, int MT, int NC, int D, int MAXG>
+template <bool QS, int XB, int G, int MT, int NC, int D, int MAXG, int WV = 4, bool XL = false>
 UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, const i32* __restrict__ scale,
                      const u8* __restrict__ xp, const u32* __restrict__ xsum, i32* __restrict__ out, i64 R, i64 K,
                      i64 C, i64 Cp, i64 S) {
-  constexpr int BM = 64 * MT, BN = 16 * NC, SPG = G / 128;
+  constexpr int THREADS = 64 * WV, BM = 16 * MT * WV, BN = 16 * NC, SPG = G / 128;
   static_assert(G % 128 == 0 && D % SPG == 0, "whole steps per group, whole groups per unrolled pass");
   __shared__ __attribute__((aligned(16))) u32 ss[MAXG][BM + 4];
   __shared__ __attribute__((aligned(16))) u32 zs[MAXG][BM + 4];
   __shared__ u32 xs[MAXG][BN];
+  // XL: the x' of every step of the block's groups, staged once: step i's half-step segment e
+  // (0..7) of plane b and column tile t is the 256-byte slab ((i NC + t) XB + b) 8 + e, 16 bytes
+  // per column.
+  constexpr int XSEG = NC * XB * 8;
+  __shared__ __attribute__((aligned(16))) u8 xl[XL ? MAXG * SPG * XSEG * 256 : 16];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kq = lane >> 4, r16 = lane & 15;
   const i64 ng = K / G;
@@ -2920,28 +2931,59 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
         xofs[t][b][h] = (u32)((((kb / 64 + e / 4) * XB * 4 + b * 4 + e % 4) * Cp + tile_c + 16 * t + r16) * 16);
       }
   u32x4b wv[D][MT];
-  i32x4 xv[D][NC][XB][2];
+  i32x4 xv[XL ? 1 : D][NC][XB][2];
   auto load = [&](int sl, i64 i) {
     const int sw = (int)(64 * i), sx = (int)(128 * XB * Cp * i);
 #pragma unroll
     for (int m = 0; m < MT; ++m) wv[sl][m] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)wofs[m], sw, 0);
+    if constexpr (!XL) {
 #pragma unroll
-    for (int t = 0; t < NC; ++t)
+      for (int t = 0; t < NC; ++t)
 #pragma unroll
-      for (int b = 0; b < XB; ++b)
+        for (int b = 0; b < XB; ++b)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          xv[sl][t][b][h] =
-              __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xofs[t][b][h], sx, 0));
+          for (int h = 0; h < 2; ++h)
+            xv[sl][t][b][h] =
+                __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xofs[t][b][h], sx, 0));
+    }
+  };
+  // Step i's x' operand of column tile t, plane b, half step h.
+  auto xop = [&](int sl, i64 i, int t, int b, int h) -> i32x4 {
+    if constexpr (XL)
+      return *reinterpret_cast<const i32x4*>(xl + ((((i * NC + t) * XB + b) * 8 + 2 * kq + h) * 16 + r16) * 16);
+    else
+      return xv[sl][t][b][h];
   };
 #pragma unroll
   for (int p = 0; p < D; ++p) load(p, p < nsteps ? p : nsteps - 1);
+  if constexpr (XL) {
+    // 16-byte units (step, t, b, e, column) in LDS order, column fastest; the host keeps a
+    // split's steps within MAXG * SPG.
+    constexpr int PU = (MAXG * SPG * XSEG * 16 + THREADS - 1) / THREADS;
+    const int nu = (int)nsteps * XSEG * 16;
+    u32x4b tmp[PU];
+#pragma unroll
+    for (int j = 0; j < PU; ++j) {
+      const int idx = tid + THREADS * j;
+      if (idx < nu) {
+        const int c = idx % 16, e = (idx / 16) % 8, b = (idx / 128) % XB, t = (idx / (128 * XB)) % NC,
+                  i = idx / (128 * XB * NC);
+        const int off = (int)((((kb / 64 + 2 * i + e / 4) * XB + b) * 4 + e % 4) * Cp + tile_c + 16 * t + c) * 16;
+        tmp[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < PU; ++j) {
+      const int idx = tid + THREADS * j;
+      if (idx < nu) *reinterpret_cast<u32x4b*>(xl + 16 * idx) = tmp[j];
+    }
+  }
   // The preload: every load issued at once, while the first steps are in flight.
-  constexpr int PL = (BM * MAXG + 255) / 256, PX = (BN * MAXG + 255) / 256;
+  constexpr int PL = (BM * MAXG + THREADS - 1) / THREADS, PX = (BN * MAXG + THREADS - 1) / THREADS;
   u32 sv[PL], zv[PL], cv[PX];
 #pragma unroll
   for (int j = 0; j < PL; ++j) {
-    const int idx = tid + 256 * j, r = idx / MAXG, gg = idx % MAXG;
+    const int idx = tid + THREADS * j, r = idx / MAXG, gg = idx % MAXG;
     const i64 row = tile_r + r < R ? tile_r + r : R - 1;
     const bool ok = r < BM && gg < ngr;
     sv[j] = ok ? (u32)scale[row * ng + g0 + gg] : 0u;
@@ -2949,12 +2991,12 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
   }
 #pragma unroll
   for (int j = 0; j < PX; ++j) {
-    const int idx = tid + 256 * j, gg = idx / BN, c = idx % BN;
+    const int idx = tid + THREADS * j, gg = idx / BN, c = idx % BN;
     cv[j] = gg < ngr ? xsum[(g0 + gg) * Cp + tile_c + c] : 0u;
   }
 #pragma unroll
   for (int j = 0; j < PL; ++j) {
-    const int idx = tid + 256 * j, r = idx / MAXG, gg = idx % MAXG;
+    const int idx = tid + THREADS * j, r = idx / MAXG, gg = idx % MAXG;
     if (r < BM) {
       ss[gg][r] = sv[j];
       zs[gg][r] = sv[j] * zv[j];
@@ -2962,7 +3004,7 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
   }
 #pragma unroll
   for (int j = 0; j < PX; ++j) {
-    const int idx = tid + 256 * j, gg = idx / BN, c = idx % BN;
+    const int idx = tid + THREADS * j, gg = idx / BN, c = idx % BN;
     if (gg < MAXG) xs[gg][c] = cv[j];
   }
   __syncthreads();
@@ -2989,8 +3031,8 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
 #pragma unroll
             for (int b = 0; b < XB; ++b) {
               P[m][t][b] =
-                  __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, xv[I][t][b][0], I % SPG == 0 ? Z : P[m][t][b], 0, 0, 0);
-              P[m][t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, xv[I][t][b][1], P[m][t][b], 0, 0, 0);
+                  __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, xop(I, i, t, b, 0), I % SPG == 0 ? Z : P[m][t][b], 0, 0, 0);
+              P[m][t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, xop(I, i, t, b, 1), P[m][t][b], 0, 0, 0);
             }
         }
         if ((I + 1) % SPG == 0) {

@@ -1294,7 +1294,8 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
   const long long group = x->l.form.group;
   const bool x32 = x->l.form.dtype == UNP_I32;
   const long long xbytes = x32 ? 4 : 1;
-  size_t stream = SIZE_MAX, prep = SIZE_MAX, dec = SIZE_MAX, prep16 = SIZE_MAX, mfma = SIZE_MAX, any = SIZE_MAX;
+  size_t stream = SIZE_MAX, prep = SIZE_MAX, dec = SIZE_MAX, decx = SIZE_MAX, prep16 = SIZE_MAX, mfma = SIZE_MAX,
+         any = SIZE_MAX;
   for (size_t i = 0; i < x->l.entries.size(); ++i) {
     const std::string& sym = x->l.entries[i].symbol;
     if (ends_with(sym, "_stream")) stream = i;
@@ -1302,10 +1303,16 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
     if (ends_with(sym, "_prep16")) prep16 = i;
     if (ends_with(sym, "_mfma")) mfma = i;
     if (ends_with(sym, "_any")) any = i;
+    if (ends_with(sym, "_dec1x")) {
+      decx = i;
+      continue;
+    }
     // The decode entry whose column tiles first cover C, else the widest (entries ascend).
     const int cols = x->l.entries[i].cols;
     if (cols > 0 && (dec == SIZE_MAX || x->l.entries[dec].cols < C)) dec = i;
   }
+  // One column tile: the entry that stages x' in LDS.
+  if (decx != SIZE_MAX && C <= x->l.entries[decx].cols) dec = decx;
   // The two-launch schedules need whole groups, a 16-byte aligned w and aligned operands.
   const bool whole = K > 0 && K % group == 0 && (w & 15) == 0 && (zp & 3) == 0 && (sc & 3) == 0 &&
                      (out & 3) == 0 && (xa & (x32 ? 3 : 0)) == 0;
@@ -1316,8 +1323,10 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
     const long long ng = K / group, Cp = (C + bn - 1) / bn * bn;  // whole column tiles of the entry
     if (R * (K / 2) < 0x7FFFFFFFLL && K * Cp * xbytes < 0x7FFFFFFFLL) {
       const long long tiles_r = (R + bm - 1) / bm, tiles_c = Cp / bn;
-      // Splits of K: about two blocks per CU, at most maxg groups per split, at least one.
-      long long S = (2LL * x->cu_count + tiles_r * tiles_c - 1) / (tiles_r * tiles_c);
+      // Splits of K: about the entry's blocks per CU (two by default), at most maxg groups per
+      // split, at least one.
+      const long long bpc = x->l.entries[dec].blocks_per_cu ? x->l.entries[dec].blocks_per_cu : 2;
+      long long S = (bpc * x->cu_count + tiles_r * tiles_c - 1) / (tiles_r * tiles_c);
       S = std::max(S, (ng + maxg - 1) / maxg);
       S = std::max(1LL, std::min(S, ng));
       const long long blocks = (tiles_r + 7) / 8 * 8 * S * tiles_c;
