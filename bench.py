@@ -123,8 +123,9 @@ def build_extras(u, synth):
     """The next rows of the hot path on the cfg2 input (an f32 8192 x 4096 matrix): the reduction
     over an outer axis (column sums; ReductionShape::new, kernel_lift.rs:854-870), and
     Access::RowReduce (kernel_lift/row_reduce_launched.rs:47-86) softmax and RMS norm, the row
-    read once and the full-width epilogue written once.  Timed apart from the suite: not part of
-    `value`."""
+    read once and the full-width epilogue written once.  Timed apart from the suite, each launch
+    after a MALL flush (the lines that write 128-256 MB would otherwise leave their dirty lines to
+    be written back during the next line's reads): not part of `value`."""
     from unpopped_amd import expr as X
     from unpopped_amd import forms as H
 
@@ -199,15 +200,19 @@ def build_extras(u, synth):
     return extras
 
 
-def time_cases(u, cases, steps):
+def time_cases(u, cases, steps, flush=None):
     """Average kernel time of each case's launch over `steps` rounds (one launch per case per round,
     on the launch stream).  Each launch carries a pair of HIP events that take the first and the last
     kernel's own dispatch timestamps (unp_hip_exec_set_timing, hipExtModuleLaunchKernel), so the time
-    is the kernels' and not the queueing gap around them, as in a rocprofv3 kernel trace."""
+    is the kernels' and not the queueing gap around them, as in a rocprofv3 kernel trace.  With
+    `flush` (a MallFlush) every launch follows a MALL-evicting read: it starts from clean caches,
+    its inputs in HBM and no earlier kernel's dirty lines left to write back while it runs."""
     events = [[(u.Event(), u.Event()) for _ in cases] for _ in range(steps)]
     u.synchronize()
     for s in range(steps):
         for i, c in enumerate(cases):
+            if flush is not None:
+                flush.run()
             c.exec.set_timing(*events[s][i])
             c.launch()
     u.synchronize()
@@ -444,6 +449,7 @@ def ceilings(u, cus: int, reps: int = 10) -> None:
         _lib.check(L.unp_hip_get_function(m, name.encode(), C.byref(f), C.byref(err)), err)
         fns[name] = f
     big = max(size for _, size, _ in CEILING_SIZES)
+    flush = MallFlush(u, cus)
     a, b, sink = u.DeviceBuffer(big), u.DeviceBuffer(big), u.DeviceBuffer(64)
     a.fill(1)
     for label, size, what in CEILING_SIZES:
@@ -471,9 +477,25 @@ def ceilings(u, cus: int, reps: int = 10) -> None:
             log(f"[bench] ceiling {label} {size} B: {cus * bpc} blocks, {ms * 1e3:.1f} us, {gbps:.0f} GB/s")
             if best is None or gbps > best[0]:
                 best = (gbps, cus * bpc, ms)
+        # The same launch with the MALL evicted before each one: a buffer under 256 MB read back to
+        # back is partly served from the MALL, which a kernel that follows other work does not see.
+        g = (C.c_uint32 * 3)(best[1], 1, 1)
+        blk = (C.c_uint32 * 3)(256, 1, 1)
+        ts = []
+        for i in range(reps):
+            flush.run()
+            e0, e1 = u.Event(), u.Event()
+            e0.record()
+            _lib.check(L.unp_hip_launch(fns[name], g, blk, 0, None, args, C.sizeof(args), C.byref(err)), err)
+            e1.record()
+            e1.synchronize()
+            ts.append(e0.elapsed_ms(e1))
+        cold = float(np.median(ts))
+        log(f"[bench] ceiling {label} {size} B cold: {cold * 1e3:.1f} us")
         print(json.dumps({"ceiling": label, "size": size, "what": what, "bytes": moved, "blocks": best[1],
                           "us": round(best[2] * 1e3, 1), "GBps": round(best[0], 1),
-                          "frac_of_peak": round(best[0] / PEAK_GBPS, 4)}), flush=True)
+                          "frac_of_peak": round(best[0] / PEAK_GBPS, 4), "cold_us": round(cold * 1e3, 1),
+                          "cold_GBps": round(moved / (cold * 1e-3) / 1e9, 1)}), flush=True)
 
 
 FLUSH_SRC = r"""
@@ -743,8 +765,8 @@ def main() -> int:
             c.launch, c.exec = c.setup()
             for _ in range(args.warmup):
                 c.launch()
-        log(f"[bench] timing {args.steps} steps of the extra lines")
-        extra = time_cases(u, xs, args.steps)
+        log(f"[bench] timing {args.steps} steps of the extra lines, each launch after a MALL flush")
+        extra = time_cases(u, xs, args.steps, flush=MallFlush(u, cus))
         attach_traffic(extra, xs)
 
     cpu = None
