@@ -1230,7 +1230,7 @@ def test_config4_gather_full(hip_device, dist):
 
 
 @pytest.mark.parametrize("C,xdt,entry", [(16, np.int8, "_dec1x"), (64, np.int8, "_dec4"), (1024, np.int8, "_stream"),
-                                          (16, np.int32, "_dec1")])
+                                          (16, np.int32, "_dec1"), (32, np.int32, "_dec1")])
 def test_dequant_gemm_full_size(hip_device, C, xdt, entry):
     """The dequantizing GEMM at the bench's LLM shape (U4 w 8192 x 28672, full-range I32 zero
     points and scales per 128 columns), with sampled rows against the oracle: rows are

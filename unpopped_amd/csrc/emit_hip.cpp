@@ -801,12 +801,12 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
   const bool big = xb == 1 && skc == 128, two = big || xb == 4;
   const int swr = big ? 2 : 4, swc = big ? 2 : 1, stm = big ? 2 : 1, stn = two ? 2 : 1, sns = two ? 3 : 4;
   // The decode schedule (up to 64 columns for I8, 128 for I32): groups of 1..4 whole 128-value steps (1..2 for I32
-  // activations, whose four digit planes take four times the x registers).  I8: two m-tiles per
-  // wave, 1, 2 or 4 column tiles of 16 sharing each unpacked w operand, two steps in flight (or
-  // one group); I32: four m-tiles, one column tile, one group in flight.
+  // activations, whose four digit planes take four times the x' bytes).  Two m-tiles per wave; I8
+  // with 1, 2 or 4 column tiles of 16 sharing each unpacked w operand, two steps in flight (or one
+  // group); I32 with one column tile and two steps in flight.
   const int spg = f.group % 128 == 0 ? f.group / 128 : 0;
   const bool dec = spg >= 1 && spg <= (xb == 1 ? 4 : 2);
-  const int dmt = xb == 1 ? 2 : 4, dd = xb == 1 ? (spg <= 1 ? 2 : spg) : spg, dmaxg = 32;
+  const int dmt = 2, dd = xb == 1 ? (spg <= 1 ? 2 : spg) : spg, dmaxg = 32;
   std::ostringstream name;
   name << "unp_dequant_gemm_" << lower_name(f.q_kind) << "_g" << f.group << "_" << lower_name(f.dtype) << "_i32";
   L.name = name.str();
@@ -816,38 +816,36 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
   src << header(L.name, f);
   const std::string sig = std::string("(const unsigned char* w, const int* zero, const int* scale, const ") + xt +
                           "* x, int* out, long long R, long long K, long long C)";
-  for (int nc = 1; dec && nc <= (xb == 1 ? 4 : 1); nc *= 2) {
+  // Decode entries: eight waves of 32 rows per block (256 rows), one block per CU, the block's x'
+  // staged in LDS.  I8 with one column tile holds its split's every step (at most 32 steps);
+  // the others stream x' through two LDS buffers of P steps, 16 KiB each (P a multiple of the
+  // steps in flight), one phase ahead.
+  auto dec_entry = [&](const char* suffix, int nc, int xm, int maxg) {
+    const int xs = nc * xb * 2048, dd2 = xb == 1 ? dd : 2;
+    const int P = xm == 1 ? 0 : std::max(dd2, 16384 / xs / dd2 * dd2);
     Entry e;
     e.fast = true;
-    e.symbol = L.name + "_dec" + std::to_string(nc);
-    e.vec = 64 * dmt;  // rows per block
-    e.cols = 16 * nc;  // columns per block
-    e.k = dmaxg;       // groups per split at most
-    src << "extern \"C\" __global__ void __launch_bounds__(256) " << e.symbol
-        << "(const unsigned char* w, const int* zero, const int* scale, const unsigned char* xp, const unsigned* xsum, "
-           "int* out, long long R, long long K, long long C, long long Cp, long long S) {\n  unp::dqg_dec<"
-        << (qs ? "true" : "false") << ", " << xb << ", " << f.group << ", " << dmt << ", " << nc << ", " << dd << ", "
-        << dmaxg << ">(w, zero, scale, xp, xsum, out, R, K, C, Cp, S);\n}\n";
-    L.entries.push_back(e);
-  }
-  if (dec && xb == 1) {
-    // One column tile with eight waves per block and the block's x' staged in LDS once (at most
-    // 32 steps: about 130 KiB of LDS with the scales, one block per CU), in place of every wave
-    // loading x' from L2 each step.
-    Entry e;
-    e.fast = true;
-    e.symbol = L.name + "_dec1x";
-    e.vec = 16 * dmt * 8;
-    e.cols = 16;
-    e.k = 32 / spg;
+    e.symbol = L.name + suffix;
+    e.vec = 16 * dmt * 8;  // rows per block
+    e.cols = 16 * nc;      // columns per block
+    e.k = maxg;            // groups per split at most
     e.threads = 512;
     e.blocks_per_cu = 1;
     src << "extern \"C\" __global__ void __launch_bounds__(512) " << e.symbol
         << "(const unsigned char* w, const int* zero, const int* scale, const unsigned char* xp, const unsigned* xsum, "
            "int* out, long long R, long long K, long long C, long long Cp, long long S) {\n  unp::dqg_dec<"
-        << (qs ? "true" : "false") << ", 1, " << f.group << ", " << dmt << ", 1, " << dd << ", " << 32 / spg
-        << ", 8, true>(w, zero, scale, xp, xsum, out, R, K, C, Cp, S);\n}\n";
+        << (qs ? "true" : "false") << ", " << xb << ", " << f.group << ", " << dmt << ", " << nc << ", " << dd2 << ", "
+        << maxg << ", 8, " << xm << ", " << P << ">(w, zero, scale, xp, xsum, out, R, K, C, Cp, S);\n}\n";
     L.entries.push_back(e);
+  };
+  if (dec && xb == 1) {
+    dec_entry("_dec1x", 1, 1, 32 / spg);
+    dec_entry("_dec2", 2, 2, dmaxg);
+    dec_entry("_dec4", 4, 2, dmaxg);
+  } else if (dec) {
+    // 56 groups per split (the scales then fill 114 KiB of LDS): at 8192 rows, 4 splits make whole
+    // rounds of 256 blocks for 32, 64 and 128 columns, where 32 groups need 7.
+    dec_entry("_dec1", 1, 2, 56);
   }
   if (skc) {
     Entry e;
@@ -904,7 +902,7 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
   std::ostringstream j;
   j << "{\"backend\":\"hip\",\"target\":\"rocm:gfx950\",\"form\":\"dequant_gemm\",\"w\":\"" << kind_name(f.q_kind)
     << "\",\"zero\":\"I32\",\"scale\":\"I32\",\"x\":\"" << kind_name(f.dtype) << "\",\"out\":\"I32\",\"group\":"
-    << f.group << ",\"chunk\":" << kc << ",\"stream_chunk\":" << skc << ",\"decode_steps\":" << (dec ? dd : 0)
+    << f.group << ",\"chunk\":" << kc << ",\"stream_chunk\":" << skc << ",\"decode_steps\":" << (dec ? (xb == 1 ? dd : 2) : 0)
     << ",\"params\":[{\"name\":\"w\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\"" << kind_name(f.q_kind)
     << "\"},{\"name\":\"zero\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\"I32\"},{\"name\":\"scale\",\"kind\":"
        "\"buffer\",\"role\":\"Read\",\"dtype\":\"I32\"},{\"name\":\"x\",\"kind\":\"buffer\",\"role\":\"Read\",\"dtype\":\""

@@ -2885,20 +2885,22 @@ UNP_DEV void dqg_prep16(const XT* __restrict__ x, u8* __restrict__ xp, u32* __re
 
 typedef unsigned int u32x4b __attribute__((ext_vector_type(4)));
 
-template <bool QS, int XB, int G, int MT, int NC, int D, int MAXG, int WV = 4, bool XL = false>
+template <bool QS, int XB, int G, int MT, int NC, int D, int MAXG, int WV, int XM, int P>
 UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, const i32* __restrict__ scale,
                      const u8* __restrict__ xp, const u32* __restrict__ xsum, i32* __restrict__ out, i64 R, i64 K,
                      i64 C, i64 Cp, i64 S) {
   constexpr int THREADS = 64 * WV, BM = 16 * MT * WV, BN = 16 * NC, SPG = G / 128;
   static_assert(G % 128 == 0 && D % SPG == 0, "whole steps per group, whole groups per unrolled pass");
+  static_assert(XM == 1 || (XM == 2 && P % D == 0), "x' staged whole, or in phases of whole unrolled passes");
   __shared__ __attribute__((aligned(16))) u32 ss[MAXG][BM + 4];
   __shared__ __attribute__((aligned(16))) u32 zs[MAXG][BM + 4];
   __shared__ u32 xs[MAXG][BN];
-  // XL: the x' of every step of the block's groups, staged once: step i's half-step segment e
-  // (0..7) of plane b and column tile t is the 256-byte slab ((i NC + t) XB + b) 8 + e, 16 bytes
-  // per column.
-  constexpr int XSEG = NC * XB * 8;
-  __shared__ __attribute__((aligned(16))) u8 xl[XL ? MAXG * SPG * XSEG * 256 : 16];
+  // x' in LDS as 16-byte units (step, column tile t, plane b, half-step segment e (0..7), column),
+  // the column fastest: XM 1 holds every step of the block's groups; XM 2 two buffers of P steps,
+  // phase f (steps f P .. f P + P - 1) in buffer f & 1.
+  constexpr int XSEG = NC * XB * 8;                        // 256-byte slabs per step
+  constexpr int XSTEPS = XM == 1 ? MAXG * SPG : 2 * P;     // steps the LDS holds
+  __shared__ __attribute__((aligned(16))) u8 xl[XSTEPS * XSEG * 256];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kq = lane >> 4, r16 = lane & 15;
   const i64 ng = K / G;
@@ -2919,64 +2921,52 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
     const i64 row = tile_r + wave * 16 * MT + 16 * m + r16;
     wofs[m] = (u32)((row < R ? row : R - 1) * (K / 2) + kb / 2 + 16 * kq);
   }
-  // Half step h of lane (kq, c) covers k = 32 kq + 16 h + [0, 16) of the step: x' segment 2 kq + h.
-  u32 xofs[NC][XB][2];
-#pragma unroll
-  for (int t = 0; t < NC; ++t)
-#pragma unroll
-    for (int b = 0; b < XB; ++b)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int e = 2 * kq + h;
-        xofs[t][b][h] = (u32)((((kb / 64 + e / 4) * XB * 4 + b * 4 + e % 4) * Cp + tile_c + 16 * t + r16) * 16);
-      }
   u32x4b wv[D][MT];
-  i32x4 xv[XL ? 1 : D][NC][XB][2];
   auto load = [&](int sl, i64 i) {
-    const int sw = (int)(64 * i), sx = (int)(128 * XB * Cp * i);
+    const int sw = (int)(64 * i);
 #pragma unroll
     for (int m = 0; m < MT; ++m) wv[sl][m] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)wofs[m], sw, 0);
-    if constexpr (!XL) {
-#pragma unroll
-      for (int t = 0; t < NC; ++t)
-#pragma unroll
-        for (int b = 0; b < XB; ++b)
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            xv[sl][t][b][h] =
-                __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xofs[t][b][h], sx, 0));
-    }
   };
-  // Step i's x' operand of column tile t, plane b, half step h.
-  auto xop = [&](int sl, i64 i, int t, int b, int h) -> i32x4 {
-    if constexpr (XL)
-      return *reinterpret_cast<const i32x4*>(xl + ((((i * NC + t) * XB + b) * 8 + 2 * kq + h) * 16 + r16) * 16);
-    else
-      return xv[sl][t][b][h];
+  // The 16-byte x' units of `steps` steps from step s0 on (unit u: column u % 16, segment
+  // (u / 16) % 8, plane, column tile, then step), steps past the block's last clamped to it.
+  constexpr int UPS = XSEG * 16;  // units per step
+  auto xunit = [&](i64 s0, int u) -> u32x4b {
+    const int c = u % 16, e = (u / 16) % 8, b = (u / 128) % XB, t = (u / (128 * XB)) % NC;
+    const i64 s = s0 + u / UPS, i = s < nsteps ? s : nsteps - 1;
+    const int off = (int)((((kb / 64 + 2 * i + e / 4) * XB + b) * 4 + e % 4) * Cp + tile_c + 16 * t + c) * 16;
+    return __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+  };
+  // Step i's x' operand of column tile t, plane b, half step h (half step h of lane (kq, c) covers
+  // k = 32 kq + 16 h + [0, 16) of the step: segment 2 kq + h).
+  auto xop = [&](i64 i, int t, int b, int h) -> i32x4 {
+    const i64 st = XM == 1 ? i : (i / P & 1) * P + i % P;
+    return *reinterpret_cast<const i32x4*>(xl + ((((st * NC + t) * XB + b) * 8 + 2 * kq + h) * 16 + r16) * 16);
   };
 #pragma unroll
   for (int p = 0; p < D; ++p) load(p, p < nsteps ? p : nsteps - 1);
-  if constexpr (XL) {
-    // 16-byte units (step, t, b, e, column) in LDS order, column fastest; the host keeps a
-    // split's steps within MAXG * SPG.
-    constexpr int PU = (MAXG * SPG * XSEG * 16 + THREADS - 1) / THREADS;
-    const int nu = (int)nsteps * XSEG * 16;
-    u32x4b tmp[PU];
+  // XM 1: every step's x' now.  XM 2: phase 0 now, each later phase while the one before runs.
+  constexpr int PU = ((XM == 1 ? MAXG * SPG : P) * UPS + THREADS - 1) / THREADS;
+  u32x4b tmp[PU];
+  auto xfetch = [&](i64 s0, int nu) {
 #pragma unroll
     for (int j = 0; j < PU; ++j) {
-      const int idx = tid + THREADS * j;
-      if (idx < nu) {
-        const int c = idx % 16, e = (idx / 16) % 8, b = (idx / 128) % XB, t = (idx / (128 * XB)) % NC,
-                  i = idx / (128 * XB * NC);
-        const int off = (int)((((kb / 64 + 2 * i + e / 4) * XB + b) * 4 + e % 4) * Cp + tile_c + 16 * t + c) * 16;
-        tmp[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
-      }
+      const int u = tid + THREADS * j;
+      if (XM == 2 || u < nu) tmp[j] = xunit(s0, u < nu ? u : 0);
     }
+  };
+  auto xstore = [&](int buf, int nu) {
 #pragma unroll
     for (int j = 0; j < PU; ++j) {
-      const int idx = tid + THREADS * j;
-      if (idx < nu) *reinterpret_cast<u32x4b*>(xl + 16 * idx) = tmp[j];
+      const int u = tid + THREADS * j;
+      if (u < nu) *reinterpret_cast<u32x4b*>(xl + 16 * (buf * P * UPS + u)) = tmp[j];
     }
+  };
+  if constexpr (XM == 1) {
+    xfetch(0, (int)nsteps * UPS);
+    xstore(0, (int)nsteps * UPS);
+  } else {
+    xfetch(0, P * UPS);
+    xstore(0, P * UPS);
   }
   // The preload: every load issued at once, while the first steps are in flight.
   constexpr int PL = (BM * MAXG + THREADS - 1) / THREADS, PX = (BN * MAXG + THREADS - 1) / THREADS;
@@ -3008,7 +2998,7 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
     if (gg < MAXG) xs[gg][c] = cv[j];
   }
   __syncthreads();
-  i32x4 P[MT][NC][XB];
+  i32x4 Pa[MT][NC][XB];
   u32 total[MT][NC][4];
 #pragma unroll
   for (int m = 0; m < MT; ++m)
@@ -3017,47 +3007,67 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
 #pragma unroll
       for (int v = 0; v < 4; ++v) total[m][t][v] = 0;
   const i32x4 Z = {0, 0, 0, 0};
-  for (i64 i0 = 0; i0 < nsteps; i0 += D) {
+  // Step i (I its place in the unrolled pass, whose start is a whole number of groups): the MFMAs
+  // of w slot I % D, and at a group's end total += scale * P - (scale * zero) * xsum.
+  auto step = [&](int I, i64 i) {
+    const int sl = I % D;
 #pragma unroll
-    for (int I = 0; I < D; ++I) {
-      const i64 i = i0 + I;
-      if (i < nsteps) {
+    for (int m = 0; m < MT; ++m) {
+      const i32x4 a0 = unpack16<QS>((u64)wv[sl][m][0] | ((u64)wv[sl][m][1] << 32));
+      const i32x4 a1 = unpack16<QS>((u64)wv[sl][m][2] | ((u64)wv[sl][m][3] << 32));
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          const i32x4 a0 = unpack16<QS>((u64)wv[I][m][0] | ((u64)wv[I][m][1] << 32));
-          const i32x4 a1 = unpack16<QS>((u64)wv[I][m][2] | ((u64)wv[I][m][3] << 32));
+      for (int t = 0; t < NC; ++t)
 #pragma unroll
-          for (int t = 0; t < NC; ++t)
-#pragma unroll
-            for (int b = 0; b < XB; ++b) {
-              P[m][t][b] =
-                  __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, xop(I, i, t, b, 0), I % SPG == 0 ? Z : P[m][t][b], 0, 0, 0);
-              P[m][t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, xop(I, i, t, b, 1), P[m][t][b], 0, 0, 0);
-            }
+        for (int b = 0; b < XB; ++b) {
+          Pa[m][t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, xop(i, t, b, 0), I % SPG == 0 ? Z : Pa[m][t][b], 0, 0, 0);
+          Pa[m][t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, xop(i, t, b, 1), Pa[m][t][b], 0, 0, 0);
         }
-        if ((I + 1) % SPG == 0) {
-          // Lane (kq, c) holds rows 4 kq + v of each m-tile, column c.
-          const int gg = (int)(i / SPG);
+    }
+    if ((I + 1) % SPG == 0) {
+      // Lane (kq, c) holds rows 4 kq + v of each m-tile, column c.
+      const int gg = (int)(i / SPG);
 #pragma unroll
-          for (int m = 0; m < MT; ++m) {
-            const int lr = wave * 16 * MT + 16 * m + 4 * kq;
-            const vec<u32, 4> s4 = *reinterpret_cast<const vec<u32, 4>*>(&ss[gg][lr]);
-            const vec<u32, 4> z4 = *reinterpret_cast<const vec<u32, 4>*>(&zs[gg][lr]);
+      for (int m = 0; m < MT; ++m) {
+        const int lr = wave * 16 * MT + 16 * m + 4 * kq;
+        const vec<u32, 4> s4 = *reinterpret_cast<const vec<u32, 4>*>(&ss[gg][lr]);
+        const vec<u32, 4> z4 = *reinterpret_cast<const vec<u32, 4>*>(&zs[gg][lr]);
 #pragma unroll
-            for (int t = 0; t < NC; ++t) {
-              const u32 xc = xs[gg][16 * t + r16];
+        for (int t = 0; t < NC; ++t) {
+          const u32 xc = xs[gg][16 * t + r16];
 #pragma unroll
-              for (int v = 0; v < 4; ++v) {
-                u32 p = (u32)P[m][t][0][v];
+          for (int v = 0; v < 4; ++v) {
+            u32 p = (u32)Pa[m][t][0][v];
 #pragma unroll
-                for (int b = 1; b < XB; ++b) p += (u32)P[m][t][b][v] << (8 * b);
-                total[m][t][v] += s4.e[v] * p - z4.e[v] * xc;
-              }
-            }
+            for (int b = 1; b < XB; ++b) p += (u32)Pa[m][t][b][v] << (8 * b);
+            total[m][t][v] += s4.e[v] * p - z4.e[v] * xc;
           }
         }
       }
-      load(I, i + D < nsteps ? i + D : nsteps - 1);
+    }
+  };
+  if constexpr (XM == 1) {
+    for (i64 i0 = 0; i0 < nsteps; i0 += D) {
+#pragma unroll
+      for (int I = 0; I < D; ++I) {
+        const i64 i = i0 + I;
+        if (i < nsteps) step(I, i);
+        load(I, i + D < nsteps ? i + D : nsteps - 1);
+      }
+    }
+  } else {
+    // One phase per pass: the next phase's x' is loaded at the pass's start and written to the
+    // other buffer at its end (whose last readers passed the previous pass's barrier), then one
+    // barrier.  Every load is unconditional (clamped), so each pass issues the same loads.
+    for (i64 i0 = 0; i0 < nsteps; i0 += P) {
+      xfetch(i0 + P, P * UPS);
+#pragma unroll
+      for (int I = 0; I < P; ++I) {
+        const i64 i = i0 + I;
+        if (i < nsteps) step(I, i);
+        load(I % D, i + D < nsteps ? i + D : nsteps - 1);
+      }
+      xstore((int)((i0 / P + 1) & 1), P * UPS);
+      __syncthreads();
     }
   }
 #pragma unroll

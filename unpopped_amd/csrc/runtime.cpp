@@ -1294,8 +1294,7 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
   const long long group = x->l.form.group;
   const bool x32 = x->l.form.dtype == UNP_I32;
   const long long xbytes = x32 ? 4 : 1;
-  size_t stream = SIZE_MAX, prep = SIZE_MAX, dec = SIZE_MAX, decx = SIZE_MAX, prep16 = SIZE_MAX, mfma = SIZE_MAX,
-         any = SIZE_MAX;
+  size_t stream = SIZE_MAX, prep = SIZE_MAX, dec = SIZE_MAX, prep16 = SIZE_MAX, mfma = SIZE_MAX, any = SIZE_MAX;
   for (size_t i = 0; i < x->l.entries.size(); ++i) {
     const std::string& sym = x->l.entries[i].symbol;
     if (ends_with(sym, "_stream")) stream = i;
@@ -1303,16 +1302,10 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
     if (ends_with(sym, "_prep16")) prep16 = i;
     if (ends_with(sym, "_mfma")) mfma = i;
     if (ends_with(sym, "_any")) any = i;
-    if (ends_with(sym, "_dec1x")) {
-      decx = i;
-      continue;
-    }
     // The decode entry whose column tiles first cover C, else the widest (entries ascend).
     const int cols = x->l.entries[i].cols;
     if (cols > 0 && (dec == SIZE_MAX || x->l.entries[dec].cols < C)) dec = i;
   }
-  // One column tile: the entry that stages x' in LDS.
-  if (decx != SIZE_MAX && C <= x->l.entries[decx].cols) dec = decx;
   // The two-launch schedules need whole groups, a 16-byte aligned w and aligned operands.
   const bool whole = K > 0 && K % group == 0 && (w & 15) == 0 && (zp & 3) == 0 && (sc & 3) == 0 &&
                      (out & 3) == 0 && (xa & (x32 ? 3 : 0)) == 0;
