@@ -2808,9 +2808,9 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
 }
 
 // ---------------------------------------------------------------------------------------
-// The decode schedule for few columns (C up to 32) and groups of whole 128-value steps: the
-// weight stream dominates, so every wave streams its own rows straight into VGPRs and no block
-// barrier sits in the main loop.
+// The decode schedule for few columns (up to 64 for I8 activations, 128 for I32) and groups of
+// whole 128-value steps: the weight stream dominates, so every wave streams its own rows of w
+// straight into VGPRs, and the activations, which every wave of a block needs in full, come from LDS.
 //
 // dqg_prep16 repacks x once for 16-column tiles, with the layout dqg_prep writes for 64-value
 // chunks: x'[kc][b][kseg][c][16 bytes] = digit plane b of x[64 kc + 16 kseg + i][c], i < 16, for
@@ -2818,25 +2818,26 @@ UNP_DEV void dqg_stream(const u8* __restrict__ w, const i32* __restrict__ zero, 
 // x[k][c] (wrapping).  It also zeroes out for the split-K atomics.  One block per (group, 16
 // columns); thread (kseg slot, column).
 //
-// dqg_dec: a block owns BM = 64 MT rows (MT 16-row m-tiles per wave), 16 NC columns (NC column
-// tiles sharing each unpacked w operand) and a range of whole groups (a split of K).  Per
-// 128-deep step a lane loads 16 bytes of w for each m-tile (row 16 m + lane % 16, k-block
-// lane / 16) and 16 bytes of x' for each column tile, half step and digit plane, D steps ahead, through buffer loads (a per-lane 32-bit offset plus a uniform step
-// offset: no 64-bit address arithmetic in the loop).  The int4 pairs become two
-// v_mfma_i32_16x16x64_i8 per m-tile and plane; the first MFMA of a group starts from a zero
-// accumulator.  Every refill is unconditional (clamped to the last step), so each pass of the
-// unrolled loop issues the same loads and the compiler's load counting stays exact across the
+// dqg_dec: a block of WV waves owns BM = 16 MT WV rows (MT 16-row m-tiles per wave), 16 NC columns
+// (NC column tiles sharing each unpacked w operand) and a range of whole groups (a split of K, at
+// most MAXG groups: the host picks S).  Per 128-deep step a lane loads 16 bytes of w for each
+// m-tile (row 16 m + lane % 16, k-block lane / 16), D steps ahead, through buffer loads (a per-lane
+// 32-bit offset plus a uniform step offset: no 64-bit address arithmetic in the loop), and reads
+// its x' operands (16 bytes per column tile, half step and digit plane) from LDS.  The int4 pairs
+// become two v_mfma_i32_16x16x64_i8 per m-tile and plane; the first MFMA of a group starts from a
+// zero accumulator.  Every refill is unconditional (clamped to the last step), so each pass of
+// the unrolled loop issues the same loads and the compiler's load counting stays exact across the
 // back edge: a conditional refill makes it drain every load once per pass.  At a group's end
 // total += scale * P - (scale * zero) * xsum, from LDS, where the block preloaded its rows'
-// scales and products scale * zero and its columns' group sums.  All splits of a row tile run
-// on one XCD, so their shared scale and zero-point cache lines come from that XCD's L2 once.
-// Splits add into out with u32 atomics, exact and order-free in Z / 2^32.
+// scales and products scale * zero and its columns' group sums.  All splits of a row tile run on
+// one XCD, so their shared scale and zero-point cache lines come from that XCD's L2 once.  Splits
+// add into out with u32 atomics, exact and order-free in Z / 2^32.
 //
-// WV waves per block (BM = 16 MT WV rows).  XL stages the x' of all of the block's steps in LDS
-// once, before the main loop (the host keeps a split within MAXG groups, MAXG * SPG steps), and
-// the waves read their x' operands from there: with one column tile the per-step x' is as many
-// bytes as a wave's w, and every wave loading it from L2 each step cost about an eighth of the
-// launch at C = 16.
+// x' in LDS (XM): 1 stages every step of the split before the main loop (one column tile of I8,
+// 2 KiB a step); 2 streams it through two buffers of P steps, each pass of the main loop loading
+// the next phase into VGPRs at its start and writing it to the other buffer at its end, then one
+// barrier.  With x' loaded from L2 by every wave each step, as many bytes as its w at one column
+// tile and two to four times as many at more columns or I32, the launches took 11-22% longer.
 // ---------------------------------------------------------------------------------------
 template <class XT, int XB>
 UNP_DEV void dqg_prep16(const XT* __restrict__ x, u8* __restrict__ xp, u32* __restrict__ xsum, i64 K, i64 C,
