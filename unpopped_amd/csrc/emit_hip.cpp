@@ -851,6 +851,7 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
     Entry e;
     e.fast = true;
     e.symbol = L.name + "_stream";
+    e.blocks_per_cu = 2;
     e.vec = 32 * swr * stm;  // rows per block
     e.k = 32 * swc * stn;    // columns per block
     src << "extern \"C\" __global__ void __launch_bounds__(256" << (two ? ", 2" : "") << ") " << e.symbol
@@ -910,13 +911,14 @@ static int32_t lower_dequant_gemm(const unp_form& f, Lowered& L, std::string& wh
     << "\"},{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\",\"dtype\":\"I32\"}"
     << ",{\"name\":\"n0\",\"kind\":\"scalar\",\"dtype\":\"I32\"},{\"name\":\"n1\",\"kind\":\"scalar\",\"dtype\":\"I32\"},{"
        "\"name\":\"n2\",\"kind\":\"scalar\",\"dtype\":\"I32\"}]"
-    << ",\"launch\":{\"block\":[256,1,1],\"grid_policy\":\"dec: a prep launch over (group, 16 columns), then "
-       "(row tiles rounded up to 8) x splits x column tiles blocks of 128 (I8) or 256 (I32) rows x 16, 32 or 64 "
-       "columns, about two blocks per CU, a split's groups at most 32 (I8 with C <= 16: blocks of 512 threads over "
-       "256 rows x 16 with the split's x' in LDS, one per CU, a split's steps at most 32) "
-       "and the splits adding into out with atomics; stream: a prep launch over (group, 64 columns), then "
-       "(row tiles x splits, rounded up to 8) x column tiles blocks of 128 x 128 (I8, 128-value chunks), 128 x 64 (I32) or 128 x 32 outputs, the splits adding into out "
-       "with atomics; mfma: one block per 64 x 64 output tile; any: threads stride over the outputs\"},\"entries\":[";
+    << ",\"launch\":{\"block\":[256,1,1],\"grid_policy\":\"device-class grids whose blocks stride over items. dec: "
+       "a prep launch (cu_count*8 blocks) over (group, 16 columns), then cu_count blocks of 512 threads over "
+       "(row tiles rounded up to 8) x splits x column tiles items of 256 rows x 16, 32 or 64 columns (I8) or x 16 "
+       "(I32), the split's x' in LDS (whole for one I8 column tile, else streamed through two buffers), a split's "
+       "groups at most 32 (56 for I32), the splits adding into out with atomics; stream: a prep launch over "
+       "(group, 64 columns), then cu_count*2 blocks over (row tiles x splits, rounded up to 8) x column tiles items "
+       "of 128 x 128 (I8, 128-value chunks), 128 x 64 (I32) or 128 x 32 outputs, the splits adding into out with "
+       "atomics; mfma: cu_count*4 blocks over 64 x 64 output tiles; any: threads stride over the outputs\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i) {
     const std::string& sym = L.entries[i].symbol;
     const bool is_stream = sym.size() > 7 && sym.compare(sym.size() - 7, 7, "_stream") == 0;

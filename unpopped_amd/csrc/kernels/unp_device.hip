@@ -2347,116 +2347,124 @@ UNP_DEV void dqgemm_mfma(const u8* __restrict__ w, const i32* __restrict__ zero,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const i64 ntn = (C + BN - 1) / BN;
-  const i64 tile_r = ((i64)blockIdx.x / ntn) * BM, tile_c = ((i64)blockIdx.x % ntn) * BN;
-  const i64 ng = K / G;
-  const int q = lane >> 5;  // lane group of the MFMA operands
-  const i64 arow = tile_r + wm * 32 + (lane & 31);
-  const bool arow_live = arow < R;
-  const int bcol = wn * 32 + (lane & 31);  // local column of this lane's B operand
-  const int cq = tid & 15, kq = tid >> 4;  // loader: columns 4 cq .. + 4, rows 4 kq + 64 p .. + 4
-  const i64 c0 = tile_c + 4 * cq;
-  const bool c0_live = c0 < C;
-  u32 total[16];
-#pragma unroll
-  for (int v = 0; v < 16; ++v) total[v] = 0;
-  for (i64 g = 0; g < ng; ++g) {
-    const int gb = (int)(g & 1);
-    i32x16 P[XB];
-#pragma unroll
-    for (int b = 0; b < XB; ++b)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) P[b][v] = 0;
-    u32 xacc = 0;
-#pragma unroll 1
-    for (int ch = 0; ch < NCH; ++ch) {
-      const i64 k0 = g * G + (i64)ch * KC;
-      // 1. x chunk -> digit planes, columns
-#pragma unroll
-      for (int kl = 4 * kq; kl < KC; kl += 64) {
-        u32 rows[XB][4];  // rows[j][i]: row i, column j (XB = 4) or the row's 4 bytes (XB = 1)
-        if constexpr (XB == 1) {
-          const signed char* x = static_cast<const signed char*>(xv);
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            rows[0][i] = c0_live ? *reinterpret_cast<const u32*>(x + (k0 + kl + i) * C + c0) : 0u;
-          u32 cols[4];
-          transpose4x4(rows[0], cols);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) *reinterpret_cast<u32*>(xs + (4 * cq + j) * LS + kl) = cols[j];
-        } else {
-          const i32* x = static_cast<const i32*>(xv);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            vec<u32, 4> r4;
-            if (c0_live) r4 = *reinterpret_cast<const vec<u32, 4>*>(x + (k0 + kl + i) * C + c0);
-            else r4.e[0] = r4.e[1] = r4.e[2] = r4.e[3] = 0u;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) rows[j][i] = (r4.e[j] + 0x00808080u) ^ 0x00808080u;
-          }
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            u32 planes[4];
-            transpose4x4(rows[j], planes);
-#pragma unroll
-            for (int b = 0; b < 4; ++b) *reinterpret_cast<u32*>(xs + (b * BN + 4 * cq + j) * LS + kl) = planes[b];
-          }
-        }
-      }
-      // 2. the rows' scale and zero * scale (rows past R: 0), once per group
-      if (ch == 0 && tid < BM) {
-        const i64 r = tile_r + tid;
-        const u32 sv = r < R ? (u32)scale[r * ng + g] : 0u;
-        const u32 zv = r < R ? (u32)zero[r * ng + g] : 0u;
-        srow[gb][tid] = sv;
-        zsrow[gb][tid] = zv * sv;
-      }
+  const i64 items = ((R + BM - 1) / BM) * ntn;  // 64 x 64 tiles; blocks stride over them
+  for (i64 item = blockIdx.x; item < items; item += gridDim.x) {
+    // The previous item's LDS is free once every wave has passed this barrier.
+    if (item != (i64)blockIdx.x) {
       __syncthreads();
-      if (tid < BN) {
-#pragma unroll
-        for (int b = 0; b < XB; ++b) {
-          const u32* col = reinterpret_cast<const u32*>(xs + (b * BN + tid) * LS);
-          int acc = 0;
-#pragma unroll 8
-          for (int i = 0; i < KC / 4; ++i) acc = __builtin_amdgcn_sdot4((int)col[i], 0x01010101, acc, false);
-          xacc += (u32)acc << (8 * b);
-        }
-        if (ch == NCH - 1) xsum[gb][tid] = xacc;
-      }
-      // 3. the chunk's MFMA steps
-      const u8* wrow = w + (arow * K + k0) / 2;
-#pragma unroll
-      for (int t = 0; t < KC / 32; ++t) {
-        const u64 packed = arow_live ? *reinterpret_cast<const u64*>(wrow + (32 * t + 16 * q) / 2) : 0ull;
-        const i32x4 a = unpack16<QS>(packed);
-#pragma unroll
-        for (int b = 0; b < XB; ++b) {
-          const i32x4 bv = *reinterpret_cast<const i32x4*>(xs + (b * BN + bcol) * LS + 32 * t + 16 * q);
-          P[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bv, P[b], 0, 0, 0);
-        }
-      }
-      __syncthreads();  // xs is free for the next chunk; xsum is written
     }
-    // 4. rescale: lane's element v is row 8 (v / 4) + 4 q + v % 4 of the wave tile, column l % 32.
-    // srow, zsrow and xsum alternate between two buffers by group, so the next group's writes
-    // (before its first barrier) never meet this group's reads.
-    const u32 xc = xsum[gb][bcol];
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int lr = wm * 32 + 8 * (v >> 2) + 4 * q + (v & 3);
-      u32 p = (u32)P[0][v];
-#pragma unroll
-      for (int b = 1; b < XB; ++b) p += (u32)P[b][v] << (8 * b);
-      total[v] += srow[gb][lr] * p - zsrow[gb][lr] * xc;
+    const i64 tile_r = (item / ntn) * BM, tile_c = (item % ntn) * BN;
+    const i64 ng = K / G;
+    const int q = lane >> 5;  // lane group of the MFMA operands
+    const i64 arow = tile_r + wm * 32 + (lane & 31);
+    const bool arow_live = arow < R;
+    const int bcol = wn * 32 + (lane & 31);  // local column of this lane's B operand
+    const int cq = tid & 15, kq = tid >> 4;  // loader: columns 4 cq .. + 4, rows 4 kq + 64 p .. + 4
+    const i64 c0 = tile_c + 4 * cq;
+    const bool c0_live = c0 < C;
+    u32 total[16];
+  #pragma unroll
+    for (int v = 0; v < 16; ++v) total[v] = 0;
+    for (i64 g = 0; g < ng; ++g) {
+      const int gb = (int)(g & 1);
+      i32x16 P[XB];
+  #pragma unroll
+      for (int b = 0; b < XB; ++b)
+  #pragma unroll
+        for (int v = 0; v < 16; ++v) P[b][v] = 0;
+      u32 xacc = 0;
+  #pragma unroll 1
+      for (int ch = 0; ch < NCH; ++ch) {
+        const i64 k0 = g * G + (i64)ch * KC;
+        // 1. x chunk -> digit planes, columns
+  #pragma unroll
+        for (int kl = 4 * kq; kl < KC; kl += 64) {
+          u32 rows[XB][4];  // rows[j][i]: row i, column j (XB = 4) or the row's 4 bytes (XB = 1)
+          if constexpr (XB == 1) {
+            const signed char* x = static_cast<const signed char*>(xv);
+  #pragma unroll
+            for (int i = 0; i < 4; ++i)
+              rows[0][i] = c0_live ? *reinterpret_cast<const u32*>(x + (k0 + kl + i) * C + c0) : 0u;
+            u32 cols[4];
+            transpose4x4(rows[0], cols);
+  #pragma unroll
+            for (int j = 0; j < 4; ++j) *reinterpret_cast<u32*>(xs + (4 * cq + j) * LS + kl) = cols[j];
+          } else {
+            const i32* x = static_cast<const i32*>(xv);
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              vec<u32, 4> r4;
+              if (c0_live) r4 = *reinterpret_cast<const vec<u32, 4>*>(x + (k0 + kl + i) * C + c0);
+              else r4.e[0] = r4.e[1] = r4.e[2] = r4.e[3] = 0u;
+  #pragma unroll
+              for (int j = 0; j < 4; ++j) rows[j][i] = (r4.e[j] + 0x00808080u) ^ 0x00808080u;
+            }
+  #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              u32 planes[4];
+              transpose4x4(rows[j], planes);
+  #pragma unroll
+              for (int b = 0; b < 4; ++b) *reinterpret_cast<u32*>(xs + (b * BN + 4 * cq + j) * LS + kl) = planes[b];
+            }
+          }
+        }
+        // 2. the rows' scale and zero * scale (rows past R: 0), once per group
+        if (ch == 0 && tid < BM) {
+          const i64 r = tile_r + tid;
+          const u32 sv = r < R ? (u32)scale[r * ng + g] : 0u;
+          const u32 zv = r < R ? (u32)zero[r * ng + g] : 0u;
+          srow[gb][tid] = sv;
+          zsrow[gb][tid] = zv * sv;
+        }
+        __syncthreads();
+        if (tid < BN) {
+  #pragma unroll
+          for (int b = 0; b < XB; ++b) {
+            const u32* col = reinterpret_cast<const u32*>(xs + (b * BN + tid) * LS);
+            int acc = 0;
+  #pragma unroll 8
+            for (int i = 0; i < KC / 4; ++i) acc = __builtin_amdgcn_sdot4((int)col[i], 0x01010101, acc, false);
+            xacc += (u32)acc << (8 * b);
+          }
+          if (ch == NCH - 1) xsum[gb][tid] = xacc;
+        }
+        // 3. the chunk's MFMA steps
+        const u8* wrow = w + (arow * K + k0) / 2;
+  #pragma unroll
+        for (int t = 0; t < KC / 32; ++t) {
+          const u64 packed = arow_live ? *reinterpret_cast<const u64*>(wrow + (32 * t + 16 * q) / 2) : 0ull;
+          const i32x4 a = unpack16<QS>(packed);
+  #pragma unroll
+          for (int b = 0; b < XB; ++b) {
+            const i32x4 bv = *reinterpret_cast<const i32x4*>(xs + (b * BN + bcol) * LS + 32 * t + 16 * q);
+            P[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bv, P[b], 0, 0, 0);
+          }
+        }
+        __syncthreads();  // xs is free for the next chunk; xsum is written
+      }
+      // 4. rescale: lane's element v is row 8 (v / 4) + 4 q + v % 4 of the wave tile, column l % 32.
+      // srow, zsrow and xsum alternate between two buffers by group, so the next group's writes
+      // (before its first barrier) never meet this group's reads.
+      const u32 xc = xsum[gb][bcol];
+  #pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int lr = wm * 32 + 8 * (v >> 2) + 4 * q + (v & 3);
+        u32 p = (u32)P[0][v];
+  #pragma unroll
+        for (int b = 1; b < XB; ++b) p += (u32)P[b][v] << (8 * b);
+        total[v] += srow[gb][lr] * p - zsrow[gb][lr] * xc;
+      }
+    }
+    const i64 c = tile_c + bcol;
+    if (c < C) {
+  #pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const i64 r = tile_r + wm * 32 + 8 * (v >> 2) + 4 * q + (v & 3);
+        if (r < R) out[r * C + c] = (i32)total[v];
+      }
     }
   }
-  const i64 c = tile_c + bcol;
-  if (c < C) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const i64 r = tile_r + wm * 32 + 8 * (v >> 2) + 4 * q + (v & 3);
-      if (r < R) out[r * C + c] = (i32)total[v];
-    }
-  }
+
 }
 
 // ---------------------------------------------------------------------------------------
@@ -2491,36 +2499,43 @@ UNP_DEV void dqg_prep(const XT* __restrict__ x, u8* __restrict__ xp, u32* __rest
   __shared__ u32 part[4][64];
   const int tid = threadIdx.x, cl = tid & 63, t4 = tid >> 6;
   const i64 slabs = Cp / 64;
-  const i64 g = (i64)blockIdx.x / slabs, c = ((i64)blockIdx.x % slabs) * 64 + cl;
-  const bool live = c < C;
-  u32 sum = 0;
-  for (i64 ks = t4; ks < G / 16; ks += 4) {
-    const i64 k0 = g * G + ks * 16;
-    u32 wd[XB][4];
-#pragma unroll
-    for (int b = 0; b < XB; ++b)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) wd[b][e] = 0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const u32 v = live ? (u32)(i32)x[(k0 + i) * C + c] : 0u;
-      sum += v;
-      const u32 z = XB == 4 ? ((v + 0x00808080u) ^ 0x00808080u) : (v & 0xFFu);
-#pragma unroll
-      for (int b = 0; b < XB; ++b) wd[b][i >> 2] |= ((z >> (8 * b)) & 0xFFu) << (8 * (i & 3));
+  const i64 items = (K / G) * slabs;  // (group, 64-column slab); blocks stride over them
+  for (i64 item = blockIdx.x; item < items; item += gridDim.x) {
+    // The previous item's LDS is free once every wave has passed this barrier.
+    if (item != (i64)blockIdx.x) {
+      __syncthreads();
     }
-    const i64 kc = k0 / KC, kseg = (k0 % KC) / 16;
-#pragma unroll
-    for (int b = 0; b < XB; ++b) {
-      vec<u32, 4> o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o.e[e] = wd[b][e];
-      *reinterpret_cast<vec<u32, 4>*>(xp + (((kc * XB + b) * (KC / 16) + kseg) * Cp + c) * 16) = o;
+    const i64 g = item / slabs, c = (item % slabs) * 64 + cl;
+    const bool live = c < C;
+    u32 sum = 0;
+    for (i64 ks = t4; ks < G / 16; ks += 4) {
+      const i64 k0 = g * G + ks * 16;
+      u32 wd[XB][4];
+  #pragma unroll
+      for (int b = 0; b < XB; ++b)
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) wd[b][e] = 0;
+  #pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const u32 v = live ? (u32)(i32)x[(k0 + i) * C + c] : 0u;
+        sum += v;
+        const u32 z = XB == 4 ? ((v + 0x00808080u) ^ 0x00808080u) : (v & 0xFFu);
+  #pragma unroll
+        for (int b = 0; b < XB; ++b) wd[b][i >> 2] |= ((z >> (8 * b)) & 0xFFu) << (8 * (i & 3));
+      }
+      const i64 kc = k0 / KC, kseg = (k0 % KC) / 16;
+  #pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        vec<u32, 4> o;
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) o.e[e] = wd[b][e];
+        *reinterpret_cast<vec<u32, 4>*>(xp + (((kc * XB + b) * (KC / 16) + kseg) * Cp + c) * 16) = o;
+      }
     }
+    part[t4][cl] = sum;
+    __syncthreads();
+    if (t4 == 0) xsum[g * Cp + c] = part[0][cl] + part[1][cl] + part[2][cl] + part[3][cl];
   }
-  part[t4][cl] = sum;
-  __syncthreads();
-  if (t4 == 0) xsum[g * Cp + c] = part[0][cl] + part[1][cl] + part[2][cl] + part[3][cl];
   for (i64 o = (i64)blockIdx.x * 256 + tid; o < n_out; o += (i64)gridDim.x * 256) out[o] = 0;
 }
 
@@ -2845,41 +2860,48 @@ UNP_DEV void dqg_prep16(const XT* __restrict__ x, u8* __restrict__ xp, u32* __re
   __shared__ u32 part[16][16];
   const int tid = threadIdx.x, cl = tid & 15, t16 = tid >> 4;
   const i64 tiles = Cp / 16;
-  const i64 g = (i64)blockIdx.x / tiles, c = ((i64)blockIdx.x % tiles) * 16 + cl;
-  const bool live = c < C;
-  u32 sum = 0;
-  for (i64 ks = t16; ks < G / 16; ks += 16) {
-    const i64 k0 = g * G + ks * 16;
-    u32 wd[XB][4];
-#pragma unroll
-    for (int b = 0; b < XB; ++b)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) wd[b][e] = 0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const u32 v = live ? (u32)(i32)x[(k0 + i) * C + c] : 0u;
-      sum += v;
-      // Signed byte digits of v (x = sum_b d_b 256^b, d_b in [-128, 127]) for I32; the byte for I8.
-      const u32 z = XB == 4 ? ((v + 0x00808080u) ^ 0x00808080u) : (v & 0xFFu);
-#pragma unroll
-      for (int b = 0; b < XB; ++b) wd[b][i >> 2] |= ((z >> (8 * b)) & 0xFFu) << (8 * (i & 3));
+  const i64 items = (K / G) * tiles;  // (group, 16-column tile); blocks stride over them
+  for (i64 item = blockIdx.x; item < items; item += gridDim.x) {
+    // The previous item's LDS is free once every wave has passed this barrier.
+    if (item != (i64)blockIdx.x) {
+      __syncthreads();
     }
-    const i64 kc = k0 / 64, kseg = (k0 % 64) / 16;
-#pragma unroll
-    for (int b = 0; b < XB; ++b) {
-      vec<u32, 4> o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o.e[e] = wd[b][e];
-      *reinterpret_cast<vec<u32, 4>*>(xp + (((kc * XB + b) * 4 + kseg) * Cp + c) * 16) = o;
+    const i64 g = item / tiles, c = (item % tiles) * 16 + cl;
+    const bool live = c < C;
+    u32 sum = 0;
+    for (i64 ks = t16; ks < G / 16; ks += 16) {
+      const i64 k0 = g * G + ks * 16;
+      u32 wd[XB][4];
+  #pragma unroll
+      for (int b = 0; b < XB; ++b)
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) wd[b][e] = 0;
+  #pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const u32 v = live ? (u32)(i32)x[(k0 + i) * C + c] : 0u;
+        sum += v;
+        // Signed byte digits of v (x = sum_b d_b 256^b, d_b in [-128, 127]) for I32; the byte for I8.
+        const u32 z = XB == 4 ? ((v + 0x00808080u) ^ 0x00808080u) : (v & 0xFFu);
+  #pragma unroll
+        for (int b = 0; b < XB; ++b) wd[b][i >> 2] |= ((z >> (8 * b)) & 0xFFu) << (8 * (i & 3));
+      }
+      const i64 kc = k0 / 64, kseg = (k0 % 64) / 16;
+  #pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        vec<u32, 4> o;
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) o.e[e] = wd[b][e];
+        *reinterpret_cast<vec<u32, 4>*>(xp + (((kc * XB + b) * 4 + kseg) * Cp + c) * 16) = o;
+      }
     }
-  }
-  part[t16][cl] = sum;
-  __syncthreads();
-  if (t16 == 0) {
-    u32 t = 0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) t += part[j][cl];
-    xsum[g * Cp + c] = t;
+    part[t16][cl] = sum;
+    __syncthreads();
+    if (t16 == 0) {
+      u32 t = 0;
+  #pragma unroll
+      for (int j = 0; j < 16; ++j) t += part[j][cl];
+      xsum[g * Cp + c] = t;
+    }
   }
   for (i64 o = (i64)blockIdx.x * 256 + tid; o < n_out; o += (i64)gridDim.x * 256) out[o] = 0;
 }
@@ -2907,187 +2929,195 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
   const i64 ng = K / G;
   const i64 tiles_r = (R + BM - 1) / BM, tiles_c = (C + BN - 1) / BN;
   // Block b: XCD b % 8; its slot b / 8 names (row tile of that XCD, split, column tile).
-  const i64 xcd = (i64)blockIdx.x % 8, slot = (i64)blockIdx.x / 8, per = S * tiles_c;
-  const i64 rt = (slot / per) * 8 + xcd, split = (slot % per) / tiles_c, ct = slot % tiles_c;
-  if (rt >= tiles_r) return;
-  const i64 tile_r = rt * BM, tile_c = ct * BN;
-  const i64 g0 = ng * split / S, g1 = ng * (split + 1) / S;
-  const int ngr = (int)(g1 - g0);  // at most MAXG: the host picks S
-  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)(u32)(R * (K / 2)), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xp, (short)0, (int)(u32)(K * Cp * XB), 0x00020000);
-  const i64 kb = g0 * G, nsteps = (i64)ngr * SPG;
-  u32 wofs[MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    const i64 row = tile_r + wave * 16 * MT + 16 * m + r16;
-    wofs[m] = (u32)((row < R ? row : R - 1) * (K / 2) + kb / 2 + 16 * kq);
-  }
-  u32x4b wv[D][MT];
-  auto load = [&](int sl, i64 i) {
-    const int sw = (int)(64 * i);
-#pragma unroll
-    for (int m = 0; m < MT; ++m) wv[sl][m] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)wofs[m], sw, 0);
-  };
-  // The 16-byte x' units of `steps` steps from step s0 on (unit u: column u % 16, segment
-  // (u / 16) % 8, plane, column tile, then step), steps past the block's last clamped to it.
-  constexpr int UPS = XSEG * 16;  // units per step
-  auto xunit = [&](i64 s0, int u) -> u32x4b {
-    const int c = u % 16, e = (u / 16) % 8, b = (u / 128) % XB, t = (u / (128 * XB)) % NC;
-    const i64 s = s0 + u / UPS, i = s < nsteps ? s : nsteps - 1;
-    const int off = (int)((((kb / 64 + 2 * i + e / 4) * XB + b) * 4 + e % 4) * Cp + tile_c + 16 * t + c) * 16;
-    return __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
-  };
-  // Step i's x' operand of column tile t, plane b, half step h (half step h of lane (kq, c) covers
-  // k = 32 kq + 16 h + [0, 16) of the step: segment 2 kq + h).
-  auto xop = [&](i64 i, int t, int b, int h) -> i32x4 {
-    const i64 st = XM == 1 ? i : (i / P & 1) * P + i % P;
-    return *reinterpret_cast<const i32x4*>(xl + ((((st * NC + t) * XB + b) * 8 + 2 * kq + h) * 16 + r16) * 16);
-  };
-#pragma unroll
-  for (int p = 0; p < D; ++p) load(p, p < nsteps ? p : nsteps - 1);
-  // XM 1: every step's x' now.  XM 2: phase 0 now, each later phase while the one before runs.
-  constexpr int PU = ((XM == 1 ? MAXG * SPG : P) * UPS + THREADS - 1) / THREADS;
-  u32x4b tmp[PU];
-  auto xfetch = [&](i64 s0, int nu) {
-#pragma unroll
-    for (int j = 0; j < PU; ++j) {
-      const int u = tid + THREADS * j;
-      if (XM == 2 || u < nu) tmp[j] = xunit(s0, u < nu ? u : 0);
-    }
-  };
-  auto xstore = [&](int buf, int nu) {
-#pragma unroll
-    for (int j = 0; j < PU; ++j) {
-      const int u = tid + THREADS * j;
-      if (u < nu) *reinterpret_cast<u32x4b*>(xl + 16 * (buf * P * UPS + u)) = tmp[j];
-    }
-  };
-  if constexpr (XM == 1) {
-    xfetch(0, (int)nsteps * UPS);
-    xstore(0, (int)nsteps * UPS);
-  } else {
-    xfetch(0, P * UPS);
-    xstore(0, P * UPS);
-  }
-  // The preload: every load issued at once, while the first steps are in flight.
-  constexpr int PL = (BM * MAXG + THREADS - 1) / THREADS, PX = (BN * MAXG + THREADS - 1) / THREADS;
-  u32 sv[PL], zv[PL], cv[PX];
-#pragma unroll
-  for (int j = 0; j < PL; ++j) {
-    const int idx = tid + THREADS * j, r = idx / MAXG, gg = idx % MAXG;
-    const i64 row = tile_r + r < R ? tile_r + r : R - 1;
-    const bool ok = r < BM && gg < ngr;
-    sv[j] = ok ? (u32)scale[row * ng + g0 + gg] : 0u;
-    zv[j] = ok ? (u32)zero[row * ng + g0 + gg] : 0u;
-  }
-#pragma unroll
-  for (int j = 0; j < PX; ++j) {
-    const int idx = tid + THREADS * j, gg = idx / BN, c = idx % BN;
-    cv[j] = gg < ngr ? xsum[(g0 + gg) * Cp + tile_c + c] : 0u;
-  }
-#pragma unroll
-  for (int j = 0; j < PL; ++j) {
-    const int idx = tid + THREADS * j, r = idx / MAXG, gg = idx % MAXG;
-    if (r < BM) {
-      ss[gg][r] = sv[j];
-      zs[gg][r] = sv[j] * zv[j];
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < PX; ++j) {
-    const int idx = tid + THREADS * j, gg = idx / BN, c = idx % BN;
-    if (gg < MAXG) xs[gg][c] = cv[j];
-  }
-  __syncthreads();
-  i32x4 Pa[MT][NC][XB];
-  u32 total[MT][NC][4];
-#pragma unroll
-  for (int m = 0; m < MT; ++m)
-#pragma unroll
-    for (int t = 0; t < NC; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) total[m][t][v] = 0;
-  const i32x4 Z = {0, 0, 0, 0};
-  // Step i (I its place in the unrolled pass, whose start is a whole number of groups): the MFMAs
-  // of w slot I % D, and at a group's end total += scale * P - (scale * zero) * xsum.
-  auto step = [&](int I, i64 i) {
-    const int sl = I % D;
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const i32x4 a0 = unpack16<QS>((u64)wv[sl][m][0] | ((u64)wv[sl][m][1] << 32));
-      const i32x4 a1 = unpack16<QS>((u64)wv[sl][m][2] | ((u64)wv[sl][m][3] << 32));
-#pragma unroll
-      for (int t = 0; t < NC; ++t)
-#pragma unroll
-        for (int b = 0; b < XB; ++b) {
-          Pa[m][t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, xop(i, t, b, 0), I % SPG == 0 ? Z : Pa[m][t][b], 0, 0, 0);
-          Pa[m][t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, xop(i, t, b, 1), Pa[m][t][b], 0, 0, 0);
-        }
-    }
-    if ((I + 1) % SPG == 0) {
-      // Lane (kq, c) holds rows 4 kq + v of each m-tile, column c.
-      const int gg = (int)(i / SPG);
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const int lr = wave * 16 * MT + 16 * m + 4 * kq;
-        const vec<u32, 4> s4 = *reinterpret_cast<const vec<u32, 4>*>(&ss[gg][lr]);
-        const vec<u32, 4> z4 = *reinterpret_cast<const vec<u32, 4>*>(&zs[gg][lr]);
-#pragma unroll
-        for (int t = 0; t < NC; ++t) {
-          const u32 xc = xs[gg][16 * t + r16];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            u32 p = (u32)Pa[m][t][0][v];
-#pragma unroll
-            for (int b = 1; b < XB; ++b) p += (u32)Pa[m][t][b][v] << (8 * b);
-            total[m][t][v] += s4.e[v] * p - z4.e[v] * xc;
-          }
-        }
-      }
-    }
-  };
-  if constexpr (XM == 1) {
-    for (i64 i0 = 0; i0 < nsteps; i0 += D) {
-#pragma unroll
-      for (int I = 0; I < D; ++I) {
-        const i64 i = i0 + I;
-        if (i < nsteps) step(I, i);
-        load(I, i + D < nsteps ? i + D : nsteps - 1);
-      }
-    }
-  } else {
-    // One phase per pass: the next phase's x' is loaded at the pass's start and written to the
-    // other buffer at its end (whose last readers passed the previous pass's barrier), then one
-    // barrier.  Every load is unconditional (clamped), so each pass issues the same loads.
-    for (i64 i0 = 0; i0 < nsteps; i0 += P) {
-      xfetch(i0 + P, P * UPS);
-#pragma unroll
-      for (int I = 0; I < P; ++I) {
-        const i64 i = i0 + I;
-        if (i < nsteps) step(I, i);
-        load(I % D, i + D < nsteps ? i + D : nsteps - 1);
-      }
-      xstore((int)((i0 / P + 1) & 1), P * UPS);
+  const i64 items = (tiles_r + 7) / 8 * 8 * S * tiles_c;  // XCD-interleaved (row tile, split, column tile)
+  for (i64 item = blockIdx.x; item < items; item += gridDim.x) {
+    // The previous item's LDS is free once every wave has passed this barrier.
+    if (item != (i64)blockIdx.x) {
       __syncthreads();
     }
-  }
-#pragma unroll
-  for (int t = 0; t < NC; ++t) {
-    const i64 c = tile_c + 16 * t + r16;
-    if (c < C) {
-#pragma unroll
-      for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const i64 r = tile_r + wave * 16 * MT + 16 * m + 4 * kq + v;
-          if (r < R) {
-            if (S == 1) out[r * C + c] = (i32)total[m][t][v];
-            else __hip_atomic_fetch_add(reinterpret_cast<u32*>(out) + r * C + c, total[m][t][v], __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
+    const i64 xcd = item % 8, slot = item / 8, per = S * tiles_c;
+    const i64 rt = (slot / per) * 8 + xcd, split = (slot % per) / tiles_c, ct = slot % tiles_c;
+    if (rt >= tiles_r) continue;
+    const i64 tile_r = rt * BM, tile_c = ct * BN;
+    const i64 g0 = ng * split / S, g1 = ng * (split + 1) / S;
+    const int ngr = (int)(g1 - g0);  // at most MAXG: the host picks S
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)(u32)(R * (K / 2)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xp, (short)0, (int)(u32)(K * Cp * XB), 0x00020000);
+    const i64 kb = g0 * G, nsteps = (i64)ngr * SPG;
+    u32 wofs[MT];
+  #pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const i64 row = tile_r + wave * 16 * MT + 16 * m + r16;
+      wofs[m] = (u32)((row < R ? row : R - 1) * (K / 2) + kb / 2 + 16 * kq);
+    }
+    u32x4b wv[D][MT];
+    auto load = [&](int sl, i64 i) {
+      const int sw = (int)(64 * i);
+  #pragma unroll
+      for (int m = 0; m < MT; ++m) wv[sl][m] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)wofs[m], sw, 0);
+    };
+    // The 16-byte x' units of `steps` steps from step s0 on (unit u: column u % 16, segment
+    // (u / 16) % 8, plane, column tile, then step), steps past the block's last clamped to it.
+    constexpr int UPS = XSEG * 16;  // units per step
+    auto xunit = [&](i64 s0, int u) -> u32x4b {
+      const int c = u % 16, e = (u / 16) % 8, b = (u / 128) % XB, t = (u / (128 * XB)) % NC;
+      const i64 s = s0 + u / UPS, i = s < nsteps ? s : nsteps - 1;
+      const int off = (int)((((kb / 64 + 2 * i + e / 4) * XB + b) * 4 + e % 4) * Cp + tile_c + 16 * t + c) * 16;
+      return __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+    };
+    // Step i's x' operand of column tile t, plane b, half step h (half step h of lane (kq, c) covers
+    // k = 32 kq + 16 h + [0, 16) of the step: segment 2 kq + h).
+    auto xop = [&](i64 i, int t, int b, int h) -> i32x4 {
+      const i64 st = XM == 1 ? i : (i / P & 1) * P + i % P;
+      return *reinterpret_cast<const i32x4*>(xl + ((((st * NC + t) * XB + b) * 8 + 2 * kq + h) * 16 + r16) * 16);
+    };
+  #pragma unroll
+    for (int p = 0; p < D; ++p) load(p, p < nsteps ? p : nsteps - 1);
+    // XM 1: every step's x' now.  XM 2: phase 0 now, each later phase while the one before runs.
+    constexpr int PU = ((XM == 1 ? MAXG * SPG : P) * UPS + THREADS - 1) / THREADS;
+    u32x4b tmp[PU];
+    auto xfetch = [&](i64 s0, int nu) {
+  #pragma unroll
+      for (int j = 0; j < PU; ++j) {
+        const int u = tid + THREADS * j;
+        if (XM == 2 || u < nu) tmp[j] = xunit(s0, u < nu ? u : 0);
+      }
+    };
+    auto xstore = [&](int buf, int nu) {
+  #pragma unroll
+      for (int j = 0; j < PU; ++j) {
+        const int u = tid + THREADS * j;
+        if (u < nu) *reinterpret_cast<u32x4b*>(xl + 16 * (buf * P * UPS + u)) = tmp[j];
+      }
+    };
+    if constexpr (XM == 1) {
+      xfetch(0, (int)nsteps * UPS);
+      xstore(0, (int)nsteps * UPS);
+    } else {
+      xfetch(0, P * UPS);
+      xstore(0, P * UPS);
+    }
+    // The preload: every load issued at once, while the first steps are in flight.
+    constexpr int PL = (BM * MAXG + THREADS - 1) / THREADS, PX = (BN * MAXG + THREADS - 1) / THREADS;
+    u32 sv[PL], zv[PL], cv[PX];
+  #pragma unroll
+    for (int j = 0; j < PL; ++j) {
+      const int idx = tid + THREADS * j, r = idx / MAXG, gg = idx % MAXG;
+      const i64 row = tile_r + r < R ? tile_r + r : R - 1;
+      const bool ok = r < BM && gg < ngr;
+      sv[j] = ok ? (u32)scale[row * ng + g0 + gg] : 0u;
+      zv[j] = ok ? (u32)zero[row * ng + g0 + gg] : 0u;
+    }
+  #pragma unroll
+    for (int j = 0; j < PX; ++j) {
+      const int idx = tid + THREADS * j, gg = idx / BN, c = idx % BN;
+      cv[j] = gg < ngr ? xsum[(g0 + gg) * Cp + tile_c + c] : 0u;
+    }
+  #pragma unroll
+    for (int j = 0; j < PL; ++j) {
+      const int idx = tid + THREADS * j, r = idx / MAXG, gg = idx % MAXG;
+      if (r < BM) {
+        ss[gg][r] = sv[j];
+        zs[gg][r] = sv[j] * zv[j];
+      }
+    }
+  #pragma unroll
+    for (int j = 0; j < PX; ++j) {
+      const int idx = tid + THREADS * j, gg = idx / BN, c = idx % BN;
+      if (gg < MAXG) xs[gg][c] = cv[j];
+    }
+    __syncthreads();
+    i32x4 Pa[MT][NC][XB];
+    u32 total[MT][NC][4];
+  #pragma unroll
+    for (int m = 0; m < MT; ++m)
+  #pragma unroll
+      for (int t = 0; t < NC; ++t)
+  #pragma unroll
+        for (int v = 0; v < 4; ++v) total[m][t][v] = 0;
+    const i32x4 Z = {0, 0, 0, 0};
+    // Step i (I its place in the unrolled pass, whose start is a whole number of groups): the MFMAs
+    // of w slot I % D, and at a group's end total += scale * P - (scale * zero) * xsum.
+    auto step = [&](int I, i64 i) {
+      const int sl = I % D;
+  #pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const i32x4 a0 = unpack16<QS>((u64)wv[sl][m][0] | ((u64)wv[sl][m][1] << 32));
+        const i32x4 a1 = unpack16<QS>((u64)wv[sl][m][2] | ((u64)wv[sl][m][3] << 32));
+  #pragma unroll
+        for (int t = 0; t < NC; ++t)
+  #pragma unroll
+          for (int b = 0; b < XB; ++b) {
+            Pa[m][t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, xop(i, t, b, 0), I % SPG == 0 ? Z : Pa[m][t][b], 0, 0, 0);
+            Pa[m][t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, xop(i, t, b, 1), Pa[m][t][b], 0, 0, 0);
+          }
+      }
+      if ((I + 1) % SPG == 0) {
+        // Lane (kq, c) holds rows 4 kq + v of each m-tile, column c.
+        const int gg = (int)(i / SPG);
+  #pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const int lr = wave * 16 * MT + 16 * m + 4 * kq;
+          const vec<u32, 4> s4 = *reinterpret_cast<const vec<u32, 4>*>(&ss[gg][lr]);
+          const vec<u32, 4> z4 = *reinterpret_cast<const vec<u32, 4>*>(&zs[gg][lr]);
+  #pragma unroll
+          for (int t = 0; t < NC; ++t) {
+            const u32 xc = xs[gg][16 * t + r16];
+  #pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              u32 p = (u32)Pa[m][t][0][v];
+  #pragma unroll
+              for (int b = 1; b < XB; ++b) p += (u32)Pa[m][t][b][v] << (8 * b);
+              total[m][t][v] += s4.e[v] * p - z4.e[v] * xc;
+            }
           }
         }
+      }
+    };
+    if constexpr (XM == 1) {
+      for (i64 i0 = 0; i0 < nsteps; i0 += D) {
+  #pragma unroll
+        for (int I = 0; I < D; ++I) {
+          const i64 i = i0 + I;
+          if (i < nsteps) step(I, i);
+          load(I, i + D < nsteps ? i + D : nsteps - 1);
+        }
+      }
+    } else {
+      // One phase per pass: the next phase's x' is loaded at the pass's start and written to the
+      // other buffer at its end (whose last readers passed the previous pass's barrier), then one
+      // barrier.  Every load is unconditional (clamped), so each pass issues the same loads.
+      for (i64 i0 = 0; i0 < nsteps; i0 += P) {
+        xfetch(i0 + P, P * UPS);
+  #pragma unroll
+        for (int I = 0; I < P; ++I) {
+          const i64 i = i0 + I;
+          if (i < nsteps) step(I, i);
+          load(I % D, i + D < nsteps ? i + D : nsteps - 1);
+        }
+        xstore((int)((i0 / P + 1) & 1), P * UPS);
+        __syncthreads();
+      }
+    }
+  #pragma unroll
+    for (int t = 0; t < NC; ++t) {
+      const i64 c = tile_c + 16 * t + r16;
+      if (c < C) {
+  #pragma unroll
+        for (int m = 0; m < MT; ++m)
+  #pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const i64 r = tile_r + wave * 16 * MT + 16 * m + 4 * kq + v;
+            if (r < R) {
+              if (S == 1) out[r * C + c] = (i32)total[m][t][v];
+              else __hip_atomic_fetch_add(reinterpret_cast<u32*>(out) + r * C + c, total[m][t][v], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+            }
+          }
+      }
     }
   }
+
 }
 
 // ---------------------------------------------------------------------------------------

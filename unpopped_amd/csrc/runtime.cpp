@@ -11,10 +11,10 @@
 // dequant launch takes a device-class grid (cu_count times the entry's blocks per CU) and its
 // blocks stride over the work, the surplus exiting.  The work decomposition itself (the column
 // reduction's chunks of the reduced axis, the scan's tiles) is sized from the extents; it sets
-// how many items the fixed grid strides over, not how many blocks run.  One path departs from
-// the rule: the dequantizing GEMM launches one block per (row tile, split of K, column tile)
-// item of its MFMA schedules and one prep block per (group, column slab), i.e. a grid that is
-// the item count.
+// how many items the fixed grid strides over, not how many blocks run.  The dequantizing GEMM's
+// decode, MFMA and prep kernels do the same over their (row tile, split of K, column tile), tile
+// and (group, column slab) items.  One entry departs from the rule: the streaming entry launches a
+// block per item (an item loop around its LDS pipeline made it spill).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -1277,9 +1277,14 @@ int32_t run_repacked(unp_exec* x, size_t prep, size_t main, uint64_t w, uint64_t
   uint64_t xp = (uint64_t)wsp.ws, xs = xp + xp_bytes;
   long long Kp = K, Cc = C, Cpp = Cp, G = group, n_out = S > 1 ? R * C : 0;
   void* pparams[] = {&xa, &xp, &xs, &Kp, &Cc, &Cpp, &G, &out, &n_out};
-  if ((rc = launch(x, prep, (uint32_t)(ng * (Cp / prep_cols)), pparams, s, err)) != UNP_OK) return rc;
+  // Device-class grids: the prep's blocks stride over its (group, column slab) items and the main
+  // kernel's over its `blocks` items, as many blocks as the entry keeps resident per CU.
+  if ((rc = launch(x, prep, (uint32_t)(x->cu_count * x->l.blocks_per_cu), pparams, s, err)) != UNP_OK) return rc;
+  // The streaming entry keeps one block per item: an item loop around its LDS pipeline made it spill.
+  const bool per_item = ends_with(x->l.entries[main].symbol, "_stream");
+  const int bpc = x->l.entries[main].blocks_per_cu ? x->l.entries[main].blocks_per_cu : 2;
   void* mparams[] = {&w, &zp, &sc, &xp, &xs, &out, &R, &K, &C, &Cpp, &S};
-  return launch(x, main, (uint32_t)blocks, mparams, s, err);
+  return launch(x, main, (uint32_t)(per_item ? blocks : x->cu_count * bpc), mparams, s, err);
 }
 
 int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, unp_error* err) {
@@ -1347,7 +1352,8 @@ int32_t run_dequant_gemm(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s,
   const bool mfma_ok = mfma != SIZE_MAX && K % group == 0 && C % 4 == 0 && xa % (x32 ? 16 : 4) == 0 &&
                        (w & 7) == 0 && (zp & 3) == 0 && (sc & 3) == 0 && (out & 3) == 0 && tiles <= 0x7FFFFFFFLL;
   const size_t entry = mfma_ok ? mfma : any;
-  const uint32_t grid = mfma_ok ? (uint32_t)tiles : (uint32_t)(x->cu_count * x->l.blocks_per_cu);
+  // Both take a device-class grid; the MFMA entry's blocks stride over its 64 x 64 tiles.
+  const uint32_t grid = (uint32_t)(x->cu_count * (mfma_ok ? 4 : x->l.blocks_per_cu));
   void* params[] = {&w, &zp, &sc, &xa, &out, &R, &K, &C};
   return launch(x, entry, grid, params, s, err);
 }
