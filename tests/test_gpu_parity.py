@@ -739,6 +739,11 @@ def _gemm_entry(w_kind, x_dtype, group):
     return H.executor(kind="dequant_gemm", q_kind=w_kind, dtype=kind, group=group).last_launch()["entry"]
 
 
+def _gemm_last_launch(w_kind, x_dtype, group):
+    kind = "I32" if x_dtype == np.int32 else "I8"
+    return H.executor(kind="dequant_gemm", q_kind=w_kind, dtype=kind, group=group).last_launch()
+
+
 def test_dequant_gemm_reference_fixture(hip_device):
     """kernel_dequant_gemm.rs:26-49 on the fixture of support/dequant.rs:145-181 (R=4, K=8, C=4,
     GROUP=4): the host loop's answer for I4 and U4 weights, and the two differ."""
@@ -1740,6 +1745,25 @@ def test_grids_do_not_follow_the_extents(hip_device):
             grids.add(ex.last_launch()["grid"][0])
         assert len(grids) == 1, (form, grids)
         assert next(iter(grids)) % cus == 0, (form, grids)
+
+
+def test_dequant_gemm_decode_and_mfma_grids_do_not_follow_the_extents(hip_device):
+    """The dequant GEMM's decode entries (one block per CU) and MFMA entry (four per CU) take the same
+    grid at every shape, their blocks striding over the items; results stay bit-exact, including a
+    shape with more items than blocks."""
+    _, cus = u.device_info()
+    for xdt, group, shapes in ((np.int8, 128, [(40, 256, 9), (5000, 2048, 16), (2048, 1024, 64)]),
+                               (np.int32, 128, [(64, 256, 16), (3000, 2048, 100)]),
+                               (np.int8, 96, [(70, 192, 8), (3000, 1152, 64)])):
+        grids = set()
+        for (R, K, C) in shapes:
+            H.say(f"[case] gemm grid {np.dtype(xdt).name} g{group} {R}x{K}x{C}")
+            w, zero, scale, x = _gemm_data(R + K + C, R, K, C, group, xdt)
+            got = H.dequant_gemm(w, zero, scale, x, R, K, C, group)
+            want = oracle.dequant_gemm_i32(w, zero, scale, x, R, K, C, group)
+            assert np.array_equal(got, want), (R, K, C)
+            grids.add(_gemm_last_launch("U4", xdt, group)["grid"][0])
+        assert len(grids) == 1 and next(iter(grids)) % cus == 0, (np.dtype(xdt).name, group, grids)
 
 
 # ---------------------------------------------------------------------------------------
