@@ -1739,8 +1739,8 @@ int32_t lower_row_reduce(const RowReduceSpec& sp, Lowered& L, std::string& why) 
   for (int k = 0; k < sp.n_inputs; ++k) j << "{\"name\":\"in" << k << "\",\"kind\":\"buffer\",\"role\":\"Read\"},";
   j << "{\"name\":\"out\",\"kind\":\"buffer\",\"role\":\"Write\"}";
   for (int d = 0; d < sp.rank; ++d) j << ",{\"name\":\"n" << d << "\",\"kind\":\"scalar\",\"dtype\":\"I32\"}";
-  j << "],\"launch\":{\"block\":[256,1,1],\"grid\":\"min(rows, cu_count*8)\",\"grid_policy\":\"one block per row, rows "
-       "block-strided\"},\"entries\":[";
+  j << "],\"launch\":{\"block\":[256,1,1],\"grid\":\"cu_count*min(8, blocks one CU holds)\",\"grid_policy\":\"one "
+       "block per row, rows block-strided; the next row's loads issued before this row's stages\"},\"entries\":[";
   for (size_t i = 0; i < L.entries.size(); ++i)
     j << (i ? "," : "") << "{\"symbol\":\"" << L.entries[i].symbol << "\",\"vec\":" << L.entries[i].vec
       << ",\"row_in_registers\":" << (L.entries[i].k ? "true" : "false") << ",\"when\":\""

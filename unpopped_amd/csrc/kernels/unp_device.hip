@@ -3311,21 +3311,34 @@ UNP_DEV void row_reduce_staged(const T* const* in, T* __restrict__ out, i64 rows
   __shared__ double redsh[NS];
   const int tid = threadIdx.x;
   const i64 nvec = cols / VEC;
-  for (i64 row = blockIdx.x; row < rows; row += gridDim.x) {
+  typedef vec<T, VEC> RowRegs[NI][R > 0 ? R : 1];
+  // With the row in registers (R > 0: 16-byte vectors, cols a multiple of VEC) every load and
+  // store of a row is a buffer access whose range is the row: a lane past the row's end reads 0
+  // and its store is dropped, and a row past the last has an empty range.  So each row issues
+  // the same R loads per input and R stores whatever its length, the compiler can count them, and
+  // a wait for this row's vectors leaves the next row's loads in flight.
+  auto row_rsrc = [&](const T* base, i64 row) {
+    const bool live = row < rows;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (live ? row : 0) * cols), (short)0,
+                                             (int)(u32)(live ? cols * (i64)sizeof(T) : 0), 0x00020000);
+  };
+  auto load_row = [&](i64 row, RowRegs& xr) {
+    if constexpr (R > 0) {
+      static_assert(sizeof(T) * VEC == 16, "the in-register rows move 16-byte vectors");
+#pragma unroll
+      for (int k = 0; k < NI; ++k) {
+        const __amdgpu_buffer_rsrc_t rk = row_rsrc(in[k], row);
+#pragma unroll
+        for (int q = 0; q < R; ++q)
+          xr[k][q] = __builtin_bit_cast(vec<T, VEC>, __builtin_amdgcn_raw_buffer_load_b128(rk, (q * THREADS + tid) * 16, 0, 2));
+      }
+    }
+  };
+  auto one_row = [&](i64 row, const RowRegs& xr) {
     const T* rin[NI];
 #pragma unroll
     for (int k = 0; k < NI; ++k) rin[k] = in[k] + row * cols;
     T* __restrict__ rout = out + row * cols;
-    vec<T, VEC> xr[NI][R > 0 ? R : 1];
-    if constexpr (R > 0) {
-#pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const i64 v = (i64)q * THREADS + tid;
-        if (v < nvec)
-#pragma unroll
-          for (int k = 0; k < NI; ++k) xr[k][q] = ld_nt<T, VEC>(rin[k] + v * VEC);
-      }
-    }
     double red[NS];
     double cv[R > 0 ? R : 1][VEC];
     rr_stage<T, NI, NS, OPS, THREADS, VEC, R, 0>(rin, xr, cols, red, part, redsh, cv);
@@ -3340,32 +3353,21 @@ UNP_DEV void row_reduce_staged(const T* const* in, T* __restrict__ out, i64 rows
       }
       st_nt<T, VEC>(rout + at * VEC, o);
     };
-    if constexpr (R > 0 && OPS::cached >= 0) {
+    if constexpr (R > 0) {
+      // Lanes past the row's end compute on what they hold and their stores are dropped.
+      const __amdgpu_buffer_rsrc_t ro = row_rsrc(out, row);
 #pragma unroll
       for (int q = 0; q < R; ++q) {
-        const i64 v = (i64)q * THREADS + tid;
-        if (v < nvec) {
-          vec<T, VEC> o;
+        vec<T, VEC> o;
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            double x[NI];
+        for (int e = 0; e < VEC; ++e) {
+          double x[NI];
 #pragma unroll
-            for (int k = 0; k < NI; ++k) x[k] = (double)xr[k][q].e[e];
-            o.e[e] = (T)OPS::epi_c(x, red, cv[q][e]);
-          }
-          st_nt<T, VEC>(rout + v * VEC, o);
+          for (int k = 0; k < NI; ++k) x[k] = (double)xr[k][q].e[e];
+          if constexpr (OPS::cached >= 0) o.e[e] = (T)OPS::epi_c(x, red, cv[q][e]);
+          else o.e[e] = (T)OPS::epi(x, red);
         }
-      }
-    } else if constexpr (R > 0) {
-#pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const i64 v = (i64)q * THREADS + tid;
-        if (v < nvec) {
-          vec<T, VEC> xv[NI];
-#pragma unroll
-          for (int k = 0; k < NI; ++k) xv[k] = xr[k][q];
-          emit(xv, v);
-        }
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4b, o), ro, (q * THREADS + tid) * 16, 0, 2);
       }
     } else {
       for (i64 v = tid; v < nvec; v += THREADS) {
@@ -3375,6 +3377,24 @@ UNP_DEV void row_reduce_staged(const T* const* in, T* __restrict__ out, i64 rows
         emit(xv, v);
       }
     }
+  };
+  const i64 G = gridDim.x;
+  if constexpr (R > 0) {
+    // Two register sets, the loop unrolled by two: the block's next row is loaded into the other
+    // set before this row's stages run, so its loads are in flight under this row's arithmetic and
+    // no copy between the sets waits on them.
+    RowRegs xa, xb;
+    load_row(blockIdx.x, xa);
+    for (i64 row = blockIdx.x; row < rows; row += 2 * G) {
+      load_row(row + G, xb);
+      one_row(row, xa);
+      if (row + G >= rows) break;
+      load_row(row + 2 * G, xa);
+      one_row(row + G, xb);
+    }
+  } else {
+    RowRegs none;
+    for (i64 row = blockIdx.x; row < rows; row += G) one_row(row, none);
   }
 }
 

@@ -89,6 +89,8 @@ struct unp_exec {
   unp::Lowered l;
   hipModule_t mod = nullptr;
   std::vector<hipFunction_t> fns;
+  // Blocks of each entry that one CU holds at once, by its registers and LDS (0: not asked).
+  std::vector<int> resident;
   int device = 0;
   int cu_count = 0;
   void* ws = nullptr;  // scan: tile status words; full reduction: block partials
@@ -418,6 +420,12 @@ int32_t unp_hip_exec_create(const unp_generated* g, unp_exec** out, unp_error* e
       return hip_fail(err, ("hipModuleGetFunction " + en.symbol).c_str(), e);
     }
     x->fns.push_back(f);
+    int per_cu = 0;
+    if (x->l.form.kind == UNP_FORM_ROW_REDUCE &&
+        hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, en.threads > 0 ? en.threads : x->l.threads, 0) !=
+            hipSuccess)
+      per_cu = 0;
+    x->resident.push_back(per_cu);
   }
   set_error(err, UNP_OK, "");
   *out = x;
@@ -1044,7 +1052,10 @@ int32_t run_row_reduce(unp_exec* x, const unp_arg* a, size_t n, hipStream_t s, u
   // entries: 0 the row in registers (4 vectors per thread), 1 in registers (8 vectors per
   // thread), 2 vector passes, 3 scalar passes
   const size_t entry = !aligned ? 3 : (cols <= 256LL * vec * 4 ? 0 : (cols <= 256LL * vec * 8 ? 1 : 2));
-  const long long cap = (long long)x->cu_count * x->l.blocks_per_cu;
+  // As many blocks as the CUs hold at once (at most blocks_per_cu each), so no blocks start late
+  // as a tail that runs at a fraction of the occupancy.
+  const int held = x->resident[entry];
+  const long long cap = (long long)x->cu_count * (held > 0 && held < x->l.blocks_per_cu ? held : x->l.blocks_per_cu);
   const uint32_t grid = (uint32_t)cap;
   std::vector<void*> params;
   std::vector<uint64_t> ptrs(A.buf.begin(), A.buf.end());
