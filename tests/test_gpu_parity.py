@@ -1160,6 +1160,39 @@ def test_row_reduce_nan_and_infinity_rows(hip_device):
             assert ulps(got, want).max() <= 2
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape", [(4099, 1000), (3333, 4096), (2049, 2000)])
+def test_row_reduce_many_rows_per_block(hip_device, dtype, shape):
+    """More rows than blocks (the grid is at most 8 per CU): each block takes several rows, its next
+    row loaded while this one runs, the odd counts ending on either half of the two-row loop, and
+    rows whose length leaves lanes past the end.  Same bars as the short rows."""
+    _, cus = u.device_info()
+    assert shape[0] > 8 * cus  # every block holds more than one row
+    # The centred quotient's f64 bar is its dyadic bit-exact test; here it runs at F32.
+    for which in ("softmax", "rms_norm") + (("centred_quotient",) if dtype == np.float32 else ()):
+        H.say(f"[case] row_reduce many rows {which} {np.dtype(dtype).name} {shape}")
+        stages, epi = getattr(X, which)()
+        x = rng(38).normal(size=shape).astype(dtype) * 3
+        got = H.row_reduce([x], stages, epi)
+        want = oracle.row_reduce([x], stages, epi)
+        if dtype == np.float32:
+            assert ulps(got, want).max() <= 2, which
+        else:
+            far = ulps(got, want) > 4
+            assert (np.abs(got - want)[far] <= f64_order_tolerance(x, want, which)[far]).all(), which
+
+
+def test_row_reduce_two_inputs_many_rows(hip_device):
+    """Two inputs through the two-row loop: 4000 rows of 300 (dyadic, so every order agrees)."""
+    H.say("[case] row_reduce two inputs 40x100x300")
+    a, b = dyadic(39, (40, 100, 300), np.float32), dyadic(40, (40, 100, 300), np.float32)
+    stages = [(X.input(0) * X.input(1), "Sum"), (X.input(0) - X.reduced(0), "Max")]
+    epi = X.fma(X.input(0), X.reduced(1), X.input(1) - X.reduced(0))
+    got = H.row_reduce([a, b], stages, epi)
+    want = oracle.row_reduce([a, b], stages, epi)
+    assert np.array_equal(got, want)
+
+
 def test_row_reduce_two_inputs_rank_three(hip_device):
     """Two inputs, rank 3 (rows are the product of the leading extents)."""
     H.say("[case] row_reduce two inputs rank 3")
