@@ -3163,8 +3163,9 @@ UNP_DEV void dqg_dec(const u8* __restrict__ w, const i32* __restrict__ zero, con
 // `epi(x, r)` over doubles, with the scalar functions below.
 //
 // One block per row (rows block-strided).  R > 0: the row is read once into registers
-// (R vectors of VEC per thread and input, cols <= THREADS * VEC * R); R == 0: each pass reads
-// the row again (the later passes hit in L2).  OPS::cached names a stage whose pre value
+// (R vectors of VEC per thread and input, cols <= THREADS * VEC * R), and the block's next row
+// is loaded into a second register set while this one runs; R == 0: each pass reads the row
+// again (the later passes hit in L2).  OPS::cached names a stage whose pre value
 // recurs in the epilogue (softmax's exp(x - max)): with the row in registers its f64 value per
 // element is kept from the stage and OPS::epi_c reads it back in place of a second
 // evaluation, which is the same f64 expression of the same operands.  Inside a pass thread t folds its positions in
