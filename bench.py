@@ -433,7 +433,8 @@ def ceilings(u, cus: int, reps: int = 10) -> None:
     """Streaming read / write / copy rates of this device (median of `reps` launches, the best of 1, 2
     and 4 blocks of 256 threads per CU), on 1 GiB and at each suite kernel's own size: the practical
     ceilings that the suite's kernels are read against, beside the 8 TB/s peak.  A copy of `size`
-    reads `size` bytes and writes `size` bytes."""
+    reads `size` bytes and writes `size` bytes.  Launches are timed by their own dispatch timestamps,
+    as the suite's kernels are."""
     import ctypes as C
 
     from unpopped_amd import _lib
@@ -448,6 +449,11 @@ def ceilings(u, cus: int, reps: int = 10) -> None:
         f = C.c_void_p()
         _lib.check(L.unp_hip_get_function(m, name.encode(), C.byref(f), C.byref(err)), err)
         fns[name] = f
+    def timed(f, g, blk, args, e0, e1):
+        # Each launch is timed by its own dispatch timestamps, as the suite's kernels are: events
+        # recorded on the stream around it would add their own latency (2-3 us on this device).
+        _lib.check(L.unp_hip_launch_timed(f, g, blk, 0, None, args, C.sizeof(args), e0._h, e1._h, C.byref(err)), err)
+
     big = max(size for _, size, _ in CEILING_SIZES)
     flush = MallFlush(u, cus)
     a, b, sink = u.DeviceBuffer(big), u.DeviceBuffer(big), u.DeviceBuffer(64)
@@ -466,9 +472,7 @@ def ceilings(u, cus: int, reps: int = 10) -> None:
             ts = []
             for i in range(reps + 2):
                 e0, e1 = u.Event(), u.Event()
-                e0.record()
-                _lib.check(L.unp_hip_launch(fns[name], g, blk, 0, None, args, C.sizeof(args), C.byref(err)), err)
-                e1.record()
+                timed(fns[name], g, blk, args, e0, e1)
                 e1.synchronize()
                 if i >= 2:
                     ts.append(e0.elapsed_ms(e1))
@@ -485,9 +489,7 @@ def ceilings(u, cus: int, reps: int = 10) -> None:
         for i in range(reps):
             flush.run()
             e0, e1 = u.Event(), u.Event()
-            e0.record()
-            _lib.check(L.unp_hip_launch(fns[name], g, blk, 0, None, args, C.sizeof(args), C.byref(err)), err)
-            e1.record()
+            timed(fns[name], g, blk, args, e0, e1)
             e1.synchronize()
             ts.append(e0.elapsed_ms(e1))
         cold = float(np.median(ts))
@@ -541,8 +543,8 @@ class MallFlush:
 def gemm_lines(u, synth, steps: int, warmup: int, shapes: str = "") -> None:
     """The dequantizing GEMM (tests/support/dequant.rs:104-181) at a weight of LLM size: U4 w
     8192 x 28672 with an I32 zero point and scale per 128 columns, times x of C columns (I8 and I32),
-    one JSON line per shape: the median of `steps` launches, each timed alone with HIP events after
-    a 512 MiB read with plain loads has evicted the weight from the MALL.  Bytes are w + zero + scale + x + out;
+    one JSON line per shape: the median of `steps` launches, each timed alone by its kernels' own
+    dispatch timestamps after a 512 MiB read with plain loads has evicted the weight from the MALL.  Bytes are w + zero + scale + x + out;
     operations 2 R K C.  ``shapes`` ("I8:16,I32:1024") keeps only those (activation, C) pairs."""
     from unpopped_amd import forms as H
 
@@ -570,9 +572,11 @@ def gemm_lines(u, synth, steps: int, warmup: int, shapes: str = "") -> None:
             for i in range(steps):
                 flush.run()
                 e0, e1 = u.Event(), u.Event()
-                e0.record()
+                # From the prep kernel's start to the main kernel's end, by their own dispatch
+                # timestamps (the gap between the two launches included).
+                ex.set_timing(e0, e1)
                 ex.launch(dw, dz, ds, dx, do, R, K, C)
-                e1.record()
+                ex.set_timing(None, None)
                 e1.synchronize()
                 ts.append(e0.elapsed_ms(e1) * 1e3)
             us = float(np.median(ts))

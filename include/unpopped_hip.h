@@ -317,6 +317,13 @@ int32_t unp_hip_get_function(unp_module* m, const char* name, unp_function** out
 int32_t unp_hip_launch(unp_function* f, const uint32_t grid[3], const uint32_t block[3],
                        uint32_t shared_bytes, void* stream, const void* kernarg, size_t kernarg_size,
                        unp_error* err);
+/* The same launch with `start` and `stop` recorded at the kernel's own dispatch timestamps
+ * (hipExtModuleLaunchKernel), so unp_hip_event_elapsed_ms(start, stop) is the kernel's time without
+ * the queueing around it, as a kernel trace shows it.  Either event may be null; grid x block must
+ * stay below 2^32 in each dimension. */
+int32_t unp_hip_launch_timed(unp_function* f, const uint32_t grid[3], const uint32_t block[3],
+                             uint32_t shared_bytes, void* stream, const void* kernarg, size_t kernarg_size,
+                             unp_event* start, unp_event* stop, unp_error* err);
 int32_t unp_hip_malloc(void** p, size_t bytes);
 int32_t unp_hip_free(void* p);
 int32_t unp_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);

@@ -121,6 +121,7 @@ def lib() -> C.CDLL:
         "unp_hip_module_unload": (i32, [P]),
         "unp_hip_get_function": (i32, [P, C.c_char_p, C.POINTER(P), E]),
         "unp_hip_launch": (i32, [P, C.POINTER(u32), C.POINTER(u32), u32, P, P, sz, E]),
+        "unp_hip_launch_timed": (i32, [P, C.POINTER(u32), C.POINTER(u32), u32, P, P, sz, P, P, E]),
         "unp_hip_malloc": (i32, [C.POINTER(P), sz]),
         "unp_hip_free": (i32, [P]),
         "unp_hip_memcpy_h2d": (i32, [P, P, sz]),

@@ -318,6 +318,32 @@ int32_t unp_hip_launch(unp_function* f, const uint32_t grid[3], const uint32_t b
   return UNP_OK;
 }
 
+int32_t unp_hip_launch_timed(unp_function* f, const uint32_t grid[3], const uint32_t block[3], uint32_t shared_bytes,
+                             void* stream, const void* kernarg, size_t kernarg_size, unp_event* start, unp_event* stop,
+                             unp_error* err) {
+  if (!f || !grid || !block || (kernarg_size && !kernarg)) {
+    set_error(err, UNP_INVALID_ARGUMENT, "null function, geometry or argument block");
+    return UNP_INVALID_ARGUMENT;
+  }
+  // hipExtModuleLaunchKernel takes work-items, not blocks.
+  uint32_t items[3];
+  for (int d = 0; d < 3; ++d) {
+    if ((uint64_t)grid[d] * block[d] > 0xFFFFFFFFull) {
+      set_error(err, UNP_INVALID_ARGUMENT, "a timed launch takes at most 2^32 - 1 work-items per dimension");
+      return UNP_INVALID_ARGUMENT;
+    }
+    items[d] = grid[d] * block[d];
+  }
+  size_t size = kernarg_size;
+  void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(kernarg), HIP_LAUNCH_PARAM_BUFFER_SIZE,
+                    &size, HIP_LAUNCH_PARAM_END};
+  const hipError_t e = hipExtModuleLaunchKernel(f->f, items[0], items[1], items[2], block[0], block[1], block[2],
+                                                shared_bytes, (hipStream_t)stream, nullptr, config,
+                                                start ? start->e : nullptr, stop ? stop->e : nullptr, 0);
+  if (e != hipSuccess) return hip_fail(err, "hipExtModuleLaunchKernel", e);
+  return UNP_OK;
+}
+
 int32_t unp_hip_malloc(void** p, size_t bytes) {
   if (!p) return UNP_INVALID_ARGUMENT;
   *p = nullptr;
