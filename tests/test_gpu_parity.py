@@ -1750,6 +1750,51 @@ def test_staged_views_of_the_dequant_gemm(hip_device):
 # Launch geometry: a device-class grid, never derived from an extent (PATENT-SWEEP.md:269)
 # ---------------------------------------------------------------------------------------
 
+def test_raw_launch_and_timed_launch(hip_device):
+    """The consumer's launch layer: a kernel compiled, loaded and launched with a packed argument
+    block through unp_hip_launch and unp_hip_launch_timed.  The timed launch's events bracket the
+    kernel, and a geometry past 2^32 work-items is refused before anything is launched."""
+    import ctypes as C
+
+    from unpopped_amd import _lib
+
+    L = _lib.lib()
+    src = ('extern "C" __global__ void __launch_bounds__(256) fill(unsigned* o, unsigned n, unsigned v) {\n'
+           '  const unsigned i = blockIdx.x * 256 + threadIdx.x;\n  if (i < n) o[i] = v + i;\n}\n')
+    co = u.HipCompiler().compile(src, "fill")
+    img = C.create_string_buffer(co, len(co))
+    m, f, err = C.c_void_p(), C.c_void_p(), _lib.Error()
+    _lib.check(L.unp_hip_module_load(img, len(co), C.byref(m), C.byref(err)), err)
+
+    class Args(C.Structure):
+        _fields_ = [("o", C.c_uint64), ("n", C.c_uint32), ("v", C.c_uint32)]
+
+    try:
+        _lib.check(L.unp_hip_get_function(m, b"fill", C.byref(f), C.byref(err)), err)
+        n = 100_003
+        out = u.DeviceBuffer(4 * n)
+        grid, block = (C.c_uint32 * 3)((n + 255) // 256, 1, 1), (C.c_uint32 * 3)(256, 1, 1)
+        H.say("[case] raw launch")
+        a = Args(out.ptr, n, 7)
+        _lib.check(L.unp_hip_launch(f, grid, block, 0, None, C.byref(a), C.sizeof(a), C.byref(err)), err)
+        u.synchronize()
+        assert (out.download(np.uint32, n) == 7 + np.arange(n, dtype=np.uint32)).all()
+        H.say("[case] timed raw launch")
+        e0, e1 = u.Event(), u.Event()
+        b = Args(out.ptr, n, 1000)
+        _lib.check(L.unp_hip_launch_timed(f, grid, block, 0, None, C.byref(b), C.sizeof(b), e0._h, e1._h,
+                                          C.byref(err)), err)
+        e1.synchronize()
+        assert 0.0 < e0.elapsed_ms(e1) < 100.0
+        assert (out.download(np.uint32, n) == 1000 + np.arange(n, dtype=np.uint32)).all()
+        # 2^24 blocks of 256 work-items: more than hipExtModuleLaunchKernel's 32-bit work-item count.
+        too_big = (C.c_uint32 * 3)(1 << 24, 1, 1)
+        rc = L.unp_hip_launch_timed(f, too_big, block, 0, None, C.byref(b), C.sizeof(b), None, None, C.byref(err))
+        assert rc == _lib.INVALID_ARGUMENT
+    finally:
+        L.unp_hip_module_unload(m)
+
+
 def test_grids_do_not_follow_the_extents(hip_device):
     """Every reduction, scan, gather and row-reduce launch takes the same grid whatever its extents:
     a multiple of the CU count fixed by the entry (blocks past the work exit)."""
