@@ -1161,11 +1161,13 @@ def test_row_reduce_nan_and_infinity_rows(hip_device):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
-@pytest.mark.parametrize("shape", [(4099, 1000), (3333, 4096), (2049, 2000)])
+@pytest.mark.parametrize("shape", [(4099, 1000), (3333, 4096), (2049, 2000), (2050, 6000)])
 def test_row_reduce_many_rows_per_block(hip_device, dtype, shape):
     """More rows than blocks (the grid is at most 8 per CU): each block takes several rows, its next
     row loaded while this one runs, the odd counts ending on either half of the two-row loop, and
-    rows whose length leaves lanes past the end.  Same bars as the short rows."""
+    rows whose length leaves lanes past the end.  The shapes reach the four-vector and eight-vector
+    register entries at both widths and, with 6000 f64 columns, the entry that re-reads the row.
+    Same bars as the short rows."""
     _, cus = u.device_info()
     assert shape[0] > 8 * cus  # every block holds more than one row
     # The centred quotient's f64 bar is its dyadic bit-exact test; here it runs at F32.
